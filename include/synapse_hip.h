@@ -1,0 +1,196 @@
+/*
+ * synapse_hip.h — C ABI of the MI355X (gfx950) `hip` backend for Synapse's
+ * quantized-linear hot path.
+ *
+ * Style follows the reference C header (synapse.h): every entry point returns
+ * a syn_status_t, no exception or abort crosses the boundary, all buffers are
+ * caller-owned unless a *_create / *_destroy pair says otherwise, and handles
+ * are opaque.  Signatures use plain pointers and sizes only.
+ *
+ * Two layers:
+ *   1. Reference-signature entry points (host pointers, synchronous): the
+ *      exact functions the reference's Rust FFI binds for this path
+ *      (crates/synapse-sys/src/lib.rs), so a build can link this library in
+ *      place of libsynapse_zig for them.  Each call uploads its operands.
+ *   2. Device-resident API (syn_hip_*): weights repacked once into HBM behind
+ *      a handle; activations stay on the device; calls are asynchronous on a
+ *      stream (NULL = the library's stream for the current device).
+ *
+ * Handles are not thread-safe (as the reference's Q4Linear cache and Metal
+ * state are not).  Reference paths below are relative to `synapse/`.
+ */
+#ifndef SYNAPSE_HIP_H
+#define SYNAPSE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes: synapse.h:27-35, same values and meaning ---- */
+typedef int32_t syn_status_t;
+#define SYN_OK 0
+#define SYN_ERR_NULL_PTR 1
+#define SYN_ERR_INVALID_ARG 2
+#define SYN_ERR_OUT_OF_MEMORY 3
+#define SYN_ERR_SHAPE_MISMATCH 4
+#define SYN_ERR_NOT_CONTIGUOUS 5
+#define SYN_ERR_INVALID_AXIS 6
+#define SYN_ERR_INVALID_DIMENSIONS 7
+#define SYN_ERR_INTERNAL 8
+/* device-side codes (new; >= 100 so the reference's check_status maps them to
+ * SynapseError::Unknown, crates/synapse-core/src/lib.rs:50-62) */
+#define SYN_ERR_NO_DEVICE 100
+#define SYN_ERR_HIP 101
+#define SYN_ERR_LAUNCH 102
+
+/* =====================================================================
+ * 1. Reference-signature entry points (host pointers, synchronous)
+ * =================================================================== */
+
+/* Replaces syn_quantize_per_channel_int8 (synapse.h:341-345,
+ * zig/src/ffi/exports.zig:1275-1288).  Zero dims -> SYN_ERR_INVALID_ARG. */
+syn_status_t syn_quantize_per_channel_int8(const float *data, size_t channels,
+                                           size_t channel_size, int8_t *out,
+                                           float *scales);
+
+/* Replaces syn_qgemm_int8 (synapse.h:363-368, exports.zig:1313-1350):
+ * C[m,n] = diag(scales_a) (A_i8[m,k] B_i8[k,n]) diag(scales_b), B in the
+ * reference's [K,N] layout.  Zero dims -> SYN_OK no-op. */
+syn_status_t syn_qgemm_int8(size_t m, size_t n, size_t k, const int8_t *a, size_t lda,
+                            const int8_t *b, size_t ldb, float *c, size_t ldc,
+                            const float *scales_a, const float *scales_b);
+
+/* Replaces syn_q4_0_gemv (crates/synapse-sys/src/lib.rs:413-419,
+ * exports.zig:1614-1628): c[n] = a[k] . dequant(B_q4[n,k]), B in the
+ * reference's pack_for_zig format.  k % 32 != 0 -> SYN_ERR_SHAPE_MISMATCH. */
+syn_status_t syn_q4_0_gemv(size_t n, size_t k, const float *a, const uint8_t *b_q4,
+                           float *c);
+
+/* =====================================================================
+ * 2. Device-resident API
+ * =================================================================== */
+
+/* -- runtime (no reference counterpart: device bookkeeping) -- */
+syn_status_t syn_hip_init(int device);
+syn_status_t syn_hip_device_count(int *count);
+const char *syn_hip_last_error(void);
+syn_status_t syn_hip_malloc(void **dptr, size_t bytes);
+syn_status_t syn_hip_free(void *dptr);
+syn_status_t syn_hip_memcpy_h2d(void *dst, const void *src, size_t bytes);
+syn_status_t syn_hip_memcpy_d2h(void *dst, const void *src, size_t bytes);
+syn_status_t syn_hip_memcpy_d2d(void *dst, const void *src, size_t bytes);
+syn_status_t syn_hip_memset(void *dst, int value, size_t bytes);
+syn_status_t syn_hip_synchronize(void);
+syn_status_t syn_hip_stream_create(void **stream);
+syn_status_t syn_hip_stream_destroy(void *stream);
+syn_status_t syn_hip_stream_synchronize(void *stream);
+
+/* hipEvent pair timing on a stream: elapsed ms between start and stop. */
+typedef struct syn_hip_timer_s syn_hip_timer_t;
+syn_status_t syn_hip_timer_create(syn_hip_timer_t **timer);
+syn_status_t syn_hip_timer_start(syn_hip_timer_t *timer, void *stream);
+syn_status_t syn_hip_timer_stop(syn_hip_timer_t *timer, void *stream);
+syn_status_t syn_hip_timer_elapsed_ms(syn_hip_timer_t *timer, float *ms);
+syn_status_t syn_hip_timer_destroy(syn_hip_timer_t *timer);
+
+/* -- activation quantizer on device: zig/src/ops/quantize.zig:12-47 --
+ * x f32 [m, k] (row stride ldx) -> q i8 [m, k] (row stride ldq) + scales[m]. */
+syn_status_t syn_hip_quantize_rows(const float *d_x, size_t m, size_t k, size_t ldx,
+                                   int8_t *d_q, size_t ldq, float *d_scales, void *stream);
+
+/* -- quantized linear handles --
+ * Formats:  INT8 = W8A8 per-row symmetric (QuantizedLinear,
+ * quantization/primitives/int8_linear.rs:10-170); Q4_0 = Q4Linear
+ * (q4_linear.rs:52-150, pack_for_zig byte format). */
+#define SYN_HIP_FMT_INT8 1
+#define SYN_HIP_FMT_Q4_0 2
+/* host weight layouts accepted by syn_hip_qlinear_create for INT8 */
+#define SYN_HIP_LAYOUT_KN 0 /* reference QuantizedLinear::weights_int8 [K,N] */
+#define SYN_HIP_LAYOUT_NK 1 /* row per output feature [N,K] */
+
+typedef struct syn_hip_qlinear_s syn_hip_qlinear_t;
+
+/* Repack already-quantized host weights once into HBM.
+ *   INT8: host_weights int8 in `layout`, host_scales f32[n].
+ *   Q4_0: host_weights = pack_for_zig bytes [n, k/32, 18]; host_scales unused. */
+syn_status_t syn_hip_qlinear_create(int fmt, size_t n, size_t k, const void *host_weights,
+                                    const float *host_scales, int layout,
+                                    syn_hip_qlinear_t **out);
+/* Quantize f32 host weights [n,k] with the reference quantizer of `fmt`
+ * (INT8: QuantizedLinear::from_f32, int8_linear.rs:35-70; Q4_0:
+ * Q4Linear::from_f32 + pack_for_zig, q4_linear.rs:64-121), then repack. */
+syn_status_t syn_hip_qlinear_from_f32(int fmt, size_t n, size_t k, const float *host_w,
+                                      syn_hip_qlinear_t **out);
+/* y[m,n] = x[m,k] W^T.  INT8 quantizes x per row first (forward,
+ * int8_linear.rs:87-117); Q4_0 runs f32 activations (Q4Linear::forward). */
+syn_status_t syn_hip_qlinear_forward(syn_hip_qlinear_t *h, size_t m, const float *d_x,
+                                     float *d_y, void *stream);
+/* INT8 only: forward_pre_quantized (int8_linear.rs:139-165). */
+syn_status_t syn_hip_qlinear_forward_pre_quantized(syn_hip_qlinear_t *h, size_t m,
+                                                   const int8_t *d_xq, size_t ldxq,
+                                                   const float *d_sx, float *d_y,
+                                                   void *stream);
+syn_status_t syn_hip_qlinear_info(const syn_hip_qlinear_t *h, size_t *n, size_t *k, int *fmt,
+                                  size_t *weight_bytes);
+syn_status_t syn_hip_qlinear_destroy(syn_hip_qlinear_t *h);
+
+/* -- INT8 W8A8 causal LM: QuantizedCausalLM (quantization/lm/int8.rs),
+ *    device-resident like MetalModelBuffers + gpu_forward_all_layers
+ *    (metal/gpu_buffers.rs:79-433, metal/gpu_forward.rs:429-839). -- */
+typedef struct {
+  uint32_t hidden, n_layers, n_heads, n_kv_heads, head_dim, inter, vocab, max_seq;
+  float eps;
+  double rope_theta;
+} syn_hip_lm_config;
+
+typedef struct syn_hip_qlm_s syn_hip_qlm_t;
+syn_status_t syn_hip_qlm_create(const syn_hip_lm_config *cfg, syn_hip_qlm_t **out);
+/* embed_tokens [vocab, hidden] f32 (tied: the lm_head is quantized from it) */
+syn_status_t syn_hip_qlm_set_embed(syn_hip_qlm_t *m, const float *embed);
+/* f32 [out,in] projections of one layer, quantized like quantize_model
+ * (int8.rs:78-152). */
+syn_status_t syn_hip_qlm_set_layer(syn_hip_qlm_t *m, uint32_t layer, const float *wq,
+                                   const float *wk, const float *wv, const float *wo,
+                                   const float *wg, const float *wu, const float *wd);
+/* Synthetic weights: SplitMix64(seed_base + tensor_id) + Box-Muller, tensor
+ * id 0 = embed, 1 + 8*layer + {0..6} = q,k,v,o,gate,up,down. */
+syn_status_t syn_hip_qlm_init_synthetic(syn_hip_qlm_t *m, uint64_t seed_base, float stddev);
+/* Quantize the tied lm_head, upload RoPE tables; call once after weights. */
+syn_status_t syn_hip_qlm_finalize(syn_hip_qlm_t *m);
+syn_status_t syn_hip_qlm_reset(syn_hip_qlm_t *m);
+/* forward_prefill (int8.rs:593-635): logits of the last prompt token. */
+syn_status_t syn_hip_qlm_forward_prefill(syn_hip_qlm_t *m, const uint32_t *ids, size_t n,
+                                         float *host_logits);
+/* forward_one (int8.rs:638-709) for `token` at the current cache length. */
+syn_status_t syn_hip_qlm_forward_one(syn_hip_qlm_t *m, uint32_t token, float *host_logits);
+/* Greedy generate (generation/pipeline.rs:197-278): max_new tokens from one
+ * prefill and max_new-1 decode steps, all on device (HIP graph per step);
+ * only the tokens are read back.  margins (nullable) gets top1-top2. */
+syn_status_t syn_hip_qlm_generate(syn_hip_qlm_t *m, const uint32_t *prompt, size_t n_prompt,
+                                  size_t max_new, uint32_t *out_tokens, float *out_margins);
+/* Timed decode: `steps` greedy decode steps after the current state, on the
+ * model stream; returns elapsed milliseconds measured with hipEvents. */
+syn_status_t syn_hip_qlm_decode_timed(syn_hip_qlm_t *m, size_t steps, float *elapsed_ms);
+/* Average duration of the lm_head GEMV launch (the largest decode matvec),
+ * timed with a hipEvent pair around each of `iters` launches on the model
+ * stream; between launches `flush_bytes` of device memory are overwritten so
+ * the 256 MB Infinity Cache does not hold the weights (as in a real step,
+ * where the layer weights stream through it in between). */
+syn_status_t syn_hip_qlm_time_lm_head(syn_hip_qlm_t *m, size_t iters, size_t flush_bytes,
+                                      float *avg_ms);
+syn_status_t syn_hip_qlm_destroy(syn_hip_qlm_t *m);
+
+/* -- harness helpers (no reference counterpart) -- */
+/* Diagnostic: y[i] = the device expf that SiLU and softmax use (bit-identical
+ * to glibc expf, which Rust's f32::exp calls on Linux). */
+syn_status_t syn_hip_eval_expf(const float *d_x, float *d_y, size_t n, void *stream);
+/* SplitMix64 + Box-Muller (f64, cast to f32) into host memory. */
+syn_status_t syn_hip_fill_normal(float *host_dst, size_t n, uint64_t seed, float stddev);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SYNAPSE_HIP_H */

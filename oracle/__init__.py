@@ -1,0 +1,333 @@
+"""CPU oracle (test infrastructure only).
+
+ctypes binding of ``liboracle.so`` — the plain-C restatement of the
+reference's quantized-linear path (see ``oracle.c`` for the per-function
+reference citations and the list of parity pins).  Only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import this package; the HIP product never does.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+
+CFLAGS = ["-O3", "-mavx2", "-mfma", "-mf16c", "-ffp-contract=off", "-fno-fast-math",
+          "-fopenmp", "-fPIC", "-shared", "-Wall", "-Wextra"]
+
+
+def build(verbose: bool = False) -> str:
+    """Compile oracle.c into liboracle.so (gcc; x86-64-v3 so it runs on the GPU box host)."""
+    cmd = ["gcc", *CFLAGS, "-o", LIB_PATH, os.path.join(HERE, "oracle.c"), "-lm"]
+    if verbose:
+        print(" ".join(cmd))
+    subprocess.run(cmd, check=True)
+    return LIB_PATH
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        _lib = C.CDLL(LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+P = C.c_void_p
+SZ = C.c_size_t
+
+
+class LmCfg(C.Structure):
+    _fields_ = [("hidden", SZ), ("n_layers", SZ), ("n_heads", SZ), ("n_kv_heads", SZ),
+                ("head_dim", SZ), ("inter", SZ), ("vocab", SZ), ("max_seq", SZ),
+                ("eps", C.c_float), ("rope_theta", C.c_double)]
+
+
+def _declare(L):
+    sig = {
+        "orc_fill_normal": (None, [P, SZ, C.c_uint64, C.c_float]),
+        "orc_fill_token_ids": (None, [P, SZ, C.c_uint64, C.c_uint32]),
+        "orc_f32_to_f16_trunc": (C.c_uint16, [C.c_float]),
+        "orc_f16_to_f32_zig": (C.c_float, [C.c_uint16]),
+        "orc_f16_to_f32_rs": (C.c_float, [C.c_uint16]),
+        "orc_quantize_per_channel_int8": (C.c_int, [P, SZ, SZ, P, P]),
+        "orc_minmax_scales": (None, [P, SZ, SZ, P]),
+        "orc_quantize_weights_int8": (None, [P, P, SZ, SZ, P]),
+        "orc_qgemm_int8": (C.c_int, [SZ, SZ, SZ, P, SZ, P, SZ, P, SZ, P, P]),
+        "orc_naive_int8_gemm": (None, [SZ, SZ, SZ, P, SZ, P, SZ, P, SZ, P, P]),
+        "orc_q4_packed_bytes": (SZ, [SZ, SZ]),
+        "orc_q4_from_f32_packed": (None, [P, SZ, SZ, P]),
+        "orc_q4_0_gemv": (C.c_int, [SZ, SZ, P, P, P]),
+        "orc_dequant_q4_0": (C.c_int, [P, SZ, P]),
+        "orc_dequant_q8_0": (C.c_int, [P, SZ, P]),
+        "orc_dequant_q4_k": (C.c_int, [P, SZ, P]),
+        "orc_dequant_q6_k": (C.c_int, [P, SZ, P]),
+        "orc_sgemm": (C.c_int, [SZ, SZ, SZ, P, SZ, C.c_int, P, SZ, C.c_int, P, SZ]),
+        "orc_rmsnorm": (None, [P, P, C.c_float, SZ, SZ, P]),
+        "orc_rope_tables": (None, [SZ, SZ, C.c_double, P, P]),
+        "orc_rope_apply": (None, [P, P, P, SZ, SZ, SZ, SZ]),
+        "orc_silu": (C.c_float, [C.c_float]),
+        "orc_expf": (C.c_float, [C.c_float]),
+        "orc_softmax_slice": (None, [P, SZ]),
+        "orc_argmax": (C.c_uint32, [P, SZ]),
+        "orc_attention_decode": (None, [P, P, P, SZ, SZ, SZ, SZ, P]),
+        "orc_fused_attention": (C.c_int, [SZ, SZ, SZ, P, P, P, P]),
+        "orc_qlm_create": (P, [C.POINTER(LmCfg)]),
+        "orc_qlm_destroy": (None, [P]),
+        "orc_qlm_set_embed": (C.c_int, [P, P]),
+        "orc_qlm_set_layer": (C.c_int, [P, SZ, P, P, P, P, P, P, P]),
+        "orc_qlm_init_synthetic": (C.c_int, [P, C.c_uint64, C.c_float]),
+        "orc_qlm_finalize": (C.c_int, [P]),
+        "orc_qlm_reset": (None, [P]),
+        "orc_qlm_cur_len": (SZ, [P]),
+        "orc_qlm_prefill": (C.c_int, [P, P, SZ, P]),
+        "orc_qlm_forward_one": (C.c_int, [P, C.c_uint32, P]),
+        "orc_qlm_generate": (C.c_int, [P, P, SZ, SZ, P, P]),
+        "orc_qlm_lm_head_weights": (P, [P]),
+        "orc_qlm_lm_head_scales": (P, [P]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"], "oracle needs C-contiguous arrays"
+    return a.ctypes.data_as(C.c_void_p)
+
+
+# ---------------------------------------------------------------- inputs
+def normal(n: int, seed: int, std: float = 1.0) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().orc_fill_normal(_p(out), n, seed, std)
+    return out
+
+
+def token_ids(n: int, seed: int, vocab: int) -> np.ndarray:
+    out = np.empty(n, np.uint32)
+    lib().orc_fill_token_ids(_p(out), n, seed, vocab)
+    return out
+
+
+# ---------------------------------------------------------------- A1/A2
+def quantize_per_channel_int8(x: np.ndarray):
+    x = np.ascontiguousarray(x, np.float32)
+    m, k = x.shape
+    q = np.empty((m, k), np.int8)
+    s = np.empty(m, np.float32)
+    rc = lib().orc_quantize_per_channel_int8(_p(x), m, k, _p(q), _p(s))
+    if rc:
+        raise ValueError(f"orc_quantize_per_channel_int8 status {rc}")
+    return q, s
+
+
+def quantize_weights_int8(w: np.ndarray):
+    """QuantizedLinear::from_f32: w [N,K] f32 -> (weights_int8 [K,N], scales [N])."""
+    w = np.ascontiguousarray(w, np.float32)
+    n, k = w.shape
+    s = np.empty(n, np.float32)
+    q = np.empty((k, n), np.int8)
+    lib().orc_minmax_scales(_p(w), n, k, _p(s))
+    lib().orc_quantize_weights_int8(_p(w), _p(s), n, k, _p(q))
+    return q, s
+
+
+def qgemm_int8(a: np.ndarray, b_kn: np.ndarray, sa: np.ndarray, sb: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, np.int8)
+    b_kn = np.ascontiguousarray(b_kn, np.int8)
+    m, k = a.shape
+    k2, n = b_kn.shape
+    assert k == k2
+    c = np.zeros((m, n), np.float32)
+    sa = np.ascontiguousarray(sa, np.float32)
+    sb = np.ascontiguousarray(sb, np.float32)
+    rc = lib().orc_qgemm_int8(m, n, k, _p(a), k, _p(b_kn), n, _p(c), n, _p(sa), _p(sb))
+    if rc:
+        raise ValueError(f"orc_qgemm_int8 status {rc}")
+    return c
+
+
+def naive_int8_gemm(a, b_kn, sa, sb):
+    a = np.ascontiguousarray(a, np.int8)
+    b_kn = np.ascontiguousarray(b_kn, np.int8)
+    m, k = a.shape
+    n = b_kn.shape[1]
+    c = np.zeros((m, n), np.float32)
+    sa = np.ascontiguousarray(sa, np.float32)
+    sb = np.ascontiguousarray(sb, np.float32)
+    lib().orc_naive_int8_gemm(m, n, k, _p(a), k, _p(b_kn), n, _p(c), n, _p(sa), _p(sb))
+    return c
+
+
+# ---------------------------------------------------------------- Q4_0
+def q4_pack(w: np.ndarray) -> np.ndarray:
+    """Q4Linear::from_f32 + pack_for_zig: w [N,K] -> bytes [N * ceil(K/32) * 18]."""
+    w = np.ascontiguousarray(w, np.float32)
+    n, k = w.shape
+    out = np.empty(lib().orc_q4_packed_bytes(n, k), np.uint8)
+    lib().orc_q4_from_f32_packed(_p(w), n, k, _p(out))
+    return out
+
+
+def q4_0_gemv(a: np.ndarray, packed: np.ndarray, n: int) -> np.ndarray:
+    a = np.ascontiguousarray(a, np.float32)
+    packed = np.ascontiguousarray(packed, np.uint8)
+    c = np.zeros(n, np.float32)
+    rc = lib().orc_q4_0_gemv(n, a.shape[0], _p(a), _p(packed), _p(c))
+    if rc:
+        raise ValueError(f"orc_q4_0_gemv status {rc}")
+    return c
+
+
+# ---------------------------------------------------------------- GGUF dequant
+def dequant(fmt: str, data: np.ndarray, numel: int) -> np.ndarray:
+    data = np.ascontiguousarray(data, np.uint8)
+    out = np.empty(numel, np.float32)
+    fn = {"q4_0": lib().orc_dequant_q4_0, "q8_0": lib().orc_dequant_q8_0,
+          "q4_k": lib().orc_dequant_q4_k, "q6_k": lib().orc_dequant_q6_k}[fmt]
+    rc = fn(_p(data), numel, _p(out))
+    if rc:
+        raise ValueError(f"dequant {fmt} status {rc}")
+    return out
+
+
+# ---------------------------------------------------------------- f32 GEMM
+def matmul_t(a: np.ndarray, w_nk: np.ndarray) -> np.ndarray:
+    """ops/matmul.rs:55-79: a [M,K] x W[N,K]^T via syn_sgemm(trans_b=1)."""
+    a = np.ascontiguousarray(a, np.float32)
+    w_nk = np.ascontiguousarray(w_nk, np.float32)
+    m, k = a.shape
+    n = w_nk.shape[0]
+    c = np.zeros((m, n), np.float32)
+    rc = lib().orc_sgemm(m, n, k, _p(a), k, 0, _p(w_nk), k, 1, _p(c), n)
+    if rc:
+        raise ValueError(f"orc_sgemm status {rc}")
+    return c
+
+
+# ---------------------------------------------------------------- ops
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    rows, h = x.shape
+    out = np.empty_like(x)
+    lib().orc_rmsnorm(_p(x), _p(np.ascontiguousarray(w, np.float32)), eps, rows, h, _p(out))
+    return out
+
+
+def rope_tables(max_pos: int, head_dim: int, base: float):
+    c = np.empty((max_pos, head_dim // 2), np.float32)
+    s = np.empty_like(c)
+    lib().orc_rope_tables(max_pos, head_dim, base, _p(c), _p(s))
+    return c, s
+
+
+def argmax(x: np.ndarray) -> int:
+    x = np.ascontiguousarray(x, np.float32)
+    return int(lib().orc_argmax(_p(x), x.size))
+
+
+def expf(x: float) -> float:
+    return float(lib().orc_expf(x))
+
+
+def silu(x: float) -> float:
+    return float(lib().orc_silu(x))
+
+
+def fused_attention(q, k, v):
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    sq, d = q.shape
+    sk = k.shape[0]
+    out = np.zeros((sq, d), np.float32)
+    lib().orc_fused_attention(sq, sk, d, _p(q), _p(k), _p(v), _p(out))
+    return out
+
+
+def attention_decode(q, kcache, vcache, seq_len, n_heads, n_kv, head_dim):
+    q = np.ascontiguousarray(q, np.float32)
+    out = np.zeros(n_heads * head_dim, np.float32)
+    lib().orc_attention_decode(_p(q), _p(np.ascontiguousarray(kcache, np.float32)),
+                               _p(np.ascontiguousarray(vcache, np.float32)), seq_len,
+                               n_heads, n_kv, head_dim, _p(out))
+    return out
+
+
+# ---------------------------------------------------------------- A15 model
+class QuantizedCausalLM:
+    """INT8 W8A8 decoder (quantization/lm/int8.rs) restated in C."""
+
+    def __init__(self, cfg: dict):
+        self.cfg = cfg
+        c = LmCfg(cfg["hidden"], cfg["n_layers"], cfg["n_heads"], cfg["n_kv_heads"],
+                  cfg["head_dim"], cfg["inter"], cfg["vocab"], cfg["max_seq"],
+                  cfg.get("eps", 1e-6), cfg.get("rope_theta", 1e6))
+        self._c = c
+        self.h = lib().orc_qlm_create(C.byref(c))
+        if not self.h:
+            raise MemoryError("orc_qlm_create failed")
+
+    def init_synthetic(self, seed_base: int = 0x5EED0000, std: float = 0.02):
+        rc = lib().orc_qlm_init_synthetic(self.h, seed_base, std)
+        if rc:
+            raise RuntimeError(f"orc_qlm_init_synthetic status {rc}")
+        self._check(lib().orc_qlm_finalize(self.h))
+
+    def set_weights(self, embed: np.ndarray, layers: list):
+        self._keep = [embed]
+        self._check(lib().orc_qlm_set_embed(self.h, _p(np.ascontiguousarray(embed, np.float32))))
+        for i, lw in enumerate(layers):
+            arrs = [np.ascontiguousarray(lw[n], np.float32)
+                    for n in ("q", "k", "v", "o", "gate", "up", "down")]
+            self._check(lib().orc_qlm_set_layer(self.h, i, *[_p(a) for a in arrs]))
+        self._check(lib().orc_qlm_finalize(self.h))
+
+    @staticmethod
+    def _check(rc):
+        if rc:
+            raise RuntimeError(f"oracle status {rc}")
+
+    def reset(self):
+        lib().orc_qlm_reset(self.h)
+
+    def prefill(self, ids) -> np.ndarray:
+        ids = np.ascontiguousarray(ids, np.uint32)
+        logits = np.empty(self.cfg["vocab"], np.float32)
+        self._check(lib().orc_qlm_prefill(self.h, _p(ids), ids.size, _p(logits)))
+        return logits
+
+    def forward_one(self, token: int) -> np.ndarray:
+        logits = np.empty(self.cfg["vocab"], np.float32)
+        self._check(lib().orc_qlm_forward_one(self.h, int(token), _p(logits)))
+        return logits
+
+    def generate(self, prompt, max_new: int):
+        prompt = np.ascontiguousarray(prompt, np.uint32)
+        toks = np.zeros(max_new, np.uint32)
+        margins = np.zeros(max_new, np.float32)
+        self._check(lib().orc_qlm_generate(self.h, _p(prompt), prompt.size, max_new,
+                                           _p(toks), _p(margins)))
+        return toks, margins
+
+    def close(self):
+        if self.h:
+            lib().orc_qlm_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

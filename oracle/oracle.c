@@ -1,0 +1,996 @@
+/*
+ * CPU oracle for the quantized-linear hot path — TEST INFRASTRUCTURE ONLY.
+ *
+ * Plain-C restatement of the reference (eren23/synapse) algorithms.  Each
+ * function names the reference file:line it restates; paths are relative to
+ * the reference's `synapse/` directory.  It is the parity checker for the HIP
+ * library and the timed "cpu_simd port" baseline; the product never links it.
+ *
+ * Floating-point contract: built with -ffp-contract=off, so every `a*b + c`
+ * written here rounds twice, as the reference's Zig (strict float mode) and
+ * Rust (no contraction) code does; fmaf() marks the places where the
+ * reference uses @mulAdd.  libm calls (expf, powf, cosf, sinf, sqrtf) go to
+ * glibc, which is what Rust's f32 methods call on Linux.
+ *
+ * Parity pins (see tests/test_oracle_*.py):
+ *   - quantizer KATs from zig/tests/test_quantize.zig:143-170, 225-246
+ *   - qgemm KATs from crates/synapse-core/src/lib.rs:1541-1567
+ *   - GGUF KATs from weight_loading/gguf.rs:700-721, 789-820
+ *   - f16 conversions checked exhaustively against IEEE (numpy float16)
+ *   - integer GEMM checked against brute force in int64
+ * Parity unpinned (no reference test, no runnable reference here):
+ *   - Q4_K / Q6_K dequant beyond the restated source text (self-made KATs only)
+ *   - exact order of Zig's @reduce(.Add) (taken as sequential, LLVM's ordered
+ *     vector.reduce.fadd) and whether Zig contracts `a*b + c` (taken as no)
+ *   - libm bit patterns of exp/pow/cos/sin on the reference's own host
+ */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ======================================================================
+ * Harness input spec: SplitMix64 + Box-Muller (f64, cast to f32).
+ * Not a reference algorithm — the synthetic-data contract shared with the
+ * HIP library's own generator.
+ * ==================================================================== */
+static uint64_t splitmix64(uint64_t *s) {
+  uint64_t z = (*s += 0x9E3779B97F4A7C15ULL);
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ULL;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBULL;
+  return z ^ (z >> 31);
+}
+
+void orc_fill_normal(float *dst, size_t n, uint64_t seed, float stddev) {
+  uint64_t s = seed;
+  const double two_pi = 6.283185307179586476925286766559;
+  const double sd = (double)stddev;
+  size_t i = 0;
+  while (i < n) {
+    double u1 = ((double)(splitmix64(&s) >> 11) + 1.0) * (1.0 / 9007199254740992.0);
+    double u2 = (double)(splitmix64(&s) >> 11) * (1.0 / 9007199254740992.0);
+    double r = sqrt(-2.0 * log(u1));
+    double z0 = r * cos(two_pi * u2);
+    double z1 = r * sin(two_pi * u2);
+    dst[i++] = (float)(z0 * sd);
+    if (i < n) dst[i++] = (float)(z1 * sd);
+  }
+}
+
+void orc_fill_token_ids(uint32_t *dst, size_t n, uint64_t seed, uint32_t vocab) {
+  uint64_t s = seed;
+  for (size_t i = 0; i < n; i++) dst[i] = (uint32_t)(splitmix64(&s) % (uint64_t)vocab);
+}
+
+/* ======================================================================
+ * f16 conversions
+ * ==================================================================== */
+static inline uint32_t f2u(float f) { uint32_t u; memcpy(&u, &f, 4); return u; }
+static inline float u2f(uint32_t u) { float f; memcpy(&f, &u, 4); return f; }
+
+/* q4_linear.rs:9-33 — truncating f32->f16; subnormal/underflow -> signed 0 */
+uint16_t orc_f32_to_f16_trunc(float val) {
+  uint32_t bits = f2u(val);
+  uint32_t sign = (bits >> 16) & 0x8000u;
+  int32_t exp = (int32_t)((bits >> 23) & 0xFFu);
+  uint32_t man = bits & 0x7FFFFFu;
+  if (exp == 0) return (uint16_t)sign;
+  if (exp == 0xFF) return (uint16_t)(sign | 0x7C00u | (man != 0 ? 0x200u : 0u));
+  int32_t new_exp = exp - 127 + 15;
+  if (new_exp >= 31) return (uint16_t)(sign | 0x7C00u);
+  if (new_exp <= 0) return (uint16_t)sign;
+  return (uint16_t)(sign | ((uint32_t)new_exp << 10) | (man >> 13));
+}
+
+/* qmatmul.zig:346-371 — IEEE-exact f16->f32 (used by the Q4_0 GEMV) */
+float orc_f16_to_f32_zig(uint16_t bits) {
+  uint32_t sign = ((uint32_t)(bits >> 15)) << 31;
+  uint32_t exp5 = (bits >> 10) & 0x1Fu;
+  uint32_t mant = bits & 0x3FFu;
+  if (exp5 == 0) {
+    if (mant == 0) return u2f(sign);
+    uint32_t m = mant, e = 0;
+    while ((m & 0x400u) == 0) { m <<= 1; e += 1; }
+    m &= 0x3FFu;
+    uint32_t exp32 = (127u - 15u + 1u - e) << 23;
+    return u2f(sign | exp32 | (m << 13));
+  } else if (exp5 == 31) {
+    return u2f(sign | 0x7F800000u | (mant << 13));
+  }
+  return u2f(sign | ((exp5 + 127u - 15u) << 23) | (mant << 13));
+}
+
+/* weight_loading/converter.rs:12-40 — used by every GGUF dequantizer.
+ * The subnormal branch starts its shift counter at 1, so subnormal inputs
+ * come out at half their IEEE value; restated as written. */
+float orc_f16_to_f32_rs(uint16_t h) {
+  uint32_t sign = (h >> 15) & 1u;
+  uint32_t exp = (h >> 10) & 0x1Fu;
+  uint32_t mant = h & 0x3FFu;
+  if (exp == 0) {
+    if (mant == 0) return u2f(sign << 31);
+    uint32_t e = 1, m = mant;
+    while ((m & 0x400u) == 0) { m <<= 1; e += 1; }
+    m = (m & 0x3FFu) << 13;
+    e = 127u - 15u + 1u - e;
+    return u2f((sign << 31) | (e << 23) | m);
+  } else if (exp == 31) {
+    return u2f((sign << 31) | (0xFFu << 23) | (mant << 13));
+  }
+  return u2f((sign << 31) | ((exp + 127u - 15u) << 23) | (mant << 13));
+}
+
+/* ======================================================================
+ * A1 — zig/src/ops/quantize.zig:12-47 via ffi/exports.zig:1275-1288
+ * ==================================================================== */
+int orc_quantize_per_channel_int8(const float *data, size_t channels, size_t channel_size,
+                                  int8_t *out, float *scales) {
+  if (!data || !out || !scales) return ORC_ERR_NULL_PTR;
+  if (channels == 0 || channel_size == 0) return ORC_ERR_INVALID_ARG; /* exports.zig:1284 */
+  for (size_t c = 0; c < channels; c++) {
+    const float *row = data + c * channel_size;
+    int8_t *orow = out + c * channel_size;
+    float max_abs = 0.0f;
+    for (size_t j = 0; j < channel_size; j++) {
+      float a = fabsf(row[j]);
+      if (a > max_abs) max_abs = a;
+    }
+    if (max_abs == 0.0f) {
+      scales[c] = 1.0f;
+      memset(orow, 0, channel_size);
+      continue;
+    }
+    scales[c] = max_abs / 127.0f;
+    float inv_scale = 127.0f / max_abs;
+    for (size_t j = 0; j < channel_size; j++) {
+      float r = roundf(row[j] * inv_scale); /* @round: half away from zero */
+      if (r > 127.0f) r = 127.0f;
+      if (r < -127.0f) r = -127.0f;
+      orow[j] = (int8_t)r;
+    }
+  }
+  return ORC_OK;
+}
+
+/* ======================================================================
+ * A2 — quantization/primitives/calibration.rs:11-24 and
+ *      int8_linear.rs:35-70 (from_f32_with_scales + transpose_i8)
+ * ==================================================================== */
+void orc_minmax_scales(const float *w, size_t channels, size_t channel_size, float *scales) {
+  for (size_t ch = 0; ch < channels; ch++) {
+    const float *row = w + ch * channel_size;
+    float max_abs = 0.0f;
+    for (size_t j = 0; j < channel_size; j++) max_abs = fmaxf(max_abs, fabsf(row[j]));
+    scales[ch] = (max_abs == 0.0f) ? 1.0f : max_abs / 127.0f;
+  }
+}
+
+/* out_kn is the reference's GEMM-ready transposed layout [in_features, out_features]. */
+void orc_quantize_weights_int8(const float *w, const float *scales, size_t out_features,
+                               size_t in_features, int8_t *out_kn) {
+  for (size_t ch = 0; ch < out_features; ch++) {
+    float s = scales[ch];
+    if (s == 0.0f) {
+      for (size_t j = 0; j < in_features; j++) out_kn[j * out_features + ch] = 0;
+      continue;
+    }
+    float inv_s = 1.0f / s;
+    for (size_t j = 0; j < in_features; j++) {
+      float v = roundf(w[ch * in_features + j] * inv_s);
+      if (v < -128.0f) v = -128.0f;
+      if (v > 127.0f) v = 127.0f;
+      out_kn[j * out_features + ch] = (int8_t)v;
+    }
+  }
+}
+
+/* ======================================================================
+ * A3/A4 — zig/src/ops/qmatmul.zig:37-99 (int8GemmTiled), :171-256
+ * (int8GemvRow), :442-548 (macro/micro kernels) via exports.zig:1313-1350
+ * ==================================================================== */
+#define ORC_KC 512
+static void int8_gemv_row(size_t n, size_t k, const int8_t *a, const int8_t *b, size_t ldb,
+                          float *c, float sa, const float *sb) {
+  size_t j = 0;
+  /* 64-column blocks: i32 accumulators, then (f32(acc)*sa)*sb (qmatmul.zig:187-225) */
+  for (; j + 64 <= n; j += 64) {
+    int32_t acc[64];
+    memset(acc, 0, sizeof(acc));
+    for (size_t p = 0; p < k; p++) {
+      const int32_t av = a[p];
+      const int8_t *bp = b + p * ldb + j;
+      for (int v = 0; v < 64; v++) acc[v] += av * (int32_t)bp[v];
+    }
+    for (int v = 0; v < 64; v++) c[j + v] = (float)acc[v] * sa * sb[j + v];
+  }
+  /* 8-column blocks (:228-246) */
+  for (; j + 8 <= n; j += 8) {
+    int32_t acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (size_t p = 0; p < k; p++) {
+      const int32_t av = a[p];
+      const int8_t *bp = b + p * ldb + j;
+      for (int v = 0; v < 8; v++) acc[v] += av * (int32_t)bp[v];
+    }
+    for (int v = 0; v < 8; v++) c[j + v] = (float)acc[v] * sa * sb[j + v];
+  }
+  /* scalar tail (:249-255) */
+  for (; j < n; j++) {
+    int32_t acc = 0;
+    for (size_t p = 0; p < k; p++) acc += (int32_t)a[p] * (int32_t)b[p * ldb + j];
+    c[j] = (float)acc * sa * sb[j];
+  }
+}
+
+int orc_qgemm_int8(size_t m, size_t n, size_t k, const int8_t *a, size_t lda, const int8_t *b,
+                   size_t ldb, float *c, size_t ldc, const float *scales_a,
+                   const float *scales_b) {
+  if (!a || !b || !c || !scales_a || !scales_b) return ORC_ERR_NULL_PTR;
+  if (m == 0 || n == 0 || k == 0) return ORC_OK; /* exports.zig:1331 */
+  if (m <= 16) {                                  /* qmatmul.zig:54-66 */
+    for (size_t i = 0; i < m; i++)
+      int8_gemv_row(n, k, a + i * lda, b, ldb, c + i * ldc, scales_a[i], scales_b);
+    return ORC_OK;
+  }
+  /* M > 16: C zeroed, then for each KC=512 chunk (in order) the exact i32
+   * partial is converted and added: C += (f32(acc_chunk)*sa)*sb.  Packing and
+   * MR/NR tiling do not change any value, so the restatement walks chunks. */
+  for (size_t i = 0; i < m; i++) memset(c + i * ldc, 0, n * sizeof(float));
+  int32_t *acc = (int32_t *)malloc(n * sizeof(int32_t));
+  if (!acc) return ORC_ERR_OUT_OF_MEMORY;
+  for (size_t pc = 0; pc < k; pc += ORC_KC) {
+    size_t kc = (k - pc < ORC_KC) ? (k - pc) : ORC_KC;
+    for (size_t i = 0; i < m; i++) {
+      memset(acc, 0, n * sizeof(int32_t));
+      const int8_t *ar = a + i * lda + pc;
+      for (size_t p = 0; p < kc; p++) {
+        const int32_t av = ar[p];
+        const int8_t *bp = b + (pc + p) * ldb;
+        for (size_t j = 0; j < n; j++) acc[j] += av * (int32_t)bp[j];
+      }
+      float *cr = c + i * ldc;
+      const float sa = scales_a[i];
+      for (size_t j = 0; j < n; j++) cr[j] = cr[j] + (float)acc[j] * sa * scales_b[j];
+    }
+  }
+  free(acc);
+  return ORC_OK;
+}
+
+/* qmatmul.zig:106-128 */
+void orc_naive_int8_gemm(size_t m, size_t n, size_t k, const int8_t *a, size_t lda,
+                         const int8_t *b, size_t ldb, float *c, size_t ldc,
+                         const float *scales_a, const float *scales_b) {
+  for (size_t i = 0; i < m; i++)
+    for (size_t j = 0; j < n; j++) {
+      int32_t acc = 0;
+      for (size_t p = 0; p < k; p++) acc += (int32_t)a[i * lda + p] * (int32_t)b[p * ldb + j];
+      c[i * ldc + j] = (float)acc * scales_a[i] * scales_b[j];
+    }
+}
+
+/* ======================================================================
+ * A6 — quantization/primitives/q4_linear.rs:64-100 (from_f32) and
+ *      :106-121 (pack_for_zig): [f16 scale (truncated) | 16 nibble bytes]
+ * ==================================================================== */
+size_t orc_q4_packed_bytes(size_t out_features, size_t in_features) {
+  return out_features * ((in_features + 31) / 32) * 18;
+}
+
+void orc_q4_from_f32_packed(const float *w, size_t out_features, size_t in_features,
+                            uint8_t *packed) {
+  size_t bpr = (in_features + 31) / 32;
+  for (size_t row = 0; row < out_features; row++) {
+    for (size_t b = 0; b < bpr; b++) {
+      float vals[32];
+      for (int i = 0; i < 32; i++) {
+        size_t col = b * 32 + (size_t)i;
+        vals[i] = col < in_features ? w[row * in_features + col] : 0.0f;
+      }
+      float max_abs = 0.0f;
+      for (int i = 0; i < 32; i++) max_abs = fmaxf(max_abs, fabsf(vals[i]));
+      float scale = (max_abs == 0.0f) ? 0.0f : max_abs / 7.0f;
+      float inv = (scale == 0.0f) ? 0.0f : 1.0f / scale;
+      uint8_t *blk = packed + (row * bpr + b) * 18;
+      uint16_t h = orc_f32_to_f16_trunc(scale);
+      blk[0] = (uint8_t)(h & 0xFF);
+      blk[1] = (uint8_t)(h >> 8);
+      for (int i = 0; i < 16; i++) {
+        float r0 = roundf(vals[2 * i] * inv), r1 = roundf(vals[2 * i + 1] * inv);
+        r0 = r0 < -8.0f ? -8.0f : (r0 > 7.0f ? 7.0f : r0);
+        r1 = r1 < -8.0f ? -8.0f : (r1 > 7.0f ? 7.0f : r1);
+        int v0 = (int)r0, v1 = (int)r1;
+        blk[2 + i] = (uint8_t)((uint8_t)(v0 + 8) | (uint8_t)((v1 + 8) << 4));
+      }
+    }
+  }
+}
+
+/* A7 — qmatmul.zig:276-343 via exports.zig:1614-1628 */
+int orc_q4_0_gemv(size_t n, size_t k, const float *a, const uint8_t *b_q4, float *c) {
+  if (!a || !b_q4 || !c) return ORC_ERR_NULL_PTR;
+  if (n == 0 || k == 0) return ORC_OK;
+  if (k % 32 != 0) return ORC_ERR_SHAPE_MISMATCH;
+  const size_t bpr = k / 32, row_bytes = bpr * 18;
+  size_t j = 0;
+  for (; j + 4 <= n; j += 4) { /* 4 rows at a time (:288-319) */
+    float sums[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (size_t blk = 0; blk < bpr; blk++) {
+      const size_t a_off = blk * 32;
+      for (int r = 0; r < 4; r++) {
+        const uint8_t *bs = b_q4 + (j + r) * row_bytes + blk * 18;
+        float scale = orc_f16_to_f32_zig((uint16_t)(bs[0] | (bs[1] << 8)));
+        float block_sum = 0.0f;
+        for (int i = 0; i < 16; i++) {
+          uint8_t byte = bs[2 + i];
+          float lo = (float)((int)(byte & 0x0F) - 8);
+          float hi = (float)((int)(byte >> 4) - 8);
+          block_sum += a[a_off + 2 * i] * lo + a[a_off + 2 * i + 1] * hi;
+        }
+        sums[r] += block_sum * scale;
+      }
+    }
+    for (int r = 0; r < 4; r++) c[j + r] = sums[r];
+  }
+  for (; j < n; j++) { /* scalar tail (:322-342): scale applied per pair */
+    float sum = 0.0f;
+    for (size_t blk = 0; blk < bpr; blk++) {
+      const size_t a_off = blk * 32;
+      const uint8_t *bs = b_q4 + j * row_bytes + blk * 18;
+      float scale = orc_f16_to_f32_zig((uint16_t)(bs[0] | (bs[1] << 8)));
+      for (int i = 0; i < 16; i++) {
+        uint8_t byte = bs[2 + i];
+        float lo = (float)((int)(byte & 0x0F) - 8);
+        float hi = (float)((int)(byte >> 4) - 8);
+        sum += (a[a_off + 2 * i] * lo + a[a_off + 2 * i + 1] * hi) * scale;
+      }
+    }
+    c[j] = sum;
+  }
+  return ORC_OK;
+}
+
+/* ======================================================================
+ * A8..A11 — weight_loading/gguf.rs:255-487 (values via converter.rs)
+ * ==================================================================== */
+static inline uint16_t rd16(const uint8_t *p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* gguf.rs:294-326 */
+int orc_dequant_q4_0(const uint8_t *data, size_t numel, float *out) {
+  if (numel % 32) return ORC_ERR_SHAPE_MISMATCH;
+  for (size_t b = 0; b < numel / 32; b++) {
+    const uint8_t *bs = data + b * 18;
+    float delta = orc_f16_to_f32_rs(rd16(bs));
+    for (int i = 0; i < 16; i++) {
+      uint8_t byte = bs[2 + i];
+      out[b * 32 + 2 * i] = delta * (float)((int)(byte & 0x0F) - 8);
+      out[b * 32 + 2 * i + 1] = delta * (float)((int)((byte >> 4) & 0x0F) - 8);
+    }
+  }
+  return ORC_OK;
+}
+
+/* gguf.rs:255-288 */
+int orc_dequant_q8_0(const uint8_t *data, size_t numel, float *out) {
+  if (numel % 32) return ORC_ERR_SHAPE_MISMATCH;
+  for (size_t b = 0; b < numel / 32; b++) {
+    const uint8_t *bs = data + b * 34;
+    float scale = orc_f16_to_f32_rs(rd16(bs));
+    for (int i = 0; i < 32; i++) out[b * 32 + i] = scale * (float)(int8_t)bs[2 + i];
+  }
+  return ORC_OK;
+}
+
+/* gguf.rs:375-431 — u8 arithmetic exactly as written (6-bit/8-bit fields) */
+int orc_dequant_q4_k(const uint8_t *data, size_t numel, float *out) {
+  if (numel % 256) return ORC_ERR_SHAPE_MISMATCH;
+  for (size_t blk = 0; blk < numel / 256; blk++) {
+    const uint8_t *bs = data + blk * 144;
+    float d = orc_f16_to_f32_rs(rd16(bs));
+    float dmin = orc_f16_to_f32_rs(rd16(bs + 2));
+    const uint8_t *sb = bs + 4;
+    uint8_t sc[8], mn[8];
+    for (int i = 0; i < 4; i++) {
+      sc[i] = (uint8_t)(sb[i] & 0x3F);
+      sc[i + 4] = (uint8_t)((sb[i + 4] & 0x0F) | (uint8_t)((sb[i] >> 6) << 4));
+      mn[i] = (uint8_t)((sb[i + 4] >> 4) | (uint8_t)((sb[i + 8] & 0x0F) << 4));
+      mn[i + 4] = (uint8_t)((sb[i + 8] >> 4) | (uint8_t)(((sb[i] >> 4) & 0x0C) << 4));
+    }
+    const uint8_t *q = bs + 16;
+    float *o = out + blk * 256;
+    for (int s = 0; s < 8; s++) {
+      float scv = d * (float)sc[s];
+      float m = dmin * (float)mn[s];
+      for (int i = 0; i < 16; i++) {
+        uint8_t byte = q[s * 16 + i];
+        o[s * 32 + 2 * i] = (float)(byte & 0x0F) * scv - m;
+        o[s * 32 + 2 * i + 1] = (float)((byte >> 4) & 0x0F) * scv - m;
+      }
+    }
+  }
+  return ORC_OK;
+}
+
+/* gguf.rs:440-487 */
+int orc_dequant_q6_k(const uint8_t *data, size_t numel, float *out) {
+  if (numel % 256) return ORC_ERR_SHAPE_MISMATCH;
+  for (size_t blk = 0; blk < numel / 256; blk++) {
+    const uint8_t *bs = data + blk * 210;
+    const uint8_t *ql = bs, *qh = bs + 128, *sc = bs + 192;
+    float d = orc_f16_to_f32_rs(rd16(bs + 208));
+    float *o = out + blk * 256;
+    for (int sub = 0; sub < 16; sub++) {
+      float scale = (float)(int8_t)sc[sub] * d;
+      for (int i = 0; i < 16; i++) {
+        int idx = sub * 16 + i;
+        uint8_t qlb = ql[idx / 2];
+        uint8_t lo = (idx % 2 == 0) ? (uint8_t)(qlb & 0x0F) : (uint8_t)(qlb >> 4);
+        uint8_t hi = (uint8_t)((qh[idx / 4] >> ((idx % 4) * 2)) & 0x03);
+        float qv = (float)((int)(lo | (hi << 4)) - 32);
+        o[idx] = qv * scale;
+      }
+    }
+  }
+  return ORC_OK;
+}
+
+/* ======================================================================
+ * A12 — zig/src/ops/matmul.zig:125-184 (sgemmTiled), :223-347 (f32GemvRow),
+ *       :454-515 (micro kernels) via exports.zig:725-761
+ * ==================================================================== */
+static void f32_gemv_row(size_t n, size_t k, const float *a, const float *b, size_t ldb,
+                         int trans_b, float *c) {
+  size_t j = 0;
+  if (trans_b) {
+    /* 32-wide and 8-wide column blocks: per column a sequential @mulAdd chain */
+    size_t n32 = n - n % 32;
+    size_t n8 = n32 + (n - n32) / 8 * 8;
+    for (; j < n8; j++) {
+      float acc = 0.0f;
+      const float *br = b + j * ldb;
+      for (size_t p = 0; p < k; p++) acc = fmaf(a[p], br[p], acc);
+      c[j] = acc;
+    }
+    for (; j < n; j++) { /* scalar tail: unfused */
+      float sum = 0.0f;
+      const float *br = b + j * ldb;
+      for (size_t p = 0; p < k; p++) sum += a[p] * br[p];
+      c[j] = sum;
+    }
+  } else {
+    size_t n32 = n - n % 32;
+    for (; j < n32; j++) {
+      float acc = 0.0f;
+      for (size_t p = 0; p < k; p++) acc = fmaf(a[p], b[p * ldb + j], acc);
+      c[j] = acc;
+    }
+    for (; j < n; j++) {
+      float sum = 0.0f;
+      for (size_t p = 0; p < k; p++) sum += a[p] * b[p * ldb + j];
+      c[j] = sum;
+    }
+  }
+}
+
+int orc_sgemm(size_t m, size_t n, size_t k, const float *a, size_t lda, int trans_a,
+              const float *b, size_t ldb, int trans_b, float *c, size_t ldc) {
+  if (!a || !b || !c) return ORC_ERR_NULL_PTR;
+  if (m == 0 || n == 0 || k == 0) return ORC_OK;
+  if (m <= 16 && !trans_a) { /* matmul.zig:142-155: GEMV per row, C overwritten */
+    for (size_t i = 0; i < m; i++) f32_gemv_row(n, k, a + i * lda, b, ldb, trans_b, c + i * ldc);
+    return ORC_OK;
+  }
+  /* GOTO path (:157-183): C accumulates; per element a sequential chain over
+   * p = 0..k-1 starting from C's value — fused (@mulAdd) inside full 8x8
+   * micro-tiles, unfused in edge tiles (rows of a partial MR panel within an
+   * MC=256 block, or columns of a partial NR panel within an NC=4096 block). */
+  for (size_t i = 0; i < m; i++) {
+    size_t ic = i / 256 * 256, mc = (m - ic < 256) ? m - ic : 256;
+    size_t ir = (i - ic) / 8 * 8;
+    int row_full = (mc - ir) >= 8;
+    for (size_t j = 0; j < n; j++) {
+      size_t jc = j / 4096 * 4096, nc = (n - jc < 4096) ? n - jc : 4096;
+      size_t jr = (j - jc) / 8 * 8;
+      int col_full = (nc - jr) >= 8;
+      float acc = c[i * ldc + j];
+      if (row_full && col_full) {
+        for (size_t p = 0; p < k; p++) {
+          float av = trans_a ? a[p * lda + i] : a[i * lda + p];
+          float bv = trans_b ? b[j * ldb + p] : b[p * ldb + j];
+          acc = fmaf(av, bv, acc);
+        }
+      } else {
+        for (size_t p = 0; p < k; p++) {
+          float av = trans_a ? a[p * lda + i] : a[i * lda + p];
+          float bv = trans_b ? b[j * ldb + p] : b[p * ldb + j];
+          acc += av * bv;
+        }
+      }
+      c[i * ldc + j] = acc;
+    }
+  }
+  return ORC_OK;
+}
+
+/* ======================================================================
+ * A14 — per-layer ops
+ * ==================================================================== */
+/* ops/norm.rs:8-38 with syn_vmul (exports.zig:366-375) and syn_vreduce_sum
+ * (vecHsum, exports.zig:503-514: four lane accumulators over i%4, reduced
+ * in lane order, then the tail). */
+void orc_rmsnorm(const float *x, const float *w, float eps, size_t rows, size_t hidden,
+                 float *out) {
+  for (size_t r = 0; r < rows; r++) {
+    const float *xr = x + r * hidden;
+    float *o = out + r * hidden;
+    float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    size_t i = 0;
+    for (; i + 4 <= hidden; i += 4)
+      for (int l = 0; l < 4; l++) acc[l] += xr[i + l] * xr[i + l];
+    float s = ((acc[0] + acc[1]) + acc[2]) + acc[3];
+    for (; i < hidden; i++) s += xr[i] * xr[i];
+    float scale = 1.0f / sqrtf(s / (float)hidden + eps);
+    for (size_t j = 0; j < hidden; j++) {
+      float t = xr[j] * w[j];
+      o[j] = t * scale;
+    }
+  }
+}
+
+/* models/lm/builder.rs:88-133 (no scaling): freq = 1/powf(base, 2i/hd) */
+void orc_rope_tables(size_t max_pos, size_t head_dim, double base, float *cos_t,
+                     float *sin_t) {
+  size_t half = head_dim / 2;
+  float fb = (float)base;
+  for (size_t pos = 0; pos < max_pos; pos++)
+    for (size_t i = 0; i < half; i++) {
+      float freq = 1.0f / powf(fb, 2.0f * (float)i / (float)head_dim);
+      float scaled = freq / 1.0f;
+      float angle = (float)pos * scaled;
+      cos_t[pos * half + i] = cosf(angle);
+      sin_t[pos * half + i] = sinf(angle);
+    }
+}
+
+/* ops/rope.rs:13-60 (RotateHalf) */
+void orc_rope_apply(float *qk, const float *cos_t, const float *sin_t, size_t seq_len,
+                    size_t num_heads, size_t head_dim, size_t pos_offset) {
+  size_t half = head_dim / 2, total = num_heads * head_dim;
+  for (size_t t = 0; t < seq_len; t++) {
+    size_t row = (pos_offset + t) * half;
+    for (size_t h = 0; h < num_heads; h++) {
+      size_t base = t * total + h * head_dim;
+      for (size_t i = 0; i < half; i++) {
+        float cv = cos_t[row + i], sv = sin_t[row + i];
+        float x1 = qk[base + i], x2 = qk[base + half + i];
+        qk[base + i] = x1 * cv - x2 * sv;
+        qk[base + half + i] = x2 * cv + x1 * sv;
+      }
+    }
+  }
+}
+
+/* Rust f32::exp on Linux = glibc expf (used by silu, softmax_slice) */
+float orc_expf(float x) { return expf(x); }
+
+/* ops/activation.rs:30-32 */
+float orc_silu(float x) { return x / (1.0f + expf(-x)); }
+
+/* ops/activation.rs:117-129 */
+void orc_softmax_slice(float *x, size_t n) {
+  float mx = -INFINITY;
+  for (size_t i = 0; i < n; i++) mx = fmaxf(mx, x[i]);
+  float sum = 0.0f;
+  for (size_t i = 0; i < n; i++) {
+    x[i] = expf(x[i] - mx);
+    sum += x[i];
+  }
+  if (sum > 0.0f)
+    for (size_t i = 0; i < n; i++) x[i] /= sum;
+}
+
+/* generation/sampler.rs:217-224 — Iterator::max_by keeps the LAST maximum */
+uint32_t orc_argmax(const float *logits, size_t n) {
+  if (n == 0) return 0;
+  size_t best = 0;
+  for (size_t i = 1; i < n; i++)
+    if (!(logits[i] < logits[best])) best = i;
+  return (uint32_t)best;
+}
+
+/* ops/attention.rs:24-147 (no sliding window): scores, softmax, weighted V.
+ * len >= 64 takes the gather + matmul_t / matmul_nn route (f32GemvRow),
+ * shorter lengths the scalar loops. */
+void orc_attention_decode(const float *q, const float *kcache, const float *vcache,
+                          size_t seq_len, size_t num_heads, size_t num_kv_heads,
+                          size_t head_dim, float *out) {
+  size_t kv_dim = num_kv_heads * head_dim, groups = num_heads / num_kv_heads;
+  float scale = 1.0f / sqrtf((float)head_dim);
+  float *scores = (float *)malloc(seq_len * sizeof(float));
+  if (seq_len >= 64) {
+    float *kb = (float *)malloc(seq_len * head_dim * sizeof(float));
+    float *vb = (float *)malloc(seq_len * head_dim * sizeof(float));
+    for (size_t h = 0; h < num_heads; h++) {
+      size_t kvh = h / groups;
+      for (size_t s = 0; s < seq_len; s++) {
+        memcpy(kb + s * head_dim, kcache + s * kv_dim + kvh * head_dim, head_dim * 4);
+        memcpy(vb + s * head_dim, vcache + s * kv_dim + kvh * head_dim, head_dim * 4);
+      }
+      f32_gemv_row(seq_len, head_dim, q + h * head_dim, kb, head_dim, 1, scores);
+      for (size_t s = 0; s < seq_len; s++) scores[s] *= scale;
+      orc_softmax_slice(scores, seq_len);
+      f32_gemv_row(head_dim, seq_len, scores, vb, head_dim, 0, out + h * head_dim);
+    }
+    free(kb);
+    free(vb);
+  } else {
+    for (size_t h = 0; h < num_heads; h++) {
+      size_t kvh = h / groups;
+      for (size_t s = 0; s < seq_len; s++) {
+        float dot = 0.0f;
+        for (size_t d = 0; d < head_dim; d++)
+          dot += q[h * head_dim + d] * kcache[s * kv_dim + kvh * head_dim + d];
+        scores[s] = dot * scale;
+      }
+      orc_softmax_slice(scores, seq_len);
+      for (size_t d = 0; d < head_dim; d++) {
+        float sum = 0.0f;
+        for (size_t s = 0; s < seq_len; s++)
+          sum += scores[s] * vcache[s * kv_dim + kvh * head_dim + d];
+        out[h * head_dim + d] = sum;
+      }
+    }
+  }
+  free(scores);
+}
+
+/* ffi/exports.zig:1364-1478 — single-head causal attention, TILE_Q=32
+ * (zig/src/ops/attention.zig:25), online max/sum then normalise. */
+int orc_fused_attention(size_t seq_q, size_t seq_k, size_t d_head, const float *q,
+                        const float *k, const float *v, float *out) {
+  if (!q || !k || !v || !out) return ORC_ERR_NULL_PTR;
+  if (seq_q == 0 || seq_k == 0 || d_head == 0) return ORC_OK;
+  const size_t TQ = 32;
+  float *s_tile = (float *)malloc(TQ * seq_k * sizeof(float));
+  if (!s_tile) return ORC_ERR_OUT_OF_MEMORY;
+  float scale = 1.0f / sqrtf((float)d_head);
+  for (size_t tq = 0; tq < seq_q; tq += TQ) {
+    size_t tqs = (seq_q - tq < TQ) ? seq_q - tq : TQ;
+    memset(s_tile, 0, tqs * seq_k * sizeof(float));
+    orc_sgemm(tqs, seq_k, d_head, q + tq * d_head, d_head, 0, k, d_head, 1, s_tile, seq_k);
+    for (size_t i = 0; i < tqs * seq_k; i++) s_tile[i] *= scale;
+    for (size_t i = 0; i < tqs; i++) {
+      size_t ms = tq + i + 1;
+      for (size_t j = ms; j < seq_k; j++) s_tile[i * seq_k + j] = -INFINITY;
+    }
+    for (size_t i = 0; i < tqs; i++) {
+      float *row = s_tile + i * seq_k;
+      float mx = -INFINITY, se = 0.0f;
+      for (size_t j = 0; j < seq_k; j++) {
+        float x = row[j];
+        if (x > mx) {
+          se = se * expf(mx - x) + 1.0f;
+          mx = x;
+        } else {
+          se += expf(x - mx);
+        }
+      }
+      float inv = 1.0f / se;
+      for (size_t j = 0; j < seq_k; j++) row[j] = expf(row[j] - mx) * inv;
+    }
+    for (size_t i = 0; i < tqs; i++) memset(out + (tq + i) * d_head, 0, d_head * sizeof(float));
+    orc_sgemm(tqs, d_head, seq_k, s_tile, seq_k, 0, v, d_head, 0, out + tq * d_head, d_head);
+  }
+  free(s_tile);
+  return ORC_OK;
+}
+
+/* ======================================================================
+ * A15 — quantization/lm/int8.rs:78-709 (quantize_model, QuantizedCausalLM),
+ *       ops/attention.rs:24-247, generation/pipeline.rs:197-278
+ * ==================================================================== */
+typedef struct {
+  int8_t *w; /* [K,N] reference layout */
+  float *s;  /* [N] */
+  size_t n, k;
+} orc_qlin;
+
+struct orc_qlm {
+  orc_lm_cfg c;
+  float *embed; /* [vocab, h] f32 (tied) */
+  orc_qlin *lin; /* per layer: q,k,v,o,gate,up,down */
+  orc_qlin lm_head;
+  float *attn_norm, *ffn_norm, *q_norm, *k_norm, *final_norm; /* gains (1.0) */
+  float *rope_cos, *rope_sin;
+  float *kc, *vc; /* per layer [max_seq, kv_dim] */
+  size_t cur;
+};
+
+static int qlin_from_f32(orc_qlin *q, const float *w, size_t n, size_t k) {
+  q->n = n;
+  q->k = k;
+  q->w = (int8_t *)malloc(n * k);
+  q->s = (float *)malloc(n * sizeof(float));
+  if (!q->w || !q->s) return ORC_ERR_OUT_OF_MEMORY;
+  orc_minmax_scales(w, n, k, q->s);
+  orc_quantize_weights_int8(w, q->s, n, k, q->w);
+  return ORC_OK;
+}
+
+/* QuantizedLinear::forward (int8_linear.rs:87-117): quantize rows, qgemm */
+static void qlin_forward(const orc_qlin *q, const float *x, size_t m, float *y, int8_t *xq,
+                         float *sx) {
+  orc_quantize_per_channel_int8(x, m, q->k, xq, sx);
+  orc_qgemm_int8(m, q->n, q->k, xq, q->k, q->w, q->n, y, q->n, sx, q->s);
+}
+static void qlin_forward_pre(const orc_qlin *q, const int8_t *xq, const float *sx, size_t m,
+                             float *y) {
+  orc_qgemm_int8(m, q->n, q->k, xq, q->k, q->w, q->n, y, q->n, sx, q->s);
+}
+
+orc_qlm *orc_qlm_create(const orc_lm_cfg *cfg) {
+  orc_qlm *m = (orc_qlm *)calloc(1, sizeof(orc_qlm));
+  if (!m) return NULL;
+  m->c = *cfg;
+  size_t h = cfg->hidden, hd = cfg->head_dim, L = cfg->n_layers;
+  size_t kv = cfg->n_kv_heads * hd;
+  m->lin = (orc_qlin *)calloc(L * 7, sizeof(orc_qlin));
+  m->attn_norm = (float *)malloc(h * 4);
+  m->ffn_norm = (float *)malloc(h * 4);
+  m->final_norm = (float *)malloc(h * 4);
+  m->q_norm = (float *)malloc(hd * 4);
+  m->k_norm = (float *)malloc(hd * 4);
+  for (size_t i = 0; i < h; i++) m->attn_norm[i] = m->ffn_norm[i] = m->final_norm[i] = 1.0f;
+  for (size_t i = 0; i < hd; i++) m->q_norm[i] = m->k_norm[i] = 1.0f;
+  m->rope_cos = (float *)malloc(cfg->max_seq * (hd / 2) * 4);
+  m->rope_sin = (float *)malloc(cfg->max_seq * (hd / 2) * 4);
+  orc_rope_tables(cfg->max_seq, hd, cfg->rope_theta, m->rope_cos, m->rope_sin);
+  m->kc = (float *)calloc(L * cfg->max_seq * kv, 4);
+  m->vc = (float *)calloc(L * cfg->max_seq * kv, 4);
+  return m;
+}
+
+void orc_qlm_destroy(orc_qlm *m) {
+  if (!m) return;
+  for (size_t i = 0; i < m->c.n_layers * 7; i++) {
+    free(m->lin[i].w);
+    free(m->lin[i].s);
+  }
+  free(m->lin);
+  free(m->lm_head.w);
+  free(m->lm_head.s);
+  free(m->embed);
+  free(m->attn_norm);
+  free(m->ffn_norm);
+  free(m->final_norm);
+  free(m->q_norm);
+  free(m->k_norm);
+  free(m->rope_cos);
+  free(m->rope_sin);
+  free(m->kc);
+  free(m->vc);
+  free(m);
+}
+
+int orc_qlm_set_embed(orc_qlm *m, const float *embed) {
+  size_t bytes = m->c.vocab * m->c.hidden * sizeof(float);
+  m->embed = (float *)malloc(bytes);
+  if (!m->embed) return ORC_ERR_OUT_OF_MEMORY;
+  memcpy(m->embed, embed, bytes);
+  return ORC_OK;
+}
+
+/* quantize_model per-layer step (int8.rs:85-101) */
+int orc_qlm_set_layer(orc_qlm *m, size_t l, const float *wq, const float *wk, const float *wv,
+                      const float *wo, const float *wg, const float *wu, const float *wd) {
+  const orc_lm_cfg *c = &m->c;
+  size_t h = c->hidden, qd = c->n_heads * c->head_dim, kvd = c->n_kv_heads * c->head_dim;
+  orc_qlin *L = m->lin + l * 7;
+  int rc = 0;
+  rc |= qlin_from_f32(&L[0], wq, qd, h);
+  rc |= qlin_from_f32(&L[1], wk, kvd, h);
+  rc |= qlin_from_f32(&L[2], wv, kvd, h);
+  rc |= qlin_from_f32(&L[3], wo, h, qd);
+  rc |= qlin_from_f32(&L[4], wg, c->inter, h);
+  rc |= qlin_from_f32(&L[5], wu, c->inter, h);
+  rc |= qlin_from_f32(&L[6], wd, h, c->inter);
+  return rc ? ORC_ERR_OUT_OF_MEMORY : ORC_OK;
+}
+
+/* Pair p of a normal stream uses draws 2p, 2p+1: a chunk starting at even
+ * element e starts from state seed + e*gamma, so chunks fill in parallel. */
+static void fill_normal_par(float *dst, size_t n, uint64_t seed, float stddev) {
+  const size_t chunk = (size_t)1 << 20; /* even */
+  long nch = (long)((n + chunk - 1) / chunk);
+#pragma omp parallel for schedule(dynamic)
+  for (long c = 0; c < nch; c++) {
+    size_t b = (size_t)c * chunk, e = b + chunk < n ? b + chunk : n;
+    orc_fill_normal(dst + b, e - b, seed + (uint64_t)b * 0x9E3779B97F4A7C15ULL, stddev);
+  }
+}
+
+/* Synthetic weights: tensor id 0 = embed, 1 + 8*l + {0..6} = q,k,v,o,gate,up,down */
+int orc_qlm_init_synthetic(orc_qlm *m, uint64_t seed_base, float stddev) {
+  const orc_lm_cfg *c = &m->c;
+  size_t h = c->hidden, qd = c->n_heads * c->head_dim, kvd = c->n_kv_heads * c->head_dim;
+  m->embed = (float *)malloc(c->vocab * h * sizeof(float));
+  if (!m->embed) return ORC_ERR_OUT_OF_MEMORY;
+  fill_normal_par(m->embed, c->vocab * h, seed_base + 0, stddev);
+  const size_t rows[7] = {qd, kvd, kvd, h, c->inter, c->inter, h};
+  const size_t cols[7] = {h, h, h, qd, h, h, c->inter};
+  int bad = 0;
+  long total = (long)(c->n_layers * 7);
+#pragma omp parallel for schedule(dynamic) reduction(| : bad)
+  for (long idx = 0; idx < total; idx++) {
+    size_t l = (size_t)idx / 7;
+    int t = (int)(idx % 7);
+    float *tmp = (float *)malloc(rows[t] * cols[t] * sizeof(float));
+    if (!tmp) { bad |= 1; continue; }
+    orc_fill_normal(tmp, rows[t] * cols[t], seed_base + 1 + 8 * l + (uint64_t)t, stddev);
+    bad |= qlin_from_f32(&m->lin[l * 7 + t], tmp, rows[t], cols[t]) != ORC_OK;
+    free(tmp);
+  }
+  return bad ? ORC_ERR_OUT_OF_MEMORY : ORC_OK;
+}
+
+/* tied lm_head quantized from embed_tokens (int8.rs:127-139) */
+int orc_qlm_finalize(orc_qlm *m) {
+  if (!m->embed) return ORC_ERR_NULL_PTR;
+  return qlin_from_f32(&m->lm_head, m->embed, m->c.vocab, m->c.hidden);
+}
+
+void orc_qlm_reset(orc_qlm *m) { m->cur = 0; }
+size_t orc_qlm_cur_len(const orc_qlm *m) { return m->cur; }
+const int8_t *orc_qlm_lm_head_weights(const orc_qlm *m) { return m->lm_head.w; }
+const float *orc_qlm_lm_head_scales(const orc_qlm *m) { return m->lm_head.s; }
+
+static void embed_rows(const orc_qlm *m, const uint32_t *ids, size_t n, float *x) {
+  size_t h = m->c.hidden;
+  for (size_t t = 0; t < n; t++) {
+    if (ids[t] < m->c.vocab)
+      memcpy(x + t * h, m->embed + (size_t)ids[t] * h, h * 4);
+    else
+      memset(x + t * h, 0, h * 4);
+  }
+}
+
+/* FFN sub-layer, SwiGLU (int8.rs:480-505) */
+static void ffn_swiglu(const orc_qlm *m, const orc_qlin *L, const float *x, size_t t, float *out,
+                       int8_t *xq, float *sx, float *g, float *u) {
+  size_t inter = m->c.inter;
+  orc_quantize_per_channel_int8(x, t, m->c.hidden, xq, sx);
+  qlin_forward_pre(&L[4], xq, sx, t, g);
+  qlin_forward_pre(&L[5], xq, sx, t, u);
+  for (size_t i = 0; i < t * inter; i++) g[i] = orc_silu(g[i]) * u[i];
+  qlin_forward(&L[6], g, t, out, xq, sx);
+}
+
+/* Decoder layer, prefill (int8.rs:194-216, 379-426) or decode (int8.rs:242-282, 429-478).
+ * prefill==1: t tokens at positions 0..t-1 (cache assumed empty);
+ * prefill==0: one token at position m->cur. */
+static void layer_forward(orc_qlm *m, size_t l, float *x, size_t t, int prefill) {
+  const orc_lm_cfg *c = &m->c;
+  size_t h = c->hidden, hd = c->head_dim, nh = c->n_heads, nkv = c->n_kv_heads;
+  size_t qd = nh * hd, kvd = nkv * hd, inter = c->inter;
+  const orc_qlin *L = m->lin + l * 7;
+  size_t big = (inter > qd ? inter : qd);
+  if (big < h) big = h;
+  float *normed = (float *)malloc(t * h * 4);
+  int8_t *xq = (int8_t *)malloc(t * big);
+  float *sx = (float *)malloc(t * 4);
+  float *q = (float *)malloc(t * qd * 4), *k = (float *)malloc(t * kvd * 4);
+  float *v = (float *)malloc(t * kvd * 4), *attn = (float *)malloc(t * qd * 4);
+  float *o = (float *)malloc(t * h * 4);
+  float *g = (float *)malloc(t * inter * 4), *u = (float *)malloc(t * inter * 4);
+  float *kcl = m->kc + l * c->max_seq * kvd, *vcl = m->vc + l * c->max_seq * kvd;
+
+  orc_rmsnorm(x, m->attn_norm, c->eps, t, h, normed);
+  orc_quantize_per_channel_int8(normed, t, h, xq, sx);
+  qlin_forward_pre(&L[0], xq, sx, t, q);
+  qlin_forward_pre(&L[1], xq, sx, t, k);
+  qlin_forward_pre(&L[2], xq, sx, t, v);
+  /* headwise q/k RMSNorm (norm.rs:78-93), RoPE, cache append */
+  orc_rmsnorm(q, m->q_norm, c->eps, t * nh, hd, q);
+  orc_rmsnorm(k, m->k_norm, c->eps, t * nkv, hd, k);
+  size_t pos0 = prefill ? 0 : m->cur;
+  orc_rope_apply(q, m->rope_cos, m->rope_sin, t, nh, hd, pos0);
+  orc_rope_apply(k, m->rope_cos, m->rope_sin, t, nkv, hd, pos0);
+  memcpy(kcl + pos0 * kvd, k, t * kvd * 4);
+  memcpy(vcl + pos0 * kvd, v, t * kvd * 4);
+  if (prefill) {
+    size_t groups = nh / nkv;
+    float *qh = (float *)malloc(t * hd * 4), *kh = (float *)malloc(t * hd * 4);
+    float *vh = (float *)malloc(t * hd * 4), *oh = (float *)malloc(t * hd * 4);
+    for (size_t head = 0; head < nh; head++) {
+      size_t kvh = head / groups;
+      for (size_t s = 0; s < t; s++) {
+        memcpy(qh + s * hd, q + s * qd + head * hd, hd * 4);
+        memcpy(kh + s * hd, k + s * kvd + kvh * hd, hd * 4);
+        memcpy(vh + s * hd, v + s * kvd + kvh * hd, hd * 4);
+      }
+      orc_fused_attention(t, t, hd, qh, kh, vh, oh);
+      for (size_t s = 0; s < t; s++) memcpy(attn + s * qd + head * hd, oh + s * hd, hd * 4);
+    }
+    free(qh);
+    free(kh);
+    free(vh);
+    free(oh);
+  } else {
+    orc_attention_decode(q, kcl, vcl, pos0 + 1, nh, nkv, hd, attn);
+  }
+  qlin_forward(&L[3], attn, t, o, xq, sx);
+  for (size_t i = 0; i < t * h; i++) x[i] = x[i] + o[i];
+  orc_rmsnorm(x, m->ffn_norm, c->eps, t, h, normed);
+  ffn_swiglu(m, L, normed, t, o, xq, sx, g, u);
+  for (size_t i = 0; i < t * h; i++) x[i] += o[i];
+  free(normed); free(xq); free(sx); free(q); free(k); free(v);
+  free(attn); free(o); free(g); free(u);
+}
+
+static void lm_head_logits(orc_qlm *m, const float *xlast, float *logits) {
+  size_t h = m->c.hidden;
+  float *normed = (float *)malloc(h * 4);
+  int8_t *xq = (int8_t *)malloc(h);
+  float sx;
+  orc_rmsnorm(xlast, m->final_norm, m->c.eps, 1, h, normed);
+  qlin_forward(&m->lm_head, normed, 1, logits, xq, &sx);
+  free(normed);
+  free(xq);
+}
+
+/* QuantizedCausalLM::forward_prefill (int8.rs:593-635) */
+int orc_qlm_prefill(orc_qlm *m, const uint32_t *ids, size_t n, float *logits) {
+  if (n == 0 || n > m->c.max_seq) return ORC_ERR_INVALID_ARG;
+  size_t h = m->c.hidden;
+  float *x = (float *)malloc(n * h * 4);
+  embed_rows(m, ids, n, x);
+  m->cur = 0;
+  for (size_t l = 0; l < m->c.n_layers; l++) layer_forward(m, l, x, n, 1);
+  m->cur = n;
+  lm_head_logits(m, x + (n - 1) * h, logits);
+  free(x);
+  return ORC_OK;
+}
+
+/* QuantizedCausalLM::forward_one (int8.rs:638-709) */
+int orc_qlm_forward_one(orc_qlm *m, uint32_t token, float *logits) {
+  if (m->cur >= m->c.max_seq) return ORC_ERR_INVALID_ARG;
+  size_t h = m->c.hidden;
+  float *x = (float *)malloc(h * 4);
+  embed_rows(m, &token, 1, x);
+  for (size_t l = 0; l < m->c.n_layers; l++) layer_forward(m, l, x, 1, 0);
+  m->cur += 1;
+  lm_head_logits(m, x, logits);
+  free(x);
+  return ORC_OK;
+}
+
+/* generate_cached greedy loop (pipeline.rs:197-278, stopping.rs:39-42):
+ * max_new tokens from one prefill + (max_new-1) forward_one calls.
+ * margins[i] = top1 - top2 logit at step i (NULL to skip). */
+static float top2_margin(const float *lg, size_t n, uint32_t best) {
+  float second = -INFINITY;
+  for (size_t i = 0; i < n; i++)
+    if (i != best && lg[i] > second) second = lg[i];
+  return lg[best] - second;
+}
+
+int orc_qlm_generate(orc_qlm *m, const uint32_t *prompt, size_t n_prompt, size_t max_new,
+                     uint32_t *out_tokens, float *margins) {
+  if (max_new == 0) return ORC_OK;
+  float *logits = (float *)malloc(m->c.vocab * 4);
+  int rc = orc_qlm_prefill(m, prompt, n_prompt, logits);
+  if (rc) { free(logits); return rc; }
+  uint32_t tok = orc_argmax(logits, m->c.vocab);
+  out_tokens[0] = tok;
+  if (margins) margins[0] = top2_margin(logits, m->c.vocab, tok);
+  for (size_t i = 1; i < max_new; i++) {
+    rc = orc_qlm_forward_one(m, tok, logits);
+    if (rc) break;
+    tok = orc_argmax(logits, m->c.vocab);
+    out_tokens[i] = tok;
+    if (margins) margins[i] = top2_margin(logits, m->c.vocab, tok);
+  }
+  free(logits);
+  return rc;
+}

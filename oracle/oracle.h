@@ -1,0 +1,119 @@
+/*
+ * CPU oracle for the quantized-linear hot path — TEST INFRASTRUCTURE ONLY.
+ *
+ * A plain-C restatement of the reference algorithms (eren23/synapse, Zig
+ * cpu_simd kernels + the Rust glue around them).  Every function cites the
+ * reference file:line it follows (paths relative to the reference's
+ * `synapse/` directory).  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the
+ * checker / the timed CPU baseline — never as part of the product path.
+ *
+ * Build: gcc -O3 -mavx2 -mfma -mf16c -ffp-contract=off -fno-fast-math
+ *        (-ffp-contract=off keeps every `a*b + c` the reference writes
+ *        unfused; explicit fmaf() calls stand for Zig's @mulAdd).
+ */
+#ifndef SYN_ORACLE_H
+#define SYN_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes: synapse.h:27-35 */
+#define ORC_OK 0
+#define ORC_ERR_NULL_PTR 1
+#define ORC_ERR_INVALID_ARG 2
+#define ORC_ERR_OUT_OF_MEMORY 3
+#define ORC_ERR_SHAPE_MISMATCH 4
+
+/* ---- harness input spec (not a reference algorithm) ---- */
+void orc_fill_normal(float *dst, size_t n, uint64_t seed, float stddev);
+void orc_fill_token_ids(uint32_t *dst, size_t n, uint64_t seed, uint32_t vocab);
+
+/* ---- f16 conversions ---- */
+uint16_t orc_f32_to_f16_trunc(float v);   /* q4_linear.rs:9-33 */
+float orc_f16_to_f32_zig(uint16_t bits);  /* qmatmul.zig:346-371 */
+float orc_f16_to_f32_rs(uint16_t bits);   /* weight_loading/converter.rs:12-40 */
+
+/* ---- A1: activation quantizer ---- */
+int orc_quantize_per_channel_int8(const float *data, size_t channels, size_t channel_size,
+                                  int8_t *out, float *scales);
+
+/* ---- A2: weight quantizer (QuantizedLinear::from_f32) ---- */
+void orc_minmax_scales(const float *w, size_t channels, size_t channel_size, float *scales);
+void orc_quantize_weights_int8(const float *w, const float *scales, size_t out_features,
+                               size_t in_features, int8_t *out_kn);
+
+/* ---- A3/A4: INT8 GEMM (int8GemmTiled) ---- */
+int orc_qgemm_int8(size_t m, size_t n, size_t k, const int8_t *a, size_t lda, const int8_t *b,
+                   size_t ldb, float *c, size_t ldc, const float *scales_a,
+                   const float *scales_b);
+void orc_naive_int8_gemm(size_t m, size_t n, size_t k, const int8_t *a, size_t lda,
+                         const int8_t *b, size_t ldb, float *c, size_t ldc,
+                         const float *scales_a, const float *scales_b);
+
+/* ---- A6/A7: Q4_0 ---- */
+size_t orc_q4_packed_bytes(size_t out_features, size_t in_features);
+void orc_q4_from_f32_packed(const float *w, size_t out_features, size_t in_features,
+                            uint8_t *packed);
+int orc_q4_0_gemv(size_t n, size_t k, const float *a, const uint8_t *b_q4, float *c);
+
+/* ---- A8..A11: GGUF dequantizers ---- */
+int orc_dequant_q4_0(const uint8_t *data, size_t numel, float *out);
+int orc_dequant_q8_0(const uint8_t *data, size_t numel, float *out);
+int orc_dequant_q4_k(const uint8_t *data, size_t numel, float *out);
+int orc_dequant_q6_k(const uint8_t *data, size_t numel, float *out);
+
+/* ---- A12: f32 SGEMM (sgemmTiled semantics) ---- */
+int orc_sgemm(size_t m, size_t n, size_t k, const float *a, size_t lda, int trans_a,
+              const float *b, size_t ldb, int trans_b, float *c, size_t ldc);
+
+/* ---- A14: per-layer ops ---- */
+void orc_rmsnorm(const float *x, const float *w, float eps, size_t rows, size_t hidden,
+                 float *out);
+void orc_rope_tables(size_t max_pos, size_t head_dim, double base, float *cos_t,
+                     float *sin_t);
+void orc_rope_apply(float *qk, const float *cos_t, const float *sin_t, size_t seq_len,
+                    size_t num_heads, size_t head_dim, size_t pos_offset);
+float orc_expf(float x);
+float orc_silu(float x);
+void orc_softmax_slice(float *x, size_t n);
+uint32_t orc_argmax(const float *logits, size_t n);
+void orc_attention_decode(const float *q, const float *kcache, const float *vcache,
+                          size_t seq_len, size_t num_heads, size_t num_kv_heads,
+                          size_t head_dim, float *out);
+int orc_fused_attention(size_t seq_q, size_t seq_k, size_t d_head, const float *q,
+                        const float *k, const float *v, float *out);
+
+/* ---- A15: INT8 W8A8 causal LM (QuantizedCausalLM) ---- */
+typedef struct {
+  size_t hidden, n_layers, n_heads, n_kv_heads, head_dim, inter, vocab, max_seq;
+  float eps;
+  double rope_theta;
+} orc_lm_cfg;
+
+typedef struct orc_qlm orc_qlm;
+orc_qlm *orc_qlm_create(const orc_lm_cfg *cfg);
+void orc_qlm_destroy(orc_qlm *m);
+int orc_qlm_set_embed(orc_qlm *m, const float *embed);
+int orc_qlm_set_layer(orc_qlm *m, size_t layer, const float *wq, const float *wk,
+                      const float *wv, const float *wo, const float *wg, const float *wu,
+                      const float *wd);
+int orc_qlm_init_synthetic(orc_qlm *m, uint64_t seed_base, float stddev);
+int orc_qlm_finalize(orc_qlm *m);
+void orc_qlm_reset(orc_qlm *m);
+size_t orc_qlm_cur_len(const orc_qlm *m);
+int orc_qlm_prefill(orc_qlm *m, const uint32_t *ids, size_t n, float *logits);
+int orc_qlm_forward_one(orc_qlm *m, uint32_t token, float *logits);
+int orc_qlm_generate(orc_qlm *m, const uint32_t *prompt, size_t n_prompt, size_t max_new,
+                     uint32_t *out_tokens, float *margins);
+const int8_t *orc_qlm_lm_head_weights(const orc_qlm *m); /* [K,N] reference layout */
+const float *orc_qlm_lm_head_scales(const orc_qlm *m);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

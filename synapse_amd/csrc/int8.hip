@@ -1,0 +1,473 @@
+// INT8 W8A8 path: activation quantizer (A1), weight quantizer at load (A2),
+// decode GEMV (A3) and the KC-chunked prefill form (A4).
+//
+// Reference semantics (zig/src/ops/qmatmul.zig):
+//   M <= 16 : C[i,j] = (f32(sum_k a[i,k] b[k,j]) * sa[i]) * sb[j]   (:54-66, :171-256)
+//   M  > 16 : C[i,j] = sum over KC=512 chunks, in order, of
+//             (f32(chunk i32 sum) * sa[i]) * sb[j]                   (:68-99, :515-525)
+// Integer sums are exact in any order, so the GPU splits K freely inside a
+// chunk; only the f32 epilogue order is fixed.
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+#include "linear.hpp"
+
+namespace syn {
+
+// --------------------------------------------------------------- quantizer
+// one workgroup per row; max|x| is order-free, the rest is elementwise
+__global__ void __launch_bounds__(256) k_quantize_rows(const float *__restrict__ x, int K,
+                                                       int ldx, int8_t *__restrict__ q, int ldq,
+                                                       float *__restrict__ scales) {
+  __shared__ float red[256];
+  const int row = blockIdx.x;
+  const float *xr = x + (size_t)row * ldx;
+  int8_t *qr = q + (size_t)row * ldq;
+  float mx = 0.0f;
+  for (int j = threadIdx.x; j < K; j += 256) {
+    const float a = fabsf(xr[j]);
+    if (a > mx) mx = a;
+  }
+  red[threadIdx.x] = mx;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
+    __syncthreads();
+  }
+  const float max_abs = red[0];
+  if (max_abs == 0.0f) {
+    for (int j = threadIdx.x; j < K; j += 256) qr[j] = 0;
+    if (threadIdx.x == 0) scales[row] = 1.0f;
+    return;
+  }
+  const float inv = 127.0f / max_abs;
+  for (int j = threadIdx.x; j < K; j += 256) {
+    float r = roundf(xr[j] * inv);
+    r = fminf(127.0f, fmaxf(-127.0f, r));
+    qr[j] = (int8_t)(int)r;
+  }
+  if (threadIdx.x == 0) scales[row] = max_abs / 127.0f;
+}
+
+syn_status_t launch_quantize_rows(const float *d_x, size_t m, size_t k, size_t ldx, int8_t *d_q,
+                                  size_t ldq, float *d_s, hipStream_t s) {
+  if (m == 0 || k == 0) return SYN_OK;
+  hipLaunchKernelGGL(k_quantize_rows, dim3((unsigned)m), dim3(256), 0, s, d_x, (int)k, (int)ldx,
+                     d_q, (int)ldq, d_s);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
+
+// --------------------------------------------------------------- GEMV
+// grid (panels, ksplit); blockDim = 64 * waves.  Lane = output row of the
+// panel; each wave walks 16-byte K chunks (one 1 KiB load per chunk) and does
+// 4 v_dot4_i32_i8 per activation row.  Waves reduce in LDS (i32, exact).
+template <int M>
+__global__ void __launch_bounds__(1024)
+    k_gemv_w8a8(const i32x4 *__restrict__ W, const float *__restrict__ ws,
+                const int8_t *__restrict__ xq, int ldx, const float *__restrict__ sx,
+                float *__restrict__ y, int ldy, int *__restrict__ part, int N, int C, int cs) {
+  extern __shared__ int red[];  // [waves][M][64]
+  const int panel = blockIdx.x, ks = blockIdx.y;
+  const int nw = blockDim.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int c0 = ks * cs;
+  const int c1 = min(C, c0 + cs);
+  const i32x4 *Wp = W + (size_t)panel * C * 64 + lane;
+  int acc[M];
+#pragma unroll
+  for (int m = 0; m < M; m++) acc[m] = 0;
+
+  int c = c0 + wave;
+  for (; c + 3 * nw < c1; c += 4 * nw) {
+    i32x4 w[4];
+#pragma unroll
+    for (int u = 0; u < 4; u++) w[u] = __builtin_nontemporal_load(Wp + (size_t)(c + u * nw) * 64);
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+#pragma unroll
+      for (int m = 0; m < M; m++) {
+        const i32x4 xv =
+            *reinterpret_cast<const i32x4 *>(xq + (size_t)m * ldx + (size_t)(c + u * nw) * 16);
+        acc[m] = __builtin_amdgcn_sdot4(w[u].x, xv.x, acc[m], false);
+        acc[m] = __builtin_amdgcn_sdot4(w[u].y, xv.y, acc[m], false);
+        acc[m] = __builtin_amdgcn_sdot4(w[u].z, xv.z, acc[m], false);
+        acc[m] = __builtin_amdgcn_sdot4(w[u].w, xv.w, acc[m], false);
+      }
+    }
+  }
+  for (; c < c1; c += nw) {
+    const i32x4 w = __builtin_nontemporal_load(Wp + (size_t)c * 64);
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+      const i32x4 xv = *reinterpret_cast<const i32x4 *>(xq + (size_t)m * ldx + (size_t)c * 16);
+      acc[m] = __builtin_amdgcn_sdot4(w.x, xv.x, acc[m], false);
+      acc[m] = __builtin_amdgcn_sdot4(w.y, xv.y, acc[m], false);
+      acc[m] = __builtin_amdgcn_sdot4(w.z, xv.z, acc[m], false);
+      acc[m] = __builtin_amdgcn_sdot4(w.w, xv.w, acc[m], false);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; m++) red[(wave * M + m) * 64 + lane] = acc[m];
+  __syncthreads();
+  const int N64 = gridDim.x * 64;
+  for (int t = threadIdx.x; t < M * 64; t += blockDim.x) {
+    const int m = t >> 6, r = t & 63;
+    int s = 0;
+    for (int w = 0; w < nw; w++) s += red[(w * M + m) * 64 + r];
+    const int row = panel * 64 + r;
+    if (gridDim.y == 1) {
+      if (row < N) {
+        const float f = (float)s * sx[m];
+        y[(size_t)m * ldy + row] = f * ws[row];
+      }
+    } else {
+      part[((size_t)ks * M + m) * N64 + row] = s;
+    }
+  }
+}
+
+// Second stage of a K split.  chunked==0: exact i32 total, then the GEMV
+// epilogue.  chunked==1: slices are the reference's KC=512 chunks and the
+// f32 epilogue is accumulated slice by slice in order (qmatmul.zig:515-525).
+__global__ void __launch_bounds__(256)
+    k_gemv_reduce(const int *__restrict__ part, int ksplit, int M, int N, int N64,
+                  const float *__restrict__ sx, const float *__restrict__ ws,
+                  float *__restrict__ y, int ldy, int chunked) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= M * N) return;
+  const int m = idx / N, row = idx - m * N;
+  if (!chunked) {
+    int s = 0;
+    for (int k = 0; k < ksplit; k++) s += part[((size_t)k * M + m) * N64 + row];
+    const float f = (float)s * sx[m];
+    y[(size_t)m * ldy + row] = f * ws[row];
+  } else {
+    float c = 0.0f;
+    for (int k = 0; k < ksplit; k++) {
+      const float f = (float)part[((size_t)k * M + m) * N64 + row] * sx[m];
+      const float t = f * ws[row];
+      c = c + t;
+    }
+    y[(size_t)m * ldy + row] = c;
+  }
+}
+
+GemvPlan make_gemv_plan(size_t n, size_t k_chunks, bool chunked_kc) {
+  GemvPlan p;
+  p.panels = (int)cdiv(n, kPanelRows);
+  p.chunks = (int)k_chunks;
+  if (chunked_kc) {
+    p.cs = 32;  // KC = 512 bytes = 32 chunks
+    p.ksplit = (int)cdiv(k_chunks, 32);
+  } else {
+    int ks = 1;
+    if (p.panels < 240) {
+      ks = (int)cdiv(256, p.panels);
+      ks = std::min<int>(ks, (int)std::max<size_t>(1, k_chunks / 4));
+    }
+    p.cs = (int)cdiv(k_chunks, ks);
+    p.ksplit = (int)cdiv(k_chunks, p.cs);
+  }
+  p.waves = std::min(16, std::max(1, p.cs));
+  return p;
+}
+
+template <int M>
+static void launch_gemv_m(const GemvPlan &p, const i32x4 *W, const float *ws, const int8_t *xq,
+                          int ldx, const float *sx, float *y, int ldy, int *part, int N,
+                          hipStream_t s) {
+  const int waves = std::min(p.waves, M >= 8 ? 8 : 16);
+  const size_t shm = (size_t)waves * M * 64 * sizeof(int);
+  hipLaunchKernelGGL(k_gemv_w8a8<M>, dim3(p.panels, p.ksplit), dim3(64 * waves), shm, s, W, ws,
+                     xq, ldx, sx, y, ldy, part, N, p.chunks, p.cs);
+}
+
+typedef void (*gemv_launcher)(const GemvPlan &, const i32x4 *, const float *, const int8_t *, int,
+                              const float *, float *, int, int *, int, hipStream_t);
+static const gemv_launcher kGemvLaunch[17] = {
+    nullptr,          launch_gemv_m<1>,  launch_gemv_m<2>,  launch_gemv_m<3>,
+    launch_gemv_m<4>, launch_gemv_m<5>,  launch_gemv_m<6>,  launch_gemv_m<7>,
+    launch_gemv_m<8>, launch_gemv_m<9>,  launch_gemv_m<10>, launch_gemv_m<11>,
+    launch_gemv_m<12>, launch_gemv_m<13>, launch_gemv_m<14>, launch_gemv_m<15>,
+    launch_gemv_m<16>};
+
+syn_status_t QLinearInt8::ensure_part(size_t elems) {
+  if (part_elems >= elems) return SYN_OK;
+  SYN_TRY(part.alloc(elems * sizeof(int)));
+  part_elems = elems;
+  return SYN_OK;
+}
+
+syn_status_t QLinearInt8::prepare(size_t max_m) {
+  const size_t mb = std::min<size_t>(16, std::max<size_t>(1, max_m));
+  const GemvPlan p = make_gemv_plan(n, (size_t)chunks, false);
+  size_t need = p.ksplit > 1 ? (size_t)p.ksplit * mb * p.panels * 64 : 0;
+  if (max_m > 16 && chunks > 32) {
+    const GemvPlan pc = make_gemv_plan(n, (size_t)chunks, true);
+    need = std::max(need, (size_t)pc.ksplit * 16 * pc.panels * 64);
+  }
+  return need ? ensure_part(need) : SYN_OK;
+}
+
+syn_status_t QLinearInt8::gemv(size_t m, const int8_t *d_xq, size_t ldx, const float *d_sx,
+                               float *d_y, size_t ldy, hipStream_t s) {
+  if (m == 0 || n == 0 || k == 0) return SYN_OK;
+  const bool chunked = m > 16;  // qmatmul.zig:61-68
+  const GemvPlan p = make_gemv_plan(n, (size_t)chunks, chunked && chunks > 32);
+  const size_t N64 = (size_t)p.panels * 64;
+  for (size_t m0 = 0; m0 < m; m0 += 16) {
+    const int mb = (int)std::min<size_t>(16, m - m0);
+    if (p.ksplit > 1) SYN_TRY(ensure_part((size_t)p.ksplit * mb * N64));
+    kGemvLaunch[mb](p, w.as<i32x4>(), scales.as<float>(), d_xq + m0 * ldx, (int)ldx, d_sx + m0,
+                    d_y + m0 * ldy, (int)ldy, part.as<int>(), (int)n, s);
+    SYN_LAUNCH_CHECK();
+    if (p.ksplit > 1) {
+      const int total = mb * (int)n;
+      hipLaunchKernelGGL(k_gemv_reduce, dim3(cdiv(total, 256)), dim3(256), 0, s,
+                         part.as<int>(), p.ksplit, mb, (int)n, (int)N64, d_sx + m0,
+                         scales.as<float>(), d_y + m0 * ldy, (int)ldy, chunked ? 1 : 0);
+      SYN_LAUNCH_CHECK();
+    }
+  }
+  return SYN_OK;
+}
+
+// --------------------------------------------------------------- load time
+// calibration.rs:11-24
+void host_minmax_scales(const float *w, size_t ch, size_t chsz, float *scales) {
+  for (size_t c = 0; c < ch; c++) {
+    float mx = 0.0f;
+    const float *r = w + c * chsz;
+    for (size_t j = 0; j < chsz; j++) mx = std::fmax(mx, std::fabs(r[j]));
+    scales[c] = (mx == 0.0f) ? 1.0f : mx / 127.0f;
+  }
+}
+
+// int8_linear.rs:42-61 (kept in [N,K]; the reference then transposes to [K,N])
+void host_quantize_weights_nk(const float *w, const float *scales, size_t n, size_t k,
+                              int8_t *out) {
+  for (size_t c = 0; c < n; c++) {
+    const float s = scales[c];
+    if (s == 0.0f) {
+      std::memset(out + c * k, 0, k);
+      continue;
+    }
+    const float inv = 1.0f / s;
+    for (size_t j = 0; j < k; j++) {
+      float v = std::round(w[c * k + j] * inv);
+      v = std::min(127.0f, std::max(-128.0f, v));
+      out[c * k + j] = (int8_t)v;
+    }
+  }
+}
+
+template <class Get>
+static syn_status_t upload_panels(QLinearInt8 &L, const float *host_scales, size_t n, size_t k,
+                                  Get get) {
+  L.n = n;
+  L.k = k;
+  L.chunks = (int)cdiv(k, 16);
+  const size_t P = cdiv(n, 64), C = (size_t)L.chunks;
+  std::vector<int8_t> buf(P * C * 64 * 16, 0);
+  for (size_t row = 0; row < n; row++) {
+    const size_t p = row / 64, r = row % 64;
+    for (size_t kk = 0; kk < k; kk++)
+      buf[((p * C + kk / 16) * 64 + r) * 16 + kk % 16] = get(row, kk);
+  }
+  std::vector<float> sc(P * 64, 0.0f);
+  std::memcpy(sc.data(), host_scales, n * sizeof(float));
+  SYN_TRY(L.w.alloc(buf.size()));
+  SYN_TRY(L.scales.alloc(sc.size() * sizeof(float)));
+  SYN_HIP(hipMemcpy(L.w.p, buf.data(), buf.size(), hipMemcpyHostToDevice));
+  SYN_HIP(hipMemcpy(L.scales.p, sc.data(), sc.size() * sizeof(float), hipMemcpyHostToDevice));
+  return SYN_OK;
+}
+
+syn_status_t QLinearInt8::upload_nk(const int8_t *h, const float *hs, size_t n_, size_t k_) {
+  return upload_panels(*this, hs, n_, k_, [&](size_t r, size_t kk) { return h[r * k_ + kk]; });
+}
+
+syn_status_t QLinearInt8::upload_kn(const int8_t *h, size_t ldb, const float *hs, size_t n_,
+                                    size_t k_) {
+  return upload_panels(*this, hs, n_, k_, [&](size_t r, size_t kk) { return h[kk * ldb + r]; });
+}
+
+syn_status_t QLinearInt8::from_f32(const float *w_nk, size_t n_, size_t k_) {
+  std::vector<float> sc(n_);
+  std::vector<int8_t> q(n_ * k_);
+  host_minmax_scales(w_nk, n_, k_, sc.data());
+  host_quantize_weights_nk(w_nk, sc.data(), n_, k_, q.data());
+  return upload_nk(q.data(), sc.data(), n_, k_);
+}
+
+}  // namespace syn
+
+// =================================================================== C ABI
+using namespace syn;
+
+struct syn_hip_qlinear_s {
+  int fmt = 0;
+  QLinearInt8 i8;
+  QLinearQ4_0 q4;
+};
+
+extern "C" {
+
+syn_status_t syn_hip_quantize_rows(const float *d_x, size_t m, size_t k, size_t ldx, int8_t *d_q,
+                                   size_t ldq, float *d_scales, void *stream) {
+  if (!d_x || !d_q || !d_scales) return SYN_ERR_NULL_PTR;
+  if (m == 0 || k == 0) return SYN_ERR_INVALID_ARG;  // exports.zig:1284
+  if (ldx < k || ldq < k) return SYN_ERR_SHAPE_MISMATCH;
+  SYN_TRY(ensure_init());
+  return launch_quantize_rows(d_x, m, k, ldx, d_q, ldq, d_scales, pick_stream(stream));
+}
+
+syn_status_t syn_hip_qlinear_create(int fmt, size_t n, size_t k, const void *host_weights,
+                                    const float *host_scales, int layout,
+                                    syn_hip_qlinear_t **out) {
+  if (!out || !host_weights) return SYN_ERR_NULL_PTR;
+  if (n == 0 || k == 0) return SYN_ERR_INVALID_ARG;
+  SYN_TRY(ensure_init());
+  auto *h = new syn_hip_qlinear_s();
+  h->fmt = fmt;
+  syn_status_t st = SYN_OK;
+  if (fmt == SYN_HIP_FMT_INT8) {
+    if (!host_scales) st = SYN_ERR_NULL_PTR;
+    else if (layout == SYN_HIP_LAYOUT_KN)
+      st = h->i8.upload_kn((const int8_t *)host_weights, n, host_scales, n, k);
+    else if (layout == SYN_HIP_LAYOUT_NK)
+      st = h->i8.upload_nk((const int8_t *)host_weights, host_scales, n, k);
+    else
+      st = SYN_ERR_INVALID_ARG;
+  } else if (fmt == SYN_HIP_FMT_Q4_0) {
+    st = (k % 32) ? SYN_ERR_SHAPE_MISMATCH : h->q4.upload_packed((const uint8_t *)host_weights, n, k);
+  } else {
+    st = SYN_ERR_INVALID_ARG;
+  }
+  if (st != SYN_OK) {
+    delete h;
+    return st;
+  }
+  *out = h;
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_qlinear_from_f32(int fmt, size_t n, size_t k, const float *host_w,
+                                      syn_hip_qlinear_t **out) {
+  if (!out || !host_w) return SYN_ERR_NULL_PTR;
+  if (n == 0 || k == 0) return SYN_ERR_INVALID_ARG;
+  SYN_TRY(ensure_init());
+  auto *h = new syn_hip_qlinear_s();
+  h->fmt = fmt;
+  syn_status_t st;
+  if (fmt == SYN_HIP_FMT_INT8) st = h->i8.from_f32(host_w, n, k);
+  else if (fmt == SYN_HIP_FMT_Q4_0) st = (k % 32) ? SYN_ERR_SHAPE_MISMATCH : h->q4.from_f32(host_w, n, k);
+  else st = SYN_ERR_INVALID_ARG;
+  if (st != SYN_OK) {
+    delete h;
+    return st;
+  }
+  *out = h;
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_qlinear_forward_pre_quantized(syn_hip_qlinear_t *h, size_t m,
+                                                   const int8_t *d_xq, size_t ldxq,
+                                                   const float *d_sx, float *d_y, void *stream) {
+  if (!h) return SYN_ERR_NULL_PTR;
+  if (h->fmt != SYN_HIP_FMT_INT8) return SYN_ERR_INVALID_ARG;
+  if (m == 0) return SYN_OK;
+  if (!d_xq || !d_sx || !d_y) return SYN_ERR_NULL_PTR;
+  // the kernel reads activation rows in whole 16-byte chunks
+  if (ldxq % 16 || ldxq < (size_t)h->i8.chunks * 16) return SYN_ERR_SHAPE_MISMATCH;
+  return h->i8.gemv(m, d_xq, ldxq, d_sx, d_y, h->i8.n, pick_stream(stream));
+}
+
+syn_status_t syn_hip_qlinear_forward(syn_hip_qlinear_t *h, size_t m, const float *d_x,
+                                     float *d_y, void *stream) {
+  if (!h) return SYN_ERR_NULL_PTR;
+  if (m == 0) return SYN_OK;
+  if (!d_x || !d_y) return SYN_ERR_NULL_PTR;
+  hipStream_t s = pick_stream(stream);
+  if (h->fmt == SYN_HIP_FMT_Q4_0) return h->q4.gemv(m, d_x, h->q4.k, d_y, h->q4.n, s);
+  if (h->fmt != SYN_HIP_FMT_INT8) return SYN_ERR_INVALID_ARG;
+  QLinearInt8 &L = h->i8;
+  const size_t ldq = (size_t)L.chunks * 16;
+  if (L.xq_rows < m) {
+    SYN_TRY(L.xq.alloc(m * ldq));
+    SYN_TRY(L.sx.alloc(m * sizeof(float)));
+    SYN_HIP(hipMemsetAsync(L.xq.p, 0, m * ldq, s));
+    L.xq_rows = m;
+  }
+  SYN_TRY(launch_quantize_rows(d_x, m, L.k, L.k, L.xq.as<int8_t>(), ldq, L.sx.as<float>(), s));
+  return L.gemv(m, L.xq.as<int8_t>(), ldq, L.sx.as<float>(), d_y, L.n, s);
+}
+
+syn_status_t syn_hip_qlinear_info(const syn_hip_qlinear_t *h, size_t *n, size_t *k, int *fmt,
+                                  size_t *weight_bytes) {
+  if (!h) return SYN_ERR_NULL_PTR;
+  const bool i8 = h->fmt == SYN_HIP_FMT_INT8;
+  if (n) *n = i8 ? h->i8.n : h->q4.n;
+  if (k) *k = i8 ? h->i8.k : h->q4.k;
+  if (fmt) *fmt = h->fmt;
+  if (weight_bytes) *weight_bytes = i8 ? h->i8.weight_bytes() : h->q4.weight_bytes();
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_qlinear_destroy(syn_hip_qlinear_t *h) {
+  delete h;
+  return SYN_OK;
+}
+
+// ---- reference-signature entry points (host pointers) ----
+syn_status_t syn_quantize_per_channel_int8(const float *data, size_t channels,
+                                           size_t channel_size, int8_t *out, float *scales) {
+  if (!data || !out || !scales) return SYN_ERR_NULL_PTR;
+  if (channels == 0 || channel_size == 0) return SYN_ERR_INVALID_ARG;
+  SYN_TRY(ensure_init());
+  hipStream_t s = default_stream();
+  DevBuf dx, dq, ds;
+  const size_t n = channels * channel_size;
+  SYN_TRY(dx.alloc(n * 4));
+  SYN_TRY(dq.alloc(n));
+  SYN_TRY(ds.alloc(channels * 4));
+  SYN_HIP(hipMemcpyAsync(dx.p, data, n * 4, hipMemcpyHostToDevice, s));
+  SYN_TRY(launch_quantize_rows(dx.as<float>(), channels, channel_size, channel_size,
+                               dq.as<int8_t>(), channel_size, ds.as<float>(), s));
+  SYN_HIP(hipMemcpyAsync(out, dq.p, n, hipMemcpyDeviceToHost, s));
+  SYN_HIP(hipMemcpyAsync(scales, ds.p, channels * 4, hipMemcpyDeviceToHost, s));
+  SYN_HIP(hipStreamSynchronize(s));
+  return SYN_OK;
+}
+
+syn_status_t syn_qgemm_int8(size_t m, size_t n, size_t k, const int8_t *a, size_t lda,
+                            const int8_t *b, size_t ldb, float *c, size_t ldc,
+                            const float *scales_a, const float *scales_b) {
+  if (!a || !b || !c || !scales_a || !scales_b) return SYN_ERR_NULL_PTR;
+  if (m == 0 || n == 0 || k == 0) return SYN_OK;  // exports.zig:1331
+  if (lda < k || ldb < n || ldc < n) return SYN_ERR_SHAPE_MISMATCH;
+  SYN_TRY(ensure_init());
+  hipStream_t s = default_stream();
+  QLinearInt8 L;
+  SYN_TRY(L.upload_kn(b, ldb, scales_b, n, k));
+  const size_t ldq = (size_t)L.chunks * 16;
+  std::vector<int8_t> ha(m * ldq, 0);
+  for (size_t i = 0; i < m; i++) std::memcpy(ha.data() + i * ldq, a + i * lda, k);
+  DevBuf dq, dsa, dc;
+  SYN_TRY(dq.alloc(ha.size()));
+  SYN_TRY(dsa.alloc(m * 4));
+  SYN_TRY(dc.alloc(m * n * 4));
+  SYN_HIP(hipMemcpyAsync(dq.p, ha.data(), ha.size(), hipMemcpyHostToDevice, s));
+  SYN_HIP(hipMemcpyAsync(dsa.p, scales_a, m * 4, hipMemcpyHostToDevice, s));
+  SYN_TRY(L.gemv(m, dq.as<int8_t>(), ldq, dsa.as<float>(), dc.as<float>(), n, s));
+  std::vector<float> hc(m * n);
+  SYN_HIP(hipMemcpyAsync(hc.data(), dc.p, m * n * 4, hipMemcpyDeviceToHost, s));
+  SYN_HIP(hipStreamSynchronize(s));
+  for (size_t i = 0; i < m; i++) std::memcpy(c + i * ldc, hc.data() + i * n, n * 4);
+  return SYN_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,526 @@
+// Decoder-layer kernels around the quantized GEMVs.  They are small and
+// latency-bound; what matters is that each reproduces the reference's float
+// operation order exactly (compiled with -ffp-contract=off; explicit
+// __builtin_fmaf only where the reference uses @mulAdd), so the token stream
+// matches the cpu_simd path bit for bit.
+#include "layer_ops.hpp"
+
+namespace syn {
+
+// ------------------------------------------------------------------ embed
+__global__ void k_embed(const float *__restrict__ embed, const uint32_t *__restrict__ ids,
+                        int hidden, int vocab, float *__restrict__ x) {
+  const int r = blockIdx.x;
+  const uint32_t id = ids[r];
+  float *xr = x + (size_t)r * hidden;
+  if (id < (uint32_t)vocab) {
+    const float *src = embed + (size_t)id * hidden;
+    for (int j = threadIdx.x; j < hidden; j += blockDim.x) xr[j] = src[j];
+  } else {
+    for (int j = threadIdx.x; j < hidden; j += blockDim.x) xr[j] = 0.0f;
+  }
+}
+
+syn_status_t launch_embed(const float *embed, const uint32_t *ids, int rows, int hidden,
+                          int vocab, float *x, hipStream_t s) {
+  hipLaunchKernelGGL(k_embed, dim3(rows), dim3(256), 0, s, embed, ids, hidden, vocab, x);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
+
+// ------------------------------------------------------------------ residual
+__global__ void k_add(float *__restrict__ x, const float *__restrict__ d, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] = x[i] + d[i];
+}
+
+syn_status_t launch_add(float *x, const float *d, int n, hipStream_t s) {
+  hipLaunchKernelGGL(k_add, dim3((n + 255) / 256), dim3(256), 0, s, x, d, n);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
+
+// Sum of squares in the order of syn_vmul + syn_vreduce_sum
+// (exports.zig:366-375, 503-514): lane accumulators acc[i%4] over the
+// 4-aligned prefix, reduced as ((a0+a1)+a2)+a3, then the tail.  v is in LDS;
+// must be called by all threads of the block (uses red[0..3] and a barrier).
+__device__ float sumsq_vec4_order(const float *v, int n, float *red) {
+  const int n4 = n & ~3;
+  if (threadIdx.x < 4) {
+    float acc = 0.0f;
+    for (int i = threadIdx.x; i < n4; i += 4) {
+      const float t = v[i] * v[i];
+      acc = acc + t;
+    }
+    red[threadIdx.x] = acc;
+  }
+  __syncthreads();
+  float s = ((red[0] + red[1]) + red[2]) + red[3];
+  for (int i = n4; i < n; i++) {
+    const float t = v[i] * v[i];
+    s = s + t;
+  }
+  return s;
+}
+
+// block-wide max of non-negative values (exact in any order)
+__device__ float block_max(float v, float *red) {
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) red[w] = v;
+  __syncthreads();
+  float m = red[0];
+  for (int i = 1; i < nw; i++) m = fmaxf(m, red[i]);
+  return m;
+}
+
+// quantize a row held in LDS (quantize.zig:12-47); all threads participate
+__device__ void quantize_row_lds(const float *v, int n, int8_t *q, float *scale_out, float *red) {
+  float mx = 0.0f;
+  for (int j = threadIdx.x; j < n; j += blockDim.x) {
+    const float a = fabsf(v[j]);
+    if (a > mx) mx = a;
+  }
+  mx = block_max(mx, red);
+  if (mx == 0.0f) {
+    for (int j = threadIdx.x; j < n; j += blockDim.x) q[j] = 0;
+    if (threadIdx.x == 0) *scale_out = 1.0f;
+    return;
+  }
+  const float inv = 127.0f / mx;
+  for (int j = threadIdx.x; j < n; j += blockDim.x) {
+    float r = roundf(v[j] * inv);
+    r = fminf(127.0f, fmaxf(-127.0f, r));
+    q[j] = (int8_t)(int)r;
+  }
+  if (threadIdx.x == 0) *scale_out = mx / 127.0f;
+}
+
+// ------------------------------------------------------------------ RMSNorm + quantize
+// ops/norm.rs:8-38: out = (x*w) * (1/sqrt(sumsq/n + eps)); then A1 on out.
+__global__ void __launch_bounds__(256)
+    k_rmsnorm_quant(float *__restrict__ x, const float *__restrict__ delta,
+                    const float *__restrict__ w, float eps, int H, int8_t *__restrict__ xq,
+                    int ldq, float *__restrict__ sx, float *__restrict__ normed) {
+  extern __shared__ float sm[];  // H
+  __shared__ float red[64];
+  __shared__ float s_scale;
+  const int row = blockIdx.x;
+  float *xr = x + (size_t)row * H;
+  for (int j = threadIdx.x; j < H; j += blockDim.x) {
+    float v = xr[j];
+    if (delta) {
+      v = v + delta[(size_t)row * H + j];
+      xr[j] = v;
+    }
+    sm[j] = v;
+  }
+  __syncthreads();
+  const float ss = sumsq_vec4_order(sm, H, red);
+  if (threadIdx.x == 0) s_scale = 1.0f / sqrtf(ss / (float)H + eps);
+  __syncthreads();
+  const float scale = s_scale;
+  for (int j = threadIdx.x; j < H; j += blockDim.x) {
+    const float t = sm[j] * w[j];
+    const float nv = t * scale;
+    sm[j] = nv;
+    if (normed) normed[(size_t)row * H + j] = nv;
+  }
+  __syncthreads();
+  quantize_row_lds(sm, H, xq + (size_t)row * ldq, sx + row, red);
+}
+
+syn_status_t launch_rmsnorm_quant(float *x, const float *delta, const float *w, float eps,
+                                  int rows, int hidden, int8_t *xq, int ldq, float *sx,
+                                  float *normed, hipStream_t s) {
+  hipLaunchKernelGGL(k_rmsnorm_quant, dim3(rows), dim3(256), hidden * sizeof(float), s, x, delta,
+                     w, eps, hidden, xq, ldq, sx, normed);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
+
+// ------------------------------------------------------------------ q/k norm, RoPE, KV append
+// ops/attention.rs:46-66: headwise RMSNorm (norm.rs:78-93), rotate-half RoPE
+// (rope.rs:13-43) at the token's position, append RoPE'd K and raw V.
+// grid (n_heads + 2*n_kv, rows), one wave per head.
+__global__ void __launch_bounds__(64)
+    k_qk_norm_rope_kv(const float *__restrict__ qkv, int ldqkv, int nh, int nkv, int hd,
+                      const float *__restrict__ qn, const float *__restrict__ kn, float eps,
+                      const float *__restrict__ cosT, const float *__restrict__ sinT,
+                      const int *__restrict__ d_pos, int pos_static, float *__restrict__ q_out,
+                      float *__restrict__ kc, float *__restrict__ vc) {
+  extern __shared__ float v[];  // hd
+  __shared__ float red[8];
+  __shared__ float s_scale;
+  const int hh = blockIdx.x, r = blockIdx.y;
+  const int pos = (d_pos ? d_pos[0] : pos_static) + r;
+  const int qd = nh * hd, kvd = nkv * hd, half = hd / 2;
+  const float *row = qkv + (size_t)r * ldqkv;
+  if (hh >= nh + nkv) {  // V head: raw copy into the cache
+    const int vh = hh - nh - nkv;
+    for (int d = threadIdx.x; d < hd; d += 64)
+      vc[(size_t)pos * kvd + vh * hd + d] = row[qd + kvd + vh * hd + d];
+    return;
+  }
+  const bool is_q = hh < nh;
+  const float *src = is_q ? row + hh * hd : row + qd + (hh - nh) * hd;
+  const float *wn = is_q ? qn : kn;
+  for (int d = threadIdx.x; d < hd; d += 64) v[d] = src[d];
+  __syncthreads();
+  if (wn) {
+    const float ss = sumsq_vec4_order(v, hd, red);
+    if (threadIdx.x == 0) s_scale = 1.0f / sqrtf(ss / (float)hd + eps);
+    __syncthreads();
+    const float scale = s_scale;
+    for (int d = threadIdx.x; d < hd; d += 64) {
+      const float t = v[d] * wn[d];
+      v[d] = t * scale;
+    }
+    __syncthreads();
+  }
+  const float *cr = cosT + (size_t)pos * half, *sr = sinT + (size_t)pos * half;
+  float *dst = is_q ? q_out + (size_t)r * qd + hh * hd : kc + (size_t)pos * kvd + (hh - nh) * hd;
+  for (int i = threadIdx.x; i < half; i += 64) {
+    const float c = cr[i], sn = sr[i];
+    const float x1 = v[i], x2 = v[half + i];
+    const float a = x1 * c, b = x2 * sn;
+    const float e = x2 * c, f = x1 * sn;
+    dst[i] = a - b;
+    dst[half + i] = e + f;
+  }
+}
+
+syn_status_t launch_qk_norm_rope_kv(const float *qkv, int ldqkv, int rows, int n_heads,
+                                    int n_kv, int head_dim, const float *q_norm,
+                                    const float *k_norm, float eps, const float *rope_cos,
+                                    const float *rope_sin, const int *d_pos, int pos_static,
+                                    float *q_out, float *kcache, float *vcache, hipStream_t s) {
+  hipLaunchKernelGGL(k_qk_norm_rope_kv, dim3(n_heads + 2 * n_kv, rows), dim3(64),
+                     head_dim * sizeof(float), s, qkv, ldqkv, n_heads, n_kv, head_dim, q_norm,
+                     k_norm, eps, rope_cos, rope_sin, d_pos, pos_static, q_out, kcache, vcache);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
+
+// ------------------------------------------------------------------ decode attention
+// ops/attention.rs:24-147 without a window.  len >= 64 follows the
+// gather + matmul_t / matmul_nn route, whose f32GemvRow (matmul.zig:223-347)
+// uses @mulAdd chains for the 32/8-wide column blocks and plain a*b+c in the
+// scalar tail; len < 64 follows the scalar loops (plain a*b+c).
+__global__ void __launch_bounds__(256)
+    k_attn_decode(const float *__restrict__ q, const float *__restrict__ kc,
+                  const float *__restrict__ vc, const int *__restrict__ d_pos, int nh, int nkv,
+                  int hd, float *__restrict__ scores, int max_seq, float *__restrict__ out) {
+  extern __shared__ float qs[];  // hd
+  __shared__ float red[64];
+  __shared__ float s_sum;
+  const int head = blockIdx.x;
+  const int kvh = head / (nh / nkv);
+  const int len = d_pos[0] + 1;
+  const int kvd = nkv * hd;
+  const bool simd = len >= 64;
+  float *e = scores + (size_t)head * max_seq;
+  for (int d = threadIdx.x; d < hd; d += blockDim.x) qs[d] = q[head * hd + d];
+  __syncthreads();
+  const float scale = 1.0f / sqrtf((float)hd);
+  const int n32 = len - len % 32;
+  const int n8 = n32 + ((len - n32) / 8) * 8;
+  float mx = -__builtin_inff();
+  for (int sidx = threadIdx.x; sidx < len; sidx += blockDim.x) {
+    const float *kr = kc + (size_t)sidx * kvd + kvh * hd;
+    float acc = 0.0f;
+    if (simd && sidx < n8) {
+      for (int d = 0; d < hd; d++) acc = __builtin_fmaf(qs[d], kr[d], acc);
+    } else {
+      for (int d = 0; d < hd; d++) {
+        const float t = qs[d] * kr[d];
+        acc = acc + t;
+      }
+    }
+    const float sc = acc * scale;
+    e[sidx] = sc;
+    mx = fmaxf(mx, sc);
+  }
+  // softmax_slice (activation.rs:117-129)
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = red[0];
+  for (int i = 1; i < (int)(blockDim.x >> 6); i++) mx = fmaxf(mx, red[i]);
+  for (int sidx = threadIdx.x; sidx < len; sidx += blockDim.x) e[sidx] = syn_expf(e[sidx] - mx);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float sum = 0.0f;
+    for (int i = 0; i < len; i++) sum = sum + e[i];
+    s_sum = sum;
+  }
+  __syncthreads();
+  const float sum = s_sum;
+  if (sum > 0.0f)
+    for (int sidx = threadIdx.x; sidx < len; sidx += blockDim.x) e[sidx] = e[sidx] / sum;
+  __syncthreads();
+  const int d32 = hd - hd % 32;
+  for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+    const float *vcol = vc + kvh * hd + d;
+    float acc = 0.0f;
+    if (simd && d < d32) {
+      for (int i = 0; i < len; i++) acc = __builtin_fmaf(e[i], vcol[(size_t)i * kvd], acc);
+    } else {
+      for (int i = 0; i < len; i++) {
+        const float t = e[i] * vcol[(size_t)i * kvd];
+        acc = acc + t;
+      }
+    }
+    out[head * hd + d] = acc;
+  }
+}
+
+syn_status_t launch_attention_decode(const float *q, const float *kcache, const float *vcache,
+                                     const int *d_pos, int n_heads, int n_kv, int head_dim,
+                                     float *scores, int max_seq, float *out, hipStream_t s) {
+  hipLaunchKernelGGL(k_attn_decode, dim3(n_heads), dim3(256), head_dim * sizeof(float), s, q,
+                     kcache, vcache, d_pos, n_heads, n_kv, head_dim, scores, max_seq, out);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
+
+// ------------------------------------------------------------------ prefill attention
+// syn_fused_attention per head (exports.zig:1364-1478): Q tiles of 32 rows;
+// S = Q K^T and O = P V through sgemmTiled, whose element order is a
+// sequential chain over k — @mulAdd inside full 8x8 micro-tiles (or in the
+// f32GemvRow 32/8-wide blocks when a tile has <= 16 rows), plain a*b+c
+// elsewhere — then scale, causal mask, online max/sum, normalise.
+// grid (n_heads, t): one workgroup per (head, query row).
+__device__ __forceinline__ bool sgemm_fused(int tqs, int il, int ncols, int j, bool gemv_trans_b) {
+  if (tqs <= 16) {  // f32GemvRow per row (matmul.zig:142-155)
+    const int n32 = ncols - ncols % 32;
+    if (gemv_trans_b) {
+      const int n8 = n32 + ((ncols - n32) / 8) * 8;
+      return j < n8;
+    }
+    return j < n32;
+  }
+  // GOTO path: MC=256 > 32 rows, NC=4096
+  const bool row_full = (tqs - (il / 8) * 8) >= 8;
+  const int jc = (j / 4096) * 4096;
+  const int nc = min(4096, ncols - jc);
+  const bool col_full = (nc - ((j - jc) / 8) * 8) >= 8;
+  return row_full && col_full;
+}
+
+__global__ void __launch_bounds__(256)
+    k_attn_prefill(const float *__restrict__ q, const float *__restrict__ kc,
+                   const float *__restrict__ vc, int t, int nh, int nkv, int hd,
+                   float *__restrict__ out) {
+  extern __shared__ float sm[];  // qs[hd] | e[t]
+  float *qs = sm, *e = sm + hd;
+  __shared__ float s_mx, s_inv;
+  const int head = blockIdx.x, i = blockIdx.y;
+  const int kvh = head / (nh / nkv);
+  const int qd = nh * hd, kvd = nkv * hd;
+  const int tq = (i / 32) * 32, tqs = min(32, t - tq), il = i - tq;
+  for (int d = threadIdx.x; d < hd; d += blockDim.x) qs[d] = q[(size_t)i * qd + head * hd + d];
+  __syncthreads();
+  const float scale = 1.0f / sqrtf((float)hd);
+  for (int j = threadIdx.x; j < t; j += blockDim.x) {
+    const float *kr = kc + (size_t)j * kvd + kvh * hd;
+    float acc = 0.0f;
+    if (sgemm_fused(tqs, il, t, j, true)) {
+      for (int d = 0; d < hd; d++) acc = __builtin_fmaf(qs[d], kr[d], acc);
+    } else {
+      for (int d = 0; d < hd; d++) {
+        const float p = qs[d] * kr[d];
+        acc = acc + p;
+      }
+    }
+    float sc = acc * scale;
+    if (j > i) sc = -__builtin_inff();
+    e[j] = sc;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float mx = -__builtin_inff(), se = 0.0f;
+    for (int j = 0; j < t; j++) {
+      const float x = e[j];
+      if (x > mx) {
+        const float p = se * syn_expf(mx - x);
+        se = p + 1.0f;
+        mx = x;
+      } else {
+        se = se + syn_expf(x - mx);
+      }
+    }
+    s_mx = mx;
+    s_inv = 1.0f / se;
+  }
+  __syncthreads();
+  const float mx = s_mx, inv = s_inv;
+  for (int j = threadIdx.x; j < t; j += blockDim.x) e[j] = syn_expf(e[j] - mx) * inv;
+  __syncthreads();
+  for (int d = threadIdx.x; d < hd; d += blockDim.x) {
+    const float *vcol = vc + kvh * hd + d;
+    float acc = 0.0f;
+    if (sgemm_fused(tqs, il, hd, d, false)) {
+      for (int p = 0; p < t; p++) acc = __builtin_fmaf(e[p], vcol[(size_t)p * kvd], acc);
+    } else {
+      for (int p = 0; p < t; p++) {
+        const float m = e[p] * vcol[(size_t)p * kvd];
+        acc = acc + m;
+      }
+    }
+    out[(size_t)i * qd + head * hd + d] = acc;
+  }
+}
+
+syn_status_t launch_attention_prefill(const float *q, const float *kcache, const float *vcache,
+                                      int t, int n_heads, int n_kv, int head_dim,
+                                      float *scores, float *out, hipStream_t s) {
+  (void)scores;
+  const size_t shm = (size_t)(head_dim + t) * sizeof(float);
+  if (shm > 64 * 1024) {
+    set_error("prefill attention: prompt too long for one workgroup's LDS row");
+    return SYN_ERR_INVALID_ARG;
+  }
+  hipLaunchKernelGGL(k_attn_prefill, dim3(n_heads, t), dim3(256), shm, s, q, kcache, vcache, t,
+                     n_heads, n_kv, head_dim, out);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
+
+// ------------------------------------------------------------------ SwiGLU + quantize
+__global__ void __launch_bounds__(256)
+    k_swiglu_quant(const float *__restrict__ gu, int ldgu, int inter, int8_t *__restrict__ hq,
+                   int ldq, float *__restrict__ sh) {
+  extern __shared__ float sm[];  // inter
+  __shared__ float red[64];
+  const int row = blockIdx.x;
+  const float *g = gu + (size_t)row * ldgu, *u = g + inter;
+  for (int j = threadIdx.x; j < inter; j += blockDim.x) {
+    const float a = syn_silu(g[j]);
+    sm[j] = a * u[j];
+  }
+  __syncthreads();
+  quantize_row_lds(sm, inter, hq + (size_t)row * ldq, sh + row, red);
+}
+
+syn_status_t launch_swiglu_quant(const float *gu, int ldgu, int rows, int inter, int8_t *hq,
+                                 int ldq, float *sh, hipStream_t s) {
+  hipLaunchKernelGGL(k_swiglu_quant, dim3(rows), dim3(256), inter * sizeof(float), s, gu, ldgu,
+                     inter, hq, ldq, sh);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
+
+// ------------------------------------------------------------------ argmax
+struct Top2 {
+  float v1;
+  int i1;
+  float v2;
+};
+
+__device__ __forceinline__ Top2 top2_merge(Top2 a, Top2 b) {
+  // winner: larger value; on equal values the larger index (last max)
+  const bool bw = (b.v1 > a.v1) || (b.v1 == a.v1 && b.i1 > a.i1);
+  const Top2 w = bw ? b : a, l = bw ? a : b;
+  Top2 r;
+  r.v1 = w.v1;
+  r.i1 = w.i1;
+  r.v2 = fmaxf(w.v2, l.v1);
+  return r;
+}
+
+__device__ Top2 block_top2(Top2 t, float *sv1, int *si1, float *sv2) {
+  for (int o = 32; o > 0; o >>= 1) {
+    Top2 u;
+    u.v1 = __shfl_xor(t.v1, o);
+    u.i1 = __shfl_xor(t.i1, o);
+    u.v2 = __shfl_xor(t.v2, o);
+    t = top2_merge(t, u);
+  }
+  const int w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    sv1[w] = t.v1;
+    si1[w] = t.i1;
+    sv2[w] = t.v2;
+  }
+  __syncthreads();
+  Top2 r{sv1[0], si1[0], sv2[0]};
+  for (int i = 1; i < nw; i++) r = top2_merge(r, Top2{sv1[i], si1[i], sv2[i]});
+  return r;
+}
+
+__global__ void __launch_bounds__(256)
+    k_argmax_stage1(const float *__restrict__ x, int n, float *pv, int *pi, float *pv2) {
+  __shared__ float sv1[4], sv2[4];
+  __shared__ int si1[4];
+  Top2 t{-__builtin_inff(), -1, -__builtin_inff()};
+  for (int i = blockIdx.x * 256 + threadIdx.x; i < n; i += gridDim.x * 256)
+    t = top2_merge(t, Top2{x[i], i, -__builtin_inff()});
+  t = block_top2(t, sv1, si1, sv2);
+  if (threadIdx.x == 0) {
+    pv[blockIdx.x] = t.v1;
+    pi[blockIdx.x] = t.i1;
+    pv2[blockIdx.x] = t.v2;
+  }
+}
+
+__global__ void __launch_bounds__(256)
+    k_argmax_stage2(const float *pv, const int *pi, const float *pv2, int np, StepState *st,
+                    uint32_t *history, float *mhist) {
+  __shared__ float sv1[4], sv2[4];
+  __shared__ int si1[4];
+  Top2 t{-__builtin_inff(), -1, -__builtin_inff()};
+  for (int i = threadIdx.x; i < np; i += 256) t = top2_merge(t, Top2{pv[i], pi[i], pv2[i]});
+  t = block_top2(t, sv1, si1, sv2);
+  if (threadIdx.x == 0) {
+    const uint32_t tok = t.i1 < 0 ? 0u : (uint32_t)t.i1;
+    st->token = tok;
+    st->margin = t.v1 - t.v2;
+    if (history) history[st->step] = tok;
+    if (mhist) mhist[st->step] = t.v1 - t.v2;
+  }
+}
+
+syn_status_t launch_argmax(const float *logits, int n, float *part_v, int *part_i,
+                           float *part_v2, StepState *state, uint32_t *history,
+                           float *margin_hist, hipStream_t s) {
+  const int blocks = 256;
+  hipLaunchKernelGGL(k_argmax_stage1, dim3(blocks), dim3(256), 0, s, logits, n, part_v, part_i,
+                     part_v2);
+  SYN_LAUNCH_CHECK();
+  hipLaunchKernelGGL(k_argmax_stage2, dim3(1), dim3(256), 0, s, part_v, part_i, part_v2, blocks,
+                     state, history, margin_hist);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
+
+__global__ void k_step_advance(StepState *st, int add_pos) {
+  if (threadIdx.x == 0) {
+    st->pos += add_pos;
+    st->step += 1;
+  }
+}
+
+syn_status_t launch_step_advance(StepState *state, int add_pos, hipStream_t s) {
+  hipLaunchKernelGGL(k_step_advance, dim3(1), dim3(64), 0, s, state, add_pos);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
+
+}  // namespace syn
+
+__global__ void k_eval_expf(const float *__restrict__ x, float *__restrict__ y, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) y[i] = syn_expf(x[i]);
+}
+
+extern "C" syn_status_t syn_hip_eval_expf(const float *d_x, float *d_y, size_t n, void *stream) {
+  if (n == 0) return SYN_OK;
+  if (!d_x || !d_y) return SYN_ERR_NULL_PTR;
+  SYN_TRY(syn::ensure_init());
+  hipLaunchKernelGGL(k_eval_expf, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     syn::pick_stream(stream), d_x, d_y, n);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}

@@ -1,0 +1,53 @@
+// Small device-resident kernels of the decoder layer.  Each one computes in
+// the reference's floating-point order so that the whole decode step is
+// bit-identical to the cpu_simd path.
+#pragma once
+
+#include "common.hpp"
+
+namespace syn {
+
+struct StepState {  // device-resident decode state (read by kernels in a graph)
+  int pos;          // tokens already in the KV cache
+  uint32_t token;   // last sampled token
+  int step;         // decode steps taken since the last reset of the counter
+  float margin;     // top1 - top2 logit of the last argmax
+};
+
+// x[r] = embed[ids[r]] (zero row for ids >= vocab), ids on device
+syn_status_t launch_embed(const float *embed, const uint32_t *ids, int rows, int hidden,
+                          int vocab, float *x, hipStream_t s);
+// per row: x += delta (if delta); normed = rmsnorm(x, w, eps); quantize(normed)
+syn_status_t launch_rmsnorm_quant(float *x, const float *delta, const float *w, float eps,
+                                  int rows, int hidden, int8_t *xq, int ldq, float *sx,
+                                  float *normed, hipStream_t s);
+// headwise q/k RMSNorm + RoPE (rotate-half) + KV-cache append for `rows` tokens
+// at positions pos0 + r (pos0 = *d_pos if d_pos else pos_static).
+syn_status_t launch_qk_norm_rope_kv(const float *qkv, int ldqkv, int rows, int n_heads,
+                                    int n_kv, int head_dim, const float *q_norm,
+                                    const float *k_norm, float eps, const float *rope_cos,
+                                    const float *rope_sin, const int *d_pos, int pos_static,
+                                    float *q_out, float *kcache, float *vcache, hipStream_t s);
+// single-query GQA attention over positions [0, *d_pos] (cache already holds
+// the new token), ops/attention.rs:24-147
+syn_status_t launch_attention_decode(const float *q, const float *kcache, const float *vcache,
+                                     const int *d_pos, int n_heads, int n_kv, int head_dim,
+                                     float *scores, int max_seq, float *out, hipStream_t s);
+// causal attention over `t` prompt tokens, exports.zig:1364-1478 per head
+syn_status_t launch_attention_prefill(const float *q, const float *kcache, const float *vcache,
+                                      int t, int n_heads, int n_kv, int head_dim,
+                                      float *scores, float *out, hipStream_t s);
+// h = silu(gate) * up (int8.rs:500-503), then quantize rows of h
+syn_status_t launch_swiglu_quant(const float *gu, int ldgu, int rows, int inter, int8_t *hq,
+                                 int ldq, float *sh, hipStream_t s);
+// greedy argmax (last maximum wins, sampler.rs:217-224) -> state->token,
+// top1-top2 margin -> state->margin, token also stored to history[state->step]
+syn_status_t launch_argmax(const float *logits, int n, float *part_v, int *part_i,
+                           float *part_v2, StepState *state, uint32_t *history,
+                           float *margin_hist, hipStream_t s);
+// state->pos += add_pos; state->step += 1
+syn_status_t launch_step_advance(StepState *state, int add_pos, hipStream_t s);
+// elementwise residual: x += d
+syn_status_t launch_add(float *x, const float *d, int n, hipStream_t s);
+
+}  // namespace syn

@@ -1,0 +1,89 @@
+// Quantized linear layers resident in HBM (host-side classes behind the
+// syn_hip_qlinear_* handles and the model drivers).
+#pragma once
+
+#include <vector>
+
+#include "common.hpp"
+
+namespace syn {
+
+// Panel layout shared by the GEMV kernels: weights are cut into panels of 64
+// output rows; inside a panel the K axis is cut into 16-byte chunks and the
+// 64 rows' copies of chunk c are stored back to back:
+//   byte (n, kbyte) -> ((n/64 * C + kbyte/16) * 64 + n%64) * 16 + kbyte%16
+// so one wave64 load instruction (lane = row) reads 1 KiB contiguously and
+// every lane owns one output row: no cross-lane reduction, and the
+// activation chunk is wave-uniform.
+constexpr int kPanelRows = 64;
+
+struct GemvPlan {
+  int panels = 0;   // ceil(N/64)
+  int chunks = 0;   // 16-byte K chunks per row (C)
+  int ksplit = 1;   // workgroups along K
+  int cs = 0;       // chunks per K slice
+  int waves = 1;    // waves per workgroup
+};
+
+GemvPlan make_gemv_plan(size_t n, size_t k_chunks, bool chunked_kc);
+
+// INT8 W8A8 linear: QuantizedLinear (quantization/primitives/int8_linear.rs)
+struct QLinearInt8 {
+  size_t n = 0, k = 0;
+  int chunks = 0;       // K16 / 16
+  DevBuf w;             // panel layout, int8
+  DevBuf scales;        // f32 [N64]
+  DevBuf part;          // int32 split-K partials
+  size_t part_elems = 0;
+  DevBuf xq, sx;        // activation quantization scratch (forward())
+  size_t xq_rows = 0;
+
+  // host_nk: int8 [n,k] row per output; scales f32[n]
+  syn_status_t upload_nk(const int8_t *host_nk, const float *host_scales, size_t n_, size_t k_);
+  syn_status_t upload_kn(const int8_t *host_kn, size_t ldb, const float *host_scales, size_t n_,
+                         size_t k_);
+  // QuantizedLinear::from_f32 (int8_linear.rs:35-70) on host, then upload.
+  syn_status_t from_f32(const float *w_nk, size_t n_, size_t k_);
+  size_t weight_bytes() const { return n * k + n * 4; }
+  // y[m, n] (row stride ldy) from pre-quantized rows xq (row stride ldx).
+  syn_status_t gemv(size_t m, const int8_t *d_xq, size_t ldx, const float *d_sx, float *d_y,
+                    size_t ldy, hipStream_t s);
+  syn_status_t ensure_part(size_t elems);
+  // allocate split-K scratch for up to max_m activation rows (needed before
+  // a graph capture: nothing may allocate while a step is being recorded)
+  syn_status_t prepare(size_t max_m);
+};
+
+// launch the device quantizer (quantize.zig:12-47) on rows of x
+syn_status_t launch_quantize_rows(const float *d_x, size_t m, size_t k, size_t ldx, int8_t *d_q,
+                                  size_t ldq, float *d_s, hipStream_t s);
+
+// host-side reference quantizers (used at load time)
+void host_minmax_scales(const float *w, size_t ch, size_t chsz, float *scales);
+void host_quantize_weights_nk(const float *w, const float *scales, size_t n, size_t k,
+                              int8_t *out_nk);
+
+// Q4_0 linear: Q4Linear (q4_linear.rs); f32 activations.
+struct QLinearQ4_0 {
+  size_t n = 0, k = 0;
+  int blocks = 0;      // K/32
+  DevBuf nib;          // [P][blocks][64][16] nibble bytes
+  DevBuf sc;           // [P][blocks][64] f16 bits
+  DevBuf part;         // f32 split-K partials
+  size_t part_elems = 0;
+  DevBuf asum;         // per-call block sums of the activation rows
+  size_t asum_rows = 0;
+  syn_status_t upload_packed(const uint8_t *packed, size_t n_, size_t k_);
+  syn_status_t from_f32(const float *w_nk, size_t n_, size_t k_);
+  size_t weight_bytes() const { return n * (k / 32) * 18; }
+  syn_status_t gemv(size_t m, const float *d_x, size_t ldx, float *d_y, size_t ldy,
+                    hipStream_t s);
+};
+
+// Q4Linear::from_f32 + pack_for_zig (q4_linear.rs:64-121), host side.
+void host_q4_pack(const float *w, size_t n, size_t k, uint8_t *packed);
+
+void fill_normal(float *dst, size_t n, uint64_t seed, float stddev);
+void fill_normal_parallel(float *dst, size_t n, uint64_t seed, float stddev);
+
+}  // namespace syn

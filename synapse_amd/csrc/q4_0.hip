@@ -1,0 +1,224 @@
+// Q4_0 path (A6/A7): Q4Linear weights (q4_linear.rs:64-121, pack_for_zig
+// bytes [f16 scale | 16 nibble bytes], element 2i = low nibble, 2i+1 = high)
+// times f32 activations, as q4_0GemvRow computes (qmatmul.zig:276-343).
+//
+// HBM layout after the one-time repack: nibble blocks in the same 64-row
+// panel interleave as the INT8 path (16 bytes per block per row, one 1 KiB
+// wave load per block), f16 scales in a parallel [panel][block][64] array.
+// Per block the kernel forms sum_j a_j*n_j with n_j in 0..15 (f32 FMAs with a
+// wave-uniform activation operand) and removes the +8 offset with the block
+// sum of the activations: dot = sum a_j n_j - 8 sum a_j.  Float outputs carry
+// the north star's tolerance (max_j|y-r| / max_j|r| <= 1e-3 per row).
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+#include "linear.hpp"
+
+namespace syn {
+
+__device__ __forceinline__ float nib_lo(uint32_t w, int byte) {
+  return (float)((w >> (8 * byte)) & 0xfu);
+}
+__device__ __forceinline__ float nib_hi(uint32_t w, int byte) {
+  return (float)((w >> (8 * byte + 4)) & 0xfu);
+}
+
+// 8 elements of one dword: bytes b -> elements 2b (lo), 2b+1 (hi)
+__device__ __forceinline__ float dot8(uint32_t w, const float *__restrict__ a, float s) {
+  const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+  for (int b = 0; b < 4; b++) {
+    s = __builtin_fmaf(a[2 * b], (float)((lo >> (8 * b)) & 0xffu), s);
+    s = __builtin_fmaf(a[2 * b + 1], (float)((hi >> (8 * b)) & 0xffu), s);
+  }
+  return s;
+}
+
+template <int M>
+__global__ void __launch_bounds__(1024)
+    k_gemv_q4_0(const u32x4 *__restrict__ nib, const uint16_t *__restrict__ sc,
+                const float *__restrict__ x, int ldx, float *__restrict__ y, int ldy,
+                float *__restrict__ part, int N, int B, int bs) {
+  extern __shared__ float smem[];
+  const int panel = blockIdx.x, ks = blockIdx.y;
+  const int nw = blockDim.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int b0 = ks * bs, b1 = min(B, b0 + bs), nb = b1 - b0;
+  float *asum = smem;            // [M][bs]
+  float *red = smem + M * bs;    // [nw][M][64]
+  for (int t = threadIdx.x; t < M * nb; t += blockDim.x) {
+    const int m = t / nb, b = b0 + (t - m * nb);
+    const float *xa = x + (size_t)m * ldx + (size_t)b * 32;
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) s += xa[i];
+    asum[m * bs + (b - b0)] = s;
+  }
+  __syncthreads();
+  float acc[M];
+#pragma unroll
+  for (int m = 0; m < M; m++) acc[m] = 0.0f;
+  const size_t pbase = (size_t)panel * B;
+  for (int b = b0 + wave; b < b1; b += nw) {
+    const u32x4 q = __builtin_nontemporal_load(nib + (pbase + b) * 64 + lane);
+    const float d = syn_f16_to_f32_ieee(__builtin_nontemporal_load(sc + (pbase + b) * 64 + lane));
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+      const float *xa = x + (size_t)m * ldx + (size_t)b * 32;
+      float s = 0.0f;
+      s = dot8(q.x, xa, s);
+      s = dot8(q.y, xa + 8, s);
+      s = dot8(q.z, xa + 16, s);
+      s = dot8(q.w, xa + 24, s);
+      const float blk = s - 8.0f * asum[m * bs + (b - b0)];
+      acc[m] = __builtin_fmaf(blk, d, acc[m]);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; m++) red[(wave * M + m) * 64 + lane] = acc[m];
+  __syncthreads();
+  const int N64 = gridDim.x * 64;
+  for (int t = threadIdx.x; t < M * 64; t += blockDim.x) {
+    const int m = t >> 6, r = t & 63;
+    float s = 0.0f;
+    for (int w = 0; w < nw; w++) s += red[(w * M + m) * 64 + r];
+    const int row = panel * 64 + r;
+    if (gridDim.y == 1) {
+      if (row < N) y[(size_t)m * ldy + row] = s;
+    } else {
+      part[((size_t)ks * M + m) * N64 + row] = s;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256)
+    k_q4_reduce(const float *__restrict__ part, int ksplit, int M, int N, int N64,
+                float *__restrict__ y, int ldy) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= M * N) return;
+  const int m = idx / N, row = idx - m * N;
+  float s = 0.0f;
+  for (int k = 0; k < ksplit; k++) s += part[((size_t)k * M + m) * N64 + row];
+  y[(size_t)m * ldy + row] = s;
+}
+
+template <int M>
+static void launch_q4_m(const GemvPlan &p, const u32x4 *nib, const uint16_t *sc, const float *x,
+                        int ldx, float *y, int ldy, float *part, int N, hipStream_t s) {
+  const int waves = std::min(p.waves, M >= 8 ? 8 : 16);
+  const size_t shm = ((size_t)M * p.cs + (size_t)waves * M * 64) * sizeof(float);
+  hipLaunchKernelGGL(k_gemv_q4_0<M>, dim3(p.panels, p.ksplit), dim3(64 * waves), shm, s, nib, sc,
+                     x, ldx, y, ldy, part, N, p.chunks, p.cs);
+}
+
+typedef void (*q4_launcher)(const GemvPlan &, const u32x4 *, const uint16_t *, const float *,
+                            int, float *, int, float *, int, hipStream_t);
+static const q4_launcher kQ4Launch[9] = {nullptr,        launch_q4_m<1>, launch_q4_m<2>,
+                                         launch_q4_m<3>, launch_q4_m<4>, launch_q4_m<5>,
+                                         launch_q4_m<6>, launch_q4_m<7>, launch_q4_m<8>};
+
+syn_status_t QLinearQ4_0::gemv(size_t m, const float *d_x, size_t ldx, float *d_y, size_t ldy,
+                               hipStream_t s) {
+  if (m == 0 || n == 0 || k == 0) return SYN_OK;
+  // "chunks" here are 32-element blocks; a K slice holds whole blocks
+  GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
+  const size_t N64 = (size_t)p.panels * 64;
+  for (size_t m0 = 0; m0 < m; m0 += 8) {
+    const int mb = (int)std::min<size_t>(8, m - m0);
+    if (p.ksplit > 1 && part_elems < (size_t)p.ksplit * mb * N64) {
+      part_elems = (size_t)p.ksplit * mb * N64;
+      SYN_TRY(part.alloc(part_elems * sizeof(float)));
+    }
+    kQ4Launch[mb](p, nib.as<u32x4>(), sc.as<uint16_t>(), d_x + m0 * ldx, (int)ldx,
+                  d_y + m0 * ldy, (int)ldy, part.as<float>(), (int)n, s);
+    SYN_LAUNCH_CHECK();
+    if (p.ksplit > 1) {
+      const int total = mb * (int)n;
+      hipLaunchKernelGGL(k_q4_reduce, dim3(cdiv(total, 256)), dim3(256), 0, s, part.as<float>(),
+                         p.ksplit, mb, (int)n, (int)N64, d_y + m0 * ldy, (int)ldy);
+      SYN_LAUNCH_CHECK();
+    }
+  }
+  return SYN_OK;
+}
+
+syn_status_t QLinearQ4_0::upload_packed(const uint8_t *packed, size_t n_, size_t k_) {
+  n = n_;
+  k = k_;
+  blocks = (int)(k_ / 32);
+  const size_t P = cdiv(n_, 64), B = (size_t)blocks;
+  std::vector<uint8_t> hn(P * B * 64 * 16, 0x88);  // padding rows: nibble 8 -> value 0
+  std::vector<uint16_t> hs(P * B * 64, 0);
+  for (size_t row = 0; row < n_; row++) {
+    const size_t p = row / 64, r = row % 64;
+    for (size_t b = 0; b < B; b++) {
+      const uint8_t *src = packed + (row * B + b) * 18;
+      hs[(p * B + b) * 64 + r] = (uint16_t)(src[0] | (src[1] << 8));
+      std::memcpy(&hn[((p * B + b) * 64 + r) * 16], src + 2, 16);
+    }
+  }
+  SYN_TRY(nib.alloc(hn.size()));
+  SYN_TRY(sc.alloc(hs.size() * 2));
+  SYN_HIP(hipMemcpy(nib.p, hn.data(), hn.size(), hipMemcpyHostToDevice));
+  SYN_HIP(hipMemcpy(sc.p, hs.data(), hs.size() * 2, hipMemcpyHostToDevice));
+  return SYN_OK;
+}
+
+// q4_linear.rs:64-121
+void host_q4_pack(const float *w, size_t n, size_t k, uint8_t *packed) {
+  const size_t bpr = (k + 31) / 32;
+  for (size_t row = 0; row < n; row++)
+    for (size_t b = 0; b < bpr; b++) {
+      float vals[32];
+      for (int i = 0; i < 32; i++) {
+        const size_t col = b * 32 + (size_t)i;
+        vals[i] = col < k ? w[row * k + col] : 0.0f;
+      }
+      float mx = 0.0f;
+      for (int i = 0; i < 32; i++) mx = std::fmax(mx, std::fabs(vals[i]));
+      const float scale = (mx == 0.0f) ? 0.0f : mx / 7.0f;
+      const float inv = (scale == 0.0f) ? 0.0f : 1.0f / scale;
+      uint8_t *blk = packed + (row * bpr + b) * 18;
+      const uint16_t h = f32_to_f16_trunc(scale);
+      blk[0] = (uint8_t)(h & 0xff);
+      blk[1] = (uint8_t)(h >> 8);
+      for (int i = 0; i < 16; i++) {
+        float r0 = std::round(vals[2 * i] * inv), r1 = std::round(vals[2 * i + 1] * inv);
+        r0 = std::min(7.0f, std::max(-8.0f, r0));
+        r1 = std::min(7.0f, std::max(-8.0f, r1));
+        const int v0 = (int)r0, v1 = (int)r1;
+        blk[2 + i] = (uint8_t)((uint8_t)(v0 + 8) | (uint8_t)((v1 + 8) << 4));
+      }
+    }
+}
+
+syn_status_t QLinearQ4_0::from_f32(const float *w_nk, size_t n_, size_t k_) {
+  std::vector<uint8_t> packed(n_ * ((k_ + 31) / 32) * 18);
+  host_q4_pack(w_nk, n_, k_, packed.data());
+  return upload_packed(packed.data(), n_, k_);
+}
+
+}  // namespace syn
+
+using namespace syn;
+
+extern "C" syn_status_t syn_q4_0_gemv(size_t n, size_t k, const float *a, const uint8_t *b_q4,
+                                      float *c) {
+  if (!a || !b_q4 || !c) return SYN_ERR_NULL_PTR;
+  if (n == 0 || k == 0) return SYN_OK;
+  if (k % 32 != 0) return SYN_ERR_SHAPE_MISMATCH;  // exports.zig:1625
+  SYN_TRY(ensure_init());
+  hipStream_t s = default_stream();
+  QLinearQ4_0 L;
+  SYN_TRY(L.upload_packed(b_q4, n, k));
+  DevBuf dx, dy;
+  SYN_TRY(dx.alloc(k * 4));
+  SYN_TRY(dy.alloc(n * 4));
+  SYN_HIP(hipMemcpyAsync(dx.p, a, k * 4, hipMemcpyHostToDevice, s));
+  SYN_TRY(L.gemv(1, dx.as<float>(), k, dy.as<float>(), n, s));
+  SYN_HIP(hipMemcpyAsync(c, dy.p, n * 4, hipMemcpyDeviceToHost, s));
+  SYN_HIP(hipStreamSynchronize(s));
+  return SYN_OK;
+}

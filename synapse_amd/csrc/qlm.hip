@@ -1,0 +1,479 @@
+// INT8 W8A8 causal LM on the device: QuantizedCausalLM
+// (quantization/lm/int8.rs:21-709) kept resident in HBM the way the Metal
+// backend keeps MetalModelBuffers (metal/gpu_buffers.rs:79-433), with the
+// whole greedy loop on the device (only token ids come back).
+//
+// Per layer (int8.rs:242-282, 429-505):
+//   x += down(prev) ; q8(rmsnorm(x))          k_rmsnorm_quant
+//   [q|k|v] = W_qkv q8                        fused GEMV (rows of Wq,Wk,Wv)
+//   head norms, RoPE(pos), KV append          k_qk_norm_rope_kv
+//   attention over the cache                  k_attn_decode
+//   o = W_o q8(attn)                          quantize + GEMV
+//   x += o ; q8(rmsnorm(x))                   k_rmsnorm_quant
+//   [g|u] = W_gu q8                           fused GEMV (rows of Wgate,Wup)
+//   q8(silu(g)*u)                             k_swiglu_quant
+//   down = W_down q8                          GEMV
+// Fusing weight rows of Q/K/V (and gate/up) is exact: each output row has its
+// own scale and integer dot product.
+#include <algorithm>
+#include <thread>
+#include <vector>
+
+#include "layer_ops.hpp"
+#include "linear.hpp"
+
+namespace syn {
+
+struct QLayer {
+  QLinearInt8 qkv, o, gu, down;
+};
+
+}  // namespace syn
+
+using namespace syn;
+
+struct syn_hip_qlm_s {
+  syn_hip_lm_config c{};
+  size_t h = 0, hd = 0, qd = 0, kvd = 0, inter = 0, L = 0, vocab = 0, S = 0;
+  size_t ldh = 0, ldq = 0, ldi = 0, n_qkv = 0;
+  std::vector<QLayer> layers;
+  std::vector<int> have_layer;
+  QLinearInt8 lm_head;
+  std::vector<float> host_embed;
+  DevBuf embed, ones_h, ones_hd, rope_cos, rope_sin, kc, vc;
+  DevBuf x, xq, sx, qkv, qrot, attn, aq, sa, o, gu, hq, sh, down, logits, scores;
+  DevBuf pv, pi, pv2, state, history, mhist, ids;
+  hipStream_t stream = nullptr;
+  hipGraphExec_t graph = nullptr;
+  bool finalized = false;
+
+  ~syn_hip_qlm_s() {
+    if (graph) (void)hipGraphExecDestroy(graph);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+  float *kc_l(size_t l) { return kc.as<float>() + l * S * kvd; }
+  float *vc_l(size_t l) { return vc.as<float>() + l * S * kvd; }
+  StepState *st() { return state.as<StepState>(); }
+
+  syn_status_t alloc_all() {
+    const size_t T = S;  // prefill rows
+    SYN_TRY(ones_h.alloc(h * 4));
+    SYN_TRY(ones_hd.alloc(hd * 4));
+    SYN_TRY(rope_cos.alloc(S * (hd / 2) * 4));
+    SYN_TRY(rope_sin.alloc(S * (hd / 2) * 4));
+    SYN_TRY(kc.alloc(L * S * kvd * 4));
+    SYN_TRY(vc.alloc(L * S * kvd * 4));
+    SYN_TRY(x.alloc(T * h * 4));
+    SYN_TRY(xq.alloc(T * ldh));
+    SYN_TRY(sx.alloc(T * 4));
+    SYN_TRY(qkv.alloc(T * n_qkv * 4));
+    SYN_TRY(qrot.alloc(T * qd * 4));
+    SYN_TRY(attn.alloc(T * qd * 4));
+    SYN_TRY(aq.alloc(T * ldq));
+    SYN_TRY(sa.alloc(T * 4));
+    SYN_TRY(o.alloc(T * h * 4));
+    SYN_TRY(gu.alloc(T * 2 * inter * 4));
+    SYN_TRY(hq.alloc(T * ldi));
+    SYN_TRY(sh.alloc(T * 4));
+    SYN_TRY(down.alloc(T * h * 4));
+    SYN_TRY(logits.alloc(vocab * 4));
+    SYN_TRY(scores.alloc(c.n_heads * S * 4));
+    SYN_TRY(pv.alloc(256 * 4));
+    SYN_TRY(pi.alloc(256 * 4));
+    SYN_TRY(pv2.alloc(256 * 4));
+    SYN_TRY(state.alloc(sizeof(StepState)));
+    SYN_TRY(history.alloc((S + 1) * 4));
+    SYN_TRY(mhist.alloc((S + 1) * 4));
+    SYN_TRY(ids.alloc(S * 4));
+    std::vector<float> one(std::max(h, hd), 1.0f);
+    SYN_HIP(hipMemcpy(ones_h.p, one.data(), h * 4, hipMemcpyHostToDevice));
+    SYN_HIP(hipMemcpy(ones_hd.p, one.data(), hd * 4, hipMemcpyHostToDevice));
+    // zero padding columns of the activation rows once (kernels never write them)
+    SYN_HIP(hipMemset(xq.p, 0, xq.bytes));
+    SYN_HIP(hipMemset(aq.p, 0, aq.bytes));
+    SYN_HIP(hipMemset(hq.p, 0, hq.bytes));
+    SYN_HIP(hipMemset(kc.p, 0, kc.bytes));
+    SYN_HIP(hipMemset(vc.p, 0, vc.bytes));
+    return SYN_OK;
+  }
+
+  syn_status_t set_layer(size_t l, const float *wq, const float *wk, const float *wv,
+                         const float *wo, const float *wg, const float *wu, const float *wd) {
+    QLayer &Ly = layers[l];
+    // q,k,v rows stacked: per-row scales make the fused GEMV exact
+    {
+      std::vector<float> sc(n_qkv);
+      std::vector<int8_t> q(n_qkv * h);
+      const float *srcs[3] = {wq, wk, wv};
+      const size_t rows[3] = {qd, kvd, kvd};
+      size_t r0 = 0;
+      for (int t = 0; t < 3; t++) {
+        host_minmax_scales(srcs[t], rows[t], h, sc.data() + r0);
+        host_quantize_weights_nk(srcs[t], sc.data() + r0, rows[t], h, q.data() + r0 * h);
+        r0 += rows[t];
+      }
+      SYN_TRY(Ly.qkv.upload_nk(q.data(), sc.data(), n_qkv, h));
+    }
+    SYN_TRY(Ly.o.from_f32(wo, h, qd));
+    {
+      std::vector<float> sc(2 * inter);
+      std::vector<int8_t> q(2 * inter * h);
+      host_minmax_scales(wg, inter, h, sc.data());
+      host_quantize_weights_nk(wg, sc.data(), inter, h, q.data());
+      host_minmax_scales(wu, inter, h, sc.data() + inter);
+      host_quantize_weights_nk(wu, sc.data() + inter, inter, h, q.data() + inter * h);
+      SYN_TRY(Ly.gu.upload_nk(q.data(), sc.data(), 2 * inter, h));
+    }
+    SYN_TRY(Ly.down.from_f32(wd, h, inter));
+    have_layer[l] = 1;
+    return SYN_OK;
+  }
+
+  // ---------------------------------------------------------- one layer
+  syn_status_t layer(size_t l, int rows, bool prefill, hipStream_t s) {
+    QLayer &Ly = layers[l];
+    const float eps = c.eps;
+    const int nh = (int)c.n_heads, nkv = (int)c.n_kv_heads;
+    SYN_TRY(launch_rmsnorm_quant(x.as<float>(), l == 0 ? nullptr : down.as<float>(),
+                                 ones_h.as<float>(), eps, rows, (int)h, xq.as<int8_t>(), (int)ldh,
+                                 sx.as<float>(), nullptr, s));
+    SYN_TRY(Ly.qkv.gemv(rows, xq.as<int8_t>(), ldh, sx.as<float>(), qkv.as<float>(), n_qkv, s));
+    SYN_TRY(launch_qk_norm_rope_kv(qkv.as<float>(), (int)n_qkv, rows, nh, nkv, (int)hd,
+                                   ones_hd.as<float>(), ones_hd.as<float>(), eps,
+                                   rope_cos.as<float>(), rope_sin.as<float>(),
+                                   prefill ? nullptr : &st()->pos, 0, qrot.as<float>(), kc_l(l),
+                                   vc_l(l), s));
+    if (prefill)
+      SYN_TRY(launch_attention_prefill(qrot.as<float>(), kc_l(l), vc_l(l), rows, nh, nkv,
+                                       (int)hd, nullptr, attn.as<float>(), s));
+    else
+      SYN_TRY(launch_attention_decode(qrot.as<float>(), kc_l(l), vc_l(l), &st()->pos, nh, nkv,
+                                      (int)hd, scores.as<float>(), (int)S, attn.as<float>(), s));
+    SYN_TRY(launch_quantize_rows(attn.as<float>(), rows, qd, qd, aq.as<int8_t>(), ldq,
+                                 sa.as<float>(), s));
+    SYN_TRY(Ly.o.gemv(rows, aq.as<int8_t>(), ldq, sa.as<float>(), o.as<float>(), h, s));
+    SYN_TRY(launch_rmsnorm_quant(x.as<float>(), o.as<float>(), ones_h.as<float>(), eps, rows,
+                                 (int)h, xq.as<int8_t>(), (int)ldh, sx.as<float>(), nullptr, s));
+    SYN_TRY(Ly.gu.gemv(rows, xq.as<int8_t>(), ldh, sx.as<float>(), gu.as<float>(), 2 * inter, s));
+    SYN_TRY(launch_swiglu_quant(gu.as<float>(), (int)(2 * inter), rows, (int)inter,
+                                hq.as<int8_t>(), (int)ldi, sh.as<float>(), s));
+    SYN_TRY(Ly.down.gemv(rows, hq.as<int8_t>(), ldi, sh.as<float>(), down.as<float>(), h, s));
+    return SYN_OK;
+  }
+
+  // final norm of row `row`, lm_head, greedy argmax, state advance
+  syn_status_t head(int row, int add_pos, hipStream_t s) {
+    float *xr = x.as<float>() + (size_t)row * h;
+    const float *dr = down.as<float>() + (size_t)row * h;
+    SYN_TRY(launch_rmsnorm_quant(xr, dr, ones_h.as<float>(), c.eps, 1, (int)h, xq.as<int8_t>(),
+                                 (int)ldh, sx.as<float>(), nullptr, s));
+    SYN_TRY(lm_head.gemv(1, xq.as<int8_t>(), ldh, sx.as<float>(), logits.as<float>(), vocab, s));
+    SYN_TRY(launch_argmax(logits.as<float>(), (int)vocab, pv.as<float>(), pi.as<int>(),
+                          pv2.as<float>(), st(), history.as<uint32_t>(), mhist.as<float>(), s));
+    return launch_step_advance(st(), add_pos, s);
+  }
+
+  syn_status_t decode_step(hipStream_t s) {
+    SYN_TRY(launch_embed(embed.as<float>(), &st()->token, 1, (int)h, (int)vocab, x.as<float>(), s));
+    for (size_t l = 0; l < L; l++) SYN_TRY(layer(l, 1, false, s));
+    return head(0, 1, s);
+  }
+
+  syn_status_t build_graph() {
+    if (graph) return SYN_OK;
+    hipGraph_t g;
+    SYN_HIP(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+    syn_status_t st_ = decode_step(stream);
+    hipError_t e = hipStreamEndCapture(stream, &g);
+    if (st_ != SYN_OK) {
+      if (e == hipSuccess) (void)hipGraphDestroy(g);
+      return st_;
+    }
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture", __FILE__, __LINE__);
+    e = hipGraphInstantiate(&graph, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) {
+      graph = nullptr;
+      return hip_fail(e, "hipGraphInstantiate", __FILE__, __LINE__);
+    }
+    return SYN_OK;
+  }
+
+  syn_status_t set_state(int pos, uint32_t token, int step) {
+    StepState hs{pos, token, step, 0.0f};
+    SYN_HIP(hipMemcpyAsync(state.p, &hs, sizeof(hs), hipMemcpyHostToDevice, stream));
+    return SYN_OK;
+  }
+
+  syn_status_t get_state(StepState *out) {
+    SYN_HIP(hipMemcpyAsync(out, state.p, sizeof(StepState), hipMemcpyDeviceToHost, stream));
+    SYN_HIP(hipStreamSynchronize(stream));
+    return SYN_OK;
+  }
+
+  syn_status_t prefill(const uint32_t *host_ids, size_t n) {
+    if (n == 0 || n > S) {
+      set_error("prefill length must be in [1, max_seq]");
+      return SYN_ERR_INVALID_ARG;
+    }
+    SYN_HIP(hipMemcpyAsync(ids.p, host_ids, n * 4, hipMemcpyHostToDevice, stream));
+    SYN_TRY(set_state(0, 0, 0));
+    SYN_TRY(launch_embed(embed.as<float>(), ids.as<uint32_t>(), (int)n, (int)h, (int)vocab,
+                         x.as<float>(), stream));
+    for (size_t l = 0; l < L; l++) SYN_TRY(layer(l, (int)n, true, stream));
+    return head((int)n - 1, (int)n, stream);
+  }
+};
+
+static syn_status_t check_model(syn_hip_qlm_t *m) {
+  if (!m) return SYN_ERR_NULL_PTR;
+  if (!m->finalized) {
+    set_error("model not finalized");
+    return SYN_ERR_INVALID_ARG;
+  }
+  return SYN_OK;
+}
+
+extern "C" {
+
+syn_status_t syn_hip_qlm_create(const syn_hip_lm_config *cfg, syn_hip_qlm_t **out) {
+  if (!cfg || !out) return SYN_ERR_NULL_PTR;
+  if (!cfg->hidden || !cfg->n_layers || !cfg->n_heads || !cfg->n_kv_heads || !cfg->head_dim ||
+      !cfg->inter || !cfg->vocab || !cfg->max_seq || cfg->n_heads % cfg->n_kv_heads ||
+      cfg->head_dim % 2 || cfg->head_dim > 1024)
+    return SYN_ERR_INVALID_ARG;
+  SYN_TRY(ensure_init());
+  auto *m = new syn_hip_qlm_s();
+  m->c = *cfg;
+  m->h = cfg->hidden;
+  m->hd = cfg->head_dim;
+  m->qd = (size_t)cfg->n_heads * cfg->head_dim;
+  m->kvd = (size_t)cfg->n_kv_heads * cfg->head_dim;
+  m->inter = cfg->inter;
+  m->L = cfg->n_layers;
+  m->vocab = cfg->vocab;
+  m->S = cfg->max_seq;
+  m->ldh = round_up(m->h, 16);
+  m->ldq = round_up(m->qd, 16);
+  m->ldi = round_up(m->inter, 16);
+  m->n_qkv = m->qd + 2 * m->kvd;
+  m->layers.resize(m->L);
+  m->have_layer.assign(m->L, 0);
+  hipError_t e = hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    m->stream = nullptr;
+    delete m;
+    return hip_fail(e, "hipStreamCreate", __FILE__, __LINE__);
+  }
+  syn_status_t st = m->alloc_all();
+  if (st != SYN_OK) {
+    delete m;
+    return st;
+  }
+  *out = m;
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_qlm_set_embed(syn_hip_qlm_t *m, const float *embed) {
+  if (!m || !embed) return SYN_ERR_NULL_PTR;
+  const size_t n = m->vocab * m->h;
+  m->host_embed.assign(embed, embed + n);
+  SYN_TRY(m->embed.alloc(n * 4));
+  SYN_HIP(hipMemcpy(m->embed.p, embed, n * 4, hipMemcpyHostToDevice));
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_qlm_set_layer(syn_hip_qlm_t *m, uint32_t layer, const float *wq,
+                                   const float *wk, const float *wv, const float *wo,
+                                   const float *wg, const float *wu, const float *wd) {
+  if (!m || !wq || !wk || !wv || !wo || !wg || !wu || !wd) return SYN_ERR_NULL_PTR;
+  if (layer >= m->L) return SYN_ERR_INVALID_ARG;
+  return m->set_layer(layer, wq, wk, wv, wo, wg, wu, wd);
+}
+
+syn_status_t syn_hip_qlm_init_synthetic(syn_hip_qlm_t *m, uint64_t seed_base, float stddev) {
+  if (!m) return SYN_ERR_NULL_PTR;
+  const size_t h = m->h;
+  {
+    std::vector<float> emb(m->vocab * h);
+    fill_normal_parallel(emb.data(), emb.size(), seed_base + 0, stddev);
+    SYN_TRY(syn_hip_qlm_set_embed(m, emb.data()));
+  }
+  const size_t rows[7] = {m->qd, m->kvd, m->kvd, h, m->inter, m->inter, h};
+  const size_t cols[7] = {h, h, h, m->qd, h, h, m->inter};
+  std::vector<std::vector<float>> w(7);
+  for (int t = 0; t < 7; t++) w[t].resize(rows[t] * cols[t]);
+  for (size_t l = 0; l < m->L; l++) {
+    std::vector<std::thread> th;
+    for (int t = 0; t < 7; t++)
+      th.emplace_back([&, t] {
+        fill_normal(w[t].data(), w[t].size(), seed_base + 1 + 8 * l + (uint64_t)t, stddev);
+      });
+    for (auto &x : th) x.join();
+    SYN_TRY(m->set_layer(l, w[0].data(), w[1].data(), w[2].data(), w[3].data(), w[4].data(),
+                         w[5].data(), w[6].data()));
+  }
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_qlm_finalize(syn_hip_qlm_t *m) {
+  if (!m) return SYN_ERR_NULL_PTR;
+  if (m->host_embed.empty()) {
+    set_error("embed_tokens not set");
+    return SYN_ERR_INVALID_ARG;
+  }
+  for (size_t l = 0; l < m->L; l++)
+    if (!m->have_layer[l]) {
+      set_error("layer " + std::to_string(l) + " not set");
+      return SYN_ERR_INVALID_ARG;
+    }
+  // tied lm_head from embed_tokens (int8.rs:132-139)
+  SYN_TRY(m->lm_head.from_f32(m->host_embed.data(), m->vocab, m->h));
+  std::vector<float>().swap(m->host_embed);
+  // RoPE tables, models/lm/builder.rs:88-133 (glibc powf/cosf/sinf, as Rust f32)
+  const size_t half = m->hd / 2;
+  std::vector<float> cs(m->S * half), sn(m->S * half);
+  const float fb = (float)m->c.rope_theta;
+  for (size_t pos = 0; pos < m->S; pos++)
+    for (size_t i = 0; i < half; i++) {
+      const float freq = 1.0f / powf(fb, 2.0f * (float)i / (float)m->hd);
+      const float scaled = freq / 1.0f;
+      const float angle = (float)pos * scaled;
+      cs[pos * half + i] = cosf(angle);
+      sn[pos * half + i] = sinf(angle);
+    }
+  SYN_HIP(hipMemcpy(m->rope_cos.p, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+  SYN_HIP(hipMemcpy(m->rope_sin.p, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+  for (auto &Ly : m->layers) {
+    SYN_TRY(Ly.qkv.prepare(m->S));
+    SYN_TRY(Ly.o.prepare(m->S));
+    SYN_TRY(Ly.gu.prepare(m->S));
+    SYN_TRY(Ly.down.prepare(m->S));
+  }
+  SYN_TRY(m->lm_head.prepare(1));
+  m->finalized = true;
+  SYN_TRY(m->set_state(0, 0, 0));
+  SYN_HIP(hipStreamSynchronize(m->stream));
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_qlm_reset(syn_hip_qlm_t *m) {
+  SYN_TRY(check_model(m));
+  SYN_TRY(m->set_state(0, 0, 0));
+  SYN_HIP(hipStreamSynchronize(m->stream));
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_qlm_forward_prefill(syn_hip_qlm_t *m, const uint32_t *ids, size_t n,
+                                         float *host_logits) {
+  SYN_TRY(check_model(m));
+  if (!ids) return SYN_ERR_NULL_PTR;
+  SYN_TRY(m->prefill(ids, n));
+  if (host_logits)
+    SYN_HIP(hipMemcpyAsync(host_logits, m->logits.p, m->vocab * 4, hipMemcpyDeviceToHost,
+                           m->stream));
+  SYN_HIP(hipStreamSynchronize(m->stream));
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_qlm_forward_one(syn_hip_qlm_t *m, uint32_t token, float *host_logits) {
+  SYN_TRY(check_model(m));
+  StepState cur;
+  SYN_TRY(m->get_state(&cur));
+  if ((size_t)cur.pos >= m->S) {
+    set_error("KV cache full");  // kvcache.zig:68-69 CacheFull
+    return SYN_ERR_INVALID_ARG;
+  }
+  SYN_TRY(m->build_graph());
+  SYN_TRY(m->set_state(cur.pos, token, cur.step));
+  SYN_HIP(hipGraphLaunch(m->graph, m->stream));
+  if (host_logits)
+    SYN_HIP(hipMemcpyAsync(host_logits, m->logits.p, m->vocab * 4, hipMemcpyDeviceToHost,
+                           m->stream));
+  SYN_HIP(hipStreamSynchronize(m->stream));
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_qlm_generate(syn_hip_qlm_t *m, const uint32_t *prompt, size_t n_prompt,
+                                  size_t max_new, uint32_t *out_tokens, float *out_margins) {
+  SYN_TRY(check_model(m));
+  if (!prompt || !out_tokens) return SYN_ERR_NULL_PTR;
+  if (max_new == 0) return SYN_OK;
+  if (n_prompt + max_new - 1 > m->S) {
+    set_error("prompt + generated tokens exceed max_seq");
+    return SYN_ERR_INVALID_ARG;
+  }
+  SYN_TRY(m->build_graph());
+  SYN_TRY(m->prefill(prompt, n_prompt));
+  for (size_t i = 1; i < max_new; i++) SYN_HIP(hipGraphLaunch(m->graph, m->stream));
+  SYN_HIP(hipMemcpyAsync(out_tokens, m->history.p, max_new * 4, hipMemcpyDeviceToHost,
+                         m->stream));
+  if (out_margins)
+    SYN_HIP(hipMemcpyAsync(out_margins, m->mhist.p, max_new * 4, hipMemcpyDeviceToHost,
+                           m->stream));
+  SYN_HIP(hipStreamSynchronize(m->stream));
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_qlm_decode_timed(syn_hip_qlm_t *m, size_t steps, float *elapsed_ms) {
+  SYN_TRY(check_model(m));
+  if (!elapsed_ms) return SYN_ERR_NULL_PTR;
+  StepState cur;
+  SYN_TRY(m->get_state(&cur));
+  if ((size_t)cur.pos + steps > m->S) {
+    set_error("decode steps exceed max_seq");
+    return SYN_ERR_INVALID_ARG;
+  }
+  SYN_TRY(m->build_graph());
+  hipEvent_t a, b;
+  SYN_HIP(hipEventCreate(&a));
+  SYN_HIP(hipEventCreate(&b));
+  SYN_HIP(hipEventRecord(a, m->stream));
+  for (size_t i = 0; i < steps; i++) SYN_HIP(hipGraphLaunch(m->graph, m->stream));
+  SYN_HIP(hipEventRecord(b, m->stream));
+  SYN_HIP(hipEventSynchronize(b));
+  SYN_HIP(hipEventElapsedTime(elapsed_ms, a, b));
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_qlm_time_lm_head(syn_hip_qlm_t *m, size_t iters, size_t flush_bytes,
+                                      float *avg_ms) {
+  SYN_TRY(check_model(m));
+  if (!avg_ms) return SYN_ERR_NULL_PTR;
+  if (iters == 0) return SYN_ERR_INVALID_ARG;
+  DevBuf flush;
+  if (flush_bytes) SYN_TRY(flush.alloc(flush_bytes));
+  hipEvent_t a, b;
+  SYN_HIP(hipEventCreate(&a));
+  SYN_HIP(hipEventCreate(&b));
+  double total = 0.0;
+  syn_status_t st = SYN_OK;
+  for (size_t i = 0; i < iters && st == SYN_OK; i++) {
+    if (flush_bytes) SYN_HIP(hipMemsetAsync(flush.p, (int)(i & 0xff), flush_bytes, m->stream));
+    SYN_HIP(hipEventRecord(a, m->stream));
+    st = m->lm_head.gemv(1, m->xq.as<int8_t>(), m->ldh, m->sx.as<float>(), m->logits.as<float>(),
+                         m->vocab, m->stream);
+    SYN_HIP(hipEventRecord(b, m->stream));
+    SYN_HIP(hipEventSynchronize(b));
+    float ms = 0.0f;
+    SYN_HIP(hipEventElapsedTime(&ms, a, b));
+    total += ms;
+  }
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  SYN_TRY(st);
+  *avg_ms = (float)(total / (double)iters);
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_qlm_destroy(syn_hip_qlm_t *m) {
+  if (m) {
+    (void)hipStreamSynchronize(m->stream);
+    delete m;
+  }
+  return SYN_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,377 @@
+"""ctypes binding of libsynapse_hip.so (the C ABI in include/synapse_hip.h).
+
+This module is the Python view of the `hip` backend used by the tests and
+the benchmark.  It loads the in-tree library and fails loudly when the
+library is missing: there is no CPU fallback anywhere in the product path.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libsynapse_hip.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "synapse_hip.h")
+
+SYN_OK = 0
+STATUS_NAMES = {0: "OK", 1: "NULL_PTR", 2: "INVALID_ARG", 3: "OUT_OF_MEMORY",
+                4: "SHAPE_MISMATCH", 5: "NOT_CONTIGUOUS", 6: "INVALID_AXIS",
+                7: "INVALID_DIMENSIONS", 8: "INTERNAL", 100: "NO_DEVICE", 101: "HIP",
+                102: "LAUNCH"}
+FMT_INT8, FMT_Q4_0 = 1, 2
+LAYOUT_KN, LAYOUT_NK = 0, 1
+
+P, SZ, ST = C.c_void_p, C.c_size_t, C.c_int32
+
+
+class LmConfig(C.Structure):
+    _fields_ = [("hidden", C.c_uint32), ("n_layers", C.c_uint32), ("n_heads", C.c_uint32),
+                ("n_kv_heads", C.c_uint32), ("head_dim", C.c_uint32), ("inter", C.c_uint32),
+                ("vocab", C.c_uint32), ("max_seq", C.c_uint32), ("eps", C.c_float),
+                ("rope_theta", C.c_double)]
+
+
+SIGNATURES = {
+    "syn_quantize_per_channel_int8": (ST, [P, SZ, SZ, P, P]),
+    "syn_qgemm_int8": (ST, [SZ, SZ, SZ, P, SZ, P, SZ, P, SZ, P, P]),
+    "syn_q4_0_gemv": (ST, [SZ, SZ, P, P, P]),
+    "syn_hip_init": (ST, [C.c_int]),
+    "syn_hip_device_count": (ST, [C.POINTER(C.c_int)]),
+    "syn_hip_last_error": (C.c_char_p, []),
+    "syn_hip_malloc": (ST, [C.POINTER(P), SZ]),
+    "syn_hip_free": (ST, [P]),
+    "syn_hip_memcpy_h2d": (ST, [P, P, SZ]),
+    "syn_hip_memcpy_d2h": (ST, [P, P, SZ]),
+    "syn_hip_memcpy_d2d": (ST, [P, P, SZ]),
+    "syn_hip_memset": (ST, [P, C.c_int, SZ]),
+    "syn_hip_synchronize": (ST, []),
+    "syn_hip_stream_create": (ST, [C.POINTER(P)]),
+    "syn_hip_stream_destroy": (ST, [P]),
+    "syn_hip_stream_synchronize": (ST, [P]),
+    "syn_hip_timer_create": (ST, [C.POINTER(P)]),
+    "syn_hip_timer_start": (ST, [P, P]),
+    "syn_hip_timer_stop": (ST, [P, P]),
+    "syn_hip_timer_elapsed_ms": (ST, [P, C.POINTER(C.c_float)]),
+    "syn_hip_timer_destroy": (ST, [P]),
+    "syn_hip_quantize_rows": (ST, [P, SZ, SZ, SZ, P, SZ, P, P]),
+    "syn_hip_qlinear_create": (ST, [C.c_int, SZ, SZ, P, P, C.c_int, C.POINTER(P)]),
+    "syn_hip_qlinear_from_f32": (ST, [C.c_int, SZ, SZ, P, C.POINTER(P)]),
+    "syn_hip_qlinear_forward": (ST, [P, SZ, P, P, P]),
+    "syn_hip_qlinear_forward_pre_quantized": (ST, [P, SZ, P, SZ, P, P, P]),
+    "syn_hip_qlinear_info": (ST, [P, C.POINTER(SZ), C.POINTER(SZ), C.POINTER(C.c_int),
+                                  C.POINTER(SZ)]),
+    "syn_hip_qlinear_destroy": (ST, [P]),
+    "syn_hip_qlm_create": (ST, [C.POINTER(LmConfig), C.POINTER(P)]),
+    "syn_hip_qlm_set_embed": (ST, [P, P]),
+    "syn_hip_qlm_set_layer": (ST, [P, C.c_uint32, P, P, P, P, P, P, P]),
+    "syn_hip_qlm_init_synthetic": (ST, [P, C.c_uint64, C.c_float]),
+    "syn_hip_qlm_finalize": (ST, [P]),
+    "syn_hip_qlm_reset": (ST, [P]),
+    "syn_hip_qlm_forward_prefill": (ST, [P, P, SZ, P]),
+    "syn_hip_qlm_forward_one": (ST, [P, C.c_uint32, P]),
+    "syn_hip_qlm_generate": (ST, [P, P, SZ, SZ, P, P]),
+    "syn_hip_qlm_decode_timed": (ST, [P, SZ, C.POINTER(C.c_float)]),
+    "syn_hip_qlm_time_lm_head": (ST, [P, SZ, SZ, C.POINTER(C.c_float)]),
+    "syn_hip_qlm_destroy": (ST, [P]),
+    "syn_hip_fill_normal": (ST, [P, SZ, C.c_uint64, C.c_float]),
+    "syn_hip_eval_expf": (ST, [P, P, SZ, P]),
+}
+
+_lib = None
+
+
+class SynapseError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        self.status = status
+        super().__init__(f"{what}: status {status} ({STATUS_NAMES.get(status, 'Unknown')})"
+                         f" {last_error()}")
+
+
+def lib():
+    """Load the in-tree HIP library (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: build it with "
+                              "`python -m synapse_amd.build` (no CPU fallback exists)")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    if _lib is None:
+        return ""
+    s = _lib.syn_hip_last_error()
+    return s.decode() if s else ""
+
+
+def check(status: int, what: str = "synapse_hip"):
+    if status != SYN_OK:
+        raise SynapseError(status, what)
+
+
+def ptr(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def device_count() -> int:
+    n = C.c_int(0)
+    lib().syn_hip_device_count(C.byref(n))
+    return n.value
+
+
+def init(device: int = 0):
+    check(lib().syn_hip_init(device), "syn_hip_init")
+
+
+class DeviceBuffer:
+    """Raw device allocation owned by Python (freed on close / GC)."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = C.c_void_p()
+        check(lib().syn_hip_malloc(C.byref(p), max(self.nbytes, 1)), "syn_hip_malloc")
+        self.ptr = p.value
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a: np.ndarray):
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        check(lib().syn_hip_memcpy_h2d(self.ptr, ptr(a), a.nbytes), "h2d")
+
+    def download(self, shape, dtype) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        assert out.nbytes <= self.nbytes
+        check(lib().syn_hip_memcpy_d2h(ptr(out), self.ptr, out.nbytes), "d2h")
+        return out
+
+    def zero(self):
+        check(lib().syn_hip_memset(self.ptr, 0, self.nbytes), "memset")
+
+    def close(self):
+        if self.ptr:
+            lib().syn_hip_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class Timer:
+    def __init__(self):
+        p = C.c_void_p()
+        check(lib().syn_hip_timer_create(C.byref(p)), "timer_create")
+        self.h = p.value
+
+    def start(self, stream=None):
+        check(lib().syn_hip_timer_start(self.h, stream))
+
+    def stop(self, stream=None):
+        check(lib().syn_hip_timer_stop(self.h, stream))
+
+    def ms(self) -> float:
+        v = C.c_float()
+        check(lib().syn_hip_timer_elapsed_ms(self.h, C.byref(v)))
+        return v.value
+
+    def __del__(self):
+        try:
+            lib().syn_hip_timer_destroy(self.h)
+        except Exception:
+            pass
+
+
+# ------------------------------------------------------------------ reference-signature calls
+def quantize_per_channel_int8(x: np.ndarray):
+    """syn_quantize_per_channel_int8 through the HIP library (host pointers)."""
+    x = np.ascontiguousarray(x, np.float32)
+    m, k = x.shape
+    q = np.empty((m, k), np.int8)
+    s = np.empty(m, np.float32)
+    check(lib().syn_quantize_per_channel_int8(ptr(x), m, k, ptr(q), ptr(s)),
+          "syn_quantize_per_channel_int8")
+    return q, s
+
+
+def qgemm_int8(a, b_kn, sa, sb) -> np.ndarray:
+    a = np.ascontiguousarray(a, np.int8)
+    b_kn = np.ascontiguousarray(b_kn, np.int8)
+    m, k = a.shape
+    n = b_kn.shape[1]
+    c = np.zeros((m, n), np.float32)
+    sa = np.ascontiguousarray(sa, np.float32)
+    sb = np.ascontiguousarray(sb, np.float32)
+    check(lib().syn_qgemm_int8(m, n, k, ptr(a), k, ptr(b_kn), n, ptr(c), n, ptr(sa), ptr(sb)),
+          "syn_qgemm_int8")
+    return c
+
+
+def q4_0_gemv(a: np.ndarray, packed: np.ndarray, n: int) -> np.ndarray:
+    a = np.ascontiguousarray(a, np.float32)
+    packed = np.ascontiguousarray(packed, np.uint8)
+    c = np.zeros(n, np.float32)
+    check(lib().syn_q4_0_gemv(n, a.shape[0], ptr(a), ptr(packed), ptr(c)), "syn_q4_0_gemv")
+    return c
+
+
+# ------------------------------------------------------------------ handles
+class QLinear:
+    """Device-resident quantized linear (INT8 W8A8 or Q4_0)."""
+
+    def __init__(self, handle, fmt):
+        self.h = handle
+        self.fmt = fmt
+        n, k, f, wb = SZ(), SZ(), C.c_int(), SZ()
+        check(lib().syn_hip_qlinear_info(self.h, C.byref(n), C.byref(k), C.byref(f),
+                                         C.byref(wb)))
+        self.n, self.k, self.weight_bytes = n.value, k.value, wb.value
+
+    @classmethod
+    def from_f32(cls, fmt: int, w_nk: np.ndarray) -> "QLinear":
+        w_nk = np.ascontiguousarray(w_nk, np.float32)
+        h = C.c_void_p()
+        check(lib().syn_hip_qlinear_from_f32(fmt, w_nk.shape[0], w_nk.shape[1], ptr(w_nk),
+                                             C.byref(h)), "qlinear_from_f32")
+        return cls(h.value, fmt)
+
+    @classmethod
+    def int8(cls, weights: np.ndarray, scales: np.ndarray, layout: int = LAYOUT_KN) -> "QLinear":
+        weights = np.ascontiguousarray(weights, np.int8)
+        scales = np.ascontiguousarray(scales, np.float32)
+        if layout == LAYOUT_KN:
+            k, n = weights.shape
+        else:
+            n, k = weights.shape
+        h = C.c_void_p()
+        check(lib().syn_hip_qlinear_create(FMT_INT8, n, k, ptr(weights), ptr(scales), layout,
+                                           C.byref(h)), "qlinear_create")
+        return cls(h.value, FMT_INT8)
+
+    @classmethod
+    def q4_0(cls, packed: np.ndarray, n: int, k: int) -> "QLinear":
+        packed = np.ascontiguousarray(packed, np.uint8)
+        h = C.c_void_p()
+        check(lib().syn_hip_qlinear_create(FMT_Q4_0, n, k, ptr(packed), None, 0, C.byref(h)),
+              "qlinear_create")
+        return cls(h.value, FMT_Q4_0)
+
+    def forward_dev(self, m: int, d_x: int, d_y: int, stream=None):
+        check(lib().syn_hip_qlinear_forward(self.h, m, d_x, d_y, stream), "qlinear_forward")
+
+    def forward_pre_quantized_dev(self, m, d_xq, ldxq, d_sx, d_y, stream=None):
+        check(lib().syn_hip_qlinear_forward_pre_quantized(self.h, m, d_xq, ldxq, d_sx, d_y,
+                                                          stream), "forward_pre_quantized")
+
+    def forward(self, x: np.ndarray) -> np.ndarray:
+        """Host convenience: upload x [m,k], run, download y [m,n]."""
+        x = np.ascontiguousarray(x, np.float32)
+        m = x.shape[0]
+        dx = DeviceBuffer.from_array(x)
+        dy = DeviceBuffer(m * self.n * 4)
+        self.forward_dev(m, dx.ptr, dy.ptr)
+        check(lib().syn_hip_stream_synchronize(None))
+        return dy.download((m, self.n), np.float32)
+
+    def close(self):
+        if self.h:
+            lib().syn_hip_qlinear_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class QuantizedCausalLM:
+    """Device-resident INT8 W8A8 decoder (mirror of QuantizedCausalLM)."""
+
+    def __init__(self, cfg: dict):
+        self.cfg = dict(cfg)
+        c = LmConfig(cfg["hidden"], cfg["n_layers"], cfg["n_heads"], cfg["n_kv_heads"],
+                     cfg["head_dim"], cfg["inter"], cfg["vocab"], cfg["max_seq"],
+                     cfg.get("eps", 1e-6), cfg.get("rope_theta", 1e6))
+        h = C.c_void_p()
+        check(lib().syn_hip_qlm_create(C.byref(c), C.byref(h)), "qlm_create")
+        self.h = h.value
+
+    def init_synthetic(self, seed_base: int = 0x5EED0000, std: float = 0.02):
+        check(lib().syn_hip_qlm_init_synthetic(self.h, seed_base, std), "qlm_init_synthetic")
+        check(lib().syn_hip_qlm_finalize(self.h), "qlm_finalize")
+
+    def set_weights(self, embed: np.ndarray, layers: list):
+        check(lib().syn_hip_qlm_set_embed(self.h, ptr(np.ascontiguousarray(embed, np.float32))))
+        for i, lw in enumerate(layers):
+            arrs = [np.ascontiguousarray(lw[n], np.float32)
+                    for n in ("q", "k", "v", "o", "gate", "up", "down")]
+            check(lib().syn_hip_qlm_set_layer(self.h, i, *[ptr(a) for a in arrs]), "set_layer")
+        check(lib().syn_hip_qlm_finalize(self.h), "qlm_finalize")
+
+    def reset(self):
+        check(lib().syn_hip_qlm_reset(self.h))
+
+    def prefill(self, ids) -> np.ndarray:
+        ids = np.ascontiguousarray(ids, np.uint32)
+        logits = np.empty(self.cfg["vocab"], np.float32)
+        check(lib().syn_hip_qlm_forward_prefill(self.h, ptr(ids), ids.size, ptr(logits)),
+              "forward_prefill")
+        return logits
+
+    def forward_one(self, token: int) -> np.ndarray:
+        logits = np.empty(self.cfg["vocab"], np.float32)
+        check(lib().syn_hip_qlm_forward_one(self.h, int(token), ptr(logits)), "forward_one")
+        return logits
+
+    def generate(self, prompt, max_new: int):
+        prompt = np.ascontiguousarray(prompt, np.uint32)
+        toks = np.zeros(max_new, np.uint32)
+        margins = np.zeros(max_new, np.float32)
+        check(lib().syn_hip_qlm_generate(self.h, ptr(prompt), prompt.size, max_new, ptr(toks),
+                                         ptr(margins)), "generate")
+        return toks, margins
+
+    def decode_timed(self, steps: int) -> float:
+        ms = C.c_float()
+        check(lib().syn_hip_qlm_decode_timed(self.h, steps, C.byref(ms)), "decode_timed")
+        return ms.value
+
+    def time_lm_head(self, iters: int = 20, flush_bytes: int = 512 << 20) -> float:
+        ms = C.c_float()
+        check(lib().syn_hip_qlm_time_lm_head(self.h, iters, flush_bytes, C.byref(ms)),
+              "time_lm_head")
+        return ms.value
+
+    def close(self):
+        if self.h:
+            lib().syn_hip_qlm_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def fill_normal(n: int, seed: int, std: float = 1.0) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    check(lib().syn_hip_fill_normal(ptr(out), n, seed, std))
+    return out

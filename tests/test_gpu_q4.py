@@ -1,0 +1,72 @@
+"""Q4_0 GEMV parity on the GPU: max_j|y-r| / max_j|r| <= 1e-3 per output row
+set (north-star float tolerance) against the oracle's q4_0GemvRow."""
+import numpy as np
+import pytest
+
+import oracle as O
+from synapse_amd import hip
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3  # north star: max relative error per row, metric max|y-r| / max|r|
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    hip.init(0)
+
+
+def _rel(got, want):
+    return float(np.abs(got - want).max() / max(np.abs(want).max(), 1e-30))
+
+
+def _random_packed(n, k, seed):
+    """Random Q4_0 blocks: nibbles uniform, f16 scales ~ N(0,0.02)/7 magnitudes."""
+    rng = np.random.default_rng(seed)
+    b = k // 32
+    blocks = rng.integers(0, 256, (n, b, 18), dtype=np.uint8)
+    sc = (np.abs(rng.standard_normal((n, b))) * 0.006 + 1e-4).astype(np.float16)
+    blocks[:, :, 0:2] = sc.view(np.uint8).reshape(n, b, 2)
+    return blocks.reshape(-1)
+
+
+@pytest.mark.parametrize("n,k", [(16, 64), (67, 2048), (5, 32), (3, 96), (64, 128)])
+def test_q4_gemv_from_f32_weights(n, k):
+    w = O.normal(n * k, n * 3 + k, 0.02).reshape(n, k)
+    a = O.normal(k, k + 1, 1.0)
+    packed = O.q4_pack(w)
+    got = hip.q4_0_gemv(a, packed, n)
+    want = O.q4_0_gemv(a, packed, n)
+    assert _rel(got, want) <= TOL * 1e-2  # observed ~1e-7; tolerance is 1e-3
+
+
+# LLaMA-3.2-1B shapes of the Q4_0 microbench (K -> N)
+@pytest.mark.parametrize("k,n", [(2048, 2048), (2048, 512), (2048, 8192), (8192, 2048),
+                                 (2048, 128256)])
+def test_q4_gemv_llama_shapes(k, n):
+    packed = _random_packed(n, k, k + n)
+    a = O.normal(k, 5, 1.0)
+    got = hip.q4_0_gemv(a, packed, n)
+    want = O.q4_0_gemv(a, packed, n)
+    assert _rel(got, want) <= TOL
+
+
+def test_q4_handle_multi_row():
+    n, k, m = 1000, 2048, 5
+    w = O.normal(n * k, 77, 0.02).reshape(n, k)
+    x = O.normal(m * k, 78, 1.0).reshape(m, k)
+    lin = hip.QLinear.from_f32(hip.FMT_Q4_0, w)
+    got = lin.forward(x)
+    packed = O.q4_pack(w)
+    for i in range(m):
+        assert _rel(got[i], O.q4_0_gemv(x[i], packed, n)) <= TOL * 1e-2
+
+
+def test_q4_errors():
+    L = hip.lib()
+    a = np.zeros(40, np.float32)
+    c = np.zeros(2, np.float32)
+    b = np.zeros(100, np.uint8)
+    assert L.syn_q4_0_gemv(2, 40, hip.ptr(a), hip.ptr(b), hip.ptr(c)) == 4  # k % 32
+    assert L.syn_q4_0_gemv(0, 32, hip.ptr(a), hip.ptr(b), hip.ptr(c)) == 0
+    assert L.syn_q4_0_gemv(2, 32, None, hip.ptr(b), hip.ptr(c)) == 1
