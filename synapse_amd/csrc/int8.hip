@@ -196,6 +196,7 @@ static const gemv_launcher kGemvLaunch[17] = {
 
 syn_status_t QLinearInt8::ensure_part(size_t elems) {
   if (part_elems >= elems) return SYN_OK;
+  SYN_HIP(hipDeviceSynchronize());  // the old buffer may still be read by queued work
   SYN_TRY(part.alloc(elems * sizeof(int)));
   part_elems = elems;
   return SYN_OK;
@@ -397,6 +398,7 @@ syn_status_t syn_hip_qlinear_forward(syn_hip_qlinear_t *h, size_t m, const float
   QLinearInt8 &L = h->i8;
   const size_t ldq = (size_t)L.chunks * 16;
   if (L.xq_rows < m) {
+    SYN_HIP(hipDeviceSynchronize());
     SYN_TRY(L.xq.alloc(m * ldq));
     SYN_TRY(L.sx.alloc(m * sizeof(float)));
     SYN_HIP(hipMemsetAsync(L.xq.p, 0, m * ldq, s));

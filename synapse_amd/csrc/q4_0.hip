@@ -129,6 +129,7 @@ syn_status_t QLinearQ4_0::gemv(size_t m, const float *d_x, size_t ldx, float *d_
     const int mb = (int)std::min<size_t>(8, m - m0);
     if (p.ksplit > 1 && part_elems < (size_t)p.ksplit * mb * N64) {
       part_elems = (size_t)p.ksplit * mb * N64;
+      SYN_HIP(hipDeviceSynchronize());
       SYN_TRY(part.alloc(part_elems * sizeof(float)));
     }
     kQ4Launch[mb](p, nib.as<u32x4>(), sc.as<uint16_t>(), d_x + m0 * ldx, (int)ldx,

@@ -201,7 +201,9 @@ struct syn_hip_qlm_s {
 
   syn_status_t set_state(int pos, uint32_t token, int step) {
     StepState hs{pos, token, step, 0.0f};
+    // synchronous: hs lives on this stack frame
     SYN_HIP(hipMemcpyAsync(state.p, &hs, sizeof(hs), hipMemcpyHostToDevice, stream));
+    SYN_HIP(hipStreamSynchronize(stream));
     return SYN_OK;
   }
 
