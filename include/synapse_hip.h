@@ -136,6 +136,13 @@ syn_status_t syn_hip_qlinear_forward_pre_quantized(syn_hip_qlinear_t *h, size_t 
 syn_status_t syn_hip_qlinear_info(const syn_hip_qlinear_t *h, size_t *n, size_t *k, int *fmt,
                                   size_t *weight_bytes);
 syn_status_t syn_hip_qlinear_destroy(syn_hip_qlinear_t *h);
+/* Benchmark helper: average ms per forward of `iters` launches on the
+ * library stream (hipEvents around the batch), activations from d_x/d_xq.
+ * INT8 times forward_pre_quantized (d_xq, ldxq, d_sx); other formats time
+ * forward (d_x). */
+syn_status_t syn_hip_qlinear_time(syn_hip_qlinear_t *h, size_t m, const float *d_x,
+                                  const int8_t *d_xq, size_t ldxq, const float *d_sx, float *d_y,
+                                  size_t iters, float *avg_ms);
 
 /* -- INT8 W8A8 causal LM: QuantizedCausalLM (quantization/lm/int8.rs),
  *    device-resident like MetalModelBuffers + gpu_forward_all_layers

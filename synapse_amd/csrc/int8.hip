@@ -205,19 +205,17 @@ syn_status_t QLinearInt8::ensure_part(size_t elems) {
 syn_status_t QLinearInt8::prepare(size_t max_m) {
   const size_t mb = std::min<size_t>(16, std::max<size_t>(1, max_m));
   const GemvPlan p = make_gemv_plan(n, (size_t)chunks, false);
-  size_t need = p.ksplit > 1 ? (size_t)p.ksplit * mb * p.panels * 64 : 0;
-  if (max_m > 16 && chunks > 32) {
-    const GemvPlan pc = make_gemv_plan(n, (size_t)chunks, true);
-    need = std::max(need, (size_t)pc.ksplit * 16 * pc.panels * 64);
-  }
+  const size_t need = p.ksplit > 1 ? (size_t)p.ksplit * mb * p.panels * 64 : 0;
   return need ? ensure_part(need) : SYN_OK;
 }
 
 syn_status_t QLinearInt8::gemv(size_t m, const int8_t *d_xq, size_t ldx, const float *d_sx,
                                float *d_y, size_t ldy, hipStream_t s) {
   if (m == 0 || n == 0 || k == 0) return SYN_OK;
-  const bool chunked = m > 16;  // qmatmul.zig:61-68
-  const GemvPlan p = make_gemv_plan(n, (size_t)chunks, chunked && chunks > 32);
+  if (m > 16)  // qmatmul.zig:68-99: packed GEMM with the KC-chunked epilogue -> MFMA kernel
+    return launch_gemm_w8a8(d_xq, ldx, d_sx, m, w.p, scales.as<float>(), n, chunks, d_y, ldy, s);
+  const bool chunked = false;  // M <= 16 runs int8GemvRow per row (qmatmul.zig:54-66)
+  const GemvPlan p = make_gemv_plan(n, (size_t)chunks, false);
   const size_t N64 = (size_t)p.panels * 64;
   for (size_t m0 = 0; m0 < m; m0 += 16) {
     const int mb = (int)std::min<size_t>(16, m - m0);
@@ -416,6 +414,37 @@ syn_status_t syn_hip_qlinear_info(const syn_hip_qlinear_t *h, size_t *n, size_t 
   if (k) *k = i8 ? h->i8.k : h->q4.k;
   if (fmt) *fmt = h->fmt;
   if (weight_bytes) *weight_bytes = i8 ? h->i8.weight_bytes() : h->q4.weight_bytes();
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_qlinear_time(syn_hip_qlinear_t *h, size_t m, const float *d_x,
+                                  const int8_t *d_xq, size_t ldxq, const float *d_sx, float *d_y,
+                                  size_t iters, float *avg_ms) {
+  if (!h || !avg_ms) return SYN_ERR_NULL_PTR;
+  if (iters == 0 || m == 0) return SYN_ERR_INVALID_ARG;
+  SYN_TRY(ensure_init());
+  hipStream_t s = default_stream();
+  auto run = [&]() -> syn_status_t {
+    if (h->fmt == SYN_HIP_FMT_INT8)
+      return syn_hip_qlinear_forward_pre_quantized(h, m, d_xq, ldxq, d_sx, d_y, s);
+    return syn_hip_qlinear_forward(h, m, d_x, d_y, s);
+  };
+  SYN_TRY(run());  // warm-up (and any one-time scratch allocation)
+  SYN_HIP(hipStreamSynchronize(s));
+  hipEvent_t a, b;
+  SYN_HIP(hipEventCreate(&a));
+  SYN_HIP(hipEventCreate(&b));
+  SYN_HIP(hipEventRecord(a, s));
+  syn_status_t st = SYN_OK;
+  for (size_t i = 0; i < iters && st == SYN_OK; i++) st = run();
+  SYN_HIP(hipEventRecord(b, s));
+  SYN_HIP(hipEventSynchronize(b));
+  float ms = 0.0f;
+  SYN_HIP(hipEventElapsedTime(&ms, a, b));
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  SYN_TRY(st);
+  *avg_ms = ms / (float)iters;
   return SYN_OK;
 }
 

@@ -58,6 +58,11 @@ struct QLinearInt8 {
 syn_status_t launch_quantize_rows(const float *d_x, size_t m, size_t k, size_t ldx, int8_t *d_q,
                                   size_t ldq, float *d_s, hipStream_t s);
 
+// INT8 MFMA GEMM for M > 16 (int8_gemm.hip); W in the panel layout
+syn_status_t launch_gemm_w8a8(const int8_t *xq, size_t ldx, const float *sx, size_t M,
+                              const void *W, const float *ws, size_t N, int C, float *y,
+                              size_t ldy, hipStream_t s);
+
 // host-side reference quantizers (used at load time)
 void host_minmax_scales(const float *w, size_t ch, size_t chsz, float *scales);
 void host_quantize_weights_nk(const float *w, const float *scales, size_t n, size_t k,

@@ -63,6 +63,7 @@ SIGNATURES = {
     "syn_hip_qlinear_info": (ST, [P, C.POINTER(SZ), C.POINTER(SZ), C.POINTER(C.c_int),
                                   C.POINTER(SZ)]),
     "syn_hip_qlinear_destroy": (ST, [P]),
+    "syn_hip_qlinear_time": (ST, [P, SZ, P, P, SZ, P, P, SZ, C.POINTER(C.c_float)]),
     "syn_hip_qlm_create": (ST, [C.POINTER(LmConfig), C.POINTER(P)]),
     "syn_hip_qlm_set_embed": (ST, [P, P]),
     "syn_hip_qlm_set_layer": (ST, [P, C.c_uint32, P, P, P, P, P, P, P]),
@@ -278,6 +279,13 @@ class QLinear:
     def forward_pre_quantized_dev(self, m, d_xq, ldxq, d_sx, d_y, stream=None):
         check(lib().syn_hip_qlinear_forward_pre_quantized(self.h, m, d_xq, ldxq, d_sx, d_y,
                                                           stream), "forward_pre_quantized")
+
+    def time(self, m: int, d_x=None, d_xq=None, ldxq=0, d_sx=None, d_y=None,
+             iters: int = 20) -> float:
+        ms = C.c_float()
+        check(lib().syn_hip_qlinear_time(self.h, m, d_x, d_xq, ldxq, d_sx, d_y, iters,
+                                         C.byref(ms)), "qlinear_time")
+        return ms.value
 
     def forward(self, x: np.ndarray) -> np.ndarray:
         """Host convenience: upload x [m,k], run, download y [m,n]."""

@@ -159,3 +159,23 @@ def test_device_expf_matches_glibc():
     idx = rng.choice(x.size, 200_000, replace=False)
     ref = np.array([libm.expf(float(v)) for v in x[idx]], np.float32)
     np.testing.assert_array_equal(_bits(got[idx]), _bits(ref))
+
+
+@pytest.mark.parametrize("m,k,n", [(128, 1024, 3072), (300, 2048, 1000), (17, 4096, 513),
+                                   (256, 4096, 1024)])
+def test_int8_gemm_mfma_bit_exact(m, k, n):
+    # M > 16: v_mfma_i32_16x16x64_i8 tiles with the KC=512 chunked epilogue
+    rng = np.random.default_rng(m + k + n)
+    q_nk = rng.integers(-128, 128, (n, k), dtype=np.int8)
+    s = rng.uniform(1e-4, 1e-2, n).astype(np.float32)
+    lin = hip.QLinear.int8(q_nk, s, hip.LAYOUT_NK)
+    xq = rng.integers(-127, 128, (m, k), dtype=np.int8)
+    sx = rng.uniform(1e-3, 0.1, m).astype(np.float32)
+    dxq = hip.DeviceBuffer.from_array(xq)
+    dsx = hip.DeviceBuffer.from_array(sx)
+    dy = hip.DeviceBuffer(m * n * 4)
+    lin.forward_pre_quantized_dev(m, dxq.ptr, k, dsx.ptr, dy.ptr)
+    hip.check(hip.lib().syn_hip_stream_synchronize(None))
+    got = dy.download((m, n), np.float32)
+    want = O.qgemm_int8(xq, np.ascontiguousarray(q_nk.T), sx, s)
+    np.testing.assert_array_equal(_bits(got), _bits(want))
