@@ -107,6 +107,11 @@ syn_status_t syn_hip_quantize_rows(const float *d_x, size_t m, size_t k, size_t 
  * (q4_linear.rs:52-150, pack_for_zig byte format). */
 #define SYN_HIP_FMT_INT8 1
 #define SYN_HIP_FMT_Q4_0 2
+/* GGUF block formats (values defined by weight_loading/gguf.rs:255-487); the
+ * reference dequantizes them to f32 at load and runs f32 matmul_t. */
+#define SYN_HIP_FMT_Q8_0 3
+#define SYN_HIP_FMT_Q4_K 4
+#define SYN_HIP_FMT_Q6_K 5
 /* host weight layouts accepted by syn_hip_qlinear_create for INT8 */
 #define SYN_HIP_LAYOUT_KN 0 /* reference QuantizedLinear::weights_int8 [K,N] */
 #define SYN_HIP_LAYOUT_NK 1 /* row per output feature [N,K] */
@@ -115,7 +120,9 @@ typedef struct syn_hip_qlinear_s syn_hip_qlinear_t;
 
 /* Repack already-quantized host weights once into HBM.
  *   INT8: host_weights int8 in `layout`, host_scales f32[n].
- *   Q4_0: host_weights = pack_for_zig bytes [n, k/32, 18]; host_scales unused. */
+ *   Q4_0: host_weights = pack_for_zig bytes [n, k/32, 18]; host_scales unused.
+ *   Q8_0/Q4_K/Q6_K: GGUF block bytes of the row-major [n,k] tensor
+ *   (k a multiple of 32 / 256); host_scales unused. */
 syn_status_t syn_hip_qlinear_create(int fmt, size_t n, size_t k, const void *host_weights,
                                     const float *host_scales, int layout,
                                     syn_hip_qlinear_t **out);
@@ -191,6 +198,12 @@ syn_status_t syn_hip_qlm_time_lm_head(syn_hip_qlm_t *m, size_t iters, size_t flu
 syn_status_t syn_hip_qlm_destroy(syn_hip_qlm_t *m);
 
 /* -- harness helpers (no reference counterpart) -- */
+/* Encode f32 [n,k] into Q8_0 / Q4_K / Q6_K block bytes.  The reference has no
+ * encoder for these formats (only dequantizers); any encoding is valid since
+ * its dequantizer defines the values.  host_out holds n*(k/32)*34 (Q8_0),
+ * n*(k/256)*144 (Q4_K) or n*(k/256)*210 (Q6_K) bytes. */
+syn_status_t syn_hip_kquant_encode(int fmt, size_t n, size_t k, const float *host_w,
+                                   uint8_t *host_out);
 /* Diagnostic: y[i] = the device expf that SiLU and softmax use (bit-identical
  * to glibc expf, which Rust's f32::exp calls on Linux). */
 syn_status_t syn_hip_eval_expf(const float *d_x, float *d_y, size_t n, void *stream);

@@ -11,6 +11,7 @@
 #include <cmath>
 #include <vector>
 
+#include "kquant.hpp"
 #include "linear.hpp"
 
 namespace syn {
@@ -311,7 +312,12 @@ struct syn_hip_qlinear_s {
   int fmt = 0;
   QLinearInt8 i8;
   QLinearQ4_0 q4;
+  QLinearKQ kq;
 };
+
+static bool is_kq(int fmt) {
+  return fmt == SYN_HIP_FMT_Q8_0 || fmt == SYN_HIP_FMT_Q4_K || fmt == SYN_HIP_FMT_Q6_K;
+}
 
 extern "C" {
 
@@ -343,6 +349,9 @@ syn_status_t syn_hip_qlinear_create(int fmt, size_t n, size_t k, const void *hos
       st = SYN_ERR_INVALID_ARG;
   } else if (fmt == SYN_HIP_FMT_Q4_0) {
     st = (k % 32) ? SYN_ERR_SHAPE_MISMATCH : h->q4.upload_packed((const uint8_t *)host_weights, n, k);
+  } else if (is_kq(fmt)) {
+    st = (k % kq_block_elems(fmt)) ? SYN_ERR_SHAPE_MISMATCH
+                                   : h->kq.upload(fmt, (const uint8_t *)host_weights, n, k);
   } else {
     st = SYN_ERR_INVALID_ARG;
   }
@@ -364,6 +373,8 @@ syn_status_t syn_hip_qlinear_from_f32(int fmt, size_t n, size_t k, const float *
   syn_status_t st;
   if (fmt == SYN_HIP_FMT_INT8) st = h->i8.from_f32(host_w, n, k);
   else if (fmt == SYN_HIP_FMT_Q4_0) st = (k % 32) ? SYN_ERR_SHAPE_MISMATCH : h->q4.from_f32(host_w, n, k);
+  else if (is_kq(fmt))
+    st = (k % kq_block_elems(fmt)) ? SYN_ERR_SHAPE_MISMATCH : h->kq.from_f32(fmt, host_w, n, k);
   else st = SYN_ERR_INVALID_ARG;
   if (st != SYN_OK) {
     delete h;
@@ -392,6 +403,7 @@ syn_status_t syn_hip_qlinear_forward(syn_hip_qlinear_t *h, size_t m, const float
   if (!d_x || !d_y) return SYN_ERR_NULL_PTR;
   hipStream_t s = pick_stream(stream);
   if (h->fmt == SYN_HIP_FMT_Q4_0) return h->q4.gemv(m, d_x, h->q4.k, d_y, h->q4.n, s);
+  if (is_kq(h->fmt)) return h->kq.gemv(m, d_x, h->kq.k, d_y, h->kq.n, s);
   if (h->fmt != SYN_HIP_FMT_INT8) return SYN_ERR_INVALID_ARG;
   QLinearInt8 &L = h->i8;
   const size_t ldq = (size_t)L.chunks * 16;
@@ -409,11 +421,18 @@ syn_status_t syn_hip_qlinear_forward(syn_hip_qlinear_t *h, size_t m, const float
 syn_status_t syn_hip_qlinear_info(const syn_hip_qlinear_t *h, size_t *n, size_t *k, int *fmt,
                                   size_t *weight_bytes) {
   if (!h) return SYN_ERR_NULL_PTR;
-  const bool i8 = h->fmt == SYN_HIP_FMT_INT8;
-  if (n) *n = i8 ? h->i8.n : h->q4.n;
-  if (k) *k = i8 ? h->i8.k : h->q4.k;
+  size_t nn, kk, wb;
+  if (h->fmt == SYN_HIP_FMT_INT8) {
+    nn = h->i8.n; kk = h->i8.k; wb = h->i8.weight_bytes();
+  } else if (h->fmt == SYN_HIP_FMT_Q4_0) {
+    nn = h->q4.n; kk = h->q4.k; wb = h->q4.weight_bytes();
+  } else {
+    nn = h->kq.n; kk = h->kq.k; wb = h->kq.weight_bytes();
+  }
+  if (n) *n = nn;
+  if (k) *k = kk;
   if (fmt) *fmt = h->fmt;
-  if (weight_bytes) *weight_bytes = i8 ? h->i8.weight_bytes() : h->q4.weight_bytes();
+  if (weight_bytes) *weight_bytes = wb;
   return SYN_OK;
 }
 

@@ -1,0 +1,502 @@
+// GGUF-block formats Q8_0 / Q4_K / Q6_K (A9-A12): load-time encoder and
+// repack, and the decode GEMV over f32 activations.
+//
+// The reference dequantizes these formats to f32 at load
+// (weight_loading/gguf.rs:217-237) and runs f32 matmul_t (ops/matmul.rs:55-79
+// -> f32GemvRow, matmul.zig:223-305).  Values are therefore defined by its
+// dequantizers, which this file decodes in registers instead:
+//   Q8_0  (gguf.rs:255-288)  34 B / 32:  [d f16][32 x i8]          v = d*q
+//   Q4_K  (gguf.rs:375-431) 144 B / 256: [d][dmin][12 B scales][128 B nibbles]
+//         sub-block s (32): v = n*(d*sc[s]) - dmin*mn[s], element 32s+2i is the
+//         low nibble of byte 16s+i, 32s+2i+1 the high nibble
+//   Q6_K  (gguf.rs:440-487) 210 B / 256: [ql 128][qh 64][sc i8 16][d f16]
+//         q(idx) = ql nibble idx%2 of byte idx/2 | (qh byte idx/4 >> 2*(idx%4) & 3)<<4,
+//         v = (q-32) * (sc[idx/16]*d)
+// with f16 decoded by the Rust converter (converter.rs:12-40; subnormals halve).
+// Float outputs carry the north star's 1e-3 per-row tolerance.
+//
+// HBM layout: blocks of 64 output rows (panels) are interleaved in 16-byte
+// planes, plane p of a block holding bytes 16p..16p+15 of every row's block:
+//   Q8_0  2 planes (the 32 quants) + f16 d in a [panel][block][64] array
+//   Q4_K  9 planes (the whole 144-byte superblock)
+//   Q6_K 13 planes (ql, qh, sc) + f16 d in a [panel][block][64] array
+// so every wave64 load (lane = row) is one contiguous 1 KiB.
+#include <algorithm>
+#include <cmath>
+#include <vector>
+
+#include "kquant.hpp"
+
+namespace syn {
+
+// ------------------------------------------------------------------ host f16
+static float h2f_rs(uint16_t h) {  // converter.rs:12-40
+  uint32_t sign = (h >> 15) & 1u, exp = (h >> 10) & 0x1fu, mant = h & 0x3ffu, out;
+  if (exp == 0) {
+    if (mant == 0) {
+      out = sign << 31;
+    } else {
+      uint32_t e = 1, m = mant;
+      while ((m & 0x400u) == 0) { m <<= 1; e++; }
+      out = (sign << 31) | ((127u - 15u + 1u - e) << 23) | ((m & 0x3ffu) << 13);
+    }
+  } else if (exp == 31) {
+    out = (sign << 31) | (0xffu << 23) | (mant << 13);
+  } else {
+    out = (sign << 31) | ((exp + 127u - 15u) << 23) | (mant << 13);
+  }
+  float f;
+  std::memcpy(&f, &out, 4);
+  return f;
+}
+
+// f32 -> f16, round to nearest even (encoder side; normal range only is used)
+static uint16_t f2h_rne(float v) {
+  uint32_t x;
+  std::memcpy(&x, &v, 4);
+  const uint32_t sign = (x >> 16) & 0x8000u;
+  x &= 0x7fffffffu;
+  if (x >= 0x47800000u) return (uint16_t)(sign | 0x7c00u);       // overflow -> inf
+  if (x < 0x38800000u) {                                         // below f16 normal range
+    float f;
+    std::memcpy(&f, &x, 4);
+    const float q = f * 16777216.0f;                             // units of 2^-24
+    return (uint16_t)(sign | (uint32_t)std::nearbyint(q));
+  }
+  const uint32_t e = ((x >> 23) - 112u) << 10, m = (x >> 13) & 0x3ffu, rest = x & 0x1fffu;
+  uint32_t h = e | m;
+  if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) h++;
+  return (uint16_t)(sign | h);
+}
+
+// A super-block scale >= v that decodes to a normal f16 (the reference's
+// converter halves subnormals, so the encoder stays out of that range).
+static uint16_t enc_scale(float v, float *decoded) {
+  uint16_t h = f2h_rne(std::fmax(v, 6.103515625e-05f));  // 2^-14, smallest normal
+  while (h2f_rs(h) < v && (h & 0x7fffu) < 0x7bffu) h++;
+  *decoded = h2f_rs(h);
+  return h;
+}
+
+size_t kq_block_bytes(int fmt) {
+  return fmt == SYN_HIP_FMT_Q8_0 ? 34 : fmt == SYN_HIP_FMT_Q4_K ? 144 : 210;
+}
+size_t kq_block_elems(int fmt) { return fmt == SYN_HIP_FMT_Q8_0 ? 32 : 256; }
+
+// ------------------------------------------------------------------ encoders
+// The reference ships dequantizers only; these encoders produce bytes in its
+// formats (any encoder is valid: the dequantizer defines the values).
+static void enc_q8_0(const float *x, uint8_t *b) {
+  float amax = 0.0f;
+  for (int i = 0; i < 32; i++) amax = std::fmax(amax, std::fabs(x[i]));
+  float d;
+  const uint16_t h = enc_scale(amax / 127.0f, &d);
+  b[0] = (uint8_t)(h & 0xff);
+  b[1] = (uint8_t)(h >> 8);
+  for (int i = 0; i < 32; i++) {
+    float q = d > 0.0f ? std::round(x[i] / d) : 0.0f;
+    q = std::min(127.0f, std::max(-127.0f, q));
+    b[2 + i] = (uint8_t)(int8_t)q;
+  }
+}
+
+// Sub-blocks 0-3 get 6-bit scales and 8-bit mins; in the reference's field
+// layout (gguf.rs:405-410) the top two bits of sc[4..7] are also bits 6-7 of
+// mn[4..7], so sub-blocks 4-7 are encoded with 4-bit scales and mins.
+static void enc_q4_k(const float *x, uint8_t *b) {
+  float scale[8], mneg[8];
+  for (int s = 0; s < 8; s++) {
+    float lo = 0.0f, hi = 0.0f;
+    for (int i = 0; i < 32; i++) {
+      lo = std::fmin(lo, x[32 * s + i]);
+      hi = std::fmax(hi, x[32 * s + i]);
+    }
+    scale[s] = (hi - lo) / 15.0f;
+    mneg[s] = -lo;
+  }
+  float dmax = 0.0f, mmax = 0.0f;
+  for (int s = 0; s < 8; s++) {
+    dmax = std::fmax(dmax, scale[s] / (s < 4 ? 63.0f : 15.0f));
+    mmax = std::fmax(mmax, mneg[s] / (s < 4 ? 255.0f : 15.0f));
+  }
+  float d, dmin;
+  const uint16_t dh = enc_scale(dmax, &d), mh = enc_scale(mmax, &dmin);
+  int sc[8], mn[8];
+  for (int s = 0; s < 8; s++) {
+    const int smax = s < 4 ? 63 : 15, mmx = s < 4 ? 255 : 15;
+    sc[s] = d > 0.0f ? (int)std::lround(scale[s] / d) : 0;
+    mn[s] = dmin > 0.0f ? (int)std::lround(mneg[s] / dmin) : 0;
+    sc[s] = std::min(smax, std::max(0, sc[s]));
+    mn[s] = std::min(mmx, std::max(0, mn[s]));
+  }
+  std::memset(b, 0, 144);
+  b[0] = (uint8_t)(dh & 0xff);
+  b[1] = (uint8_t)(dh >> 8);
+  b[2] = (uint8_t)(mh & 0xff);
+  b[3] = (uint8_t)(mh >> 8);
+  uint8_t *sb = b + 4;
+  for (int i = 0; i < 4; i++) {
+    sb[i] = (uint8_t)(sc[i] | ((sc[i + 4] >> 4) << 6));
+    sb[i + 4] = (uint8_t)((sc[i + 4] & 0xf) | ((mn[i] & 0xf) << 4));
+    sb[i + 8] = (uint8_t)((mn[i] >> 4) | ((mn[i + 4] & 0xf) << 4));
+  }
+  for (int s = 0; s < 8; s++) {
+    const float scv = d * (float)sc[s], m = dmin * (float)mn[s];
+    for (int i = 0; i < 16; i++) {
+      int n0 = 0, n1 = 0;
+      if (scv > 0.0f) {
+        n0 = (int)std::lround((x[32 * s + 2 * i] + m) / scv);
+        n1 = (int)std::lround((x[32 * s + 2 * i + 1] + m) / scv);
+      }
+      n0 = std::min(15, std::max(0, n0));
+      n1 = std::min(15, std::max(0, n1));
+      b[16 + 16 * s + i] = (uint8_t)(n0 | (n1 << 4));
+    }
+  }
+}
+
+static void enc_q6_k(const float *x, uint8_t *b) {
+  float sscale[16];
+  float smax = 0.0f;
+  for (int s = 0; s < 16; s++) {
+    float amax = 0.0f;
+    for (int i = 0; i < 16; i++) amax = std::fmax(amax, std::fabs(x[16 * s + i]));
+    sscale[s] = amax / 31.0f;
+    smax = std::fmax(smax, sscale[s]);
+  }
+  float d;
+  const uint16_t dh = enc_scale(smax / 127.0f, &d);
+  std::memset(b, 0, 210);
+  for (int s = 0; s < 16; s++) {
+    int sc = d > 0.0f ? (int)std::lround(sscale[s] / d) : 0;
+    sc = std::min(127, std::max(-127, sc));
+    b[192 + s] = (uint8_t)(int8_t)sc;
+    const float scale = (float)sc * d;
+    for (int i = 0; i < 16; i++) {
+      const int idx = 16 * s + i;
+      int q = scale > 0.0f ? (int)std::lround(x[idx] / scale) + 32 : 32;
+      q = std::min(63, std::max(0, q));
+      b[idx / 2] |= (uint8_t)((q & 0xf) << (4 * (idx % 2)));
+      b[128 + idx / 4] |= (uint8_t)((q >> 4) << (2 * (idx % 4)));
+    }
+  }
+  b[208] = (uint8_t)(dh & 0xff);
+  b[209] = (uint8_t)(dh >> 8);
+}
+
+void kq_encode(int fmt, const float *w, size_t n, size_t k, uint8_t *out) {
+  const size_t be = kq_block_elems(fmt), bb = kq_block_bytes(fmt), nb = k / be;
+  for (size_t r = 0; r < n; r++)
+    for (size_t j = 0; j < nb; j++) {
+      const float *x = w + r * k + j * be;
+      uint8_t *b = out + (r * nb + j) * bb;
+      if (fmt == SYN_HIP_FMT_Q8_0) enc_q8_0(x, b);
+      else if (fmt == SYN_HIP_FMT_Q4_K) enc_q4_k(x, b);
+      else enc_q6_k(x, b);
+    }
+}
+
+// ------------------------------------------------------------------ repack
+static int kq_planes(int fmt) {
+  return fmt == SYN_HIP_FMT_Q8_0 ? 2 : fmt == SYN_HIP_FMT_Q4_K ? 9 : 13;
+}
+
+syn_status_t QLinearKQ::upload(int fmt_, const uint8_t *gguf, size_t n_, size_t k_) {
+  fmt = fmt_;
+  n = n_;
+  k = k_;
+  const size_t be = kq_block_elems(fmt), bb = kq_block_bytes(fmt);
+  blocks = (int)(k / be);
+  planes = kq_planes(fmt);
+  const size_t P = cdiv(n, 64), B = (size_t)blocks, NP = (size_t)planes;
+  std::vector<uint8_t> hp(P * B * NP * 64 * 16, 0);
+  std::vector<uint16_t> hd;
+  const bool sep_d = fmt != SYN_HIP_FMT_Q4_K;
+  if (sep_d) hd.assign(P * B * 64, 0);
+  // padding rows decode to zero: Q8_0 d = 0, Q4_K d = dmin = 0, Q6_K d = 0
+  for (size_t row = 0; row < n; row++) {
+    const size_t p = row / 64, r = row % 64;
+    for (size_t b = 0; b < B; b++) {
+      const uint8_t *src = gguf + (row * B + b) * bb;
+      const uint8_t *qsrc = src;
+      if (fmt == SYN_HIP_FMT_Q8_0) {
+        hd[(p * B + b) * 64 + r] = (uint16_t)(src[0] | (src[1] << 8));
+        qsrc = src + 2;
+      } else if (fmt == SYN_HIP_FMT_Q6_K) {
+        hd[(p * B + b) * 64 + r] = (uint16_t)(src[208] | (src[209] << 8));
+      }
+      for (size_t pl = 0; pl < NP; pl++)
+        std::memcpy(&hp[(((p * B + b) * NP + pl) * 64 + r) * 16], qsrc + pl * 16, 16);
+    }
+  }
+  SYN_TRY(wq.alloc(hp.size()));
+  SYN_HIP(hipMemcpy(wq.p, hp.data(), hp.size(), hipMemcpyHostToDevice));
+  if (sep_d) {
+    SYN_TRY(wd.alloc(hd.size() * 2));
+    SYN_HIP(hipMemcpy(wd.p, hd.data(), hd.size() * 2, hipMemcpyHostToDevice));
+  }
+  return SYN_OK;
+}
+
+syn_status_t QLinearKQ::from_f32(int fmt_, const float *w, size_t n_, size_t k_) {
+  std::vector<uint8_t> bytes(n_ * (k_ / kq_block_elems(fmt_)) * kq_block_bytes(fmt_));
+  kq_encode(fmt_, w, n_, k_, bytes.data());
+  return upload(fmt_, bytes.data(), n_, k_);
+}
+
+size_t QLinearKQ::weight_bytes() const { return n * (size_t)blocks * kq_block_bytes(fmt); }
+
+// ------------------------------------------------------------------ GEMV kernels
+// 8 elements of one dword of low/high nibble pairs: bytes b -> (2b lo, 2b+1 hi)
+__device__ __forceinline__ float kq_dot8_nib(uint32_t w, const float *__restrict__ a, float s) {
+  const uint32_t lo = w & 0x0f0f0f0fu, hi = (w >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+  for (int b = 0; b < 4; b++) {
+    s = __builtin_fmaf(a[2 * b], (float)((lo >> (8 * b)) & 0xffu), s);
+    s = __builtin_fmaf(a[2 * b + 1], (float)((hi >> (8 * b)) & 0xffu), s);
+  }
+  return s;
+}
+
+__device__ __forceinline__ float kq_dot4_i8(uint32_t w, const float *__restrict__ a, float s) {
+#pragma unroll
+  for (int b = 0; b < 4; b++) s = __builtin_fmaf(a[b], (float)(int8_t)(w >> (8 * b)), s);
+  return s;
+}
+
+// activation block sums (per `grp` elements) of this workgroup's K range into LDS
+template <int M>
+__device__ __forceinline__ void kq_asums(const float *__restrict__ x, int ldx, int e0, int ne,
+                                         int grp, float *asum, int stride) {
+  for (int t = threadIdx.x; t < M * (ne / grp); t += blockDim.x) {
+    const int m = t / (ne / grp), g = t - m * (ne / grp);
+    const float *xa = x + (size_t)m * ldx + e0 + g * grp;
+    float s = 0.0f;
+    for (int i = 0; i < grp; i++) s += xa[i];
+    asum[m * stride + g] = s;
+  }
+}
+
+// grid (panels, ksplit); lane = output row; blocks [b0, b1) of this slice
+template <int FMT, int M>
+__global__ void __launch_bounds__(1024)
+    k_gemv_kq(const u32x4 *__restrict__ W, const uint16_t *__restrict__ Wd,
+              const float *__restrict__ x, int ldx, float *__restrict__ y, int ldy,
+              float *__restrict__ part, int N, int B, int bs) {
+  constexpr int NP = FMT == SYN_HIP_FMT_Q8_0 ? 2 : FMT == SYN_HIP_FMT_Q4_K ? 9 : 13;
+  constexpr int BE = FMT == SYN_HIP_FMT_Q8_0 ? 32 : 256;
+  constexpr int GRP = FMT == SYN_HIP_FMT_Q4_K ? 32 : 16;  // asum group (unused for Q8_0)
+  constexpr int GPB = BE / GRP;
+  extern __shared__ float smem[];
+  const int panel = blockIdx.x, ks = blockIdx.y;
+  const int nw = blockDim.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int b0 = ks * bs, b1 = min(B, b0 + bs), nb = b1 - b0;
+  float *asum = smem;                                   // [M][bs*GPB]
+  float *red = smem + (FMT == SYN_HIP_FMT_Q8_0 ? 0 : M * bs * GPB);  // [nw][M][64]
+  if (FMT != SYN_HIP_FMT_Q8_0) {
+    kq_asums<M>(x, ldx, b0 * BE, nb * BE, GRP, asum, bs * GPB);
+    __syncthreads();
+  }
+  float acc[M];
+#pragma unroll
+  for (int m = 0; m < M; m++) acc[m] = 0.0f;
+  const size_t pbase = (size_t)panel * B;
+  for (int b = b0 + wave; b < b1; b += nw) {
+    const u32x4 *Wb = W + ((pbase + b) * NP) * 64 + lane;
+    if (FMT == SYN_HIP_FMT_Q8_0) {
+      const u32x4 q0 = __builtin_nontemporal_load(Wb);
+      const u32x4 q1 = __builtin_nontemporal_load(Wb + 64);
+      const float d = syn_f16_to_f32_rs(Wd[(pbase + b) * 64 + lane]);
+#pragma unroll
+      for (int m = 0; m < M; m++) {
+        const float *xa = x + (size_t)m * ldx + (size_t)b * 32;
+        float s = 0.0f;
+        s = kq_dot4_i8(q0.x, xa, s);
+        s = kq_dot4_i8(q0.y, xa + 4, s);
+        s = kq_dot4_i8(q0.z, xa + 8, s);
+        s = kq_dot4_i8(q0.w, xa + 12, s);
+        s = kq_dot4_i8(q1.x, xa + 16, s);
+        s = kq_dot4_i8(q1.y, xa + 20, s);
+        s = kq_dot4_i8(q1.z, xa + 24, s);
+        s = kq_dot4_i8(q1.w, xa + 28, s);
+        acc[m] = __builtin_fmaf(s, d, acc[m]);
+      }
+    } else if (FMT == SYN_HIP_FMT_Q4_K) {
+      u32x4 pl[9];
+#pragma unroll
+      for (int p = 0; p < 9; p++) pl[p] = __builtin_nontemporal_load(Wb + p * 64);
+      const float d = syn_f16_to_f32_rs(pl[0].x & 0xffffu);
+      const float dmin = syn_f16_to_f32_rs(pl[0].x >> 16);
+      // 12 scale bytes = bytes 4..15 of plane 0 (gguf.rs:405-410, u8 arithmetic)
+      uint32_t sbw[3] = {pl[0].y, pl[0].z, pl[0].w};
+      auto SB = [&](int i) -> uint32_t { return (sbw[i >> 2] >> (8 * (i & 3))) & 0xffu; };
+#pragma unroll
+      for (int s = 0; s < 8; s++) {
+        uint32_t sc, mn;
+        if (s < 4) {
+          sc = SB(s) & 63u;
+          mn = ((SB(s + 4) >> 4) | ((SB(s + 8) & 15u) << 4)) & 0xffu;
+        } else {
+          sc = (SB(s) & 15u) | ((SB(s - 4) >> 6) << 4);
+          mn = ((SB(s + 4) >> 4) | (((SB(s - 4) >> 4) & 12u) << 4)) & 0xffu;
+        }
+        const float scf = d * (float)sc;
+        const float mf = dmin * (float)mn;
+        const u32x4 q = pl[1 + s];
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+          const float *xa = x + (size_t)m * ldx + (size_t)b * 256 + s * 32;
+          float t = 0.0f;
+          t = kq_dot8_nib(q.x, xa, t);
+          t = kq_dot8_nib(q.y, xa + 8, t);
+          t = kq_dot8_nib(q.z, xa + 16, t);
+          t = kq_dot8_nib(q.w, xa + 24, t);
+          const float as = asum[m * bs * GPB + (b - b0) * GPB + s];
+          acc[m] = __builtin_fmaf(scf, t, acc[m]);
+          acc[m] = __builtin_fmaf(-mf, as, acc[m]);
+        }
+      }
+    } else {  // Q6_K
+      u32x4 pl[13];
+#pragma unroll
+      for (int p = 0; p < 13; p++) pl[p] = __builtin_nontemporal_load(Wb + p * 64);
+      const float d = syn_f16_to_f32_rs(Wd[(pbase + b) * 64 + lane]);
+      const uint32_t scw[4] = {pl[12].x, pl[12].y, pl[12].z, pl[12].w};
+#pragma unroll
+      for (int s = 0; s < 16; s++) {
+        // ql bytes 8s..8s+7: plane s/2, dwords 2*(s%2), 2*(s%2)+1
+        const u32x4 qp = pl[s >> 1];
+        const uint32_t lo0 = (s & 1) ? qp.z : qp.x, lo1 = (s & 1) ? qp.w : qp.y;
+        // qh bytes 4s..4s+3: plane 8 + s/4, dword s%4
+        const u32x4 hp = pl[8 + (s >> 2)];
+        const uint32_t hi = (s & 3) == 0 ? hp.x : (s & 3) == 1 ? hp.y : (s & 3) == 2 ? hp.z : hp.w;
+        const float scale = (float)(int8_t)(scw[s >> 2] >> (8 * (s & 3))) * d;
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+          const float *xa = x + (size_t)m * ldx + (size_t)b * 256 + s * 16;
+          float t = 0.0f;
+#pragma unroll
+          for (int i = 0; i < 16; i++) {
+            const uint32_t lo = ((i < 8 ? lo0 : lo1) >> (4 * (i & 7))) & 15u;
+            const uint32_t h2 = (hi >> (2 * i)) & 3u;
+            t = __builtin_fmaf(xa[i], (float)(lo | (h2 << 4)), t);
+          }
+          const float as = asum[m * bs * GPB + (b - b0) * GPB + s];
+          const float v = t - 32.0f * as;
+          acc[m] = __builtin_fmaf(v, scale, acc[m]);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < M; m++) red[(wave * M + m) * 64 + lane] = acc[m];
+  __syncthreads();
+  const int N64 = gridDim.x * 64;
+  for (int t = threadIdx.x; t < M * 64; t += blockDim.x) {
+    const int m = t >> 6, r = t & 63;
+    float s = 0.0f;
+    for (int w = 0; w < nw; w++) s += red[(w * M + m) * 64 + r];
+    const int row = panel * 64 + r;
+    if (gridDim.y == 1) {
+      if (row < N) y[(size_t)m * ldy + row] = s;
+    } else {
+      part[((size_t)ks * M + m) * N64 + row] = s;
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256)
+    k_kq_reduce(const float *__restrict__ part, int ksplit, int M, int N, int N64,
+                float *__restrict__ y, int ldy) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= M * N) return;
+  const int m = idx / N, row = idx - m * N;
+  float s = 0.0f;
+  for (int k = 0; k < ksplit; k++) s += part[((size_t)k * M + m) * N64 + row];
+  y[(size_t)m * ldy + row] = s;
+}
+
+template <int FMT, int M>
+static void launch_kq(const GemvPlan &p, const void *W, const uint16_t *Wd, const float *x,
+                      int ldx, float *y, int ldy, float *part, int N, hipStream_t s) {
+  constexpr int BE = FMT == SYN_HIP_FMT_Q8_0 ? 32 : 256;
+  constexpr int GRP = FMT == SYN_HIP_FMT_Q4_K ? 32 : 16;
+  const int waves = std::min(p.waves, M >= 4 ? 8 : 16);
+  const size_t as = FMT == SYN_HIP_FMT_Q8_0 ? 0 : (size_t)M * p.cs * (BE / GRP);
+  const size_t shm = (as + (size_t)waves * M * 64) * sizeof(float);
+  hipLaunchKernelGGL((k_gemv_kq<FMT, M>), dim3(p.panels, p.ksplit), dim3(64 * waves), shm, s,
+                     (const u32x4 *)W, Wd, x, ldx, y, ldy, part, N, p.chunks, p.cs);
+}
+
+template <int FMT>
+static void launch_kq_m(int m, const GemvPlan &p, const void *W, const uint16_t *Wd,
+                        const float *x, int ldx, float *y, int ldy, float *part, int N,
+                        hipStream_t s) {
+  switch (m) {
+    case 1: launch_kq<FMT, 1>(p, W, Wd, x, ldx, y, ldy, part, N, s); break;
+    case 2: launch_kq<FMT, 2>(p, W, Wd, x, ldx, y, ldy, part, N, s); break;
+    case 3: launch_kq<FMT, 3>(p, W, Wd, x, ldx, y, ldy, part, N, s); break;
+    default: launch_kq<FMT, 4>(p, W, Wd, x, ldx, y, ldy, part, N, s); break;
+  }
+}
+
+syn_status_t QLinearKQ::gemv(size_t m, const float *d_x, size_t ldx, float *d_y, size_t ldy,
+                             hipStream_t s) {
+  if (m == 0 || n == 0 || k == 0) return SYN_OK;
+  const GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
+  const size_t N64 = (size_t)p.panels * 64;
+  for (size_t m0 = 0; m0 < m; m0 += 4) {
+    const int mb = (int)std::min<size_t>(4, m - m0);
+    if (p.ksplit > 1 && part_elems < (size_t)p.ksplit * mb * N64) {
+      SYN_HIP(hipDeviceSynchronize());
+      part_elems = (size_t)p.ksplit * 4 * N64;
+      SYN_TRY(part.alloc(part_elems * sizeof(float)));
+    }
+    const float *xm = d_x + m0 * ldx;
+    float *ym = d_y + m0 * ldy;
+    const uint16_t *Wd = wd.as<uint16_t>();
+    if (fmt == SYN_HIP_FMT_Q8_0)
+      launch_kq_m<SYN_HIP_FMT_Q8_0>(mb, p, wq.p, Wd, xm, (int)ldx, ym, (int)ldy, part.as<float>(),
+                                    (int)n, s);
+    else if (fmt == SYN_HIP_FMT_Q4_K)
+      launch_kq_m<SYN_HIP_FMT_Q4_K>(mb, p, wq.p, Wd, xm, (int)ldx, ym, (int)ldy, part.as<float>(),
+                                    (int)n, s);
+    else
+      launch_kq_m<SYN_HIP_FMT_Q6_K>(mb, p, wq.p, Wd, xm, (int)ldx, ym, (int)ldy, part.as<float>(),
+                                    (int)n, s);
+    SYN_LAUNCH_CHECK();
+    if (p.ksplit > 1) {
+      const int total = mb * (int)n;
+      hipLaunchKernelGGL(k_kq_reduce, dim3(cdiv(total, 256)), dim3(256), 0, s, part.as<float>(),
+                         p.ksplit, mb, (int)n, (int)N64, ym, (int)ldy);
+      SYN_LAUNCH_CHECK();
+    }
+  }
+  return SYN_OK;
+}
+
+syn_status_t QLinearKQ::prepare(size_t max_m) {
+  const GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
+  if (p.ksplit <= 1) return SYN_OK;
+  (void)max_m;
+  const size_t need = (size_t)p.ksplit * 4 * p.panels * 64;
+  if (part_elems >= need) return SYN_OK;
+  part_elems = need;
+  return part.alloc(need * sizeof(float));
+}
+
+}  // namespace syn
+
+extern "C" syn_status_t syn_hip_kquant_encode(int fmt, size_t n, size_t k, const float *host_w,
+                                              uint8_t *host_out) {
+  using namespace syn;
+  if (!host_w || !host_out) return SYN_ERR_NULL_PTR;
+  if (fmt != SYN_HIP_FMT_Q8_0 && fmt != SYN_HIP_FMT_Q4_K && fmt != SYN_HIP_FMT_Q6_K)
+    return SYN_ERR_INVALID_ARG;
+  if (n == 0 || k == 0) return SYN_ERR_INVALID_ARG;
+  if (k % kq_block_elems(fmt)) return SYN_ERR_SHAPE_MISMATCH;
+  kq_encode(fmt, host_w, n, k, host_out);
+  return SYN_OK;
+}

@@ -1,0 +1,31 @@
+// GGUF-block formats Q8_0 / Q4_K / Q6_K resident in HBM (kquant.hip).
+#pragma once
+
+#include "linear.hpp"
+
+namespace syn {
+
+size_t kq_block_bytes(int fmt);
+size_t kq_block_elems(int fmt);
+// encode f32 [n,k] rows into the reference's block byte format
+void kq_encode(int fmt, const float *w, size_t n, size_t k, uint8_t *out);
+
+struct QLinearKQ {
+  int fmt = 0;
+  size_t n = 0, k = 0;
+  int blocks = 0;  // blocks per row
+  int planes = 0;  // 16-byte planes per block
+  DevBuf wq;       // [P][blocks][planes][64][16]
+  DevBuf wd;       // [P][blocks][64] f16 d (Q8_0, Q6_K)
+  DevBuf part;
+  size_t part_elems = 0;
+  syn_status_t upload(int fmt, const uint8_t *gguf, size_t n, size_t k);
+  syn_status_t from_f32(int fmt, const float *w, size_t n, size_t k);
+  size_t weight_bytes() const;
+  // y[m,n] = x[m,k] W^T, f32 activations (M rows, any M)
+  syn_status_t gemv(size_t m, const float *d_x, size_t ldx, float *d_y, size_t ldy,
+                    hipStream_t s);
+  syn_status_t prepare(size_t max_m);
+};
+
+}  // namespace syn

@@ -20,7 +20,8 @@ STATUS_NAMES = {0: "OK", 1: "NULL_PTR", 2: "INVALID_ARG", 3: "OUT_OF_MEMORY",
                 4: "SHAPE_MISMATCH", 5: "NOT_CONTIGUOUS", 6: "INVALID_AXIS",
                 7: "INVALID_DIMENSIONS", 8: "INTERNAL", 100: "NO_DEVICE", 101: "HIP",
                 102: "LAUNCH"}
-FMT_INT8, FMT_Q4_0 = 1, 2
+FMT_INT8, FMT_Q4_0, FMT_Q8_0, FMT_Q4_K, FMT_Q6_K = 1, 2, 3, 4, 5
+KQ_BLOCK = {FMT_Q8_0: (32, 34), FMT_Q4_K: (256, 144), FMT_Q6_K: (256, 210)}
 LAYOUT_KN, LAYOUT_NK = 0, 1
 
 P, SZ, ST = C.c_void_p, C.c_size_t, C.c_int32
@@ -78,6 +79,7 @@ SIGNATURES = {
     "syn_hip_qlm_destroy": (ST, [P]),
     "syn_hip_fill_normal": (ST, [P, SZ, C.c_uint64, C.c_float]),
     "syn_hip_eval_expf": (ST, [P, P, SZ, P]),
+    "syn_hip_kquant_encode": (ST, [C.c_int, SZ, SZ, P, P]),
 }
 
 _lib = None
@@ -273,6 +275,15 @@ class QLinear:
               "qlinear_create")
         return cls(h.value, FMT_Q4_0)
 
+    @classmethod
+    def gguf(cls, fmt: int, blocks: np.ndarray, n: int, k: int) -> "QLinear":
+        """Q8_0 / Q4_K / Q6_K block bytes of a row-major [n, k] tensor."""
+        blocks = np.ascontiguousarray(blocks, np.uint8)
+        h = C.c_void_p()
+        check(lib().syn_hip_qlinear_create(fmt, n, k, ptr(blocks), None, 0, C.byref(h)),
+              "qlinear_create")
+        return cls(h.value, fmt)
+
     def forward_dev(self, m: int, d_x: int, d_y: int, stream=None):
         check(lib().syn_hip_qlinear_forward(self.h, m, d_x, d_y, stream), "qlinear_forward")
 
@@ -377,6 +388,16 @@ class QuantizedCausalLM:
             self.close()
         except Exception:
             pass
+
+
+def kquant_encode(fmt: int, w: np.ndarray) -> np.ndarray:
+    """Encode f32 [n, k] into GGUF block bytes (host-side encoder of the library)."""
+    w = np.ascontiguousarray(w, np.float32)
+    n, k = w.shape
+    be, bb = KQ_BLOCK[fmt]
+    out = np.empty(n * (k // be) * bb, np.uint8)
+    check(lib().syn_hip_kquant_encode(fmt, n, k, ptr(w), ptr(out)), "kquant_encode")
+    return out
 
 
 def fill_normal(n: int, seed: int, std: float = 1.0) -> np.ndarray:

@@ -1,0 +1,95 @@
+"""Q8_0 / Q4_K / Q6_K on the GPU against the reference semantics: the oracle
+dequantizes the same bytes (gguf.rs:255-487) and runs matmul_t
+(ops/matmul.rs:55-79, sgemm/f32GemvRow order).  Tolerance: the north star's
+max_j|y-r| / max_j|r| <= 1e-3 per output row set."""
+import numpy as np
+import pytest
+
+import oracle as O
+from synapse_amd import hip
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+FMTS = {"q8_0": hip.FMT_Q8_0, "q4_k": hip.FMT_Q4_K, "q6_k": hip.FMT_Q6_K}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    hip.init(0)
+
+
+def _rel(got, want):
+    return float(np.abs(got - want).max() / max(np.abs(want).max(), 1e-30))
+
+
+@pytest.mark.parametrize("name", list(FMTS))
+def test_encoder_roundtrip_quality(name):
+    # the library's encoder writes the reference byte format; the oracle's
+    # dequantizer (reference semantics) must give back the weights closely
+    n, k = 64, 1024
+    w = O.normal(n * k, 11, 0.02).reshape(n, k)
+    blocks = hip.kquant_encode(FMTS[name], w)
+    deq = O.dequant(name, blocks, n * k).reshape(n, k)
+    err = np.abs(deq - w).max() / np.abs(w).max()
+    assert err < {"q8_0": 0.01, "q4_k": 0.12, "q6_k": 0.04}[name], err
+    # correlation close to 1
+    c = float(np.corrcoef(deq.ravel(), w.ravel())[0, 1])
+    assert c > {"q8_0": 0.9999, "q4_k": 0.99, "q6_k": 0.999}[name], c
+
+
+CASES = [("q8_0", 4096, 4096, 1), ("q8_0", 4096, 1024, 3), ("q8_0", 14336, 4096, 1),
+         ("q8_0", 96, 100, 4), ("q4_k", 3072, 3072, 1), ("q4_k", 3072, 1024, 2),
+         ("q4_k", 3072, 8192, 1), ("q4_k", 512, 67, 5), ("q6_k", 8192, 3072, 1),
+         ("q6_k", 3072, 1000, 3), ("q6_k", 256, 65, 7)]
+
+
+@pytest.mark.parametrize("name,k,n,m", CASES)
+def test_kquant_gemv_vs_reference(name, k, n, m):
+    w = O.normal(n * k, k + n, 0.02).reshape(n, k)
+    blocks = hip.kquant_encode(FMTS[name], w)
+    lin = hip.QLinear.gguf(FMTS[name], blocks, n, k)
+    x = O.normal(m * k, 7 * m + k, 1.0).reshape(m, k)
+    got = lin.forward(x)
+    deq = O.dequant(name, blocks, n * k).reshape(n, k)
+    want = O.matmul_t(x, deq)
+    for i in range(m):
+        assert _rel(got[i], want[i]) <= TOL * 0.1, (i, _rel(got[i], want[i]))
+
+
+def test_q6_k_lm_head_shape():
+    # LLaMA-3.2-3B lm_head: 128256 x 3072 Q6_K, random blocks
+    n, k = 128256, 3072
+    rng = np.random.default_rng(5)
+    nb = k // 256
+    blk = rng.integers(0, 256, (n, nb, 210), dtype=np.uint8)
+    blk[:, :, 192:208] = rng.integers(-40, 41, (n, nb, 16), dtype=np.int8).view(np.uint8)
+    d = (rng.uniform(1e-5, 3e-5, (n, nb))).astype(np.float16)
+    blk[:, :, 208:210] = d.view(np.uint8).reshape(n, nb, 2)
+    blk = blk.reshape(-1)
+    lin = hip.QLinear.gguf(hip.FMT_Q6_K, blk, n, k)
+    x = O.normal(k, 3, 1.0).reshape(1, k)
+    got = lin.forward(x)[0]
+    deq = O.dequant("q6_k", blk, n * k).reshape(n, k)
+    want = O.matmul_t(x, deq)[0]
+    assert _rel(got, want) <= TOL * 0.1
+
+
+def test_subnormal_scale_semantics():
+    # converter.rs halves subnormal f16 scales; the device decoder must agree
+    n, k = 64, 32
+    blk = np.zeros((n, 34), np.uint8)
+    blk[:, 0:2] = np.array([0x0200], np.uint16).view(np.uint8)  # subnormal d
+    blk[:, 2:] = np.arange(1, 33, dtype=np.int8).view(np.uint8)
+    blk = blk.reshape(-1)
+    lin = hip.QLinear.gguf(hip.FMT_Q8_0, blk, n, k)
+    x = np.ones((1, k), np.float32)
+    got = lin.forward(x)[0]
+    deq = O.dequant("q8_0", blk, n * k).reshape(n, k)
+    np.testing.assert_allclose(got, deq.sum(axis=1), rtol=1e-6)
+    assert deq[0, 0] == np.float32(2.0 ** -16)  # half of IEEE 2^-15
+
+
+def test_kquant_shape_errors():
+    w = np.zeros((4, 100), np.float32)
+    with pytest.raises(hip.SynapseError):
+        hip.QLinear.from_f32(hip.FMT_Q4_K, w)  # k % 256
