@@ -197,6 +197,37 @@ syn_status_t syn_hip_qlm_time_lm_head(syn_hip_qlm_t *m, size_t iters, size_t flu
                                       float *avg_ms);
 syn_status_t syn_hip_qlm_destroy(syn_hip_qlm_t *m);
 
+/* -- f32 causal LM over GGUF-block weights: CausalLM (models/lm/causal_lm.rs:
+ *    195-278, decoder_layer.rs:51-138, 590-730), the reference path for models
+ *    whose weights are Q8_0 / Q4_K / Q6_K (dequantized at load there, decoded
+ *    in the kernels here).  Projections 0..6 = q,k,v,o,gate,up,down. -- */
+typedef struct {
+  syn_hip_lm_config base;
+  int32_t fmt_qkv, fmt_o, fmt_gate_up, fmt_down, fmt_lm_head; /* SYN_HIP_FMT_Q* */
+  int32_t qk_norm; /* 1: per-head q/k RMSNorm (gains 1.0), 0: none (LLaMA) */
+} syn_hip_klm_config;
+
+typedef struct syn_hip_klm_s syn_hip_klm_t;
+syn_status_t syn_hip_klm_create(const syn_hip_klm_config *cfg, syn_hip_klm_t **out);
+syn_status_t syn_hip_klm_set_embed(syn_hip_klm_t *m, const float *embed);
+syn_status_t syn_hip_klm_set_proj(syn_hip_klm_t *m, uint32_t layer, int proj,
+                                  const uint8_t *gguf_bytes);
+syn_status_t syn_hip_klm_set_lm_head(syn_hip_klm_t *m, const uint8_t *gguf_bytes);
+/* Synthetic weights (seed spec as syn_hip_qlm_init_synthetic; untied lm_head
+ * is tensor id 1 + 8*n_layers), encoded with the library's block encoder. */
+syn_status_t syn_hip_klm_init_synthetic(syn_hip_klm_t *m, uint64_t seed_base, float stddev);
+syn_status_t syn_hip_klm_finalize(syn_hip_klm_t *m);
+syn_status_t syn_hip_klm_reset(syn_hip_klm_t *m);
+syn_status_t syn_hip_klm_forward_prefill(syn_hip_klm_t *m, const uint32_t *ids, size_t n,
+                                         float *host_logits);
+syn_status_t syn_hip_klm_forward_one(syn_hip_klm_t *m, uint32_t token, float *host_logits);
+syn_status_t syn_hip_klm_generate(syn_hip_klm_t *m, const uint32_t *prompt, size_t n_prompt,
+                                  size_t max_new, uint32_t *out_tokens, float *out_margins);
+/* hipEvent timing of one prefill of `prompt` and `steps` greedy decode steps. */
+syn_status_t syn_hip_klm_time(syn_hip_klm_t *m, const uint32_t *prompt, size_t n_prompt,
+                              size_t steps, float *prefill_ms, float *decode_ms);
+syn_status_t syn_hip_klm_destroy(syn_hip_klm_t *m);
+
 /* -- harness helpers (no reference counterpart) -- */
 /* Encode f32 [n,k] into Q8_0 / Q4_K / Q6_K block bytes.  The reference has no
  * encoder for these formats (only dequantizers); any encoding is valid since

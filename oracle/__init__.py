@@ -95,6 +95,16 @@ def _declare(L):
         "orc_qlm_generate": (C.c_int, [P, P, SZ, SZ, P, P]),
         "orc_qlm_lm_head_weights": (P, [P]),
         "orc_qlm_lm_head_scales": (P, [P]),
+        "orc_flm_create": (P, [C.POINTER(LmCfg), C.c_int]),
+        "orc_flm_destroy": (None, [P]),
+        "orc_flm_set_embed": (C.c_int, [P, P]),
+        "orc_flm_set_proj": (C.c_int, [P, SZ, C.c_int, C.c_int, P]),
+        "orc_flm_set_lm_head": (C.c_int, [P, C.c_int, P]),
+        "orc_flm_reset": (None, [P]),
+        "orc_flm_prefill": (C.c_int, [P, P, SZ, P]),
+        "orc_flm_forward_one": (C.c_int, [P, C.c_uint32, P]),
+        "orc_flm_generate": (C.c_int, [P, P, SZ, SZ, P, P]),
+        "orc_swiglu_fused": (None, [P, P, P, SZ]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -324,6 +334,71 @@ class QuantizedCausalLM:
     def close(self):
         if self.h:
             lib().orc_qlm_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+FMT_CODES = {"q8_0": 3, "q4_k": 4, "q6_k": 5}
+
+
+class CausalLM:
+    """f32 decoder over GGUF-dequantized weights (models/lm/causal_lm.rs)."""
+
+    def __init__(self, cfg: dict, qk_norm: bool = False):
+        self.cfg = cfg
+        c = LmCfg(cfg["hidden"], cfg["n_layers"], cfg["n_heads"], cfg["n_kv_heads"],
+                  cfg["head_dim"], cfg["inter"], cfg["vocab"], cfg["max_seq"],
+                  cfg.get("eps", 1e-5), cfg.get("rope_theta", 5e5))
+        self._c = c
+        self.h = lib().orc_flm_create(C.byref(c), 1 if qk_norm else 0)
+        if not self.h:
+            raise MemoryError("orc_flm_create failed")
+
+    def _check(self, rc):
+        if rc:
+            raise RuntimeError(f"oracle status {rc}")
+
+    def set_embed(self, embed):
+        self._check(lib().orc_flm_set_embed(self.h, _p(np.ascontiguousarray(embed, np.float32))))
+
+    def set_proj(self, layer: int, proj: int, fmt: str, blocks: np.ndarray):
+        self._check(lib().orc_flm_set_proj(self.h, layer, proj, FMT_CODES[fmt],
+                                           _p(np.ascontiguousarray(blocks, np.uint8))))
+
+    def set_lm_head(self, fmt: str, blocks: np.ndarray):
+        self._check(lib().orc_flm_set_lm_head(self.h, FMT_CODES[fmt],
+                                              _p(np.ascontiguousarray(blocks, np.uint8))))
+
+    def reset(self):
+        lib().orc_flm_reset(self.h)
+
+    def prefill(self, ids):
+        ids = np.ascontiguousarray(ids, np.uint32)
+        out = np.empty(self.cfg["vocab"], np.float32)
+        self._check(lib().orc_flm_prefill(self.h, _p(ids), ids.size, _p(out)))
+        return out
+
+    def forward_one(self, token: int):
+        out = np.empty(self.cfg["vocab"], np.float32)
+        self._check(lib().orc_flm_forward_one(self.h, int(token), _p(out)))
+        return out
+
+    def generate(self, prompt, max_new: int):
+        prompt = np.ascontiguousarray(prompt, np.uint32)
+        toks = np.zeros(max_new, np.uint32)
+        margins = np.zeros(max_new, np.float32)
+        self._check(lib().orc_flm_generate(self.h, _p(prompt), prompt.size, max_new, _p(toks),
+                                           _p(margins)))
+        return toks, margins
+
+    def close(self):
+        if self.h:
+            lib().orc_flm_destroy(self.h)
             self.h = None
 
     def __del__(self):

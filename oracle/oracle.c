@@ -994,3 +994,233 @@ int orc_qlm_generate(orc_qlm *m, const uint32_t *prompt, size_t n_prompt, size_t
   free(logits);
   return rc;
 }
+
+/* ======================================================================
+ * f32 CausalLM (models/lm/causal_lm.rs:195-278, decoder_layer.rs:51-138,
+ * 590-730): weights dequantized at load (gguf.rs:217-237), every projection
+ * through matmul_t (orc_sgemm with trans_b), SwiGLU through Zig swigluFused.
+ * ==================================================================== */
+/* zig/src/ops/silu.zig:85-114: vector part (i < n - n%4) computes
+ * sig = 1/(1+exp(-g)); dst = (g*sig)*u; the scalar tail (g/(1+exp(-g)))*u */
+void orc_swiglu_fused(float *dst, const float *gate, const float *up, size_t n) {
+  size_t n4 = n - n % 4;
+  for (size_t i = 0; i < n4; i++) {
+    float g = gate[i];
+    float sig = 1.0f / (1.0f + expf(-g));
+    float t = g * sig;
+    dst[i] = t * up[i];
+  }
+  for (size_t i = n4; i < n; i++) {
+    float g = gate[i];
+    float t = g / (1.0f + expf(-g));
+    dst[i] = t * up[i];
+  }
+}
+
+struct orc_flm {
+  orc_lm_cfg c;
+  int qk_norm;
+  float *embed;
+  float **w;        /* [L*7] f32 [N,K] */
+  float *lm_head;   /* f32 [vocab, h] */
+  float *ones_h, *ones_hd;
+  float *rope_cos, *rope_sin;
+  float *kc, *vc;
+  size_t cur;
+};
+
+static int dequant_fmt(int fmt, const uint8_t *b, size_t numel, float *out) {
+  if (fmt == ORC_FMT_Q8_0) return orc_dequant_q8_0(b, numel, out);
+  if (fmt == ORC_FMT_Q4_K) return orc_dequant_q4_k(b, numel, out);
+  if (fmt == ORC_FMT_Q6_K) return orc_dequant_q6_k(b, numel, out);
+  return ORC_ERR_INVALID_ARG;
+}
+
+orc_flm *orc_flm_create(const orc_lm_cfg *cfg, int qk_norm) {
+  orc_flm *m = (orc_flm *)calloc(1, sizeof(orc_flm));
+  if (!m) return NULL;
+  m->c = *cfg;
+  m->qk_norm = qk_norm;
+  size_t h = cfg->hidden, hd = cfg->head_dim, kv = cfg->n_kv_heads * hd;
+  m->w = (float **)calloc(cfg->n_layers * 7, sizeof(float *));
+  m->ones_h = (float *)malloc(h * 4);
+  m->ones_hd = (float *)malloc(hd * 4);
+  for (size_t i = 0; i < h; i++) m->ones_h[i] = 1.0f;
+  for (size_t i = 0; i < hd; i++) m->ones_hd[i] = 1.0f;
+  m->rope_cos = (float *)malloc(cfg->max_seq * (hd / 2) * 4);
+  m->rope_sin = (float *)malloc(cfg->max_seq * (hd / 2) * 4);
+  orc_rope_tables(cfg->max_seq, hd, cfg->rope_theta, m->rope_cos, m->rope_sin);
+  m->kc = (float *)calloc(cfg->n_layers * cfg->max_seq * kv, 4);
+  m->vc = (float *)calloc(cfg->n_layers * cfg->max_seq * kv, 4);
+  return m;
+}
+
+void orc_flm_destroy(orc_flm *m) {
+  if (!m) return;
+  for (size_t i = 0; i < m->c.n_layers * 7; i++) free(m->w[i]);
+  free(m->w);
+  free(m->embed);
+  free(m->lm_head);
+  free(m->ones_h);
+  free(m->ones_hd);
+  free(m->rope_cos);
+  free(m->rope_sin);
+  free(m->kc);
+  free(m->vc);
+  free(m);
+}
+
+int orc_flm_set_embed(orc_flm *m, const float *embed) {
+  size_t bytes = m->c.vocab * m->c.hidden * 4;
+  m->embed = (float *)malloc(bytes);
+  if (!m->embed) return ORC_ERR_OUT_OF_MEMORY;
+  memcpy(m->embed, embed, bytes);
+  return ORC_OK;
+}
+
+static void flm_proj_shape(const orc_flm *m, int proj, size_t *n, size_t *k) {
+  const orc_lm_cfg *c = &m->c;
+  size_t h = c->hidden, qd = c->n_heads * c->head_dim, kvd = c->n_kv_heads * c->head_dim;
+  const size_t rows[7] = {qd, kvd, kvd, h, c->inter, c->inter, h};
+  const size_t cols[7] = {h, h, h, qd, h, h, c->inter};
+  *n = rows[proj];
+  *k = cols[proj];
+}
+
+int orc_flm_set_proj(orc_flm *m, size_t layer, int proj, int fmt, const uint8_t *bytes) {
+  if (layer >= m->c.n_layers || proj < 0 || proj > 6) return ORC_ERR_INVALID_ARG;
+  size_t n, k;
+  flm_proj_shape(m, proj, &n, &k);
+  float *w = (float *)malloc(n * k * 4);
+  if (!w) return ORC_ERR_OUT_OF_MEMORY;
+  int rc = dequant_fmt(fmt, bytes, n * k, w);
+  if (rc) { free(w); return rc; }
+  free(m->w[layer * 7 + proj]);
+  m->w[layer * 7 + proj] = w;
+  return ORC_OK;
+}
+
+int orc_flm_set_lm_head(orc_flm *m, int fmt, const uint8_t *bytes) {
+  size_t n = m->c.vocab * m->c.hidden;
+  m->lm_head = (float *)malloc(n * 4);
+  if (!m->lm_head) return ORC_ERR_OUT_OF_MEMORY;
+  return dequant_fmt(fmt, bytes, n, m->lm_head);
+}
+
+void orc_flm_reset(orc_flm *m) { m->cur = 0; }
+
+static void flm_matmul_t(const float *x, const float *w, size_t m, size_t k, size_t n, float *y) {
+  memset(y, 0, m * n * 4);
+  orc_sgemm(m, n, k, x, k, 0, w, k, 1, y, n);
+}
+
+static void flm_layer(orc_flm *m, size_t l, float *x, size_t t, int prefill) {
+  const orc_lm_cfg *c = &m->c;
+  size_t h = c->hidden, hd = c->head_dim, nh = c->n_heads, nkv = c->n_kv_heads;
+  size_t qd = nh * hd, kvd = nkv * hd, inter = c->inter;
+  float **W = m->w + l * 7;
+  float *normed = (float *)malloc(t * h * 4);
+  float *q = (float *)malloc(t * qd * 4), *k = (float *)malloc(t * kvd * 4);
+  float *v = (float *)malloc(t * kvd * 4), *attn = (float *)malloc(t * qd * 4);
+  float *o = (float *)malloc(t * h * 4);
+  float *g = (float *)malloc(t * inter * 4), *u = (float *)malloc(t * inter * 4);
+  float *hb = (float *)malloc(t * inter * 4);
+  float *kcl = m->kc + l * c->max_seq * kvd, *vcl = m->vc + l * c->max_seq * kvd;
+
+  orc_rmsnorm(x, m->ones_h, c->eps, t, h, normed);
+  flm_matmul_t(normed, W[0], t, h, qd, q);
+  flm_matmul_t(normed, W[1], t, h, kvd, k);
+  flm_matmul_t(normed, W[2], t, h, kvd, v);
+  if (m->qk_norm) {
+    orc_rmsnorm(q, m->ones_hd, c->eps, t * nh, hd, q);
+    orc_rmsnorm(k, m->ones_hd, c->eps, t * nkv, hd, k);
+  }
+  size_t pos0 = prefill ? 0 : m->cur;
+  orc_rope_apply(q, m->rope_cos, m->rope_sin, t, nh, hd, pos0);
+  orc_rope_apply(k, m->rope_cos, m->rope_sin, t, nkv, hd, pos0);
+  memcpy(kcl + pos0 * kvd, k, t * kvd * 4);
+  memcpy(vcl + pos0 * kvd, v, t * kvd * 4);
+  if (prefill) {
+    size_t groups = nh / nkv;
+    float *qh = (float *)malloc(t * hd * 4), *kh = (float *)malloc(t * hd * 4);
+    float *vh = (float *)malloc(t * hd * 4), *oh = (float *)malloc(t * hd * 4);
+    for (size_t head = 0; head < nh; head++) {
+      size_t kvh = head / groups;
+      for (size_t s = 0; s < t; s++) {
+        memcpy(qh + s * hd, q + s * qd + head * hd, hd * 4);
+        memcpy(kh + s * hd, k + s * kvd + kvh * hd, hd * 4);
+        memcpy(vh + s * hd, v + s * kvd + kvh * hd, hd * 4);
+      }
+      orc_fused_attention(t, t, hd, qh, kh, vh, oh);
+      for (size_t s = 0; s < t; s++) memcpy(attn + s * qd + head * hd, oh + s * hd, hd * 4);
+    }
+    free(qh); free(kh); free(vh); free(oh);
+  } else {
+    orc_attention_decode(q, kcl, vcl, pos0 + 1, nh, nkv, hd, attn);
+  }
+  flm_matmul_t(attn, W[3], t, qd, h, o);
+  for (size_t i = 0; i < t * h; i++) x[i] = x[i] + o[i];
+  orc_rmsnorm(x, m->ones_h, c->eps, t, h, normed);
+  flm_matmul_t(normed, W[4], t, h, inter, g);
+  flm_matmul_t(normed, W[5], t, h, inter, u);
+  orc_swiglu_fused(hb, g, u, t * inter);
+  flm_matmul_t(hb, W[6], t, inter, h, o);
+  for (size_t i = 0; i < t * h; i++) x[i] += o[i];
+  free(normed); free(q); free(k); free(v); free(attn); free(o); free(g); free(u); free(hb);
+}
+
+static void flm_head(orc_flm *m, const float *xlast, float *logits) {
+  size_t h = m->c.hidden;
+  float *normed = (float *)malloc(h * 4);
+  orc_rmsnorm(xlast, m->ones_h, m->c.eps, 1, h, normed);
+  flm_matmul_t(normed, m->lm_head, 1, h, m->c.vocab, logits);
+  free(normed);
+}
+
+int orc_flm_prefill(orc_flm *m, const uint32_t *ids, size_t n, float *logits) {
+  if (n == 0 || n > m->c.max_seq) return ORC_ERR_INVALID_ARG;
+  size_t h = m->c.hidden;
+  float *x = (float *)malloc(n * h * 4);
+  for (size_t t = 0; t < n; t++) {
+    if (ids[t] < m->c.vocab) memcpy(x + t * h, m->embed + (size_t)ids[t] * h, h * 4);
+    else memset(x + t * h, 0, h * 4);
+  }
+  for (size_t l = 0; l < m->c.n_layers; l++) flm_layer(m, l, x, n, 1);
+  m->cur = n;
+  flm_head(m, x + (n - 1) * h, logits);
+  free(x);
+  return ORC_OK;
+}
+
+int orc_flm_forward_one(orc_flm *m, uint32_t token, float *logits) {
+  if (m->cur >= m->c.max_seq) return ORC_ERR_INVALID_ARG;
+  size_t h = m->c.hidden;
+  float *x = (float *)malloc(h * 4);
+  if (token < m->c.vocab) memcpy(x, m->embed + (size_t)token * h, h * 4);
+  else memset(x, 0, h * 4);
+  for (size_t l = 0; l < m->c.n_layers; l++) flm_layer(m, l, x, 1, 0);
+  m->cur += 1;
+  flm_head(m, x, logits);
+  free(x);
+  return ORC_OK;
+}
+
+int orc_flm_generate(orc_flm *m, const uint32_t *prompt, size_t n_prompt, size_t max_new,
+                     uint32_t *out_tokens, float *margins) {
+  if (max_new == 0) return ORC_OK;
+  float *logits = (float *)malloc(m->c.vocab * 4);
+  int rc = orc_flm_prefill(m, prompt, n_prompt, logits);
+  if (rc) { free(logits); return rc; }
+  uint32_t tok = orc_argmax(logits, m->c.vocab);
+  out_tokens[0] = tok;
+  if (margins) margins[0] = top2_margin(logits, m->c.vocab, tok);
+  for (size_t i = 1; i < max_new; i++) {
+    rc = orc_flm_forward_one(m, tok, logits);
+    if (rc) break;
+    tok = orc_argmax(logits, m->c.vocab);
+    out_tokens[i] = tok;
+    if (margins) margins[i] = top2_margin(logits, m->c.vocab, tok);
+  }
+  free(logits);
+  return rc;
+}

@@ -113,6 +113,26 @@ int orc_qlm_generate(orc_qlm *m, const uint32_t *prompt, size_t n_prompt, size_t
 const int8_t *orc_qlm_lm_head_weights(const orc_qlm *m); /* [K,N] reference layout */
 const float *orc_qlm_lm_head_scales(const orc_qlm *m);
 
+/* ---- f32 CausalLM over GGUF-dequantized weights (models/lm/causal_lm.rs,
+ *      decoder_layer.rs): the reference path for Q4_K / Q6_K / Q8_0 models ---- */
+#define ORC_FMT_Q8_0 3
+#define ORC_FMT_Q4_K 4
+#define ORC_FMT_Q6_K 5
+typedef struct orc_flm orc_flm;
+/* qk_norm: 1 = Qwen3-style q/k RMSNorm (gains 1.0), 0 = none (LLaMA) */
+orc_flm *orc_flm_create(const orc_lm_cfg *cfg, int qk_norm);
+void orc_flm_destroy(orc_flm *m);
+int orc_flm_set_embed(orc_flm *m, const float *embed);
+/* one projection of one layer from GGUF bytes: proj 0..6 = q,k,v,o,gate,up,down */
+int orc_flm_set_proj(orc_flm *m, size_t layer, int proj, int fmt, const uint8_t *bytes);
+int orc_flm_set_lm_head(orc_flm *m, int fmt, const uint8_t *bytes);
+void orc_flm_reset(orc_flm *m);
+int orc_flm_prefill(orc_flm *m, const uint32_t *ids, size_t n, float *logits);
+int orc_flm_forward_one(orc_flm *m, uint32_t token, float *logits);
+int orc_flm_generate(orc_flm *m, const uint32_t *prompt, size_t n_prompt, size_t max_new,
+                     uint32_t *out_tokens, float *margins);
+void orc_swiglu_fused(float *dst, const float *gate, const float *up, size_t n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,470 @@
+// f32 causal LM over GGUF-block weights (Q8_0 / Q4_K / Q6_K) on the device:
+// the reference's CausalLM (models/lm/causal_lm.rs:195-278,
+// decoder_layer.rs:51-138, 590-730) for the formats it dequantizes at load,
+// with the weights kept in their block format in HBM and decoded in the
+// GEMV/GEMM kernels.  Same greedy loop and HIP-graph decode step as the INT8
+// driver; activations stay f32 between layers (no activation quantization
+// on this path, as in the reference).
+#include <algorithm>
+#include <thread>
+#include <vector>
+
+#include "kquant.hpp"
+#include "layer_ops.hpp"
+
+using namespace syn;
+
+struct syn_hip_klm_s {
+  syn_hip_klm_config c{};
+  size_t h = 0, hd = 0, qd = 0, kvd = 0, inter = 0, L = 0, vocab = 0, S = 0, n_qkv = 0;
+  struct Layer {
+    QLinearKQ qkv, o, gu, down;
+    std::vector<std::vector<uint8_t>> pending;  // q,k,v,gate,up bytes until stacked
+    int have = 0;                               // bitmask of the 7 projections
+  };
+  std::vector<Layer> layers;
+  QLinearKQ lm_head;
+  bool have_lm = false, have_embed = false;
+  DevBuf embed, ones_h, ones_hd, rope_cos, rope_sin, kc, vc;
+  DevBuf x, normed, qkv, qrot, attn, o, gu, hbuf, down, logits, scores;
+  DevBuf pv, pi, pv2, state, history, mhist, ids;
+  hipStream_t stream = nullptr;
+  hipGraphExec_t graph = nullptr;
+  bool finalized = false;
+
+  ~syn_hip_klm_s() {
+    if (graph) (void)hipGraphExecDestroy(graph);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+  float *kc_l(size_t l) { return kc.as<float>() + l * S * kvd; }
+  float *vc_l(size_t l) { return vc.as<float>() + l * S * kvd; }
+  StepState *st() { return state.as<StepState>(); }
+  int fmt_of(int proj) const {
+    if (proj <= 2) return c.fmt_qkv;
+    if (proj == 3) return c.fmt_o;
+    if (proj <= 5) return c.fmt_gate_up;
+    return c.fmt_down;
+  }
+  void proj_shape(int proj, size_t *n, size_t *k) const {
+    const size_t rows[7] = {qd, kvd, kvd, h, inter, inter, h};
+    const size_t cols[7] = {h, h, h, qd, h, h, inter};
+    *n = rows[proj];
+    *k = cols[proj];
+  }
+  size_t proj_bytes(int proj) const {
+    size_t n, k;
+    proj_shape(proj, &n, &k);
+    const int f = fmt_of(proj);
+    return n * (k / kq_block_elems(f)) * kq_block_bytes(f);
+  }
+
+  syn_status_t alloc_all() {
+    const size_t T = S;
+    SYN_TRY(ones_h.alloc(h * 4));
+    SYN_TRY(ones_hd.alloc(hd * 4));
+    SYN_TRY(rope_cos.alloc(S * (hd / 2) * 4));
+    SYN_TRY(rope_sin.alloc(S * (hd / 2) * 4));
+    SYN_TRY(kc.alloc(L * S * kvd * 4));
+    SYN_TRY(vc.alloc(L * S * kvd * 4));
+    SYN_TRY(x.alloc(T * h * 4));
+    SYN_TRY(normed.alloc(T * h * 4));
+    SYN_TRY(qkv.alloc(T * n_qkv * 4));
+    SYN_TRY(qrot.alloc(T * qd * 4));
+    SYN_TRY(attn.alloc(T * qd * 4));
+    SYN_TRY(o.alloc(T * h * 4));
+    SYN_TRY(gu.alloc(T * 2 * inter * 4));
+    SYN_TRY(hbuf.alloc(T * inter * 4));
+    SYN_TRY(down.alloc(T * h * 4));
+    SYN_TRY(logits.alloc(vocab * 4));
+    SYN_TRY(scores.alloc(c.base.n_heads * S * 4));
+    SYN_TRY(pv.alloc(256 * 4));
+    SYN_TRY(pi.alloc(256 * 4));
+    SYN_TRY(pv2.alloc(256 * 4));
+    SYN_TRY(state.alloc(sizeof(StepState)));
+    SYN_TRY(history.alloc((S + 1) * 4));
+    SYN_TRY(mhist.alloc((S + 1) * 4));
+    SYN_TRY(ids.alloc(S * 4));
+    std::vector<float> one(std::max(h, hd), 1.0f);
+    SYN_HIP(hipMemcpy(ones_h.p, one.data(), h * 4, hipMemcpyHostToDevice));
+    SYN_HIP(hipMemcpy(ones_hd.p, one.data(), hd * 4, hipMemcpyHostToDevice));
+    SYN_HIP(hipMemset(kc.p, 0, kc.bytes));
+    SYN_HIP(hipMemset(vc.p, 0, vc.bytes));
+    return SYN_OK;
+  }
+
+  syn_status_t set_proj(size_t l, int proj, const uint8_t *bytes) {
+    Layer &Ly = layers[l];
+    const size_t nbytes = proj_bytes(proj);
+    if (proj == 3) {
+      SYN_TRY(Ly.o.upload(fmt_of(3), bytes, h, qd));
+    } else if (proj == 6) {
+      SYN_TRY(Ly.down.upload(fmt_of(6), bytes, h, inter));
+    } else {
+      const int slot = proj <= 2 ? proj : proj - 1;  // q,k,v,gate,up -> 0..4
+      Ly.pending[slot].assign(bytes, bytes + nbytes);
+    }
+    Ly.have |= 1 << proj;
+    if ((Ly.have & 7) == 7 && !Ly.pending[0].empty()) {  // stack q|k|v rows
+      std::vector<uint8_t> cat;
+      for (int t = 0; t < 3; t++) cat.insert(cat.end(), Ly.pending[t].begin(), Ly.pending[t].end());
+      SYN_TRY(Ly.qkv.upload(fmt_of(0), cat.data(), n_qkv, h));
+      for (int t = 0; t < 3; t++) std::vector<uint8_t>().swap(Ly.pending[t]);
+    }
+    if ((Ly.have & 0x30) == 0x30 && !Ly.pending[3].empty()) {  // stack gate|up rows
+      std::vector<uint8_t> cat(Ly.pending[3]);
+      cat.insert(cat.end(), Ly.pending[4].begin(), Ly.pending[4].end());
+      SYN_TRY(Ly.gu.upload(fmt_of(4), cat.data(), 2 * inter, h));
+      for (int t = 3; t < 5; t++) std::vector<uint8_t>().swap(Ly.pending[t]);
+    }
+    return SYN_OK;
+  }
+
+  syn_status_t layer(size_t l, int rows, bool prefill, hipStream_t s) {
+    Layer &Ly = layers[l];
+    const float eps = c.base.eps;
+    const int nh = (int)c.base.n_heads, nkv = (int)c.base.n_kv_heads;
+    const float *qn = c.qk_norm ? ones_hd.as<float>() : nullptr;
+    SYN_TRY(launch_rmsnorm_quant(x.as<float>(), l == 0 ? nullptr : down.as<float>(),
+                                 ones_h.as<float>(), eps, rows, (int)h, nullptr, 0, nullptr,
+                                 normed.as<float>(), s));
+    SYN_TRY(Ly.qkv.gemv(rows, normed.as<float>(), h, qkv.as<float>(), n_qkv, s));
+    SYN_TRY(launch_qk_norm_rope_kv(qkv.as<float>(), (int)n_qkv, rows, nh, nkv, (int)hd, qn, qn,
+                                   eps, rope_cos.as<float>(), rope_sin.as<float>(),
+                                   prefill ? nullptr : &st()->pos, 0, qrot.as<float>(), kc_l(l),
+                                   vc_l(l), s));
+    if (prefill)
+      SYN_TRY(launch_attention_prefill(qrot.as<float>(), kc_l(l), vc_l(l), rows, nh, nkv,
+                                       (int)hd, nullptr, attn.as<float>(), s));
+    else
+      SYN_TRY(launch_attention_decode(qrot.as<float>(), kc_l(l), vc_l(l), &st()->pos, nh, nkv,
+                                      (int)hd, scores.as<float>(), (int)S, attn.as<float>(), s));
+    SYN_TRY(Ly.o.gemv(rows, attn.as<float>(), qd, o.as<float>(), h, s));
+    SYN_TRY(launch_rmsnorm_quant(x.as<float>(), o.as<float>(), ones_h.as<float>(), eps, rows,
+                                 (int)h, nullptr, 0, nullptr, normed.as<float>(), s));
+    SYN_TRY(Ly.gu.gemv(rows, normed.as<float>(), h, gu.as<float>(), 2 * inter, s));
+    SYN_TRY(launch_swiglu_f32(gu.as<float>(), (int)(2 * inter), rows, (int)inter,
+                              hbuf.as<float>(), (int)inter, s));
+    SYN_TRY(Ly.down.gemv(rows, hbuf.as<float>(), inter, down.as<float>(), h, s));
+    return SYN_OK;
+  }
+
+  syn_status_t head(int row, int add_pos, hipStream_t s) {
+    float *xr = x.as<float>() + (size_t)row * h;
+    const float *dr = down.as<float>() + (size_t)row * h;
+    SYN_TRY(launch_rmsnorm_quant(xr, dr, ones_h.as<float>(), c.base.eps, 1, (int)h, nullptr, 0,
+                                 nullptr, normed.as<float>(), s));
+    SYN_TRY(lm_head.gemv(1, normed.as<float>(), h, logits.as<float>(), vocab, s));
+    SYN_TRY(launch_argmax(logits.as<float>(), (int)vocab, pv.as<float>(), pi.as<int>(),
+                          pv2.as<float>(), st(), history.as<uint32_t>(), mhist.as<float>(), s));
+    return launch_step_advance(st(), add_pos, s);
+  }
+
+  syn_status_t decode_step(hipStream_t s) {
+    SYN_TRY(launch_embed(embed.as<float>(), &st()->token, 1, (int)h, (int)vocab, x.as<float>(), s));
+    for (size_t l = 0; l < L; l++) SYN_TRY(layer(l, 1, false, s));
+    return head(0, 1, s);
+  }
+
+  syn_status_t build_graph() {
+    if (graph) return SYN_OK;
+    hipGraph_t g;
+    SYN_HIP(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+    syn_status_t st_ = decode_step(stream);
+    hipError_t e = hipStreamEndCapture(stream, &g);
+    if (st_ != SYN_OK) {
+      if (e == hipSuccess) (void)hipGraphDestroy(g);
+      return st_;
+    }
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture", __FILE__, __LINE__);
+    e = hipGraphInstantiate(&graph, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    if (e != hipSuccess) {
+      graph = nullptr;
+      return hip_fail(e, "hipGraphInstantiate", __FILE__, __LINE__);
+    }
+    return SYN_OK;
+  }
+
+  syn_status_t set_state(int pos, uint32_t token, int step) {
+    StepState hs{pos, token, step, 0.0f};
+    SYN_HIP(hipMemcpyAsync(state.p, &hs, sizeof(hs), hipMemcpyHostToDevice, stream));
+    SYN_HIP(hipStreamSynchronize(stream));
+    return SYN_OK;
+  }
+
+  syn_status_t get_state(StepState *out) {
+    SYN_HIP(hipMemcpyAsync(out, state.p, sizeof(StepState), hipMemcpyDeviceToHost, stream));
+    SYN_HIP(hipStreamSynchronize(stream));
+    return SYN_OK;
+  }
+
+  syn_status_t prefill(const uint32_t *host_ids, size_t n) {
+    if (n == 0 || n > S) {
+      set_error("prefill length must be in [1, max_seq]");
+      return SYN_ERR_INVALID_ARG;
+    }
+    SYN_HIP(hipMemcpyAsync(ids.p, host_ids, n * 4, hipMemcpyHostToDevice, stream));
+    SYN_TRY(set_state(0, 0, 0));
+    SYN_TRY(launch_embed(embed.as<float>(), ids.as<uint32_t>(), (int)n, (int)h, (int)vocab,
+                         x.as<float>(), stream));
+    for (size_t l = 0; l < L; l++) SYN_TRY(layer(l, (int)n, true, stream));
+    return head((int)n - 1, (int)n, stream);
+  }
+};
+
+static bool kq_fmt_ok(int f) {
+  return f == SYN_HIP_FMT_Q8_0 || f == SYN_HIP_FMT_Q4_K || f == SYN_HIP_FMT_Q6_K;
+}
+
+static syn_status_t check_klm(syn_hip_klm_t *m) {
+  if (!m) return SYN_ERR_NULL_PTR;
+  if (!m->finalized) {
+    set_error("model not finalized");
+    return SYN_ERR_INVALID_ARG;
+  }
+  return SYN_OK;
+}
+
+extern "C" {
+
+syn_status_t syn_hip_klm_create(const syn_hip_klm_config *cfg, syn_hip_klm_t **out) {
+  if (!cfg || !out) return SYN_ERR_NULL_PTR;
+  const syn_hip_lm_config &b = cfg->base;
+  if (!b.hidden || !b.n_layers || !b.n_heads || !b.n_kv_heads || !b.head_dim || !b.inter ||
+      !b.vocab || !b.max_seq || b.n_heads % b.n_kv_heads || b.head_dim % 2 || b.head_dim > 1024)
+    return SYN_ERR_INVALID_ARG;
+  const int fm[5] = {cfg->fmt_qkv, cfg->fmt_o, cfg->fmt_gate_up, cfg->fmt_down, cfg->fmt_lm_head};
+  for (int f : fm)
+    if (!kq_fmt_ok(f)) return SYN_ERR_INVALID_ARG;
+  // K of every projection must be a whole number of blocks
+  const size_t qd = (size_t)b.n_heads * b.head_dim;
+  if (b.hidden % kq_block_elems(cfg->fmt_qkv) || b.hidden % kq_block_elems(cfg->fmt_gate_up) ||
+      qd % kq_block_elems(cfg->fmt_o) || b.inter % kq_block_elems(cfg->fmt_down) ||
+      b.hidden % kq_block_elems(cfg->fmt_lm_head))
+    return SYN_ERR_SHAPE_MISMATCH;
+  SYN_TRY(ensure_init());
+  auto *m = new syn_hip_klm_s();
+  m->c = *cfg;
+  m->h = b.hidden;
+  m->hd = b.head_dim;
+  m->qd = qd;
+  m->kvd = (size_t)b.n_kv_heads * b.head_dim;
+  m->inter = b.inter;
+  m->L = b.n_layers;
+  m->vocab = b.vocab;
+  m->S = b.max_seq;
+  m->n_qkv = m->qd + 2 * m->kvd;
+  m->layers.resize(m->L);
+  for (auto &Ly : m->layers) Ly.pending.resize(5);
+  hipError_t e = hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    m->stream = nullptr;
+    delete m;
+    return hip_fail(e, "hipStreamCreate", __FILE__, __LINE__);
+  }
+  syn_status_t st = m->alloc_all();
+  if (st != SYN_OK) {
+    delete m;
+    return st;
+  }
+  *out = m;
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_klm_set_embed(syn_hip_klm_t *m, const float *embed) {
+  if (!m || !embed) return SYN_ERR_NULL_PTR;
+  SYN_TRY(m->embed.alloc(m->vocab * m->h * 4));
+  SYN_HIP(hipMemcpy(m->embed.p, embed, m->vocab * m->h * 4, hipMemcpyHostToDevice));
+  m->have_embed = true;
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_klm_set_proj(syn_hip_klm_t *m, uint32_t layer, int proj,
+                                  const uint8_t *gguf_bytes) {
+  if (!m || !gguf_bytes) return SYN_ERR_NULL_PTR;
+  if (layer >= m->L || proj < 0 || proj > 6) return SYN_ERR_INVALID_ARG;
+  return m->set_proj(layer, proj, gguf_bytes);
+}
+
+syn_status_t syn_hip_klm_set_lm_head(syn_hip_klm_t *m, const uint8_t *gguf_bytes) {
+  if (!m || !gguf_bytes) return SYN_ERR_NULL_PTR;
+  SYN_TRY(m->lm_head.upload(m->c.fmt_lm_head, gguf_bytes, m->vocab, m->h));
+  m->have_lm = true;
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_klm_init_synthetic(syn_hip_klm_t *m, uint64_t seed_base, float stddev) {
+  if (!m) return SYN_ERR_NULL_PTR;
+  const size_t h = m->h;
+  {
+    std::vector<float> emb(m->vocab * h);
+    fill_normal_parallel(emb.data(), emb.size(), seed_base + 0, stddev);
+    SYN_TRY(syn_hip_klm_set_embed(m, emb.data()));
+  }
+  for (size_t l = 0; l < m->L; l++) {
+    std::vector<std::vector<uint8_t>> bytes(7);
+    std::vector<std::thread> th;
+    for (int t = 0; t < 7; t++)
+      th.emplace_back([&, t] {
+        size_t n, k;
+        m->proj_shape(t, &n, &k);
+        std::vector<float> w(n * k);
+        fill_normal(w.data(), w.size(), seed_base + 1 + 8 * l + (uint64_t)t, stddev);
+        bytes[t].resize(m->proj_bytes(t));
+        kq_encode(m->fmt_of(t), w.data(), n, k, bytes[t].data());
+      });
+    for (auto &x : th) x.join();
+    for (int t = 0; t < 7; t++) SYN_TRY(m->set_proj(l, t, bytes[t].data()));
+  }
+  {  // untied lm_head: tensor id 1 + 8 * n_layers, encoded in row chunks on threads
+    const int f = m->c.fmt_lm_head;
+    const size_t rb = (h / kq_block_elems(f)) * kq_block_bytes(f);
+    std::vector<float> w(m->vocab * h);
+    fill_normal_parallel(w.data(), w.size(), seed_base + 1 + 8 * m->L, stddev);
+    std::vector<uint8_t> bytes(m->vocab * rb);
+    const unsigned nt = 16;
+    std::vector<std::thread> th;
+    for (unsigned t = 0; t < nt; t++)
+      th.emplace_back([&, t] {
+        const size_t r0 = m->vocab * t / nt, r1 = m->vocab * (t + 1) / nt;
+        kq_encode(f, w.data() + r0 * h, r1 - r0, h, bytes.data() + r0 * rb);
+      });
+    for (auto &x : th) x.join();
+    SYN_TRY(syn_hip_klm_set_lm_head(m, bytes.data()));
+  }
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_klm_finalize(syn_hip_klm_t *m) {
+  if (!m) return SYN_ERR_NULL_PTR;
+  if (!m->have_embed || !m->have_lm) {
+    set_error("embed_tokens or lm_head not set");
+    return SYN_ERR_INVALID_ARG;
+  }
+  for (size_t l = 0; l < m->L; l++)
+    if (m->layers[l].have != 0x7f) {
+      set_error("layer " + std::to_string(l) + " incomplete");
+      return SYN_ERR_INVALID_ARG;
+    }
+  const size_t half = m->hd / 2;
+  std::vector<float> cs(m->S * half), sn(m->S * half);
+  const float fb = (float)m->c.base.rope_theta;
+  for (size_t pos = 0; pos < m->S; pos++)
+    for (size_t i = 0; i < half; i++) {  // models/lm/builder.rs:121-129
+      const float freq = 1.0f / powf(fb, 2.0f * (float)i / (float)m->hd);
+      const float scaled = freq / 1.0f;
+      const float angle = (float)pos * scaled;
+      cs[pos * half + i] = cosf(angle);
+      sn[pos * half + i] = sinf(angle);
+    }
+  SYN_HIP(hipMemcpy(m->rope_cos.p, cs.data(), cs.size() * 4, hipMemcpyHostToDevice));
+  SYN_HIP(hipMemcpy(m->rope_sin.p, sn.data(), sn.size() * 4, hipMemcpyHostToDevice));
+  for (auto &Ly : m->layers) {
+    SYN_TRY(Ly.qkv.prepare(m->S));
+    SYN_TRY(Ly.o.prepare(m->S));
+    SYN_TRY(Ly.gu.prepare(m->S));
+    SYN_TRY(Ly.down.prepare(m->S));
+  }
+  SYN_TRY(m->lm_head.prepare(1));
+  m->finalized = true;
+  SYN_TRY(m->set_state(0, 0, 0));
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_klm_reset(syn_hip_klm_t *m) {
+  SYN_TRY(check_klm(m));
+  return m->set_state(0, 0, 0);
+}
+
+syn_status_t syn_hip_klm_forward_prefill(syn_hip_klm_t *m, const uint32_t *ids, size_t n,
+                                         float *host_logits) {
+  SYN_TRY(check_klm(m));
+  if (!ids) return SYN_ERR_NULL_PTR;
+  SYN_TRY(m->prefill(ids, n));
+  if (host_logits)
+    SYN_HIP(hipMemcpyAsync(host_logits, m->logits.p, m->vocab * 4, hipMemcpyDeviceToHost,
+                           m->stream));
+  SYN_HIP(hipStreamSynchronize(m->stream));
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_klm_forward_one(syn_hip_klm_t *m, uint32_t token, float *host_logits) {
+  SYN_TRY(check_klm(m));
+  StepState cur;
+  SYN_TRY(m->get_state(&cur));
+  if ((size_t)cur.pos >= m->S) {
+    set_error("KV cache full");
+    return SYN_ERR_INVALID_ARG;
+  }
+  SYN_TRY(m->build_graph());
+  SYN_TRY(m->set_state(cur.pos, token, cur.step));
+  SYN_HIP(hipGraphLaunch(m->graph, m->stream));
+  if (host_logits)
+    SYN_HIP(hipMemcpyAsync(host_logits, m->logits.p, m->vocab * 4, hipMemcpyDeviceToHost,
+                           m->stream));
+  SYN_HIP(hipStreamSynchronize(m->stream));
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_klm_generate(syn_hip_klm_t *m, const uint32_t *prompt, size_t n_prompt,
+                                  size_t max_new, uint32_t *out_tokens, float *out_margins) {
+  SYN_TRY(check_klm(m));
+  if (!prompt || !out_tokens) return SYN_ERR_NULL_PTR;
+  if (max_new == 0) return SYN_OK;
+  if (n_prompt + max_new - 1 > m->S) {
+    set_error("prompt + generated tokens exceed max_seq");
+    return SYN_ERR_INVALID_ARG;
+  }
+  SYN_TRY(m->build_graph());
+  SYN_TRY(m->prefill(prompt, n_prompt));
+  for (size_t i = 1; i < max_new; i++) SYN_HIP(hipGraphLaunch(m->graph, m->stream));
+  SYN_HIP(hipMemcpyAsync(out_tokens, m->history.p, max_new * 4, hipMemcpyDeviceToHost,
+                         m->stream));
+  if (out_margins)
+    SYN_HIP(hipMemcpyAsync(out_margins, m->mhist.p, max_new * 4, hipMemcpyDeviceToHost,
+                           m->stream));
+  SYN_HIP(hipStreamSynchronize(m->stream));
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_klm_time(syn_hip_klm_t *m, const uint32_t *prompt, size_t n_prompt,
+                              size_t steps, float *prefill_ms, float *decode_ms) {
+  SYN_TRY(check_klm(m));
+  if (!prompt || !prefill_ms || !decode_ms) return SYN_ERR_NULL_PTR;
+  if (n_prompt + steps > m->S) {
+    set_error("prompt + decode steps exceed max_seq");
+    return SYN_ERR_INVALID_ARG;
+  }
+  SYN_TRY(m->build_graph());
+  hipEvent_t a, b, c;
+  SYN_HIP(hipEventCreate(&a));
+  SYN_HIP(hipEventCreate(&b));
+  SYN_HIP(hipEventCreate(&c));
+  SYN_HIP(hipMemcpyAsync(m->ids.p, prompt, n_prompt * 4, hipMemcpyHostToDevice, m->stream));
+  SYN_TRY(m->set_state(0, 0, 0));
+  SYN_HIP(hipEventRecord(a, m->stream));
+  SYN_TRY(launch_embed(m->embed.as<float>(), m->ids.as<uint32_t>(), (int)n_prompt, (int)m->h,
+                       (int)m->vocab, m->x.as<float>(), m->stream));
+  for (size_t l = 0; l < m->L; l++) SYN_TRY(m->layer(l, (int)n_prompt, true, m->stream));
+  SYN_TRY(m->head((int)n_prompt - 1, (int)n_prompt, m->stream));
+  SYN_HIP(hipEventRecord(b, m->stream));
+  for (size_t i = 0; i < steps; i++) SYN_HIP(hipGraphLaunch(m->graph, m->stream));
+  SYN_HIP(hipEventRecord(c, m->stream));
+  SYN_HIP(hipEventSynchronize(c));
+  SYN_HIP(hipEventElapsedTime(prefill_ms, a, b));
+  SYN_HIP(hipEventElapsedTime(decode_ms, b, c));
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  (void)hipEventDestroy(c);
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_klm_destroy(syn_hip_klm_t *m) {
+  if (m) {
+    (void)hipStreamSynchronize(m->stream);
+    delete m;
+  }
+  return SYN_OK;
+}
+
+}  // extern "C"

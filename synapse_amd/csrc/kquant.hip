@@ -445,6 +445,7 @@ static void launch_kq_m(int m, const GemvPlan &p, const void *W, const uint16_t 
 syn_status_t QLinearKQ::gemv(size_t m, const float *d_x, size_t ldx, float *d_y, size_t ldy,
                              hipStream_t s) {
   if (m == 0 || n == 0 || k == 0) return SYN_OK;
+  if (m > 8) return gemm(m, d_x, ldx, d_y, ldy, s);
   const GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
   const size_t N64 = (size_t)p.panels * 64;
   for (size_t m0 = 0; m0 < m; m0 += 4) {
@@ -478,9 +479,12 @@ syn_status_t QLinearKQ::gemv(size_t m, const float *d_x, size_t ldx, float *d_y,
 }
 
 syn_status_t QLinearKQ::prepare(size_t max_m) {
+  if (max_m > 8 && xh_elems < max_m * k) {
+    SYN_TRY(xh.alloc(max_m * k * 2));
+    xh_elems = max_m * k;
+  }
   const GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
   if (p.ksplit <= 1) return SYN_OK;
-  (void)max_m;
   const size_t need = (size_t)p.ksplit * 4 * p.panels * 64;
   if (part_elems >= need) return SYN_OK;
   part_elems = need;

@@ -19,11 +19,16 @@ struct QLinearKQ {
   DevBuf wd;       // [P][blocks][64] f16 d (Q8_0, Q6_K)
   DevBuf part;
   size_t part_elems = 0;
+  DevBuf xh;  // f16 activations for the MFMA GEMM
+  size_t xh_elems = 0;
   syn_status_t upload(int fmt, const uint8_t *gguf, size_t n, size_t k);
   syn_status_t from_f32(int fmt, const float *w, size_t n, size_t k);
   size_t weight_bytes() const;
-  // y[m,n] = x[m,k] W^T, f32 activations (M rows, any M)
+  // y[m,n] = x[m,k] W^T, f32 activations (M rows, any M; M > 8 runs gemm())
   syn_status_t gemv(size_t m, const float *d_x, size_t ldx, float *d_y, size_t ldy,
+                    hipStream_t s);
+  // f16 MFMA prefill GEMM (kquant_gemm.hip)
+  syn_status_t gemm(size_t m, const float *d_x, size_t ldx, float *d_y, size_t ldy,
                     hipStream_t s);
   syn_status_t prepare(size_t max_m);
 };

@@ -127,6 +127,7 @@ __global__ void __launch_bounds__(256)
     sm[j] = nv;
     if (normed) normed[(size_t)row * H + j] = nv;
   }
+  if (!xq) return;  // f32 path: normed rows only
   __syncthreads();
   quantize_row_lds(sm, H, xq + (size_t)row * ldq, sx + row, red);
 }
@@ -408,6 +409,35 @@ syn_status_t launch_swiglu_quant(const float *gu, int ldgu, int rows, int inter,
                                  int ldq, float *sh, hipStream_t s) {
   hipLaunchKernelGGL(k_swiglu_quant, dim3(rows), dim3(256), inter * sizeof(float), s, gu, ldgu,
                      inter, hq, ldq, sh);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
+
+// ------------------------------------------------------------------ SwiGLU (f32 path)
+// zig/src/ops/silu.zig:85-114 (syn_swiglu, used by the f32 decoder
+// decoder_layer.rs:690-700): on the 4-aligned prefix sig = 1/(1+exp(-g)),
+// h = (g*sig)*u; on the tail h = (g/(1+exp(-g)))*u.
+__global__ void k_swiglu_f32(const float *__restrict__ gu, int ldgu, int inter,
+                             float *__restrict__ h, int ldh) {
+  const int row = blockIdx.y;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= inter) return;
+  const float g = gu[(size_t)row * ldgu + i], u = gu[(size_t)row * ldgu + inter + i];
+  const int n4 = inter - inter % 4;
+  float t;
+  if (i < n4) {
+    const float sig = 1.0f / (1.0f + syn_expf(-g));
+    t = g * sig;
+  } else {
+    t = g / (1.0f + syn_expf(-g));
+  }
+  h[(size_t)row * ldh + i] = t * u;
+}
+
+syn_status_t launch_swiglu_f32(const float *gu, int ldgu, int rows, int inter, float *h, int ldh,
+                               hipStream_t s) {
+  hipLaunchKernelGGL(k_swiglu_f32, dim3((inter + 255) / 256, rows), dim3(256), 0, s, gu, ldgu,
+                     inter, h, ldh);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
 }

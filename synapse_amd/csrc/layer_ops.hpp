@@ -18,6 +18,7 @@ struct StepState {  // device-resident decode state (read by kernels in a graph)
 syn_status_t launch_embed(const float *embed, const uint32_t *ids, int rows, int hidden,
                           int vocab, float *x, hipStream_t s);
 // per row: x += delta (if delta); normed = rmsnorm(x, w, eps); quantize(normed)
+// (xq == nullptr: no quantization, normed must be given)
 syn_status_t launch_rmsnorm_quant(float *x, const float *delta, const float *w, float eps,
                                   int rows, int hidden, int8_t *xq, int ldq, float *sx,
                                   float *normed, hipStream_t s);
@@ -40,6 +41,9 @@ syn_status_t launch_attention_prefill(const float *q, const float *kcache, const
 // h = silu(gate) * up (int8.rs:500-503), then quantize rows of h
 syn_status_t launch_swiglu_quant(const float *gu, int ldgu, int rows, int inter, int8_t *hq,
                                  int ldq, float *sh, hipStream_t s);
+// f32-path SwiGLU (Zig swigluFused order) from [gate | up] rows
+syn_status_t launch_swiglu_f32(const float *gu, int ldgu, int rows, int inter, float *h, int ldh,
+                               hipStream_t s);
 // greedy argmax (last maximum wins, sampler.rs:217-224) -> state->token,
 // top1-top2 margin -> state->margin, token also stored to history[state->step]
 syn_status_t launch_argmax(const float *logits, int n, float *part_v, int *part_i,

@@ -34,6 +34,12 @@ class LmConfig(C.Structure):
                 ("rope_theta", C.c_double)]
 
 
+class KLmConfig(C.Structure):
+    _fields_ = [("base", LmConfig), ("fmt_qkv", C.c_int32), ("fmt_o", C.c_int32),
+                ("fmt_gate_up", C.c_int32), ("fmt_down", C.c_int32),
+                ("fmt_lm_head", C.c_int32), ("qk_norm", C.c_int32)]
+
+
 SIGNATURES = {
     "syn_quantize_per_channel_int8": (ST, [P, SZ, SZ, P, P]),
     "syn_qgemm_int8": (ST, [SZ, SZ, SZ, P, SZ, P, SZ, P, SZ, P, P]),
@@ -77,6 +83,18 @@ SIGNATURES = {
     "syn_hip_qlm_decode_timed": (ST, [P, SZ, C.POINTER(C.c_float)]),
     "syn_hip_qlm_time_lm_head": (ST, [P, SZ, SZ, C.POINTER(C.c_float)]),
     "syn_hip_qlm_destroy": (ST, [P]),
+    "syn_hip_klm_create": (ST, [C.POINTER(KLmConfig), C.POINTER(P)]),
+    "syn_hip_klm_set_embed": (ST, [P, P]),
+    "syn_hip_klm_set_proj": (ST, [P, C.c_uint32, C.c_int, P]),
+    "syn_hip_klm_set_lm_head": (ST, [P, P]),
+    "syn_hip_klm_init_synthetic": (ST, [P, C.c_uint64, C.c_float]),
+    "syn_hip_klm_finalize": (ST, [P]),
+    "syn_hip_klm_reset": (ST, [P]),
+    "syn_hip_klm_forward_prefill": (ST, [P, P, SZ, P]),
+    "syn_hip_klm_forward_one": (ST, [P, C.c_uint32, P]),
+    "syn_hip_klm_generate": (ST, [P, P, SZ, SZ, P, P]),
+    "syn_hip_klm_time": (ST, [P, P, SZ, SZ, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
+    "syn_hip_klm_destroy": (ST, [P]),
     "syn_hip_fill_normal": (ST, [P, SZ, C.c_uint64, C.c_float]),
     "syn_hip_eval_expf": (ST, [P, P, SZ, P]),
     "syn_hip_kquant_encode": (ST, [C.c_int, SZ, SZ, P, P]),
@@ -381,6 +399,76 @@ class QuantizedCausalLM:
     def close(self):
         if self.h:
             lib().syn_hip_qlm_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class KQuantCausalLM:
+    """Device-resident f32 decoder over Q8_0/Q4_K/Q6_K weights (CausalLM)."""
+
+    def __init__(self, cfg: dict, fmt_qkv=FMT_Q4_K, fmt_o=FMT_Q4_K, fmt_gate_up=FMT_Q4_K,
+                 fmt_down=FMT_Q6_K, fmt_lm_head=FMT_Q6_K, qk_norm=False):
+        self.cfg = dict(cfg)
+        base = LmConfig(cfg["hidden"], cfg["n_layers"], cfg["n_heads"], cfg["n_kv_heads"],
+                        cfg["head_dim"], cfg["inter"], cfg["vocab"], cfg["max_seq"],
+                        cfg.get("eps", 1e-5), cfg.get("rope_theta", 5e5))
+        c = KLmConfig(base, fmt_qkv, fmt_o, fmt_gate_up, fmt_down, fmt_lm_head,
+                      1 if qk_norm else 0)
+        h = C.c_void_p()
+        check(lib().syn_hip_klm_create(C.byref(c), C.byref(h)), "klm_create")
+        self.h = h.value
+
+    def init_synthetic(self, seed_base: int = 0x5EED0000, std: float = 0.02):
+        check(lib().syn_hip_klm_init_synthetic(self.h, seed_base, std), "klm_init_synthetic")
+        check(lib().syn_hip_klm_finalize(self.h), "klm_finalize")
+
+    def set_embed(self, embed):
+        check(lib().syn_hip_klm_set_embed(self.h, ptr(np.ascontiguousarray(embed, np.float32))))
+
+    def set_proj(self, layer: int, proj: int, blocks: np.ndarray):
+        check(lib().syn_hip_klm_set_proj(self.h, layer, proj,
+                                         ptr(np.ascontiguousarray(blocks, np.uint8))), "set_proj")
+
+    def set_lm_head(self, blocks: np.ndarray):
+        check(lib().syn_hip_klm_set_lm_head(self.h, ptr(np.ascontiguousarray(blocks, np.uint8))))
+
+    def finalize(self):
+        check(lib().syn_hip_klm_finalize(self.h), "klm_finalize")
+
+    def prefill(self, ids):
+        ids = np.ascontiguousarray(ids, np.uint32)
+        out = np.empty(self.cfg["vocab"], np.float32)
+        check(lib().syn_hip_klm_forward_prefill(self.h, ptr(ids), ids.size, ptr(out)), "prefill")
+        return out
+
+    def forward_one(self, token: int):
+        out = np.empty(self.cfg["vocab"], np.float32)
+        check(lib().syn_hip_klm_forward_one(self.h, int(token), ptr(out)), "forward_one")
+        return out
+
+    def generate(self, prompt, max_new: int):
+        prompt = np.ascontiguousarray(prompt, np.uint32)
+        toks = np.zeros(max_new, np.uint32)
+        margins = np.zeros(max_new, np.float32)
+        check(lib().syn_hip_klm_generate(self.h, ptr(prompt), prompt.size, max_new, ptr(toks),
+                                         ptr(margins)), "generate")
+        return toks, margins
+
+    def time(self, prompt, steps: int):
+        prompt = np.ascontiguousarray(prompt, np.uint32)
+        p, d = C.c_float(), C.c_float()
+        check(lib().syn_hip_klm_time(self.h, ptr(prompt), prompt.size, steps, C.byref(p),
+                                     C.byref(d)), "klm_time")
+        return p.value, d.value
+
+    def close(self):
+        if self.h:
+            lib().syn_hip_klm_destroy(self.h)
             self.h = None
 
     def __del__(self):

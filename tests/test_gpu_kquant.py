@@ -93,3 +93,37 @@ def test_kquant_shape_errors():
     w = np.zeros((4, 100), np.float32)
     with pytest.raises(hip.SynapseError):
         hip.QLinear.from_f32(hip.FMT_Q4_K, w)  # k % 256
+
+
+GEMM_CASES = [("q8_0", 40, 4096, 1024), ("q8_0", 300, 1024, 512), ("q4_k", 64, 3072, 384),
+              ("q6_k", 33, 2048, 200), ("q4_k", 9, 512, 130), ("q8_0", 129, 96, 257)]
+
+
+@pytest.mark.parametrize("name,m,k,n", GEMM_CASES)
+def test_kquant_gemm_vs_reference(name, m, k, n):
+    # M > 8: f16 MFMA prefill GEMM; reference = dequant + sgemmTiled semantics
+    w = O.normal(n * k, 3 * k + n, 0.02).reshape(n, k)
+    blocks = hip.kquant_encode(FMTS[name], w)
+    lin = hip.QLinear.gguf(FMTS[name], blocks, n, k)
+    x = O.normal(m * k, m + k, 1.0).reshape(m, k)
+    got = lin.forward(x)
+    deq = O.dequant(name, blocks, n * k).reshape(n, k)
+    want = O.matmul_t(x, deq)
+    worst = max(_rel(got[i], want[i]) for i in range(m))
+    print(f"{name} {m}x{k}->{n}: worst per-row rel err {worst:.2e}")
+    assert worst <= TOL, worst
+
+
+def test_kquant_gemm_mistral_shape_sampled_rows():
+    # config 4 shape (Q8_0 gate/up 4096 -> 14336, M = 512): check sampled rows in f64
+    m, k, n = 512, 4096, 14336
+    rng = np.random.default_rng(9)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    blocks = hip.kquant_encode(hip.FMT_Q8_0, w)
+    lin = hip.QLinear.gguf(hip.FMT_Q8_0, blocks, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    got = lin.forward(x)
+    deq = O.dequant("q8_0", blocks, n * k).reshape(n, k).astype(np.float64)
+    for i in (0, 1, 255, 511):
+        want = deq @ x[i].astype(np.float64)
+        assert _rel(got[i], want) <= TOL
