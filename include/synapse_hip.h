@@ -228,6 +228,31 @@ syn_status_t syn_hip_klm_time(syn_hip_klm_t *m, const uint32_t *prompt, size_t n
                               size_t steps, float *prefill_ms, float *decode_ms);
 syn_status_t syn_hip_klm_destroy(syn_hip_klm_t *m);
 
+/* -- INT8 Mamba: QuantizedMambaModel (quantization/ssm/int8_mamba.rs:21-224).
+ *    in_proj/out_proj W8A8 INT8, x_proj/dt_proj/lm_head f32 (tied to the
+ *    embedding), selective scan as in zig/src/ops/selective_scan.zig:30-90.
+ *    int8_xdt = 1 also runs x_proj and dt_proj as INT8 W8A8 (no reference
+ *    counterpart; BASELINE config 5's variant).  max_tokens bounds prompt +
+ *    generated tokens of one sequence. -- */
+typedef struct {
+  uint32_t d_model, d_inner, d_state, d_conv, dt_rank, n_layers, vocab, max_tokens;
+  float eps;
+  int32_t int8_xdt;
+} syn_hip_mamba_config;
+
+typedef struct syn_hip_mamba_s syn_hip_mamba_t;
+syn_status_t syn_hip_mamba_create(const syn_hip_mamba_config *cfg, syn_hip_mamba_t **out);
+syn_status_t syn_hip_mamba_init_synthetic(syn_hip_mamba_t *m, uint64_t seed_base, float stddev);
+/* QuantizedMambaModel::prefill (per-token recurrence, :177-203) */
+syn_status_t syn_hip_mamba_prefill(syn_hip_mamba_t *m, const uint32_t *ids, size_t n,
+                                   float *host_logits);
+/* QuantizedMambaModel::decode_one (:205-224) */
+syn_status_t syn_hip_mamba_decode_one(syn_hip_mamba_t *m, uint32_t token, float *host_logits);
+syn_status_t syn_hip_mamba_generate(syn_hip_mamba_t *m, const uint32_t *prompt, size_t n_prompt,
+                                    size_t max_new, uint32_t *out_tokens, float *out_margins);
+syn_status_t syn_hip_mamba_decode_timed(syn_hip_mamba_t *m, size_t steps, float *elapsed_ms);
+syn_status_t syn_hip_mamba_destroy(syn_hip_mamba_t *m);
+
 /* -- harness helpers (no reference counterpart) -- */
 /* Encode f32 [n,k] into Q8_0 / Q4_K / Q6_K block bytes.  The reference has no
  * encoder for these formats (only dequantizers); any encoding is valid since

@@ -53,6 +53,11 @@ class LmCfg(C.Structure):
                 ("eps", C.c_float), ("rope_theta", C.c_double)]
 
 
+class MambaCfg(C.Structure):
+    _fields_ = [("d_model", SZ), ("d_inner", SZ), ("d_state", SZ), ("d_conv", SZ),
+                ("dt_rank", SZ), ("n_layers", SZ), ("vocab", SZ), ("eps", C.c_float)]
+
+
 def _declare(L):
     sig = {
         "orc_fill_normal": (None, [P, SZ, C.c_uint64, C.c_float]),
@@ -105,6 +110,16 @@ def _declare(L):
         "orc_flm_forward_one": (C.c_int, [P, C.c_uint32, P]),
         "orc_flm_generate": (C.c_int, [P, P, SZ, SZ, P, P]),
         "orc_swiglu_fused": (None, [P, P, P, SZ]),
+        "orc_mamba_create": (P, [C.POINTER(MambaCfg)]),
+        "orc_mamba_destroy": (None, [P]),
+        "orc_mamba_init_synthetic": (C.c_int, [P, C.c_uint64]),
+        "orc_mamba_reset": (None, [P]),
+        "orc_mamba_prefill": (C.c_int, [P, P, SZ, P]),
+        "orc_mamba_decode_one": (C.c_int, [P, C.c_uint32, P]),
+        "orc_mamba_generate": (C.c_int, [P, P, SZ, SZ, P, P]),
+        "orc_softplus": (C.c_float, [C.c_float]),
+        "orc_rmsnorm_seq": (None, [P, P, C.c_float, SZ, P]),
+        "orc_selective_scan_step": (None, [P, P, P, P, P, P, P, P, SZ, SZ]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -399,6 +414,50 @@ class CausalLM:
     def close(self):
         if self.h:
             lib().orc_flm_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class QuantizedMamba:
+    """INT8 Mamba (quantization/ssm/int8_mamba.rs) restated in C."""
+
+    def __init__(self, cfg: dict):
+        self.cfg = cfg
+        c = MambaCfg(cfg["d_model"], cfg["d_inner"], cfg["d_state"], cfg["d_conv"],
+                     cfg["dt_rank"], cfg["n_layers"], cfg["vocab"], cfg.get("eps", 1e-5))
+        self._c = c
+        self.h = lib().orc_mamba_create(C.byref(c))
+
+    def init_synthetic(self, seed_base: int = 0x5EED0000):
+        if lib().orc_mamba_init_synthetic(self.h, seed_base):
+            raise RuntimeError("orc_mamba_init_synthetic failed")
+
+    def prefill(self, ids):
+        ids = np.ascontiguousarray(ids, np.uint32)
+        out = np.empty(self.cfg["vocab"], np.float32)
+        lib().orc_mamba_prefill(self.h, _p(ids), ids.size, _p(out))
+        return out
+
+    def decode_one(self, token: int):
+        out = np.empty(self.cfg["vocab"], np.float32)
+        lib().orc_mamba_decode_one(self.h, int(token), _p(out))
+        return out
+
+    def generate(self, prompt, max_new: int):
+        prompt = np.ascontiguousarray(prompt, np.uint32)
+        toks = np.zeros(max_new, np.uint32)
+        margins = np.zeros(max_new, np.float32)
+        lib().orc_mamba_generate(self.h, _p(prompt), prompt.size, max_new, _p(toks), _p(margins))
+        return toks, margins
+
+    def close(self):
+        if self.h:
+            lib().orc_mamba_destroy(self.h)
             self.h = None
 
     def __del__(self):

@@ -1224,3 +1224,245 @@ int orc_flm_generate(orc_flm *m, const uint32_t *prompt, size_t n_prompt, size_t
   free(logits);
   return rc;
 }
+
+/* ======================================================================
+ * INT8 Mamba (quantization/ssm/int8_mamba.rs:21-224)
+ * ==================================================================== */
+/* ops/activation.rs:88-90 */
+float orc_softplus(float x) { return x > 20.0f ? x : logf(1.0f + expf(x)); }
+
+/* ops/pure_rust_ops.rs:96-112: one sequential sum of squares */
+void orc_rmsnorm_seq(const float *x, const float *w, float eps, size_t hidden, float *out) {
+  float s = 0.0f;
+  for (size_t i = 0; i < hidden; i++) {
+    float t = x[i] * x[i];
+    s = s + t;
+  }
+  float scale = 1.0f / sqrtf(s / (float)hidden + eps);
+  for (size_t j = 0; j < hidden; j++) {
+    float t = x[j] * w[j];
+    out[j] = t * scale;
+  }
+}
+
+/* zig/src/ops/selective_scan.zig:30-90 */
+void orc_selective_scan_step(const float *x, const float *delta, const float *a_log,
+                             const float *b, const float *c, const float *d, float *state,
+                             float *y, size_t d_inner, size_t d_state) {
+  for (size_t i = 0; i < d_inner; i++) {
+    float dt = delta[i], xi = x[i];
+    float dt_x = dt * xi;
+    float yi = 0.0f;
+    float *h = state + i * d_state;
+    const float *al = a_log + i * d_state;
+    size_t j = 0;
+    for (; j + 4 <= d_state; j += 4) {
+      float contrib[4];
+      for (int l = 0; l < 4; l++) {
+        float e = expf(al[j + l]);
+        float ad = expf(-dt * e);
+        float p1 = ad * h[j + l], p2 = dt_x * b[j + l];
+        float hn = p1 + p2;
+        h[j + l] = hn;
+        contrib[l] = c[j + l] * hn;
+      }
+      yi += ((contrib[0] + contrib[1]) + contrib[2]) + contrib[3];
+    }
+    for (; j < d_state; j++) {
+      float a = -expf(al[j]);
+      float ad = expf(dt * a);
+      float hn = ad * h[j] + dt * b[j] * xi;
+      h[j] = hn;
+      yi += c[j] * hn;
+    }
+    y[i] = yi + d[i] * xi;
+  }
+}
+
+typedef struct {
+  orc_qlin in_proj, out_proj;            /* [2*d_inner, d_model], [d_model, d_inner] */
+  float *conv_w, *conv_b;                /* [d_inner, d_conv], [d_inner] */
+  float *x_proj, *dt_proj, *dt_bias;     /* [dt_rank+2*d_state, d_inner], [d_inner, dt_rank], [d_inner] */
+  float *a_log, *d_param, *norm_w;       /* [d_inner, d_state], [d_inner], [d_model] */
+  float *conv_state, *ssm_state;         /* [d_inner, d_conv], [d_inner, d_state] */
+} orc_mblock;
+
+struct orc_mamba {
+  orc_mamba_cfg c;
+  float *embed, *final_norm;
+  orc_qlin lm_dummy;
+  orc_mblock *blk;
+};
+
+orc_mamba *orc_mamba_create(const orc_mamba_cfg *cfg) {
+  orc_mamba *m = (orc_mamba *)calloc(1, sizeof(orc_mamba));
+  if (!m) return NULL;
+  m->c = *cfg;
+  m->blk = (orc_mblock *)calloc(cfg->n_layers, sizeof(orc_mblock));
+  return m;
+}
+
+void orc_mamba_destroy(orc_mamba *m) {
+  if (!m) return;
+  for (size_t l = 0; l < m->c.n_layers; l++) {
+    orc_mblock *b = &m->blk[l];
+    free(b->in_proj.w); free(b->in_proj.s); free(b->out_proj.w); free(b->out_proj.s);
+    free(b->conv_w); free(b->conv_b); free(b->x_proj); free(b->dt_proj); free(b->dt_bias);
+    free(b->a_log); free(b->d_param); free(b->norm_w); free(b->conv_state); free(b->ssm_state);
+  }
+  free(m->blk);
+  free(m->embed);
+  free(m->final_norm);
+  free(m);
+}
+
+/* Synthetic weights (harness spec): embed (tied lm_head) id 0, block l:
+ * 1+16l+{0 in_proj, 1 conv1d, 2 x_proj, 3 dt_proj, 4 out_proj} ~ N(0, 0.02);
+ * conv bias 0, dt bias log(expm1(0.01)), a_log[i][s] = log(s+1), D = 1, norms 1. */
+int orc_mamba_init_synthetic(orc_mamba *m, uint64_t seed_base) {
+  const orc_mamba_cfg *c = &m->c;
+  size_t dm = c->d_model, di = c->d_inner, ds = c->d_state, dc = c->d_conv, dr = c->dt_rank;
+  m->embed = (float *)malloc(c->vocab * dm * 4);
+  m->final_norm = (float *)malloc(dm * 4);
+  if (!m->embed || !m->final_norm) return ORC_ERR_OUT_OF_MEMORY;
+  fill_normal_par(m->embed, c->vocab * dm, seed_base, 0.02f);
+  for (size_t i = 0; i < dm; i++) m->final_norm[i] = 1.0f;
+  const float dt_bias = logf(expm1f(0.01f));
+  int bad = 0;
+#pragma omp parallel for schedule(dynamic) reduction(| : bad)
+  for (long ll = 0; ll < (long)c->n_layers; ll++) {
+    size_t l = (size_t)ll;
+    orc_mblock *b = &m->blk[l];
+    uint64_t sb = seed_base + 1 + 16 * l;
+    float *w = (float *)malloc(2 * di * dm * 4);
+    orc_fill_normal(w, 2 * di * dm, sb + 0, 0.02f);
+    bad |= qlin_from_f32(&b->in_proj, w, 2 * di, dm);
+    orc_fill_normal(w, dm * di, sb + 4, 0.02f);
+    bad |= qlin_from_f32(&b->out_proj, w, dm, di);
+    free(w);
+    b->conv_w = (float *)malloc(di * dc * 4);
+    orc_fill_normal(b->conv_w, di * dc, sb + 1, 0.02f);
+    b->conv_b = (float *)calloc(di, 4);
+    b->x_proj = (float *)malloc((dr + 2 * ds) * di * 4);
+    orc_fill_normal(b->x_proj, (dr + 2 * ds) * di, sb + 2, 0.02f);
+    b->dt_proj = (float *)malloc(di * dr * 4);
+    orc_fill_normal(b->dt_proj, di * dr, sb + 3, 0.02f);
+    b->dt_bias = (float *)malloc(di * 4);
+    b->a_log = (float *)malloc(di * ds * 4);
+    b->d_param = (float *)malloc(di * 4);
+    b->norm_w = (float *)malloc(dm * 4);
+    for (size_t i = 0; i < di; i++) {
+      b->dt_bias[i] = dt_bias;
+      b->d_param[i] = 1.0f;
+      for (size_t s2 = 0; s2 < ds; s2++) b->a_log[i * ds + s2] = logf((float)(s2 + 1));
+    }
+    for (size_t i = 0; i < dm; i++) b->norm_w[i] = 1.0f;
+    b->conv_state = (float *)calloc(di * dc, 4);
+    b->ssm_state = (float *)calloc(di * ds, 4);
+  }
+  return bad ? ORC_ERR_OUT_OF_MEMORY : ORC_OK;
+}
+
+void orc_mamba_reset(orc_mamba *m) {
+  for (size_t l = 0; l < m->c.n_layers; l++) {
+    memset(m->blk[l].conv_state, 0, m->c.d_inner * m->c.d_conv * 4);
+    memset(m->blk[l].ssm_state, 0, m->c.d_inner * m->c.d_state * 4);
+  }
+}
+
+/* QuantizedMambaBlock::forward_one (int8_mamba.rs:78-109) */
+static void mamba_block_one(const orc_mamba *m, orc_mblock *b, const float *hid, float *out) {
+  const orc_mamba_cfg *c = &m->c;
+  size_t dm = c->d_model, di = c->d_inner, ds = c->d_state, dc = c->d_conv, dr = c->dt_rank;
+  float *normed = (float *)malloc(dm * 4), *proj = (float *)malloc(2 * di * 4);
+  float *xc = (float *)malloc(di * 4), *xp = (float *)malloc((dr + 2 * ds) * 4);
+  float *dtp = (float *)malloc(di * 4), *delta = (float *)malloc(di * 4);
+  float *y = (float *)malloc(di * 4), *g = (float *)malloc(di * 4), *o = (float *)malloc(dm * 4);
+  int8_t *xq = (int8_t *)malloc(2 * di > dm ? 2 * di : dm);
+  float sx;
+  orc_rmsnorm_seq(hid, b->norm_w, c->eps, dm, normed);
+  qlin_forward(&b->in_proj, normed, 1, proj, xq, &sx);
+  for (size_t i = 0; i < di; i++) { /* conv1d_step :43-56 */
+    float *buf = b->conv_state + i * dc;
+    memmove(buf, buf + 1, (dc - 1) * 4);
+    buf[dc - 1] = proj[i];
+    const float *w = b->conv_w + i * dc;
+    float sum = 0.0f;
+    for (size_t k = 0; k < dc; k++) {
+      float t = buf[k] * w[k];
+      sum = sum + t;
+    }
+    xc[i] = orc_silu(sum + b->conv_b[i]);
+  }
+  /* ssm_forward_step :59-75: x_proj and dt_proj are f32 matmul_t */
+  memset(xp, 0, (dr + 2 * ds) * 4);
+  orc_sgemm(1, dr + 2 * ds, di, xc, di, 0, b->x_proj, di, 1, xp, dr + 2 * ds);
+  memset(dtp, 0, di * 4);
+  orc_sgemm(1, di, dr, xp, dr, 0, b->dt_proj, dr, 1, dtp, di);
+  for (size_t i = 0; i < di; i++) delta[i] = orc_softplus(dtp[i] + b->dt_bias[i]);
+  orc_selective_scan_step(xc, delta, b->a_log, xp + dr, xp + dr + ds, b->d_param, b->ssm_state, y,
+                          di, ds);
+  for (size_t i = 0; i < di; i++) g[i] = orc_silu(proj[di + i]) * y[i];
+  qlin_forward(&b->out_proj, g, 1, o, xq, &sx);
+  for (size_t i = 0; i < dm; i++) out[i] = o[i] + hid[i];
+  free(normed); free(proj); free(xc); free(xp); free(dtp); free(delta); free(y); free(g);
+  free(o); free(xq);
+}
+
+static void mamba_token(orc_mamba *m, uint32_t token, float *hid) {
+  size_t dm = m->c.d_model;
+  float *tmp = (float *)malloc(dm * 4);
+  if (token < m->c.vocab) memcpy(hid, m->embed + (size_t)token * dm, dm * 4);
+  else memset(hid, 0, dm * 4);
+  for (size_t l = 0; l < m->c.n_layers; l++) {
+    mamba_block_one(m, &m->blk[l], hid, tmp);
+    memcpy(hid, tmp, dm * 4);
+  }
+  free(tmp);
+}
+
+static void mamba_logits(orc_mamba *m, const float *hid, float *logits) {
+  size_t dm = m->c.d_model;
+  float *normed = (float *)malloc(dm * 4);
+  orc_rmsnorm_seq(hid, m->final_norm, m->c.eps, dm, normed);
+  memset(logits, 0, m->c.vocab * 4);
+  orc_sgemm(1, m->c.vocab, dm, normed, dm, 0, m->embed, dm, 1, logits, m->c.vocab);
+  free(normed);
+}
+
+/* prefill :177-203 (per-token loop inside each block = token-major order) */
+int orc_mamba_prefill(orc_mamba *m, const uint32_t *ids, size_t n, float *logits) {
+  if (n == 0) return ORC_ERR_INVALID_ARG;
+  float *hid = (float *)malloc(m->c.d_model * 4);
+  for (size_t t = 0; t < n; t++) mamba_token(m, ids[t], hid);
+  mamba_logits(m, hid, logits);
+  free(hid);
+  return ORC_OK;
+}
+
+int orc_mamba_decode_one(orc_mamba *m, uint32_t token, float *logits) {
+  float *hid = (float *)malloc(m->c.d_model * 4);
+  mamba_token(m, token, hid);
+  mamba_logits(m, hid, logits);
+  free(hid);
+  return ORC_OK;
+}
+
+int orc_mamba_generate(orc_mamba *m, const uint32_t *prompt, size_t n_prompt, size_t max_new,
+                       uint32_t *out_tokens, float *margins) {
+  if (max_new == 0) return ORC_OK;
+  float *logits = (float *)malloc(m->c.vocab * 4);
+  int rc = orc_mamba_prefill(m, prompt, n_prompt, logits);
+  if (rc) { free(logits); return rc; }
+  uint32_t tok = orc_argmax(logits, m->c.vocab);
+  out_tokens[0] = tok;
+  if (margins) margins[0] = top2_margin(logits, m->c.vocab, tok);
+  for (size_t i = 1; i < max_new; i++) {
+    orc_mamba_decode_one(m, tok, logits);
+    tok = orc_argmax(logits, m->c.vocab);
+    out_tokens[i] = tok;
+    if (margins) margins[i] = top2_margin(logits, m->c.vocab, tok);
+  }
+  free(logits);
+  return ORC_OK;
+}

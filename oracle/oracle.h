@@ -133,6 +133,28 @@ int orc_flm_generate(orc_flm *m, const uint32_t *prompt, size_t n_prompt, size_t
                      uint32_t *out_tokens, float *margins);
 void orc_swiglu_fused(float *dst, const float *gate, const float *up, size_t n);
 
+/* ---- INT8 Mamba (quantization/ssm/int8_mamba.rs): in_proj/out_proj W8A8,
+ *      x_proj/dt_proj/lm_head f32, selective scan zig/src/ops/selective_scan.zig ---- */
+typedef struct {
+  size_t d_model, d_inner, d_state, d_conv, dt_rank, n_layers, vocab;
+  float eps;
+} orc_mamba_cfg;
+typedef struct orc_mamba orc_mamba;
+orc_mamba *orc_mamba_create(const orc_mamba_cfg *cfg);
+void orc_mamba_destroy(orc_mamba *m);
+/* synthetic weights (seed spec documented in oracle.c) */
+int orc_mamba_init_synthetic(orc_mamba *m, uint64_t seed_base);
+void orc_mamba_reset(orc_mamba *m);
+int orc_mamba_prefill(orc_mamba *m, const uint32_t *ids, size_t n, float *logits);
+int orc_mamba_decode_one(orc_mamba *m, uint32_t token, float *logits);
+int orc_mamba_generate(orc_mamba *m, const uint32_t *prompt, size_t n_prompt, size_t max_new,
+                       uint32_t *out_tokens, float *margins);
+float orc_softplus(float x);
+void orc_rmsnorm_seq(const float *x, const float *w, float eps, size_t hidden, float *out);
+void orc_selective_scan_step(const float *x, const float *delta, const float *a_log,
+                             const float *b, const float *c, const float *d, float *state,
+                             float *y, size_t d_inner, size_t d_state);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,539 @@
+// INT8 Mamba on the device (A16): QuantizedMambaModel
+// (quantization/ssm/int8_mamba.rs:21-224).  in_proj / out_proj are W8A8 INT8
+// GEMVs (QuantizedLinear); x_proj, dt_proj and the (tied) lm_head are f32
+// matmul_t in the reference and run here as exact-order f32 GEMVs; conv1d,
+// softplus and the selective scan (zig/src/ops/selective_scan.zig:30-90) are
+// one small kernel each.  With `int8_xdt` set, x_proj and dt_proj are INT8
+// W8A8 as well (BASELINE config 5's variant; no reference counterpart).
+//
+// Float order follows the reference everywhere except softplus's log: the
+// reference calls glibc logf, whose last bit differs from a correctly rounded
+// log on ~7% of inputs in [1, 1.1); the device computes log in double and
+// rounds once, so this path is held to the float tolerance, not bit equality.
+#include <algorithm>
+#include <thread>
+#include <vector>
+
+#include "layer_ops.hpp"
+#include "linear.hpp"
+
+using namespace syn;
+
+namespace syn {
+
+// ops/pure_rust_ops.rs:96-112 (one sequential sum of squares) + optional
+// residual add + A1 quantization of the normed row (single workgroup)
+__global__ void __launch_bounds__(256)
+    k_mamba_norm(float *__restrict__ x, const float *__restrict__ delta,
+                 const float *__restrict__ w, float eps, int H, int8_t *__restrict__ xq,
+                 float *__restrict__ sx, float *__restrict__ normed) {
+  extern __shared__ float sm[];
+  __shared__ float red[64];
+  __shared__ float s_scale;
+  for (int j = threadIdx.x; j < H; j += blockDim.x) {
+    float v = x[j];
+    if (delta) {
+      v = delta[j] + v;  // int8_mamba.rs:108: o + h
+      x[j] = v;
+    }
+    sm[j] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float s = 0.0f;
+    for (int i = 0; i < H; i++) {
+      const float t = sm[i] * sm[i];
+      s = s + t;
+    }
+    s_scale = 1.0f / sqrtf(s / (float)H + eps);
+  }
+  __syncthreads();
+  const float scale = s_scale;
+  float mx = 0.0f;
+  for (int j = threadIdx.x; j < H; j += blockDim.x) {
+    const float t = sm[j] * w[j];
+    const float nv = t * scale;
+    sm[j] = nv;
+    if (normed) normed[j] = nv;
+    const float a = fabsf(nv);
+    if (a > mx) mx = a;
+  }
+  if (!xq) return;
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = red[0];
+  for (int i = 1; i < (int)(blockDim.x >> 6); i++) mx = fmaxf(mx, red[i]);
+  if (mx == 0.0f) {
+    for (int j = threadIdx.x; j < H; j += blockDim.x) xq[j] = 0;
+    if (threadIdx.x == 0) *sx = 1.0f;
+    return;
+  }
+  const float inv = 127.0f / mx;
+  for (int j = threadIdx.x; j < H; j += blockDim.x) {
+    float r = roundf(sm[j] * inv);
+    r = fminf(127.0f, fmaxf(-127.0f, r));
+    xq[j] = (int8_t)(int)r;
+  }
+  if (threadIdx.x == 0) *sx = mx / 127.0f;
+}
+
+// conv1d_step (int8_mamba.rs:43-56) + SiLU, one thread per channel
+__global__ void k_mamba_conv(const float *__restrict__ proj, float *__restrict__ conv_state,
+                             const float *__restrict__ cw, const float *__restrict__ cb, int di,
+                             int dc, float *__restrict__ xc) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= di) return;
+  float *buf = conv_state + (size_t)i * dc;
+  for (int k = 0; k + 1 < dc; k++) buf[k] = buf[k + 1];
+  buf[dc - 1] = proj[i];
+  const float *wr = cw + (size_t)i * dc;
+  float sum = 0.0f;
+  for (int k = 0; k < dc; k++) {
+    const float t = buf[k] * wr[k];
+    sum = sum + t;
+  }
+  xc[i] = syn_silu(sum + cb[i]);
+}
+
+// f32 GEMV in f32GemvRow order (matmul.zig:223-305, trans_b): lane = output
+// row; a sequential chain over k, @mulAdd for rows in the 32/8-wide column
+// blocks (row < n8), plain a*b+c in the tail.  W in [panel][K][64] so each
+// wave load is 256 contiguous bytes; x is wave-uniform.
+__global__ void __launch_bounds__(64)
+    k_gemv_f32_exact(const float *__restrict__ Wp, const float *__restrict__ x, int N, int K,
+                     int n8, float *__restrict__ y) {
+  const int panel = blockIdx.x, lane = threadIdx.x;
+  const int row = panel * 64 + lane;
+  const float *w = Wp + (size_t)panel * K * 64 + lane;
+  float acc = 0.0f;
+  if (row < n8) {
+    int k = 0;
+    for (; k + 8 <= K; k += 8) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) v[u] = w[(size_t)(k + u) * 64];
+#pragma unroll
+      for (int u = 0; u < 8; u++) acc = __builtin_fmaf(x[k + u], v[u], acc);
+    }
+    for (; k < K; k++) acc = __builtin_fmaf(x[k], w[(size_t)k * 64], acc);
+  } else {
+    for (int k = 0; k < K; k++) {
+      const float t = x[k] * w[(size_t)k * 64];
+      acc = acc + t;
+    }
+  }
+  if (row < N) y[row] = acc;
+}
+
+__device__ __forceinline__ float syn_softplus(float v) {  // ops/activation.rs:88-90
+  if (v > 20.0f) return v;
+  const float t = 1.0f + syn_expf(v);
+  return (float)log((double)t);
+}
+
+// dt_proj (f32 chain over dt_rank, or precomputed by the INT8 variant),
+// softplus, selective scan step and the SiLU(z) gate; one thread per channel.
+__global__ void k_mamba_scan(const float *__restrict__ xp, const float *__restrict__ dtw,
+                             const float *__restrict__ dtp_pre, const float *__restrict__ dtb,
+                             const float *__restrict__ a_log, const float *__restrict__ dparam,
+                             const float *__restrict__ xc, const float *__restrict__ proj,
+                             float *__restrict__ ssm, int di, int ds, int dr, int n8,
+                             float *__restrict__ gated) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= di) return;
+  float dtp;
+  if (dtp_pre) {
+    dtp = dtp_pre[i];
+  } else {
+    const float *wr = dtw + (size_t)i * dr;
+    dtp = 0.0f;
+    if (i < n8) {
+      for (int k = 0; k < dr; k++) dtp = __builtin_fmaf(xp[k], wr[k], dtp);
+    } else {
+      for (int k = 0; k < dr; k++) {
+        const float t = xp[k] * wr[k];
+        dtp = dtp + t;
+      }
+    }
+  }
+  const float dt = syn_softplus(dtp + dtb[i]);
+  const float xi = xc[i];
+  const float dt_x = dt * xi;
+  const float *b = xp + dr, *c = xp + dr + ds;
+  float *h = ssm + (size_t)i * ds;
+  const float *al = a_log + (size_t)i * ds;
+  float yi = 0.0f;
+  int j = 0;
+  for (; j + 4 <= ds; j += 4) {
+    float contrib[4];
+#pragma unroll
+    for (int l = 0; l < 4; l++) {
+      const float e = syn_expf(al[j + l]);
+      const float ad = syn_expf(-dt * e);
+      const float p1 = ad * h[j + l], p2 = dt_x * b[j + l];
+      const float hn = p1 + p2;
+      h[j + l] = hn;
+      contrib[l] = c[j + l] * hn;
+    }
+    yi = yi + (((contrib[0] + contrib[1]) + contrib[2]) + contrib[3]);
+  }
+  for (; j < ds; j++) {
+    const float a = -syn_expf(al[j]);
+    const float ad = syn_expf(dt * a);
+    const float p1 = ad * h[j], p2 = (dt * b[j]) * xi;
+    const float hn = p1 + p2;
+    h[j] = hn;
+    const float t = c[j] * hn;
+    yi = yi + t;
+  }
+  const float y = yi + dparam[i] * xi;
+  gated[i] = syn_silu(proj[di + i]) * y;  // int8_mamba.rs:102
+}
+
+static std::vector<float> to_panels(const float *w_nk, size_t n, size_t k) {
+  const size_t P = cdiv(n, 64);
+  std::vector<float> out(P * k * 64, 0.0f);
+  for (size_t r = 0; r < n; r++)
+    for (size_t kk = 0; kk < k; kk++) out[((r / 64) * k + kk) * 64 + r % 64] = w_nk[r * k + kk];
+  return out;
+}
+
+static int n8_of(int n) {
+  const int n32 = n - n % 32;
+  return n32 + ((n - n32) / 8) * 8;
+}
+
+}  // namespace syn
+
+struct syn_hip_mamba_s {
+  syn_hip_mamba_config c{};
+  size_t dm = 0, di = 0, ds = 0, dc = 0, dr = 0, L = 0, vocab = 0, nx = 0;
+  struct Block {
+    QLinearInt8 in_proj, out_proj, x_i8, dt_i8;
+    DevBuf conv_w, conv_b, xproj_p, dtproj, dt_bias, a_log, dparam, norm_w;
+  };
+  std::vector<Block> blk;
+  DevBuf embed, lm_p, final_norm, conv_state, ssm_state;
+  DevBuf x, xq, sx, proj, xc, xp, dtp, g, gq, sg, xcq, sxc, xpq, sxp, o, normed, logits;
+  DevBuf pv, pi, pv2, state, history, mhist;
+  size_t hist_cap = 0;
+  hipStream_t stream = nullptr;
+  hipGraphExec_t graph = nullptr;
+  bool ready = false;
+
+  ~syn_hip_mamba_s() {
+    if (graph) (void)hipGraphExecDestroy(graph);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+  StepState *st() { return state.as<StepState>(); }
+
+  syn_status_t layer(size_t l, hipStream_t s) {
+    Block &B = blk[l];
+    const size_t ldq_m = round_up(dm, 16), ldq_i = round_up(di, 16), ldq_r = round_up(dr, 16);
+    hipLaunchKernelGGL(k_mamba_norm, dim3(1), dim3(256), dm * 4, s, x.as<float>(),
+                       l == 0 ? nullptr : o.as<float>(), B.norm_w.as<float>(), c.eps, (int)dm,
+                       xq.as<int8_t>(), sx.as<float>(), nullptr);
+    SYN_LAUNCH_CHECK();
+    SYN_TRY(B.in_proj.gemv(1, xq.as<int8_t>(), ldq_m, sx.as<float>(), proj.as<float>(), 2 * di, s));
+    hipLaunchKernelGGL(k_mamba_conv, dim3(cdiv(di, 256)), dim3(256), 0, s, proj.as<float>(),
+                       conv_state.as<float>() + l * di * dc, B.conv_w.as<float>(),
+                       B.conv_b.as<float>(), (int)di, (int)dc, xc.as<float>());
+    SYN_LAUNCH_CHECK();
+    const float *dtp_pre = nullptr;
+    if (c.int8_xdt) {
+      SYN_TRY(launch_quantize_rows(xc.as<float>(), 1, di, di, xcq.as<int8_t>(), ldq_i,
+                                   sxc.as<float>(), s));
+      SYN_TRY(B.x_i8.gemv(1, xcq.as<int8_t>(), ldq_i, sxc.as<float>(), xp.as<float>(), nx, s));
+      SYN_TRY(launch_quantize_rows(xp.as<float>(), 1, dr, dr, xpq.as<int8_t>(), ldq_r,
+                                   sxp.as<float>(), s));
+      SYN_TRY(B.dt_i8.gemv(1, xpq.as<int8_t>(), ldq_r, sxp.as<float>(), dtp.as<float>(), di, s));
+      dtp_pre = dtp.as<float>();
+    } else {
+      hipLaunchKernelGGL(k_gemv_f32_exact, dim3(cdiv(nx, 64)), dim3(64), 0, s,
+                         B.xproj_p.as<float>(), xc.as<float>(), (int)nx, (int)di, n8_of((int)nx),
+                         xp.as<float>());
+      SYN_LAUNCH_CHECK();
+    }
+    hipLaunchKernelGGL(k_mamba_scan, dim3(cdiv(di, 256)), dim3(256), 0, s, xp.as<float>(),
+                       B.dtproj.as<float>(), dtp_pre, B.dt_bias.as<float>(), B.a_log.as<float>(),
+                       B.dparam.as<float>(), xc.as<float>(), proj.as<float>(),
+                       ssm_state.as<float>() + l * di * ds, (int)di, (int)ds, (int)dr,
+                       n8_of((int)di), g.as<float>());
+    SYN_LAUNCH_CHECK();
+    SYN_TRY(launch_quantize_rows(g.as<float>(), 1, di, di, gq.as<int8_t>(), ldq_i, sg.as<float>(), s));
+    SYN_TRY(B.out_proj.gemv(1, gq.as<int8_t>(), ldq_i, sg.as<float>(), o.as<float>(), dm, s));
+    return SYN_OK;
+  }
+
+  syn_status_t step(hipStream_t s) {
+    SYN_TRY(launch_embed(embed.as<float>(), &st()->token, 1, (int)dm, (int)vocab, x.as<float>(), s));
+    for (size_t l = 0; l < L; l++) SYN_TRY(layer(l, s));
+    hipLaunchKernelGGL(k_mamba_norm, dim3(1), dim3(256), dm * 4, s, x.as<float>(), o.as<float>(),
+                       final_norm.as<float>(), c.eps, (int)dm, nullptr, nullptr,
+                       normed.as<float>());
+    SYN_LAUNCH_CHECK();
+    hipLaunchKernelGGL(k_gemv_f32_exact, dim3(cdiv(vocab, 64)), dim3(64), 0, s,
+                       lm_p.as<float>(), normed.as<float>(), (int)vocab, (int)dm,
+                       n8_of((int)vocab), logits.as<float>());
+    SYN_LAUNCH_CHECK();
+    SYN_TRY(launch_argmax(logits.as<float>(), (int)vocab, pv.as<float>(), pi.as<int>(),
+                          pv2.as<float>(), st(), history.as<uint32_t>(), mhist.as<float>(), s));
+    return launch_step_advance(st(), 1, s);
+  }
+
+  syn_status_t build_graph() {
+    if (graph) return SYN_OK;
+    hipGraph_t gr;
+    SYN_HIP(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+    syn_status_t st_ = step(stream);
+    hipError_t e = hipStreamEndCapture(stream, &gr);
+    if (st_ != SYN_OK) {
+      if (e == hipSuccess) (void)hipGraphDestroy(gr);
+      return st_;
+    }
+    if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture", __FILE__, __LINE__);
+    e = hipGraphInstantiate(&graph, gr, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(gr);
+    if (e != hipSuccess) {
+      graph = nullptr;
+      return hip_fail(e, "hipGraphInstantiate", __FILE__, __LINE__);
+    }
+    return SYN_OK;
+  }
+
+  syn_status_t set_state(int pos, uint32_t token, int step_) {
+    StepState hs{pos, token, step_, 0.0f};
+    SYN_HIP(hipMemcpyAsync(state.p, &hs, sizeof(hs), hipMemcpyHostToDevice, stream));
+    SYN_HIP(hipStreamSynchronize(stream));
+    return SYN_OK;
+  }
+
+  syn_status_t reset() {
+    SYN_HIP(hipMemsetAsync(conv_state.p, 0, conv_state.bytes, stream));
+    SYN_HIP(hipMemsetAsync(ssm_state.p, 0, ssm_state.bytes, stream));
+    return set_state(0, 0, 0);
+  }
+
+  // prefill = the per-token loop of the reference (int8_mamba.rs:177-203)
+  syn_status_t prefill(const uint32_t *ids, size_t n) {
+    SYN_TRY(build_graph());
+    SYN_TRY(reset());
+    for (size_t t = 0; t < n; t++) {
+      SYN_TRY(set_state((int)t, ids[t], 0));
+      SYN_HIP(hipGraphLaunch(graph, stream));
+    }
+    return SYN_OK;
+  }
+};
+
+extern "C" {
+
+syn_status_t syn_hip_mamba_create(const syn_hip_mamba_config *cfg, syn_hip_mamba_t **out) {
+  if (!cfg || !out) return SYN_ERR_NULL_PTR;
+  if (!cfg->d_model || !cfg->d_inner || !cfg->d_state || !cfg->d_conv || !cfg->dt_rank ||
+      !cfg->n_layers || !cfg->vocab || cfg->max_tokens == 0)
+    return SYN_ERR_INVALID_ARG;
+  SYN_TRY(ensure_init());
+  auto *m = new syn_hip_mamba_s();
+  m->c = *cfg;
+  m->dm = cfg->d_model;
+  m->di = cfg->d_inner;
+  m->ds = cfg->d_state;
+  m->dc = cfg->d_conv;
+  m->dr = cfg->dt_rank;
+  m->L = cfg->n_layers;
+  m->vocab = cfg->vocab;
+  m->nx = m->dr + 2 * m->ds;
+  m->hist_cap = cfg->max_tokens + 1;
+  m->blk.resize(m->L);
+  hipError_t e = hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    m->stream = nullptr;
+    delete m;
+    return hip_fail(e, "hipStreamCreate", __FILE__, __LINE__);
+  }
+  *out = m;
+  return SYN_OK;
+}
+
+// Synthetic weights (harness spec, same as the oracle): embed (= tied lm_head)
+// tensor id 0; block l: 1+16l+{0 in_proj, 1 conv1d, 2 x_proj, 3 dt_proj,
+// 4 out_proj} ~ N(0, stddev); conv bias 0, dt bias log(expm1(0.01)),
+// a_log[i][s] = log(s+1), D = 1, norm gains 1.
+syn_status_t syn_hip_mamba_init_synthetic(syn_hip_mamba_t *m, uint64_t seed_base, float stddev) {
+  if (!m) return SYN_ERR_NULL_PTR;
+  const size_t dm = m->dm, di = m->di, ds = m->ds, dc = m->dc, dr = m->dr, nx = m->nx;
+  {
+    std::vector<float> emb(m->vocab * dm);
+    fill_normal_parallel(emb.data(), emb.size(), seed_base, stddev);
+    SYN_TRY(m->embed.alloc(emb.size() * 4));
+    SYN_HIP(hipMemcpy(m->embed.p, emb.data(), emb.size() * 4, hipMemcpyHostToDevice));
+    std::vector<float> lp = to_panels(emb.data(), m->vocab, dm);
+    SYN_TRY(m->lm_p.alloc(lp.size() * 4));
+    SYN_HIP(hipMemcpy(m->lm_p.p, lp.data(), lp.size() * 4, hipMemcpyHostToDevice));
+  }
+  const float dt_bias = logf(expm1f(0.01f));
+  auto up = [](DevBuf &b, const std::vector<float> &v) -> syn_status_t {
+    SYN_TRY(b.alloc(v.size() * 4));
+    SYN_HIP(hipMemcpy(b.p, v.data(), v.size() * 4, hipMemcpyHostToDevice));
+    return SYN_OK;
+  };
+  for (size_t l = 0; l < m->L; l++) {
+    auto &B = m->blk[l];
+    const uint64_t sb = seed_base + 1 + 16 * l;
+    std::vector<float> win(2 * di * dm), wout(dm * di), cw(di * dc), xw(nx * di), dw(di * dr);
+    std::thread t0([&] { fill_normal(win.data(), win.size(), sb + 0, stddev); });
+    std::thread t1([&] { fill_normal(wout.data(), wout.size(), sb + 4, stddev); });
+    fill_normal(cw.data(), cw.size(), sb + 1, stddev);
+    fill_normal(xw.data(), xw.size(), sb + 2, stddev);
+    fill_normal(dw.data(), dw.size(), sb + 3, stddev);
+    t0.join();
+    t1.join();
+    SYN_TRY(B.in_proj.from_f32(win.data(), 2 * di, dm));
+    SYN_TRY(B.out_proj.from_f32(wout.data(), dm, di));
+    SYN_TRY(up(B.conv_w, cw));
+    SYN_TRY(up(B.conv_b, std::vector<float>(di, 0.0f)));
+    SYN_TRY(up(B.xproj_p, to_panels(xw.data(), nx, di)));
+    SYN_TRY(up(B.dtproj, dw));
+    if (m->c.int8_xdt) {
+      SYN_TRY(B.x_i8.from_f32(xw.data(), nx, di));
+      SYN_TRY(B.dt_i8.from_f32(dw.data(), di, dr));
+    }
+    SYN_TRY(up(B.dt_bias, std::vector<float>(di, dt_bias)));
+    std::vector<float> al(di * ds);
+    for (size_t i = 0; i < di; i++)
+      for (size_t s2 = 0; s2 < ds; s2++) al[i * ds + s2] = logf((float)(s2 + 1));
+    SYN_TRY(up(B.a_log, al));
+    SYN_TRY(up(B.dparam, std::vector<float>(di, 1.0f)));
+    SYN_TRY(up(B.norm_w, std::vector<float>(dm, 1.0f)));
+    SYN_TRY(B.in_proj.prepare(1));
+    SYN_TRY(B.out_proj.prepare(1));
+    if (m->c.int8_xdt) {
+      SYN_TRY(B.x_i8.prepare(1));
+      SYN_TRY(B.dt_i8.prepare(1));
+    }
+  }
+  SYN_TRY(up(m->final_norm, std::vector<float>(dm, 1.0f)));
+  SYN_TRY(m->conv_state.alloc(m->L * di * dc * 4));
+  SYN_TRY(m->ssm_state.alloc(m->L * di * ds * 4));
+  SYN_TRY(m->x.alloc(dm * 4));
+  SYN_TRY(m->xq.alloc(round_up(dm, 16)));
+  SYN_TRY(m->sx.alloc(16));
+  SYN_TRY(m->proj.alloc(2 * di * 4));
+  SYN_TRY(m->xc.alloc(di * 4));
+  SYN_TRY(m->xp.alloc(nx * 4));
+  SYN_TRY(m->dtp.alloc(di * 4));
+  SYN_TRY(m->g.alloc(di * 4));
+  SYN_TRY(m->gq.alloc(round_up(di, 16)));
+  SYN_TRY(m->sg.alloc(16));
+  SYN_TRY(m->xcq.alloc(round_up(di, 16)));
+  SYN_TRY(m->sxc.alloc(16));
+  SYN_TRY(m->xpq.alloc(round_up(dr, 16)));
+  SYN_TRY(m->sxp.alloc(16));
+  SYN_TRY(m->o.alloc(dm * 4));
+  SYN_TRY(m->normed.alloc(dm * 4));
+  SYN_TRY(m->logits.alloc(m->vocab * 4));
+  SYN_TRY(m->pv.alloc(256 * 4));
+  SYN_TRY(m->pi.alloc(256 * 4));
+  SYN_TRY(m->pv2.alloc(256 * 4));
+  SYN_TRY(m->state.alloc(sizeof(StepState)));
+  SYN_TRY(m->history.alloc(m->hist_cap * 4));
+  SYN_TRY(m->mhist.alloc(m->hist_cap * 4));
+  SYN_HIP(hipMemset(m->xq.p, 0, m->xq.bytes));
+  SYN_HIP(hipMemset(m->gq.p, 0, m->gq.bytes));
+  SYN_HIP(hipMemset(m->xcq.p, 0, m->xcq.bytes));
+  SYN_HIP(hipMemset(m->xpq.p, 0, m->xpq.bytes));
+  m->ready = true;
+  return m->reset();
+}
+
+static syn_status_t check_mamba(syn_hip_mamba_t *m) {
+  if (!m) return SYN_ERR_NULL_PTR;
+  if (!m->ready) {
+    set_error("mamba model has no weights");
+    return SYN_ERR_INVALID_ARG;
+  }
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_mamba_prefill(syn_hip_mamba_t *m, const uint32_t *ids, size_t n,
+                                   float *host_logits) {
+  SYN_TRY(check_mamba(m));
+  if (!ids) return SYN_ERR_NULL_PTR;
+  if (n == 0 || n > m->c.max_tokens) return SYN_ERR_INVALID_ARG;
+  SYN_TRY(m->prefill(ids, n));
+  if (host_logits)
+    SYN_HIP(hipMemcpyAsync(host_logits, m->logits.p, m->vocab * 4, hipMemcpyDeviceToHost,
+                           m->stream));
+  SYN_HIP(hipStreamSynchronize(m->stream));
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_mamba_decode_one(syn_hip_mamba_t *m, uint32_t token, float *host_logits) {
+  SYN_TRY(check_mamba(m));
+  SYN_TRY(m->build_graph());
+  StepState cur;
+  SYN_HIP(hipMemcpyAsync(&cur, m->state.p, sizeof(cur), hipMemcpyDeviceToHost, m->stream));
+  SYN_HIP(hipStreamSynchronize(m->stream));
+  if ((size_t)cur.step + 1 >= m->hist_cap) {
+    set_error("max_tokens reached");
+    return SYN_ERR_INVALID_ARG;
+  }
+  SYN_TRY(m->set_state(cur.pos, token, cur.step));
+  SYN_HIP(hipGraphLaunch(m->graph, m->stream));
+  if (host_logits)
+    SYN_HIP(hipMemcpyAsync(host_logits, m->logits.p, m->vocab * 4, hipMemcpyDeviceToHost,
+                           m->stream));
+  SYN_HIP(hipStreamSynchronize(m->stream));
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_mamba_generate(syn_hip_mamba_t *m, const uint32_t *prompt, size_t n_prompt,
+                                    size_t max_new, uint32_t *out_tokens, float *out_margins) {
+  SYN_TRY(check_mamba(m));
+  if (!prompt || !out_tokens) return SYN_ERR_NULL_PTR;
+  if (max_new == 0) return SYN_OK;
+  if (n_prompt == 0 || n_prompt > m->c.max_tokens || max_new + 1 > m->hist_cap) return SYN_ERR_INVALID_ARG;
+  SYN_TRY(m->prefill(prompt, n_prompt));
+  for (size_t i = 1; i < max_new; i++) SYN_HIP(hipGraphLaunch(m->graph, m->stream));
+  SYN_HIP(hipMemcpyAsync(out_tokens, m->history.p, max_new * 4, hipMemcpyDeviceToHost, m->stream));
+  if (out_margins)
+    SYN_HIP(hipMemcpyAsync(out_margins, m->mhist.p, max_new * 4, hipMemcpyDeviceToHost, m->stream));
+  SYN_HIP(hipStreamSynchronize(m->stream));
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_mamba_decode_timed(syn_hip_mamba_t *m, size_t steps, float *elapsed_ms) {
+  SYN_TRY(check_mamba(m));
+  if (!elapsed_ms) return SYN_ERR_NULL_PTR;
+  SYN_TRY(m->build_graph());
+  StepState cur;
+  SYN_HIP(hipMemcpyAsync(&cur, m->state.p, sizeof(cur), hipMemcpyDeviceToHost, m->stream));
+  SYN_HIP(hipStreamSynchronize(m->stream));
+  if ((size_t)cur.step + steps >= m->hist_cap) {
+    set_error("decode steps exceed max_tokens");
+    return SYN_ERR_INVALID_ARG;
+  }
+  hipEvent_t a, b;
+  SYN_HIP(hipEventCreate(&a));
+  SYN_HIP(hipEventCreate(&b));
+  SYN_HIP(hipEventRecord(a, m->stream));
+  for (size_t i = 0; i < steps; i++) SYN_HIP(hipGraphLaunch(m->graph, m->stream));
+  SYN_HIP(hipEventRecord(b, m->stream));
+  SYN_HIP(hipEventSynchronize(b));
+  SYN_HIP(hipEventElapsedTime(elapsed_ms, a, b));
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_mamba_destroy(syn_hip_mamba_t *m) {
+  if (m) {
+    (void)hipStreamSynchronize(m->stream);
+    delete m;
+  }
+  return SYN_OK;
+}
+
+}  // extern "C"

@@ -40,6 +40,13 @@ class KLmConfig(C.Structure):
                 ("fmt_lm_head", C.c_int32), ("qk_norm", C.c_int32)]
 
 
+class MambaConfig(C.Structure):
+    _fields_ = [("d_model", C.c_uint32), ("d_inner", C.c_uint32), ("d_state", C.c_uint32),
+                ("d_conv", C.c_uint32), ("dt_rank", C.c_uint32), ("n_layers", C.c_uint32),
+                ("vocab", C.c_uint32), ("max_tokens", C.c_uint32), ("eps", C.c_float),
+                ("int8_xdt", C.c_int32)]
+
+
 SIGNATURES = {
     "syn_quantize_per_channel_int8": (ST, [P, SZ, SZ, P, P]),
     "syn_qgemm_int8": (ST, [SZ, SZ, SZ, P, SZ, P, SZ, P, SZ, P, P]),
@@ -95,6 +102,13 @@ SIGNATURES = {
     "syn_hip_klm_generate": (ST, [P, P, SZ, SZ, P, P]),
     "syn_hip_klm_time": (ST, [P, P, SZ, SZ, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
     "syn_hip_klm_destroy": (ST, [P]),
+    "syn_hip_mamba_create": (ST, [C.POINTER(MambaConfig), C.POINTER(P)]),
+    "syn_hip_mamba_init_synthetic": (ST, [P, C.c_uint64, C.c_float]),
+    "syn_hip_mamba_prefill": (ST, [P, P, SZ, P]),
+    "syn_hip_mamba_decode_one": (ST, [P, C.c_uint32, P]),
+    "syn_hip_mamba_generate": (ST, [P, P, SZ, SZ, P, P]),
+    "syn_hip_mamba_decode_timed": (ST, [P, SZ, C.POINTER(C.c_float)]),
+    "syn_hip_mamba_destroy": (ST, [P]),
     "syn_hip_fill_normal": (ST, [P, SZ, C.c_uint64, C.c_float]),
     "syn_hip_eval_expf": (ST, [P, P, SZ, P]),
     "syn_hip_kquant_encode": (ST, [C.c_int, SZ, SZ, P, P]),
@@ -469,6 +483,57 @@ class KQuantCausalLM:
     def close(self):
         if self.h:
             lib().syn_hip_klm_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class QuantizedMamba:
+    """Device-resident INT8 Mamba (QuantizedMambaModel)."""
+
+    def __init__(self, cfg: dict, int8_xdt: bool = False):
+        self.cfg = dict(cfg)
+        c = MambaConfig(cfg["d_model"], cfg["d_inner"], cfg["d_state"], cfg["d_conv"],
+                        cfg["dt_rank"], cfg["n_layers"], cfg["vocab"], cfg["max_tokens"],
+                        cfg.get("eps", 1e-5), 1 if int8_xdt else 0)
+        h = C.c_void_p()
+        check(lib().syn_hip_mamba_create(C.byref(c), C.byref(h)), "mamba_create")
+        self.h = h.value
+
+    def init_synthetic(self, seed_base: int = 0x5EED0000, std: float = 0.02):
+        check(lib().syn_hip_mamba_init_synthetic(self.h, seed_base, std), "mamba_init")
+
+    def prefill(self, ids):
+        ids = np.ascontiguousarray(ids, np.uint32)
+        out = np.empty(self.cfg["vocab"], np.float32)
+        check(lib().syn_hip_mamba_prefill(self.h, ptr(ids), ids.size, ptr(out)), "prefill")
+        return out
+
+    def decode_one(self, token: int):
+        out = np.empty(self.cfg["vocab"], np.float32)
+        check(lib().syn_hip_mamba_decode_one(self.h, int(token), ptr(out)), "decode_one")
+        return out
+
+    def generate(self, prompt, max_new: int):
+        prompt = np.ascontiguousarray(prompt, np.uint32)
+        toks = np.zeros(max_new, np.uint32)
+        margins = np.zeros(max_new, np.float32)
+        check(lib().syn_hip_mamba_generate(self.h, ptr(prompt), prompt.size, max_new, ptr(toks),
+                                           ptr(margins)), "generate")
+        return toks, margins
+
+    def decode_timed(self, steps: int) -> float:
+        ms = C.c_float()
+        check(lib().syn_hip_mamba_decode_timed(self.h, steps, C.byref(ms)), "decode_timed")
+        return ms.value
+
+    def close(self):
+        if self.h:
+            lib().syn_hip_mamba_destroy(self.h)
             self.h = None
 
     def __del__(self):

@@ -1,0 +1,79 @@
+"""INT8 Mamba (config 5 path) on the GPU vs the oracle's QuantizedMambaModel.
+
+Everything but softplus's log follows the reference's float order; the device
+log is correctly rounded while glibc's logf is not always, so the bar is the
+north star's float one (cosine >= 0.9999) plus greedy-token agreement while
+the oracle's margins are above float noise."""
+import numpy as np
+import pytest
+
+import oracle as O
+from synapse_amd import hip
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    hip.init(0)
+
+
+def _cos(a, b):
+    a, b = a.astype(np.float64), b.astype(np.float64)
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+
+def _pair(cfg, max_tokens):
+    o = O.QuantizedMamba(cfg)
+    o.init_synthetic()
+    g = hip.QuantizedMamba(dict(cfg, max_tokens=max_tokens))
+    g.init_synthetic()
+    return o, g
+
+
+TINY = dict(d_model=64, d_inner=128, d_state=16, d_conv=4, dt_rank=8, n_layers=2, vocab=256)
+MAMBA370 = dict(d_model=1024, d_inner=2048, d_state=16, d_conv=4, dt_rank=64, n_layers=48,
+                vocab=50280)
+
+
+def test_tiny_prefill_decode():
+    o, g = _pair(TINY, 64)
+    ids = O.token_ids(8, 0x5EED0000 + 0xFFFF, TINY["vocab"])
+    lo, lg = o.prefill(ids), g.prefill(ids)
+    assert _cos(lo, lg) >= 0.9999
+    tok = O.argmax(lo)
+    for _ in range(10):
+        lo, lg = o.decode_one(tok), g.decode_one(tok)
+        assert _cos(lo, lg) >= 0.9999
+        tok = O.argmax(lo)
+
+
+def test_tiny_generate_tokens():
+    o, g = _pair(TINY, 64)
+    ids = O.token_ids(8, 0x5EED0000 + 0xFFFF, TINY["vocab"])
+    to, mo = o.generate(ids, 32)
+    tg, _ = g.generate(ids, 32)
+    thin = next((i for i, m in enumerate(mo) if m < 1e-3), len(mo))
+    np.testing.assert_array_equal(tg[:thin], to[:thin])
+
+
+def test_int8_xdt_variant_runs_close():
+    o, _ = _pair(TINY, 64)
+    g = hip.QuantizedMamba(dict(TINY, max_tokens=64), int8_xdt=True)
+    g.init_synthetic()
+    ids = O.token_ids(8, 0x5EED0000 + 0xFFFF, TINY["vocab"])
+    lo, lg = o.prefill(ids), g.prefill(ids)
+    assert _cos(lo, lg) > 0.99  # INT8 x_proj/dt_proj: a different (labelled) model variant
+
+
+def test_mamba_370m_shape():
+    o, g = _pair(MAMBA370, 64)
+    ids = O.token_ids(16, 0x5EED0000 + 0xFFFF, MAMBA370["vocab"])
+    lo, lg = o.prefill(ids), g.prefill(ids)
+    print("prefill cos", _cos(lo, lg))
+    assert _cos(lo, lg) >= 0.9999
+    to, mo = o.generate(ids, 16)
+    tg, _ = g.generate(ids, 16)
+    print("tokens", tg.tolist(), to.tolist(), "min margin", float(mo.min()))
+    thin = next((i for i, m in enumerate(mo) if m < 1e-3), len(mo))
+    np.testing.assert_array_equal(tg[:thin], to[:thin])

@@ -357,3 +357,62 @@ def test_model_prefill_consistency():
     assert np.abs(full - one).max() <= 1e-5 * max(1.0, np.abs(full).max()) + 1e-3
     toks, margins = m.generate(ids, 8)
     assert toks.shape == (8,) and (margins >= 0).all()
+
+
+# ---------------------------------------------------------------- Mamba pieces
+def test_selective_scan_reference_values():
+    # tests/integration/reference_correctness.rs:43-87 (d_state = 2: scalar tail path)
+    a_log = np.full(4, -1.0, np.float32)
+    d = np.zeros(2, np.float32)
+    state = np.zeros(4, np.float32)
+    ys = []
+    for x, b, c in (([1.0, 2.0], [1.0, 0.5], [1.0, 1.0]), ([0.5, 1.0], [0.5, 1.0], [1.0, 0.5])):
+        x = np.array(x, np.float32)
+        y = np.zeros(2, np.float32)
+        O.lib().orc_selective_scan_step(O._p(x), O._p(np.full(2, 0.5, np.float32)), O._p(a_log),
+                                        O._p(np.array(b, np.float32)), O._p(np.array(c, np.float32)),
+                                        O._p(d), O._p(state), O._p(y), 2, 2)
+        ys += y.tolist()
+    assert abs(ys[0] - 0.75) < 1e-5 and abs(ys[1] - 1.5) < 1e-5
+    assert abs(ys[2] - 0.76996) < 1e-3 and abs(ys[3] - 1.53993) < 1e-3
+
+
+def test_selective_scan_vector_path_vs_f64():
+    di, ds = 8, 16
+    x = O.normal(di, 1, 1.0)
+    dt = np.abs(O.normal(di, 2, 0.1)) + 0.01
+    al = O.normal(di * ds, 3, 0.5)
+    b, c, dd = O.normal(ds, 4, 1.0), O.normal(ds, 5, 1.0), O.normal(di, 6, 1.0)
+    st0 = O.normal(di * ds, 7, 1.0)
+    st = st0.copy()
+    y = np.zeros(di, np.float32)
+    O.lib().orc_selective_scan_step(O._p(x), O._p(dt.astype(np.float32)), O._p(al), O._p(b), O._p(c),
+                                    O._p(dd), O._p(st), O._p(y), di, ds)
+    h = (np.exp(-dt.astype(np.float64)[:, None] * np.exp(al.astype(np.float64).reshape(di, ds)))
+         * st0.reshape(di, ds) + (dt[:, None] * x[:, None]) * b[None, :])
+    np.testing.assert_allclose(st.reshape(di, ds), h, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(y, h @ c + dd * x, rtol=1e-5, atol=1e-5)
+
+
+def test_softplus_and_seq_rmsnorm():
+    # ops/activation.rs:88-90; pure_rust_ops.rs:96-112
+    assert O.lib().orc_softplus(25.0) == 25.0
+    assert abs(O.lib().orc_softplus(0.0) - np.log(2.0)) < 1e-7
+    x = O.normal(1024, 8, 2.0)
+    out = np.empty_like(x)
+    O.lib().orc_rmsnorm_seq(O._p(x), O._p(np.ones(1024, np.float32)), 1e-5, 1024, O._p(out))
+    np.testing.assert_allclose(np.sqrt((out.astype(np.float64) ** 2).mean()), 1.0, rtol=1e-5)
+
+
+def test_mamba_prefill_equals_token_loop():
+    cfg = dict(d_model=64, d_inner=128, d_state=16, d_conv=4, dt_rank=8, n_layers=2, vocab=256)
+    m = O.QuantizedMamba(cfg)
+    m.init_synthetic()
+    ids = O.token_ids(6, 3, 256)
+    full = m.prefill(ids)
+    m2 = O.QuantizedMamba(cfg)
+    m2.init_synthetic()
+    m2.prefill(ids[:3])
+    for t in ids[3:5]:
+        m2.decode_one(int(t))
+    np.testing.assert_array_equal(m2.decode_one(int(ids[5])), full)
