@@ -99,6 +99,11 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--lm-head-iters", type=int, default=20)
+    ap.add_argument("--unfused", action="store_true",
+                    help="one kernel per reference op instead of the fused decode layer")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch the decode kernels eagerly instead of replaying a HIP graph "
+                         "(for profilers that do not follow graph launches)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only (the decode path is single-GPU; "
@@ -111,6 +116,7 @@ def main():
     t0 = time.perf_counter()
     model = hip.QuantizedCausalLM(cfg)
     model.init_synthetic(SEED_BASE, 0.02)
+    model.set_options(fused=not args.unfused, graph=not args.eager)
     load_s = time.perf_counter() - t0
     import numpy as np
     ids = np.array(prompt_ids(), np.uint32)

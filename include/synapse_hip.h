@@ -195,6 +195,13 @@ syn_status_t syn_hip_qlm_decode_timed(syn_hip_qlm_t *m, size_t steps, float *ela
  * where the layer weights stream through it in between). */
 syn_status_t syn_hip_qlm_time_lm_head(syn_hip_qlm_t *m, size_t iters, size_t flush_bytes,
                                       float *avg_ms);
+/* Decode-step options (no reference counterpart; both settings compute the
+ * same bits).  fused_decode = 1 (default when the shape fits the fused
+ * kernels' LDS rows): five kernels per layer, each a split-K GEMV whose
+ * prologue forms its own input activation; 0: one kernel per reference op.
+ * graph_replay = 1 (default): each decode step is a replayed HIP graph; 0:
+ * kernels are launched eagerly (for profilers that cannot follow graphs). */
+syn_status_t syn_hip_qlm_set_options(syn_hip_qlm_t *m, int fused_decode, int graph_replay);
 syn_status_t syn_hip_qlm_destroy(syn_hip_qlm_t *m);
 
 /* -- f32 causal LM over GGUF-block weights: CausalLM (models/lm/causal_lm.rs:

@@ -106,7 +106,9 @@ static __constant__ uint64_t syn_exp2_tab[32] = {
 // x86-64 FMA ifunc build.  Checked on the CPU against the host's expf over all
 // 2^32 inputs; keeps SiLU and softmax bit-identical to the reference's
 // f32::exp on Linux.
-__device__ __forceinline__ float syn_expf(float x) {
+// tab: the 32-entry table above, or a copy of it (in LDS, so that a lookup
+// does not wait behind outstanding global loads)
+__device__ __forceinline__ float syn_expf_tab(float x, const uint64_t *tab) {
   const double InvLn2N = 0x1.71547652b82fep+0 * 32.0;
   const double SHIFT = 0x1.8p+52;
   const double C0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32;
@@ -125,7 +127,7 @@ __device__ __forceinline__ float syn_expf(float x) {
   const uint64_t ki = (uint64_t)__double_as_longlong(kd);
   kd -= SHIFT;
   const double r = __builtin_fma(InvLn2N, xd, -kd);
-  uint64_t t = syn_exp2_tab[ki & 31u];
+  uint64_t t = tab[ki & 31u];
   t += ki << 47;
   const double s = __longlong_as_double((long long)t);
   const double z = __builtin_fma(C0, r, C1);
@@ -136,8 +138,13 @@ __device__ __forceinline__ float syn_expf(float x) {
   return (float)y;
 }
 
+__device__ __forceinline__ float syn_expf(float x) { return syn_expf_tab(x, syn_exp2_tab); }
+
 // reference SiLU: x / (1 + exp(-x))  (ops/activation.rs:30-32)
 __device__ __forceinline__ float syn_silu(float x) { return x / (1.0f + syn_expf(-x)); }
+__device__ __forceinline__ float syn_silu_tab(float x, const uint64_t *tab) {
+  return x / (1.0f + syn_expf_tab(-x, tab));
+}
 
 // Rust converter f16->f32 (weight_loading/converter.rs:12-40): subnormal
 // inputs come out at half their IEEE value (shift counter starts at 1).

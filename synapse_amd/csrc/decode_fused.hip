@@ -1,0 +1,1271 @@
+// Fused INT8 W8A8 decode step (one token, batch 1).
+//
+// The unfused step launches one kernel per reference op (13 per layer).  At
+// batch 1 every one of them is latency-bound, so the step is rebuilt as five
+// kernels per layer, each a split-K GEMV whose prologue computes the GEMV's
+// input activation itself:
+//
+//   K1  x = x_mid + down(prev)        ; q8(rmsnorm(x))  ; QKV     rows
+//   K2  per head: q/k/v rows, head norms, RoPE, KV append, attention
+//   K3  q8(attn)                                         ; O       rows
+//   K4  x_mid = x + o                 ; q8(rmsnorm(x))  ; gate|up rows
+//   K5  q8(silu(gate) * up)                              ; down    rows
+//
+// then the final norm, the lm_head GEMV with per-panel top-2, and one merge.
+// A split-K GEMV adds its exact int32 partial dot products into per-layer
+// accumulators with atomics (integer sums are exact in any order); the
+// consumer applies the reference epilogue (f32(acc)*sx)*sw.  The prologue is
+// computed redundantly by every workgroup (it reads a few KB from L2), which
+// removes all inter-workgroup synchronisation inside a kernel.  Each wave
+// issues its weight loads before the prologue, so the HBM latency of the GEMV
+// hides behind the prologue's dependency chains, and the prologue batches its
+// own loads so that each thread has several in flight.
+//
+// Every float operation is the one of the unfused kernels (layer_ops.hip),
+// which follow the reference's order: the fused step is bit-identical to it.
+#include <algorithm>
+
+#include "decode_fused.hpp"
+#include "linear.hpp"
+
+namespace syn {
+
+// Optional phase timestamps of workgroup 0, thread 0 (compiled in only with
+// -DSYN_PHASE_TIMING; read back with syn_hip_debug_phase_ts).
+// Timestamps stay in registers until SYN_TS_FLUSH at the end of the kernel,
+// so the instrumented build issues no extra memory operations mid-kernel.
+#ifdef SYN_PHASE_TIMING
+static __device__ unsigned long long syn_phase_ts[256];
+#define SYN_TS_DECL unsigned long long syn_ts_[16] = {};
+#define SYN_TS(i) syn_ts_[(i)] = __builtin_amdgcn_s_memtime()
+#define SYN_TSR(i) syn_ts_[(i)] = __builtin_amdgcn_s_memrealtime()
+#define SYN_TS_FLUSH(base)                                                       \
+  do {                                                                         \
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)                \
+      for (int i_ = 0; i_ < 16; i_++) syn_phase_ts[(base) + i_] = syn_ts_[i_]; \
+  } while (0)
+#else
+#define SYN_TS_DECL
+#define SYN_TS(i) \
+  do {            \
+  } while (0)
+#define SYN_TSR(i) \
+  do {             \
+  } while (0)
+#define SYN_TS_FLUSH(base) \
+  do {                     \
+  } while (0)
+#endif
+
+// ------------------------------------------------------------------ helpers
+__device__ __forceinline__ float row_value(const RowSrc &s, int r) {
+  const float f = (float)s.acc[r] * s.sx[0];
+  return f * s.ws[r];
+}
+
+// Rows of a prologue vector held per thread: element j = threadIdx.x + u*NT.
+constexpr int RB = 8;
+
+template <int NT>
+__device__ __forceinline__ void bar() {
+  if constexpr (NT > 64) __syncthreads();
+  else __builtin_amdgcn_wave_barrier();
+}
+
+// One step of a wave max over non-negative values through a DPP lane move;
+// lanes whose source is outside the row/wave read 0, which max ignores.
+template <int CTRL>
+__device__ __forceinline__ float dpp_fmax(float v) {
+  const int s = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true);
+  return fmaxf(v, __int_as_float(s));
+}
+
+// max over the 64 lanes of non-negative values: row_shr 1/2/4/8 leave each
+// row's max in its lane 15, row_bcast 15/31 carry them to lane 63
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+  v = dpp_fmax<0x111>(v);
+  v = dpp_fmax<0x112>(v);
+  v = dpp_fmax<0x114>(v);
+  v = dpp_fmax<0x118>(v);
+  v = dpp_fmax<0x142>(v);
+  v = dpp_fmax<0x143>(v);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Workgroup max of non-negative values, first half: each wave leaves its max
+// in red[slot + wave].  The caller's next barrier publishes it.
+template <int NT>
+__device__ __forceinline__ void wg_max_post(float v, float *red, int slot) {
+  v = wave_max_nonneg(v);
+  if ((threadIdx.x & 63) == 0) red[slot + (threadIdx.x >> 6)] = v;
+}
+
+// second half (after a barrier)
+template <int NT>
+__device__ __forceinline__ float wg_max_get(const float *red, int slot) {
+  float m = red[slot];
+#pragma unroll
+  for (int i = 1; i < NT / 64; i++) m = fmaxf(m, red[slot + i]);
+  return m;
+}
+
+// Chains of the reference sum-of-squares order (syn_vmul + syn_vreduce_sum,
+// exports.zig:366-375, 503-514): acc[l] = sequential sum of sq[4i+l] over the
+// 4-aligned prefix, combined as ((a0+a1)+a2)+a3, then the tail in order.
+// sq holds the squares of the prefix transposed (chain l contiguous at
+// sq[l*q4 ..]) followed by the tail squares at sq[n4 ..]; lanes 0-3 run the
+// chains, loading the next 32 values while adding the current 32.  Callers
+// place a barrier between writing sq and this call; red[32..35] is used.
+template <int NT>
+__device__ float sumsq_chains(const float *sq, int n, float *red) {
+  const int n4 = n & ~3, q4 = n4 >> 2;
+  if (threadIdx.x < 4) {
+    const float *p = sq + threadIdx.x * q4;
+    float acc = 0.0f;
+    int i = 0;
+    if (q4 > 0 && (q4 & 31) == 0) {
+      const float4 *p4 = reinterpret_cast<const float4 *>(p);
+      const int groups = q4 >> 5;
+      float4 a[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) a[k] = p4[k];
+      for (int gi = 0; gi < groups; gi++) {
+        const int nx = min(gi + 1, groups - 1) * 8;
+        float4 b[8];
+#pragma unroll
+        for (int k = 0; k < 8; k++) b[k] = p4[nx + k];
+#pragma unroll
+        for (int k = 0; k < 8; k++) {
+          acc = acc + a[k].x;
+          acc = acc + a[k].y;
+          acc = acc + a[k].z;
+          acc = acc + a[k].w;
+        }
+#pragma unroll
+        for (int k = 0; k < 8; k++) a[k] = b[k];
+      }
+      i = q4;
+    } else if ((q4 & 3) == 0) {
+      for (; i + 16 <= q4; i += 16) {
+        const float4 a = *reinterpret_cast<const float4 *>(p + i);
+        const float4 b = *reinterpret_cast<const float4 *>(p + i + 4);
+        const float4 c = *reinterpret_cast<const float4 *>(p + i + 8);
+        const float4 d = *reinterpret_cast<const float4 *>(p + i + 12);
+        acc = acc + a.x; acc = acc + a.y; acc = acc + a.z; acc = acc + a.w;
+        acc = acc + b.x; acc = acc + b.y; acc = acc + b.z; acc = acc + b.w;
+        acc = acc + c.x; acc = acc + c.y; acc = acc + c.z; acc = acc + c.w;
+        acc = acc + d.x; acc = acc + d.y; acc = acc + d.z; acc = acc + d.w;
+      }
+    }
+    for (; i < q4; i++) acc = acc + p[i];
+    red[32 + threadIdx.x] = acc;
+  }
+  bar<NT>();
+  float s = ((red[32] + red[33]) + red[34]) + red[35];
+  for (int i = n4; i < n; i++) s = s + sq[i];
+  return s;
+}
+
+// where the square of element j goes in the sumsq_chains layout
+__device__ __forceinline__ int sq_slot(int j, int n) {
+  const int n4 = n & ~3;
+  return j < n4 ? (j & 3) * (n4 >> 2) + (j >> 2) : j;
+}
+
+// Sum of squares of v[0..n) held in LDS, reference order.
+template <int NT>
+__device__ float sumsq_lds(const float *v, int n, float *sq, float *red) {
+  for (int j = threadIdx.x; j < n; j += NT) {
+    const float x = v[j];
+    sq[sq_slot(j, n)] = x * x;
+  }
+  bar<NT>();
+  return sumsq_chains<NT>(sq, n, red);
+}
+
+// Sequential sum of v[0..n) (a single accumulator, in index order).
+__device__ __forceinline__ float seq_sum(const float *v, int n) {
+  float s = 0.0f;
+  int i = 0;
+  if ((reinterpret_cast<uintptr_t>(v) & 15) == 0) {
+    for (; i + 16 <= n; i += 16) {
+      const float4 a = *reinterpret_cast<const float4 *>(v + i);
+      const float4 b = *reinterpret_cast<const float4 *>(v + i + 4);
+      const float4 c = *reinterpret_cast<const float4 *>(v + i + 8);
+      const float4 d = *reinterpret_cast<const float4 *>(v + i + 12);
+      s = s + a.x; s = s + a.y; s = s + a.z; s = s + a.w;
+      s = s + b.x; s = s + b.y; s = s + b.z; s = s + b.w;
+      s = s + c.x; s = s + c.y; s = s + c.z; s = s + c.w;
+      s = s + d.x; s = s + d.y; s = s + d.z; s = s + d.w;
+    }
+  }
+  for (; i < n; i++) s = s + v[i];
+  return s;
+}
+
+// quantizePerChannelInt8 (quantize.zig:12-47) of a row held in registers
+// (element j = threadIdx.x + u*NT, valid for j < n), given the row's max|v|:
+// writes q[j] and returns the row scale.
+template <int NT>
+__device__ float quantize_regs_with_max(const float (&v)[RB], int n, float mx, int8_t *q) {
+  if (mx == 0.0f) {
+#pragma unroll
+    for (int u = 0; u < RB; u++)
+      if (threadIdx.x + u * NT < n) q[threadIdx.x + u * NT] = 0;
+    return 1.0f;
+  }
+  const float inv = 127.0f / mx;
+#pragma unroll
+  for (int u = 0; u < RB; u++) {
+    const int j = threadIdx.x + u * NT;
+    if (j < n) {
+      float r = roundf(v[u] * inv);
+      r = fminf(127.0f, fmaxf(-127.0f, r));
+      q[j] = (int8_t)(int)r;
+    }
+  }
+  return mx / 127.0f;
+}
+
+// per-thread max|v[u]| over its valid elements (the reference's `if a > m`)
+template <int NT>
+__device__ __forceinline__ float local_absmax(const float (&v)[RB], int n) {
+  float mx = 0.0f;
+#pragma unroll
+  for (int u = 0; u < RB; u++) {
+    const float a = fabsf(v[u]);
+    if (threadIdx.x + u * NT < n && a > mx) mx = a;
+  }
+  return mx;
+}
+
+// the whole quantizer: workgroup max (one barrier), then quantize_regs_with_max
+template <int NT>
+__device__ float quantize_regs(const float (&v)[RB], int n, int8_t *q, float *red, int slot) {
+  wg_max_post<NT>(local_absmax<NT>(v, n), red, slot);
+  bar<NT>();
+  return quantize_regs_with_max<NT>(v, n, wg_max_get<NT>(red, slot), q);
+}
+
+// device address of the expf table (per device; resolved once)
+static const uint64_t *exp_table_address() {
+  static const uint64_t *addr[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  if (!addr[dev]) {
+    void *p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(syn_exp2_tab)) != hipSuccess) return nullptr;
+    addr[dev] = static_cast<const uint64_t *>(p);
+  }
+  return addr[dev];
+}
+
+// ------------------------------------------------------------------ split-K GEMV
+enum { PRO_NORM = 0, PRO_QUANT = 1, PRO_SWIGLU = 2 };
+
+struct ProArgs {
+  // PRO_NORM: x = (base ? base : embed[st->token]) + delta
+  const float *base;
+  const float *embed;
+  const StepState *st;
+  int vocab;
+  RowSrc delta;
+  float *res_out;
+  const float *nw;
+  const float *zero_row;  // H zeros (the embedding row of an id >= vocab)
+  float eps;
+  // PRO_QUANT
+  const float *vec;
+  // PRO_SWIGLU; exp_tab = device address of syn_exp2_tab, passed as a plain
+  // pointer so its load is ordered like any other (a __constant__ load may be
+  // moved behind the weight loads)
+  RowSrc gu;
+  const uint64_t *exp_tab;
+  // all: prologue vector length (the GEMV's K) and the scale output
+  int H;
+  float *s_out;
+};
+
+struct GemvArgs {
+  const i32x4 *W;
+  int C, cs;
+  int *acc;
+};
+
+// grid (panels, ks).  dynamic LDS: sq[round4(H)] floats (PRO_NORM) | xq[C*16].
+// Everything a workgroup reads from memory is requested at entry: its weight
+// chunks, then the prologue's inputs; the prologue then runs from registers.
+// Loads are unconditional from clamped (in-bounds) addresses and the values
+// of out-of-range lanes are ignored where they are used: a conditional load
+// would make the compiler wait for it on the spot.
+template <int PRO, int NT, int U>
+__global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
+  constexpr int NW = NT / 64;
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ float red[64];
+  __shared__ int redi[NW * 64];
+  const int H = a.H;
+  float *sq = reinterpret_cast<float *>(smem);
+  int8_t *xq = reinterpret_cast<int8_t *>(smem) + (PRO == PRO_NORM ? ((H + 3) & ~3) * 4 : 0);
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int panel = blockIdx.x, ks = blockIdx.y;
+  const int c0 = ks * g.cs, c1 = min(g.C, c0 + g.cs);  // c0 < c1 by the plan
+  SYN_TS_DECL
+  SYN_TS(0);
+  SYN_TSR(14);
+
+  // Vector loads retire in issue order, so the prologue's inputs (L2 hits)
+  // are requested before the weight chunks (HBM): the prologue then waits
+  // only for its own data while the weights stream in behind it.
+  i32x4 w[U];
+  const i32x4 *Wp = g.W + (size_t)panel * g.C * 64 + lane;
+  auto issue_weights = [&]() {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int c = min(c0 + wave + u * NW, c1 - 1);
+      w[u] = __builtin_nontemporal_load(Wp + (size_t)c * 64);
+    }
+    asm volatile("" ::: "memory");  // keep the weight requests here, ahead of the prologue
+    SYN_TS(1);
+  };
+
+  // 1. prologue inputs (element j = tid + u*NT, clamped to H-1), 2. the
+  //    weight chunks, 3. the activation row x[] in registers
+  float x[RB];
+  float nwv[RB];
+  if constexpr (PRO == PRO_NORM) {
+    const float *src = a.base;
+    if (!src) {
+      const uint32_t tok = a.st->token;
+      src = tok < (uint32_t)a.vocab ? a.embed + (size_t)tok * H : a.zero_row;
+    }
+#pragma unroll
+    for (int u = 0; u < RB; u++) {
+      const int j = min(tid + u * NT, H - 1);
+      x[u] = src[j];
+      nwv[u] = a.nw[j];
+    }
+    // without a delta the loads below read the norm gains instead (in-bounds,
+    // values unused), so that no load sits behind a branch
+    const bool has_delta = a.delta.acc != nullptr;
+    const int *dacc = has_delta ? a.delta.acc : reinterpret_cast<const int *>(a.nw);
+    const float *dws = has_delta ? a.delta.ws : a.nw;
+    const float *dsxp = has_delta ? a.delta.sx : a.nw;
+    int da[RB];
+    float dw[RB];
+#pragma unroll
+    for (int u = 0; u < RB; u++) {
+      const int j = min(tid + u * NT, H - 1);
+      da[u] = dacc[j];
+      dw[u] = dws[j];
+    }
+    const float dsx = dsxp[0];
+    issue_weights();
+    if (has_delta) {
+#pragma unroll
+      for (int u = 0; u < RB; u++) {
+        const float f = (float)da[u] * dsx;
+        const float d = f * dw[u];
+        x[u] = x[u] + d;
+      }
+    }
+  } else if constexpr (PRO == PRO_QUANT) {
+#pragma unroll
+    for (int u = 0; u < RB; u++) x[u] = a.vec[min(tid + u * NT, H - 1)];
+    issue_weights();
+  } else {
+    // expf's 2^(i/32) table goes to LDS first: a lookup in global memory
+    // would wait behind the outstanding weight loads
+    __shared__ uint64_t exp_tab[32];
+    const uint64_t tv = a.exp_tab[tid & 31];
+    int ga[RB], ua[RB];
+    float gw[RB], uw[RB];
+#pragma unroll
+    for (int u = 0; u < RB; u++) {
+      const int j = min(tid + u * NT, H - 1);
+      ga[u] = a.gu.acc[j];
+      ua[u] = a.gu.acc[H + j];
+      gw[u] = a.gu.ws[j];
+      uw[u] = a.gu.ws[H + j];
+    }
+    const float gsx = a.gu.sx[0];
+    issue_weights();
+    if (tid < 32) exp_tab[tid] = tv;
+    bar<NT>();
+#pragma unroll
+    for (int u = 0; u < RB; u++) {
+      // silu(gate) * up (int8.rs:500-503), each factor the GEMV epilogue
+      const float fg = (float)ga[u] * gsx, fu = (float)ua[u] * gsx;
+      const float gv = fg * gw[u], uv = fu * uw[u];
+      const float act = syn_silu_tab(gv, exp_tab);
+      x[u] = act * uv;
+    }
+  }
+  for (int j = H + tid; j < g.C * 16; j += NT) xq[j] = 0;
+  SYN_TS(2);
+
+  float sv;
+  if constexpr (PRO == PRO_NORM) {
+    // RMSNorm (ops/norm.rs:8-38): out = (x*w) * (1/sqrt(sumsq/n + eps)),
+    // then the quantizer's max|out|.  Scaling by the positive `scale` is a
+    // monotonic rounding, so max|t*scale| = fl(max|t| * scale): the max of
+    // t = x*w is reduced while lanes 0-3 run the sum-of-squares chains.
+    float t[RB];
+#pragma unroll
+    for (int u = 0; u < RB; u++) {
+      const int j = tid + u * NT;
+      if (j < H) sq[sq_slot(j, H)] = x[u] * x[u];
+      t[u] = x[u] * nwv[u];
+    }
+    wg_max_post<NT>(local_absmax<NT>(t, H), red, 0);
+    bar<NT>();
+    SYN_TS(3);
+    const float ss = sumsq_chains<NT>(sq, H, red);
+    SYN_TS(4);
+    const float scale = 1.0f / sqrtf(ss / (float)H + a.eps);
+    float nv[RB];
+#pragma unroll
+    for (int u = 0; u < RB; u++) nv[u] = t[u] * scale;
+    float mx = wg_max_get<NT>(red, 0) * scale;
+    if (!(mx <= 3.402823466e38f) || !(scale > 0.0f)) {  // inf/nan rows: reduce explicitly
+      wg_max_post<NT>(local_absmax<NT>(nv, H), red, 16);
+      bar<NT>();
+      mx = wg_max_get<NT>(red, 16);
+    }
+    sv = quantize_regs_with_max<NT>(nv, H, mx, xq);
+  } else {
+    sv = quantize_regs<NT>(x, H, xq, red, 0);
+  }
+  SYN_TS(5);
+  bar<NT>();
+  SYN_TS(6);
+
+  // 3. integer dot products of this wave's chunks, reduced over the waves
+  int acc = 0;
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const int c = c0 + wave + u * NW;
+    if (c < c1) {
+      const i32x4 xv = *reinterpret_cast<const i32x4 *>(xq + c * 16);
+      acc = __builtin_amdgcn_sdot4(w[u].x, xv.x, acc, false);
+      acc = __builtin_amdgcn_sdot4(w[u].y, xv.y, acc, false);
+      acc = __builtin_amdgcn_sdot4(w[u].z, xv.z, acc, false);
+      acc = __builtin_amdgcn_sdot4(w[u].w, xv.w, acc, false);
+    }
+  }
+  SYN_TS(7);
+  redi[wave * 64 + lane] = acc;
+  bar<NT>();
+  SYN_TS(8);
+  if (wave == 0) {
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < NW; i++) s += redi[i * 64 + lane];
+    atomicAdd(g.acc + panel * 64 + lane, s);
+  }
+  SYN_TS(9);
+
+  // 4. workgroup 0 publishes the prologue's results for later kernels
+  if (panel == 0 && ks == 0) {
+    if constexpr (PRO == PRO_NORM) {
+      if (a.res_out) {
+#pragma unroll
+        for (int u = 0; u < RB; u++)
+          if (tid + u * NT < H) a.res_out[tid + u * NT] = x[u];
+      }
+    }
+    if (tid == 0) a.s_out[0] = sv;
+  }
+  SYN_TSR(15);
+  SYN_TS_FLUSH(PRO * 16);
+}
+
+// threads per workgroup for a prologue row of H elements (RB rows each)
+static int fused_nt_for(int H) { return H <= RB * 256 ? 256 : H <= RB * 512 ? 512 : 1024; }
+
+// Each wave takes exactly U chunks of every K split (cs = U * waves), with U
+// in {1, 2, 4, 8} chosen so the grid is closest to [target, 2*target]
+// workgroups; only the last split can be partial.
+SplitGemv plan_split_gemv(const void *W, const float *ws, int N, int C, int target_wg, int nt) {
+  SplitGemv g;
+  g.W = W;
+  g.ws = ws;
+  g.N = N;
+  g.N64 = (int)round_up((size_t)N, 64);  // accumulator rows
+  g.C = C;
+  g.nt = std::max(nt, fused_nt_for(C * 16));
+  const int panels = g.N64 / 64, nw = g.nt / 64;
+  int best_u = 8;
+  double best = 1e30;
+  for (int u = 1; u <= 8; u *= 2) {
+    const int cs = u * nw;
+    const int ks = (int)cdiv((size_t)C, (size_t)cs);
+    const double wg = (double)panels * ks;
+    // distance from [target, 2*target] plus the waste of a partial last split
+    double cost = wg < target_wg ? (target_wg - wg) / target_wg
+                : wg > 2.0 * target_wg ? (wg - 2.0 * target_wg) / target_wg : 0.0;
+    cost += (double)(ks * cs - C) / C;
+    if (cost < best - 1e-9) {
+      best = cost;
+      best_u = u;
+    }
+  }
+  g.u = best_u;
+  g.cs = best_u * nw;
+  g.ks = (int)cdiv((size_t)C, (size_t)g.cs);
+  return g;
+}
+
+static size_t fused_lds_bytes(int H, int C) { return round_up((size_t)H, 4) * 4 + (size_t)C * 16; }
+
+bool fused_gemv_fits(int H) {
+  return H <= RB * 1024 && fused_lds_bytes(H, (int)cdiv((size_t)H, 16)) <= 60 * 1024;
+}
+
+template <int PRO, int NT>
+static syn_status_t launch_fused_nt(const ProArgs &a, const SplitGemv &g, hipStream_t s) {
+  GemvArgs ga{reinterpret_cast<const i32x4 *>(g.W), g.C, g.cs, g.acc};
+  const dim3 grid(g.N64 / 64, g.ks);
+  const size_t shm = fused_lds_bytes(a.H, g.C);
+  switch (g.u) {
+    case 1: hipLaunchKernelGGL((k_fused_gemv<PRO, NT, 1>), grid, dim3(NT), shm, s, a, ga); break;
+    case 2: hipLaunchKernelGGL((k_fused_gemv<PRO, NT, 2>), grid, dim3(NT), shm, s, a, ga); break;
+    case 4: hipLaunchKernelGGL((k_fused_gemv<PRO, NT, 4>), grid, dim3(NT), shm, s, a, ga); break;
+    default: hipLaunchKernelGGL((k_fused_gemv<PRO, NT, 8>), grid, dim3(NT), shm, s, a, ga); break;
+  }
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
+
+template <int PRO>
+static syn_status_t launch_fused(const ProArgs &a, const SplitGemv &g, hipStream_t s) {
+  if (!g.acc || !g.W) {
+    set_error("fused decode GEMV: plan not prepared");
+    return SYN_ERR_INTERNAL;
+  }
+  if (a.H > g.C * 16 || !fused_gemv_fits(a.H) || a.H > RB * g.nt) {
+    set_error("fused decode GEMV: activation row does not fit the fused kernel");
+    return SYN_ERR_INVALID_ARG;
+  }
+  if (g.nt == 1024) return launch_fused_nt<PRO, 1024>(a, g, s);
+  if (g.nt == 512) return launch_fused_nt<PRO, 512>(a, g, s);
+  return launch_fused_nt<PRO, 256>(a, g, s);
+}
+
+syn_status_t launch_fused_norm_gemv(const float *base, const float *embed, const StepState *st,
+                                    int vocab, const float *zero_row, RowSrc delta,
+                                    float *res_out, const float *nw, float eps, int H,
+                                    float *s_out, const SplitGemv &g, hipStream_t s) {
+  ProArgs a{};
+  a.base = base;
+  a.embed = embed;
+  a.st = st;
+  a.vocab = vocab;
+  a.delta = delta;
+  a.res_out = res_out;
+  a.nw = nw;
+  a.zero_row = zero_row;
+  a.eps = eps;
+  a.H = H;
+  a.s_out = s_out;
+  return launch_fused<PRO_NORM>(a, g, s);
+}
+
+syn_status_t launch_fused_quant_gemv(const float *vec, int H, float *s_out, const SplitGemv &g,
+                                     hipStream_t s) {
+  ProArgs a{};
+  a.vec = vec;
+  a.H = H;
+  a.s_out = s_out;
+  return launch_fused<PRO_QUANT>(a, g, s);
+}
+
+syn_status_t launch_fused_swiglu_gemv(RowSrc gu, int inter, float *s_out, const SplitGemv &g,
+                                      hipStream_t s) {
+  ProArgs a{};
+  a.exp_tab = exp_table_address();
+  if (!a.exp_tab) {
+    set_error("fused decode: expf table address unavailable");
+    return SYN_ERR_HIP;
+  }
+  a.gu = gu;
+  a.H = inter;
+  a.s_out = s_out;
+  return launch_fused<PRO_SWIGLU>(a, g, s);
+}
+
+// ------------------------------------------------------------------ attention
+// One workgroup per query head.  Prologue = k_qk_norm_rope_kv for the head
+// and its KV head (both query heads of a KV group write the same K/V values
+// into the cache), and the new position's K/V rows are then taken from LDS.
+// Attention = k_attn_decode (ops/attention.rs:24-147): the len >= 64 route
+// uses fused multiply-add chains in f32GemvRow's 32/8-wide column blocks.
+
+// shared prologue: q/k/v rows of this head from the QKV accumulators, head
+// RMSNorms (norm.rs:78-93), rotate-half RoPE at pos (rope.rs:13-43) and the
+// cache append.  qv/kv/vv/sq are LDS rows of hd floats.
+template <int NT>
+__device__ void attn_prologue(const RowSrc &qkv, int head, int kvh, int qd, int kvd, int hd,
+                              const float *qn, const float *kn, float eps, const float *cosT,
+                              const float *sinT, int pos, float *kc, float *vc, int max_seq,
+                              float *qv, float *kv, float *vv, float *sq, float *red) {
+  const int half = hd / 2;
+  for (int d = threadIdx.x; d < hd; d += NT) {
+    qv[d] = row_value(qkv, head * hd + d);
+    kv[d] = row_value(qkv, qd + kvh * hd + d);
+    vv[d] = row_value(qkv, qd + kvd + kvh * hd + d);
+  }
+  __syncthreads();
+  if (qn) {
+    const float ss = sumsq_lds<NT>(qv, hd, sq, red);
+    const float scale = 1.0f / sqrtf(ss / (float)hd + eps);
+    __syncthreads();
+    for (int d = threadIdx.x; d < hd; d += NT) {
+      const float t = qv[d] * qn[d];
+      qv[d] = t * scale;
+    }
+    __syncthreads();
+  }
+  if (kn) {
+    const float ss = sumsq_lds<NT>(kv, hd, sq, red);
+    const float scale = 1.0f / sqrtf(ss / (float)hd + eps);
+    __syncthreads();
+    for (int d = threadIdx.x; d < hd; d += NT) {
+      const float t = kv[d] * kn[d];
+      kv[d] = t * scale;
+    }
+    __syncthreads();
+  }
+  const float *cr = cosT + (size_t)pos * half, *sr = sinT + (size_t)pos * half;
+  for (int i = threadIdx.x; i < half; i += NT) {
+    const float c = cr[i], sn = sr[i];
+    {
+      const float x1 = qv[i], x2 = qv[half + i];
+      const float p = x1 * c, q = x2 * sn, r = x2 * c, t = x1 * sn;
+      qv[i] = p - q;
+      qv[half + i] = r + t;
+    }
+    {
+      const float x1 = kv[i], x2 = kv[half + i];
+      const float p = x1 * c, q = x2 * sn, r = x2 * c, t = x1 * sn;
+      kv[i] = p - q;
+      kv[half + i] = r + t;
+    }
+  }
+  __syncthreads();
+  for (int d = threadIdx.x; d < hd; d += NT) {
+    kc[kv_k_index(pos, kvh, d, hd, max_seq)] = kv[d];
+    vc[kv_v_index(pos, kvh, d, hd, max_seq)] = vv[d];
+  }
+}
+
+// softmax_slice (activation.rs:117-129) over e[0..len): max, exp(x - max),
+// sequential sum, divide when the sum is positive
+template <int NT>
+__device__ void attn_softmax(float *e, int len, float mx, float *red) {
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));  // scores may be negative
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = mx;
+  __syncthreads();
+  mx = red[0];
+#pragma unroll
+  for (int i = 1; i < NT / 64; i++) mx = fmaxf(mx, red[i]);
+  for (int sidx = threadIdx.x; sidx < len; sidx += NT) e[sidx] = syn_expf(e[sidx] - mx);
+  __syncthreads();
+  if (threadIdx.x == 0) red[40] = seq_sum(e, len);
+  __syncthreads();
+  const float sum = red[40];
+  if (sum > 0.0f)
+    for (int sidx = threadIdx.x; sidx < len; sidx += NT) e[sidx] = e[sidx] / sum;
+  __syncthreads();
+}
+
+// Generic form (any head_dim): scores and P.V read the cache directly.
+// dynamic LDS: qv[hd] | kv[hd] | vv[hd] | sq[hd] | e[max_seq rounded to 4]
+__global__ void __launch_bounds__(256)
+    k_fused_attention(RowSrc qkv, int nh, int nkv, int hd, const float *__restrict__ qn,
+                      const float *__restrict__ kn, float eps, const float *__restrict__ cosT,
+                      const float *__restrict__ sinT, const StepState *__restrict__ st,
+                      float *__restrict__ kc, float *__restrict__ vc, int max_seq,
+                      float *__restrict__ out) {
+  constexpr int NT = 256;
+  extern __shared__ __align__(16) float sm[];
+  __shared__ float red[64];
+  const int head = blockIdx.x;
+  const int kvh = head / (nh / nkv);
+  const int qd = nh * hd, kvd = nkv * hd;
+  float *qv = sm, *kv = qv + hd, *vv = kv + hd, *sq = vv + hd, *e = sq + hd;
+  const int pos = st->pos;
+  const int len = pos + 1;
+  attn_prologue<NT>(qkv, head, kvh, qd, kvd, hd, qn, kn, eps, cosT, sinT, pos, kc, vc, max_seq,
+                    qv, kv, vv, sq, red);
+  const float scale = 1.0f / sqrtf((float)hd);
+  const bool simd = len >= 64;
+  const int n32 = len - len % 32;
+  const int n8 = n32 + ((len - n32) / 8) * 8;
+  float mx = -__builtin_inff();
+  for (int sidx = threadIdx.x; sidx < len; sidx += NT) {
+    const bool fused = simd && sidx < n8;
+    float acc = 0.0f;
+    for (int d = 0; d < hd; d++) {
+      const float kval = sidx == pos ? kv[d] : kc[kv_k_index(sidx, kvh, d, hd, max_seq)];
+      if (fused) {
+        acc = __builtin_fmaf(qv[d], kval, acc);
+      } else {
+        const float t = qv[d] * kval;
+        acc = acc + t;
+      }
+    }
+    const float sc = acc * scale;
+    e[sidx] = sc;
+    mx = fmaxf(mx, sc);
+  }
+  attn_softmax<NT>(e, len, mx, red);
+  const int d32 = hd - hd % 32;
+  for (int d = threadIdx.x; d < hd; d += NT) {
+    const bool fused = simd && d < d32;
+    float acc = 0.0f;
+    for (int i = 0; i < len; i++) {
+      const float vval = i == pos ? vv[d] : vc[kv_v_index(i, kvh, d, hd, max_seq)];
+      if (fused) {
+        acc = __builtin_fmaf(e[i], vval, acc);
+      } else {
+        const float t = e[i] * vval;
+        acc = acc + t;
+      }
+    }
+    out[head * hd + d] = acc;
+  }
+}
+
+// max over the wave of any floats (invalid DPP sources keep -inf)
+template <int CTRL>
+__device__ __forceinline__ float dpp_fmax_any(float v) {
+  const int s = __builtin_amdgcn_update_dpp((int)0xff800000u, __float_as_int(v), CTRL, 0xf, 0xf,
+                                            false);
+  return fmaxf(v, __int_as_float(s));
+}
+__device__ __forceinline__ float wave_max_any(float v) {
+  v = dpp_fmax_any<0x111>(v);
+  v = dpp_fmax_any<0x112>(v);
+  v = dpp_fmax_any<0x114>(v);
+  v = dpp_fmax_any<0x118>(v);
+  v = dpp_fmax_any<0x142>(v);
+  v = dpp_fmax_any<0x143>(v);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Fast form for head_dim % 4 == 0 and <= 128: 8 waves in three roles, each
+// wave's loads requested at kernel entry (at most 48 per wave, inside the 63
+// a wave can have in flight), unconditionally from clamped addresses.
+//  waves 0-3  scores: lane = position 64w + lane of each pass of 256; the K
+//             row comes from the tiled cache as 16-byte loads (1 KiB per wave
+//             load) and stays in registers for the lane's dot-product chain;
+//  waves 4-5  P.V: lane = output column d; V values come 4 positions per
+//             16-byte load, the first 192 positions kept in registers, one
+//             sequential chain over positions per column;
+//  waves 6-7  prologue: lane = d, the q/k/v rows, head norms, RoPE, append.
+// dynamic LDS: qv | kv | vv | sq (hd each) | e[max_seq rounded to 4]
+constexpr int kAttnPass = 256;  // positions per score pass (4 waves x 64)
+constexpr int kPre = 48;        // prefetch registers (float4) per lane
+
+__global__ void __launch_bounds__(512)
+    k_fused_attention_fast(RowSrc qkv, int nh, int nkv, int hd, const float *__restrict__ qn,
+                           const float *__restrict__ kn, float eps,
+                           const float *__restrict__ cosT, const float *__restrict__ sinT,
+                           const uint64_t *exp_tab_g, const StepState *__restrict__ st,
+                           float *__restrict__ kc, float *__restrict__ vc, int max_seq,
+                           float *__restrict__ out) {
+  constexpr int NT = 512;
+  extern __shared__ __align__(16) float sm[];
+  __shared__ float red[64];
+  __shared__ uint64_t exp_tab[32];
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int head = blockIdx.x;
+  const int kvh = head / (nh / nkv);
+  const int qd = nh * hd, kvd = nkv * hd, hd4 = hd >> 2, half = hd >> 1;
+  float *qv = sm, *kv = qv + hd, *vv = kv + hd, *sq = vv + hd;
+  float *e = sq + hd;
+  SYN_TS_DECL
+  SYN_TS(0);
+  const int pos = st->pos;
+  const int len = pos + 1;
+  const int tiles = (max_seq + 63) >> 6, s4 = (max_seq + 3) >> 2;
+  const float4 *K4 = reinterpret_cast<const float4 *>(kc) + (size_t)kvh * tiles * hd4 * 64;
+  const float4 *V4 = reinterpret_cast<const float4 *>(vc) + (size_t)kvh * s4 * hd;
+  const int ngroups = (len + 3) >> 2;
+  const bool qk_wave = wave < 4;
+  const bool pv_wave = wave == 4 || wave == 5;
+  const int dcol = (wave & 1) * 64 + lane;  // column of P.V and prologue lanes
+  const bool pro_wave = wave >= 6;
+
+  float4 pre[kPre];
+  auto load_k = [&](int tile) {
+    const float4 *src = K4 + (size_t)min(tile, tiles - 1) * hd4 * 64 + lane;
+#pragma unroll
+    for (int c = 0; c < 32; c++) pre[c] = src[(size_t)min(c, hd4 - 1) * 64];
+  };
+  int aq = 0, ak = 0, av = 0;
+  float wq = 0.0f, wk = 0.0f, wv = 0.0f, gq = 0.0f, gk = 0.0f, cs = 0.0f, sn = 0.0f, qsx = 0.0f;
+  uint64_t tv = 0;
+  if (qk_wave) {
+    tv = exp_tab_g[lane & 31];
+    load_k(wave);
+  } else if (pv_wave) {
+    const float4 *src = V4 + min(dcol, hd - 1);
+#pragma unroll
+    for (int i = 0; i < kPre; i++) pre[i] = src[(size_t)min(i, ngroups - 1) * hd];
+  } else {
+    const int dc = min(dcol, hd - 1), hc = min(dcol, half - 1);
+    aq = qkv.acc[head * hd + dc];
+    ak = qkv.acc[qd + kvh * hd + dc];
+    av = qkv.acc[qd + kvd + kvh * hd + dc];
+    wq = qkv.ws[head * hd + dc];
+    wk = qkv.ws[qd + kvh * hd + dc];
+    wv = qkv.ws[qd + kvd + kvh * hd + dc];
+    gq = qn ? qn[dc] : 0.0f;
+    gk = kn ? kn[dc] : 0.0f;
+    cs = cosT[(size_t)pos * half + hc];
+    sn = sinT[(size_t)pos * half + hc];
+    qsx = qkv.sx[0];
+  }
+  asm volatile("" ::: "memory");
+  SYN_TS(1);
+
+  const int d = dcol;
+  const bool pro_lane = pro_wave && d < hd;
+  if (tid < 32) exp_tab[tid] = tv;
+  if (pro_lane) {
+    float f;
+    f = (float)aq * qsx; qv[d] = f * wq;
+    f = (float)ak * qsx; kv[d] = f * wk;
+    f = (float)av * qsx; vv[d] = f * wv;
+  }
+  __syncthreads();
+  SYN_TS(2);
+  // headwise RMSNorm (norm.rs:78-93) of q and k
+  if (qn || kn) {
+    if (pro_lane) {
+      sq[sq_slot(d, hd)] = qv[d] * qv[d];
+      e[sq_slot(d, hd)] = kv[d] * kv[d];  // e is free until the scores
+    }
+    __syncthreads();
+    const float ssq = qn ? sumsq_chains<NT>(sq, hd, red) : 0.0f;
+    __syncthreads();
+    const float ssk = kn ? sumsq_chains<NT>(e, hd, red) : 0.0f;
+    if (pro_lane) {
+      if (qn) {
+        const float scale = 1.0f / sqrtf(ssq / (float)hd + eps);
+        const float t = qv[d] * gq;
+        qv[d] = t * scale;
+      }
+      if (kn) {
+        const float scale = 1.0f / sqrtf(ssk / (float)hd + eps);
+        const float t = kv[d] * gk;
+        kv[d] = t * scale;
+      }
+    }
+    __syncthreads();
+  }
+  SYN_TS(3);
+  // rotate-half RoPE at pos (rope.rs:13-43); lane i < half owns (i, half+i)
+  if (pro_wave && d < half) {
+    {
+      const float x1 = qv[d], x2 = qv[half + d];
+      const float p = x1 * cs, q = x2 * sn, r = x2 * cs, t = x1 * sn;
+      qv[d] = p - q;
+      qv[half + d] = r + t;
+    }
+    {
+      const float x1 = kv[d], x2 = kv[half + d];
+      const float p = x1 * cs, q = x2 * sn, r = x2 * cs, t = x1 * sn;
+      kv[d] = p - q;
+      kv[half + d] = r + t;
+    }
+  }
+  __syncthreads();
+  if (pro_lane) {
+    kc[kv_k_index(pos, kvh, d, hd, max_seq)] = kv[d];
+    vc[kv_v_index(pos, kvh, d, hd, max_seq)] = vv[d];
+  }
+  SYN_TS(4);
+
+  // scores (waves 0-3): the lane of position pos takes its K row from LDS,
+  // its prefetched row predates the append
+  const float scale = 1.0f / sqrtf((float)hd);
+  const bool simd = len >= 64;
+  const int n32 = len - len % 32;
+  const int n8 = n32 + ((len - n32) / 8) * 8;
+  float mx = -__builtin_inff();
+  if (qk_wave) {
+    const float4 *q4 = reinterpret_cast<const float4 *>(qv);
+    const float4 *k4 = reinterpret_cast<const float4 *>(kv);
+    for (int p0 = 0; p0 < len; p0 += kAttnPass) {
+      if (p0 > 0) load_k((p0 >> 6) + wave);
+      const int p = p0 + wave * 64 + lane;
+      if (p == pos) {
+#pragma unroll
+        for (int c = 0; c < 32; c++)
+          if (c < hd4) pre[c] = k4[c];
+      }
+      if (p < len) {
+        float acc = 0.0f;
+        if (simd && p < n8) {
+#pragma unroll
+          for (int c = 0; c < 32; c++) {
+            if (c < hd4) {
+              const float4 qq = q4[c];
+              acc = __builtin_fmaf(qq.x, pre[c].x, acc);
+              acc = __builtin_fmaf(qq.y, pre[c].y, acc);
+              acc = __builtin_fmaf(qq.z, pre[c].z, acc);
+              acc = __builtin_fmaf(qq.w, pre[c].w, acc);
+            }
+          }
+        } else {
+#pragma unroll
+          for (int c = 0; c < 32; c++) {
+            if (c < hd4) {
+              const float4 qq = q4[c];
+              float t;
+              t = qq.x * pre[c].x; acc = acc + t;
+              t = qq.y * pre[c].y; acc = acc + t;
+              t = qq.z * pre[c].z; acc = acc + t;
+              t = qq.w * pre[c].w; acc = acc + t;
+            }
+          }
+        }
+        const float sc = acc * scale;
+        e[p] = sc;
+        mx = fmaxf(mx, sc);
+      }
+    }
+    mx = wave_max_any(mx);
+    if (lane == 0) red[wave] = mx;
+  }
+  SYN_TS(5);
+  __syncthreads();
+  // softmax_slice (activation.rs:117-129)
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  for (int sidx = tid; sidx < len; sidx += NT) e[sidx] = syn_expf_tab(e[sidx] - mx, exp_tab);
+  __syncthreads();
+  if (tid == 0) red[40] = seq_sum(e, len);
+  __syncthreads();
+  const float sum = red[40];
+  if (sum > 0.0f)
+    for (int sidx = tid; sidx < len; sidx += NT) e[sidx] = e[sidx] / sum;
+  __syncthreads();
+  SYN_TS(6);
+
+  // P.V (waves 4-5): one chain over positions per output column; the new
+  // position's value comes from LDS
+  if (pv_wave && d < hd) {
+    const int d32 = hd - hd % 32;
+    const bool fused = simd && d < d32;
+    const float vnew = vv[d];
+    const float4 *e4 = reinterpret_cast<const float4 *>(e);
+    float acc = 0.0f;
+    auto chain4 = [&](int g, float4 v) {
+      const float4 ev = e4[g];
+      const int p = 4 * g;
+      const float v0 = p + 0 == pos ? vnew : v.x, v1 = p + 1 == pos ? vnew : v.y;
+      const float v2 = p + 2 == pos ? vnew : v.z, v3 = p + 3 == pos ? vnew : v.w;
+      if (fused) {
+        if (p + 0 < len) acc = __builtin_fmaf(ev.x, v0, acc);
+        if (p + 1 < len) acc = __builtin_fmaf(ev.y, v1, acc);
+        if (p + 2 < len) acc = __builtin_fmaf(ev.z, v2, acc);
+        if (p + 3 < len) acc = __builtin_fmaf(ev.w, v3, acc);
+      } else {
+        float t;
+        if (p + 0 < len) { t = ev.x * v0; acc = acc + t; }
+        if (p + 1 < len) { t = ev.y * v1; acc = acc + t; }
+        if (p + 2 < len) { t = ev.z * v2; acc = acc + t; }
+        if (p + 3 < len) { t = ev.w * v3; acc = acc + t; }
+      }
+    };
+#pragma unroll
+    for (int g = 0; g < kPre; g++)
+      if (g < ngroups) chain4(g, pre[g]);
+    for (int g0 = kPre; g0 < ngroups; g0 += 16) {  // beyond the prefetched groups
+      float4 vb[16];
+#pragma unroll
+      for (int k = 0; k < 16; k++) vb[k] = V4[(size_t)min(g0 + k, ngroups - 1) * hd + d];
+#pragma unroll
+      for (int k = 0; k < 16; k++)
+        if (g0 + k < ngroups) chain4(g0 + k, vb[k]);
+    }
+    out[head * hd + d] = acc;
+  }
+  SYN_TS(7);
+  SYN_TS_FLUSH(48);
+}
+
+static bool attention_fast_ok(int hd) { return hd % 4 == 0 && hd <= 128; }
+
+static size_t attention_lds_bytes(int hd, int max_seq) {
+  return ((size_t)4 * hd + round_up((size_t)max_seq, 4)) * sizeof(float);
+}
+
+bool fused_attention_fits(int hd, int max_seq) {
+  return attention_lds_bytes(hd, max_seq) <= 60 * 1024;
+}
+
+syn_status_t launch_fused_attention(RowSrc qkv, int nh, int nkv, int hd, const float *qn,
+                                    const float *kn, float eps, const float *cosT,
+                                    const float *sinT, const StepState *st, float *kc, float *vc,
+                                    int max_seq, float *out, hipStream_t s) {
+  if (!fused_attention_fits(hd, max_seq)) {
+    set_error("fused decode attention: max_seq too long for LDS");
+    return SYN_ERR_INVALID_ARG;
+  }
+  const size_t shm = attention_lds_bytes(hd, max_seq);
+  if (attention_fast_ok(hd)) {
+    const uint64_t *tab = exp_table_address();
+    if (!tab) {
+      set_error("fused decode: expf table address unavailable");
+      return SYN_ERR_HIP;
+    }
+    hipLaunchKernelGGL(k_fused_attention_fast, dim3(nh), dim3(512), shm, s, qkv, nh, nkv, hd, qn,
+                       kn, eps, cosT, sinT, tab, st, kc, vc, max_seq, out);
+  } else {
+    hipLaunchKernelGGL(k_fused_attention, dim3(nh), dim3(256), shm, s, qkv, nh, nkv, hd, qn, kn,
+                       eps, cosT, sinT, st, kc, vc, max_seq, out);
+  }
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
+
+// ------------------------------------------------------------------ head
+// final residual + RMSNorm + quantize, one workgroup of 1024 threads;
+// dynamic LDS: sq[round4(H)]
+__global__ void __launch_bounds__(1024)
+    k_fused_final_norm(const float *__restrict__ base, RowSrc delta, const float *__restrict__ nw,
+                       float eps, int H, int8_t *__restrict__ xq, float *__restrict__ s_out) {
+  constexpr int NT = 1024;
+  extern __shared__ __align__(16) float fsm[];
+  __shared__ float red[64];
+  const int tid = threadIdx.x;
+  float x[RB], nwv[RB];
+  int da[RB];
+  float dw[RB];
+  const bool has_delta = delta.acc != nullptr;
+#pragma unroll
+  for (int u = 0; u < RB; u++) {
+    const int j = min(tid + u * NT, H - 1);
+    x[u] = base[j];
+    nwv[u] = nw[j];
+    da[u] = has_delta ? delta.acc[j] : 0;
+    dw[u] = has_delta ? delta.ws[j] : 0.0f;
+  }
+  if (has_delta) {
+    const float dsx = delta.sx[0];
+#pragma unroll
+    for (int u = 0; u < RB; u++) {
+      const float f = (float)da[u] * dsx;
+      const float d = f * dw[u];
+      x[u] = x[u] + d;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < RB; u++) {
+    const int j = tid + u * NT;
+    if (j < H) fsm[sq_slot(j, H)] = x[u] * x[u];
+  }
+  float t[RB];
+#pragma unroll
+  for (int u = 0; u < RB; u++) t[u] = x[u] * nwv[u];
+  wg_max_post<NT>(local_absmax<NT>(t, H), red, 0);
+  __syncthreads();
+  const float ss = sumsq_chains<NT>(fsm, H, red);
+  const float scale = 1.0f / sqrtf(ss / (float)H + eps);
+  float nv[RB];
+#pragma unroll
+  for (int u = 0; u < RB; u++) nv[u] = t[u] * scale;
+  float mx = wg_max_get<NT>(red, 0) * scale;  // max|t*scale| = fl(max|t| * scale)
+  if (!(mx <= 3.402823466e38f) || !(scale > 0.0f)) {
+    wg_max_post<NT>(local_absmax<NT>(nv, H), red, 16);
+    __syncthreads();
+    mx = wg_max_get<NT>(red, 16);
+  }
+  const float sv = quantize_regs_with_max<NT>(nv, H, mx, xq);
+  if (tid == 0) s_out[0] = sv;
+}
+
+syn_status_t launch_fused_final_norm(const float *base, RowSrc delta, const float *nw, float eps,
+                                     int H, int8_t *xq, float *s_out, hipStream_t s) {
+  if (H > RB * 1024) {
+    set_error("fused final norm: hidden too large");
+    return SYN_ERR_INVALID_ARG;
+  }
+  hipLaunchKernelGGL(k_fused_final_norm, dim3(1), dim3(1024), round_up((size_t)H, 4) * 4, s, base,
+                     delta, nw, eps, H, xq, s_out);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
+
+__global__ void __launch_bounds__(256) k_zero_i32(int *__restrict__ p, size_t n) {
+  const size_t n4 = n / 4;
+  i32x4 *p4 = reinterpret_cast<i32x4 *>(p);
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256)
+    p4[i] = i32x4{0, 0, 0, 0};
+  for (size_t i = n4 * 4 + (size_t)blockIdx.x * 256 + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * 256)
+    p[i] = 0;
+}
+
+syn_status_t launch_zero_i32(int *p, size_t n, hipStream_t s) {
+  if (n == 0) return SYN_OK;
+  if (reinterpret_cast<uintptr_t>(p) & 15) {
+    set_error("launch_zero_i32: buffer must be 16-byte aligned");
+    return SYN_ERR_INVALID_ARG;
+  }
+  const unsigned blocks = (unsigned)std::min<size_t>(512, cdiv(cdiv(n, 4), 256));
+  hipLaunchKernelGGL(k_zero_i32, dim3(blocks), dim3(256), 0, s, p, n);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
+
+struct Top2v {
+  float v1;
+  int i1;
+  float v2;
+};
+
+// larger value wins; on equal values the larger index (the last maximum,
+// sampler.rs:217-224); v2 = the largest value other than the winner
+__device__ __forceinline__ Top2v top2v_merge(Top2v a, Top2v b) {
+  const bool bw = (b.v1 > a.v1) || (b.v1 == a.v1 && b.i1 > a.i1);
+  const Top2v w = bw ? b : a, l = bw ? a : b;
+  return Top2v{w.v1, w.i1, fmaxf(w.v2, l.v1)};
+}
+
+__device__ __forceinline__ Top2v wave_top2(Top2v t) {
+  for (int o = 32; o > 0; o >>= 1) {
+    Top2v u;
+    u.v1 = __shfl_xor(t.v1, o);
+    u.i1 = __shfl_xor(t.i1, o);
+    u.v2 = __shfl_xor(t.v2, o);
+    t = top2v_merge(t, u);
+  }
+  return t;
+}
+
+// one workgroup per 64-row panel; each wave takes every NW-th K chunk
+template <int NW, int U>
+__global__ void __launch_bounds__(NW * 64)
+    k_lmhead_top2(const i32x4 *__restrict__ W, const float *__restrict__ ws, int N, int C,
+                  const int8_t *__restrict__ xq, const float *__restrict__ sx,
+                  float *__restrict__ logits, float *__restrict__ pv, int *__restrict__ pi,
+                  float *__restrict__ pv2) {
+  __shared__ int redi[NW * 64];
+  const int panel = blockIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const i32x4 *Wp = W + (size_t)panel * C * 64 + lane;
+  int acc = 0;
+  for (int c0 = 0; c0 < C; c0 += NW * U) {
+    i32x4 w[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int c = c0 + wave + u * NW;
+      if (c < C) w[u] = __builtin_nontemporal_load(Wp + (size_t)c * 64);
+      else w[u] = i32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int c = c0 + wave + u * NW;
+      if (c < C) {
+        const i32x4 xv = *reinterpret_cast<const i32x4 *>(xq + (size_t)c * 16);
+        acc = __builtin_amdgcn_sdot4(w[u].x, xv.x, acc, false);
+        acc = __builtin_amdgcn_sdot4(w[u].y, xv.y, acc, false);
+        acc = __builtin_amdgcn_sdot4(w[u].z, xv.z, acc, false);
+        acc = __builtin_amdgcn_sdot4(w[u].w, xv.w, acc, false);
+      }
+    }
+  }
+  redi[wave * 64 + lane] = acc;
+  __syncthreads();
+  if (wave == 0) {
+    int s = 0;
+#pragma unroll
+    for (int i = 0; i < NW; i++) s += redi[i * 64 + lane];
+    const int row = panel * 64 + lane;
+    Top2v t{-__builtin_inff(), -1, -__builtin_inff()};
+    if (row < N) {
+      const float f = (float)s * sx[0];
+      const float v = f * ws[row];
+      logits[row] = v;
+      t = Top2v{v, row, -__builtin_inff()};
+    }
+    t = wave_top2(t);
+    if (lane == 0) {
+      pv[panel] = t.v1;
+      pi[panel] = t.i1;
+      pv2[panel] = t.v2;
+    }
+  }
+}
+
+syn_status_t launch_lmhead_top2(const void *W, const float *ws, int N, int C, const int8_t *xq,
+                                const float *sx, float *logits, float *pv, int *pi, float *pv2,
+                                hipStream_t s) {
+  const int P = (int)cdiv((size_t)N, 64);
+  hipLaunchKernelGGL((k_lmhead_top2<8, 8>), dim3(P), dim3(512), 0, s,
+                     reinterpret_cast<const i32x4 *>(W), ws, N, C, xq, sx, logits, pv, pi, pv2);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
+
+__global__ void __launch_bounds__(1024)
+    k_argmax_advance(const float *__restrict__ pv, const int *__restrict__ pi,
+                     const float *__restrict__ pv2, int np, StepState *st,
+                     uint32_t *__restrict__ history, float *__restrict__ mhist) {
+  __shared__ float s1[16], s2[16];
+  __shared__ int si[16];
+  Top2v t{-__builtin_inff(), -1, -__builtin_inff()};
+  for (int i = threadIdx.x; i < np; i += 1024) t = top2v_merge(t, Top2v{pv[i], pi[i], pv2[i]});
+  t = wave_top2(t);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    s1[w] = t.v1;
+    si[w] = t.i1;
+    s2[w] = t.v2;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    Top2v r{s1[0], si[0], s2[0]};
+    for (int i = 1; i < 16; i++) r = top2v_merge(r, Top2v{s1[i], si[i], s2[i]});
+    const uint32_t tok = r.i1 < 0 ? 0u : (uint32_t)r.i1;
+    const float margin = r.v1 - r.v2;
+    const int step = st->step;
+    st->token = tok;
+    st->margin = margin;
+    if (history) history[step] = tok;
+    if (mhist) mhist[step] = margin;
+    st->pos += 1;
+    st->step = step + 1;
+  }
+}
+
+syn_status_t launch_argmax_advance(const float *pv, const int *pi, const float *pv2, int np,
+                                   StepState *st, uint32_t *history, float *mhist,
+                                   hipStream_t s) {
+  hipLaunchKernelGGL(k_argmax_advance, dim3(1), dim3(1024), 0, s, pv, pi, pv2, np, st, history,
+                     mhist);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
+
+}  // namespace syn
+
+#ifdef SYN_PHASE_TIMING
+extern "C" syn_status_t syn_hip_debug_phase_ts(unsigned long long *host, int n) {
+  if (!host || n <= 0 || n > 256) return SYN_ERR_INVALID_ARG;
+  SYN_HIP(hipDeviceSynchronize());
+  SYN_HIP(hipMemcpyFromSymbol(host, HIP_SYMBOL(syn::syn_phase_ts), (size_t)n * 8, 0,
+                              hipMemcpyDeviceToHost));
+  return SYN_OK;
+}
+#endif

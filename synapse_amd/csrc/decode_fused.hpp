@@ -1,0 +1,72 @@
+// Fused INT8 W8A8 decode step (batch 1): five kernels per decoder layer
+// instead of one per reference op.  See decode_fused.hip for the kernels.
+#pragma once
+
+#include "layer_ops.hpp"
+
+namespace syn {
+
+// The rows of a split-K INT8 GEMV as a consumer sees them:
+//   value(r) = (f32(acc[r]) * sx[0]) * ws[r]
+// (the M <= 16 epilogue of int8GemvRow, qmatmul.zig:171-256), where acc is
+// the exact int32 dot product, accumulated over the K split with atomics.
+struct RowSrc {
+  const int *acc = nullptr;
+  const float *sx = nullptr;
+  const float *ws = nullptr;
+};
+
+// One INT8 linear in the panel layout, with the K split used in the step.
+struct SplitGemv {
+  const void *W = nullptr;   // panel layout (linear.hpp)
+  const float *ws = nullptr; // per-row scales [N64]
+  int N = 0, N64 = 0, C = 0; // rows, padded rows, 16-byte K chunks
+  int ks = 1, cs = 0;        // K split, chunks per split
+  int nt = 256;              // threads per workgroup
+  int u = 1;                 // chunks per wave (prefetched at kernel entry)
+  int *acc = nullptr;        // int32 accumulators [N64], zero before the step
+  RowSrc rows(const float *sx) const { return RowSrc{acc, sx, ws}; }
+};
+
+// Choose the K split so that about `target_wg` workgroups stream the matrix
+// and every wave holds at most 8 chunks (128 bytes per lane) in flight.
+SplitGemv plan_split_gemv(const void *W, const float *ws, int N, int C, int target_wg, int nt);
+
+// x = (base ? base : embed[state->token] or zero_row) + delta ; res_out = x
+// (workgroup 0); xq = q8(rmsnorm(x, nw, eps)); s_out = its scale (workgroup
+// 0); acc += xq . W over this split of K
+syn_status_t launch_fused_norm_gemv(const float *base, const float *embed, const StepState *st,
+                                    int vocab, const float *zero_row, RowSrc delta,
+                                    float *res_out, const float *nw, float eps, int H,
+                                    float *s_out, const SplitGemv &g, hipStream_t s);
+// xq = q8(vec) ; s_out ; acc += xq . W
+syn_status_t launch_fused_quant_gemv(const float *vec, int H, float *s_out, const SplitGemv &g,
+                                     hipStream_t s);
+// h = silu(gate) * up from the stacked [gate | up] rows ; xq = q8(h) ; acc += xq . W
+syn_status_t launch_fused_swiglu_gemv(RowSrc gu, int inter, float *s_out, const SplitGemv &g,
+                                      hipStream_t s);
+// per query head: q/k/v rows from the QKV partials, head RMSNorm, RoPE at
+// state->pos, KV append, attention over positions [0, pos]
+syn_status_t launch_fused_attention(RowSrc qkv, int nh, int nkv, int hd, const float *qn,
+                                    const float *kn, float eps, const float *cosT,
+                                    const float *sinT, const StepState *st, float *kc, float *vc,
+                                    int max_seq, float *out, hipStream_t s);
+bool fused_attention_fits(int hd, int max_seq);
+// the fused GEMV prologue holds its activation row (f32 twice + int8) in LDS
+bool fused_gemv_fits(int H);
+// final residual + RMSNorm + quantize into global xq / s_out (one workgroup)
+syn_status_t launch_fused_final_norm(const float *base, RowSrc delta, const float *nw, float eps,
+                                     int H, int8_t *xq, float *s_out, hipStream_t s);
+// lm_head GEMV (one workgroup per 64-row panel) -> logits + per-panel top-2
+syn_status_t launch_lmhead_top2(const void *W, const float *ws, int N, int C, const int8_t *xq,
+                                const float *sx, float *logits, float *pv, int *pi, float *pv2,
+                                hipStream_t s);
+// zero n int32 (the step's split-K accumulators; a kernel, not a memset
+// node, so the step can be captured in a graph)
+syn_status_t launch_zero_i32(int *p, size_t n, hipStream_t s);
+// merge the per-panel top-2 -> token, margin, history; pos += 1, step += 1
+syn_status_t launch_argmax_advance(const float *pv, const int *pi, const float *pv2, int np,
+                                   StepState *st, uint32_t *history, float *mhist,
+                                   hipStream_t s);
+
+}  // namespace syn

@@ -36,8 +36,11 @@ struct syn_hip_klm_s {
     if (graph) (void)hipGraphExecDestroy(graph);
     if (stream) (void)hipStreamDestroy(stream);
   }
-  float *kc_l(size_t l) { return kc.as<float>() + l * S * kvd; }
-  float *vc_l(size_t l) { return vc.as<float>() + l * S * kvd; }
+  // per-layer KV caches in the decode attention's tiled layout (layer_ops.hpp)
+  size_t k_elems() const { return kv_k_elems((int)(kvd / hd), (int)hd, (int)S); }
+  size_t v_elems() const { return kv_v_elems((int)(kvd / hd), (int)hd, (int)S); }
+  float *kc_l(size_t l) { return kc.as<float>() + l * k_elems(); }
+  float *vc_l(size_t l) { return vc.as<float>() + l * v_elems(); }
   StepState *st() { return state.as<StepState>(); }
   int fmt_of(int proj) const {
     if (proj <= 2) return c.fmt_qkv;
@@ -64,8 +67,8 @@ struct syn_hip_klm_s {
     SYN_TRY(ones_hd.alloc(hd * 4));
     SYN_TRY(rope_cos.alloc(S * (hd / 2) * 4));
     SYN_TRY(rope_sin.alloc(S * (hd / 2) * 4));
-    SYN_TRY(kc.alloc(L * S * kvd * 4));
-    SYN_TRY(vc.alloc(L * S * kvd * 4));
+    SYN_TRY(kc.alloc(L * k_elems() * 4));
+    SYN_TRY(vc.alloc(L * v_elems() * 4));
     SYN_TRY(x.alloc(T * h * 4));
     SYN_TRY(normed.alloc(T * h * 4));
     SYN_TRY(qkv.alloc(T * n_qkv * 4));
@@ -131,10 +134,10 @@ struct syn_hip_klm_s {
     SYN_TRY(launch_qk_norm_rope_kv(qkv.as<float>(), (int)n_qkv, rows, nh, nkv, (int)hd, qn, qn,
                                    eps, rope_cos.as<float>(), rope_sin.as<float>(),
                                    prefill ? nullptr : &st()->pos, 0, qrot.as<float>(), kc_l(l),
-                                   vc_l(l), s));
+                                   vc_l(l), (int)S, s));
     if (prefill)
       SYN_TRY(launch_attention_prefill(qrot.as<float>(), kc_l(l), vc_l(l), rows, nh, nkv,
-                                       (int)hd, nullptr, attn.as<float>(), s));
+                                       (int)hd, (int)S, nullptr, attn.as<float>(), s));
     else
       SYN_TRY(launch_attention_decode(qrot.as<float>(), kc_l(l), vc_l(l), &st()->pos, nh, nkv,
                                       (int)hd, scores.as<float>(), (int)S, attn.as<float>(), s));

@@ -150,7 +150,7 @@ __global__ void __launch_bounds__(64)
                       const float *__restrict__ qn, const float *__restrict__ kn, float eps,
                       const float *__restrict__ cosT, const float *__restrict__ sinT,
                       const int *__restrict__ d_pos, int pos_static, float *__restrict__ q_out,
-                      float *__restrict__ kc, float *__restrict__ vc) {
+                      float *__restrict__ kc, float *__restrict__ vc, int max_seq) {
   extern __shared__ float v[];  // hd
   __shared__ float red[8];
   __shared__ float s_scale;
@@ -161,7 +161,7 @@ __global__ void __launch_bounds__(64)
   if (hh >= nh + nkv) {  // V head: raw copy into the cache
     const int vh = hh - nh - nkv;
     for (int d = threadIdx.x; d < hd; d += 64)
-      vc[(size_t)pos * kvd + vh * hd + d] = row[qd + kvd + vh * hd + d];
+      vc[kv_v_index(pos, vh, d, hd, max_seq)] = row[qd + kvd + vh * hd + d];
     return;
   }
   const bool is_q = hh < nh;
@@ -181,14 +181,20 @@ __global__ void __launch_bounds__(64)
     __syncthreads();
   }
   const float *cr = cosT + (size_t)pos * half, *sr = sinT + (size_t)pos * half;
-  float *dst = is_q ? q_out + (size_t)r * qd + hh * hd : kc + (size_t)pos * kvd + (hh - nh) * hd;
+  const int kh = hh - nh;
   for (int i = threadIdx.x; i < half; i += 64) {
     const float c = cr[i], sn = sr[i];
     const float x1 = v[i], x2 = v[half + i];
     const float a = x1 * c, b = x2 * sn;
     const float e = x2 * c, f = x1 * sn;
-    dst[i] = a - b;
-    dst[half + i] = e + f;
+    if (is_q) {
+      float *dst = q_out + (size_t)r * qd + hh * hd;
+      dst[i] = a - b;
+      dst[half + i] = e + f;
+    } else {
+      kc[kv_k_index(pos, kh, i, hd, max_seq)] = a - b;
+      kc[kv_k_index(pos, kh, half + i, hd, max_seq)] = e + f;
+    }
   }
 }
 
@@ -196,10 +202,12 @@ syn_status_t launch_qk_norm_rope_kv(const float *qkv, int ldqkv, int rows, int n
                                     int n_kv, int head_dim, const float *q_norm,
                                     const float *k_norm, float eps, const float *rope_cos,
                                     const float *rope_sin, const int *d_pos, int pos_static,
-                                    float *q_out, float *kcache, float *vcache, hipStream_t s) {
+                                    float *q_out, float *kcache, float *vcache, int max_seq,
+                                    hipStream_t s) {
   hipLaunchKernelGGL(k_qk_norm_rope_kv, dim3(n_heads + 2 * n_kv, rows), dim3(64),
                      head_dim * sizeof(float), s, qkv, ldqkv, n_heads, n_kv, head_dim, q_norm,
-                     k_norm, eps, rope_cos, rope_sin, d_pos, pos_static, q_out, kcache, vcache);
+                     k_norm, eps, rope_cos, rope_sin, d_pos, pos_static, q_out, kcache, vcache,
+                     max_seq);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
 }
@@ -229,13 +237,13 @@ __global__ void __launch_bounds__(256)
   const int n8 = n32 + ((len - n32) / 8) * 8;
   float mx = -__builtin_inff();
   for (int sidx = threadIdx.x; sidx < len; sidx += blockDim.x) {
-    const float *kr = kc + (size_t)sidx * kvd + kvh * hd;
     float acc = 0.0f;
     if (simd && sidx < n8) {
-      for (int d = 0; d < hd; d++) acc = __builtin_fmaf(qs[d], kr[d], acc);
+      for (int d = 0; d < hd; d++)
+        acc = __builtin_fmaf(qs[d], kc[kv_k_index(sidx, kvh, d, hd, max_seq)], acc);
     } else {
       for (int d = 0; d < hd; d++) {
-        const float t = qs[d] * kr[d];
+        const float t = qs[d] * kc[kv_k_index(sidx, kvh, d, hd, max_seq)];
         acc = acc + t;
       }
     }
@@ -263,13 +271,13 @@ __global__ void __launch_bounds__(256)
   __syncthreads();
   const int d32 = hd - hd % 32;
   for (int d = threadIdx.x; d < hd; d += blockDim.x) {
-    const float *vcol = vc + kvh * hd + d;
     float acc = 0.0f;
     if (simd && d < d32) {
-      for (int i = 0; i < len; i++) acc = __builtin_fmaf(e[i], vcol[(size_t)i * kvd], acc);
+      for (int i = 0; i < len; i++)
+        acc = __builtin_fmaf(e[i], vc[kv_v_index(i, kvh, d, hd, max_seq)], acc);
     } else {
       for (int i = 0; i < len; i++) {
-        const float t = e[i] * vcol[(size_t)i * kvd];
+        const float t = e[i] * vc[kv_v_index(i, kvh, d, hd, max_seq)];
         acc = acc + t;
       }
     }
@@ -312,7 +320,7 @@ __device__ __forceinline__ bool sgemm_fused(int tqs, int il, int ncols, int j, b
 
 __global__ void __launch_bounds__(256)
     k_attn_prefill(const float *__restrict__ q, const float *__restrict__ kc,
-                   const float *__restrict__ vc, int t, int nh, int nkv, int hd,
+                   const float *__restrict__ vc, int t, int nh, int nkv, int hd, int max_seq,
                    float *__restrict__ out) {
   extern __shared__ float sm[];  // qs[hd] | e[t]
   float *qs = sm, *e = sm + hd;
@@ -325,13 +333,13 @@ __global__ void __launch_bounds__(256)
   __syncthreads();
   const float scale = 1.0f / sqrtf((float)hd);
   for (int j = threadIdx.x; j < t; j += blockDim.x) {
-    const float *kr = kc + (size_t)j * kvd + kvh * hd;
     float acc = 0.0f;
     if (sgemm_fused(tqs, il, t, j, true)) {
-      for (int d = 0; d < hd; d++) acc = __builtin_fmaf(qs[d], kr[d], acc);
+      for (int d = 0; d < hd; d++)
+        acc = __builtin_fmaf(qs[d], kc[kv_k_index(j, kvh, d, hd, max_seq)], acc);
     } else {
       for (int d = 0; d < hd; d++) {
-        const float p = qs[d] * kr[d];
+        const float p = qs[d] * kc[kv_k_index(j, kvh, d, hd, max_seq)];
         acc = acc + p;
       }
     }
@@ -360,13 +368,13 @@ __global__ void __launch_bounds__(256)
   for (int j = threadIdx.x; j < t; j += blockDim.x) e[j] = syn_expf(e[j] - mx) * inv;
   __syncthreads();
   for (int d = threadIdx.x; d < hd; d += blockDim.x) {
-    const float *vcol = vc + kvh * hd + d;
     float acc = 0.0f;
     if (sgemm_fused(tqs, il, hd, d, false)) {
-      for (int p = 0; p < t; p++) acc = __builtin_fmaf(e[p], vcol[(size_t)p * kvd], acc);
+      for (int p = 0; p < t; p++)
+        acc = __builtin_fmaf(e[p], vc[kv_v_index(p, kvh, d, hd, max_seq)], acc);
     } else {
       for (int p = 0; p < t; p++) {
-        const float m = e[p] * vcol[(size_t)p * kvd];
+        const float m = e[p] * vc[kv_v_index(p, kvh, d, hd, max_seq)];
         acc = acc + m;
       }
     }
@@ -375,7 +383,7 @@ __global__ void __launch_bounds__(256)
 }
 
 syn_status_t launch_attention_prefill(const float *q, const float *kcache, const float *vcache,
-                                      int t, int n_heads, int n_kv, int head_dim,
+                                      int t, int n_heads, int n_kv, int head_dim, int max_seq,
                                       float *scores, float *out, hipStream_t s) {
   (void)scores;
   const size_t shm = (size_t)(head_dim + t) * sizeof(float);
@@ -384,7 +392,7 @@ syn_status_t launch_attention_prefill(const float *q, const float *kcache, const
     return SYN_ERR_INVALID_ARG;
   }
   hipLaunchKernelGGL(k_attn_prefill, dim3(n_heads, t), dim3(256), shm, s, q, kcache, vcache, t,
-                     n_heads, n_kv, head_dim, out);
+                     n_heads, n_kv, head_dim, max_seq, out);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
 }

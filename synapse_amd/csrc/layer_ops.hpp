@@ -7,6 +7,28 @@
 
 namespace syn {
 
+// KV cache layout (per layer), laid out for the decode attention's loads:
+//  K: [kv_head][position tile of 64][d/4][64 positions][4 d]  - a wave whose
+//     lanes are positions reads 1 KiB contiguously per 16-byte load;
+//  V: [kv_head][position/4][d][4 positions]                   - a wave whose
+//     lanes are output columns d reads 4 positions per 16-byte load.
+// head_dim is padded to a multiple of 4 in K (the pad is never read as data)
+// and max_seq to multiples of 64 (K) and 4 (V).
+__host__ __device__ __forceinline__ size_t kv_k_index(int p, int g, int d, int hd, int max_seq) {
+  const int hd4 = (hd + 3) >> 2, tiles = (max_seq + 63) >> 6;
+  return ((((size_t)g * tiles + (p >> 6)) * hd4 + (d >> 2)) * 64 + (p & 63)) * 4 + (d & 3);
+}
+__host__ __device__ __forceinline__ size_t kv_v_index(int p, int g, int d, int hd, int max_seq) {
+  const int s4 = (max_seq + 3) >> 2;
+  return (((size_t)g * s4 + (p >> 2)) * hd + d) * 4 + (p & 3);
+}
+inline size_t kv_k_elems(int nkv, int hd, int max_seq) {
+  return (size_t)nkv * ((max_seq + 63) / 64) * 64 * (((hd + 3) / 4) * 4);
+}
+inline size_t kv_v_elems(int nkv, int hd, int max_seq) {
+  return (size_t)nkv * ((max_seq + 3) / 4) * 4 * hd;
+}
+
 struct StepState {  // device-resident decode state (read by kernels in a graph)
   int pos;          // tokens already in the KV cache
   uint32_t token;   // last sampled token
@@ -28,7 +50,8 @@ syn_status_t launch_qk_norm_rope_kv(const float *qkv, int ldqkv, int rows, int n
                                     int n_kv, int head_dim, const float *q_norm,
                                     const float *k_norm, float eps, const float *rope_cos,
                                     const float *rope_sin, const int *d_pos, int pos_static,
-                                    float *q_out, float *kcache, float *vcache, hipStream_t s);
+                                    float *q_out, float *kcache, float *vcache, int max_seq,
+                                    hipStream_t s);
 // single-query GQA attention over positions [0, *d_pos] (cache already holds
 // the new token), ops/attention.rs:24-147
 syn_status_t launch_attention_decode(const float *q, const float *kcache, const float *vcache,
@@ -36,7 +59,7 @@ syn_status_t launch_attention_decode(const float *q, const float *kcache, const 
                                      float *scores, int max_seq, float *out, hipStream_t s);
 // causal attention over `t` prompt tokens, exports.zig:1364-1478 per head
 syn_status_t launch_attention_prefill(const float *q, const float *kcache, const float *vcache,
-                                      int t, int n_heads, int n_kv, int head_dim,
+                                      int t, int n_heads, int n_kv, int head_dim, int max_seq,
                                       float *scores, float *out, hipStream_t s);
 // h = silu(gate) * up (int8.rs:500-503), then quantize rows of h
 syn_status_t launch_swiglu_quant(const float *gu, int ldgu, int rows, int inter, int8_t *hq,

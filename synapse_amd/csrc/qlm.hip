@@ -19,6 +19,7 @@
 #include <thread>
 #include <vector>
 
+#include "decode_fused.hpp"
 #include "layer_ops.hpp"
 #include "linear.hpp"
 
@@ -26,6 +27,7 @@ namespace syn {
 
 struct QLayer {
   QLinearInt8 qkv, o, gu, down;
+  SplitGemv f_qkv, f_o, f_gu, f_down;  // fused decode plans over these weights
 };
 
 }  // namespace syn
@@ -40,29 +42,40 @@ struct syn_hip_qlm_s {
   std::vector<int> have_layer;
   QLinearInt8 lm_head;
   std::vector<float> host_embed;
-  DevBuf embed, ones_h, ones_hd, rope_cos, rope_sin, kc, vc;
+  DevBuf embed, ones_h, ones_hd, zeros_h, rope_cos, rope_sin, kc, vc;
   DevBuf x, xq, sx, qkv, qrot, attn, aq, sa, o, gu, hq, sh, down, logits, scores;
   DevBuf pv, pi, pv2, state, history, mhist, ids;
+  // fused decode step (decode_fused.hip): residual rows, activation scales
+  // [qkv, o, gate|up, down, lm_head] and the split-K accumulators
+  DevBuf xin, xmid, scal, acc;
+  size_t acc_elems = 0;
   hipStream_t stream = nullptr;
   hipGraphExec_t graph = nullptr;
   bool finalized = false;
+  bool fused = true;      // fused five-kernel decode layer (else one kernel per op)
+  bool use_graph = true;  // replay the decode step as a HIP graph (else launch eagerly)
 
   ~syn_hip_qlm_s() {
     if (graph) (void)hipGraphExecDestroy(graph);
     if (stream) (void)hipStreamDestroy(stream);
   }
-  float *kc_l(size_t l) { return kc.as<float>() + l * S * kvd; }
-  float *vc_l(size_t l) { return vc.as<float>() + l * S * kvd; }
+  // per-layer KV caches in the decode attention's tiled layout (layer_ops.hpp)
+  size_t k_elems() const { return kv_k_elems((int)(kvd / hd), (int)hd, (int)S); }
+  size_t v_elems() const { return kv_v_elems((int)(kvd / hd), (int)hd, (int)S); }
+  float *kc_l(size_t l) { return kc.as<float>() + l * k_elems(); }
+  float *vc_l(size_t l) { return vc.as<float>() + l * v_elems(); }
   StepState *st() { return state.as<StepState>(); }
 
   syn_status_t alloc_all() {
     const size_t T = S;  // prefill rows
     SYN_TRY(ones_h.alloc(h * 4));
     SYN_TRY(ones_hd.alloc(hd * 4));
+    SYN_TRY(zeros_h.alloc(h * 4));
+    SYN_HIP(hipMemset(zeros_h.p, 0, h * 4));
     SYN_TRY(rope_cos.alloc(S * (hd / 2) * 4));
     SYN_TRY(rope_sin.alloc(S * (hd / 2) * 4));
-    SYN_TRY(kc.alloc(L * S * kvd * 4));
-    SYN_TRY(vc.alloc(L * S * kvd * 4));
+    SYN_TRY(kc.alloc(L * k_elems() * 4));
+    SYN_TRY(vc.alloc(L * v_elems() * 4));
     SYN_TRY(x.alloc(T * h * 4));
     SYN_TRY(xq.alloc(T * ldh));
     SYN_TRY(sx.alloc(T * 4));
@@ -78,9 +91,13 @@ struct syn_hip_qlm_s {
     SYN_TRY(down.alloc(T * h * 4));
     SYN_TRY(logits.alloc(vocab * 4));
     SYN_TRY(scores.alloc(c.n_heads * S * 4));
-    SYN_TRY(pv.alloc(256 * 4));
-    SYN_TRY(pi.alloc(256 * 4));
-    SYN_TRY(pv2.alloc(256 * 4));
+    const size_t np = std::max<size_t>(256, cdiv(vocab, 64));
+    SYN_TRY(pv.alloc(np * 4));
+    SYN_TRY(pi.alloc(np * 4));
+    SYN_TRY(pv2.alloc(np * 4));
+    SYN_TRY(xin.alloc(h * 4));
+    SYN_TRY(xmid.alloc(h * 4));
+    SYN_TRY(scal.alloc(64));
     SYN_TRY(state.alloc(sizeof(StepState)));
     SYN_TRY(history.alloc((S + 1) * 4));
     SYN_TRY(mhist.alloc((S + 1) * 4));
@@ -142,10 +159,10 @@ struct syn_hip_qlm_s {
                                    ones_hd.as<float>(), ones_hd.as<float>(), eps,
                                    rope_cos.as<float>(), rope_sin.as<float>(),
                                    prefill ? nullptr : &st()->pos, 0, qrot.as<float>(), kc_l(l),
-                                   vc_l(l), s));
+                                   vc_l(l), (int)S, s));
     if (prefill)
       SYN_TRY(launch_attention_prefill(qrot.as<float>(), kc_l(l), vc_l(l), rows, nh, nkv,
-                                       (int)hd, nullptr, attn.as<float>(), s));
+                                       (int)hd, (int)S, nullptr, attn.as<float>(), s));
     else
       SYN_TRY(launch_attention_decode(qrot.as<float>(), kc_l(l), vc_l(l), &st()->pos, nh, nkv,
                                       (int)hd, scores.as<float>(), (int)S, attn.as<float>(), s));
@@ -174,9 +191,104 @@ struct syn_hip_qlm_s {
   }
 
   syn_status_t decode_step(hipStream_t s) {
+    if (fused) return decode_step_fused(s);
     SYN_TRY(launch_embed(embed.as<float>(), &st()->token, 1, (int)h, (int)vocab, x.as<float>(), s));
     for (size_t l = 0; l < L; l++) SYN_TRY(layer(l, 1, false, s));
     return head(0, 1, s);
+  }
+
+  // Split-K plans for the fused step (one per layer: the weights differ, the
+  // shapes do not) and their int32 accumulators, one set per layer so that a
+  // single zeroing kernel at the start of the step resets all of them.
+  syn_status_t prepare_fused() {
+    int cus = 256;
+    int dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess)
+      (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    size_t per_layer = 0;
+    for (auto &Ly : layers) {
+      Ly.f_qkv = plan_split_gemv(Ly.qkv.w.p, Ly.qkv.scales.as<float>(), (int)n_qkv,
+                                 Ly.qkv.chunks, cus, 256);
+      Ly.f_o = plan_split_gemv(Ly.o.w.p, Ly.o.scales.as<float>(), (int)h, Ly.o.chunks, cus, 256);
+      Ly.f_gu = plan_split_gemv(Ly.gu.w.p, Ly.gu.scales.as<float>(), (int)(2 * inter),
+                                Ly.gu.chunks, cus, 256);
+      Ly.f_down = plan_split_gemv(Ly.down.w.p, Ly.down.scales.as<float>(), (int)h,
+                                  Ly.down.chunks, cus, 512);
+      per_layer = (size_t)Ly.f_qkv.N64 + Ly.f_o.N64 + Ly.f_gu.N64 + Ly.f_down.N64;
+    }
+    acc_elems = per_layer * L;
+    SYN_TRY(acc.alloc(acc_elems * 4));
+    int *p = acc.as<int>();
+    for (auto &Ly : layers) {
+      SplitGemv *g[4] = {&Ly.f_qkv, &Ly.f_o, &Ly.f_gu, &Ly.f_down};
+      for (int i = 0; i < 4; i++) {
+        g[i]->acc = p;
+        p += g[i]->N64;
+      }
+    }
+    return SYN_OK;
+  }
+
+  bool fused_supported() const {
+    return fused_attention_fits((int)hd, (int)S) && fused_gemv_fits((int)h) &&
+           fused_gemv_fits((int)qd) && fused_gemv_fits((int)inter);
+  }
+
+  // one decode token in 5 kernels per layer + 3 (decode_fused.hip)
+  syn_status_t decode_step_fused(hipStream_t s) {
+    float *sc = scal.as<float>();
+    float *s_qkv = sc + 0, *s_o = sc + 1, *s_gu = sc + 2, *s_down = sc + 3, *s_head = sc + 4;
+    const float eps = c.eps;
+    const int nh = (int)c.n_heads, nkv = (int)c.n_kv_heads;
+    SYN_TRY(launch_zero_i32(acc.as<int>(), acc_elems, s));
+    for (size_t l = 0; l < L; l++) {
+      QLayer &Ly = layers[l];
+      const RowSrc prev = l == 0 ? RowSrc{} : layers[l - 1].f_down.rows(s_down);
+      SYN_TRY(launch_fused_norm_gemv(l == 0 ? nullptr : xmid.as<float>(), embed.as<float>(),
+                                     st(), (int)vocab, zeros_h.as<float>(), prev, xin.as<float>(), ones_h.as<float>(),
+                                     eps, (int)h, s_qkv, Ly.f_qkv, s));
+      SYN_TRY(launch_fused_attention(Ly.f_qkv.rows(s_qkv), nh, nkv, (int)hd, ones_hd.as<float>(),
+                                     ones_hd.as<float>(), eps, rope_cos.as<float>(),
+                                     rope_sin.as<float>(), st(), kc_l(l), vc_l(l), (int)S,
+                                     attn.as<float>(), s));
+      SYN_TRY(launch_fused_quant_gemv(attn.as<float>(), (int)qd, s_o, Ly.f_o, s));
+      SYN_TRY(launch_fused_norm_gemv(xin.as<float>(), nullptr, st(), (int)vocab, nullptr,
+                                     Ly.f_o.rows(s_o), xmid.as<float>(), ones_h.as<float>(), eps,
+                                     (int)h, s_gu, Ly.f_gu, s));
+      SYN_TRY(launch_fused_swiglu_gemv(Ly.f_gu.rows(s_gu), (int)inter, s_down, Ly.f_down, s));
+    }
+    SYN_TRY(launch_fused_final_norm(xmid.as<float>(), layers[L - 1].f_down.rows(s_down),
+                                    ones_h.as<float>(), eps, (int)h, xq.as<int8_t>(), s_head, s));
+    SYN_TRY(launch_lmhead_top2(lm_head.w.p, lm_head.scales.as<float>(), (int)vocab,
+                               lm_head.chunks, xq.as<int8_t>(), s_head, logits.as<float>(),
+                               pv.as<float>(), pi.as<int>(), pv2.as<float>(), s));
+    return launch_argmax_advance(pv.as<float>(), pi.as<int>(), pv2.as<float>(),
+                                 (int)cdiv(vocab, 64), st(), history.as<uint32_t>(),
+                                 mhist.as<float>(), s);
+  }
+
+  // one decode step on the model stream: graph replay or eager launches
+  syn_status_t run_step() {
+    if (!use_graph) return decode_step(stream);
+    SYN_TRY(build_graph());
+    SYN_HIP(hipGraphLaunch(graph, stream));
+    return SYN_OK;
+  }
+
+  syn_status_t set_options(int fused_decode, int graph_replay) {
+    const bool f = fused_decode != 0 && fused_supported();
+    if (fused_decode && !f) {
+      set_error("fused decode: shape outside the fused kernels' LDS limits");
+      return SYN_ERR_INVALID_ARG;
+    }
+    if (f != fused && graph) {
+      SYN_HIP(hipStreamSynchronize(stream));
+      (void)hipGraphExecDestroy(graph);
+      graph = nullptr;
+    }
+    fused = f;
+    use_graph = graph_replay != 0;
+    return SYN_OK;
   }
 
   syn_status_t build_graph() {
@@ -353,6 +465,8 @@ syn_status_t syn_hip_qlm_finalize(syn_hip_qlm_t *m) {
     SYN_TRY(Ly.down.prepare(m->S));
   }
   SYN_TRY(m->lm_head.prepare(1));
+  SYN_TRY(m->prepare_fused());
+  m->fused = m->fused_supported();
   m->finalized = true;
   SYN_TRY(m->set_state(0, 0, 0));
   SYN_HIP(hipStreamSynchronize(m->stream));
@@ -386,9 +500,9 @@ syn_status_t syn_hip_qlm_forward_one(syn_hip_qlm_t *m, uint32_t token, float *ho
     set_error("KV cache full");  // kvcache.zig:68-69 CacheFull
     return SYN_ERR_INVALID_ARG;
   }
-  SYN_TRY(m->build_graph());
+  if (m->use_graph) SYN_TRY(m->build_graph());
   SYN_TRY(m->set_state(cur.pos, token, cur.step));
-  SYN_HIP(hipGraphLaunch(m->graph, m->stream));
+  SYN_TRY(m->run_step());
   if (host_logits)
     SYN_HIP(hipMemcpyAsync(host_logits, m->logits.p, m->vocab * 4, hipMemcpyDeviceToHost,
                            m->stream));
@@ -405,9 +519,9 @@ syn_status_t syn_hip_qlm_generate(syn_hip_qlm_t *m, const uint32_t *prompt, size
     set_error("prompt + generated tokens exceed max_seq");
     return SYN_ERR_INVALID_ARG;
   }
-  SYN_TRY(m->build_graph());
+  if (m->use_graph) SYN_TRY(m->build_graph());
   SYN_TRY(m->prefill(prompt, n_prompt));
-  for (size_t i = 1; i < max_new; i++) SYN_HIP(hipGraphLaunch(m->graph, m->stream));
+  for (size_t i = 1; i < max_new; i++) SYN_TRY(m->run_step());
   SYN_HIP(hipMemcpyAsync(out_tokens, m->history.p, max_new * 4, hipMemcpyDeviceToHost,
                          m->stream));
   if (out_margins)
@@ -426,12 +540,12 @@ syn_status_t syn_hip_qlm_decode_timed(syn_hip_qlm_t *m, size_t steps, float *ela
     set_error("decode steps exceed max_seq");
     return SYN_ERR_INVALID_ARG;
   }
-  SYN_TRY(m->build_graph());
+  if (m->use_graph) SYN_TRY(m->build_graph());
   hipEvent_t a, b;
   SYN_HIP(hipEventCreate(&a));
   SYN_HIP(hipEventCreate(&b));
   SYN_HIP(hipEventRecord(a, m->stream));
-  for (size_t i = 0; i < steps; i++) SYN_HIP(hipGraphLaunch(m->graph, m->stream));
+  for (size_t i = 0; i < steps; i++) SYN_TRY(m->run_step());
   SYN_HIP(hipEventRecord(b, m->stream));
   SYN_HIP(hipEventSynchronize(b));
   SYN_HIP(hipEventElapsedTime(elapsed_ms, a, b));
@@ -468,6 +582,11 @@ syn_status_t syn_hip_qlm_time_lm_head(syn_hip_qlm_t *m, size_t iters, size_t flu
   SYN_TRY(st);
   *avg_ms = (float)(total / (double)iters);
   return SYN_OK;
+}
+
+syn_status_t syn_hip_qlm_set_options(syn_hip_qlm_t *m, int fused_decode, int graph_replay) {
+  SYN_TRY(check_model(m));
+  return m->set_options(fused_decode, graph_replay);
 }
 
 syn_status_t syn_hip_qlm_destroy(syn_hip_qlm_t *m) {

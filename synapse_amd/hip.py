@@ -89,6 +89,7 @@ SIGNATURES = {
     "syn_hip_qlm_generate": (ST, [P, P, SZ, SZ, P, P]),
     "syn_hip_qlm_decode_timed": (ST, [P, SZ, C.POINTER(C.c_float)]),
     "syn_hip_qlm_time_lm_head": (ST, [P, SZ, SZ, C.POINTER(C.c_float)]),
+    "syn_hip_qlm_set_options": (ST, [P, C.c_int, C.c_int]),
     "syn_hip_qlm_destroy": (ST, [P]),
     "syn_hip_klm_create": (ST, [C.POINTER(KLmConfig), C.POINTER(P)]),
     "syn_hip_klm_set_embed": (ST, [P, P]),
@@ -403,6 +404,11 @@ class QuantizedCausalLM:
         ms = C.c_float()
         check(lib().syn_hip_qlm_decode_timed(self.h, steps, C.byref(ms)), "decode_timed")
         return ms.value
+
+    def set_options(self, fused: bool = True, graph: bool = True):
+        """Decode-step form: fused five-kernel layers or one kernel per op; HIP
+        graph replay or eager launches (same results either way)."""
+        check(lib().syn_hip_qlm_set_options(self.h, int(fused), int(graph)), "set_options")
 
     def time_lm_head(self, iters: int = 20, flush_bytes: int = 512 << 20) -> float:
         ms = C.c_float()
