@@ -8,10 +8,15 @@ a 16-token random prompt, then greedy decode.  A "step" is one decode token
 (one forward_one + argmax, all on the device, replayed as a HIP graph).
 
 Prints ONE JSON line.  `value` = decode tokens/s.  `roofline` covers the
-dominant decode matvec (the tied lm_head, 151936 x 1024 INT8 GEMV) timed per
-launch with hipEvents on the model stream, with the Infinity Cache flushed
-between launches.  `cpu_baseline` = the oracle (C restatement of the
-reference cpu_simd path, single thread) decoding the same model on the host.
+dominant decode matvec (the tied lm_head, 151936 x 1024 INT8 GEMV, as the
+decode step launches it) timed per launch with hipEvents on the model
+stream, with the Infinity Cache flushed between launches.  `cpu_baseline` =
+the oracle (C restatement of the reference cpu_simd path, single thread)
+decoding the same model on the host.  `secondary` = the other BASELINE
+configurations measured on the same GPU (synapse_amd/microbench.py): the
+config-1 GEMVs one launch at a time, the config-2 Q4_0 microbench, the
+config-3 K-quant GEMVs and decoder, the config-4 Q8_0 prefill GEMMs, the
+INT8 prefill GEMM, and the config-5 Mamba decoder (--no-secondary skips it).
 """
 from __future__ import annotations
 
@@ -62,6 +67,83 @@ def prompt_ids():
     return out
 
 
+LLAMA3B = dict(hidden=3072, n_layers=28, n_heads=24, n_kv_heads=8, head_dim=128, inter=8192,
+               vocab=128256, eps=1e-5, rope_theta=5e5)
+MAMBA370M = dict(d_model=1024, d_inner=2048, d_state=16, d_conv=4, dt_rank=64, n_layers=48,
+                 vocab=50280, eps=1e-5)
+
+
+def _ids(n, vocab, seed):
+    """Uniform random ids in [0, vocab) (SplitMix64, as prompt_ids)."""
+    s, out, M = seed, [], (1 << 64) - 1
+    for _ in range(n):
+        s = (s + 0x9E3779B97F4A7C15) & M
+        z = s
+        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & M
+        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & M
+        z ^= z >> 31
+        out.append(z % vocab)
+    return out
+
+
+def kquant_weight_bytes(c):
+    """Config 3 bytes per decode token: Q4_K q,k,v,o,gate,up; Q6_K down, lm_head."""
+    h, q, kv, i, v, L = (c["hidden"], c["n_heads"] * c["head_dim"],
+                         c["n_kv_heads"] * c["head_dim"], c["inter"], c["vocab"], c["n_layers"])
+    q4k = lambda n, k: n * (k // 256) * 144
+    q6k = lambda n, k: n * (k // 256) * 210
+    layer = q4k(q, h) + 2 * q4k(kv, h) + q4k(h, q) + 2 * q4k(i, h) + q6k(h, i)
+    return L * layer + q6k(v, h)
+
+
+def secondary(hip, np):
+    """The other BASELINE configurations, measured on the same GPU."""
+    from synapse_amd import microbench as mb
+    out = {}
+    t0 = time.perf_counter()
+    out["config1_int8_gemv_qwen3"] = {
+        "note": "one launch per GEMV (the decode step fuses them), >= 1 GiB rotated",
+        "gemvs": mb.int8_suite()}
+    out["config2_q4_0_gemv_llama1b"] = {
+        "note": "batch-1 Q4_0 GEMV, f32 activations, >= 1 GiB of weight copies rotated",
+        "gemvs": mb.q4_0_suite()}
+    out["config3_kquant_gemv_llama3b"] = {
+        "note": "batch-1 Q4_K / Q6_K GEMV at the LLaMA-3.2-3B shapes, >= 1 GiB rotated",
+        "gemvs": mb.kquant_suite()}
+    # config 3 decoder: 256-token prompt, 128 greedy decode steps
+    cfg = dict(LLAMA3B, max_seq=256 + 128 + 1)
+    m = hip.KQuantCausalLM(cfg)
+    m.init_synthetic(SEED_BASE, 0.02)
+    ids = np.array(_ids(256, cfg["vocab"], PROMPT_SEED), np.uint32)
+    pf_ms, dec_ms = m.time(ids, 128)
+    m.close()
+    wb = kquant_weight_bytes(LLAMA3B)
+    out["config3_kquant_decode_llama3b"] = {
+        "prefill_256_ms": round(pf_ms, 2), "decode_tok_s": round(128e3 / dec_ms, 1),
+        "decode_ms_per_token": round(dec_ms / 128, 3), "weight_bytes_per_token": wb,
+        "decode_weight_gbs": round(wb / (dec_ms / 128 * 1e-3) / 1e9, 1)}
+    out["config4_q8_0_prefill_mistral7b"] = [mb.q8_0_prefill_suite(512),
+                                             mb.q8_0_prefill_suite(2048)]
+    out["int8_prefill_gemm"] = [mb.int8_prefill_record(128, 1024, 3072),
+                                mb.int8_prefill_record(2048, 4096, 4096)]
+    mam = {}
+    for xdt in (False, True):
+        mc = dict(MAMBA370M, max_tokens=64 + 128 + 1)
+        mm = hip.QuantizedMamba(mc, int8_xdt=xdt)
+        mm.init_synthetic(SEED_BASE, 0.02)
+        mm.prefill(np.array(_ids(64, mc["vocab"], PROMPT_SEED), np.uint32))
+        ms = mm.decode_timed(128)
+        mm.close()
+        mam["int8_x_dt_proj" if xdt else "reference_semantics"] = {
+            "decode_tok_s": round(128e3 / ms, 1), "decode_ms_per_token": round(ms / 128, 3)}
+    mam["int8_projection_gemvs"] = [
+        mb.gemv_record(hip.FMT_INT8, 4096, 1024, "in_proj 1024->4096"),
+        mb.gemv_record(hip.FMT_INT8, 1024, 2048, "out_proj 2048->1024")]
+    out["config5_mamba370m"] = mam
+    out["seconds"] = round(time.perf_counter() - t0, 1)
+    return out
+
+
 def cpu_baseline(budget_s: float):
     """Oracle decode on the host: 1 thread, same model and prompt."""
     import numpy as np
@@ -98,6 +180,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the other BASELINE configurations (configs 2-5 and GEMMs)")
     ap.add_argument("--lm-head-iters", type=int, default=20)
     ap.add_argument("--unfused", action="store_true",
                     help="one kernel per reference op instead of the fused decode layer")
@@ -160,12 +244,16 @@ def main():
         "bytes_per_token": step_bytes,
         "wall_ms_timed_region": round(wall_ms, 2),
         "model_load_s": round(load_s, 1),
-        "roofline": {"bound": "hbm", "kernel": "k_gemv_w8a8<1> lm_head 151936x1024",
+        "roofline": {"bound": "hbm",
+                     "kernel": ("k_lmhead_top2<8,8>" if not args.unfused else "k_gemv_w8a8<1>")
+                               + " lm_head 151936x1024",
                      "achieved": round(lm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "avg_launch_us": round(lm_ms * 1e3, 2),
                      "bytes_per_launch": lm_head_bytes(QWEN3)},
     }
+    if not args.no_secondary:
+        line["secondary"] = secondary(hip, np)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(line), flush=True)

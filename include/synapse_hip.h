@@ -150,6 +150,14 @@ syn_status_t syn_hip_qlinear_destroy(syn_hip_qlinear_t *h);
 syn_status_t syn_hip_qlinear_time(syn_hip_qlinear_t *h, size_t m, const float *d_x,
                                   const int8_t *d_xq, size_t ldxq, const float *d_sx, float *d_y,
                                   size_t iters, float *avg_ms);
+/* Benchmark helper: as syn_hip_qlinear_time, launching round-robin over
+ * `count` handles (copies of one matrix in distinct memory, so that a
+ * working set larger than the 256 MB Infinity Cache is streamed from HBM)
+ * for `rounds` rounds; average ms per launch. */
+syn_status_t syn_hip_qlinear_time_set(syn_hip_qlinear_t *const *hs, size_t count, size_t m,
+                                      const float *d_x, const int8_t *d_xq, size_t ldxq,
+                                      const float *d_sx, float *d_y, size_t rounds,
+                                      float *avg_ms);
 
 /* -- INT8 W8A8 causal LM: QuantizedCausalLM (quantization/lm/int8.rs),
  *    device-resident like MetalModelBuffers + gpu_forward_all_layers

@@ -467,6 +467,41 @@ syn_status_t syn_hip_qlinear_time(syn_hip_qlinear_t *h, size_t m, const float *d
   return SYN_OK;
 }
 
+syn_status_t syn_hip_qlinear_time_set(syn_hip_qlinear_t *const *hs, size_t count, size_t m,
+                                      const float *d_x, const int8_t *d_xq, size_t ldxq,
+                                      const float *d_sx, float *d_y, size_t rounds,
+                                      float *avg_ms) {
+  if (!hs || !avg_ms) return SYN_ERR_NULL_PTR;
+  if (count == 0 || rounds == 0 || m == 0) return SYN_ERR_INVALID_ARG;
+  for (size_t i = 0; i < count; i++)
+    if (!hs[i]) return SYN_ERR_NULL_PTR;
+  SYN_TRY(ensure_init());
+  hipStream_t s = default_stream();
+  auto run = [&](syn_hip_qlinear_t *h) -> syn_status_t {
+    if (h->fmt == SYN_HIP_FMT_INT8)
+      return syn_hip_qlinear_forward_pre_quantized(h, m, d_xq, ldxq, d_sx, d_y, s);
+    return syn_hip_qlinear_forward(h, m, d_x, d_y, s);
+  };
+  for (size_t i = 0; i < count; i++) SYN_TRY(run(hs[i]));  // warm-up, one-time scratch
+  SYN_HIP(hipStreamSynchronize(s));
+  hipEvent_t a, b;
+  SYN_HIP(hipEventCreate(&a));
+  SYN_HIP(hipEventCreate(&b));
+  SYN_HIP(hipEventRecord(a, s));
+  syn_status_t st = SYN_OK;
+  for (size_t r = 0; r < rounds && st == SYN_OK; r++)
+    for (size_t i = 0; i < count && st == SYN_OK; i++) st = run(hs[i]);
+  SYN_HIP(hipEventRecord(b, s));
+  SYN_HIP(hipEventSynchronize(b));
+  float ms = 0.0f;
+  SYN_HIP(hipEventElapsedTime(&ms, a, b));
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  SYN_TRY(st);
+  *avg_ms = ms / (float)(rounds * count);
+  return SYN_OK;
+}
+
 syn_status_t syn_hip_qlinear_destroy(syn_hip_qlinear_t *h) {
   delete h;
   return SYN_OK;

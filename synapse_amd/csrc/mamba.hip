@@ -27,7 +27,8 @@ __global__ void __launch_bounds__(256)
     k_mamba_norm(float *__restrict__ x, const float *__restrict__ delta,
                  const float *__restrict__ w, float eps, int H, int8_t *__restrict__ xq,
                  float *__restrict__ sx, float *__restrict__ normed) {
-  extern __shared__ float sm[];
+  extern __shared__ __align__(16) float sm[];  // H | squares[H rounded to 4]
+  float *sq = sm + ((H + 3) & ~3);
   __shared__ float red[64];
   __shared__ float s_scale;
   for (int j = threadIdx.x; j < H; j += blockDim.x) {
@@ -39,12 +40,24 @@ __global__ void __launch_bounds__(256)
     sm[j] = v;
   }
   __syncthreads();
+  // one sequential sum of the rounded squares; the squares are formed in
+  // parallel first, then lane 0 adds them in index order with 16-byte reads
+  for (int j = threadIdx.x; j < H; j += blockDim.x) sq[j] = sm[j] * sm[j];
+  __syncthreads();
   if (threadIdx.x == 0) {
     float s = 0.0f;
-    for (int i = 0; i < H; i++) {
-      const float t = sm[i] * sm[i];
-      s = s + t;
+    int i = 0;
+    for (; i + 16 <= H; i += 16) {
+      const float4 a = *reinterpret_cast<const float4 *>(sq + i);
+      const float4 b = *reinterpret_cast<const float4 *>(sq + i + 4);
+      const float4 c = *reinterpret_cast<const float4 *>(sq + i + 8);
+      const float4 d = *reinterpret_cast<const float4 *>(sq + i + 12);
+      s = s + a.x; s = s + a.y; s = s + a.z; s = s + a.w;
+      s = s + b.x; s = s + b.y; s = s + b.z; s = s + b.w;
+      s = s + c.x; s = s + c.y; s = s + c.z; s = s + c.w;
+      s = s + d.x; s = s + d.y; s = s + d.z; s = s + d.w;
     }
+    for (; i < H; i++) s = s + sq[i];
     s_scale = 1.0f / sqrtf(s / (float)H + eps);
   }
   __syncthreads();
@@ -97,33 +110,80 @@ __global__ void k_mamba_conv(const float *__restrict__ proj, float *__restrict__
 }
 
 // f32 GEMV in f32GemvRow order (matmul.zig:223-305, trans_b): lane = output
-// row; a sequential chain over k, @mulAdd for rows in the 32/8-wide column
-// blocks (row < n8), plain a*b+c in the tail.  W in [panel][K][64] so each
-// wave load is 256 contiguous bytes; x is wave-uniform.
-__global__ void __launch_bounds__(64)
-    k_gemv_f32_exact(const float *__restrict__ Wp, const float *__restrict__ x, int N, int K,
+// row; one sequential chain over k per row, @mulAdd for rows in the 32/8-wide
+// column blocks (row < n8), plain a*b+c in the tail.  W in [panel][K/4][64][4]
+// (16 bytes of one row per lane, 1 KiB per wave load).  The chain cannot be
+// split, so it is spread over time instead of over lanes: each of the 16
+// waves requests its K/16 slice of the panel at entry (all loads in flight at
+// once) and the running sums pass from wave to wave through LDS, in k order.
+// A wave requests its slice of the next pass as soon as its turn in the
+// current pass is over, so every pass after the first is loaded in advance.
+constexpr int kChainWaves = 16, kChainG = 16;  // waves, float4 groups per wave and pass
+
+__global__ void __launch_bounds__(1024)
+    k_gemv_f32_exact(const float4 *__restrict__ Wp, const float *__restrict__ x, int N, int K,
                      int n8, float *__restrict__ y) {
-  const int panel = blockIdx.x, lane = threadIdx.x;
+  extern __shared__ __align__(16) float xs[];  // K rounded to 4
+  __shared__ float carry[64];
+  const int panel = blockIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int K4 = (K + 3) >> 2;
   const int row = panel * 64 + lane;
-  const float *w = Wp + (size_t)panel * K * 64 + lane;
+  const bool fused = row < n8;
+  const float4 *w = Wp + (size_t)panel * K4 * 64 + lane;
+  constexpr int per_pass = kChainWaves * kChainG;  // float4 groups per pass
+  float4 v[kChainG];
+  auto load = [&](int g0) {
+    const int gw = g0 + wave * kChainG;
+#pragma unroll
+    for (int u = 0; u < kChainG; u++) v[u] = w[(size_t)min(gw + u, K4 - 1) * 64];
+  };
+  load(0);
+  for (int k = threadIdx.x; k < K; k += 1024) xs[k] = x[k];
+  __syncthreads();
   float acc = 0.0f;
-  if (row < n8) {
-    int k = 0;
-    for (; k + 8 <= K; k += 8) {
-      float v[8];
+  for (int g0 = 0; g0 < K4; g0 += per_pass) {
+    const int gw = g0 + wave * kChainG;
+    for (int wv = 0; wv < kChainWaves; wv++) {
+      if (wave == wv) {
+        acc = (g0 == 0 && wv == 0) ? 0.0f : carry[lane];
 #pragma unroll
-      for (int u = 0; u < 8; u++) v[u] = w[(size_t)(k + u) * 64];
+        for (int u = 0; u < kChainG; u++) {
+          const int kb = (gw + u) * 4;
+          const float vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
 #pragma unroll
-      for (int u = 0; u < 8; u++) acc = __builtin_fmaf(x[k + u], v[u], acc);
-    }
-    for (; k < K; k++) acc = __builtin_fmaf(x[k], w[(size_t)k * 64], acc);
-  } else {
-    for (int k = 0; k < K; k++) {
-      const float t = x[k] * w[(size_t)k * 64];
-      acc = acc + t;
+          for (int c = 0; c < 4; c++) {
+            if (kb + c < K) {
+              if (fused) {
+                acc = __builtin_fmaf(xs[kb + c], vv[c], acc);
+              } else {
+                const float t = xs[kb + c] * vv[c];
+                acc = acc + t;
+              }
+            }
+          }
+        }
+        carry[lane] = acc;
+        if (g0 + per_pass < K4) load(g0 + per_pass);
+      }
+      __syncthreads();
     }
   }
-  if (row < N) y[row] = acc;
+  if (threadIdx.x < 64 && row < N) y[row] = carry[lane];
+}
+
+static syn_status_t launch_gemv_f32_exact(const float *Wp, const float *x, int N, int K, int n8,
+                                          float *y, hipStream_t s) {
+  const size_t shm = round_up((size_t)K, 4) * 4;
+  if (shm > 60 * 1024) {
+    set_error("f32 GEMV: K too large for the LDS activation row");
+    return SYN_ERR_INVALID_ARG;
+  }
+  hipLaunchKernelGGL(k_gemv_f32_exact, dim3((unsigned)cdiv((size_t)N, 64)), dim3(1024), shm, s,
+                     reinterpret_cast<const float4 *>(Wp), x, N, K, n8, y);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
 }
 
 __device__ __forceinline__ float syn_softplus(float v) {  // ops/activation.rs:88-90
@@ -134,6 +194,11 @@ __device__ __forceinline__ float syn_softplus(float v) {  // ops/activation.rs:8
 
 // dt_proj (f32 chain over dt_rank, or precomputed by the INT8 variant),
 // softplus, selective scan step and the SiLU(z) gate; one thread per channel.
+// The thread's dt_proj row, A_log row and state row are requested together
+// before the chains (rows of up to kScanDr / kScanDs values; longer rows take
+// the looped form).
+constexpr int kScanDr = 64, kScanDs = 16;
+
 __global__ void k_mamba_scan(const float *__restrict__ xp, const float *__restrict__ dtw,
                              const float *__restrict__ dtp_pre, const float *__restrict__ dtb,
                              const float *__restrict__ a_log, const float *__restrict__ dparam,
@@ -142,17 +207,45 @@ __global__ void k_mamba_scan(const float *__restrict__ xp, const float *__restri
                              float *__restrict__ gated) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= di) return;
+  const bool fits = dr <= kScanDr && ds <= kScanDs;
+  float wr[kScanDr], al[kScanDs], hs[kScanDs];
+  const float *wrow = dtw ? dtw + (size_t)i * dr : nullptr;
+  float *h = ssm + (size_t)i * ds;
+  const float *arow = a_log + (size_t)i * ds;
+  if (fits) {
+    if (!dtp_pre) {
+#pragma unroll
+      for (int k = 0; k < kScanDr; k++) wr[k] = wrow[min(k, dr - 1)];
+    }
+#pragma unroll
+    for (int j = 0; j < kScanDs; j++) {
+      al[j] = arow[min(j, ds - 1)];
+      hs[j] = h[min(j, ds - 1)];
+    }
+  }
   float dtp;
   if (dtp_pre) {
     dtp = dtp_pre[i];
   } else {
-    const float *wr = dtw + (size_t)i * dr;
     dtp = 0.0f;
-    if (i < n8) {
-      for (int k = 0; k < dr; k++) dtp = __builtin_fmaf(xp[k], wr[k], dtp);
+    if (fits) {
+      if (i < n8) {
+#pragma unroll
+        for (int k = 0; k < kScanDr; k++)
+          if (k < dr) dtp = __builtin_fmaf(xp[k], wr[k], dtp);
+      } else {
+#pragma unroll
+        for (int k = 0; k < kScanDr; k++)
+          if (k < dr) {
+            const float t = xp[k] * wr[k];
+            dtp = dtp + t;
+          }
+      }
+    } else if (i < n8) {
+      for (int k = 0; k < dr; k++) dtp = __builtin_fmaf(xp[k], wrow[k], dtp);
     } else {
       for (int k = 0; k < dr; k++) {
-        const float t = xp[k] * wr[k];
+        const float t = xp[k] * wrow[k];
         dtp = dtp + t;
       }
     }
@@ -161,41 +254,67 @@ __global__ void k_mamba_scan(const float *__restrict__ xp, const float *__restri
   const float xi = xc[i];
   const float dt_x = dt * xi;
   const float *b = xp + dr, *c = xp + dr + ds;
-  float *h = ssm + (size_t)i * ds;
-  const float *al = a_log + (size_t)i * ds;
   float yi = 0.0f;
   int j = 0;
-  for (; j + 4 <= ds; j += 4) {
+#pragma unroll
+  for (int jj = 0; jj + 4 <= kScanDs; jj += 4) {
+    if (!fits || jj + 4 > ds) break;
     float contrib[4];
 #pragma unroll
     for (int l = 0; l < 4; l++) {
-      const float e = syn_expf(al[j + l]);
+      const float e = syn_expf(al[jj + l]);
       const float ad = syn_expf(-dt * e);
-      const float p1 = ad * h[j + l], p2 = dt_x * b[j + l];
+      const float p1 = ad * hs[jj + l], p2 = dt_x * b[jj + l];
       const float hn = p1 + p2;
-      h[j + l] = hn;
-      contrib[l] = c[j + l] * hn;
+      h[jj + l] = hn;
+      contrib[l] = c[jj + l] * hn;
     }
     yi = yi + (((contrib[0] + contrib[1]) + contrib[2]) + contrib[3]);
+    j = jj + 4;
   }
-  for (; j < ds; j++) {
-    const float a = -syn_expf(al[j]);
+  if (!fits) {
+    for (; j + 4 <= ds; j += 4) {
+      float contrib[4];
+      for (int l = 0; l < 4; l++) {
+        const float e = syn_expf(arow[j + l]);
+        const float ad = syn_expf(-dt * e);
+        const float p1 = ad * h[j + l], p2 = dt_x * b[j + l];
+        const float hn = p1 + p2;
+        h[j + l] = hn;
+        contrib[l] = c[j + l] * hn;
+      }
+      yi = yi + (((contrib[0] + contrib[1]) + contrib[2]) + contrib[3]);
+    }
+  }
+  // tail (selective_scan.zig's scalar remainder): compile-time indices when
+  // the rows are in registers
+  auto tail = [&](int jj, float av, float hv) {
+    const float a = -syn_expf(av);
     const float ad = syn_expf(dt * a);
-    const float p1 = ad * h[j], p2 = (dt * b[j]) * xi;
+    const float p1 = ad * hv, p2 = (dt * b[jj]) * xi;
     const float hn = p1 + p2;
-    h[j] = hn;
-    const float t = c[j] * hn;
+    h[jj] = hn;
+    const float t = c[jj] * hn;
     yi = yi + t;
+  };
+  if (fits) {
+#pragma unroll
+    for (int jj = 0; jj < kScanDs; jj++)
+      if (jj >= j && jj < ds) tail(jj, al[jj], hs[jj]);
+  } else {
+    for (; j < ds; j++) tail(j, arow[j], h[j]);
   }
   const float y = yi + dparam[i] * xi;
   gated[i] = syn_silu(proj[di + i]) * y;  // int8_mamba.rs:102
 }
 
+// [n,k] -> [panel][k/4][64][4] (k padded with zeros to a multiple of 4)
 static std::vector<float> to_panels(const float *w_nk, size_t n, size_t k) {
-  const size_t P = cdiv(n, 64);
-  std::vector<float> out(P * k * 64, 0.0f);
+  const size_t P = cdiv(n, 64), K4 = cdiv(k, 4);
+  std::vector<float> out(P * K4 * 64 * 4, 0.0f);
   for (size_t r = 0; r < n; r++)
-    for (size_t kk = 0; kk < k; kk++) out[((r / 64) * k + kk) * 64 + r % 64] = w_nk[r * k + kk];
+    for (size_t kk = 0; kk < k; kk++)
+      out[(((r / 64) * K4 + kk / 4) * 64 + r % 64) * 4 + kk % 4] = w_nk[r * k + kk];
   return out;
 }
 
@@ -231,7 +350,7 @@ struct syn_hip_mamba_s {
   syn_status_t layer(size_t l, hipStream_t s) {
     Block &B = blk[l];
     const size_t ldq_m = round_up(dm, 16), ldq_i = round_up(di, 16), ldq_r = round_up(dr, 16);
-    hipLaunchKernelGGL(k_mamba_norm, dim3(1), dim3(256), dm * 4, s, x.as<float>(),
+    hipLaunchKernelGGL(k_mamba_norm, dim3(1), dim3(256), round_up(dm, 4) * 8, s, x.as<float>(),
                        l == 0 ? nullptr : o.as<float>(), B.norm_w.as<float>(), c.eps, (int)dm,
                        xq.as<int8_t>(), sx.as<float>(), nullptr);
     SYN_LAUNCH_CHECK();
@@ -250,10 +369,8 @@ struct syn_hip_mamba_s {
       SYN_TRY(B.dt_i8.gemv(1, xpq.as<int8_t>(), ldq_r, sxp.as<float>(), dtp.as<float>(), di, s));
       dtp_pre = dtp.as<float>();
     } else {
-      hipLaunchKernelGGL(k_gemv_f32_exact, dim3(cdiv(nx, 64)), dim3(64), 0, s,
-                         B.xproj_p.as<float>(), xc.as<float>(), (int)nx, (int)di, n8_of((int)nx),
-                         xp.as<float>());
-      SYN_LAUNCH_CHECK();
+      SYN_TRY(launch_gemv_f32_exact(B.xproj_p.as<float>(), xc.as<float>(), (int)nx, (int)di,
+                                    n8_of((int)nx), xp.as<float>(), s));
     }
     hipLaunchKernelGGL(k_mamba_scan, dim3(cdiv(di, 256)), dim3(256), 0, s, xp.as<float>(),
                        B.dtproj.as<float>(), dtp_pre, B.dt_bias.as<float>(), B.a_log.as<float>(),
@@ -269,14 +386,13 @@ struct syn_hip_mamba_s {
   syn_status_t step(hipStream_t s) {
     SYN_TRY(launch_embed(embed.as<float>(), &st()->token, 1, (int)dm, (int)vocab, x.as<float>(), s));
     for (size_t l = 0; l < L; l++) SYN_TRY(layer(l, s));
-    hipLaunchKernelGGL(k_mamba_norm, dim3(1), dim3(256), dm * 4, s, x.as<float>(), o.as<float>(),
+    hipLaunchKernelGGL(k_mamba_norm, dim3(1), dim3(256), round_up(dm, 4) * 8, s, x.as<float>(),
+                       o.as<float>(),
                        final_norm.as<float>(), c.eps, (int)dm, nullptr, nullptr,
                        normed.as<float>());
     SYN_LAUNCH_CHECK();
-    hipLaunchKernelGGL(k_gemv_f32_exact, dim3(cdiv(vocab, 64)), dim3(64), 0, s,
-                       lm_p.as<float>(), normed.as<float>(), (int)vocab, (int)dm,
-                       n8_of((int)vocab), logits.as<float>());
-    SYN_LAUNCH_CHECK();
+    SYN_TRY(launch_gemv_f32_exact(lm_p.as<float>(), normed.as<float>(), (int)vocab, (int)dm,
+                                  n8_of((int)vocab), logits.as<float>(), s));
     SYN_TRY(launch_argmax(logits.as<float>(), (int)vocab, pv.as<float>(), pi.as<int>(),
                           pv2.as<float>(), st(), history.as<uint32_t>(), mhist.as<float>(), s));
     return launch_step_advance(st(), 1, s);

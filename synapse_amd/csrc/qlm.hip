@@ -569,8 +569,16 @@ syn_status_t syn_hip_qlm_time_lm_head(syn_hip_qlm_t *m, size_t iters, size_t flu
   for (size_t i = 0; i < iters && st == SYN_OK; i++) {
     if (flush_bytes) SYN_HIP(hipMemsetAsync(flush.p, (int)(i & 0xff), flush_bytes, m->stream));
     SYN_HIP(hipEventRecord(a, m->stream));
-    st = m->lm_head.gemv(1, m->xq.as<int8_t>(), m->ldh, m->sx.as<float>(), m->logits.as<float>(),
-                         m->vocab, m->stream);
+    // the kernel the decode step runs: the fused step's lm_head with per-panel
+    // top-2, or the plain GEMV of the one-kernel-per-op step
+    if (m->fused)
+      st = launch_lmhead_top2(m->lm_head.w.p, m->lm_head.scales.as<float>(), (int)m->vocab,
+                              m->lm_head.chunks, m->xq.as<int8_t>(), m->sx.as<float>(),
+                              m->logits.as<float>(), m->pv.as<float>(), m->pi.as<int>(),
+                              m->pv2.as<float>(), m->stream);
+    else
+      st = m->lm_head.gemv(1, m->xq.as<int8_t>(), m->ldh, m->sx.as<float>(),
+                           m->logits.as<float>(), m->vocab, m->stream);
     SYN_HIP(hipEventRecord(b, m->stream));
     SYN_HIP(hipEventSynchronize(b));
     float ms = 0.0f;

@@ -78,6 +78,7 @@ SIGNATURES = {
                                   C.POINTER(SZ)]),
     "syn_hip_qlinear_destroy": (ST, [P]),
     "syn_hip_qlinear_time": (ST, [P, SZ, P, P, SZ, P, P, SZ, C.POINTER(C.c_float)]),
+    "syn_hip_qlinear_time_set": (ST, [P, SZ, SZ, P, P, SZ, P, P, SZ, C.POINTER(C.c_float)]),
     "syn_hip_qlm_create": (ST, [C.POINTER(LmConfig), C.POINTER(P)]),
     "syn_hip_qlm_set_embed": (ST, [P, P]),
     "syn_hip_qlm_set_layer": (ST, [P, C.c_uint32, P, P, P, P, P, P, P]),
@@ -329,6 +330,17 @@ class QLinear:
         ms = C.c_float()
         check(lib().syn_hip_qlinear_time(self.h, m, d_x, d_xq, ldxq, d_sx, d_y, iters,
                                          C.byref(ms)), "qlinear_time")
+        return ms.value
+
+    @staticmethod
+    def time_set(linears, m: int, d_x=None, d_xq=None, ldxq=0, d_sx=None, d_y=None,
+                 rounds: int = 10) -> float:
+        """Average ms per launch, round-robin over several handles (copies of
+        one matrix), so that the working set can exceed the Infinity Cache."""
+        arr = (C.c_void_p * len(linears))(*[l.h for l in linears])
+        ms = C.c_float()
+        check(lib().syn_hip_qlinear_time_set(arr, len(linears), m, d_x, d_xq, ldxq, d_sx, d_y,
+                                             rounds, C.byref(ms)), "qlinear_time_set")
         return ms.value
 
     def forward(self, x: np.ndarray) -> np.ndarray:

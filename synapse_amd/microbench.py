@@ -1,0 +1,178 @@
+"""Kernel-level measurements of the quantized-linear path on one GPU.
+
+Each function builds synthetic weights of the benchmark shapes, uploads them
+through the library's C ABI and times back-to-back launches with hipEvents
+(syn_hip_qlinear_time_set).  Decode GEMVs at batch 1 are HBM-bound: to
+measure HBM and not the 256 MB Infinity Cache, each shape is timed
+round-robin over enough copies of its matrix to stream >= 1 GiB per round.
+
+Weight values do not change the kernels' work, so the block bytes are
+random with fixed, finite f16 scales (Q4_0 / Q8_0 / Q4_K / Q6_K) and int8
+weights are random bytes with random per-row scales.
+
+Algorithmic bytes per GEMV (the roofline numerator) = weight blocks and
+scales + activation in + output out; GEMM work = 2*M*N*K flops.
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+from . import hip
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense bf16/f16
+MFMA_I8_PEAK_TOPS = 5000.0     # dense int8
+F16_SCALE = 0x1E66             # a finite f16 (about 0.0062)
+
+BLOCK = {hip.FMT_Q4_0: (32, 18), hip.FMT_Q8_0: (32, 34), hip.FMT_Q4_K: (256, 144),
+         hip.FMT_Q6_K: (256, 210)}
+NAMES = {hip.FMT_INT8: "int8", hip.FMT_Q4_0: "q4_0", hip.FMT_Q8_0: "q8_0",
+         hip.FMT_Q4_K: "q4_k", hip.FMT_Q6_K: "q6_k"}
+
+
+def weight_bytes(fmt: int, n: int, k: int) -> int:
+    if fmt == hip.FMT_INT8:
+        return n * k + 4 * n
+    el, b = BLOCK[fmt]
+    return n * (k // el) * b
+
+
+def gemv_bytes(fmt: int, n: int, k: int) -> int:
+    """Algorithmic HBM bytes of one batch-1 GEMV launch."""
+    act = k if fmt == hip.FMT_INT8 else 4 * k
+    return weight_bytes(fmt, n, k) + act + 4 * n
+
+
+def _blocks(fmt: int, n: int, k: int, rng) -> np.ndarray:
+    """Random block bytes of an [n, k] matrix with finite f16 scales."""
+    el, b = BLOCK[fmt]
+    nb = n * (k // el)
+    raw = rng.integers(0, 256, size=(nb, b), dtype=np.uint8)
+    f16 = np.array([F16_SCALE & 0xFF, F16_SCALE >> 8], np.uint8)
+    if fmt in (hip.FMT_Q4_0, hip.FMT_Q8_0):
+        raw[:, 0:2] = f16                      # d at the front
+    elif fmt == hip.FMT_Q4_K:
+        raw[:, 0:2] = f16                      # d, dmin
+        raw[:, 2:4] = f16
+    else:
+        raw[:, 208:210] = f16                  # Q6_K: d at the end
+    return raw.reshape(-1)
+
+
+def _make(fmt: int, n: int, k: int, rng):
+    """One device copy of a synthetic [n, k] matrix in `fmt`."""
+    if fmt == hip.FMT_INT8:
+        w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
+        sc = (rng.random(n, dtype=np.float32) * 1e-3 + 1e-4).astype(np.float32)
+        return lambda: hip.QLinear.int8(w, sc, hip.LAYOUT_NK)
+    blocks = _blocks(fmt, n, k, rng)
+    if fmt == hip.FMT_Q4_0:
+        return lambda: hip.QLinear.q4_0(blocks, n, k)
+    return lambda: hip.QLinear.gguf(fmt, blocks, n, k)
+
+
+def copies_for(nbytes: int, target: int = 1 << 30, cap: int = 512) -> int:
+    return max(2, min(cap, math.ceil(target / max(1, nbytes))))
+
+
+def time_gemv(fmt: int, n: int, k: int, m: int = 1, rounds: int = 4, target: int = 1 << 30,
+              seed: int = 0):
+    """Average launch time (ms) of y[m,n] = x[m,k] W^T over rotating copies."""
+    rng = np.random.default_rng(seed)
+    make = _make(fmt, n, k, rng)
+    ncopy = copies_for(weight_bytes(fmt, n, k), target)
+    lins = [make() for _ in range(ncopy)]
+    x = hip.DeviceBuffer(max(4, m * k * 4))
+    x.upload(rng.standard_normal(m * k, dtype=np.float32))
+    y = hip.DeviceBuffer(max(4, m * n * 4))
+    xq = sx = None
+    try:
+        if fmt == hip.FMT_INT8:
+            ldq = (k + 15) // 16 * 16
+            xq = hip.DeviceBuffer(m * ldq)
+            xq.upload(rng.integers(-127, 128, size=m * ldq, dtype=np.int8))
+            sx = hip.DeviceBuffer(4 * m)
+            sx.upload(np.full(m, 0.01, np.float32))
+            ms = hip.QLinear.time_set(lins, m, d_xq=xq.ptr, ldxq=ldq, d_sx=sx.ptr, d_y=y.ptr,
+                                      rounds=rounds)
+        else:
+            ms = hip.QLinear.time_set(lins, m, d_x=x.ptr, d_y=y.ptr, rounds=rounds)
+    finally:
+        for l in lins:
+            l.close()
+        for b in (x, y, xq, sx):
+            if b is not None:
+                b.close()
+    return ms, ncopy
+
+
+def gemv_record(fmt: int, n: int, k: int, label: str, rounds: int = 4) -> dict:
+    ms, ncopy = time_gemv(fmt, n, k, 1, rounds)
+    nbytes = gemv_bytes(fmt, n, k)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"matrix": label, "fmt": NAMES[fmt], "k": k, "n": n, "us": round(ms * 1e3, 2),
+            "bytes": nbytes, "gb_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+            "copies": ncopy}
+
+
+def gemm_record(fmt: int, m: int, n: int, k: int, label: str, rounds: int = 3) -> dict:
+    ms, ncopy = time_gemv(fmt, n, k, m, rounds, target=256 << 20)
+    flops = 2.0 * m * n * k
+    tf = flops / (ms * 1e-3) / 1e12
+    peak = MFMA_I8_PEAK_TOPS if fmt == hip.FMT_INT8 else MFMA_F16_PEAK_TFLOPS
+    return {"matrix": label, "fmt": NAMES[fmt], "m": m, "k": k, "n": n,
+            "us": round(ms * 1e3, 1), "tflops": round(tf, 1), "mfma_frac": round(tf / peak, 4),
+            "peak_tflops": peak, "copies": ncopy}
+
+
+# ---- the BASELINE configurations ------------------------------------------
+# config 2: Q4_0 GEMV at LLaMA-3.2-1B shapes (K -> N)
+Q4_0_SHAPES = [("q/o 2048->2048", 2048, 2048), ("k/v 2048->512", 2048, 512),
+               ("gate/up 2048->8192", 2048, 8192), ("down 8192->2048", 8192, 2048),
+               ("lm_head 2048->128256", 2048, 128256)]
+# config 1: the INT8 W8A8 GEMVs of one Qwen3-0.6B decode step (q|k|v and
+# gate|up stacked as the model runs them)
+INT8_QWEN3_SHAPES = [("qkv 1024->4096", 1024, 4096), ("o 2048->1024", 2048, 1024),
+                     ("gate|up 1024->6144", 1024, 6144), ("down 3072->1024", 3072, 1024),
+                     ("lm_head 1024->151936", 1024, 151936)]
+# config 3: LLaMA-3.2-3B Q4_K attention and gate/up, Q6_K down and lm_head
+KQ_LLAMA3B_SHAPES = [(hip.FMT_Q4_K, "q/o 3072->3072", 3072, 3072),
+                     (hip.FMT_Q4_K, "k/v 3072->1024", 3072, 1024),
+                     (hip.FMT_Q4_K, "gate/up 3072->8192", 3072, 8192),
+                     (hip.FMT_Q6_K, "down 8192->3072", 8192, 3072),
+                     (hip.FMT_Q6_K, "lm_head 3072->128256", 3072, 128256)]
+# config 4: Mistral-7B Q8_0 prefill GEMMs
+Q8_0_MISTRAL = [("q 4096->4096", 4096, 4096, 1), ("k/v 4096->1024", 4096, 1024, 2),
+                ("gate/up 4096->14336", 4096, 14336, 2), ("down 14336->4096", 14336, 4096, 1)]
+
+
+def q4_0_suite(rounds: int = 4) -> list:
+    return [gemv_record(hip.FMT_Q4_0, n, k, lab, rounds) for lab, k, n in Q4_0_SHAPES]
+
+
+def int8_suite(rounds: int = 4) -> list:
+    return [gemv_record(hip.FMT_INT8, n, k, lab, rounds) for lab, k, n in INT8_QWEN3_SHAPES]
+
+
+def kquant_suite(rounds: int = 4) -> list:
+    return [gemv_record(f, n, k, lab, rounds) for f, lab, k, n in KQ_LLAMA3B_SHAPES]
+
+
+def q8_0_prefill_suite(m: int, rounds: int = 3) -> dict:
+    """One Mistral-7B matrix set (q, k, v, o-shaped q, gate, up, down) at M
+    tokens: per-matrix records and the set's aggregate TFLOP/s."""
+    recs = [gemm_record(hip.FMT_Q8_0, m, n, k, lab, rounds) for lab, k, n, _ in Q8_0_MISTRAL]
+    total_flops = sum(2.0 * m * r["n"] * r["k"] * cnt
+                      for r, (_, _, _, cnt) in zip(recs, Q8_0_MISTRAL))
+    total_s = sum(r["us"] * 1e-6 * cnt for r, (_, _, _, cnt) in zip(recs, Q8_0_MISTRAL))
+    tf = total_flops / total_s / 1e12
+    return {"m": m, "gflop": round(total_flops / 1e9, 2), "ms": round(total_s * 1e3, 3),
+            "tflops": round(tf, 1), "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+            "matrices": recs}
+
+
+def int8_prefill_record(m: int = 128, k: int = 1024, n: int = 3072) -> dict:
+    """The reference's published INT8 prefill GEMM shape (128x1024 -> 3072)."""
+    return gemm_record(hip.FMT_INT8, m, n, k, f"int8 prefill {m}x{k}->{n}")
