@@ -35,7 +35,14 @@ PROMPT = 16
 SEED_BASE = 0x5EED0000
 PROMPT_SEED = SEED_BASE + 0xFFFF
 HBM_PEAK_GBS = 8000.0
-REF_DECODE_TOKS = 27.3  # BASELINE.md: Qwen3-0.6B INT8 decode, reference cpu_simd (Apple Silicon)
+REF_DECODE_TOKS = 27.3  # Qwen3-0.6B INT8 decode, reference cpu_simd (Apple Silicon)
+# HBM traffic per launch of the fused step's lm_head kernel (k_lmhead_top2),
+# from rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE (KiB per dispatch), each
+# scaled by what the counter reads for a 256 MiB device copy (FETCH_SIZE reads
+# half the copied bytes: factor 2.0; WRITE_SIZE exact: 1.0); commands and
+# readings in profiles/lm_head_int8_qwen3_k_lmhead_top2.md
+LM_HEAD_FETCH_KIB, LM_HEAD_FETCH_FACTOR = 76301.0, 262144.0 / 131084.7
+LM_HEAD_WRITE_KIB, LM_HEAD_WRITE_FACTOR = 816.5, 262144.0 / 262144.0
 
 
 def step_weight_bytes(c):
@@ -216,7 +223,11 @@ def main():
     toks = 1000.0 / ms_per_step
     step_bytes = step_weight_bytes(QWEN3)
 
-    lm_ms = model.time_lm_head(args.lm_head_iters)
+    # lm_head kernel as the fused step launches it, back to back over two
+    # weight copies (HBM-streamed); the one-kernel-per-op step: single launches
+    # with the Infinity Cache flushed in between
+    lm_ms = (model.time_lm_head(args.lm_head_iters) if args.unfused
+             else model.time_lm_head_rotating(2 * args.lm_head_iters))
     lm_gbs = lm_head_bytes(QWEN3) / (lm_ms * 1e-3) / 1e9
     model.close()
 
@@ -248,7 +259,10 @@ def main():
                      "kernel": ("k_lmhead_top2<8,8>" if not args.unfused else "k_gemv_w8a8<1>")
                                + " lm_head 151936x1024",
                      "achieved": round(lm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(lm_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(lm_gbs / HBM_PEAK_GBS, 4),
+                     "traffic": None if args.unfused else round(
+                         1024 * (LM_HEAD_FETCH_KIB * LM_HEAD_FETCH_FACTOR
+                                 + LM_HEAD_WRITE_KIB * LM_HEAD_WRITE_FACTOR)),
                      "avg_launch_us": round(lm_ms * 1e3, 2),
                      "bytes_per_launch": lm_head_bytes(QWEN3)},
     }

@@ -203,6 +203,11 @@ syn_status_t syn_hip_qlm_decode_timed(syn_hip_qlm_t *m, size_t steps, float *ela
  * where the layer weights stream through it in between). */
 syn_status_t syn_hip_qlm_time_lm_head(syn_hip_qlm_t *m, size_t iters, size_t flush_bytes,
                                       float *avg_ms);
+/* Average duration of the fused decode step's lm_head kernel over `iters`
+ * back-to-back launches alternating between the model's weights and a
+ * temporary device copy (2 x the weights exceed the Infinity Cache, so every
+ * launch streams from HBM); one hipEvent pair around the batch. */
+syn_status_t syn_hip_qlm_time_lm_head_rotating(syn_hip_qlm_t *m, size_t iters, float *avg_ms);
 /* Decode-step options (no reference counterpart; both settings compute the
  * same bits).  fused_decode = 1 (default when the shape fits the fused
  * kernels' LDS rows): five kernels per layer, each a split-K GEMV whose

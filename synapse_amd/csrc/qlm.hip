@@ -597,6 +597,49 @@ syn_status_t syn_hip_qlm_set_options(syn_hip_qlm_t *m, int fused_decode, int gra
   return m->set_options(fused_decode, graph_replay);
 }
 
+syn_status_t syn_hip_qlm_time_lm_head_rotating(syn_hip_qlm_t *m, size_t iters, float *avg_ms) {
+  SYN_TRY(check_model(m));
+  if (!avg_ms) return SYN_ERR_NULL_PTR;
+  if (iters == 0) return SYN_ERR_INVALID_ARG;
+  if (!m->fused) {
+    set_error("rotating lm_head timing measures the fused decode step's kernel");
+    return SYN_ERR_INVALID_ARG;
+  }
+  // a second copy of the weights: alternating launches stream 2 x 156 MB,
+  // more than the Infinity Cache holds, so every launch reads HBM
+  DevBuf w2, s2;
+  SYN_TRY(w2.alloc(m->lm_head.w.bytes));
+  SYN_TRY(s2.alloc(m->lm_head.scales.bytes));
+  SYN_HIP(hipMemcpyAsync(w2.p, m->lm_head.w.p, w2.bytes, hipMemcpyDeviceToDevice, m->stream));
+  SYN_HIP(hipMemcpyAsync(s2.p, m->lm_head.scales.p, s2.bytes, hipMemcpyDeviceToDevice,
+                         m->stream));
+  auto launch = [&](size_t i) -> syn_status_t {
+    const void *W = (i & 1) ? w2.p : m->lm_head.w.p;
+    const float *ws = (i & 1) ? s2.as<float>() : m->lm_head.scales.as<float>();
+    return launch_lmhead_top2(W, ws, (int)m->vocab, m->lm_head.chunks, m->xq.as<int8_t>(),
+                              m->sx.as<float>(), m->logits.as<float>(), m->pv.as<float>(),
+                              m->pi.as<int>(), m->pv2.as<float>(), m->stream);
+  };
+  SYN_TRY(launch(0));
+  SYN_TRY(launch(1));
+  SYN_HIP(hipStreamSynchronize(m->stream));
+  hipEvent_t a, b;
+  SYN_HIP(hipEventCreate(&a));
+  SYN_HIP(hipEventCreate(&b));
+  SYN_HIP(hipEventRecord(a, m->stream));
+  syn_status_t st = SYN_OK;
+  for (size_t i = 0; i < iters && st == SYN_OK; i++) st = launch(i);
+  SYN_HIP(hipEventRecord(b, m->stream));
+  SYN_HIP(hipEventSynchronize(b));
+  float ms = 0.0f;
+  SYN_HIP(hipEventElapsedTime(&ms, a, b));
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  SYN_TRY(st);
+  *avg_ms = ms / (float)iters;
+  return SYN_OK;
+}
+
 syn_status_t syn_hip_qlm_destroy(syn_hip_qlm_t *m) {
   if (m) {
     (void)hipStreamSynchronize(m->stream);

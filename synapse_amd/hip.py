@@ -91,6 +91,7 @@ SIGNATURES = {
     "syn_hip_qlm_decode_timed": (ST, [P, SZ, C.POINTER(C.c_float)]),
     "syn_hip_qlm_time_lm_head": (ST, [P, SZ, SZ, C.POINTER(C.c_float)]),
     "syn_hip_qlm_set_options": (ST, [P, C.c_int, C.c_int]),
+    "syn_hip_qlm_time_lm_head_rotating": (ST, [P, SZ, C.POINTER(C.c_float)]),
     "syn_hip_qlm_destroy": (ST, [P]),
     "syn_hip_klm_create": (ST, [C.POINTER(KLmConfig), C.POINTER(P)]),
     "syn_hip_klm_set_embed": (ST, [P, P]),
@@ -421,6 +422,12 @@ class QuantizedCausalLM:
         """Decode-step form: fused five-kernel layers or one kernel per op; HIP
         graph replay or eager launches (same results either way)."""
         check(lib().syn_hip_qlm_set_options(self.h, int(fused), int(graph)), "set_options")
+
+    def time_lm_head_rotating(self, iters: int = 40) -> float:
+        ms = C.c_float()
+        check(lib().syn_hip_qlm_time_lm_head_rotating(self.h, iters, C.byref(ms)),
+              "time_lm_head_rotating")
+        return ms.value
 
     def time_lm_head(self, iters: int = 20, flush_bytes: int = 512 << 20) -> float:
         ms = C.c_float()

@@ -161,7 +161,7 @@ def kquant_suite(rounds: int = 4) -> list:
 
 
 def q8_0_prefill_suite(m: int, rounds: int = 3) -> dict:
-    """One Mistral-7B matrix set (q, k, v, o-shaped q, gate, up, down) at M
+    """One Mistral-7B matrix set (q, k, v, gate, up, down: 201,326,592 weights) at M
     tokens: per-matrix records and the set's aggregate TFLOP/s."""
     recs = [gemm_record(hip.FMT_Q8_0, m, n, k, lab, rounds) for lab, k, n, _ in Q8_0_MISTRAL]
     total_flops = sum(2.0 * m * r["n"] * r["k"] * cnt
@@ -176,3 +176,35 @@ def q8_0_prefill_suite(m: int, rounds: int = 3) -> dict:
 def int8_prefill_record(m: int = 128, k: int = 1024, n: int = 3072) -> dict:
     """The reference's published INT8 prefill GEMM shape (128x1024 -> 3072)."""
     return gemm_record(hip.FMT_INT8, m, n, k, f"int8 prefill {m}x{k}->{n}")
+
+
+def copy_calibration(nbytes: int, reps: int = 3) -> float:
+    """Device-to-device copies of `nbytes` (the runtime's copy kernel): the
+    known traffic that scales FETCH_SIZE / WRITE_SIZE counter readings."""
+    src = hip.DeviceBuffer(nbytes)
+    dst = hip.DeviceBuffer(nbytes)
+    src.zero()
+    t = hip.Timer()
+    t.start()
+    for _ in range(reps):
+        hip.check(hip.lib().syn_hip_memcpy_d2d(dst.ptr, src.ptr, nbytes), "d2d")
+    t.stop()
+    ms = t.ms() / reps
+    src.close()
+    dst.close()
+    return ms
+
+
+if __name__ == "__main__":
+    import json
+    import sys
+
+    hip.init(0)
+    if len(sys.argv) > 2 and sys.argv[1] == "copy":
+        n = int(sys.argv[2])
+        ms = copy_calibration(n)
+        print(json.dumps({"copy_bytes": n, "ms": round(ms, 4),
+                          "gb_s_read_plus_write": round(2 * n / (ms * 1e-3) / 1e9, 1)}))
+    else:
+        print("usage: python -m synapse_amd.microbench copy NBYTES", file=sys.stderr)
+        sys.exit(2)
