@@ -149,16 +149,15 @@ __device__ __forceinline__ float syn_silu_tab(float x, const uint64_t *tab) {
 // Rust converter f16->f32 (weight_loading/converter.rs:12-40): subnormal
 // inputs come out at half their IEEE value (shift counter starts at 1).
 __device__ __forceinline__ float syn_f16_to_f32_rs(uint32_t h) {
+  // branch-free (selects), so it can sit in software-pipelined loops
   const uint32_t sign = (h >> 15) & 1u, exp = (h >> 10) & 0x1fu, mant = h & 0x3ffu;
-  if (exp == 0) {
-    if (mant == 0) return __uint_as_float(sign << 31);
-    const uint32_t lz = __clz(mant) - 21;  // shifts until bit 10 is set
-    const uint32_t e = 1u + lz;
-    const uint32_t m = ((mant << lz) & 0x3ffu) << 13;
-    return __uint_as_float((sign << 31) | ((127u - 15u + 1u - e) << 23) | m);
-  }
-  if (exp == 31) return __uint_as_float((sign << 31) | (0xffu << 23) | (mant << 13));
-  return __uint_as_float((sign << 31) | ((exp + 127u - 15u) << 23) | (mant << 13));
+  const uint32_t s = sign << 31;
+  const uint32_t normal = s | ((exp + 127u - 15u) << 23) | (mant << 13);
+  const uint32_t lz = __clz(mant | 1u) - 21;  // shifts until bit 10 is set (mant != 0)
+  const uint32_t sub = s | ((127u - 15u + 1u - (1u + lz)) << 23) | (((mant << lz) & 0x3ffu) << 13);
+  const uint32_t special = s | (0xffu << 23) | (mant << 13);
+  const uint32_t r = exp == 0 ? (mant == 0 ? s : sub) : (exp == 31 ? special : normal);
+  return __uint_as_float(r);
 }
 
 // IEEE f16->f32 (qmatmul.zig:346-371 semantics)

@@ -205,6 +205,7 @@ syn_status_t QLinearKQ::upload(int fmt_, const uint8_t *gguf, size_t n_, size_t 
   fmt = fmt_;
   n = n_;
   k = k_;
+  q8_scales_f16_exact = true;
   const size_t be = kq_block_elems(fmt), bb = kq_block_bytes(fmt);
   blocks = (int)(k / be);
   planes = kq_planes(fmt);
@@ -220,8 +221,13 @@ syn_status_t QLinearKQ::upload(int fmt_, const uint8_t *gguf, size_t n_, size_t 
       const uint8_t *src = gguf + (row * B + b) * bb;
       const uint8_t *qsrc = src;
       if (fmt == SYN_HIP_FMT_Q8_0) {
-        hd[(p * B + b) * 64 + r] = (uint16_t)(src[0] | (src[1] << 8));
+        const uint16_t d = (uint16_t)(src[0] | (src[1] << 8));
+        hd[(p * B + b) * 64 + r] = d;
         qsrc = src + 2;
+        // converter.rs:12-40 halves subnormals: an odd subnormal mantissa
+        // then falls between f16 values, and a NaN is no f16 value either
+        const uint32_t e = (d >> 10) & 0x1fu, m = d & 0x3ffu;
+        if ((e == 0 && (m & 1u)) || (e == 31 && m)) q8_scales_f16_exact = false;
       } else if (fmt == SYN_HIP_FMT_Q6_K) {
         hd[(p * B + b) * 64 + r] = (uint16_t)(src[208] | (src[209] << 8));
       }

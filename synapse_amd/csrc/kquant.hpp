@@ -21,6 +21,9 @@ struct QLinearKQ {
   size_t part_elems = 0;
   DevBuf xh;  // f16 activations for the MFMA GEMM
   size_t xh_elems = 0;
+  // Q8_0: every block scale (as the reference converts it) is an f16 value,
+  // so the GEMM may multiply in f16 (set at upload)
+  bool q8_scales_f16_exact = true;
   syn_status_t upload(int fmt, const uint8_t *gguf, size_t n, size_t k);
   syn_status_t from_f32(int fmt, const float *w, size_t n, size_t k);
   size_t weight_bytes() const;

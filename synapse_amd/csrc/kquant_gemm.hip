@@ -11,6 +11,7 @@
 // result well inside the 1e-3 per-row tolerance (measured in the tests).
 #include <algorithm>
 
+#include "decode_fused.hpp"
 #include "kquant.hpp"
 
 namespace syn {
@@ -18,15 +19,15 @@ namespace syn {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int QBM = 128, QBN = 128, QBK = 32, QLD = QBK + 8;  // LDS row stride in halfs
-
+// x f32 [M, ldx] -> xh f16 [M, ldh], columns K..ldh-1 zero (K, ldh multiples of 4)
 __global__ void k_f32_to_f16(const float *__restrict__ x, int ldx, _Float16 *__restrict__ xh,
                              int ldh, int M, int K) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  const int per_row = K / 4;
+  const int per_row = ldh / 4;
   if (i >= M * per_row) return;
   const int m = i / per_row, c = (i - m * per_row) * 4;
-  const float4 v = *reinterpret_cast<const float4 *>(x + (size_t)m * ldx + c);
+  float4 v = float4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (c < K) v = *reinterpret_cast<const float4 *>(x + (size_t)m * ldx + c);
   _Float16 *o = xh + (size_t)m * ldh + c;
   o[0] = (_Float16)v.x;
   o[1] = (_Float16)v.y;
@@ -34,146 +35,273 @@ __global__ void k_f32_to_f16(const float *__restrict__ x, int ldx, _Float16 *__r
   o[3] = (_Float16)v.w;
 }
 
-// Decode 16 consecutive weights (k = 16*half .. +15 of K step ks) of row n.
+// ---------------------------------------------------------------------------
+// Pipelined form.  A workgroup (8 waves, 4 x 2, each a 64 x 64 sub-tile) owns
+// a 256 x 128 tile of Y and walks its K range 64 elements per step.  Each
+// thread keeps the raw global bytes of the next kDepth steps in a register
+// ring (activations: 4 x 16 B; weights: the planes and scale of 16 elements
+// of one row), so a step's loads are issued kDepth steps before the step is
+// staged: the thread writes its activation chunks to LDS, decodes its 16
+// weights into f16 in LDS (the reference dequantizer's value rounded once to
+// f16), re-fills the ring slot with the loads of step + kDepth, and the waves
+// run 2 x 16 v_mfma_f32_16x16x32_f16 over the staged tile.  Loads are
+// unconditional from clamped (in-bounds) rows and steps.  Shapes with fewer
+// tiles than the GPU has CUs split K over the grid's z dimension and add
+// their partial tiles with f32 atomics into a zeroed Y.
+constexpr int PGM = 256, PGN = 128, PGK = 64, PGLD = PGK + 8;  // LDS row stride in halfs
+constexpr int PGT = 512;                                        // threads
+constexpr int kDepth = 3;
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+struct RawW {
+  u32x4 q0, q1, q2;  // quant planes (format-dependent)
+  uint32_t d;        // f16 bits of the block scale (Q8_0, Q6_K)
+};
+
+__device__ __forceinline__ uint32_t u32x4_word(const u32x4 &v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+// elements 16q .. 16q+15 of step `step` of row n (q = 0..3)
 template <int FMT>
-__device__ __forceinline__ void kq_decode16(const u32x4 *__restrict__ W,
-                                            const uint16_t *__restrict__ Wd, int B, int n, int N,
-                                            int ks, int half, _Float16 *out) {
-  if (n >= N) {
-#pragma unroll
-    for (int i = 0; i < 16; i++) out[i] = (_Float16)0.0f;
-    return;
-  }
+__device__ __forceinline__ void pg_load_w(RawW &r, const u32x4 *__restrict__ W,
+                                          const uint16_t *__restrict__ Wd, int B, int n, int step,
+                                          int q) {
   const size_t panel = (size_t)(n >> 6), rp = (size_t)(n & 63);
+  if (FMT == SYN_HIP_FMT_Q8_0) {  // block 2*step + q/2 (clamped, see pg_decode_w), plane q%2
+    const size_t blk = (size_t)min(2 * step + (q >> 1), B - 1);
+    r.q0 = W[((panel * B + blk) * 2 + (q & 1)) * 64 + rp];
+    r.d = Wd[(panel * B + blk) * 64 + rp];
+  } else if (FMT == SYN_HIP_FMT_Q4_K) {  // sub-block 2*(step%4) + q/2, nibble bytes 8*(q%2)..+7
+    const size_t sb = (size_t)(step >> 2);
+    const int sub = 2 * (step & 3) + (q >> 1);
+    r.q0 = W[((panel * B + sb) * 9 + 0) * 64 + rp];
+    r.q1 = W[((panel * B + sb) * 9 + 1 + sub) * 64 + rp];
+  } else {  // Q6_K: elements e0 = 64*(step%4) + 16q .. +15 of superblock step/4
+    const size_t sb = (size_t)(step >> 2);
+    const int st = step & 3;
+    r.q0 = W[((panel * B + sb) * 13 + 2 * st + (q >> 1)) * 64 + rp];  // ql bytes
+    r.q1 = W[((panel * B + sb) * 13 + 8 + st) * 64 + rp];             // qh bytes
+    r.q2 = W[((panel * B + sb) * 13 + 12) * 64 + rp];                 // scales
+    r.d = Wd[(panel * B + sb) * 64 + rp];
+  }
+}
+
+// the 16 weights as 8 f16 pairs (element order), each the reference
+// dequantizer's f32 value (gguf.rs:255-487) rounded once to f16.  Q8_0 with K
+// % 64 == 32: the block past the row's end decodes to zeros, against the
+// zero padding of the activations.
+template <int FMT, bool EXACT>
+__device__ __forceinline__ void pg_decode_w(const RawW &r, int step, int q, int B,
+                                            uint32_t (&out)[8]) {
   if (FMT == SYN_HIP_FMT_Q8_0) {
-    const size_t blk = (size_t)ks;
-    const float d = syn_f16_to_f32_rs(Wd[(panel * B + blk) * 64 + rp]);
-    const u32x4 q = W[((panel * B + blk) * 2 + half) * 64 + rp];
-    const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+    const bool valid = 2 * step + (q >> 1) < B;
+    const float d = valid ? syn_f16_to_f32_rs(r.d) : 0.0f;
+    if (EXACT) {
+      // every scale of the matrix is an f16 value (checked at upload), and
+      // d*q is exact in f32 (11 x 8 significant bits), so rounding it to f16
+      // equals one f16 multiply of the exact f16 values d and q; q comes from
+      // the byte as f16(1024 + (q ^ 0x80)) - 1152, built with byte permutes
+      const _Float16 dh = (_Float16)d;
+      const f16x2 dd = f16x2{dh, dh}, bias = f16x2{(_Float16)-1152.0f, (_Float16)-1152.0f};
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const float v = d * (float)(int8_t)(w[i >> 2] >> (8 * (i & 3)));  // gguf.rs:283
-      out[i] = (_Float16)v;
+      for (int w = 0; w < 4; w++) {
+        const uint32_t u = u32x4_word(r.q0, w) ^ 0x80808080u;
+        const uint32_t p01 = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+        const uint32_t p23 = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+        const f16x2 v01 = (__builtin_bit_cast(f16x2, p01) + bias) * dd;
+        const f16x2 v23 = (__builtin_bit_cast(f16x2, p23) + bias) * dd;
+        out[2 * w] = __builtin_bit_cast(uint32_t, v01);
+        out[2 * w + 1] = __builtin_bit_cast(uint32_t, v23);
+      }
+    } else {  // some scale is not an f16 value (a halved subnormal): f32 products
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        f16x2 v;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const int e = 2 * i + h;
+          const uint32_t w = u32x4_word(r.q0, e >> 2);
+          v[h] = (_Float16)(d * (float)(int8_t)(w >> (8 * (e & 3))));  // gguf.rs:283
+        }
+        out[i] = __builtin_bit_cast(uint32_t, v);
+      }
     }
   } else if (FMT == SYN_HIP_FMT_Q4_K) {
-    const size_t sb = (size_t)(ks >> 3);
-    const int s = ks & 7;
-    const u32x4 h = W[((panel * B + sb) * 9 + 0) * 64 + rp];
-    const u32x4 q = W[((panel * B + sb) * 9 + 1 + s) * 64 + rp];
-    const float d = syn_f16_to_f32_rs(h.x & 0xffffu), dmin = syn_f16_to_f32_rs(h.x >> 16);
-    const uint32_t sbw[3] = {h.y, h.z, h.w};
+    const int s = 2 * (step & 3) + (q >> 1);
+    const float d = syn_f16_to_f32_rs(r.q0.x & 0xffffu), dmin = syn_f16_to_f32_rs(r.q0.x >> 16);
+    const uint32_t sbw[3] = {r.q0.y, r.q0.z, r.q0.w};
     auto SB = [&](int i) -> uint32_t { return (sbw[i >> 2] >> (8 * (i & 3))) & 0xffu; };
-    uint32_t sc, mn;
-    if (s < 4) {
-      sc = SB(s) & 63u;
-      mn = ((SB(s + 4) >> 4) | ((SB(s + 8) & 15u) << 4)) & 0xffu;
-    } else {
-      sc = (SB(s) & 15u) | ((SB(s - 4) >> 6) << 4);
-      mn = ((SB(s + 4) >> 4) | (((SB(s - 4) >> 4) & 12u) << 4)) & 0xffu;
-    }
+    // gguf.rs:383-399 for sub-block s (both branches evaluated, one selected)
+    const int sl = s & 3;
+    const uint32_t sc_lo = SB(sl) & 63u;
+    const uint32_t mn_lo = ((SB(sl + 4) >> 4) | ((SB(sl + 8) & 15u) << 4)) & 0xffu;
+    const uint32_t sc_hi = (SB(sl + 4) & 15u) | ((SB(sl) >> 6) << 4);
+    const uint32_t mn_hi = ((SB(sl + 8) >> 4) | (((SB(sl) >> 4) & 12u) << 4)) & 0xffu;
+    const uint32_t sc = s < 4 ? sc_lo : sc_hi, mn = s < 4 ? mn_lo : mn_hi;
     const float scf = d * (float)sc, mf = dmin * (float)mn;  // gguf.rs:416-417
-    // elements 16*half + 2i, +2i+1 <- byte 8*half + i (low, high nibble)
-    const uint32_t w0 = half ? q.z : q.x, w1 = half ? q.w : q.y;
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const uint32_t byte = ((i < 4 ? w0 : w1) >> (8 * (i & 3))) & 0xffu;
+    for (int i = 0; i < 8; i++) {  // element 2i: low nibble of byte i, 2i+1: high
+      const int bi = 8 * (q & 1) + i;
+      const uint32_t byte = (u32x4_word(r.q1, bi >> 2) >> (8 * (bi & 3))) & 0xffu;
       const float lo = (float)(byte & 15u) * scf - mf;  // gguf.rs:424-425
       const float hi = (float)(byte >> 4) * scf - mf;
-      out[2 * i] = (_Float16)lo;
-      out[2 * i + 1] = (_Float16)hi;
+      out[i] = __builtin_bit_cast(uint32_t, f16x2{(_Float16)lo, (_Float16)hi});
     }
-  } else {  // Q6_K: K step ks covers sub-blocks 2j, 2j+1 of superblock ks/8
-    const size_t sb = (size_t)(ks >> 3);
-    const int j = ks & 7, s = 2 * j + half;
-    const u32x4 ql = W[((panel * B + sb) * 13 + (s >> 1)) * 64 + rp];
-    const u32x4 qh = W[((panel * B + sb) * 13 + 8 + (s >> 2)) * 64 + rp];
-    const u32x4 sc = W[((panel * B + sb) * 13 + 12) * 64 + rp];
-    const float d = syn_f16_to_f32_rs(Wd[(panel * B + sb) * 64 + rp]);
-    const uint32_t lo0 = (s & 1) ? ql.z : ql.x, lo1 = (s & 1) ? ql.w : ql.y;
-    const uint32_t hw[4] = {qh.x, qh.y, qh.z, qh.w};
-    const uint32_t hi = hw[s & 3];
-    const uint32_t sw[4] = {sc.x, sc.y, sc.z, sc.w};
-    const float scale = (float)(int8_t)(sw[s >> 2] >> (8 * (s & 3))) * d;  // gguf.rs:466
+  } else {
+    const int st = step & 3;
+    const float d = syn_f16_to_f32_rs(r.d);
+    // ql byte (e0+i)/2 = plane byte 8*(q%2) + i/2, nibble i%2; qh byte
+    // (e0+i)/4 = plane byte 4q + i/4, bits 2*(i%4); scale (e0+i)/16 = 4st + q
+    const int si = 4 * st + q;
+    const float scale = (float)(int8_t)(u32x4_word(r.q2, si >> 2) >> (8 * (si & 3))) * d;
 #pragma unroll
-    for (int i = 0; i < 16; i++) {
-      const uint32_t lo = ((i < 8 ? lo0 : lo1) >> (4 * (i & 7))) & 15u;
-      const uint32_t h2 = (hi >> (2 * i)) & 3u;
-      const float qv = (float)((int)(lo | (h2 << 4)) - 32);
-      out[i] = (_Float16)(qv * scale);  // gguf.rs:480-481
+    for (int i = 0; i < 8; i++) {
+      f16x2 v;
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const int e = 2 * i + h;
+        const int lb = 8 * (q & 1) + (e >> 1);
+        const uint32_t qlb = (u32x4_word(r.q0, lb >> 2) >> (8 * (lb & 3))) & 0xffu;
+        const uint32_t lo = (e & 1) ? (qlb >> 4) : (qlb & 15u);
+        const int hb = 4 * q + (e >> 2);
+        const uint32_t qhb = (u32x4_word(r.q1, hb >> 2) >> (8 * (hb & 3))) & 0xffu;
+        const uint32_t h2 = (qhb >> (2 * (e & 3))) & 3u;
+        const float qv = (float)((int)(lo | (h2 << 4)) - 32);
+        v[h] = (_Float16)(qv * scale);  // gguf.rs:480-481
+      }
+      out[i] = __builtin_bit_cast(uint32_t, v);
     }
   }
 }
 
-template <int FMT>
-__global__ void __launch_bounds__(256)
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// LDS: two stages of A [256][72] and B [128][72] f16 (110,592 bytes)
+constexpr int PG_STAGE = (PGM + PGN) * PGLD;
+
+template <int FMT, bool EXACT>
+__global__ void __launch_bounds__(PGT)
     k_gemm_kq(const _Float16 *__restrict__ Xh, int ldh, int M, int K,
               const u32x4 *__restrict__ W, const uint16_t *__restrict__ Wd, int N, int B,
-              float *__restrict__ Y, int ldy) {
-  __shared__ __attribute__((aligned(16))) _Float16 As[QBM * QLD];
-  __shared__ __attribute__((aligned(16))) _Float16 Bs[QBN * QLD];
+              float *__restrict__ Y, int ldy, int steps_per_split) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int n0 = blockIdx.x * QBN, m0 = blockIdx.y * QBM;
+  const int n0 = blockIdx.x * PGN, m0 = blockIdx.y * PGM;
   const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
-  const int lr = lane & 15, lg = lane >> 4;
-  const int ksteps = K / QBK;
-  f32x4 acc[4][4];
+  const int l32 = lane & 31, lh = lane >> 5;
+  const int s_begin = blockIdx.z * steps_per_split;
+  const int nsteps = min((K + PGK - 1) / PGK - s_begin, steps_per_split);
+  // 2 x 2 tiles of 32 x 32 per wave; lane l of a tile holds column l%32 and
+  // rows 8*(r/4) + 4*(l/32) + r%4 for r = 0..15 (v_mfma_f32_32x32x16_f16)
+  f32x16 acc[2][2];
 #pragma unroll
-  for (int mt = 0; mt < 4; mt++)
+  for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-    for (int nt = 0; nt < 4; nt++) acc[mt][nt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[mt][nt][r] = 0.0f;
 
-  // A: 128 rows x 32 halfs = 512 x 16 B, two per thread
-  u32x4 ga[2];
-  auto fetch_a = [&](int ks) {
+  // A: 256 rows x 64 halfs = 2048 chunks of 16 B, four per thread
+  const _Float16 *arow[4];
 #pragma unroll
-    for (int it = 0; it < 2; it++) {
-      const int idx = tid + it * 256, r = idx >> 2, c = (idx & 3) * 8;
-      ga[it] = u32x4{0u, 0u, 0u, 0u};
-      if (m0 + r < M)
-        ga[it] = *reinterpret_cast<const u32x4 *>(Xh + (size_t)(m0 + r) * ldh + ks * QBK + c);
+  for (int i = 0; i < 4; i++) {
+    const int idx = tid + i * PGT;
+    arow[i] = Xh + (size_t)min(m0 + (idx >> 3), M - 1) * ldh + (idx & 7) * 8;
+  }
+  // W: row n0 + tid/4 (clamped), elements 16*(tid%4) .. +15 of the step
+  const int brow = tid >> 2, bq = tid & 3;
+  const int bn = min(n0 + brow, N - 1);
+
+  u32x4 ra[kDepth][4];
+  RawW rw[kDepth];
+  auto load = [&](int slot, int t) {  // step t of this split (clamped)
+    const int step = s_begin + min(t, nsteps - 1);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      ra[slot][i] = *reinterpret_cast<const u32x4 *>(arow[i] + (size_t)step * PGK);
+    pg_load_w<FMT>(rw[slot], W, Wd, B, bn, step, bq);
+  };
+  // stage ring slot `slot` (step t) into LDS stage `buf`, then refill the slot
+  auto stage = [&](int slot, int t, int buf) {
+    _Float16 *As = lds + buf * PG_STAGE, *Bs = As + PGM * PGLD;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int idx = tid + i * PGT;
+      *reinterpret_cast<u32x4 *>(&As[(idx >> 3) * PGLD + (idx & 7) * 8]) = ra[slot][i];
+    }
+    uint32_t wv[8];
+    pg_decode_w<FMT, EXACT>(rw[slot], s_begin + t, bq, B, wv);
+    u32x4 *dst = reinterpret_cast<u32x4 *>(&Bs[brow * PGLD + bq * 16]);
+    dst[0] = u32x4{wv[0], wv[1], wv[2], wv[3]};
+    dst[1] = u32x4{wv[4], wv[5], wv[6], wv[7]};
+    load(slot, t + kDepth);
+  };
+  // operand fragments of a whole step are read from LDS before its MFMAs
+  f16x8 fa[4][2], fb[4][2];
+  auto frag = [&](int buf) {
+    const _Float16 *As = lds + buf * PG_STAGE, *Bs = As + PGM * PGLD;
+#pragma unroll
+    for (int k16 = 0; k16 < 4; k16++) {
+#pragma unroll
+      for (int mt = 0; mt < 2; mt++)
+        fa[k16][mt] = *reinterpret_cast<const f16x8 *>(
+            &As[(wm + mt * 32 + l32) * PGLD + k16 * 16 + lh * 8]);
+#pragma unroll
+      for (int nt = 0; nt < 2; nt++)
+        fb[k16][nt] = *reinterpret_cast<const f16x8 *>(
+            &Bs[(wn + nt * 32 + l32) * PGLD + k16 * 16 + lh * 8]);
     }
   };
-  _Float16 wb[16];
-  const int brow = tid >> 1, bhalf = tid & 1;
+  auto mma = [&](int k16) {
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+      for (int nt = 0; nt < 2; nt++)
+        acc[mt][nt] =
+            __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[k16][mt], fb[k16][nt], acc[mt][nt], 0, 0, 0);
+  };
 
-  fetch_a(0);
-  kq_decode16<FMT>(W, Wd, B, n0 + brow, N, 0, bhalf, wb);
-  for (int ks = 0; ks < ksteps; ks++) {
+#pragma unroll
+  for (int i = 0; i < kDepth; i++) load(i, i);
+  stage(0, 0, 0);
+  __syncthreads();
+  // step t: MFMAs on stage t%2; step t+1 is staged into the other stage in
+  // the middle of them (its decode and LDS stores overlap the matrix cores);
+  // one barrier per step.  The steady-state body has no conditionals, so the
+  // compiler's load counters see the ring's 2-step lead.
+  auto step_body = [&](int j, int t, bool stage_next) {
+    const int buf = j & 1;
+    frag(buf);
+    mma(0);
+    mma(1);
+    if (stage_next) stage((j + 1) % kDepth, t + 1, buf ^ 1);
+    mma(2);
+    mma(3);
     __syncthreads();
+  };
+  int t0 = 0;
+  for (; t0 + 2 * kDepth < nsteps; t0 += 2 * kDepth) {
 #pragma unroll
-    for (int it = 0; it < 2; it++) {
-      const int idx = tid + it * 256;
-      *reinterpret_cast<u32x4 *>(&As[(idx >> 2) * QLD + (idx & 3) * 8]) = ga[it];
-    }
-#pragma unroll
-    for (int i = 0; i < 16; i++) Bs[brow * QLD + bhalf * 16 + i] = wb[i];
-    __syncthreads();
-    if (ks + 1 < ksteps) {  // next step's loads and decode overlap the MFMAs
-      fetch_a(ks + 1);
-      kq_decode16<FMT>(W, Wd, B, n0 + brow, N, ks + 1, bhalf, wb);
-    }
-    f16x8 a[4], b[4];
-#pragma unroll
-    for (int mt = 0; mt < 4; mt++)
-      a[mt] = *reinterpret_cast<const f16x8 *>(&As[(wm + mt * 16 + lr) * QLD + lg * 8]);
-#pragma unroll
-    for (int nt = 0; nt < 4; nt++)
-      b[nt] = *reinterpret_cast<const f16x8 *>(&Bs[(wn + nt * 16 + lr) * QLD + lg * 8]);
-#pragma unroll
-    for (int mt = 0; mt < 4; mt++)
-#pragma unroll
-      for (int nt = 0; nt < 4; nt++)
-        acc[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[mt], b[nt], acc[mt][nt], 0, 0, 0);
+    for (int j = 0; j < 2 * kDepth; j++) step_body(j, t0 + j, true);
   }
 #pragma unroll
-  for (int mt = 0; mt < 4; mt++)
+  for (int j = 0; j < 2 * kDepth; j++)
+    if (t0 + j < nsteps) step_body(j, t0 + j, t0 + j + 1 < nsteps);
+  const bool atomic = gridDim.z > 1;
 #pragma unroll
-    for (int nt = 0; nt < 4; nt++) {
-      const int n = n0 + wn + nt * 16 + lr;
+  for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int m = m0 + wm + mt * 16 + 4 * lg + r;
-        if (m < M && n < N) Y[(size_t)m * ldy + n] = acc[mt][nt][r];
+    for (int nt = 0; nt < 2; nt++) {
+      const int n = n0 + wn + nt * 32 + l32;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int m = m0 + wm + mt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+        if (m < M && n < N) {
+          if (atomic) atomicAdd(&Y[(size_t)m * ldy + n], acc[mt][nt][r]);
+          else Y[(size_t)m * ldy + n] = acc[mt][nt][r];
+        }
       }
     }
 }
@@ -184,29 +312,61 @@ syn_status_t QLinearKQ::gemm(size_t m, const float *d_x, size_t ldx, float *d_y,
     set_error("GEMM activation stride must be a multiple of 4 floats");
     return SYN_ERR_SHAPE_MISMATCH;
   }
-  const size_t ldh = k;  // k is a multiple of 32
+  const size_t ldh = round_up(k, PGK);  // zero-padded to whole K steps
   if (xh_elems < m * ldh) {
     SYN_HIP(hipDeviceSynchronize());
     SYN_TRY(xh.alloc(m * ldh * 2));
     xh_elems = m * ldh;
   }
-  const int total = (int)(m * (k / 4));
+  const int total = (int)(m * (ldh / 4));
   hipLaunchKernelGGL(k_f32_to_f16, dim3(cdiv(total, 256)), dim3(256), 0, s, d_x, (int)ldx,
                      xh.as<_Float16>(), (int)ldh, (int)m, (int)k);
   SYN_LAUNCH_CHECK();
-  dim3 grid((unsigned)cdiv(n, QBN), (unsigned)cdiv(m, QBM));
+  // split K when the tiles alone cannot fill the GPU (>= 8 steps per split)
+  const int tiles_n = (int)cdiv(n, PGN), tiles_m = (int)cdiv(m, PGM);
+  const int steps = (int)cdiv(k, PGK);
+  int ksplit = 1;
+  if (tiles_n * tiles_m < 256)
+    ksplit = std::max(1, std::min((int)cdiv(384, (size_t)(tiles_n * tiles_m)), steps / 8));
+  const int per = (int)cdiv((size_t)steps, (size_t)ksplit);
+  ksplit = (int)cdiv((size_t)steps, (size_t)per);
+  if (ksplit > 1) {
+    // Y accumulates the splits' partial tiles; a kernel (not a memset node)
+    // clears it so the call can sit in a captured graph
+    if (ldy % 4 || reinterpret_cast<uintptr_t>(d_y) % 16) {
+      for (size_t r = 0; r < m; r++) SYN_TRY(launch_zero_i32(reinterpret_cast<int *>(d_y + r * ldy), n, s));
+    } else {
+      SYN_TRY(launch_zero_i32(reinterpret_cast<int *>(d_y), (m - 1) * ldy + n, s));
+    }
+  }
+  dim3 grid((unsigned)tiles_n, (unsigned)tiles_m, (unsigned)ksplit);
+  const size_t shm = 2 * (size_t)PG_STAGE * sizeof(_Float16);
+  static bool attr_set[4] = {false, false, false, false};
+  const bool exact = fmt != SYN_HIP_FMT_Q8_0 || q8_scales_f16_exact;
+  const int fi = fmt == SYN_HIP_FMT_Q8_0 ? (exact ? 0 : 3) : fmt == SYN_HIP_FMT_Q4_K ? 1 : 2;
+  const void *fns[4] = {(const void *)k_gemm_kq<SYN_HIP_FMT_Q8_0, true>,
+                        (const void *)k_gemm_kq<SYN_HIP_FMT_Q4_K, true>,
+                        (const void *)k_gemm_kq<SYN_HIP_FMT_Q6_K, true>,
+                        (const void *)k_gemm_kq<SYN_HIP_FMT_Q8_0, false>};
+  if (!attr_set[fi]) {  // more than the default 64 KiB of dynamic LDS
+    SYN_HIP(hipFuncSetAttribute(fns[fi], hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm));
+    attr_set[fi] = true;
+  }
   const u32x4 *W = wq.as<u32x4>();
   const uint16_t *Wd = wd.as<uint16_t>();
   const _Float16 *X = xh.as<_Float16>();
-  if (fmt == SYN_HIP_FMT_Q8_0)
-    hipLaunchKernelGGL(k_gemm_kq<SYN_HIP_FMT_Q8_0>, grid, dim3(256), 0, s, X, (int)ldh, (int)m,
-                       (int)k, W, Wd, (int)n, blocks, d_y, (int)ldy);
-  else if (fmt == SYN_HIP_FMT_Q4_K)
-    hipLaunchKernelGGL(k_gemm_kq<SYN_HIP_FMT_Q4_K>, grid, dim3(256), 0, s, X, (int)ldh, (int)m,
-                       (int)k, W, Wd, (int)n, blocks, d_y, (int)ldy);
+  if (fi == 0)
+    hipLaunchKernelGGL((k_gemm_kq<SYN_HIP_FMT_Q8_0, true>), grid, dim3(PGT), shm, s, X, (int)ldh,
+                       (int)m, (int)k, W, Wd, (int)n, blocks, d_y, (int)ldy, per);
+  else if (fi == 3)
+    hipLaunchKernelGGL((k_gemm_kq<SYN_HIP_FMT_Q8_0, false>), grid, dim3(PGT), shm, s, X,
+                       (int)ldh, (int)m, (int)k, W, Wd, (int)n, blocks, d_y, (int)ldy, per);
+  else if (fi == 1)
+    hipLaunchKernelGGL((k_gemm_kq<SYN_HIP_FMT_Q4_K, true>), grid, dim3(PGT), shm, s, X, (int)ldh,
+                       (int)m, (int)k, W, Wd, (int)n, blocks, d_y, (int)ldy, per);
   else
-    hipLaunchKernelGGL(k_gemm_kq<SYN_HIP_FMT_Q6_K>, grid, dim3(256), 0, s, X, (int)ldh, (int)m,
-                       (int)k, W, Wd, (int)n, blocks, d_y, (int)ldy);
+    hipLaunchKernelGGL((k_gemm_kq<SYN_HIP_FMT_Q6_K, true>), grid, dim3(PGT), shm, s, X, (int)ldh,
+                       (int)m, (int)k, W, Wd, (int)n, blocks, d_y, (int)ldy, per);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
 }

@@ -1,0 +1,171 @@
+// Achievable-peak probes of the GPU the library runs on (harness helpers,
+// no reference counterpart): dense MFMA loops for f16 and i8, and an HBM
+// streaming read.  The roofline fractions the benchmark reports use the
+// published peaks; these give the measured ceilings beside them.
+#include "common.hpp"
+
+namespace syn {
+
+typedef _Float16 pf16x8 __attribute__((ext_vector_type(8)));
+typedef float pf32x4 __attribute__((ext_vector_type(4)));
+
+// 8 independent accumulator chains per wave; operands change each iteration
+// so nothing is hoisted
+__global__ void __launch_bounds__(256) k_probe_mfma_f16(int iters, float *__restrict__ out) {
+  pf16x8 a, b;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    a[i] = (_Float16)(0.001f * (float)(threadIdx.x + i));
+    b[i] = (_Float16)(0.002f * (float)(threadIdx.x - i));
+  }
+  pf32x4 acc[8];
+#pragma unroll
+  for (int c = 0; c < 8; c++) acc[c] = pf32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int it = 0; it < iters; it++) {
+#pragma unroll
+    for (int c = 0; c < 8; c++) acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[c], 0, 0, 0);
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 8; c++) s += acc[c][0] + acc[c][1] + acc[c][2] + acc[c][3];
+  if (s == 12345.678f) out[blockIdx.x] = s;  // keeps the loop alive; never true in practice
+}
+
+typedef float pf32x16 __attribute__((ext_vector_type(16)));
+
+__global__ void __launch_bounds__(256) k_probe_mfma_f16_32(int iters, float *__restrict__ out) {
+  pf16x8 a, b;
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    a[i] = (_Float16)(0.001f * (float)(threadIdx.x + i));
+    b[i] = (_Float16)(0.002f * (float)(threadIdx.x - i));
+  }
+  pf32x16 acc[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[c][r] = 0.0f;
+  for (int it = 0; it < iters; it++) {
+#pragma unroll
+    for (int c = 0; c < 4; c++)
+      acc[c] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, acc[c], 0, 0, 0);
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 4; c++) s += acc[c][0] + acc[c][5] + acc[c][10] + acc[c][15];
+  if (s == 12345.678f) out[blockIdx.x] = s;
+}
+
+__global__ void __launch_bounds__(256) k_probe_mfma_i8(int iters, int *__restrict__ out) {
+  i32x4 a, b;
+  a = i32x4{(int)threadIdx.x, 3, 5, 7};
+  b = i32x4{11, (int)threadIdx.x, 13, 17};
+  i32x4 acc[8];
+#pragma unroll
+  for (int c = 0; c < 8; c++) acc[c] = i32x4{0, 0, 0, 0};
+  for (int it = 0; it < iters; it++) {
+#pragma unroll
+    for (int c = 0; c < 8; c++) acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc[c], 0, 0, 0);
+  }
+  int s = 0;
+#pragma unroll
+  for (int c = 0; c < 8; c++) s += acc[c][0] + acc[c][1] + acc[c][2] + acc[c][3];
+  if (s == 123456789) out[blockIdx.x] = s;
+}
+
+// streaming read: each thread sums 16-byte words over a grid-stride loop
+__global__ void __launch_bounds__(256) k_probe_read(const i32x4 *__restrict__ p, size_t n16,
+                                                    int *__restrict__ out) {
+  i32x4 s = i32x4{0, 0, 0, 0};
+  const size_t stride = (size_t)gridDim.x * 256;
+  size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const i32x4 a = __builtin_nontemporal_load(p + i), b = __builtin_nontemporal_load(p + i + stride);
+    const i32x4 c = __builtin_nontemporal_load(p + i + 2 * stride),
+                d = __builtin_nontemporal_load(p + i + 3 * stride);
+    s += a ^ b ^ c ^ d;
+  }
+  for (; i < n16; i += stride) s += __builtin_nontemporal_load(p + i);
+  if ((s.x ^ s.y ^ s.z ^ s.w) == 0x5eed5eed) out[blockIdx.x] = 1;
+}
+
+}  // namespace syn
+
+using namespace syn;
+
+extern "C" syn_status_t syn_hip_probe_mfma(int kind, size_t iters, double *tflops) {
+  if (!tflops) return SYN_ERR_NULL_PTR;
+  if (iters == 0 || iters > (1u << 24) || kind < 0 || kind > 2) return SYN_ERR_INVALID_ARG;
+  SYN_TRY(ensure_init());
+  int dev = 0, cus = 256;
+  SYN_HIP(hipGetDevice(&dev));
+  SYN_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  const int blocks = cus * 8;  // 8 waves per SIMD
+  DevBuf out;
+  SYN_TRY(out.alloc((size_t)blocks * 4));
+  hipStream_t s = default_stream();
+  hipEvent_t a, b;
+  SYN_HIP(hipEventCreate(&a));
+  SYN_HIP(hipEventCreate(&b));
+  for (int rep = 0; rep < 2; rep++) {  // the first run warms up clocks
+    SYN_HIP(hipEventRecord(a, s));
+    if (kind == 0)
+      hipLaunchKernelGGL(k_probe_mfma_f16, dim3(blocks), dim3(256), 0, s, (int)iters,
+                         out.as<float>());
+    else if (kind == 1)
+      hipLaunchKernelGGL(k_probe_mfma_i8, dim3(blocks), dim3(256), 0, s, (int)iters,
+                         out.as<int>());
+    else
+      hipLaunchKernelGGL(k_probe_mfma_f16_32, dim3(blocks), dim3(256), 0, s, (int)iters,
+                         out.as<float>());
+    SYN_LAUNCH_CHECK();
+    SYN_HIP(hipEventRecord(b, s));
+    SYN_HIP(hipEventSynchronize(b));
+  }
+  float ms = 0.0f;
+  SYN_HIP(hipEventElapsedTime(&ms, a, b));
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  // per MFMA: 16x16x32 f16 = 16384 flops (8 chains); 16x16x64 i8 = 32768
+  // ops (8 chains); 32x32x16 f16 = 32768 flops (4 chains)
+  const double per = kind == 0 ? 16384.0 : 32768.0;
+  const double chains = kind == 2 ? 4.0 : 8.0;
+  const double ops = (double)blocks * 4 /* waves */ * chains * (double)iters * per;
+  *tflops = ops / ((double)ms * 1e-3) / 1e12;
+  return SYN_OK;
+}
+
+extern "C" syn_status_t syn_hip_probe_hbm_read(size_t bytes, double *gb_s) {
+  if (!gb_s) return SYN_ERR_NULL_PTR;
+  if (bytes < (1u << 20)) return SYN_ERR_INVALID_ARG;
+  SYN_TRY(ensure_init());
+  bytes &= ~(size_t)15;
+  DevBuf buf, out;
+  SYN_TRY(buf.alloc(bytes));
+  hipStream_t s = default_stream();
+  SYN_HIP(hipMemsetAsync(buf.p, 1, bytes, s));
+  int dev = 0, cus = 256;
+  SYN_HIP(hipGetDevice(&dev));
+  SYN_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  const int blocks = cus * 16;
+  SYN_TRY(out.alloc((size_t)blocks * 4));
+  hipEvent_t a, b;
+  SYN_HIP(hipEventCreate(&a));
+  SYN_HIP(hipEventCreate(&b));
+  float best = 1e30f;
+  for (int rep = 0; rep < 4; rep++) {
+    SYN_HIP(hipEventRecord(a, s));
+    hipLaunchKernelGGL(k_probe_read, dim3(blocks), dim3(256), 0, s, buf.as<i32x4>(), bytes / 16,
+                       out.as<int>());
+    SYN_LAUNCH_CHECK();
+    SYN_HIP(hipEventRecord(b, s));
+    SYN_HIP(hipEventSynchronize(b));
+    float ms = 0.0f;
+    SYN_HIP(hipEventElapsedTime(&ms, a, b));
+    if (rep > 0 && ms < best) best = ms;
+  }
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  *gb_s = (double)bytes / ((double)best * 1e-3) / 1e9;
+  return SYN_OK;
+}

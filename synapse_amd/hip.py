@@ -113,6 +113,8 @@ SIGNATURES = {
     "syn_hip_mamba_decode_timed": (ST, [P, SZ, C.POINTER(C.c_float)]),
     "syn_hip_mamba_destroy": (ST, [P]),
     "syn_hip_fill_normal": (ST, [P, SZ, C.c_uint64, C.c_float]),
+    "syn_hip_probe_mfma": (ST, [C.c_int, SZ, C.POINTER(C.c_double)]),
+    "syn_hip_probe_hbm_read": (ST, [SZ, C.POINTER(C.c_double)]),
     "syn_hip_eval_expf": (ST, [P, P, SZ, P]),
     "syn_hip_kquant_encode": (ST, [C.c_int, SZ, SZ, P, P]),
 }
@@ -582,3 +584,17 @@ def fill_normal(n: int, seed: int, std: float = 1.0) -> np.ndarray:
     out = np.empty(n, np.float32)
     check(lib().syn_hip_fill_normal(ptr(out), n, seed, std))
     return out
+
+
+def probe_mfma(kind: int, iters: int = 20000) -> float:
+    """Measured dense MFMA rate: kind 0 = f16 (TFLOP/s), 1 = i8 (TOP/s)."""
+    v = C.c_double()
+    check(lib().syn_hip_probe_mfma(kind, iters, C.byref(v)), "probe_mfma")
+    return v.value
+
+
+def probe_hbm_read(nbytes: int = 4 << 30) -> float:
+    """Measured streaming-read bandwidth of HBM (GB/s)."""
+    v = C.c_double()
+    check(lib().syn_hip_probe_hbm_read(nbytes, C.byref(v)), "probe_hbm_read")
+    return v.value
