@@ -246,6 +246,9 @@ syn_status_t syn_hip_klm_generate(syn_hip_klm_t *m, const uint32_t *prompt, size
 /* hipEvent timing of one prefill of `prompt` and `steps` greedy decode steps. */
 syn_status_t syn_hip_klm_time(syn_hip_klm_t *m, const uint32_t *prompt, size_t n_prompt,
                               size_t steps, float *prefill_ms, float *decode_ms);
+/* Decode steps replay a captured HIP graph (graph != 0, the default) or launch
+ * the same kernels eagerly (for profilers that do not follow graph launches). */
+syn_status_t syn_hip_klm_set_options(syn_hip_klm_t *m, int graph);
 syn_status_t syn_hip_klm_destroy(syn_hip_klm_t *m);
 
 /* -- INT8 Mamba: QuantizedMambaModel (quantization/ssm/int8_mamba.rs:21-224).
@@ -271,6 +274,9 @@ syn_status_t syn_hip_mamba_decode_one(syn_hip_mamba_t *m, uint32_t token, float 
 syn_status_t syn_hip_mamba_generate(syn_hip_mamba_t *m, const uint32_t *prompt, size_t n_prompt,
                                     size_t max_new, uint32_t *out_tokens, float *out_margins);
 syn_status_t syn_hip_mamba_decode_timed(syn_hip_mamba_t *m, size_t steps, float *elapsed_ms);
+/* Token steps replay a captured HIP graph (graph != 0, the default) or launch
+ * the same kernels eagerly. */
+syn_status_t syn_hip_mamba_set_options(syn_hip_mamba_t *m, int graph);
 syn_status_t syn_hip_mamba_destroy(syn_hip_mamba_t *m);
 
 /* -- harness helpers (no reference counterpart) -- */

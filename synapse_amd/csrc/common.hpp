@@ -75,6 +75,7 @@ struct DevBuf {
 };
 
 inline size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+__host__ __device__ inline int round_up4(int x) { return (x + 3) & ~3; }
 inline size_t cdiv(size_t x, size_t a) { return (x + a - 1) / a; }
 
 // ---------------------------------------------------------------- host f16

@@ -27,6 +27,7 @@
 
 #include "decode_fused.hpp"
 #include "linear.hpp"
+#include "reduce_order.hpp"
 
 namespace syn {
 
@@ -59,18 +60,13 @@ static __device__ unsigned long long syn_phase_ts[256];
 
 // ------------------------------------------------------------------ helpers
 __device__ __forceinline__ float row_value(const RowSrc &s, int r) {
+  if (s.f) return s.f[r];
   const float f = (float)s.acc[r] * s.sx[0];
   return f * s.ws[r];
 }
 
 // Rows of a prologue vector held per thread: element j = threadIdx.x + u*NT.
 constexpr int RB = 8;
-
-template <int NT>
-__device__ __forceinline__ void bar() {
-  if constexpr (NT > 64) __syncthreads();
-  else __builtin_amdgcn_wave_barrier();
-}
 
 // One step of a wave max over non-negative values through a DPP lane move;
 // lanes whose source is outside the row/wave read 0, which max ignores.
@@ -107,100 +103,6 @@ __device__ __forceinline__ float wg_max_get(const float *red, int slot) {
 #pragma unroll
   for (int i = 1; i < NT / 64; i++) m = fmaxf(m, red[slot + i]);
   return m;
-}
-
-// Chains of the reference sum-of-squares order (syn_vmul + syn_vreduce_sum,
-// exports.zig:366-375, 503-514): acc[l] = sequential sum of sq[4i+l] over the
-// 4-aligned prefix, combined as ((a0+a1)+a2)+a3, then the tail in order.
-// sq holds the squares of the prefix transposed (chain l contiguous at
-// sq[l*q4 ..]) followed by the tail squares at sq[n4 ..]; lanes 0-3 run the
-// chains, loading the next 32 values while adding the current 32.  Callers
-// place a barrier between writing sq and this call; red[32..35] is used.
-template <int NT>
-__device__ float sumsq_chains(const float *sq, int n, float *red) {
-  const int n4 = n & ~3, q4 = n4 >> 2;
-  if (threadIdx.x < 4) {
-    const float *p = sq + threadIdx.x * q4;
-    float acc = 0.0f;
-    int i = 0;
-    if (q4 > 0 && (q4 & 31) == 0) {
-      const float4 *p4 = reinterpret_cast<const float4 *>(p);
-      const int groups = q4 >> 5;
-      float4 a[8];
-#pragma unroll
-      for (int k = 0; k < 8; k++) a[k] = p4[k];
-      for (int gi = 0; gi < groups; gi++) {
-        const int nx = min(gi + 1, groups - 1) * 8;
-        float4 b[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) b[k] = p4[nx + k];
-#pragma unroll
-        for (int k = 0; k < 8; k++) {
-          acc = acc + a[k].x;
-          acc = acc + a[k].y;
-          acc = acc + a[k].z;
-          acc = acc + a[k].w;
-        }
-#pragma unroll
-        for (int k = 0; k < 8; k++) a[k] = b[k];
-      }
-      i = q4;
-    } else if ((q4 & 3) == 0) {
-      for (; i + 16 <= q4; i += 16) {
-        const float4 a = *reinterpret_cast<const float4 *>(p + i);
-        const float4 b = *reinterpret_cast<const float4 *>(p + i + 4);
-        const float4 c = *reinterpret_cast<const float4 *>(p + i + 8);
-        const float4 d = *reinterpret_cast<const float4 *>(p + i + 12);
-        acc = acc + a.x; acc = acc + a.y; acc = acc + a.z; acc = acc + a.w;
-        acc = acc + b.x; acc = acc + b.y; acc = acc + b.z; acc = acc + b.w;
-        acc = acc + c.x; acc = acc + c.y; acc = acc + c.z; acc = acc + c.w;
-        acc = acc + d.x; acc = acc + d.y; acc = acc + d.z; acc = acc + d.w;
-      }
-    }
-    for (; i < q4; i++) acc = acc + p[i];
-    red[32 + threadIdx.x] = acc;
-  }
-  bar<NT>();
-  float s = ((red[32] + red[33]) + red[34]) + red[35];
-  for (int i = n4; i < n; i++) s = s + sq[i];
-  return s;
-}
-
-// where the square of element j goes in the sumsq_chains layout
-__device__ __forceinline__ int sq_slot(int j, int n) {
-  const int n4 = n & ~3;
-  return j < n4 ? (j & 3) * (n4 >> 2) + (j >> 2) : j;
-}
-
-// Sum of squares of v[0..n) held in LDS, reference order.
-template <int NT>
-__device__ float sumsq_lds(const float *v, int n, float *sq, float *red) {
-  for (int j = threadIdx.x; j < n; j += NT) {
-    const float x = v[j];
-    sq[sq_slot(j, n)] = x * x;
-  }
-  bar<NT>();
-  return sumsq_chains<NT>(sq, n, red);
-}
-
-// Sequential sum of v[0..n) (a single accumulator, in index order).
-__device__ __forceinline__ float seq_sum(const float *v, int n) {
-  float s = 0.0f;
-  int i = 0;
-  if ((reinterpret_cast<uintptr_t>(v) & 15) == 0) {
-    for (; i + 16 <= n; i += 16) {
-      const float4 a = *reinterpret_cast<const float4 *>(v + i);
-      const float4 b = *reinterpret_cast<const float4 *>(v + i + 4);
-      const float4 c = *reinterpret_cast<const float4 *>(v + i + 8);
-      const float4 d = *reinterpret_cast<const float4 *>(v + i + 12);
-      s = s + a.x; s = s + a.y; s = s + a.z; s = s + a.w;
-      s = s + b.x; s = s + b.y; s = s + b.z; s = s + b.w;
-      s = s + c.x; s = s + c.y; s = s + c.z; s = s + c.w;
-      s = s + d.x; s = s + d.y; s = s + d.z; s = s + d.w;
-    }
-  }
-  for (; i < n; i++) s = s + v[i];
-  return s;
 }
 
 // quantizePerChannelInt8 (quantize.zig:12-47) of a row held in registers
@@ -770,6 +672,7 @@ __device__ __forceinline__ float wave_max_any(float v) {
 constexpr int kAttnPass = 256;  // positions per score pass (4 waves x 64)
 constexpr int kPre = 48;        // prefetch registers (float4) per lane
 
+template <bool F32>
 __global__ void __launch_bounds__(512)
     k_fused_attention_fast(RowSrc qkv, int nh, int nkv, int hd, const float *__restrict__ qn,
                            const float *__restrict__ kn, float eps,
@@ -820,17 +723,23 @@ __global__ void __launch_bounds__(512)
     for (int i = 0; i < kPre; i++) pre[i] = src[(size_t)min(i, ngroups - 1) * hd];
   } else {
     const int dc = min(dcol, hd - 1), hc = min(dcol, half - 1);
-    aq = qkv.acc[head * hd + dc];
-    ak = qkv.acc[qd + kvh * hd + dc];
-    av = qkv.acc[qd + kvd + kvh * hd + dc];
-    wq = qkv.ws[head * hd + dc];
-    wk = qkv.ws[qd + kvh * hd + dc];
-    wv = qkv.ws[qd + kvd + kvh * hd + dc];
+    if constexpr (F32) {  // f32 rows: carried in wq/wk/wv
+      wq = qkv.f[head * hd + dc];
+      wk = qkv.f[qd + kvh * hd + dc];
+      wv = qkv.f[qd + kvd + kvh * hd + dc];
+    } else {
+      aq = qkv.acc[head * hd + dc];
+      ak = qkv.acc[qd + kvh * hd + dc];
+      av = qkv.acc[qd + kvd + kvh * hd + dc];
+      wq = qkv.ws[head * hd + dc];
+      wk = qkv.ws[qd + kvh * hd + dc];
+      wv = qkv.ws[qd + kvd + kvh * hd + dc];
+    }
     gq = qn ? qn[dc] : 0.0f;
     gk = kn ? kn[dc] : 0.0f;
     cs = cosT[(size_t)pos * half + hc];
     sn = sinT[(size_t)pos * half + hc];
-    qsx = qkv.sx[0];
+    if constexpr (!F32) qsx = qkv.sx[0];
   }
   asm volatile("" ::: "memory");
   SYN_TS(1);
@@ -839,10 +748,16 @@ __global__ void __launch_bounds__(512)
   const bool pro_lane = pro_wave && d < hd;
   if (tid < 32) exp_tab[tid] = tv;
   if (pro_lane) {
-    float f;
-    f = (float)aq * qsx; qv[d] = f * wq;
-    f = (float)ak * qsx; kv[d] = f * wk;
-    f = (float)av * qsx; vv[d] = f * wv;
+    if constexpr (F32) {
+      qv[d] = wq;
+      kv[d] = wk;
+      vv[d] = wv;
+    } else {
+      float f;
+      f = (float)aq * qsx; qv[d] = f * wq;
+      f = (float)ak * qsx; kv[d] = f * wk;
+      f = (float)av * qsx; vv[d] = f * wv;
+    }
   }
   __syncthreads();
   SYN_TS(2);
@@ -1027,8 +942,12 @@ syn_status_t launch_fused_attention(RowSrc qkv, int nh, int nkv, int hd, const f
       set_error("fused decode: expf table address unavailable");
       return SYN_ERR_HIP;
     }
-    hipLaunchKernelGGL(k_fused_attention_fast, dim3(nh), dim3(512), shm, s, qkv, nh, nkv, hd, qn,
-                       kn, eps, cosT, sinT, tab, st, kc, vc, max_seq, out);
+    if (qkv.f)
+      hipLaunchKernelGGL(k_fused_attention_fast<true>, dim3(nh), dim3(512), shm, s, qkv, nh, nkv,
+                         hd, qn, kn, eps, cosT, sinT, tab, st, kc, vc, max_seq, out);
+    else
+      hipLaunchKernelGGL(k_fused_attention_fast<false>, dim3(nh), dim3(512), shm, s, qkv, nh, nkv,
+                         hd, qn, kn, eps, cosT, sinT, tab, st, kc, vc, max_seq, out);
   } else {
     hipLaunchKernelGGL(k_fused_attention, dim3(nh), dim3(256), shm, s, qkv, nh, nkv, hd, qn, kn,
                        eps, cosT, sinT, st, kc, vc, max_seq, out);

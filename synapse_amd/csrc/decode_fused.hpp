@@ -10,10 +10,13 @@ namespace syn {
 //   value(r) = (f32(acc[r]) * sx[0]) * ws[r]
 // (the M <= 16 epilogue of int8GemvRow, qmatmul.zig:171-256), where acc is
 // the exact int32 dot product, accumulated over the K split with atomics.
+// With `f` set the rows are a plain f32 vector instead: value(r) = f[r]
+// (the f32 decoders' GEMV outputs).
 struct RowSrc {
   const int *acc = nullptr;
   const float *sx = nullptr;
   const float *ws = nullptr;
+  const float *f = nullptr;
 };
 
 // One INT8 linear in the panel layout, with the K split used in the step.

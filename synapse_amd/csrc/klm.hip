@@ -9,6 +9,7 @@
 #include <thread>
 #include <vector>
 
+#include "decode_fused.hpp"
 #include "kquant.hpp"
 #include "layer_ops.hpp"
 
@@ -31,6 +32,7 @@ struct syn_hip_klm_s {
   hipStream_t stream = nullptr;
   hipGraphExec_t graph = nullptr;
   bool finalized = false;
+  bool use_graph = true;  // replay the captured decode step, else launch eagerly
 
   ~syn_hip_klm_s() {
     if (graph) (void)hipGraphExecDestroy(graph);
@@ -131,16 +133,26 @@ struct syn_hip_klm_s {
                                  ones_h.as<float>(), eps, rows, (int)h, nullptr, 0, nullptr,
                                  normed.as<float>(), s));
     SYN_TRY(Ly.qkv.gemv(rows, normed.as<float>(), h, qkv.as<float>(), n_qkv, s));
-    SYN_TRY(launch_qk_norm_rope_kv(qkv.as<float>(), (int)n_qkv, rows, nh, nkv, (int)hd, qn, qn,
-                                   eps, rope_cos.as<float>(), rope_sin.as<float>(),
-                                   prefill ? nullptr : &st()->pos, 0, qrot.as<float>(), kc_l(l),
-                                   vc_l(l), (int)S, s));
-    if (prefill)
-      SYN_TRY(launch_attention_prefill(qrot.as<float>(), kc_l(l), vc_l(l), rows, nh, nkv,
-                                       (int)hd, (int)S, nullptr, attn.as<float>(), s));
-    else
-      SYN_TRY(launch_attention_decode(qrot.as<float>(), kc_l(l), vc_l(l), &st()->pos, nh, nkv,
-                                      (int)hd, scores.as<float>(), (int)S, attn.as<float>(), s));
+    if (!prefill && fused_attention_fits((int)hd, (int)S)) {
+      // one kernel per query head: head norms, RoPE, KV append and attention
+      RowSrc src;
+      src.f = qkv.as<float>();
+      SYN_TRY(launch_fused_attention(src, nh, nkv, (int)hd, qn, qn, eps, rope_cos.as<float>(),
+                                     rope_sin.as<float>(), st(), kc_l(l), vc_l(l), (int)S,
+                                     attn.as<float>(), s));
+    } else {
+      SYN_TRY(launch_qk_norm_rope_kv(qkv.as<float>(), (int)n_qkv, rows, nh, nkv, (int)hd, qn, qn,
+                                     eps, rope_cos.as<float>(), rope_sin.as<float>(),
+                                     prefill ? nullptr : &st()->pos, 0, qrot.as<float>(),
+                                     kc_l(l), vc_l(l), (int)S, s));
+      if (prefill)
+        SYN_TRY(launch_attention_prefill(qrot.as<float>(), kc_l(l), vc_l(l), rows, nh, nkv,
+                                         (int)hd, (int)S, nullptr, attn.as<float>(), s));
+      else
+        SYN_TRY(launch_attention_decode(qrot.as<float>(), kc_l(l), vc_l(l), &st()->pos, nh, nkv,
+                                        (int)hd, scores.as<float>(), (int)S, attn.as<float>(),
+                                        s));
+    }
     SYN_TRY(Ly.o.gemv(rows, attn.as<float>(), qd, o.as<float>(), h, s));
     SYN_TRY(launch_rmsnorm_quant(x.as<float>(), o.as<float>(), ones_h.as<float>(), eps, rows,
                                  (int)h, nullptr, 0, nullptr, normed.as<float>(), s));
@@ -185,6 +197,14 @@ struct syn_hip_klm_s {
       graph = nullptr;
       return hip_fail(e, "hipGraphInstantiate", __FILE__, __LINE__);
     }
+    return SYN_OK;
+  }
+
+  // one decode step on `stream`: graph replay or the same kernels launched eagerly
+  syn_status_t run_step() {
+    if (!use_graph) return decode_step(stream);
+    SYN_TRY(build_graph());
+    SYN_HIP(hipGraphLaunch(graph, stream));
     return SYN_OK;
   }
 
@@ -399,9 +419,8 @@ syn_status_t syn_hip_klm_forward_one(syn_hip_klm_t *m, uint32_t token, float *ho
     set_error("KV cache full");
     return SYN_ERR_INVALID_ARG;
   }
-  SYN_TRY(m->build_graph());
   SYN_TRY(m->set_state(cur.pos, token, cur.step));
-  SYN_HIP(hipGraphLaunch(m->graph, m->stream));
+  SYN_TRY(m->run_step());
   if (host_logits)
     SYN_HIP(hipMemcpyAsync(host_logits, m->logits.p, m->vocab * 4, hipMemcpyDeviceToHost,
                            m->stream));
@@ -418,9 +437,9 @@ syn_status_t syn_hip_klm_generate(syn_hip_klm_t *m, const uint32_t *prompt, size
     set_error("prompt + generated tokens exceed max_seq");
     return SYN_ERR_INVALID_ARG;
   }
-  SYN_TRY(m->build_graph());
+  if (m->use_graph) SYN_TRY(m->build_graph());
   SYN_TRY(m->prefill(prompt, n_prompt));
-  for (size_t i = 1; i < max_new; i++) SYN_HIP(hipGraphLaunch(m->graph, m->stream));
+  for (size_t i = 1; i < max_new; i++) SYN_TRY(m->run_step());
   SYN_HIP(hipMemcpyAsync(out_tokens, m->history.p, max_new * 4, hipMemcpyDeviceToHost,
                          m->stream));
   if (out_margins)
@@ -438,7 +457,7 @@ syn_status_t syn_hip_klm_time(syn_hip_klm_t *m, const uint32_t *prompt, size_t n
     set_error("prompt + decode steps exceed max_seq");
     return SYN_ERR_INVALID_ARG;
   }
-  SYN_TRY(m->build_graph());
+  if (m->use_graph) SYN_TRY(m->build_graph());
   hipEvent_t a, b, c;
   SYN_HIP(hipEventCreate(&a));
   SYN_HIP(hipEventCreate(&b));
@@ -451,7 +470,7 @@ syn_status_t syn_hip_klm_time(syn_hip_klm_t *m, const uint32_t *prompt, size_t n
   for (size_t l = 0; l < m->L; l++) SYN_TRY(m->layer(l, (int)n_prompt, true, m->stream));
   SYN_TRY(m->head((int)n_prompt - 1, (int)n_prompt, m->stream));
   SYN_HIP(hipEventRecord(b, m->stream));
-  for (size_t i = 0; i < steps; i++) SYN_HIP(hipGraphLaunch(m->graph, m->stream));
+  for (size_t i = 0; i < steps; i++) SYN_TRY(m->run_step());
   SYN_HIP(hipEventRecord(c, m->stream));
   SYN_HIP(hipEventSynchronize(c));
   SYN_HIP(hipEventElapsedTime(prefill_ms, a, b));
@@ -459,6 +478,12 @@ syn_status_t syn_hip_klm_time(syn_hip_klm_t *m, const uint32_t *prompt, size_t n
   (void)hipEventDestroy(a);
   (void)hipEventDestroy(b);
   (void)hipEventDestroy(c);
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_klm_set_options(syn_hip_klm_t *m, int graph) {
+  if (!m) return SYN_ERR_NULL_PTR;
+  m->use_graph = graph != 0;
   return SYN_OK;
 }
 

@@ -4,6 +4,7 @@
 // __builtin_fmaf only where the reference uses @mulAdd), so the token stream
 // matches the cpu_simd path bit for bit.
 #include "layer_ops.hpp"
+#include "reduce_order.hpp"
 
 namespace syn {
 
@@ -99,44 +100,56 @@ __device__ void quantize_row_lds(const float *v, int n, int8_t *q, float *scale_
 
 // ------------------------------------------------------------------ RMSNorm + quantize
 // ops/norm.rs:8-38: out = (x*w) * (1/sqrt(sumsq/n + eps)); then A1 on out.
-__global__ void __launch_bounds__(256)
+// One workgroup of NT threads per row.  The squares are written in the
+// sumsq_chains layout, so the four reference chains run from LDS with
+// 16-byte loads.  dynamic LDS: v[H] | sq[H]
+template <int NT>
+__global__ void __launch_bounds__(NT)
     k_rmsnorm_quant(float *__restrict__ x, const float *__restrict__ delta,
                     const float *__restrict__ w, float eps, int H, int8_t *__restrict__ xq,
                     int ldq, float *__restrict__ sx, float *__restrict__ normed) {
-  extern __shared__ float sm[];  // H
+  extern __shared__ __align__(16) float sm[];
   __shared__ float red[64];
-  __shared__ float s_scale;
+  float *v = sm, *sq = sm + round_up4(H);
   const int row = blockIdx.x;
   float *xr = x + (size_t)row * H;
-  for (int j = threadIdx.x; j < H; j += blockDim.x) {
-    float v = xr[j];
+  for (int j = threadIdx.x; j < H; j += NT) {
+    float a = xr[j];
     if (delta) {
-      v = v + delta[(size_t)row * H + j];
-      xr[j] = v;
+      a = a + delta[(size_t)row * H + j];
+      xr[j] = a;
     }
-    sm[j] = v;
+    v[j] = a;
+    sq[sq_slot(j, H)] = a * a;
   }
   __syncthreads();
-  const float ss = sumsq_vec4_order(sm, H, red);
-  if (threadIdx.x == 0) s_scale = 1.0f / sqrtf(ss / (float)H + eps);
-  __syncthreads();
-  const float scale = s_scale;
-  for (int j = threadIdx.x; j < H; j += blockDim.x) {
-    const float t = sm[j] * w[j];
+  const float ss = sumsq_chains<NT>(sq, H, red);
+  const float scale = 1.0f / sqrtf(ss / (float)H + eps);
+  for (int j = threadIdx.x; j < H; j += NT) {
+    const float t = v[j] * w[j];
     const float nv = t * scale;
-    sm[j] = nv;
+    v[j] = nv;
     if (normed) normed[(size_t)row * H + j] = nv;
   }
   if (!xq) return;  // f32 path: normed rows only
   __syncthreads();
-  quantize_row_lds(sm, H, xq + (size_t)row * ldq, sx + row, red);
+  quantize_row_lds(v, H, xq + (size_t)row * ldq, sx + row, red);
 }
 
 syn_status_t launch_rmsnorm_quant(float *x, const float *delta, const float *w, float eps,
                                   int rows, int hidden, int8_t *xq, int ldq, float *sx,
                                   float *normed, hipStream_t s) {
-  hipLaunchKernelGGL(k_rmsnorm_quant, dim3(rows), dim3(256), hidden * sizeof(float), s, x, delta,
-                     w, eps, hidden, xq, ldq, sx, normed);
+  const size_t shm = 2 * round_up((size_t)hidden, 4) * sizeof(float);
+  if (shm > 64 * 1024) {
+    set_error("rmsnorm: hidden size too large for the LDS row");
+    return SYN_ERR_INVALID_ARG;
+  }
+  if (hidden >= 2048)
+    hipLaunchKernelGGL(k_rmsnorm_quant<1024>, dim3(rows), dim3(1024), shm, s, x, delta, w, eps,
+                       hidden, xq, ldq, sx, normed);
+  else
+    hipLaunchKernelGGL(k_rmsnorm_quant<256>, dim3(rows), dim3(256), shm, s, x, delta, w, eps,
+                       hidden, xq, ldq, sx, normed);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
 }

@@ -116,14 +116,51 @@ __global__ void k_mamba_conv(const float *__restrict__ proj, float *__restrict__
 // split, so it is spread over time instead of over lanes: each of the 16
 // waves requests its K/16 slice of the panel at entry (all loads in flight at
 // once) and the running sums pass from wave to wave through LDS, in k order.
-// A wave requests its slice of the next pass as soon as its turn in the
-// current pass is over, so every pass after the first is loaded in advance.
+// Wave w waits at w barriers, runs its part of the chain, hands the sums on,
+// requests its slice of the next pass and then waits at the remaining
+// 16 - w barriers of the pass: every wave meets the same barriers, and the
+// loads are issued in straight-line code (no branch holds them back), so
+// each pass after the first is already loaded when its turn comes.
 constexpr int kChainWaves = 16, kChainG = 16;  // waves, float4 groups per wave and pass
 
+// Part of a row's chain over the groups gw .. gw+15 (k = 4*gw ...), with
+// the activations of the part in xa (the same for every lane).  In the TAIL
+// form (the part reaches past K) terms with k >= K are skipped by a select,
+// so the chain is exactly the reference's.
+template <bool FUSED, bool TAIL>
+__device__ __forceinline__ float f32_chain_part(float acc, const float4 (&v)[kChainG],
+                                                const float (&xa)[4 * kChainG], int gw, int K) {
+#pragma unroll
+  for (int u = 0; u < kChainG; u++) {
+    const float wa[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      float nacc;
+      if (FUSED) {
+        nacc = __builtin_fmaf(xa[4 * u + c], wa[c], acc);
+      } else {
+        const float t = xa[4 * u + c] * wa[c];
+        nacc = acc + t;
+      }
+      acc = (!TAIL || (gw + u) * 4 + c < K) ? nacc : acc;
+    }
+  }
+  return acc;
+}
+
+template <bool FUSED>
+__device__ __forceinline__ float f32_chain_any(float acc, const float4 (&v)[kChainG],
+                                               const float (&xa)[4 * kChainG], int gw, int K) {
+  if ((gw + kChainG) * 4 <= K) return f32_chain_part<FUSED, false>(acc, v, xa, gw, K);
+  return f32_chain_part<FUSED, true>(acc, v, xa, gw, K);
+}
+
+// The activation row is read with wave-uniform addresses (scalar loads into
+// SGPRs, which the FMAs take as operands), padded to whole passes in `xpad`
+// by the caller so that every read is in bounds.
 __global__ void __launch_bounds__(1024)
-    k_gemv_f32_exact(const float4 *__restrict__ Wp, const float *__restrict__ x, int N, int K,
+    k_gemv_f32_exact(const float4 *__restrict__ Wp, const float *__restrict__ xpad, int N, int K,
                      int n8, float *__restrict__ y) {
-  extern __shared__ __align__(16) float xs[];  // K rounded to 4
   __shared__ float carry[64];
   const int panel = blockIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -131,56 +168,66 @@ __global__ void __launch_bounds__(1024)
   const int K4 = (K + 3) >> 2;
   const int row = panel * 64 + lane;
   const bool fused = row < n8;
+  const bool all_fused = panel * 64 + 64 <= n8;  // uniform over the workgroup
   const float4 *w = Wp + (size_t)panel * K4 * 64 + lane;
   constexpr int per_pass = kChainWaves * kChainG;  // float4 groups per pass
   float4 v[kChainG];
+  float xa[4 * kChainG];
   auto load = [&](int g0) {
     const int gw = g0 + wave * kChainG;
 #pragma unroll
     for (int u = 0; u < kChainG; u++) v[u] = w[(size_t)min(gw + u, K4 - 1) * 64];
-  };
-  load(0);
-  for (int k = threadIdx.x; k < K; k += 1024) xs[k] = x[k];
-  __syncthreads();
-  float acc = 0.0f;
-  for (int g0 = 0; g0 < K4; g0 += per_pass) {
-    const int gw = g0 + wave * kChainG;
-    for (int wv = 0; wv < kChainWaves; wv++) {
-      if (wave == wv) {
-        acc = (g0 == 0 && wv == 0) ? 0.0f : carry[lane];
+    const float4 *x4 = reinterpret_cast<const float4 *>(xpad) + gw;
 #pragma unroll
-        for (int u = 0; u < kChainG; u++) {
-          const int kb = (gw + u) * 4;
-          const float vv[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-#pragma unroll
-          for (int c = 0; c < 4; c++) {
-            if (kb + c < K) {
-              if (fused) {
-                acc = __builtin_fmaf(xs[kb + c], vv[c], acc);
-              } else {
-                const float t = xs[kb + c] * vv[c];
-                acc = acc + t;
-              }
-            }
-          }
-        }
-        carry[lane] = acc;
-        if (g0 + per_pass < K4) load(g0 + per_pass);
-      }
-      __syncthreads();
+    for (int u = 0; u < kChainG; u++) {
+      const float4 t = x4[u];
+      xa[4 * u] = t.x;
+      xa[4 * u + 1] = t.y;
+      xa[4 * u + 2] = t.z;
+      xa[4 * u + 3] = t.w;
     }
+  };
+  // Barriers of a pass: wave w waits at w plain barriers, runs its part,
+  // publishes the sums with a full barrier (LDS write completed first), then
+  // requests the next pass and waits at the remaining plain barriers.  Only
+  // the publishing barrier waits for the wave's outstanding memory counters,
+  // so the next pass's scalar and vector loads stay in flight across the
+  // plain ones; the asm statements keep the compiler from moving LDS
+  // accesses across them.
+  load(0);
+  for (int g0 = 0; g0 < K4; g0 += per_pass) {
+    for (int t = 0; t < wave; t++) __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    float acc = (g0 == 0 && wave == 0) ? 0.0f : carry[lane];
+    const int gw = g0 + wave * kChainG;
+    if (all_fused || fused)
+      acc = f32_chain_any<true>(acc, v, xa, gw, K);
+    else
+      acc = f32_chain_any<false>(acc, v, xa, gw, K);
+    carry[lane] = acc;
+    __syncthreads();
+    load(g0 + per_pass < K4 ? g0 + per_pass : g0);
+    for (int t = wave + 1; t < kChainWaves; t++) __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
   }
+  __syncthreads();
   if (threadIdx.x < 64 && row < N) y[row] = carry[lane];
 }
 
-static syn_status_t launch_gemv_f32_exact(const float *Wp, const float *x, int N, int K, int n8,
-                                          float *y, hipStream_t s) {
-  const size_t shm = round_up((size_t)K, 4) * 4;
-  if (shm > 60 * 1024) {
-    set_error("f32 GEMV: K too large for the LDS activation row");
+// floats the activation buffer of a K-long exact f32 GEMV must hold (whole
+// passes; the pad is read but never used)
+static size_t f32_exact_x_elems(size_t K) {
+  const size_t per_pass = (size_t)kChainWaves * kChainG * 4;
+  return cdiv(K, per_pass) * per_pass;
+}
+
+static syn_status_t launch_gemv_f32_exact(const float *Wp, const float *x, size_t x_elems, int N,
+                                          int K, int n8, float *y, hipStream_t s) {
+  if (x_elems < f32_exact_x_elems((size_t)K)) {
+    set_error("f32 GEMV: activation buffer shorter than the padded row");
     return SYN_ERR_INVALID_ARG;
   }
-  hipLaunchKernelGGL(k_gemv_f32_exact, dim3((unsigned)cdiv((size_t)N, 64)), dim3(1024), shm, s,
+  hipLaunchKernelGGL(k_gemv_f32_exact, dim3((unsigned)cdiv((size_t)N, 64)), dim3(1024), 0, s,
                      reinterpret_cast<const float4 *>(Wp), x, N, K, n8, y);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
@@ -339,6 +386,7 @@ struct syn_hip_mamba_s {
   size_t hist_cap = 0;
   hipStream_t stream = nullptr;
   hipGraphExec_t graph = nullptr;
+  bool use_graph = true;  // replay the captured step, else launch eagerly
   bool ready = false;
 
   ~syn_hip_mamba_s() {
@@ -369,8 +417,8 @@ struct syn_hip_mamba_s {
       SYN_TRY(B.dt_i8.gemv(1, xpq.as<int8_t>(), ldq_r, sxp.as<float>(), dtp.as<float>(), di, s));
       dtp_pre = dtp.as<float>();
     } else {
-      SYN_TRY(launch_gemv_f32_exact(B.xproj_p.as<float>(), xc.as<float>(), (int)nx, (int)di,
-                                    n8_of((int)nx), xp.as<float>(), s));
+      SYN_TRY(launch_gemv_f32_exact(B.xproj_p.as<float>(), xc.as<float>(), xc.bytes / 4,
+                                    (int)nx, (int)di, n8_of((int)nx), xp.as<float>(), s));
     }
     hipLaunchKernelGGL(k_mamba_scan, dim3(cdiv(di, 256)), dim3(256), 0, s, xp.as<float>(),
                        B.dtproj.as<float>(), dtp_pre, B.dt_bias.as<float>(), B.a_log.as<float>(),
@@ -391,8 +439,8 @@ struct syn_hip_mamba_s {
                        final_norm.as<float>(), c.eps, (int)dm, nullptr, nullptr,
                        normed.as<float>());
     SYN_LAUNCH_CHECK();
-    SYN_TRY(launch_gemv_f32_exact(lm_p.as<float>(), normed.as<float>(), (int)vocab, (int)dm,
-                                  n8_of((int)vocab), logits.as<float>(), s));
+    SYN_TRY(launch_gemv_f32_exact(lm_p.as<float>(), normed.as<float>(), normed.bytes / 4,
+                                  (int)vocab, (int)dm, n8_of((int)vocab), logits.as<float>(), s));
     SYN_TRY(launch_argmax(logits.as<float>(), (int)vocab, pv.as<float>(), pi.as<int>(),
                           pv2.as<float>(), st(), history.as<uint32_t>(), mhist.as<float>(), s));
     return launch_step_advance(st(), 1, s);
@@ -418,6 +466,14 @@ struct syn_hip_mamba_s {
     return SYN_OK;
   }
 
+  // one token step on `stream`: graph replay or the same kernels launched eagerly
+  syn_status_t run_step() {
+    if (!use_graph) return step(stream);
+    SYN_TRY(build_graph());
+    SYN_HIP(hipGraphLaunch(graph, stream));
+    return SYN_OK;
+  }
+
   syn_status_t set_state(int pos, uint32_t token, int step_) {
     StepState hs{pos, token, step_, 0.0f};
     SYN_HIP(hipMemcpyAsync(state.p, &hs, sizeof(hs), hipMemcpyHostToDevice, stream));
@@ -433,11 +489,11 @@ struct syn_hip_mamba_s {
 
   // prefill = the per-token loop of the reference (int8_mamba.rs:177-203)
   syn_status_t prefill(const uint32_t *ids, size_t n) {
-    SYN_TRY(build_graph());
+    if (use_graph) SYN_TRY(build_graph());
     SYN_TRY(reset());
     for (size_t t = 0; t < n; t++) {
       SYN_TRY(set_state((int)t, ids[t], 0));
-      SYN_HIP(hipGraphLaunch(graph, stream));
+      SYN_TRY(run_step());
     }
     return SYN_OK;
   }
@@ -537,7 +593,7 @@ syn_status_t syn_hip_mamba_init_synthetic(syn_hip_mamba_t *m, uint64_t seed_base
   SYN_TRY(m->xq.alloc(round_up(dm, 16)));
   SYN_TRY(m->sx.alloc(16));
   SYN_TRY(m->proj.alloc(2 * di * 4));
-  SYN_TRY(m->xc.alloc(di * 4));
+  SYN_TRY(m->xc.alloc(f32_exact_x_elems(di) * 4));  // padded for the f32 GEMV
   SYN_TRY(m->xp.alloc(nx * 4));
   SYN_TRY(m->dtp.alloc(di * 4));
   SYN_TRY(m->g.alloc(di * 4));
@@ -548,7 +604,7 @@ syn_status_t syn_hip_mamba_init_synthetic(syn_hip_mamba_t *m, uint64_t seed_base
   SYN_TRY(m->xpq.alloc(round_up(dr, 16)));
   SYN_TRY(m->sxp.alloc(16));
   SYN_TRY(m->o.alloc(dm * 4));
-  SYN_TRY(m->normed.alloc(dm * 4));
+  SYN_TRY(m->normed.alloc(f32_exact_x_elems(dm) * 4));
   SYN_TRY(m->logits.alloc(m->vocab * 4));
   SYN_TRY(m->pv.alloc(256 * 4));
   SYN_TRY(m->pi.alloc(256 * 4));
@@ -588,7 +644,6 @@ syn_status_t syn_hip_mamba_prefill(syn_hip_mamba_t *m, const uint32_t *ids, size
 
 syn_status_t syn_hip_mamba_decode_one(syn_hip_mamba_t *m, uint32_t token, float *host_logits) {
   SYN_TRY(check_mamba(m));
-  SYN_TRY(m->build_graph());
   StepState cur;
   SYN_HIP(hipMemcpyAsync(&cur, m->state.p, sizeof(cur), hipMemcpyDeviceToHost, m->stream));
   SYN_HIP(hipStreamSynchronize(m->stream));
@@ -597,7 +652,7 @@ syn_status_t syn_hip_mamba_decode_one(syn_hip_mamba_t *m, uint32_t token, float 
     return SYN_ERR_INVALID_ARG;
   }
   SYN_TRY(m->set_state(cur.pos, token, cur.step));
-  SYN_HIP(hipGraphLaunch(m->graph, m->stream));
+  SYN_TRY(m->run_step());
   if (host_logits)
     SYN_HIP(hipMemcpyAsync(host_logits, m->logits.p, m->vocab * 4, hipMemcpyDeviceToHost,
                            m->stream));
@@ -612,7 +667,7 @@ syn_status_t syn_hip_mamba_generate(syn_hip_mamba_t *m, const uint32_t *prompt, 
   if (max_new == 0) return SYN_OK;
   if (n_prompt == 0 || n_prompt > m->c.max_tokens || max_new + 1 > m->hist_cap) return SYN_ERR_INVALID_ARG;
   SYN_TRY(m->prefill(prompt, n_prompt));
-  for (size_t i = 1; i < max_new; i++) SYN_HIP(hipGraphLaunch(m->graph, m->stream));
+  for (size_t i = 1; i < max_new; i++) SYN_TRY(m->run_step());
   SYN_HIP(hipMemcpyAsync(out_tokens, m->history.p, max_new * 4, hipMemcpyDeviceToHost, m->stream));
   if (out_margins)
     SYN_HIP(hipMemcpyAsync(out_margins, m->mhist.p, max_new * 4, hipMemcpyDeviceToHost, m->stream));
@@ -623,7 +678,7 @@ syn_status_t syn_hip_mamba_generate(syn_hip_mamba_t *m, const uint32_t *prompt, 
 syn_status_t syn_hip_mamba_decode_timed(syn_hip_mamba_t *m, size_t steps, float *elapsed_ms) {
   SYN_TRY(check_mamba(m));
   if (!elapsed_ms) return SYN_ERR_NULL_PTR;
-  SYN_TRY(m->build_graph());
+  if (m->use_graph) SYN_TRY(m->build_graph());
   StepState cur;
   SYN_HIP(hipMemcpyAsync(&cur, m->state.p, sizeof(cur), hipMemcpyDeviceToHost, m->stream));
   SYN_HIP(hipStreamSynchronize(m->stream));
@@ -635,12 +690,18 @@ syn_status_t syn_hip_mamba_decode_timed(syn_hip_mamba_t *m, size_t steps, float 
   SYN_HIP(hipEventCreate(&a));
   SYN_HIP(hipEventCreate(&b));
   SYN_HIP(hipEventRecord(a, m->stream));
-  for (size_t i = 0; i < steps; i++) SYN_HIP(hipGraphLaunch(m->graph, m->stream));
+  for (size_t i = 0; i < steps; i++) SYN_TRY(m->run_step());
   SYN_HIP(hipEventRecord(b, m->stream));
   SYN_HIP(hipEventSynchronize(b));
   SYN_HIP(hipEventElapsedTime(elapsed_ms, a, b));
   (void)hipEventDestroy(a);
   (void)hipEventDestroy(b);
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_mamba_set_options(syn_hip_mamba_t *m, int graph) {
+  if (!m) return SYN_ERR_NULL_PTR;
+  m->use_graph = graph != 0;
   return SYN_OK;
 }
 

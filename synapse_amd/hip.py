@@ -104,6 +104,7 @@ SIGNATURES = {
     "syn_hip_klm_forward_one": (ST, [P, C.c_uint32, P]),
     "syn_hip_klm_generate": (ST, [P, P, SZ, SZ, P, P]),
     "syn_hip_klm_time": (ST, [P, P, SZ, SZ, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
+    "syn_hip_klm_set_options": (ST, [P, C.c_int]),
     "syn_hip_klm_destroy": (ST, [P]),
     "syn_hip_mamba_create": (ST, [C.POINTER(MambaConfig), C.POINTER(P)]),
     "syn_hip_mamba_init_synthetic": (ST, [P, C.c_uint64, C.c_float]),
@@ -111,6 +112,7 @@ SIGNATURES = {
     "syn_hip_mamba_decode_one": (ST, [P, C.c_uint32, P]),
     "syn_hip_mamba_generate": (ST, [P, P, SZ, SZ, P, P]),
     "syn_hip_mamba_decode_timed": (ST, [P, SZ, C.POINTER(C.c_float)]),
+    "syn_hip_mamba_set_options": (ST, [P, C.c_int]),
     "syn_hip_mamba_destroy": (ST, [P]),
     "syn_hip_fill_normal": (ST, [P, SZ, C.c_uint64, C.c_float]),
     "syn_hip_probe_mfma": (ST, [C.c_int, SZ, C.POINTER(C.c_double)]),
@@ -507,6 +509,10 @@ class KQuantCausalLM:
                                      C.byref(d)), "klm_time")
         return p.value, d.value
 
+    def set_options(self, graph: bool = True):
+        """HIP graph replay of the decode step, or eager launches (same results)."""
+        check(lib().syn_hip_klm_set_options(self.h, int(graph)), "set_options")
+
     def close(self):
         if self.h:
             lib().syn_hip_klm_destroy(self.h)
@@ -557,6 +563,10 @@ class QuantizedMamba:
         ms = C.c_float()
         check(lib().syn_hip_mamba_decode_timed(self.h, steps, C.byref(ms)), "decode_timed")
         return ms.value
+
+    def set_options(self, graph: bool = True):
+        """HIP graph replay of the token step, or eager launches (same results)."""
+        check(lib().syn_hip_mamba_set_options(self.h, int(graph)), "set_options")
 
     def close(self):
         if self.h:
