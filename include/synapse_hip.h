@@ -274,9 +274,11 @@ syn_status_t syn_hip_mamba_decode_one(syn_hip_mamba_t *m, uint32_t token, float 
 syn_status_t syn_hip_mamba_generate(syn_hip_mamba_t *m, const uint32_t *prompt, size_t n_prompt,
                                     size_t max_new, uint32_t *out_tokens, float *out_margins);
 syn_status_t syn_hip_mamba_decode_timed(syn_hip_mamba_t *m, size_t steps, float *elapsed_ms);
-/* Token steps replay a captured HIP graph (graph != 0, the default) or launch
- * the same kernels eagerly. */
-syn_status_t syn_hip_mamba_set_options(syn_hip_mamba_t *m, int graph);
+/* Token step form: fused split-K GEMV kernels whose prologues form their own
+ * inputs (fused != 0, the default when the shapes fit) or one kernel per
+ * reference op; HIP graph replay (graph != 0, the default) or eager launches.
+ * Both forms compute the same float operations. */
+syn_status_t syn_hip_mamba_set_options(syn_hip_mamba_t *m, int fused, int graph);
 syn_status_t syn_hip_mamba_destroy(syn_hip_mamba_t *m);
 
 /* -- harness helpers (no reference counterpart) -- */

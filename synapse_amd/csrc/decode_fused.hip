@@ -59,11 +59,6 @@ static __device__ unsigned long long syn_phase_ts[256];
 #endif
 
 // ------------------------------------------------------------------ helpers
-__device__ __forceinline__ float row_value(const RowSrc &s, int r) {
-  if (s.f) return s.f[r];
-  const float f = (float)s.acc[r] * s.sx[0];
-  return f * s.ws[r];
-}
 
 // Rows of a prologue vector held per thread: element j = threadIdx.x + u*NT.
 constexpr int RB = 8;
@@ -163,7 +158,12 @@ static const uint64_t *exp_table_address() {
 }
 
 // ------------------------------------------------------------------ split-K GEMV
-enum { PRO_NORM = 0, PRO_QUANT = 1, PRO_SWIGLU = 2 };
+// PRO_NORM: residual + RMSNorm (sum of squares in the 4-chain order of
+// ops/norm.rs) + quantize; PRO_MNORM: the same with one sequential sum of
+// squares (pure_rust_ops.rs:96-112, the Mamba blocks' norm); PRO_QUANT:
+// quantize an f32 vector; PRO_SWIGLU: silu(gate) * up of GEMV rows, then
+// quantize; PRO_ROWS: quantize GEMV rows (RowSrc values)
+enum { PRO_NORM = 0, PRO_QUANT = 1, PRO_SWIGLU = 2, PRO_MNORM = 3, PRO_ROWS = 4 };
 
 struct ProArgs {
   // PRO_NORM: x = (base ? base : embed[st->token]) + delta
@@ -178,6 +178,8 @@ struct ProArgs {
   float eps;
   // PRO_QUANT
   const float *vec;
+  // PRO_ROWS
+  RowSrc rows;
   // PRO_SWIGLU; exp_tab = device address of syn_exp2_tab, passed as a plain
   // pointer so its load is ordered like any other (a __constant__ load may be
   // moved behind the weight loads)
@@ -203,12 +205,13 @@ struct GemvArgs {
 template <int PRO, int NT, int U>
 __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
   constexpr int NW = NT / 64;
+  constexpr bool NORM = PRO == PRO_NORM || PRO == PRO_MNORM;
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ float red[64];
   __shared__ int redi[NW * 64];
   const int H = a.H;
   float *sq = reinterpret_cast<float *>(smem);
-  int8_t *xq = reinterpret_cast<int8_t *>(smem) + (PRO == PRO_NORM ? ((H + 3) & ~3) * 4 : 0);
+  int8_t *xq = reinterpret_cast<int8_t *>(smem) + (NORM ? ((H + 3) & ~3) * 4 : 0);
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
@@ -237,7 +240,7 @@ __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
   //    weight chunks, 3. the activation row x[] in registers
   float x[RB];
   float nwv[RB];
-  if constexpr (PRO == PRO_NORM) {
+  if constexpr (NORM) {
     const float *src = a.base;
     if (!src) {
       const uint32_t tok = a.st->token;
@@ -277,6 +280,22 @@ __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
 #pragma unroll
     for (int u = 0; u < RB; u++) x[u] = a.vec[min(tid + u * NT, H - 1)];
     issue_weights();
+  } else if constexpr (PRO == PRO_ROWS) {
+    int ra[RB];
+    float rw[RB];
+#pragma unroll
+    for (int u = 0; u < RB; u++) {
+      const int j = min(tid + u * NT, H - 1);
+      ra[u] = a.rows.acc[j];
+      rw[u] = a.rows.ws[j];
+    }
+    const float rsx = a.rows.sx[0];
+    issue_weights();
+#pragma unroll
+    for (int u = 0; u < RB; u++) {
+      const float f = (float)ra[u] * rsx;
+      x[u] = f * rw[u];
+    }
   } else {
     // expf's 2^(i/32) table goes to LDS first: a lookup in global memory
     // would wait behind the outstanding weight loads
@@ -309,22 +328,30 @@ __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
   SYN_TS(2);
 
   float sv;
-  if constexpr (PRO == PRO_NORM) {
+  if constexpr (NORM) {
     // RMSNorm (ops/norm.rs:8-38): out = (x*w) * (1/sqrt(sumsq/n + eps)),
     // then the quantizer's max|out|.  Scaling by the positive `scale` is a
     // monotonic rounding, so max|t*scale| = fl(max|t| * scale): the max of
-    // t = x*w is reduced while lanes 0-3 run the sum-of-squares chains.
+    // t = x*w is reduced while lanes 0-3 run the sum-of-squares chains (or
+    // lane 0 the single sequential sum).
     float t[RB];
 #pragma unroll
     for (int u = 0; u < RB; u++) {
       const int j = tid + u * NT;
-      if (j < H) sq[sq_slot(j, H)] = x[u] * x[u];
+      if (j < H) sq[PRO == PRO_MNORM ? j : sq_slot(j, H)] = x[u] * x[u];
       t[u] = x[u] * nwv[u];
     }
     wg_max_post<NT>(local_absmax<NT>(t, H), red, 0);
     bar<NT>();
     SYN_TS(3);
-    const float ss = sumsq_chains<NT>(sq, H, red);
+    float ss;
+    if constexpr (PRO == PRO_MNORM) {
+      if (tid == 0) red[36] = seq_sum(sq, H);
+      bar<NT>();
+      ss = red[36];
+    } else {
+      ss = sumsq_chains<NT>(sq, H, red);
+    }
     SYN_TS(4);
     const float scale = 1.0f / sqrtf(ss / (float)H + a.eps);
     float nv[RB];
@@ -371,7 +398,7 @@ __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
 
   // 4. workgroup 0 publishes the prologue's results for later kernels
   if (panel == 0 && ks == 0) {
-    if constexpr (PRO == PRO_NORM) {
+    if constexpr (NORM) {
       if (a.res_out) {
 #pragma unroll
         for (int u = 0; u < RB; u++)
@@ -451,6 +478,10 @@ static syn_status_t launch_fused(const ProArgs &a, const SplitGemv &g, hipStream
     set_error("fused decode GEMV: activation row does not fit the fused kernel");
     return SYN_ERR_INVALID_ARG;
   }
+  if (PRO == PRO_ROWS && (!a.rows.acc || !a.rows.ws || !a.rows.sx)) {
+    set_error("fused decode GEMV: row source must be GEMV accumulators");
+    return SYN_ERR_INVALID_ARG;
+  }
   if (g.nt == 1024) return launch_fused_nt<PRO, 1024>(a, g, s);
   if (g.nt == 512) return launch_fused_nt<PRO, 512>(a, g, s);
   return launch_fused_nt<PRO, 256>(a, g, s);
@@ -459,7 +490,8 @@ static syn_status_t launch_fused(const ProArgs &a, const SplitGemv &g, hipStream
 syn_status_t launch_fused_norm_gemv(const float *base, const float *embed, const StepState *st,
                                     int vocab, const float *zero_row, RowSrc delta,
                                     float *res_out, const float *nw, float eps, int H,
-                                    float *s_out, const SplitGemv &g, hipStream_t s) {
+                                    float *s_out, const SplitGemv &g, hipStream_t s,
+                                    bool sequential_sumsq) {
   ProArgs a{};
   a.base = base;
   a.embed = embed;
@@ -472,7 +504,16 @@ syn_status_t launch_fused_norm_gemv(const float *base, const float *embed, const
   a.eps = eps;
   a.H = H;
   a.s_out = s_out;
-  return launch_fused<PRO_NORM>(a, g, s);
+  return sequential_sumsq ? launch_fused<PRO_MNORM>(a, g, s) : launch_fused<PRO_NORM>(a, g, s);
+}
+
+syn_status_t launch_fused_rows_gemv(RowSrc rows, int H, float *s_out, const SplitGemv &g,
+                                    hipStream_t s) {
+  ProArgs a{};
+  a.rows = rows;
+  a.H = H;
+  a.s_out = s_out;
+  return launch_fused<PRO_ROWS>(a, g, s);
 }
 
 syn_status_t launch_fused_quant_gemv(const float *vec, int H, float *s_out, const SplitGemv &g,

@@ -17,7 +17,25 @@ struct RowSrc {
   const float *sx = nullptr;
   const float *ws = nullptr;
   const float *f = nullptr;
+  __host__ __device__ bool empty() const { return !acc && !f; }
 };
+
+__device__ __forceinline__ float row_value(const RowSrc &s, int r) {
+  if (s.f) return s.f[r];
+  const float f = (float)s.acc[r] * s.sx[0];
+  return f * s.ws[r];
+}
+// the same with the source kind fixed at compile time (no branch, so the
+// loads can stay in flight)
+template <bool ACC>
+__device__ __forceinline__ float row_value_t(const RowSrc &s, int r) {
+  if constexpr (ACC) {
+    const float f = (float)s.acc[r] * s.sx[0];
+    return f * s.ws[r];
+  } else {
+    return s.f[r];
+  }
+}
 
 // One INT8 linear in the panel layout, with the K split used in the step.
 struct SplitGemv {
@@ -37,11 +55,17 @@ SplitGemv plan_split_gemv(const void *W, const float *ws, int N, int C, int targ
 
 // x = (base ? base : embed[state->token] or zero_row) + delta ; res_out = x
 // (workgroup 0); xq = q8(rmsnorm(x, nw, eps)); s_out = its scale (workgroup
-// 0); acc += xq . W over this split of K
+// 0); acc += xq . W over this split of K.  The sum of squares runs in the
+// 4-chain order of ops/norm.rs, or as one sequential sum (the Mamba blocks'
+// pure_rust rmsnorm) with sequential_sumsq.
 syn_status_t launch_fused_norm_gemv(const float *base, const float *embed, const StepState *st,
                                     int vocab, const float *zero_row, RowSrc delta,
                                     float *res_out, const float *nw, float eps, int H,
-                                    float *s_out, const SplitGemv &g, hipStream_t s);
+                                    float *s_out, const SplitGemv &g, hipStream_t s,
+                                    bool sequential_sumsq = false);
+// xq = q8(rows[0..H)) of another split GEMV's rows ; s_out ; acc += xq . W
+syn_status_t launch_fused_rows_gemv(RowSrc rows, int H, float *s_out, const SplitGemv &g,
+                                    hipStream_t s);
 // xq = q8(vec) ; s_out ; acc += xq . W
 syn_status_t launch_fused_quant_gemv(const float *vec, int H, float *s_out, const SplitGemv &g,
                                      hipStream_t s);

@@ -240,7 +240,6 @@ __global__ void __launch_bounds__(256)
   const int head = blockIdx.x;
   const int kvh = head / (nh / nkv);
   const int len = d_pos[0] + 1;
-  const int kvd = nkv * hd;
   const bool simd = len >= 64;
   float *e = scores + (size_t)head * max_seq;
   for (int d = threadIdx.x; d < hd; d += blockDim.x) qs[d] = q[head * hd + d];
@@ -340,7 +339,7 @@ __global__ void __launch_bounds__(256)
   __shared__ float s_mx, s_inv;
   const int head = blockIdx.x, i = blockIdx.y;
   const int kvh = head / (nh / nkv);
-  const int qd = nh * hd, kvd = nkv * hd;
+  const int qd = nh * hd;
   const int tq = (i / 32) * 32, tqs = min(32, t - tq), il = i - tq;
   for (int d = threadIdx.x; d < hd; d += blockDim.x) qs[d] = q[(size_t)i * qd + head * hd + d];
   __syncthreads();

@@ -14,6 +14,7 @@
 #include <thread>
 #include <vector>
 
+#include "decode_fused.hpp"
 #include "layer_ops.hpp"
 #include "linear.hpp"
 
@@ -24,17 +25,17 @@ namespace syn {
 // ops/pure_rust_ops.rs:96-112 (one sequential sum of squares) + optional
 // residual add + A1 quantization of the normed row (single workgroup)
 __global__ void __launch_bounds__(256)
-    k_mamba_norm(float *__restrict__ x, const float *__restrict__ delta,
-                 const float *__restrict__ w, float eps, int H, int8_t *__restrict__ xq,
-                 float *__restrict__ sx, float *__restrict__ normed) {
+    k_mamba_norm(float *__restrict__ x, RowSrc delta, const float *__restrict__ w, float eps,
+                 int H, int8_t *__restrict__ xq, float *__restrict__ sx,
+                 float *__restrict__ normed) {
   extern __shared__ __align__(16) float sm[];  // H | squares[H rounded to 4]
   float *sq = sm + ((H + 3) & ~3);
   __shared__ float red[64];
   __shared__ float s_scale;
   for (int j = threadIdx.x; j < H; j += blockDim.x) {
     float v = x[j];
-    if (delta) {
-      v = delta[j] + v;  // int8_mamba.rs:108: o + h
+    if (!delta.empty()) {
+      v = row_value(delta, j) + v;  // int8_mamba.rs:108: o + h
       x[j] = v;
     }
     sm[j] = v;
@@ -92,14 +93,14 @@ __global__ void __launch_bounds__(256)
 }
 
 // conv1d_step (int8_mamba.rs:43-56) + SiLU, one thread per channel
-__global__ void k_mamba_conv(const float *__restrict__ proj, float *__restrict__ conv_state,
+__global__ void k_mamba_conv(RowSrc proj, float *__restrict__ conv_state,
                              const float *__restrict__ cw, const float *__restrict__ cb, int di,
                              int dc, float *__restrict__ xc) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= di) return;
   float *buf = conv_state + (size_t)i * dc;
   for (int k = 0; k + 1 < dc; k++) buf[k] = buf[k + 1];
-  buf[dc - 1] = proj[i];
+  buf[dc - 1] = row_value(proj, i);
   const float *wr = cw + (size_t)i * dc;
   float sum = 0.0f;
   for (int k = 0; k < dc; k++) {
@@ -239,120 +240,107 @@ __device__ __forceinline__ float syn_softplus(float v) {  // ops/activation.rs:8
   return (float)log((double)t);
 }
 
-// dt_proj (f32 chain over dt_rank, or precomputed by the INT8 variant),
-// softplus, selective scan step and the SiLU(z) gate; one thread per channel.
-// The thread's dt_proj row, A_log row and state row are requested together
-// before the chains (rows of up to kScanDr / kScanDs values; longer rows take
-// the looped form).
-constexpr int kScanDr = 64, kScanDs = 16;
+// dt_proj (f32 chain over dt_rank, or taken from the INT8 variant's GEMV),
+// softplus, selective scan step and the SiLU(z) gate; one lane per channel,
+// one wave per workgroup.  The per-channel parameters and the state are
+// stored channel-minor ([j][d_inner]: element (i, j) at j*d_inner + i), so
+// every load and store of a wave is 256 contiguous bytes; all of a lane's
+// loads are requested at entry (up to DR dt_proj weights and DS state and
+// A_log values in registers; DR = 0 streams longer dt_proj rows).
+// x_proj's output (dt_rank + 2*d_state values, the same for every channel)
+// is staged in LDS.
+constexpr int kScanDs = 16, kScanDr = 64;
 
-__global__ void k_mamba_scan(const float *__restrict__ xp, const float *__restrict__ dtw,
-                             const float *__restrict__ dtp_pre, const float *__restrict__ dtb,
-                             const float *__restrict__ a_log, const float *__restrict__ dparam,
-                             const float *__restrict__ xc, const float *__restrict__ proj,
-                             float *__restrict__ ssm, int di, int ds, int dr, int n8,
-                             float *__restrict__ gated) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= di) return;
-  const bool fits = dr <= kScanDr && ds <= kScanDs;
-  float wr[kScanDr], al[kScanDs], hs[kScanDs];
-  const float *wrow = dtw ? dtw + (size_t)i * dr : nullptr;
-  float *h = ssm + (size_t)i * ds;
-  const float *arow = a_log + (size_t)i * ds;
-  if (fits) {
-    if (!dtp_pre) {
+template <int DR, bool CHAIN, bool ZACC, bool XACC>
+__global__ void __launch_bounds__(64)
+    k_mamba_scan(RowSrc xps, const float *__restrict__ dtwT, RowSrc dtps,
+                 const float *__restrict__ dtb, const float *__restrict__ alT,
+                 const float *__restrict__ dparam, const float *__restrict__ xc, RowSrc z,
+                 float *__restrict__ hT, int di, int ds, int dr, int n8,
+                 float *__restrict__ gated) {
+  constexpr int DS = kScanDs;
+  extern __shared__ float xp[];  // dr + 2*ds
+  const int i0 = blockIdx.x * 64 + threadIdx.x;
+  const int i = min(i0, di - 1);
+  float wr[DR > 0 ? DR : 1], al[DS], hs[DS];
+  if constexpr (CHAIN && DR > 0) {
 #pragma unroll
-      for (int k = 0; k < kScanDr; k++) wr[k] = wrow[min(k, dr - 1)];
-    }
-#pragma unroll
-    for (int j = 0; j < kScanDs; j++) {
-      al[j] = arow[min(j, ds - 1)];
-      hs[j] = h[min(j, ds - 1)];
-    }
+    for (int k = 0; k < DR; k++) wr[k] = dtwT[(size_t)min(k, dr - 1) * di + i];
   }
-  float dtp;
-  if (dtp_pre) {
-    dtp = dtp_pre[i];
-  } else {
-    dtp = 0.0f;
-    if (fits) {
-      if (i < n8) {
 #pragma unroll
-        for (int k = 0; k < kScanDr; k++)
-          if (k < dr) dtp = __builtin_fmaf(xp[k], wr[k], dtp);
-      } else {
+  for (int j = 0; j < DS; j++) {
+    al[j] = alT[(size_t)min(j, ds - 1) * di + i];
+    hs[j] = hT[(size_t)min(j, ds - 1) * di + i];
+  }
+  const float dtbi = dtb[i], xi = xc[i], dpi = dparam[i];
+  const float zi = row_value_t<ZACC>(z, i);
+  float dtp = 0.0f;
+  if constexpr (!CHAIN) dtp = row_value_t<ZACC>(dtps, i);
+  for (int k = threadIdx.x; k < dr + 2 * ds; k += 64) xp[k] = row_value_t<XACC>(xps, k);
+  __syncthreads();
+  if constexpr (CHAIN) {
+    // f32GemvRow order: @mulAdd for channels in the 32/8-wide blocks
+    // (i < n8), plain a*b+c for the rest
+    const bool fused = i0 < n8;
+    float pf = 0.0f, pp = 0.0f;
+    if constexpr (DR > 0) {
 #pragma unroll
-        for (int k = 0; k < kScanDr; k++)
-          if (k < dr) {
-            const float t = xp[k] * wr[k];
-            dtp = dtp + t;
-          }
-      }
-    } else if (i < n8) {
-      for (int k = 0; k < dr; k++) dtp = __builtin_fmaf(xp[k], wrow[k], dtp);
+      for (int k = 0; k < DR; k++)
+        if (k < dr) {
+          pf = __builtin_fmaf(xp[k], wr[k], pf);
+          const float t = xp[k] * wr[k];
+          pp = pp + t;
+        }
     } else {
       for (int k = 0; k < dr; k++) {
-        const float t = xp[k] * wrow[k];
-        dtp = dtp + t;
+        const float w = dtwT[(size_t)k * di + i];
+        pf = __builtin_fmaf(xp[k], w, pf);
+        const float t = xp[k] * w;
+        pp = pp + t;
       }
     }
+    dtp = fused ? pf : pp;
   }
-  const float dt = syn_softplus(dtp + dtb[i]);
-  const float xi = xc[i];
+  const float dt = syn_softplus(dtp + dtbi);
   const float dt_x = dt * xi;
   const float *b = xp + dr, *c = xp + dr + ds;
   float yi = 0.0f;
-  int j = 0;
+  // groups of 4 states (selective_scan.zig's SIMD loop), then the scalar tail
 #pragma unroll
-  for (int jj = 0; jj + 4 <= kScanDs; jj += 4) {
-    if (!fits || jj + 4 > ds) break;
-    float contrib[4];
-#pragma unroll
-    for (int l = 0; l < 4; l++) {
-      const float e = syn_expf(al[jj + l]);
-      const float ad = syn_expf(-dt * e);
-      const float p1 = ad * hs[jj + l], p2 = dt_x * b[jj + l];
-      const float hn = p1 + p2;
-      h[jj + l] = hn;
-      contrib[l] = c[jj + l] * hn;
-    }
-    yi = yi + (((contrib[0] + contrib[1]) + contrib[2]) + contrib[3]);
-    j = jj + 4;
-  }
-  if (!fits) {
-    for (; j + 4 <= ds; j += 4) {
+  for (int jj = 0; jj + 4 <= DS; jj += 4) {
+    if (jj + 4 <= ds) {
       float contrib[4];
+#pragma unroll
       for (int l = 0; l < 4; l++) {
-        const float e = syn_expf(arow[j + l]);
+        const float e = syn_expf(al[jj + l]);
         const float ad = syn_expf(-dt * e);
-        const float p1 = ad * h[j + l], p2 = dt_x * b[j + l];
+        const float p1 = ad * hs[jj + l], p2 = dt_x * b[jj + l];
         const float hn = p1 + p2;
-        h[j + l] = hn;
-        contrib[l] = c[j + l] * hn;
+        hs[jj + l] = hn;
+        contrib[l] = c[jj + l] * hn;
       }
       yi = yi + (((contrib[0] + contrib[1]) + contrib[2]) + contrib[3]);
     }
   }
-  // tail (selective_scan.zig's scalar remainder): compile-time indices when
-  // the rows are in registers
-  auto tail = [&](int jj, float av, float hv) {
-    const float a = -syn_expf(av);
-    const float ad = syn_expf(dt * a);
-    const float p1 = ad * hv, p2 = (dt * b[jj]) * xi;
-    const float hn = p1 + p2;
-    h[jj] = hn;
-    const float t = c[jj] * hn;
-    yi = yi + t;
-  };
-  if (fits) {
+  const int j4 = ds & ~3;
 #pragma unroll
-    for (int jj = 0; jj < kScanDs; jj++)
-      if (jj >= j && jj < ds) tail(jj, al[jj], hs[jj]);
-  } else {
-    for (; j < ds; j++) tail(j, arow[j], h[j]);
+  for (int jj = 0; jj < DS; jj++) {
+    if (jj >= j4 && jj < ds) {
+      const float a = -syn_expf(al[jj]);
+      const float ad = syn_expf(dt * a);
+      const float p1 = ad * hs[jj], p2 = (dt * b[jj]) * xi;
+      const float hn = p1 + p2;
+      hs[jj] = hn;
+      const float t = c[jj] * hn;
+      yi = yi + t;
+    }
   }
-  const float y = yi + dparam[i] * xi;
-  gated[i] = syn_silu(proj[di + i]) * y;  // int8_mamba.rs:102
+  if (i0 >= di) return;
+#pragma unroll
+  for (int j = 0; j < DS; j++)
+    if (j < ds) hT[(size_t)j * di + i] = hs[j];
+  const float y = yi + dpi * xi;
+  gated[i] = syn_silu(zi) * y;  // int8_mamba.rs:102
 }
 
 // [n,k] -> [panel][k/4][64][4] (k padded with zeros to a multiple of 4)
@@ -362,6 +350,14 @@ static std::vector<float> to_panels(const float *w_nk, size_t n, size_t k) {
   for (size_t r = 0; r < n; r++)
     for (size_t kk = 0; kk < k; kk++)
       out[(((r / 64) * K4 + kk / 4) * 64 + r % 64) * 4 + kk % 4] = w_nk[r * k + kk];
+  return out;
+}
+
+// [n_ch][m] (row per channel) -> [m][n_ch]: the scan kernel's layout
+static std::vector<float> channel_minor(const float *a, size_t n_ch, size_t m) {
+  std::vector<float> out(n_ch * m);
+  for (size_t i = 0; i < n_ch; i++)
+    for (size_t j = 0; j < m; j++) out[j * n_ch + i] = a[i * m + j];
   return out;
 }
 
@@ -378,15 +374,19 @@ struct syn_hip_mamba_s {
   struct Block {
     QLinearInt8 in_proj, out_proj, x_i8, dt_i8;
     DevBuf conv_w, conv_b, xproj_p, dtproj, dt_bias, a_log, dparam, norm_w;
+    SplitGemv f_in, f_out, f_x, f_dt;  // fused step: split-K plans + accumulators
   };
   std::vector<Block> blk;
   DevBuf embed, lm_p, final_norm, conv_state, ssm_state;
   DevBuf x, xq, sx, proj, xc, xp, dtp, g, gq, sg, xcq, sxc, xpq, sxp, o, normed, logits;
   DevBuf pv, pi, pv2, state, history, mhist;
+  DevBuf acc, xres, scal, zeros_m;  // fused step: accumulators, residual ping-pong, scales
+  size_t acc_elems = 0;
   size_t hist_cap = 0;
   hipStream_t stream = nullptr;
   hipGraphExec_t graph = nullptr;
   bool use_graph = true;  // replay the captured step, else launch eagerly
+  bool fused = false;     // fused split-K GEMV step (when the shapes fit)
   bool ready = false;
 
   ~syn_hip_mamba_s() {
@@ -394,48 +394,71 @@ struct syn_hip_mamba_s {
     if (stream) (void)hipStreamDestroy(stream);
   }
   StepState *st() { return state.as<StepState>(); }
-
-  syn_status_t layer(size_t l, hipStream_t s) {
+  static RowSrc f32_rows(const float *p) {
+    RowSrc r;
+    r.f = p;
+    return r;
+  }
+  static RowSrc offset_rows(RowSrc r, size_t off) {  // rows off.. of a split GEMV's output
+    r.acc += off;
+    r.ws += off;
+    return r;
+  }
+  syn_status_t launch_scan(size_t l, RowSrc xps, RowSrc dtps, RowSrc z, hipStream_t s) {
     Block &B = blk[l];
-    const size_t ldq_m = round_up(dm, 16), ldq_i = round_up(di, 16), ldq_r = round_up(dr, 16);
-    hipLaunchKernelGGL(k_mamba_norm, dim3(1), dim3(256), round_up(dm, 4) * 8, s, x.as<float>(),
-                       l == 0 ? nullptr : o.as<float>(), B.norm_w.as<float>(), c.eps, (int)dm,
-                       xq.as<int8_t>(), sx.as<float>(), nullptr);
+    const dim3 grid((unsigned)cdiv(di, 64)), wg(64);
+    const size_t shm = nx * sizeof(float);
+    float *hT = ssm_state.as<float>() + l * di * ds;
+    const int n8 = n8_of((int)di);
+#define SYN_SCAN_ARGS                                                                        \
+  xps, B.dtproj.as<float>(), dtps, B.dt_bias.as<float>(), B.a_log.as<float>(),               \
+      B.dparam.as<float>(), xc.as<float>(), z, hT, (int)di, (int)ds, (int)dr, n8, g.as<float>()
+    // row sources: z and dt_proj's output are GEMV accumulators in the fused
+    // step and f32 otherwise; x_proj's output is accumulators only for the
+    // fused INT8 x_proj
+    const bool zacc = z.acc != nullptr, xacc = xps.acc != nullptr;
+    const bool chain = dtps.empty();
+    if (!chain && (dtps.acc != nullptr) != zacc) {
+      set_error("mamba scan: dt_proj and z rows must be of the same kind");
+      return SYN_ERR_INTERNAL;
+    }
+    const bool short_dr = dr <= (size_t)kScanDr;
+    if (!chain && zacc && xacc)
+      hipLaunchKernelGGL((k_mamba_scan<kScanDr, false, true, true>), grid, wg, shm, s,
+                         SYN_SCAN_ARGS);
+    else if (!chain && !zacc && !xacc)
+      hipLaunchKernelGGL((k_mamba_scan<kScanDr, false, false, false>), grid, wg, shm, s,
+                         SYN_SCAN_ARGS);
+    else if (chain && zacc && !xacc && short_dr)
+      hipLaunchKernelGGL((k_mamba_scan<kScanDr, true, true, false>), grid, wg, shm, s,
+                         SYN_SCAN_ARGS);
+    else if (chain && zacc && !xacc)
+      hipLaunchKernelGGL((k_mamba_scan<0, true, true, false>), grid, wg, shm, s, SYN_SCAN_ARGS);
+    else if (chain && !zacc && !xacc && short_dr)
+      hipLaunchKernelGGL((k_mamba_scan<kScanDr, true, false, false>), grid, wg, shm, s,
+                         SYN_SCAN_ARGS);
+    else if (chain && !zacc && !xacc)
+      hipLaunchKernelGGL((k_mamba_scan<0, true, false, false>), grid, wg, shm, s,
+                         SYN_SCAN_ARGS);
+    else {
+      set_error("mamba scan: unsupported row sources");
+      return SYN_ERR_INTERNAL;
+    }
+#undef SYN_SCAN_ARGS
     SYN_LAUNCH_CHECK();
-    SYN_TRY(B.in_proj.gemv(1, xq.as<int8_t>(), ldq_m, sx.as<float>(), proj.as<float>(), 2 * di, s));
-    hipLaunchKernelGGL(k_mamba_conv, dim3(cdiv(di, 256)), dim3(256), 0, s, proj.as<float>(),
+    return SYN_OK;
+  }
+  syn_status_t launch_conv(size_t l, RowSrc proj_x, hipStream_t s) {
+    Block &B = blk[l];
+    hipLaunchKernelGGL(k_mamba_conv, dim3(cdiv(di, 256)), dim3(256), 0, s, proj_x,
                        conv_state.as<float>() + l * di * dc, B.conv_w.as<float>(),
                        B.conv_b.as<float>(), (int)di, (int)dc, xc.as<float>());
     SYN_LAUNCH_CHECK();
-    const float *dtp_pre = nullptr;
-    if (c.int8_xdt) {
-      SYN_TRY(launch_quantize_rows(xc.as<float>(), 1, di, di, xcq.as<int8_t>(), ldq_i,
-                                   sxc.as<float>(), s));
-      SYN_TRY(B.x_i8.gemv(1, xcq.as<int8_t>(), ldq_i, sxc.as<float>(), xp.as<float>(), nx, s));
-      SYN_TRY(launch_quantize_rows(xp.as<float>(), 1, dr, dr, xpq.as<int8_t>(), ldq_r,
-                                   sxp.as<float>(), s));
-      SYN_TRY(B.dt_i8.gemv(1, xpq.as<int8_t>(), ldq_r, sxp.as<float>(), dtp.as<float>(), di, s));
-      dtp_pre = dtp.as<float>();
-    } else {
-      SYN_TRY(launch_gemv_f32_exact(B.xproj_p.as<float>(), xc.as<float>(), xc.bytes / 4,
-                                    (int)nx, (int)di, n8_of((int)nx), xp.as<float>(), s));
-    }
-    hipLaunchKernelGGL(k_mamba_scan, dim3(cdiv(di, 256)), dim3(256), 0, s, xp.as<float>(),
-                       B.dtproj.as<float>(), dtp_pre, B.dt_bias.as<float>(), B.a_log.as<float>(),
-                       B.dparam.as<float>(), xc.as<float>(), proj.as<float>(),
-                       ssm_state.as<float>() + l * di * ds, (int)di, (int)ds, (int)dr,
-                       n8_of((int)di), g.as<float>());
-    SYN_LAUNCH_CHECK();
-    SYN_TRY(launch_quantize_rows(g.as<float>(), 1, di, di, gq.as<int8_t>(), ldq_i, sg.as<float>(), s));
-    SYN_TRY(B.out_proj.gemv(1, gq.as<int8_t>(), ldq_i, sg.as<float>(), o.as<float>(), dm, s));
     return SYN_OK;
   }
-
-  syn_status_t step(hipStream_t s) {
-    SYN_TRY(launch_embed(embed.as<float>(), &st()->token, 1, (int)dm, (int)vocab, x.as<float>(), s));
-    for (size_t l = 0; l < L; l++) SYN_TRY(layer(l, s));
-    hipLaunchKernelGGL(k_mamba_norm, dim3(1), dim3(256), round_up(dm, 4) * 8, s, x.as<float>(),
-                       o.as<float>(),
+  // final residual + norm (pure_rust rmsnorm) and the tied f32 lm_head
+  syn_status_t head(float *xbuf, RowSrc last_o, hipStream_t s) {
+    hipLaunchKernelGGL(k_mamba_norm, dim3(1), dim3(256), round_up(dm, 4) * 8, s, xbuf, last_o,
                        final_norm.as<float>(), c.eps, (int)dm, nullptr, nullptr,
                        normed.as<float>());
     SYN_LAUNCH_CHECK();
@@ -445,6 +468,118 @@ struct syn_hip_mamba_s {
                           pv2.as<float>(), st(), history.as<uint32_t>(), mhist.as<float>(), s));
     return launch_step_advance(st(), 1, s);
   }
+
+  // one kernel per reference op
+  syn_status_t layer(size_t l, hipStream_t s) {
+    Block &B = blk[l];
+    const size_t ldq_m = round_up(dm, 16), ldq_i = round_up(di, 16), ldq_r = round_up(dr, 16);
+    hipLaunchKernelGGL(k_mamba_norm, dim3(1), dim3(256), round_up(dm, 4) * 8, s, x.as<float>(),
+                       l == 0 ? RowSrc{} : f32_rows(o.as<float>()), B.norm_w.as<float>(), c.eps,
+                       (int)dm, xq.as<int8_t>(), sx.as<float>(), nullptr);
+    SYN_LAUNCH_CHECK();
+    SYN_TRY(B.in_proj.gemv(1, xq.as<int8_t>(), ldq_m, sx.as<float>(), proj.as<float>(), 2 * di, s));
+    SYN_TRY(launch_conv(l, f32_rows(proj.as<float>()), s));
+    RowSrc dtps;
+    if (c.int8_xdt) {
+      SYN_TRY(launch_quantize_rows(xc.as<float>(), 1, di, di, xcq.as<int8_t>(), ldq_i,
+                                   sxc.as<float>(), s));
+      SYN_TRY(B.x_i8.gemv(1, xcq.as<int8_t>(), ldq_i, sxc.as<float>(), xp.as<float>(), nx, s));
+      SYN_TRY(launch_quantize_rows(xp.as<float>(), 1, dr, dr, xpq.as<int8_t>(), ldq_r,
+                                   sxp.as<float>(), s));
+      SYN_TRY(B.dt_i8.gemv(1, xpq.as<int8_t>(), ldq_r, sxp.as<float>(), dtp.as<float>(), di, s));
+      dtps = f32_rows(dtp.as<float>());
+    } else {
+      SYN_TRY(launch_gemv_f32_exact(B.xproj_p.as<float>(), xc.as<float>(), xc.bytes / 4,
+                                    (int)nx, (int)di, n8_of((int)nx), xp.as<float>(), s));
+    }
+    SYN_TRY(launch_scan(l, f32_rows(xp.as<float>()), dtps, f32_rows(proj.as<float>() + di), s));
+    SYN_TRY(launch_quantize_rows(g.as<float>(), 1, di, di, gq.as<int8_t>(), ldq_i, sg.as<float>(), s));
+    SYN_TRY(B.out_proj.gemv(1, gq.as<int8_t>(), ldq_i, sg.as<float>(), o.as<float>(), dm, s));
+    return SYN_OK;
+  }
+
+  syn_status_t step_unfused(hipStream_t s) {
+    SYN_TRY(launch_embed(embed.as<float>(), &st()->token, 1, (int)dm, (int)vocab, x.as<float>(), s));
+    for (size_t l = 0; l < L; l++) SYN_TRY(layer(l, s));
+    return head(x.as<float>(), f32_rows(o.as<float>()), s);
+  }
+
+  // Fused step: each INT8 GEMV is a split-K kernel whose prologue forms its
+  // own input (decode_fused.hip): [residual + norm + q8 ; in_proj], conv,
+  // [q8 ; x_proj] (or the exact f32 x_proj), [q8 of x_proj rows ; dt_proj],
+  // scan, [q8 ; out_proj].  The same float operations as step_unfused.
+  syn_status_t prepare_fused() {
+    int cus = 256, dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess)
+      (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    size_t per_layer = 0;
+    for (auto &B : blk) {
+      B.f_in = plan_split_gemv(B.in_proj.w.p, B.in_proj.scales.as<float>(), (int)(2 * di),
+                               B.in_proj.chunks, cus, 256);
+      B.f_out = plan_split_gemv(B.out_proj.w.p, B.out_proj.scales.as<float>(), (int)dm,
+                                B.out_proj.chunks, cus, 256);
+      per_layer = (size_t)B.f_in.N64 + B.f_out.N64;
+      if (c.int8_xdt) {
+        B.f_x = plan_split_gemv(B.x_i8.w.p, B.x_i8.scales.as<float>(), (int)nx, B.x_i8.chunks,
+                                cus, 256);
+        B.f_dt = plan_split_gemv(B.dt_i8.w.p, B.dt_i8.scales.as<float>(), (int)di,
+                                 B.dt_i8.chunks, cus, 256);
+        per_layer += (size_t)B.f_x.N64 + B.f_dt.N64;
+      }
+    }
+    acc_elems = per_layer * L;
+    SYN_TRY(acc.alloc(acc_elems * 4));
+    int *p = acc.as<int>();
+    for (auto &B : blk) {
+      SplitGemv *gs[4] = {&B.f_in, &B.f_out, &B.f_x, &B.f_dt};
+      for (int i = 0; i < (c.int8_xdt ? 4 : 2); i++) {
+        gs[i]->acc = p;
+        p += gs[i]->N64;
+      }
+    }
+    SYN_TRY(xres.alloc(2 * dm * 4));
+    SYN_TRY(scal.alloc(16 * 4));
+    SYN_TRY(zeros_m.alloc(dm * 4));
+    SYN_HIP(hipMemset(zeros_m.p, 0, zeros_m.bytes));
+    return SYN_OK;
+  }
+
+  bool fused_supported() const {
+    return fused_gemv_fits((int)dm) && fused_gemv_fits((int)di) && fused_gemv_fits((int)dr);
+  }
+
+  syn_status_t step_fused(hipStream_t s) {
+    float *sc = scal.as<float>();
+    float *s_in = sc + 0, *s_x = sc + 1, *s_dt = sc + 2, *s_out = sc + 3;
+    float *xr[2] = {xres.as<float>(), xres.as<float>() + dm};
+    SYN_TRY(launch_zero_i32(acc.as<int>(), acc_elems, s));
+    for (size_t l = 0; l < L; l++) {
+      Block &B = blk[l];
+      const RowSrc prev = l == 0 ? RowSrc{} : blk[l - 1].f_out.rows(s_out);
+      SYN_TRY(launch_fused_norm_gemv(l == 0 ? nullptr : xr[(l - 1) & 1], embed.as<float>(), st(),
+                                     (int)vocab, zeros_m.as<float>(), prev, xr[l & 1],
+                                     B.norm_w.as<float>(), c.eps, (int)dm, s_in, B.f_in, s,
+                                     /*sequential_sumsq=*/true));
+      const RowSrc proj_rows = B.f_in.rows(s_in);
+      SYN_TRY(launch_conv(l, proj_rows, s));
+      RowSrc xps, dtps;
+      if (c.int8_xdt) {
+        SYN_TRY(launch_fused_quant_gemv(xc.as<float>(), (int)di, s_x, B.f_x, s));
+        xps = B.f_x.rows(s_x);
+        SYN_TRY(launch_fused_rows_gemv(xps, (int)dr, s_dt, B.f_dt, s));
+        dtps = B.f_dt.rows(s_dt);
+      } else {
+        SYN_TRY(launch_gemv_f32_exact(B.xproj_p.as<float>(), xc.as<float>(), xc.bytes / 4,
+                                      (int)nx, (int)di, n8_of((int)nx), xp.as<float>(), s));
+        xps = f32_rows(xp.as<float>());
+      }
+      SYN_TRY(launch_scan(l, xps, dtps, offset_rows(proj_rows, di), s));
+      SYN_TRY(launch_fused_quant_gemv(g.as<float>(), (int)di, s_out, B.f_out, s));
+    }
+    return head(xr[(L - 1) & 1], blk[L - 1].f_out.rows(s_out), s);
+  }
+
+  syn_status_t step(hipStream_t s) { return fused ? step_fused(s) : step_unfused(s); }
 
   syn_status_t build_graph() {
     if (graph) return SYN_OK;
@@ -506,6 +641,10 @@ syn_status_t syn_hip_mamba_create(const syn_hip_mamba_config *cfg, syn_hip_mamba
   if (!cfg->d_model || !cfg->d_inner || !cfg->d_state || !cfg->d_conv || !cfg->dt_rank ||
       !cfg->n_layers || !cfg->vocab || cfg->max_tokens == 0)
     return SYN_ERR_INVALID_ARG;
+  if (cfg->d_state > (uint32_t)kScanDs) {  // the scan keeps a channel's state in registers
+    set_error("mamba: d_state above 16 is not supported by the scan kernel");
+    return SYN_ERR_INVALID_ARG;
+  }
   SYN_TRY(ensure_init());
   auto *m = new syn_hip_mamba_s();
   m->c = *cfg;
@@ -567,7 +706,7 @@ syn_status_t syn_hip_mamba_init_synthetic(syn_hip_mamba_t *m, uint64_t seed_base
     SYN_TRY(up(B.conv_w, cw));
     SYN_TRY(up(B.conv_b, std::vector<float>(di, 0.0f)));
     SYN_TRY(up(B.xproj_p, to_panels(xw.data(), nx, di)));
-    SYN_TRY(up(B.dtproj, dw));
+    SYN_TRY(up(B.dtproj, channel_minor(dw.data(), di, dr)));
     if (m->c.int8_xdt) {
       SYN_TRY(B.x_i8.from_f32(xw.data(), nx, di));
       SYN_TRY(B.dt_i8.from_f32(dw.data(), di, dr));
@@ -576,7 +715,7 @@ syn_status_t syn_hip_mamba_init_synthetic(syn_hip_mamba_t *m, uint64_t seed_base
     std::vector<float> al(di * ds);
     for (size_t i = 0; i < di; i++)
       for (size_t s2 = 0; s2 < ds; s2++) al[i * ds + s2] = logf((float)(s2 + 1));
-    SYN_TRY(up(B.a_log, al));
+    SYN_TRY(up(B.a_log, channel_minor(al.data(), di, ds)));
     SYN_TRY(up(B.dparam, std::vector<float>(di, 1.0f)));
     SYN_TRY(up(B.norm_w, std::vector<float>(dm, 1.0f)));
     SYN_TRY(B.in_proj.prepare(1));
@@ -616,6 +755,10 @@ syn_status_t syn_hip_mamba_init_synthetic(syn_hip_mamba_t *m, uint64_t seed_base
   SYN_HIP(hipMemset(m->gq.p, 0, m->gq.bytes));
   SYN_HIP(hipMemset(m->xcq.p, 0, m->xcq.bytes));
   SYN_HIP(hipMemset(m->xpq.p, 0, m->xpq.bytes));
+  if (m->fused_supported()) {
+    SYN_TRY(m->prepare_fused());
+    m->fused = true;
+  }
   m->ready = true;
   return m->reset();
 }
@@ -699,9 +842,21 @@ syn_status_t syn_hip_mamba_decode_timed(syn_hip_mamba_t *m, size_t steps, float 
   return SYN_OK;
 }
 
-syn_status_t syn_hip_mamba_set_options(syn_hip_mamba_t *m, int graph) {
-  if (!m) return SYN_ERR_NULL_PTR;
-  m->use_graph = graph != 0;
+syn_status_t syn_hip_mamba_set_options(syn_hip_mamba_t *m, int fused, int graph) {
+  SYN_TRY(check_mamba(m));
+  if (fused && !m->fused_supported()) {
+    set_error("fused mamba step: d_model / d_inner / dt_rank too large for the fused GEMV");
+    return SYN_ERR_INVALID_ARG;
+  }
+  if (fused && !m->acc.p) SYN_TRY(m->prepare_fused());
+  const bool f = fused != 0, g = graph != 0;
+  if (f != m->fused && m->graph) {  // the captured step is the other form
+    SYN_HIP(hipStreamSynchronize(m->stream));
+    SYN_HIP(hipGraphExecDestroy(m->graph));
+    m->graph = nullptr;
+  }
+  m->fused = f;
+  m->use_graph = g;
   return SYN_OK;
 }
 

@@ -112,7 +112,7 @@ SIGNATURES = {
     "syn_hip_mamba_decode_one": (ST, [P, C.c_uint32, P]),
     "syn_hip_mamba_generate": (ST, [P, P, SZ, SZ, P, P]),
     "syn_hip_mamba_decode_timed": (ST, [P, SZ, C.POINTER(C.c_float)]),
-    "syn_hip_mamba_set_options": (ST, [P, C.c_int]),
+    "syn_hip_mamba_set_options": (ST, [P, C.c_int, C.c_int]),
     "syn_hip_mamba_destroy": (ST, [P]),
     "syn_hip_fill_normal": (ST, [P, SZ, C.c_uint64, C.c_float]),
     "syn_hip_probe_mfma": (ST, [C.c_int, SZ, C.POINTER(C.c_double)]),
@@ -564,9 +564,10 @@ class QuantizedMamba:
         check(lib().syn_hip_mamba_decode_timed(self.h, steps, C.byref(ms)), "decode_timed")
         return ms.value
 
-    def set_options(self, graph: bool = True):
-        """HIP graph replay of the token step, or eager launches (same results)."""
-        check(lib().syn_hip_mamba_set_options(self.h, int(graph)), "set_options")
+    def set_options(self, fused: bool = True, graph: bool = True):
+        """Token-step form: fused split-K GEMV kernels or one kernel per op;
+        HIP graph replay or eager launches (same results either way)."""
+        check(lib().syn_hip_mamba_set_options(self.h, int(fused), int(graph)), "set_options")
 
     def close(self):
         if self.h:

@@ -77,3 +77,35 @@ def test_mamba_370m_shape():
     print("tokens", tg.tolist(), to.tolist(), "min margin", float(mo.min()))
     thin = next((i for i, m in enumerate(mo) if m < 1e-3), len(mo))
     np.testing.assert_array_equal(tg[:thin], to[:thin])
+
+
+RAGGED = dict(d_model=72, d_inner=136, d_state=16, d_conv=4, dt_rank=12, n_layers=3, vocab=301)
+
+
+def _bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("xdt", [False, True], ids=["ref", "int8xdt"])
+@pytest.mark.parametrize("cfg", [TINY, RAGGED, dict(MAMBA370, n_layers=4)],
+                         ids=["tiny", "ragged", "370m4"])
+def test_fused_step_matches_unfused(cfg, xdt):
+    # the fused split-K step computes the unfused step's float operations:
+    # logits and tokens agree bit for bit, graph or eager
+    print("case", cfg, "int8_xdt", xdt, flush=True)
+    g = hip.QuantizedMamba(dict(cfg, max_tokens=64), int8_xdt=xdt)
+    g.init_synthetic()
+    ids = O.token_ids(6, 0x5EED0000 + 0xFFFF, cfg["vocab"])
+    runs = {}
+    for fused in (True, False):
+        for graph in (True, False):
+            g.set_options(fused=fused, graph=graph)
+            lg = g.prefill(ids)
+            toks, margins = g.generate(ids, 12)
+            runs[(fused, graph)] = (lg, toks, margins)
+    ref = runs[(False, False)]
+    for key, (lg, toks, margins) in runs.items():
+        np.testing.assert_array_equal(_bits(lg), _bits(ref[0]), err_msg=f"fused,graph={key}")
+        np.testing.assert_array_equal(toks, ref[1], err_msg=f"fused,graph={key}")
+        np.testing.assert_array_equal(_bits(margins), _bits(ref[2]), err_msg=f"fused,graph={key}")
+    g.close()
