@@ -35,52 +35,106 @@ __device__ __forceinline__ float dot8(uint32_t w, const float *__restrict__ a, f
   return s;
 }
 
-template <int M>
+
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+}
+
+// grid (panels, ksplit); lane = output row, blocks [b0, b1) of this slice.
+// Load order: the activation blocks whose sums this thread forms (first
+// round, the waves that have any), then the first round of weight blocks,
+// so that the block sums only wait for the activations and the weights'
+// HBM latency overlaps them.  The dot products read the activations with
+// wave-uniform addresses (scalar loads).
+template <int M, int U>
 __global__ void __launch_bounds__(1024)
     k_gemv_q4_0(const u32x4 *__restrict__ nib, const uint16_t *__restrict__ sc,
                 const float *__restrict__ x, int ldx, float *__restrict__ y, int ldy,
                 float *__restrict__ part, int N, int B, int bs) {
-  extern __shared__ float smem[];
+  extern __shared__ __align__(16) float smem[];
+  const int NT = blockDim.x;
   const int panel = blockIdx.x, ks = blockIdx.y;
-  const int nw = blockDim.x >> 6;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
+  const int nw = NT >> 6;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
   const int b0 = ks * bs, b1 = min(B, b0 + bs), nb = b1 - b0;
   float *asum = smem;            // [M][bs]
   float *red = smem + M * bs;    // [nw][M][64]
-  for (int t = threadIdx.x; t < M * nb; t += blockDim.x) {
-    const int m = t / nb, b = b0 + (t - m * nb);
-    const float *xa = x + (size_t)m * ldx + (size_t)b * 32;
+  const size_t pbase = (size_t)panel * B;
+  const int nsum = M * nb;       // block sums of the slice
+  const bool sum_wave = wave * 64 < nsum;
+  float4 xa4[8];
+  int tslot = 0;
+  if (sum_wave) {
+    const int t = min(tid, nsum - 1);
+    const int m = M == 1 ? 0 : t / nb, bl = t - m * nb;
+    const float4 *src = reinterpret_cast<const float4 *>(x + (size_t)m * ldx + (size_t)(b0 + bl) * 32);
+#pragma unroll
+    for (int i = 0; i < 8; i++) xa4[i] = src[i];
+    tslot = m * bs + bl;
+  }
+  u32x4 q[U];
+  uint16_t dh[U];
+  auto issue = [&](int bb) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int b = min(bb + u * nw, b1 - 1);
+      q[u] = __builtin_nontemporal_load(nib + (pbase + b) * 64 + lane);
+      dh[u] = __builtin_nontemporal_load(sc + (pbase + b) * 64 + lane);
+    }
+  };
+  int bb = b0 + wave;
+  issue(min(bb, b1 - 1));
+  asm volatile("" ::: "memory");
+  if (sum_wave) {
     float s = 0.0f;
 #pragma unroll
+    for (int i = 0; i < 8; i++) {
+      s += xa4[i].x;
+      s += xa4[i].y;
+      s += xa4[i].z;
+      s += xa4[i].w;
+    }
+    asum[tslot] = s;  // clamped threads store the same value again
+  }
+  for (int t = tid + NT; t < nsum; t += NT) {  // slices with more sums than threads
+    const int m = t / nb, bl = t - m * nb;
+    const float *xa = x + (size_t)m * ldx + (size_t)(b0 + bl) * 32;
+    float s = 0.0f;
     for (int i = 0; i < 32; i++) s += xa[i];
-    asum[m * bs + (b - b0)] = s;
+    asum[m * bs + bl] = s;
   }
   __syncthreads();
   float acc[M];
 #pragma unroll
   for (int m = 0; m < M; m++) acc[m] = 0.0f;
-  const size_t pbase = (size_t)panel * B;
-  for (int b = b0 + wave; b < b1; b += nw) {
-    const u32x4 q = __builtin_nontemporal_load(nib + (pbase + b) * 64 + lane);
-    const float d = syn_f16_to_f32_ieee(__builtin_nontemporal_load(sc + (pbase + b) * 64 + lane));
+  for (; bb < b1; bb += nw * U) {
 #pragma unroll
-    for (int m = 0; m < M; m++) {
-      const float *xa = x + (size_t)m * ldx + (size_t)b * 32;
-      float s = 0.0f;
-      s = dot8(q.x, xa, s);
-      s = dot8(q.y, xa + 8, s);
-      s = dot8(q.z, xa + 16, s);
-      s = dot8(q.w, xa + 24, s);
-      const float blk = s - 8.0f * asum[m * bs + (b - b0)];
-      acc[m] = __builtin_fmaf(blk, d, acc[m]);
+    for (int u = 0; u < U; u++) {
+      const int b = bb + u * nw;
+      if (b < b1) {
+        const float d = f16_bits_to_f32(dh[u]);
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+          const float *xa = x + (size_t)m * ldx + (size_t)b * 32;
+          float s = 0.0f;
+          s = dot8(q[u].x, xa, s);
+          s = dot8(q[u].y, xa + 8, s);
+          s = dot8(q[u].z, xa + 16, s);
+          s = dot8(q[u].w, xa + 24, s);
+          const float blk = s - 8.0f * asum[m * bs + (b - b0)];
+          acc[m] = __builtin_fmaf(blk, d, acc[m]);
+        }
+      }
     }
+    if (bb + nw * U < b1) issue(bb + nw * U);
   }
 #pragma unroll
   for (int m = 0; m < M; m++) red[(wave * M + m) * 64 + lane] = acc[m];
   __syncthreads();
   const int N64 = gridDim.x * 64;
-  for (int t = threadIdx.x; t < M * 64; t += blockDim.x) {
+  for (int t = tid; t < M * 64; t += NT) {
     const int m = t >> 6, r = t & 63;
     float s = 0.0f;
     for (int w = 0; w < nw; w++) s += red[(w * M + m) * 64 + r];
@@ -89,6 +143,121 @@ __global__ void __launch_bounds__(1024)
       if (row < N) y[(size_t)m * ldy + row] = s;
     } else {
       part[((size_t)ks * M + m) * N64 + row] = s;
+    }
+  }
+}
+
+// Batch-1 form with mixed-precision FMAs.  A nibble e masked in place inside
+// the low 8 bits of a 16-bit half is the f16 subnormal e * 2^-24 (positions
+// 0-3) or 16e * 2^-24 (positions 4-7): exact, so each element costs one
+// v_fma_mix_f32 (f16 weight operand, f32 activation and accumulator) and a
+// dword of 8 nibbles one shift and four masks:
+//   w & 0x000f000f -> (e0, e4)      w & 0x00f000f0 -> 16 (e1, e5)
+//   (w>>8) & ...   -> (e2, e6)      (w>>8) & ...   -> 16 (e3, e7)
+// Products and sums stay in f32 (activations are not rounded); the block dot
+// is (s0 + s1/16) * 2^24, then Q4_0's -8 offset comes off as 8 * sum(x).
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ h2_t as_h2(uint32_t v) { return __builtin_bit_cast(h2_t, v); }
+
+template <int U>
+__global__ void __launch_bounds__(512)
+    k_gemv_q4_0h(const u32x4 *__restrict__ nib, const uint16_t *__restrict__ sc,
+                 const float *__restrict__ x, float *__restrict__ y, float *__restrict__ part,
+                 int N, int B, int bs) {
+  extern __shared__ __align__(16) float hsm[];
+  constexpr int NT = 512, NW = NT / 64;
+  const int panel = blockIdx.x, ks = blockIdx.y;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int b0 = ks * bs, b1 = min(B, b0 + bs), nb = b1 - b0;
+  float *asum = hsm;        // [bs]
+  float *red = hsm + bs;    // [NW][64]
+  const size_t pbase = (size_t)panel * B;
+  // 1. activation blocks of this thread's block sum (waves that have one)
+  const bool sum_wave = wave * 64 < nb;
+  float4 xa4[8];
+  if (sum_wave) {
+    const float4 *src =
+        reinterpret_cast<const float4 *>(x + (size_t)(b0 + min(tid, nb - 1)) * 32);
+#pragma unroll
+    for (int i = 0; i < 8; i++) xa4[i] = src[i];
+  }
+  // 2. the first round of weight blocks
+  u32x4 q[U];
+  uint16_t dh[U];
+  auto issue = [&](int bb) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int b = min(bb + u * NW, b1 - 1);
+      q[u] = __builtin_nontemporal_load(nib + (pbase + b) * 64 + lane);
+      dh[u] = __builtin_nontemporal_load(sc + (pbase + b) * 64 + lane);
+    }
+  };
+  int bb = b0 + wave;
+  issue(min(bb, b1 - 1));
+  asm volatile("" ::: "memory");
+  if (sum_wave) {
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      s += xa4[i].x;
+      s += xa4[i].y;
+      s += xa4[i].z;
+      s += xa4[i].w;
+    }
+    if (tid < nb) asum[tid] = s;
+  }
+  for (int t = tid + NT; t < nb; t += NT) {  // slices of more than 512 blocks
+    const float *xa = x + (size_t)(b0 + t) * 32;
+    float s = 0.0f;
+    for (int i = 0; i < 32; i++) s += xa[i];
+    asum[t] = s;
+  }
+  __syncthreads();
+  float acc = 0.0f;
+  for (; bb < b1; bb += NW * U) {
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const int b = bb + u * NW;
+      if (b < b1) {
+        const float *xa = x + (size_t)b * 32;
+        const uint32_t wd[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+        float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          const uint32_t w = wd[c], w8 = wd[c] >> 8;
+          const float *xc = xa + 8 * c;
+          const h2_t p0 = as_h2(w & 0x000f000fu), p1 = as_h2(w & 0x00f000f0u);
+          const h2_t p2 = as_h2(w8 & 0x000f000fu), p3 = as_h2(w8 & 0x00f000f0u);
+          s0 = __builtin_fmaf((float)p0.x, xc[0], s0);
+          s1 = __builtin_fmaf((float)p1.x, xc[1], s1);
+          s0 = __builtin_fmaf((float)p2.x, xc[2], s0);
+          s1 = __builtin_fmaf((float)p3.x, xc[3], s1);
+          s0 = __builtin_fmaf((float)p0.y, xc[4], s0);
+          s1 = __builtin_fmaf((float)p1.y, xc[5], s1);
+          s0 = __builtin_fmaf((float)p2.y, xc[6], s0);
+          s1 = __builtin_fmaf((float)p3.y, xc[7], s1);
+        }
+        const float dot = __builtin_fmaf(s1, 0.0625f, s0) * 16777216.0f;
+        const float blk = dot - 8.0f * asum[b - b0];
+        acc = __builtin_fmaf(blk, f16_bits_to_f32(dh[u]), acc);
+      }
+    }
+    if (bb + NW * U < b1) issue(bb + NW * U);
+  }
+  red[wave * 64 + lane] = acc;
+  __syncthreads();
+  if (tid < 64) {
+    float s = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; w++) s += red[w * 64 + tid];
+    const int row = panel * 64 + tid;
+    if (gridDim.y == 1) {
+      if (row < N) y[row] = s;
+    } else {
+      part[(size_t)ks * gridDim.x * 64 + row] = s;
     }
   }
 }
@@ -104,13 +273,20 @@ __global__ void __launch_bounds__(256)
   y[(size_t)m * ldy + row] = s;
 }
 
+// U blocks in flight per wave: 8 with 8 waves when a slice has >= 64
+// blocks (four workgroups per CU stream the matrix), else 4 with up to 16
 template <int M>
 static void launch_q4_m(const GemvPlan &p, const u32x4 *nib, const uint16_t *sc, const float *x,
                         int ldx, float *y, int ldy, float *part, int N, hipStream_t s) {
-  const int waves = std::min(p.waves, M >= 8 ? 8 : 16);
+  const bool wide = p.cs >= 64;
+  const int waves = wide ? 8 : std::min(p.waves, M >= 8 ? 8 : 16);
   const size_t shm = ((size_t)M * p.cs + (size_t)waves * M * 64) * sizeof(float);
-  hipLaunchKernelGGL(k_gemv_q4_0<M>, dim3(p.panels, p.ksplit), dim3(64 * waves), shm, s, nib, sc,
-                     x, ldx, y, ldy, part, N, p.chunks, p.cs);
+  if (wide)
+    hipLaunchKernelGGL((k_gemv_q4_0<M, 8>), dim3(p.panels, p.ksplit), dim3(64 * waves), shm, s,
+                       nib, sc, x, ldx, y, ldy, part, N, p.chunks, p.cs);
+  else
+    hipLaunchKernelGGL((k_gemv_q4_0<M, 4>), dim3(p.panels, p.ksplit), dim3(64 * waves), shm, s,
+                       nib, sc, x, ldx, y, ldy, part, N, p.chunks, p.cs);
 }
 
 typedef void (*q4_launcher)(const GemvPlan &, const u32x4 *, const uint16_t *, const float *,
@@ -132,8 +308,16 @@ syn_status_t QLinearQ4_0::gemv(size_t m, const float *d_x, size_t ldx, float *d_
       SYN_HIP(hipDeviceSynchronize());
       SYN_TRY(part.alloc(part_elems * sizeof(float)));
     }
-    kQ4Launch[mb](p, nib.as<u32x4>(), sc.as<uint16_t>(), d_x + m0 * ldx, (int)ldx,
-                  d_y + m0 * ldy, (int)ldy, part.as<float>(), (int)n, s);
+    const size_t shm_h = ((size_t)p.cs + 8 * 64) * 4;
+    if (mb == 1 && shm_h <= 60 * 1024) {
+      // two blocks per wave and round: measured best at the LLaMA shapes
+      hipLaunchKernelGGL(k_gemv_q4_0h<2>, dim3(p.panels, p.ksplit), dim3(512), shm_h, s,
+                         nib.as<u32x4>(), sc.as<uint16_t>(), d_x + m0 * ldx, d_y + m0 * ldy,
+                         part.as<float>(), (int)n, p.chunks, p.cs);
+    } else {
+      kQ4Launch[mb](p, nib.as<u32x4>(), sc.as<uint16_t>(), d_x + m0 * ldx, (int)ldx,
+                    d_y + m0 * ldy, (int)ldy, part.as<float>(), (int)n, s);
+    }
     SYN_LAUNCH_CHECK();
     if (p.ksplit > 1) {
       const int total = mb * (int)n;
