@@ -2,13 +2,13 @@
 //
 // The reference runs these formats as f32 sgemmTiled over weights
 // dequantized at load (ops/matmul.rs:55-79, matmul.zig:157-183).  Here a
-// workgroup owns a 128 x 128 tile of Y = X W^T and walks K 32 elements at a
-// time (one Q8_0 block / one Q4_K sub-block / two Q6_K sub-blocks): the
-// weight tile is decoded once per workgroup from the HBM plane layout into
-// f16 in LDS (value = the reference dequantizer's f32 value rounded to f16),
-// activations are pre-converted to f16, and v_mfma_f32_16x16x32_f16
-// accumulates in f32.  The two f16 roundings (relative 2^-11 each) keep the
-// result well inside the 1e-3 per-row tolerance (measured in the tests).
+// workgroup owns a 256 x 128 tile of Y = X W^T and walks K 64 elements at a
+// time: the weight tile is decoded once per workgroup from the HBM plane
+// layout into f16 in LDS (value = the reference dequantizer's f32 value
+// rounded to f16), activations are pre-converted to f16, and
+// v_mfma_f32_32x32x16_f16 accumulates in f32.  The two f16 roundings
+// (relative 2^-11 each) keep the result well inside the 1e-3 per-row
+// tolerance (measured in the tests).
 #include <algorithm>
 
 #include "decode_fused.hpp"
@@ -36,21 +36,14 @@ __global__ void k_f32_to_f16(const float *__restrict__ x, int ldx, _Float16 *__r
 }
 
 // ---------------------------------------------------------------------------
-// Pipelined form.  A workgroup (8 waves, 4 x 2, each a 64 x 64 sub-tile) owns
-// a 256 x 128 tile of Y and walks its K range 64 elements per step.  Each
-// thread keeps the raw global bytes of the next kDepth steps in a register
-// ring (activations: 4 x 16 B; weights: the planes and scale of 16 elements
-// of one row), so a step's loads are issued kDepth steps before the step is
-// staged: the thread writes its activation chunks to LDS, decodes its 16
-// weights into f16 in LDS (the reference dequantizer's value rounded once to
-// f16), re-fills the ring slot with the loads of step + kDepth, and the waves
-// run 2 x 16 v_mfma_f32_16x16x32_f16 over the staged tile.  Loads are
-// unconditional from clamped (in-bounds) rows and steps.  Shapes with fewer
-// tiles than the GPU has CUs split K over the grid's z dimension and add
-// their partial tiles with f32 atomics into a zeroed Y.
+// Tiling.  A workgroup owns a 256 x 128 tile of Y and walks its K range 64
+// elements per step through two LDS stages of A [256][72] and B [128][72]
+// f16.  Weights are decoded from the HBM plane layout into f16 (the reference
+// dequantizer's value rounded once to f16); loads are unconditional from
+// clamped (in-bounds) rows and steps.  Shapes with fewer tiles than the GPU
+// has CUs split K over the grid's z dimension and add their partial tiles
+// with f32 atomics into a zeroed Y.
 constexpr int PGM = 256, PGN = 128, PGK = 64, PGLD = PGK + 8;  // LDS row stride in halfs
-constexpr int PGT = 512;                                        // threads
-constexpr int kDepth = 3;
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
@@ -181,20 +174,94 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // LDS: two stages of A [256][72] and B [128][72] f16 (110,592 bytes)
 constexpr int PG_STAGE = (PGM + PGN) * PGLD;
 
+// ---------------------------------------------------------------------------
+// Wave-specialised form: 12 waves, 8 consumers and 4 producers.  The eight
+// consumer waves (4 x 2, each a 64 x 64 sub-tile of the 256 x 128 tile) only
+// read operand fragments from LDS and issue MFMAs; the four producer waves
+// only move data: they keep the raw global bytes of the next kPDepth steps in
+// a register ring, write step t+1's activations and decoded f16 weights into
+// the other LDS stage while the consumers multiply step t, and refill the
+// ring.  One barrier per step separates the stages.  On each SIMD the matrix
+// core work of two consumer waves overlaps the loads, decode and LDS stores
+// of one producer wave.  Each role runs its own loop (its values stay out of
+// the other role's registers); both meet the same barriers.
+constexpr int PGT2 = 768, kPDepth = 2;
+
 template <int FMT, bool EXACT>
-__global__ void __launch_bounds__(PGT)
-    k_gemm_kq(const _Float16 *__restrict__ Xh, int ldh, int M, int K,
-              const u32x4 *__restrict__ W, const uint16_t *__restrict__ Wd, int N, int B,
-              float *__restrict__ Y, int ldy, int steps_per_split) {
+__global__ void __launch_bounds__(PGT2)
+    k_gemm_kq2(const _Float16 *__restrict__ Xh, int ldh, int M, int K,
+               const u32x4 *__restrict__ W, const uint16_t *__restrict__ Wd, int N, int B,
+               float *__restrict__ Y, int ldy, int steps_per_split) {
   extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int n0 = blockIdx.x * PGN, m0 = blockIdx.y * PGM;
-  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
-  const int l32 = lane & 31, lh = lane >> 5;
   const int s_begin = blockIdx.z * steps_per_split;
   const int nsteps = min((K + PGK - 1) / PGK - s_begin, steps_per_split);
-  // 2 x 2 tiles of 32 x 32 per wave; lane l of a tile holds column l%32 and
-  // rows 8*(r/4) + 4*(l/32) + r%4 for r = 0..15 (v_mfma_f32_32x32x16_f16)
+  if (wave >= 8) {
+    // ------------------------------------------------------------ producer
+    const int pt = tid - 512;  // 0..255
+    // A: 2048 chunks of 16 B per step, eight per producer thread
+    const _Float16 *arow[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const int idx = pt + i * 256;
+      arow[i] = Xh + (size_t)min(m0 + (idx >> 3), M - 1) * ldh + (idx & 7) * 8;
+    }
+    // W: row n0 + pt/2 (clamped), quarters 2*(pt%2), 2*(pt%2)+1 of the step
+    const int brow = pt >> 1, bq0 = 2 * (pt & 1);
+    const int bn = min(n0 + brow, N - 1);
+    u32x4 ra[kPDepth][8];
+    RawW rw[kPDepth][2];
+    auto load = [&](int slot, int t) {
+      const int step = s_begin + min(t, nsteps - 1);
+#pragma unroll
+      for (int i = 0; i < 8; i++)
+        ra[slot][i] = *reinterpret_cast<const u32x4 *>(arow[i] + (size_t)step * PGK);
+      pg_load_w<FMT>(rw[slot][0], W, Wd, B, bn, step, bq0);
+      pg_load_w<FMT>(rw[slot][1], W, Wd, B, bn, step, bq0 + 1);
+    };
+    auto stage = [&](int slot, int t, int buf) {
+      _Float16 *As = lds + buf * PG_STAGE, *Bs = As + PGM * PGLD;
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const int idx = pt + i * 256;
+        *reinterpret_cast<u32x4 *>(&As[(idx >> 3) * PGLD + (idx & 7) * 8]) = ra[slot][i];
+      }
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        uint32_t wv[8];
+        pg_decode_w<FMT, EXACT>(rw[slot][h], s_begin + t, bq0 + h, B, wv);
+        u32x4 *dst = reinterpret_cast<u32x4 *>(&Bs[brow * PGLD + (bq0 + h) * 16]);
+        dst[0] = u32x4{wv[0], wv[1], wv[2], wv[3]};
+        dst[1] = u32x4{wv[4], wv[5], wv[6], wv[7]};
+      }
+      load(slot, t + kPDepth);
+    };
+#pragma unroll
+    for (int i = 0; i < kPDepth; i++) load(i, i);
+    stage(0, 0, 0);
+    __syncthreads();
+    // iteration t stages step t+1 (ring slot (t+1) % kPDepth) into stage (t+1)%2
+    int t0 = 0;
+    for (; t0 + 2 * kPDepth < nsteps; t0 += 2 * kPDepth) {
+#pragma unroll
+      for (int j = 0; j < 2 * kPDepth; j++) {
+        stage((j + 1) % kPDepth, t0 + j + 1, (j + 1) & 1);
+        __syncthreads();
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2 * kPDepth; j++) {
+      if (t0 + j < nsteps) {
+        if (t0 + j + 1 < nsteps) stage((j + 1) % kPDepth, t0 + j + 1, (j + 1) & 1);
+        __syncthreads();
+      }
+    }
+    return;
+  }
+  // -------------------------------------------------------------- consumer
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  const int l32 = lane & 31, lh = lane >> 5;
   f32x16 acc[2][2];
 #pragma unroll
   for (int mt = 0; mt < 2; mt++)
@@ -202,46 +269,15 @@ __global__ void __launch_bounds__(PGT)
     for (int nt = 0; nt < 2; nt++)
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[mt][nt][r] = 0.0f;
-
-  // A: 256 rows x 64 halfs = 2048 chunks of 16 B, four per thread
-  const _Float16 *arow[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int idx = tid + i * PGT;
-    arow[i] = Xh + (size_t)min(m0 + (idx >> 3), M - 1) * ldh + (idx & 7) * 8;
-  }
-  // W: row n0 + tid/4 (clamped), elements 16*(tid%4) .. +15 of the step
-  const int brow = tid >> 2, bq = tid & 3;
-  const int bn = min(n0 + brow, N - 1);
-
-  u32x4 ra[kDepth][4];
-  RawW rw[kDepth];
-  auto load = [&](int slot, int t) {  // step t of this split (clamped)
-    const int step = s_begin + min(t, nsteps - 1);
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-      ra[slot][i] = *reinterpret_cast<const u32x4 *>(arow[i] + (size_t)step * PGK);
-    pg_load_w<FMT>(rw[slot], W, Wd, B, bn, step, bq);
-  };
-  // stage ring slot `slot` (step t) into LDS stage `buf`, then refill the slot
-  auto stage = [&](int slot, int t, int buf) {
-    _Float16 *As = lds + buf * PG_STAGE, *Bs = As + PGM * PGLD;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const int idx = tid + i * PGT;
-      *reinterpret_cast<u32x4 *>(&As[(idx >> 3) * PGLD + (idx & 7) * 8]) = ra[slot][i];
-    }
-    uint32_t wv[8];
-    pg_decode_w<FMT, EXACT>(rw[slot], s_begin + t, bq, B, wv);
-    u32x4 *dst = reinterpret_cast<u32x4 *>(&Bs[brow * PGLD + bq * 16]);
-    dst[0] = u32x4{wv[0], wv[1], wv[2], wv[3]};
-    dst[1] = u32x4{wv[4], wv[5], wv[6], wv[7]};
-    load(slot, t + kDepth);
-  };
-  // operand fragments of a whole step are read from LDS before its MFMAs
+  // Two consumer groups half a step apart: waves 0-3 read step t's
+  // fragments and multiply them; waves 4-7 first multiply step t-1's
+  // fragments (held in registers across the barrier), then read step t's.
+  // Each SIMD holds one wave of each group, so one wave's LDS reads overlap
+  // the other's matrix-core work.
+  const bool lag = wave >= 4;
   f16x8 fa[4][2], fb[4][2];
-  auto frag = [&](int buf) {
-    const _Float16 *As = lds + buf * PG_STAGE, *Bs = As + PGM * PGLD;
+  auto read = [&](int t) {
+    const _Float16 *As = lds + (t & 1) * PG_STAGE, *Bs = As + PGM * PGLD;
 #pragma unroll
     for (int k16 = 0; k16 < 4; k16++) {
 #pragma unroll
@@ -254,41 +290,33 @@ __global__ void __launch_bounds__(PGT)
             &Bs[(wn + nt * 32 + l32) * PGLD + k16 * 16 + lh * 8]);
     }
   };
-  auto mma = [&](int k16) {
+  auto mma = [&]() {
 #pragma unroll
-    for (int mt = 0; mt < 2; mt++)
+    for (int k16 = 0; k16 < 4; k16++)
 #pragma unroll
-      for (int nt = 0; nt < 2; nt++)
-        acc[mt][nt] =
-            __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[k16][mt], fb[k16][nt], acc[mt][nt], 0, 0, 0);
+      for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++)
+          acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[k16][mt], fb[k16][nt],
+                                                               acc[mt][nt], 0, 0, 0);
   };
-
-#pragma unroll
-  for (int i = 0; i < kDepth; i++) load(i, i);
-  stage(0, 0, 0);
-  __syncthreads();
-  // step t: MFMAs on stage t%2; step t+1 is staged into the other stage in
-  // the middle of them (its decode and LDS stores overlap the matrix cores);
-  // one barrier per step.  The steady-state body has no conditionals, so the
-  // compiler's load counters see the ring's 2-step lead.
-  auto step_body = [&](int j, int t, bool stage_next) {
-    const int buf = j & 1;
-    frag(buf);
-    mma(0);
-    mma(1);
-    if (stage_next) stage((j + 1) % kDepth, t + 1, buf ^ 1);
-    mma(2);
-    mma(3);
+  __syncthreads();  // step 0 staged
+  if (!lag) {
+    for (int t = 0; t < nsteps; t++) {
+      read(t);
+      mma();
+      __syncthreads();
+    }
+  } else {
+    read(0);
     __syncthreads();
-  };
-  int t0 = 0;
-  for (; t0 + 2 * kDepth < nsteps; t0 += 2 * kDepth) {
-#pragma unroll
-    for (int j = 0; j < 2 * kDepth; j++) step_body(j, t0 + j, true);
+    for (int t = 1; t < nsteps; t++) {
+      mma();
+      read(t);
+      __syncthreads();
+    }
+    mma();
   }
-#pragma unroll
-  for (int j = 0; j < 2 * kDepth; j++)
-    if (t0 + j < nsteps) step_body(j, t0 + j, t0 + j + 1 < nsteps);
   const bool atomic = gridDim.z > 1;
 #pragma unroll
   for (int mt = 0; mt < 2; mt++)
@@ -344,10 +372,10 @@ syn_status_t QLinearKQ::gemm(size_t m, const float *d_x, size_t ldx, float *d_y,
   static bool attr_set[4] = {false, false, false, false};
   const bool exact = fmt != SYN_HIP_FMT_Q8_0 || q8_scales_f16_exact;
   const int fi = fmt == SYN_HIP_FMT_Q8_0 ? (exact ? 0 : 3) : fmt == SYN_HIP_FMT_Q4_K ? 1 : 2;
-  const void *fns[4] = {(const void *)k_gemm_kq<SYN_HIP_FMT_Q8_0, true>,
-                        (const void *)k_gemm_kq<SYN_HIP_FMT_Q4_K, true>,
-                        (const void *)k_gemm_kq<SYN_HIP_FMT_Q6_K, true>,
-                        (const void *)k_gemm_kq<SYN_HIP_FMT_Q8_0, false>};
+  const void *fns[4] = {(const void *)k_gemm_kq2<SYN_HIP_FMT_Q8_0, true>,
+                        (const void *)k_gemm_kq2<SYN_HIP_FMT_Q4_K, true>,
+                        (const void *)k_gemm_kq2<SYN_HIP_FMT_Q6_K, true>,
+                        (const void *)k_gemm_kq2<SYN_HIP_FMT_Q8_0, false>};
   if (!attr_set[fi]) {  // more than the default 64 KiB of dynamic LDS
     SYN_HIP(hipFuncSetAttribute(fns[fi], hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm));
     attr_set[fi] = true;
@@ -356,17 +384,17 @@ syn_status_t QLinearKQ::gemm(size_t m, const float *d_x, size_t ldx, float *d_y,
   const uint16_t *Wd = wd.as<uint16_t>();
   const _Float16 *X = xh.as<_Float16>();
   if (fi == 0)
-    hipLaunchKernelGGL((k_gemm_kq<SYN_HIP_FMT_Q8_0, true>), grid, dim3(PGT), shm, s, X, (int)ldh,
-                       (int)m, (int)k, W, Wd, (int)n, blocks, d_y, (int)ldy, per);
+    hipLaunchKernelGGL((k_gemm_kq2<SYN_HIP_FMT_Q8_0, true>), grid, dim3(PGT2), shm, s, X,
+                       (int)ldh, (int)m, (int)k, W, Wd, (int)n, blocks, d_y, (int)ldy, per);
   else if (fi == 3)
-    hipLaunchKernelGGL((k_gemm_kq<SYN_HIP_FMT_Q8_0, false>), grid, dim3(PGT), shm, s, X,
+    hipLaunchKernelGGL((k_gemm_kq2<SYN_HIP_FMT_Q8_0, false>), grid, dim3(PGT2), shm, s, X,
                        (int)ldh, (int)m, (int)k, W, Wd, (int)n, blocks, d_y, (int)ldy, per);
   else if (fi == 1)
-    hipLaunchKernelGGL((k_gemm_kq<SYN_HIP_FMT_Q4_K, true>), grid, dim3(PGT), shm, s, X, (int)ldh,
-                       (int)m, (int)k, W, Wd, (int)n, blocks, d_y, (int)ldy, per);
+    hipLaunchKernelGGL((k_gemm_kq2<SYN_HIP_FMT_Q4_K, true>), grid, dim3(PGT2), shm, s, X,
+                       (int)ldh, (int)m, (int)k, W, Wd, (int)n, blocks, d_y, (int)ldy, per);
   else
-    hipLaunchKernelGGL((k_gemm_kq<SYN_HIP_FMT_Q6_K, true>), grid, dim3(PGT), shm, s, X, (int)ldh,
-                       (int)m, (int)k, W, Wd, (int)n, blocks, d_y, (int)ldy, per);
+    hipLaunchKernelGGL((k_gemm_kq2<SYN_HIP_FMT_Q6_K, true>), grid, dim3(PGT2), shm, s, X,
+                       (int)ldh, (int)m, (int)k, W, Wd, (int)n, blocks, d_y, (int)ldy, per);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
 }
