@@ -2,130 +2,204 @@
 //
 // Reference: int8GemmTiled for M > 16 (qmatmul.zig:68-99, 442-548): the
 // exact i32 sum of each KC = 512 chunk of K is converted and added in chunk
-// order, C += (f32(acc_chunk) * sa[i]) * sb[j].  Here each workgroup owns a
-// 128 x 128 tile of C; K advances 64 bytes per step through
-// v_mfma_i32_16x16x64_i8 (exact integer products), and every 8 steps (one KC
-// chunk) the i32 accumulators are folded into an f32 tile in that order.
+// order, C += (f32(acc_chunk) * sa[i]) * sb[j].  Here K advances 64 bytes per
+// step through v_mfma_i32_32x32x32_i8 (exact integer products), and every 8
+// steps (one KC chunk) the i32 accumulators are folded into an f32 tile in
+// that order, so the result is bit-identical to the reference.
 //
 // Operands: activations int8 [M, ldx] row-major; weights in the 64-row panel
 // layout (linear.hpp), so a 64-byte K step of a panel is 4 contiguous 1 KiB
-// chunk blocks.  LDS holds A [128][64] and B [128][64] (+16 B row padding).
-// Lane mapping (16x16x64): lane l supplies row/col l%16 and K bytes
-// 16*(l/16)..+15 of both operands; the 4 result registers of lane l are rows
-// 4*(l/16)+r, column l%16.
+// chunk blocks.
 #include <algorithm>
 
 #include "linear.hpp"
 
 namespace syn {
 
-constexpr int GBM = 128, GBN = 128, GBK = 64, GPAD = 16, GLD = GBK + GPAD;
+// ---------------------------------------------------------------------------
+// Wave-specialised form.  A workgroup owns a TM x 128 tile of C (TM = 256 or
+// 128): TM/32 consumer waves (TM/64 x 2, each 64 x 64 as 2 x 2 tiles of
+// 32 x 32) read operand fragments from LDS and issue MFMAs;
+// four producer waves keep the next kWDepth K steps of raw int8 bytes in a
+// register ring and copy step t+1 into the other LDS stage while the
+// consumers multiply step t.  One barrier per 64-byte K step; every 8 steps
+// (one KC = 512 chunk) the consumers fold the exact i32 chunk sums into the
+// f32 tile in chunk order, C += (f32(acc) * sa) * sb, as the reference does.
+// The two consumer groups run half a step apart (waves 4-7 multiply the
+// previous step while waves 0-3 read the current one).  LDS rows are 80
+// bytes (64 + 16 pad), which spreads 16 consecutive rows' 16-byte fragment
+// reads over all 64 banks.  Operand layout (32x32x32 i8): lane l holds
+// row/column l%32 and K bytes 16*(l/32)..+15 of a 32-byte K slice; result
+// register r of lane l is row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+constexpr int WBN = 128, WBK = 64, WLD = WBK + 16;
+constexpr int kWDepth = 3;
+template <int TM> constexpr int w_stage() { return (TM + WBN) * WLD; }  // bytes per LDS stage
 
-__global__ void __launch_bounds__(256)
-    k_gemm_w8a8(const int8_t *__restrict__ xq, int ldx, const float *__restrict__ sx, int M,
-                const i32x4 *__restrict__ W, const float *__restrict__ ws, int N, int C,
-                float *__restrict__ y, int ldy) {
-  __shared__ __attribute__((aligned(16))) int8_t As[GBM * GLD];
-  __shared__ __attribute__((aligned(16))) int8_t Bs[GBN * GLD];
+typedef int i32x16 __attribute__((ext_vector_type(16)));
+
+template <int TM>
+__global__ void __launch_bounds__(TM * 2 + 256)
+    k_gemm_w8a8_ws(const int8_t *__restrict__ xq, int ldx, const float *__restrict__ sx, int M,
+                   const i32x4 *__restrict__ W, const float *__restrict__ ws, int N, int C,
+                   float *__restrict__ y, int ldy) {
+  constexpr int W_STAGE = w_stage<TM>(), NC = TM / 32, AI = TM / 64;
+  extern __shared__ __attribute__((aligned(16))) int8_t wlds[];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int n0 = blockIdx.x * GBN, m0 = blockIdx.y * GBM;
-  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
-  const int P = (N + 63) >> 6;
+  const int n0 = blockIdx.x * WBN, m0 = blockIdx.y * TM;
   const int nsteps = (C + 3) >> 2;
-  const int lr = lane & 15, lg = lane >> 4;
-
-  float sa[4][4], sb[4];
+  const int P = (N + 63) >> 6;
+  if (wave >= NC) {
+    // ------------------------------------------------------------ producer
+    const int pt = tid - NC * 64;  // 0..255
+    // A: TM rows x 4 chunks per step, TM/64 per thread (row pt/4 + 64 i,
+    // chunk pt%4); B: 128 rows x 4 chunks, two per thread (row pt%64 of
+    // panel pt/128, chunks (pt/64)%2 and +2)
+    const int ac = pt & 3;
+    const int8_t *arow[AI];
 #pragma unroll
-  for (int mt = 0; mt < 4; mt++)
+    for (int i = 0; i < AI; i++)
+      arow[i] = xq + (size_t)min(m0 + (pt >> 2) + 64 * i, M - 1) * ldx + ac * 16;
+    const int br = pt & 63, bpp = pt >> 7, bc0 = (pt >> 6) & 1;
+    const int bpanel = min((n0 >> 6) + bpp, P - 1);
+    const i32x4 *bsrc = W + (size_t)bpanel * C * 64 + br;
+    i32x4 ra[kWDepth][AI], rb[kWDepth][2];
+    auto load = [&](int slot, int t) {
+      const int step = min(t, nsteps - 1);
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int m = m0 + wm + mt * 16 + 4 * lg + r;
-      sa[mt][r] = m < M ? sx[m] : 0.0f;
-    }
+      for (int i = 0; i < AI; i++)
+        ra[slot][i] = *reinterpret_cast<const i32x4 *>(arow[i] + (size_t)step * WBK);
 #pragma unroll
-  for (int nt = 0; nt < 4; nt++) {
-    const int n = n0 + wn + nt * 16 + lr;
-    sb[nt] = n < N ? ws[n] : 0.0f;
-  }
-
-  i32x4 acc[4][4];
-  float cf[4][4][4];
+      for (int h = 0; h < 2; h++) {
+        const int c = min(step * 4 + bc0 + 2 * h, C - 1);
+        rb[slot][h] = __builtin_nontemporal_load(bsrc + (size_t)c * 64);
+      }
+    };
+    auto stage = [&](int slot, int t, int buf) {
+      int8_t *As = wlds + buf * W_STAGE, *Bs = As + TM * WLD;
+      const bool a_in = t * 4 + ac < C;  // chunks past K are zero
 #pragma unroll
-  for (int mt = 0; mt < 4; mt++)
+      for (int i = 0; i < AI; i++) {
+        const i32x4 v = a_in ? ra[slot][i] : i32x4{0, 0, 0, 0};
+        *reinterpret_cast<i32x4 *>(&As[((pt >> 2) + 64 * i) * WLD + ac * 16]) = v;
+      }
 #pragma unroll
-    for (int nt = 0; nt < 4; nt++) {
-      acc[mt][nt] = i32x4{0, 0, 0, 0};
+      for (int h = 0; h < 2; h++) {
+        const int c = bc0 + 2 * h;
+        const i32x4 v = t * 4 + c < C ? rb[slot][h] : i32x4{0, 0, 0, 0};
+        *reinterpret_cast<i32x4 *>(&Bs[(bpp * 64 + br) * WLD + c * 16]) = v;
+      }
+      load(slot, t + kWDepth);
+    };
 #pragma unroll
-      for (int r = 0; r < 4; r++) cf[mt][nt][r] = 0.0f;
-    }
-
-  // global -> register staging for one K step (2 x 16 B per thread per operand)
-  i32x4 ga[2], gb[2];
-  auto fetch = [&](int step) {
-#pragma unroll
-    for (int it = 0; it < 2; it++) {
-      const int idx = tid + it * 256;
-      const int r = idx >> 2, cc = idx & 3;
-      const int row = m0 + r, kb = step * GBK + cc * 16;
-      ga[it] = i32x4{0, 0, 0, 0};
-      if (row < M && kb < ldx) ga[it] = *reinterpret_cast<const i32x4 *>(xq + (size_t)row * ldx + kb);
-      const int br = idx & 63, bc = (idx >> 6) & 3, pp = idx >> 8;
-      const int panel = (n0 >> 6) + pp, chunk = step * 4 + bc;
-      gb[it] = i32x4{0, 0, 0, 0};
-      if (panel < P && chunk < C) gb[it] = __builtin_nontemporal_load(W + ((size_t)panel * C + chunk) * 64 + br);
-    }
-  };
-  auto stash = [&]() {
-#pragma unroll
-    for (int it = 0; it < 2; it++) {
-      const int idx = tid + it * 256;
-      *reinterpret_cast<i32x4 *>(&As[(idx >> 2) * GLD + (idx & 3) * 16]) = ga[it];
-      const int br = idx & 63, bc = (idx >> 6) & 3, pp = idx >> 8;
-      *reinterpret_cast<i32x4 *>(&Bs[(pp * 64 + br) * GLD + bc * 16]) = gb[it];
-    }
-  };
-
-  fetch(0);
-  for (int step = 0; step < nsteps; step++) {
-    __syncthreads();  // previous step's LDS reads are done
-    stash();
+    for (int i = 0; i < kWDepth; i++) load(i, i);
+    stage(0, 0, 0);
     __syncthreads();
-    if (step + 1 < nsteps) fetch(step + 1);  // overlaps the MFMAs below
-    i32x4 a[4], b[4];
+    int t0 = 0;
+    for (; t0 + 2 * kWDepth < nsteps; t0 += 2 * kWDepth) {
 #pragma unroll
-    for (int mt = 0; mt < 4; mt++)
-      a[mt] = *reinterpret_cast<const i32x4 *>(&As[(wm + mt * 16 + lr) * GLD + lg * 16]);
-#pragma unroll
-    for (int nt = 0; nt < 4; nt++)
-      b[nt] = *reinterpret_cast<const i32x4 *>(&Bs[(wn + nt * 16 + lr) * GLD + lg * 16]);
-#pragma unroll
-    for (int mt = 0; mt < 4; mt++)
-#pragma unroll
-      for (int nt = 0; nt < 4; nt++)
-        acc[mt][nt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a[mt], b[nt], acc[mt][nt], 0, 0, 0);
-    if (((step + 1) & 7) == 0 || step + 1 == nsteps) {  // end of a KC=512 chunk
-#pragma unroll
-      for (int mt = 0; mt < 4; mt++)
-#pragma unroll
-        for (int nt = 0; nt < 4; nt++) {
-#pragma unroll
-          for (int r = 0; r < 4; r++) {
-            const float f = (float)acc[mt][nt][r] * sa[mt][r];
-            const float t = f * sb[nt];
-            cf[mt][nt][r] = cf[mt][nt][r] + t;
-          }
-          acc[mt][nt] = i32x4{0, 0, 0, 0};
-        }
+      for (int j = 0; j < 2 * kWDepth; j++) {
+        stage((j + 1) % kWDepth, t0 + j + 1, (j + 1) & 1);
+        __syncthreads();
+      }
     }
+#pragma unroll
+    for (int j = 0; j < 2 * kWDepth; j++) {
+      if (t0 + j < nsteps) {
+        if (t0 + j + 1 < nsteps) stage((j + 1) % kWDepth, t0 + j + 1, (j + 1) & 1);
+        __syncthreads();
+      }
+    }
+    return;
+  }
+  // -------------------------------------------------------------- consumer
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * 64;
+  const int l32 = lane & 31, lh = lane >> 5;
+  // the tile's row scales go to LDS (read at each chunk fold), the two
+  // column scales of the lane stay in registers
+  float *sa_l = reinterpret_cast<float *>(wlds + 2 * W_STAGE);
+  if (tid < TM) sa_l[tid] = sx[min(m0 + tid, M - 1)];
+  float sb[2];
+#pragma unroll
+  for (int nt = 0; nt < 2; nt++) sb[nt] = ws[min(n0 + wn + nt * 32 + l32, P * 64 - 1)];
+  i32x16 acc[2][2];
+  float cf[2][2][16];
+#pragma unroll
+  for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+    for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        acc[mt][nt][r] = 0;
+        cf[mt][nt][r] = 0.0f;
+      }
+  i32x4 fa[2][2], fb[2][2];
+  auto read = [&](int t) {
+    const int8_t *As = wlds + (t & 1) * W_STAGE, *Bs = As + TM * WLD;
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++) {
+#pragma unroll
+      for (int mt = 0; mt < 2; mt++)
+        fa[kk][mt] = *reinterpret_cast<const i32x4 *>(
+            &As[(wm + mt * 32 + l32) * WLD + kk * 32 + lh * 16]);
+#pragma unroll
+      for (int nt = 0; nt < 2; nt++)
+        fb[kk][nt] = *reinterpret_cast<const i32x4 *>(
+            &Bs[(wn + nt * 32 + l32) * WLD + kk * 32 + lh * 16]);
+    }
+  };
+  auto mma = [&]() {
+#pragma unroll
+    for (int kk = 0; kk < 2; kk++)
+#pragma unroll
+      for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+        for (int nt = 0; nt < 2; nt++)
+          acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[kk][mt], fb[kk][nt],
+                                                              acc[mt][nt], 0, 0, 0);
+  };
+  // end of a KC = 512 chunk (8 steps) or of K: C += (f32(acc)*sa)*sb
+  auto fold = [&]() {
+#pragma unroll
+    for (int mt = 0; mt < 2; mt++)
+#pragma unroll
+      for (int nt = 0; nt < 2; nt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const float f = (float)acc[mt][nt][r] * sa_l[wm + mt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3)];
+          const float t = f * sb[nt];
+          cf[mt][nt][r] = cf[mt][nt][r] + t;
+          acc[mt][nt][r] = 0;
+        }
+  };
+  const bool lag = wave >= NC / 2;
+  __syncthreads();  // step 0 staged
+  if (!lag) {
+    for (int t = 0; t < nsteps; t++) {
+      read(t);
+      mma();
+      if (((t + 1) & 7) == 0 || t + 1 == nsteps) fold();
+      __syncthreads();
+    }
+  } else {
+    read(0);
+    __syncthreads();
+    for (int t = 1; t < nsteps; t++) {
+      mma();
+      if ((t & 7) == 0) fold();  // step t-1 ended a chunk
+      read(t);
+      __syncthreads();
+    }
+    mma();
+    fold();
   }
 #pragma unroll
-  for (int mt = 0; mt < 4; mt++)
+  for (int mt = 0; mt < 2; mt++)
 #pragma unroll
-    for (int nt = 0; nt < 4; nt++) {
-      const int n = n0 + wn + nt * 16 + lr;
+    for (int nt = 0; nt < 2; nt++) {
+      const int n = n0 + wn + nt * 32 + l32;
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int m = m0 + wm + mt * 16 + 4 * lg + r;
+      for (int r = 0; r < 16; r++) {
+        const int m = m0 + wm + mt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
         if (m < M && n < N) y[(size_t)m * ldy + n] = cf[mt][nt][r];
       }
     }
@@ -138,9 +212,19 @@ syn_status_t launch_gemm_w8a8(const int8_t *xq, size_t ldx, const float *sx, siz
     set_error("activation row stride must be a multiple of 16 bytes");
     return SYN_ERR_SHAPE_MISMATCH;
   }
-  dim3 grid((unsigned)cdiv(N, GBN), (unsigned)cdiv(M, GBM));
-  hipLaunchKernelGGL(k_gemm_w8a8, grid, dim3(256), 0, s, xq, (int)ldx, sx, (int)M,
-                     (const i32x4 *)W, ws, (int)N, C, y, (int)ldy);
+  // 256-row tiles, or 128-row tiles when the larger ones cannot fill the GPU
+  // (K is never split: the chunked f32 epilogue must run in chunk order)
+  if (cdiv(M, 256) * cdiv(N, WBN) >= 256) {
+    dim3 grid((unsigned)cdiv(N, WBN), (unsigned)cdiv(M, 256));
+    const size_t shm = 2 * (size_t)w_stage<256>() + 256 * sizeof(float);
+    hipLaunchKernelGGL(k_gemm_w8a8_ws<256>, grid, dim3(768), shm, s, xq, (int)ldx, sx, (int)M,
+                       (const i32x4 *)W, ws, (int)N, C, y, (int)ldy);
+  } else {
+    dim3 grid((unsigned)cdiv(N, WBN), (unsigned)cdiv(M, 128));
+    const size_t shm = 2 * (size_t)w_stage<128>() + 128 * sizeof(float);
+    hipLaunchKernelGGL(k_gemm_w8a8_ws<128>, grid, dim3(512), shm, s, xq, (int)ldx, sx, (int)M,
+                       (const i32x4 *)W, ws, (int)N, C, y, (int)ldy);
+  }
   SYN_LAUNCH_CHECK();
   return SYN_OK;
 }

@@ -164,7 +164,7 @@ def test_device_expf_matches_glibc():
 @pytest.mark.parametrize("m,k,n", [(128, 1024, 3072), (300, 2048, 1000), (17, 4096, 513),
                                    (256, 4096, 1024)])
 def test_int8_gemm_mfma_bit_exact(m, k, n):
-    # M > 16: v_mfma_i32_16x16x64_i8 tiles with the KC=512 chunked epilogue
+    # M > 16: v_mfma_i32_32x32x32_i8 tiles with the KC=512 chunked epilogue
     rng = np.random.default_rng(m + k + n)
     q_nk = rng.integers(-128, 128, (n, k), dtype=np.int8)
     s = rng.uniform(1e-4, 1e-2, n).astype(np.float32)
