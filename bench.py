@@ -108,6 +108,12 @@ def secondary(hip, np):
     from synapse_amd import microbench as mb
     out = {}
     t0 = time.perf_counter()
+    # measured ceilings of this GPU beside the published peaks
+    out["measured_peaks"] = {
+        "hbm_read_gb_s": round(hip.probe_hbm_read(4 << 30), 1),
+        "mfma_f16_32x32x16_tflops": round(hip.probe_mfma(2, 20000), 1),
+        "mfma_i8_32x32x32_tops": round(hip.probe_mfma(3, 20000), 1),
+        "published": {"hbm_gb_s": 8000.0, "f16_tflops": 2500.0, "i8_tops": 5000.0}}
     out["config1_int8_gemv_qwen3"] = {
         "note": "one launch per GEMV (the decode step fuses them), >= 1 GiB rotated",
         "gemvs": mb.int8_suite()}
@@ -132,6 +138,7 @@ def secondary(hip, np):
     out["config4_q8_0_prefill_mistral7b"] = [mb.q8_0_prefill_suite(512),
                                              mb.q8_0_prefill_suite(2048)]
     out["int8_prefill_gemm"] = [mb.int8_prefill_record(128, 1024, 3072),
+                                mb.int8_prefill_record(512, 4096, 4096),
                                 mb.int8_prefill_record(2048, 4096, 4096)]
     mam = {}
     for xdt in (False, True):

@@ -293,7 +293,8 @@ syn_status_t syn_hip_kquant_encode(int fmt, size_t n, size_t k, const float *hos
 syn_status_t syn_hip_eval_expf(const float *d_x, float *d_y, size_t n, void *stream);
 /* Achievable-peak probes: kind 0 = dense v_mfma_f32_16x16x32_f16 loop,
  * 1 = dense v_mfma_i32_16x16x64_i8 loop, 2 = dense v_mfma_f32_32x32x16_f16
- * loop (TFLOP/s or TOP/s, 8 waves per SIMD);
+ * loop, 3 = dense v_mfma_i32_32x32x32_i8 loop (TFLOP/s or TOP/s, 8 waves per
+ * SIMD);
  * HBM streaming read of `bytes` (best of 3 after a warm-up, GB/s). */
 syn_status_t syn_hip_probe_mfma(int kind, size_t iters, double *tflops);
 syn_status_t syn_hip_probe_hbm_read(size_t bytes, double *gb_s);

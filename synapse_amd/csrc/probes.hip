@@ -73,6 +73,26 @@ __global__ void __launch_bounds__(256) k_probe_mfma_i8(int iters, int *__restric
   if (s == 123456789) out[blockIdx.x] = s;
 }
 
+typedef int pi32x16 __attribute__((ext_vector_type(16)));
+
+__global__ void __launch_bounds__(256) k_probe_mfma_i8_32(int iters, int *__restrict__ out) {
+  const i32x4 a = i32x4{(int)threadIdx.x, 3, 5, 7};
+  const i32x4 b = i32x4{11, (int)threadIdx.x, 13, 17};
+  pi32x16 acc[4];
+#pragma unroll
+  for (int c = 0; c < 4; c++)
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[c][r] = 0;
+  for (int it = 0; it < iters; it++) {
+#pragma unroll
+    for (int c = 0; c < 4; c++) acc[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc[c], 0, 0, 0);
+  }
+  int s = 0;
+#pragma unroll
+  for (int c = 0; c < 4; c++) s += acc[c][0] + acc[c][5] + acc[c][10] + acc[c][15];
+  if (s == 123456789) out[blockIdx.x] = s;
+}
+
 // streaming read: each thread sums 16-byte words over a grid-stride loop
 __global__ void __launch_bounds__(256) k_probe_read(const i32x4 *__restrict__ p, size_t n16,
                                                     int *__restrict__ out) {
@@ -95,7 +115,7 @@ using namespace syn;
 
 extern "C" syn_status_t syn_hip_probe_mfma(int kind, size_t iters, double *tflops) {
   if (!tflops) return SYN_ERR_NULL_PTR;
-  if (iters == 0 || iters > (1u << 24) || kind < 0 || kind > 2) return SYN_ERR_INVALID_ARG;
+  if (iters == 0 || iters > (1u << 24) || kind < 0 || kind > 3) return SYN_ERR_INVALID_ARG;
   SYN_TRY(ensure_init());
   int dev = 0, cus = 256;
   SYN_HIP(hipGetDevice(&dev));
@@ -115,9 +135,12 @@ extern "C" syn_status_t syn_hip_probe_mfma(int kind, size_t iters, double *tflop
     else if (kind == 1)
       hipLaunchKernelGGL(k_probe_mfma_i8, dim3(blocks), dim3(256), 0, s, (int)iters,
                          out.as<int>());
-    else
+    else if (kind == 2)
       hipLaunchKernelGGL(k_probe_mfma_f16_32, dim3(blocks), dim3(256), 0, s, (int)iters,
                          out.as<float>());
+    else
+      hipLaunchKernelGGL(k_probe_mfma_i8_32, dim3(blocks), dim3(256), 0, s, (int)iters,
+                         out.as<int>());
     SYN_LAUNCH_CHECK();
     SYN_HIP(hipEventRecord(b, s));
     SYN_HIP(hipEventSynchronize(b));
@@ -127,9 +150,10 @@ extern "C" syn_status_t syn_hip_probe_mfma(int kind, size_t iters, double *tflop
   (void)hipEventDestroy(a);
   (void)hipEventDestroy(b);
   // per MFMA: 16x16x32 f16 = 16384 flops (8 chains); 16x16x64 i8 = 32768
-  // ops (8 chains); 32x32x16 f16 = 32768 flops (4 chains)
-  const double per = kind == 0 ? 16384.0 : 32768.0;
-  const double chains = kind == 2 ? 4.0 : 8.0;
+  // ops (8 chains); 32x32x16 f16 = 32768 flops (4 chains); 32x32x32 i8 =
+  // 65536 ops (4 chains)
+  const double per = kind == 0 ? 16384.0 : kind == 3 ? 65536.0 : 32768.0;
+  const double chains = kind >= 2 ? 4.0 : 8.0;
   const double ops = (double)blocks * 4 /* waves */ * chains * (double)iters * per;
   *tflops = ops / ((double)ms * 1e-3) / 1e12;
   return SYN_OK;

@@ -598,7 +598,8 @@ def fill_normal(n: int, seed: int, std: float = 1.0) -> np.ndarray:
 
 
 def probe_mfma(kind: int, iters: int = 20000) -> float:
-    """Measured dense MFMA rate: kind 0 = f16 (TFLOP/s), 1 = i8 (TOP/s)."""
+    """Measured dense MFMA rate: kind 0 = f16 16x16x32, 2 = f16 32x32x16 (TFLOP/s);
+    1 = i8 16x16x64, 3 = i8 32x32x32 (TOP/s)."""
     v = C.c_double()
     check(lib().syn_hip_probe_mfma(kind, iters, C.byref(v)), "probe_mfma")
     return v.value

@@ -168,7 +168,8 @@ def q8_0_prefill_suite(m: int, rounds: int = 3) -> dict:
                       for r, (_, _, _, cnt) in zip(recs, Q8_0_MISTRAL))
     total_s = sum(r["us"] * 1e-6 * cnt for r, (_, _, _, cnt) in zip(recs, Q8_0_MISTRAL))
     tf = total_flops / total_s / 1e12
-    return {"m": m, "gflop": round(total_flops / 1e9, 2), "ms": round(total_s * 1e3, 3),
+    return {"note": "whole QLinear calls: f32->f16 activation conversion kernel + GEMM kernel",
+            "m": m, "gflop": round(total_flops / 1e9, 2), "ms": round(total_s * 1e3, 3),
             "tflops": round(tf, 1), "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
             "matrices": recs}
 
