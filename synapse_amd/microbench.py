@@ -196,16 +196,51 @@ def copy_calibration(nbytes: int, reps: int = 3) -> float:
     return ms
 
 
+FMT_BY_NAME = {v: k for k, v in NAMES.items()}
+
+
+def _decoder_run(which: str, steps: int, graph: bool):
+    """Prefill + `steps` decode steps of a BASELINE decoder (for profilers:
+    graph=False launches the step's kernels eagerly)."""
+    import bench  # the configs and prompt ids of the benchmark
+    if which == "klm":
+        cfg = dict(bench.LLAMA3B, max_seq=256 + steps + 1)
+        m = hip.KQuantCausalLM(cfg)
+        m.init_synthetic(bench.SEED_BASE, 0.02)
+        m.set_options(graph=graph)
+        ids = np.array(bench._ids(256, cfg["vocab"], bench.PROMPT_SEED), np.uint32)
+        pf, dec = m.time(ids, steps)
+        m.close()
+        return {"decoder": "klm", "prefill_ms": round(pf, 3), "decode_ms_per_token": round(dec / steps, 4)}
+    xdt = which == "mamba-int8"
+    mc = dict(bench.MAMBA370M, max_tokens=64 + steps + 1)
+    mm = hip.QuantizedMamba(mc, int8_xdt=xdt)
+    mm.init_synthetic(bench.SEED_BASE, 0.02)
+    mm.set_options(fused=True, graph=graph)
+    mm.prefill(np.array(bench._ids(64, mc["vocab"], bench.PROMPT_SEED), np.uint32))
+    ms = mm.decode_timed(steps)
+    mm.close()
+    return {"decoder": which, "decode_ms_per_token": round(ms / steps, 4)}
+
+
 if __name__ == "__main__":
     import json
     import sys
 
     hip.init(0)
-    if len(sys.argv) > 2 and sys.argv[1] == "copy":
-        n = int(sys.argv[2])
+    a = sys.argv[1:]
+    if len(a) == 2 and a[0] == "copy":
+        n = int(a[1])
         ms = copy_calibration(n)
         print(json.dumps({"copy_bytes": n, "ms": round(ms, 4),
                           "gb_s_read_plus_write": round(2 * n / (ms * 1e-3) / 1e9, 1)}))
+    elif len(a) == 4 and a[0] == "gemv":  # gemv FMT N K
+        print(json.dumps(gemv_record(FMT_BY_NAME[a[1]], int(a[2]), int(a[3]), "gemv")))
+    elif len(a) == 5 and a[0] == "gemm":  # gemm FMT M N K
+        print(json.dumps(gemm_record(FMT_BY_NAME[a[1]], int(a[2]), int(a[3]), int(a[4]), "gemm")))
+    elif len(a) in (2, 3) and a[0] in ("klm", "mamba-ref", "mamba-int8"):  # DECODER STEPS [eager]
+        print(json.dumps(_decoder_run(a[0], int(a[1]), graph=not (len(a) == 3 and a[2] == "eager"))))
     else:
-        print("usage: python -m synapse_amd.microbench copy NBYTES", file=sys.stderr)
+        print("usage: python -m synapse_amd.microbench copy NBYTES | gemv FMT N K | "
+              "gemm FMT M N K | {klm,mamba-ref,mamba-int8} STEPS [eager]", file=sys.stderr)
         sys.exit(2)
