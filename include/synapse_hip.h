@@ -217,6 +217,49 @@ syn_status_t syn_hip_qlm_time_lm_head_rotating(syn_hip_qlm_t *m, size_t iters, f
 syn_status_t syn_hip_qlm_set_options(syn_hip_qlm_t *m, int fused_decode, int graph_replay);
 syn_status_t syn_hip_qlm_destroy(syn_hip_qlm_t *m);
 
+/* -- GGUF files (weight_loading/gguf.rs:49-151, 551-591): a read-only
+ *    mapping and its tensor table, so block bytes go to the device without
+ *    being dequantized on the host.  Versions 2 and 3; tensor data aligned to
+ *    32 bytes as the reference assumes.  dims[0] is the fastest axis (a
+ *    weight of N rows over K inputs has dims {K, N}).  Pointers returned
+ *    point into the mapping and stay valid until syn_hip_gguf_close. -- */
+#define SYN_HIP_GGML_F32 0
+#define SYN_HIP_GGML_F16 1
+#define SYN_HIP_GGML_Q4_0 2
+#define SYN_HIP_GGML_Q4_1 3
+#define SYN_HIP_GGML_Q8_0 8
+#define SYN_HIP_GGML_Q4_K 12
+#define SYN_HIP_GGML_Q6_K 14
+/* metadata value types */
+#define SYN_HIP_GGUF_UINT8 0
+#define SYN_HIP_GGUF_INT8 1
+#define SYN_HIP_GGUF_UINT16 2
+#define SYN_HIP_GGUF_INT16 3
+#define SYN_HIP_GGUF_UINT32 4
+#define SYN_HIP_GGUF_INT32 5
+#define SYN_HIP_GGUF_FLOAT32 6
+#define SYN_HIP_GGUF_BOOL 7
+#define SYN_HIP_GGUF_STRING 8
+#define SYN_HIP_GGUF_ARRAY 9
+#define SYN_HIP_GGUF_UINT64 10
+#define SYN_HIP_GGUF_INT64 11
+#define SYN_HIP_GGUF_FLOAT64 12
+typedef struct syn_hip_gguf_s syn_hip_gguf_t;
+/* parse_gguf (gguf.rs:75-151): bad magic, version, shapes, unsupported types
+ * or tensors outside the file -> SYN_ERR_INVALID_ARG */
+syn_status_t syn_hip_gguf_open(const char *path, syn_hip_gguf_t **out);
+syn_status_t syn_hip_gguf_tensor_count(const syn_hip_gguf_t *g, size_t *n);
+syn_status_t syn_hip_gguf_find(const syn_hip_gguf_t *g, const char *name, size_t *index);
+/* any output pointer may be NULL; dims4 receives 4 values (unused = 1) */
+syn_status_t syn_hip_gguf_tensor_info(const syn_hip_gguf_t *g, size_t index, const char **name,
+                                      uint32_t *ggml_type, uint32_t *n_dims, uint64_t *dims4,
+                                      uint64_t *nbytes, const void **data);
+/* scalar metadata (integers of any width as u64, floats as double) */
+syn_status_t syn_hip_gguf_meta_u64(const syn_hip_gguf_t *g, const char *key, uint64_t *value);
+syn_status_t syn_hip_gguf_meta_f64(const syn_hip_gguf_t *g, const char *key, double *value);
+syn_status_t syn_hip_gguf_meta_str(const syn_hip_gguf_t *g, const char *key, const char **value);
+syn_status_t syn_hip_gguf_close(syn_hip_gguf_t *g);
+
 /* -- f32 causal LM over GGUF-block weights: CausalLM (models/lm/causal_lm.rs:
  *    195-278, decoder_layer.rs:51-138, 590-730), the reference path for models
  *    whose weights are Q8_0 / Q4_K / Q6_K (dequantized at load there, decoded
@@ -224,7 +267,7 @@ syn_status_t syn_hip_qlm_destroy(syn_hip_qlm_t *m);
 typedef struct {
   syn_hip_lm_config base;
   int32_t fmt_qkv, fmt_o, fmt_gate_up, fmt_down, fmt_lm_head; /* SYN_HIP_FMT_Q* */
-  int32_t qk_norm; /* 1: per-head q/k RMSNorm (gains 1.0), 0: none (LLaMA) */
+  int32_t qk_norm; /* 1: per-head q/k RMSNorm (Qwen3), 0: none (LLaMA) */
 } syn_hip_klm_config;
 
 typedef struct syn_hip_klm_s syn_hip_klm_t;
@@ -233,6 +276,25 @@ syn_status_t syn_hip_klm_set_embed(syn_hip_klm_t *m, const float *embed);
 syn_status_t syn_hip_klm_set_proj(syn_hip_klm_t *m, uint32_t layer, int proj,
                                   const uint8_t *gguf_bytes);
 syn_status_t syn_hip_klm_set_lm_head(syn_hip_klm_t *m, const uint8_t *gguf_bytes);
+/* RMSNorm gains (decoder_layer.rs:590-730, causal_lm.rs:262-270); every gain
+ * is 1.0 until set.  Per layer: attention and FFN norms [hidden], q/k head
+ * norms [head_dim] (used when qk_norm = 1); a NULL pointer leaves that gain
+ * as it is.  The final norm is [hidden]. */
+syn_status_t syn_hip_klm_set_norms(syn_hip_klm_t *m, uint32_t layer, const float *attn_norm,
+                                   const float *ffn_norm, const float *q_norm,
+                                   const float *k_norm);
+syn_status_t syn_hip_klm_set_final_norm(syn_hip_klm_t *m, const float *norm);
+/* Every weight of the model from an open GGUF file (engine/loading.rs:55-80
+ * with load_gguf, gguf.rs:43-151): projections, norms, embedding and lm_head
+ * by llama.cpp names (blk.N.attn_q.weight, token_embd.weight, output.weight,
+ * ...) or the HuggingFace names of the reference's weight map
+ * (model.layers.N.self_attn.q_proj.weight, ...).  Projection and lm_head
+ * tensors must hold the configured block format with dims {K, N}; they are
+ * uploaded as stored.  Norms and the embedding may be F32, F16, Q8_0, Q4_K
+ * or Q6_K (converted to f32 as the reference does).  Missing norms stay 1.0;
+ * a missing lm_head is tied to token_embd (which must then hold the lm_head
+ * format).  Call syn_hip_klm_finalize afterwards. */
+syn_status_t syn_hip_klm_load_gguf(syn_hip_klm_t *m, const syn_hip_gguf_t *g);
 /* Synthetic weights (seed spec as syn_hip_qlm_init_synthetic; untied lm_head
  * is tensor id 1 + 8*n_layers), encoded with the library's block encoder. */
 syn_status_t syn_hip_klm_init_synthetic(syn_hip_klm_t *m, uint64_t seed_base, float stddev);
@@ -288,6 +350,12 @@ syn_status_t syn_hip_mamba_destroy(syn_hip_mamba_t *m);
  * n*(k/256)*144 (Q4_K) or n*(k/256)*210 (Q6_K) bytes. */
 syn_status_t syn_hip_kquant_encode(int fmt, size_t n, size_t k, const float *host_w,
                                    uint8_t *host_out);
+/* Host dequantizer of the same formats, as the reference converts them at
+ * load (gguf.rs:255-288 Q8_0, 375-438 Q4_K, 440-487 Q6_K): nblocks blocks ->
+ * nblocks*32 (Q8_0) or nblocks*256 values.  The K-quant model's GGUF loader
+ * uses it for embeddings stored in a block format. */
+syn_status_t syn_hip_kquant_decode(int fmt, size_t nblocks, const uint8_t *host_blocks,
+                                   float *host_out);
 /* Diagnostic: y[i] = the device expf that SiLU and softmax use (bit-identical
  * to glibc expf, which Rust's f32::exp calls on Linux). */
 syn_status_t syn_hip_eval_expf(const float *d_x, float *d_y, size_t n, void *stream);

@@ -106,6 +106,8 @@ def _declare(L):
         "orc_flm_set_proj": (C.c_int, [P, SZ, C.c_int, C.c_int, P]),
         "orc_flm_set_lm_head": (C.c_int, [P, C.c_int, P]),
         "orc_flm_reset": (None, [P]),
+        "orc_flm_set_norms": (C.c_int, [P, C.c_size_t, P, P, P, P]),
+        "orc_flm_set_final_norm": (C.c_int, [P, P]),
         "orc_flm_prefill": (C.c_int, [P, P, SZ, P]),
         "orc_flm_forward_one": (C.c_int, [P, C.c_uint32, P]),
         "orc_flm_generate": (C.c_int, [P, P, SZ, SZ, P, P]),
@@ -388,6 +390,16 @@ class CausalLM:
     def set_lm_head(self, fmt: str, blocks: np.ndarray):
         self._check(lib().orc_flm_set_lm_head(self.h, FMT_CODES[fmt],
                                               _p(np.ascontiguousarray(blocks, np.uint8))))
+
+    def set_norms(self, layer: int, attn=None, ffn=None, q=None, k=None):
+        arrs = [None if a is None else np.ascontiguousarray(a, np.float32)
+                for a in (attn, ffn, q, k)]
+        self._check(lib().orc_flm_set_norms(self.h, layer,
+                                            *[None if a is None else _p(a) for a in arrs]))
+
+    def set_final_norm(self, gain):
+        self._check(lib().orc_flm_set_final_norm(self.h,
+                                                 _p(np.ascontiguousarray(gain, np.float32))))
 
     def reset(self):
         lib().orc_flm_reset(self.h)

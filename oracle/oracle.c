@@ -1023,7 +1023,9 @@ struct orc_flm {
   float *embed;
   float **w;        /* [L*7] f32 [N,K] */
   float *lm_head;   /* f32 [vocab, h] */
-  float *ones_h, *ones_hd;
+  /* RMSNorm gains, 1.0 until set: attention / FFN [L][h], q / k head norms
+     [L][hd], final [h] (decoder_layer.rs:590-730, causal_lm.rs:267-268) */
+  float *attn_nw, *ffn_nw, *q_nw, *k_nw, *final_nw;
   float *rope_cos, *rope_sin;
   float *kc, *vc;
   size_t cur;
@@ -1043,10 +1045,15 @@ orc_flm *orc_flm_create(const orc_lm_cfg *cfg, int qk_norm) {
   m->qk_norm = qk_norm;
   size_t h = cfg->hidden, hd = cfg->head_dim, kv = cfg->n_kv_heads * hd;
   m->w = (float **)calloc(cfg->n_layers * 7, sizeof(float *));
-  m->ones_h = (float *)malloc(h * 4);
-  m->ones_hd = (float *)malloc(hd * 4);
-  for (size_t i = 0; i < h; i++) m->ones_h[i] = 1.0f;
-  for (size_t i = 0; i < hd; i++) m->ones_hd[i] = 1.0f;
+  size_t L = cfg->n_layers;
+  m->attn_nw = (float *)malloc(L * h * 4);
+  m->ffn_nw = (float *)malloc(L * h * 4);
+  m->q_nw = (float *)malloc(L * hd * 4);
+  m->k_nw = (float *)malloc(L * hd * 4);
+  m->final_nw = (float *)malloc(h * 4);
+  for (size_t i = 0; i < L * h; i++) m->attn_nw[i] = m->ffn_nw[i] = 1.0f;
+  for (size_t i = 0; i < L * hd; i++) m->q_nw[i] = m->k_nw[i] = 1.0f;
+  for (size_t i = 0; i < h; i++) m->final_nw[i] = 1.0f;
   m->rope_cos = (float *)malloc(cfg->max_seq * (hd / 2) * 4);
   m->rope_sin = (float *)malloc(cfg->max_seq * (hd / 2) * 4);
   orc_rope_tables(cfg->max_seq, hd, cfg->rope_theta, m->rope_cos, m->rope_sin);
@@ -1061,8 +1068,11 @@ void orc_flm_destroy(orc_flm *m) {
   free(m->w);
   free(m->embed);
   free(m->lm_head);
-  free(m->ones_h);
-  free(m->ones_hd);
+  free(m->attn_nw);
+  free(m->ffn_nw);
+  free(m->q_nw);
+  free(m->k_nw);
+  free(m->final_nw);
   free(m->rope_cos);
   free(m->rope_sin);
   free(m->kc);
@@ -1107,6 +1117,22 @@ int orc_flm_set_lm_head(orc_flm *m, int fmt, const uint8_t *bytes) {
   return dequant_fmt(fmt, bytes, n, m->lm_head);
 }
 
+int orc_flm_set_norms(orc_flm *m, size_t layer, const float *attn, const float *ffn,
+                      const float *q, const float *k) {
+  size_t h = m->c.hidden, hd = m->c.head_dim;
+  if (layer >= m->c.n_layers) return ORC_ERR_INVALID_ARG;
+  if (attn) memcpy(m->attn_nw + layer * h, attn, h * 4);
+  if (ffn) memcpy(m->ffn_nw + layer * h, ffn, h * 4);
+  if (q) memcpy(m->q_nw + layer * hd, q, hd * 4);
+  if (k) memcpy(m->k_nw + layer * hd, k, hd * 4);
+  return ORC_OK;
+}
+
+int orc_flm_set_final_norm(orc_flm *m, const float *w) {
+  memcpy(m->final_nw, w, m->c.hidden * 4);
+  return ORC_OK;
+}
+
 void orc_flm_reset(orc_flm *m) { m->cur = 0; }
 
 static void flm_matmul_t(const float *x, const float *w, size_t m, size_t k, size_t n, float *y) {
@@ -1127,13 +1153,13 @@ static void flm_layer(orc_flm *m, size_t l, float *x, size_t t, int prefill) {
   float *hb = (float *)malloc(t * inter * 4);
   float *kcl = m->kc + l * c->max_seq * kvd, *vcl = m->vc + l * c->max_seq * kvd;
 
-  orc_rmsnorm(x, m->ones_h, c->eps, t, h, normed);
+  orc_rmsnorm(x, m->attn_nw + l * h, c->eps, t, h, normed);
   flm_matmul_t(normed, W[0], t, h, qd, q);
   flm_matmul_t(normed, W[1], t, h, kvd, k);
   flm_matmul_t(normed, W[2], t, h, kvd, v);
   if (m->qk_norm) {
-    orc_rmsnorm(q, m->ones_hd, c->eps, t * nh, hd, q);
-    orc_rmsnorm(k, m->ones_hd, c->eps, t * nkv, hd, k);
+    orc_rmsnorm(q, m->q_nw + l * hd, c->eps, t * nh, hd, q);
+    orc_rmsnorm(k, m->k_nw + l * hd, c->eps, t * nkv, hd, k);
   }
   size_t pos0 = prefill ? 0 : m->cur;
   orc_rope_apply(q, m->rope_cos, m->rope_sin, t, nh, hd, pos0);
@@ -1160,7 +1186,7 @@ static void flm_layer(orc_flm *m, size_t l, float *x, size_t t, int prefill) {
   }
   flm_matmul_t(attn, W[3], t, qd, h, o);
   for (size_t i = 0; i < t * h; i++) x[i] = x[i] + o[i];
-  orc_rmsnorm(x, m->ones_h, c->eps, t, h, normed);
+  orc_rmsnorm(x, m->ffn_nw + l * h, c->eps, t, h, normed);
   flm_matmul_t(normed, W[4], t, h, inter, g);
   flm_matmul_t(normed, W[5], t, h, inter, u);
   orc_swiglu_fused(hb, g, u, t * inter);
@@ -1172,7 +1198,7 @@ static void flm_layer(orc_flm *m, size_t l, float *x, size_t t, int prefill) {
 static void flm_head(orc_flm *m, const float *xlast, float *logits) {
   size_t h = m->c.hidden;
   float *normed = (float *)malloc(h * 4);
-  orc_rmsnorm(xlast, m->ones_h, m->c.eps, 1, h, normed);
+  orc_rmsnorm(xlast, m->final_nw, m->c.eps, 1, h, normed);
   flm_matmul_t(normed, m->lm_head, 1, h, m->c.vocab, logits);
   free(normed);
 }

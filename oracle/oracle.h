@@ -126,6 +126,10 @@ int orc_flm_set_embed(orc_flm *m, const float *embed);
 /* one projection of one layer from GGUF bytes: proj 0..6 = q,k,v,o,gate,up,down */
 int orc_flm_set_proj(orc_flm *m, size_t layer, int proj, int fmt, const uint8_t *bytes);
 int orc_flm_set_lm_head(orc_flm *m, int fmt, const uint8_t *bytes);
+/* RMSNorm gains (all 1.0 until set); NULL leaves one as it is */
+int orc_flm_set_norms(orc_flm *m, size_t layer, const float *attn, const float *ffn,
+                      const float *q, const float *k);
+int orc_flm_set_final_norm(orc_flm *m, const float *w);
 void orc_flm_reset(orc_flm *m);
 int orc_flm_prefill(orc_flm *m, const uint32_t *ids, size_t n, float *logits);
 int orc_flm_forward_one(orc_flm *m, uint32_t token, float *logits);

@@ -857,8 +857,13 @@ __global__ void __launch_bounds__(512)
   const int n8 = n32 + ((len - n32) / 8) * 8;
   float mx = -__builtin_inff();
   if (qk_wave) {
-    const float4 *q4 = reinterpret_cast<const float4 *>(qv);
     const float4 *k4 = reinterpret_cast<const float4 *>(kv);
+    // q in two VGPRs (lane d holds q[d] and q[64+d]); the chains take q[d]
+    // through v_readlane as a scalar operand, so no LDS read sits on them
+    const float qa = qv[min(lane, hd - 1)], qb = qv[min(64 + lane, hd - 1)];
+    auto qd = [&](int d) -> float {
+      return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(d < 64 ? qa : qb), d & 63));
+    };
     for (int p0 = 0; p0 < len; p0 += kAttnPass) {
       if (p0 > 0) load_k((p0 >> 6) + wave);
       const int p = p0 + wave * 64 + lane;
@@ -873,23 +878,21 @@ __global__ void __launch_bounds__(512)
 #pragma unroll
           for (int c = 0; c < 32; c++) {
             if (c < hd4) {
-              const float4 qq = q4[c];
-              acc = __builtin_fmaf(qq.x, pre[c].x, acc);
-              acc = __builtin_fmaf(qq.y, pre[c].y, acc);
-              acc = __builtin_fmaf(qq.z, pre[c].z, acc);
-              acc = __builtin_fmaf(qq.w, pre[c].w, acc);
+              acc = __builtin_fmaf(qd(4 * c), pre[c].x, acc);
+              acc = __builtin_fmaf(qd(4 * c + 1), pre[c].y, acc);
+              acc = __builtin_fmaf(qd(4 * c + 2), pre[c].z, acc);
+              acc = __builtin_fmaf(qd(4 * c + 3), pre[c].w, acc);
             }
           }
         } else {
 #pragma unroll
           for (int c = 0; c < 32; c++) {
             if (c < hd4) {
-              const float4 qq = q4[c];
               float t;
-              t = qq.x * pre[c].x; acc = acc + t;
-              t = qq.y * pre[c].y; acc = acc + t;
-              t = qq.z * pre[c].z; acc = acc + t;
-              t = qq.w * pre[c].w; acc = acc + t;
+              t = qd(4 * c) * pre[c].x; acc = acc + t;
+              t = qd(4 * c + 1) * pre[c].y; acc = acc + t;
+              t = qd(4 * c + 2) * pre[c].z; acc = acc + t;
+              t = qd(4 * c + 3) * pre[c].w; acc = acc + t;
             }
           }
         }

@@ -6,6 +6,8 @@
 // driver; activations stay f32 between layers (no activation quantization
 // on this path, as in the reference).
 #include <algorithm>
+#include <cstring>
+#include <string>
 #include <thread>
 #include <vector>
 
@@ -26,7 +28,10 @@ struct syn_hip_klm_s {
   std::vector<Layer> layers;
   QLinearKQ lm_head;
   bool have_lm = false, have_embed = false;
-  DevBuf embed, ones_h, ones_hd, rope_cos, rope_sin, kc, vc;
+  DevBuf embed, rope_cos, rope_sin, kc, vc;
+  // RMSNorm gains: attention and FFN norms [L][h], q/k head norms [L][hd],
+  // final norm [h] (1.0 until set)
+  DevBuf attn_nw, ffn_nw, q_nw, k_nw, final_nw;
   DevBuf x, normed, qkv, qrot, attn, o, gu, hbuf, down, logits, scores;
   DevBuf pv, pi, pv2, state, history, mhist, ids;
   hipStream_t stream = nullptr;
@@ -65,8 +70,6 @@ struct syn_hip_klm_s {
 
   syn_status_t alloc_all() {
     const size_t T = S;
-    SYN_TRY(ones_h.alloc(h * 4));
-    SYN_TRY(ones_hd.alloc(hd * 4));
     SYN_TRY(rope_cos.alloc(S * (hd / 2) * 4));
     SYN_TRY(rope_sin.alloc(S * (hd / 2) * 4));
     SYN_TRY(kc.alloc(L * k_elems() * 4));
@@ -90,8 +93,18 @@ struct syn_hip_klm_s {
     SYN_TRY(mhist.alloc((S + 1) * 4));
     SYN_TRY(ids.alloc(S * 4));
     std::vector<float> one(std::max(h, hd), 1.0f);
-    SYN_HIP(hipMemcpy(ones_h.p, one.data(), h * 4, hipMemcpyHostToDevice));
-    SYN_HIP(hipMemcpy(ones_hd.p, one.data(), hd * 4, hipMemcpyHostToDevice));
+    SYN_TRY(attn_nw.alloc(L * h * 4));
+    SYN_TRY(ffn_nw.alloc(L * h * 4));
+    SYN_TRY(q_nw.alloc(L * hd * 4));
+    SYN_TRY(k_nw.alloc(L * hd * 4));
+    SYN_TRY(final_nw.alloc(h * 4));
+    for (size_t l = 0; l < L; l++) {
+      SYN_HIP(hipMemcpy(attn_nw.as<float>() + l * h, one.data(), h * 4, hipMemcpyHostToDevice));
+      SYN_HIP(hipMemcpy(ffn_nw.as<float>() + l * h, one.data(), h * 4, hipMemcpyHostToDevice));
+      SYN_HIP(hipMemcpy(q_nw.as<float>() + l * hd, one.data(), hd * 4, hipMemcpyHostToDevice));
+      SYN_HIP(hipMemcpy(k_nw.as<float>() + l * hd, one.data(), hd * 4, hipMemcpyHostToDevice));
+    }
+    SYN_HIP(hipMemcpy(final_nw.p, one.data(), h * 4, hipMemcpyHostToDevice));
     SYN_HIP(hipMemset(kc.p, 0, kc.bytes));
     SYN_HIP(hipMemset(vc.p, 0, vc.bytes));
     return SYN_OK;
@@ -128,20 +141,21 @@ struct syn_hip_klm_s {
     Layer &Ly = layers[l];
     const float eps = c.base.eps;
     const int nh = (int)c.base.n_heads, nkv = (int)c.base.n_kv_heads;
-    const float *qn = c.qk_norm ? ones_hd.as<float>() : nullptr;
+    const float *qn = c.qk_norm ? q_nw.as<float>() + l * hd : nullptr;
+    const float *kn = c.qk_norm ? k_nw.as<float>() + l * hd : nullptr;
     SYN_TRY(launch_rmsnorm_quant(x.as<float>(), l == 0 ? nullptr : down.as<float>(),
-                                 ones_h.as<float>(), eps, rows, (int)h, nullptr, 0, nullptr,
-                                 normed.as<float>(), s));
+                                 attn_nw.as<float>() + l * h, eps, rows, (int)h, nullptr, 0,
+                                 nullptr, normed.as<float>(), s));
     SYN_TRY(Ly.qkv.gemv(rows, normed.as<float>(), h, qkv.as<float>(), n_qkv, s));
     if (!prefill && fused_attention_fits((int)hd, (int)S)) {
       // one kernel per query head: head norms, RoPE, KV append and attention
       RowSrc src;
       src.f = qkv.as<float>();
-      SYN_TRY(launch_fused_attention(src, nh, nkv, (int)hd, qn, qn, eps, rope_cos.as<float>(),
+      SYN_TRY(launch_fused_attention(src, nh, nkv, (int)hd, qn, kn, eps, rope_cos.as<float>(),
                                      rope_sin.as<float>(), st(), kc_l(l), vc_l(l), (int)S,
                                      attn.as<float>(), s));
     } else {
-      SYN_TRY(launch_qk_norm_rope_kv(qkv.as<float>(), (int)n_qkv, rows, nh, nkv, (int)hd, qn, qn,
+      SYN_TRY(launch_qk_norm_rope_kv(qkv.as<float>(), (int)n_qkv, rows, nh, nkv, (int)hd, qn, kn,
                                      eps, rope_cos.as<float>(), rope_sin.as<float>(),
                                      prefill ? nullptr : &st()->pos, 0, qrot.as<float>(),
                                      kc_l(l), vc_l(l), (int)S, s));
@@ -154,8 +168,8 @@ struct syn_hip_klm_s {
                                         s));
     }
     SYN_TRY(Ly.o.gemv(rows, attn.as<float>(), qd, o.as<float>(), h, s));
-    SYN_TRY(launch_rmsnorm_quant(x.as<float>(), o.as<float>(), ones_h.as<float>(), eps, rows,
-                                 (int)h, nullptr, 0, nullptr, normed.as<float>(), s));
+    SYN_TRY(launch_rmsnorm_quant(x.as<float>(), o.as<float>(), ffn_nw.as<float>() + l * h, eps,
+                                 rows, (int)h, nullptr, 0, nullptr, normed.as<float>(), s));
     SYN_TRY(Ly.gu.gemv(rows, normed.as<float>(), h, gu.as<float>(), 2 * inter, s));
     SYN_TRY(launch_swiglu_f32(gu.as<float>(), (int)(2 * inter), rows, (int)inter,
                               hbuf.as<float>(), (int)inter, s));
@@ -166,7 +180,7 @@ struct syn_hip_klm_s {
   syn_status_t head(int row, int add_pos, hipStream_t s) {
     float *xr = x.as<float>() + (size_t)row * h;
     const float *dr = down.as<float>() + (size_t)row * h;
-    SYN_TRY(launch_rmsnorm_quant(xr, dr, ones_h.as<float>(), c.base.eps, 1, (int)h, nullptr, 0,
+    SYN_TRY(launch_rmsnorm_quant(xr, dr, final_nw.as<float>(), c.base.eps, 1, (int)h, nullptr, 0,
                                  nullptr, normed.as<float>(), s));
     SYN_TRY(lm_head.gemv(1, normed.as<float>(), h, logits.as<float>(), vocab, s));
     SYN_TRY(launch_argmax(logits.as<float>(), (int)vocab, pv.as<float>(), pi.as<int>(),
@@ -479,6 +493,175 @@ syn_status_t syn_hip_klm_time(syn_hip_klm_t *m, const uint32_t *prompt, size_t n
   (void)hipEventDestroy(b);
   (void)hipEventDestroy(c);
   return SYN_OK;
+}
+
+syn_status_t syn_hip_klm_set_norms(syn_hip_klm_t *m, uint32_t layer, const float *attn_norm,
+                                   const float *ffn_norm, const float *q_norm,
+                                   const float *k_norm) {
+  if (!m) return SYN_ERR_NULL_PTR;
+  if (layer >= m->L) return SYN_ERR_INVALID_ARG;
+  const size_t h = m->h, hd = m->hd;
+  if (attn_norm)
+    SYN_HIP(hipMemcpy(m->attn_nw.as<float>() + layer * h, attn_norm, h * 4, hipMemcpyHostToDevice));
+  if (ffn_norm)
+    SYN_HIP(hipMemcpy(m->ffn_nw.as<float>() + layer * h, ffn_norm, h * 4, hipMemcpyHostToDevice));
+  if (q_norm)
+    SYN_HIP(hipMemcpy(m->q_nw.as<float>() + layer * hd, q_norm, hd * 4, hipMemcpyHostToDevice));
+  if (k_norm)
+    SYN_HIP(hipMemcpy(m->k_nw.as<float>() + layer * hd, k_norm, hd * 4, hipMemcpyHostToDevice));
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_klm_set_final_norm(syn_hip_klm_t *m, const float *norm) {
+  if (!m || !norm) return SYN_ERR_NULL_PTR;
+  SYN_HIP(hipMemcpy(m->final_nw.p, norm, m->h * 4, hipMemcpyHostToDevice));
+  return SYN_OK;
+}
+
+// ------------------------------------------------------------------ GGUF
+// Tensor names: llama.cpp's (blk.N.*) or the HuggingFace names the
+// reference's weight map uses (weight_map.rs: model.layers.N.*).
+namespace {
+
+int ggml_of_fmt(int fmt) {
+  return fmt == SYN_HIP_FMT_Q8_0 ? SYN_HIP_GGML_Q8_0
+       : fmt == SYN_HIP_FMT_Q4_K ? SYN_HIP_GGML_Q4_K : SYN_HIP_GGML_Q6_K;
+}
+
+struct GgufTensor {
+  uint32_t type = 0, n_dims = 0;
+  uint64_t dims[4] = {1, 1, 1, 1};
+  uint64_t nbytes = 0;
+  const uint8_t *data = nullptr;
+};
+
+// first of `names` present in the file
+bool gguf_get(const syn_hip_gguf_t *g, std::initializer_list<std::string> names, GgufTensor *t,
+              std::string *found) {
+  for (const std::string &n : names) {
+    size_t idx = 0;
+    if (syn_hip_gguf_find(g, n.c_str(), &idx) != SYN_OK) continue;
+    const void *d = nullptr;
+    syn_hip_gguf_tensor_info(g, idx, nullptr, &t->type, &t->n_dims, t->dims, &t->nbytes, &d);
+    t->data = static_cast<const uint8_t *>(d);
+    *found = n;
+    return true;
+  }
+  return false;
+}
+
+// f32 values of an F32 / F16 / Q8_0 / Q4_K / Q6_K tensor (gguf.rs:115-139)
+syn_status_t gguf_to_f32(const GgufTensor &t, size_t numel, const std::string &name,
+                         std::vector<float> &out) {
+  out.resize(numel);
+  if (t.type == SYN_HIP_GGML_F32) {
+    std::memcpy(out.data(), t.data, numel * 4);
+  } else if (t.type == SYN_HIP_GGML_F16) {
+    for (size_t i = 0; i < numel; i++) {
+      uint16_t h;
+      std::memcpy(&h, t.data + 2 * i, 2);
+      out[i] = f16_to_f32_reference(h);
+    }
+  } else if (t.type == SYN_HIP_GGML_Q8_0 || t.type == SYN_HIP_GGML_Q4_K ||
+             t.type == SYN_HIP_GGML_Q6_K) {
+    const int fmt = t.type == SYN_HIP_GGML_Q8_0 ? SYN_HIP_FMT_Q8_0
+                  : t.type == SYN_HIP_GGML_Q4_K ? SYN_HIP_FMT_Q4_K : SYN_HIP_FMT_Q6_K;
+    kq_dequant(fmt, t.data, numel / kq_block_elems(fmt), out.data());
+  } else {
+    set_error("GGUF: tensor " + name + " has a type the loader cannot read as f32");
+    return SYN_ERR_INVALID_ARG;
+  }
+  return SYN_OK;
+}
+
+}  // namespace
+
+syn_status_t syn_hip_klm_load_gguf(syn_hip_klm_t *m, const syn_hip_gguf_t *g) {
+  if (!m || !g) return SYN_ERR_NULL_PTR;
+  const size_t h = m->h, hd = m->hd, L = m->L;
+  GgufTensor t;
+  std::string nm;
+  auto expect = [&](size_t n, size_t k, int fmt) -> syn_status_t {
+    const bool dims_ok = t.n_dims == 2 && t.dims[0] == k && t.dims[1] == n;
+    if (!dims_ok || (int)t.type != ggml_of_fmt(fmt)) {
+      set_error("GGUF: tensor " + nm + " has type " + std::to_string(t.type) + " and dims " +
+                std::to_string(t.dims[0]) + "x" + std::to_string(t.dims[1]) + "; the model expects " +
+                std::to_string(k) + "x" + std::to_string(n) + " of GGML type " +
+                std::to_string(ggml_of_fmt(fmt)));
+      return SYN_ERR_SHAPE_MISMATCH;
+    }
+    return SYN_OK;
+  };
+  auto missing = [&](const std::string &what) -> syn_status_t {
+    set_error("GGUF: no tensor for " + what);
+    return SYN_ERR_INVALID_ARG;
+  };
+  static const char *kLlama[7] = {"attn_q", "attn_k", "attn_v", "attn_output",
+                                  "ffn_gate", "ffn_up", "ffn_down"};
+  static const char *kHf[7] = {"self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj",
+                               "self_attn.o_proj", "mlp.gate_proj", "mlp.up_proj",
+                               "mlp.down_proj"};
+  for (size_t l = 0; l < L; l++) {
+    const std::string b = "blk." + std::to_string(l) + ".";
+    const std::string hf = "model.layers." + std::to_string(l) + ".";
+    for (int p = 0; p < 7; p++) {
+      if (!gguf_get(g, {b + kLlama[p] + ".weight", hf + kHf[p] + ".weight"}, &t, &nm))
+        return missing(b + kLlama[p]);
+      size_t n, k;
+      m->proj_shape(p, &n, &k);
+      SYN_TRY(expect(n, k, m->fmt_of(p)));
+      SYN_TRY(m->set_proj(l, p, t.data));
+    }
+    std::vector<float> an, fn, qn, kn;
+    if (gguf_get(g, {b + "attn_norm.weight", hf + "input_layernorm.weight"}, &t, &nm)) {
+      if (t.dims[0] != h) return missing(nm + " of the hidden size");
+      SYN_TRY(gguf_to_f32(t, h, nm, an));
+    }
+    if (gguf_get(g, {b + "ffn_norm.weight", hf + "post_attention_layernorm.weight"}, &t, &nm)) {
+      if (t.dims[0] != h) return missing(nm + " of the hidden size");
+      SYN_TRY(gguf_to_f32(t, h, nm, fn));
+    }
+    if (m->c.qk_norm) {
+      if (gguf_get(g, {b + "attn_q_norm.weight", hf + "self_attn.q_norm.weight"}, &t, &nm)) {
+        if (t.dims[0] != hd) return missing(nm + " of the head size");
+        SYN_TRY(gguf_to_f32(t, hd, nm, qn));
+      }
+      if (gguf_get(g, {b + "attn_k_norm.weight", hf + "self_attn.k_norm.weight"}, &t, &nm)) {
+        if (t.dims[0] != hd) return missing(nm + " of the head size");
+        SYN_TRY(gguf_to_f32(t, hd, nm, kn));
+      }
+    }
+    SYN_TRY(syn_hip_klm_set_norms(m, (uint32_t)l, an.empty() ? nullptr : an.data(),
+                                  fn.empty() ? nullptr : fn.data(),
+                                  qn.empty() ? nullptr : qn.data(),
+                                  kn.empty() ? nullptr : kn.data()));
+  }
+  GgufTensor emb;
+  std::string emb_name;
+  if (!gguf_get(g, {"token_embd.weight", "model.embed_tokens.weight"}, &emb, &emb_name))
+    return missing("token_embd");
+  if (emb.n_dims != 2 || emb.dims[0] != h || emb.dims[1] != m->vocab) {
+    set_error("GGUF: " + emb_name + " is not [vocab, hidden]");
+    return SYN_ERR_SHAPE_MISMATCH;
+  }
+  {
+    std::vector<float> e;
+    SYN_TRY(gguf_to_f32(emb, m->vocab * h, emb_name, e));
+    SYN_TRY(syn_hip_klm_set_embed(m, e.data()));
+  }
+  if (gguf_get(g, {"output_norm.weight", "model.norm.weight"}, &t, &nm)) {
+    if (t.dims[0] != h) return missing(nm + " of the hidden size");
+    std::vector<float> fnw;
+    SYN_TRY(gguf_to_f32(t, h, nm, fnw));
+    SYN_TRY(syn_hip_klm_set_final_norm(m, fnw.data()));
+  }
+  // lm_head: its own tensor, or tied to the embedding when the file has none
+  if (!gguf_get(g, {"output.weight", "lm_head.weight"}, &t, &nm)) {
+    t = emb;
+    nm = emb_name + " (tied lm_head)";
+  }
+  SYN_TRY(expect(m->vocab, h, m->c.fmt_lm_head));
+  return syn_hip_klm_set_lm_head(m, t.data);
 }
 
 syn_status_t syn_hip_klm_set_options(syn_hip_klm_t *m, int graph) {

@@ -78,6 +78,51 @@ static uint16_t enc_scale(float v, float *decoded) {
   return h;
 }
 
+float f16_to_f32_reference(uint16_t h) { return h2f_rs(h); }
+
+// gguf.rs:255-288 (Q8_0), 375-431 (Q4_K), 440-487 (Q6_K), in their order
+void kq_dequant(int fmt, const uint8_t *b, size_t nblocks, float *out) {
+  for (size_t blk = 0; blk < nblocks; blk++) {
+    if (fmt == SYN_HIP_FMT_Q8_0) {
+      const uint8_t *p = b + blk * 34;
+      const float d = h2f_rs((uint16_t)(p[0] | (p[1] << 8)));
+      for (int i = 0; i < 32; i++) out[blk * 32 + i] = d * (float)(int8_t)p[2 + i];
+    } else if (fmt == SYN_HIP_FMT_Q4_K) {
+      const uint8_t *p = b + blk * 144;
+      const float d = h2f_rs((uint16_t)(p[0] | (p[1] << 8)));
+      const float dmin = h2f_rs((uint16_t)(p[2] | (p[3] << 8)));
+      const uint8_t *sc = p + 4, *qs = p + 16;
+      uint8_t scales[8], mins[8];
+      for (int i = 0; i < 4; i++) {
+        scales[i] = sc[i] & 63;
+        scales[i + 4] = (uint8_t)((sc[i + 4] & 15) | ((sc[i] >> 6) << 4));
+        mins[i] = (uint8_t)((sc[i + 4] >> 4) | ((sc[i + 8] & 15) << 4));
+        mins[i + 4] = (uint8_t)((sc[i + 8] >> 4) | (((sc[i] >> 4) & 12) << 4));
+      }
+      for (int s = 0; s < 8; s++) {
+        const float scf = d * (float)scales[s], mf = dmin * (float)mins[s];
+        for (int i = 0; i < 16; i++) {
+          const uint8_t byte = qs[16 * s + i];
+          out[blk * 256 + 32 * s + 2 * i] = (float)(byte & 15) * scf - mf;
+          out[blk * 256 + 32 * s + 2 * i + 1] = (float)(byte >> 4) * scf - mf;
+        }
+      }
+    } else {
+      const uint8_t *p = b + blk * 210;
+      const uint8_t *ql = p, *qh = p + 128;
+      const int8_t *sc = reinterpret_cast<const int8_t *>(p + 192);
+      const float d = h2f_rs((uint16_t)(p[208] | (p[209] << 8)));
+      for (int idx = 0; idx < 256; idx++) {
+        const uint8_t qlb = ql[idx / 2];
+        const uint32_t lo = (idx % 2) ? (qlb >> 4) : (qlb & 15u);
+        const uint32_t hi = (qh[idx / 4] >> (2 * (idx % 4))) & 3u;
+        const float q = (float)((int)(lo | (hi << 4)) - 32);
+        out[blk * 256 + idx] = q * ((float)sc[idx / 16] * d);
+      }
+    }
+  }
+}
+
 size_t kq_block_bytes(int fmt) {
   return fmt == SYN_HIP_FMT_Q8_0 ? 34 : fmt == SYN_HIP_FMT_Q4_K ? 144 : 210;
 }
@@ -728,5 +773,15 @@ extern "C" syn_status_t syn_hip_kquant_encode(int fmt, size_t n, size_t k, const
   if (n == 0 || k == 0) return SYN_ERR_INVALID_ARG;
   if (k % kq_block_elems(fmt)) return SYN_ERR_SHAPE_MISMATCH;
   kq_encode(fmt, host_w, n, k, host_out);
+  return SYN_OK;
+}
+
+extern "C" syn_status_t syn_hip_kquant_decode(int fmt, size_t nblocks, const uint8_t *host_blocks,
+                                              float *host_out) {
+  using namespace syn;
+  if (!host_blocks || !host_out) return SYN_ERR_NULL_PTR;
+  if (fmt != SYN_HIP_FMT_Q8_0 && fmt != SYN_HIP_FMT_Q4_K && fmt != SYN_HIP_FMT_Q6_K)
+    return SYN_ERR_INVALID_ARG;
+  kq_dequant(fmt, host_blocks, nblocks, host_out);
   return SYN_OK;
 }

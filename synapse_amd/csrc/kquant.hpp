@@ -9,6 +9,11 @@ size_t kq_block_bytes(int fmt);
 size_t kq_block_elems(int fmt);
 // encode f32 [n,k] rows into the reference's block byte format
 void kq_encode(int fmt, const float *w, size_t n, size_t k, uint8_t *out);
+// host dequantizers of the reference (gguf.rs:255-288, 375-487): `nblocks`
+// blocks of `fmt` bytes -> f32 values
+void kq_dequant(int fmt, const uint8_t *bytes, size_t nblocks, float *out);
+// the reference's f16 -> f32 converter (converter.rs:12-40, subnormals halve)
+float f16_to_f32_reference(uint16_t h);
 
 struct QLinearKQ {
   int fmt = 0;

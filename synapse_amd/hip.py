@@ -105,6 +105,19 @@ SIGNATURES = {
     "syn_hip_klm_generate": (ST, [P, P, SZ, SZ, P, P]),
     "syn_hip_klm_time": (ST, [P, P, SZ, SZ, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
     "syn_hip_klm_set_options": (ST, [P, C.c_int]),
+    "syn_hip_klm_set_norms": (ST, [P, C.c_uint32, P, P, P, P]),
+    "syn_hip_klm_set_final_norm": (ST, [P, P]),
+    "syn_hip_klm_load_gguf": (ST, [P, P]),
+    "syn_hip_gguf_open": (ST, [C.c_char_p, C.POINTER(P)]),
+    "syn_hip_gguf_tensor_count": (ST, [P, C.POINTER(SZ)]),
+    "syn_hip_gguf_find": (ST, [P, C.c_char_p, C.POINTER(SZ)]),
+    "syn_hip_gguf_tensor_info": (ST, [P, SZ, C.POINTER(C.c_char_p), C.POINTER(C.c_uint32),
+                                      C.POINTER(C.c_uint32), C.POINTER(C.c_uint64),
+                                      C.POINTER(C.c_uint64), C.POINTER(P)]),
+    "syn_hip_gguf_meta_u64": (ST, [P, C.c_char_p, C.POINTER(C.c_uint64)]),
+    "syn_hip_gguf_meta_f64": (ST, [P, C.c_char_p, C.POINTER(C.c_double)]),
+    "syn_hip_gguf_meta_str": (ST, [P, C.c_char_p, C.POINTER(C.c_char_p)]),
+    "syn_hip_gguf_close": (ST, [P]),
     "syn_hip_klm_destroy": (ST, [P]),
     "syn_hip_mamba_create": (ST, [C.POINTER(MambaConfig), C.POINTER(P)]),
     "syn_hip_mamba_init_synthetic": (ST, [P, C.c_uint64, C.c_float]),
@@ -119,6 +132,7 @@ SIGNATURES = {
     "syn_hip_probe_hbm_read": (ST, [SZ, C.POINTER(C.c_double)]),
     "syn_hip_eval_expf": (ST, [P, P, SZ, P]),
     "syn_hip_kquant_encode": (ST, [C.c_int, SZ, SZ, P, P]),
+    "syn_hip_kquant_decode": (ST, [C.c_int, SZ, P, P]),
 }
 
 _lib = None
@@ -513,10 +527,103 @@ class KQuantCausalLM:
         """HIP graph replay of the decode step, or eager launches (same results)."""
         check(lib().syn_hip_klm_set_options(self.h, int(graph)), "set_options")
 
+    def set_norms(self, layer: int, attn=None, ffn=None, q=None, k=None):
+        """RMSNorm gains of one layer (None leaves a gain as it is; all start at 1.0)."""
+        arrs = [None if a is None else np.ascontiguousarray(a, np.float32)
+                for a in (attn, ffn, q, k)]
+        check(lib().syn_hip_klm_set_norms(self.h, layer,
+                                          *[None if a is None else ptr(a) for a in arrs]),
+              "set_norms")
+
+    def set_final_norm(self, gain):
+        check(lib().syn_hip_klm_set_final_norm(self.h,
+                                               ptr(np.ascontiguousarray(gain, np.float32))),
+              "set_final_norm")
+
+    def load_gguf(self, gguf: "Gguf"):
+        """Every weight from a GGUF file (llama.cpp or HuggingFace tensor names), then finalize."""
+        check(lib().syn_hip_klm_load_gguf(self.h, gguf.h), "klm_load_gguf")
+        check(lib().syn_hip_klm_finalize(self.h), "klm_finalize")
+
     def close(self):
         if self.h:
             lib().syn_hip_klm_destroy(self.h)
             self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class GgufTensorInfo:
+    __slots__ = ("name", "ggml_type", "dims", "nbytes", "data")
+
+    def __init__(self, name, ggml_type, dims, nbytes, data):
+        self.name, self.ggml_type, self.dims, self.nbytes, self.data = (
+            name, ggml_type, dims, nbytes, data)
+
+    def bytes(self) -> np.ndarray:
+        """A copy of the tensor's stored bytes."""
+        return np.ctypeslib.as_array((C.c_uint8 * self.nbytes).from_address(self.data)).copy()
+
+
+class Gguf:
+    """Read-only mapping of a GGUF v2/v3 file (host code only, no device use)."""
+
+    def __init__(self, path):
+        h = C.c_void_p()
+        check(lib().syn_hip_gguf_open(str(path).encode(), C.byref(h)), "gguf_open")
+        self.h = h.value
+
+    def __len__(self):
+        n = SZ()
+        check(lib().syn_hip_gguf_tensor_count(self.h, C.byref(n)), "gguf_tensor_count")
+        return n.value
+
+    def index(self, name: str):
+        i = SZ()
+        rc = lib().syn_hip_gguf_find(self.h, name.encode(), C.byref(i))
+        return i.value if rc == 0 else None
+
+    def info(self, index: int) -> GgufTensorInfo:
+        name, t, nd = C.c_char_p(), C.c_uint32(), C.c_uint32()
+        dims, nb, data = (C.c_uint64 * 4)(), C.c_uint64(), C.c_void_p()
+        check(lib().syn_hip_gguf_tensor_info(self.h, index, C.byref(name), C.byref(t),
+                                             C.byref(nd), dims, C.byref(nb), C.byref(data)),
+              "gguf_tensor_info")
+        return GgufTensorInfo(name.value.decode(), t.value, tuple(dims[:nd.value]), nb.value,
+                              data.value)
+
+    def tensors(self):
+        return [self.info(i) for i in range(len(self))]
+
+    def meta_u64(self, key: str):
+        v = C.c_uint64()
+        return v.value if lib().syn_hip_gguf_meta_u64(self.h, key.encode(), C.byref(v)) == 0 \
+            else None
+
+    def meta_f64(self, key: str):
+        v = C.c_double()
+        return v.value if lib().syn_hip_gguf_meta_f64(self.h, key.encode(), C.byref(v)) == 0 \
+            else None
+
+    def meta_str(self, key: str):
+        v = C.c_char_p()
+        return v.value.decode() if lib().syn_hip_gguf_meta_str(self.h, key.encode(),
+                                                                C.byref(v)) == 0 else None
+
+    def close(self):
+        if self.h:
+            lib().syn_hip_gguf_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
 
     def __del__(self):
         try:
@@ -588,6 +695,16 @@ def kquant_encode(fmt: int, w: np.ndarray) -> np.ndarray:
     be, bb = KQ_BLOCK[fmt]
     out = np.empty(n * (k // be) * bb, np.uint8)
     check(lib().syn_hip_kquant_encode(fmt, n, k, ptr(w), ptr(out)), "kquant_encode")
+    return out
+
+
+def kquant_decode(fmt: int, blocks: np.ndarray) -> np.ndarray:
+    """Host dequantization of Q8_0 / Q4_K / Q6_K block bytes (the reference's values)."""
+    blocks = np.ascontiguousarray(blocks, np.uint8)
+    be, bb = KQ_BLOCK[fmt]
+    nb = blocks.size // bb
+    out = np.empty(nb * be, np.float32)
+    check(lib().syn_hip_kquant_decode(fmt, nb, ptr(blocks), ptr(out)), "kquant_decode")
     return out
 
 

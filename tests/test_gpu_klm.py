@@ -10,6 +10,7 @@ import pytest
 
 import oracle as O
 from synapse_amd import hip
+from tests import gguf_writer as W
 
 pytestmark = pytest.mark.gpu
 
@@ -102,3 +103,107 @@ def test_llama_3b_widths_two_layers():
         print("decode", step, "cos", _cos(lo, lg), "rel", _rel(lg, lo))
         assert _cos(lo, lg) >= 0.9999
         tok = O.argmax(lo)
+
+
+# ------------------------------------------------------------------ GGUF files
+GGML = {hip.FMT_Q8_0: 8, hip.FMT_Q4_K: 12, hip.FMT_Q6_K: 14}
+LLAMA_NAMES = ["attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down"]
+HF_NAMES = ["self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj", "self_attn.o_proj",
+            "mlp.gate_proj", "mlp.up_proj", "mlp.down_proj"]
+
+
+def _gguf_model(tmp_path, cfg, fmts, qk_norm, hf, tied, seed=0x5EED1000):
+    """One set of weights and norm gains written to a GGUF file, set into the
+    oracle, and set into a device model through the per-tensor API."""
+    fq, fo, fgu, fd, flm = fmts
+    h, hd = cfg["hidden"], cfg["head_dim"]
+    qd, kvd, inter = cfg["n_heads"] * hd, cfg["n_kv_heads"] * hd, cfg["inter"]
+    o = O.CausalLM(cfg, qk_norm=qk_norm)
+    api = hip.KQuantCausalLM(cfg, fq, fo, fgu, fd, flm, qk_norm=qk_norm)
+    tensors = []
+
+    def gain(n, s):  # f16-representable gains around 1, stored as F16 or F32
+        return (1.0 + O.normal(n, s, 0.2)).astype(np.float16).astype(np.float32)
+
+    shapes = [(qd, h, fq), (kvd, h, fq), (kvd, h, fq), (h, qd, fo), (inter, h, fgu),
+              (inter, h, fgu), (h, inter, fd)]
+    for layer in range(cfg["n_layers"]):
+        pre = f"model.layers.{layer}." if hf else f"blk.{layer}."
+        for p, (n, k, f) in enumerate(shapes):
+            b = hip.kquant_encode(f, O.normal(n * k, seed + 16 * layer + p, 0.02).reshape(n, k))
+            o.set_proj(layer, p, NAMES[f], b)
+            api.set_proj(layer, p, b)
+            nm = HF_NAMES[p] if hf else LLAMA_NAMES[p]
+            tensors.append((pre + nm + ".weight", GGML[f], [k, n], b.tobytes()))
+        an, fn = gain(h, seed + 16 * layer + 8), gain(h, seed + 16 * layer + 9)
+        qn = gain(hd, seed + 16 * layer + 10) if qk_norm else None
+        kn = gain(hd, seed + 16 * layer + 11) if qk_norm else None
+        o.set_norms(layer, an, fn, qn, kn)
+        api.set_norms(layer, an, fn, qn, kn)
+        names = (["input_layernorm", "post_attention_layernorm", "self_attn.q_norm",
+                  "self_attn.k_norm"] if hf else
+                 ["attn_norm", "ffn_norm", "attn_q_norm", "attn_k_norm"])
+        tensors.append((pre + names[0] + ".weight", 0, [h], an.tobytes()))
+        tensors.append((pre + names[1] + ".weight", 1, [h], fn.astype(np.float16).tobytes()))
+        if qk_norm:
+            tensors.append((pre + names[2] + ".weight", 1, [hd], qn.astype(np.float16).tobytes()))
+            tensors.append((pre + names[3] + ".weight", 0, [hd], kn.tobytes()))
+    final = gain(h, seed + 0xF00)
+    o.set_final_norm(final)
+    api.set_final_norm(final)
+    tensors.append(("model.norm.weight" if hf else "output_norm.weight", 0, [h],
+                    final.tobytes()))
+    vocab = cfg["vocab"]
+    wl = O.normal(vocab * h, seed + 0xF01, 0.02).reshape(vocab, h)
+    if tied:
+        # token_embd in the lm_head format and no output.weight: both use it
+        b = hip.kquant_encode(flm, wl)
+        emb = O.dequant(NAMES[flm], b, vocab * h).reshape(vocab, h)
+        tensors.append(("model.embed_tokens.weight" if hf else "token_embd.weight", GGML[flm],
+                        [h, vocab], b.tobytes()))
+    else:
+        emb = O.normal(vocab * h, seed + 0xF02, 0.02).reshape(vocab, h)
+        b = hip.kquant_encode(flm, wl)
+        tensors.append(("model.embed_tokens.weight" if hf else "token_embd.weight", 0,
+                        [h, vocab], emb.tobytes()))
+        tensors.append(("lm_head.weight" if hf else "output.weight", GGML[flm], [h, vocab],
+                        b.tobytes()))
+    o.set_embed(emb)
+    api.set_embed(emb)
+    o.set_lm_head(NAMES[flm], b)
+    api.set_lm_head(b)
+    api.finalize()
+    path = W.write_gguf(tmp_path / "model.gguf", tensors,
+                        [("general.architecture", W.STRING, "llama")])
+    return o, api, path
+
+
+@pytest.mark.parametrize("hf,tied,qk_norm,fmts", [
+    (False, False, False, LLAMA_FMTS),
+    (True, True, True, (hip.FMT_Q8_0,) * 5),
+    (False, True, True, (hip.FMT_Q4_K, hip.FMT_Q6_K, hip.FMT_Q4_K, hip.FMT_Q6_K, hip.FMT_Q6_K)),
+])
+def test_load_gguf_matches_api_and_oracle(tmp_path, hf, tied, qk_norm, fmts):
+    o, api, path = _gguf_model(tmp_path, TINY, fmts, qk_norm, hf, tied)
+    with hip.Gguf(path) as f:
+        g = hip.KQuantCausalLM(TINY, *fmts, qk_norm=qk_norm)
+        g.load_gguf(f)
+    ids = O.token_ids(12, 0x5EED0000 + 0xFFFF, TINY["vocab"])
+    lo, la, lg = o.prefill(ids), api.prefill(ids), g.prefill(ids)
+    # same bytes and gains through both routes: identical device results
+    np.testing.assert_array_equal(lg, la)
+    assert _cos(lo, lg) >= 0.9999 and _rel(lg, lo) < 5e-3, (_cos(lo, lg), _rel(lg, lo))
+    tok = O.argmax(lo)
+    for step in range(8):
+        lo, la, lg = o.forward_one(tok), api.forward_one(tok), g.forward_one(tok)
+        np.testing.assert_array_equal(lg, la)
+        assert _cos(lo, lg) >= 0.9999 and _rel(lg, lo) < 5e-3, (step, _rel(lg, lo))
+        tok = O.argmax(lo)
+
+
+def test_load_gguf_rejects_wrong_format(tmp_path):
+    _, _, path = _gguf_model(tmp_path, TINY, LLAMA_FMTS, False, False, False)
+    with hip.Gguf(path) as f:
+        g = hip.KQuantCausalLM(TINY, *((hip.FMT_Q8_0,) * 5))
+        with pytest.raises(hip.SynapseError, match="GGML type"):
+            g.load_gguf(f)
