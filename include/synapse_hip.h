@@ -177,10 +177,25 @@ syn_status_t syn_hip_qlm_set_embed(syn_hip_qlm_t *m, const float *embed);
 syn_status_t syn_hip_qlm_set_layer(syn_hip_qlm_t *m, uint32_t layer, const float *wq,
                                    const float *wk, const float *wv, const float *wo,
                                    const float *wg, const float *wu, const float *wd);
+/* Untied lm_head, f32 [vocab, hidden] (int8.rs:125-130); without it the
+ * lm_head is quantized from embed_tokens (int8.rs:132-139). */
+syn_status_t syn_hip_qlm_set_lm_head(syn_hip_qlm_t *m, const float *w);
+/* RMSNorm gains (int8.rs:33-56, applied as apply_norm / apply_headwise_rmsnorm,
+ * ops/norm.rs:64-93); all 1.0 until set, NULL leaves a gain as it is.  Per
+ * layer: attention and FFN norms [hidden], q/k head norms [head_dim]; final
+ * norm [hidden]. */
+syn_status_t syn_hip_qlm_set_norms(syn_hip_qlm_t *m, uint32_t layer, const float *attn_norm,
+                                   const float *ffn_norm, const float *q_norm,
+                                   const float *k_norm);
+syn_status_t syn_hip_qlm_set_final_norm(syn_hip_qlm_t *m, const float *norm);
+/* Per-head q/k RMSNorm on (1, the default: Qwen3) or off (models whose layers
+ * have no q/k norm weights, where the reference skips it, norm.rs:86-88).
+ * Before finalize. */
+syn_status_t syn_hip_qlm_set_qk_norm(syn_hip_qlm_t *m, int enabled);
 /* Synthetic weights: SplitMix64(seed_base + tensor_id) + Box-Muller, tensor
  * id 0 = embed, 1 + 8*layer + {0..6} = q,k,v,o,gate,up,down. */
 syn_status_t syn_hip_qlm_init_synthetic(syn_hip_qlm_t *m, uint64_t seed_base, float stddev);
-/* Quantize the tied lm_head, upload RoPE tables; call once after weights. */
+/* Quantize the lm_head, upload RoPE tables; call once after weights. */
 syn_status_t syn_hip_qlm_finalize(syn_hip_qlm_t *m);
 syn_status_t syn_hip_qlm_reset(syn_hip_qlm_t *m);
 /* forward_prefill (int8.rs:593-635): logits of the last prompt token. */

@@ -93,6 +93,10 @@ def _declare(L):
         "orc_qlm_set_layer": (C.c_int, [P, SZ, P, P, P, P, P, P, P]),
         "orc_qlm_init_synthetic": (C.c_int, [P, C.c_uint64, C.c_float]),
         "orc_qlm_finalize": (C.c_int, [P]),
+        "orc_qlm_set_norms": (C.c_int, [P, SZ, P, P, P, P]),
+        "orc_qlm_set_final_norm": (C.c_int, [P, P]),
+        "orc_qlm_set_qk_norm": (None, [P, C.c_int]),
+        "orc_qlm_set_lm_head": (C.c_int, [P, P]),
         "orc_qlm_reset": (None, [P]),
         "orc_qlm_cur_len": (SZ, [P]),
         "orc_qlm_prefill": (C.c_int, [P, P, SZ, P]),
@@ -312,13 +316,25 @@ class QuantizedCausalLM:
             raise RuntimeError(f"orc_qlm_init_synthetic status {rc}")
         self._check(lib().orc_qlm_finalize(self.h))
 
-    def set_weights(self, embed: np.ndarray, layers: list):
+    def set_weights(self, embed: np.ndarray, layers: list, final_norm=None, lm_head=None,
+                    qk_norm: bool = True):
         self._keep = [embed]
         self._check(lib().orc_qlm_set_embed(self.h, _p(np.ascontiguousarray(embed, np.float32))))
+        lib().orc_qlm_set_qk_norm(self.h, int(qk_norm))
         for i, lw in enumerate(layers):
             arrs = [np.ascontiguousarray(lw[n], np.float32)
                     for n in ("q", "k", "v", "o", "gate", "up", "down")]
             self._check(lib().orc_qlm_set_layer(self.h, i, *[_p(a) for a in arrs]))
+            gains = [None if lw.get(n) is None else np.ascontiguousarray(lw[n], np.float32)
+                     for n in ("attn_norm", "ffn_norm", "q_norm", "k_norm")]
+            self._check(lib().orc_qlm_set_norms(self.h, i, *[None if g is None else _p(g)
+                                                             for g in gains]))
+        if final_norm is not None:
+            self._check(lib().orc_qlm_set_final_norm(
+                self.h, _p(np.ascontiguousarray(final_norm, np.float32))))
+        if lm_head is not None:
+            self._check(lib().orc_qlm_set_lm_head(
+                self.h, _p(np.ascontiguousarray(lm_head, np.float32))))
         self._check(lib().orc_qlm_finalize(self.h))
 
     @staticmethod

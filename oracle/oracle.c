@@ -700,7 +700,11 @@ struct orc_qlm {
   float *embed; /* [vocab, h] f32 (tied) */
   orc_qlin *lin; /* per layer: q,k,v,o,gate,up,down */
   orc_qlin lm_head;
-  float *attn_norm, *ffn_norm, *q_norm, *k_norm, *final_norm; /* gains (1.0) */
+  /* RMSNorm gains, 1.0 until set: attention / FFN [L][h], q / k head norms
+     [L][hd], final [h] (int8.rs:33-56) */
+  float *attn_norm, *ffn_norm, *q_norm, *k_norm, *final_norm;
+  int qk_norm;      /* 0: no head norms (empty weights skip it, norm.rs:86-88) */
+  float *lm_head_f; /* untied lm_head f32 [vocab, h], or NULL (tied) */
   float *rope_cos, *rope_sin;
   float *kc, *vc; /* per layer [max_seq, kv_dim] */
   size_t cur;
@@ -735,13 +739,15 @@ orc_qlm *orc_qlm_create(const orc_lm_cfg *cfg) {
   size_t h = cfg->hidden, hd = cfg->head_dim, L = cfg->n_layers;
   size_t kv = cfg->n_kv_heads * hd;
   m->lin = (orc_qlin *)calloc(L * 7, sizeof(orc_qlin));
-  m->attn_norm = (float *)malloc(h * 4);
-  m->ffn_norm = (float *)malloc(h * 4);
+  m->attn_norm = (float *)malloc(L * h * 4);
+  m->ffn_norm = (float *)malloc(L * h * 4);
   m->final_norm = (float *)malloc(h * 4);
-  m->q_norm = (float *)malloc(hd * 4);
-  m->k_norm = (float *)malloc(hd * 4);
-  for (size_t i = 0; i < h; i++) m->attn_norm[i] = m->ffn_norm[i] = m->final_norm[i] = 1.0f;
-  for (size_t i = 0; i < hd; i++) m->q_norm[i] = m->k_norm[i] = 1.0f;
+  m->q_norm = (float *)malloc(L * hd * 4);
+  m->k_norm = (float *)malloc(L * hd * 4);
+  for (size_t i = 0; i < L * h; i++) m->attn_norm[i] = m->ffn_norm[i] = 1.0f;
+  for (size_t i = 0; i < h; i++) m->final_norm[i] = 1.0f;
+  for (size_t i = 0; i < L * hd; i++) m->q_norm[i] = m->k_norm[i] = 1.0f;
+  m->qk_norm = 1;
   m->rope_cos = (float *)malloc(cfg->max_seq * (hd / 2) * 4);
   m->rope_sin = (float *)malloc(cfg->max_seq * (hd / 2) * 4);
   orc_rope_tables(cfg->max_seq, hd, cfg->rope_theta, m->rope_cos, m->rope_sin);
@@ -765,6 +771,7 @@ void orc_qlm_destroy(orc_qlm *m) {
   free(m->final_norm);
   free(m->q_norm);
   free(m->k_norm);
+  free(m->lm_head_f);
   free(m->rope_cos);
   free(m->rope_sin);
   free(m->kc);
@@ -833,10 +840,39 @@ int orc_qlm_init_synthetic(orc_qlm *m, uint64_t seed_base, float stddev) {
   return bad ? ORC_ERR_OUT_OF_MEMORY : ORC_OK;
 }
 
-/* tied lm_head quantized from embed_tokens (int8.rs:127-139) */
+int orc_qlm_set_norms(orc_qlm *m, size_t l, const float *attn, const float *ffn,
+                      const float *q, const float *k) {
+  size_t h = m->c.hidden, hd = m->c.head_dim;
+  if (l >= m->c.n_layers) return ORC_ERR_INVALID_ARG;
+  if (attn) memcpy(m->attn_norm + l * h, attn, h * 4);
+  if (ffn) memcpy(m->ffn_norm + l * h, ffn, h * 4);
+  if (q) memcpy(m->q_norm + l * hd, q, hd * 4);
+  if (k) memcpy(m->k_norm + l * hd, k, hd * 4);
+  return ORC_OK;
+}
+
+int orc_qlm_set_final_norm(orc_qlm *m, const float *w) {
+  memcpy(m->final_norm, w, m->c.hidden * 4);
+  return ORC_OK;
+}
+
+void orc_qlm_set_qk_norm(orc_qlm *m, int enabled) { m->qk_norm = enabled != 0; }
+
+int orc_qlm_set_lm_head(orc_qlm *m, const float *w) {
+  size_t bytes = m->c.vocab * m->c.hidden * 4;
+  free(m->lm_head_f);
+  m->lm_head_f = (float *)malloc(bytes);
+  if (!m->lm_head_f) return ORC_ERR_OUT_OF_MEMORY;
+  memcpy(m->lm_head_f, w, bytes);
+  return ORC_OK;
+}
+
+/* lm_head quantized from its own weight, else tied to embed_tokens
+   (int8.rs:125-139) */
 int orc_qlm_finalize(orc_qlm *m) {
   if (!m->embed) return ORC_ERR_NULL_PTR;
-  return qlin_from_f32(&m->lm_head, m->embed, m->c.vocab, m->c.hidden);
+  return qlin_from_f32(&m->lm_head, m->lm_head_f ? m->lm_head_f : m->embed, m->c.vocab,
+                       m->c.hidden);
 }
 
 void orc_qlm_reset(orc_qlm *m) { m->cur = 0; }
@@ -884,14 +920,16 @@ static void layer_forward(orc_qlm *m, size_t l, float *x, size_t t, int prefill)
   float *g = (float *)malloc(t * inter * 4), *u = (float *)malloc(t * inter * 4);
   float *kcl = m->kc + l * c->max_seq * kvd, *vcl = m->vc + l * c->max_seq * kvd;
 
-  orc_rmsnorm(x, m->attn_norm, c->eps, t, h, normed);
+  orc_rmsnorm(x, m->attn_norm + l * h, c->eps, t, h, normed);
   orc_quantize_per_channel_int8(normed, t, h, xq, sx);
   qlin_forward_pre(&L[0], xq, sx, t, q);
   qlin_forward_pre(&L[1], xq, sx, t, k);
   qlin_forward_pre(&L[2], xq, sx, t, v);
   /* headwise q/k RMSNorm (norm.rs:78-93), RoPE, cache append */
-  orc_rmsnorm(q, m->q_norm, c->eps, t * nh, hd, q);
-  orc_rmsnorm(k, m->k_norm, c->eps, t * nkv, hd, k);
+  if (m->qk_norm) {
+    orc_rmsnorm(q, m->q_norm + l * hd, c->eps, t * nh, hd, q);
+    orc_rmsnorm(k, m->k_norm + l * hd, c->eps, t * nkv, hd, k);
+  }
   size_t pos0 = prefill ? 0 : m->cur;
   orc_rope_apply(q, m->rope_cos, m->rope_sin, t, nh, hd, pos0);
   orc_rope_apply(k, m->rope_cos, m->rope_sin, t, nkv, hd, pos0);
@@ -920,7 +958,7 @@ static void layer_forward(orc_qlm *m, size_t l, float *x, size_t t, int prefill)
   }
   qlin_forward(&L[3], attn, t, o, xq, sx);
   for (size_t i = 0; i < t * h; i++) x[i] = x[i] + o[i];
-  orc_rmsnorm(x, m->ffn_norm, c->eps, t, h, normed);
+  orc_rmsnorm(x, m->ffn_norm + l * h, c->eps, t, h, normed);
   ffn_swiglu(m, L, normed, t, o, xq, sx, g, u);
   for (size_t i = 0; i < t * h; i++) x[i] += o[i];
   free(normed); free(xq); free(sx); free(q); free(k); free(v);

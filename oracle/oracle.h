@@ -103,6 +103,13 @@ int orc_qlm_set_layer(orc_qlm *m, size_t layer, const float *wq, const float *wk
                       const float *wv, const float *wo, const float *wg, const float *wu,
                       const float *wd);
 int orc_qlm_init_synthetic(orc_qlm *m, uint64_t seed_base, float stddev);
+/* RMSNorm gains (all 1.0 until set; NULL leaves one as it is), head norms
+   on/off, untied lm_head f32 [vocab, h] (quantized at finalize) */
+int orc_qlm_set_norms(orc_qlm *m, size_t layer, const float *attn, const float *ffn,
+                      const float *q, const float *k);
+int orc_qlm_set_final_norm(orc_qlm *m, const float *w);
+void orc_qlm_set_qk_norm(orc_qlm *m, int enabled);
+int orc_qlm_set_lm_head(orc_qlm *m, const float *w);
 int orc_qlm_finalize(orc_qlm *m);
 void orc_qlm_reset(orc_qlm *m);
 size_t orc_qlm_cur_len(const orc_qlm *m);

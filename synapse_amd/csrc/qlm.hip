@@ -41,8 +41,12 @@ struct syn_hip_qlm_s {
   std::vector<QLayer> layers;
   std::vector<int> have_layer;
   QLinearInt8 lm_head;
-  std::vector<float> host_embed;
-  DevBuf embed, ones_h, ones_hd, zeros_h, rope_cos, rope_sin, kc, vc;
+  std::vector<float> host_embed, host_lm_head;  // f32 until finalize quantizes them
+  bool qk_norm = true;  // per-head q/k RMSNorm (Qwen3); off for models without the gains
+  DevBuf embed, zeros_h, rope_cos, rope_sin, kc, vc;
+  // RMSNorm gains (int8.rs:33-56): attention and FFN norms [L][h], q/k head
+  // norms [L][hd], final norm [h]; 1.0 until set
+  DevBuf attn_nw, ffn_nw, q_nw, k_nw, final_nw;
   DevBuf x, xq, sx, qkv, qrot, attn, aq, sa, o, gu, hq, sh, down, logits, scores;
   DevBuf pv, pi, pv2, state, history, mhist, ids;
   // fused decode step (decode_fused.hip): residual rows, activation scales
@@ -65,11 +69,13 @@ struct syn_hip_qlm_s {
   float *kc_l(size_t l) { return kc.as<float>() + l * k_elems(); }
   float *vc_l(size_t l) { return vc.as<float>() + l * v_elems(); }
   StepState *st() { return state.as<StepState>(); }
+  const float *an(size_t l) { return attn_nw.as<float>() + l * h; }
+  const float *fn(size_t l) { return ffn_nw.as<float>() + l * h; }
+  const float *qn(size_t l) { return qk_norm ? q_nw.as<float>() + l * hd : nullptr; }
+  const float *kn(size_t l) { return qk_norm ? k_nw.as<float>() + l * hd : nullptr; }
 
   syn_status_t alloc_all() {
     const size_t T = S;  // prefill rows
-    SYN_TRY(ones_h.alloc(h * 4));
-    SYN_TRY(ones_hd.alloc(hd * 4));
     SYN_TRY(zeros_h.alloc(h * 4));
     SYN_HIP(hipMemset(zeros_h.p, 0, h * 4));
     SYN_TRY(rope_cos.alloc(S * (hd / 2) * 4));
@@ -103,8 +109,18 @@ struct syn_hip_qlm_s {
     SYN_TRY(mhist.alloc((S + 1) * 4));
     SYN_TRY(ids.alloc(S * 4));
     std::vector<float> one(std::max(h, hd), 1.0f);
-    SYN_HIP(hipMemcpy(ones_h.p, one.data(), h * 4, hipMemcpyHostToDevice));
-    SYN_HIP(hipMemcpy(ones_hd.p, one.data(), hd * 4, hipMemcpyHostToDevice));
+    SYN_TRY(attn_nw.alloc(L * h * 4));
+    SYN_TRY(ffn_nw.alloc(L * h * 4));
+    SYN_TRY(q_nw.alloc(L * hd * 4));
+    SYN_TRY(k_nw.alloc(L * hd * 4));
+    SYN_TRY(final_nw.alloc(h * 4));
+    for (size_t l = 0; l < L; l++) {
+      SYN_HIP(hipMemcpy(attn_nw.as<float>() + l * h, one.data(), h * 4, hipMemcpyHostToDevice));
+      SYN_HIP(hipMemcpy(ffn_nw.as<float>() + l * h, one.data(), h * 4, hipMemcpyHostToDevice));
+      SYN_HIP(hipMemcpy(q_nw.as<float>() + l * hd, one.data(), hd * 4, hipMemcpyHostToDevice));
+      SYN_HIP(hipMemcpy(k_nw.as<float>() + l * hd, one.data(), hd * 4, hipMemcpyHostToDevice));
+    }
+    SYN_HIP(hipMemcpy(final_nw.p, one.data(), h * 4, hipMemcpyHostToDevice));
     // zero padding columns of the activation rows once (kernels never write them)
     SYN_HIP(hipMemset(xq.p, 0, xq.bytes));
     SYN_HIP(hipMemset(aq.p, 0, aq.bytes));
@@ -152,13 +168,12 @@ struct syn_hip_qlm_s {
     const float eps = c.eps;
     const int nh = (int)c.n_heads, nkv = (int)c.n_kv_heads;
     SYN_TRY(launch_rmsnorm_quant(x.as<float>(), l == 0 ? nullptr : down.as<float>(),
-                                 ones_h.as<float>(), eps, rows, (int)h, xq.as<int8_t>(), (int)ldh,
+                                 an(l), eps, rows, (int)h, xq.as<int8_t>(), (int)ldh,
                                  sx.as<float>(), nullptr, s));
     SYN_TRY(Ly.qkv.gemv(rows, xq.as<int8_t>(), ldh, sx.as<float>(), qkv.as<float>(), n_qkv, s));
     SYN_TRY(launch_qk_norm_rope_kv(qkv.as<float>(), (int)n_qkv, rows, nh, nkv, (int)hd,
-                                   ones_hd.as<float>(), ones_hd.as<float>(), eps,
-                                   rope_cos.as<float>(), rope_sin.as<float>(),
-                                   prefill ? nullptr : &st()->pos, 0, qrot.as<float>(), kc_l(l),
+                                   qn(l), kn(l), eps, rope_cos.as<float>(),
+                                   rope_sin.as<float>(), prefill ? nullptr : &st()->pos, 0, qrot.as<float>(), kc_l(l),
                                    vc_l(l), (int)S, s));
     if (prefill)
       SYN_TRY(launch_attention_prefill(qrot.as<float>(), kc_l(l), vc_l(l), rows, nh, nkv,
@@ -169,7 +184,7 @@ struct syn_hip_qlm_s {
     SYN_TRY(launch_quantize_rows(attn.as<float>(), rows, qd, qd, aq.as<int8_t>(), ldq,
                                  sa.as<float>(), s));
     SYN_TRY(Ly.o.gemv(rows, aq.as<int8_t>(), ldq, sa.as<float>(), o.as<float>(), h, s));
-    SYN_TRY(launch_rmsnorm_quant(x.as<float>(), o.as<float>(), ones_h.as<float>(), eps, rows,
+    SYN_TRY(launch_rmsnorm_quant(x.as<float>(), o.as<float>(), fn(l), eps, rows,
                                  (int)h, xq.as<int8_t>(), (int)ldh, sx.as<float>(), nullptr, s));
     SYN_TRY(Ly.gu.gemv(rows, xq.as<int8_t>(), ldh, sx.as<float>(), gu.as<float>(), 2 * inter, s));
     SYN_TRY(launch_swiglu_quant(gu.as<float>(), (int)(2 * inter), rows, (int)inter,
@@ -182,7 +197,7 @@ struct syn_hip_qlm_s {
   syn_status_t head(int row, int add_pos, hipStream_t s) {
     float *xr = x.as<float>() + (size_t)row * h;
     const float *dr = down.as<float>() + (size_t)row * h;
-    SYN_TRY(launch_rmsnorm_quant(xr, dr, ones_h.as<float>(), c.eps, 1, (int)h, xq.as<int8_t>(),
+    SYN_TRY(launch_rmsnorm_quant(xr, dr, final_nw.as<float>(), c.eps, 1, (int)h, xq.as<int8_t>(),
                                  (int)ldh, sx.as<float>(), nullptr, s));
     SYN_TRY(lm_head.gemv(1, xq.as<int8_t>(), ldh, sx.as<float>(), logits.as<float>(), vocab, s));
     SYN_TRY(launch_argmax(logits.as<float>(), (int)vocab, pv.as<float>(), pi.as<int>(),
@@ -245,20 +260,20 @@ struct syn_hip_qlm_s {
       QLayer &Ly = layers[l];
       const RowSrc prev = l == 0 ? RowSrc{} : layers[l - 1].f_down.rows(s_down);
       SYN_TRY(launch_fused_norm_gemv(l == 0 ? nullptr : xmid.as<float>(), embed.as<float>(),
-                                     st(), (int)vocab, zeros_h.as<float>(), prev, xin.as<float>(), ones_h.as<float>(),
-                                     eps, (int)h, s_qkv, Ly.f_qkv, s));
-      SYN_TRY(launch_fused_attention(Ly.f_qkv.rows(s_qkv), nh, nkv, (int)hd, ones_hd.as<float>(),
-                                     ones_hd.as<float>(), eps, rope_cos.as<float>(),
+                                     st(), (int)vocab, zeros_h.as<float>(), prev, xin.as<float>(),
+                                     an(l), eps, (int)h, s_qkv, Ly.f_qkv, s));
+      SYN_TRY(launch_fused_attention(Ly.f_qkv.rows(s_qkv), nh, nkv, (int)hd, qn(l), kn(l), eps,
+                                     rope_cos.as<float>(),
                                      rope_sin.as<float>(), st(), kc_l(l), vc_l(l), (int)S,
                                      attn.as<float>(), s));
       SYN_TRY(launch_fused_quant_gemv(attn.as<float>(), (int)qd, s_o, Ly.f_o, s));
       SYN_TRY(launch_fused_norm_gemv(xin.as<float>(), nullptr, st(), (int)vocab, nullptr,
-                                     Ly.f_o.rows(s_o), xmid.as<float>(), ones_h.as<float>(), eps,
+                                     Ly.f_o.rows(s_o), xmid.as<float>(), fn(l), eps,
                                      (int)h, s_gu, Ly.f_gu, s));
       SYN_TRY(launch_fused_swiglu_gemv(Ly.f_gu.rows(s_gu), (int)inter, s_down, Ly.f_down, s));
     }
     SYN_TRY(launch_fused_final_norm(xmid.as<float>(), layers[L - 1].f_down.rows(s_down),
-                                    ones_h.as<float>(), eps, (int)h, xq.as<int8_t>(), s_head, s));
+                                    final_nw.as<float>(), eps, (int)h, xq.as<int8_t>(), s_head, s));
     SYN_TRY(launch_lmhead_top2(lm_head.w.p, lm_head.scales.as<float>(), (int)vocab,
                                lm_head.chunks, xq.as<int8_t>(), s_head, logits.as<float>(),
                                pv.as<float>(), pi.as<int>(), pv2.as<float>(), s));
@@ -405,6 +420,49 @@ syn_status_t syn_hip_qlm_set_layer(syn_hip_qlm_t *m, uint32_t layer, const float
   return m->set_layer(layer, wq, wk, wv, wo, wg, wu, wd);
 }
 
+syn_status_t syn_hip_qlm_set_lm_head(syn_hip_qlm_t *m, const float *w) {
+  if (!m || !w) return SYN_ERR_NULL_PTR;
+  if (m->finalized) {
+    set_error("lm_head must be set before finalize");
+    return SYN_ERR_INVALID_ARG;
+  }
+  m->host_lm_head.assign(w, w + m->vocab * m->h);
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_qlm_set_norms(syn_hip_qlm_t *m, uint32_t layer, const float *attn_norm,
+                                   const float *ffn_norm, const float *q_norm,
+                                   const float *k_norm) {
+  if (!m) return SYN_ERR_NULL_PTR;
+  if (layer >= m->L) return SYN_ERR_INVALID_ARG;
+  const size_t h = m->h, hd = m->hd;
+  if (attn_norm)
+    SYN_HIP(hipMemcpy(m->attn_nw.as<float>() + layer * h, attn_norm, h * 4, hipMemcpyHostToDevice));
+  if (ffn_norm)
+    SYN_HIP(hipMemcpy(m->ffn_nw.as<float>() + layer * h, ffn_norm, h * 4, hipMemcpyHostToDevice));
+  if (q_norm)
+    SYN_HIP(hipMemcpy(m->q_nw.as<float>() + layer * hd, q_norm, hd * 4, hipMemcpyHostToDevice));
+  if (k_norm)
+    SYN_HIP(hipMemcpy(m->k_nw.as<float>() + layer * hd, k_norm, hd * 4, hipMemcpyHostToDevice));
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_qlm_set_final_norm(syn_hip_qlm_t *m, const float *norm) {
+  if (!m || !norm) return SYN_ERR_NULL_PTR;
+  SYN_HIP(hipMemcpy(m->final_nw.p, norm, m->h * 4, hipMemcpyHostToDevice));
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_qlm_set_qk_norm(syn_hip_qlm_t *m, int enabled) {
+  if (!m) return SYN_ERR_NULL_PTR;
+  if (m->finalized) {
+    set_error("qk_norm must be chosen before finalize");
+    return SYN_ERR_INVALID_ARG;
+  }
+  m->qk_norm = enabled != 0;
+  return SYN_OK;
+}
+
 syn_status_t syn_hip_qlm_init_synthetic(syn_hip_qlm_t *m, uint64_t seed_base, float stddev) {
   if (!m) return SYN_ERR_NULL_PTR;
   const size_t h = m->h;
@@ -441,9 +499,12 @@ syn_status_t syn_hip_qlm_finalize(syn_hip_qlm_t *m) {
       set_error("layer " + std::to_string(l) + " not set");
       return SYN_ERR_INVALID_ARG;
     }
-  // tied lm_head from embed_tokens (int8.rs:132-139)
-  SYN_TRY(m->lm_head.from_f32(m->host_embed.data(), m->vocab, m->h));
+  // lm_head quantized from its own weight, else tied to embed_tokens
+  // (int8.rs:125-139)
+  const std::vector<float> &lm = m->host_lm_head.empty() ? m->host_embed : m->host_lm_head;
+  SYN_TRY(m->lm_head.from_f32(lm.data(), m->vocab, m->h));
   std::vector<float>().swap(m->host_embed);
+  std::vector<float>().swap(m->host_lm_head);
   // RoPE tables, models/lm/builder.rs:88-133 (glibc powf/cosf/sinf, as Rust f32)
   const size_t half = m->hd / 2;
   std::vector<float> cs(m->S * half), sn(m->S * half);

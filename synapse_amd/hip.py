@@ -83,6 +83,10 @@ SIGNATURES = {
     "syn_hip_qlm_set_embed": (ST, [P, P]),
     "syn_hip_qlm_set_layer": (ST, [P, C.c_uint32, P, P, P, P, P, P, P]),
     "syn_hip_qlm_init_synthetic": (ST, [P, C.c_uint64, C.c_float]),
+    "syn_hip_qlm_set_lm_head": (ST, [P, P]),
+    "syn_hip_qlm_set_norms": (ST, [P, C.c_uint32, P, P, P, P]),
+    "syn_hip_qlm_set_final_norm": (ST, [P, P]),
+    "syn_hip_qlm_set_qk_norm": (ST, [P, C.c_int]),
     "syn_hip_qlm_finalize": (ST, [P]),
     "syn_hip_qlm_reset": (ST, [P]),
     "syn_hip_qlm_forward_prefill": (ST, [P, P, SZ, P]),
@@ -400,12 +404,26 @@ class QuantizedCausalLM:
         check(lib().syn_hip_qlm_init_synthetic(self.h, seed_base, std), "qlm_init_synthetic")
         check(lib().syn_hip_qlm_finalize(self.h), "qlm_finalize")
 
-    def set_weights(self, embed: np.ndarray, layers: list):
+    def set_weights(self, embed: np.ndarray, layers: list, final_norm=None, lm_head=None,
+                    qk_norm: bool = True):
+        """f32 weights: layers[i] holds q,k,v,o,gate,up,down [out, in] and optionally
+        the gains attn_norm, ffn_norm, q_norm, k_norm; lm_head None = tied."""
         check(lib().syn_hip_qlm_set_embed(self.h, ptr(np.ascontiguousarray(embed, np.float32))))
+        check(lib().syn_hip_qlm_set_qk_norm(self.h, int(qk_norm)), "set_qk_norm")
         for i, lw in enumerate(layers):
             arrs = [np.ascontiguousarray(lw[n], np.float32)
                     for n in ("q", "k", "v", "o", "gate", "up", "down")]
             check(lib().syn_hip_qlm_set_layer(self.h, i, *[ptr(a) for a in arrs]), "set_layer")
+            gains = [None if lw.get(n) is None else np.ascontiguousarray(lw[n], np.float32)
+                     for n in ("attn_norm", "ffn_norm", "q_norm", "k_norm")]
+            check(lib().syn_hip_qlm_set_norms(self.h, i, *[None if g is None else ptr(g)
+                                                           for g in gains]), "set_norms")
+        if final_norm is not None:
+            check(lib().syn_hip_qlm_set_final_norm(
+                self.h, ptr(np.ascontiguousarray(final_norm, np.float32))), "set_final_norm")
+        if lm_head is not None:
+            check(lib().syn_hip_qlm_set_lm_head(
+                self.h, ptr(np.ascontiguousarray(lm_head, np.float32))), "set_lm_head")
         check(lib().syn_hip_qlm_finalize(self.h), "qlm_finalize")
 
     def reset(self):

@@ -111,3 +111,50 @@ def test_qwen3_shape_64_greedy_steps():
     print("min top1-top2 margin", float(mo.min()))
     np.testing.assert_array_equal(tg, to)
     np.testing.assert_array_equal(_bits(mg), _bits(mo))
+
+
+def _weights_with_gains(cfg, seed=0x5EED3000, untied=True):
+    """f32 weights, non-unit RMSNorm gains and (optionally) an untied lm_head."""
+    h, hd = cfg["hidden"], cfg["head_dim"]
+    qd, kvd, inter = cfg["n_heads"] * hd, cfg["n_kv_heads"] * hd, cfg["inter"]
+    shapes = {"q": (qd, h), "k": (kvd, h), "v": (kvd, h), "o": (h, qd), "gate": (inter, h),
+              "up": (inter, h), "down": (h, inter)}
+    layers = []
+    for layer in range(cfg["n_layers"]):
+        lw = {}
+        for i, (n, (r, c)) in enumerate(shapes.items()):
+            lw[n] = O.normal(r * c, seed + 16 * layer + i, 0.05).reshape(r, c)
+        for i, (n, d) in enumerate((("attn_norm", h), ("ffn_norm", h), ("q_norm", hd),
+                                    ("k_norm", hd))):
+            lw[n] = 1.0 + O.normal(d, seed + 16 * layer + 8 + i, 0.3)
+        layers.append(lw)
+    embed = O.normal(cfg["vocab"] * h, seed + 0xE0, 0.05).reshape(cfg["vocab"], h)
+    final = 1.0 + O.normal(h, seed + 0xE1, 0.3)
+    lm = O.normal(cfg["vocab"] * h, seed + 0xE2, 0.05).reshape(cfg["vocab"], h) if untied else None
+    return embed, layers, final, lm
+
+
+@pytest.mark.parametrize("fused", [True, False])
+@pytest.mark.parametrize("qk_norm,untied", [(True, True), (False, False)])
+def test_norm_gains_and_untied_lm_head_bit_exact(fused, qk_norm, untied):
+    # gains enter as (x*w)*scale in the reference's order, so the whole model
+    # stays bit-exact with them; qk_norm off skips the head norms
+    cfg = SMALL
+    embed, layers, final, lm = _weights_with_gains(cfg, untied=untied)
+    o = O.QuantizedCausalLM(cfg)
+    o.set_weights(embed, layers, final, lm, qk_norm=qk_norm)
+    g = hip.QuantizedCausalLM(cfg)
+    g.set_weights(embed, layers, final, lm, qk_norm=qk_norm)
+    g.set_options(fused=fused)
+    ids = O.token_ids(24, PROMPT_SEED, cfg["vocab"])
+    lo, lg = o.prefill(ids), g.prefill(ids)
+    np.testing.assert_array_equal(_bits(lg), _bits(lo))
+    tok = O.argmax(lo)
+    for step in range(24):
+        lo, lg = o.forward_one(tok), g.forward_one(tok)
+        np.testing.assert_array_equal(_bits(lg), _bits(lo), err_msg=f"step {step}")
+        tok = O.argmax(lo)
+    to, mo = o.generate(ids, 16)
+    tg, mg = g.generate(ids, 16)
+    np.testing.assert_array_equal(tg, to)
+    np.testing.assert_array_equal(_bits(mg), _bits(mo))
