@@ -245,6 +245,7 @@ syn_status_t syn_hip_qlm_destroy(syn_hip_qlm_t *m);
 #define SYN_HIP_GGML_Q8_0 8
 #define SYN_HIP_GGML_Q4_K 12
 #define SYN_HIP_GGML_Q6_K 14
+#define SYN_HIP_GGML_BF16 30 /* read here; the reference rejects it */
 /* metadata value types */
 #define SYN_HIP_GGUF_UINT8 0
 #define SYN_HIP_GGUF_INT8 1
@@ -274,6 +275,56 @@ syn_status_t syn_hip_gguf_meta_u64(const syn_hip_gguf_t *g, const char *key, uin
 syn_status_t syn_hip_gguf_meta_f64(const syn_hip_gguf_t *g, const char *key, double *value);
 syn_status_t syn_hip_gguf_meta_str(const syn_hip_gguf_t *g, const char *key, const char **value);
 syn_status_t syn_hip_gguf_close(syn_hip_gguf_t *g);
+/* numel f32 values of tensor `index` as the reference's parse_gguf returns
+ * them (gguf.rs:208-233): F32, F16 (converter.rs:12-40), Q4_0 (element 2i =
+ * low nibble, 2i+1 = high), Q4_1, Q8_0, Q4_K, Q6_K; also BF16 (type 30). */
+syn_status_t syn_hip_gguf_to_f32(const syn_hip_gguf_t *g, size_t index, float *out);
+
+/* -- safetensors (weight_loading/safetensors.rs:21-302): a file, or a
+ *    directory holding model.safetensors.index.json (the shards it lists,
+ *    only the tensors in its weight_map, each from its named shard) or one
+ *    .safetensors file.  dtypes as the reference: F32, F16, BF16, I64, I32,
+ *    U8 (others -> SYN_ERR_INVALID_ARG at open).  shape8 is row-major
+ *    (slowest axis first, unused = 0); pointers point into the mapping and
+ *    stay valid until syn_hip_safetensors_close. -- */
+#define SYN_HIP_ST_F32 0
+#define SYN_HIP_ST_F16 1
+#define SYN_HIP_ST_BF16 2
+#define SYN_HIP_ST_I64 3
+#define SYN_HIP_ST_I32 4
+#define SYN_HIP_ST_U8 5
+typedef struct syn_hip_safetensors_s syn_hip_safetensors_t;
+syn_status_t syn_hip_safetensors_open(const char *path, syn_hip_safetensors_t **out);
+syn_status_t syn_hip_safetensors_tensor_count(const syn_hip_safetensors_t *st, size_t *n);
+syn_status_t syn_hip_safetensors_find(const syn_hip_safetensors_t *st, const char *name,
+                                      size_t *index);
+syn_status_t syn_hip_safetensors_tensor_info(const syn_hip_safetensors_t *st, size_t index,
+                                             const char **name, uint32_t *dtype,
+                                             uint32_t *n_dims, uint64_t *shape8,
+                                             uint64_t *nbytes, const void **data);
+/* a string of the header's __metadata__ */
+syn_status_t syn_hip_safetensors_meta(const syn_hip_safetensors_t *st, const char *key,
+                                      const char **value);
+/* numel f32 values as parse_safetensors converts them (F16 and BF16 by
+ * converter.rs:12-46, integers cast) */
+syn_status_t syn_hip_safetensors_to_f32(const syn_hip_safetensors_t *st, size_t index,
+                                        float *out);
+/* The Q4_0 triple expand_q4_tensors reads (safetensors.rs:80-170:
+ * <base>.q4_nibbles U8 [rows, bpr, 16], <base>.q4_scales F16 [rows, bpr],
+ * <base>.q4_orig_cols I64 [1]) as pack_for_zig bytes [rows, bpr, 18] without
+ * dequantizing.  packed may be NULL to query rows and cols (orig_cols). */
+syn_status_t syn_hip_safetensors_q4_pack(const syn_hip_safetensors_t *st, const char *base,
+                                         uint8_t *packed, size_t *rows, size_t *cols);
+syn_status_t syn_hip_safetensors_close(syn_hip_safetensors_t *st);
+
+/* Linear layers straight from file bytes (no dequantization):
+ * a 2-D GGUF tensor of type Q4_0 (the reference's RawQ4Tensor, gguf.rs:49-57),
+ * Q8_0, Q4_K or Q6_K, dims {K, N}; or a safetensors Q4_0 triple whose
+ * orig_cols is a multiple of 32. */
+syn_status_t syn_hip_qlinear_from_gguf(const syn_hip_gguf_t *g, const char *name,
+                                       syn_hip_qlinear_t **out);
+syn_status_t syn_hip_qlinear_from_safetensors_q4(const syn_hip_safetensors_t *st,
+                                                 const char *base, syn_hip_qlinear_t **out);
 
 /* -- f32 causal LM over GGUF-block weights: CausalLM (models/lm/causal_lm.rs:
  *    195-278, decoder_layer.rs:51-138, 590-730), the reference path for models
@@ -310,6 +361,16 @@ syn_status_t syn_hip_klm_set_final_norm(syn_hip_klm_t *m, const float *norm);
  * a missing lm_head is tied to token_embd (which must then hold the lm_head
  * format).  Call syn_hip_klm_finalize afterwards. */
 syn_status_t syn_hip_klm_load_gguf(syn_hip_klm_t *m, const syn_hip_gguf_t *g);
+/* INT8 decoder weights from a file (engine/loading.rs:29-130 with
+ * quantize_model, int8.rs:78-152): HuggingFace names
+ * (model.layers.N.self_attn.q_proj.weight, ..., fused qkv_proj / gate_up_proj
+ * split by the q/k/v widths, weight_map.rs:780-829) or llama.cpp GGUF names
+ * (blk.N.attn_q.weight, ...); any tensor type the container's to_f32 reads,
+ * converted as the reference does, then quantized.  Head norms are on when
+ * layer 0 has q_norm weights; lm_head is tied when the file has none.  Call
+ * syn_hip_qlm_finalize afterwards. */
+syn_status_t syn_hip_qlm_load_gguf(syn_hip_qlm_t *m, const syn_hip_gguf_t *g);
+syn_status_t syn_hip_qlm_load_safetensors(syn_hip_qlm_t *m, const syn_hip_safetensors_t *st);
 /* Synthetic weights (seed spec as syn_hip_qlm_init_synthetic; untied lm_head
  * is tensor id 1 + 8*n_layers), encoded with the library's block encoder. */
 syn_status_t syn_hip_klm_init_synthetic(syn_hip_klm_t *m, uint64_t seed_base, float stddev);

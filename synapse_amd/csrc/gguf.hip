@@ -30,12 +30,14 @@ namespace {
 constexpr uint32_t kGgufMagic = 0x46554747u;
 constexpr size_t kGgufAlign = 32;
 
-// ggml tensor types the reference loads (gguf.rs:12-19) and their block sizes
+// ggml tensor types the reference loads (gguf.rs:12-19), plus BF16, and their
+// block sizes
 size_t ggml_type_bytes(uint32_t type, uint64_t numel, bool *ok) {
   *ok = true;
   switch (type) {
     case SYN_HIP_GGML_F32: return numel * 4;
     case SYN_HIP_GGML_F16: return numel * 2;
+    case SYN_HIP_GGML_BF16: return numel * 2;
     case SYN_HIP_GGML_Q4_0: if (numel % 32) break; return numel / 32 * 18;
     case SYN_HIP_GGML_Q4_1: if (numel % 32) break; return numel / 32 * 20;
     case SYN_HIP_GGML_Q8_0: if (numel % 32) break; return numel / 32 * 34;

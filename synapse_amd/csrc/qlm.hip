@@ -22,6 +22,7 @@
 #include "decode_fused.hpp"
 #include "layer_ops.hpp"
 #include "linear.hpp"
+#include "weights.hpp"
 
 namespace syn {
 
@@ -461,6 +462,123 @@ syn_status_t syn_hip_qlm_set_qk_norm(syn_hip_qlm_t *m, int enabled) {
   }
   m->qk_norm = enabled != 0;
   return SYN_OK;
+}
+
+// --------------------------------------------------------- weight files
+// Every tensor of the model by HuggingFace names (the reference's weight
+// map, weight_map.rs; fused qkv_proj / gate_up_proj split as
+// split_fused_projections does, weight_map.rs:780-829, by the q/k/v widths)
+// or llama.cpp's GGUF names; converted to f32 as the reference's loaders do,
+// then quantized like quantize_model (int8.rs:78-152).
+static syn_status_t qlm_load(syn_hip_qlm_t *m, const WeightSource &src) {
+  const size_t h = m->h, hd = m->hd, qd = m->qd, kvd = m->kvd, inter = m->inter;
+  TensorView t;
+  auto need = [&](bool ok, const std::string &what) -> syn_status_t {
+    if (ok) return SYN_OK;
+    set_error("weights: no tensor for " + what);
+    return SYN_ERR_INVALID_ARG;
+  };
+  auto shape_err = [&](const TensorView &v, const std::string &want) -> syn_status_t {
+    std::string got;
+    for (int d = 0; d < v.n_dims; d++) got += (d ? "x" : "") + std::to_string(v.shape[d]);
+    set_error("weights: tensor " + v.name + " is " + got + ", the model expects " + want);
+    return SYN_ERR_SHAPE_MISMATCH;
+  };
+  auto matrix = [&](const TensorView &v, size_t rows, size_t cols,
+                    std::vector<float> &out) -> syn_status_t {
+    if (!v.is_matrix(rows, cols)) return shape_err(v, std::to_string(rows) + "x" + std::to_string(cols));
+    out.resize(rows * cols);
+    return tensor_to_f32(v, out.data());
+  };
+  auto vec = [&](const TensorView &v, size_t n, std::vector<float> &out) -> syn_status_t {
+    if (!v.is_vector(n)) return shape_err(v, std::to_string(n));
+    out.resize(n);
+    return tensor_to_f32(v, out.data());
+  };
+  static const char *kHf[7] = {"self_attn.q_proj", "self_attn.k_proj", "self_attn.v_proj",
+                               "self_attn.o_proj", "mlp.gate_proj", "mlp.up_proj",
+                               "mlp.down_proj"};
+  static const char *kLlama[7] = {"attn_q", "attn_k", "attn_v", "attn_output",
+                                  "ffn_gate", "ffn_up", "ffn_down"};
+  const size_t rows[7] = {qd, kvd, kvd, h, inter, inter, h};
+  const size_t cols[7] = {h, h, h, qd, h, h, inter};
+  // head norms: the reference applies them when the weights exist
+  const bool qk = src.find_any({"model.layers.0.self_attn.q_norm.weight",
+                                "blk.0.attn_q_norm.weight"}, &t);
+  SYN_TRY(syn_hip_qlm_set_qk_norm(m, qk ? 1 : 0));
+  std::vector<std::vector<float>> w(7);
+  for (size_t l = 0; l < m->L; l++) {
+    const std::string hf = "model.layers." + std::to_string(l) + ".";
+    const std::string bl = "blk." + std::to_string(l) + ".";
+    for (int p = 0; p < 7; p++) {
+      if (src.find_any({hf + kHf[p] + ".weight", bl + kLlama[p] + ".weight"}, &t)) {
+        SYN_TRY(matrix(t, rows[p], cols[p], w[p]));
+      } else if (p <= 2 && src.find(hf + "self_attn.qkv_proj.weight", &t)) {
+        std::vector<float> all;
+        SYN_TRY(matrix(t, qd + 2 * kvd, h, all));
+        const size_t r0 = p == 0 ? 0 : p == 1 ? qd : qd + kvd;
+        w[p].assign(all.begin() + r0 * h, all.begin() + (r0 + rows[p]) * h);
+      } else if ((p == 4 || p == 5) && src.find(hf + "mlp.gate_up_proj.weight", &t)) {
+        std::vector<float> all;
+        SYN_TRY(matrix(t, 2 * inter, h, all));
+        const size_t r0 = p == 4 ? 0 : inter;
+        w[p].assign(all.begin() + r0 * h, all.begin() + (r0 + inter) * h);
+      } else {
+        return need(false, hf + kHf[p] + ".weight");
+      }
+    }
+    SYN_TRY(m->set_layer(l, w[0].data(), w[1].data(), w[2].data(), w[3].data(), w[4].data(),
+                         w[5].data(), w[6].data()));
+    std::vector<float> an, fn, qn, kn;
+    if (src.find_any({hf + "input_layernorm.weight", bl + "attn_norm.weight"}, &t))
+      SYN_TRY(vec(t, h, an));
+    if (src.find_any({hf + "post_attention_layernorm.weight", bl + "ffn_norm.weight"}, &t))
+      SYN_TRY(vec(t, h, fn));
+    if (qk) {
+      SYN_TRY(need(src.find_any({hf + "self_attn.q_norm.weight", bl + "attn_q_norm.weight"}, &t),
+                   hf + "self_attn.q_norm.weight"));
+      SYN_TRY(vec(t, hd, qn));
+      SYN_TRY(need(src.find_any({hf + "self_attn.k_norm.weight", bl + "attn_k_norm.weight"}, &t),
+                   hf + "self_attn.k_norm.weight"));
+      SYN_TRY(vec(t, hd, kn));
+    }
+    SYN_TRY(syn_hip_qlm_set_norms(m, (uint32_t)l, an.empty() ? nullptr : an.data(),
+                                  fn.empty() ? nullptr : fn.data(),
+                                  qn.empty() ? nullptr : qn.data(),
+                                  kn.empty() ? nullptr : kn.data()));
+  }
+  std::vector<float> v;
+  SYN_TRY(need(src.find_any({"model.embed_tokens.weight", "token_embd.weight"}, &t),
+               "model.embed_tokens.weight"));
+  SYN_TRY(matrix(t, m->vocab, h, v));
+  SYN_TRY(syn_hip_qlm_set_embed(m, v.data()));
+  if (src.find_any({"model.norm.weight", "output_norm.weight"}, &t)) {
+    SYN_TRY(vec(t, h, v));
+    SYN_TRY(syn_hip_qlm_set_final_norm(m, v.data()));
+  }
+  if (src.find_any({"lm_head.weight", "output.weight"}, &t)) {
+    SYN_TRY(matrix(t, m->vocab, h, v));
+    SYN_TRY(syn_hip_qlm_set_lm_head(m, v.data()));
+  }
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_qlm_load_gguf(syn_hip_qlm_t *m, const syn_hip_gguf_t *g) {
+  if (!m || !g) return SYN_ERR_NULL_PTR;
+  if (m->finalized) {
+    set_error("weights must be loaded before finalize");
+    return SYN_ERR_INVALID_ARG;
+  }
+  return qlm_load(m, *gguf_source(g));
+}
+
+syn_status_t syn_hip_qlm_load_safetensors(syn_hip_qlm_t *m, const syn_hip_safetensors_t *st) {
+  if (!m || !st) return SYN_ERR_NULL_PTR;
+  if (m->finalized) {
+    set_error("weights must be loaded before finalize");
+    return SYN_ERR_INVALID_ARG;
+  }
+  return qlm_load(m, *safetensors_source(st));
 }
 
 syn_status_t syn_hip_qlm_init_synthetic(syn_hip_qlm_t *m, uint64_t seed_base, float stddev) {

@@ -122,6 +122,22 @@ SIGNATURES = {
     "syn_hip_gguf_meta_f64": (ST, [P, C.c_char_p, C.POINTER(C.c_double)]),
     "syn_hip_gguf_meta_str": (ST, [P, C.c_char_p, C.POINTER(C.c_char_p)]),
     "syn_hip_gguf_close": (ST, [P]),
+    "syn_hip_gguf_to_f32": (ST, [P, SZ, P]),
+    "syn_hip_safetensors_open": (ST, [C.c_char_p, C.POINTER(P)]),
+    "syn_hip_safetensors_tensor_count": (ST, [P, C.POINTER(SZ)]),
+    "syn_hip_safetensors_find": (ST, [P, C.c_char_p, C.POINTER(SZ)]),
+    "syn_hip_safetensors_tensor_info": (ST, [P, SZ, C.POINTER(C.c_char_p),
+                                             C.POINTER(C.c_uint32), C.POINTER(C.c_uint32),
+                                             C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
+                                             C.POINTER(P)]),
+    "syn_hip_safetensors_meta": (ST, [P, C.c_char_p, C.POINTER(C.c_char_p)]),
+    "syn_hip_safetensors_to_f32": (ST, [P, SZ, P]),
+    "syn_hip_safetensors_q4_pack": (ST, [P, C.c_char_p, P, C.POINTER(SZ), C.POINTER(SZ)]),
+    "syn_hip_safetensors_close": (ST, [P]),
+    "syn_hip_qlinear_from_gguf": (ST, [P, C.c_char_p, C.POINTER(P)]),
+    "syn_hip_qlinear_from_safetensors_q4": (ST, [P, C.c_char_p, C.POINTER(P)]),
+    "syn_hip_qlm_load_gguf": (ST, [P, P]),
+    "syn_hip_qlm_load_safetensors": (ST, [P, P]),
     "syn_hip_klm_destroy": (ST, [P]),
     "syn_hip_mamba_create": (ST, [C.POINTER(MambaConfig), C.POINTER(P)]),
     "syn_hip_mamba_init_synthetic": (ST, [P, C.c_uint64, C.c_float]),
@@ -341,6 +357,24 @@ class QLinear:
               "qlinear_create")
         return cls(h.value, fmt)
 
+    @classmethod
+    def from_gguf(cls, gguf: "Gguf", name: str) -> "QLinear":
+        """A Q4_0 / Q8_0 / Q4_K / Q6_K GGUF tensor, uploaded as stored."""
+        h = C.c_void_p()
+        check(lib().syn_hip_qlinear_from_gguf(gguf.h, name.encode(), C.byref(h)),
+              "qlinear_from_gguf")
+        fmt = {2: FMT_Q4_0, 8: FMT_Q8_0, 12: FMT_Q4_K, 14: FMT_Q6_K}[
+            gguf.info(gguf.index(name)).ggml_type]
+        return cls(h.value, fmt)
+
+    @classmethod
+    def from_safetensors_q4(cls, st: "Safetensors", base: str) -> "QLinear":
+        """A safetensors Q4_0 triple, uploaded without dequantizing."""
+        h = C.c_void_p()
+        check(lib().syn_hip_qlinear_from_safetensors_q4(st.h, base.encode(), C.byref(h)),
+              "qlinear_from_safetensors_q4")
+        return cls(h.value, FMT_Q4_0)
+
     def forward_dev(self, m: int, d_x: int, d_y: int, stream=None):
         check(lib().syn_hip_qlinear_forward(self.h, m, d_x, d_y, stream), "qlinear_forward")
 
@@ -424,6 +458,16 @@ class QuantizedCausalLM:
         if lm_head is not None:
             check(lib().syn_hip_qlm_set_lm_head(
                 self.h, ptr(np.ascontiguousarray(lm_head, np.float32))), "set_lm_head")
+        check(lib().syn_hip_qlm_finalize(self.h), "qlm_finalize")
+
+    def load_gguf(self, gguf: "Gguf"):
+        """Every weight from a GGUF file (HuggingFace or llama.cpp names), then finalize."""
+        check(lib().syn_hip_qlm_load_gguf(self.h, gguf.h), "qlm_load_gguf")
+        check(lib().syn_hip_qlm_finalize(self.h), "qlm_finalize")
+
+    def load_safetensors(self, st: "Safetensors"):
+        """Every weight from a safetensors file or sharded checkpoint, then finalize."""
+        check(lib().syn_hip_qlm_load_safetensors(self.h, st.h), "qlm_load_safetensors")
         check(lib().syn_hip_qlm_finalize(self.h), "qlm_finalize")
 
     def reset(self):
@@ -617,6 +661,13 @@ class Gguf:
     def tensors(self):
         return [self.info(i) for i in range(len(self))]
 
+    def to_f32(self, index: int) -> np.ndarray:
+        """f32 values of a tensor as the reference's parse_gguf returns them."""
+        t = self.info(index)
+        out = np.empty(int(np.prod(t.dims)), np.float32)
+        check(lib().syn_hip_gguf_to_f32(self.h, index, ptr(out)), "gguf_to_f32")
+        return out
+
     def meta_u64(self, key: str):
         v = C.c_uint64()
         return v.value if lib().syn_hip_gguf_meta_u64(self.h, key.encode(), C.byref(v)) == 0 \
@@ -635,6 +686,88 @@ class Gguf:
     def close(self):
         if self.h:
             lib().syn_hip_gguf_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+ST_DTYPES = {0: "F32", 1: "F16", 2: "BF16", 3: "I64", 4: "I32", 5: "U8"}
+
+
+class SafetensorsTensorInfo(GgufTensorInfo):
+    __slots__ = ()
+
+    @property
+    def dtype(self) -> str:
+        return ST_DTYPES[self.ggml_type]
+
+
+class Safetensors:
+    """Read-only mapping of a safetensors file or sharded checkpoint directory."""
+
+    def __init__(self, path):
+        h = C.c_void_p()
+        check(lib().syn_hip_safetensors_open(str(path).encode(), C.byref(h)), "safetensors_open")
+        self.h = h.value
+
+    def __len__(self):
+        n = SZ()
+        check(lib().syn_hip_safetensors_tensor_count(self.h, C.byref(n)), "tensor_count")
+        return n.value
+
+    def index(self, name: str):
+        i = SZ()
+        rc = lib().syn_hip_safetensors_find(self.h, name.encode(), C.byref(i))
+        return i.value if rc == 0 else None
+
+    def info(self, index: int) -> SafetensorsTensorInfo:
+        name, t, nd = C.c_char_p(), C.c_uint32(), C.c_uint32()
+        dims, nb, data = (C.c_uint64 * 8)(), C.c_uint64(), C.c_void_p()
+        check(lib().syn_hip_safetensors_tensor_info(self.h, index, C.byref(name), C.byref(t),
+                                                    C.byref(nd), dims, C.byref(nb),
+                                                    C.byref(data)), "tensor_info")
+        return SafetensorsTensorInfo(name.value.decode(), t.value, tuple(dims[:nd.value]),
+                                     nb.value, data.value)
+
+    def names(self):
+        return [self.info(i).name for i in range(len(self))]
+
+    def to_f32(self, index: int) -> np.ndarray:
+        """f32 values as the reference's parse_safetensors converts them."""
+        t = self.info(index)
+        out = np.empty(int(np.prod(t.dims, dtype=np.int64)), np.float32)
+        check(lib().syn_hip_safetensors_to_f32(self.h, index, ptr(out)), "safetensors_to_f32")
+        return out.reshape(t.dims)
+
+    def meta(self, key: str):
+        v = C.c_char_p()
+        return v.value.decode() if lib().syn_hip_safetensors_meta(self.h, key.encode(),
+                                                                   C.byref(v)) == 0 else None
+
+    def q4_pack(self, base: str):
+        """A Q4_0 triple (<base>.q4_nibbles/.q4_scales/.q4_orig_cols) as pack_for_zig bytes."""
+        r, c = SZ(), SZ()
+        check(lib().syn_hip_safetensors_q4_pack(self.h, base.encode(), None, C.byref(r),
+                                                C.byref(c)), "q4_pack")
+        bpr = self.info(self.index(base + ".q4_nibbles")).dims[1]
+        out = np.empty(r.value * bpr * 18, np.uint8)
+        check(lib().syn_hip_safetensors_q4_pack(self.h, base.encode(), ptr(out), C.byref(r),
+                                                C.byref(c)), "q4_pack")
+        return out, r.value, c.value
+
+    def close(self):
+        if self.h:
+            lib().syn_hip_safetensors_close(self.h)
             self.h = None
 
     def __enter__(self):
