@@ -161,6 +161,15 @@ __device__ __forceinline__ float syn_f16_to_f32_rs(uint32_t h) {
   return __uint_as_float(r);
 }
 
+// The same values through the hardware conversion: IEEE f16 -> f32 (exact,
+// f16 denormals are on) halved for subnormal inputs.  No data-dependent
+// control flow, so a pipelined loop keeps precise memory-counter waits; NaN
+// payloads may differ from the bit-built value (a NaN stays a NaN).
+__device__ __forceinline__ float syn_f16_to_f32_rs_hw(uint32_t h) {
+  const float f = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+  return f * ((h & 0x7c00u) == 0 ? 0.5f : 1.0f);
+}
+
 // IEEE f16->f32 (qmatmul.zig:346-371 semantics)
 __device__ __forceinline__ float syn_f16_to_f32_ieee(uint32_t h) {
   const uint32_t sign = (h >> 15) & 1u, exp = (h >> 10) & 0x1fu, mant = h & 0x3ffu;

@@ -2,10 +2,12 @@
 //
 // The reference runs these formats as f32 sgemmTiled over weights
 // dequantized at load (ops/matmul.rs:55-79, matmul.zig:157-183).  Here a
-// workgroup owns a 256 x 128 tile of Y = X W^T and walks K 64 elements at a
-// time: the weight tile is decoded once per workgroup from the HBM plane
-// layout into f16 in LDS (value = the reference dequantizer's f32 value
-// rounded to f16), activations are pre-converted to f16, and
+// workgroup owns a 256 x 256 tile of Y = X W^T (four waves, k_gemm_kq5; used
+// when such tiles cover three quarters of the CUs) or a 256 x 128 tile
+// (twelve waves, k_gemm_kq2, split over K for small grids) and walks K 64
+// elements at a time: the weight tile is decoded once per workgroup from the
+// HBM plane layout into f16 in LDS (value = the reference dequantizer's f32
+// value rounded to f16), activations are pre-converted to f16, and
 // v_mfma_f32_32x32x16_f16 accumulates in f32.  The two f16 roundings
 // (relative 2^-11 each) keep the result well inside the 1e-3 per-row
 // tolerance (measured in the tests).
@@ -90,7 +92,7 @@ __device__ __forceinline__ void pg_decode_w(const RawW &r, int step, int q, int 
                                             uint32_t (&out)[8]) {
   if (FMT == SYN_HIP_FMT_Q8_0) {
     const bool valid = 2 * step + (q >> 1) < B;
-    const float d = valid ? syn_f16_to_f32_rs(r.d) : 0.0f;
+    const float d = valid ? syn_f16_to_f32_rs_hw(r.d) : 0.0f;
     if (EXACT) {
       // every scale of the matrix is an f16 value (checked at upload), and
       // d*q is exact in f32 (11 x 8 significant bits), so rounding it to f16
@@ -123,7 +125,7 @@ __device__ __forceinline__ void pg_decode_w(const RawW &r, int step, int q, int 
     }
   } else if (FMT == SYN_HIP_FMT_Q4_K) {
     const int s = 2 * (step & 3) + (q >> 1);
-    const float d = syn_f16_to_f32_rs(r.q0.x & 0xffffu), dmin = syn_f16_to_f32_rs(r.q0.x >> 16);
+    const float d = syn_f16_to_f32_rs_hw(r.q0.x & 0xffffu), dmin = syn_f16_to_f32_rs_hw(r.q0.x >> 16);
     const uint32_t sbw[3] = {r.q0.y, r.q0.z, r.q0.w};
     auto SB = [&](int i) -> uint32_t { return (sbw[i >> 2] >> (8 * (i & 3))) & 0xffu; };
     // gguf.rs:383-399 for sub-block s (both branches evaluated, one selected)
@@ -144,7 +146,7 @@ __device__ __forceinline__ void pg_decode_w(const RawW &r, int step, int q, int 
     }
   } else {
     const int st = step & 3;
-    const float d = syn_f16_to_f32_rs(r.d);
+    const float d = syn_f16_to_f32_rs_hw(r.d);
     // ql byte (e0+i)/2 = plane byte 8*(q%2) + i/2, nibble i%2; qh byte
     // (e0+i)/4 = plane byte 4q + i/4, bits 2*(i%4); scale (e0+i)/16 = 4st + q
     const int si = 4 * st + q;
@@ -334,6 +336,211 @@ __global__ void __launch_bounds__(PGT2)
     }
 }
 
+// ---------------------------------------------------------------------------
+// 256 x 256 tiles, four waves (one per SIMD), each a 128 x 128 sub-tile: 4 x 4
+// MFMA tiles, 256 f32 accumulators per lane (the accumulation registers of
+// the SIMD, which a single resident wave has to itself).  Per 64-element K
+// step a wave reads 32 KiB of fragments from LDS for 64 MFMAs, half the LDS
+// bytes per multiply-add of 64 x 64 sub-tiles.
+//
+// Fetching: thread i brings row i of the weight tile (every distinct plane of
+// the step once) and eight 16-byte activation chunks.  Two register bundles
+// alternate: iteration t issues the fetch of step t+2 into one bundle at its
+// start, then, between its four k16 rounds of MFMAs, decodes a quarter of
+// step t+1 from the other bundle into the free LDS stage.  The loop has no
+// data-dependent branches, so the memory-counter waits stay exact (the
+// oldest bundle only).
+constexpr int PG3M = 256, PG3N = 256;
+constexpr int PG3_STAGE = (PG3M + PG3N) * PGLD;  // halfs per stage
+
+template <int FMT>
+struct WBundle;
+template <>
+struct WBundle<SYN_HIP_FMT_Q8_0> {  // blocks 2s, 2s+1: planes 0, 1 and scales
+  u32x4 pl[4];
+  uint32_t d[2];  // the dword holding the row's f16 scale (half rp % 2)
+};
+template <>
+struct WBundle<SYN_HIP_FMT_Q4_K> {  // scale plane, sub-block planes 2(s%4), 2(s%4)+1
+  u32x4 sc, pl[2];
+};
+template <>
+struct WBundle<SYN_HIP_FMT_Q6_K> {  // ql planes 2st, 2st+1, qh plane 8+st, scales, d
+  u32x4 ql[2], qh, sc;
+  uint32_t d;  // the dword holding the row's f16 scale (half rp % 2)
+};
+
+// The f16 scales are fetched as the aligned dword holding them (rows 2j and
+// 2j+1): a 16-bit load would be masked right after it arrives, which makes
+// the compiler wait for it at once instead of a step later.
+template <int FMT>
+__device__ __forceinline__ void pg_fetch_w(WBundle<FMT> &w, const u32x4 *__restrict__ W,
+                                           const uint16_t *__restrict__ Wd, int B, int n,
+                                           int step) {
+  const size_t panel = (size_t)(n >> 6), rp = (size_t)(n & 63);
+  const uint32_t *Wd32 = reinterpret_cast<const uint32_t *>(Wd);
+  if constexpr (FMT == SYN_HIP_FMT_Q8_0) {
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const size_t blk = (size_t)min(2 * step + h, B - 1);
+      w.pl[2 * h] = W[((panel * B + blk) * 2 + 0) * 64 + rp];
+      w.pl[2 * h + 1] = W[((panel * B + blk) * 2 + 1) * 64 + rp];
+      w.d[h] = Wd32[((panel * B + blk) * 64 + rp) >> 1];
+    }
+  } else if constexpr (FMT == SYN_HIP_FMT_Q4_K) {
+    const size_t sb = (size_t)(step >> 2);
+    const int sub = 2 * (step & 3);
+    w.sc = W[((panel * B + sb) * 9 + 0) * 64 + rp];
+    w.pl[0] = W[((panel * B + sb) * 9 + 1 + sub) * 64 + rp];
+    w.pl[1] = W[((panel * B + sb) * 9 + 2 + sub) * 64 + rp];
+  } else {
+    const size_t sb = (size_t)(step >> 2);
+    const int st = step & 3;
+    w.ql[0] = W[((panel * B + sb) * 13 + 2 * st) * 64 + rp];
+    w.ql[1] = W[((panel * B + sb) * 13 + 2 * st + 1) * 64 + rp];
+    w.qh = W[((panel * B + sb) * 13 + 8 + st) * 64 + rp];
+    w.sc = W[((panel * B + sb) * 13 + 12) * 64 + rp];
+    w.d = Wd32[((panel * B + sb) * 64 + rp) >> 1];
+  }
+}
+
+// the RawW of quarter q (pg_load_w's view) inside a bundle; odd: row n is odd
+template <int FMT>
+__device__ __forceinline__ RawW pg_quarter(const WBundle<FMT> &w, int q, bool odd) {
+  RawW r;
+  if constexpr (FMT == SYN_HIP_FMT_Q8_0) {
+    r.q0 = w.pl[q];
+    r.d = odd ? w.d[q >> 1] >> 16 : w.d[q >> 1] & 0xffffu;
+  } else if constexpr (FMT == SYN_HIP_FMT_Q4_K) {
+    r.q0 = w.sc;
+    r.q1 = w.pl[q >> 1];
+  } else {
+    r.q0 = w.ql[q >> 1];
+    r.q1 = w.qh;
+    r.q2 = w.sc;
+    r.d = odd ? w.d >> 16 : w.d & 0xffffu;
+  }
+  return r;
+}
+
+template <int FMT>
+struct Fetch {
+  u32x4 a[8];
+  WBundle<FMT> w;
+};
+
+template <int FMT, bool EXACT>
+__global__ void __launch_bounds__(256)
+    k_gemm_kq5(const _Float16 *__restrict__ Xh, int ldh, int M, int K,
+               const u32x4 *__restrict__ W, const uint16_t *__restrict__ Wd, int N, int B,
+               float *__restrict__ Y, int ldy, int steps_per_split) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int n0 = blockIdx.x * PG3N, m0 = blockIdx.y * PG3M;
+  const int s_begin = blockIdx.z * steps_per_split;
+  const int nsteps = min((K + PGK - 1) / PGK - s_begin, steps_per_split);
+  // A: 2048 chunks of 8 halfs per step, eight per thread (row idx/8, idx =
+  // tid + 256 i); W: row tid (clamped)
+  const _Float16 *arow[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    const int idx = tid + i * 256;
+    arow[i] = Xh + (size_t)min(m0 + (idx >> 3), M - 1) * ldh + (idx & 7) * 8;
+  }
+  const int bn = min(n0 + tid, N - 1);
+  auto fetch = [&](Fetch<FMT> &f, int t) {
+    const int step = s_begin + min(t, nsteps - 1);
+#pragma unroll
+    for (int i = 0; i < 8; i++)
+      f.a[i] = *reinterpret_cast<const u32x4 *>(arow[i] + (size_t)step * PGK);
+    pg_fetch_w<FMT>(f.w, W, Wd, B, bn, step);
+  };
+  // part p (0..3) of staging step t: A chunks 2p, 2p+1 and weight quarter p
+  auto stage_part = [&](const Fetch<FMT> &f, int t, int buf, int p) {
+    _Float16 *As = lds + buf * PG3_STAGE, *Bs = As + PG3M * PGLD;
+#pragma unroll
+    for (int i = 2 * p; i < 2 * p + 2; i++) {
+      const int idx = tid + i * 256;
+      *reinterpret_cast<u32x4 *>(&As[(idx >> 3) * PGLD + (idx & 7) * 8]) = f.a[i];
+    }
+    uint32_t wv[8];
+    pg_decode_w<FMT, EXACT>(pg_quarter<FMT>(f.w, p, bn & 1), s_begin + t, p, B, wv);
+    u32x4 *dst = reinterpret_cast<u32x4 *>(&Bs[tid * PGLD + p * 16]);
+    dst[0] = u32x4{wv[0], wv[1], wv[2], wv[3]};
+    dst[1] = u32x4{wv[4], wv[5], wv[6], wv[7]};
+  };
+  const int wm = (wave >> 1) * 128, wn = (wave & 1) * 128;
+  const int l32 = lane & 31, lh = lane >> 5;
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[mt][nt][r] = 0.0f;
+  f16x8 fa[2][4], fb[2][4];
+  auto read = [&](int t, int k16, int b) {
+    const _Float16 *As = lds + (t & 1) * PG3_STAGE, *Bs = As + PG3M * PGLD;
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+      fa[b][mt] = *reinterpret_cast<const f16x8 *>(
+          &As[(wm + mt * 32 + l32) * PGLD + k16 * 16 + lh * 8]);
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++)
+      fb[b][nt] = *reinterpret_cast<const f16x8 *>(
+          &Bs[(wn + nt * 32 + l32) * PGLD + k16 * 16 + lh * 8]);
+  };
+  auto mma = [&](int b) {
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+      for (int nt = 0; nt < 4; nt++)
+        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[b][mt], fb[b][nt], acc[mt][nt],
+                                                             0, 0, 0);
+  };
+  // iteration t: fetch step t+2 into `next`, multiply step t, stage step t+1
+  // from `cur` (the last iterations fetch and stage clamped, in-bounds data
+  // that no one reads)
+  auto iteration = [&](int t, Fetch<FMT> &cur, Fetch<FMT> &next) {
+    fetch(next, t + 2);
+    read(t, 0, 0);
+#pragma unroll
+    for (int k16 = 0; k16 < 4; k16++) {
+      if (k16 < 3) read(t, k16 + 1, (k16 + 1) & 1);
+      mma(k16 & 1);
+      stage_part(cur, t + 1, (t + 1) & 1, k16);
+    }
+    __syncthreads();
+  };
+  Fetch<FMT> f0, f1;
+  fetch(f0, 0);
+  fetch(f1, 1);
+#pragma unroll
+  for (int p = 0; p < 4; p++) stage_part(f0, 0, 0, p);
+  __syncthreads();
+  int t = 0;
+  for (; t + 2 <= nsteps; t += 2) {
+    iteration(t, f1, f0);
+    iteration(t + 1, f0, f1);
+  }
+  if (t < nsteps) iteration(t, f1, f0);
+  const bool atomic = gridDim.z > 1;
+#pragma unroll
+  for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++) {
+      const int n = n0 + wn + nt * 32 + l32;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int m = m0 + wm + mt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+        if (m < M && n < N) {
+          if (atomic) atomicAdd(&Y[(size_t)m * ldy + n], acc[mt][nt][r]);
+          else Y[(size_t)m * ldy + n] = acc[mt][nt][r];
+        }
+      }
+    }
+}
+
 syn_status_t QLinearKQ::gemm(size_t m, const float *d_x, size_t ldx, float *d_y, size_t ldy,
                              hipStream_t s) {
   if (ldx % 4) {
@@ -350,11 +557,18 @@ syn_status_t QLinearKQ::gemm(size_t m, const float *d_x, size_t ldx, float *d_y,
   hipLaunchKernelGGL(k_f32_to_f16, dim3(cdiv(total, 256)), dim3(256), 0, s, d_x, (int)ldx,
                      xh.as<_Float16>(), (int)ldh, (int)m, (int)k);
   SYN_LAUNCH_CHECK();
-  // split K when the tiles alone cannot fill the GPU (>= 8 steps per split)
-  const int tiles_n = (int)cdiv(n, PGN), tiles_m = (int)cdiv(m, PGM);
+  const bool exact = fmt != SYN_HIP_FMT_Q8_0 || q8_scales_f16_exact;
+  const u32x4 *W = wq.as<u32x4>();
+  const uint16_t *Wd = wd.as<uint16_t>();
+  const _Float16 *X = xh.as<_Float16>();
   const int steps = (int)cdiv(k, PGK);
+  // Enough 256 x 256 tiles for three quarters of the CUs: the four-wave
+  // kernel, one K pass per tile.  Fewer: 256 x 128 tiles (twice as many),
+  // split over K when even those cannot fill the GPU.
+  const bool big = cdiv(n, PG3N) * cdiv(m, PG3M) >= 192;
+  const int tiles_n = (int)cdiv(n, big ? PG3N : PGN), tiles_m = (int)cdiv(m, big ? PG3M : PGM);
   int ksplit = 1;
-  if (tiles_n * tiles_m < 256)
+  if (!big && tiles_n * tiles_m < 256)  // >= 8 steps per split
     ksplit = std::max(1, std::min((int)cdiv(384, (size_t)(tiles_n * tiles_m)), steps / 8));
   const int per = (int)cdiv((size_t)steps, (size_t)ksplit);
   ksplit = (int)cdiv((size_t)steps, (size_t)per);
@@ -368,33 +582,38 @@ syn_status_t QLinearKQ::gemm(size_t m, const float *d_x, size_t ldx, float *d_y,
     }
   }
   dim3 grid((unsigned)tiles_n, (unsigned)tiles_m, (unsigned)ksplit);
-  const size_t shm = 2 * (size_t)PG_STAGE * sizeof(_Float16);
-  static bool attr_set[4] = {false, false, false, false};
-  const bool exact = fmt != SYN_HIP_FMT_Q8_0 || q8_scales_f16_exact;
-  const int fi = fmt == SYN_HIP_FMT_Q8_0 ? (exact ? 0 : 3) : fmt == SYN_HIP_FMT_Q4_K ? 1 : 2;
-  const void *fns[4] = {(const void *)k_gemm_kq2<SYN_HIP_FMT_Q8_0, true>,
-                        (const void *)k_gemm_kq2<SYN_HIP_FMT_Q4_K, true>,
-                        (const void *)k_gemm_kq2<SYN_HIP_FMT_Q6_K, true>,
-                        (const void *)k_gemm_kq2<SYN_HIP_FMT_Q8_0, false>};
-  if (!attr_set[fi]) {  // more than the default 64 KiB of dynamic LDS
-    SYN_HIP(hipFuncSetAttribute(fns[fi], hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm));
-    attr_set[fi] = true;
+  const size_t shm = 2 * (size_t)(big ? PG3_STAGE : PG_STAGE) * sizeof(_Float16);
+  const unsigned threads = big ? 256 : PGT2;
+  auto launch = [&](auto kern, bool &attr_set) -> syn_status_t {
+    if (!attr_set) {  // more than the default 64 KiB of dynamic LDS
+      SYN_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  (int)shm));
+      attr_set = true;
+    }
+    hipLaunchKernelGGL(kern, grid, dim3(threads), shm, s, X, (int)ldh, (int)m, (int)k, W, Wd,
+                       (int)n, blocks, d_y, (int)ldy, per);
+    return SYN_OK;
+  };
+  static bool attr[8] = {false, false, false, false, false, false, false, false};
+  if (big) {
+    if (fmt == SYN_HIP_FMT_Q8_0 && exact)
+      SYN_TRY(launch(k_gemm_kq5<SYN_HIP_FMT_Q8_0, true>, attr[0]));
+    else if (fmt == SYN_HIP_FMT_Q8_0)
+      SYN_TRY(launch(k_gemm_kq5<SYN_HIP_FMT_Q8_0, false>, attr[1]));
+    else if (fmt == SYN_HIP_FMT_Q4_K)
+      SYN_TRY(launch(k_gemm_kq5<SYN_HIP_FMT_Q4_K, true>, attr[2]));
+    else
+      SYN_TRY(launch(k_gemm_kq5<SYN_HIP_FMT_Q6_K, true>, attr[3]));
+  } else {
+    if (fmt == SYN_HIP_FMT_Q8_0 && exact)
+      SYN_TRY(launch(k_gemm_kq2<SYN_HIP_FMT_Q8_0, true>, attr[4]));
+    else if (fmt == SYN_HIP_FMT_Q8_0)
+      SYN_TRY(launch(k_gemm_kq2<SYN_HIP_FMT_Q8_0, false>, attr[5]));
+    else if (fmt == SYN_HIP_FMT_Q4_K)
+      SYN_TRY(launch(k_gemm_kq2<SYN_HIP_FMT_Q4_K, true>, attr[6]));
+    else
+      SYN_TRY(launch(k_gemm_kq2<SYN_HIP_FMT_Q6_K, true>, attr[7]));
   }
-  const u32x4 *W = wq.as<u32x4>();
-  const uint16_t *Wd = wd.as<uint16_t>();
-  const _Float16 *X = xh.as<_Float16>();
-  if (fi == 0)
-    hipLaunchKernelGGL((k_gemm_kq2<SYN_HIP_FMT_Q8_0, true>), grid, dim3(PGT2), shm, s, X,
-                       (int)ldh, (int)m, (int)k, W, Wd, (int)n, blocks, d_y, (int)ldy, per);
-  else if (fi == 3)
-    hipLaunchKernelGGL((k_gemm_kq2<SYN_HIP_FMT_Q8_0, false>), grid, dim3(PGT2), shm, s, X,
-                       (int)ldh, (int)m, (int)k, W, Wd, (int)n, blocks, d_y, (int)ldy, per);
-  else if (fi == 1)
-    hipLaunchKernelGGL((k_gemm_kq2<SYN_HIP_FMT_Q4_K, true>), grid, dim3(PGT2), shm, s, X,
-                       (int)ldh, (int)m, (int)k, W, Wd, (int)n, blocks, d_y, (int)ldy, per);
-  else
-    hipLaunchKernelGGL((k_gemm_kq2<SYN_HIP_FMT_Q6_K, true>), grid, dim3(PGT2), shm, s, X,
-                       (int)ldh, (int)m, (int)k, W, Wd, (int)n, blocks, d_y, (int)ldy, per);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
 }

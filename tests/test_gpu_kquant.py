@@ -127,3 +127,23 @@ def test_kquant_gemm_mistral_shape_sampled_rows():
     for i in (0, 1, 255, 511):
         want = deq @ x[i].astype(np.float64)
         assert _rel(got[i], want) <= TOL
+
+
+@pytest.mark.parametrize("name", ["q8_0", "q4_k", "q6_k"])
+def test_kquant_gemm_256x256_tiles(name):
+    # 8 x 24 tiles of 256 x 256 (the four-wave kernel), ragged M and N
+    m, k, n = 2000, 512, 6100
+    rng = np.random.default_rng(11)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    blocks = hip.kquant_encode(FMTS[name], w)
+    lin = hip.QLinear.gguf(FMTS[name], blocks, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    got = lin.forward(x)
+    deq = O.dequant(name, blocks, n * k).reshape(n, k).astype(np.float64)
+    for i in (0, 1, 127, 255, 256, 1024, 1999):
+        want = deq @ x[i].astype(np.float64)
+        assert _rel(got[i], want) <= TOL, i
+    # every output column of one row block, against the f64 product
+    want = x[1792:1800].astype(np.float64) @ deq.T
+    worst = max(_rel(got[1792 + i], want[i]) for i in range(8))
+    assert worst <= TOL, worst
