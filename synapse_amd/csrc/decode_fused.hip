@@ -24,6 +24,7 @@
 // Every float operation is the one of the unfused kernels (layer_ops.hip),
 // which follow the reference's order: the fused step is bit-identical to it.
 #include <algorithm>
+#include <type_traits>
 
 #include "decode_fused.hpp"
 #include "linear.hpp"
@@ -699,269 +700,298 @@ __device__ __forceinline__ float wave_max_any(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
-// Fast form for head_dim % 4 == 0 and <= 128: 8 waves in three roles, each
-// wave's loads requested at kernel entry (at most 48 per wave, inside the 63
-// a wave can have in flight), unconditionally from clamped addresses.
-//  waves 0-3  scores: lane = position 64w + lane of each pass of 256; the K
-//             row comes from the tiled cache as 16-byte loads (1 KiB per wave
-//             load) and stays in registers for the lane's dot-product chain;
-//  waves 4-5  P.V: lane = output column d; V values come 4 positions per
-//             16-byte load, the first 192 positions kept in registers, one
-//             sequential chain over positions per column;
-//  waves 6-7  prologue: lane = d, the q/k/v rows, head norms, RoPE, append.
-// dynamic LDS: qv | kv | vv | sq (hd each) | e[max_seq rounded to 4]
-constexpr int kAttnPass = 256;  // positions per score pass (4 waves x 64)
-constexpr int kPre = 48;        // prefetch registers (float4) per lane
+constexpr int kPre = 48;  // V groups (4 positions each) prefetched into registers
 
-template <bool F32>
-__global__ void __launch_bounds__(512)
-    k_fused_attention_fast(RowSrc qkv, int nh, int nkv, int hd, const float *__restrict__ qn,
-                           const float *__restrict__ kn, float eps,
-                           const float *__restrict__ cosT, const float *__restrict__ sinT,
-                           const uint64_t *exp_tab_g, const StepState *__restrict__ st,
-                           float *__restrict__ kc, float *__restrict__ vc, int max_seq,
-                           float *__restrict__ out) {
-  constexpr int NT = 512;
-  extern __shared__ __align__(16) float sm[];
-  __shared__ float red[64];
-  __shared__ uint64_t exp_tab[32];
-  const int tid = threadIdx.x;
+// ------------------------------------------------------------------ split attention
+// Decode attention for head sizes 16/32/64/128 in two kernels that spread
+// the work of a head over many workgroups (one workgroup per head runs every
+// position's chain and pulls the whole cache of its KV head through one CU).
+//  k_attn_scores      grid (heads, chunks of kScoreP positions): prologue
+//                     (q/k rows, head RMSNorms, RoPE; the chunk holding the
+//                     new position also appends its K/V rows), then one
+//                     dot-product chain per position -> scores[head][p];
+//  k_attn_softmax_pv  grid (heads, groups of kPvCols columns): softmax of the
+//                     head's scores (in every workgroup), then one P.V chain
+//                     per column.
+// Every float operation, and its order, is the one of ops/attention.rs:24-147
+// (the generic k_fused_attention above computes the same values).
+constexpr int kScoreP = 16;  // positions per scores workgroup
+constexpr int kPvCols = 16;  // columns per P.V workgroup
+
+template <bool F32, int HD>
+__global__ void __launch_bounds__(256)
+    k_attn_scores(RowSrc qkv, int nh, int nkv, const float *__restrict__ qn,
+                  const float *__restrict__ kn, float eps, const float *__restrict__ cosT,
+                  const float *__restrict__ sinT, const StepState *__restrict__ st,
+                  float *__restrict__ kc, float *__restrict__ vc, int max_seq,
+                  float *__restrict__ scores) {
+  __shared__ __align__(16) float qv[128], kv[128], sqq[128], sqk[128];
+  __shared__ float red[8];
+  const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lane = tid & 63;
-  const int head = blockIdx.x;
-  const int kvh = head / (nh / nkv);
-  const int qd = nh * hd, kvd = nkv * hd, hd4 = hd >> 2, half = hd >> 1;
-  float *qv = sm, *kv = qv + hd, *vv = kv + hd, *sq = vv + hd;
-  float *e = sq + hd;
+  constexpr int hd = HD, hd4 = HD / 4, half = HD / 2;
+  const int head = blockIdx.x, p0 = blockIdx.y * kScoreP;
+  const int grp = nh / nkv, kvh = head / grp;
+  const int qd = nh * hd, kvd = nkv * hd;
+  const int tiles = (max_seq + 63) >> 6;
   SYN_TS_DECL
   SYN_TS(0);
-  const int pos = st->pos;
-  const int len = pos + 1;
-  const int tiles = (max_seq + 63) >> 6, s4 = (max_seq + 3) >> 2;
-  const float4 *K4 = reinterpret_cast<const float4 *>(kc) + (size_t)kvh * tiles * hd4 * 64;
-  const float4 *V4 = reinterpret_cast<const float4 *>(vc) + (size_t)kvh * s4 * hd;
-  const int ngroups = (len + 3) >> 2;
-  const bool qk_wave = wave < 4;
-  const bool pv_wave = wave == 4 || wave == 5;
-  const int dcol = (wave & 1) * 64 + lane;  // column of P.V and prologue lanes
-  const bool pro_wave = wave >= 6;
+  SYN_TSR(14);
 
-  float4 pre[kPre];
-  auto load_k = [&](int tile) {
-    const float4 *src = K4 + (size_t)min(tile, tiles - 1) * hd4 * 64 + lane;
+  // Loads that do not depend on the decode position are requested before
+  // it is read (a dependent load would wait one memory round trip for it):
+  // waves 0 and 1 (lane = position p0 + lane % kScoreP) the chunk's K rows
+  // from the tiled cache, every thread its q/k/v row values and gain.
+  const int p = p0 + (lane & (kScoreP - 1));
+  float4 pre[hd4];
+  if (wave < 2) {
+    const int pc = min(p, max_seq - 1);
+    const float4 *src = reinterpret_cast<const float4 *>(kc) +
+                        ((size_t)kvh * tiles + (pc >> 6)) * hd4 * 64 + (pc & 63);
 #pragma unroll
-    for (int c = 0; c < 32; c++) pre[c] = src[(size_t)min(c, hd4 - 1) * 64];
-  };
-  int aq = 0, ak = 0, av = 0;
-  float wq = 0.0f, wk = 0.0f, wv = 0.0f, gq = 0.0f, gk = 0.0f, cs = 0.0f, sn = 0.0f, qsx = 0.0f;
-  uint64_t tv = 0;
-  if (qk_wave) {
-    tv = exp_tab_g[lane & 31];
-    load_k(wave);
-  } else if (pv_wave) {
-    const float4 *src = V4 + min(dcol, hd - 1);
-#pragma unroll
-    for (int i = 0; i < kPre; i++) pre[i] = src[(size_t)min(i, ngroups - 1) * hd];
-  } else {
-    const int dc = min(dcol, hd - 1), hc = min(dcol, half - 1);
-    if constexpr (F32) {  // f32 rows: carried in wq/wk/wv
-      wq = qkv.f[head * hd + dc];
-      wk = qkv.f[qd + kvh * hd + dc];
-      wv = qkv.f[qd + kvd + kvh * hd + dc];
-    } else {
-      aq = qkv.acc[head * hd + dc];
-      ak = qkv.acc[qd + kvh * hd + dc];
-      av = qkv.acc[qd + kvd + kvh * hd + dc];
-      wq = qkv.ws[head * hd + dc];
-      wk = qkv.ws[qd + kvh * hd + dc];
-      wv = qkv.ws[qd + kvd + kvh * hd + dc];
-    }
-    gq = qn ? qn[dc] : 0.0f;
-    gk = kn ? kn[dc] : 0.0f;
-    cs = cosT[(size_t)pos * half + hc];
-    sn = sinT[(size_t)pos * half + hc];
-    if constexpr (!F32) qsx = qkv.sx[0];
+    for (int c = 0; c < hd4; c++) pre[c] = src[(size_t)c * 64];
   }
-  asm volatile("" ::: "memory");
+  // threads 0-127 own q[d], threads 128-255 own k[d] and v[d]
+  const bool is_q = tid < 128;
+  const int d = tid & 127;
+  const int dc = min(d, hd - 1), hc = min(d, half - 1);
+  const int r0 = is_q ? head * hd + dc : qd + kvh * hd + dc;
+  const int r1 = qd + kvd + kvh * hd + dc;
+  float x0, x1;
+  if constexpr (F32) {
+    x0 = qkv.f[r0];
+    x1 = qkv.f[r1];
+  } else {
+    const int a0 = qkv.acc[r0], a1 = qkv.acc[r1];
+    const float w0 = qkv.ws[r0], w1 = qkv.ws[r1], sx = qkv.sx[0];
+    float f;
+    f = (float)a0 * sx; x0 = f * w0;
+    f = (float)a1 * sx; x1 = f * w1;
+  }
+  const float *gn = is_q ? qn : kn;
+  const float g = gn ? gn[dc] : 0.0f;
   SYN_TS(1);
 
-  const int d = dcol;
-  const bool pro_lane = pro_wave && d < hd;
-  if (tid < 32) exp_tab[tid] = tv;
-  if (pro_lane) {
-    if constexpr (F32) {
-      qv[d] = wq;
-      kv[d] = wk;
-      vv[d] = wv;
-    } else {
-      float f;
-      f = (float)aq * qsx; qv[d] = f * wq;
-      f = (float)ak * qsx; kv[d] = f * wk;
-      f = (float)av * qsx; vv[d] = f * wv;
-    }
-  }
-  __syncthreads();
+  const int pos = st->pos;
+  const int len = pos + 1;
+  if (p0 >= len) return;
+  const bool has_new = pos < p0 + kScoreP;         // this chunk holds the new position
+  const bool append = has_new && head % grp == 0;  // one writer per KV head
+  const float cs = cosT[(size_t)pos * half + hc], sn = sinT[(size_t)pos * half + hc];
+  float *myv = is_q ? qv : kv;
+  float *mysq = is_q ? sqq : sqk;
+  const bool mine = is_q || has_new;  // k is needed only where the new position is
   SYN_TS(2);
-  // headwise RMSNorm (norm.rs:78-93) of q and k
-  if (qn || kn) {
-    if (pro_lane) {
-      sq[sq_slot(d, hd)] = qv[d] * qv[d];
-      e[sq_slot(d, hd)] = kv[d] * kv[d];  // e is free until the scores
-    }
-    __syncthreads();
-    const float ssq = qn ? sumsq_chains<NT>(sq, hd, red) : 0.0f;
-    __syncthreads();
-    const float ssk = kn ? sumsq_chains<NT>(e, hd, red) : 0.0f;
-    if (pro_lane) {
-      if (qn) {
-        const float scale = 1.0f / sqrtf(ssq / (float)hd + eps);
-        const float t = qv[d] * gq;
-        qv[d] = t * scale;
-      }
-      if (kn) {
-        const float scale = 1.0f / sqrtf(ssk / (float)hd + eps);
-        const float t = kv[d] * gk;
-        kv[d] = t * scale;
-      }
-    }
-    __syncthreads();
-  }
-  SYN_TS(3);
-  // rotate-half RoPE at pos (rope.rs:13-43); lane i < half owns (i, half+i)
-  if (pro_wave && d < half) {
-    {
-      const float x1 = qv[d], x2 = qv[half + d];
-      const float p = x1 * cs, q = x2 * sn, r = x2 * cs, t = x1 * sn;
-      qv[d] = p - q;
-      qv[half + d] = r + t;
-    }
-    {
-      const float x1 = kv[d], x2 = kv[half + d];
-      const float p = x1 * cs, q = x2 * sn, r = x2 * cs, t = x1 * sn;
-      kv[d] = p - q;
-      kv[half + d] = r + t;
-    }
+  if (d < hd) {
+    myv[d] = x0;
+    mysq[sq_slot(d, hd)] = x0 * x0;
   }
   __syncthreads();
-  if (pro_lane) {
-    kc[kv_k_index(pos, kvh, d, hd, max_seq)] = kv[d];
-    vc[kv_v_index(pos, kvh, d, hd, max_seq)] = vv[d];
+  SYN_TS(3);
+  // head RMSNorms (norm.rs:78-93): the q chains on wave 0, the k chains on
+  // wave 2, at the same time
+  if (lane < 4) {
+    if (wave == 0 && qn) red[lane] = sumsq_chain(sqq, hd, lane);
+    if (wave == 2 && kn && has_new) red[4 + lane] = sumsq_chain(sqk, hd, lane);
   }
+  __syncthreads();
   SYN_TS(4);
+  if (gn && mine && d < hd) {
+    const float ss = sumsq_combine(red + (is_q ? 0 : 4), mysq, hd);
+    const float scale = 1.0f / sqrtf(ss / (float)hd + eps);
+    const float t = myv[d] * g;
+    myv[d] = t * scale;
+  }
+  __syncthreads();
+  // rotate-half RoPE at pos (rope.rs:13-43); lane i < half owns (i, half+i)
+  if (mine && d < half) {
+    const float a = myv[d], b = myv[half + d];
+    const float pp = a * cs, qq = b * sn, rr = b * cs, tt = a * sn;
+    myv[d] = pp - qq;
+    myv[half + d] = rr + tt;
+  }
+  __syncthreads();
+  if (append && !is_q && d < hd) {
+    kc[kv_k_index(pos, kvh, d, hd, max_seq)] = kv[d];
+    vc[kv_v_index(pos, kvh, d, hd, max_seq)] = x1;
+  }
+  SYN_TS(5);
 
-  // scores (waves 0-3): the lane of position pos takes its K row from LDS,
-  // its prefetched row predates the append
-  const float scale = 1.0f / sqrtf((float)hd);
+  // scores: the positions below n8 take fused multiply-add chains (wave 0),
+  // the others plain ones (wave 1), as f32GemvRow's column blocks do.  Each
+  // wave runs its chain for all 64 lanes without branches (q comes from LDS
+  // as broadcast reads, which the compiler issues ahead of the chain) and
+  // stores the positions of its kind.
   const bool simd = len >= 64;
   const int n32 = len - len % 32;
   const int n8 = n32 + ((len - n32) / 8) * 8;
-  float mx = -__builtin_inff();
-  if (qk_wave) {
+  const bool fused_wave = wave == 0 && simd && p0 < n8;
+  const bool plain_wave = wave == 1 && (!simd || p0 + kScoreP > n8);
+  if (fused_wave || plain_wave) {
+    const float scale = 1.0f / sqrtf((float)hd);
+    const float4 *q4 = reinterpret_cast<const float4 *>(qv);
+    // the lane of position pos takes the new K row from LDS (a select, no branch)
+    const bool is_new = p == pos;
     const float4 *k4 = reinterpret_cast<const float4 *>(kv);
-    // q in two VGPRs (lane d holds q[d] and q[64+d]); the chains take q[d]
-    // through v_readlane as a scalar operand, so no LDS read sits on them
-    const float qa = qv[min(lane, hd - 1)], qb = qv[min(64 + lane, hd - 1)];
-    auto qd = [&](int d) -> float {
-      return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(d < 64 ? qa : qb), d & 63));
-    };
-    for (int p0 = 0; p0 < len; p0 += kAttnPass) {
-      if (p0 > 0) load_k((p0 >> 6) + wave);
-      const int p = p0 + wave * 64 + lane;
-      if (p == pos) {
 #pragma unroll
-        for (int c = 0; c < 32; c++)
-          if (c < hd4) pre[c] = k4[c];
-      }
-      if (p < len) {
-        float acc = 0.0f;
-        if (simd && p < n8) {
-#pragma unroll
-          for (int c = 0; c < 32; c++) {
-            if (c < hd4) {
-              acc = __builtin_fmaf(qd(4 * c), pre[c].x, acc);
-              acc = __builtin_fmaf(qd(4 * c + 1), pre[c].y, acc);
-              acc = __builtin_fmaf(qd(4 * c + 2), pre[c].z, acc);
-              acc = __builtin_fmaf(qd(4 * c + 3), pre[c].w, acc);
-            }
-          }
-        } else {
-#pragma unroll
-          for (int c = 0; c < 32; c++) {
-            if (c < hd4) {
-              float t;
-              t = qd(4 * c) * pre[c].x; acc = acc + t;
-              t = qd(4 * c + 1) * pre[c].y; acc = acc + t;
-              t = qd(4 * c + 2) * pre[c].z; acc = acc + t;
-              t = qd(4 * c + 3) * pre[c].w; acc = acc + t;
-            }
-          }
-        }
-        const float sc = acc * scale;
-        e[p] = sc;
-        mx = fmaxf(mx, sc);
-      }
+    for (int c = 0; c < hd4; c++) {
+      const float4 kn4 = k4[c];
+      pre[c].x = is_new ? kn4.x : pre[c].x;
+      pre[c].y = is_new ? kn4.y : pre[c].y;
+      pre[c].z = is_new ? kn4.z : pre[c].z;
+      pre[c].w = is_new ? kn4.w : pre[c].w;
     }
-    mx = wave_max_any(mx);
-    if (lane == 0) red[wave] = mx;
-  }
-  SYN_TS(5);
-  __syncthreads();
-  // softmax_slice (activation.rs:117-129)
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  for (int sidx = tid; sidx < len; sidx += NT) e[sidx] = syn_expf_tab(e[sidx] - mx, exp_tab);
-  __syncthreads();
-  if (tid == 0) red[40] = seq_sum(e, len);
-  __syncthreads();
-  const float sum = red[40];
-  if (sum > 0.0f)
-    for (int sidx = tid; sidx < len; sidx += NT) e[sidx] = e[sidx] / sum;
-  __syncthreads();
-  SYN_TS(6);
-
-  // P.V (waves 4-5): one chain over positions per output column; the new
-  // position's value comes from LDS
-  if (pv_wave && d < hd) {
-    const int d32 = hd - hd % 32;
-    const bool fused = simd && d < d32;
-    const float vnew = vv[d];
-    const float4 *e4 = reinterpret_cast<const float4 *>(e);
     float acc = 0.0f;
-    auto chain4 = [&](int g, float4 v) {
-      const float4 ev = e4[g];
-      const int p = 4 * g;
-      const float v0 = p + 0 == pos ? vnew : v.x, v1 = p + 1 == pos ? vnew : v.y;
-      const float v2 = p + 2 == pos ? vnew : v.z, v3 = p + 3 == pos ? vnew : v.w;
-      if (fused) {
-        if (p + 0 < len) acc = __builtin_fmaf(ev.x, v0, acc);
-        if (p + 1 < len) acc = __builtin_fmaf(ev.y, v1, acc);
-        if (p + 2 < len) acc = __builtin_fmaf(ev.z, v2, acc);
-        if (p + 3 < len) acc = __builtin_fmaf(ev.w, v3, acc);
-      } else {
-        float t;
-        if (p + 0 < len) { t = ev.x * v0; acc = acc + t; }
-        if (p + 1 < len) { t = ev.y * v1; acc = acc + t; }
-        if (p + 2 < len) { t = ev.z * v2; acc = acc + t; }
-        if (p + 3 < len) { t = ev.w * v3; acc = acc + t; }
+    if (fused_wave) {
+#pragma unroll
+      for (int c = 0; c < hd4; c++) {
+        const float4 qc = q4[c];
+        acc = __builtin_fmaf(qc.x, pre[c].x, acc);
+        acc = __builtin_fmaf(qc.y, pre[c].y, acc);
+        acc = __builtin_fmaf(qc.z, pre[c].z, acc);
+        acc = __builtin_fmaf(qc.w, pre[c].w, acc);
       }
-    };
+    } else {
 #pragma unroll
-    for (int g = 0; g < kPre; g++)
-      if (g < ngroups) chain4(g, pre[g]);
-    for (int g0 = kPre; g0 < ngroups; g0 += 16) {  // beyond the prefetched groups
-      float4 vb[16];
-#pragma unroll
-      for (int k = 0; k < 16; k++) vb[k] = V4[(size_t)min(g0 + k, ngroups - 1) * hd + d];
-#pragma unroll
-      for (int k = 0; k < 16; k++)
-        if (g0 + k < ngroups) chain4(g0 + k, vb[k]);
+      for (int c = 0; c < hd4; c++) {
+        const float4 qc = q4[c];
+        float t;
+        t = qc.x * pre[c].x; acc = acc + t;
+        t = qc.y * pre[c].y; acc = acc + t;
+        t = qc.z * pre[c].z; acc = acc + t;
+        t = qc.w * pre[c].w; acc = acc + t;
+      }
     }
-    out[head * hd + d] = acc;
+    SYN_TS(6);
+    const bool mine_p = fused_wave == (simd && p < n8);
+    if (lane < kScoreP && p < len && mine_p) scores[(size_t)head * max_seq + p] = acc * scale;
   }
   SYN_TS(7);
+  SYN_TSR(15);
   SYN_TS_FLUSH(48);
 }
 
-static bool attention_fast_ok(int hd) { return hd % 4 == 0 && hd <= 128; }
+// softmax_slice (activation.rs:117-129) of the head's scores, then P.V for
+// kPvCols columns; dynamic LDS: e[max_seq rounded to 4]
+__global__ void __launch_bounds__(256)
+    k_attn_softmax_pv(int nh, int nkv, int hd, const uint64_t *exp_tab_g,
+                      const StepState *__restrict__ st, const float *__restrict__ vc, int max_seq,
+                      const float *__restrict__ scores, float *__restrict__ out) {
+  constexpr int NT = 256;
+  extern __shared__ __align__(16) float e[];
+  __shared__ float red[64];
+  __shared__ uint64_t exp_tab[32];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int head = blockIdx.x, kvh = head / (nh / nkv);
+  const int s4 = (max_seq + 3) >> 2;
+  const float4 *V4 = reinterpret_cast<const float4 *>(vc) + (size_t)kvh * s4 * hd;
+  const int d = blockIdx.y * kPvCols + (lane & (kPvCols - 1));
+  const int dcl = min(d, hd - 1);
+  // Loads that do not depend on the decode position first (wave 0: V of
+  // this workgroup's columns, 4 positions per 16-byte load; every thread the
+  // score of position tid and its expf table word), then the position.
+  float4 pre[kPre];
+  if (wave == 0) {
+#pragma unroll
+    for (int i = 0; i < kPre; i++) pre[i] = V4[(size_t)min(i, s4 - 1) * hd + dcl];
+  }
+  const uint64_t tv = exp_tab_g[tid & 31];
+  const float *sh = scores + (size_t)head * max_seq;
+  const float s0 = sh[min(tid, max_seq - 1)];
+  SYN_TS_DECL
+  SYN_TS(0);
+  SYN_TSR(14);
+  const int pos = st->pos;
+  const int len = pos + 1, ngroups = (len + 3) >> 2;
+  float mx = -__builtin_inff();
+  if (tid < len) {
+    e[tid] = s0;
+    mx = s0;
+  }
+  for (int i = tid + NT; i < len; i += NT) {
+    const float v = sh[i];
+    e[i] = v;
+    mx = fmaxf(mx, v);
+  }
+  if (tid < 32) exp_tab[tid] = tv;
+  SYN_TS(1);
+  mx = wave_max_any(mx);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  SYN_TS(2);
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  for (int i = tid; i < len; i += NT) e[i] = syn_expf_tab(e[i] - mx, exp_tab);
+  __syncthreads();
+  SYN_TS(3);
+  // the sequential sum of the exponentials (thread 0), then the division
+  if (tid == 0) red[40] = seq_sum_pipelined(e, len);
+  __syncthreads();
+  SYN_TS(4);
+  const float sum = red[40];
+  if (sum > 0.0f)
+    for (int i = tid; i < len; i += NT) e[i] = e[i] / sum;
+  __syncthreads();
+  SYN_TS(5);
+  if (wave != 0) return;
+
+  // P.V (wave 0, lane = column; lanes >= kPvCols repeat the first kPvCols
+  // columns and store nothing): one chain over the positions per column,
+  // fused multiply-adds on the len >= 64 route for columns inside whole
+  // 32-column blocks (all columns of these head sizes), plain ones
+  // otherwise.  Positions go in blocks of 16 behind one wave-uniform branch
+  // each; inside a block the probabilities are LDS broadcast reads issued
+  // ahead of the chain and positions past the end are dropped by selects.
+  const float4 *e4 = reinterpret_cast<const float4 *>(e);
+  auto chain = [&](auto fused_t) {
+    constexpr bool F = decltype(fused_t)::value;
+    float acc = 0.0f;
+    auto step = [&](bool valid, float ev, float v) {
+      if constexpr (F) {
+        const float r = __builtin_fmaf(ev, v, acc);
+        acc = valid ? r : acc;
+      } else {
+        const float t = ev * v;
+        const float r = acc + t;
+        acc = valid ? r : acc;
+      }
+    };
+    auto block = [&](int g0, const float4 (&vb)[4]) {
+      float4 eb[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) eb[k] = e4[min(g0 + k, s4 - 1)];
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const int q = 4 * (g0 + k);
+        step(q + 0 < len, eb[k].x, vb[k].x);
+        step(q + 1 < len, eb[k].y, vb[k].y);
+        step(q + 2 < len, eb[k].z, vb[k].z);
+        step(q + 3 < len, eb[k].w, vb[k].w);
+      }
+    };
+#pragma unroll
+    for (int b = 0; b < kPre / 4; b++) {
+      if (4 * b < ngroups) {
+        const float4 vb[4] = {pre[4 * b], pre[4 * b + 1], pre[4 * b + 2], pre[4 * b + 3]};
+        block(4 * b, vb);
+      }
+    }
+    for (int g0 = kPre; g0 < ngroups; g0 += 4) {  // beyond the prefetched groups
+      float4 vb[4];
+#pragma unroll
+      for (int k = 0; k < 4; k++) vb[k] = V4[(size_t)min(g0 + k, s4 - 1) * hd + dcl];
+      block(g0, vb);
+    }
+    return acc;
+  };
+  const float acc = len >= 64 && hd % 32 == 0 ? chain(std::true_type{}) : chain(std::false_type{});
+  if (lane < kPvCols && d < hd) out[head * hd + d] = acc;
+  SYN_TS(6);
+  SYN_TSR(15);
+  SYN_TS_FLUSH(64);
+}
+
+static bool attention_fast_ok(int hd) { return hd == 16 || hd == 32 || hd == 64 || hd == 128; }
 
 static size_t attention_lds_bytes(int hd, int max_seq) {
   return ((size_t)4 * hd + round_up((size_t)max_seq, 4)) * sizeof(float);
@@ -974,7 +1004,7 @@ bool fused_attention_fits(int hd, int max_seq) {
 syn_status_t launch_fused_attention(RowSrc qkv, int nh, int nkv, int hd, const float *qn,
                                     const float *kn, float eps, const float *cosT,
                                     const float *sinT, const StepState *st, float *kc, float *vc,
-                                    int max_seq, float *out, hipStream_t s) {
+                                    int max_seq, float *scores, float *out, hipStream_t s) {
   if (!fused_attention_fits(hd, max_seq)) {
     set_error("fused decode attention: max_seq too long for LDS");
     return SYN_ERR_INVALID_ARG;
@@ -986,12 +1016,26 @@ syn_status_t launch_fused_attention(RowSrc qkv, int nh, int nkv, int hd, const f
       set_error("fused decode: expf table address unavailable");
       return SYN_ERR_HIP;
     }
-    if (qkv.f)
-      hipLaunchKernelGGL(k_fused_attention_fast<true>, dim3(nh), dim3(512), shm, s, qkv, nh, nkv,
-                         hd, qn, kn, eps, cosT, sinT, tab, st, kc, vc, max_seq, out);
-    else
-      hipLaunchKernelGGL(k_fused_attention_fast<false>, dim3(nh), dim3(512), shm, s, qkv, nh, nkv,
-                         hd, qn, kn, eps, cosT, sinT, tab, st, kc, vc, max_seq, out);
+    const dim3 sgrid((unsigned)nh, (unsigned)cdiv((size_t)max_seq, (size_t)kScoreP));
+    auto scores_kernel = [&](auto hdc) {
+      constexpr int H = decltype(hdc)::value;
+      if (qkv.f)
+        hipLaunchKernelGGL((k_attn_scores<true, H>), sgrid, dim3(256), 0, s, qkv, nh, nkv, qn, kn,
+                           eps, cosT, sinT, st, kc, vc, max_seq, scores);
+      else
+        hipLaunchKernelGGL((k_attn_scores<false, H>), sgrid, dim3(256), 0, s, qkv, nh, nkv, qn,
+                           kn, eps, cosT, sinT, st, kc, vc, max_seq, scores);
+    };
+    switch (hd) {
+      case 16: scores_kernel(std::integral_constant<int, 16>{}); break;
+      case 32: scores_kernel(std::integral_constant<int, 32>{}); break;
+      case 64: scores_kernel(std::integral_constant<int, 64>{}); break;
+      default: scores_kernel(std::integral_constant<int, 128>{}); break;
+    }
+    SYN_LAUNCH_CHECK();
+    const size_t eshm = round_up((size_t)max_seq, 4) * sizeof(float);
+    hipLaunchKernelGGL(k_attn_softmax_pv, dim3((unsigned)nh, (unsigned)cdiv((size_t)hd, (size_t)kPvCols)),
+                       dim3(256), eshm, s, nh, nkv, hd, tab, st, vc, max_seq, scores, out);
   } else {
     hipLaunchKernelGGL(k_fused_attention, dim3(nh), dim3(256), shm, s, qkv, nh, nkv, hd, qn, kn,
                        eps, cosT, sinT, st, kc, vc, max_seq, out);

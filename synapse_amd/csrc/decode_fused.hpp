@@ -73,11 +73,12 @@ syn_status_t launch_fused_quant_gemv(const float *vec, int H, float *s_out, cons
 syn_status_t launch_fused_swiglu_gemv(RowSrc gu, int inter, float *s_out, const SplitGemv &g,
                                       hipStream_t s);
 // per query head: q/k/v rows from the QKV partials, head RMSNorm, RoPE at
-// state->pos, KV append, attention over positions [0, pos]
+// state->pos, KV append, attention over positions [0, pos]; scores is
+// [nh][max_seq] f32 scratch
 syn_status_t launch_fused_attention(RowSrc qkv, int nh, int nkv, int hd, const float *qn,
                                     const float *kn, float eps, const float *cosT,
                                     const float *sinT, const StepState *st, float *kc, float *vc,
-                                    int max_seq, float *out, hipStream_t s);
+                                    int max_seq, float *scores, float *out, hipStream_t s);
 bool fused_attention_fits(int hd, int max_seq);
 // the fused GEMV prologue holds its activation row (f32 twice + int8) in LDS
 bool fused_gemv_fits(int H);

@@ -153,7 +153,7 @@ struct syn_hip_klm_s {
       src.f = qkv.as<float>();
       SYN_TRY(launch_fused_attention(src, nh, nkv, (int)hd, qn, kn, eps, rope_cos.as<float>(),
                                      rope_sin.as<float>(), st(), kc_l(l), vc_l(l), (int)S,
-                                     attn.as<float>(), s));
+                                     scores.as<float>(), attn.as<float>(), s));
     } else {
       SYN_TRY(launch_qk_norm_rope_kv(qkv.as<float>(), (int)n_qkv, rows, nh, nkv, (int)hd, qn, kn,
                                      eps, rope_cos.as<float>(), rope_sin.as<float>(),

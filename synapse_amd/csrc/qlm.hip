@@ -266,7 +266,7 @@ struct syn_hip_qlm_s {
       SYN_TRY(launch_fused_attention(Ly.f_qkv.rows(s_qkv), nh, nkv, (int)hd, qn(l), kn(l), eps,
                                      rope_cos.as<float>(),
                                      rope_sin.as<float>(), st(), kc_l(l), vc_l(l), (int)S,
-                                     attn.as<float>(), s));
+                                     scores.as<float>(), attn.as<float>(), s));
       SYN_TRY(launch_fused_quant_gemv(attn.as<float>(), (int)qd, s_o, Ly.f_o, s));
       SYN_TRY(launch_fused_norm_gemv(xin.as<float>(), nullptr, st(), (int)vocab, nullptr,
                                      Ly.f_o.rows(s_o), xmid.as<float>(), fn(l), eps,
