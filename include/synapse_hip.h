@@ -168,6 +168,32 @@ typedef struct {
   double rope_theta;
 } syn_hip_lm_config;
 
+/* -- Sampling (generation/sampler.rs) -------------------------------------- */
+/* CombinedSampler (sampler.rs:152-157): repetition penalty -> temperature ->
+ * top-k -> top-p -> softmax + categorical draw.  temperature <= 0 or
+ * top_k == 1: argmax; top_k == 0 or >= vocab: no top-k; top_p outside
+ * (0, 1): no top-p; repetition_penalty within f32::EPSILON of 1: none. */
+typedef struct {
+  float temperature;
+  uint32_t top_k;
+  float top_p;
+  float repetition_penalty;
+} syn_hip_sampler;
+/* CombinedSampler::sample_with_history (sampler.rs:161-201) on the device:
+ * d_logits f32 [vocab] (not modified), d_history the generated tokens
+ * [n_history], u the draw rng.gen::<f32>() the reference would take.  The
+ * token goes to d_token (device), asynchronously on `stream`.  d_status
+ * (device, nullable) gets 0, or 1 when top-p would have to sort more than
+ * 4096 candidates (top-p without top-k over a large vocabulary; the token is
+ * then 0).  No counterpart in the reference's C ABI (sampling runs in Rust
+ * there). */
+syn_status_t syn_hip_sample(const float *d_logits, size_t vocab, const uint32_t *d_history,
+                            size_t n_history, const syn_hip_sampler *params, float u,
+                            uint32_t *d_token, int *d_status, void *stream);
+/* The first n draws of StdRng::seed_from_u64(seed).gen::<f32>() (rand 0.8.5;
+ * host computation). */
+syn_status_t syn_hip_stdrng_f32(uint64_t seed, size_t n, float *out);
+
 typedef struct syn_hip_qlm_s syn_hip_qlm_t;
 syn_status_t syn_hip_qlm_create(const syn_hip_lm_config *cfg, syn_hip_qlm_t **out);
 /* embed_tokens [vocab, hidden] f32 (tied: the lm_head is quantized from it) */
@@ -230,6 +256,14 @@ syn_status_t syn_hip_qlm_time_lm_head_rotating(syn_hip_qlm_t *m, size_t iters, f
  * graph_replay = 1 (default): each decode step is a replayed HIP graph; 0:
  * kernels are launched eagerly (for profilers that cannot follow graphs). */
 syn_status_t syn_hip_qlm_set_options(syn_hip_qlm_t *m, int fused_decode, int graph_replay);
+/* Sampling for generate / decode steps: the CombinedSampler of
+ * generation/sampler.rs:152-201 (NULL params: greedy, the default), with the
+ * draws of StdRng::seed_from_u64(seed) (pipeline.rs:162-165).  The draws are
+ * generated on the host at this call and uploaded once; every step samples
+ * on the device.  The margin history then holds the chosen token's
+ * probability (0 on the greedy route). */
+syn_status_t syn_hip_qlm_set_sampler(syn_hip_qlm_t *m, const syn_hip_sampler *params,
+                                     uint64_t seed);
 syn_status_t syn_hip_qlm_destroy(syn_hip_qlm_t *m);
 
 /* -- GGUF files (weight_loading/gguf.rs:49-151, 551-591): a read-only

@@ -85,6 +85,14 @@ def _declare(L):
         "orc_expf": (C.c_float, [C.c_float]),
         "orc_softmax_slice": (None, [P, SZ]),
         "orc_argmax": (C.c_uint32, [P, SZ]),
+        "orc_repetition_penalty": (None, [P, SZ, P, SZ, C.c_float]),
+        "orc_softmax_inplace": (None, [P, SZ]),
+        "orc_top_k_filter": (None, [P, SZ, SZ]),
+        "orc_top_p_filter": (None, [P, SZ, C.c_float]),
+        "orc_sample_combined": (C.c_uint32, [P, SZ, P, SZ, C.c_float, SZ, C.c_float, C.c_float,
+                                             C.c_float]),
+        "orc_chacha_block": (None, [P, C.c_uint64, C.c_uint64, C.c_int, P]),
+        "orc_stdrng_f32": (None, [C.c_uint64, SZ, P]),
         "orc_attention_decode": (None, [P, P, P, SZ, SZ, SZ, SZ, P]),
         "orc_fused_attention": (C.c_int, [SZ, SZ, SZ, P, P, P, P]),
         "orc_qlm_create": (P, [C.POINTER(LmCfg)]),
@@ -266,6 +274,60 @@ def rope_tables(max_pos: int, head_dim: int, base: float):
 def argmax(x: np.ndarray) -> int:
     x = np.ascontiguousarray(x, np.float32)
     return int(lib().orc_argmax(_p(x), x.size))
+
+
+# ---------------------------------------------------------------- sampling
+def repetition_penalty(logits: np.ndarray, history, penalty: float) -> np.ndarray:
+    x = np.array(logits, np.float32, copy=True)
+    h = np.ascontiguousarray(history, np.uint32)
+    lib().orc_repetition_penalty(_p(x), x.size, _p(h), h.size, penalty)
+    return x
+
+
+def softmax(logits: np.ndarray) -> np.ndarray:
+    x = np.array(logits, np.float32, copy=True)
+    lib().orc_softmax_inplace(_p(x), x.size)
+    return x
+
+
+def top_k_filter(logits: np.ndarray, k: int) -> np.ndarray:
+    x = np.array(logits, np.float32, copy=True)
+    lib().orc_top_k_filter(_p(x), x.size, k)
+    return x
+
+
+def top_p_filter(logits: np.ndarray, p: float) -> np.ndarray:
+    x = np.array(logits, np.float32, copy=True)
+    lib().orc_top_p_filter(_p(x), x.size, p)
+    return x
+
+
+def sample_combined(logits: np.ndarray, history=(), temperature: float = 1.0, top_k: int = 0,
+                    top_p: float = 1.0, repetition_penalty: float = 1.0, u: float = 0.5) -> int:
+    """CombinedSampler::sample_with_history with the uniform draw u given."""
+    x = np.array(logits, np.float32, copy=True)
+    h = np.ascontiguousarray(np.asarray(history, np.uint32).reshape(-1))
+    if h.size == 0:
+        h = np.zeros(1, np.uint32)
+        nh = 0
+    else:
+        nh = h.size
+    return int(lib().orc_sample_combined(_p(x), x.size, _p(h), nh, temperature, top_k, top_p,
+                                         repetition_penalty, u))
+
+
+def chacha_block(key, counter: int, stream: int, rounds: int) -> np.ndarray:
+    k = np.ascontiguousarray(key, np.uint32)
+    out = np.zeros(16, np.uint32)
+    lib().orc_chacha_block(_p(k), counter, stream, rounds, _p(out))
+    return out
+
+
+def stdrng_f32(seed: int, n: int) -> np.ndarray:
+    """The first n draws of StdRng::seed_from_u64(seed).gen::<f32>()."""
+    out = np.zeros(n, np.float32)
+    lib().orc_stdrng_f32(seed, n, _p(out))
+    return out
 
 
 def expf(x: float) -> float:

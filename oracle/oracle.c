@@ -26,6 +26,7 @@
  */
 #include "oracle.h"
 
+#include <float.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -1529,4 +1530,195 @@ int orc_mamba_generate(orc_mamba *m, const uint32_t *prompt, size_t n_prompt, si
   }
   free(logits);
   return ORC_OK;
+}
+
+/* ======================================================================
+ * Sampling (generation/sampler.rs) and the random stream that feeds it.
+ * ====================================================================== */
+
+/* RepetitionPenalty::apply (sampler.rs:130-149): every occurrence in the
+ * history divides a positive logit by the penalty or multiplies a
+ * non-positive one, in history order. */
+void orc_repetition_penalty(float *logits, size_t n, const uint32_t *hist, size_t nh,
+                            float penalty) {
+  if (fabsf(penalty - 1.0f) < FLT_EPSILON) return;
+  for (size_t i = 0; i < nh; i++) {
+    const size_t idx = hist[i];
+    if (idx < n) {
+      if (logits[idx] > 0.0f) logits[idx] /= penalty;
+      else logits[idx] *= penalty;
+    }
+  }
+}
+
+/* f32::max fold from -inf (sampler.rs:234, 275-278): NaN-ignoring */
+static float max_fold(const float *x, size_t n) {
+  float m = -INFINITY;
+  for (size_t i = 0; i < n; i++) m = fmaxf(m, x[i]);
+  return m;
+}
+
+/* softmax_inplace (sampler.rs:233-245): exp(l - max), sequential sum in index
+ * order, division when the sum is positive */
+void orc_softmax_inplace(float *x, size_t n) {
+  const float mx = max_fold(x, n);
+  float sum = 0.0f;
+  for (size_t i = 0; i < n; i++) {
+    x[i] = expf(x[i] - mx);
+    sum += x[i];
+  }
+  if (sum > 0.0f)
+    for (size_t i = 0; i < n; i++) x[i] /= sum;
+}
+
+static int cmp_desc_f32(const void *a, const void *b) {
+  const float x = *(const float *)a, y = *(const float *)b;
+  return x > y ? -1 : x < y ? 1 : 0;
+}
+
+/* top_k_filter (sampler.rs:262-276): the k-th largest value is the
+ * threshold, every logit below it becomes -inf */
+void orc_top_k_filter(float *logits, size_t n, size_t k) {
+  if (k > n) k = n;
+  if (k == 0) return;
+  float *s = (float *)malloc(n * sizeof(float));
+  memcpy(s, logits, n * sizeof(float));
+  qsort(s, n, sizeof(float), cmp_desc_f32);
+  const float thr = s[k - 1];
+  free(s);
+  for (size_t i = 0; i < n; i++)
+    if (logits[i] < thr) logits[i] = -INFINITY;
+}
+
+typedef struct {
+  float p;
+  uint32_t i;
+} orc_prob_idx;
+
+/* probabilities descending; equal probabilities by index ascending (the
+ * reference's unstable sort leaves their order unspecified) */
+static int cmp_prob_desc(const void *a, const void *b) {
+  const orc_prob_idx *x = (const orc_prob_idx *)a, *y = (const orc_prob_idx *)b;
+  if (x->p > y->p) return -1;
+  if (x->p < y->p) return 1;
+  return x->i < y->i ? -1 : x->i > y->i ? 1 : 0;
+}
+
+/* top_p_filter (sampler.rs:279-319): softmax, sort by probability
+ * descending, keep tokens until the cumulative probability reaches p */
+void orc_top_p_filter(float *logits, size_t n, float p) {
+  orc_prob_idx *pr = (orc_prob_idx *)malloc(n * sizeof(orc_prob_idx));
+  float *v = (float *)malloc(n * sizeof(float));
+  memcpy(v, logits, n * sizeof(float));
+  orc_softmax_inplace(v, n);
+  for (size_t i = 0; i < n; i++) {
+    pr[i].p = v[i];
+    pr[i].i = (uint32_t)i;
+  }
+  qsort(pr, n, sizeof(orc_prob_idx), cmp_prob_desc);
+  unsigned char *keep = (unsigned char *)calloc(n, 1);
+  float cum = 0.0f;
+  for (size_t j = 0; j < n; j++) {
+    keep[pr[j].i] = 1;
+    cum += pr[j].p;
+    if (cum >= p) break;
+  }
+  for (size_t i = 0; i < n; i++)
+    if (!keep[i]) logits[i] = -INFINITY;
+  free(keep);
+  free(v);
+  free(pr);
+}
+
+/* categorical_sample (sampler.rs:248-259) with the uniform draw u given */
+static uint32_t categorical(const float *probs, size_t n, float u) {
+  float cum = 0.0f;
+  for (size_t i = 0; i < n; i++) {
+    cum += probs[i];
+    if (u < cum) return (uint32_t)i;
+  }
+  return (uint32_t)(n - 1);
+}
+
+/* CombinedSampler::sample_with_history (sampler.rs:161-201): repetition
+ * penalty -> temperature -> top-k -> top-p -> softmax + categorical draw.
+ * logits are modified in place as in the reference; u is the draw
+ * rng.gen::<f32>() the reference would take (used only on the sampling
+ * route). */
+uint32_t orc_sample_combined(float *logits, size_t n, const uint32_t *hist, size_t nh,
+                             float temperature, size_t top_k, float top_p, float rep_penalty,
+                             float u) {
+  if (fabsf(rep_penalty - 1.0f) > FLT_EPSILON)
+    orc_repetition_penalty(logits, n, hist, nh, rep_penalty);
+  if (temperature <= 0.0f) return orc_argmax(logits, n);
+  const float inv_t = 1.0f / temperature;
+  for (size_t i = 0; i < n; i++) logits[i] *= inv_t;
+  if (top_k > 0 && top_k < n) {
+    if (top_k == 1) return orc_argmax(logits, n);
+    orc_top_k_filter(logits, n, top_k);
+  }
+  if (top_p > 0.0f && top_p < 1.0f) orc_top_p_filter(logits, n, top_p);
+  orc_softmax_inplace(logits, n);
+  return categorical(logits, n, u);
+}
+
+/* ---- the random stream: rand 0.8.5 StdRng = rand_chacha 0.3.1 ChaCha12Rng,
+ * seeded by rand_core 0.6.4 SeedableRng::seed_from_u64 (third-party crates,
+ * not vendored in the reference; restated from their published algorithms,
+ * parity unpinned beyond the ChaCha block test vector of RFC 8439) ---- */
+
+static uint32_t rotl32(uint32_t x, int r) { return (x << r) | (x >> (32 - r)); }
+
+/* one ChaCha block with a 64-bit block counter (words 12-13) and a 64-bit
+ * stream id (words 14-15), `rounds` rounds (20 for ChaCha20, 12 for
+ * ChaCha12) */
+void orc_chacha_block(const uint32_t key[8], uint64_t counter, uint64_t stream, int rounds,
+                      uint32_t out[16]) {
+  uint32_t s[16] = {0x61707865u, 0x3320646eu, 0x79622d32u, 0x6b206574u,
+                    key[0], key[1], key[2], key[3], key[4], key[5], key[6], key[7],
+                    (uint32_t)counter, (uint32_t)(counter >> 32),
+                    (uint32_t)stream, (uint32_t)(stream >> 32)};
+  uint32_t x[16];
+  memcpy(x, s, sizeof(x));
+#define QR(a, b, c, d)                 \
+  x[a] += x[b]; x[d] = rotl32(x[d] ^ x[a], 16); \
+  x[c] += x[d]; x[b] = rotl32(x[b] ^ x[c], 12); \
+  x[a] += x[b]; x[d] = rotl32(x[d] ^ x[a], 8);  \
+  x[c] += x[d]; x[b] = rotl32(x[b] ^ x[c], 7);
+  for (int r = 0; r < rounds; r += 2) {
+    QR(0, 4, 8, 12) QR(1, 5, 9, 13) QR(2, 6, 10, 14) QR(3, 7, 11, 15)
+    QR(0, 5, 10, 15) QR(1, 6, 11, 12) QR(2, 7, 8, 13) QR(3, 4, 9, 14)
+  }
+#undef QR
+  for (int i = 0; i < 16; i++) out[i] = x[i] + s[i];
+}
+
+/* seed_from_u64: the 32-byte seed from a PCG32 sequence (state advanced
+ * first, XSH-RR output), little-endian words */
+static void seed_from_u64(uint64_t state, uint32_t key[8]) {
+  const uint64_t MUL = 6364136223846793005ull, INC = 11634580027462260723ull;
+  for (int i = 0; i < 8; i++) {
+    state = state * MUL + INC;
+    const uint32_t xorshifted = (uint32_t)(((state >> 18) ^ state) >> 27);
+    const uint32_t rot = (uint32_t)(state >> 59);
+    key[i] = (xorshifted >> rot) | (xorshifted << ((32 - rot) & 31));
+  }
+}
+
+/* the first n draws of StdRng::seed_from_u64(seed).gen::<f32>():
+ * next_u32 walks the 64-word buffer of four consecutive ChaCha12 blocks
+ * (counter from 0, stream 0), and each draw is (u32 >> 8) * 2^-24 */
+void orc_stdrng_f32(uint64_t seed, size_t n, float *out) {
+  uint32_t key[8], buf[64];
+  seed_from_u64(seed, key);
+  uint64_t ctr = 0;
+  size_t idx = 64;
+  for (size_t i = 0; i < n; i++) {
+    if (idx >= 64) {
+      for (int b = 0; b < 4; b++) orc_chacha_block(key, ctr + (uint64_t)b, 0, 12, buf + 16 * b);
+      ctr += 4;
+      idx = 0;
+    }
+    out[i] = (float)(buf[idx++] >> 8) * (1.0f / 16777216.0f);
+  }
 }

@@ -166,6 +166,19 @@ void orc_selective_scan_step(const float *x, const float *delta, const float *a_
                              const float *b, const float *c, const float *d, float *state,
                              float *y, size_t d_inner, size_t d_state);
 
+/* ---- sampling (generation/sampler.rs) ---- */
+void orc_repetition_penalty(float *logits, size_t n, const uint32_t *hist, size_t nh,
+                            float penalty);
+void orc_softmax_inplace(float *x, size_t n);
+void orc_top_k_filter(float *logits, size_t n, size_t k);
+void orc_top_p_filter(float *logits, size_t n, float p);
+uint32_t orc_sample_combined(float *logits, size_t n, const uint32_t *hist, size_t nh,
+                             float temperature, size_t top_k, float top_p, float rep_penalty,
+                             float u);
+void orc_chacha_block(const uint32_t key[8], uint64_t counter, uint64_t stream, int rounds,
+                      uint32_t out[16]);
+void orc_stdrng_f32(uint64_t seed, size_t n, float *out);
+
 #ifdef __cplusplus
 }
 #endif

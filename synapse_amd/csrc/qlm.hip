@@ -19,6 +19,7 @@
 #include <thread>
 #include <vector>
 
+#include "sampler.hpp"
 #include "decode_fused.hpp"
 #include "layer_ops.hpp"
 #include "linear.hpp"
@@ -59,6 +60,12 @@ struct syn_hip_qlm_s {
   bool finalized = false;
   bool fused = true;      // fused five-kernel decode layer (else one kernel per op)
   bool use_graph = true;  // replay the decode step as a HIP graph (else launch eagerly)
+  // sampling (sampler.hip): CombinedSampler settings, its scratch, and the
+  // draws of the seeded StdRng, one per generated token (index = step)
+  bool sampling = false;
+  SampleArgs sargs;
+  SampleScratch sscr;
+  DevBuf u_draws;
 
   ~syn_hip_qlm_s() {
     if (graph) (void)hipGraphExecDestroy(graph);
@@ -201,6 +208,10 @@ struct syn_hip_qlm_s {
     SYN_TRY(launch_rmsnorm_quant(xr, dr, final_nw.as<float>(), c.eps, 1, (int)h, xq.as<int8_t>(),
                                  (int)ldh, sx.as<float>(), nullptr, s));
     SYN_TRY(lm_head.gemv(1, xq.as<int8_t>(), ldh, sx.as<float>(), logits.as<float>(), vocab, s));
+    if (sampling)
+      return launch_sample(logits.as<float>(), (int)vocab, history.as<uint32_t>(), 0, sargs,
+                           u_draws.as<float>(), st(), add_pos, history.as<uint32_t>(),
+                           mhist.as<float>(), sscr, nullptr, s);
     SYN_TRY(launch_argmax(logits.as<float>(), (int)vocab, pv.as<float>(), pi.as<int>(),
                           pv2.as<float>(), st(), history.as<uint32_t>(), mhist.as<float>(), s));
     return launch_step_advance(st(), add_pos, s);
@@ -278,9 +289,39 @@ struct syn_hip_qlm_s {
     SYN_TRY(launch_lmhead_top2(lm_head.w.p, lm_head.scales.as<float>(), (int)vocab,
                                lm_head.chunks, xq.as<int8_t>(), s_head, logits.as<float>(),
                                pv.as<float>(), pi.as<int>(), pv2.as<float>(), s));
+    if (sampling)
+      return launch_sample(logits.as<float>(), (int)vocab, history.as<uint32_t>(), 0, sargs,
+                           u_draws.as<float>(), st(), 1, history.as<uint32_t>(),
+                           mhist.as<float>(), sscr, nullptr, s);
     return launch_argmax_advance(pv.as<float>(), pi.as<int>(), pv2.as<float>(),
                                  (int)cdiv(vocab, 64), st(), history.as<uint32_t>(),
                                  mhist.as<float>(), s);
+  }
+
+  // sampler settings; the captured decode step changes with them
+  syn_status_t set_sampler(const syn_hip_sampler *p, uint64_t seed) {
+    SYN_HIP(hipStreamSynchronize(stream));
+    if (graph) {
+      (void)hipGraphExecDestroy(graph);
+      graph = nullptr;
+    }
+    if (!p) {
+      sampling = false;
+      return SYN_OK;
+    }
+    if (!(p->temperature == p->temperature) || !(p->top_p == p->top_p) ||
+        !(p->repetition_penalty == p->repetition_penalty)) {
+      set_error("sampler parameters must not be NaN");
+      return SYN_ERR_INVALID_ARG;
+    }
+    sargs = make_sample_args(*p);
+    SYN_TRY(sscr.ensure(vocab));
+    std::vector<float> u(S + 1);
+    host_stdrng_f32(seed, u.size(), u.data());
+    SYN_TRY(u_draws.alloc(u.size() * 4));
+    SYN_HIP(hipMemcpy(u_draws.p, u.data(), u.size() * 4, hipMemcpyHostToDevice));
+    sampling = true;
+    return SYN_OK;
   }
 
   // one decode step on the model stream: graph replay or eager launches
@@ -774,6 +815,12 @@ syn_status_t syn_hip_qlm_time_lm_head(syn_hip_qlm_t *m, size_t iters, size_t flu
 syn_status_t syn_hip_qlm_set_options(syn_hip_qlm_t *m, int fused_decode, int graph_replay) {
   SYN_TRY(check_model(m));
   return m->set_options(fused_decode, graph_replay);
+}
+
+syn_status_t syn_hip_qlm_set_sampler(syn_hip_qlm_t *m, const syn_hip_sampler *params,
+                                     uint64_t seed) {
+  SYN_TRY(check_model(m));
+  return m->set_sampler(params, seed);
 }
 
 syn_status_t syn_hip_qlm_time_lm_head_rotating(syn_hip_qlm_t *m, size_t iters, float *avg_ms) {

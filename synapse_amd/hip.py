@@ -27,6 +27,12 @@ LAYOUT_KN, LAYOUT_NK = 0, 1
 P, SZ, ST = C.c_void_p, C.c_size_t, C.c_int32
 
 
+class SamplerParams(C.Structure):
+    """syn_hip_sampler: CombinedSampler (generation/sampler.rs:152-157)."""
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_uint32), ("top_p", C.c_float),
+                ("repetition_penalty", C.c_float)]
+
+
 class LmConfig(C.Structure):
     _fields_ = [("hidden", C.c_uint32), ("n_layers", C.c_uint32), ("n_heads", C.c_uint32),
                 ("n_kv_heads", C.c_uint32), ("head_dim", C.c_uint32), ("inter", C.c_uint32),
@@ -95,6 +101,9 @@ SIGNATURES = {
     "syn_hip_qlm_decode_timed": (ST, [P, SZ, C.POINTER(C.c_float)]),
     "syn_hip_qlm_time_lm_head": (ST, [P, SZ, SZ, C.POINTER(C.c_float)]),
     "syn_hip_qlm_set_options": (ST, [P, C.c_int, C.c_int]),
+    "syn_hip_qlm_set_sampler": (ST, [P, C.POINTER(SamplerParams), C.c_uint64]),
+    "syn_hip_sample": (ST, [P, SZ, P, SZ, C.POINTER(SamplerParams), C.c_float, P, P, P]),
+    "syn_hip_stdrng_f32": (ST, [C.c_uint64, SZ, P]),
     "syn_hip_qlm_time_lm_head_rotating": (ST, [P, SZ, C.POINTER(C.c_float)]),
     "syn_hip_qlm_destroy": (ST, [P]),
     "syn_hip_klm_create": (ST, [C.POINTER(KLmConfig), C.POINTER(P)]),
@@ -503,6 +512,12 @@ class QuantizedCausalLM:
         graph replay or eager launches (same results either way)."""
         check(lib().syn_hip_qlm_set_options(self.h, int(fused), int(graph)), "set_options")
 
+    def set_sampler(self, params=None, seed: int = 0):
+        """CombinedSampler settings for generate / decode steps (None: greedy),
+        with the draws of StdRng::seed_from_u64(seed)."""
+        check(lib().syn_hip_qlm_set_sampler(self.h, None if params is None else C.byref(params),
+                                            seed), "set_sampler")
+
     def time_lm_head_rotating(self, iters: int = 40) -> float:
         ms = C.c_float()
         check(lib().syn_hip_qlm_time_lm_head_rotating(self.h, iters, C.byref(ms)),
@@ -837,6 +852,41 @@ class QuantizedMamba:
             self.close()
         except Exception:
             pass
+
+
+def sampler_params(temperature=1.0, top_k=0, top_p=1.0, repetition_penalty=1.0):
+    return SamplerParams(temperature, top_k, top_p, repetition_penalty)
+
+
+def sample(logits: np.ndarray, history=(), temperature=1.0, top_k=0, top_p=1.0,
+           repetition_penalty=1.0, u=0.5):
+    """syn_hip_sample on host arrays (uploads, samples on the device, reads the
+    token back): CombinedSampler::sample_with_history with the draw u."""
+    x = np.ascontiguousarray(logits, np.float32)
+    h = np.ascontiguousarray(np.asarray(history, np.uint32).reshape(-1))
+    dx = DeviceBuffer.from_array(x)
+    dh = DeviceBuffer.from_array(h if h.size else np.zeros(1, np.uint32))
+    dt = DeviceBuffer(4)
+    ds = DeviceBuffer(4)
+    try:
+        prm = sampler_params(temperature, top_k, top_p, repetition_penalty)
+        check(lib().syn_hip_sample(dx.ptr, x.size, dh.ptr, h.size, C.byref(prm), u, dt.ptr,
+                                   ds.ptr, None), "sample")
+        check(lib().syn_hip_stream_synchronize(None))
+        tok = int(dt.download(1, np.uint32)[0])
+        status = int(ds.download(1, np.int32)[0])
+    finally:
+        for b in (dx, dh, dt, ds):
+            b.close()
+    if status:
+        raise SynapseError(2, "sample: top-p over more than 4096 candidates")
+    return tok
+
+
+def stdrng_f32(seed: int, n: int) -> np.ndarray:
+    out = np.zeros(max(n, 1), np.float32)
+    check(lib().syn_hip_stdrng_f32(seed, n, ptr(out)), "stdrng_f32")
+    return out[:n]
 
 
 def kquant_encode(fmt: int, w: np.ndarray) -> np.ndarray:
