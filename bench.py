@@ -120,6 +120,10 @@ def secondary(hip, np):
     out["config2_q4_0_gemv_llama1b"] = {
         "note": "batch-1 Q4_0 GEMV, f32 activations, >= 1 GiB of weight copies rotated",
         "gemvs": mb.q4_0_suite()}
+    out["ternary_gemv_llama1b_shapes"] = {
+        "note": "TernaryLinear batch-1 GEMV (not a BASELINE config; the quantized-linear "
+                "format of ternary_linear.rs), >= 1 GiB of weight copies rotated",
+        "gemvs": mb.ternary_suite()}
     out["config3_kquant_gemv_llama3b"] = {
         "note": "batch-1 Q4_K / Q6_K GEMV at the LLaMA-3.2-3B shapes, >= 1 GiB rotated",
         "gemvs": mb.kquant_suite()}

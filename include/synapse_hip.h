@@ -112,6 +112,10 @@ syn_status_t syn_hip_quantize_rows(const float *d_x, size_t m, size_t k, size_t 
 #define SYN_HIP_FMT_Q8_0 3
 #define SYN_HIP_FMT_Q4_K 4
 #define SYN_HIP_FMT_Q6_K 5
+/* TernaryLinear (quantization/primitives/ternary_linear.rs): blocks of 16
+ * weights, each an f32 scale and four code bytes (0b00 -1, 0b01 0, 0b10 +1,
+ * 0b11 0; weight 4b+j at bits 2j of byte b); f32 activations. */
+#define SYN_HIP_FMT_TERNARY 6
 /* host weight layouts accepted by syn_hip_qlinear_create for INT8 */
 #define SYN_HIP_LAYOUT_KN 0 /* reference QuantizedLinear::weights_int8 [K,N] */
 #define SYN_HIP_LAYOUT_NK 1 /* row per output feature [N,K] */

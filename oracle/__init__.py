@@ -93,6 +93,8 @@ def _declare(L):
                                              C.c_float]),
         "orc_chacha_block": (None, [P, C.c_uint64, C.c_uint64, C.c_int, P]),
         "orc_stdrng_f32": (None, [C.c_uint64, SZ, P]),
+        "orc_ternary_from_f32": (None, [P, SZ, SZ, P]),
+        "orc_ternary_forward": (None, [P, SZ, SZ, P, SZ, P]),
         "orc_attention_decode": (None, [P, P, P, SZ, SZ, SZ, SZ, P]),
         "orc_fused_attention": (C.c_int, [SZ, SZ, SZ, P, P, P, P]),
         "orc_qlm_create": (P, [C.POINTER(LmCfg)]),
@@ -328,6 +330,25 @@ def stdrng_f32(seed: int, n: int) -> np.ndarray:
     out = np.zeros(n, np.float32)
     lib().orc_stdrng_f32(seed, n, _p(out))
     return out
+
+
+# ---------------------------------------------------------------- ternary
+def ternary_from_f32(w: np.ndarray) -> np.ndarray:
+    """TernaryLinear::from_f32: w [N,K] -> blocks [N * ceil(K/16) * 8] bytes
+    (f32 scale, then 4 code bytes, per block of 16 weights)."""
+    w = np.ascontiguousarray(w, np.float32)
+    n, k = w.shape
+    out = np.zeros(n * ((k + 15) // 16) * 8, np.uint8)
+    lib().orc_ternary_from_f32(_p(w), n, k, _p(out))
+    return out
+
+
+def ternary_forward(blocks: np.ndarray, n: int, k: int, x: np.ndarray) -> np.ndarray:
+    blocks = np.ascontiguousarray(blocks, np.uint8)
+    x = np.ascontiguousarray(x, np.float32).reshape(-1, k)
+    y = np.zeros((x.shape[0], n), np.float32)
+    lib().orc_ternary_forward(_p(blocks), n, k, _p(x), x.shape[0], _p(y))
+    return y
 
 
 def expf(x: float) -> float:

@@ -1722,3 +1722,78 @@ void orc_stdrng_f32(uint64_t seed, size_t n, float *out) {
     out[i] = (float)(buf[idx++] >> 8) * (1.0f / 16777216.0f);
   }
 }
+
+/* ======================================================================
+ * Ternary linear (quantization/primitives/ternary_linear.rs)
+ * ====================================================================== */
+
+/* TernaryLinear::from_f32 (ternary_linear.rs:100-161): per row, threshold
+ * 0.5 * mean|w| (sequential sum), codes +1 / -1 / 0, scale = mean |w| of
+ * the non-zero codes (or mean|w| when there are none); blocks of 16 weights
+ * = f32 scale + 4 code bytes (0b00 -1, 0b01 0, 0b10 +1; weight 4b+j at bits
+ * 2j of byte b); K padded with zero codes to a multiple of 16. */
+void orc_ternary_from_f32(const float *w, size_t n, size_t k, uint8_t *blocks) {
+  const size_t bpr = (k + 15) / 16;
+  for (size_t r = 0; r < n; r++) {
+    const float *row = w + r * k;
+    float s = 0.0f;
+    for (size_t i = 0; i < k; i++) s += fabsf(row[i]);
+    const float mean_abs = k ? s / (float)k : 0.0f;
+    const float thr = 0.5f * mean_abs;
+    float nz_sum = 0.0f;
+    size_t nz = 0;
+    for (size_t i = 0; i < k; i++) {
+      if (row[i] > thr || row[i] < -thr) {
+        nz_sum += fabsf(row[i]);
+        nz++;
+      }
+    }
+    const float scale = nz ? nz_sum / (float)nz : mean_abs;
+    for (size_t b = 0; b < bpr; b++) {
+      uint8_t *blk = blocks + (r * bpr + b) * 8;
+      memcpy(blk, &scale, 4);
+      for (int byte = 0; byte < 4; byte++) {
+        uint8_t v = 0;
+        for (int j = 0; j < 4; j++) {
+          const size_t col = b * 16 + (size_t)byte * 4 + (size_t)j;
+          uint8_t code = 1;  /* zero (and the padding) */
+          if (col < k) {
+            if (row[col] > thr) code = 2;
+            else if (row[col] < -thr) code = 0;
+          }
+          v |= (uint8_t)(code << (2 * j));
+        }
+        blk[4 + byte] = v;
+      }
+    }
+  }
+}
+
+/* TernaryLinear::forward (ternary_linear.rs:179-215): per block the codes add
+ * or subtract x in column order (zero and reserved codes skip), then
+ * acc += block_acc * scale, blocks in order; columns >= k are skipped. */
+void orc_ternary_forward(const uint8_t *blocks, size_t n, size_t k, const float *x, size_t m,
+                         float *y) {
+  const size_t bpr = (k + 15) / 16;
+  for (size_t i = 0; i < m; i++) {
+    const float *xr = x + i * k;
+    for (size_t j = 0; j < n; j++) {
+      float acc = 0.0f;
+      for (size_t b = 0; b < bpr; b++) {
+        const uint8_t *blk = blocks + (j * bpr + b) * 8;
+        float scale;
+        memcpy(&scale, blk, 4);
+        float bacc = 0.0f;
+        for (int wi = 0; wi < 16; wi++) {
+          const size_t col = b * 16 + (size_t)wi;
+          if (col >= k) continue;
+          const int code = (blk[4 + wi / 4] >> (2 * (wi % 4))) & 3;
+          if (code == 2) bacc += xr[col];
+          else if (code == 0) bacc -= xr[col];
+        }
+        acc += bacc * scale;
+      }
+      y[i * n + j] = acc;
+    }
+  }
+}

@@ -179,6 +179,11 @@ void orc_chacha_block(const uint32_t key[8], uint64_t counter, uint64_t stream, 
                       uint32_t out[16]);
 void orc_stdrng_f32(uint64_t seed, size_t n, float *out);
 
+/* ---- ternary linear (quantization/primitives/ternary_linear.rs) ---- */
+void orc_ternary_from_f32(const float *w, size_t n, size_t k, uint8_t *blocks);
+void orc_ternary_forward(const uint8_t *blocks, size_t n, size_t k, const float *x, size_t m,
+                         float *y);
+
 #ifdef __cplusplus
 }
 #endif

@@ -313,6 +313,7 @@ struct syn_hip_qlinear_s {
   QLinearInt8 i8;
   QLinearQ4_0 q4;
   QLinearKQ kq;
+  QLinearTernary ter;
 };
 
 static bool is_kq(int fmt) {
@@ -352,6 +353,8 @@ syn_status_t syn_hip_qlinear_create(int fmt, size_t n, size_t k, const void *hos
   } else if (is_kq(fmt)) {
     st = (k % kq_block_elems(fmt)) ? SYN_ERR_SHAPE_MISMATCH
                                    : h->kq.upload(fmt, (const uint8_t *)host_weights, n, k);
+  } else if (fmt == SYN_HIP_FMT_TERNARY) {
+    st = h->ter.upload_blocks((const uint8_t *)host_weights, n, k);
   } else {
     st = SYN_ERR_INVALID_ARG;
   }
@@ -375,6 +378,7 @@ syn_status_t syn_hip_qlinear_from_f32(int fmt, size_t n, size_t k, const float *
   else if (fmt == SYN_HIP_FMT_Q4_0) st = (k % 32) ? SYN_ERR_SHAPE_MISMATCH : h->q4.from_f32(host_w, n, k);
   else if (is_kq(fmt))
     st = (k % kq_block_elems(fmt)) ? SYN_ERR_SHAPE_MISMATCH : h->kq.from_f32(fmt, host_w, n, k);
+  else if (fmt == SYN_HIP_FMT_TERNARY) st = h->ter.from_f32(host_w, n, k);
   else st = SYN_ERR_INVALID_ARG;
   if (st != SYN_OK) {
     delete h;
@@ -404,6 +408,7 @@ syn_status_t syn_hip_qlinear_forward(syn_hip_qlinear_t *h, size_t m, const float
   hipStream_t s = pick_stream(stream);
   if (h->fmt == SYN_HIP_FMT_Q4_0) return h->q4.gemv(m, d_x, h->q4.k, d_y, h->q4.n, s);
   if (is_kq(h->fmt)) return h->kq.gemv(m, d_x, h->kq.k, d_y, h->kq.n, s);
+  if (h->fmt == SYN_HIP_FMT_TERNARY) return h->ter.gemv(m, d_x, h->ter.k, d_y, h->ter.n, s);
   if (h->fmt != SYN_HIP_FMT_INT8) return SYN_ERR_INVALID_ARG;
   QLinearInt8 &L = h->i8;
   const size_t ldq = (size_t)L.chunks * 16;
@@ -426,6 +431,8 @@ syn_status_t syn_hip_qlinear_info(const syn_hip_qlinear_t *h, size_t *n, size_t 
     nn = h->i8.n; kk = h->i8.k; wb = h->i8.weight_bytes();
   } else if (h->fmt == SYN_HIP_FMT_Q4_0) {
     nn = h->q4.n; kk = h->q4.k; wb = h->q4.weight_bytes();
+  } else if (h->fmt == SYN_HIP_FMT_TERNARY) {
+    nn = h->ter.n; kk = h->ter.k; wb = h->ter.weight_bytes();
   } else {
     nn = h->kq.n; kk = h->kq.k; wb = h->kq.weight_bytes();
   }

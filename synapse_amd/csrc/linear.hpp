@@ -85,6 +85,20 @@ struct QLinearQ4_0 {
                     hipStream_t s);
 };
 
+// Ternary linear: TernaryLinear (ternary_linear.rs); f32 activations.
+struct QLinearTernary {
+  size_t n = 0, k = 0;
+  int bpr = 0;         // blocks of 16 weights per row
+  DevBuf codes;        // u32 [P][bpr][64]
+  DevBuf scales;       // f32 [P][bpr][64]
+  // the reference's blocks: per block an f32 scale and four code bytes
+  syn_status_t upload_blocks(const uint8_t *blocks, size_t n_, size_t k_);
+  syn_status_t from_f32(const float *w_nk, size_t n_, size_t k_);
+  size_t weight_bytes() const { return n * (size_t)bpr * 8; }
+  syn_status_t gemv(size_t m, const float *d_x, size_t ldx, float *d_y, size_t ldy,
+                    hipStream_t s);
+};
+
 // Q4Linear::from_f32 + pack_for_zig (q4_linear.rs:64-121), host side.
 void host_q4_pack(const float *w, size_t n, size_t k, uint8_t *packed);
 

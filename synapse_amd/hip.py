@@ -20,7 +20,7 @@ STATUS_NAMES = {0: "OK", 1: "NULL_PTR", 2: "INVALID_ARG", 3: "OUT_OF_MEMORY",
                 4: "SHAPE_MISMATCH", 5: "NOT_CONTIGUOUS", 6: "INVALID_AXIS",
                 7: "INVALID_DIMENSIONS", 8: "INTERNAL", 100: "NO_DEVICE", 101: "HIP",
                 102: "LAUNCH"}
-FMT_INT8, FMT_Q4_0, FMT_Q8_0, FMT_Q4_K, FMT_Q6_K = 1, 2, 3, 4, 5
+FMT_INT8, FMT_Q4_0, FMT_Q8_0, FMT_Q4_K, FMT_Q6_K, FMT_TERNARY = 1, 2, 3, 4, 5, 6
 KQ_BLOCK = {FMT_Q8_0: (32, 34), FMT_Q4_K: (256, 144), FMT_Q6_K: (256, 210)}
 LAYOUT_KN, LAYOUT_NK = 0, 1
 
@@ -356,6 +356,15 @@ class QLinear:
         check(lib().syn_hip_qlinear_create(FMT_Q4_0, n, k, ptr(packed), None, 0, C.byref(h)),
               "qlinear_create")
         return cls(h.value, FMT_Q4_0)
+
+    @classmethod
+    def ternary(cls, blocks: np.ndarray, n: int, k: int) -> "QLinear":
+        """TernaryLinear blocks (f32 scale + 4 code bytes per 16 weights) of [n, k]."""
+        blocks = np.ascontiguousarray(blocks, np.uint8)
+        h = C.c_void_p()
+        check(lib().syn_hip_qlinear_create(FMT_TERNARY, n, k, ptr(blocks), None, 0, C.byref(h)),
+              "qlinear_create")
+        return cls(h.value, FMT_TERNARY)
 
     @classmethod
     def gguf(cls, fmt: int, blocks: np.ndarray, n: int, k: int) -> "QLinear":

@@ -29,12 +29,14 @@ F16_SCALE = 0x1E66             # a finite f16 (about 0.0062)
 BLOCK = {hip.FMT_Q4_0: (32, 18), hip.FMT_Q8_0: (32, 34), hip.FMT_Q4_K: (256, 144),
          hip.FMT_Q6_K: (256, 210)}
 NAMES = {hip.FMT_INT8: "int8", hip.FMT_Q4_0: "q4_0", hip.FMT_Q8_0: "q8_0",
-         hip.FMT_Q4_K: "q4_k", hip.FMT_Q6_K: "q6_k"}
+         hip.FMT_Q4_K: "q4_k", hip.FMT_Q6_K: "q6_k", hip.FMT_TERNARY: "ternary"}
 
 
 def weight_bytes(fmt: int, n: int, k: int) -> int:
     if fmt == hip.FMT_INT8:
         return n * k + 4 * n
+    if fmt == hip.FMT_TERNARY:
+        return n * ((k + 15) // 16) * 8
     el, b = BLOCK[fmt]
     return n * (k // el) * b
 
@@ -67,6 +69,11 @@ def _make(fmt: int, n: int, k: int, rng):
         w = rng.integers(-127, 128, size=(n, k), dtype=np.int8)
         sc = (rng.random(n, dtype=np.float32) * 1e-3 + 1e-4).astype(np.float32)
         return lambda: hip.QLinear.int8(w, sc, hip.LAYOUT_NK)
+    if fmt == hip.FMT_TERNARY:
+        raw = rng.integers(0, 256, size=(n * ((k + 15) // 16), 8), dtype=np.uint8)
+        raw[:, 0:4] = np.frombuffer(np.float32(0.01).tobytes(), np.uint8)  # scale
+        tb = raw.reshape(-1)
+        return lambda: hip.QLinear.ternary(tb, n, k)
     blocks = _blocks(fmt, n, k, rng)
     if fmt == hip.FMT_Q4_0:
         return lambda: hip.QLinear.q4_0(blocks, n, k)
@@ -146,6 +153,11 @@ KQ_LLAMA3B_SHAPES = [(hip.FMT_Q4_K, "q/o 3072->3072", 3072, 3072),
 # config 4: Mistral-7B Q8_0 prefill GEMMs
 Q8_0_MISTRAL = [("q 4096->4096", 4096, 4096, 1), ("k/v 4096->1024", 4096, 1024, 2),
                 ("gate/up 4096->14336", 4096, 14336, 2), ("down 14336->4096", 14336, 4096, 1)]
+
+
+def ternary_suite(rounds: int = 4) -> list:
+    """TernaryLinear GEMVs at the LLaMA-3.2-1B shapes of config 2 (0.5 B/weight)."""
+    return [gemv_record(hip.FMT_TERNARY, n, k, lab, rounds) for lab, k, n in Q4_0_SHAPES]
 
 
 def q4_0_suite(rounds: int = 4) -> list:
