@@ -228,9 +228,22 @@ syn_status_t syn_hip_qlm_init_synthetic(syn_hip_qlm_t *m, uint64_t seed_base, fl
 /* Quantize the lm_head, upload RoPE tables; call once after weights. */
 syn_status_t syn_hip_qlm_finalize(syn_hip_qlm_t *m);
 syn_status_t syn_hip_qlm_reset(syn_hip_qlm_t *m);
-/* forward_prefill (int8.rs:593-635): logits of the last prompt token. */
+/* forward_prefill (int8.rs:593-635) into an empty cache (a fresh ModelState):
+ * logits of the last prompt token. */
 syn_status_t syn_hip_qlm_forward_prefill(syn_hip_qlm_t *m, const uint32_t *ids, size_t n,
                                          float *host_logits);
+/* forward_prefill into the cache as it stands (int8.rs:593-635 with
+ * cached_attention_prefill, ops/attention.rs:153-247): the n rows are
+ * appended after the cached ones, rotated at positions 0..n-1 and attend
+ * among themselves, as in the reference. */
+syn_status_t syn_hip_qlm_forward_prefill_append(syn_hip_qlm_t *m, const uint32_t *ids,
+                                                size_t n, float *host_logits);
+/* KVCache::truncate_to -> syn_kvcache_truncate (kv_cache/cache.rs:307-312,
+ * exports.zig:1935-1939, kvcache.zig:109-113): the cache length becomes
+ * new_len if that is shorter; contents are kept. */
+syn_status_t syn_hip_qlm_truncate(syn_hip_qlm_t *m, size_t new_len);
+/* KVCache::current_len (kv_cache/cache.rs:301-304). */
+syn_status_t syn_hip_qlm_cache_len(syn_hip_qlm_t *m, size_t *out_len);
 /* forward_one (int8.rs:638-709) for `token` at the current cache length. */
 syn_status_t syn_hip_qlm_forward_one(syn_hip_qlm_t *m, uint32_t token, float *host_logits);
 /* Greedy generate (generation/pipeline.rs:197-278): max_new tokens from one
@@ -238,6 +251,16 @@ syn_status_t syn_hip_qlm_forward_one(syn_hip_qlm_t *m, uint32_t token, float *ho
  * only the tokens are read back.  margins (nullable) gets top1-top2. */
 syn_status_t syn_hip_qlm_generate(syn_hip_qlm_t *m, const uint32_t *prompt, size_t n_prompt,
                                   size_t max_new, uint32_t *out_tokens, float *out_margins);
+/* Speculative generate (generation/pipeline.rs:281-395, speculative_k = k,
+ * max_new_tokens = max_new, the model's sampler settings): per round k draft
+ * tokens from forward_one (QuantizedCausalLM has no draft forward,
+ * int8.rs:739), truncate to the round's start, verify forward_prefill of
+ * [last accepted, drafts], accept all drafts, then a bonus token from
+ * forward_one of the last draft when all k were accepted.  The whole loop is
+ * enqueued without a host round trip; k = 0 is generate. */
+syn_status_t syn_hip_qlm_generate_speculative(syn_hip_qlm_t *m, const uint32_t *prompt,
+                                              size_t n_prompt, size_t max_new, size_t k,
+                                              uint32_t *out_tokens, float *out_margins);
 /* Timed decode: `steps` greedy decode steps after the current state, on the
  * model stream; returns elapsed milliseconds measured with hipEvents. */
 syn_status_t syn_hip_qlm_decode_timed(syn_hip_qlm_t *m, size_t steps, float *elapsed_ms);

@@ -110,6 +110,8 @@ def _declare(L):
         "orc_qlm_reset": (None, [P]),
         "orc_qlm_cur_len": (SZ, [P]),
         "orc_qlm_prefill": (C.c_int, [P, P, SZ, P]),
+        "orc_qlm_prefill_append": (C.c_int, [P, P, SZ, P]),
+        "orc_qlm_truncate": (None, [P, SZ]),
         "orc_qlm_forward_one": (C.c_int, [P, C.c_uint32, P]),
         "orc_qlm_generate": (C.c_int, [P, P, SZ, SZ, P, P]),
         "orc_qlm_lm_head_weights": (P, [P]),
@@ -446,6 +448,75 @@ class QuantizedCausalLM:
         self._check(lib().orc_qlm_generate(self.h, _p(prompt), prompt.size, max_new,
                                            _p(toks), _p(margins)))
         return toks, margins
+
+    def prefill_append(self, ids) -> np.ndarray:
+        """forward_prefill into the cache as it stands (int8.rs:593-635 with
+        cached_attention_prefill, ops/attention.rs:153-247)."""
+        ids = np.ascontiguousarray(ids, np.uint32)
+        logits = np.empty(self.cfg["vocab"], np.float32)
+        self._check(lib().orc_qlm_prefill_append(self.h, _p(ids), ids.size, _p(logits)))
+        return logits
+
+    def truncate(self, new_len: int):
+        """KvCache.truncateTo (kvcache.zig:109-113)."""
+        lib().orc_qlm_truncate(self.h, new_len)
+
+    def cache_len(self) -> int:
+        return int(lib().orc_qlm_cur_len(self.h))
+
+    def generate_speculative(self, prompt, max_new: int, k: int, sampler=None, seed: int = 0):
+        """TextGenerator::generate_speculative (generation/pipeline.rs:281-395)
+        on this model, max_new_tokens as the only stop condition.
+        QuantizedCausalLM has no forward_one_draft (int8.rs:739), so the
+        trait default (models/traits.rs:64-68) drafts with forward_one.
+        sampler: None (GreedySampler) or CombinedSampler settings
+        (sample_combined keywords), fed by StdRng::seed_from_u64(seed) one
+        draw per sample call.  Returns (tokens, margins): the top1 - top2
+        logit of each greedy choice (zeros when sampling)."""
+        k = max(1, k)  # pipeline.rs:294
+        draws = stdrng_f32(seed, max_new + k + 1) if sampler is not None else None
+        calls = [0]
+        margins = []
+
+        def sample(logits, generated):  # pipeline.rs:475-489
+            if sampler is None:
+                tok = argmax(logits)
+                second = np.max(np.delete(logits, tok)) if logits.size > 1 else np.float32(-np.inf)
+                margins.append(np.float32(logits[tok] - second))
+            else:
+                tok = sample_combined(logits, np.array(generated, np.uint32),
+                                      u=float(draws[calls[0]]), **sampler)
+                margins.append(np.float32(0.0))
+            calls[0] += 1
+            return int(tok)
+
+        gen = []
+        out_margins = []
+        logits = self.prefill(prompt)
+        gen.append(sample(logits, gen))
+        out_margins.append(margins[-1])
+        while len(gen) < max_new:  # stopping.rs:39-42
+            save = self.cache_len()
+            drafts, dmarg = [], []
+            last = gen[-1]
+            for _ in range(k):
+                tok = sample(self.forward_one(last), gen)
+                drafts.append(tok)
+                dmarg.append(margins[-1])
+                last = tok
+            self.truncate(save)
+            self.prefill_append([gen[-1]] + drafts)  # verify; logits unused
+            accepted = 0
+            for tok, mg in zip(drafts, dmarg):
+                gen.append(tok)
+                out_margins.append(mg)
+                accepted += 1
+                if len(gen) >= max_new:
+                    break
+            if accepted == k and len(gen) < max_new:  # bonus token
+                gen.append(sample(self.forward_one(gen[-1]), gen))
+                out_margins.append(margins[-1])
+        return np.array(gen, np.uint32), np.array(out_margins, np.float32)
 
     def close(self):
         if self.h:

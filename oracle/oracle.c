@@ -903,8 +903,9 @@ static void ffn_swiglu(const orc_qlm *m, const orc_qlin *L, const float *x, size
 }
 
 /* Decoder layer, prefill (int8.rs:194-216, 379-426) or decode (int8.rs:242-282, 429-478).
- * prefill==1: t tokens at positions 0..t-1 (cache assumed empty);
- * prefill==0: one token at position m->cur. */
+ * prefill==1: t tokens rotated at positions 0..t-1 and appended at cache rows
+ * m->cur.. (cached_attention_prefill, ops/attention.rs:173-198), attending among
+ * themselves (:200-244); prefill==0: one token at position m->cur. */
 static void layer_forward(orc_qlm *m, size_t l, float *x, size_t t, int prefill) {
   const orc_lm_cfg *c = &m->c;
   size_t h = c->hidden, hd = c->head_dim, nh = c->n_heads, nkv = c->n_kv_heads;
@@ -931,11 +932,11 @@ static void layer_forward(orc_qlm *m, size_t l, float *x, size_t t, int prefill)
     orc_rmsnorm(q, m->q_norm + l * hd, c->eps, t * nh, hd, q);
     orc_rmsnorm(k, m->k_norm + l * hd, c->eps, t * nkv, hd, k);
   }
-  size_t pos0 = prefill ? 0 : m->cur;
+  size_t pos0 = prefill ? 0 : m->cur, row0 = m->cur;
   orc_rope_apply(q, m->rope_cos, m->rope_sin, t, nh, hd, pos0);
   orc_rope_apply(k, m->rope_cos, m->rope_sin, t, nkv, hd, pos0);
-  memcpy(kcl + pos0 * kvd, k, t * kvd * 4);
-  memcpy(vcl + pos0 * kvd, v, t * kvd * 4);
+  memcpy(kcl + row0 * kvd, k, t * kvd * 4);
+  memcpy(vcl + row0 * kvd, v, t * kvd * 4);
   if (prefill) {
     size_t groups = nh / nkv;
     float *qh = (float *)malloc(t * hd * 4), *kh = (float *)malloc(t * hd * 4);
@@ -955,7 +956,7 @@ static void layer_forward(orc_qlm *m, size_t l, float *x, size_t t, int prefill)
     free(vh);
     free(oh);
   } else {
-    orc_attention_decode(q, kcl, vcl, pos0 + 1, nh, nkv, hd, attn);
+    orc_attention_decode(q, kcl, vcl, row0 + 1, nh, nkv, hd, attn);
   }
   qlin_forward(&L[3], attn, t, o, xq, sx);
   for (size_t i = 0; i < t * h; i++) x[i] = x[i] + o[i];
@@ -977,18 +978,31 @@ static void lm_head_logits(orc_qlm *m, const float *xlast, float *logits) {
   free(xq);
 }
 
-/* QuantizedCausalLM::forward_prefill (int8.rs:593-635) */
-int orc_qlm_prefill(orc_qlm *m, const uint32_t *ids, size_t n, float *logits) {
-  if (n == 0 || n > m->c.max_seq) return ORC_ERR_INVALID_ARG;
+/* QuantizedCausalLM::forward_prefill (int8.rs:593-635) into the cache as it
+ * stands: the n rows go after the m->cur cached ones */
+int orc_qlm_prefill_append(orc_qlm *m, const uint32_t *ids, size_t n, float *logits) {
+  if (n == 0 || m->cur + n > m->c.max_seq) return ORC_ERR_INVALID_ARG;
   size_t h = m->c.hidden;
   float *x = (float *)malloc(n * h * 4);
   embed_rows(m, ids, n, x);
-  m->cur = 0;
   for (size_t l = 0; l < m->c.n_layers; l++) layer_forward(m, l, x, n, 1);
-  m->cur = n;
+  m->cur += n;
   lm_head_logits(m, x + (n - 1) * h, logits);
   free(x);
   return ORC_OK;
+}
+
+/* forward_prefill on a fresh ModelState (empty cache) */
+int orc_qlm_prefill(orc_qlm *m, const uint32_t *ids, size_t n, float *logits) {
+  if (n == 0 || n > m->c.max_seq) return ORC_ERR_INVALID_ARG;
+  m->cur = 0;
+  return orc_qlm_prefill_append(m, ids, n, logits);
+}
+
+/* KvCache.truncateTo (kvcache.zig:109-113) on every layer: only a shorter
+ * length applies, contents are kept */
+void orc_qlm_truncate(orc_qlm *m, size_t new_len) {
+  if (new_len < m->cur) m->cur = new_len;
 }
 
 /* QuantizedCausalLM::forward_one (int8.rs:638-709) */

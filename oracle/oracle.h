@@ -114,6 +114,8 @@ int orc_qlm_finalize(orc_qlm *m);
 void orc_qlm_reset(orc_qlm *m);
 size_t orc_qlm_cur_len(const orc_qlm *m);
 int orc_qlm_prefill(orc_qlm *m, const uint32_t *ids, size_t n, float *logits);
+int orc_qlm_prefill_append(orc_qlm *m, const uint32_t *ids, size_t n, float *logits);
+void orc_qlm_truncate(orc_qlm *m, size_t new_len);
 int orc_qlm_forward_one(orc_qlm *m, uint32_t token, float *logits);
 int orc_qlm_generate(orc_qlm *m, const uint32_t *prompt, size_t n_prompt, size_t max_new,
                      uint32_t *out_tokens, float *margins);

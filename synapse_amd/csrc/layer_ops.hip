@@ -157,24 +157,29 @@ syn_status_t launch_rmsnorm_quant(float *x, const float *delta, const float *w, 
 // ------------------------------------------------------------------ q/k norm, RoPE, KV append
 // ops/attention.rs:46-66: headwise RMSNorm (norm.rs:78-93), rotate-half RoPE
 // (rope.rs:13-43) at the token's position, append RoPE'd K and raw V.
+// Cache row = position + cache_off: a prefill into a non-empty cache
+// (cached_attention_prefill, ops/attention.rs:177-198) rotates at positions
+// 0.. of the new tokens but appends after the rows already held.
 // grid (n_heads + 2*n_kv, rows), one wave per head.
 __global__ void __launch_bounds__(64)
     k_qk_norm_rope_kv(const float *__restrict__ qkv, int ldqkv, int nh, int nkv, int hd,
                       const float *__restrict__ qn, const float *__restrict__ kn, float eps,
                       const float *__restrict__ cosT, const float *__restrict__ sinT,
-                      const int *__restrict__ d_pos, int pos_static, float *__restrict__ q_out,
-                      float *__restrict__ kc, float *__restrict__ vc, int max_seq) {
+                      const int *__restrict__ d_pos, int pos_static, int cache_off,
+                      float *__restrict__ q_out, float *__restrict__ kc, float *__restrict__ vc,
+                      int max_seq) {
   extern __shared__ float v[];  // hd
   __shared__ float red[8];
   __shared__ float s_scale;
   const int hh = blockIdx.x, r = blockIdx.y;
   const int pos = (d_pos ? d_pos[0] : pos_static) + r;
+  const int crow = pos + cache_off;
   const int qd = nh * hd, kvd = nkv * hd, half = hd / 2;
   const float *row = qkv + (size_t)r * ldqkv;
   if (hh >= nh + nkv) {  // V head: raw copy into the cache
     const int vh = hh - nh - nkv;
     for (int d = threadIdx.x; d < hd; d += 64)
-      vc[kv_v_index(pos, vh, d, hd, max_seq)] = row[qd + kvd + vh * hd + d];
+      vc[kv_v_index(crow, vh, d, hd, max_seq)] = row[qd + kvd + vh * hd + d];
     return;
   }
   const bool is_q = hh < nh;
@@ -205,8 +210,8 @@ __global__ void __launch_bounds__(64)
       dst[i] = a - b;
       dst[half + i] = e + f;
     } else {
-      kc[kv_k_index(pos, kh, i, hd, max_seq)] = a - b;
-      kc[kv_k_index(pos, kh, half + i, hd, max_seq)] = e + f;
+      kc[kv_k_index(crow, kh, i, hd, max_seq)] = a - b;
+      kc[kv_k_index(crow, kh, half + i, hd, max_seq)] = e + f;
     }
   }
 }
@@ -216,11 +221,11 @@ syn_status_t launch_qk_norm_rope_kv(const float *qkv, int ldqkv, int rows, int n
                                     const float *k_norm, float eps, const float *rope_cos,
                                     const float *rope_sin, const int *d_pos, int pos_static,
                                     float *q_out, float *kcache, float *vcache, int max_seq,
-                                    hipStream_t s) {
+                                    hipStream_t s, int cache_off) {
   hipLaunchKernelGGL(k_qk_norm_rope_kv, dim3(n_heads + 2 * n_kv, rows), dim3(64),
                      head_dim * sizeof(float), s, qkv, ldqkv, n_heads, n_kv, head_dim, q_norm,
-                     k_norm, eps, rope_cos, rope_sin, d_pos, pos_static, q_out, kcache, vcache,
-                     max_seq);
+                     k_norm, eps, rope_cos, rope_sin, d_pos, pos_static, cache_off, q_out, kcache,
+                     vcache, max_seq);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
 }
@@ -311,7 +316,9 @@ syn_status_t launch_attention_decode(const float *q, const float *kcache, const 
 // S = Q K^T and O = P V through sgemmTiled, whose element order is a
 // sequential chain over k — @mulAdd inside full 8x8 micro-tiles (or in the
 // f32GemvRow 32/8-wide blocks when a tile has <= 16 rows), plain a*b+c
-// elsewhere — then scale, causal mask, online max/sum, normalise.
+// elsewhere — then scale, causal mask, online max/sum, normalise.  The
+// keys and values are the t rows appended by this prefill (cache rows
+// cache_off ..): attention.rs:200-244 attends among the new tokens only.
 // grid (n_heads, t): one workgroup per (head, query row).
 __device__ __forceinline__ bool sgemm_fused(int tqs, int il, int ncols, int j, bool gemv_trans_b) {
   if (tqs <= 16) {  // f32GemvRow per row (matmul.zig:142-155)
@@ -333,7 +340,7 @@ __device__ __forceinline__ bool sgemm_fused(int tqs, int il, int ncols, int j, b
 __global__ void __launch_bounds__(256)
     k_attn_prefill(const float *__restrict__ q, const float *__restrict__ kc,
                    const float *__restrict__ vc, int t, int nh, int nkv, int hd, int max_seq,
-                   float *__restrict__ out) {
+                   int cache_off, float *__restrict__ out) {
   extern __shared__ float sm[];  // qs[hd] | e[t]
   float *qs = sm, *e = sm + hd;
   __shared__ float s_mx, s_inv;
@@ -348,10 +355,10 @@ __global__ void __launch_bounds__(256)
     float acc = 0.0f;
     if (sgemm_fused(tqs, il, t, j, true)) {
       for (int d = 0; d < hd; d++)
-        acc = __builtin_fmaf(qs[d], kc[kv_k_index(j, kvh, d, hd, max_seq)], acc);
+        acc = __builtin_fmaf(qs[d], kc[kv_k_index(cache_off + j, kvh, d, hd, max_seq)], acc);
     } else {
       for (int d = 0; d < hd; d++) {
-        const float p = qs[d] * kc[kv_k_index(j, kvh, d, hd, max_seq)];
+        const float p = qs[d] * kc[kv_k_index(cache_off + j, kvh, d, hd, max_seq)];
         acc = acc + p;
       }
     }
@@ -383,10 +390,10 @@ __global__ void __launch_bounds__(256)
     float acc = 0.0f;
     if (sgemm_fused(tqs, il, hd, d, false)) {
       for (int p = 0; p < t; p++)
-        acc = __builtin_fmaf(e[p], vc[kv_v_index(p, kvh, d, hd, max_seq)], acc);
+        acc = __builtin_fmaf(e[p], vc[kv_v_index(cache_off + p, kvh, d, hd, max_seq)], acc);
     } else {
       for (int p = 0; p < t; p++) {
-        const float m = e[p] * vc[kv_v_index(p, kvh, d, hd, max_seq)];
+        const float m = e[p] * vc[kv_v_index(cache_off + p, kvh, d, hd, max_seq)];
         acc = acc + m;
       }
     }
@@ -396,7 +403,7 @@ __global__ void __launch_bounds__(256)
 
 syn_status_t launch_attention_prefill(const float *q, const float *kcache, const float *vcache,
                                       int t, int n_heads, int n_kv, int head_dim, int max_seq,
-                                      float *scores, float *out, hipStream_t s) {
+                                      float *scores, float *out, hipStream_t s, int cache_off) {
   (void)scores;
   const size_t shm = (size_t)(head_dim + t) * sizeof(float);
   if (shm > 64 * 1024) {
@@ -404,7 +411,7 @@ syn_status_t launch_attention_prefill(const float *q, const float *kcache, const
     return SYN_ERR_INVALID_ARG;
   }
   hipLaunchKernelGGL(k_attn_prefill, dim3(n_heads, t), dim3(256), shm, s, q, kcache, vcache, t,
-                     n_heads, n_kv, head_dim, max_seq, out);
+                     n_heads, n_kv, head_dim, max_seq, cache_off, out);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
 }
@@ -554,6 +561,19 @@ __global__ void k_step_advance(StepState *st, int add_pos) {
 
 syn_status_t launch_step_advance(StepState *state, int add_pos, hipStream_t s) {
   hipLaunchKernelGGL(k_step_advance, dim3(1), dim3(64), 0, s, state, add_pos);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
+
+__global__ void k_state_set(StepState *st, int pos, int nhist) {
+  if (threadIdx.x == 0) {
+    if (pos >= 0) st->pos = pos;
+    st->nhist = nhist;
+  }
+}
+
+syn_status_t launch_state_set(StepState *state, int pos, int nhist, hipStream_t s) {
+  hipLaunchKernelGGL(k_state_set, dim3(1), dim3(64), 0, s, state, pos, nhist);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
 }

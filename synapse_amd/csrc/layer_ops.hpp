@@ -34,6 +34,8 @@ struct StepState {  // device-resident decode state (read by kernels in a graph)
   uint32_t token;   // last sampled token
   int step;         // decode steps taken since the last reset of the counter
   float margin;     // top1 - top2 logit of the last argmax
+  int nhist = -1;   // tokens of the history the sampler's repetition penalty
+                    // reads (-1: all `step` sampled so far)
 };
 
 // x[r] = embed[ids[r]] (zero row for ids >= vocab), ids on device
@@ -45,22 +47,24 @@ syn_status_t launch_rmsnorm_quant(float *x, const float *delta, const float *w, 
                                   int rows, int hidden, int8_t *xq, int ldq, float *sx,
                                   float *normed, hipStream_t s);
 // headwise q/k RMSNorm + RoPE (rotate-half) + KV-cache append for `rows` tokens
-// at positions pos0 + r (pos0 = *d_pos if d_pos else pos_static).
+// at positions pos0 + r (pos0 = *d_pos if d_pos else pos_static), written to
+// cache rows pos0 + r + cache_off.
 syn_status_t launch_qk_norm_rope_kv(const float *qkv, int ldqkv, int rows, int n_heads,
                                     int n_kv, int head_dim, const float *q_norm,
                                     const float *k_norm, float eps, const float *rope_cos,
                                     const float *rope_sin, const int *d_pos, int pos_static,
                                     float *q_out, float *kcache, float *vcache, int max_seq,
-                                    hipStream_t s);
+                                    hipStream_t s, int cache_off = 0);
 // single-query GQA attention over positions [0, *d_pos] (cache already holds
 // the new token), ops/attention.rs:24-147
 syn_status_t launch_attention_decode(const float *q, const float *kcache, const float *vcache,
                                      const int *d_pos, int n_heads, int n_kv, int head_dim,
                                      float *scores, int max_seq, float *out, hipStream_t s);
-// causal attention over `t` prompt tokens, exports.zig:1364-1478 per head
+// causal attention over `t` prompt tokens (cache rows cache_off ..),
+// exports.zig:1364-1478 per head
 syn_status_t launch_attention_prefill(const float *q, const float *kcache, const float *vcache,
                                       int t, int n_heads, int n_kv, int head_dim, int max_seq,
-                                      float *scores, float *out, hipStream_t s);
+                                      float *scores, float *out, hipStream_t s, int cache_off = 0);
 // h = silu(gate) * up (int8.rs:500-503), then quantize rows of h
 syn_status_t launch_swiglu_quant(const float *gu, int ldgu, int rows, int inter, int8_t *hq,
                                  int ldq, float *sh, hipStream_t s);
@@ -74,6 +78,8 @@ syn_status_t launch_argmax(const float *logits, int n, float *part_v, int *part_
                            float *margin_hist, hipStream_t s);
 // state->pos += add_pos; state->step += 1
 syn_status_t launch_step_advance(StepState *state, int add_pos, hipStream_t s);
+// state->pos = pos (if pos >= 0), state->nhist = nhist
+syn_status_t launch_state_set(StepState *state, int pos, int nhist, hipStream_t s);
 // elementwise residual: x += d
 syn_status_t launch_add(float *x, const float *d, int n, hipStream_t s);
 

@@ -171,7 +171,8 @@ struct syn_hip_qlm_s {
   }
 
   // ---------------------------------------------------------- one layer
-  syn_status_t layer(size_t l, int rows, bool prefill, hipStream_t s) {
+  // cache_off (prefill only): cache row of the first of `rows` tokens
+  syn_status_t layer(size_t l, int rows, bool prefill, hipStream_t s, int cache_off = 0) {
     QLayer &Ly = layers[l];
     const float eps = c.eps;
     const int nh = (int)c.n_heads, nkv = (int)c.n_kv_heads;
@@ -181,11 +182,12 @@ struct syn_hip_qlm_s {
     SYN_TRY(Ly.qkv.gemv(rows, xq.as<int8_t>(), ldh, sx.as<float>(), qkv.as<float>(), n_qkv, s));
     SYN_TRY(launch_qk_norm_rope_kv(qkv.as<float>(), (int)n_qkv, rows, nh, nkv, (int)hd,
                                    qn(l), kn(l), eps, rope_cos.as<float>(),
-                                   rope_sin.as<float>(), prefill ? nullptr : &st()->pos, 0, qrot.as<float>(), kc_l(l),
-                                   vc_l(l), (int)S, s));
+                                   rope_sin.as<float>(), prefill ? nullptr : &st()->pos, 0,
+                                   qrot.as<float>(), kc_l(l), vc_l(l), (int)S, s,
+                                   prefill ? cache_off : 0));
     if (prefill)
       SYN_TRY(launch_attention_prefill(qrot.as<float>(), kc_l(l), vc_l(l), rows, nh, nkv,
-                                       (int)hd, (int)S, nullptr, attn.as<float>(), s));
+                                       (int)hd, (int)S, nullptr, attn.as<float>(), s, cache_off));
     else
       SYN_TRY(launch_attention_decode(qrot.as<float>(), kc_l(l), vc_l(l), &st()->pos, nh, nkv,
                                       (int)hd, scores.as<float>(), (int)S, attn.as<float>(), s));
@@ -382,6 +384,15 @@ struct syn_hip_qlm_s {
     return SYN_OK;
   }
 
+  // the layers of QuantizedCausalLM::forward_prefill (int8.rs:593-618) over
+  // n tokens whose ids are on the device, appended at cache rows cache_off ..
+  syn_status_t prefill_rows(const uint32_t *d_ids, int n, int cache_off) {
+    SYN_TRY(launch_embed(embed.as<float>(), d_ids, n, (int)h, (int)vocab, x.as<float>(), stream));
+    for (size_t l = 0; l < L; l++) SYN_TRY(layer(l, n, true, stream, cache_off));
+    return SYN_OK;
+  }
+
+  // forward_prefill into an empty cache (the pipeline's fresh ModelState)
   syn_status_t prefill(const uint32_t *host_ids, size_t n) {
     if (n == 0 || n > S) {
       set_error("prefill length must be in [1, max_seq]");
@@ -389,10 +400,90 @@ struct syn_hip_qlm_s {
     }
     SYN_HIP(hipMemcpyAsync(ids.p, host_ids, n * 4, hipMemcpyHostToDevice, stream));
     SYN_TRY(set_state(0, 0, 0));
-    SYN_TRY(launch_embed(embed.as<float>(), ids.as<uint32_t>(), (int)n, (int)h, (int)vocab,
-                         x.as<float>(), stream));
-    for (size_t l = 0; l < L; l++) SYN_TRY(layer(l, (int)n, true, stream));
+    SYN_TRY(prefill_rows(ids.as<uint32_t>(), (int)n, 0));
     return head((int)n - 1, (int)n, stream);
+  }
+
+  // forward_prefill into the cache as it stands: the n new rows are appended
+  // after the cached ones, rotated at positions 0..n-1 and attending among
+  // themselves (cached_attention_prefill, ops/attention.rs:153-247)
+  syn_status_t prefill_append(const uint32_t *host_ids, size_t n) {
+    StepState cur;
+    SYN_TRY(get_state(&cur));
+    if (n == 0 || (size_t)cur.pos + n > S) {
+      set_error("prefill rows must be in [1, max_seq - cached rows]");
+      return SYN_ERR_INVALID_ARG;
+    }
+    SYN_HIP(hipMemcpyAsync(ids.p, host_ids, n * 4, hipMemcpyHostToDevice, stream));
+    SYN_TRY(prefill_rows(ids.as<uint32_t>(), (int)n, cur.pos));
+    return head((int)n - 1, (int)n, stream);
+  }
+
+  // KvCache.truncateTo (kvcache.zig:109-113): only a shorter length applies
+  syn_status_t truncate(size_t new_len) {
+    StepState cur;
+    SYN_TRY(get_state(&cur));
+    if (new_len < (size_t)cur.pos) SYN_TRY(set_state((int)new_len, cur.token, cur.step));
+    return SYN_OK;
+  }
+
+  // TextGenerator::generate_speculative (pipeline.rs:281-395) with max_new
+  // as the only stop condition.  QuantizedCausalLM has no draft forward
+  // (int8.rs:739), so a draft token is a full forward_one; the verify pass is
+  // forward_prefill of [last accepted, drafts] after truncating the cache to
+  // the round's start, its logits unused; every draft is accepted; when all k
+  // were, a bonus token comes from forward_one of the last draft.  Drafts
+  // sample with the penalty history as it stood at the round's start
+  // (generated_tokens); draw i of the seeded stream goes to sample call i.
+  // The loop runs on the stream without a host round trip: positions and
+  // counts follow from k and max_new alone.
+  syn_status_t generate_speculative(const uint32_t *prompt, size_t n_prompt, size_t max_new,
+                                    size_t k) {
+    if (n_prompt == 0 || n_prompt > S) {
+      set_error("prefill length must be in [1, max_seq]");
+      return SYN_ERR_INVALID_ARG;
+    }
+    // the rows and sample calls the loop will use
+    size_t pos = n_prompt, gen = 1, calls = 1, top = n_prompt;
+    while (gen < max_new) {
+      const size_t save = pos, acc = std::min(k, max_new - gen);
+      top = std::max(top, save + k + 1);
+      calls += k;
+      gen += acc;
+      pos = save + k + 1;
+      if (acc == k && gen < max_new) {
+        top = std::max(top, pos + 1);
+        pos += 1;
+        gen += 1;
+        calls += 1;
+      }
+    }
+    if (top > S || calls > S + 1) {
+      set_error("speculative decode: rows or sample calls exceed max_seq");
+      return SYN_ERR_INVALID_ARG;
+    }
+    if (use_graph) SYN_TRY(build_graph());
+    SYN_TRY(prefill(prompt, n_prompt));
+    pos = n_prompt;
+    gen = 1;
+    while (gen < max_new) {
+      const size_t save = pos, s0 = gen;
+      // draft: k forward_one + sample, penalty history = the s0 generated tokens
+      SYN_TRY(launch_state_set(st(), -1, (int)s0, stream));
+      for (size_t i = 0; i < k; i++) SYN_TRY(run_step());
+      // truncate to save, verify [history[s0-1], drafts] at cache rows save ..
+      SYN_TRY(prefill_rows(history.as<uint32_t>() + (s0 - 1), (int)(k + 1), (int)save));
+      SYN_TRY(launch_state_set(st(), (int)(save + k + 1), -1, stream));
+      const size_t acc = std::min(k, max_new - gen);
+      gen += acc;
+      pos = save + k + 1;
+      if (acc == k && gen < max_new) {  // bonus token
+        SYN_TRY(run_step());
+        gen += 1;
+        pos += 1;
+      }
+    }
+    return SYN_OK;
   }
 };
 
@@ -712,6 +803,32 @@ syn_status_t syn_hip_qlm_forward_prefill(syn_hip_qlm_t *m, const uint32_t *ids, 
   return SYN_OK;
 }
 
+syn_status_t syn_hip_qlm_forward_prefill_append(syn_hip_qlm_t *m, const uint32_t *ids,
+                                                size_t n, float *host_logits) {
+  SYN_TRY(check_model(m));
+  if (!ids) return SYN_ERR_NULL_PTR;
+  SYN_TRY(m->prefill_append(ids, n));
+  if (host_logits)
+    SYN_HIP(hipMemcpyAsync(host_logits, m->logits.p, m->vocab * 4, hipMemcpyDeviceToHost,
+                           m->stream));
+  SYN_HIP(hipStreamSynchronize(m->stream));
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_qlm_truncate(syn_hip_qlm_t *m, size_t new_len) {
+  SYN_TRY(check_model(m));
+  return m->truncate(new_len);
+}
+
+syn_status_t syn_hip_qlm_cache_len(syn_hip_qlm_t *m, size_t *out_len) {
+  SYN_TRY(check_model(m));
+  if (!out_len) return SYN_ERR_NULL_PTR;
+  StepState cur;
+  SYN_TRY(m->get_state(&cur));
+  *out_len = (size_t)cur.pos;
+  return SYN_OK;
+}
+
 syn_status_t syn_hip_qlm_forward_one(syn_hip_qlm_t *m, uint32_t token, float *host_logits) {
   SYN_TRY(check_model(m));
   StepState cur;
@@ -742,6 +859,23 @@ syn_status_t syn_hip_qlm_generate(syn_hip_qlm_t *m, const uint32_t *prompt, size
   if (m->use_graph) SYN_TRY(m->build_graph());
   SYN_TRY(m->prefill(prompt, n_prompt));
   for (size_t i = 1; i < max_new; i++) SYN_TRY(m->run_step());
+  SYN_HIP(hipMemcpyAsync(out_tokens, m->history.p, max_new * 4, hipMemcpyDeviceToHost,
+                         m->stream));
+  if (out_margins)
+    SYN_HIP(hipMemcpyAsync(out_margins, m->mhist.p, max_new * 4, hipMemcpyDeviceToHost,
+                           m->stream));
+  SYN_HIP(hipStreamSynchronize(m->stream));
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_qlm_generate_speculative(syn_hip_qlm_t *m, const uint32_t *prompt,
+                                              size_t n_prompt, size_t max_new, size_t k,
+                                              uint32_t *out_tokens, float *out_margins) {
+  SYN_TRY(check_model(m));
+  if (!prompt || !out_tokens) return SYN_ERR_NULL_PTR;
+  if (k == 0) return syn_hip_qlm_generate(m, prompt, n_prompt, max_new, out_tokens, out_margins);
+  if (max_new == 0) return SYN_OK;
+  SYN_TRY(m->generate_speculative(prompt, n_prompt, max_new, k));
   SYN_HIP(hipMemcpyAsync(out_tokens, m->history.p, max_new * 4, hipMemcpyDeviceToHost,
                          m->stream));
   if (out_margins)

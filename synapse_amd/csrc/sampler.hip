@@ -180,7 +180,7 @@ __global__ void __launch_bounds__(kSampNT)
   __shared__ int s_err;  // block-uniform error flag
   const int tid = threadIdx.x;
   const int step = st ? st->step : 0;
-  const int nh = st ? step : nh_arg;
+  const int nh = st ? (st->nhist >= 0 ? st->nhist : step) : nh_arg;
   const float u = u_src[st ? step : 0];
   if (tid == 0) s_err = 0;
 

@@ -98,6 +98,10 @@ SIGNATURES = {
     "syn_hip_qlm_forward_prefill": (ST, [P, P, SZ, P]),
     "syn_hip_qlm_forward_one": (ST, [P, C.c_uint32, P]),
     "syn_hip_qlm_generate": (ST, [P, P, SZ, SZ, P, P]),
+    "syn_hip_qlm_forward_prefill_append": (ST, [P, P, SZ, P]),
+    "syn_hip_qlm_truncate": (ST, [P, SZ]),
+    "syn_hip_qlm_cache_len": (ST, [P, C.POINTER(SZ)]),
+    "syn_hip_qlm_generate_speculative": (ST, [P, P, SZ, SZ, SZ, P, P]),
     "syn_hip_qlm_decode_timed": (ST, [P, SZ, C.POINTER(C.c_float)]),
     "syn_hip_qlm_time_lm_head": (ST, [P, SZ, SZ, C.POINTER(C.c_float)]),
     "syn_hip_qlm_set_options": (ST, [P, C.c_int, C.c_int]),
@@ -509,6 +513,34 @@ class QuantizedCausalLM:
         margins = np.zeros(max_new, np.float32)
         check(lib().syn_hip_qlm_generate(self.h, ptr(prompt), prompt.size, max_new, ptr(toks),
                                          ptr(margins)), "generate")
+        return toks, margins
+
+    def prefill_append(self, ids) -> np.ndarray:
+        """forward_prefill into the cache as it stands (rows appended after the
+        cached ones, rotated from position 0, attending among themselves)."""
+        ids = np.ascontiguousarray(ids, np.uint32)
+        logits = np.empty(self.cfg["vocab"], np.float32)
+        check(lib().syn_hip_qlm_forward_prefill_append(self.h, ptr(ids), ids.size, ptr(logits)),
+              "forward_prefill_append")
+        return logits
+
+    def truncate(self, new_len: int):
+        """KVCache::truncate_to: a shorter cache length applies, a longer one is ignored."""
+        check(lib().syn_hip_qlm_truncate(self.h, new_len), "truncate")
+
+    def cache_len(self) -> int:
+        n = SZ()
+        check(lib().syn_hip_qlm_cache_len(self.h, C.byref(n)), "cache_len")
+        return n.value
+
+    def generate_speculative(self, prompt, max_new: int, k: int):
+        """generate_speculative (pipeline.rs:281-395) with speculative_k = k."""
+        prompt = np.ascontiguousarray(prompt, np.uint32)
+        toks = np.zeros(max_new, np.uint32)
+        margins = np.zeros(max_new, np.float32)
+        check(lib().syn_hip_qlm_generate_speculative(self.h, ptr(prompt), prompt.size, max_new, k,
+                                                     ptr(toks), ptr(margins)),
+              "generate_speculative")
         return toks, margins
 
     def decode_timed(self, steps: int) -> float:
