@@ -133,12 +133,25 @@ def secondary(hip, np):
     m.init_synthetic(SEED_BASE, 0.02)
     ids = np.array(_ids(256, cfg["vocab"], PROMPT_SEED), np.uint32)
     pf_ms, dec_ms = m.time(ids, 128)
+    # speculative decode with the reference's default draft (first L/3 layers)
+    spec = {}
+    for name, fn in (("generate", lambda: m.generate(ids, 64)),
+                     ("speculative_k4", lambda: m.generate_speculative(ids, 64, 4))):
+        fn()
+        t = time.perf_counter()
+        fn()
+        spec[name] = {"ms": round((time.perf_counter() - t) * 1e3, 2)}
+        spec[name]["tok_s"] = round(64e3 / spec[name]["ms"], 1)
+    spec["note"] = ("256-token prompt + 64 greedy tokens per call; drafts from the first "
+                    f"{LLAMA3B['n_layers'] // 3} of {LLAMA3B['n_layers']} layers "
+                    "(forward_one_draft), every draft accepted")
     m.close()
     wb = kquant_weight_bytes(LLAMA3B)
     out["config3_kquant_decode_llama3b"] = {
         "prefill_256_ms": round(pf_ms, 2), "decode_tok_s": round(128e3 / dec_ms, 1),
         "decode_ms_per_token": round(dec_ms / 128, 3), "weight_bytes_per_token": wb,
-        "decode_weight_gbs": round(wb / (dec_ms / 128 * 1e-3) / 1e9, 1)}
+        "decode_weight_gbs": round(wb / (dec_ms / 128 * 1e-3) / 1e9, 1),
+        "speculative_decode": spec}
     out["config4_q8_0_prefill_mistral7b"] = [mb.q8_0_prefill_suite(512),
                                              mb.q8_0_prefill_suite(2048)]
     out["int8_prefill_gemm"] = [mb.int8_prefill_record(128, 1024, 3072),
@@ -160,6 +173,27 @@ def secondary(hip, np):
     out["config5_mamba370m"] = mam
     out["seconds"] = round(time.perf_counter() - t0, 1)
     return out
+
+
+def speculative_record(model, np, k: int = 4, max_new: int = 64, reps: int = 3):
+    """generate vs generate_speculative (speculative_k = k) on the config-1
+    model: whole calls (16-token prefill + max_new tokens, tokens read back),
+    wall clock, best of `reps`.  The INT8 model drafts with full forward_one
+    steps (int8.rs:739), so each round adds a (k+1)-row verify prefill."""
+    ids = np.array(prompt_ids(), np.uint32)
+    res = {}
+    for name, fn in (("generate", lambda: model.generate(ids, max_new)),
+                     (f"speculative_k{k}", lambda: model.generate_speculative(ids, max_new, k))):
+        fn()
+        best = float("inf")
+        for _ in range(reps):
+            t = time.perf_counter()
+            fn()
+            best = min(best, time.perf_counter() - t)
+        res[name] = {"ms": round(best * 1e3, 2), "tok_s": round(max_new / best, 1)}
+    res["note"] = (f"{PROMPT}-token prompt + {max_new} tokens per call, greedy; drafts are full "
+                   "forward_one steps (no INT8 draft model in the reference), every draft accepted")
+    return res
 
 
 def cpu_baseline(budget_s: float):
@@ -240,6 +274,7 @@ def main():
     lm_ms = (model.time_lm_head(args.lm_head_iters) if args.unfused
              else model.time_lm_head_rotating(2 * args.lm_head_iters))
     lm_gbs = lm_head_bytes(QWEN3) / (lm_ms * 1e-3) / 1e9
+    spec = None if args.no_secondary else speculative_record(model, np)
     model.close()
 
     line = {
@@ -279,6 +314,7 @@ def main():
     }
     if not args.no_secondary:
         line["secondary"] = secondary(hip, np)
+        line["secondary"]["config1_speculative_decode"] = spec
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
     print(json.dumps(line), flush=True)

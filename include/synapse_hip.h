@@ -442,6 +442,25 @@ syn_status_t syn_hip_klm_forward_prefill(syn_hip_klm_t *m, const uint32_t *ids, 
 syn_status_t syn_hip_klm_forward_one(syn_hip_klm_t *m, uint32_t token, float *host_logits);
 syn_status_t syn_hip_klm_generate(syn_hip_klm_t *m, const uint32_t *prompt, size_t n_prompt,
                                   size_t max_new, uint32_t *out_tokens, float *out_margins);
+/* forward_prefill into the cache as it stands (causal_lm.rs:195-239 with
+ * cached_attention_prefill, ops/attention.rs:153-247); truncate_to and
+ * current_len of the cache (kv_cache/cache.rs:301-312, kvcache.zig:109-113). */
+syn_status_t syn_hip_klm_forward_prefill_append(syn_hip_klm_t *m, const uint32_t *ids,
+                                                size_t n, float *host_logits);
+syn_status_t syn_hip_klm_truncate(syn_hip_klm_t *m, size_t new_len);
+syn_status_t syn_hip_klm_cache_len(syn_hip_klm_t *m, size_t *out_len);
+/* CausalLM::forward_one_draft (causal_lm.rs:283-323): the first n_layers
+ * layers, zero K/V rows appended to the others, final norm, lm_head. */
+syn_status_t syn_hip_klm_forward_one_draft(syn_hip_klm_t *m, uint32_t token, size_t n_layers,
+                                           float *host_logits);
+/* Greedy speculative generate (generation/pipeline.rs:281-395): k drafts per
+ * round from forward_one_draft with draft_layers layers (0: n_layers / 3,
+ * pipeline.rs:28, 295-299), truncate, verify forward_prefill, accept all,
+ * bonus token; enqueued without a host round trip.  k = 0 is generate. */
+syn_status_t syn_hip_klm_generate_speculative(syn_hip_klm_t *m, const uint32_t *prompt,
+                                              size_t n_prompt, size_t max_new, size_t k,
+                                              size_t draft_layers, uint32_t *out_tokens,
+                                              float *out_margins);
 /* hipEvent timing of one prefill of `prompt` and `steps` greedy decode steps. */
 syn_status_t syn_hip_klm_time(syn_hip_klm_t *m, const uint32_t *prompt, size_t n_prompt,
                               size_t steps, float *prefill_ms, float *decode_ms);

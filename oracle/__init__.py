@@ -125,6 +125,10 @@ def _declare(L):
         "orc_flm_set_norms": (C.c_int, [P, C.c_size_t, P, P, P, P]),
         "orc_flm_set_final_norm": (C.c_int, [P, P]),
         "orc_flm_prefill": (C.c_int, [P, P, SZ, P]),
+        "orc_flm_prefill_append": (C.c_int, [P, P, SZ, P]),
+        "orc_flm_truncate": (None, [P, SZ]),
+        "orc_flm_cur_len": (SZ, [P]),
+        "orc_flm_forward_one_draft": (C.c_int, [P, C.c_uint32, SZ, P]),
         "orc_flm_forward_one": (C.c_int, [P, C.c_uint32, P]),
         "orc_flm_generate": (C.c_int, [P, P, SZ, SZ, P, P]),
         "orc_swiglu_fused": (None, [P, P, P, SZ]),
@@ -465,58 +469,10 @@ class QuantizedCausalLM:
         return int(lib().orc_qlm_cur_len(self.h))
 
     def generate_speculative(self, prompt, max_new: int, k: int, sampler=None, seed: int = 0):
-        """TextGenerator::generate_speculative (generation/pipeline.rs:281-395)
-        on this model, max_new_tokens as the only stop condition.
-        QuantizedCausalLM has no forward_one_draft (int8.rs:739), so the
-        trait default (models/traits.rs:64-68) drafts with forward_one.
-        sampler: None (GreedySampler) or CombinedSampler settings
-        (sample_combined keywords), fed by StdRng::seed_from_u64(seed) one
-        draw per sample call.  Returns (tokens, margins): the top1 - top2
-        logit of each greedy choice (zeros when sampling)."""
-        k = max(1, k)  # pipeline.rs:294
-        draws = stdrng_f32(seed, max_new + k + 1) if sampler is not None else None
-        calls = [0]
-        margins = []
-
-        def sample(logits, generated):  # pipeline.rs:475-489
-            if sampler is None:
-                tok = argmax(logits)
-                second = np.max(np.delete(logits, tok)) if logits.size > 1 else np.float32(-np.inf)
-                margins.append(np.float32(logits[tok] - second))
-            else:
-                tok = sample_combined(logits, np.array(generated, np.uint32),
-                                      u=float(draws[calls[0]]), **sampler)
-                margins.append(np.float32(0.0))
-            calls[0] += 1
-            return int(tok)
-
-        gen = []
-        out_margins = []
-        logits = self.prefill(prompt)
-        gen.append(sample(logits, gen))
-        out_margins.append(margins[-1])
-        while len(gen) < max_new:  # stopping.rs:39-42
-            save = self.cache_len()
-            drafts, dmarg = [], []
-            last = gen[-1]
-            for _ in range(k):
-                tok = sample(self.forward_one(last), gen)
-                drafts.append(tok)
-                dmarg.append(margins[-1])
-                last = tok
-            self.truncate(save)
-            self.prefill_append([gen[-1]] + drafts)  # verify; logits unused
-            accepted = 0
-            for tok, mg in zip(drafts, dmarg):
-                gen.append(tok)
-                out_margins.append(mg)
-                accepted += 1
-                if len(gen) >= max_new:
-                    break
-            if accepted == k and len(gen) < max_new:  # bonus token
-                gen.append(sample(self.forward_one(gen[-1]), gen))
-                out_margins.append(margins[-1])
-        return np.array(gen, np.uint32), np.array(out_margins, np.float32)
+        """generate_speculative (generation/pipeline.rs:281-395).
+        QuantizedCausalLM has no forward_one_draft (int8.rs:739), so the trait
+        default (models/traits.rs:64-68) drafts with forward_one."""
+        return speculative_loop(self, prompt, max_new, k, self.forward_one, sampler, seed)
 
     def close(self):
         if self.h:
@@ -585,6 +541,31 @@ class CausalLM:
         self._check(lib().orc_flm_forward_one(self.h, int(token), _p(out)))
         return out
 
+    def forward_one_draft(self, token: int, n_draft: int):
+        """CausalLM::forward_one_draft (causal_lm.rs:283-323)."""
+        out = np.empty(self.cfg["vocab"], np.float32)
+        self._check(lib().orc_flm_forward_one_draft(self.h, int(token), n_draft, _p(out)))
+        return out
+
+    def prefill_append(self, ids):
+        ids = np.ascontiguousarray(ids, np.uint32)
+        out = np.empty(self.cfg["vocab"], np.float32)
+        self._check(lib().orc_flm_prefill_append(self.h, _p(ids), ids.size, _p(out)))
+        return out
+
+    def truncate(self, new_len: int):
+        lib().orc_flm_truncate(self.h, new_len)
+
+    def cache_len(self) -> int:
+        return int(lib().orc_flm_cur_len(self.h))
+
+    def generate_speculative(self, prompt, max_new: int, k: int, draft_layers: int = 0):
+        """generate_speculative (pipeline.rs:281-395), greedy: drafts from the
+        first draft_layers layers (0: num_layers / 3, pipeline.rs:28, 295-299)."""
+        n = draft_layers if draft_layers > 0 else self.cfg["n_layers"] // 3
+        return speculative_loop(self, prompt, max_new, k,
+                                lambda t: self.forward_one_draft(t, n))
+
     def generate(self, prompt, max_new: int):
         prompt = np.ascontiguousarray(prompt, np.uint32)
         toks = np.zeros(max_new, np.uint32)
@@ -647,3 +628,56 @@ class QuantizedMamba:
             self.close()
         except Exception:
             pass
+
+
+def speculative_loop(model, prompt, max_new: int, k: int, draft, sampler=None, seed: int = 0):
+    """TextGenerator::generate_speculative (generation/pipeline.rs:281-395)
+    with max_new_tokens as the only stop condition.  model: prefill,
+    prefill_append, forward_one, truncate, cache_len; draft(token) -> logits
+    is the model's forward_one_draft.  sampler: None (GreedySampler) or
+    CombinedSampler settings (sample_combined keywords), fed by
+    StdRng::seed_from_u64(seed) one draw per sample call.  Returns (tokens,
+    margins): the top1 - top2 logit of each greedy choice (zeros when
+    sampling)."""
+    k = max(1, k)  # pipeline.rs:294
+    draws = stdrng_f32(seed, max_new + k + 1) if sampler is not None else None
+    calls = [0]
+    margins = []
+
+    def sample(logits, generated):  # pipeline.rs:475-489
+        if sampler is None:
+            tok = argmax(logits)
+            second = np.max(np.delete(logits, tok)) if logits.size > 1 else np.float32(-np.inf)
+            margins.append(np.float32(logits[tok] - second))
+        else:
+            tok = sample_combined(logits, np.array(generated, np.uint32),
+                                  u=float(draws[calls[0]]), **sampler)
+            margins.append(np.float32(0.0))
+        calls[0] += 1
+        return int(tok)
+
+    gen, out_margins = [], []
+    gen.append(sample(model.prefill(prompt), gen))
+    out_margins.append(margins[-1])
+    while len(gen) < max_new:  # stopping.rs:39-42
+        save = model.cache_len()
+        drafts, dmarg = [], []
+        last = gen[-1]
+        for _ in range(k):
+            tok = sample(draft(last), gen)
+            drafts.append(tok)
+            dmarg.append(margins[-1])
+            last = tok
+        model.truncate(save)
+        model.prefill_append([gen[-1]] + drafts)  # verify; logits unused
+        accepted = 0
+        for tok, mg in zip(drafts, dmarg):
+            gen.append(tok)
+            out_margins.append(mg)
+            accepted += 1
+            if len(gen) >= max_new:
+                break
+        if accepted == k and len(gen) < max_new:  # bonus token
+            gen.append(sample(model.forward_one(gen[-1]), gen))
+            out_margins.append(margins[-1])
+    return np.array(gen, np.uint32), np.array(out_margins, np.float32)

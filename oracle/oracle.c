@@ -1214,11 +1214,12 @@ static void flm_layer(orc_flm *m, size_t l, float *x, size_t t, int prefill) {
     orc_rmsnorm(q, m->q_nw + l * hd, c->eps, t * nh, hd, q);
     orc_rmsnorm(k, m->k_nw + l * hd, c->eps, t * nkv, hd, k);
   }
-  size_t pos0 = prefill ? 0 : m->cur;
+  /* prefill: rotated at 0..t-1, appended at rows m->cur.. (as the INT8 layer) */
+  size_t pos0 = prefill ? 0 : m->cur, row0 = m->cur;
   orc_rope_apply(q, m->rope_cos, m->rope_sin, t, nh, hd, pos0);
   orc_rope_apply(k, m->rope_cos, m->rope_sin, t, nkv, hd, pos0);
-  memcpy(kcl + pos0 * kvd, k, t * kvd * 4);
-  memcpy(vcl + pos0 * kvd, v, t * kvd * 4);
+  memcpy(kcl + row0 * kvd, k, t * kvd * 4);
+  memcpy(vcl + row0 * kvd, v, t * kvd * 4);
   if (prefill) {
     size_t groups = nh / nkv;
     float *qh = (float *)malloc(t * hd * 4), *kh = (float *)malloc(t * hd * 4);
@@ -1235,7 +1236,7 @@ static void flm_layer(orc_flm *m, size_t l, float *x, size_t t, int prefill) {
     }
     free(qh); free(kh); free(vh); free(oh);
   } else {
-    orc_attention_decode(q, kcl, vcl, pos0 + 1, nh, nkv, hd, attn);
+    orc_attention_decode(q, kcl, vcl, row0 + 1, nh, nkv, hd, attn);
   }
   flm_matmul_t(attn, W[3], t, qd, h, o);
   for (size_t i = 0; i < t * h; i++) x[i] = x[i] + o[i];
@@ -1256,8 +1257,10 @@ static void flm_head(orc_flm *m, const float *xlast, float *logits) {
   free(normed);
 }
 
-int orc_flm_prefill(orc_flm *m, const uint32_t *ids, size_t n, float *logits) {
-  if (n == 0 || n > m->c.max_seq) return ORC_ERR_INVALID_ARG;
+/* CausalLM::forward_prefill (causal_lm.rs:195-239) into the cache as it
+ * stands: rows appended after the m->cur cached ones */
+int orc_flm_prefill_append(orc_flm *m, const uint32_t *ids, size_t n, float *logits) {
+  if (n == 0 || m->cur + n > m->c.max_seq) return ORC_ERR_INVALID_ARG;
   size_t h = m->c.hidden;
   float *x = (float *)malloc(n * h * 4);
   for (size_t t = 0; t < n; t++) {
@@ -1265,10 +1268,42 @@ int orc_flm_prefill(orc_flm *m, const uint32_t *ids, size_t n, float *logits) {
     else memset(x + t * h, 0, h * 4);
   }
   for (size_t l = 0; l < m->c.n_layers; l++) flm_layer(m, l, x, n, 1);
-  m->cur = n;
+  m->cur += n;
   flm_head(m, x + (n - 1) * h, logits);
   free(x);
   return ORC_OK;
+}
+
+void orc_flm_truncate(orc_flm *m, size_t new_len) {
+  if (new_len < m->cur) m->cur = new_len;  /* kvcache.zig:109-113 */
+}
+
+size_t orc_flm_cur_len(const orc_flm *m) { return m->cur; }
+
+/* CausalLM::forward_one_draft (causal_lm.rs:283-323): the first n_draft
+ * layers, zero K and V rows appended to the others, final norm, lm_head */
+int orc_flm_forward_one_draft(orc_flm *m, uint32_t token, size_t n_draft, float *logits) {
+  if (m->cur >= m->c.max_seq) return ORC_ERR_INVALID_ARG;
+  size_t h = m->c.hidden, kvd = m->c.n_kv_heads * m->c.head_dim;
+  size_t n = n_draft < m->c.n_layers ? n_draft : m->c.n_layers;
+  float *x = (float *)malloc(h * 4);
+  if (token < m->c.vocab) memcpy(x, m->embed + (size_t)token * h, h * 4);
+  else memset(x, 0, h * 4);
+  for (size_t l = 0; l < n; l++) flm_layer(m, l, x, 1, 0);
+  for (size_t l = n; l < m->c.n_layers; l++) {
+    memset(m->kc + (l * m->c.max_seq + m->cur) * kvd, 0, kvd * 4);
+    memset(m->vc + (l * m->c.max_seq + m->cur) * kvd, 0, kvd * 4);
+  }
+  m->cur += 1;
+  flm_head(m, x, logits);
+  free(x);
+  return ORC_OK;
+}
+
+int orc_flm_prefill(orc_flm *m, const uint32_t *ids, size_t n, float *logits) {
+  if (n == 0 || n > m->c.max_seq) return ORC_ERR_INVALID_ARG;
+  m->cur = 0;
+  return orc_flm_prefill_append(m, ids, n, logits);
 }
 
 int orc_flm_forward_one(orc_flm *m, uint32_t token, float *logits) {

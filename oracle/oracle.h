@@ -141,6 +141,10 @@ int orc_flm_set_norms(orc_flm *m, size_t layer, const float *attn, const float *
 int orc_flm_set_final_norm(orc_flm *m, const float *w);
 void orc_flm_reset(orc_flm *m);
 int orc_flm_prefill(orc_flm *m, const uint32_t *ids, size_t n, float *logits);
+int orc_flm_prefill_append(orc_flm *m, const uint32_t *ids, size_t n, float *logits);
+void orc_flm_truncate(orc_flm *m, size_t new_len);
+size_t orc_flm_cur_len(const orc_flm *m);
+int orc_flm_forward_one_draft(orc_flm *m, uint32_t token, size_t n_draft, float *logits);
 int orc_flm_forward_one(orc_flm *m, uint32_t token, float *logits);
 int orc_flm_generate(orc_flm *m, const uint32_t *prompt, size_t n_prompt, size_t max_new,
                      uint32_t *out_tokens, float *margins);

@@ -41,6 +41,7 @@ struct syn_hip_klm_s {
 
   ~syn_hip_klm_s() {
     if (graph) (void)hipGraphExecDestroy(graph);
+    if (draft_graph) (void)hipGraphExecDestroy(draft_graph);
     if (stream) (void)hipStreamDestroy(stream);
   }
   // per-layer KV caches in the decode attention's tiled layout (layer_ops.hpp)
@@ -137,7 +138,8 @@ struct syn_hip_klm_s {
     return SYN_OK;
   }
 
-  syn_status_t layer(size_t l, int rows, bool prefill, hipStream_t s) {
+  // cache_off (prefill only): cache row of the first of `rows` tokens
+  syn_status_t layer(size_t l, int rows, bool prefill, hipStream_t s, int cache_off = 0) {
     Layer &Ly = layers[l];
     const float eps = c.base.eps;
     const int nh = (int)c.base.n_heads, nkv = (int)c.base.n_kv_heads;
@@ -158,10 +160,11 @@ struct syn_hip_klm_s {
       SYN_TRY(launch_qk_norm_rope_kv(qkv.as<float>(), (int)n_qkv, rows, nh, nkv, (int)hd, qn, kn,
                                      eps, rope_cos.as<float>(), rope_sin.as<float>(),
                                      prefill ? nullptr : &st()->pos, 0, qrot.as<float>(),
-                                     kc_l(l), vc_l(l), (int)S, s));
+                                     kc_l(l), vc_l(l), (int)S, s, prefill ? cache_off : 0));
       if (prefill)
         SYN_TRY(launch_attention_prefill(qrot.as<float>(), kc_l(l), vc_l(l), rows, nh, nkv,
-                                         (int)hd, (int)S, nullptr, attn.as<float>(), s));
+                                         (int)hd, (int)S, nullptr, attn.as<float>(), s,
+                                         cache_off));
       else
         SYN_TRY(launch_attention_decode(qrot.as<float>(), kc_l(l), vc_l(l), &st()->pos, nh, nkv,
                                         (int)hd, scores.as<float>(), (int)S, attn.as<float>(),
@@ -188,10 +191,48 @@ struct syn_hip_klm_s {
     return launch_step_advance(st(), add_pos, s);
   }
 
-  syn_status_t decode_step(hipStream_t s) {
+  // n_layers < L: CausalLM::forward_one_draft (causal_lm.rs:283-323), the
+  // first n_layers layers, zero K/V rows appended to the others
+  syn_status_t decode_step(hipStream_t s, size_t n_layers = SIZE_MAX) {
+    const size_t n = std::min(n_layers, L);
     SYN_TRY(launch_embed(embed.as<float>(), &st()->token, 1, (int)h, (int)vocab, x.as<float>(), s));
-    for (size_t l = 0; l < L; l++) SYN_TRY(layer(l, 1, false, s));
+    for (size_t l = 0; l < n; l++) SYN_TRY(layer(l, 1, false, s));
+    if (n < L)
+      SYN_TRY(launch_kv_zero_rows(kc_l(n), vc_l(n), k_elems(), v_elems(), (int)(L - n),
+                                  (int)c.base.n_kv_heads, (int)hd, (int)S, st(), s));
     return head(0, 1, s);
+  }
+
+  // the draft step as its own graph (rebuilt when the layer count changes)
+  hipGraphExec_t draft_graph = nullptr;
+  size_t draft_layers = 0;
+  syn_status_t run_draft(size_t n_layers) {
+    if (!use_graph) return decode_step(stream, n_layers);
+    if (draft_graph && draft_layers != n_layers) {
+      SYN_HIP(hipStreamSynchronize(stream));
+      (void)hipGraphExecDestroy(draft_graph);
+      draft_graph = nullptr;
+    }
+    if (!draft_graph) {
+      hipGraph_t g;
+      SYN_HIP(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal));
+      syn_status_t st_ = decode_step(stream, n_layers);
+      hipError_t e = hipStreamEndCapture(stream, &g);
+      if (st_ != SYN_OK) {
+        if (e == hipSuccess) (void)hipGraphDestroy(g);
+        return st_;
+      }
+      if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture", __FILE__, __LINE__);
+      e = hipGraphInstantiate(&draft_graph, g, nullptr, nullptr, 0);
+      (void)hipGraphDestroy(g);
+      if (e != hipSuccess) {
+        draft_graph = nullptr;
+        return hip_fail(e, "hipGraphInstantiate", __FILE__, __LINE__);
+      }
+      draft_layers = n_layers;
+    }
+    SYN_HIP(hipGraphLaunch(draft_graph, stream));
+    return SYN_OK;
   }
 
   syn_status_t build_graph() {
@@ -235,6 +276,15 @@ struct syn_hip_klm_s {
     return SYN_OK;
   }
 
+  // the layers of CausalLM::forward_prefill (causal_lm.rs:195-224) over n
+  // tokens whose ids are on the device, appended at cache rows cache_off ..
+  syn_status_t prefill_rows(const uint32_t *d_ids, int n, int cache_off) {
+    SYN_TRY(launch_embed(embed.as<float>(), d_ids, n, (int)h, (int)vocab, x.as<float>(), stream));
+    for (size_t l = 0; l < L; l++) SYN_TRY(layer(l, n, true, stream, cache_off));
+    return SYN_OK;
+  }
+
+  // forward_prefill into an empty cache (a fresh ModelState)
   syn_status_t prefill(const uint32_t *host_ids, size_t n) {
     if (n == 0 || n > S) {
       set_error("prefill length must be in [1, max_seq]");
@@ -242,10 +292,79 @@ struct syn_hip_klm_s {
     }
     SYN_HIP(hipMemcpyAsync(ids.p, host_ids, n * 4, hipMemcpyHostToDevice, stream));
     SYN_TRY(set_state(0, 0, 0));
-    SYN_TRY(launch_embed(embed.as<float>(), ids.as<uint32_t>(), (int)n, (int)h, (int)vocab,
-                         x.as<float>(), stream));
-    for (size_t l = 0; l < L; l++) SYN_TRY(layer(l, (int)n, true, stream));
+    SYN_TRY(prefill_rows(ids.as<uint32_t>(), (int)n, 0));
     return head((int)n - 1, (int)n, stream);
+  }
+
+  // forward_prefill into the cache as it stands (rows appended after the
+  // cached ones, rotated from position 0, attending among themselves)
+  syn_status_t prefill_append(const uint32_t *host_ids, size_t n) {
+    StepState cur;
+    SYN_TRY(get_state(&cur));
+    if (n == 0 || (size_t)cur.pos + n > S) {
+      set_error("prefill rows must be in [1, max_seq - cached rows]");
+      return SYN_ERR_INVALID_ARG;
+    }
+    SYN_HIP(hipMemcpyAsync(ids.p, host_ids, n * 4, hipMemcpyHostToDevice, stream));
+    SYN_TRY(prefill_rows(ids.as<uint32_t>(), (int)n, cur.pos));
+    return head((int)n - 1, (int)n, stream);
+  }
+
+  syn_status_t truncate(size_t new_len) {  // kvcache.zig:109-113
+    StepState cur;
+    SYN_TRY(get_state(&cur));
+    if (new_len < (size_t)cur.pos) SYN_TRY(set_state((int)new_len, cur.token, cur.step));
+    return SYN_OK;
+  }
+
+  // generate_speculative (pipeline.rs:281-395), greedy, max_new as the stop
+  // condition; drafts from the first n_draft layers (forward_one_draft).
+  // Same loop as the INT8 decoder's: k draft steps, the verify prefill of
+  // [last accepted, drafts] at the round's start, every draft accepted, a
+  // bonus full step after a full round; enqueued without host round trips.
+  syn_status_t generate_speculative(const uint32_t *prompt, size_t n_prompt, size_t max_new,
+                                    size_t k, size_t n_draft) {
+    if (n_prompt == 0 || n_prompt > S) {
+      set_error("prefill length must be in [1, max_seq]");
+      return SYN_ERR_INVALID_ARG;
+    }
+    size_t pos = n_prompt, gen = 1, calls = 1, top = n_prompt;
+    while (gen < max_new) {
+      const size_t save = pos, acc = std::min(k, max_new - gen);
+      top = std::max(top, save + k + 1);
+      calls += k;
+      gen += acc;
+      pos = save + k + 1;
+      if (acc == k && gen < max_new) {
+        top = std::max(top, pos + 1);
+        pos += 1;
+        gen += 1;
+        calls += 1;
+      }
+    }
+    if (top > S || calls > S + 1) {
+      set_error("speculative decode: rows or sample calls exceed max_seq");
+      return SYN_ERR_INVALID_ARG;
+    }
+    if (use_graph) SYN_TRY(build_graph());
+    SYN_TRY(prefill(prompt, n_prompt));
+    pos = n_prompt;
+    gen = 1;
+    while (gen < max_new) {
+      const size_t save = pos, s0 = gen;
+      for (size_t i = 0; i < k; i++) SYN_TRY(run_draft(n_draft));
+      SYN_TRY(prefill_rows(history.as<uint32_t>() + (s0 - 1), (int)(k + 1), (int)save));
+      SYN_TRY(launch_state_set(st(), (int)(save + k + 1), -1, stream));
+      const size_t acc = std::min(k, max_new - gen);
+      gen += acc;
+      pos = save + k + 1;
+      if (acc == k && gen < max_new) {
+        SYN_TRY(run_step());
+        gen += 1;
+        pos += 1;
+      }
+    }
+    return SYN_OK;
   }
 };
 
@@ -420,6 +539,70 @@ syn_status_t syn_hip_klm_forward_prefill(syn_hip_klm_t *m, const uint32_t *ids, 
   SYN_TRY(m->prefill(ids, n));
   if (host_logits)
     SYN_HIP(hipMemcpyAsync(host_logits, m->logits.p, m->vocab * 4, hipMemcpyDeviceToHost,
+                           m->stream));
+  SYN_HIP(hipStreamSynchronize(m->stream));
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_klm_forward_prefill_append(syn_hip_klm_t *m, const uint32_t *ids,
+                                                size_t n, float *host_logits) {
+  SYN_TRY(check_klm(m));
+  if (!ids) return SYN_ERR_NULL_PTR;
+  SYN_TRY(m->prefill_append(ids, n));
+  if (host_logits)
+    SYN_HIP(hipMemcpyAsync(host_logits, m->logits.p, m->vocab * 4, hipMemcpyDeviceToHost,
+                           m->stream));
+  SYN_HIP(hipStreamSynchronize(m->stream));
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_klm_truncate(syn_hip_klm_t *m, size_t new_len) {
+  SYN_TRY(check_klm(m));
+  return m->truncate(new_len);
+}
+
+syn_status_t syn_hip_klm_cache_len(syn_hip_klm_t *m, size_t *out_len) {
+  SYN_TRY(check_klm(m));
+  if (!out_len) return SYN_ERR_NULL_PTR;
+  StepState cur;
+  SYN_TRY(m->get_state(&cur));
+  *out_len = (size_t)cur.pos;
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_klm_forward_one_draft(syn_hip_klm_t *m, uint32_t token, size_t n_layers,
+                                           float *host_logits) {
+  SYN_TRY(check_klm(m));
+  StepState cur;
+  SYN_TRY(m->get_state(&cur));
+  if ((size_t)cur.pos >= m->S) {
+    set_error("KV cache full");
+    return SYN_ERR_INVALID_ARG;
+  }
+  SYN_TRY(m->set_state(cur.pos, token, cur.step));
+  SYN_TRY(m->run_draft(n_layers));
+  if (host_logits)
+    SYN_HIP(hipMemcpyAsync(host_logits, m->logits.p, m->vocab * 4, hipMemcpyDeviceToHost,
+                           m->stream));
+  SYN_HIP(hipStreamSynchronize(m->stream));
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_klm_generate_speculative(syn_hip_klm_t *m, const uint32_t *prompt,
+                                              size_t n_prompt, size_t max_new, size_t k,
+                                              size_t draft_layers, uint32_t *out_tokens,
+                                              float *out_margins) {
+  SYN_TRY(check_klm(m));
+  if (!prompt || !out_tokens) return SYN_ERR_NULL_PTR;
+  if (k == 0) return syn_hip_klm_generate(m, prompt, n_prompt, max_new, out_tokens, out_margins);
+  if (max_new == 0) return SYN_OK;
+  // speculative_draft_layers, else num_layers / DEFAULT_DRAFT_LAYER_FRACTION (pipeline.rs:295-299)
+  const size_t n_draft = draft_layers > 0 ? draft_layers : m->L / 3;
+  SYN_TRY(m->generate_speculative(prompt, n_prompt, max_new, k, n_draft));
+  SYN_HIP(hipMemcpyAsync(out_tokens, m->history.p, max_new * 4, hipMemcpyDeviceToHost,
+                         m->stream));
+  if (out_margins)
+    SYN_HIP(hipMemcpyAsync(out_margins, m->mhist.p, max_new * 4, hipMemcpyDeviceToHost,
                            m->stream));
   SYN_HIP(hipStreamSynchronize(m->stream));
   return SYN_OK;

@@ -565,6 +565,30 @@ syn_status_t launch_step_advance(StepState *state, int add_pos, hipStream_t s) {
   return SYN_OK;
 }
 
+// zero K and V rows at position st->pos of `layers` consecutive layer caches
+// (the draft forward's padding, causal_lm.rs:306-315); grid (layers)
+__global__ void k_kv_zero_rows(float *__restrict__ kc, float *__restrict__ vc, size_t k_stride,
+                               size_t v_stride, int nkv, int hd, int max_seq,
+                               const StepState *__restrict__ st) {
+  const int pos = st->pos;
+  float *kl = kc + (size_t)blockIdx.x * k_stride, *vl = vc + (size_t)blockIdx.x * v_stride;
+  for (int i = threadIdx.x; i < nkv * hd; i += blockDim.x) {
+    const int g = i / hd, d = i - g * hd;
+    kl[kv_k_index(pos, g, d, hd, max_seq)] = 0.0f;
+    vl[kv_v_index(pos, g, d, hd, max_seq)] = 0.0f;
+  }
+}
+
+syn_status_t launch_kv_zero_rows(float *kc, float *vc, size_t k_stride, size_t v_stride,
+                                 int layers, int nkv, int hd, int max_seq, const StepState *st,
+                                 hipStream_t s) {
+  if (layers <= 0) return SYN_OK;
+  hipLaunchKernelGGL(k_kv_zero_rows, dim3(layers), dim3(256), 0, s, kc, vc, k_stride, v_stride,
+                     nkv, hd, max_seq, st);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
+
 __global__ void k_state_set(StepState *st, int pos, int nhist) {
   if (threadIdx.x == 0) {
     if (pos >= 0) st->pos = pos;

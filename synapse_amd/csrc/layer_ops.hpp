@@ -78,6 +78,10 @@ syn_status_t launch_argmax(const float *logits, int n, float *part_v, int *part_
                            float *margin_hist, hipStream_t s);
 // state->pos += add_pos; state->step += 1
 syn_status_t launch_step_advance(StepState *state, int add_pos, hipStream_t s);
+// zero K/V rows at position state->pos of `layers` layer caches (strides in floats)
+syn_status_t launch_kv_zero_rows(float *kc, float *vc, size_t k_stride, size_t v_stride,
+                                 int layers, int nkv, int hd, int max_seq, const StepState *st,
+                                 hipStream_t s);
 // state->pos = pos (if pos >= 0), state->nhist = nhist
 syn_status_t launch_state_set(StepState *state, int pos, int nhist, hipStream_t s);
 // elementwise residual: x += d

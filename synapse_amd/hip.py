@@ -111,6 +111,11 @@ SIGNATURES = {
     "syn_hip_qlm_time_lm_head_rotating": (ST, [P, SZ, C.POINTER(C.c_float)]),
     "syn_hip_qlm_destroy": (ST, [P]),
     "syn_hip_klm_create": (ST, [C.POINTER(KLmConfig), C.POINTER(P)]),
+    "syn_hip_klm_forward_prefill_append": (ST, [P, P, SZ, P]),
+    "syn_hip_klm_truncate": (ST, [P, SZ]),
+    "syn_hip_klm_cache_len": (ST, [P, C.POINTER(SZ)]),
+    "syn_hip_klm_forward_one_draft": (ST, [P, C.c_uint32, SZ, P]),
+    "syn_hip_klm_generate_speculative": (ST, [P, P, SZ, SZ, SZ, SZ, P, P]),
     "syn_hip_klm_set_embed": (ST, [P, P]),
     "syn_hip_klm_set_proj": (ST, [P, C.c_uint32, C.c_int, P]),
     "syn_hip_klm_set_lm_head": (ST, [P, P]),
@@ -632,6 +637,36 @@ class KQuantCausalLM:
         margins = np.zeros(max_new, np.float32)
         check(lib().syn_hip_klm_generate(self.h, ptr(prompt), prompt.size, max_new, ptr(toks),
                                          ptr(margins)), "generate")
+        return toks, margins
+
+    def prefill_append(self, ids):
+        ids = np.ascontiguousarray(ids, np.uint32)
+        out = np.empty(self.cfg["vocab"], np.float32)
+        check(lib().syn_hip_klm_forward_prefill_append(self.h, ptr(ids), ids.size, ptr(out)),
+              "klm_forward_prefill_append")
+        return out
+
+    def truncate(self, new_len: int):
+        check(lib().syn_hip_klm_truncate(self.h, new_len), "klm_truncate")
+
+    def cache_len(self) -> int:
+        n = SZ()
+        check(lib().syn_hip_klm_cache_len(self.h, C.byref(n)), "klm_cache_len")
+        return n.value
+
+    def forward_one_draft(self, token: int, n_layers: int):
+        out = np.empty(self.cfg["vocab"], np.float32)
+        check(lib().syn_hip_klm_forward_one_draft(self.h, int(token), n_layers, ptr(out)),
+              "klm_forward_one_draft")
+        return out
+
+    def generate_speculative(self, prompt, max_new: int, k: int, draft_layers: int = 0):
+        prompt = np.ascontiguousarray(prompt, np.uint32)
+        toks = np.zeros(max_new, np.uint32)
+        margins = np.zeros(max_new, np.float32)
+        check(lib().syn_hip_klm_generate_speculative(self.h, ptr(prompt), prompt.size, max_new, k,
+                                                     draft_layers, ptr(toks), ptr(margins)),
+              "klm_generate_speculative")
         return toks, margins
 
     def time(self, prompt, steps: int):

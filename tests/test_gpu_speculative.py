@@ -128,3 +128,57 @@ def test_rows_beyond_max_seq_are_refused(tiny):
     ids = _ids(TINY, 30)
     with pytest.raises(hip.SynapseError):
         g.generate_speculative(ids, 18, 4)  # 30 + 3 rounds x 6 rows > 48
+
+
+# ---- K-quant decoder: forward_one_draft with the first layers ---------------
+from tests.test_gpu_klm import LLAMA_FMTS, build_pair  # noqa: E402
+
+KCFG = dict(hidden=256, n_layers=4, n_heads=4, n_kv_heads=2, head_dim=64, inter=512, vocab=300,
+            max_seq=96, eps=1e-5, rope_theta=5e5)
+
+
+def _cos(a, b):
+    a, b = a.astype(np.float64), b.astype(np.float64)
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+
+@pytest.fixture(scope="module")
+def kpair():
+    o, g = build_pair(KCFG, LLAMA_FMTS)
+    yield o, g
+    o.close()
+    g.close()
+
+
+def test_klm_draft_and_append_track_the_oracle(kpair):
+    o, g = kpair
+    ids = _ids(KCFG, 7, 5)
+    for m in (o, g):
+        m.prefill(ids)
+    for t, n in ((3, 1), (50, 2), (7, 4)):
+        lo, lg = o.forward_one_draft(t, n), g.forward_one_draft(t, n)
+        assert _cos(lo, lg) >= 0.9999, (t, n, _cos(lo, lg))
+    lo, lg = o.prefill_append(_ids(KCFG, 4, 6)), g.prefill_append(_ids(KCFG, 4, 6))
+    assert _cos(lo, lg) >= 0.9999
+    for m in (o, g):
+        m.truncate(9)
+    lo, lg = o.forward_one(11), g.forward_one(11)
+    assert _cos(lo, lg) >= 0.9999
+    assert o.cache_len() == g.cache_len() == 10
+
+
+@pytest.mark.parametrize("graph", [True, False])
+@pytest.mark.parametrize("k,draft_layers", [(2, 0), (4, 2), (3, 4)])
+def test_klm_speculative_matches_oracle(kpair, graph, k, draft_layers):
+    o, g = kpair
+    ids = _ids(KCFG, 8, 7)
+    want, wm = o.generate_speculative(ids, 24, k, draft_layers=draft_layers)
+    g.set_options(graph=graph)
+    got, _ = g.generate_speculative(ids, 24, k, draft_layers=draft_layers)
+    g.set_options()
+    # the f32 path sums in another order: tokens agree while the oracle's
+    # greedy margin is above float noise
+    thin = next((i for i, m in enumerate(wm) if m < 1e-4), len(wm))
+    assert thin > 4
+    assert got[:thin].tolist() == want[:thin].tolist()
+    assert g.cache_len() == o.cache_len()

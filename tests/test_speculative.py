@@ -1,4 +1,5 @@
-"""Speculative decode on the INT8 decoder, oracle side: forward_prefill into a
+"""Speculative decode, oracle side (INT8 decoder and the f32 CausalLM of the
+K-quant path, whose forward_one_draft runs the first layers only): forward_prefill into a
 non-empty cache (int8.rs:593-635 with cached_attention_prefill,
 ops/attention.rs:153-247), KvCache.truncateTo (kvcache.zig:109-113) and
 generate_speculative (generation/pipeline.rs:281-395).  The reference has no
@@ -151,3 +152,88 @@ def test_sampled_first_round_matches_plain_sampling(model):
                                  u=float(u[1 + i]), **params)
         want.append(last)
     assert spec[:k + 1].tolist() == want
+
+
+# ---- the f32 CausalLM (K-quant decoder): a real draft forward ---------------
+KCFG = dict(hidden=128, n_layers=3, n_heads=4, n_kv_heads=2, head_dim=32, inter=256, vocab=200,
+            max_seq=96, eps=1e-5, rope_theta=5e5)
+
+
+def _flm(cfg, seed=0x5EED0000):
+    """An oracle CausalLM over Q8_0 blocks (layer l's weights depend only on l)."""
+    from synapse_amd import hip  # the library's host-side block encoder
+    o = O.CausalLM(cfg)
+    h, qd = cfg["hidden"], cfg["n_heads"] * cfg["head_dim"]
+    kvd, inter = cfg["n_kv_heads"] * cfg["head_dim"], cfg["inter"]
+    o.set_embed(O.normal(cfg["vocab"] * h, seed, 0.1).reshape(cfg["vocab"], h))
+    shapes = [(qd, h), (kvd, h), (kvd, h), (h, qd), (inter, h), (inter, h), (h, inter)]
+    for layer in range(cfg["n_layers"]):
+        for p, (n, k) in enumerate(shapes):
+            w = O.normal(n * k, seed + 1 + 8 * layer + p, 0.1).reshape(n, k)
+            o.set_proj(layer, p, "q8_0", hip.kquant_encode(hip.FMT_Q8_0, w))
+    w = O.normal(cfg["vocab"] * h, seed + 1 + 8 * 64, 0.1).reshape(cfg["vocab"], h)
+    o.set_lm_head("q8_0", hip.kquant_encode(hip.FMT_Q8_0, w))
+    return o
+
+
+@pytest.fixture(scope="module")
+def flm():
+    o = _flm(KCFG)
+    yield o
+    o.close()
+
+
+def test_draft_with_all_layers_is_forward_one(flm):
+    ids = _ids(6, 11)
+    flm.prefill(ids)
+    a = flm.forward_one(17)
+    flm.truncate(6)
+    b = flm.forward_one_draft(17, KCFG["n_layers"])
+    np.testing.assert_array_equal(_bits(a), _bits(b))
+
+
+@pytest.mark.parametrize("n", [1, 2])
+def test_draft_is_the_shallow_model(flm, n):
+    """forward_one_draft with n layers = forward_one of a model built from the
+    first n layers alone (same embedding, final norm and lm_head)."""
+    small = _flm(dict(KCFG, n_layers=n))
+    ids = _ids(5, 12)
+    for m in (flm, small):
+        m.prefill(ids)
+    # the shallow model's prefill fills its n layers as the deep model's first n
+    for t in (3, 99, 41):
+        np.testing.assert_array_equal(_bits(flm.forward_one_draft(t, n)),
+                                      _bits(small.forward_one(t)))
+    assert flm.cache_len() == small.cache_len() == 8
+    small.close()
+
+
+def test_draft_pads_the_skipped_layers_with_zero_rows(flm):
+    """A 1-layer draft leaves zero K/V rows in layers 1..: the next full step
+    then differs from the one after a full step of the same token."""
+    ids = _ids(5, 13)
+    flm.prefill(ids)
+    flm.forward_one_draft(7, 1)
+    after_draft = flm.forward_one(9)
+    flm.truncate(5)
+    flm.forward_one(7)
+    after_full = flm.forward_one(9)
+    assert not np.array_equal(after_draft, after_full)
+
+
+@pytest.mark.parametrize("k", [1, 3])
+def test_flm_speculative_all_layer_draft_first_round(flm, k):
+    ids = _ids(6, 14)
+    plain, pm = flm.generate(ids, 10)
+    spec, sm = flm.generate_speculative(ids, 10, k, draft_layers=KCFG["n_layers"])
+    np.testing.assert_array_equal(spec[:k + 1], plain[:k + 1])
+    np.testing.assert_array_equal(_bits(sm[:k + 1]), _bits(pm[:k + 1]))
+
+
+@pytest.mark.parametrize("max_new,k", [(9, 2), (16, 4)])
+def test_flm_speculative_rows_and_default_draft(flm, max_new, k):
+    ids = _ids(6, 15)
+    a, _ = flm.generate_speculative(ids, max_new, k)  # draft_layers 0: n_layers / 3 = 1
+    assert flm.cache_len() == _rows_after(6, max_new, k)
+    b, _ = flm.generate_speculative(ids, max_new, k, draft_layers=1)
+    np.testing.assert_array_equal(a, b)
