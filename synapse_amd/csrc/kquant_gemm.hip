@@ -500,14 +500,20 @@ __global__ void __launch_bounds__(256)
   };
   // iteration t: fetch step t+2 into `next`, multiply step t, stage step t+1
   // from `cur` (the last iterations fetch and stage clamped, in-bounds data
-  // that no one reads)
+  // that no one reads).  The MFMAs of step t's last k16 group wait until the
+  // next iteration has issued its first fragment reads: their operands are
+  // in registers (read before the barrier), so they cover the LDS latency
+  // that follows the barrier.
+  // (Not for Q8_0 with f32 products, whose decode registers would spill.)
+  constexpr bool kDefer = !(FMT == SYN_HIP_FMT_Q8_0 && !EXACT);
   auto iteration = [&](int t, Fetch<FMT> &cur, Fetch<FMT> &next) {
     fetch(next, t + 2);
     read(t, 0, 0);
+    if (kDefer && t > 0) mma(1);
 #pragma unroll
     for (int k16 = 0; k16 < 4; k16++) {
       if (k16 < 3) read(t, k16 + 1, (k16 + 1) & 1);
-      mma(k16 & 1);
+      if (k16 < 3 || !kDefer) mma(k16 & 1);
       stage_part(cur, t + 1, (t + 1) & 1, k16);
     }
     __syncthreads();
@@ -524,6 +530,7 @@ __global__ void __launch_bounds__(256)
     iteration(t + 1, f0, f1);
   }
   if (t < nsteps) iteration(t, f1, f0);
+  if (kDefer) mma(1);
   const bool atomic = gridDim.z > 1;
 #pragma unroll
   for (int mt = 0; mt < 4; mt++)
