@@ -341,9 +341,10 @@ __global__ void __launch_bounds__(256)
     k_attn_prefill(const float *__restrict__ q, const float *__restrict__ kc,
                    const float *__restrict__ vc, int t, int nh, int nkv, int hd, int max_seq,
                    int cache_off, float *__restrict__ out) {
-  extern __shared__ float sm[];  // qs[hd] | e[t]
-  float *qs = sm, *e = sm + hd;
+  extern __shared__ float sm[];  // qs[hd] | e[t] | c[t]
+  float *qs = sm, *e = sm + hd, *cj = sm + hd + t;
   __shared__ float s_mx, s_inv;
+  __shared__ float cmax[256];
   const int head = blockIdx.x, i = blockIdx.y;
   const int kvh = head / (nh / nkv);
   const int qd = nh * hd;
@@ -367,17 +368,45 @@ __global__ void __launch_bounds__(256)
     e[j] = sc;
   }
   __syncthreads();
+  // Online max / sum in the reference's order: at position j the running max
+  // is the max of e[0..j-1], so every exponential is known up front.  Thread
+  // i takes the contiguous chunk i of the positions: chunk maxima, their
+  // exclusive prefix, then per position the exponential the reference takes
+  // there (exp(mx - x) at a new maximum, stored negated; else exp(x - mx)).
+  // Only the dependent chain se = se * c + 1 / se + c stays on one thread.
+  const int per = (t + (int)blockDim.x - 1) / (int)blockDim.x;
+  const int j0 = min((int)threadIdx.x * per, t), j1 = min(j0 + per, t);
+  float lm = -__builtin_inff();
+  for (int j = j0; j < j1; j++) lm = fmaxf(lm, e[j]);
+  cmax[threadIdx.x] = lm;
+  __syncthreads();
+  float run = -__builtin_inff();
+  for (int i = 0; i < (int)threadIdx.x; i++) run = fmaxf(run, cmax[i]);
+  for (int j = j0; j < j1; j++) {
+    const float x = e[j];
+    cj[j] = x > run ? -syn_expf(run - x) : syn_expf(x - run);
+    run = fmaxf(run, x);
+  }
+  __syncthreads();
   if (threadIdx.x == 0) {
     float mx = -__builtin_inff(), se = 0.0f;
-    for (int j = 0; j < t; j++) {
-      const float x = e[j];
-      if (x > mx) {
-        const float p = se * syn_expf(mx - x);
-        se = p + 1.0f;
-        mx = x;
-      } else {
-        se = se + syn_expf(x - mx);
+    for (int i = 0; i < (int)blockDim.x; i++) mx = fmaxf(mx, cmax[i]);
+    int j = 0;
+    for (; j + 8 <= t; j += 8) {
+      float c[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) c[u] = cj[j + u];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const float cu = fabsf(c[u]);
+        const float p = se * cu;
+        se = __builtin_signbit(c[u]) ? p + 1.0f : se + cu;
       }
+    }
+    for (; j < t; j++) {
+      const float cu = fabsf(cj[j]);
+      const float p = se * cu;
+      se = __builtin_signbit(cj[j]) ? p + 1.0f : se + cu;
     }
     s_mx = mx;
     s_inv = 1.0f / se;
@@ -401,14 +430,247 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// Row-block form of k_attn_prefill: one workgroup per (head, 16 query rows),
+// the head's K and V rows staged through LDS 64 positions at a time, so each
+// row of the cache is read once per 16 queries instead of once per query.
+// Every score, sum and product is the one k_attn_prefill forms, in the same
+// order (the same chains per (row, position) and (row, column)).
+constexpr int kPfRows = 16, kPfChunk = 64;
+
+__global__ void __launch_bounds__(256)
+    k_attn_prefill_rows(const float *__restrict__ q, const float *__restrict__ kc,
+                        const float *__restrict__ vc, int t, int nh, int nkv, int hd, int max_seq,
+                        int cache_off, float *__restrict__ out) {
+  extern __shared__ float sm[];
+  // qs[16][hd] | kv[64][hd + 1] | e[16][t] | c[16][t]
+  const int ldk = hd + 1;
+  float *qs = sm, *kv = qs + kPfRows * hd, *e = kv + kPfChunk * ldk, *cj = e + kPfRows * t;
+  __shared__ float s_mx[kPfRows], s_inv[kPfRows];
+  // the exp table in LDS: a per-lane lookup in it does not wait on memory
+  __shared__ uint64_t etab[32];
+  if (threadIdx.x < 32) etab[threadIdx.x] = syn_exp2_tab[threadIdx.x];
+  const int head = blockIdx.x, i0 = blockIdx.y * kPfRows;
+  const int kvh = head / (nh / nkv);
+  const int qd = nh * hd;
+  const int nrow = min(kPfRows, t - i0);
+  const int tid = threadIdx.x;
+  for (int x = tid; x < kPfRows * hd; x += blockDim.x) {
+    const int r = x / hd, d = x - r * hd;
+    qs[x] = r < nrow ? q[(size_t)(i0 + r) * qd + head * hd + d] : 0.0f;
+  }
+  const float scale = 1.0f / sqrtf((float)hd);
+  // ---- scores: 16 rows x 64 positions per chunk, 4 (row, position) pairs a thread
+  for (int p0 = 0; p0 < t; p0 += kPfChunk) {
+    const int np = min(kPfChunk, t - p0);
+    __syncthreads();  // qs written / the previous chunk consumed
+    // K rows: four consecutive columns are contiguous in the cache layout;
+    // eight 16-byte loads in flight per thread before the LDS stores
+    const int hd4 = hd / 4, nk = np * hd4;
+    for (int x0 = tid; x0 < nk; x0 += 8 * (int)blockDim.x) {
+      float4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int x = min(x0 + u * (int)blockDim.x, nk - 1);
+        const int pp = x / hd4, d4 = x - pp * hd4;
+        v[u] = *reinterpret_cast<const float4 *>(
+            kc + kv_k_index(cache_off + p0 + pp, kvh, 4 * d4, hd, max_seq));
+      }
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int x = x0 + u * (int)blockDim.x;
+        if (x < nk) {
+          const int pp = x / hd4, d4 = x - pp * hd4;
+          float *dst = kv + pp * ldk + 4 * d4;
+          dst[0] = v[u].x;
+          dst[1] = v[u].y;
+          dst[2] = v[u].z;
+          dst[3] = v[u].w;
+        }
+      }
+    }
+    __syncthreads();
+    // thread: position pp of the chunk for rows rb, rb+4, rb+8, rb+12 (one K
+    // row read per step, four independent chains; the fused / plain choice
+    // of each chain is a select, so all four keep their own order)
+    const int pp = tid % kPfChunk, rb = tid / kPfChunk;
+    if (pp < np) {
+      const int j = p0 + pp;
+      float acc[4];
+      bool fz[4];
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int i = i0 + rb + 4 * u;
+        const int tq = (i / 32) * 32, tqs = min(32, t - tq), il = i - tq;
+        fz[u] = sgemm_fused(tqs, il, t, j, true);
+        acc[u] = 0.0f;
+      }
+      const float *kr = kv + pp * ldk;
+#pragma unroll 8
+      for (int d = 0; d < hd; d++) {
+        const float kd = kr[d];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          const float qv = qs[(rb + 4 * u) * hd + d];
+          const float f = __builtin_fmaf(qv, kd, acc[u]);
+          const float pr = qv * kd;
+          const float g = acc[u] + pr;
+          acc[u] = fz[u] ? f : g;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; u++) {
+        const int r = rb + 4 * u, i = i0 + r;
+        if (r < nrow) {
+          float sc = acc[u] * scale;
+          if (j > i) sc = -__builtin_inff();
+          e[r * t + j] = sc;
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // ---- online max / sum per row (k_attn_prefill's order): 16 threads a row
+  // precompute the exponentials over contiguous chunks, one thread a row
+  // runs the dependent chain
+  {
+    const int r = tid / 16, part = tid % 16;
+    const int per = (t + 15) / 16;
+    const int j0 = min(part * per, t), j1 = min(j0 + per, t);
+    float *er = e + r * t, *cr = cj + r * t;
+    float lm = -__builtin_inff();
+    if (r < nrow)
+      for (int j = j0; j < j1; j++) lm = fmaxf(lm, er[j]);
+    // exclusive prefix of the chunk maxima within the 16-lane group
+    float run = -__builtin_inff(), all = -__builtin_inff();
+    for (int o = 0; o < 16; o++) {
+      const float v = __shfl(lm, (tid & ~15) + o);
+      if (o < part) run = fmaxf(run, v);
+      all = fmaxf(all, v);
+    }
+    if (r < nrow)
+      for (int j = j0; j < j1; j++) {
+        const float x = er[j];
+        cr[j] = x > run ? -syn_expf_tab(run - x, etab) : syn_expf_tab(x - run, etab);
+        run = fmaxf(run, x);
+      }
+    __syncthreads();
+    if (part == 0 && r < nrow) {
+      float se = 0.0f;
+      int j = 0;
+      for (; j + 8 <= t; j += 8) {
+        float c[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) c[u] = cr[j + u];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+          const float cu = fabsf(c[u]);
+          const float pr = se * cu;
+          se = __builtin_signbit(c[u]) ? pr + 1.0f : se + cu;
+        }
+      }
+      for (; j < t; j++) {
+        const float cu = fabsf(cr[j]);
+        const float pr = se * cu;
+        se = __builtin_signbit(cr[j]) ? pr + 1.0f : se + cu;
+      }
+      s_mx[r] = all;
+      s_inv[r] = 1.0f / se;
+    }
+    __syncthreads();
+  }
+  for (int x = tid; x < nrow * t; x += blockDim.x) {
+    const int r = x / t;
+    e[x] = syn_expf_tab(e[x] - s_mx[r], etab) * s_inv[r];
+  }
+  // ---- P V: 16 rows x hd columns, chains over the positions in order.
+  // hd divides 256: thread = column d for rows r0, r0 + 256/hd, ... (one V
+  // read per position, hd/16 independent chains)
+  const int d = tid % hd, rstep = (int)blockDim.x / hd, r0 = tid / hd, nch = kPfRows / rstep;
+  constexpr int kMaxPer = 8;
+  float acc[kMaxPer];
+  bool fz[kMaxPer];
+#pragma unroll
+  for (int u = 0; u < kMaxPer; u++) {
+    const int i = i0 + r0 + u * rstep;
+    const int tq = (i / 32) * 32, tqs = min(32, t - tq), il = i - tq;
+    fz[u] = sgemm_fused(tqs, il, hd, d, false);
+    acc[u] = 0.0f;
+  }
+  for (int p0 = 0; p0 < t; p0 += kPfChunk) {
+    const int np = min(kPfChunk, t - p0);
+    __syncthreads();
+    const int nv = np * hd;  // eight loads in flight per thread
+    for (int x0 = tid; x0 < nv; x0 += 8 * (int)blockDim.x) {
+      float v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int x = min(x0 + u * (int)blockDim.x, nv - 1);
+        const int pp = x / hd, dd = x - pp * hd;
+        v[u] = vc[kv_v_index(cache_off + p0 + pp, kvh, dd, hd, max_seq)];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int x = x0 + u * (int)blockDim.x;
+        if (x < nv) {
+          const int pp = x / hd, dd = x - pp * hd;
+          kv[pp * ldk + dd] = v[u];
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int pp = 0; pp < np; pp++) {
+      const float v = kv[pp * ldk + d];
+#pragma unroll
+      for (int u = 0; u < kMaxPer; u++) {
+        if (u < nch) {
+          const float ev = e[(r0 + u * rstep) * t + p0 + pp];
+          const float f = __builtin_fmaf(ev, v, acc[u]);
+          const float m = ev * v;
+          const float g = acc[u] + m;
+          acc[u] = fz[u] ? f : g;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kMaxPer; u++) {
+    const int r = r0 + u * rstep;
+    if (u < nch && r < nrow) out[(size_t)(i0 + r) * qd + head * hd + d] = acc[u];
+  }
+}
+
 syn_status_t launch_attention_prefill(const float *q, const float *kcache, const float *vcache,
                                       int t, int n_heads, int n_kv, int head_dim, int max_seq,
                                       float *scores, float *out, hipStream_t s, int cache_off) {
   (void)scores;
-  const size_t shm = (size_t)(head_dim + t) * sizeof(float);
-  if (shm > 64 * 1024) {
-    set_error("prefill attention: prompt too long for one workgroup's LDS row");
+  // row-block kernel when its LDS rows fit (hd <= 128: 8 outputs a thread)
+  const size_t shm_rows = (size_t)(kPfRows * head_dim + kPfChunk * (head_dim + 1) +
+                                   2 * kPfRows * t) * sizeof(float);
+  if ((head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128) &&
+      shm_rows <= 144 * 1024) {
+    static bool attr_rows = false;
+    if (!attr_rows) {
+      SYN_HIP(hipFuncSetAttribute((const void *)k_attn_prefill_rows,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, 144 * 1024));
+      attr_rows = true;
+    }
+    hipLaunchKernelGGL(k_attn_prefill_rows, dim3(n_heads, (t + kPfRows - 1) / kPfRows),
+                       dim3(256), shm_rows, s, q, kcache, vcache, t, n_heads, n_kv, head_dim,
+                       max_seq, cache_off, out);
+    SYN_LAUNCH_CHECK();
+    return SYN_OK;
+  }
+  const size_t shm = (size_t)(head_dim + 2 * t) * sizeof(float);
+  if (shm > 144 * 1024) {
+    set_error("prefill attention: prompt too long for one workgroup's LDS rows");
     return SYN_ERR_INVALID_ARG;
+  }
+  static bool attr = false;
+  if (!attr) {  // more than the default 64 KiB of dynamic LDS
+    SYN_HIP(hipFuncSetAttribute((const void *)k_attn_prefill,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, 144 * 1024));
+    attr = true;
   }
   hipLaunchKernelGGL(k_attn_prefill, dim3(n_heads, t), dim3(256), shm, s, q, kcache, vcache, t,
                      n_heads, n_kv, head_dim, max_seq, cache_off, out);

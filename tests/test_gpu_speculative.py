@@ -182,3 +182,17 @@ def test_klm_speculative_matches_oracle(kpair, graph, k, draft_layers):
     assert thin > 4
     assert got[:thin].tolist() == want[:thin].tolist()
     assert g.cache_len() == o.cache_len()
+
+
+@pytest.mark.parametrize("n", [1, 17, 64, 100, 150])
+def test_long_prefill_and_append_bit_exact(mid, n):
+    """Prefill attention over several 64-position chunks and partial 16-row
+    blocks, into an empty cache and appended after cached rows."""
+    o, g = mid
+    ids = _ids(MID, n, 9)
+    np.testing.assert_array_equal(_bits(g.prefill(ids)), _bits(o.prefill(ids)))
+    if n <= 100:
+        extra = _ids(MID, 37, 10)
+        np.testing.assert_array_equal(_bits(g.prefill_append(extra)),
+                                      _bits(o.prefill_append(extra)))
+        np.testing.assert_array_equal(_bits(g.forward_one(5)), _bits(o.forward_one(5)))
