@@ -437,10 +437,12 @@ __global__ void __launch_bounds__(256)
 // order (the same chains per (row, position) and (row, column)).
 constexpr int kPfRows = 16, kPfChunk = 64;
 
+template <int HD>
 __global__ void __launch_bounds__(256)
     k_attn_prefill_rows(const float *__restrict__ q, const float *__restrict__ kc,
-                        const float *__restrict__ vc, int t, int nh, int nkv, int hd, int max_seq,
+                        const float *__restrict__ vc, int t, int nh, int nkv, int max_seq,
                         int cache_off, float *__restrict__ out) {
+  constexpr int hd = HD;  // compile-time: LDS offsets become immediates
   extern __shared__ float sm[];
   // qs[16][hd] | kv[64][hd + 1] | e[16][t] | c[16][t]
   const int ldk = hd + 1;
@@ -505,16 +507,38 @@ __global__ void __launch_bounds__(256)
         acc[u] = 0.0f;
       }
       const float *kr = kv + pp * ldk;
+      // the four chains usually agree on fused / plain: then one loop form
+      const bool all_f = fz[0] && fz[1] && fz[2] && fz[3];
+      const bool none_f = !fz[0] && !fz[1] && !fz[2] && !fz[3];
+      if (all_f) {
 #pragma unroll 8
-      for (int d = 0; d < hd; d++) {
-        const float kd = kr[d];
+        for (int d = 0; d < hd; d++) {
+          const float kd = kr[d];
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-          const float qv = qs[(rb + 4 * u) * hd + d];
-          const float f = __builtin_fmaf(qv, kd, acc[u]);
-          const float pr = qv * kd;
-          const float g = acc[u] + pr;
-          acc[u] = fz[u] ? f : g;
+          for (int u = 0; u < 4; u++) acc[u] = __builtin_fmaf(qs[(rb + 4 * u) * hd + d], kd, acc[u]);
+        }
+      } else if (none_f) {
+#pragma unroll 8
+        for (int d = 0; d < hd; d++) {
+          const float kd = kr[d];
+#pragma unroll
+          for (int u = 0; u < 4; u++) {
+            const float pr = qs[(rb + 4 * u) * hd + d] * kd;
+            acc[u] = acc[u] + pr;
+          }
+        }
+      } else {
+#pragma unroll 8
+        for (int d = 0; d < hd; d++) {
+          const float kd = kr[d];
+#pragma unroll
+          for (int u = 0; u < 4; u++) {
+            const float qv = qs[(rb + 4 * u) * hd + d];
+            const float f = __builtin_fmaf(qv, kd, acc[u]);
+            const float pr = qv * kd;
+            const float g = acc[u] + pr;
+            acc[u] = fz[u] ? f : g;
+          }
         }
       }
 #pragma unroll
@@ -618,17 +642,45 @@ __global__ void __launch_bounds__(256)
       }
     }
     __syncthreads();
-#pragma unroll 4
-    for (int pp = 0; pp < np; pp++) {
-      const float v = kv[pp * ldk + d];
+    bool all_f = true, none_f = true;
 #pragma unroll
-      for (int u = 0; u < kMaxPer; u++) {
-        if (u < nch) {
-          const float ev = e[(r0 + u * rstep) * t + p0 + pp];
-          const float f = __builtin_fmaf(ev, v, acc[u]);
-          const float m = ev * v;
-          const float g = acc[u] + m;
-          acc[u] = fz[u] ? f : g;
+    for (int u = 0; u < kMaxPer; u++)
+      if (u < nch) {
+        all_f = all_f && fz[u];
+        none_f = none_f && !fz[u];
+      }
+    if (all_f) {
+#pragma unroll 4
+      for (int pp = 0; pp < np; pp++) {
+        const float v = kv[pp * ldk + d];
+#pragma unroll
+        for (int u = 0; u < kMaxPer; u++)
+          if (u < nch) acc[u] = __builtin_fmaf(e[(r0 + u * rstep) * t + p0 + pp], v, acc[u]);
+      }
+    } else if (none_f) {
+#pragma unroll 4
+      for (int pp = 0; pp < np; pp++) {
+        const float v = kv[pp * ldk + d];
+#pragma unroll
+        for (int u = 0; u < kMaxPer; u++)
+          if (u < nch) {
+            const float m = e[(r0 + u * rstep) * t + p0 + pp] * v;
+            acc[u] = acc[u] + m;
+          }
+      }
+    } else {
+#pragma unroll 4
+      for (int pp = 0; pp < np; pp++) {
+        const float v = kv[pp * ldk + d];
+#pragma unroll
+        for (int u = 0; u < kMaxPer; u++) {
+          if (u < nch) {
+            const float ev = e[(r0 + u * rstep) * t + p0 + pp];
+            const float f = __builtin_fmaf(ev, v, acc[u]);
+            const float m = ev * v;
+            const float g = acc[u] + m;
+            acc[u] = fz[u] ? f : g;
+          }
         }
       }
     }
@@ -649,17 +701,24 @@ syn_status_t launch_attention_prefill(const float *q, const float *kcache, const
                                    2 * kPfRows * t) * sizeof(float);
   if ((head_dim == 16 || head_dim == 32 || head_dim == 64 || head_dim == 128) &&
       shm_rows <= 144 * 1024) {
-    static bool attr_rows = false;
-    if (!attr_rows) {
-      SYN_HIP(hipFuncSetAttribute((const void *)k_attn_prefill_rows,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, 144 * 1024));
-      attr_rows = true;
+    static bool attr_rows[4] = {false, false, false, false};
+    auto run = [&](auto kern, int which) -> syn_status_t {
+      if (!attr_rows[which]) {
+        SYN_HIP(hipFuncSetAttribute((const void *)kern,
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, 144 * 1024));
+        attr_rows[which] = true;
+      }
+      hipLaunchKernelGGL(kern, dim3(n_heads, (t + kPfRows - 1) / kPfRows), dim3(256), shm_rows,
+                         s, q, kcache, vcache, t, n_heads, n_kv, max_seq, cache_off, out);
+      SYN_LAUNCH_CHECK();
+      return SYN_OK;
+    };
+    switch (head_dim) {
+      case 16: return run(k_attn_prefill_rows<16>, 0);
+      case 32: return run(k_attn_prefill_rows<32>, 1);
+      case 64: return run(k_attn_prefill_rows<64>, 2);
+      default: return run(k_attn_prefill_rows<128>, 3);
     }
-    hipLaunchKernelGGL(k_attn_prefill_rows, dim3(n_heads, (t + kPfRows - 1) / kPfRows),
-                       dim3(256), shm_rows, s, q, kcache, vcache, t, n_heads, n_kv, head_dim,
-                       max_seq, cache_off, out);
-    SYN_LAUNCH_CHECK();
-    return SYN_OK;
   }
   const size_t shm = (size_t)(head_dim + 2 * t) * sizeof(float);
   if (shm > 144 * 1024) {
