@@ -103,6 +103,17 @@ def kquant_weight_bytes(c):
     return L * layer + q6k(v, h)
 
 
+def guarded(fn, *a):
+    """Run one secondary record; a failure is recorded in the line instead of
+    ending the run before the headline is printed."""
+    try:
+        return fn(*a)
+    except Exception as e:  # noqa: BLE001 - any failure of a secondary is reported
+        import traceback
+        traceback.print_exc(file=sys.stderr)
+        return {"error": f"{type(e).__name__}: {e}"}
+
+
 def secondary(hip, np):
     """The other BASELINE configurations, measured on the same GPU."""
     from synapse_amd import microbench as mb
@@ -248,7 +259,9 @@ def main():
 
     from synapse_amd import hip
     hip.init(0)
-    cfg = dict(QWEN3, max_seq=PROMPT + args.warmup + args.steps + 1)
+    # rows for the timed decode and for the speculative record (k = 4, 64
+    # tokens: a round appends k + 2 rows for k + 1 tokens)
+    cfg = dict(QWEN3, max_seq=PROMPT + max(args.warmup + args.steps, 2 * 64 + 8) + 1)
     t0 = time.perf_counter()
     model = hip.QuantizedCausalLM(cfg)
     model.init_synthetic(SEED_BASE, 0.02)
@@ -274,7 +287,7 @@ def main():
     lm_ms = (model.time_lm_head(args.lm_head_iters) if args.unfused
              else model.time_lm_head_rotating(2 * args.lm_head_iters))
     lm_gbs = lm_head_bytes(QWEN3) / (lm_ms * 1e-3) / 1e9
-    spec = None if args.no_secondary else speculative_record(model, np)
+    spec = None if args.no_secondary else guarded(speculative_record, model, np)
     model.close()
 
     line = {
@@ -313,10 +326,10 @@ def main():
                      "bytes_per_launch": lm_head_bytes(QWEN3)},
     }
     if not args.no_secondary:
-        line["secondary"] = secondary(hip, np)
+        line["secondary"] = guarded(secondary, hip, np)
         line["secondary"]["config1_speculative_decode"] = spec
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        line["cpu_baseline"] = guarded(cpu_baseline, args.cpu_seconds)
     print(json.dumps(line), flush=True)
 
 
