@@ -2,24 +2,27 @@
 //
 // The unfused step launches one kernel per reference op (13 per layer).  At
 // batch 1 every one of them is latency-bound, so the step is rebuilt as five
-// kernels per layer, each a split-K GEMV whose prologue computes the GEMV's
-// input activation itself:
+// kernels per layer:
 //
-//   K1  x = x_mid + down(prev)        ; q8(rmsnorm(x))  ; QKV     rows
-//   K2  per head: q/k/v rows, head norms, RoPE, KV append, attention
-//   K3  q8(attn)                                         ; O       rows
-//   K4  x_mid = x + o                 ; q8(rmsnorm(x))  ; gate|up rows
-//   K5  q8(silu(gate) * up)                              ; down    rows
+//   K1  x = x_mid + down(prev) ; q8(rmsnorm(x))       ; QKV rows (split K)
+//   K2  per query head: q/k/v rows, head norms, RoPE, KV append, scores,
+//       softmax, P.V (k_attn_head)
+//   K3  q8(attn)                                       ; O rows (split K)
+//   K4  x_mid = x + o ; q8(rmsnorm(x_mid)) ; gate and up rows over the whole
+//       K, h = silu(gate) * up, max |h| (k_gu_swiglu)
+//   K5  q8 of this split's K range of h with that max  ; down rows (split K)
 //
 // then the final norm, the lm_head GEMV with per-panel top-2, and one merge.
 // A split-K GEMV adds its exact int32 partial dot products into per-layer
 // accumulators with atomics (integer sums are exact in any order); the
-// consumer applies the reference epilogue (f32(acc)*sx)*sw.  The prologue is
-// computed redundantly by every workgroup (it reads a few KB from L2), which
-// removes all inter-workgroup synchronisation inside a kernel.  Each wave
-// issues its weight loads before the prologue, so the HBM latency of the GEMV
-// hides behind the prologue's dependency chains, and the prologue batches its
-// own loads so that each thread has several in flight.
+// consumer applies the reference epilogue (f32(acc)*sx)*sw.  A prologue that
+// needs a whole row (RMSNorm, a quantizer's max) is computed redundantly by
+// every workgroup (it reads a few KB from L2), which removes all
+// inter-workgroup synchronisation inside a kernel.  Each wave issues its
+// weight loads before the prologue, so the HBM latency of the GEMV hides
+// behind the prologue's dependency chains, and the prologue batches its own
+// loads so that each thread has several in flight.  Dependent float chains
+// run from registers (reduce_order.hpp pin_regs).
 //
 // Every float operation is the one of the unfused kernels (layer_ops.hip),
 // which follow the reference's order: the fused step is bit-identical to it.
@@ -163,8 +166,10 @@ static const uint64_t *exp_table_address() {
 // ops/norm.rs) + quantize; PRO_MNORM: the same with one sequential sum of
 // squares (pure_rust_ops.rs:96-112, the Mamba blocks' norm); PRO_QUANT:
 // quantize an f32 vector; PRO_SWIGLU: silu(gate) * up of GEMV rows, then
-// quantize; PRO_ROWS: quantize GEMV rows (RowSrc values)
-enum { PRO_NORM = 0, PRO_QUANT = 1, PRO_SWIGLU = 2, PRO_MNORM = 3, PRO_ROWS = 4 };
+// quantize; PRO_ROWS: quantize GEMV rows (RowSrc values); PRO_HQ: quantize
+// this split's K range of an f32 vector whose max |v| another kernel has
+// already reduced (hmax)
+enum { PRO_NORM = 0, PRO_QUANT = 1, PRO_SWIGLU = 2, PRO_MNORM = 3, PRO_ROWS = 4, PRO_HQ = 5 };
 
 struct ProArgs {
   // PRO_NORM: x = (base ? base : embed[st->token]) + delta
@@ -177,8 +182,9 @@ struct ProArgs {
   const float *nw;
   const float *zero_row;  // H zeros (the embedding row of an id >= vocab)
   float eps;
-  // PRO_QUANT
+  // PRO_QUANT, PRO_HQ (with hmax = max |vec| as f32 bits)
   const float *vec;
+  const unsigned *hmax;
   // PRO_ROWS
   RowSrc rows;
   // PRO_SWIGLU; exp_tab = device address of syn_exp2_tab, passed as a plain
@@ -196,6 +202,119 @@ struct GemvArgs {
   int C, cs;
   int *acc;
 };
+
+// ------------------------------------------------------------------ prologue parts
+// PRO_NORM / PRO_MNORM loads: x = (base | embed row of st->token | zero row)
+// + delta rows, the norm gains; issue() is called once these are requested,
+// so the caller's weight loads queue behind them (element j = tid + u*NT,
+// clamped to H-1)
+template <int NT, class Issue>
+__device__ __forceinline__ void norm_prologue_load(const ProArgs &a, int H, float (&x)[RB],
+                                                   float (&nwv)[RB], Issue issue) {
+  const int tid = threadIdx.x;
+  const float *src = a.base;
+  if (!src) {
+    const uint32_t tok = a.st->token;
+    src = tok < (uint32_t)a.vocab ? a.embed + (size_t)tok * H : a.zero_row;
+  }
+#pragma unroll
+  for (int u = 0; u < RB; u++) {
+    const int j = min(tid + u * NT, H - 1);
+    x[u] = src[j];
+    nwv[u] = a.nw[j];
+  }
+  // without a delta the loads below read the norm gains instead (in-bounds,
+  // values unused), so that no load sits behind a branch
+  const bool has_delta = a.delta.acc != nullptr;
+  const int *dacc = has_delta ? a.delta.acc : reinterpret_cast<const int *>(a.nw);
+  const float *dws = has_delta ? a.delta.ws : a.nw;
+  const float *dsxp = has_delta ? a.delta.sx : a.nw;
+  int da[RB];
+  float dw[RB];
+#pragma unroll
+  for (int u = 0; u < RB; u++) {
+    const int j = min(tid + u * NT, H - 1);
+    da[u] = dacc[j];
+    dw[u] = dws[j];
+  }
+  const float dsx = dsxp[0];
+  issue();
+  if (has_delta) {
+#pragma unroll
+    for (int u = 0; u < RB; u++) {
+      const float f = (float)da[u] * dsx;
+      const float d = f * dw[u];
+      x[u] = x[u] + d;
+    }
+  }
+}
+
+// RMSNorm (ops/norm.rs:8-38): out = (x*w) * (1/sqrt(sumsq/n + eps)), then
+// the quantizer's max|out|; returns the row scale with xq[0..H) written.
+// Scaling by the positive `scale` is a monotonic rounding, so max|t*scale|
+// = fl(max|t| * scale): the max of t = x*w is reduced while lanes 0-3 run
+// the sum-of-squares chains (or lane 0 the single sequential sum, SEQ).
+// sq: LDS, round4(H) floats.
+template <int NT, bool SEQ>
+__device__ float norm_quant(float eps, int H, const float (&x)[RB], const float (&nwv)[RB],
+                            float *sq, int8_t *xq, float *red) {
+  const int tid = threadIdx.x;
+  float t[RB];
+#pragma unroll
+  for (int u = 0; u < RB; u++) {
+    const int j = tid + u * NT;
+    if (j < H) sq[SEQ ? j : sq_slot(j, H)] = x[u] * x[u];
+    t[u] = x[u] * nwv[u];
+  }
+  wg_max_post<NT>(local_absmax<NT>(t, H), red, 0);
+  bar<NT>();
+  float ss;
+  if constexpr (SEQ) {
+    if (tid == 0) red[36] = seq_sum(sq, H);
+    bar<NT>();
+    ss = red[36];
+  } else {
+    ss = sumsq_chains<NT>(sq, H, red);
+  }
+  const float scale = 1.0f / sqrtf(ss / (float)H + eps);
+  float nv[RB];
+#pragma unroll
+  for (int u = 0; u < RB; u++) nv[u] = t[u] * scale;
+  float mx = wg_max_get<NT>(red, 0) * scale;
+  if (!(mx <= 3.402823466e38f) || !(scale > 0.0f)) {  // inf/nan rows: reduce explicitly
+    wg_max_post<NT>(local_absmax<NT>(nv, H), red, 16);
+    bar<NT>();
+    mx = wg_max_get<NT>(red, 16);
+  }
+  return quantize_regs_with_max<NT>(nv, H, mx, xq);
+}
+
+// quantizePerChannelInt8 (quantize.zig:12-47) of elements [k0, k1) of a row
+// whose max|v| is mx, held as element j = k0 + tid + u*NT; writes xq[j] and
+// returns the row scale
+template <int NT>
+__device__ float quantize_range_with_max(const float (&v)[RB], int k0, int k1, float mx,
+                                         int8_t *xq) {
+  const int tid = threadIdx.x;
+  if (mx == 0.0f) {
+#pragma unroll
+    for (int u = 0; u < RB; u++)
+      if (k0 + tid + u * NT < k1) xq[k0 + tid + u * NT] = 0;
+    return 1.0f;
+  }
+  const float inv = 127.0f / mx;
+#pragma unroll
+  for (int u = 0; u < RB; u++) {
+    const int j = k0 + tid + u * NT;
+    if (j < k1) {
+      float r = roundf(v[u] * inv);
+      r = fminf(127.0f, fmaxf(-127.0f, r));
+      xq[j] = (int8_t)(int)r;
+    }
+  }
+  return mx / 127.0f;
+}
+
 
 // grid (panels, ks).  dynamic LDS: sq[round4(H)] floats (PRO_NORM) | xq[C*16].
 // Everything a workgroup reads from memory is requested at entry: its weight
@@ -241,42 +360,17 @@ __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
   //    weight chunks, 3. the activation row x[] in registers
   float x[RB];
   float nwv[RB];
+  float hq = 1.0f;
   if constexpr (NORM) {
-    const float *src = a.base;
-    if (!src) {
-      const uint32_t tok = a.st->token;
-      src = tok < (uint32_t)a.vocab ? a.embed + (size_t)tok * H : a.zero_row;
-    }
+    norm_prologue_load<NT>(a, H, x, nwv, issue_weights);
+  } else if constexpr (PRO == PRO_HQ) {
+    // element j = c0*16 + tid + u*NT of this split's K range
+    const int k0 = c0 * 16, k1 = min(c1 * 16, H);
 #pragma unroll
-    for (int u = 0; u < RB; u++) {
-      const int j = min(tid + u * NT, H - 1);
-      x[u] = src[j];
-      nwv[u] = a.nw[j];
-    }
-    // without a delta the loads below read the norm gains instead (in-bounds,
-    // values unused), so that no load sits behind a branch
-    const bool has_delta = a.delta.acc != nullptr;
-    const int *dacc = has_delta ? a.delta.acc : reinterpret_cast<const int *>(a.nw);
-    const float *dws = has_delta ? a.delta.ws : a.nw;
-    const float *dsxp = has_delta ? a.delta.sx : a.nw;
-    int da[RB];
-    float dw[RB];
-#pragma unroll
-    for (int u = 0; u < RB; u++) {
-      const int j = min(tid + u * NT, H - 1);
-      da[u] = dacc[j];
-      dw[u] = dws[j];
-    }
-    const float dsx = dsxp[0];
+    for (int u = 0; u < RB; u++) x[u] = a.vec[min(k0 + tid + u * NT, H - 1)];
+    const float mx = __uint_as_float(a.hmax[0]);
     issue_weights();
-    if (has_delta) {
-#pragma unroll
-      for (int u = 0; u < RB; u++) {
-        const float f = (float)da[u] * dsx;
-        const float d = f * dw[u];
-        x[u] = x[u] + d;
-      }
-    }
+    hq = quantize_range_with_max<NT>(x, k0, k1, mx, xq);
   } else if constexpr (PRO == PRO_QUANT) {
 #pragma unroll
     for (int u = 0; u < RB; u++) x[u] = a.vec[min(tid + u * NT, H - 1)];
@@ -330,41 +424,9 @@ __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
 
   float sv;
   if constexpr (NORM) {
-    // RMSNorm (ops/norm.rs:8-38): out = (x*w) * (1/sqrt(sumsq/n + eps)),
-    // then the quantizer's max|out|.  Scaling by the positive `scale` is a
-    // monotonic rounding, so max|t*scale| = fl(max|t| * scale): the max of
-    // t = x*w is reduced while lanes 0-3 run the sum-of-squares chains (or
-    // lane 0 the single sequential sum).
-    float t[RB];
-#pragma unroll
-    for (int u = 0; u < RB; u++) {
-      const int j = tid + u * NT;
-      if (j < H) sq[PRO == PRO_MNORM ? j : sq_slot(j, H)] = x[u] * x[u];
-      t[u] = x[u] * nwv[u];
-    }
-    wg_max_post<NT>(local_absmax<NT>(t, H), red, 0);
-    bar<NT>();
-    SYN_TS(3);
-    float ss;
-    if constexpr (PRO == PRO_MNORM) {
-      if (tid == 0) red[36] = seq_sum(sq, H);
-      bar<NT>();
-      ss = red[36];
-    } else {
-      ss = sumsq_chains<NT>(sq, H, red);
-    }
-    SYN_TS(4);
-    const float scale = 1.0f / sqrtf(ss / (float)H + a.eps);
-    float nv[RB];
-#pragma unroll
-    for (int u = 0; u < RB; u++) nv[u] = t[u] * scale;
-    float mx = wg_max_get<NT>(red, 0) * scale;
-    if (!(mx <= 3.402823466e38f) || !(scale > 0.0f)) {  // inf/nan rows: reduce explicitly
-      wg_max_post<NT>(local_absmax<NT>(nv, H), red, 16);
-      bar<NT>();
-      mx = wg_max_get<NT>(red, 16);
-    }
-    sv = quantize_regs_with_max<NT>(nv, H, mx, xq);
+    sv = norm_quant<NT, PRO == PRO_MNORM>(a.eps, H, x, nwv, sq, xq, red);
+  } else if constexpr (PRO == PRO_HQ) {
+    sv = hq;
   } else {
     sv = quantize_regs<NT>(x, H, xq, red, 0);
   }
@@ -540,6 +602,176 @@ syn_status_t launch_fused_swiglu_gemv(RowSrc gu, int inter, float *s_out, const 
   return launch_fused<PRO_SWIGLU>(a, g, s);
 }
 
+// ------------------------------------------------------------------ gate|up + SwiGLU
+// x_mid = x + delta, RMSNorm, quantize (the PRO_NORM prologue), then for 16
+// rows j of the intermediate size both GEMVs over the whole K: gate row j
+// and up row inter + j of the stacked [gate | up] matrix, and the SwiGLU
+// epilogue h[j] = silu(gate_j) * up_j (int8.rs:500-503), each factor the
+// M <= 16 epilogue (f32(acc)*sx)*sw.  No K split, so a workgroup holds the
+// final values of its rows: SwiGLU runs once per element instead of once
+// per down-GEMV workgroup.  The workgroup's max |h| goes to hmax by an
+// atomic max of the f32 bits (|h| >= 0, so the bit order is the value
+// order; NaN is skipped as the reference quantizer's `if a > m` skips it),
+// so the down GEMV quantizes h without reducing it again.
+struct GuArgs {
+  const i32x4 *W;   // stacked [gate | up] rows, panel layout
+  const float *ws;  // per-row scales of the stacked rows
+  int C, inter;
+  float *h;
+  unsigned *hmax;
+  const uint64_t *exp_tab;
+};
+
+// 16 rows j per workgroup, 256 threads.  Load instruction t (of 2*CG, CG =
+// ceil(C/4) chunk groups per matrix) covers matrix t / CG (gate, up) and
+// chunks 4*(t % CG) .. +3 of the 16 rows: lane l reads row l % 16, chunk
+// 4*(t % CG) + l / 16 (four 256-byte runs of the panel layout).  Wave w
+// takes instructions w, w + 4, ...; the partial sums of a row meet over
+// lanes (xor 16, 32) and waves (LDS).
+constexpr int kGuRows = 16;
+
+// grid (ceil(inter / 16)); dynamic LDS: sq[round4(H)] floats | xq[C*16]
+template <int UI>
+__global__ void __launch_bounds__(256) k_gu_swiglu(ProArgs a, GuArgs g) {
+  constexpr int NT = 256, NW = NT / 64;
+  extern __shared__ __align__(16) unsigned char smem[];
+  __shared__ float red[64];
+  __shared__ int redi[2 * NW * kGuRows];
+  __shared__ uint64_t exp_tab[32];
+  const int H = a.H;
+  float *sq = reinterpret_cast<float *>(smem);
+  int8_t *xq = reinterpret_cast<int8_t *>(smem) + ((H + 3) & ~3) * 4;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r = lane & (kGuRows - 1), cp = lane >> 4;
+  const int j0 = blockIdx.x * kGuRows;
+  const int jc = min(j0 + r, g.inter - 1);
+  const int CG = (g.C + 3) >> 2, T = 2 * CG;
+  const uint64_t tv = g.exp_tab[tid & 31];
+  const float wsg = g.ws[jc], wsu = g.ws[g.inter + jc];
+  i32x4 w[UI];
+  auto issue = [&]() {
+#pragma unroll
+    for (int i = 0; i < UI; i++) {
+      const int t = min(wave + i * NW, T - 1);
+      const int m = t >= CG, c = min(4 * (t - m * CG) + cp, g.C - 1);
+      const int row = m * g.inter + jc;
+      w[i] = __builtin_nontemporal_load(g.W + ((size_t)(row >> 6) * g.C + c) * 64 + (row & 63));
+    }
+    asm volatile("" ::: "memory");  // keep the weight requests ahead of the prologue
+  };
+  float x[RB], nwv[RB];
+  norm_prologue_load<NT>(a, H, x, nwv, issue);
+  if (tid < 32) exp_tab[tid] = tv;
+  for (int i = H + tid; i < g.C * 16; i += NT) xq[i] = 0;
+  const float sv = norm_quant<NT, false>(a.eps, H, x, nwv, sq, xq, red);
+  bar<NT>();
+  int ag = 0, au = 0;
+#pragma unroll
+  for (int i = 0; i < UI; i++) {
+    const int t = wave + i * NW;
+    if (t < T) {
+      const int m = t >= CG, c = 4 * (t - m * CG) + cp;
+      const i32x4 xv = *reinterpret_cast<const i32x4 *>(xq + min(c, g.C - 1) * 16);
+      int d = 0;
+      d = __builtin_amdgcn_sdot4(w[i].x, xv.x, d, false);
+      d = __builtin_amdgcn_sdot4(w[i].y, xv.y, d, false);
+      d = __builtin_amdgcn_sdot4(w[i].z, xv.z, d, false);
+      d = __builtin_amdgcn_sdot4(w[i].w, xv.w, d, false);
+      d = c < g.C ? d : 0;
+      if (m) au += d;
+      else ag += d;
+    }
+  }
+  ag += __shfl_xor(ag, 16);
+  au += __shfl_xor(au, 16);
+  ag += __shfl_xor(ag, 32);
+  au += __shfl_xor(au, 32);
+  if (lane < kGuRows) {
+    redi[wave * kGuRows + lane] = ag;
+    redi[(NW + wave) * kGuRows + lane] = au;
+  }
+  bar<NT>();
+  if (wave == 0) {
+    float m = 0.0f;
+    if (lane < kGuRows) {
+      int sg = 0, su = 0;
+#pragma unroll
+      for (int i = 0; i < NW; i++) {
+        sg += redi[i * kGuRows + lane];
+        su += redi[(NW + i) * kGuRows + lane];
+      }
+      const int j = j0 + lane;
+      if (j < g.inter) {
+        const float fg = (float)sg * sv, fu = (float)su * sv;
+        const float gv = fg * wsg, uv = fu * wsu;
+        const float act = syn_silu_tab(gv, exp_tab);
+        const float hv = act * uv;
+        g.h[j] = hv;
+        const float av = fabsf(hv);
+        if (av > m) m = av;
+      }
+    }
+    m = wave_max_nonneg(m);
+    if (lane == 0) atomicMax(g.hmax, __float_as_uint(m));
+  }
+  if (blockIdx.x == 0) {  // the residual row for the next layer, the scale
+    if (a.res_out) {
+#pragma unroll
+      for (int u = 0; u < RB; u++)
+        if (tid + u * NT < H) a.res_out[tid + u * NT] = x[u];
+    }
+    if (tid == 0) a.s_out[0] = sv;
+  }
+}
+
+bool gu_swiglu_fits(int H) { return H <= RB * 256; }
+
+syn_status_t launch_gu_swiglu(const float *base, RowSrc delta, float *res_out, const float *nw,
+                              float eps, int H, float *s_out, const void *W, const float *ws,
+                              int C, int inter, float *h, unsigned *hmax, hipStream_t s) {
+  if (!gu_swiglu_fits(H) || inter <= 0 || C != (int)cdiv((size_t)H, 16)) {
+    set_error("gate|up SwiGLU GEMV: hidden size outside the kernel's limits");
+    return SYN_ERR_INVALID_ARG;
+  }
+  ProArgs a{};
+  a.base = base;
+  a.delta = delta;
+  a.res_out = res_out;
+  a.nw = nw;
+  a.eps = eps;
+  a.H = H;
+  a.s_out = s_out;
+  GuArgs g{reinterpret_cast<const i32x4 *>(W), ws, C, inter, h, hmax, exp_table_address()};
+  if (!g.exp_tab) {
+    set_error("fused decode: expf table address unavailable");
+    return SYN_ERR_HIP;
+  }
+  const size_t shm = round_up((size_t)H, 4) * 4 + (size_t)g.C * 16;
+  const dim3 grid((unsigned)cdiv((size_t)inter, kGuRows));
+  const int ui = (int)cdiv(2 * cdiv((size_t)g.C, 4), 4);  // load instructions per wave
+  if (ui <= 2) hipLaunchKernelGGL((k_gu_swiglu<2>), grid, dim3(256), shm, s, a, g);
+  else if (ui <= 4) hipLaunchKernelGGL((k_gu_swiglu<4>), grid, dim3(256), shm, s, a, g);
+  else if (ui <= 8) hipLaunchKernelGGL((k_gu_swiglu<8>), grid, dim3(256), shm, s, a, g);
+  else hipLaunchKernelGGL((k_gu_swiglu<16>), grid, dim3(256), shm, s, a, g);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
+
+syn_status_t launch_fused_hq_gemv(const float *vec, const unsigned *hmax, int H, float *s_out,
+                                  const SplitGemv &g, hipStream_t s) {
+  if (!vec || !hmax) {
+    set_error("fused decode GEMV: quantized-range prologue needs the vector and its max");
+    return SYN_ERR_INVALID_ARG;
+  }
+  ProArgs a{};
+  a.vec = vec;
+  a.hmax = hmax;
+  a.H = H;
+  a.s_out = s_out;
+  return launch_fused<PRO_HQ>(a, g, s);
+}
+
 // ------------------------------------------------------------------ attention
 // One workgroup per query head.  Prologue = k_qk_norm_rope_kv for the head
 // and its KV head (both query heads of a KV group write the same K/V values
@@ -700,63 +932,210 @@ __device__ __forceinline__ float wave_max_any(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
-constexpr int kPre = 48;  // V groups (4 positions each) prefetched into registers
+// ------------------------------------------------------------------ head attention
+// Decode attention in one kernel: grid (query heads, HD / CB column blocks),
+// 256 threads.  Every workgroup of a head computes the head's prologue (q/k/v
+// rows, head RMSNorms, RoPE), all of its scores and the softmax, then the P.V
+// chains of its CB columns; the workgroup of column block 0 of the first
+// query head of a KV group appends the new K/V rows.  Compared with a scores
+// kernel followed by a softmax + P.V kernel this removes one kernel boundary
+// per layer, and every dependent chain runs from registers: q and the
+// probabilities are read from LDS in blocks of 32 values that are issued
+// before the previous block's arithmetic (pin_regs), the K row of a lane's
+// position is loaded at kernel entry, and V reaches LDS through gfx950's
+// direct global -> LDS loads, one 128-position chunk ahead of the chain.
+// Every float operation and its order is the one of ops/attention.rs:24-147
+// (scores: fused multiply-adds for positions below n8 when len >= 64, a
+// rounded product and add otherwise; softmax_slice; P.V: fused multiply-adds
+// over the positions when len >= 64 and the column lies in a whole 32-column
+// block).
+constexpr int kAttnNT = 256;
+constexpr int kPvChunk = 128;            // positions per staged V chunk
+constexpr int kPvGroups = kPvChunk / 4;  // 4-position groups per chunk
 
-// ------------------------------------------------------------------ split attention
-// Decode attention for head sizes 16/32/64/128 in two kernels that spread
-// the work of a head over many workgroups (one workgroup per head runs every
-// position's chain and pulls the whole cache of its KV head through one CU).
-//  k_attn_scores      grid (heads, chunks of kScoreP positions): prologue
-//                     (q/k rows, head RMSNorms, RoPE; the chunk holding the
-//                     new position also appends its K/V rows), then one
-//                     dot-product chain per position -> scores[head][p];
-//  k_attn_softmax_pv  grid (heads, groups of kPvCols columns): softmax of the
-//                     head's scores (in every workgroup), then one P.V chain
-//                     per column.
-// Every float operation, and its order, is the one of ops/attention.rs:24-147
-// (the generic k_fused_attention above computes the same values).
-constexpr int kScoreP = 16;  // positions per scores workgroup
-constexpr int kPvCols = 16;  // columns per P.V workgroup
+// lane l's 16 bytes at src land at lds_base + 16 * l (gfx950
+// global_load_lds_dwordx4; lds_base is wave-uniform)
+__device__ __forceinline__ void g2lds16(const void *src, void *lds_base) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds_base, 16,
+                                   0, 0);
+}
 
+// V groups [g0, g0 + ngroups) (4 positions of one column per 16 bytes,
+// indices clamped to the cache; ngroups rounded up to whole wave
+// instructions) of columns [cb0, cb0 + CB) into dst[group][CB], issued by
+// waves w0 .. w0 + nw - 1
+template <int CB>
+__device__ __forceinline__ void stage_v_chunk(const f32x4 *V4, int hd, int s4, int cb0, int g0,
+                                              f32x4 *dst, int wave, int w0, int nw, int lane,
+                                              int ngroups) {
+  constexpr int GPI = 64 / CB;  // groups per wave instruction
+  const int gl = lane / CB, col = lane % CB;
+  for (int gi = (wave - w0) * GPI; gi < ngroups; gi += nw * GPI) {
+    const int g = min(g0 + gi + gl, s4 - 1);
+    g2lds16(V4 + (size_t)g * hd + cb0 + col, dst + gi * CB);
+  }
+}
+
+// score chain sum_d q[d] * k[d], d = 0 .. HD-1 in order: q from LDS
+// (broadcast), the K row in registers
+template <int HD, bool FUSED>
+__device__ __forceinline__ float q_dot_chain(const f32x4 *q4, const f32x4 (&kr)[HD / 4]) {
+  constexpr int NB = HD / 4;
+  constexpr int BS = NB < 8 ? NB : 8;
+  constexpr int NBLK = NB / BS;
+  float acc = 0.0f;
+  f32x4 qa[BS], qb[BS];
+  auto load = [&](f32x4(&r)[BS], int blk) {
+#pragma unroll
+    for (int k = 0; k < BS; k++) r[k] = q4[blk * BS + k];
+  };
+  auto step = [&](f32x4(&r)[BS], int blk) {
+#pragma unroll
+    for (int k = 0; k < BS; k++) {
+      const f32x4 kv = kr[blk * BS + k];
+      if constexpr (FUSED) {
+        acc = __builtin_fmaf(r[k].x, kv.x, acc);
+        acc = __builtin_fmaf(r[k].y, kv.y, acc);
+        acc = __builtin_fmaf(r[k].z, kv.z, acc);
+        acc = __builtin_fmaf(r[k].w, kv.w, acc);
+      } else {
+        float t;
+        t = r[k].x * kv.x; acc = acc + t;
+        t = r[k].y * kv.y; acc = acc + t;
+        t = r[k].z * kv.z; acc = acc + t;
+        t = r[k].w * kv.w; acc = acc + t;
+      }
+    }
+  };
+  load(qa, 0);
+#pragma unroll
+  for (int blk = 0; blk < NBLK; blk += 2) {
+    if (blk + 1 < NBLK) load(qb, blk + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    pin_regs(qa);
+    step(qa, blk);
+    if (blk + 1 < NBLK) {
+      if (blk + 2 < NBLK) load(qa, blk + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      pin_regs(qb);
+      step(qb, blk + 1);
+    }
+  }
+  return acc;
+}
+
+// P.V chain of one column over whole 4-position groups [0, ng) of a staged
+// chunk: probabilities e4 (LDS, broadcast), the column's V at vt[g * CB]
+template <bool FUSED, int CB>
+__device__ __forceinline__ float pv_chain(const f32x4 *e4, const f32x4 *vt, int ng, float acc) {
+  auto step = [&](const f32x4 &E, const f32x4 &Vv) {
+    if constexpr (FUSED) {
+      acc = __builtin_fmaf(E.x, Vv.x, acc);
+      acc = __builtin_fmaf(E.y, Vv.y, acc);
+      acc = __builtin_fmaf(E.z, Vv.z, acc);
+      acc = __builtin_fmaf(E.w, Vv.w, acc);
+    } else {
+      float t;
+      t = E.x * Vv.x; acc = acc + t;
+      t = E.y * Vv.y; acc = acc + t;
+      t = E.z * Vv.z; acc = acc + t;
+      t = E.w * Vv.w; acc = acc + t;
+    }
+  };
+  f32x4 ea[8], va[8], eb[8], vb[8];
+  auto load = [&](f32x4(&E)[8], f32x4(&Vr)[8], int blk) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      E[k] = e4[blk * 8 + k];
+      Vr[k] = vt[(blk * 8 + k) * CB];
+    }
+  };
+  auto run = [&](f32x4(&E)[8], f32x4(&Vr)[8]) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) step(E[k], Vr[k]);
+  };
+  const int nb = ng >> 3;
+  int blk = 0;
+  if (nb > 0) {
+    load(ea, va, 0);
+    for (; blk + 1 < nb; blk += 2) {
+      load(eb, vb, blk + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      pin_regs(ea);
+      pin_regs(va);
+      run(ea, va);
+      load(ea, va, min(blk + 2, nb - 1));  // in bounds; unused past the end
+      __builtin_amdgcn_sched_barrier(0);
+      pin_regs(eb);
+      pin_regs(vb);
+      run(eb, vb);
+    }
+    if (blk < nb) {
+      pin_regs(ea);
+      pin_regs(va);
+      run(ea, va);
+    }
+  }
+  // the last ng % 8 groups: one batch of reads, then the chains
+  const int rg = ng - nb * 8;
+  if (rg > 0) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const int g = nb * 8 + min(k, rg - 1);
+      ea[k] = e4[g];
+      va[k] = vt[g * CB];
+    }
+    pin_regs(ea);
+    pin_regs(va);
+#pragma unroll
+    for (int k = 0; k < 8; k++)
+      if (k < rg) step(ea[k], va[k]);
+  }
+  return acc;
+}
+
+template <int HD>
+constexpr int attn_cb() {
+  return HD < 64 ? HD : 64;
+}
+
+// dynamic LDS: e[round_up4(max_seq)] | V chunks [2][kPvGroups][CB] f32x4
 template <bool F32, int HD>
-__global__ void __launch_bounds__(256)
-    k_attn_scores(RowSrc qkv, int nh, int nkv, const float *__restrict__ qn,
-                  const float *__restrict__ kn, float eps, const float *__restrict__ cosT,
-                  const float *__restrict__ sinT, const StepState *__restrict__ st,
-                  float *__restrict__ kc, float *__restrict__ vc, int max_seq,
-                  float *__restrict__ scores) {
-  __shared__ __align__(16) float qv[128], kv[128], sqq[128], sqk[128];
-  __shared__ float red[8];
+__global__ void __launch_bounds__(kAttnNT)
+    k_attn_head(RowSrc qkv, int nh, int nkv, const float *__restrict__ qn,
+                const float *__restrict__ kn, float eps, const float *__restrict__ cosT,
+                const float *__restrict__ sinT, const StepState *__restrict__ st,
+                float *__restrict__ kc, float *__restrict__ vc, int max_seq,
+                const uint64_t *__restrict__ exp_tab_g, float *__restrict__ out) {
+  constexpr int CB = attn_cb<HD>(), HD4 = HD / 4, HALF = HD / 2;
+  extern __shared__ __align__(16) float dsm[];
+  __shared__ __align__(16) float qv[HD], kv[HD], sqq[HD], sqk[HD], vnew[HD];
+  __shared__ float red[16];
+  __shared__ uint64_t exp_tab[32];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  constexpr int hd = HD, hd4 = HD / 4, half = HD / 2;
-  const int head = blockIdx.x, p0 = blockIdx.y * kScoreP;
+  const int head = blockIdx.x, cb0 = blockIdx.y * CB;
   const int grp = nh / nkv, kvh = head / grp;
-  const int qd = nh * hd, kvd = nkv * hd;
-  const int tiles = (max_seq + 63) >> 6;
+  const int qd = nh * HD, kvd = nkv * HD;
+  const int tiles = (max_seq + 63) >> 6, s4 = (max_seq + 3) >> 2;
+  float *e = dsm;
+  f32x4 *vbuf = reinterpret_cast<f32x4 *>(dsm + round_up4(max_seq));
+  const f32x4 *V4 = reinterpret_cast<const f32x4 *>(vc) + (size_t)kvh * s4 * HD;
+  const f32x4 *K4 = reinterpret_cast<const f32x4 *>(kc) + (size_t)kvh * tiles * HD4 * 64;
   SYN_TS_DECL
   SYN_TS(0);
   SYN_TSR(14);
 
-  // Loads that do not depend on the decode position are requested before
-  // it is read (a dependent load would wait one memory round trip for it):
-  // waves 0 and 1 (lane = position p0 + lane % kScoreP) the chunk's K rows
-  // from the tiled cache, every thread its q/k/v row values and gain.
-  const int p = p0 + (lane & (kScoreP - 1));
-  float4 pre[hd4];
-  if (wave < 2) {
-    const int pc = min(p, max_seq - 1);
-    const float4 *src = reinterpret_cast<const float4 *>(kc) +
-                        ((size_t)kvh * tiles + (pc >> 6)) * hd4 * 64 + (pc & 63);
-#pragma unroll
-    for (int c = 0; c < hd4; c++) pre[c] = src[(size_t)c * 64];
-  }
+  // 1. what does not depend on the decode position: the q / k / v row
+  //    values and gains, the expf table word, the K row of position tid and
+  //    the V of the first 64 positions of this block's columns (straight
+  //    into LDS) for wave 0 (every decode attends to position 0)
   // threads 0-127 own q[d], threads 128-255 own k[d] and v[d]
   const bool is_q = tid < 128;
   const int d = tid & 127;
-  const int dc = min(d, hd - 1), hc = min(d, half - 1);
-  const int r0 = is_q ? head * hd + dc : qd + kvh * hd + dc;
-  const int r1 = qd + kvd + kvh * hd + dc;
+  const int dc = min(d, HD - 1), hc = min(d, HALF - 1);
+  const int r0 = is_q ? head * HD + dc : qd + kvh * HD + dc;
+  const int r1 = qd + kvd + kvh * HD + dc;
   float x0, x1;
   if constexpr (F32) {
     x0 = qkv.f[r0];
@@ -770,226 +1149,178 @@ __global__ void __launch_bounds__(256)
   }
   const float *gn = is_q ? qn : kn;
   const float g = gn ? gn[dc] : 0.0f;
-  SYN_TS(1);
-
+  const uint64_t tv = exp_tab_g[tid & 31];
+  f32x4 kr[HD4];
+  auto load_k_rows = [&](int p) {
+    const int pc = min(p, max_seq - 1);
+    const f32x4 *src = K4 + (size_t)(pc >> 6) * HD4 * 64 + (pc & 63);
+#pragma unroll
+    for (int c = 0; c < HD4; c++) kr[c] = src[(size_t)c * 64];
+  };
+  if (wave == 0) {
+    load_k_rows(tid);
+    stage_v_chunk<CB>(V4, HD, s4, cb0, 0, vbuf, 0, 0, 1, lane, 16);
+  }
   const int pos = st->pos;
   const int len = pos + 1;
-  if (p0 >= len) return;
-  const bool has_new = pos < p0 + kScoreP;         // this chunk holds the new position
-  const bool append = has_new && head % grp == 0;  // one writer per KV head
-  const float cs = cosT[(size_t)pos * half + hc], sn = sinT[(size_t)pos * half + hc];
+  SYN_TS(1);
+  // then the rest of the first pass of K rows and of the first V chunk,
+  // for the positions the decode attends to
+  if (wave != 0) {
+    if (wave * 64 < len) load_k_rows(tid);
+    if (len > 64) stage_v_chunk<CB>(V4, HD, s4, cb0, 16, vbuf + 16 * CB, wave, 1, 3, lane,
+                                    min(kPvGroups, (len + 3) >> 2) - 16);
+  }
+
+  // 2. q and k: head RMSNorms (norm.rs:78-93; the q chains on wave 0 and
+  //    the k chains on wave 2 at the same time) and rotate-half RoPE at pos
+  //    (rope.rs:13-43)
+  const float cs = cosT[(size_t)pos * HALF + hc], sn = sinT[(size_t)pos * HALF + hc];
   float *myv = is_q ? qv : kv;
   float *mysq = is_q ? sqq : sqk;
-  const bool mine = is_q || has_new;  // k is needed only where the new position is
-  SYN_TS(2);
-  if (d < hd) {
+  if (d < HD) {
     myv[d] = x0;
-    mysq[sq_slot(d, hd)] = x0 * x0;
+    mysq[sq_slot(d, HD)] = x0 * x0;
+    if (!is_q) vnew[d] = x1;
+  }
+  if (tid < 32) exp_tab[tid] = tv;
+  __syncthreads();
+  SYN_TS(2);
+  if (lane < 4) {
+    if (wave == 0 && qn) red[lane] = sumsq_chain(sqq, HD, lane);
+    if (wave == 2 && kn) red[4 + lane] = sumsq_chain(sqk, HD, lane);
   }
   __syncthreads();
   SYN_TS(3);
-  // head RMSNorms (norm.rs:78-93): the q chains on wave 0, the k chains on
-  // wave 2, at the same time
-  if (lane < 4) {
-    if (wave == 0 && qn) red[lane] = sumsq_chain(sqq, hd, lane);
-    if (wave == 2 && kn && has_new) red[4 + lane] = sumsq_chain(sqk, hd, lane);
-  }
-  __syncthreads();
-  SYN_TS(4);
-  if (gn && mine && d < hd) {
-    const float ss = sumsq_combine(red + (is_q ? 0 : 4), mysq, hd);
-    const float scale = 1.0f / sqrtf(ss / (float)hd + eps);
+  if (gn && d < HD) {
+    const float ss = sumsq_combine(red + (is_q ? 0 : 4), mysq, HD);
+    const float scale = 1.0f / sqrtf(ss / (float)HD + eps);
     const float t = myv[d] * g;
     myv[d] = t * scale;
   }
   __syncthreads();
-  // rotate-half RoPE at pos (rope.rs:13-43); lane i < half owns (i, half+i)
-  if (mine && d < half) {
-    const float a = myv[d], b = myv[half + d];
+  if (d < HALF) {
+    const float a = myv[d], b = myv[HALF + d];
     const float pp = a * cs, qq = b * sn, rr = b * cs, tt = a * sn;
     myv[d] = pp - qq;
-    myv[half + d] = rr + tt;
+    myv[HALF + d] = rr + tt;
   }
   __syncthreads();
-  if (append && !is_q && d < hd) {
-    kc[kv_k_index(pos, kvh, d, hd, max_seq)] = kv[d];
-    vc[kv_v_index(pos, kvh, d, hd, max_seq)] = x1;
+  if (head % grp == 0 && blockIdx.y == 0 && !is_q && d < HD) {  // one writer per KV head
+    kc[kv_k_index(pos, kvh, d, HD, max_seq)] = kv[d];
+    vc[kv_v_index(pos, kvh, d, HD, max_seq)] = x1;
   }
-  SYN_TS(5);
+  SYN_TS(4);
 
-  // scores: the positions below n8 take fused multiply-add chains (wave 0),
-  // the others plain ones (wave 1), as f32GemvRow's column blocks do.  Each
-  // wave runs its chain for all 64 lanes without branches (q comes from LDS
-  // as broadcast reads, which the compiler issues ahead of the chain) and
-  // stores the positions of its kind.
+  // 3. scores, kAttnNT positions per pass (lane = position).  A wave runs
+  //    the fused chain if any of its positions is below n8 and the plain
+  //    one if any is not; each lane keeps its own kind.  The lane of the
+  //    new position takes the K row from LDS.
+  const float scale = 1.0f / sqrtf((float)HD);
   const bool simd = len >= 64;
   const int n32 = len - len % 32;
   const int n8 = n32 + ((len - n32) / 8) * 8;
-  const bool fused_wave = wave == 0 && simd && p0 < n8;
-  const bool plain_wave = wave == 1 && (!simd || p0 + kScoreP > n8);
-  if (fused_wave || plain_wave) {
-    const float scale = 1.0f / sqrtf((float)hd);
-    const float4 *q4 = reinterpret_cast<const float4 *>(qv);
-    // the lane of position pos takes the new K row from LDS (a select, no branch)
-    const bool is_new = p == pos;
-    const float4 *k4 = reinterpret_cast<const float4 *>(kv);
+  const f32x4 *q4 = reinterpret_cast<const f32x4 *>(qv);
+  float mx = -__builtin_inff();
+  for (int base = 0; base < len; base += kAttnNT) {
+    if (base > 0) load_k_rows(base + tid);
+    const int w0 = base + wave * 64;  // first position of this wave
+    if (w0 < len) {
+      const int p = base + tid;
+      if (w0 <= pos && pos < w0 + 64) {
+        const bool is_new = p == pos;
+        const f32x4 *k4 = reinterpret_cast<const f32x4 *>(kv);
 #pragma unroll
-    for (int c = 0; c < hd4; c++) {
-      const float4 kn4 = k4[c];
-      pre[c].x = is_new ? kn4.x : pre[c].x;
-      pre[c].y = is_new ? kn4.y : pre[c].y;
-      pre[c].z = is_new ? kn4.z : pre[c].z;
-      pre[c].w = is_new ? kn4.w : pre[c].w;
-    }
-    float acc = 0.0f;
-    if (fused_wave) {
-#pragma unroll
-      for (int c = 0; c < hd4; c++) {
-        const float4 qc = q4[c];
-        acc = __builtin_fmaf(qc.x, pre[c].x, acc);
-        acc = __builtin_fmaf(qc.y, pre[c].y, acc);
-        acc = __builtin_fmaf(qc.z, pre[c].z, acc);
-        acc = __builtin_fmaf(qc.w, pre[c].w, acc);
+        for (int c = 0; c < HD4; c++) {
+          const f32x4 kn4 = k4[c];
+          kr[c] = is_new ? kn4 : kr[c];
+        }
       }
-    } else {
-#pragma unroll
-      for (int c = 0; c < hd4; c++) {
-        const float4 qc = q4[c];
-        float t;
-        t = qc.x * pre[c].x; acc = acc + t;
-        t = qc.y * pre[c].y; acc = acc + t;
-        t = qc.z * pre[c].z; acc = acc + t;
-        t = qc.w * pre[c].w; acc = acc + t;
+      float sf = 0.0f, sp = 0.0f;
+      if (simd && w0 < n8) sf = q_dot_chain<HD, true>(q4, kr);
+      if (!simd || w0 + 63 >= n8) sp = q_dot_chain<HD, false>(q4, kr);
+      const float acc = simd && p < n8 ? sf : sp;
+      if (p < len) {
+        const float sc = acc * scale;
+        e[p] = sc;
+        mx = fmaxf(mx, sc);
       }
     }
-    SYN_TS(6);
-    const bool mine_p = fused_wave == (simd && p < n8);
-    if (lane < kScoreP && p < len && mine_p) scores[(size_t)head * max_seq + p] = acc * scale;
   }
+
+  SYN_TS(5);
+  // 4. softmax_slice (activation.rs:117-129): max, exp(x - max), the
+  //    sequential sum (thread 0), the division when the sum is positive
+  mx = wave_max_any(mx);
+  if (lane == 0) red[8 + wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[8], red[9]), fmaxf(red[10], red[11]));
+  SYN_TS(6);
+  for (int i = tid; i < len; i += kAttnNT) e[i] = syn_expf_tab(e[i] - mx, exp_tab);
+  __syncthreads();
   SYN_TS(7);
+  if (tid == 0) red[12] = lds_seq_sum(e, len, 0.0f);
+  __syncthreads();
+  SYN_TS(8);
+  const float sum = red[12];
+  if (sum > 0.0f)
+    for (int i = tid; i < len; i += kAttnNT) e[i] = e[i] / sum;
+
+  // 5. P.V: wave 0 runs the chains (lane = column; lanes >= CB repeat
+  //    columns and store nothing) over 128-position chunks while waves 1-3
+  //    stage the next chunk into the other buffer
+  const bool fused_pv = simd && (HD % 32) == 0;
+  const int col = lane % CB;
+  const f32x4 *e4 = reinterpret_cast<const f32x4 *>(e);
+  float acc = 0.0f;
+  SYN_TS(9);
+  for (int c = 0, cpos = 0; cpos < len; c++, cpos += kPvChunk) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    SYN_TS(10);
+    f32x4 *buf = vbuf + (c & 1) * kPvGroups * CB;
+    if (wave != 0) {
+      if (cpos + kPvChunk < len)
+        stage_v_chunk<CB>(V4, HD, s4, cb0, (c + 1) * kPvGroups,
+                          vbuf + ((c + 1) & 1) * kPvGroups * CB, wave, 1, kAttnNT / 64 - 1, lane,
+                          min(kPvGroups, (len - cpos - kPvChunk + 3) >> 2));
+    } else {
+      if (pos >= cpos && pos < cpos + kPvChunk && lane < CB) {  // this step's V row
+        float *slot = reinterpret_cast<float *>(buf + ((pos - cpos) >> 2) * CB + col) + (pos & 3);
+        *slot = vnew[cb0 + col];
+      }
+      const int clen = min(kPvChunk, len - cpos);
+      const int ngf = clen >> 2, rem = clen & 3;
+      const f32x4 *ec = e4 + c * kPvGroups;
+      acc = fused_pv ? pv_chain<true, CB>(ec, buf + col, ngf, acc)
+                     : pv_chain<false, CB>(ec, buf + col, ngf, acc);
+      if (rem) {
+        const f32x4 E = ec[ngf], Vv = buf[ngf * CB + col];
+        auto one = [&](float ev, float v) {
+          if (fused_pv) {
+            acc = __builtin_fmaf(ev, v, acc);
+          } else {
+            const float t = ev * v;
+            acc = acc + t;
+          }
+        };
+        one(E.x, Vv.x);
+        if (rem > 1) one(E.y, Vv.y);
+        if (rem > 2) one(E.z, Vv.z);
+      }
+    }
+  }
+  if (wave == 0 && lane < CB) out[head * HD + cb0 + lane] = acc;
+  SYN_TS(11);
   SYN_TSR(15);
   SYN_TS_FLUSH(48);
 }
 
-// softmax_slice (activation.rs:117-129) of the head's scores, then P.V for
-// kPvCols columns; dynamic LDS: e[max_seq rounded to 4]
-__global__ void __launch_bounds__(256)
-    k_attn_softmax_pv(int nh, int nkv, int hd, const uint64_t *exp_tab_g,
-                      const StepState *__restrict__ st, const float *__restrict__ vc, int max_seq,
-                      const float *__restrict__ scores, float *__restrict__ out) {
-  constexpr int NT = 256;
-  extern __shared__ __align__(16) float e[];
-  __shared__ float red[64];
-  __shared__ uint64_t exp_tab[32];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int head = blockIdx.x, kvh = head / (nh / nkv);
-  const int s4 = (max_seq + 3) >> 2;
-  const float4 *V4 = reinterpret_cast<const float4 *>(vc) + (size_t)kvh * s4 * hd;
-  const int d = blockIdx.y * kPvCols + (lane & (kPvCols - 1));
-  const int dcl = min(d, hd - 1);
-  // Loads that do not depend on the decode position first (wave 0: V of
-  // this workgroup's columns, 4 positions per 16-byte load; every thread the
-  // score of position tid and its expf table word), then the position.
-  float4 pre[kPre];
-  if (wave == 0) {
-#pragma unroll
-    for (int i = 0; i < kPre; i++) pre[i] = V4[(size_t)min(i, s4 - 1) * hd + dcl];
-  }
-  const uint64_t tv = exp_tab_g[tid & 31];
-  const float *sh = scores + (size_t)head * max_seq;
-  const float s0 = sh[min(tid, max_seq - 1)];
-  SYN_TS_DECL
-  SYN_TS(0);
-  SYN_TSR(14);
-  const int pos = st->pos;
-  const int len = pos + 1, ngroups = (len + 3) >> 2;
-  float mx = -__builtin_inff();
-  if (tid < len) {
-    e[tid] = s0;
-    mx = s0;
-  }
-  for (int i = tid + NT; i < len; i += NT) {
-    const float v = sh[i];
-    e[i] = v;
-    mx = fmaxf(mx, v);
-  }
-  if (tid < 32) exp_tab[tid] = tv;
-  SYN_TS(1);
-  mx = wave_max_any(mx);
-  if (lane == 0) red[wave] = mx;
-  __syncthreads();
-  SYN_TS(2);
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  for (int i = tid; i < len; i += NT) e[i] = syn_expf_tab(e[i] - mx, exp_tab);
-  __syncthreads();
-  SYN_TS(3);
-  // the sequential sum of the exponentials (thread 0), then the division
-  if (tid == 0) red[40] = seq_sum_pipelined(e, len);
-  __syncthreads();
-  SYN_TS(4);
-  const float sum = red[40];
-  if (sum > 0.0f)
-    for (int i = tid; i < len; i += NT) e[i] = e[i] / sum;
-  __syncthreads();
-  SYN_TS(5);
-  if (wave != 0) return;
-
-  // P.V (wave 0, lane = column; lanes >= kPvCols repeat the first kPvCols
-  // columns and store nothing): one chain over the positions per column,
-  // fused multiply-adds on the len >= 64 route for columns inside whole
-  // 32-column blocks (all columns of these head sizes), plain ones
-  // otherwise.  Positions go in blocks of 16 behind one wave-uniform branch
-  // each; inside a block the probabilities are LDS broadcast reads issued
-  // ahead of the chain and positions past the end are dropped by selects.
-  const float4 *e4 = reinterpret_cast<const float4 *>(e);
-  auto chain = [&](auto fused_t) {
-    constexpr bool F = decltype(fused_t)::value;
-    float acc = 0.0f;
-    auto step = [&](bool valid, float ev, float v) {
-      if constexpr (F) {
-        const float r = __builtin_fmaf(ev, v, acc);
-        acc = valid ? r : acc;
-      } else {
-        const float t = ev * v;
-        const float r = acc + t;
-        acc = valid ? r : acc;
-      }
-    };
-    auto block = [&](int g0, const float4 (&vb)[4]) {
-      float4 eb[4];
-#pragma unroll
-      for (int k = 0; k < 4; k++) eb[k] = e4[min(g0 + k, s4 - 1)];
-#pragma unroll
-      for (int k = 0; k < 4; k++) {
-        const int q = 4 * (g0 + k);
-        step(q + 0 < len, eb[k].x, vb[k].x);
-        step(q + 1 < len, eb[k].y, vb[k].y);
-        step(q + 2 < len, eb[k].z, vb[k].z);
-        step(q + 3 < len, eb[k].w, vb[k].w);
-      }
-    };
-#pragma unroll
-    for (int b = 0; b < kPre / 4; b++) {
-      if (4 * b < ngroups) {
-        const float4 vb[4] = {pre[4 * b], pre[4 * b + 1], pre[4 * b + 2], pre[4 * b + 3]};
-        block(4 * b, vb);
-      }
-    }
-    for (int g0 = kPre; g0 < ngroups; g0 += 4) {  // beyond the prefetched groups
-      float4 vb[4];
-#pragma unroll
-      for (int k = 0; k < 4; k++) vb[k] = V4[(size_t)min(g0 + k, s4 - 1) * hd + dcl];
-      block(g0, vb);
-    }
-    return acc;
-  };
-  const float acc = len >= 64 && hd % 32 == 0 ? chain(std::true_type{}) : chain(std::false_type{});
-  if (lane < kPvCols && d < hd) out[head * hd + d] = acc;
-  SYN_TS(6);
-  SYN_TSR(15);
-  SYN_TS_FLUSH(64);
+static size_t attn_head_lds_bytes(int hd, int max_seq) {
+  const int cb = hd < 64 ? hd : 64;
+  return (size_t)round_up4(max_seq) * 4 + 2 * (size_t)kPvGroups * cb * 16;
 }
+constexpr size_t kAttnHeadMaxLds = 152 * 1024;  // of 160 KiB, leaving the static rows
 
 static bool attention_fast_ok(int hd) { return hd == 16 || hd == 32 || hd == 64 || hd == 128; }
 
@@ -998,6 +1329,7 @@ static size_t attention_lds_bytes(int hd, int max_seq) {
 }
 
 bool fused_attention_fits(int hd, int max_seq) {
+  if (attention_fast_ok(hd)) return attn_head_lds_bytes(hd, max_seq) <= kAttnHeadMaxLds;
   return attention_lds_bytes(hd, max_seq) <= 60 * 1024;
 }
 
@@ -1005,41 +1337,46 @@ syn_status_t launch_fused_attention(RowSrc qkv, int nh, int nkv, int hd, const f
                                     const float *kn, float eps, const float *cosT,
                                     const float *sinT, const StepState *st, float *kc, float *vc,
                                     int max_seq, float *scores, float *out, hipStream_t s) {
+  (void)scores;
   if (!fused_attention_fits(hd, max_seq)) {
     set_error("fused decode attention: max_seq too long for LDS");
     return SYN_ERR_INVALID_ARG;
   }
-  const size_t shm = attention_lds_bytes(hd, max_seq);
   if (attention_fast_ok(hd)) {
     const uint64_t *tab = exp_table_address();
     if (!tab) {
       set_error("fused decode: expf table address unavailable");
       return SYN_ERR_HIP;
     }
-    const dim3 sgrid((unsigned)nh, (unsigned)cdiv((size_t)max_seq, (size_t)kScoreP));
-    auto scores_kernel = [&](auto hdc) {
-      constexpr int H = decltype(hdc)::value;
-      if (qkv.f)
-        hipLaunchKernelGGL((k_attn_scores<true, H>), sgrid, dim3(256), 0, s, qkv, nh, nkv, qn, kn,
-                           eps, cosT, sinT, st, kc, vc, max_seq, scores);
-      else
-        hipLaunchKernelGGL((k_attn_scores<false, H>), sgrid, dim3(256), 0, s, qkv, nh, nkv, qn,
-                           kn, eps, cosT, sinT, st, kc, vc, max_seq, scores);
+    const size_t shm = attn_head_lds_bytes(hd, max_seq);
+    static bool attr[2][4] = {};
+    auto run = [&](auto kern, int which) -> syn_status_t {
+      bool &done = attr[qkv.f ? 1 : 0][which];
+      if (!done) {  // more than the default 64 KiB of dynamic LDS
+        SYN_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    (int)kAttnHeadMaxLds));
+        done = true;
+      }
+      const int cb = hd < 64 ? hd : 64;
+      hipLaunchKernelGGL(kern, dim3((unsigned)nh, (unsigned)(hd / cb)), dim3(kAttnNT), shm, s, qkv,
+                         nh, nkv, qn, kn, eps, cosT, sinT, st, kc, vc, max_seq, tab, out);
+      SYN_LAUNCH_CHECK();
+      return SYN_OK;
     };
-    switch (hd) {
-      case 16: scores_kernel(std::integral_constant<int, 16>{}); break;
-      case 32: scores_kernel(std::integral_constant<int, 32>{}); break;
-      case 64: scores_kernel(std::integral_constant<int, 64>{}); break;
-      default: scores_kernel(std::integral_constant<int, 128>{}); break;
-    }
-    SYN_LAUNCH_CHECK();
-    const size_t eshm = round_up((size_t)max_seq, 4) * sizeof(float);
-    hipLaunchKernelGGL(k_attn_softmax_pv, dim3((unsigned)nh, (unsigned)cdiv((size_t)hd, (size_t)kPvCols)),
-                       dim3(256), eshm, s, nh, nkv, hd, tab, st, vc, max_seq, scores, out);
-  } else {
-    hipLaunchKernelGGL(k_fused_attention, dim3(nh), dim3(256), shm, s, qkv, nh, nkv, hd, qn, kn,
-                       eps, cosT, sinT, st, kc, vc, max_seq, out);
+    auto pick = [&](auto f32c) -> syn_status_t {
+      constexpr bool F = decltype(f32c)::value;
+      switch (hd) {
+        case 16: return run(k_attn_head<F, 16>, 0);
+        case 32: return run(k_attn_head<F, 32>, 1);
+        case 64: return run(k_attn_head<F, 64>, 2);
+        default: return run(k_attn_head<F, 128>, 3);
+      }
+    };
+    return qkv.f ? pick(std::true_type{}) : pick(std::false_type{});
   }
+  const size_t shm = attention_lds_bytes(hd, max_seq);
+  hipLaunchKernelGGL(k_fused_attention, dim3(nh), dim3(256), shm, s, qkv, nh, nkv, hd, qn, kn,
+                     eps, cosT, sinT, st, kc, vc, max_seq, out);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
 }

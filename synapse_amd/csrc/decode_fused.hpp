@@ -72,6 +72,18 @@ syn_status_t launch_fused_quant_gemv(const float *vec, int H, float *s_out, cons
 // h = silu(gate) * up from the stacked [gate | up] rows ; xq = q8(h) ; acc += xq . W
 syn_status_t launch_fused_swiglu_gemv(RowSrc gu, int inter, float *s_out, const SplitGemv &g,
                                       hipStream_t s);
+// x_mid = x + delta (res_out, workgroup 0); xq = q8(rmsnorm(x_mid));
+// h = silu(gate) * up over whole rows of the stacked [gate | up] matrix W
+// (int8 panel layout, 2*inter rows of C = ceil(H/16) chunks); hmax = max |h|
+// as f32 bits (atomic max; zero before the step); s_out = xq's scale
+syn_status_t launch_gu_swiglu(const float *base, RowSrc delta, float *res_out, const float *nw,
+                              float eps, int H, float *s_out, const void *W, const float *ws,
+                              int C, int inter, float *h, unsigned *hmax, hipStream_t s);
+bool gu_swiglu_fits(int H);
+// xq = q8(vec) over this split's K range with the max *hmax reduced
+// elsewhere ; s_out ; acc += xq . W
+syn_status_t launch_fused_hq_gemv(const float *vec, const unsigned *hmax, int H, float *s_out,
+                                  const SplitGemv &g, hipStream_t s);
 // per query head: q/k/v rows from the QKV partials, head RMSNorm, RoPE at
 // state->pos, KV append, attention over positions [0, pos]; scores is
 // [nh][max_seq] f32 scratch

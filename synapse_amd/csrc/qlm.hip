@@ -245,7 +245,8 @@ struct syn_hip_qlm_s {
                                   Ly.down.chunks, cus, 512);
       per_layer = (size_t)Ly.f_qkv.N64 + Ly.f_o.N64 + Ly.f_gu.N64 + Ly.f_down.N64;
     }
-    acc_elems = per_layer * L;
+    // then one max |h| slot per layer for the gate|up SwiGLU kernel
+    acc_elems = per_layer * L + round_up(L, 64);
     SYN_TRY(acc.alloc(acc_elems * 4));
     int *p = acc.as<int>();
     for (auto &Ly : layers) {
@@ -281,10 +282,21 @@ struct syn_hip_qlm_s {
                                      rope_sin.as<float>(), st(), kc_l(l), vc_l(l), (int)S,
                                      scores.as<float>(), attn.as<float>(), s));
       SYN_TRY(launch_fused_quant_gemv(attn.as<float>(), (int)qd, s_o, Ly.f_o, s));
-      SYN_TRY(launch_fused_norm_gemv(xin.as<float>(), nullptr, st(), (int)vocab, nullptr,
-                                     Ly.f_o.rows(s_o), xmid.as<float>(), fn(l), eps,
-                                     (int)h, s_gu, Ly.f_gu, s));
-      SYN_TRY(launch_fused_swiglu_gemv(Ly.f_gu.rows(s_gu), (int)inter, s_down, Ly.f_down, s));
+      if (gu_swiglu_fits((int)h)) {
+        // gate|up over whole rows with the SwiGLU epilogue, then the down
+        // GEMV quantizes only its K range of h with the published max
+        unsigned *hmax = reinterpret_cast<unsigned *>(acc.as<int>() + acc_elems) -
+                         round_up(L, 64) + l;
+        SYN_TRY(launch_gu_swiglu(xin.as<float>(), Ly.f_o.rows(s_o), xmid.as<float>(), fn(l), eps,
+                                 (int)h, s_gu, Ly.gu.w.p, Ly.gu.scales.as<float>(), Ly.gu.chunks,
+                                 (int)inter, gu.as<float>(), hmax, s));
+        SYN_TRY(launch_fused_hq_gemv(gu.as<float>(), hmax, (int)inter, s_down, Ly.f_down, s));
+      } else {
+        SYN_TRY(launch_fused_norm_gemv(xin.as<float>(), nullptr, st(), (int)vocab, nullptr,
+                                       Ly.f_o.rows(s_o), xmid.as<float>(), fn(l), eps,
+                                       (int)h, s_gu, Ly.f_gu, s));
+        SYN_TRY(launch_fused_swiglu_gemv(Ly.f_gu.rows(s_gu), (int)inter, s_down, Ly.f_down, s));
+      }
     }
     SYN_TRY(launch_fused_final_norm(xmid.as<float>(), layers[L - 1].f_down.rows(s_down),
                                     final_nw.as<float>(), eps, (int)h, xq.as<int8_t>(), s_head, s));

@@ -13,52 +13,90 @@ __device__ __forceinline__ void bar() {
   else __builtin_amdgcn_wave_barrier();
 }
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Makes the registers of `a` an input and output of an empty asm statement:
+// every load that produces them completes before this point, and no
+// arithmetic that uses them moves ahead of it.  A dependent add chain that
+// follows then runs from registers (one VALU op every ~4.7 clocks) instead
+// of waiting for an LDS read every few operations (~20 clocks each).
+template <int N>
+__device__ __forceinline__ void pin_regs(f32x4 (&a)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; i++) asm volatile("" : "+v"(a[i]));
+}
+
+// acc + v[0] + v[1] + ... + v[n-1], added one at a time in index order (v
+// in LDS, 16-byte aligned, readable up to round_up4(n)).  The values pass
+// through registers in blocks of 32; the reads of the next block are issued
+// before the adds of the current one, so the chain never waits for LDS.
+__device__ __forceinline__ float lds_seq_sum(const float *v, int n, float acc) {
+  const f32x4 *v4 = reinterpret_cast<const f32x4 *>(v);
+  const int nb = n >> 5;
+  f32x4 a[8], b[8];
+  auto load = [&](f32x4(&r)[8], int blk) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) r[k] = v4[blk * 8 + k];
+  };
+  auto add = [&](f32x4(&r)[8]) {
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      acc = acc + r[k].x;
+      acc = acc + r[k].y;
+      acc = acc + r[k].z;
+      acc = acc + r[k].w;
+    }
+  };
+  int blk = 0;
+  if (nb > 0) {
+    load(a, 0);
+    for (; blk + 1 < nb; blk += 2) {
+      load(b, blk + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      pin_regs(a);
+      add(a);
+      load(a, min(blk + 2, nb - 1));  // in bounds; unused past the end
+      __builtin_amdgcn_sched_barrier(0);
+      pin_regs(b);
+      add(b);
+    }
+    if (blk < nb) {
+      pin_regs(a);
+      add(a);
+    }
+  }
+  // the last n % 32 values: one batch of reads (up to round_up4(n), which
+  // the callers' buffers hold), then the adds of the valid ones
+  const int rem = n - nb * 32;
+  if (rem > 0) {
+    const int ng = (rem + 3) >> 2;
+#pragma unroll
+    for (int k = 0; k < 8; k++) a[k] = v4[nb * 8 + min(k, ng - 1)];
+    pin_regs(a);
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const float c[4] = {a[k].x, a[k].y, a[k].z, a[k].w};
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const float r = acc + c[j];
+        acc = k * 4 + j < rem ? r : acc;
+      }
+    }
+  }
+  return acc;
+}
+
 // One chain of the reference sum-of-squares order (syn_vmul +
 // syn_vreduce_sum, exports.zig:366-375, 503-514): the sequential sum of
 // sq[4i+l] over the 4-aligned prefix, for chain l in 0..3.  sq holds the
 // squares of the prefix transposed (chain l contiguous at sq[l*q4 ..])
-// followed by the tail squares at sq[n4 ..]; the next 32 values are loaded
-// while the current 32 are added.
+// followed by the tail squares at sq[n4 ..]; sq is 16-byte aligned.
 __device__ __forceinline__ float sumsq_chain(const float *sq, int n, int l) {
   const int n4 = n & ~3, q4 = n4 >> 2;
   const float *p = sq + l * q4;
+  if ((q4 & 3) == 0) return lds_seq_sum(p, q4, 0.0f);  // chain start stays 16-byte aligned
   float acc = 0.0f;
-  int i = 0;
-  if (q4 > 0 && (q4 & 31) == 0) {
-    const float4 *p4 = reinterpret_cast<const float4 *>(p);
-    const int groups = q4 >> 5;
-    float4 a[8];
-#pragma unroll
-    for (int k = 0; k < 8; k++) a[k] = p4[k];
-    for (int gi = 0; gi < groups; gi++) {
-      const int nx = min(gi + 1, groups - 1) * 8;
-      float4 b[8];
-#pragma unroll
-      for (int k = 0; k < 8; k++) b[k] = p4[nx + k];
-#pragma unroll
-      for (int k = 0; k < 8; k++) {
-        acc = acc + a[k].x;
-        acc = acc + a[k].y;
-        acc = acc + a[k].z;
-        acc = acc + a[k].w;
-      }
-#pragma unroll
-      for (int k = 0; k < 8; k++) a[k] = b[k];
-    }
-    i = q4;
-  } else if ((q4 & 3) == 0) {
-    for (; i + 16 <= q4; i += 16) {
-      const float4 a = *reinterpret_cast<const float4 *>(p + i);
-      const float4 b = *reinterpret_cast<const float4 *>(p + i + 4);
-      const float4 c = *reinterpret_cast<const float4 *>(p + i + 8);
-      const float4 d = *reinterpret_cast<const float4 *>(p + i + 12);
-      acc = acc + a.x; acc = acc + a.y; acc = acc + a.z; acc = acc + a.w;
-      acc = acc + b.x; acc = acc + b.y; acc = acc + b.z; acc = acc + b.w;
-      acc = acc + c.x; acc = acc + c.y; acc = acc + c.z; acc = acc + c.w;
-      acc = acc + d.x; acc = acc + d.y; acc = acc + d.z; acc = acc + d.w;
-    }
-  }
-  for (; i < q4; i++) acc = acc + p[i];
+  for (int i = 0; i < q4; i++) acc = acc + p[i];
   return acc;
 }
 
@@ -98,50 +136,15 @@ __device__ float sumsq_lds(const float *v, int n, float *sq, float *red) {
 
 // Sequential sum of v[0..n) (a single accumulator, in index order).
 __device__ __forceinline__ float seq_sum(const float *v, int n) {
+  if ((reinterpret_cast<uintptr_t>(v) & 15) == 0) return lds_seq_sum(v, n, 0.0f);
   float s = 0.0f;
-  int i = 0;
-  if ((reinterpret_cast<uintptr_t>(v) & 15) == 0) {
-    for (; i + 16 <= n; i += 16) {
-      const float4 a = *reinterpret_cast<const float4 *>(v + i);
-      const float4 b = *reinterpret_cast<const float4 *>(v + i + 4);
-      const float4 c = *reinterpret_cast<const float4 *>(v + i + 8);
-      const float4 d = *reinterpret_cast<const float4 *>(v + i + 12);
-      s = s + a.x; s = s + a.y; s = s + a.z; s = s + a.w;
-      s = s + b.x; s = s + b.y; s = s + b.z; s = s + b.w;
-      s = s + c.x; s = s + c.y; s = s + c.z; s = s + c.w;
-      s = s + d.x; s = s + d.y; s = s + d.z; s = s + d.w;
-    }
-  }
-  for (; i < n; i++) s = s + v[i];
+  for (int i = 0; i < n; i++) s = s + v[i];
   return s;
 }
 
-// The same sequential sum with its LDS reads double-buffered: the next 16
-// values are requested while the current 16 are added (v 16-byte aligned).
+// The same sequential sum (v 16-byte aligned).
 __device__ __forceinline__ float seq_sum_pipelined(const float *v, int n) {
-  const float4 *v4 = reinterpret_cast<const float4 *>(v);
-  const int nb = n >> 4;  // whole blocks of 16
-  float s = 0.0f;
-  float4 a[4];
-#pragma unroll
-  for (int k = 0; k < 4; k++) a[k] = v4[k];
-  for (int b = 0; b < nb; b++) {
-    float4 c[4];
-    const int nx = min(b + 1, max(nb - 1, 0)) * 4;
-#pragma unroll
-    for (int k = 0; k < 4; k++) c[k] = v4[nx + k];
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-      s = s + a[k].x;
-      s = s + a[k].y;
-      s = s + a[k].z;
-      s = s + a[k].w;
-    }
-#pragma unroll
-    for (int k = 0; k < 4; k++) a[k] = c[k];
-  }
-  for (int i = nb * 16; i < n; i++) s = s + v[i];
-  return s;
+  return lds_seq_sum(v, n, 0.0f);
 }
 
 }  // namespace syn

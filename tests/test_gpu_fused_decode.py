@@ -18,6 +18,14 @@ RAGGED = dict(hidden=202, n_layers=3, n_heads=5, n_kv_heads=1, head_dim=50, inte
               vocab=777, max_seq=100)
 MHA = dict(hidden=256, n_layers=2, n_heads=4, n_kv_heads=4, head_dim=64, inter=512,
            vocab=4099, max_seq=80)
+# head sizes of the one-kernel head attention: positions past 64 (fused
+# chains), 128 (second staged V chunk) and 256 (second pass of score lanes)
+LONG128 = dict(hidden=256, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=128, inter=512,
+               vocab=1000, max_seq=300)
+HD32 = dict(hidden=192, n_layers=2, n_heads=6, n_kv_heads=3, head_dim=32, inter=384,
+            vocab=700, max_seq=160)
+HD16 = dict(hidden=128, n_layers=2, n_heads=8, n_kv_heads=2, head_dim=16, inter=256,
+            vocab=500, max_seq=150)
 
 
 @pytest.fixture(scope="module", autouse=True)
@@ -29,15 +37,17 @@ def _bits(a):
     return np.ascontiguousarray(a, np.float32).view(np.uint32)
 
 
-@pytest.mark.parametrize("cfg", [SMALL, RAGGED, MHA], ids=["small", "ragged", "mha"])
-def test_fused_matches_oracle_and_unfused(cfg):
+@pytest.mark.parametrize("cfg,cap", [(SMALL, 70), (RAGGED, 70), (MHA, 70), (LONG128, 289),
+                                     (HD32, 149), (HD16, 139)],
+                         ids=["small", "ragged", "mha", "hd128-long", "hd32", "hd16"])
+def test_fused_matches_oracle_and_unfused(cfg, cap):
     print("case", cfg, flush=True)
     o = O.QuantizedCausalLM(cfg)
     o.init_synthetic()
     g = hip.QuantizedCausalLM(cfg)
     g.init_synthetic()
     ids = O.token_ids(12, PROMPT_SEED, cfg["vocab"])
-    n_new = min(70, cfg["max_seq"] - ids.size + 1)
+    n_new = min(cap, cfg["max_seq"] - ids.size + 1)
     to, mo = o.generate(ids, n_new)
     runs = {}
     for fused in (True, False):
