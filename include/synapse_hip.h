@@ -139,6 +139,16 @@ syn_status_t syn_hip_qlinear_from_f32(int fmt, size_t n, size_t k, const float *
  * int8_linear.rs:87-117); Q4_0 runs f32 activations (Q4Linear::forward). */
 syn_status_t syn_hip_qlinear_forward(syn_hip_qlinear_t *h, size_t m, const float *d_x,
                                      float *d_y, void *stream);
+/* No counterpart in the reference: syn_hip_qlinear_forward for INT8 handles
+ * that allocates nothing, for callers that cannot call hipMalloc (code under
+ * HIP graph capture, tight serving loops).  The quantized activation rows,
+ * their scales and the split-K partials live in a fixed 4 MiB device array
+ * of the library (one per GPU, held until the process ends); a call whose
+ * rows need more returns SYN_ERR_INVALID_ARG.  Every call on a GPU shares
+ * that array, so calls that overlap on one GPU (different streams or host
+ * threads) race.  Results are bit-identical to syn_hip_qlinear_forward. */
+syn_status_t syn_hip_qlinear_forward_noalloc(syn_hip_qlinear_t *h, size_t m, const float *d_x,
+                                             float *d_y, void *stream);
 /* INT8 only: forward_pre_quantized (int8_linear.rs:139-165). */
 syn_status_t syn_hip_qlinear_forward_pre_quantized(syn_hip_qlinear_t *h, size_t m,
                                                    const int8_t *d_xq, size_t ldxq,

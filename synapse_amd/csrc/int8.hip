@@ -11,6 +11,8 @@
 #include <cmath>
 #include <vector>
 
+#include <mutex>
+#include <string>
 #include "kquant.hpp"
 #include "linear.hpp"
 
@@ -210,8 +212,20 @@ syn_status_t QLinearInt8::prepare(size_t max_m) {
   return need ? ensure_part(need) : SYN_OK;
 }
 
+size_t QLinearInt8::part_elems_for(size_t m) const {
+  if (m == 0 || m > 16 || n == 0 || k == 0) return 0;  // M > 16 runs the GEMM, no partials
+  const GemvPlan p = make_gemv_plan(n, (size_t)chunks, false);
+  return p.ksplit > 1 ? (size_t)p.ksplit * m * p.panels * 64 : 0;
+}
+
 syn_status_t QLinearInt8::gemv(size_t m, const int8_t *d_xq, size_t ldx, const float *d_sx,
                                float *d_y, size_t ldy, hipStream_t s) {
+  SYN_TRY(ensure_part(part_elems_for(std::min<size_t>(m, 16))));
+  return gemv_part(m, d_xq, ldx, d_sx, d_y, ldy, part.as<int>(), s);
+}
+
+syn_status_t QLinearInt8::gemv_part(size_t m, const int8_t *d_xq, size_t ldx, const float *d_sx,
+                                    float *d_y, size_t ldy, int *d_part, hipStream_t s) {
   if (m == 0 || n == 0 || k == 0) return SYN_OK;
   if (m > 16)  // qmatmul.zig:68-99: packed GEMM with the KC-chunked epilogue -> MFMA kernel
     return launch_gemm_w8a8(d_xq, ldx, d_sx, m, w.p, scales.as<float>(), n, chunks, d_y, ldy, s);
@@ -220,15 +234,14 @@ syn_status_t QLinearInt8::gemv(size_t m, const int8_t *d_xq, size_t ldx, const f
   const size_t N64 = (size_t)p.panels * 64;
   for (size_t m0 = 0; m0 < m; m0 += 16) {
     const int mb = (int)std::min<size_t>(16, m - m0);
-    if (p.ksplit > 1) SYN_TRY(ensure_part((size_t)p.ksplit * mb * N64));
     kGemvLaunch[mb](p, w.as<i32x4>(), scales.as<float>(), d_xq + m0 * ldx, (int)ldx, d_sx + m0,
-                    d_y + m0 * ldy, (int)ldy, part.as<int>(), (int)n, s);
+                    d_y + m0 * ldy, (int)ldy, d_part, (int)n, s);
     SYN_LAUNCH_CHECK();
     if (p.ksplit > 1) {
       const int total = mb * (int)n;
-      hipLaunchKernelGGL(k_gemv_reduce, dim3(cdiv(total, 256)), dim3(256), 0, s,
-                         part.as<int>(), p.ksplit, mb, (int)n, (int)N64, d_sx + m0,
-                         scales.as<float>(), d_y + m0 * ldy, (int)ldy, chunked ? 1 : 0);
+      hipLaunchKernelGGL(k_gemv_reduce, dim3(cdiv(total, 256)), dim3(256), 0, s, d_part,
+                         p.ksplit, mb, (int)n, (int)N64, d_sx + m0, scales.as<float>(),
+                         d_y + m0 * ldy, (int)ldy, chunked ? 1 : 0);
       SYN_LAUNCH_CHECK();
     }
   }
@@ -301,6 +314,46 @@ syn_status_t QLinearInt8::from_f32(const float *w_nk, size_t n_, size_t k_) {
   host_minmax_scales(w_nk, n_, k_, sc.data());
   host_quantize_weights_nk(w_nk, sc.data(), n_, k_, q.data());
   return upload_nk(q.data(), sc.data(), n_, k_);
+}
+
+// ------------------------------------------------- allocation-free forward
+// Device scratch of syn_hip_qlinear_forward_noalloc, for callers that cannot
+// allocate (HIP graph capture, serving loops): quantized activation rows,
+// their scales and the split-K partials of one call.  Each GPU the library
+// runs on holds its own copy until the process ends; every call on a GPU
+// shares it, so calls that overlap on one GPU race.
+constexpr size_t kNoAllocScratchBytes = 4u << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+// zero bytes [k, ldq) of each of m rows
+__global__ void k_zero_row_pad(int8_t *q, size_t m, size_t k, size_t ldq) {
+  for (size_t r = blockIdx.x; r < m; r += gridDim.x)
+    for (size_t j = k + threadIdx.x; j < ldq; j += blockDim.x) q[r * ldq + j] = 0;
+}
+
+// the device address of `scratch` on the current device, resolved on the
+// first call per device (host code never passes the array's name itself)
+static syn_status_t noalloc_scratch(unsigned char **out) {
+  static std::mutex mu;
+  static unsigned char *addr[64] = {};
+  int dev = 0;
+  SYN_HIP(hipGetDevice(&dev));
+  if (dev < 0 || dev >= 64) {
+    set_error("qlinear_forward_noalloc: device index out of range");
+    return SYN_ERR_INVALID_ARG;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void *p = nullptr;
+    SYN_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    if (!p) {
+      set_error("qlinear_forward_noalloc: scratch address unavailable");
+      return SYN_ERR_HIP;
+    }
+    addr[dev] = static_cast<unsigned char *>(p);
+  }
+  *out = addr[dev];
+  return SYN_OK;
 }
 
 }  // namespace syn
@@ -421,6 +474,42 @@ syn_status_t syn_hip_qlinear_forward(syn_hip_qlinear_t *h, size_t m, const float
   }
   SYN_TRY(launch_quantize_rows(d_x, m, L.k, L.k, L.xq.as<int8_t>(), ldq, L.sx.as<float>(), s));
   return L.gemv(m, L.xq.as<int8_t>(), ldq, L.sx.as<float>(), d_y, L.n, s);
+}
+
+syn_status_t syn_hip_qlinear_forward_noalloc(syn_hip_qlinear_t *h, size_t m, const float *d_x,
+                                             float *d_y, void *stream) {
+  if (!h) return SYN_ERR_NULL_PTR;
+  if (h->fmt != SYN_HIP_FMT_INT8) {
+    set_error("qlinear_forward_noalloc: INT8 handles only (the other formats use no scratch)");
+    return SYN_ERR_INVALID_ARG;
+  }
+  if (m == 0) return SYN_OK;
+  if (!d_x || !d_y) return SYN_ERR_NULL_PTR;
+  QLinearInt8 &L = h->i8;
+  const size_t ldq = (size_t)L.chunks * 16;
+  // scratch: quantized rows [m, ldq] | row scales [m] | split-K partials
+  const size_t off_sx = round_up(m * ldq, 256);
+  const size_t off_part = round_up(off_sx + m * sizeof(float), 256);
+  const size_t need = off_part + L.part_elems_for(std::min<size_t>(m, 16)) * sizeof(int);
+  if (need > kNoAllocScratchBytes) {
+    set_error("qlinear_forward_noalloc: " + std::to_string(m) + " rows of this linear need " +
+              std::to_string(need) + " bytes of scratch, more than the fixed " +
+              std::to_string(kNoAllocScratchBytes));
+    return SYN_ERR_INVALID_ARG;
+  }
+  unsigned char *base = nullptr;
+  SYN_TRY(noalloc_scratch(&base));
+  hipStream_t s = pick_stream(stream);
+  int8_t *xq = reinterpret_cast<int8_t *>(base);
+  float *sx = reinterpret_cast<float *>(base + off_sx);
+  int *part = reinterpret_cast<int *>(base + off_part);
+  if (ldq > L.k) {  // the row padding the kernels read in whole 16-byte chunks starts at zero
+    hipLaunchKernelGGL(k_zero_row_pad, dim3((unsigned)std::min<size_t>(m, 65535)), dim3(64), 0, s,
+                       xq, m, L.k, ldq);
+    SYN_LAUNCH_CHECK();
+  }
+  SYN_TRY(launch_quantize_rows(d_x, m, L.k, L.k, xq, ldq, sx, s));
+  return L.gemv_part(m, xq, ldq, sx, d_y, L.n, part, s);
 }
 
 syn_status_t syn_hip_qlinear_info(const syn_hip_qlinear_t *h, size_t *n, size_t *k, int *fmt,

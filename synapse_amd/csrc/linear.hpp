@@ -48,6 +48,11 @@ struct QLinearInt8 {
   // y[m, n] (row stride ldy) from pre-quantized rows xq (row stride ldx).
   syn_status_t gemv(size_t m, const int8_t *d_xq, size_t ldx, const float *d_sx, float *d_y,
                     size_t ldy, hipStream_t s);
+  // the same with the split-K partials in d_part (part_elems_for(min(m, 16))
+  // int32; unused when that is 0)
+  syn_status_t gemv_part(size_t m, const int8_t *d_xq, size_t ldx, const float *d_sx,
+                         float *d_y, size_t ldy, int *d_part, hipStream_t s);
+  size_t part_elems_for(size_t m) const;
   syn_status_t ensure_part(size_t elems);
   // allocate split-K scratch for up to max_m activation rows (needed before
   // a graph capture: nothing may allocate while a step is being recorded)

@@ -79,6 +79,7 @@ SIGNATURES = {
     "syn_hip_qlinear_create": (ST, [C.c_int, SZ, SZ, P, P, C.c_int, C.POINTER(P)]),
     "syn_hip_qlinear_from_f32": (ST, [C.c_int, SZ, SZ, P, C.POINTER(P)]),
     "syn_hip_qlinear_forward": (ST, [P, SZ, P, P, P]),
+    "syn_hip_qlinear_forward_noalloc": (ST, [P, SZ, P, P, P]),
     "syn_hip_qlinear_forward_pre_quantized": (ST, [P, SZ, P, SZ, P, P, P]),
     "syn_hip_qlinear_info": (ST, [P, C.POINTER(SZ), C.POINTER(SZ), C.POINTER(C.c_int),
                                   C.POINTER(SZ)]),
@@ -404,6 +405,11 @@ class QLinear:
 
     def forward_dev(self, m: int, d_x: int, d_y: int, stream=None):
         check(lib().syn_hip_qlinear_forward(self.h, m, d_x, d_y, stream), "qlinear_forward")
+
+    def forward_noalloc_dev(self, m: int, d_x: int, d_y: int, stream=None):
+        """INT8: forward with the library's fixed device scratch (no allocation)."""
+        check(lib().syn_hip_qlinear_forward_noalloc(self.h, m, d_x, d_y, stream),
+              "qlinear_forward_noalloc")
 
     def forward_pre_quantized_dev(self, m, d_xq, ldxq, d_sx, d_y, stream=None):
         check(lib().syn_hip_qlinear_forward_pre_quantized(self.h, m, d_xq, ldxq, d_sx, d_y,
