@@ -135,11 +135,13 @@ def _declare(L):
         "orc_mamba_create": (P, [C.POINTER(MambaCfg)]),
         "orc_mamba_destroy": (None, [P]),
         "orc_mamba_init_synthetic": (C.c_int, [P, C.c_uint64]),
+        "orc_mamba_init_synthetic_std": (C.c_int, [P, C.c_uint64, C.c_float]),
         "orc_mamba_reset": (None, [P]),
         "orc_mamba_prefill": (C.c_int, [P, P, SZ, P]),
         "orc_mamba_decode_one": (C.c_int, [P, C.c_uint32, P]),
         "orc_mamba_generate": (C.c_int, [P, P, SZ, SZ, P, P]),
         "orc_softplus": (C.c_float, [C.c_float]),
+        "orc_conv1d_step": (None, [P, P, P, P, SZ, SZ, P]),
         "orc_rmsnorm_seq": (None, [P, P, C.c_float, SZ, P]),
         "orc_selective_scan_step": (None, [P, P, P, P, P, P, P, P, SZ, SZ]),
     }
@@ -386,6 +388,27 @@ def attention_decode(q, kcache, vcache, seq_len, n_heads, n_kv, head_dim):
 
 
 # ---------------------------------------------------------------- A15 model
+def conv1d_step(x: np.ndarray, w: np.ndarray, bias: np.ndarray, state: np.ndarray) -> np.ndarray:
+    """QuantizedMambaBlock::conv1d_step (int8_mamba.rs:43-56); state
+    [d_inner, d_conv] is updated in place."""
+    d_inner, d_conv = state.shape
+    assert state.dtype == np.float32 and state.flags.c_contiguous
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    bias = np.ascontiguousarray(bias, np.float32)
+    out = np.empty(d_inner, np.float32)
+    lib().orc_conv1d_step(_p(x), _p(w), _p(bias), _p(state), d_inner, d_conv, _p(out))
+    return out
+
+
+def swiglu_fused(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    gate = np.ascontiguousarray(gate, np.float32)
+    up = np.ascontiguousarray(up, np.float32)
+    out = np.empty_like(gate)
+    lib().orc_swiglu_fused(_p(out), _p(gate), _p(up), gate.size)
+    return out
+
+
 class QuantizedCausalLM:
     """INT8 W8A8 decoder (quantization/lm/int8.rs) restated in C."""
 
@@ -596,8 +619,9 @@ class QuantizedMamba:
         self._c = c
         self.h = lib().orc_mamba_create(C.byref(c))
 
-    def init_synthetic(self, seed_base: int = 0x5EED0000):
-        if lib().orc_mamba_init_synthetic(self.h, seed_base):
+    def init_synthetic(self, seed_base: int = 0x5EED0000, std: float = 0.02):
+        """std: the projections' and conv taps' (the embedding keeps 0.02)"""
+        if lib().orc_mamba_init_synthetic_std(self.h, seed_base, std):
             raise RuntimeError("orc_mamba_init_synthetic failed")
 
     def prefill(self, ids):

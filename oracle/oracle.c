@@ -18,6 +18,10 @@
  *   - GGUF KATs from weight_loading/gguf.rs:700-721, 789-820
  *   - f16 conversions checked exhaustively against IEEE (numpy float16)
  *   - integer GEMM checked against brute force in int64
+ *   - the three decoders (INT8 Qwen3-style, f32 CausalLM over Q8_0, INT8
+ *     Mamba) against independent float64 numpy forwards, with planted wiring
+ *     mistakes shown to fail; conv1d_step by its impulse response; the fused
+ *     SwiGLU against numpy
  * Parity unpinned (no reference test, no runnable reference here):
  *   - Q4_K / Q6_K dequant beyond the restated source text (self-made KATs only)
  *   - exact order of Zig's @reduce(.Add) (taken as sequential, LLVM's ordered
@@ -1434,6 +1438,12 @@ void orc_mamba_destroy(orc_mamba *m) {
  * 1+16l+{0 in_proj, 1 conv1d, 2 x_proj, 3 dt_proj, 4 out_proj} ~ N(0, 0.02);
  * conv bias 0, dt bias log(expm1(0.01)), a_log[i][s] = log(s+1), D = 1, norms 1. */
 int orc_mamba_init_synthetic(orc_mamba *m, uint64_t seed_base) {
+  return orc_mamba_init_synthetic_std(m, seed_base, 0.02f);
+}
+
+/* the same seed spec with `std` for the projections and the conv taps (the
+   embedding keeps 0.02) */
+int orc_mamba_init_synthetic_std(orc_mamba *m, uint64_t seed_base, float std) {
   const orc_mamba_cfg *c = &m->c;
   size_t dm = c->d_model, di = c->d_inner, ds = c->d_state, dc = c->d_conv, dr = c->dt_rank;
   m->embed = (float *)malloc(c->vocab * dm * 4);
@@ -1449,18 +1459,18 @@ int orc_mamba_init_synthetic(orc_mamba *m, uint64_t seed_base) {
     orc_mblock *b = &m->blk[l];
     uint64_t sb = seed_base + 1 + 16 * l;
     float *w = (float *)malloc(2 * di * dm * 4);
-    orc_fill_normal(w, 2 * di * dm, sb + 0, 0.02f);
+    orc_fill_normal(w, 2 * di * dm, sb + 0, std);
     bad |= qlin_from_f32(&b->in_proj, w, 2 * di, dm);
-    orc_fill_normal(w, dm * di, sb + 4, 0.02f);
+    orc_fill_normal(w, dm * di, sb + 4, std);
     bad |= qlin_from_f32(&b->out_proj, w, dm, di);
     free(w);
     b->conv_w = (float *)malloc(di * dc * 4);
-    orc_fill_normal(b->conv_w, di * dc, sb + 1, 0.02f);
+    orc_fill_normal(b->conv_w, di * dc, sb + 1, std);
     b->conv_b = (float *)calloc(di, 4);
     b->x_proj = (float *)malloc((dr + 2 * ds) * di * 4);
-    orc_fill_normal(b->x_proj, (dr + 2 * ds) * di, sb + 2, 0.02f);
+    orc_fill_normal(b->x_proj, (dr + 2 * ds) * di, sb + 2, std);
     b->dt_proj = (float *)malloc(di * dr * 4);
-    orc_fill_normal(b->dt_proj, di * dr, sb + 3, 0.02f);
+    orc_fill_normal(b->dt_proj, di * dr, sb + 3, std);
     b->dt_bias = (float *)malloc(di * 4);
     b->a_log = (float *)malloc(di * ds * 4);
     b->d_param = (float *)malloc(di * 4);
@@ -1484,6 +1494,25 @@ void orc_mamba_reset(orc_mamba *m) {
   }
 }
 
+/* QuantizedMambaBlock::conv1d_step (int8_mamba.rs:43-56): per channel the
+   d_conv-long window shifts left by one, the new sample enters at the end,
+   and out = sum_k window[k] * w[k] (in k order) + bias */
+void orc_conv1d_step(const float *x, const float *w, const float *bias, float *state,
+                     size_t d_inner, size_t d_conv, float *out) {
+  for (size_t i = 0; i < d_inner; i++) {
+    float *buf = state + i * d_conv;
+    memmove(buf, buf + 1, (d_conv - 1) * 4);
+    buf[d_conv - 1] = x[i];
+    const float *wi = w + i * d_conv;
+    float sum = 0.0f;
+    for (size_t k = 0; k < d_conv; k++) {
+      float t = buf[k] * wi[k];
+      sum = sum + t;
+    }
+    out[i] = sum + bias[i];
+  }
+}
+
 /* QuantizedMambaBlock::forward_one (int8_mamba.rs:78-109) */
 static void mamba_block_one(const orc_mamba *m, orc_mblock *b, const float *hid, float *out) {
   const orc_mamba_cfg *c = &m->c;
@@ -1496,18 +1525,8 @@ static void mamba_block_one(const orc_mamba *m, orc_mblock *b, const float *hid,
   float sx;
   orc_rmsnorm_seq(hid, b->norm_w, c->eps, dm, normed);
   qlin_forward(&b->in_proj, normed, 1, proj, xq, &sx);
-  for (size_t i = 0; i < di; i++) { /* conv1d_step :43-56 */
-    float *buf = b->conv_state + i * dc;
-    memmove(buf, buf + 1, (dc - 1) * 4);
-    buf[dc - 1] = proj[i];
-    const float *w = b->conv_w + i * dc;
-    float sum = 0.0f;
-    for (size_t k = 0; k < dc; k++) {
-      float t = buf[k] * w[k];
-      sum = sum + t;
-    }
-    xc[i] = orc_silu(sum + b->conv_b[i]);
-  }
+  orc_conv1d_step(proj, b->conv_w, b->conv_b, b->conv_state, di, dc, xc);
+  for (size_t i = 0; i < di; i++) xc[i] = orc_silu(xc[i]);
   /* ssm_forward_step :59-75: x_proj and dt_proj are f32 matmul_t */
   memset(xp, 0, (dr + 2 * ds) * 4);
   orc_sgemm(1, dr + 2 * ds, di, xc, di, 0, b->x_proj, di, 1, xp, dr + 2 * ds);

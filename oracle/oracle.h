@@ -161,12 +161,15 @@ orc_mamba *orc_mamba_create(const orc_mamba_cfg *cfg);
 void orc_mamba_destroy(orc_mamba *m);
 /* synthetic weights (seed spec documented in oracle.c) */
 int orc_mamba_init_synthetic(orc_mamba *m, uint64_t seed_base);
+int orc_mamba_init_synthetic_std(orc_mamba *m, uint64_t seed_base, float std);
 void orc_mamba_reset(orc_mamba *m);
 int orc_mamba_prefill(orc_mamba *m, const uint32_t *ids, size_t n, float *logits);
 int orc_mamba_decode_one(orc_mamba *m, uint32_t token, float *logits);
 int orc_mamba_generate(orc_mamba *m, const uint32_t *prompt, size_t n_prompt, size_t max_new,
                        uint32_t *out_tokens, float *margins);
 float orc_softplus(float x);
+void orc_conv1d_step(const float *x, const float *w, const float *bias, float *state,
+                     size_t d_inner, size_t d_conv, float *out);
 void orc_rmsnorm_seq(const float *x, const float *w, float eps, size_t hidden, float *out);
 void orc_selective_scan_step(const float *x, const float *delta, const float *a_log,
                              const float *b, const float *c, const float *d, float *state,
