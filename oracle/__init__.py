@@ -142,6 +142,8 @@ def _declare(L):
         "orc_mamba_generate": (C.c_int, [P, P, SZ, SZ, P, P]),
         "orc_softplus": (C.c_float, [C.c_float]),
         "orc_conv1d_step": (None, [P, P, P, P, SZ, SZ, P]),
+        "orc_set_threads": (None, [C.c_int]),
+        "orc_get_threads": (C.c_int, []),
         "orc_rmsnorm_seq": (None, [P, P, C.c_float, SZ, P]),
         "orc_selective_scan_step": (None, [P, P, P, P, P, P, P, P, SZ, SZ]),
     }
@@ -388,6 +390,12 @@ def attention_decode(q, kcache, vcache, seq_len, n_heads, n_kv, head_dim):
 
 
 # ---------------------------------------------------------------- A15 model
+def set_threads(n: int):
+    """OpenMP threads of the oracle's large f32 products (the values do not
+    depend on it; 1 times the reference's single-threaded kernels)."""
+    lib().orc_set_threads(int(n))
+
+
 def conv1d_step(x: np.ndarray, w: np.ndarray, bias: np.ndarray, state: np.ndarray) -> np.ndarray:
     """QuantizedMambaBlock::conv1d_step (int8_mamba.rs:43-56); state
     [d_inner, d_conv] is updated in place."""

@@ -445,31 +445,35 @@ int orc_dequant_q6_k(const uint8_t *data, size_t numel, float *out) {
  * ==================================================================== */
 static void f32_gemv_row(size_t n, size_t k, const float *a, const float *b, size_t ldb,
                          int trans_b, float *c) {
-  size_t j = 0;
+  /* every output column is its own chain, so the columns are spread over
+   * OpenMP threads for large matrices (the values do not depend on it) */
+  const int par = (double)n * (double)k > 1048576.0;
   if (trans_b) {
     /* 32-wide and 8-wide column blocks: per column a sequential @mulAdd chain */
-    size_t n32 = n - n % 32;
-    size_t n8 = n32 + (n - n32) / 8 * 8;
-    for (; j < n8; j++) {
+    const long n32 = (long)(n - n % 32);
+    const long n8 = n32 + (long)((n - (size_t)n32) / 8 * 8);
+#pragma omp parallel for schedule(static) if (par)
+    for (long j = 0; j < n8; j++) {
       float acc = 0.0f;
-      const float *br = b + j * ldb;
+      const float *br = b + (size_t)j * ldb;
       for (size_t p = 0; p < k; p++) acc = fmaf(a[p], br[p], acc);
       c[j] = acc;
     }
-    for (; j < n; j++) { /* scalar tail: unfused */
+    for (size_t j = (size_t)n8; j < n; j++) { /* scalar tail: unfused */
       float sum = 0.0f;
       const float *br = b + j * ldb;
       for (size_t p = 0; p < k; p++) sum += a[p] * br[p];
       c[j] = sum;
     }
   } else {
-    size_t n32 = n - n % 32;
-    for (; j < n32; j++) {
+    const long n32 = (long)(n - n % 32);
+#pragma omp parallel for schedule(static) if (par)
+    for (long j = 0; j < n32; j++) {
       float acc = 0.0f;
-      for (size_t p = 0; p < k; p++) acc = fmaf(a[p], b[p * ldb + j], acc);
+      for (size_t p = 0; p < k; p++) acc = fmaf(a[p], b[p * ldb + (size_t)j], acc);
       c[j] = acc;
     }
-    for (; j < n; j++) {
+    for (size_t j = (size_t)n32; j < n; j++) {
       float sum = 0.0f;
       for (size_t p = 0; p < k; p++) sum += a[p] * b[p * ldb + j];
       c[j] = sum;
@@ -489,7 +493,10 @@ int orc_sgemm(size_t m, size_t n, size_t k, const float *a, size_t lda, int tran
    * p = 0..k-1 starting from C's value — fused (@mulAdd) inside full 8x8
    * micro-tiles, unfused in edge tiles (rows of a partial MR panel within an
    * MC=256 block, or columns of a partial NR panel within an NC=4096 block). */
-  for (size_t i = 0; i < m; i++) {
+  const int par = (double)m * (double)n * (double)k > 4194304.0;
+#pragma omp parallel for schedule(dynamic) if (par)
+  for (long ii = 0; ii < (long)m; ii++) {
+    const size_t i = (size_t)ii;
     size_t ic = i / 256 * 256, mc = (m - ic < 256) ? m - ic : 256;
     size_t ir = (i - ic) / 8 * 8;
     int row_full = (mc - ir) >= 8;
@@ -516,6 +523,12 @@ int orc_sgemm(size_t m, size_t n, size_t k, const float *a, size_t lda, int tran
   }
   return ORC_OK;
 }
+
+/* OpenMP threads for the large f32 products (the values do not depend on
+ * it); 1 reproduces the reference's single-threaded timing */
+#include <omp.h>
+void orc_set_threads(int n) { omp_set_num_threads(n > 0 ? n : 1); }
+int orc_get_threads(void) { return omp_get_max_threads(); }
 
 /* ======================================================================
  * A14 — per-layer ops

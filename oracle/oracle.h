@@ -175,6 +175,10 @@ void orc_selective_scan_step(const float *x, const float *delta, const float *a_
                              const float *b, const float *c, const float *d, float *state,
                              float *y, size_t d_inner, size_t d_state);
 
+/* OpenMP threads of the large f32 products (results do not depend on it) */
+void orc_set_threads(int n);
+int orc_get_threads(void);
+
 /* ---- sampling (generation/sampler.rs) ---- */
 void orc_repetition_penalty(float *logits, size_t n, const uint32_t *hist, size_t nh,
                             float penalty);

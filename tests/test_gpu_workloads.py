@@ -1,0 +1,139 @@
+"""BASELINE configurations 3 and 4 at their own workloads on the device, and
+the head_dim-128 prefill attention bit for bit.
+
+- Config 4 (Mistral-7B Q8_0 prefill GEMMs): all four matrices at M = 512 and
+  M = 2048; sampled output rows against the float64 product of the
+  dequantized weights (gguf.rs:255-288 values, matmul_t semantics).
+- Config 3 (LLaMA-3.2-3B widths, Q4_K attention and gate/up, Q6_K down and
+  lm_head): four layers at full width with the 256-token prompt and 128
+  decode steps against the oracle's f32 CausalLM (cosine >= 0.9999 at every
+  step: the prefill runs the f16 MFMA GEMM and k_attn_prefill_rows<128> on
+  256 rows, the decode attention runs at positions 256-383); and the full
+  28-layer model through properties (finite logits; the prefill of n tokens
+  matches the prefill of n - 1 followed by forward_one).
+- INT8 decoder with head_dim 128 and GQA: prefills of 65, 150 and 256 tokens
+  into an empty cache, then an appended prefill after the cached rows and a
+  decode step, bit-identical to the oracle."""
+import numpy as np
+import pytest
+
+import oracle as O
+from synapse_amd import hip
+from tests.test_gpu_klm import LLAMA_FMTS, build_pair
+
+pytestmark = pytest.mark.gpu
+
+SEED = 0x5EED0000
+TOL = 1e-3  # max |y - r| / max |r| per output row (the north star's float bar)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def gpu():
+    hip.init(0)
+    O.set_threads(16)
+
+
+def _bits(x):
+    return np.asarray(x, np.float32).view(np.uint32)
+
+
+def _cos(a, b):
+    a, b = a.astype(np.float64), b.astype(np.float64)
+    return float(a @ b / (np.linalg.norm(a) * np.linalg.norm(b)))
+
+
+def _rel(a, b):
+    return float(np.abs(a - b).max() / np.abs(b).max())
+
+
+# ---------------------------------------------------------------- config 4
+MISTRAL = [("q", 4096, 4096), ("kv", 4096, 1024), ("gate_up", 4096, 14336),
+           ("down", 14336, 4096)]
+
+
+@pytest.mark.parametrize("label,k,n", MISTRAL, ids=[m[0] for m in MISTRAL])
+def test_config4_q8_0_prefill_gemm(label, k, n):
+    print("case", label, k, n, flush=True)
+    rng = np.random.default_rng(k + n)
+    w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+    blocks = hip.kquant_encode(hip.FMT_Q8_0, w)
+    del w
+    lin = hip.QLinear.gguf(hip.FMT_Q8_0, blocks, n, k)
+    deq = O.dequant("q8_0", blocks, n * k).reshape(n, k).astype(np.float64)
+    for m in (512, 2048):
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        got = lin.forward(x)
+        rows = (0, 1, 255, m // 2 + 3, m - 2, m - 1)
+        want = x[list(rows)].astype(np.float64) @ deq.T
+        worst = max(_rel(got[r], want[i]) for i, r in enumerate(rows))
+        print(f"  M={m}: worst sampled-row rel err {worst:.2e}", flush=True)
+        assert worst <= TOL, (m, worst)
+
+
+# ---------------------------------------------------------------- config 3
+LLAMA3B = dict(hidden=3072, n_layers=28, n_heads=24, n_kv_heads=8, head_dim=128, inter=8192,
+               vocab=128256, eps=1e-5, rope_theta=5e5)
+
+
+def test_config3_llama3b_four_layers_prompt256_decode128():
+    cfg = dict(LLAMA3B, n_layers=4, max_seq=256 + 128 + 1)
+    o, g = build_pair(cfg, LLAMA_FMTS)
+    ids = O.token_ids(256, SEED + 0xFFFF, cfg["vocab"])
+    lo, lg = o.prefill(ids), g.prefill(ids)
+    print("prefill cos", _cos(lo, lg), "rel", _rel(lg, lo), flush=True)
+    assert _cos(lo, lg) >= 0.9999
+    tok = O.argmax(lo)
+    worst = 1.0
+    for step in range(128):
+        lo, lg = o.forward_one(tok), g.forward_one(tok)
+        c = _cos(lo, lg)
+        worst = min(worst, c)
+        assert c >= 0.9999, (step, c)
+        tok = O.argmax(lo)
+    print("decode positions 256-383: worst cos", worst, flush=True)
+    o.close()
+    g.close()
+
+
+def test_config3_full_28_layers_properties():
+    cfg = dict(LLAMA3B, max_seq=64)
+    g = hip.KQuantCausalLM(cfg)
+    g.init_synthetic(SEED, 0.02)
+    ids = O.token_ids(24, SEED + 0xFFFF, cfg["vocab"])
+    full = g.prefill(ids)
+    assert np.isfinite(full).all()
+    g.prefill(ids[:-1])
+    step = g.forward_one(int(ids[-1]))
+    assert np.isfinite(step).all()
+    print("prefill(n) vs prefill(n-1) + forward_one: cos", _cos(full, step), "rel",
+          _rel(step, full), flush=True)
+    assert _cos(full, step) >= 0.9999
+    toks, _ = g.generate(ids, 8)
+    assert ((0 <= toks) & (toks < cfg["vocab"])).all()
+    g.close()
+
+
+# ---------------------------------------------------------------- INT8 hd 128
+HD128 = dict(hidden=256, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=128, inter=512,
+             vocab=512, max_seq=300)
+
+
+@pytest.fixture(scope="module")
+def hd128():
+    o = O.QuantizedCausalLM(HD128)
+    o.init_synthetic(SEED, 0.15)
+    g = hip.QuantizedCausalLM(HD128)
+    g.init_synthetic(SEED, 0.15)
+    yield o, g
+    o.close()
+    g.close()
+
+
+@pytest.mark.parametrize("t", [65, 150, 256])
+def test_int8_prefill_attention_hd128_bit_exact(hd128, t):
+    o, g = hd128
+    ids = O.token_ids(t, SEED + 0xFFFF + t, HD128["vocab"])
+    np.testing.assert_array_equal(_bits(g.prefill(ids)), _bits(o.prefill(ids)))
+    extra = O.token_ids(20, SEED + 0xFFFF + 1000 + t, HD128["vocab"])
+    np.testing.assert_array_equal(_bits(g.prefill_append(extra)), _bits(o.prefill_append(extra)))
+    np.testing.assert_array_equal(_bits(g.forward_one(7)), _bits(o.forward_one(7)))
