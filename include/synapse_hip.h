@@ -69,6 +69,29 @@ syn_status_t syn_qgemm_int8(size_t m, size_t n, size_t k, const int8_t *a, size_
 syn_status_t syn_q4_0_gemv(size_t n, size_t k, const float *a, const uint8_t *b_q4,
                            float *c);
 
+/* Replaces syn_sgemm (synapse.h:176-184, exports.zig:725-761): C = op(A) op(B),
+ * row-major, trans != 0 uses the transpose; M <= 16 with A as is overwrites C
+ * (one f32GemvRow per row), otherwise C accumulates (zero it first), with the
+ * reference's per-element chain order (matmul.zig:125-184).  Zero dims ->
+ * SYN_OK no-op; null pointers -> SYN_ERR_NULL_PTR. */
+syn_status_t syn_sgemm(size_t m, size_t n, size_t k, const float *a, size_t lda, int trans_a,
+                       const float *b, size_t ldb, int trans_b, float *c, size_t ldc);
+
+/* The four entry points above under names the reference's static Zig archive
+ * (libsynapse_zig.a, which defines the unprefixed ones) does not define, so a
+ * binary can link both and reach these. */
+syn_status_t syn_hip_quantize_per_channel_int8(const float *data, size_t channels,
+                                               size_t channel_size, int8_t *out,
+                                               float *scales);
+syn_status_t syn_hip_qgemm_int8(size_t m, size_t n, size_t k, const int8_t *a, size_t lda,
+                                const int8_t *b, size_t ldb, float *c, size_t ldc,
+                                const float *scales_a, const float *scales_b);
+syn_status_t syn_hip_q4_0_gemv(size_t n, size_t k, const float *a, const uint8_t *b_q4,
+                               float *c);
+syn_status_t syn_hip_sgemm(size_t m, size_t n, size_t k, const float *a, size_t lda,
+                           int trans_a, const float *b, size_t ldb, int trans_b, float *c,
+                           size_t ldc);
+
 /* =====================================================================
  * 2. Device-resident API
  * =================================================================== */
@@ -119,12 +142,20 @@ syn_status_t syn_hip_quantize_rows(const float *d_x, size_t m, size_t k, size_t 
 /* host weight layouts accepted by syn_hip_qlinear_create for INT8 */
 #define SYN_HIP_LAYOUT_KN 0 /* reference QuantizedLinear::weights_int8 [K,N] */
 #define SYN_HIP_LAYOUT_NK 1 /* row per output feature [N,K] */
+/* Q4_0 block scales read as the reference's dequantize_q4_0 reads them
+ * (weight_loading/gguf.rs:294-326 with converter.rs:12-40: subnormal f16
+ * deltas come out halved), the f32 map load_gguf_with_raw_q4 builds for the
+ * reference's f32 prefill (gguf.rs:59-64).  Any other layout value for Q4_0
+ * reads them as the Zig Q4 GEMV does (IEEE f16ToF32, qmatmul.zig:346-371),
+ * the path of the raw-block map (RawQ4Tensor) and of Q4Linear. */
+#define SYN_HIP_LAYOUT_GGUF_DEQUANT 2
 
 typedef struct syn_hip_qlinear_s syn_hip_qlinear_t;
 
 /* Repack already-quantized host weights once into HBM.
  *   INT8: host_weights int8 in `layout`, host_scales f32[n].
- *   Q4_0: host_weights = pack_for_zig bytes [n, k/32, 18]; host_scales unused.
+ *   Q4_0: host_weights = pack_for_zig bytes [n, k/32, 18] (= GGUF Q4_0 blocks);
+ *         host_scales unused; layout SYN_HIP_LAYOUT_GGUF_DEQUANT or 0.
  *   Q8_0/Q4_K/Q6_K: GGUF block bytes of the row-major [n,k] tensor
  *   (k a multiple of 32 / 256); host_scales unused. */
 syn_status_t syn_hip_qlinear_create(int fmt, size_t n, size_t k, const void *host_weights,

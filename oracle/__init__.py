@@ -254,6 +254,21 @@ def dequant(fmt: str, data: np.ndarray, numel: int) -> np.ndarray:
 
 
 # ---------------------------------------------------------------- f32 GEMM
+def sgemm(a: np.ndarray, b: np.ndarray, trans_a: bool = False, trans_b: bool = False,
+          c: np.ndarray = None) -> np.ndarray:
+    """syn_sgemm / sgemmTiled (exports.zig:725-761, matmul.zig:125-184)."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    m, k = (a.shape[1], a.shape[0]) if trans_a else a.shape
+    n = b.shape[0] if trans_b else b.shape[1]
+    out = np.zeros((m, n), np.float32) if c is None else np.array(c, np.float32, copy=True)
+    rc = lib().orc_sgemm(m, n, k, _p(a), a.shape[1], int(trans_a), _p(b), b.shape[1],
+                         int(trans_b), _p(out), n)
+    if rc:
+        raise ValueError(f"orc_sgemm status {rc}")
+    return out
+
+
 def matmul_t(a: np.ndarray, w_nk: np.ndarray) -> np.ndarray:
     """ops/matmul.rs:55-79: a [M,K] x W[N,K]^T via syn_sgemm(trans_b=1)."""
     a = np.ascontiguousarray(a, np.float32)

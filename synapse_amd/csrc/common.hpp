@@ -104,7 +104,10 @@ static __constant__ uint64_t syn_exp2_tab[32] = {
 
 // glibc 2.35 expf (the published exp2f_data / e_expf.c algorithm, 32-entry
 // table, degree-3 polynomial in double) including the FMA contractions of the
-// x86-64 FMA ifunc build.  Checked on the CPU against the host's expf over all
+// x86-64 FMA ifunc build.  Upstream: glibc sysdeps/ieee754/flt-32/e_expf.c
+// and e_exp2f_data.c (LGPL-2.1-or-later), contributed from ARM's
+// optimized-routines (math/expf.c, exp2f_data.c; MIT OR Apache-2.0 WITH
+// LLVM-exception).  The table values here were recomputed from 2^(i/32).  Checked on the CPU against the host's expf over all
 // 2^32 inputs; keeps SiLU and softmax bit-identical to the reference's
 // f32::exp on Linux.
 // tab: the 32-entry table above, or a copy of it (in LDS, so that a lookup

@@ -403,6 +403,7 @@ syn_status_t syn_hip_qlinear_create(int fmt, size_t n, size_t k, const void *hos
       st = SYN_ERR_INVALID_ARG;
   } else if (fmt == SYN_HIP_FMT_Q4_0) {
     st = (k % 32) ? SYN_ERR_SHAPE_MISMATCH : h->q4.upload_packed((const uint8_t *)host_weights, n, k);
+    h->q4.rs_f16_scales = layout == SYN_HIP_LAYOUT_GGUF_DEQUANT;
   } else if (is_kq(fmt)) {
     st = (k % kq_block_elems(fmt)) ? SYN_ERR_SHAPE_MISMATCH
                                    : h->kq.upload(fmt, (const uint8_t *)host_weights, n, k);

@@ -83,6 +83,9 @@ struct QLinearQ4_0 {
   size_t part_elems = 0;
   DevBuf asum;         // per-call block sums of the activation rows
   size_t asum_rows = 0;
+  // block scales read with the Rust f16 converter (subnormals halved): the
+  // reference's GGUF Q4_0 path; false = the Zig GEMV's IEEE conversion
+  bool rs_f16_scales = false;
   syn_status_t upload_packed(const uint8_t *packed, size_t n_, size_t k_);
   syn_status_t from_f32(const float *w_nk, size_t n_, size_t k_);
   size_t weight_bytes() const { return n * (k / 32) * 18; }

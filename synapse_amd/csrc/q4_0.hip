@@ -40,6 +40,15 @@ __device__ __forceinline__ float f16_bits_to_f32(uint32_t h) {
   return (float)__builtin_bit_cast(_Float16, (uint16_t)h);
 }
 
+// A block scale as the handle's loader defines it: the Zig GEMV's IEEE
+// f16ToF32 (qmatmul.zig:346-371, sub = 1), or the Rust converter of the
+// GGUF path (converter.rs:12-40 via gguf.rs:294-326), which returns half
+// the IEEE value for subnormal inputs (sub = 0.5; exact in f32).
+__device__ __forceinline__ float q4_scale(uint32_t h, float sub) {
+  const float d = f16_bits_to_f32(h);
+  return (h & 0x7c00u) == 0 ? d * sub : d;
+}
+
 // grid (panels, ksplit); lane = output row, blocks [b0, b1) of this slice.
 // Load order: the activation blocks whose sums this thread forms (first
 // round, the waves that have any), then the first round of weight blocks,
@@ -50,7 +59,7 @@ template <int M, int U>
 __global__ void __launch_bounds__(1024)
     k_gemv_q4_0(const u32x4 *__restrict__ nib, const uint16_t *__restrict__ sc,
                 const float *__restrict__ x, int ldx, float *__restrict__ y, int ldy,
-                float *__restrict__ part, int N, int B, int bs) {
+                float *__restrict__ part, int N, int B, int bs, float sub) {
   extern __shared__ __align__(16) float smem[];
   const int NT = blockDim.x;
   const int panel = blockIdx.x, ks = blockIdx.y;
@@ -114,7 +123,7 @@ __global__ void __launch_bounds__(1024)
     for (int u = 0; u < U; u++) {
       const int b = bb + u * nw;
       if (b < b1) {
-        const float d = f16_bits_to_f32(dh[u]);
+        const float d = q4_scale(dh[u], sub);
 #pragma unroll
         for (int m = 0; m < M; m++) {
           const float *xa = x + (size_t)m * ldx + (size_t)b * 32;
@@ -164,7 +173,7 @@ template <int U>
 __global__ void __launch_bounds__(512)
     k_gemv_q4_0h(const u32x4 *__restrict__ nib, const uint16_t *__restrict__ sc,
                  const float *__restrict__ x, float *__restrict__ y, float *__restrict__ part,
-                 int N, int B, int bs) {
+                 int N, int B, int bs, float sub) {
   extern __shared__ __align__(16) float hsm[];
   constexpr int NT = 512, NW = NT / 64;
   const int panel = blockIdx.x, ks = blockIdx.y;
@@ -242,7 +251,7 @@ __global__ void __launch_bounds__(512)
         }
         const float dot = __builtin_fmaf(s1, 0.0625f, s0) * 16777216.0f;
         const float blk = dot - 8.0f * asum[b - b0];
-        acc = __builtin_fmaf(blk, f16_bits_to_f32(dh[u]), acc);
+        acc = __builtin_fmaf(blk, q4_scale(dh[u], sub), acc);
       }
     }
     if (bb + NW * U < b1) issue(bb + NW * U);
@@ -277,20 +286,21 @@ __global__ void __launch_bounds__(256)
 // blocks (four workgroups per CU stream the matrix), else 4 with up to 16
 template <int M>
 static void launch_q4_m(const GemvPlan &p, const u32x4 *nib, const uint16_t *sc, const float *x,
-                        int ldx, float *y, int ldy, float *part, int N, hipStream_t s) {
+                        int ldx, float *y, int ldy, float *part, int N, float sub,
+                        hipStream_t s) {
   const bool wide = p.cs >= 64;
   const int waves = wide ? 8 : std::min(p.waves, M >= 8 ? 8 : 16);
   const size_t shm = ((size_t)M * p.cs + (size_t)waves * M * 64) * sizeof(float);
   if (wide)
     hipLaunchKernelGGL((k_gemv_q4_0<M, 8>), dim3(p.panels, p.ksplit), dim3(64 * waves), shm, s,
-                       nib, sc, x, ldx, y, ldy, part, N, p.chunks, p.cs);
+                       nib, sc, x, ldx, y, ldy, part, N, p.chunks, p.cs, sub);
   else
     hipLaunchKernelGGL((k_gemv_q4_0<M, 4>), dim3(p.panels, p.ksplit), dim3(64 * waves), shm, s,
-                       nib, sc, x, ldx, y, ldy, part, N, p.chunks, p.cs);
+                       nib, sc, x, ldx, y, ldy, part, N, p.chunks, p.cs, sub);
 }
 
 typedef void (*q4_launcher)(const GemvPlan &, const u32x4 *, const uint16_t *, const float *,
-                            int, float *, int, float *, int, hipStream_t);
+                            int, float *, int, float *, int, float, hipStream_t);
 static const q4_launcher kQ4Launch[9] = {nullptr,        launch_q4_m<1>, launch_q4_m<2>,
                                          launch_q4_m<3>, launch_q4_m<4>, launch_q4_m<5>,
                                          launch_q4_m<6>, launch_q4_m<7>, launch_q4_m<8>};
@@ -298,6 +308,7 @@ static const q4_launcher kQ4Launch[9] = {nullptr,        launch_q4_m<1>, launch_
 syn_status_t QLinearQ4_0::gemv(size_t m, const float *d_x, size_t ldx, float *d_y, size_t ldy,
                                hipStream_t s) {
   if (m == 0 || n == 0 || k == 0) return SYN_OK;
+  const float sub = rs_f16_scales ? 0.5f : 1.0f;
   // "chunks" here are 32-element blocks; a K slice holds whole blocks
   GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
   const size_t N64 = (size_t)p.panels * 64;
@@ -313,10 +324,10 @@ syn_status_t QLinearQ4_0::gemv(size_t m, const float *d_x, size_t ldx, float *d_
       // two blocks per wave and round: measured best at the LLaMA shapes
       hipLaunchKernelGGL(k_gemv_q4_0h<2>, dim3(p.panels, p.ksplit), dim3(512), shm_h, s,
                          nib.as<u32x4>(), sc.as<uint16_t>(), d_x + m0 * ldx, d_y + m0 * ldy,
-                         part.as<float>(), (int)n, p.chunks, p.cs);
+                         part.as<float>(), (int)n, p.chunks, p.cs, sub);
     } else {
       kQ4Launch[mb](p, nib.as<u32x4>(), sc.as<uint16_t>(), d_x + m0 * ldx, (int)ldx,
-                    d_y + m0 * ldy, (int)ldy, part.as<float>(), (int)n, s);
+                    d_y + m0 * ldy, (int)ldy, part.as<float>(), (int)n, sub, s);
     }
     SYN_LAUNCH_CHECK();
     if (p.ksplit > 1) {

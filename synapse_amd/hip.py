@@ -22,7 +22,7 @@ STATUS_NAMES = {0: "OK", 1: "NULL_PTR", 2: "INVALID_ARG", 3: "OUT_OF_MEMORY",
                 102: "LAUNCH"}
 FMT_INT8, FMT_Q4_0, FMT_Q8_0, FMT_Q4_K, FMT_Q6_K, FMT_TERNARY = 1, 2, 3, 4, 5, 6
 KQ_BLOCK = {FMT_Q8_0: (32, 34), FMT_Q4_K: (256, 144), FMT_Q6_K: (256, 210)}
-LAYOUT_KN, LAYOUT_NK = 0, 1
+LAYOUT_KN, LAYOUT_NK, LAYOUT_GGUF_DEQUANT = 0, 1, 2
 
 P, SZ, ST = C.c_void_p, C.c_size_t, C.c_int32
 
@@ -57,6 +57,11 @@ SIGNATURES = {
     "syn_quantize_per_channel_int8": (ST, [P, SZ, SZ, P, P]),
     "syn_qgemm_int8": (ST, [SZ, SZ, SZ, P, SZ, P, SZ, P, SZ, P, P]),
     "syn_q4_0_gemv": (ST, [SZ, SZ, P, P, P]),
+    "syn_sgemm": (ST, [SZ, SZ, SZ, P, SZ, C.c_int, P, SZ, C.c_int, P, SZ]),
+    "syn_hip_quantize_per_channel_int8": (ST, [P, SZ, SZ, P, P]),
+    "syn_hip_qgemm_int8": (ST, [SZ, SZ, SZ, P, SZ, P, SZ, P, SZ, P, P]),
+    "syn_hip_q4_0_gemv": (ST, [SZ, SZ, P, P, P]),
+    "syn_hip_sgemm": (ST, [SZ, SZ, SZ, P, SZ, C.c_int, P, SZ, C.c_int, P, SZ]),
     "syn_hip_init": (ST, [C.c_int]),
     "syn_hip_device_count": (ST, [C.POINTER(C.c_int)]),
     "syn_hip_last_error": (C.c_char_p, []),
@@ -318,6 +323,20 @@ def qgemm_int8(a, b_kn, sa, sb) -> np.ndarray:
     return c
 
 
+def sgemm(a: np.ndarray, b: np.ndarray, trans_a: bool = False, trans_b: bool = False,
+          c: np.ndarray = None) -> np.ndarray:
+    """syn_sgemm (synapse.h:176-184): op(A) op(B), accumulated into c (zeros
+    if None) on the GOTO path, overwritten on the M <= 16 GEMV path."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    m, k = (a.shape[1], a.shape[0]) if trans_a else a.shape
+    n = b.shape[0] if trans_b else b.shape[1]
+    out = np.zeros((m, n), np.float32) if c is None else np.array(c, np.float32, copy=True)
+    check(lib().syn_sgemm(m, n, k, ptr(a), a.shape[1], int(trans_a), ptr(b), b.shape[1],
+                          int(trans_b), ptr(out), n), "syn_sgemm")
+    return out
+
+
 def q4_0_gemv(a: np.ndarray, packed: np.ndarray, n: int) -> np.ndarray:
     a = np.ascontiguousarray(a, np.float32)
     packed = np.ascontiguousarray(packed, np.uint8)
@@ -360,11 +379,14 @@ class QLinear:
         return cls(h.value, FMT_INT8)
 
     @classmethod
-    def q4_0(cls, packed: np.ndarray, n: int, k: int) -> "QLinear":
+    def q4_0(cls, packed: np.ndarray, n: int, k: int, gguf_dequant: bool = False) -> "QLinear":
+        """pack_for_zig / GGUF Q4_0 blocks; gguf_dequant reads the block scales
+        as the reference's dequantize_q4_0 (subnormals halved)."""
         packed = np.ascontiguousarray(packed, np.uint8)
         h = C.c_void_p()
-        check(lib().syn_hip_qlinear_create(FMT_Q4_0, n, k, ptr(packed), None, 0, C.byref(h)),
-              "qlinear_create")
+        check(lib().syn_hip_qlinear_create(FMT_Q4_0, n, k, ptr(packed), None,
+                                           LAYOUT_GGUF_DEQUANT if gguf_dequant else 0,
+                                           C.byref(h)), "qlinear_create")
         return cls(h.value, FMT_Q4_0)
 
     @classmethod

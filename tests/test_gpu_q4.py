@@ -70,3 +70,26 @@ def test_q4_errors():
     assert L.syn_q4_0_gemv(2, 40, hip.ptr(a), hip.ptr(b), hip.ptr(c)) == 4  # k % 32
     assert L.syn_q4_0_gemv(0, 32, hip.ptr(a), hip.ptr(b), hip.ptr(c)) == 0
     assert L.syn_q4_0_gemv(2, 32, None, hip.ptr(b), hip.ptr(c)) == 1
+
+
+def test_gguf_q4_0_subnormal_scale_semantics():
+    """A Q4_0 block whose f16 delta is subnormal: the reference reads it as the
+    Zig Q4 GEMV does (IEEE, qmatmul.zig:346-371) on the raw-block path, and
+    halved on the dequantize_q4_0 path (gguf.rs:294-326, converter.rs:12-40);
+    a handle created with gguf_dequant follows the latter."""
+    n, k = 64, 64
+    blk = np.zeros((n, k // 32, 18), np.uint8)
+    deltas = np.array([0x0201, 0x0100, 0x3C00, 0x0003], np.uint16)  # 1.0 and three subnormals
+    for r in range(n):
+        for b in range(k // 32):
+            blk[r, b, 0:2] = np.array([deltas[(r + b) % 4]], np.uint16).view(np.uint8)
+            blk[r, b, 2:] = ((np.arange(16) * 7 + r + b) % 256).astype(np.uint8)
+    packed = blk.reshape(-1)
+    x = O.normal(k, 12, 1.0)
+    ieee = hip.QLinear.q4_0(packed, n, k).forward(x[None, :])[0]
+    np.testing.assert_allclose(ieee, O.q4_0_gemv(x, packed, n), rtol=1e-5)
+    halved = hip.QLinear.q4_0(packed, n, k, gguf_dequant=True).forward(x[None, :])[0]
+    deq = O.dequant("q4_0", packed, n * k).reshape(n, k).astype(np.float64)
+    np.testing.assert_allclose(halved, deq @ x.astype(np.float64), rtol=1e-5, atol=0)
+    # the two readings differ exactly by the halving of the subnormal blocks
+    assert not np.allclose(ieee, halved)
