@@ -8,15 +8,22 @@ a 16-token random prompt, then greedy decode.  A "step" is one decode token
 (one forward_one + argmax, all on the device, replayed as a HIP graph).
 
 Prints ONE JSON line.  `value` = decode tokens/s.  `roofline` covers the
-dominant decode matvec (the tied lm_head, 151936 x 1024 INT8 GEMV, as the
-decode step launches it) timed per launch with hipEvents on the model
-stream, with the Infinity Cache flushed between launches.  `cpu_baseline` =
-the oracle (C restatement of the reference cpu_simd path, single thread)
-decoding the same model on the host.  `secondary` = the other BASELINE
-configurations measured on the same GPU (synapse_amd/microbench.py): the
-config-1 GEMVs one launch at a time, the config-2 Q4_0 microbench, the
-config-3 K-quant GEMVs and decoder, the config-4 Q8_0 prefill GEMMs, the
-INT8 prefill GEMM, and the config-5 Mamba decoder (--no-secondary skips it).
+dominant kernel of the timed step: eager fused steps right after the timed
+region launch every kernel with start/stop hipEvents (hipExtLaunchKernelGGL,
+the dispatch's own timestamps, on the model stream;
+syn_hip_qlm_time_step_kernels), and the kernel kind with the largest time
+per step is reported against its algorithmic bytes; `roofline.step` is the
+whole graph-replayed step against its weight bytes, `roofline.lm_head` the
+lm_head GEMV, and `step_kernels` every kind.  `cpu_baseline` = the oracle (C
+restatement of the reference cpu_simd path, single thread) decoding the same
+model on the host, with `cpu_baseline.secondary` the same oracle on bounded
+samples of configs 2-5.  `secondary` = the other BASELINE configurations
+measured on the same GPU (synapse_amd/microbench.py): the config-1 GEMVs
+one launch at a time, the config-2 Q4_0 microbench (1000 launches per
+matrix), the config-3 K-quant GEMVs and decoder, the config-4 Q8_0 prefill
+GEMMs, the INT8 prefill GEMM, and the config-5 Mamba decoder
+(--no-secondary skips them).  A secondary that fails is recorded as
+{"error": ...} and the line is still printed.
 """
 from __future__ import annotations
 
@@ -43,6 +50,10 @@ REF_DECODE_TOKS = 27.3  # Qwen3-0.6B INT8 decode, reference cpu_simd (Apple Sili
 # readings in profiles/lm_head_int8_qwen3_k_lmhead_top2.md
 LM_HEAD_FETCH_KIB, LM_HEAD_FETCH_FACTOR = 76301.0, 262144.0 / 131084.7
 LM_HEAD_WRITE_KIB, LM_HEAD_WRITE_FACTOR = 816.5, 262144.0 / 262144.0
+# HBM traffic per launch of the step's kernels, from the same two counter runs
+# (FETCH_SIZE and WRITE_SIZE per dispatch, scaled as above); None until a
+# counter run of that kernel is recorded under profiles/
+STEP_KERNEL_TRAFFIC = {}
 
 
 def step_weight_bytes(c):
@@ -51,6 +62,28 @@ def step_weight_bytes(c):
                          c["n_kv_heads"] * c["head_dim"], c["inter"], c["vocab"], c["n_layers"])
     per_layer = (q * h + 2 * kv * h + h * q + 3 * i * h) + 4 * (q + 2 * kv + h + 2 * i + h)
     return L * per_layer + v * h + 4 * v
+
+
+def step_kernel_bytes(c, pos):
+    """Algorithmic HBM bytes of one launch of each fused-step kernel kind at
+    decode position `pos`: a GEMV moves N*K int8 weights + 4N scales + K
+    int8 activations + 4N outputs (the per-matvec formula of the metric);
+    the attention reads the K and V cache rows of positions 0..pos."""
+    h, q, kv, i, v = (c["hidden"], c["n_heads"] * c["head_dim"],
+                      c["n_kv_heads"] * c["head_dim"], c["inter"], c["vocab"])
+    gemv = lambda n, k: n * k + 8 * n + k
+    return {"qkv": gemv(q + 2 * kv, h), "o": gemv(h, q), "gate_up": gemv(2 * i, h),
+            "down": gemv(h, i), "lm_head": gemv(v, h),
+            "attention": 2 * 4 * kv * (pos + 1)}
+
+
+STEP_KERNEL_NAMES = {
+    "qkv": "k_fused_gemv<0,256,U> (residual + RMSNorm + quantize + QKV GEMV)",
+    "attention": "k_attn_head<false,128> (head norms, RoPE, KV append, attention)",
+    "o": "k_fused_gemv<1,256,U> (quantize + O GEMV)",
+    "gate_up": "k_gu_swiglu<8> (residual + RMSNorm + quantize + gate|up GEMV + SwiGLU)",
+    "down": "k_fused_gemv<5,512,U> (quantize h range + down GEMV)",
+    "lm_head": "k_lmhead_top2<8,8> (lm_head GEMV + per-panel top-2)"}
 
 
 def lm_head_bytes(c):
@@ -129,7 +162,8 @@ def secondary(hip, np):
         "note": "one launch per GEMV (the decode step fuses them), >= 1 GiB rotated",
         "gemvs": mb.int8_suite()}
     out["config2_q4_0_gemv_llama1b"] = {
-        "note": "batch-1 Q4_0 GEMV, f32 activations, >= 1 GiB of weight copies rotated",
+        "note": "batch-1 Q4_0 GEMV, f32 activations, 1000 launches per matrix round-robin "
+                "over >= 1 GiB of weight copies",
         "gemvs": mb.q4_0_suite()}
     out["ternary_gemv_llama1b_shapes"] = {
         "note": "TernaryLinear batch-1 GEMV (not a BASELINE config; the quantized-linear "
@@ -207,6 +241,104 @@ def speculative_record(model, np, k: int = 4, max_new: int = 64, reps: int = 3):
     return res
 
 
+def _median_s(fn, reps):
+    ts = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t)
+    return sorted(ts)[len(ts) // 2]
+
+
+def cpu_baselines_secondary(np):
+    """The oracle single-threaded (the reference's kernels are) on bounded
+    samples of configs 2-5, in the units of the GPU records beside them."""
+    import oracle as O
+    from synapse_amd import microbench as mb
+    O.set_threads(1)
+    out = {"cores": 1, "kind": "port",
+           "note": "oracle/oracle.c, one thread (O.set_threads(1)); the reference's Zig/Rust "
+                   "kernels cannot be built in this image"}
+    t0 = time.perf_counter()
+    # config 2: q4_0GemvRow (qmatmul.zig:276-343) at the five LLaMA-1B shapes
+    # (the time does not depend on the values: random nibbles, scale 0.01)
+    rng = np.random.default_rng(1)
+    rows = []
+    for lab, k, n in mb.Q4_0_SHAPES:
+        packed = rng.integers(0, 256, size=(n * (k // 32), 18), dtype=np.uint8)
+        packed[:, 0:2] = np.array([np.float16(0.01)]).view(np.uint8)
+        packed = packed.reshape(-1)
+        x = rng.standard_normal(k).astype(np.float32)
+        reps = 3 if n * k > 50_000_000 else 7
+        s = _median_s(lambda: O.q4_0_gemv(x, packed, n), reps)
+        nb = n * (k // 32) * 18 + 4 * k + 4 * n
+        rows.append({"matrix": lab, "us": round(s * 1e6, 1), "gb_s": round(nb / s / 1e9, 2)})
+    out["config2_q4_0_gemv"] = {"sample": "median of 3-7 calls per matrix", "gemvs": rows}
+    # config 3: the f32 CausalLM over Q4_K / Q6_K weights (matmul.zig:223-347
+    # per token): one LLaMA-3B-width layer (Q4_K q/k/v/o/gate/up, Q6_K down)
+    # with a small vocabulary, and the 128256 x 3072 f32 lm_head GEMV on its
+    # own; a token = 28 layers + the lm_head
+    cfg = dict(LLAMA3B, n_layers=1, vocab=256, max_seq=32)
+    o = kquant_oracle_model(cfg, np)
+    o.prefill(np.array(_ids(4, cfg["vocab"], PROMPT_SEED), np.uint32))
+    t_layer = _median_s(lambda: o.forward_one(1), 3)
+    o.close()
+    w_lm = np.full((LLAMA3B["vocab"], LLAMA3B["hidden"]), 0.01, np.float32)
+    xh = rng.standard_normal((1, LLAMA3B["hidden"])).astype(np.float32)
+    t_lm = _median_s(lambda: O.matmul_t(xh, w_lm), 2)
+    del w_lm
+    t28 = LLAMA3B["n_layers"] * t_layer + t_lm
+    out["config3_kquant_decode"] = {
+        "tok_s": round(1.0 / t28, 3), "ms_per_token": round(t28 * 1e3, 1),
+        "sample": f"one full-width layer (+ a 256-row head) {t_layer * 1e3:.0f} ms, the "
+                  f"lm_head GEMV {t_lm * 1e3:.0f} ms; a token = 28 x layer + lm_head"}
+    # config 4: sgemmTiled's GOTO path (matmul.zig:157-183) on dequantized Q8_0
+    # weights, the q matrix 4096 -> 4096 at M = 32 (the same code runs M = 512)
+    k = n = 4096
+    w = rng.standard_normal((n, k), dtype=np.float32) * np.float32(0.02)
+    x = rng.standard_normal((32, k), dtype=np.float32)
+    s = _median_s(lambda: O.matmul_t(x, w), 1)
+    out["config4_q8_0_prefill_gemm"] = {
+        "tflops": round(2.0 * 32 * n * k / s / 1e12, 5), "ms": round(s * 1e3, 1),
+        "sample": "q 4096->4096 at M = 32, one call (f32 weights as the reference runs them)"}
+    # config 5: the INT8 Mamba decode (int8_mamba.rs:78-109), 370M shape
+    mc = dict(MAMBA370M)
+    mm = O.QuantizedMamba(mc)
+    mm.init_synthetic(SEED_BASE)
+    mm.prefill(np.array(_ids(4, mc["vocab"], PROMPT_SEED), np.uint32))
+    s = _median_s(lambda: mm.decode_one(1), 5)
+    mm.close()
+    out["config5_mamba_decode"] = {
+        "tok_s": round(1.0 / s, 3), "ms_per_token": round(s * 1e3, 1),
+        "sample": "median of 5 decode steps after a 4-token prompt (reference semantics: "
+                  "x_proj, dt_proj and lm_head f32)"}
+    out["seconds"] = round(time.perf_counter() - t0, 1)
+    O.set_threads(16)
+    return out
+
+
+def kquant_oracle_model(cfg, np):
+    """The oracle's f32 CausalLM over config 3's block formats (Q4_K attention
+    and gate/up, Q6_K down and lm_head), synthetic weights from the seed spec
+    encoded by the library's host encoder (the bytes the GPU model loads)."""
+    import oracle as O
+    from synapse_amd import hip
+    h, hd = cfg["hidden"], cfg["head_dim"]
+    qd, kvd, inter = cfg["n_heads"] * hd, cfg["n_kv_heads"] * hd, cfg["inter"]
+    q4k, q6k = (hip.FMT_Q4_K, "q4_k"), (hip.FMT_Q6_K, "q6_k")
+    o = O.CausalLM(cfg, qk_norm=False)
+    o.set_embed(O.normal(cfg["vocab"] * h, SEED_BASE, 0.02).reshape(cfg["vocab"], h))
+    shapes = [(qd, h, q4k), (kvd, h, q4k), (kvd, h, q4k), (h, qd, q4k), (inter, h, q4k),
+              (inter, h, q4k), (h, inter, q6k)]
+    for layer in range(cfg["n_layers"]):
+        for p, (n, k, (fmt, name)) in enumerate(shapes):
+            w = O.normal(n * k, SEED_BASE + 1 + 8 * layer + p, 0.02).reshape(n, k)
+            o.set_proj(layer, p, name, hip.kquant_encode(fmt, w))
+    w = O.normal(cfg["vocab"] * h, SEED_BASE + 1 + 8 * cfg["n_layers"], 0.02)
+    o.set_lm_head("q6_k", hip.kquant_encode(hip.FMT_Q6_K, w.reshape(cfg["vocab"], h)))
+    return o
+
+
 def cpu_baseline(budget_s: float):
     """Oracle decode on the host: 1 thread, same model and prompt."""
     import numpy as np
@@ -259,9 +391,11 @@ def main():
 
     from synapse_amd import hip
     hip.init(0)
-    # rows for the timed decode and for the speculative record (k = 4, 64
-    # tokens: a round appends k + 2 rows for k + 1 tokens)
-    cfg = dict(QWEN3, max_seq=PROMPT + max(args.warmup + args.steps, 2 * 64 + 8) + 1)
+    # rows for the timed decode (and the per-kernel timing steps after it) and
+    # for the speculative record (k = 4, 64 tokens: a round appends k + 2
+    # rows for k + 1 tokens)
+    kern_steps = 8
+    cfg = dict(QWEN3, max_seq=PROMPT + max(args.warmup + args.steps + kern_steps, 2 * 64 + 8) + 1)
     t0 = time.perf_counter()
     model = hip.QuantizedCausalLM(cfg)
     model.init_synthetic(SEED_BASE, 0.02)
@@ -287,6 +421,20 @@ def main():
     lm_ms = (model.time_lm_head(args.lm_head_iters) if args.unfused
              else model.time_lm_head_rotating(2 * args.lm_head_iters))
     lm_gbs = lm_head_bytes(QWEN3) / (lm_ms * 1e-3) / 1e9
+    # every kernel of the step, timed by its own start/stop events in eager
+    # steps right after the timed region
+    kern = None
+    if not args.unfused:
+        pos0 = PROMPT + args.warmup + args.steps
+        kern = guarded(model.time_step_kernels, kern_steps)
+        if "error" not in kern:
+            kb = step_kernel_bytes(QWEN3, pos0 + kern_steps // 2)
+            for k, rec in kern.items():
+                rec["us_per_step"] = round(rec["avg_us"] * rec["launches_per_step"], 2)
+                if k in kb:
+                    rec["bytes_per_launch"] = kb[k]
+                    rec["gb_s"] = round(kb[k] / (rec["avg_us"] * 1e-6) / 1e9, 1)
+                    rec["hbm_frac"] = round(rec["gb_s"] / HBM_PEAK_GBS, 4)
     spec = None if args.no_secondary else guarded(speculative_record, model, np)
     model.close()
 
@@ -314,22 +462,50 @@ def main():
         "bytes_per_token": step_bytes,
         "wall_ms_timed_region": round(wall_ms, 2),
         "model_load_s": round(load_s, 1),
-        "roofline": {"bound": "hbm",
-                     "kernel": ("k_lmhead_top2<8,8>" if not args.unfused else "k_gemv_w8a8<1>")
-                               + " lm_head 151936x1024",
-                     "achieved": round(lm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(lm_gbs / HBM_PEAK_GBS, 4),
-                     "traffic": None if args.unfused else round(
-                         1024 * (LM_HEAD_FETCH_KIB * LM_HEAD_FETCH_FACTOR
-                                 + LM_HEAD_WRITE_KIB * LM_HEAD_WRITE_FACTOR)),
-                     "avg_launch_us": round(lm_ms * 1e3, 2),
-                     "bytes_per_launch": lm_head_bytes(QWEN3)},
     }
+    lm_rec = {"kernel": ("k_lmhead_top2<8,8>" if not args.unfused else "k_gemv_w8a8<1>")
+                        + " lm_head 151936x1024",
+              "achieved": round(lm_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+              "frac": round(lm_gbs / HBM_PEAK_GBS, 4),
+              "traffic": None if args.unfused else round(
+                  1024 * (LM_HEAD_FETCH_KIB * LM_HEAD_FETCH_FACTOR
+                          + LM_HEAD_WRITE_KIB * LM_HEAD_WRITE_FACTOR)),
+              "avg_launch_us": round(lm_ms * 1e3, 2), "bytes_per_launch": lm_head_bytes(QWEN3),
+              "timing": "hipEvent pair around back-to-back launches alternating two weight "
+                        "copies (2 x 156 MB > the 256 MB Infinity Cache)"}
+    step_rec = {"kernel": "the whole decode step (graph replay)",
+                "achieved": line["decode_weight_gbs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": line["decode_weight_hbm_frac"], "bytes_per_step": step_bytes,
+                "ms_per_step": round(ms_per_step, 4)}
+    if kern and "error" not in kern:
+        # the dominant kernel of the step: the largest time per step
+        dom = max((k for k in kern if k in STEP_KERNEL_NAMES),
+                  key=lambda k: kern[k]["us_per_step"])
+        d = kern[dom]
+        line["roofline"] = {
+            "bound": "hbm", "kernel": STEP_KERNEL_NAMES[dom], "achieved": d["gb_s"],
+            "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": d["hbm_frac"],
+            "traffic": STEP_KERNEL_TRAFFIC.get(dom), "avg_launch_us": d["avg_us"],
+            "bytes_per_launch": d["bytes_per_launch"],
+            "share_of_step": round(d["us_per_step"] / (ms_per_step * 1e3), 4),
+            "timing": "start/stop hipEvents of every launch (hipExtLaunchKernelGGL: the "
+                      "dispatch's own timestamps) of eager fused steps on the model stream, "
+                      f"positions {PROMPT + args.warmup + args.steps}-"
+                      f"{PROMPT + args.warmup + args.steps + kern_steps}",
+            "step": step_rec, "lm_head": lm_rec}
+        line["step_kernels"] = kern
+    else:
+        line["roofline"] = dict(bound="hbm", **lm_rec)
+        line["roofline"]["step"] = step_rec
+        if kern:
+            line["step_kernels"] = kern
     if not args.no_secondary:
         line["secondary"] = guarded(secondary, hip, np)
         line["secondary"]["config1_speculative_decode"] = spec
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = guarded(cpu_baseline, args.cpu_seconds)
+        if not args.no_secondary:
+            line["cpu_baseline"]["secondary"] = guarded(cpu_baselines_secondary, np)
     print(json.dumps(line), flush=True)
 
 

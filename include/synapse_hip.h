@@ -239,6 +239,7 @@ syn_status_t syn_hip_sample(const float *d_logits, size_t vocab, const uint32_t 
  * host computation). */
 syn_status_t syn_hip_stdrng_f32(uint64_t seed, size_t n, float *out);
 
+
 typedef struct syn_hip_qlm_s syn_hip_qlm_t;
 syn_status_t syn_hip_qlm_create(const syn_hip_lm_config *cfg, syn_hip_qlm_t **out);
 /* embed_tokens [vocab, hidden] f32 (tied: the lm_head is quantized from it) */
@@ -317,6 +318,23 @@ syn_status_t syn_hip_qlm_time_lm_head(syn_hip_qlm_t *m, size_t iters, size_t flu
  * temporary device copy (2 x the weights exceed the Infinity Cache, so every
  * launch streams from HBM); one hipEvent pair around the batch. */
 syn_status_t syn_hip_qlm_time_lm_head_rotating(syn_hip_qlm_t *m, size_t iters, float *avg_ms);
+/* Benchmark helper: `steps` fused decode steps launched eagerly, every kernel
+ * through hipExtLaunchKernelGGL with a start/stop event pair (the dispatch's
+ * own start and end timestamps); per kernel kind the average microseconds per
+ * launch and the launch count (arrays of SYN_HIP_STEP_KINDS).  The steps
+ * advance the model like any decode. */
+#define SYN_HIP_STEP_ZERO 0       /* accumulator zeroing */
+#define SYN_HIP_STEP_QKV 1        /* residual + RMSNorm + quantize + QKV GEMV */
+#define SYN_HIP_STEP_ATTENTION 2  /* head norms, RoPE, KV append, attention */
+#define SYN_HIP_STEP_O 3          /* quantize + O GEMV */
+#define SYN_HIP_STEP_GATE_UP 4    /* residual + RMSNorm + quantize + gate|up (+ SwiGLU) */
+#define SYN_HIP_STEP_DOWN 5       /* (SwiGLU +) quantize + down GEMV */
+#define SYN_HIP_STEP_FINAL_NORM 6
+#define SYN_HIP_STEP_LM_HEAD 7
+#define SYN_HIP_STEP_SELECT 8     /* argmax (or sampling) and state advance */
+#define SYN_HIP_STEP_KINDS 9
+syn_status_t syn_hip_qlm_time_step_kernels(syn_hip_qlm_t *m, size_t steps, float *avg_us,
+                                           uint32_t *launches);
 /* Decode-step options (no reference counterpart; both settings compute the
  * same bits).  fused_decode = 1 (default when the shape fits the fused
  * kernels' LDS rows): five kernels per layer, each a split-K GEMV whose

@@ -1,6 +1,7 @@
 // Shared host/device helpers for the gfx950 backend.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
@@ -40,6 +41,26 @@ syn_status_t hip_fail(hipError_t e, const char *what, const char *file, int line
 syn_status_t ensure_init();
 hipStream_t default_stream();
 inline hipStream_t pick_stream(void *s) { return s ? (hipStream_t)s : default_stream(); }
+
+// Kernel timing with the dispatch's own timestamps: when `start` is set, the
+// next SYN_LAUNCH records the kernel's start and end on these events
+// (hipExtLaunchKernelGGL) and clears them; otherwise it is a plain launch.
+// Host-thread local; set only by benchmark helpers, never under capture.
+struct LaunchEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+LaunchEvents &launch_events();
+#define SYN_LAUNCH(kern, grid, block, shm, stream, ...)                                   \
+  do {                                                                                  \
+    ::syn::LaunchEvents &ev_ = ::syn::launch_events();                                  \
+    if (ev_.start) {                                                                    \
+      hipExtLaunchKernelGGL(kern, grid, block, shm, stream, ev_.start, ev_.stop, 0u,    \
+                            __VA_ARGS__);                                               \
+      ev_.start = ev_.stop = nullptr;                                                   \
+    } else {                                                                            \
+      hipLaunchKernelGGL(kern, grid, block, shm, stream, __VA_ARGS__);                  \
+    }                                                                                   \
+  } while (0)
 
 // RAII device buffer (hipMalloc'd once at set-up, never on a hot path).
 struct DevBuf {

@@ -522,10 +522,10 @@ static syn_status_t launch_fused_nt(const ProArgs &a, const SplitGemv &g, hipStr
   const dim3 grid(g.N64 / 64, g.ks);
   const size_t shm = fused_lds_bytes(a.H, g.C);
   switch (g.u) {
-    case 1: hipLaunchKernelGGL((k_fused_gemv<PRO, NT, 1>), grid, dim3(NT), shm, s, a, ga); break;
-    case 2: hipLaunchKernelGGL((k_fused_gemv<PRO, NT, 2>), grid, dim3(NT), shm, s, a, ga); break;
-    case 4: hipLaunchKernelGGL((k_fused_gemv<PRO, NT, 4>), grid, dim3(NT), shm, s, a, ga); break;
-    default: hipLaunchKernelGGL((k_fused_gemv<PRO, NT, 8>), grid, dim3(NT), shm, s, a, ga); break;
+    case 1: SYN_LAUNCH((k_fused_gemv<PRO, NT, 1>), grid, dim3(NT), shm, s, a, ga); break;
+    case 2: SYN_LAUNCH((k_fused_gemv<PRO, NT, 2>), grid, dim3(NT), shm, s, a, ga); break;
+    case 4: SYN_LAUNCH((k_fused_gemv<PRO, NT, 4>), grid, dim3(NT), shm, s, a, ga); break;
+    default: SYN_LAUNCH((k_fused_gemv<PRO, NT, 8>), grid, dim3(NT), shm, s, a, ga); break;
   }
   SYN_LAUNCH_CHECK();
   return SYN_OK;
@@ -750,10 +750,10 @@ syn_status_t launch_gu_swiglu(const float *base, RowSrc delta, float *res_out, c
   const size_t shm = round_up((size_t)H, 4) * 4 + (size_t)g.C * 16;
   const dim3 grid((unsigned)cdiv((size_t)inter, kGuRows));
   const int ui = (int)cdiv(2 * cdiv((size_t)g.C, 4), 4);  // load instructions per wave
-  if (ui <= 2) hipLaunchKernelGGL((k_gu_swiglu<2>), grid, dim3(256), shm, s, a, g);
-  else if (ui <= 4) hipLaunchKernelGGL((k_gu_swiglu<4>), grid, dim3(256), shm, s, a, g);
-  else if (ui <= 8) hipLaunchKernelGGL((k_gu_swiglu<8>), grid, dim3(256), shm, s, a, g);
-  else hipLaunchKernelGGL((k_gu_swiglu<16>), grid, dim3(256), shm, s, a, g);
+  if (ui <= 2) SYN_LAUNCH((k_gu_swiglu<2>), grid, dim3(256), shm, s, a, g);
+  else if (ui <= 4) SYN_LAUNCH((k_gu_swiglu<4>), grid, dim3(256), shm, s, a, g);
+  else if (ui <= 8) SYN_LAUNCH((k_gu_swiglu<8>), grid, dim3(256), shm, s, a, g);
+  else SYN_LAUNCH((k_gu_swiglu<16>), grid, dim3(256), shm, s, a, g);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
 }
@@ -1358,7 +1358,7 @@ syn_status_t launch_fused_attention(RowSrc qkv, int nh, int nkv, int hd, const f
         done = true;
       }
       const int cb = hd < 64 ? hd : 64;
-      hipLaunchKernelGGL(kern, dim3((unsigned)nh, (unsigned)(hd / cb)), dim3(kAttnNT), shm, s, qkv,
+      SYN_LAUNCH(kern, dim3((unsigned)nh, (unsigned)(hd / cb)), dim3(kAttnNT), shm, s, qkv,
                          nh, nkv, qn, kn, eps, cosT, sinT, st, kc, vc, max_seq, tab, out);
       SYN_LAUNCH_CHECK();
       return SYN_OK;
@@ -1375,7 +1375,7 @@ syn_status_t launch_fused_attention(RowSrc qkv, int nh, int nkv, int hd, const f
     return qkv.f ? pick(std::true_type{}) : pick(std::false_type{});
   }
   const size_t shm = attention_lds_bytes(hd, max_seq);
-  hipLaunchKernelGGL(k_fused_attention, dim3(nh), dim3(256), shm, s, qkv, nh, nkv, hd, qn, kn,
+  SYN_LAUNCH(k_fused_attention, dim3(nh), dim3(256), shm, s, qkv, nh, nkv, hd, qn, kn,
                      eps, cosT, sinT, st, kc, vc, max_seq, out);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
@@ -1443,7 +1443,7 @@ syn_status_t launch_fused_final_norm(const float *base, RowSrc delta, const floa
     set_error("fused final norm: hidden too large");
     return SYN_ERR_INVALID_ARG;
   }
-  hipLaunchKernelGGL(k_fused_final_norm, dim3(1), dim3(1024), round_up((size_t)H, 4) * 4, s, base,
+  SYN_LAUNCH(k_fused_final_norm, dim3(1), dim3(1024), round_up((size_t)H, 4) * 4, s, base,
                      delta, nw, eps, H, xq, s_out);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
@@ -1466,7 +1466,7 @@ syn_status_t launch_zero_i32(int *p, size_t n, hipStream_t s) {
     return SYN_ERR_INVALID_ARG;
   }
   const unsigned blocks = (unsigned)std::min<size_t>(512, cdiv(cdiv(n, 4), 256));
-  hipLaunchKernelGGL(k_zero_i32, dim3(blocks), dim3(256), 0, s, p, n);
+  SYN_LAUNCH(k_zero_i32, dim3(blocks), dim3(256), 0, s, p, n);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
 }
@@ -1556,7 +1556,7 @@ syn_status_t launch_lmhead_top2(const void *W, const float *ws, int N, int C, co
                                 const float *sx, float *logits, float *pv, int *pi, float *pv2,
                                 hipStream_t s) {
   const int P = (int)cdiv((size_t)N, 64);
-  hipLaunchKernelGGL((k_lmhead_top2<8, 8>), dim3(P), dim3(512), 0, s,
+  SYN_LAUNCH((k_lmhead_top2<8, 8>), dim3(P), dim3(512), 0, s,
                      reinterpret_cast<const i32x4 *>(W), ws, N, C, xq, sx, logits, pv, pi, pv2);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
@@ -1596,7 +1596,7 @@ __global__ void __launch_bounds__(1024)
 syn_status_t launch_argmax_advance(const float *pv, const int *pi, const float *pv2, int np,
                                    StepState *st, uint32_t *history, float *mhist,
                                    hipStream_t s) {
-  hipLaunchKernelGGL(k_argmax_advance, dim3(1), dim3(1024), 0, s, pv, pi, pv2, np, st, history,
+  SYN_LAUNCH(k_argmax_advance, dim3(1), dim3(1024), 0, s, pv, pi, pv2, np, st, history,
                      mhist);
   SYN_LAUNCH_CHECK();
   return SYN_OK;

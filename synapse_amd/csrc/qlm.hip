@@ -58,6 +58,32 @@ struct syn_hip_qlm_s {
   hipStream_t stream = nullptr;
   hipGraphExec_t graph = nullptr;
   bool finalized = false;
+  // per-launch event pairs of an eager fused step (syn_hip_qlm_time_step_kernels)
+  struct TraceEntry {
+    int kind;
+    hipEvent_t start, end;
+  };
+  std::vector<TraceEntry> *trace = nullptr;
+  // the next SYN_LAUNCH records its kernel's own start and end on two events
+  syn_status_t trace_begin(hipStream_t) {
+    if (!trace) return SYN_OK;
+    LaunchEvents &ev = launch_events();
+    SYN_HIP(hipEventCreate(&ev.start));
+    SYN_HIP(hipEventCreate(&ev.stop));
+    trace->push_back(TraceEntry{-1, ev.start, ev.stop});
+    return SYN_OK;
+  }
+  syn_status_t trace_end(int kind, hipStream_t) {
+    if (!trace) return SYN_OK;
+    LaunchEvents &ev = launch_events();
+    if (ev.start) {  // the launcher did not go through SYN_LAUNCH
+      ev.start = ev.stop = nullptr;
+      set_error("time_step_kernels: a step kernel is not event-timed");
+      return SYN_ERR_INTERNAL;
+    }
+    trace->back().kind = kind;
+    return SYN_OK;
+  }
   bool fused = true;      // fused five-kernel decode layer (else one kernel per op)
   bool use_graph = true;  // replay the decode step as a HIP graph (else launch eagerly)
   // sampling (sampler.hip): CombinedSampler settings, its scratch, and the
@@ -270,46 +296,69 @@ struct syn_hip_qlm_s {
     float *s_qkv = sc + 0, *s_o = sc + 1, *s_gu = sc + 2, *s_down = sc + 3, *s_head = sc + 4;
     const float eps = c.eps;
     const int nh = (int)c.n_heads, nkv = (int)c.n_kv_heads;
+    SYN_TRY(trace_begin(s));
     SYN_TRY(launch_zero_i32(acc.as<int>(), acc_elems, s));
+    SYN_TRY(trace_end(SYN_HIP_STEP_ZERO, s));
     for (size_t l = 0; l < L; l++) {
       QLayer &Ly = layers[l];
       const RowSrc prev = l == 0 ? RowSrc{} : layers[l - 1].f_down.rows(s_down);
+      SYN_TRY(trace_begin(s));
       SYN_TRY(launch_fused_norm_gemv(l == 0 ? nullptr : xmid.as<float>(), embed.as<float>(),
                                      st(), (int)vocab, zeros_h.as<float>(), prev, xin.as<float>(),
                                      an(l), eps, (int)h, s_qkv, Ly.f_qkv, s));
+      SYN_TRY(trace_end(SYN_HIP_STEP_QKV, s));
+      SYN_TRY(trace_begin(s));
       SYN_TRY(launch_fused_attention(Ly.f_qkv.rows(s_qkv), nh, nkv, (int)hd, qn(l), kn(l), eps,
                                      rope_cos.as<float>(),
                                      rope_sin.as<float>(), st(), kc_l(l), vc_l(l), (int)S,
                                      scores.as<float>(), attn.as<float>(), s));
+      SYN_TRY(trace_end(SYN_HIP_STEP_ATTENTION, s));
+      SYN_TRY(trace_begin(s));
       SYN_TRY(launch_fused_quant_gemv(attn.as<float>(), (int)qd, s_o, Ly.f_o, s));
+      SYN_TRY(trace_end(SYN_HIP_STEP_O, s));
       if (gu_swiglu_fits((int)h)) {
         // gate|up over whole rows with the SwiGLU epilogue, then the down
         // GEMV quantizes only its K range of h with the published max
         unsigned *hmax = reinterpret_cast<unsigned *>(acc.as<int>() + acc_elems) -
                          round_up(L, 64) + l;
+        SYN_TRY(trace_begin(s));
         SYN_TRY(launch_gu_swiglu(xin.as<float>(), Ly.f_o.rows(s_o), xmid.as<float>(), fn(l), eps,
                                  (int)h, s_gu, Ly.gu.w.p, Ly.gu.scales.as<float>(), Ly.gu.chunks,
                                  (int)inter, gu.as<float>(), hmax, s));
+        SYN_TRY(trace_end(SYN_HIP_STEP_GATE_UP, s));
+        SYN_TRY(trace_begin(s));
         SYN_TRY(launch_fused_hq_gemv(gu.as<float>(), hmax, (int)inter, s_down, Ly.f_down, s));
+        SYN_TRY(trace_end(SYN_HIP_STEP_DOWN, s));
       } else {
+        SYN_TRY(trace_begin(s));
         SYN_TRY(launch_fused_norm_gemv(xin.as<float>(), nullptr, st(), (int)vocab, nullptr,
                                        Ly.f_o.rows(s_o), xmid.as<float>(), fn(l), eps,
                                        (int)h, s_gu, Ly.f_gu, s));
+        SYN_TRY(trace_end(SYN_HIP_STEP_GATE_UP, s));
+        SYN_TRY(trace_begin(s));
         SYN_TRY(launch_fused_swiglu_gemv(Ly.f_gu.rows(s_gu), (int)inter, s_down, Ly.f_down, s));
+        SYN_TRY(trace_end(SYN_HIP_STEP_DOWN, s));
       }
     }
+    SYN_TRY(trace_begin(s));
     SYN_TRY(launch_fused_final_norm(xmid.as<float>(), layers[L - 1].f_down.rows(s_down),
                                     final_nw.as<float>(), eps, (int)h, xq.as<int8_t>(), s_head, s));
+    SYN_TRY(trace_end(SYN_HIP_STEP_FINAL_NORM, s));
+    SYN_TRY(trace_begin(s));
     SYN_TRY(launch_lmhead_top2(lm_head.w.p, lm_head.scales.as<float>(), (int)vocab,
                                lm_head.chunks, xq.as<int8_t>(), s_head, logits.as<float>(),
                                pv.as<float>(), pi.as<int>(), pv2.as<float>(), s));
+    SYN_TRY(trace_end(SYN_HIP_STEP_LM_HEAD, s));
+    SYN_TRY(trace_begin(s));
     if (sampling)
-      return launch_sample(logits.as<float>(), (int)vocab, history.as<uint32_t>(), 0, sargs,
-                           u_draws.as<float>(), st(), 1, history.as<uint32_t>(),
-                           mhist.as<float>(), sscr, nullptr, s);
-    return launch_argmax_advance(pv.as<float>(), pi.as<int>(), pv2.as<float>(),
-                                 (int)cdiv(vocab, 64), st(), history.as<uint32_t>(),
-                                 mhist.as<float>(), s);
+      SYN_TRY(launch_sample(logits.as<float>(), (int)vocab, history.as<uint32_t>(), 0, sargs,
+                            u_draws.as<float>(), st(), 1, history.as<uint32_t>(),
+                            mhist.as<float>(), sscr, nullptr, s));
+    else
+      SYN_TRY(launch_argmax_advance(pv.as<float>(), pi.as<int>(), pv2.as<float>(),
+                                    (int)cdiv(vocab, 64), st(), history.as<uint32_t>(),
+                                    mhist.as<float>(), s));
+    return trace_end(SYN_HIP_STEP_SELECT, s);
   }
 
   // sampler settings; the captured decode step changes with them
@@ -967,6 +1016,49 @@ syn_status_t syn_hip_qlm_set_sampler(syn_hip_qlm_t *m, const syn_hip_sampler *pa
                                      uint64_t seed) {
   SYN_TRY(check_model(m));
   return m->set_sampler(params, seed);
+}
+
+syn_status_t syn_hip_qlm_time_step_kernels(syn_hip_qlm_t *m, size_t steps, float *avg_us,
+                                           uint32_t *launches) {
+  SYN_TRY(check_model(m));
+  if (!avg_us || !launches) return SYN_ERR_NULL_PTR;
+  if (!m->fused) {
+    set_error("time_step_kernels: the fused decode step only");
+    return SYN_ERR_INVALID_ARG;
+  }
+  StepState cur;
+  SYN_TRY(m->get_state(&cur));
+  if (steps == 0 || (size_t)cur.pos + steps > m->S) {
+    set_error("time_step_kernels: steps must be in [1, max_seq - cached rows]");
+    return SYN_ERR_INVALID_ARG;
+  }
+  std::vector<syn_hip_qlm_s::TraceEntry> tr;
+  tr.reserve(steps * (5 * m->L + 4));
+  m->trace = &tr;
+  syn_status_t st = SYN_OK;
+  for (size_t i = 0; i < steps && st == SYN_OK; i++) st = m->decode_step(m->stream);
+  m->trace = nullptr;
+  launch_events() = LaunchEvents{};
+  hipError_t e = hipStreamSynchronize(m->stream);
+  double sum[SYN_HIP_STEP_KINDS] = {};
+  uint32_t cnt[SYN_HIP_STEP_KINDS] = {};
+  for (const auto &t : tr) {
+    float ms = 0.0f;
+    if (st == SYN_OK && e == hipSuccess && hipEventElapsedTime(&ms, t.start, t.end) == hipSuccess &&
+        t.kind >= 0 && t.kind < SYN_HIP_STEP_KINDS) {
+      sum[t.kind] += ms;
+      cnt[t.kind]++;
+    }
+    (void)hipEventDestroy(t.start);
+    (void)hipEventDestroy(t.end);
+  }
+  SYN_TRY(st);
+  SYN_HIP(e);
+  for (int k = 0; k < SYN_HIP_STEP_KINDS; k++) {
+    launches[k] = cnt[k];
+    avg_us[k] = cnt[k] ? (float)(sum[k] / cnt[k] * 1e3) : 0.0f;
+  }
+  return SYN_OK;
 }
 
 syn_status_t syn_hip_qlm_time_lm_head_rotating(syn_hip_qlm_t *m, size_t iters, float *avg_ms) {

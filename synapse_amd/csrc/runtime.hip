@@ -44,6 +44,11 @@ syn_status_t ensure_init() {
   return SYN_OK;
 }
 
+LaunchEvents &launch_events() {
+  thread_local LaunchEvents e;
+  return e;
+}
+
 hipStream_t default_stream() {
   int dev = 0;
   (void)hipGetDevice(&dev);

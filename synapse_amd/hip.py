@@ -115,6 +115,7 @@ SIGNATURES = {
     "syn_hip_sample": (ST, [P, SZ, P, SZ, C.POINTER(SamplerParams), C.c_float, P, P, P]),
     "syn_hip_stdrng_f32": (ST, [C.c_uint64, SZ, P]),
     "syn_hip_qlm_time_lm_head_rotating": (ST, [P, SZ, C.POINTER(C.c_float)]),
+    "syn_hip_qlm_time_step_kernels": (ST, [P, SZ, P, P]),
     "syn_hip_qlm_destroy": (ST, [P]),
     "syn_hip_klm_create": (ST, [C.POINTER(KLmConfig), C.POINTER(P)]),
     "syn_hip_klm_forward_prefill_append": (ST, [P, P, SZ, P]),
@@ -597,6 +598,19 @@ class QuantizedCausalLM:
         check(lib().syn_hip_qlm_time_lm_head_rotating(self.h, iters, C.byref(ms)),
               "time_lm_head_rotating")
         return ms.value
+
+    STEP_KINDS = ("zero", "qkv", "attention", "o", "gate_up", "down", "final_norm", "lm_head",
+                  "select")
+
+    def time_step_kernels(self, steps: int = 8) -> dict:
+        """Eager fused steps with a hipEvent pair around every kernel: per kind
+        the average us per launch and the launches per step."""
+        n = len(self.STEP_KINDS)
+        us = (C.c_float * n)()
+        cnt = (C.c_uint32 * n)()
+        check(lib().syn_hip_qlm_time_step_kernels(self.h, steps, us, cnt), "time_step_kernels")
+        return {k: {"avg_us": round(us[i], 3), "launches_per_step": cnt[i] / steps}
+                for i, k in enumerate(self.STEP_KINDS) if cnt[i]}
 
     def time_lm_head(self, iters: int = 20, flush_bytes: int = 512 << 20) -> float:
         ms = C.c_float()

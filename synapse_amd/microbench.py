@@ -85,11 +85,14 @@ def copies_for(nbytes: int, target: int = 1 << 30, cap: int = 512) -> int:
 
 
 def time_gemv(fmt: int, n: int, k: int, m: int = 1, rounds: int = 4, target: int = 1 << 30,
-              seed: int = 0):
-    """Average launch time (ms) of y[m,n] = x[m,k] W^T over rotating copies."""
+              seed: int = 0, launches: int = 0):
+    """Average launch time (ms) of y[m,n] = x[m,k] W^T over rotating copies
+    (`rounds` passes over the copies, or enough for `launches` launches)."""
     rng = np.random.default_rng(seed)
     make = _make(fmt, n, k, rng)
     ncopy = copies_for(weight_bytes(fmt, n, k), target)
+    if launches:
+        rounds = max(rounds, math.ceil(launches / ncopy))
     lins = [make() for _ in range(ncopy)]
     x = hip.DeviceBuffer(max(4, m * k * 4))
     x.upload(rng.standard_normal(m * k, dtype=np.float32))
@@ -115,13 +118,15 @@ def time_gemv(fmt: int, n: int, k: int, m: int = 1, rounds: int = 4, target: int
     return ms, ncopy
 
 
-def gemv_record(fmt: int, n: int, k: int, label: str, rounds: int = 4) -> dict:
-    ms, ncopy = time_gemv(fmt, n, k, 1, rounds)
+def gemv_record(fmt: int, n: int, k: int, label: str, rounds: int = 4,
+                launches: int = 0) -> dict:
+    ms, ncopy = time_gemv(fmt, n, k, 1, rounds, launches=launches)
     nbytes = gemv_bytes(fmt, n, k)
     gbs = nbytes / (ms * 1e-3) / 1e9
+    rounds = max(rounds, math.ceil(launches / ncopy)) if launches else rounds
     return {"matrix": label, "fmt": NAMES[fmt], "k": k, "n": n, "us": round(ms * 1e3, 2),
             "bytes": nbytes, "gb_s": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
-            "copies": ncopy}
+            "copies": ncopy, "launches": ncopy * rounds}
 
 
 def gemm_record(fmt: int, m: int, n: int, k: int, label: str, rounds: int = 3) -> dict:
@@ -160,8 +165,10 @@ def ternary_suite(rounds: int = 4) -> list:
     return [gemv_record(hip.FMT_TERNARY, n, k, lab, rounds) for lab, k, n in Q4_0_SHAPES]
 
 
-def q4_0_suite(rounds: int = 4) -> list:
-    return [gemv_record(hip.FMT_Q4_0, n, k, lab, rounds) for lab, k, n in Q4_0_SHAPES]
+def q4_0_suite(rounds: int = 4, launches: int = 1000) -> list:
+    """Config 2: each matrix at `launches` launches (1000, the configuration's
+    iteration count), round-robin over >= 1 GiB of weight copies."""
+    return [gemv_record(hip.FMT_Q4_0, n, k, lab, rounds, launches) for lab, k, n in Q4_0_SHAPES]
 
 
 def int8_suite(rounds: int = 4) -> list:
