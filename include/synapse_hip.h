@@ -523,9 +523,12 @@ syn_status_t syn_hip_klm_generate_speculative(syn_hip_klm_t *m, const uint32_t *
 /* hipEvent timing of one prefill of `prompt` and `steps` greedy decode steps. */
 syn_status_t syn_hip_klm_time(syn_hip_klm_t *m, const uint32_t *prompt, size_t n_prompt,
                               size_t steps, float *prefill_ms, float *decode_ms);
-/* Decode steps replay a captured HIP graph (graph != 0, the default) or launch
+/* Decode-step form: fused != 0 (the default) runs five kernels per layer
+ * with tree-ordered sums (models whose shapes the fused step supports;
+ * others keep the op-by-op step), fused == 0 one kernel per reference op;
+ * graph != 0 (the default) replays a captured HIP graph, graph == 0 launches
  * the same kernels eagerly (for profilers that do not follow graph launches). */
-syn_status_t syn_hip_klm_set_options(syn_hip_klm_t *m, int graph);
+syn_status_t syn_hip_klm_set_options(syn_hip_klm_t *m, int fused, int graph);
 syn_status_t syn_hip_klm_destroy(syn_hip_klm_t *m);
 
 /* -- INT8 Mamba: QuantizedMambaModel (quantization/ssm/int8_mamba.rs:21-224).

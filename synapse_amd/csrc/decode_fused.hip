@@ -30,36 +30,17 @@
 #include <type_traits>
 
 #include "decode_fused.hpp"
+#include "phase_ts.hpp"
 #include "linear.hpp"
 #include "reduce_order.hpp"
 
 namespace syn {
 
-// Optional phase timestamps of workgroup 0, thread 0 (compiled in only with
-// -DSYN_PHASE_TIMING; read back with syn_hip_debug_phase_ts).
-// Timestamps stay in registers until SYN_TS_FLUSH at the end of the kernel,
-// so the instrumented build issues no extra memory operations mid-kernel.
 #ifdef SYN_PHASE_TIMING
 static __device__ unsigned long long syn_phase_ts[256];
-#define SYN_TS_DECL unsigned long long syn_ts_[16] = {};
-#define SYN_TS(i) syn_ts_[(i)] = __builtin_amdgcn_s_memtime()
-#define SYN_TSR(i) syn_ts_[(i)] = __builtin_amdgcn_s_memrealtime()
-#define SYN_TS_FLUSH(base)                                                       \
-  do {                                                                         \
-    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)                \
-      for (int i_ = 0; i_ < 16; i_++) syn_phase_ts[(base) + i_] = syn_ts_[i_]; \
-  } while (0)
+#define SYN_TS_FLUSH(base) SYN_TS_FLUSH_TO(syn_phase_ts, base)
 #else
-#define SYN_TS_DECL
-#define SYN_TS(i) \
-  do {            \
-  } while (0)
-#define SYN_TSR(i) \
-  do {             \
-  } while (0)
-#define SYN_TS_FLUSH(base) \
-  do {                     \
-  } while (0)
+#define SYN_TS_FLUSH(base) SYN_TS_FLUSH_TO(unused, base)
 #endif
 
 // ------------------------------------------------------------------ helpers
@@ -647,6 +628,9 @@ __global__ void __launch_bounds__(256) k_gu_swiglu(ProArgs a, GuArgs g) {
   const int j0 = blockIdx.x * kGuRows;
   const int jc = min(j0 + r, g.inter - 1);
   const int CG = (g.C + 3) >> 2, T = 2 * CG;
+  SYN_TS_DECL
+  SYN_TS(0);
+  SYN_TSR(14);
   const uint64_t tv = g.exp_tab[tid & 31];
   const float wsg = g.ws[jc], wsu = g.ws[g.inter + jc];
   i32x4 w[UI];
@@ -662,10 +646,13 @@ __global__ void __launch_bounds__(256) k_gu_swiglu(ProArgs a, GuArgs g) {
   };
   float x[RB], nwv[RB];
   norm_prologue_load<NT>(a, H, x, nwv, issue);
+  SYN_TS(1);
   if (tid < 32) exp_tab[tid] = tv;
   for (int i = H + tid; i < g.C * 16; i += NT) xq[i] = 0;
   const float sv = norm_quant<NT, false>(a.eps, H, x, nwv, sq, xq, red);
+  SYN_TS(2);
   bar<NT>();
+  SYN_TS(3);
   int ag = 0, au = 0;
 #pragma unroll
   for (int i = 0; i < UI; i++) {
@@ -683,6 +670,7 @@ __global__ void __launch_bounds__(256) k_gu_swiglu(ProArgs a, GuArgs g) {
       else ag += d;
     }
   }
+  SYN_TS(4);
   ag += __shfl_xor(ag, 16);
   au += __shfl_xor(au, 16);
   ag += __shfl_xor(ag, 32);
@@ -692,6 +680,7 @@ __global__ void __launch_bounds__(256) k_gu_swiglu(ProArgs a, GuArgs g) {
     redi[(NW + wave) * kGuRows + lane] = au;
   }
   bar<NT>();
+  SYN_TS(5);
   if (wave == 0) {
     float m = 0.0f;
     if (lane < kGuRows) {
@@ -715,6 +704,7 @@ __global__ void __launch_bounds__(256) k_gu_swiglu(ProArgs a, GuArgs g) {
     m = wave_max_nonneg(m);
     if (lane == 0) atomicMax(g.hmax, __float_as_uint(m));
   }
+  SYN_TS(6);
   if (blockIdx.x == 0) {  // the residual row for the next layer, the scale
     if (a.res_out) {
 #pragma unroll
@@ -723,6 +713,8 @@ __global__ void __launch_bounds__(256) k_gu_swiglu(ProArgs a, GuArgs g) {
     }
     if (tid == 0) a.s_out[0] = sv;
   }
+  SYN_TSR(15);
+  SYN_TS_FLUSH(112);
 }
 
 bool gu_swiglu_fits(int H) { return H <= RB * 256; }
@@ -1469,31 +1461,6 @@ syn_status_t launch_zero_i32(int *p, size_t n, hipStream_t s) {
   SYN_LAUNCH(k_zero_i32, dim3(blocks), dim3(256), 0, s, p, n);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
-}
-
-struct Top2v {
-  float v1;
-  int i1;
-  float v2;
-};
-
-// larger value wins; on equal values the larger index (the last maximum,
-// sampler.rs:217-224); v2 = the largest value other than the winner
-__device__ __forceinline__ Top2v top2v_merge(Top2v a, Top2v b) {
-  const bool bw = (b.v1 > a.v1) || (b.v1 == a.v1 && b.i1 > a.i1);
-  const Top2v w = bw ? b : a, l = bw ? a : b;
-  return Top2v{w.v1, w.i1, fmaxf(w.v2, l.v1)};
-}
-
-__device__ __forceinline__ Top2v wave_top2(Top2v t) {
-  for (int o = 32; o > 0; o >>= 1) {
-    Top2v u;
-    u.v1 = __shfl_xor(t.v1, o);
-    u.i1 = __shfl_xor(t.i1, o);
-    u.v2 = __shfl_xor(t.v2, o);
-    t = top2v_merge(t, u);
-  }
-  return t;
 }
 
 // one workgroup per 64-row panel; each wave takes every NW-th K chunk

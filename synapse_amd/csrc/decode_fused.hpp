@@ -97,6 +97,32 @@ bool fused_gemv_fits(int H);
 // final residual + RMSNorm + quantize into global xq / s_out (one workgroup)
 syn_status_t launch_fused_final_norm(const float *base, RowSrc delta, const float *nw, float eps,
                                      int H, int8_t *xq, float *s_out, hipStream_t s);
+// per-panel top-2 of the lm_head rows (merged by launch_argmax_advance)
+struct Top2v {
+  float v1;
+  int i1;
+  float v2;
+};
+
+// larger value wins; on equal values the larger index (the last maximum,
+// sampler.rs:217-224); v2 = the largest value other than the winner
+__device__ __forceinline__ Top2v top2v_merge(Top2v a, Top2v b) {
+  const bool bw = (b.v1 > a.v1) || (b.v1 == a.v1 && b.i1 > a.i1);
+  const Top2v w = bw ? b : a, l = bw ? a : b;
+  return Top2v{w.v1, w.i1, fmaxf(w.v2, l.v1)};
+}
+
+__device__ __forceinline__ Top2v wave_top2(Top2v t) {
+  for (int o = 32; o > 0; o >>= 1) {
+    Top2v u;
+    u.v1 = __shfl_xor(t.v1, o);
+    u.i1 = __shfl_xor(t.i1, o);
+    u.v2 = __shfl_xor(t.v2, o);
+    t = top2v_merge(t, u);
+  }
+  return t;
+}
+
 // lm_head GEMV (one workgroup per 64-row panel) -> logits + per-panel top-2
 syn_status_t launch_lmhead_top2(const void *W, const float *ws, int N, int C, const int8_t *xq,
                                 const float *sx, float *logits, float *pv, int *pi, float *pv2,

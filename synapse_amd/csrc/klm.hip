@@ -12,6 +12,7 @@
 #include <vector>
 
 #include "decode_fused.hpp"
+#include "klm_fused.hpp"
 #include "kquant.hpp"
 #include "layer_ops.hpp"
 
@@ -38,6 +39,12 @@ struct syn_hip_klm_s {
   hipGraphExec_t graph = nullptr;
   bool finalized = false;
   bool use_graph = true;  // replay the captured decode step, else launch eagerly
+  bool use_fused = true;  // five-kernel decode layers (klm_fused.hip) when the model fits
+  // fused decode step: split plans, the fixed-point residual r [h] and QKV
+  // accumulator [n_qkv], attention chunk partials, lm_head per-panel top-2
+  bool fused_ok = false;
+  KqfPlan fp_qkv, fp_o, fp_gu, fp_down, fp_lm;
+  DevBuf f_r, f_qkv, f_ao, f_aml, f_pv, f_pi, f_pv2;
 
   ~syn_hip_klm_s() {
     if (graph) (void)hipGraphExecDestroy(graph);
@@ -193,8 +200,94 @@ struct syn_hip_klm_s {
 
   // n_layers < L: CausalLM::forward_one_draft (causal_lm.rs:283-323), the
   // first n_layers layers, zero K/V rows appended to the others
+  // the fused step's buffers and launch plans (all layers share shapes and formats)
+  syn_status_t setup_fused() {
+    fused_ok = false;
+    const int fm[5] = {c.fmt_qkv, c.fmt_o, c.fmt_gate_up, c.fmt_down, c.fmt_lm_head};
+    if (!kqf_fits((int)h, (int)qd, (int)inter, (int)c.base.n_heads, (int)c.base.n_kv_heads,
+                  (int)hd, (int)S, fm, 5))
+      return SYN_OK;
+    const Layer &L0 = layers[0];
+    fp_qkv = kqf_plan(L0.qkv, false);
+    fp_o = kqf_plan(L0.o, false);
+    fp_gu = kqf_plan(L0.gu, true);
+    fp_down = kqf_plan(L0.down, false);
+    fp_lm = kqf_plan(lm_head, false);
+    fp_lm.bs = fp_lm.units;  // the top-2 epilogue needs whole dot products
+    fp_lm.ks = 1;
+    const size_t nch = (size_t)kqf_chunks((int)S), nh = c.base.n_heads;
+    SYN_TRY(f_r.alloc(h * 8));
+    SYN_TRY(f_qkv.alloc(n_qkv * 8));
+    SYN_HIP(hipMemset(f_qkv.p, 0, f_qkv.bytes));  // later steps leave it cleared
+    SYN_TRY(f_ao.alloc(nh * nch * hd * 4));
+    SYN_TRY(f_aml.alloc(nh * nch * 2 * 4));
+    SYN_HIP(hipMemset(f_ao.p, 0, f_ao.bytes));
+    SYN_HIP(hipMemset(f_aml.p, 0, f_aml.bytes));
+    SYN_TRY(f_pv.alloc((size_t)fp_lm.groups * 4));
+    SYN_TRY(f_pi.alloc((size_t)fp_lm.groups * 4));
+    SYN_TRY(f_pv2.alloc((size_t)fp_lm.groups * 4));
+    fused_ok = true;
+    return SYN_OK;
+  }
+
+  // fused decode step (klm_fused.hip): five kernels per layer, then the
+  // lm_head with per-panel top-2 and the merge that advances the state
+  syn_status_t decode_step_fused(hipStream_t s, size_t n) {
+    const float eps = c.base.eps;
+    const int nh = (int)c.base.n_heads, nkv = (int)c.base.n_kv_heads;
+    long long *r = f_r.as<long long>(), *aq = f_qkv.as<long long>();
+    for (size_t l = 0; l < n; l++) {
+      Layer &Ly = layers[l];
+      KqfIn a;  // K1: QKV rows of rmsnorm(r) (layer 0: of the token's embedding row)
+      a.r = r;
+      a.embed = embed.as<float>();
+      a.vocab = (int)vocab;
+      a.r_out = r;
+      a.st = st();
+      a.gain = attn_nw.as<float>() + l * h;
+      a.eps = eps;
+      a.H = (int)h;
+      SYN_TRY(kqf_gemv(Ly.qkv, fp_qkv, l == 0 ? KQF_PRO_EMBED : KQF_PRO_NORM, a, aq, nullptr, 0,
+                       s));
+      SYN_TRY(kqf_attention(aq, nh, nkv, (int)hd, c.qk_norm ? q_nw.as<float>() + l * hd : nullptr,
+                            c.qk_norm ? k_nw.as<float>() + l * hd : nullptr, eps,
+                            rope_cos.as<float>(), rope_sin.as<float>(), st(), kc_l(l), vc_l(l),
+                            (int)S, f_ao.as<float>(), f_aml.as<float>(), s));
+      KqfIn b;  // K3: combine of the attention chunks; r += o; the QKV accumulator cleared
+      b.ao = f_ao.as<float>();
+      b.aml = f_aml.as<float>();
+      b.hd = (int)hd;
+      b.nch = kqf_chunks((int)S);
+      b.st = st();
+      SYN_TRY(kqf_gemv(Ly.o, fp_o, KQF_PRO_ATTN, b, r, aq, (int)n_qkv, s));
+      KqfIn g;  // K4: gate|up of rmsnorm(r), SwiGLU
+      g.r = r;
+      g.gain = ffn_nw.as<float>() + l * h;
+      g.eps = eps;
+      g.H = (int)h;
+      SYN_TRY(kqf_gate_up(Ly.gu, fp_gu, g, (int)inter, hbuf.as<float>(), s));
+      KqfIn d;  // K5: r += down(h)
+      d.x = hbuf.as<float>();
+      SYN_TRY(kqf_gemv(Ly.down, fp_down, KQF_PRO_NONE, d, r, nullptr, 0, s));
+    }
+    if (n < L)
+      SYN_TRY(launch_kv_zero_rows(kc_l(n), vc_l(n), k_elems(), v_elems(), (int)(L - n),
+                                  (int)c.base.n_kv_heads, (int)hd, (int)S, st(), s));
+    KqfIn f;  // final norm of r
+    f.r = r;
+    f.gain = final_nw.as<float>();
+    f.eps = eps;
+    f.H = (int)h;
+    SYN_TRY(kqf_lm_head(lm_head, fp_lm, f, logits.as<float>(), f_pv.as<float>(),
+                        f_pi.as<int>(), f_pv2.as<float>(), s));
+    return launch_argmax_advance(f_pv.as<float>(), f_pi.as<int>(), f_pv2.as<float>(),
+                                 fp_lm.groups, st(), history.as<uint32_t>(), mhist.as<float>(),
+                                 s);
+  }
+
   syn_status_t decode_step(hipStream_t s, size_t n_layers = SIZE_MAX) {
     const size_t n = std::min(n_layers, L);
+    if (use_fused && fused_ok && n > 0) return decode_step_fused(s, n);
     SYN_TRY(launch_embed(embed.as<float>(), &st()->token, 1, (int)h, (int)vocab, x.as<float>(), s));
     for (size_t l = 0; l < n; l++) SYN_TRY(layer(l, 1, false, s));
     if (n < L)
@@ -522,6 +615,7 @@ syn_status_t syn_hip_klm_finalize(syn_hip_klm_t *m) {
     SYN_TRY(Ly.down.prepare(m->S));
   }
   SYN_TRY(m->lm_head.prepare(1));
+  SYN_TRY(m->setup_fused());
   m->finalized = true;
   SYN_TRY(m->set_state(0, 0, 0));
   return SYN_OK;
@@ -847,8 +941,18 @@ syn_status_t syn_hip_klm_load_gguf(syn_hip_klm_t *m, const syn_hip_gguf_t *g) {
   return syn_hip_klm_set_lm_head(m, t.data);
 }
 
-syn_status_t syn_hip_klm_set_options(syn_hip_klm_t *m, int graph) {
+syn_status_t syn_hip_klm_set_options(syn_hip_klm_t *m, int fused, int graph) {
   if (!m) return SYN_ERR_NULL_PTR;
+  SYN_HIP(hipStreamSynchronize(m->stream));
+  if (m->graph && (m->use_fused != (fused != 0))) {  // the captured step changes form
+    (void)hipGraphExecDestroy(m->graph);
+    m->graph = nullptr;
+  }
+  if (m->draft_graph && (m->use_fused != (fused != 0))) {
+    (void)hipGraphExecDestroy(m->draft_graph);
+    m->draft_graph = nullptr;
+  }
+  m->use_fused = fused != 0;
   m->use_graph = graph != 0;
   return SYN_OK;
 }

@@ -1,0 +1,66 @@
+// Fused f32 decode step of the K-quant CausalLM (klm_fused.hip).
+#pragma once
+
+#include "kquant.hpp"
+#include "layer_ops.hpp"
+
+namespace syn {
+
+// Launch shape of one split-K GEMV: `groups` row groups (64-row panels, or
+// 32 gate + 32 up rows) x `ks` splits of `bs` 256-element units each.
+struct KqfPlan {
+  int groups = 0, units = 0, bs = 0, ks = 0;
+};
+
+// The decode GEMV's input row.  The residual stream and the split-K
+// accumulators are fixed point, value * 2^32 in an int64 (sums of them are
+// exact, so the split-K atomics are order-independent and deterministic).
+struct KqfIn {
+  // NORM: rmsnorm of the residual r; EMBED: rmsnorm of the embedding row of
+  // st->token (a zero row past the vocabulary), whose fixed-point form
+  // workgroup (0,0) stores to r_out.  The GEMV reads row * gain and scales
+  // its dot products by 1/rms(row).
+  const long long *r = nullptr;
+  const float *embed = nullptr;
+  int vocab = 0;
+  long long *r_out = nullptr;
+  const float *gain = nullptr;
+  float eps = 0.0f;
+  int H = 0;
+  // NONE: the f32 row itself
+  const float *x = nullptr;
+  // ATTN: the combine of the attention's per-chunk partials
+  const float *ao = nullptr, *aml = nullptr;
+  int hd = 0, nch = 0;
+  const StepState *st = nullptr;
+};
+
+enum { KQF_PRO_NONE = 0, KQF_PRO_NORM = 1, KQF_PRO_EMBED = 2, KQF_PRO_ATTN = 3 };
+
+// whether the fused step supports a model of these shapes and formats
+bool kqf_fits(int H, int qd, int inter, int nh, int nkv, int hd, int max_seq, const int *fmts,
+              int nfmt);
+// split plan of a GEMV over n rows and k inputs (gu: gate|up pairs, whole K)
+KqfPlan kqf_plan(const QLinearKQ &w, bool gu);
+// split-K GEMV whose splits add their fixed-point dot products into acc[row]
+// with atomics; zero[0 .. nzero) is cleared first (the QKV accumulator, for
+// the next layer, by the O projection)
+syn_status_t kqf_gemv(const QLinearKQ &w, const KqfPlan &p, int pro, const KqfIn &in,
+                      long long *acc, long long *zero, int nzero, hipStream_t s);
+// gate|up rows (w = [gate; up], inter rows each) over the whole K of
+// rmsnorm(r) and h = silu(gate) * up
+syn_status_t kqf_gate_up(const QLinearKQ &w, const KqfPlan &p, const KqfIn &in, int inter,
+                         float *h, hipStream_t s);
+// lm_head rows of rmsnorm(r) -> logits and the per-panel top-2 (pv, pi, pv2)
+syn_status_t kqf_lm_head(const QLinearKQ &w, const KqfPlan &p, const KqfIn &in, float *logits,
+                         float *pv, int *pi, float *pv2, hipStream_t s);
+// attention of one token per (kv head, 64-position chunk): q/k/v from the
+// fixed-point QKV accumulator, head norms (qn/kn may be null), RoPE, KV
+// append at st->pos, chunk softmax and P.V -> ao [nh][nch][hd], aml [nh][nch][2]
+syn_status_t kqf_attention(const long long *qkv, int nh, int nkv, int hd, const float *qn,
+                           const float *kn, float eps, const float *cosT, const float *sinT,
+                           const StepState *st, float *kc, float *vc, int max_seq, float *ao,
+                           float *aml, hipStream_t s);
+inline int kqf_chunks(int max_seq) { return (max_seq + 63) / 64; }
+
+}  // namespace syn

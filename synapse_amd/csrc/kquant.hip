@@ -25,6 +25,7 @@
 #include <cmath>
 #include <vector>
 
+#include "kq_unit.hpp"
 #include "kquant.hpp"
 
 namespace syn {
@@ -459,42 +460,7 @@ __global__ void __launch_bounds__(1024)
 }
 
 // ------------------------------------------------------------------ batch-1 GEMV
-// Q4_K / Q6_K at M = 1 with mixed-precision FMAs (v_fma_mix_f32: f16 weight
-// operand, f32 activation and accumulator).  Quant fields masked in place
-// inside the low 8 bits of a 16-bit half are exact f16 subnormals q * 2^-24
-// times a power of two set by their bit offset, so each element costs one
-// FMA and a few masks per dword instead of an extract, a convert and an FMA:
-//   nibbles (Q4_K, Q6_K low bits), element k at bits 4k of a dword:
-//     w & 0x000f000f -> (e0, e4)   w & 0x00f000f0 -> 16 (e1, e5)   (w>>8): (e2,e6), 16 (e3,e7)
-//   2-bit fields (Q6_K high bits), element m at bits 2m of a dword:
-//     h & 0x00030003 -> (m0, m8)   & 0x000c000c -> 4 (m1, m9)   & 0x00300030 -> 16 (m2, m10)
-//     & 0x00c000c0 -> 64 (m3, m11)                               (h>>8): m4..m7 with m12..m15
-// Each power-of-two class has its own f32 accumulator; the classes are
-// combined with exact power-of-two FMAs, so the values are the f32 path's
-// (up to summation order).  Sub-block sums of the activations (Q4_K's dmin
-// term, Q6_K's -32 offset) are loaded ahead of the weights and formed while
-// the weights stream in.
-typedef _Float16 kq_h2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ kq_h2 kq_as_h2(uint32_t v) { return __builtin_bit_cast(kq_h2, v); }
-
-// sum_k e_k x_k over the 8 nibbles of w, scaled by 2^-24: returns into
-// a (class x1) and b (class x16)
-__device__ __forceinline__ void kq_nib8(uint32_t w, const float *__restrict__ xc, float &a,
-                                        float &b) {
-  const uint32_t w8 = w >> 8;
-  const kq_h2 p0 = kq_as_h2(w & 0x000f000fu), p1 = kq_as_h2(w & 0x00f000f0u);
-  const kq_h2 p2 = kq_as_h2(w8 & 0x000f000fu), p3 = kq_as_h2(w8 & 0x00f000f0u);
-  a = __builtin_fmaf((float)p0.x, xc[0], a);
-  b = __builtin_fmaf((float)p1.x, xc[1], b);
-  a = __builtin_fmaf((float)p2.x, xc[2], a);
-  b = __builtin_fmaf((float)p3.x, xc[3], b);
-  a = __builtin_fmaf((float)p0.y, xc[4], a);
-  b = __builtin_fmaf((float)p1.y, xc[5], b);
-  a = __builtin_fmaf((float)p2.y, xc[6], a);
-  b = __builtin_fmaf((float)p3.y, xc[7], b);
-}
-
+// Q4_K / Q6_K at M = 1: one lane per row, the unit decoders of kq_unit.hpp.
 template <int FMT, int NW, int U>
 __global__ void __launch_bounds__(NW * 64)
     k_gemv_kqh(const u32x4 *__restrict__ W, const uint16_t *__restrict__ Wd,
@@ -565,75 +531,10 @@ __global__ void __launch_bounds__(NW * 64)
       if (b < b1) {
         const float *xs = x + (size_t)b * 256;
         const float *as = asum + (b - b0) * GPB;
-        if constexpr (FMT == SYN_HIP_FMT_Q4_K) {
-          const float d = syn_f16_to_f32_rs(pl[u][0].x & 0xffffu);
-          const float dmin = syn_f16_to_f32_rs(pl[u][0].x >> 16);
-          const uint32_t sbw[3] = {pl[u][0].y, pl[u][0].z, pl[u][0].w};
-          auto SB = [&](int i) -> uint32_t { return (sbw[i >> 2] >> (8 * (i & 3))) & 0xffu; };
-#pragma unroll
-          for (int sb = 0; sb < 8; sb++) {
-            uint32_t sc, mn;  // gguf.rs:405-410, u8 arithmetic
-            if (sb < 4) {
-              sc = SB(sb) & 63u;
-              mn = ((SB(sb + 4) >> 4) | ((SB(sb + 8) & 15u) << 4)) & 0xffu;
-            } else {
-              sc = (SB(sb) & 15u) | ((SB(sb - 4) >> 6) << 4);
-              mn = ((SB(sb + 4) >> 4) | (((SB(sb - 4) >> 4) & 12u) << 4)) & 0xffu;
-            }
-            const float scf = d * (float)sc;
-            const float mf = dmin * (float)mn;
-            const u32x4 q = pl[u][1 + sb];
-            const float *xc = xs + sb * 32;
-            float a = 0.0f, c16 = 0.0f;
-            kq_nib8(q.x, xc, a, c16);
-            kq_nib8(q.y, xc + 8, a, c16);
-            kq_nib8(q.z, xc + 16, a, c16);
-            kq_nib8(q.w, xc + 24, a, c16);
-            const float t = __builtin_fmaf(c16, 0.0625f, a) * 16777216.0f;
-            acc = __builtin_fmaf(scf, t, acc);
-            acc = __builtin_fmaf(-mf, as[sb], acc);
-          }
-        } else {  // Q6_K
-          const float d = syn_f16_to_f32_rs(dh[u]);
-          const uint32_t scw[4] = {pl[u][12].x, pl[u][12].y, pl[u][12].z, pl[u][12].w};
-#pragma unroll
-          for (int g = 0; g < 16; g++) {
-            // ql bytes 8g..8g+7: plane g/2, dwords 2*(g%2), 2*(g%2)+1
-            const u32x4 qp = pl[u][g >> 1];
-            const uint32_t lo0 = (g & 1) ? qp.z : qp.x, lo1 = (g & 1) ? qp.w : qp.y;
-            // qh bytes 4g..4g+3: plane 8 + g/4, dword g%4
-            const u32x4 hp = pl[u][8 + (g >> 2)];
-            const uint32_t hi = (g & 3) == 0 ? hp.x : (g & 3) == 1 ? hp.y : (g & 3) == 2 ? hp.z : hp.w;
-            const float scale = (float)(int8_t)(scw[g >> 2] >> (8 * (g & 3))) * d;
-            const float *xc = xs + g * 16;
-            float l1 = 0.0f, l16 = 0.0f;
-            kq_nib8(lo0, xc, l1, l16);
-            kq_nib8(lo1, xc + 8, l1, l16);
-            float h1 = 0.0f, h4 = 0.0f, h16 = 0.0f, h64 = 0.0f;
-#pragma unroll
-            for (int half = 0; half < 2; half++) {
-              const uint32_t hw = hi >> (8 * half);
-              const float *xh = xc + 4 * half;
-              const kq_h2 a0 = kq_as_h2(hw & 0x00030003u), a1 = kq_as_h2(hw & 0x000c000cu);
-              const kq_h2 a2 = kq_as_h2(hw & 0x00300030u), a3 = kq_as_h2(hw & 0x00c000c0u);
-              h1 = __builtin_fmaf((float)a0.x, xh[0], h1);
-              h4 = __builtin_fmaf((float)a1.x, xh[1], h4);
-              h16 = __builtin_fmaf((float)a2.x, xh[2], h16);
-              h64 = __builtin_fmaf((float)a3.x, xh[3], h64);
-              h1 = __builtin_fmaf((float)a0.y, xh[8], h1);
-              h4 = __builtin_fmaf((float)a1.y, xh[9], h4);
-              h16 = __builtin_fmaf((float)a2.y, xh[10], h16);
-              h64 = __builtin_fmaf((float)a3.y, xh[11], h64);
-            }
-            // q = lo + 16 hi; sum q x = 2^24 * (lo + 16 hi) with the classes rescaled
-            const float hs = __builtin_fmaf(
-                h64, 0.015625f, __builtin_fmaf(h16, 0.0625f, __builtin_fmaf(h4, 0.25f, h1)));
-            const float ls = __builtin_fmaf(l16, 0.0625f, l1);
-            const float t = __builtin_fmaf(hs, 16.0f, ls) * 16777216.0f;
-            const float v = t - 32.0f * as[g];
-            acc = __builtin_fmaf(v, scale, acc);
-          }
-        }
+        if constexpr (FMT == SYN_HIP_FMT_Q4_K)
+          kq4_unit(pl[u], xs, as, acc);
+        else
+          kq6_unit(pl[u], dh[u], xs, as, acc);
       }
     }
     if (bb + NW * U < b1) issue(bb + NW * U);

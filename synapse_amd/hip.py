@@ -133,7 +133,7 @@ SIGNATURES = {
     "syn_hip_klm_forward_one": (ST, [P, C.c_uint32, P]),
     "syn_hip_klm_generate": (ST, [P, P, SZ, SZ, P, P]),
     "syn_hip_klm_time": (ST, [P, P, SZ, SZ, C.POINTER(C.c_float), C.POINTER(C.c_float)]),
-    "syn_hip_klm_set_options": (ST, [P, C.c_int]),
+    "syn_hip_klm_set_options": (ST, [P, C.c_int, C.c_int]),
     "syn_hip_klm_set_norms": (ST, [P, C.c_uint32, P, P, P, P]),
     "syn_hip_klm_set_final_norm": (ST, [P, P]),
     "syn_hip_klm_load_gguf": (ST, [P, P]),
@@ -718,9 +718,10 @@ class KQuantCausalLM:
                                      C.byref(d)), "klm_time")
         return p.value, d.value
 
-    def set_options(self, graph: bool = True):
-        """HIP graph replay of the decode step, or eager launches (same results)."""
-        check(lib().syn_hip_klm_set_options(self.h, int(graph)), "set_options")
+    def set_options(self, fused: bool = True, graph: bool = True):
+        """Decode-step form: fused five-kernel layers (tree-ordered sums) or one
+        kernel per op; HIP graph replay or eager launches (same results)."""
+        check(lib().syn_hip_klm_set_options(self.h, int(fused), int(graph)), "set_options")
 
     def set_norms(self, layer: int, attn=None, ffn=None, q=None, k=None):
         """RMSNorm gains of one layer (None leaves a gain as it is; all start at 1.0)."""

@@ -207,3 +207,98 @@ def test_load_gguf_rejects_wrong_format(tmp_path):
         g = hip.KQuantCausalLM(TINY, *((hip.FMT_Q8_0,) * 5))
         with pytest.raises(hip.SynapseError, match="GGML type"):
             g.load_gguf(f)
+
+
+# ------------------------------------------------------------------ fused decode step
+# The fused step (klm_fused.hip: five kernels per layer, split-K partials
+# summed by the consumer, flash-decoding attention over 64-position chunks)
+# sums in another order than the op-by-op step, so it is held to the
+# oracle's tolerance and to the op-by-op step within rounding; graph replay,
+# eager launches and repeated runs of it must agree bit for bit.
+FUSED_CASES = [
+    # (n_heads, n_kv_heads, head_dim, fmts, qk_norm): GQA group sizes 1..8
+    (16, 16, 16, LLAMA_FMTS, False),
+    (8, 2, 32, LLAMA_FMTS, True),
+    (6, 2, 64, (hip.FMT_Q8_0,) * 5, True),
+    (16, 2, 128, LLAMA_FMTS, False),
+    (4, 1, 128, (hip.FMT_Q6_K, hip.FMT_Q4_K, hip.FMT_Q8_0, hip.FMT_Q4_K, hip.FMT_Q4_K), False),
+]
+
+
+def _fused_cfg(nh, nkv, hd, max_seq=150):
+    # max_seq not a multiple of 64: the last chunk of the cache is partial
+    return dict(hidden=512, n_layers=2, n_heads=nh, n_kv_heads=nkv, head_dim=hd, inter=768,
+                vocab=520, max_seq=max_seq, eps=1e-5, rope_theta=1e4)
+
+
+def _teacher_forced(g, ids, toks):
+    g.prefill(ids)
+    return [g.forward_one(t) for t in toks]
+
+
+@pytest.mark.parametrize("nh,nkv,hd,fmts,qkn", FUSED_CASES)
+def test_fused_step_tracks_oracle_and_op_by_op(nh, nkv, hd, fmts, qkn):
+    cfg = _fused_cfg(nh, nkv, hd)
+    o, g = build_pair(cfg, fmts, qk_norm=qkn)
+    ids = O.token_ids(60, 0x5EED0000 + 0xFFFF, cfg["vocab"])
+    # decode from position 60 across the chunk boundary at 64 to 89
+    toks = [int(t) for t in O.token_ids(30, 0x5EED0000 + 0x7777, cfg["vocab"])]
+    print(f"case nh={nh} nkv={nkv} hd={hd} qk_norm={qkn}", flush=True)
+    g.set_options(fused=False, graph=True)
+    unf = _teacher_forced(g, ids, toks)
+    g.set_options(fused=True, graph=True)
+    fus = _teacher_forced(g, ids, toks)
+    o.prefill(ids)
+    for step, t in enumerate(toks):
+        lo = o.forward_one(t)
+        assert _cos(lo, fus[step]) >= 0.9999 and _rel(fus[step], lo) < 5e-3, (step,)
+        assert _cos(unf[step], fus[step]) >= 0.99999 and _rel(fus[step], unf[step]) < 2e-4, step
+
+
+@pytest.mark.parametrize("nh,nkv,hd,fmts,qkn", [FUSED_CASES[1], FUSED_CASES[3]])
+def test_fused_step_graph_eager_and_reruns_identical(nh, nkv, hd, fmts, qkn):
+    cfg = _fused_cfg(nh, nkv, hd)
+    _, g = build_pair(cfg, fmts, qk_norm=qkn)
+    # an 8-token prompt takes the GEMV prefill (the MFMA prefill GEMM adds
+    # split-K tiles with float atomics, whose rounding varies run to run)
+    ids = O.token_ids(8, 0x5EED0000 + 0xFFFF, cfg["vocab"])
+    outs = []
+    for graph in (True, False, True):
+        g.set_options(fused=True, graph=graph)
+        outs.append(g.generate(ids, 135))  # positions 8 .. 141: chunk boundaries 64, 128
+    for toks, margins in outs[1:]:
+        np.testing.assert_array_equal(toks, outs[0][0])
+        np.testing.assert_array_equal(margins, outs[0][1])
+
+
+def test_fused_step_fills_the_cache_to_max_seq():
+    # the last decode step writes cache row max_seq - 1 (partial last chunk)
+    cfg = _fused_cfg(8, 2, 128, max_seq=130)
+    o, g = build_pair(cfg, LLAMA_FMTS)
+    ids = O.token_ids(100, 0x5EED0000 + 0xFFFF, cfg["vocab"])
+    toks = [int(t) for t in O.token_ids(30, 0x5EED0000 + 0x5555, cfg["vocab"])]
+    fus = _teacher_forced(g, ids, toks)
+    o.prefill(ids)
+    for step, t in enumerate(toks):
+        lo = o.forward_one(t)
+        assert _cos(lo, fus[step]) >= 0.9999 and _rel(fus[step], lo) < 5e-3, step
+
+
+def test_fused_step_llama_3b_widths():
+    # LLaMA-3.2-3B layer widths: the split plans of the benchmark model
+    cfg = dict(hidden=3072, n_layers=2, n_heads=24, n_kv_heads=8, head_dim=128, inter=8192,
+               vocab=128256, max_seq=200, eps=1e-5, rope_theta=5e5)
+    o, g = build_pair(cfg, LLAMA_FMTS)
+    ids = O.token_ids(120, 0x5EED0000 + 0xFFFF, cfg["vocab"])
+    toks = [int(t) for t in O.token_ids(16, 0x5EED0000 + 0x3333, cfg["vocab"])]
+    g.set_options(fused=False, graph=True)
+    unf = _teacher_forced(g, ids, toks)
+    g.set_options(fused=True, graph=True)
+    fus = _teacher_forced(g, ids, toks)
+    o.prefill(ids)
+    for step, t in enumerate(toks):
+        lo = o.forward_one(t)
+        print("step", step, "cos", _cos(lo, fus[step]), "rel", _rel(fus[step], lo),
+              "vs op-by-op", _rel(fus[step], unf[step]), flush=True)
+        assert _cos(lo, fus[step]) >= 0.9999
+        assert _cos(unf[step], fus[step]) >= 0.99999 and _rel(fus[step], unf[step]) < 2e-4
