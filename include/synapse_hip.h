@@ -584,6 +584,10 @@ syn_status_t syn_hip_eval_expf(const float *d_x, float *d_y, size_t n, void *str
  * HBM streaming read of `bytes` (best of 3 after a warm-up, GB/s). */
 syn_status_t syn_hip_probe_mfma(int kind, size_t iters, double *tflops);
 syn_status_t syn_hip_probe_hbm_read(size_t bytes, double *gb_s);
+/* The device's reference-order sequential sum of n <= 16384 host values:
+ * out3[0] = one lane's chain, out3[1] = the wave-cooperative chain of the
+ * Mamba norms, out3[2] = that chain's clocks (a check of the summation order). */
+syn_status_t syn_hip_probe_seq_sum(const float *host, size_t n, float *out3);
 /* SplitMix64 + Box-Muller (f64, cast to f32) into host memory. */
 syn_status_t syn_hip_fill_normal(float *host_dst, size_t n, uint64_t seed, float stddev);
 

@@ -130,7 +130,7 @@ __device__ float quantize_regs(const float (&v)[RB], int n, int8_t *q, float *re
 }
 
 // device address of the expf table (per device; resolved once)
-static const uint64_t *exp_table_address() {
+const uint64_t *exp_table_address() {
   static const uint64_t *addr[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
@@ -149,8 +149,17 @@ static const uint64_t *exp_table_address() {
 // quantize an f32 vector; PRO_SWIGLU: silu(gate) * up of GEMV rows, then
 // quantize; PRO_ROWS: quantize GEMV rows (RowSrc values); PRO_HQ: quantize
 // this split's K range of an f32 vector whose max |v| another kernel has
-// already reduced (hmax)
-enum { PRO_NORM = 0, PRO_QUANT = 1, PRO_SWIGLU = 2, PRO_MNORM = 3, PRO_ROWS = 4, PRO_HQ = 5 };
+// already reduced (hmax); PRO_CONV: the Mamba block's conv1d step + SiLU of
+// GEMV rows over a 4-tap ring state (int8_mamba.rs:43-56), then quantize
+enum {
+  PRO_NORM = 0,
+  PRO_QUANT = 1,
+  PRO_SWIGLU = 2,
+  PRO_MNORM = 3,
+  PRO_ROWS = 4,
+  PRO_HQ = 5,
+  PRO_CONV = 6
+};
 
 struct ProArgs {
   // PRO_NORM: x = (base ? base : embed[st->token]) + delta
@@ -168,11 +177,17 @@ struct ProArgs {
   const unsigned *hmax;
   // PRO_ROWS
   RowSrc rows;
-  // PRO_SWIGLU; exp_tab = device address of syn_exp2_tab, passed as a plain
+  // PRO_SWIGLU, PRO_CONV; exp_tab = device address of syn_exp2_tab, passed as a plain
   // pointer so its load is ordered like any other (a __constant__ load may be
   // moved behind the weight loads)
   RowSrc gu;
   const uint64_t *exp_tab;
+  // PRO_CONV: rows (the new inputs), ring [H][4] (slot p % 4 holds the input
+  // of position p), conv weights [H][4] and bias, conv_out = the conv + SiLU
+  // values (workgroup 0, with the new ring slot)
+  float *ring;
+  const float *conv_w, *conv_b;
+  float *conv_out;
   // all: prologue vector length (the GEMV's K) and the scale output
   int H;
   float *s_out;
@@ -251,7 +266,10 @@ __device__ float norm_quant(float eps, int H, const float (&x)[RB], const float 
   bar<NT>();
   float ss;
   if constexpr (SEQ) {
-    if (tid == 0) red[36] = seq_sum(sq, H);
+    if (tid < 64) {  // wave 0 runs the single chain
+      const float r = wave_seq_sum(sq, H, 0.0f);
+      if (tid == 0) red[36] = r;
+    }
     bar<NT>();
     ss = red[36];
   } else {
@@ -356,6 +374,49 @@ __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
 #pragma unroll
     for (int u = 0; u < RB; u++) x[u] = a.vec[min(tid + u * NT, H - 1)];
     issue_weights();
+  } else if constexpr (PRO == PRO_CONV) {
+    // expf's table to LDS first (a global lookup would wait behind the weights)
+    __shared__ uint64_t exp_tab[32];
+    const uint64_t tv = a.exp_tab[tid & 31];
+    int ra[RB];
+    float rw[RB];
+    float4 tp[RB], cw[RB];
+    float cb[RB];
+#pragma unroll
+    for (int u = 0; u < RB; u++) {
+      const int j = min(tid + u * NT, H - 1);
+      ra[u] = a.rows.acc[j];
+      rw[u] = a.rows.ws[j];
+      tp[u] = reinterpret_cast<const float4 *>(a.ring)[j];
+      cw[u] = reinterpret_cast<const float4 *>(a.conv_w)[j];
+      cb[u] = a.conv_b[j];
+    }
+    const float rsx = a.rows.sx[0];
+    const int pos = a.st->pos;
+    issue_weights();
+    if (tid < 32) exp_tab[tid] = tv;
+    bar<NT>();
+    // taps oldest to newest: slots (pos+1)%4, (pos+2)%4, (pos+3)%4, then the input
+    auto slot = [](const float4 &t, int k) {
+      return k == 0 ? t.x : k == 1 ? t.y : k == 2 ? t.z : t.w;
+    };
+    const int k0 = (pos + 1) & 3, k1 = (pos + 2) & 3, k2 = (pos + 3) & 3;
+#pragma unroll
+    for (int u = 0; u < RB; u++) {
+      const float f = (float)ra[u] * rsx;
+      const float xt = f * rw[u];
+      float sum = 0.0f, t;
+      t = slot(tp[u], k0) * cw[u].x;
+      sum = sum + t;
+      t = slot(tp[u], k1) * cw[u].y;
+      sum = sum + t;
+      t = slot(tp[u], k2) * cw[u].z;
+      sum = sum + t;
+      t = xt * cw[u].w;
+      sum = sum + t;
+      x[u] = syn_silu_tab(sum + cb[u], exp_tab);
+      nwv[u] = xt;  // the new ring entry, published by workgroup 0
+    }
   } else if constexpr (PRO == PRO_ROWS) {
     int ra[RB];
     float rw[RB];
@@ -447,6 +508,17 @@ __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
 #pragma unroll
         for (int u = 0; u < RB; u++)
           if (tid + u * NT < H) a.res_out[tid + u * NT] = x[u];
+      }
+    }
+    if constexpr (PRO == PRO_CONV) {
+      const int ps = a.st->pos & 3;
+#pragma unroll
+      for (int u = 0; u < RB; u++) {
+        const int j = tid + u * NT;
+        if (j < H) {
+          a.conv_out[j] = x[u];
+          a.ring[(size_t)j * 4 + ps] = nwv[u];
+        }
       }
     }
     if (tid == 0) a.s_out[0] = sv;
@@ -558,6 +630,30 @@ syn_status_t launch_fused_rows_gemv(RowSrc rows, int H, float *s_out, const Spli
   a.H = H;
   a.s_out = s_out;
   return launch_fused<PRO_ROWS>(a, g, s);
+}
+
+syn_status_t launch_fused_conv_gemv(RowSrc rows, const StepState *st, float *ring,
+                                    const float *conv_w, const float *conv_b, float *conv_out,
+                                    int H, float *s_out, const SplitGemv &g, hipStream_t s) {
+  ProArgs a{};
+  a.exp_tab = exp_table_address();
+  if (!a.exp_tab) {
+    set_error("fused decode: expf table address unavailable");
+    return SYN_ERR_HIP;
+  }
+  a.rows = rows;
+  a.st = st;
+  a.ring = ring;
+  a.conv_w = conv_w;
+  a.conv_b = conv_b;
+  a.conv_out = conv_out;
+  a.H = H;
+  a.s_out = s_out;
+  if (!rows.acc || !rows.ws || !rows.sx) {
+    set_error("fused conv GEMV: rows must be GEMV accumulators");
+    return SYN_ERR_INTERNAL;
+  }
+  return launch_fused<PRO_CONV>(a, g, s);
 }
 
 syn_status_t launch_fused_quant_gemv(const float *vec, int H, float *s_out, const SplitGemv &g,

@@ -66,6 +66,15 @@ syn_status_t launch_fused_norm_gemv(const float *base, const float *embed, const
 // xq = q8(rows[0..H)) of another split GEMV's rows ; s_out ; acc += xq . W
 syn_status_t launch_fused_rows_gemv(RowSrc rows, int H, float *s_out, const SplitGemv &g,
                                     hipStream_t s);
+// device address of the expf table syn_exp2_tab (per device), for kernels
+// that stage it in LDS
+const uint64_t *exp_table_address();
+// x = silu(conv1d step of rows over the 4-tap ring, weights conv_w [H][4],
+// bias conv_b) (int8_mamba.rs:43-56) ; xq = q8(x) ; s_out ; acc += xq . W;
+// workgroup 0 writes x to conv_out and rows to ring slot st->pos % 4
+syn_status_t launch_fused_conv_gemv(RowSrc rows, const StepState *st, float *ring,
+                                    const float *conv_w, const float *conv_b, float *conv_out,
+                                    int H, float *s_out, const SplitGemv &g, hipStream_t s);
 // xq = q8(vec) ; s_out ; acc += xq . W
 syn_status_t launch_fused_quant_gemv(const float *vec, int H, float *s_out, const SplitGemv &g,
                                      hipStream_t s);

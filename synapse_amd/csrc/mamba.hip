@@ -6,10 +6,11 @@
 // one small kernel each.  With `int8_xdt` set, x_proj and dt_proj are INT8
 // W8A8 as well (BASELINE config 5's variant; no reference counterpart).
 //
-// Float order follows the reference everywhere except softplus's log: the
-// reference calls glibc logf, whose last bit differs from a correctly rounded
-// log on ~7% of inputs in [1, 1.1); the device computes log in double and
-// rounds once, so this path is held to the float tolerance, not bit equality.
+// The op-by-op step's float order follows the reference everywhere except
+// softplus's log: the reference calls glibc logf, whose last bit differs from
+// a correctly rounded log on ~7% of inputs in [1, 1.1); the device computes
+// log in double and rounds once, so this path is held to the float tolerance,
+// not bit equality.
 #include <algorithm>
 #include <thread>
 #include <vector>
@@ -17,6 +18,7 @@
 #include "decode_fused.hpp"
 #include "layer_ops.hpp"
 #include "linear.hpp"
+#include "reduce_order.hpp"
 
 using namespace syn;
 
@@ -42,24 +44,12 @@ __global__ void __launch_bounds__(256)
   }
   __syncthreads();
   // one sequential sum of the rounded squares; the squares are formed in
-  // parallel first, then lane 0 adds them in index order with 16-byte reads
+  // parallel first, then wave 0 adds them in index order (wave_seq_sum)
   for (int j = threadIdx.x; j < H; j += blockDim.x) sq[j] = sm[j] * sm[j];
   __syncthreads();
-  if (threadIdx.x == 0) {
-    float s = 0.0f;
-    int i = 0;
-    for (; i + 16 <= H; i += 16) {
-      const float4 a = *reinterpret_cast<const float4 *>(sq + i);
-      const float4 b = *reinterpret_cast<const float4 *>(sq + i + 4);
-      const float4 c = *reinterpret_cast<const float4 *>(sq + i + 8);
-      const float4 d = *reinterpret_cast<const float4 *>(sq + i + 12);
-      s = s + a.x; s = s + a.y; s = s + a.z; s = s + a.w;
-      s = s + b.x; s = s + b.y; s = s + b.z; s = s + b.w;
-      s = s + c.x; s = s + c.y; s = s + c.z; s = s + c.w;
-      s = s + d.x; s = s + d.y; s = s + d.z; s = s + d.w;
-    }
-    for (; i < H; i++) s = s + sq[i];
-    s_scale = 1.0f / sqrtf(s / (float)H + eps);
+  if (threadIdx.x < 64) {
+    const float s = wave_seq_sum(sq, H, 0.0f);
+    if (threadIdx.x == 0) s_scale = 1.0f / sqrtf(s / (float)H + eps);
   }
   __syncthreads();
   const float scale = s_scale;
@@ -92,21 +82,27 @@ __global__ void __launch_bounds__(256)
   if (threadIdx.x == 0) *sx = mx / 127.0f;
 }
 
-// conv1d_step (int8_mamba.rs:43-56) + SiLU, one thread per channel
+// conv1d_step (int8_mamba.rs:43-56) + SiLU, one thread per channel.  The
+// state is a ring of dc inputs per channel: slot p % dc holds the input of
+// position p (so a step writes only the slot of its own position, which no
+// reader of the step needs); the taps run oldest to newest as the
+// reference's shifted buffer.
 __global__ void k_mamba_conv(RowSrc proj, float *__restrict__ conv_state,
                              const float *__restrict__ cw, const float *__restrict__ cb, int di,
-                             int dc, float *__restrict__ xc) {
+                             int dc, const StepState *__restrict__ st, float *__restrict__ xc) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= di) return;
+  const int pos = st->pos;
   float *buf = conv_state + (size_t)i * dc;
-  for (int k = 0; k + 1 < dc; k++) buf[k] = buf[k + 1];
-  buf[dc - 1] = row_value(proj, i);
+  const float xt = row_value(proj, i);
   const float *wr = cw + (size_t)i * dc;
   float sum = 0.0f;
   for (int k = 0; k < dc; k++) {
-    const float t = buf[k] * wr[k];
+    const float v = k + 1 < dc ? buf[(pos + 1 + k) % dc] : xt;
+    const float t = v * wr[k];
     sum = sum + t;
   }
+  buf[pos % dc] = xt;
   xc[i] = syn_silu(sum + cb[i]);
 }
 
@@ -239,14 +235,20 @@ __device__ __forceinline__ float syn_softplus(float v) {  // ops/activation.rs:8
   const float t = 1.0f + syn_expf(v);
   return (float)log((double)t);
 }
+__device__ __forceinline__ float syn_softplus_tab(float v, const uint64_t *tab) {
+  if (v > 20.0f) return v;
+  const float t = 1.0f + syn_expf_tab(v, tab);
+  return (float)log((double)t);
+}
 
 // dt_proj (f32 chain over dt_rank, or taken from the INT8 variant's GEMV),
 // softplus, selective scan step and the SiLU(z) gate; one lane per channel,
-// one wave per workgroup.  The per-channel parameters and the state are
-// stored channel-minor ([j][d_inner]: element (i, j) at j*d_inner + i), so
-// every load and store of a wave is 256 contiguous bytes; all of a lane's
-// loads are requested at entry (up to DR dt_proj weights and DS state and
-// A_log values in registers; DR = 0 streams longer dt_proj rows).
+// one wave per workgroup.  The per-channel parameters are stored
+// channel-minor ([j][d_inner]: element (i, j) at j*d_inner + i), so every
+// load of a wave is 256 contiguous bytes; the state is channel-major
+// ([d_inner][d_state], shared with k_mamba_dtscan).  All of a lane's loads
+// are requested at entry (up to DR dt_proj weights and DS state and A_log
+// values in registers; DR = 0 streams longer dt_proj rows).
 // x_proj's output (dt_rank + 2*d_state values, the same for every channel)
 // is staged in LDS.
 constexpr int kScanDs = 16, kScanDr = 64;
@@ -270,7 +272,7 @@ __global__ void __launch_bounds__(64)
 #pragma unroll
   for (int j = 0; j < DS; j++) {
     al[j] = alT[(size_t)min(j, ds - 1) * di + i];
-    hs[j] = hT[(size_t)min(j, ds - 1) * di + i];
+    hs[j] = hT[(size_t)i * ds + min(j, ds - 1)];
   }
   const float dtbi = dtb[i], xi = xc[i], dpi = dparam[i];
   const float zi = row_value_t<ZACC>(z, i);
@@ -338,9 +340,106 @@ __global__ void __launch_bounds__(64)
   if (i0 >= di) return;
 #pragma unroll
   for (int j = 0; j < DS; j++)
-    if (j < ds) hT[(size_t)j * di + i] = hs[j];
+    if (j < ds) hT[(size_t)i * ds + j] = hs[j];
   const float y = yi + dpi * xi;
   gated[i] = syn_silu(zi) * y;  // int8_mamba.rs:102
+}
+
+// Fused step of the INT8 x_proj / dt_proj variant: dt_proj (W8A8 over the
+// A1-quantized dt rows of x_proj), softplus, the selective-scan step
+// (selective_scan.zig:30-90) and the SiLU(z) gate, with 16 lanes per channel
+// (lane = state).  The dt_proj dot product is split 4 bytes per lane and
+// summed exactly (int32) across the 16-lane row; the sum over states follows
+// the reference (each group of 4 summed in order, then the groups in order)
+// through lane moves, so the results are k_mamba_scan's.  Every workgroup
+// re-forms x_proj's rows and their quantization (dr + 2*ds values).
+// d_state = 16; grid ceil(di / 16), 256 threads.
+// sums over the lane's row of 16 lanes (DPP: xor 1, xor 2, mirror in 8,
+// mirror in 16), the result in every lane of the row
+__device__ __forceinline__ int row16_isum(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xf, 0xf, false);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xf, 0xf, false);
+  return v;
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+}
+// the scan's y over 16 states, one per lane of a 16-lane row, in
+// selective_scan.zig's order: y = 0 + (((c0+c1)+c2)+c3) + (((c4+c5)+c6)+c7) + ...
+__device__ __forceinline__ float row16_scan_sum(float c, int lane) {
+  // each quad's ordered sum, in every lane of the quad (quad_perm broadcasts)
+  const float q = ((dpp_f<0x00>(c) + dpp_f<0x55>(c)) + dpp_f<0xAA>(c)) + dpp_f<0xFF>(c);
+  // the four quads of the row, in order
+  const int base = lane & ~15;
+  const float q0 = __shfl(q, base), q1 = __shfl(q, base + 4), q2 = __shfl(q, base + 8),
+              q3 = __shfl(q, base + 12);
+  return (((0.0f + q0) + q1) + q2) + q3;
+}
+
+__global__ void __launch_bounds__(256)
+    k_mamba_dtscan(RowSrc xps, int dr, int ds, const int *__restrict__ Wdt, int Cdt,
+                   const float *__restrict__ wsdt, const float *__restrict__ dtb,
+                   const float *__restrict__ alc, const float *__restrict__ dparam,
+                   const float *__restrict__ xc, RowSrc z, float *__restrict__ hc, int di,
+                   const uint64_t *__restrict__ exp_tab_g, float *__restrict__ gated) {
+  __shared__ float xpf[kScanDr + 2 * kScanDs];
+  __shared__ int xq4[kScanDr / 4];
+  __shared__ float s_q;
+  __shared__ uint64_t exp_tab[32];  // expf's table in LDS: lookups without memory waits
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int sidx = lane & 15;                   // state, and dt_proj k-group
+  const int c = blockIdx.x * 16 + (tid >> 4);   // channel
+  const int ci = min(c, di - 1);
+  const int sj = min(sidx, ds - 1);
+  // every load first: dt_proj's 4 weight bytes (row c, k = 4*sidx..), the
+  // channel's parameters and state, x_proj's rows
+  const bool wlane = (sidx >> 2) < Cdt;
+  const int wdw = wlane ? Wdt[(((size_t)(ci >> 6) * Cdt + (sidx >> 2)) * 64 + (ci & 63)) * 4 +
+                              (sidx & 3)]
+                        : 0;
+  const float al = alc[(size_t)ci * ds + sj];
+  const float h0 = hc[(size_t)ci * ds + sj];
+  const float wsc = wsdt[ci], dtbi = dtb[ci], xi = xc[ci], dpi = dparam[ci];
+  const float zi = row_value_t<true>(z, ci);
+  const int nxp = dr + 2 * ds;
+  if (tid < 32) exp_tab[tid] = exp_tab_g[tid];
+  for (int k = tid; k < nxp; k += 256) xpf[k] = row_value_t<true>(xps, k);
+  __syncthreads();
+  // A1 quantization of the dt rows (quantize.zig:12-47), one wave
+  if (tid < 64) {
+    const float v = tid < dr ? xpf[tid] : 0.0f;
+    float mx = fabsf(v);
+    for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    int8_t q = 0;
+    if (mx != 0.0f && tid < dr) {
+      float r = roundf(v * (127.0f / mx));
+      r = fminf(127.0f, fmaxf(-127.0f, r));
+      q = (int8_t)(int)r;
+    }
+    reinterpret_cast<int8_t *>(xq4)[tid] = q;
+    if (tid == 0) s_q = mx == 0.0f ? 1.0f : mx / 127.0f;
+  }
+  __syncthreads();
+  // dt_proj row c: exact int32 dot over the row's 16 lanes, the GEMV epilogue
+  // (f32(acc) * sx) * sw, then softplus
+  const int part = wlane ? __builtin_amdgcn_sdot4(wdw, xq4[sidx], 0, false) : 0;
+  const int acc = row16_isum(part);
+  const float dtf = (float)acc * s_q;
+  const float dt = syn_softplus_tab(dtf * wsc + dtbi, exp_tab);
+  // scan step of state sidx
+  const bool live = sidx < ds;  // all 16 (the launcher requires d_state = 16)
+  const float b = xpf[dr + sj], cc = xpf[dr + ds + sj];
+  const float e = syn_expf_tab(al, exp_tab);
+  const float ad = syn_expf_tab(-dt * e, exp_tab);
+  const float p1 = ad * h0, p2 = (dt * xi) * b;
+  const float hn = p1 + p2;
+  const float y = row16_scan_sum(cc * hn, lane);
+  if (c >= di) return;
+  if (live) hc[(size_t)c * ds + sidx] = hn;
+  if (sidx == 0) gated[c] = syn_silu_tab(zi, exp_tab) * (y + dpi * xi);  // int8_mamba.rs:102
 }
 
 // [n,k] -> [panel][k/4][64][4] (k padded with zeros to a multiple of 4)
@@ -374,7 +473,8 @@ struct syn_hip_mamba_s {
   struct Block {
     QLinearInt8 in_proj, out_proj, x_i8, dt_i8;
     DevBuf conv_w, conv_b, xproj_p, dtproj, dt_bias, a_log, dparam, norm_w;
-    SplitGemv f_in, f_out, f_x, f_dt;  // fused step: split-K plans + accumulators
+    DevBuf a_log_cm;  // a_log channel-major [d_inner][d_state] (k_mamba_dtscan)
+    SplitGemv f_in, f_out, f_x;  // fused step: split-K plans + accumulators
   };
   std::vector<Block> blk;
   DevBuf embed, lm_p, final_norm, conv_state, ssm_state;
@@ -448,11 +548,31 @@ struct syn_hip_mamba_s {
     SYN_LAUNCH_CHECK();
     return SYN_OK;
   }
+  // fused INT8 x/dt variant: dt_proj + softplus + scan + gate (k_mamba_dtscan)
+  syn_status_t launch_dtscan(size_t l, RowSrc xps, RowSrc z, hipStream_t s) {
+    Block &B = blk[l];
+    if (dr > (size_t)kScanDr || ds != (size_t)kScanDs) {
+      set_error("mamba dt/scan: dt_rank above 64 or d_state other than 16");
+      return SYN_ERR_INVALID_ARG;
+    }
+    const uint64_t *exp_tab = exp_table_address();
+    if (!exp_tab) {
+      set_error("mamba dt/scan: expf table address unavailable");
+      return SYN_ERR_HIP;
+    }
+    hipLaunchKernelGGL(k_mamba_dtscan, dim3((unsigned)cdiv(di, 16)), dim3(256), 0, s, xps, (int)dr,
+                       (int)ds, reinterpret_cast<const int *>(B.dt_i8.w.p), B.dt_i8.chunks,
+                       B.dt_i8.scales.as<float>(), B.dt_bias.as<float>(),
+                       B.a_log_cm.as<float>(), B.dparam.as<float>(), xc.as<float>(), z,
+                       ssm_state.as<float>() + l * di * ds, (int)di, exp_tab, g.as<float>());
+    SYN_LAUNCH_CHECK();
+    return SYN_OK;
+  }
   syn_status_t launch_conv(size_t l, RowSrc proj_x, hipStream_t s) {
     Block &B = blk[l];
     hipLaunchKernelGGL(k_mamba_conv, dim3(cdiv(di, 256)), dim3(256), 0, s, proj_x,
                        conv_state.as<float>() + l * di * dc, B.conv_w.as<float>(),
-                       B.conv_b.as<float>(), (int)di, (int)dc, xc.as<float>());
+                       B.conv_b.as<float>(), (int)di, (int)dc, st(), xc.as<float>());
     SYN_LAUNCH_CHECK();
     return SYN_OK;
   }
@@ -506,8 +626,11 @@ struct syn_hip_mamba_s {
 
   // Fused step: each INT8 GEMV is a split-K kernel whose prologue forms its
   // own input (decode_fused.hip): [residual + norm + q8 ; in_proj], conv,
-  // [q8 ; x_proj] (or the exact f32 x_proj), [q8 of x_proj rows ; dt_proj],
-  // scan, [q8 ; out_proj].  The same float operations as step_unfused.
+  // [q8 ; x_proj] (or the exact f32 x_proj), then for the INT8 x/dt variant
+  // [q8 of x_proj's dt rows ; dt_proj ; softplus ; scan] in one kernel
+  // (k_mamba_dtscan), else the scan, and [q8 ; out_proj].  The same float
+  // operations as step_unfused: the INT8 activation quantization makes the
+  // model's outputs sensitive to any change of summation order.
   syn_status_t prepare_fused() {
     int cus = 256, dev = 0;
     if (hipGetDevice(&dev) == hipSuccess)
@@ -520,19 +643,18 @@ struct syn_hip_mamba_s {
                                 B.out_proj.chunks, cus, 256);
       per_layer = (size_t)B.f_in.N64 + B.f_out.N64;
       if (c.int8_xdt) {
+        // every workgroup of x_proj forms the conv of all channels: few of them
         B.f_x = plan_split_gemv(B.x_i8.w.p, B.x_i8.scales.as<float>(), (int)nx, B.x_i8.chunks,
-                                cus, 256);
-        B.f_dt = plan_split_gemv(B.dt_i8.w.p, B.dt_i8.scales.as<float>(), (int)di,
-                                 B.dt_i8.chunks, cus, 256);
-        per_layer += (size_t)B.f_x.N64 + B.f_dt.N64;
+                                32, 256);
+        per_layer += (size_t)B.f_x.N64;
       }
     }
     acc_elems = per_layer * L;
     SYN_TRY(acc.alloc(acc_elems * 4));
     int *p = acc.as<int>();
     for (auto &B : blk) {
-      SplitGemv *gs[4] = {&B.f_in, &B.f_out, &B.f_x, &B.f_dt};
-      for (int i = 0; i < (c.int8_xdt ? 4 : 2); i++) {
+      SplitGemv *gs[3] = {&B.f_in, &B.f_out, &B.f_x};
+      for (int i = 0; i < (c.int8_xdt ? 3 : 2); i++) {
         gs[i]->acc = p;
         p += gs[i]->N64;
       }
@@ -545,12 +667,13 @@ struct syn_hip_mamba_s {
   }
 
   bool fused_supported() const {
-    return fused_gemv_fits((int)dm) && fused_gemv_fits((int)di) && fused_gemv_fits((int)dr);
+    return fused_gemv_fits((int)dm) && fused_gemv_fits((int)di) && fused_gemv_fits((int)dr) &&
+           (!c.int8_xdt || (ds == (size_t)kScanDs && dr <= (size_t)kScanDr && dc == 4));
   }
 
   syn_status_t step_fused(hipStream_t s) {
     float *sc = scal.as<float>();
-    float *s_in = sc + 0, *s_x = sc + 1, *s_dt = sc + 2, *s_out = sc + 3;
+    float *s_in = sc + 0, *s_x = sc + 1, *s_out = sc + 3;
     float *xr[2] = {xres.as<float>(), xres.as<float>() + dm};
     SYN_TRY(launch_zero_i32(acc.as<int>(), acc_elems, s));
     for (size_t l = 0; l < L; l++) {
@@ -561,19 +684,18 @@ struct syn_hip_mamba_s {
                                      B.norm_w.as<float>(), c.eps, (int)dm, s_in, B.f_in, s,
                                      /*sequential_sumsq=*/true));
       const RowSrc proj_rows = B.f_in.rows(s_in);
-      SYN_TRY(launch_conv(l, proj_rows, s));
-      RowSrc xps, dtps;
-      if (c.int8_xdt) {
-        SYN_TRY(launch_fused_quant_gemv(xc.as<float>(), (int)di, s_x, B.f_x, s));
-        xps = B.f_x.rows(s_x);
-        SYN_TRY(launch_fused_rows_gemv(xps, (int)dr, s_dt, B.f_dt, s));
-        dtps = B.f_dt.rows(s_dt);
+      if (c.int8_xdt) {  // [conv ; q8 ; x_proj], then [dt_proj ; scan]
+        SYN_TRY(launch_fused_conv_gemv(proj_rows, st(), conv_state.as<float>() + l * di * dc,
+                                       B.conv_w.as<float>(), B.conv_b.as<float>(),
+                                       xc.as<float>(), (int)di, s_x, B.f_x, s));
+        SYN_TRY(launch_dtscan(l, B.f_x.rows(s_x), offset_rows(proj_rows, di), s));
       } else {
+        SYN_TRY(launch_conv(l, proj_rows, s));
         SYN_TRY(launch_gemv_f32_exact(B.xproj_p.as<float>(), xc.as<float>(), xc.bytes / 4,
                                       (int)nx, (int)di, n8_of((int)nx), xp.as<float>(), s));
-        xps = f32_rows(xp.as<float>());
+        SYN_TRY(launch_scan(l, f32_rows(xp.as<float>()), RowSrc{}, offset_rows(proj_rows, di),
+                            s));
       }
-      SYN_TRY(launch_scan(l, xps, dtps, offset_rows(proj_rows, di), s));
       SYN_TRY(launch_fused_quant_gemv(g.as<float>(), (int)di, s_out, B.f_out, s));
     }
     return head(xr[(L - 1) & 1], blk[L - 1].f_out.rows(s_out), s);
@@ -716,6 +838,7 @@ syn_status_t syn_hip_mamba_init_synthetic(syn_hip_mamba_t *m, uint64_t seed_base
     for (size_t i = 0; i < di; i++)
       for (size_t s2 = 0; s2 < ds; s2++) al[i * ds + s2] = logf((float)(s2 + 1));
     SYN_TRY(up(B.a_log, channel_minor(al.data(), di, ds)));
+    SYN_TRY(up(B.a_log_cm, al));
     SYN_TRY(up(B.dparam, std::vector<float>(di, 1.0f)));
     SYN_TRY(up(B.norm_w, std::vector<float>(dm, 1.0f)));
     SYN_TRY(B.in_proj.prepare(1));

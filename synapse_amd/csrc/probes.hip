@@ -3,6 +3,7 @@
 // streaming read.  The roofline fractions the benchmark reports use the
 // published peaks; these give the measured ceilings beside them.
 #include "common.hpp"
+#include "reduce_order.hpp"
 
 namespace syn {
 
@@ -109,9 +110,41 @@ __global__ void __launch_bounds__(256) k_probe_read(const i32x4 *__restrict__ p,
   if ((s.x ^ s.y ^ s.z ^ s.w) == 0x5eed5eed) out[blockIdx.x] = 1;
 }
 
+// the reference-order sequential sums of n values: out[0] one lane's chain
+// (seq_sum), out[1] the wave-cooperative chain (wave_seq_sum); out[2] the
+// clocks of the wave chain
+__global__ void __launch_bounds__(64) k_probe_seq_sum(const float *v, int n, float *out) {
+  extern __shared__ __align__(16) float sv[];
+  for (int j = threadIdx.x; j < ((n + 3) & ~3); j += 64) sv[j] = j < n ? v[j] : 0.0f;
+  __syncthreads();
+  const unsigned long long t0 = __builtin_amdgcn_s_memtime();
+  const float w = wave_seq_sum(sv, n, 0.0f);
+  const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+  if (threadIdx.x == 0) {
+    out[0] = seq_sum(sv, n);
+    out[1] = w;
+    out[2] = (float)(t1 - t0);
+  }
+}
+
 }  // namespace syn
 
 using namespace syn;
+
+extern "C" syn_status_t syn_hip_probe_seq_sum(const float *host, size_t n, float *out3) {
+  if (!host || !out3) return SYN_ERR_NULL_PTR;
+  if (n == 0 || n > 16384) return SYN_ERR_INVALID_ARG;
+  SYN_TRY(ensure_init());
+  DevBuf dv, dout;
+  SYN_TRY(dv.alloc(n * 4));
+  SYN_TRY(dout.alloc(16));
+  SYN_HIP(hipMemcpy(dv.p, host, n * 4, hipMemcpyHostToDevice));
+  hipLaunchKernelGGL(k_probe_seq_sum, dim3(1), dim3(64), ((n + 3) & ~(size_t)3) * 4, 0,
+                     dv.as<float>(), (int)n, dout.as<float>());
+  SYN_LAUNCH_CHECK();
+  SYN_HIP(hipMemcpy(out3, dout.p, 12, hipMemcpyDeviceToHost));
+  return SYN_OK;
+}
 
 extern "C" syn_status_t syn_hip_probe_mfma(int kind, size_t iters, double *tflops) {
   if (!tflops) return SYN_ERR_NULL_PTR;

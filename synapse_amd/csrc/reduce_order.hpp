@@ -134,6 +134,57 @@ __device__ float sumsq_lds(const float *v, int n, float *sq, float *red) {
   return sumsq_chains<NT>(sq, n, red);
 }
 
+// acc0 + v[0] + ... + v[n-1] one at a time in index order, run by a whole
+// wave (v in LDS, 16-byte aligned, readable up to round_up4(n)).  Lane l
+// holds v[16l .. 16l+16) of each 1024-value pass in registers; the running sum visits the lanes in order:
+// lane l adds its 16 values, then a DPP wave_ror:1 hands the sum to lane l+1
+// (lane 63 to lane 0 for the next pass).  Every add is one dependent VALU
+// op of the wave (the other lanes' sums are discarded), so the chain runs
+// at the register rate with no memory access inside it.  Values at index
+// >= n are skipped by a select.  Returns the sum in every lane.
+__device__ __forceinline__ float wave_seq_sum(const float *v, int n, float acc0) {
+  const int lane = threadIdx.x & 63;
+  float acc = acc0;
+  auto rot = [](float x) {  // lane l+1 <- lane l, lane 0 <- lane 63
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x13C, 0xf, 0xf,
+                                                      false));
+  };
+  for (int base = 0; base < n; base += 1024) {
+    f32x4 r[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int j = min(base + 16 * lane + 4 * k, (n - 1) & ~3);  // in bounds; unused past n
+      r[k] = *reinterpret_cast<const f32x4 *>(v + j);
+    }
+    pin_regs(r);
+    const int left = min(n - base, 1024), full = left >> 4;
+    for (int l = 0; l < full; l++) {  // turns of 16 values
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        acc = acc + r[k].x;
+        acc = acc + r[k].y;
+        acc = acc + r[k].z;
+        acc = acc + r[k].w;
+      }
+      acc = rot(acc);
+    }
+    if (left & 15) {  // the last, partial turn
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const float c[4] = {r[k].x, r[k].y, r[k].z, r[k].w};
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          if (4 * k + i < (left & 15)) acc = acc + c[i];
+      }
+      acc = rot(acc);
+    }
+    // the pass's sum now sits in the lane after its last turn
+    const int turns = (left + 15) >> 4;
+    acc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), turns & 63));
+  }
+  return acc;
+}
+
 // Sequential sum of v[0..n) (a single accumulator, in index order).
 __device__ __forceinline__ float seq_sum(const float *v, int n) {
   if ((reinterpret_cast<uintptr_t>(v) & 15) == 0) return lds_seq_sum(v, n, 0.0f);

@@ -175,6 +175,7 @@ SIGNATURES = {
     "syn_hip_fill_normal": (ST, [P, SZ, C.c_uint64, C.c_float]),
     "syn_hip_probe_mfma": (ST, [C.c_int, SZ, C.POINTER(C.c_double)]),
     "syn_hip_probe_hbm_read": (ST, [SZ, C.POINTER(C.c_double)]),
+    "syn_hip_probe_seq_sum": (ST, [P, SZ, P]),
     "syn_hip_eval_expf": (ST, [P, P, SZ, P]),
     "syn_hip_kquant_encode": (ST, [C.c_int, SZ, SZ, P, P]),
     "syn_hip_kquant_decode": (ST, [C.c_int, SZ, P, P]),
@@ -1040,6 +1041,15 @@ def probe_mfma(kind: int, iters: int = 20000) -> float:
     v = C.c_double()
     check(lib().syn_hip_probe_mfma(kind, iters, C.byref(v)), "probe_mfma")
     return v.value
+
+
+def probe_seq_sum(values):
+    """(one-lane chain, wave chain, wave-chain clocks) of the device's
+    reference-order sequential sum of `values` (float32)."""
+    v = np.ascontiguousarray(values, np.float32)
+    out = np.zeros(3, np.float32)
+    check(lib().syn_hip_probe_seq_sum(ptr(v), v.size, ptr(out)), "probe_seq_sum")
+    return float(out[0]), float(out[1]), float(out[2])
 
 
 def probe_hbm_read(nbytes: int = 4 << 30) -> float:

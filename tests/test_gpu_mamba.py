@@ -109,3 +109,21 @@ def test_fused_step_matches_unfused(cfg, xdt):
         np.testing.assert_array_equal(toks, ref[1], err_msg=f"fused,graph={key}")
         np.testing.assert_array_equal(_bits(margins), _bits(ref[2]), err_msg=f"fused,graph={key}")
     g.close()
+
+
+@pytest.mark.parametrize("n", [1, 3, 15, 16, 17, 64, 1000, 1024, 1025, 2048, 3000])
+def test_sequential_sum_order(n):
+    # the Mamba norms' sum of squares is one sequential float32 chain
+    # (pure_rust_ops.rs:96-112); the device's one-lane and wave-cooperative
+    # chains must both equal it bit for bit (numpy's float32 accumulate adds
+    # one element at a time).  Values of mixed magnitude make a wrong order
+    # show in the last bits.
+    rng = np.random.default_rng(n)
+    v = (rng.standard_normal(n) * np.exp(rng.uniform(-8, 8, n))).astype(np.float32) ** 2
+    want = np.add.accumulate(v, dtype=np.float32)[-1]
+    lane, wave, clk = hip.probe_seq_sum(v)
+    assert np.float32(lane).view(np.uint32) == want.view(np.uint32), (lane, want)
+    assert np.float32(wave).view(np.uint32) == want.view(np.uint32), (wave, want)
+    tree = np.float32(np.sum(v, dtype=np.float32))  # numpy's pairwise order
+    if n >= 64:
+        print(n, "wave chain clocks", clk, "pairwise differs:", tree != want)
