@@ -68,6 +68,10 @@ __device__ __forceinline__ void pg_load_w(RawW &r, const u32x4 *__restrict__ W,
     const size_t blk = (size_t)min(2 * step + (q >> 1), B - 1);
     r.q0 = W[((panel * B + blk) * 2 + (q & 1)) * 64 + rp];
     r.d = Wd[(panel * B + blk) * 64 + rp];
+  } else if (FMT == SYN_HIP_FMT_Q4_0) {  // block 2*step + q/2 (clamped), its one nibble plane
+    const size_t blk = (size_t)min(2 * step + (q >> 1), B - 1);
+    r.q0 = W[(panel * B + blk) * 64 + rp];
+    r.d = Wd[(panel * B + blk) * 64 + rp];
   } else if (FMT == SYN_HIP_FMT_Q4_K) {  // sub-block 2*(step%4) + q/2, nibble bytes 8*(q%2)..+7
     const size_t sb = (size_t)(step >> 2);
     const int sub = 2 * (step & 3) + (q >> 1);
@@ -121,6 +125,27 @@ __device__ __forceinline__ void pg_decode_w(const RawW &r, int step, int q, int 
           v[h] = (_Float16)(d * (float)(int8_t)(w >> (8 * (e & 3))));  // gguf.rs:283
         }
         out[i] = __builtin_bit_cast(uint32_t, v);
+      }
+    }
+  } else if (FMT == SYN_HIP_FMT_Q4_0) {
+    // Q4Linear blocks (q4_linear.rs:64-121): element 2i = low nibble of byte
+    // i, 2i+1 = high; value = (nibble - 8) * d.  nibble - 8 and d are exact
+    // f16 values, so one f16 multiply rounds the exact product once.  The
+    // pair (1024 + lo, 1024 + hi) of byte i comes from a byte permute.
+    const bool valid = 2 * step + (q >> 1) < B;
+    const _Float16 dh = valid ? __builtin_bit_cast(_Float16, (uint16_t)r.d) : (_Float16)0.0f;
+    const f16x2 dd = f16x2{dh, dh}, bias = f16x2{(_Float16)-1032.0f, (_Float16)-1032.0f};
+#pragma unroll
+    for (int w = 0; w < 2; w++) {
+      const uint32_t v = u32x4_word(r.q0, 2 * (q & 1) + w);
+      const uint32_t lo = v & 0x0f0f0f0fu, hi = (v >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+      for (int b = 0; b < 4; b++) {
+        // bytes: lo.b, 0, hi.b, 0 -> halfs 0x64 lo.b, 0x64 hi.b
+        const uint32_t sel = (uint32_t)b | (0x0cu << 8) | ((uint32_t)(4 + b) << 16) | (0x0cu << 24);
+        const uint32_t pr = __builtin_amdgcn_perm(hi, lo, sel) | 0x64006400u;
+        const f16x2 val = (__builtin_bit_cast(f16x2, pr) + bias) * dd;
+        out[4 * w + b] = __builtin_bit_cast(uint32_t, val);
       }
     }
   } else if (FMT == SYN_HIP_FMT_Q4_K) {
@@ -361,6 +386,11 @@ struct WBundle<SYN_HIP_FMT_Q8_0> {  // blocks 2s, 2s+1: planes 0, 1 and scales
   uint32_t d[2];  // the dword holding the row's f16 scale (half rp % 2)
 };
 template <>
+struct WBundle<SYN_HIP_FMT_Q4_0> {  // blocks 2s, 2s+1: their nibble planes and scales
+  u32x4 pl[2];
+  uint32_t d[2];  // the dword holding the row's f16 scale (half rp % 2)
+};
+template <>
 struct WBundle<SYN_HIP_FMT_Q4_K> {  // scale plane, sub-block planes 2(s%4), 2(s%4)+1
   u32x4 sc, pl[2];
 };
@@ -387,6 +417,13 @@ __device__ __forceinline__ void pg_fetch_w(WBundle<FMT> &w, const u32x4 *__restr
       w.pl[2 * h + 1] = W[((panel * B + blk) * 2 + 1) * 64 + rp];
       w.d[h] = Wd32[((panel * B + blk) * 64 + rp) >> 1];
     }
+  } else if constexpr (FMT == SYN_HIP_FMT_Q4_0) {
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      const size_t blk = (size_t)min(2 * step + h, B - 1);
+      w.pl[h] = W[(panel * B + blk) * 64 + rp];
+      w.d[h] = Wd32[((panel * B + blk) * 64 + rp) >> 1];
+    }
   } else if constexpr (FMT == SYN_HIP_FMT_Q4_K) {
     const size_t sb = (size_t)(step >> 2);
     const int sub = 2 * (step & 3);
@@ -410,6 +447,9 @@ __device__ __forceinline__ RawW pg_quarter(const WBundle<FMT> &w, int q, bool od
   RawW r;
   if constexpr (FMT == SYN_HIP_FMT_Q8_0) {
     r.q0 = w.pl[q];
+    r.d = odd ? w.d[q >> 1] >> 16 : w.d[q >> 1] & 0xffffu;
+  } else if constexpr (FMT == SYN_HIP_FMT_Q4_0) {
+    r.q0 = w.pl[q >> 1];
     r.d = odd ? w.d[q >> 1] >> 16 : w.d[q >> 1] & 0xffffu;
   } else if constexpr (FMT == SYN_HIP_FMT_Q4_K) {
     r.q0 = w.sc;
@@ -548,8 +588,10 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-syn_status_t QLinearKQ::gemm(size_t m, const float *d_x, size_t ldx, float *d_y, size_t ldy,
-                             hipStream_t s) {
+// f32 activation rows -> zero-padded f16 rows of ldh = round_up(k, PGK)
+// halfs in xh (grown on demand)
+static syn_status_t to_f16_rows(size_t m, size_t k, const float *d_x, size_t ldx, DevBuf &xh,
+                                size_t &xh_elems, hipStream_t s) {
   if (ldx % 4) {
     set_error("GEMM activation stride must be a multiple of 4 floats");
     return SYN_ERR_SHAPE_MISMATCH;
@@ -564,10 +606,16 @@ syn_status_t QLinearKQ::gemm(size_t m, const float *d_x, size_t ldx, float *d_y,
   hipLaunchKernelGGL(k_f32_to_f16, dim3(cdiv(total, 256)), dim3(256), 0, s, d_x, (int)ldx,
                      xh.as<_Float16>(), (int)ldh, (int)m, (int)k);
   SYN_LAUNCH_CHECK();
-  const bool exact = fmt != SYN_HIP_FMT_Q8_0 || q8_scales_f16_exact;
-  const u32x4 *W = wq.as<u32x4>();
-  const uint16_t *Wd = wd.as<uint16_t>();
-  const _Float16 *X = xh.as<_Float16>();
+  return SYN_OK;
+}
+
+// Y[m, n] = Xh[m, k] W^T for a weight matrix of format fmt in the plane
+// layout (W, Wd, B blocks per row); exact: the weights decode with f16
+// products (see pg_decode_w)
+static syn_status_t kq_gemm_f16(int fmt, bool exact, const u32x4 *W, const uint16_t *Wd,
+                                int blocks, size_t n, size_t k, const _Float16 *X, size_t m,
+                                float *d_y, size_t ldy, hipStream_t s) {
+  const size_t ldh = round_up(k, PGK);
   const int steps = (int)cdiv(k, PGK);
   // Enough 256 x 256 tiles for three quarters of the CUs: the four-wave
   // kernel, one K pass per tile.  Fewer: 256 x 128 tiles (twice as many),
@@ -583,7 +631,8 @@ syn_status_t QLinearKQ::gemm(size_t m, const float *d_x, size_t ldx, float *d_y,
     // Y accumulates the splits' partial tiles; a kernel (not a memset node)
     // clears it so the call can sit in a captured graph
     if (ldy % 4 || reinterpret_cast<uintptr_t>(d_y) % 16) {
-      for (size_t r = 0; r < m; r++) SYN_TRY(launch_zero_i32(reinterpret_cast<int *>(d_y + r * ldy), n, s));
+      for (size_t r = 0; r < m; r++)
+        SYN_TRY(launch_zero_i32(reinterpret_cast<int *>(d_y + r * ldy), n, s));
     } else {
       SYN_TRY(launch_zero_i32(reinterpret_cast<int *>(d_y), (m - 1) * ldy + n, s));
     }
@@ -601,12 +650,14 @@ syn_status_t QLinearKQ::gemm(size_t m, const float *d_x, size_t ldx, float *d_y,
                        (int)n, blocks, d_y, (int)ldy, per);
     return SYN_OK;
   };
-  static bool attr[8] = {false, false, false, false, false, false, false, false};
+  static bool attr[10] = {};
   if (big) {
     if (fmt == SYN_HIP_FMT_Q8_0 && exact)
       SYN_TRY(launch(k_gemm_kq5<SYN_HIP_FMT_Q8_0, true>, attr[0]));
     else if (fmt == SYN_HIP_FMT_Q8_0)
       SYN_TRY(launch(k_gemm_kq5<SYN_HIP_FMT_Q8_0, false>, attr[1]));
+    else if (fmt == SYN_HIP_FMT_Q4_0)
+      SYN_TRY(launch(k_gemm_kq5<SYN_HIP_FMT_Q4_0, true>, attr[8]));
     else if (fmt == SYN_HIP_FMT_Q4_K)
       SYN_TRY(launch(k_gemm_kq5<SYN_HIP_FMT_Q4_K, true>, attr[2]));
     else
@@ -616,6 +667,8 @@ syn_status_t QLinearKQ::gemm(size_t m, const float *d_x, size_t ldx, float *d_y,
       SYN_TRY(launch(k_gemm_kq2<SYN_HIP_FMT_Q8_0, true>, attr[4]));
     else if (fmt == SYN_HIP_FMT_Q8_0)
       SYN_TRY(launch(k_gemm_kq2<SYN_HIP_FMT_Q8_0, false>, attr[5]));
+    else if (fmt == SYN_HIP_FMT_Q4_0)
+      SYN_TRY(launch(k_gemm_kq2<SYN_HIP_FMT_Q4_0, true>, attr[9]));
     else if (fmt == SYN_HIP_FMT_Q4_K)
       SYN_TRY(launch(k_gemm_kq2<SYN_HIP_FMT_Q4_K, true>, attr[6]));
     else
@@ -623,6 +676,28 @@ syn_status_t QLinearKQ::gemm(size_t m, const float *d_x, size_t ldx, float *d_y,
   }
   SYN_LAUNCH_CHECK();
   return SYN_OK;
+}
+
+syn_status_t QLinearKQ::gemm(size_t m, const float *d_x, size_t ldx, float *d_y, size_t ldy,
+                             hipStream_t s) {
+  SYN_TRY(to_f16_rows(m, k, d_x, ldx, xh, xh_elems, s));
+  const bool exact = fmt != SYN_HIP_FMT_Q8_0 || q8_scales_f16_exact;
+  return kq_gemm_f16(fmt, exact, wq.as<u32x4>(), wd.as<uint16_t>(), blocks, n, k,
+                     xh.as<_Float16>(), m, d_y, ldy, s);
+}
+
+// Q4_0 rows on the same GEMM (its nibble planes sit in the Q8_0 plane layout
+// with one plane per block); only when every block scale, as the handle's
+// loader reads it, is the IEEE value of its f16 bits (gemm_ok())
+syn_status_t QLinearQ4_0::gemm(size_t m, const float *d_x, size_t ldx, float *d_y, size_t ldy,
+                               hipStream_t s) {
+  if (!gemm_ok()) {
+    set_error("Q4_0 GEMM: halved subnormal block scales need the GEMV path");
+    return SYN_ERR_INVALID_ARG;
+  }
+  SYN_TRY(to_f16_rows(m, k, d_x, ldx, xh, xh_elems, s));
+  return kq_gemm_f16(SYN_HIP_FMT_Q4_0, true, nib.as<u32x4>(), sc.as<uint16_t>(), blocks, n, k,
+                     xh.as<_Float16>(), m, d_y, ldy, s);
 }
 
 }  // namespace syn

@@ -86,11 +86,21 @@ struct QLinearQ4_0 {
   // block scales read with the Rust f16 converter (subnormals halved): the
   // reference's GGUF Q4_0 path; false = the Zig GEMV's IEEE conversion
   bool rs_f16_scales = false;
+  bool has_subnormal_scale = false;  // some block scale is an f16 subnormal (set at upload)
+  DevBuf xh;                         // f16 activations for the MFMA GEMM
+  size_t xh_elems = 0;
   syn_status_t upload_packed(const uint8_t *packed, size_t n_, size_t k_);
   syn_status_t from_f32(const float *w_nk, size_t n_, size_t k_);
   size_t weight_bytes() const { return n * (k / 32) * 18; }
+  // y[m,n] = x[m,k] W^T, f32 activations; m > 16 runs gemm() when gemm_ok()
   syn_status_t gemv(size_t m, const float *d_x, size_t ldx, float *d_y, size_t ldy,
                     hipStream_t s);
+  // f16 MFMA prefill GEMM (kquant_gemm.hip): weights (nibble - 8) * d and
+  // activations rounded once to f16, f32 accumulation
+  syn_status_t gemm(size_t m, const float *d_x, size_t ldx, float *d_y, size_t ldy,
+                    hipStream_t s);
+  // the GEMM decodes the scales as IEEE f16 values: not for halved subnormals
+  bool gemm_ok() const { return !(rs_f16_scales && has_subnormal_scale); }
 };
 
 // Ternary linear: TernaryLinear (ternary_linear.rs); f32 activations.

@@ -308,6 +308,7 @@ static const q4_launcher kQ4Launch[9] = {nullptr,        launch_q4_m<1>, launch_
 syn_status_t QLinearQ4_0::gemv(size_t m, const float *d_x, size_t ldx, float *d_y, size_t ldy,
                                hipStream_t s) {
   if (m == 0 || n == 0 || k == 0) return SYN_OK;
+  if (m > 16 && gemm_ok() && ldx % 4 == 0) return gemm(m, d_x, ldx, d_y, ldy, s);
   const float sub = rs_f16_scales ? 0.5f : 1.0f;
   // "chunks" here are 32-element blocks; a K slice holds whole blocks
   GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
@@ -347,11 +348,14 @@ syn_status_t QLinearQ4_0::upload_packed(const uint8_t *packed, size_t n_, size_t
   const size_t P = cdiv(n_, 64), B = (size_t)blocks;
   std::vector<uint8_t> hn(P * B * 64 * 16, 0x88);  // padding rows: nibble 8 -> value 0
   std::vector<uint16_t> hs(P * B * 64, 0);
+  has_subnormal_scale = false;
   for (size_t row = 0; row < n_; row++) {
     const size_t p = row / 64, r = row % 64;
     for (size_t b = 0; b < B; b++) {
       const uint8_t *src = packed + (row * B + b) * 18;
-      hs[(p * B + b) * 64 + r] = (uint16_t)(src[0] | (src[1] << 8));
+      const uint16_t d = (uint16_t)(src[0] | (src[1] << 8));
+      hs[(p * B + b) * 64 + r] = d;
+      if ((d & 0x7c00u) == 0 && (d & 0x3ffu) != 0) has_subnormal_scale = true;
       std::memcpy(&hn[((p * B + b) * 64 + r) * 16], src + 2, 16);
     }
   }

@@ -93,3 +93,49 @@ def test_gguf_q4_0_subnormal_scale_semantics():
     np.testing.assert_allclose(halved, deq @ x.astype(np.float64), rtol=1e-5, atol=0)
     # the two readings differ exactly by the halving of the subnormal blocks
     assert not np.allclose(ieee, halved)
+
+
+# ------------------------------------------------------------------ prefill GEMM
+# M > 16 rows run the f16 MFMA GEMM (kquant_gemm.hip with the Q4_0 plane
+# decoder): weights (nibble - 8) * d and activations rounded once to f16, f32
+# accumulation; each row must stay within the per-row tolerance of the
+# reference's q4_0GemvRow (the oracle) and of the device GEMV.
+@pytest.mark.parametrize("m,n,k", [(17, 96, 64), (40, 200, 96), (256, 2048, 2048),
+                                   (512, 512, 2048), (2048, 1024, 2048)])
+def test_q4_gemm_rows_match_gemv_rows(m, n, k):
+    packed = _random_packed(n, k, m * 7 + n + k)
+    x = O.normal(m * k, m + 3, 1.0).reshape(m, k)
+    lin = hip.QLinear.q4_0(packed, n, k)
+    got = lin.forward(x)
+    rows = sorted(set([0, 1, m // 2, m - 1] + list(range(0, m, max(1, m // 24)))))
+    worst = 0.0
+    for i in rows:
+        want = O.q4_0_gemv(x[i], packed, n)
+        worst = max(worst, _rel(got[i], want))
+        dev = lin.forward(x[i:i + 1])[0]  # the GEMV kernel for one row
+        assert _rel(got[i], dev) <= TOL
+    print(f"m={m} n={n} k={k} worst row rel {worst:.2e}")
+    assert worst <= TOL
+
+
+def test_q4_gemm_halved_subnormal_scales_use_the_gemv():
+    # gguf_dequant handles whose scales include subnormals keep the GEMV
+    # (its scale reading halves them); IEEE handles run the GEMM
+    n, k, m = 64, 64, 24
+    blk = np.zeros((n, k // 32, 18), np.uint8)
+    for r in range(n):
+        for b in range(k // 32):
+            d = 0x0003 if (r + b) % 3 == 0 else 0x2C00
+            blk[r, b, 0:2] = np.array([d], np.uint16).view(np.uint8)
+            blk[r, b, 2:] = ((np.arange(16) * 5 + r + 3 * b) % 256).astype(np.uint8)
+    packed = blk.reshape(-1)
+    x = O.normal(m * k, 31, 1.0).reshape(m, k)
+    halved = hip.QLinear.q4_0(packed, n, k, gguf_dequant=True).forward(x)
+    deq = O.dequant("q4_0", packed, n * k).reshape(n, k).astype(np.float64)
+    want = x.astype(np.float64) @ deq.T
+    # per-row metric: elementwise relative error of near-cancelling dot
+    # products says nothing about the scale reading
+    assert max(_rel(halved[i], want[i]) for i in range(m)) <= 1e-5
+    ieee = hip.QLinear.q4_0(packed, n, k).forward(x)
+    for i in (0, m - 1):
+        assert _rel(ieee[i], O.q4_0_gemv(x[i], packed, n)) <= TOL
