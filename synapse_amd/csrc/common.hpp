@@ -194,6 +194,13 @@ __device__ __forceinline__ float syn_f16_to_f32_rs_hw(uint32_t h) {
   return f * ((h & 0x7c00u) == 0 ? 0.5f : 1.0f);
 }
 
+// lane l's 16 bytes at src land at lds_base + 16 * l (gfx950
+// global_load_lds_dwordx4; lds_base is wave-uniform)
+__device__ __forceinline__ void g2lds16(const void *src, void *lds_base) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds_base, 16,
+                                   0, 0);
+}
+
 // IEEE f16->f32 (qmatmul.zig:346-371 semantics)
 __device__ __forceinline__ float syn_f16_to_f32_ieee(uint32_t h) {
   const uint32_t sign = (h >> 15) & 1u, exp = (h >> 10) & 0x1fu, mant = h & 0x3ffu;

@@ -1041,13 +1041,6 @@ constexpr int kAttnNT = 256;
 constexpr int kPvChunk = 128;            // positions per staged V chunk
 constexpr int kPvGroups = kPvChunk / 4;  // 4-position groups per chunk
 
-// lane l's 16 bytes at src land at lds_base + 16 * l (gfx950
-// global_load_lds_dwordx4; lds_base is wave-uniform)
-__device__ __forceinline__ void g2lds16(const void *src, void *lds_base) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)lds_base, 16,
-                                   0, 0);
-}
-
 // V groups [g0, g0 + ngroups) (4 positions of one column per 16 bytes,
 // indices clamped to the cache; ngroups rounded up to whole wave
 // instructions) of columns [cb0, cb0 + CB) into dst[group][CB], issued by

@@ -1,14 +1,17 @@
 // Prefill GEMM for the GGUF block formats on the f16 matrix cores (A12/A13).
 //
 // The reference runs these formats as f32 sgemmTiled over weights
-// dequantized at load (ops/matmul.rs:55-79, matmul.zig:157-183).  Here a
+// dequantized at load (ops/matmul.rs:55-79, matmul.zig:157-183); Q4_0 rows
+// run q4_0GemvRow one row at a time (q4_linear.rs:126-150).  Here a
 // workgroup owns a 256 x 256 tile of Y = X W^T (four waves, k_gemm_kq5; used
 // when such tiles cover three quarters of the CUs) or a 256 x 128 tile
 // (twelve waves, k_gemm_kq2, split over K for small grids) and walks K 64
 // elements at a time: the weight tile is decoded once per workgroup from the
 // HBM plane layout into f16 in LDS (value = the reference dequantizer's f32
 // value rounded to f16), activations are pre-converted to f16, and
-// v_mfma_f32_32x32x16_f16 accumulates in f32.  The two f16 roundings
+// v_mfma_f32_32x32x16_f16 accumulates in f32.  Q4_0 on large grids runs
+// k_gemm_kqr instead: both operands reach LDS by direct global->LDS loads
+// and each wave decodes its weight fragments in registers.  The two f16 roundings
 // (relative 2^-11 each) keep the result well inside the 1e-3 per-row
 // tolerance (measured in the tests).
 #include <algorithm>
@@ -21,20 +24,26 @@ namespace syn {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-// x f32 [M, ldx] -> xh f16 [M, ldh], columns K..ldh-1 zero (K, ldh multiples of 4)
+// x f32 [M, ldx] -> xh f16 [M, ldh], columns K..ldh-1 zero (K a multiple of
+// 8, ldh of 64, ldx of 4).  perm8: each 8-element chunk is stored in the k
+// order 0,2,4,6,1,3,5,7 of the Q4_0 direct-load kernel's fragments (k_gemm_kqr).
 __global__ void k_f32_to_f16(const float *__restrict__ x, int ldx, _Float16 *__restrict__ xh,
-                             int ldh, int M, int K) {
+                             int ldh, int M, int K, int perm8) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  const int per_row = ldh / 4;
+  const int per_row = ldh / 8;
   if (i >= M * per_row) return;
-  const int m = i / per_row, c = (i - m * per_row) * 4;
-  float4 v = float4{0.0f, 0.0f, 0.0f, 0.0f};
-  if (c < K) v = *reinterpret_cast<const float4 *>(x + (size_t)m * ldx + c);
-  _Float16 *o = xh + (size_t)m * ldh + c;
-  o[0] = (_Float16)v.x;
-  o[1] = (_Float16)v.y;
-  o[2] = (_Float16)v.z;
-  o[3] = (_Float16)v.w;
+  const int m = i / per_row, c = (i - m * per_row) * 8;
+  float4 a = float4{0.0f, 0.0f, 0.0f, 0.0f}, b = a;
+  if (c < K) {
+    a = *reinterpret_cast<const float4 *>(x + (size_t)m * ldx + c);
+    b = *reinterpret_cast<const float4 *>(x + (size_t)m * ldx + c + 4);
+  }
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  const h8 o = perm8 ? h8{(_Float16)a.x, (_Float16)a.z, (_Float16)b.x, (_Float16)b.z,
+                          (_Float16)a.y, (_Float16)a.w, (_Float16)b.y, (_Float16)b.w}
+                     : h8{(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
+                          (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
+  *reinterpret_cast<h8 *>(xh + (size_t)m * ldh + c) = o;
 }
 
 // ---------------------------------------------------------------------------
@@ -588,12 +597,236 @@ __global__ void __launch_bounds__(256)
     }
 }
 
+// ---------------------------------------------------------------------------
+// Direct-load form (Q4_0).  Four waves own a 256 x 256 tile; wave (wr, wc)
+// the 128 x 128 sub-tile at rows wr*128, columns wc*128.  Both operands go
+// from global memory straight into LDS (gfx950 global_load_lds_dwordx4: no
+// registers, no ds_write), KR_NS stages deep, two steps ahead:
+//  - activations (f16) in the padded [256][72] layout (the pad slot of each
+//    row keeps the fragment reads free of bank conflicts; the direct loads
+//    fill it with a copy of the row's first chunk);
+//  - the raw weight bytes as stored: each (panel, block) of the nibble plane
+//    layout is 64 rows x 16 bytes, one 1 KiB direct load, plus the f16
+//    scales of the step's 4 panels x 2 blocks.
+// Each wave reads the raw bytes of its 128 columns and decodes them to f16
+// in registers (the two waves of a column half decode the same weights: VALU
+// work that runs beside the matrix cores).  One barrier per 64-element step
+// publishes the next stage.
+//
+// k order.  Lane l of a fragment holds column (or row) l % 32 and 8 k
+// values; lanes l < 32 take block 2s of step s and lanes l >= 32 block
+// 2s+1, so MFMA group g (0..3) covers elements 8g..8g+7 of both blocks
+// (activation chunks g and 4+g of the step).  A fragment holds the element
+// order 0,2,4,6,1,3,5,7 of its 8 nibbles; the activations are converted in
+// the same order (k_f32_to_f16 perm8).  The MFMA sums over k in any order.
+constexpr int KR_NS = 3;                       // stages
+constexpr int KR_SLOTS = PGLD / 8;             // 16-byte slots per activation row (8 + 1 pad)
+constexpr int KR_A = PG3M * PGLD * 2;          // activation bytes per stage (36,864)
+constexpr int KR_ADMA = PG3M * KR_SLOTS / 256; // activation direct loads per thread (9)
+constexpr int KR_WCH = 8;                      // weight KiB per stage: 4 panels x 2 blocks
+constexpr int KR_STAGE_BYTES = KR_A + (KR_WCH + 1) * 1024;  // + 1 KiB of scales
+// direct loads a wave issues per stage (activations, its 2 weight chunks, the
+// scales): the count kr_publish leaves outstanding per stage in flight
+constexpr int KR_AFTER = KR_ADMA + KR_WCH / 4 + 1;
+
+// One direct global->LDS load of 16 bytes per lane into lds_addr + 16 * lane
+// (lds_addr wave-uniform).  Issued as inline assembly so that the compiler's
+// memory-counter bookkeeping does not see it: it would otherwise wait for
+// every direct load before the next LDS read it cannot prove disjoint from
+// it.  kr_publish waits for these loads explicitly.
+__device__ __forceinline__ void kr_dma(const void *src, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr)
+               : "memory", "m0");
+}
+
+// Wait until this wave's direct loads of the next stage have landed (the
+// AFTER loads issued since are the stage after next) and its LDS reads of
+// the current stage have returned, then meet the other waves, after which
+// the current stage may be overwritten.  A plain s_barrier:
+// __syncthreads()'s fence would wait for every outstanding load, the
+// prefetches included.
+template <int AFTER>
+__device__ __forceinline__ void kr_publish() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(AFTER) : "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// the B fragment of MFMA group g from the lane's block (32 nibbles) and f16
+// scale pair d: 8 f16 weights (nibble - 8) * d, each exact before one f16
+// rounding (see pg_decode_w)
+__device__ __forceinline__ f16x8 kr_decode(const u32x4 &q, int g, f16x2 d) {
+  const f16x2 bias = f16x2{(_Float16)-1032.0f, (_Float16)-1032.0f};
+  const uint32_t v = u32x4_word(q, g);
+  const uint32_t lo = v & 0x0f0f0f0fu, hi = (v >> 4) & 0x0f0f0f0fu;
+  const uint32_t p[4] = {__builtin_amdgcn_perm(0x64646464u, lo, 0x04010400u),
+                         __builtin_amdgcn_perm(0x64646464u, lo, 0x04030402u),
+                         __builtin_amdgcn_perm(0x64646464u, hi, 0x04010400u),
+                         __builtin_amdgcn_perm(0x64646464u, hi, 0x04030402u)};
+  uint32_t o[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+    o[i] = __builtin_bit_cast(uint32_t, (__builtin_bit_cast(f16x2, p[i]) + bias) * d);
+  return __builtin_bit_cast(f16x8, u32x4{o[0], o[1], o[2], o[3]});
+}
+
+__global__ void __launch_bounds__(256)
+    k_gemm_kqr(const _Float16 *__restrict__ Xh, int ldh, int M, int K,
+               const u32x4 *__restrict__ W, const uint16_t *__restrict__ Wd, int N, int B,
+               float *__restrict__ Y, int ldy, int steps_per_split) {
+  extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
+  constexpr int WCH = KR_WCH, STAGE = KR_STAGE_BYTES;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int l32 = lane & 31, lh = lane >> 5, wr = wave >> 1, wc = wave & 1;
+  const int n0 = blockIdx.x * PG3N, m0 = blockIdx.y * PG3M;
+  const int s_begin = blockIdx.z * steps_per_split;
+  const int nsteps = min((K + PGK - 1) / PGK - s_begin, steps_per_split);
+  const int last_panel = (N - 1) >> 6;
+  // activation slot s = (wave * KR_ADMA + i) * 64 + lane of a stage is row
+  // s / 9, chunk s % 9 (the pad chunk reloads chunk 0); rows past M read
+  // row M - 1 (never stored)
+  uint32_t aoff[KR_ADMA];
+#pragma unroll
+  for (int i = 0; i < KR_ADMA; i++) {
+    const int s = (wave * KR_ADMA + i) * 64 + lane, row = s / KR_SLOTS, c = s % KR_SLOTS;
+    aoff[i] = (uint32_t)min(m0 + row, M - 1) * (uint32_t)ldh + (uint32_t)(c < 8 ? c : 0) * 8u;
+  }
+  // weight chunk j = p * 2 + b of a stage: panel p of the tile (clamped to
+  // the matrix's last), block 2s + b (clamped to B - 1), issued by wave
+  // j / 2; the scales by every wave: lane l brings bytes 16 (l % 8) .. of
+  // panel l / 16, block (l / 8) % 2
+  const uint8_t *Wb = reinterpret_cast<const uint8_t *>(W);
+  const uint8_t *Wdb = reinterpret_cast<const uint8_t *>(Wd);
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) _Float16 *)lds;
+  auto dma = [&](int t, int stage) {
+    const int step = s_begin + min(t, nsteps - 1);
+    const _Float16 *src = Xh + (size_t)step * PGK;
+    const uint32_t sb = lds_base + (uint32_t)(stage * STAGE);
+    const uint32_t wa = (uint32_t)__builtin_amdgcn_readfirstlane(wave * KR_ADMA * 1024);
+#pragma unroll
+    for (int i = 0; i < KR_ADMA; i++) kr_dma(src + aoff[i], sb + wa + (uint32_t)(i * 1024));
+#pragma unroll
+    for (int i = 0; i < WCH / 4; i++) {
+      const int j = __builtin_amdgcn_readfirstlane(wave * (WCH / 4) + i);
+      const int p = j >> 1, b = j & 1;
+      const size_t panel = (size_t)min((n0 >> 6) + p, last_panel);
+      const size_t blk = (size_t)min(2 * step + b, B - 1);
+      kr_dma(Wb + (panel * B + blk) * 1024 + lane * 16, sb + (uint32_t)(KR_A + j * 1024));
+    }
+    {  // every wave loads the same scale bytes (no branch; identical writes)
+      const int q = lane >> 3, p = q >> 1, b = q & 1;
+      const size_t panel = (size_t)min((n0 >> 6) + p, last_panel);
+      const size_t blk = (size_t)min(2 * step + b, B - 1);
+      kr_dma(Wdb + (panel * B + blk) * 128 + (lane & 7) * 16,
+             sb + (uint32_t)(KR_A + WCH * 1024));
+    }
+  };
+
+  f32x16 acc[4][4];
+#pragma unroll
+  for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[mt][nt][r] = 0.0f;
+
+  const int arow = ((wr * 128 + l32) * PGLD + lh * 32) * 2;  // the lane's row, chunk 4*lh
+  u32x4 q[4];     // raw nibbles of the lane's block (2s + lh) for its 4 column groups
+  f16x2 dd[4];    // their f16 scales
+  f16x8 fa[2][4], fb[2][4];
+  // step t's raw weights, scales and MFMA group 0 operands from stage `stage`
+  auto open_step = [&](int t, int stage) {
+    const uint8_t *st = reinterpret_cast<const uint8_t *>(lds) + stage * STAGE;
+    // all ones while block 2s + lh exists (the clamped block past the end
+    // of an odd B decodes to zeros, against zero activations)
+    const uint32_t dm = (uint32_t)((2 * (s_begin + t) + lh - B) >> 31) & 0xffffu;
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++) {
+      const int p = wc * 2 + (nt >> 1), rp = (nt & 1) * 32 + l32;
+      q[nt] = *reinterpret_cast<const u32x4 *>(st + KR_A + (p * 2 + lh) * 1024 + rp * 16);
+      // every scale reads as its IEEE value (QLinearQ4_0::gemm_ok)
+      const uint16_t bits = *reinterpret_cast<const uint16_t *>(
+                                st + KR_A + WCH * 1024 + ((p * 2 + lh) * 64 + rp) * 2) &
+                            (uint16_t)dm;
+      const _Float16 v = __builtin_bit_cast(_Float16, bits);
+      dd[nt] = f16x2{v, v};
+    }
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+      fa[0][mt] = *reinterpret_cast<const f16x8 *>(st + arow + mt * 32 * PGLD * 2);
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++) fb[0][nt] = kr_decode(q[nt], 0, dd[nt]);
+  };
+  auto mma = [&](int b) {
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+      for (int nt = 0; nt < 4; nt++)
+        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[b][mt], fb[b][nt], acc[mt][nt],
+                                                             0, 0, 0);
+  };
+
+  // Step t lives in stage t % 3.  Iteration t: groups 0-2 of step t (each
+  // MFMA group beside the reads and decode of the next group); the barrier
+  // that publishes step t+1; the load of step t+3 into the stage step t
+  // has left; step t+1's group 0 operands beside step t's last group.
+  dma(0, 0);
+  dma(1, 1);
+  dma(2, 2);
+  kr_publish<2 * KR_AFTER>();
+  open_step(0, 0);
+  for (int t = 0; t < nsteps; t++) {
+    const int cur = t % KR_NS, nxt = cur == KR_NS - 1 ? 0 : cur + 1;
+    const uint8_t *sa = reinterpret_cast<const uint8_t *>(lds) + cur * STAGE + arow;
+#pragma unroll
+    for (int g = 0; g < 3; g++) {
+      const int b = g & 1;
+#pragma unroll
+      for (int mt = 0; mt < 4; mt++)
+        fa[b ^ 1][mt] = *reinterpret_cast<const f16x8 *>(sa + mt * 32 * PGLD * 2 + (g + 1) * 16);
+#pragma unroll
+      for (int nt = 0; nt < 4; nt++) fb[b ^ 1][nt] = kr_decode(q[nt], g + 1, dd[nt]);
+      mma(b);
+    }
+    kr_publish<KR_AFTER>();
+    dma(t + 3, cur);
+    // group 3 of step t runs from fa[1] / fb[1] while group 0 of step t+1
+    // (a clamped, unused step after the last) fills fa[0] / fb[0]
+    const f16x8 a3[4] = {fa[1][0], fa[1][1], fa[1][2], fa[1][3]};
+    const f16x8 b3[4] = {fb[1][0], fb[1][1], fb[1][2], fb[1][3]};
+    open_step(t + 1, nxt);
+#pragma unroll
+    for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+      for (int nt = 0; nt < 4; nt++)
+        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a3[mt], b3[nt], acc[mt][nt], 0, 0, 0);
+  }
+  // the prefetches past the last step must land before the workgroup's LDS
+  // can go to another workgroup
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  const bool atomic = gridDim.z > 1;
+#pragma unroll
+  for (int mt = 0; mt < 4; mt++)
+#pragma unroll
+    for (int nt = 0; nt < 4; nt++) {
+      const int n = n0 + wc * 128 + nt * 32 + l32;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int m = m0 + wr * 128 + mt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+        if (m < M && n < N) {
+          if (atomic) atomicAdd(&Y[(size_t)m * ldy + n], acc[mt][nt][r]);
+          else Y[(size_t)m * ldy + n] = acc[mt][nt][r];
+        }
+      }
+    }
+}
+
 // f32 activation rows -> zero-padded f16 rows of ldh = round_up(k, PGK)
-// halfs in xh (grown on demand)
+// halfs in xh (grown on demand), in the k_gemm_kqr Q4_0 chunk order if perm8
 static syn_status_t to_f16_rows(size_t m, size_t k, const float *d_x, size_t ldx, DevBuf &xh,
-                                size_t &xh_elems, hipStream_t s) {
-  if (ldx % 4) {
-    set_error("GEMM activation stride must be a multiple of 4 floats");
+                                size_t &xh_elems, bool perm8, hipStream_t s) {
+  if (ldx % 4 || k % 8) {
+    set_error("GEMM activation stride must be a multiple of 4 floats and K of 8");
     return SYN_ERR_SHAPE_MISMATCH;
   }
   const size_t ldh = round_up(k, PGK);  // zero-padded to whole K steps
@@ -602,21 +835,64 @@ static syn_status_t to_f16_rows(size_t m, size_t k, const float *d_x, size_t ldx
     SYN_TRY(xh.alloc(m * ldh * 2));
     xh_elems = m * ldh;
   }
-  const int total = (int)(m * (ldh / 4));
+  const int total = (int)(m * (ldh / 8));
   hipLaunchKernelGGL(k_f32_to_f16, dim3(cdiv(total, 256)), dim3(256), 0, s, d_x, (int)ldx,
-                     xh.as<_Float16>(), (int)ldh, (int)m, (int)k);
+                     xh.as<_Float16>(), (int)ldh, (int)m, (int)k, perm8 ? 1 : 0);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
 }
 
-// Y[m, n] = Xh[m, k] W^T for a weight matrix of format fmt in the plane
-// layout (W, Wd, B blocks per row); exact: the weights decode with f16
-// products (see pg_decode_w)
+// Y (ksplit > 1: the splits add their partial tiles into it) cleared by a
+// kernel, not a memset node, so the call can sit in a captured graph
+static syn_status_t zero_y(float *d_y, size_t m, size_t n, size_t ldy, hipStream_t s) {
+  if (ldy % 4 || reinterpret_cast<uintptr_t>(d_y) % 16) {
+    for (size_t r = 0; r < m; r++)
+      SYN_TRY(launch_zero_i32(reinterpret_cast<int *>(d_y + r * ldy), n, s));
+    return SYN_OK;
+  }
+  return launch_zero_i32(reinterpret_cast<int *>(d_y), (m - 1) * ldy + n, s);
+}
+
+template <class Kern>
+static syn_status_t launch_gemm(Kern kern, bool &attr_set, dim3 grid, unsigned threads, size_t shm,
+                                const _Float16 *X, size_t ldh, size_t m, size_t k,
+                                const u32x4 *W, const uint16_t *Wd, size_t n, int blocks,
+                                float *d_y, size_t ldy, int per, hipStream_t s) {
+  if (!attr_set) {  // more than the default 64 KiB of dynamic LDS
+    SYN_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)shm));
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(kern, grid, dim3(threads), shm, s, X, (int)ldh, (int)m, (int)k, W, Wd,
+                     (int)n, blocks, d_y, (int)ldy, per);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
+
+// Y[m, n] = X[m, k] W^T for a weight matrix of format fmt in the plane
+// layout (W, Wd, B blocks per row), X f32 rows converted to f16 in xh;
+// exact: the weights decode with f16 products (see pg_decode_w)
 static syn_status_t kq_gemm_f16(int fmt, bool exact, const u32x4 *W, const uint16_t *Wd,
-                                int blocks, size_t n, size_t k, const _Float16 *X, size_t m,
-                                float *d_y, size_t ldy, hipStream_t s) {
+                                int blocks, size_t n, size_t k, const float *d_x, size_t ldx,
+                                DevBuf &xh, size_t &xh_elems, size_t m, float *d_y, size_t ldy,
+                                hipStream_t s) {
   const size_t ldh = round_up(k, PGK);
   const int steps = (int)cdiv(k, PGK);
+  static bool attr[11] = {};
+  // Q4_0 on enough 256 x 256 tiles for three quarters of the CUs: the
+  // direct-load kernel (measured ahead of k_gemm_kq5 there; for Q8_0 the
+  // two tie, and k_gemm_kq2 leads on split-K grids)
+  const int tiles256 = (int)(cdiv(n, PG3N) * cdiv(m, PG3M));
+  if (fmt == SYN_HIP_FMT_Q4_0 && tiles256 >= 192 && m * ldh < (1u << 31)) {
+    SYN_TRY(to_f16_rows(m, k, d_x, ldx, xh, xh_elems, true, s));
+    const int tiles_n = (int)cdiv(n, PG3N), tiles_m = (int)cdiv(m, PG3M);
+    const dim3 grid((unsigned)tiles_n, (unsigned)tiles_m, 1);
+    const int per = steps;
+    return launch_gemm(k_gemm_kqr, attr[10], grid, 256, (size_t)KR_NS * KR_STAGE_BYTES,
+                       xh.as<_Float16>(), ldh, m, k, W, Wd, n, blocks, d_y, ldy, per, s);
+  }
+  SYN_TRY(to_f16_rows(m, k, d_x, ldx, xh, xh_elems, false, s));
+  const _Float16 *X = xh.as<_Float16>();
   // Enough 256 x 256 tiles for three quarters of the CUs: the four-wave
   // kernel, one K pass per tile.  Fewer: 256 x 128 tiles (twice as many),
   // split over K when even those cannot fill the GPU.
@@ -627,63 +903,33 @@ static syn_status_t kq_gemm_f16(int fmt, bool exact, const u32x4 *W, const uint1
     ksplit = std::max(1, std::min((int)cdiv(384, (size_t)(tiles_n * tiles_m)), steps / 8));
   const int per = (int)cdiv((size_t)steps, (size_t)ksplit);
   ksplit = (int)cdiv((size_t)steps, (size_t)per);
-  if (ksplit > 1) {
-    // Y accumulates the splits' partial tiles; a kernel (not a memset node)
-    // clears it so the call can sit in a captured graph
-    if (ldy % 4 || reinterpret_cast<uintptr_t>(d_y) % 16) {
-      for (size_t r = 0; r < m; r++)
-        SYN_TRY(launch_zero_i32(reinterpret_cast<int *>(d_y + r * ldy), n, s));
-    } else {
-      SYN_TRY(launch_zero_i32(reinterpret_cast<int *>(d_y), (m - 1) * ldy + n, s));
-    }
-  }
-  dim3 grid((unsigned)tiles_n, (unsigned)tiles_m, (unsigned)ksplit);
+  if (ksplit > 1) SYN_TRY(zero_y(d_y, m, n, ldy, s));
+  const dim3 grid((unsigned)tiles_n, (unsigned)tiles_m, (unsigned)ksplit);
   const size_t shm = 2 * (size_t)(big ? PG3_STAGE : PG_STAGE) * sizeof(_Float16);
   const unsigned threads = big ? 256 : PGT2;
   auto launch = [&](auto kern, bool &attr_set) -> syn_status_t {
-    if (!attr_set) {  // more than the default 64 KiB of dynamic LDS
-      SYN_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                  (int)shm));
-      attr_set = true;
-    }
-    hipLaunchKernelGGL(kern, grid, dim3(threads), shm, s, X, (int)ldh, (int)m, (int)k, W, Wd,
-                       (int)n, blocks, d_y, (int)ldy, per);
-    return SYN_OK;
+    return launch_gemm(kern, attr_set, grid, threads, shm, X, ldh, m, k, W, Wd, n, blocks, d_y,
+                       ldy, per, s);
   };
-  static bool attr[10] = {};
   if (big) {
-    if (fmt == SYN_HIP_FMT_Q8_0 && exact)
-      SYN_TRY(launch(k_gemm_kq5<SYN_HIP_FMT_Q8_0, true>, attr[0]));
-    else if (fmt == SYN_HIP_FMT_Q8_0)
-      SYN_TRY(launch(k_gemm_kq5<SYN_HIP_FMT_Q8_0, false>, attr[1]));
-    else if (fmt == SYN_HIP_FMT_Q4_0)
-      SYN_TRY(launch(k_gemm_kq5<SYN_HIP_FMT_Q4_0, true>, attr[8]));
-    else if (fmt == SYN_HIP_FMT_Q4_K)
-      SYN_TRY(launch(k_gemm_kq5<SYN_HIP_FMT_Q4_K, true>, attr[2]));
-    else
-      SYN_TRY(launch(k_gemm_kq5<SYN_HIP_FMT_Q6_K, true>, attr[3]));
-  } else {
-    if (fmt == SYN_HIP_FMT_Q8_0 && exact)
-      SYN_TRY(launch(k_gemm_kq2<SYN_HIP_FMT_Q8_0, true>, attr[4]));
-    else if (fmt == SYN_HIP_FMT_Q8_0)
-      SYN_TRY(launch(k_gemm_kq2<SYN_HIP_FMT_Q8_0, false>, attr[5]));
-    else if (fmt == SYN_HIP_FMT_Q4_0)
-      SYN_TRY(launch(k_gemm_kq2<SYN_HIP_FMT_Q4_0, true>, attr[9]));
-    else if (fmt == SYN_HIP_FMT_Q4_K)
-      SYN_TRY(launch(k_gemm_kq2<SYN_HIP_FMT_Q4_K, true>, attr[6]));
-    else
-      SYN_TRY(launch(k_gemm_kq2<SYN_HIP_FMT_Q6_K, true>, attr[7]));
+    if (fmt == SYN_HIP_FMT_Q8_0 && exact) return launch(k_gemm_kq5<SYN_HIP_FMT_Q8_0, true>, attr[0]);
+    if (fmt == SYN_HIP_FMT_Q8_0) return launch(k_gemm_kq5<SYN_HIP_FMT_Q8_0, false>, attr[1]);
+    if (fmt == SYN_HIP_FMT_Q4_0) return launch(k_gemm_kq5<SYN_HIP_FMT_Q4_0, true>, attr[8]);
+    if (fmt == SYN_HIP_FMT_Q4_K) return launch(k_gemm_kq5<SYN_HIP_FMT_Q4_K, true>, attr[2]);
+    return launch(k_gemm_kq5<SYN_HIP_FMT_Q6_K, true>, attr[3]);
   }
-  SYN_LAUNCH_CHECK();
-  return SYN_OK;
+  if (fmt == SYN_HIP_FMT_Q8_0 && exact) return launch(k_gemm_kq2<SYN_HIP_FMT_Q8_0, true>, attr[4]);
+  if (fmt == SYN_HIP_FMT_Q8_0) return launch(k_gemm_kq2<SYN_HIP_FMT_Q8_0, false>, attr[5]);
+  if (fmt == SYN_HIP_FMT_Q4_0) return launch(k_gemm_kq2<SYN_HIP_FMT_Q4_0, true>, attr[9]);
+  if (fmt == SYN_HIP_FMT_Q4_K) return launch(k_gemm_kq2<SYN_HIP_FMT_Q4_K, true>, attr[6]);
+  return launch(k_gemm_kq2<SYN_HIP_FMT_Q6_K, true>, attr[7]);
 }
 
 syn_status_t QLinearKQ::gemm(size_t m, const float *d_x, size_t ldx, float *d_y, size_t ldy,
                              hipStream_t s) {
-  SYN_TRY(to_f16_rows(m, k, d_x, ldx, xh, xh_elems, s));
   const bool exact = fmt != SYN_HIP_FMT_Q8_0 || q8_scales_f16_exact;
-  return kq_gemm_f16(fmt, exact, wq.as<u32x4>(), wd.as<uint16_t>(), blocks, n, k,
-                     xh.as<_Float16>(), m, d_y, ldy, s);
+  return kq_gemm_f16(fmt, exact, wq.as<u32x4>(), wd.as<uint16_t>(), blocks, n, k, d_x, ldx, xh,
+                     xh_elems, m, d_y, ldy, s);
 }
 
 // Q4_0 rows on the same GEMM (its nibble planes sit in the Q8_0 plane layout
@@ -695,9 +941,8 @@ syn_status_t QLinearQ4_0::gemm(size_t m, const float *d_x, size_t ldx, float *d_
     set_error("Q4_0 GEMM: halved subnormal block scales need the GEMV path");
     return SYN_ERR_INVALID_ARG;
   }
-  SYN_TRY(to_f16_rows(m, k, d_x, ldx, xh, xh_elems, s));
   return kq_gemm_f16(SYN_HIP_FMT_Q4_0, true, nib.as<u32x4>(), sc.as<uint16_t>(), blocks, n, k,
-                     xh.as<_Float16>(), m, d_y, ldy, s);
+                     d_x, ldx, xh, xh_elems, m, d_y, ldy, s);
 }
 
 }  // namespace syn

@@ -101,7 +101,9 @@ def test_gguf_q4_0_subnormal_scale_semantics():
 # accumulation; each row must stay within the per-row tolerance of the
 # reference's q4_0GemvRow (the oracle) and of the device GEMV.
 @pytest.mark.parametrize("m,n,k", [(17, 96, 64), (40, 200, 96), (256, 2048, 2048),
-                                   (512, 512, 2048), (2048, 1024, 2048)])
+                                   (512, 512, 2048), (2048, 1024, 2048),
+                                   # >= 192 tiles of 256 x 256: the direct-load kernel
+                                   (2048, 6144, 96), (2000, 12300, 64), (2048, 8192, 2048)])
 def test_q4_gemm_rows_match_gemv_rows(m, n, k):
     packed = _random_packed(n, k, m * 7 + n + k)
     x = O.normal(m * k, m + 3, 1.0).reshape(m, k)
