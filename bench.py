@@ -111,6 +111,22 @@ LLAMA3B = dict(hidden=3072, n_layers=28, n_heads=24, n_kv_heads=8, head_dim=128,
                vocab=128256, eps=1e-5, rope_theta=5e5)
 MAMBA370M = dict(d_model=1024, d_inner=2048, d_state=16, d_conv=4, dt_rank=64, n_layers=48,
                  vocab=50280, eps=1e-5)
+# LFM2.5-350M (models/ssm/hybrid/config.rs:132-156): 0 = LIV conv, 1 = GQA
+LFM25 = dict(hidden=1024, n_layers=16, vocab=65536, n_heads=16, n_kv_heads=8, head_dim=64,
+             inner=1024, conv_kernel=3, inter=6656, eps=1e-5, rope_theta=1e6,
+             layer_kinds=[0, 0, 1, 0, 0, 1, 0, 0, 1, 0, 1, 0, 1, 0, 1, 0])
+
+
+def hybrid_weight_bytes(c):
+    """Bytes one decode step streams: the Q4_0 projections (18 bytes per 32
+    weights) and the tied f32 lm_head."""
+    h, inner, f = c["hidden"], c["inner"], c["inter"]
+    qd, kvd = c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"]
+    q4 = 0
+    for kind in c["layer_kinds"]:
+        q4 += (3 * inner * h + h * inner) if kind == 0 else ((qd + 2 * kvd) * h + h * qd)
+        q4 += 3 * f * h
+    return q4 // 32 * 18 + c["vocab"] * h * 4
 
 
 def _ids(n, vocab, seed):
@@ -216,6 +232,20 @@ def secondary(hip, np):
         mb.gemv_record(hip.FMT_INT8, 4096, 1024, "in_proj 1024->4096"),
         mb.gemv_record(hip.FMT_INT8, 1024, 2048, "out_proj 2048->1024")]
     out["config5_mamba370m"] = mam
+    # hybrid LFM2.5-350M Q4 decode (metal/hybrid_gpu_forward.rs's path): not a
+    # BASELINE configuration; 8-token prompt, 128 greedy decode steps
+    hc = dict(LFM25, max_seq=8 + 128 + 1)
+    hm = hip.HybridLM(hc)
+    hm.init_synthetic(SEED_BASE, 0.02)
+    hm.prefill(np.array(_ids(8, hc["vocab"], PROMPT_SEED), np.uint32))
+    ms = hm.decode_timed(128)
+    hm.close()
+    hb = hybrid_weight_bytes(LFM25)
+    out["hybrid_lfm25_q4_0_decode"] = {
+        "decode_tok_s": round(128e3 / ms, 1), "decode_ms_per_token": round(ms / 128, 4),
+        "weight_bytes_per_token": hb, "decode_weight_gbs": round(hb / (ms / 128 * 1e-3) / 1e9, 1),
+        "note": "16 layers (10 LIV conv, 6 GQA), Q4_0 projections, tied f32 lm_head (65536 x "
+                "1024), graph replay of the op-by-op step"}
     out["seconds"] = round(time.perf_counter() - t0, 1)
     return out
 
@@ -312,6 +342,27 @@ def cpu_baselines_secondary(np):
         "tok_s": round(1.0 / s, 3), "ms_per_token": round(s * 1e3, 1),
         "sample": "median of 5 decode steps after a 4-token prompt (reference semantics: "
                   "x_proj, dt_proj and lm_head f32)"}
+    # hybrid LFM2.5-350M Q4 decode: one-conv, one-GQA and conv+GQA models at
+    # full widths give a conv layer, a GQA layer and the head; a token = 10
+    # conv + 6 GQA layers + the head
+    ts = {}
+    for name, kinds in (("c", [0]), ("a", [1]), ("ca", [0, 1])):
+        hc = dict(LFM25, n_layers=len(kinds), layer_kinds=kinds, max_seq=16)
+        hm = O.HybridLM(hc)
+        hm.init_synthetic(SEED_BASE, 0.02)
+        hm.decode_one(1)
+        ts[name] = _median_s(lambda: hm.decode_one(2), 3)
+        hm.close()
+    t_conv, t_gqa = ts["ca"] - ts["a"], ts["ca"] - ts["c"]
+    t_head = ts["c"] + ts["a"] - ts["ca"]
+    nc = sum(1 for k in LFM25["layer_kinds"] if k == 0)
+    t_tok = nc * t_conv + (LFM25["n_layers"] - nc) * t_gqa + t_head
+    out["hybrid_lfm25_q4_0_decode"] = {
+        "tok_s": round(1.0 / t_tok, 3), "ms_per_token": round(t_tok * 1e3, 1),
+        "sample": f"median of 3 decode steps of 1- and 2-layer models at full widths: conv "
+                  f"layer {t_conv * 1e3:.1f} ms, GQA layer {t_gqa * 1e3:.1f} ms, head "
+                  f"{t_head * 1e3:.1f} ms; a token = {nc} conv + {LFM25['n_layers'] - nc} GQA "
+                  "layers + head"}
     out["seconds"] = round(time.perf_counter() - t0, 1)
     O.set_threads(16)
     return out

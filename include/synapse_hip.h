@@ -561,6 +561,46 @@ syn_status_t syn_hip_mamba_decode_timed(syn_hip_mamba_t *m, size_t steps, float 
 syn_status_t syn_hip_mamba_set_options(syn_hip_mamba_t *m, int fused, int graph);
 syn_status_t syn_hip_mamba_destroy(syn_hip_mamba_t *m);
 
+/* -- Hybrid LFM2.5 decoder, Q4 decode path: HybridModel::decode_one
+ *    (models/ssm/hybrid/model.rs:240-290) over LIV conv and GQA layers
+ *    (layer.rs:593-654, 878-954, 1055-1078) after quantize_for_decode: every
+ *    projection a Q4_0 GEMV (q4_0GemvRow), the lm_head tied to the f32
+ *    embedding.  layer_kinds[l]: 0 = LIV conv (double-gated, in_proj rows
+ *    [B | C | x]), 1 = GQA with q/k head norms.  The reference's Metal decode
+ *    counterpart is metal/hybrid_gpu_forward.rs:16 (hybrid_forward_all_layers);
+ *    its prompt goes through the CPU f32 forward first, this decoder feeds a
+ *    prompt through the decode step.  max_seq bounds prompt + generated
+ *    tokens (<= 32768). -- */
+typedef struct {
+  uint32_t hidden, n_layers, vocab, n_heads, n_kv_heads, head_dim, inner, conv_kernel, inter,
+      max_seq;
+  float eps, rope_theta;
+  int32_t conv_bias;
+  uint8_t layer_kinds[64];
+} syn_hip_hlm_config;
+
+typedef struct syn_hip_hlm_s syn_hip_hlm_t;
+syn_status_t syn_hip_hlm_create(const syn_hip_hlm_config *cfg, syn_hip_hlm_t **out);
+/* synthetic weights (the oracle's orc_hlm_init_synthetic spec) */
+syn_status_t syn_hip_hlm_init_synthetic(syn_hip_hlm_t *m, uint64_t seed_base, float stddev);
+/* conv states to zero, position 0 */
+syn_status_t syn_hip_hlm_reset(syn_hip_hlm_t *m);
+syn_status_t syn_hip_hlm_position(syn_hip_hlm_t *m, size_t *pos);
+/* HybridModel::decode_one: logits of `token` at the current position */
+syn_status_t syn_hip_hlm_decode_one(syn_hip_hlm_t *m, uint32_t token, float *host_logits);
+/* decode_one over ids[0..n); host_logits (may be null) of the last */
+syn_status_t syn_hip_hlm_prefill(syn_hip_hlm_t *m, const uint32_t *ids, size_t n,
+                                 float *host_logits);
+/* greedy: the prompt through decode_one, then max_new argmax tokens
+ * (last maximum wins) with their top1 - top2 margins */
+syn_status_t syn_hip_hlm_generate(syn_hip_hlm_t *m, const uint32_t *prompt, size_t n_prompt,
+                                  size_t max_new, uint32_t *out_tokens, float *out_margins);
+/* hipEvent time of `steps` greedy decode steps from the current state */
+syn_status_t syn_hip_hlm_decode_timed(syn_hip_hlm_t *m, size_t steps, float *elapsed_ms);
+/* graph != 0 (the default): replay a captured HIP graph of the step */
+syn_status_t syn_hip_hlm_set_options(syn_hip_hlm_t *m, int graph);
+syn_status_t syn_hip_hlm_destroy(syn_hip_hlm_t *m);
+
 /* -- harness helpers (no reference counterpart) -- */
 /* Encode f32 [n,k] into Q8_0 / Q4_K / Q6_K block bytes.  The reference has no
  * encoder for these formats (only dequantizers); any encoding is valid since

@@ -140,6 +140,14 @@ def _declare(L):
         "orc_mamba_prefill": (C.c_int, [P, P, SZ, P]),
         "orc_mamba_decode_one": (C.c_int, [P, C.c_uint32, P]),
         "orc_mamba_generate": (C.c_int, [P, P, SZ, SZ, P, P]),
+        "orc_hlm_create": (P, [P]),
+        "orc_hlm_destroy": (None, [P]),
+        "orc_hlm_init_synthetic": (C.c_int, [P, C.c_uint64, C.c_float]),
+        "orc_hlm_reset": (None, [P]),
+        "orc_hlm_pos": (SZ, [P]),
+        "orc_hlm_conv_step": (None, [P, SZ, SZ, P, P, P, P]),
+        "orc_hlm_decode_one": (C.c_int, [P, C.c_uint32, P]),
+        "orc_hlm_generate": (C.c_int, [P, P, SZ, SZ, P, P]),
         "orc_softplus": (C.c_float, [C.c_float]),
         "orc_conv1d_step": (None, [P, P, P, P, SZ, SZ, P]),
         "orc_set_threads": (None, [C.c_int]),
@@ -630,6 +638,87 @@ class CausalLM:
             self.close()
         except Exception:
             pass
+
+
+class HlmCfg(C.Structure):
+    _fields_ = [("hidden", SZ), ("n_layers", SZ), ("vocab", SZ), ("n_heads", SZ),
+                ("n_kv_heads", SZ), ("head_dim", SZ), ("inner", SZ), ("conv_kernel", SZ),
+                ("inter", SZ), ("max_seq", SZ), ("eps", C.c_float), ("rope_theta", C.c_float),
+                ("conv_bias", C.c_int), ("layer_kinds", C.c_uint8 * 64)]
+
+
+# LFM2.5-350M (models/ssm/hybrid/config.rs:132-156): C = LIV conv (0), A = GQA (1)
+LFM25_KINDS = [0, 0, 1, 0, 0, 1, 0, 0, 1, 0, 1, 0, 1, 0, 1, 0]
+LFM25_350M = dict(hidden=1024, n_layers=16, vocab=65536, n_heads=16, n_kv_heads=8, head_dim=64,
+                  inner=1024, conv_kernel=3, inter=6656, eps=1e-5, rope_theta=1e6,
+                  layer_kinds=LFM25_KINDS)
+
+
+def hlm_cfg(cfg: dict) -> HlmCfg:
+    kinds = (C.c_uint8 * 64)(*cfg["layer_kinds"])
+    return HlmCfg(cfg["hidden"], cfg["n_layers"], cfg["vocab"], cfg["n_heads"],
+                  cfg["n_kv_heads"], cfg["head_dim"], cfg["inner"], cfg["conv_kernel"],
+                  cfg["inter"], cfg["max_seq"], cfg.get("eps", 1e-5), cfg.get("rope_theta", 1e6),
+                  int(cfg.get("conv_bias", 0)), kinds)
+
+
+class HybridLM:
+    """Hybrid LFM2.5 decoder, Q4 decode path (models/ssm/hybrid) restated in C."""
+
+    def __init__(self, cfg: dict):
+        self.cfg = cfg
+        self._c = hlm_cfg(cfg)
+        self.h = lib().orc_hlm_create(C.byref(self._c))
+        if not self.h:
+            raise ValueError("orc_hlm_create: unsupported configuration")
+
+    def init_synthetic(self, seed_base: int = 0x5EED0000, std: float = 0.02):
+        if lib().orc_hlm_init_synthetic(self.h, seed_base, std):
+            raise RuntimeError("orc_hlm_init_synthetic failed")
+
+    def reset(self):
+        lib().orc_hlm_reset(self.h)
+
+    @property
+    def pos(self) -> int:
+        return lib().orc_hlm_pos(self.h)
+
+    def decode_one(self, token: int):
+        out = np.empty(self.cfg["vocab"], np.float32)
+        if lib().orc_hlm_decode_one(self.h, int(token), _p(out)):
+            raise RuntimeError("orc_hlm_decode_one failed (cache full?)")
+        return out
+
+    def generate(self, prompt, max_new: int):
+        prompt = np.ascontiguousarray(prompt, np.uint32)
+        toks = np.zeros(max_new, np.uint32)
+        margins = np.zeros(max_new, np.float32)
+        if lib().orc_hlm_generate(self.h, _p(prompt), prompt.size, max_new, _p(toks),
+                                  _p(margins)):
+            raise RuntimeError("orc_hlm_generate failed")
+        return toks, margins
+
+    def close(self):
+        if self.h:
+            lib().orc_hlm_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def hlm_conv_step(proj, inner: int, ck: int, state, w, bias=None):
+    """orc_hlm_conv_step: one LIV double-gated conv step; updates `state` in place."""
+    proj = np.ascontiguousarray(proj, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty(inner, np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    lib().orc_hlm_conv_step(_p(proj), inner, ck, _p(state), _p(w), None if b is None else _p(b),
+                            _p(out))
+    return out
 
 
 class QuantizedMamba:

@@ -1878,3 +1878,286 @@ void orc_ternary_forward(const uint8_t *blocks, size_t n, size_t k, const float 
     }
   }
 }
+
+/* ---- Hybrid LFM2.5 decoder, Q4 decode path (models/ssm/hybrid/{layer,model}.rs):
+ * LIV conv and GQA layers with every projection a Q4Linear GEMV
+ * (q4_0GemvRow after quantize_for_decode, layer.rs:570-581, 832-846), the
+ * tied f32 lm_head as matmul_t (model.rs:240-290). ---- */
+struct orc_hlm {
+  orc_hlm_cfg c;
+  size_t qd, kvd, nq4;
+  float *embed, *final_nw, *rope_cos, *rope_sin;
+  float **attn_nw, **ffn_nw, **conv_w, **conv_b, **q_nw, **k_nw;
+  uint8_t **w_in, **w_out, **w_q, **w_k, **w_v, **w_o, **w_gate, **w_up, **w_down;
+  float **conv_state, **kc, **vc;
+  size_t pos;
+};
+
+orc_hlm *orc_hlm_create(const orc_hlm_cfg *cfg) {
+  if (!cfg || cfg->n_layers == 0 || cfg->n_layers > 64 || cfg->hidden % 32 ||
+      cfg->inner % 32 || cfg->inter % 32 || cfg->n_kv_heads == 0 ||
+      cfg->n_heads % cfg->n_kv_heads || cfg->head_dim % 2 || cfg->conv_kernel == 0)
+    return NULL;
+  orc_hlm *m = (orc_hlm *)calloc(1, sizeof(orc_hlm));
+  m->c = *cfg;
+  m->qd = cfg->n_heads * cfg->head_dim;
+  m->kvd = cfg->n_kv_heads * cfg->head_dim;
+  size_t L = cfg->n_layers;
+#define HLM_ARR(f, T) m->f = (T *)calloc(L, sizeof(T))
+  HLM_ARR(attn_nw, float *); HLM_ARR(ffn_nw, float *); HLM_ARR(conv_w, float *);
+  HLM_ARR(conv_b, float *); HLM_ARR(q_nw, float *); HLM_ARR(k_nw, float *);
+  HLM_ARR(w_in, uint8_t *); HLM_ARR(w_out, uint8_t *); HLM_ARR(w_q, uint8_t *);
+  HLM_ARR(w_k, uint8_t *); HLM_ARR(w_v, uint8_t *); HLM_ARR(w_o, uint8_t *);
+  HLM_ARR(w_gate, uint8_t *); HLM_ARR(w_up, uint8_t *); HLM_ARR(w_down, uint8_t *);
+  HLM_ARR(conv_state, float *); HLM_ARR(kc, float *); HLM_ARR(vc, float *);
+#undef HLM_ARR
+  size_t half = cfg->head_dim / 2;
+  m->rope_cos = (float *)malloc(cfg->max_seq * half * 4);
+  m->rope_sin = (float *)malloc(cfg->max_seq * half * 4);
+  /* model.rs:708-720: freq = 1 / theta^(2i/hd), angle = pos * freq (f32) */
+  orc_rope_tables(cfg->max_seq, cfg->head_dim, cfg->rope_theta, m->rope_cos, m->rope_sin);
+  return m;
+}
+
+void orc_hlm_destroy(orc_hlm *m) {
+  if (!m) return;
+  for (size_t l = 0; l < m->c.n_layers; l++) {
+    free(m->attn_nw[l]); free(m->ffn_nw[l]); free(m->conv_w[l]); free(m->conv_b[l]);
+    free(m->q_nw[l]); free(m->k_nw[l]); free(m->w_in[l]); free(m->w_out[l]);
+    free(m->w_q[l]); free(m->w_k[l]); free(m->w_v[l]); free(m->w_o[l]);
+    free(m->w_gate[l]); free(m->w_up[l]); free(m->w_down[l]);
+    free(m->conv_state[l]); free(m->kc[l]); free(m->vc[l]);
+  }
+  free(m->attn_nw); free(m->ffn_nw); free(m->conv_w); free(m->conv_b); free(m->q_nw);
+  free(m->k_nw); free(m->w_in); free(m->w_out); free(m->w_q); free(m->w_k); free(m->w_v);
+  free(m->w_o); free(m->w_gate); free(m->w_up); free(m->w_down); free(m->conv_state);
+  free(m->kc); free(m->vc);
+  free(m->embed); free(m->final_nw); free(m->rope_cos); free(m->rope_sin);
+  free(m);
+}
+
+/* Q4Linear::from_f32 + pack_for_zig of an N(0, std) [n][k] tensor */
+static uint8_t *hlm_q4(size_t n, size_t k, uint64_t seed, float std) {
+  float *w = (float *)malloc(n * k * 4);
+  orc_fill_normal(w, n * k, seed, std);
+  uint8_t *p = (uint8_t *)malloc(orc_q4_packed_bytes(n, k));
+  orc_q4_from_f32_packed(w, n, k, p);
+  free(w);
+  return p;
+}
+
+/* norm gains 1 + N(0, 0.1) */
+static float *hlm_gain(size_t n, uint64_t seed) {
+  float *g = (float *)malloc(n * 4);
+  orc_fill_normal(g, n, seed, 0.1f);
+  for (size_t i = 0; i < n; i++) g[i] = 1.0f + g[i];
+  return g;
+}
+
+/* Synthetic weights (harness spec, shared with the device):
+ * embed (= tied lm_head) tensor 0 ~ N(0, std); layer l, seeds s = seed_base
+ * + 1 + 16 l: conv: in_proj s+0, conv taps s+1, out_proj s+2, conv bias
+ * s+3 (if enabled); GQA: q s+0, k s+1, v s+2, o s+3, q/k norm gains s+6,
+ * s+7; both: attn/ffn norm gains s+8, s+9, gate s+10, up s+11, down s+12
+ * (projections ~ N(0, std), Q4-quantized; gains 1 + N(0, 0.1)); final norm
+ * gain seed_base + 1 + 16 L. */
+int orc_hlm_init_synthetic(orc_hlm *m, uint64_t seed_base, float std) {
+  const orc_hlm_cfg *c = &m->c;
+  size_t H = c->hidden, I = c->inner, ck = c->conv_kernel, F = c->inter;
+  m->embed = (float *)malloc(c->vocab * H * 4);
+  orc_fill_normal(m->embed, c->vocab * H, seed_base, std);
+  for (size_t l = 0; l < c->n_layers; l++) {
+    uint64_t s = seed_base + 1 + 16 * l;
+    if (c->layer_kinds[l] == 0) {
+      m->w_in[l] = hlm_q4(3 * I, H, s + 0, std);
+      m->conv_w[l] = (float *)malloc(I * ck * 4);
+      orc_fill_normal(m->conv_w[l], I * ck, s + 1, std);
+      m->w_out[l] = hlm_q4(H, I, s + 2, std);
+      if (c->conv_bias) {
+        m->conv_b[l] = (float *)malloc(I * 4);
+        orc_fill_normal(m->conv_b[l], I, s + 3, std);
+      }
+      m->conv_state[l] = (float *)calloc(I * ck, 4);
+    } else {
+      m->w_q[l] = hlm_q4(m->qd, H, s + 0, std);
+      m->w_k[l] = hlm_q4(m->kvd, H, s + 1, std);
+      m->w_v[l] = hlm_q4(m->kvd, H, s + 2, std);
+      m->w_o[l] = hlm_q4(H, m->qd, s + 3, std);
+      m->q_nw[l] = hlm_gain(c->head_dim, s + 6);
+      m->k_nw[l] = hlm_gain(c->head_dim, s + 7);
+      m->kc[l] = (float *)calloc(c->max_seq * m->kvd, 4);
+      m->vc[l] = (float *)calloc(c->max_seq * m->kvd, 4);
+    }
+    m->attn_nw[l] = hlm_gain(H, s + 8);
+    m->ffn_nw[l] = hlm_gain(H, s + 9);
+    m->w_gate[l] = hlm_q4(F, H, s + 10, std);
+    m->w_up[l] = hlm_q4(F, H, s + 11, std);
+    m->w_down[l] = hlm_q4(H, F, s + 12, std);
+  }
+  m->final_nw = hlm_gain(H, seed_base + 1 + 16 * c->n_layers);
+  m->pos = 0;
+  return ORC_OK;
+}
+
+void orc_hlm_reset(orc_hlm *m) {
+  for (size_t l = 0; l < m->c.n_layers; l++)
+    if (m->conv_state[l]) memset(m->conv_state[l], 0, m->c.inner * m->c.conv_kernel * 4);
+  m->pos = 0;
+}
+size_t orc_hlm_pos(const orc_hlm *m) { return m->pos; }
+
+/* layer.rs:25-42 conv1d_step_single over every channel of the double-gated
+ * LIV conv (layer.rs:609-627): proj = [B | C | x], conv input B*x, output
+ * C * (sum_j buf[j] w[j] (+ bias)).  The state row of a channel holds its
+ * last `ck` inputs, oldest first. */
+void orc_hlm_conv_step(const float *proj, size_t inner, size_t ck, float *state,
+                       const float *w, const float *bias, float *out) {
+  for (size_t i = 0; i < inner; i++) {
+    float b_gate = proj[i], c_gate = proj[inner + i], x_sig = proj[2 * inner + i];
+    float bx = b_gate * x_sig;
+    float *buf = state + i * ck;
+    memmove(buf, buf + 1, (ck - 1) * 4);
+    buf[ck - 1] = bx;
+    /* Iterator::sum of f32 folds from -0.0 */
+    float sum = -0.0f;
+    for (size_t j = 0; j < ck; j++) {
+      float t = buf[j] * w[i * ck + j];
+      sum = sum + t;
+    }
+    float cv = bias ? sum + bias[i] : sum;
+    out[i] = c_gate * cv;
+  }
+}
+
+/* layer.rs:865-876: per head, scale = 1/sqrt(sum x^2 / hd + eps), x *= w * scale */
+static void hlm_head_norm(float *data, const float *w, size_t heads, size_t hd, float eps) {
+  for (size_t h = 0; h < heads; h++) {
+    float *d = data + h * hd;
+    float s = -0.0f;
+    for (size_t j = 0; j < hd; j++) {
+      float t = d[j] * d[j];
+      s = s + t;
+    }
+    float scale = 1.0f / sqrtf(s / (float)hd + eps);
+    for (size_t j = 0; j < hd; j++) d[j] = d[j] * (w[j] * scale);
+  }
+}
+
+/* residual add (layer.rs:640-641, 1068-1069: h + a) */
+static void hlm_add(float *x, const float *d, size_t n) {
+  for (size_t i = 0; i < n; i++) x[i] = x[i] + d[i];
+}
+
+/* layer.rs:80-101 swiglu_ffn_forward_q4 with m = 1 */
+static void hlm_ffn(orc_hlm *m, size_t l, const float *x, float *out) {
+  size_t H = m->c.hidden, F = m->c.inter;
+  float *normed = (float *)malloc(H * 4), *g = (float *)malloc(F * 4), *u = (float *)malloc(F * 4);
+  orc_rmsnorm_seq(x, m->ffn_nw[l], m->c.eps, H, normed);
+  orc_q4_0_gemv(F, H, normed, m->w_gate[l], g);
+  orc_q4_0_gemv(F, H, normed, m->w_up[l], u);
+  for (size_t i = 0; i < F; i++) g[i] = orc_silu(g[i]) * u[i];
+  orc_q4_0_gemv(H, F, g, m->w_down[l], out);
+  free(normed); free(g); free(u);
+}
+
+/* layer.rs:593-654 LivConvDecoderLayer::forward_one (double-gated) */
+static void hlm_conv_layer(orc_hlm *m, size_t l, float *x) {
+  size_t H = m->c.hidden, I = m->c.inner;
+  float *normed = (float *)malloc(H * 4), *proj = (float *)malloc(3 * I * 4);
+  float *co = (float *)malloc(I * 4), *o = (float *)malloc(H * 4);
+  orc_rmsnorm_seq(x, m->attn_nw[l], m->c.eps, H, normed);
+  orc_q4_0_gemv(3 * I, H, normed, m->w_in[l], proj);
+  orc_hlm_conv_step(proj, I, m->c.conv_kernel, m->conv_state[l], m->conv_w[l], m->conv_b[l], co);
+  orc_q4_0_gemv(H, I, co, m->w_out[l], o);
+  hlm_add(x, o, H);
+  hlm_ffn(m, l, x, o);
+  hlm_add(x, o, H);
+  free(normed); free(proj); free(co); free(o);
+}
+
+/* layer.rs:878-954 attn_forward_one + :1055-1078 forward_one */
+static void hlm_gqa_layer(orc_hlm *m, size_t l, float *x) {
+  const orc_hlm_cfg *c = &m->c;
+  size_t H = c->hidden, hd = c->head_dim, nq = c->n_heads, nkv = c->n_kv_heads;
+  size_t qd = m->qd, kvd = m->kvd, pos = m->pos, seq = pos + 1;
+  float *normed = (float *)malloc(H * 4), *q = (float *)malloc(qd * 4);
+  float *k = (float *)malloc(kvd * 4), *v = (float *)malloc(kvd * 4);
+  float *att = (float *)malloc(qd * 4), *o = (float *)malloc(H * 4);
+  float *scores = (float *)malloc(seq * 4);
+  orc_rmsnorm_seq(x, m->attn_nw[l], c->eps, H, normed);
+  orc_q4_0_gemv(qd, H, normed, m->w_q[l], q);
+  orc_q4_0_gemv(kvd, H, normed, m->w_k[l], k);
+  orc_q4_0_gemv(kvd, H, normed, m->w_v[l], v);
+  hlm_head_norm(q, m->q_nw[l], nq, hd, c->eps);
+  hlm_head_norm(k, m->k_nw[l], nkv, hd, c->eps);
+  orc_rope_apply(q, m->rope_cos, m->rope_sin, 1, nq, hd, pos);
+  orc_rope_apply(k, m->rope_cos, m->rope_sin, 1, nkv, hd, pos);
+  memcpy(m->kc[l] + pos * kvd, k, kvd * 4);
+  memcpy(m->vc[l] + pos * kvd, v, kvd * 4);
+  size_t group = nq / nkv;
+  float scale = 1.0f / sqrtf((float)hd);
+  for (size_t qh = 0; qh < nq; qh++) {
+    size_t kvh = qh / group;
+    for (size_t p = 0; p < seq; p++) {
+      const float *kp = m->kc[l] + p * kvd + kvh * hd;
+      float dot = 0.0f;
+      for (size_t d = 0; d < hd; d++) {
+        float t = q[qh * hd + d] * kp[d];
+        dot = dot + t;
+      }
+      scores[p] = dot * scale;
+    }
+    orc_softmax_slice(scores, seq);
+    for (size_t d = 0; d < hd; d++) {
+      float val = 0.0f;
+      for (size_t p = 0; p < seq; p++) {
+        float t = scores[p] * m->vc[l][p * kvd + kvh * hd + d];
+        val = val + t;
+      }
+      att[qh * hd + d] = val;
+    }
+  }
+  orc_q4_0_gemv(H, qd, att, m->w_o[l], o);
+  hlm_add(x, o, H);
+  hlm_ffn(m, l, x, o);
+  hlm_add(x, o, H);
+  free(normed); free(q); free(k); free(v); free(att); free(o); free(scores);
+}
+
+/* model.rs:240-290 decode_one (LFM2.5: no embedding norm) */
+int orc_hlm_decode_one(orc_hlm *m, uint32_t token, float *logits) {
+  const orc_hlm_cfg *c = &m->c;
+  size_t H = c->hidden;
+  if (m->pos >= c->max_seq) return ORC_ERR_INVALID_ARG;
+  float *x = (float *)calloc(H, 4), *normed = (float *)malloc(H * 4);
+  if (token < c->vocab) memcpy(x, m->embed + (size_t)token * H, H * 4);
+  for (size_t l = 0; l < c->n_layers; l++) {
+    if (c->layer_kinds[l] == 0) hlm_conv_layer(m, l, x);
+    else hlm_gqa_layer(m, l, x);
+  }
+  m->pos++;
+  orc_rmsnorm_seq(x, m->final_nw, c->eps, H, normed);
+  memset(logits, 0, c->vocab * 4);
+  orc_sgemm(1, c->vocab, H, normed, H, 0, m->embed, H, 1, logits, c->vocab);
+  free(x); free(normed);
+  return ORC_OK;
+}
+
+/* greedy generation: decode_one over the prompt, then argmax feedback */
+int orc_hlm_generate(orc_hlm *m, const uint32_t *prompt, size_t n_prompt, size_t max_new,
+                     uint32_t *out_tokens, float *out_margins) {
+  float *lg = (float *)malloc(m->c.vocab * 4);
+  int rc = ORC_OK;
+  for (size_t i = 0; i < n_prompt && rc == ORC_OK; i++) rc = orc_hlm_decode_one(m, prompt[i], lg);
+  for (size_t t = 0; t < max_new && rc == ORC_OK; t++) {
+    uint32_t tok = orc_argmax(lg, m->c.vocab);
+    float second = -INFINITY;
+    for (size_t i = 0; i < m->c.vocab; i++)
+      if (i != tok && lg[i] > second) second = lg[i];
+    out_tokens[t] = tok;
+    if (out_margins) out_margins[t] = lg[tok] - second;
+    if (t + 1 < max_new) rc = orc_hlm_decode_one(m, tok, lg);
+  }
+  free(lg);
+  return rc;
+}

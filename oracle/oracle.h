@@ -197,6 +197,29 @@ void orc_ternary_from_f32(const float *w, size_t n, size_t k, uint8_t *blocks);
 void orc_ternary_forward(const uint8_t *blocks, size_t n, size_t k, const float *x, size_t m,
                          float *y);
 
+
+/* ---- Hybrid LFM2.5 decoder, Q4 decode path (models/ssm/hybrid): layer
+ * kinds 0 = LIV conv (double-gated), 1 = GQA; every projection a Q4 GEMV,
+ * the lm_head tied to the f32 embedding. ---- */
+typedef struct {
+  size_t hidden, n_layers, vocab, n_heads, n_kv_heads, head_dim, inner, conv_kernel, inter,
+      max_seq;
+  float eps, rope_theta;
+  int conv_bias;
+  uint8_t layer_kinds[64];
+} orc_hlm_cfg;
+typedef struct orc_hlm orc_hlm;
+orc_hlm *orc_hlm_create(const orc_hlm_cfg *cfg);
+void orc_hlm_destroy(orc_hlm *m);
+int orc_hlm_init_synthetic(orc_hlm *m, uint64_t seed_base, float std);
+void orc_hlm_reset(orc_hlm *m);
+size_t orc_hlm_pos(const orc_hlm *m);
+void orc_hlm_conv_step(const float *proj, size_t inner, size_t ck, float *state,
+                       const float *w, const float *bias, float *out);
+int orc_hlm_decode_one(orc_hlm *m, uint32_t token, float *logits);
+int orc_hlm_generate(orc_hlm *m, const uint32_t *prompt, size_t n_prompt, size_t max_new,
+                     uint32_t *out_tokens, float *out_margins);
+
 #ifdef __cplusplus
 }
 #endif

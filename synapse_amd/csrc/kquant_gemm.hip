@@ -633,10 +633,16 @@ constexpr int KR_AFTER = KR_ADMA + KR_WCH / 4 + 1;
 // (lds_addr wave-uniform).  Issued as inline assembly so that the compiler's
 // memory-counter bookkeeping does not see it: it would otherwise wait for
 // every direct load before the next LDS read it cannot prove disjoint from
-// it.  kr_publish waits for these loads explicitly.
+// it.  kr_publish waits for these loads explicitly.  M0 (the LDS address)
+// is a reserved register: the statement restores its value.
 __device__ __forceinline__ void kr_dma(const void *src, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr)
-               : "memory", "m0");
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\ts_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(src), "s"(lds_addr)
+      : "memory");
 }
 
 // Wait until this wave's direct loads of the next stage have landed (the

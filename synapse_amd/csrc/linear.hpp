@@ -91,6 +91,9 @@ struct QLinearQ4_0 {
   size_t xh_elems = 0;
   syn_status_t upload_packed(const uint8_t *packed, size_t n_, size_t k_);
   syn_status_t from_f32(const float *w_nk, size_t n_, size_t k_);
+  // allocate the split-K partials of GEMV batches up to max_m rows (so that
+  // gemv() allocates nothing, e.g. under HIP graph capture)
+  syn_status_t prepare(size_t max_m);
   size_t weight_bytes() const { return n * (k / 32) * 18; }
   // y[m,n] = x[m,k] W^T, f32 activations; m > 16 runs gemm() when gemm_ok()
   syn_status_t gemv(size_t m, const float *d_x, size_t ldx, float *d_y, size_t ldy,

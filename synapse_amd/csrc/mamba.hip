@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "decode_fused.hpp"
+#include "f32_ops.hpp"
 #include "layer_ops.hpp"
 #include "linear.hpp"
 #include "reduce_order.hpp"
@@ -213,13 +214,13 @@ __global__ void __launch_bounds__(1024)
 
 // floats the activation buffer of a K-long exact f32 GEMV must hold (whole
 // passes; the pad is read but never used)
-static size_t f32_exact_x_elems(size_t K) {
+size_t f32_exact_x_elems(size_t K) {
   const size_t per_pass = (size_t)kChainWaves * kChainG * 4;
   return cdiv(K, per_pass) * per_pass;
 }
 
-static syn_status_t launch_gemv_f32_exact(const float *Wp, const float *x, size_t x_elems, int N,
-                                          int K, int n8, float *y, hipStream_t s) {
+syn_status_t launch_gemv_f32_exact(const float *Wp, const float *x, size_t x_elems, int N, int K,
+                                   int n8, float *y, hipStream_t s) {
   if (x_elems < f32_exact_x_elems((size_t)K)) {
     set_error("f32 GEMV: activation buffer shorter than the padded row");
     return SYN_ERR_INVALID_ARG;
@@ -443,7 +444,7 @@ __global__ void __launch_bounds__(256)
 }
 
 // [n,k] -> [panel][k/4][64][4] (k padded with zeros to a multiple of 4)
-static std::vector<float> to_panels(const float *w_nk, size_t n, size_t k) {
+std::vector<float> to_panels(const float *w_nk, size_t n, size_t k) {
   const size_t P = cdiv(n, 64), K4 = cdiv(k, 4);
   std::vector<float> out(P * K4 * 64 * 4, 0.0f);
   for (size_t r = 0; r < n; r++)
@@ -460,9 +461,19 @@ static std::vector<float> channel_minor(const float *a, size_t n_ch, size_t m) {
   return out;
 }
 
-static int n8_of(int n) {
+int n8_of(int n) {
   const int n32 = n - n % 32;
   return n32 + ((n - n32) / 8) * 8;
+}
+
+syn_status_t launch_rmsnorm_seq(float *x, const float *delta, const float *w, float eps, int H,
+                                float *normed, hipStream_t s) {
+  RowSrc d;
+  d.f = delta;
+  hipLaunchKernelGGL(k_mamba_norm, dim3(1), dim3(256), round_up((size_t)H, 4) * 8, s, x, d, w, eps,
+                     H, nullptr, nullptr, normed);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
 }
 
 }  // namespace syn

@@ -341,6 +341,17 @@ syn_status_t QLinearQ4_0::gemv(size_t m, const float *d_x, size_t ldx, float *d_
   return SYN_OK;
 }
 
+syn_status_t QLinearQ4_0::prepare(size_t max_m) {
+  const GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
+  const size_t need = (size_t)p.ksplit * std::min<size_t>(8, max_m) * (size_t)p.panels * 64;
+  if (p.ksplit > 1 && part_elems < need) {
+    part_elems = need;
+    SYN_HIP(hipDeviceSynchronize());
+    SYN_TRY(part.alloc(part_elems * sizeof(float)));
+  }
+  return SYN_OK;
+}
+
 syn_status_t QLinearQ4_0::upload_packed(const uint8_t *packed, size_t n_, size_t k_) {
   n = n_;
   k = k_;

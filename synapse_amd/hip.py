@@ -53,6 +53,14 @@ class MambaConfig(C.Structure):
                 ("int8_xdt", C.c_int32)]
 
 
+class HybridConfig(C.Structure):
+    _fields_ = [("hidden", C.c_uint32), ("n_layers", C.c_uint32), ("vocab", C.c_uint32),
+                ("n_heads", C.c_uint32), ("n_kv_heads", C.c_uint32), ("head_dim", C.c_uint32),
+                ("inner", C.c_uint32), ("conv_kernel", C.c_uint32), ("inter", C.c_uint32),
+                ("max_seq", C.c_uint32), ("eps", C.c_float), ("rope_theta", C.c_float),
+                ("conv_bias", C.c_int32), ("layer_kinds", C.c_uint8 * 64)]
+
+
 SIGNATURES = {
     "syn_quantize_per_channel_int8": (ST, [P, SZ, SZ, P, P]),
     "syn_qgemm_int8": (ST, [SZ, SZ, SZ, P, SZ, P, SZ, P, SZ, P, P]),
@@ -172,6 +180,16 @@ SIGNATURES = {
     "syn_hip_mamba_decode_timed": (ST, [P, SZ, C.POINTER(C.c_float)]),
     "syn_hip_mamba_set_options": (ST, [P, C.c_int, C.c_int]),
     "syn_hip_mamba_destroy": (ST, [P]),
+    "syn_hip_hlm_create": (ST, [C.POINTER(HybridConfig), C.POINTER(P)]),
+    "syn_hip_hlm_init_synthetic": (ST, [P, C.c_uint64, C.c_float]),
+    "syn_hip_hlm_reset": (ST, [P]),
+    "syn_hip_hlm_position": (ST, [P, C.POINTER(SZ)]),
+    "syn_hip_hlm_decode_one": (ST, [P, C.c_uint32, P]),
+    "syn_hip_hlm_prefill": (ST, [P, P, SZ, P]),
+    "syn_hip_hlm_generate": (ST, [P, P, SZ, SZ, P, P]),
+    "syn_hip_hlm_decode_timed": (ST, [P, SZ, C.POINTER(C.c_float)]),
+    "syn_hip_hlm_set_options": (ST, [P, C.c_int]),
+    "syn_hip_hlm_destroy": (ST, [P]),
     "syn_hip_fill_normal": (ST, [P, SZ, C.c_uint64, C.c_float]),
     "syn_hip_probe_mfma": (ST, [C.c_int, SZ, C.POINTER(C.c_double)]),
     "syn_hip_probe_hbm_read": (ST, [SZ, C.POINTER(C.c_double)]),
@@ -965,6 +983,74 @@ class QuantizedMamba:
     def close(self):
         if self.h:
             lib().syn_hip_mamba_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class HybridLM:
+    """Device-resident hybrid LFM2.5 decoder, Q4 decode path (models/ssm/hybrid).
+    cfg: hidden, n_layers, vocab, n_heads, n_kv_heads, head_dim, inner,
+    conv_kernel, inter, max_seq, eps, rope_theta, conv_bias, layer_kinds
+    (0 LIV conv, 1 GQA)."""
+
+    def __init__(self, cfg: dict):
+        self.cfg = dict(cfg)
+        kinds = (C.c_uint8 * 64)(*cfg["layer_kinds"])
+        c = HybridConfig(cfg["hidden"], cfg["n_layers"], cfg["vocab"], cfg["n_heads"],
+                         cfg["n_kv_heads"], cfg["head_dim"], cfg["inner"], cfg["conv_kernel"],
+                         cfg["inter"], cfg["max_seq"], cfg.get("eps", 1e-5),
+                         cfg.get("rope_theta", 1e6), int(cfg.get("conv_bias", 0)), kinds)
+        h = C.c_void_p()
+        check(lib().syn_hip_hlm_create(C.byref(c), C.byref(h)), "hlm_create")
+        self.h = h.value
+
+    def init_synthetic(self, seed_base: int = 0x5EED0000, std: float = 0.02):
+        check(lib().syn_hip_hlm_init_synthetic(self.h, seed_base, std), "hlm_init")
+
+    def reset(self):
+        check(lib().syn_hip_hlm_reset(self.h), "hlm_reset")
+
+    @property
+    def pos(self) -> int:
+        v = C.c_size_t()
+        check(lib().syn_hip_hlm_position(self.h, C.byref(v)), "hlm_position")
+        return v.value
+
+    def decode_one(self, token: int):
+        out = np.empty(self.cfg["vocab"], np.float32)
+        check(lib().syn_hip_hlm_decode_one(self.h, int(token), ptr(out)), "hlm_decode_one")
+        return out
+
+    def prefill(self, ids):
+        ids = np.ascontiguousarray(ids, np.uint32)
+        out = np.empty(self.cfg["vocab"], np.float32)
+        check(lib().syn_hip_hlm_prefill(self.h, ptr(ids), ids.size, ptr(out)), "hlm_prefill")
+        return out
+
+    def generate(self, prompt, max_new: int):
+        prompt = np.ascontiguousarray(prompt, np.uint32)
+        toks = np.zeros(max_new, np.uint32)
+        margins = np.zeros(max_new, np.float32)
+        check(lib().syn_hip_hlm_generate(self.h, ptr(prompt), prompt.size, max_new, ptr(toks),
+                                         ptr(margins)), "hlm_generate")
+        return toks, margins
+
+    def decode_timed(self, steps: int) -> float:
+        ms = C.c_float()
+        check(lib().syn_hip_hlm_decode_timed(self.h, steps, C.byref(ms)), "hlm_decode_timed")
+        return ms.value
+
+    def set_options(self, graph: bool = True):
+        check(lib().syn_hip_hlm_set_options(self.h, int(graph)), "hlm_set_options")
+
+    def close(self):
+        if self.h:
+            lib().syn_hip_hlm_destroy(self.h)
             self.h = None
 
     def __del__(self):
