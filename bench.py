@@ -436,8 +436,8 @@ def main():
                          "(for profilers that do not follow graph launches)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py: this build measures one GPU only (the decode path is single-GPU; "
-              "sharding is described in DESIGN.md); run with --gpus 1", file=sys.stderr)
+        print("bench.py: this build measures one GPU only (the decode path runs on a single "
+              "GPU); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
     from synapse_amd import hip
@@ -501,7 +501,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": round(toks / REF_DECODE_TOKS, 2),
         "vs_baseline_ref": f"{REF_DECODE_TOKS} tok/s, reference cpu_simd Qwen3-0.6B INT8 decode "
-                           "(Apple Silicon, BASELINE.md)",
+                           "(Apple Silicon, status/benchmark_matrix.md:23)",
         "dtype": "int8",
         "data": "synthetic (random N(0,0.02) weights, random prompt ids)",
         "config": {"workload": "qwen3-0.6b-shape int8 w8a8 greedy decode after a 16-token prompt",

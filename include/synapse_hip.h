@@ -79,7 +79,7 @@ syn_status_t syn_sgemm(size_t m, size_t n, size_t k, const float *a, size_t lda,
 
 /* The four entry points above under names the reference's static Zig archive
  * (libsynapse_zig.a, which defines the unprefixed ones) does not define, so a
- * binary can link both and reach these (INTEGRATION.md). */
+ * binary can link both and reach these. */
 syn_status_t syn_hip_quantize_per_channel_int8(const float *data, size_t channels,
                                                size_t channel_size, int8_t *out,
                                                float *scales);

@@ -90,7 +90,7 @@ syn_status_t syn_sgemm(size_t m, size_t n, size_t k, const float *a, size_t lda,
 }
 
 // the same entry points under names a static reference archive does not
-// define (see INTEGRATION.md for the link route)
+// define, so a binary that links that archive can still reach these
 syn_status_t syn_hip_sgemm(size_t m, size_t n, size_t k, const float *a, size_t lda, int trans_a,
                            const float *b, size_t ldb, int trans_b, float *c, size_t ldc) {
   return syn_sgemm(m, n, k, a, lda, trans_a, b, ldb, trans_b, c, ldc);
