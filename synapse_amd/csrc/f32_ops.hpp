@@ -19,9 +19,5 @@ size_t f32_exact_x_elems(size_t K);
 // f32_exact_x_elems(K) floats
 syn_status_t launch_gemv_f32_exact(const float *Wp, const float *x, size_t x_elems, int N, int K,
                                    int n8, float *y, hipStream_t s);
-// x += delta (if delta); normed = rmsnorm(x, w, eps) with one sequential sum
-// of squares (ops/pure_rust_ops.rs:96-112); one row of H floats
-syn_status_t launch_rmsnorm_seq(float *x, const float *delta, const float *w, float eps, int H,
-                                float *normed, hipStream_t s);
 
 }  // namespace syn

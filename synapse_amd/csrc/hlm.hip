@@ -5,8 +5,8 @@
 // q4_0GemvRow kernel of q4_0.hip, f32 activations), q|k|v and gate|up
 // stacked into one handle each (their rows are independent), the lm_head the
 // tied f32 embedding in f32GemvRow order (the exact-order GEMV of mamba.hip).
-// The small ops follow the reference's float order: RMSNorm with one
-// sequential sum of squares (pure_rust_ops.rs:96-112), the double-gated conv
+// The small ops follow the reference's float order except RMSNorm's sum of
+// squares (pure_rust_ops.rs:96-112's formula, tree-ordered sum): the double-gated conv
 // step (B*x, shift, sequential tap sum, C*y), head norms with x * (w * s),
 // rotate-half RoPE, attention with sequential dot products, softmax_slice
 // and a sequential P.V, SwiGLU silu(g) * u with glibc's expf.  The Q4 GEMV
@@ -154,6 +154,39 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// x += delta (if delta); normed = (x * w) * (1 / sqrt(sum(x^2) / H + eps))
+// (pure_rust_ops.rs:96-112's formula) with the sum of squares in tree order:
+// one workgroup of 1024 threads, wave sums by shuffles, then the 16 wave
+// sums in order.  The decoder is graded by tolerance (its Q4 GEMVs sum in
+// their own order), and the sequential chain of the reference's order costs
+// a 1024-deep dependent add chain per norm.
+__global__ void __launch_bounds__(1024)
+    k_hlm_norm(float *__restrict__ x, const float *__restrict__ delta,
+               const float *__restrict__ w, float eps, int H, float *__restrict__ normed) {
+  __shared__ float red[16];
+  const int tid = threadIdx.x;
+  float ss = 0.0f;
+  for (int j = tid; j < H; j += 1024) {
+    float v = x[j];
+    if (delta) {
+      v = v + delta[j];
+      x[j] = v;
+    }
+    ss = __builtin_fmaf(v, v, ss);
+  }
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  float tot = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; i++) tot += red[i];
+  const float scale = 1.0f / sqrtf(tot / (float)H + eps);
+  for (int j = tid; j < H; j += 1024) {
+    const float t = x[j] * w[j];
+    normed[j] = t * scale;
+  }
+}
+
 // layer.rs:99: h = silu(gate) * up over the stacked [gate | up] row
 __global__ void __launch_bounds__(256)
     k_hlm_swiglu(const float *__restrict__ gu, int F, float *__restrict__ h) {
@@ -164,6 +197,13 @@ __global__ void __launch_bounds__(256)
 }  // namespace syn
 
 using namespace syn;
+
+static syn_status_t launch_hlm_norm(float *x, const float *delta, const float *w, float eps, int H,
+                                   float *normed, hipStream_t s) {
+  hipLaunchKernelGGL(k_hlm_norm, dim3(1), dim3(1024), 0, s, x, delta, w, eps, H, normed);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
 
 struct syn_hip_hlm_s {
   syn_hip_hlm_config c{};
@@ -195,7 +235,7 @@ struct syn_hip_hlm_s {
     SYN_TRY(launch_embed(embed.as<float>(), &st()->token, 1, (int)H, (int)V, x.as<float>(), s));
     for (size_t l = 0; l < L; l++) {
       Layer &Ly = layers[l];
-      SYN_TRY(launch_rmsnorm_seq(x.as<float>(), l == 0 ? nullptr : down.as<float>(),
+      SYN_TRY(launch_hlm_norm(x.as<float>(), l == 0 ? nullptr : down.as<float>(),
                                  Ly.attn_nw.as<float>(), eps, (int)H, normed.as<float>(), s));
       if (Ly.kind == 0) {
         SYN_TRY(Ly.in.gemv(1, normed.as<float>(), H, proj.as<float>(), 3 * I, s));
@@ -219,7 +259,7 @@ struct syn_hip_hlm_s {
         SYN_LAUNCH_CHECK();
         SYN_TRY(Ly.o.gemv(1, attn.as<float>(), qd, o.as<float>(), H, s));
       }
-      SYN_TRY(launch_rmsnorm_seq(x.as<float>(), o.as<float>(), Ly.ffn_nw.as<float>(), eps,
+      SYN_TRY(launch_hlm_norm(x.as<float>(), o.as<float>(), Ly.ffn_nw.as<float>(), eps,
                                  (int)H, normed.as<float>(), s));
       SYN_TRY(Ly.gu.gemv(1, normed.as<float>(), H, gu.as<float>(), 2 * F, s));
       hipLaunchKernelGGL(k_hlm_swiglu, dim3((unsigned)cdiv(F, 256)), dim3(256), 0, s,
@@ -227,7 +267,7 @@ struct syn_hip_hlm_s {
       SYN_LAUNCH_CHECK();
       SYN_TRY(Ly.down.gemv(1, hbuf.as<float>(), F, down.as<float>(), H, s));
     }
-    SYN_TRY(launch_rmsnorm_seq(x.as<float>(), down.as<float>(), final_nw.as<float>(), eps, (int)H,
+    SYN_TRY(launch_hlm_norm(x.as<float>(), down.as<float>(), final_nw.as<float>(), eps, (int)H,
                                normed.as<float>(), s));
     SYN_TRY(launch_gemv_f32_exact(lm_p.as<float>(), normed.as<float>(), normed.bytes / 4, (int)V,
                                   (int)H, n8_of((int)V), logits.as<float>(), s));

@@ -466,16 +466,6 @@ int n8_of(int n) {
   return n32 + ((n - n32) / 8) * 8;
 }
 
-syn_status_t launch_rmsnorm_seq(float *x, const float *delta, const float *w, float eps, int H,
-                                float *normed, hipStream_t s) {
-  RowSrc d;
-  d.f = delta;
-  hipLaunchKernelGGL(k_mamba_norm, dim3(1), dim3(256), round_up((size_t)H, 4) * 8, s, x, d, w, eps,
-                     H, nullptr, nullptr, normed);
-  SYN_LAUNCH_CHECK();
-  return SYN_OK;
-}
-
 }  // namespace syn
 
 struct syn_hip_mamba_s {
