@@ -29,17 +29,28 @@
 
 namespace syn {
 
+// Output row `row` of a Q4_0 GEMV from its split-K partials (PartRows):
+// summed from 0.0f in slice order, the reduce kernel's order, so a consumer
+// that reads the partials sees the values the reduce launch would write.
+__device__ __forceinline__ float part_row(const PartRows &r, int row) {
+  if (r.ks == 1) return r.p[row];
+  float s = 0.0f;
+  for (int k = 0; k < r.ks; k++) s += r.p[(size_t)k * r.stride + row];
+  return s;
+}
+
 // layer.rs:25-42 conv1d_step_single over the double-gated LIV conv
 // (layer.rs:609-627): proj = [B | C | x]; the channel's state row holds its
 // last ck inputs B*x, oldest first; out = C * (sum_j state[j] w[j] (+ bias)),
 // the sum folded from -0.0 in tap order.  One thread per channel.
 __global__ void __launch_bounds__(256)
-    k_hlm_conv(const float *__restrict__ proj, int inner, int ck, float *__restrict__ state,
+    k_hlm_conv(PartRows proj, int inner, int ck, float *__restrict__ state,
                const float *__restrict__ w, const float *__restrict__ bias,
                float *__restrict__ out) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= inner) return;
-  const float b_gate = proj[i], c_gate = proj[inner + i], x_sig = proj[2 * inner + i];
+  const float b_gate = part_row(proj, i), c_gate = part_row(proj, inner + i),
+              x_sig = part_row(proj, 2 * inner + i);
   const float bx = b_gate * x_sig;
   float *buf = state + (size_t)i * ck;
   const float *wr = w + (size_t)i * ck;
@@ -59,7 +70,7 @@ __global__ void __launch_bounds__(256)
 // RoPE (-> K cache row pos), v heads are copied to the V cache row pos.
 // Head norm layer.rs:865-876, RoPE layer.rs:848-863 at position pos.
 __global__ void __launch_bounds__(64)
-    k_hlm_qk(const float *__restrict__ qkv, int nh, int nkv, int hd,
+    k_hlm_qk(PartRows qkv, int nh, int nkv, int hd,
              const float *__restrict__ qn, const float *__restrict__ kn, float eps,
              const float *__restrict__ cosT, const float *__restrict__ sinT,
              const StepState *__restrict__ st, float *__restrict__ q_out,
@@ -68,14 +79,14 @@ __global__ void __launch_bounds__(64)
   float *sq = hv + ((hd + 3) & ~3);
   const int h = blockIdx.x, lane = threadIdx.x;
   const int pos = st->pos, kvd = nkv * hd, half = hd >> 1;
-  const float *src = qkv + (size_t)h * hd;
+  const int src = h * hd;
   if (h >= nh + nkv) {  // v head
     float *dst = vc + (size_t)pos * kvd + (size_t)(h - nh - nkv) * hd;
-    for (int d = lane; d < hd; d += 64) dst[d] = src[d];
+    for (int d = lane; d < hd; d += 64) dst[d] = part_row(qkv, src + d);
     return;
   }
   for (int d = lane; d < hd; d += 64) {
-    const float v = src[d];
+    const float v = part_row(qkv, src + d);
     hv[d] = v;
     sq[d] = v * v;
   }
@@ -154,22 +165,22 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// x += delta (if delta); normed = (x * w) * (1 / sqrt(sum(x^2) / H + eps))
+// x += delta (if delta.p); normed = (x * w) * (1 / sqrt(sum(x^2) / H + eps))
 // (pure_rust_ops.rs:96-112's formula) with the sum of squares in tree order:
 // one workgroup of 1024 threads, wave sums by shuffles, then the 16 wave
 // sums in order.  The decoder is graded by tolerance (its Q4 GEMVs sum in
 // their own order), and the sequential chain of the reference's order costs
 // a 1024-deep dependent add chain per norm.
 __global__ void __launch_bounds__(1024)
-    k_hlm_norm(float *__restrict__ x, const float *__restrict__ delta,
-               const float *__restrict__ w, float eps, int H, float *__restrict__ normed) {
+    k_hlm_norm(float *__restrict__ x, PartRows delta, const float *__restrict__ w, float eps,
+               int H, float *__restrict__ normed) {
   __shared__ float red[16];
   const int tid = threadIdx.x;
   float ss = 0.0f;
   for (int j = tid; j < H; j += 1024) {
     float v = x[j];
-    if (delta) {
-      v = v + delta[j];
+    if (delta.p) {
+      v = v + part_row(delta, j);
       x[j] = v;
     }
     ss = __builtin_fmaf(v, v, ss);
@@ -189,16 +200,16 @@ __global__ void __launch_bounds__(1024)
 
 // layer.rs:99: h = silu(gate) * up over the stacked [gate | up] row
 __global__ void __launch_bounds__(256)
-    k_hlm_swiglu(const float *__restrict__ gu, int F, float *__restrict__ h) {
+    k_hlm_swiglu(PartRows gu, int F, float *__restrict__ h) {
   const int i = blockIdx.x * 256 + threadIdx.x;
-  if (i < F) h[i] = syn_silu(gu[i]) * gu[F + i];
+  if (i < F) h[i] = syn_silu(part_row(gu, i)) * part_row(gu, F + i);
 }
 
 }  // namespace syn
 
 using namespace syn;
 
-static syn_status_t launch_hlm_norm(float *x, const float *delta, const float *w, float eps, int H,
+static syn_status_t launch_hlm_norm(float *x, PartRows delta, const float *w, float eps, int H,
                                    float *normed, hipStream_t s) {
   hipLaunchKernelGGL(k_hlm_norm, dim3(1), dim3(1024), 0, s, x, delta, w, eps, H, normed);
   SYN_LAUNCH_CHECK();
@@ -232,43 +243,45 @@ struct syn_hip_hlm_s {
   // st()->pos; logits -> argmax -> st()->token, pos += 1
   syn_status_t decode_step(hipStream_t s) {
     const float eps = c.eps;
+    // each Q4 GEMV leaves its split-K partials to the kernel that reads its
+    // output (PartRows): no reduce launches
+    PartRows pin, pout, pgu, pdown;
     SYN_TRY(launch_embed(embed.as<float>(), &st()->token, 1, (int)H, (int)V, x.as<float>(), s));
     for (size_t l = 0; l < L; l++) {
       Layer &Ly = layers[l];
-      SYN_TRY(launch_hlm_norm(x.as<float>(), l == 0 ? nullptr : down.as<float>(),
-                                 Ly.attn_nw.as<float>(), eps, (int)H, normed.as<float>(), s));
+      SYN_TRY(launch_hlm_norm(x.as<float>(), l == 0 ? PartRows{} : pdown, Ly.attn_nw.as<float>(),
+                              eps, (int)H, normed.as<float>(), s));
       if (Ly.kind == 0) {
-        SYN_TRY(Ly.in.gemv(1, normed.as<float>(), H, proj.as<float>(), 3 * I, s));
-        hipLaunchKernelGGL(k_hlm_conv, dim3((unsigned)cdiv(I, 256)), dim3(256), 0, s,
-                           proj.as<float>(), (int)I, (int)ck, Ly.conv_state.as<float>(),
-                           Ly.conv_w.as<float>(), c.conv_bias ? Ly.conv_b.as<float>() : nullptr,
-                           conv_out.as<float>());
+        SYN_TRY(Ly.in.gemv_parts(normed.as<float>(), proj.as<float>(), &pin, s));
+        hipLaunchKernelGGL(k_hlm_conv, dim3((unsigned)cdiv(I, 256)), dim3(256), 0, s, pin,
+                           (int)I, (int)ck, Ly.conv_state.as<float>(), Ly.conv_w.as<float>(),
+                           c.conv_bias ? Ly.conv_b.as<float>() : nullptr, conv_out.as<float>());
         SYN_LAUNCH_CHECK();
-        SYN_TRY(Ly.out.gemv(1, conv_out.as<float>(), I, o.as<float>(), H, s));
+        SYN_TRY(Ly.out.gemv_parts(conv_out.as<float>(), o.as<float>(), &pout, s));
       } else {
-        SYN_TRY(Ly.qkv.gemv(1, normed.as<float>(), H, proj.as<float>(), qd + 2 * kvd, s));
+        SYN_TRY(Ly.qkv.gemv_parts(normed.as<float>(), proj.as<float>(), &pin, s));
         hipLaunchKernelGGL(k_hlm_qk, dim3((unsigned)(nh + 2 * nkv)), dim3(64),
-                           2 * round_up(hd, 4) * 4, s, proj.as<float>(), (int)nh, (int)nkv,
-                           (int)hd, Ly.q_nw.as<float>(), Ly.k_nw.as<float>(), eps,
-                           rope_cos.as<float>(), rope_sin.as<float>(), st(), qrot.as<float>(),
-                           Ly.kc.as<float>(), Ly.vc.as<float>());
+                           2 * round_up(hd, 4) * 4, s, pin, (int)nh, (int)nkv, (int)hd,
+                           Ly.q_nw.as<float>(), Ly.k_nw.as<float>(), eps, rope_cos.as<float>(),
+                           rope_sin.as<float>(), st(), qrot.as<float>(), Ly.kc.as<float>(),
+                           Ly.vc.as<float>());
         SYN_LAUNCH_CHECK();
         hipLaunchKernelGGL(k_hlm_attn, dim3((unsigned)nh), dim3(256), ldw * 4, s,
                            qrot.as<float>(), Ly.kc.as<float>(), Ly.vc.as<float>(), st(), (int)nh,
                            (int)nkv, (int)hd, 1.0f / sqrtf((float)hd), attn.as<float>());
         SYN_LAUNCH_CHECK();
-        SYN_TRY(Ly.o.gemv(1, attn.as<float>(), qd, o.as<float>(), H, s));
+        SYN_TRY(Ly.o.gemv_parts(attn.as<float>(), o.as<float>(), &pout, s));
       }
-      SYN_TRY(launch_hlm_norm(x.as<float>(), o.as<float>(), Ly.ffn_nw.as<float>(), eps,
-                                 (int)H, normed.as<float>(), s));
-      SYN_TRY(Ly.gu.gemv(1, normed.as<float>(), H, gu.as<float>(), 2 * F, s));
-      hipLaunchKernelGGL(k_hlm_swiglu, dim3((unsigned)cdiv(F, 256)), dim3(256), 0, s,
-                         gu.as<float>(), (int)F, hbuf.as<float>());
+      SYN_TRY(launch_hlm_norm(x.as<float>(), pout, Ly.ffn_nw.as<float>(), eps, (int)H,
+                              normed.as<float>(), s));
+      SYN_TRY(Ly.gu.gemv_parts(normed.as<float>(), gu.as<float>(), &pgu, s));
+      hipLaunchKernelGGL(k_hlm_swiglu, dim3((unsigned)cdiv(F, 256)), dim3(256), 0, s, pgu,
+                         (int)F, hbuf.as<float>());
       SYN_LAUNCH_CHECK();
-      SYN_TRY(Ly.down.gemv(1, hbuf.as<float>(), F, down.as<float>(), H, s));
+      SYN_TRY(Ly.down.gemv_parts(hbuf.as<float>(), down.as<float>(), &pdown, s));
     }
-    SYN_TRY(launch_hlm_norm(x.as<float>(), down.as<float>(), final_nw.as<float>(), eps, (int)H,
-                               normed.as<float>(), s));
+    SYN_TRY(launch_hlm_norm(x.as<float>(), pdown, final_nw.as<float>(), eps, (int)H,
+                            normed.as<float>(), s));
     SYN_TRY(launch_gemv_f32_exact(lm_p.as<float>(), normed.as<float>(), normed.bytes / 4, (int)V,
                                   (int)H, n8_of((int)V), logits.as<float>(), s));
     SYN_TRY(launch_argmax(logits.as<float>(), (int)V, pv.as<float>(), pi.as<int>(),

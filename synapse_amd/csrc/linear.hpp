@@ -73,6 +73,16 @@ void host_minmax_scales(const float *w, size_t ch, size_t chsz, float *scales);
 void host_quantize_weights_nk(const float *w, const float *scales, size_t n, size_t k,
                               int8_t *out_nk);
 
+// The split-K partials of one GEMV output row set, left for the kernel that
+// consumes the output: row r = sum over k < ks of p[k * stride + r], summed
+// from 0.0f in k order (the order of the reduce kernel); ks = 1 is the output
+// itself (stride unused).
+struct PartRows {
+  const float *p = nullptr;
+  int ks = 1;
+  int stride = 0;
+};
+
 // Q4_0 linear: Q4Linear (q4_linear.rs); f32 activations.
 struct QLinearQ4_0 {
   size_t n = 0, k = 0;
@@ -98,6 +108,10 @@ struct QLinearQ4_0 {
   // y[m,n] = x[m,k] W^T, f32 activations; m > 16 runs gemm() when gemm_ok()
   syn_status_t gemv(size_t m, const float *d_x, size_t ldx, float *d_y, size_t ldy,
                     hipStream_t s);
+  // one activation row without the reduce launch: the GEMV kernel writes its
+  // split-K partials (prepare(1) must have run) and *out names them; with a
+  // single K slice it writes y[n] and *out names y
+  syn_status_t gemv_parts(const float *d_x, float *d_y, PartRows *out, hipStream_t s);
   // f16 MFMA prefill GEMM (kquant_gemm.hip): weights (nibble - 8) * d and
   // activations rounded once to f16, f32 accumulation
   syn_status_t gemm(size_t m, const float *d_x, size_t ldx, float *d_y, size_t ldy,

@@ -341,6 +341,27 @@ syn_status_t QLinearQ4_0::gemv(size_t m, const float *d_x, size_t ldx, float *d_
   return SYN_OK;
 }
 
+syn_status_t QLinearQ4_0::gemv_parts(const float *d_x, float *d_y, PartRows *out,
+                                     hipStream_t s) {
+  if (!d_x || !d_y || !out) return SYN_ERR_NULL_PTR;
+  if (n == 0 || k == 0) return SYN_ERR_INVALID_ARG;
+  const float sub = rs_f16_scales ? 0.5f : 1.0f;
+  const GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
+  const size_t N64 = (size_t)p.panels * 64;
+  const size_t shm_h = ((size_t)p.cs + 8 * 64) * 4;
+  if (shm_h > 60 * 1024) return SYN_ERR_INVALID_ARG;  // K slice too long for this kernel
+  if (p.ksplit > 1 && part_elems < (size_t)p.ksplit * N64) return SYN_ERR_INVALID_ARG;
+  hipLaunchKernelGGL(k_gemv_q4_0h<2>, dim3(p.panels, p.ksplit), dim3(512), shm_h, s,
+                     nib.as<u32x4>(), sc.as<uint16_t>(), d_x, d_y, part.as<float>(), (int)n,
+                     p.chunks, p.cs, sub);
+  SYN_LAUNCH_CHECK();
+  if (p.ksplit > 1)
+    *out = PartRows{part.as<float>(), p.ksplit, (int)N64};
+  else
+    *out = PartRows{d_y, 1, 0};
+  return SYN_OK;
+}
+
 syn_status_t QLinearQ4_0::prepare(size_t max_m) {
   const GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
   const size_t need = (size_t)p.ksplit * std::min<size_t>(8, max_m) * (size_t)p.panels * 64;
