@@ -597,8 +597,17 @@ syn_status_t syn_hip_hlm_generate(syn_hip_hlm_t *m, const uint32_t *prompt, size
                                   size_t max_new, uint32_t *out_tokens, float *out_margins);
 /* hipEvent time of `steps` greedy decode steps from the current state */
 syn_status_t syn_hip_hlm_decode_timed(syn_hip_hlm_t *m, size_t steps, float *elapsed_ms);
-/* graph != 0 (the default): replay a captured HIP graph of the step */
-syn_status_t syn_hip_hlm_set_options(syn_hip_hlm_t *m, int graph);
+/* fused != 0 (the default): five kernels per layer when the shapes fit
+ * (hidden 256..2048 in whole 256s, inner, inter, n_heads * head_dim multiples
+ * of 256, head_dim 16..128, n_heads / n_kv_heads <= 8, IEEE block scales):
+ * the Q4_0 rows of split-K workgroups add into fixed-point accumulators,
+ * RMSNorm, SwiGLU and the attention combine run in the GEMVs' prologues and
+ * epilogues, the lm_head carries a per-panel top-2; else the op-by-op step.
+ * Both are graded against the reference by tolerance.
+ * graph != 0 (the default): replay a captured HIP graph of the step */
+syn_status_t syn_hip_hlm_set_options(syn_hip_hlm_t *m, int fused, int graph);
+/* *active = 1 when decode steps run the fused form */
+syn_status_t syn_hip_hlm_fused_active(syn_hip_hlm_t *m, int *active);
 syn_status_t syn_hip_hlm_destroy(syn_hip_hlm_t *m);
 
 /* -- harness helpers (no reference counterpart) -- */

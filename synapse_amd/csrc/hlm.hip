@@ -23,8 +23,10 @@
 
 #include "decode_fused.hpp"
 #include "f32_ops.hpp"
+#include "klm_fused.hpp"
 #include "layer_ops.hpp"
 #include "linear.hpp"
+#include "liv_conv.hpp"
 #include "reduce_order.hpp"
 
 namespace syn {
@@ -39,30 +41,22 @@ __device__ __forceinline__ float part_row(const PartRows &r, int row) {
   return s;
 }
 
-// layer.rs:25-42 conv1d_step_single over the double-gated LIV conv
-// (layer.rs:609-627): proj = [B | C | x]; the channel's state row holds its
-// last ck inputs B*x, oldest first; out = C * (sum_j state[j] w[j] (+ bias)),
-// the sum folded from -0.0 in tap order.  One thread per channel.
+// The LIV conv step (liv_conv_channel) of the in_proj output, read from the
+// Q4 GEMV's split-K partials: proj = [B | C | x], one thread per channel,
+// the state half of the position read and the next one written.
 __global__ void __launch_bounds__(256)
-    k_hlm_conv(PartRows proj, int inner, int ck, float *__restrict__ state,
-               const float *__restrict__ w, const float *__restrict__ bias,
-               float *__restrict__ out) {
+    k_hlm_conv(PartRows proj, int inner, int ck, const StepState *__restrict__ st,
+               float *__restrict__ state, const float *__restrict__ w,
+               const float *__restrict__ bias, float *__restrict__ out) {
   const int i = blockIdx.x * 256 + threadIdx.x;
   if (i >= inner) return;
-  const float b_gate = part_row(proj, i), c_gate = part_row(proj, inner + i),
-              x_sig = part_row(proj, 2 * inner + i);
-  const float bx = b_gate * x_sig;
-  float *buf = state + (size_t)i * ck;
-  const float *wr = w + (size_t)i * ck;
-  float sum = -0.0f;
-  for (int j = 0; j < ck; j++) {
-    const float v = j + 1 < ck ? buf[j + 1] : bx;
-    buf[j] = v;
-    const float t = v * wr[j];
-    sum = sum + t;
-  }
-  const float cv = bias ? sum + bias[i] : sum;
-  out[i] = c_gate * cv;
+  const int pos = st->pos;
+  const size_t half = (size_t)inner * ck;
+  const float *sold = state + (size_t)(pos & 1) * half + (size_t)i * ck;
+  float *snew = state + (size_t)((pos + 1) & 1) * half + (size_t)i * ck;
+  out[i] = liv_conv_channel(part_row(proj, i), part_row(proj, inner + i),
+                            part_row(proj, 2 * inner + i), ck, sold, snew, w + (size_t)i * ck,
+                            bias ? bias + i : nullptr);
 }
 
 // Heads of the stacked q|k|v row, one wave each: q heads [0, nh) get the
@@ -73,16 +67,16 @@ __global__ void __launch_bounds__(64)
     k_hlm_qk(PartRows qkv, int nh, int nkv, int hd,
              const float *__restrict__ qn, const float *__restrict__ kn, float eps,
              const float *__restrict__ cosT, const float *__restrict__ sinT,
-             const StepState *__restrict__ st, float *__restrict__ q_out,
+             const StepState *__restrict__ st, int S, float *__restrict__ q_out,
              float *__restrict__ kc, float *__restrict__ vc) {
   extern __shared__ __align__(16) float hv[];  // the head [hd] | its squares [hd]
   float *sq = hv + ((hd + 3) & ~3);
   const int h = blockIdx.x, lane = threadIdx.x;
-  const int pos = st->pos, kvd = nkv * hd, half = hd >> 1;
+  const int pos = st->pos, half = hd >> 1;
   const int src = h * hd;
   if (h >= nh + nkv) {  // v head
-    float *dst = vc + (size_t)pos * kvd + (size_t)(h - nh - nkv) * hd;
-    for (int d = lane; d < hd; d += 64) dst[d] = part_row(qkv, src + d);
+    const int g = h - nh - nkv;
+    for (int d = lane; d < hd; d += 64) vc[kv_v_index(pos, g, d, hd, S)] = part_row(qkv, src + d);
     return;
   }
   for (int d = lane; d < hd; d += 64) {
@@ -100,13 +94,17 @@ __global__ void __launch_bounds__(64)
     hv[d] = hv[d] * ws;
   }
   __syncthreads();
-  float *dst = h < nh ? q_out + (size_t)h * hd : kc + (size_t)pos * kvd + (size_t)(h - nh) * hd;
   const float *cr = cosT + (size_t)pos * half, *sr = sinT + (size_t)pos * half;
   for (int i = lane; i < half; i += 64) {
     const float x1 = hv[i], x2 = hv[half + i], c = cr[i], sn = sr[i];
     const float a = x1 * c, b = x2 * sn, e = x2 * c, f = x1 * sn;
-    dst[i] = a - b;
-    dst[half + i] = e + f;
+    if (h < nh) {
+      q_out[(size_t)h * hd + i] = a - b;
+      q_out[(size_t)h * hd + half + i] = e + f;
+    } else {
+      kc[kv_k_index(pos, h - nh, i, hd, S)] = a - b;
+      kc[kv_k_index(pos, h - nh, half + i, hd, S)] = e + f;
+    }
   }
 }
 
@@ -118,21 +116,20 @@ __global__ void __launch_bounds__(64)
 __global__ void __launch_bounds__(256)
     k_hlm_attn(const float *__restrict__ q, const float *__restrict__ kc,
                const float *__restrict__ vc, const StepState *__restrict__ st, int nh, int nkv,
-               int hd, float scale, float *__restrict__ out) {
+               int hd, int S, float scale, float *__restrict__ out) {
   extern __shared__ __align__(16) float row[];
   __shared__ float qs[256];
   __shared__ float red[4];
   __shared__ float s_sum;
   const int qh = blockIdx.x, tid = threadIdx.x;
-  const int kvh = qh / (nh / nkv), kvd = nkv * hd, seq = st->pos + 1;
+  const int kvh = qh / (nh / nkv), seq = st->pos + 1;
   for (int d = tid; d < hd; d += 256) qs[d] = q[(size_t)qh * hd + d];
   __syncthreads();
   float mx = -INFINITY;
   for (int p = tid; p < seq; p += 256) {
-    const float *kp = kc + (size_t)p * kvd + (size_t)kvh * hd;
     float dot = 0.0f;
     for (int d = 0; d < hd; d++) {
-      const float t = qs[d] * kp[d];
+      const float t = qs[d] * kc[kv_k_index(p, kvh, d, hd, S)];
       dot = dot + t;
     }
     const float sc = dot * scale;
@@ -155,10 +152,9 @@ __global__ void __launch_bounds__(256)
     for (int p = tid; p < seq; p += 256) row[p] = row[p] / sum;
   __syncthreads();
   for (int d = tid; d < hd; d += 256) {
-    const float *vp = vc + (size_t)kvh * hd + d;
     float val = 0.0f;
     for (int p = 0; p < seq; p++) {
-      const float t = row[p] * vp[(size_t)p * kvd];
+      const float t = row[p] * vc[kv_v_index(p, kvh, d, hd, S)];
       val = val + t;
     }
     out[(size_t)qh * hd + d] = val;
@@ -205,9 +201,123 @@ __global__ void __launch_bounds__(256)
   if (i < F) h[i] = syn_silu(part_row(gu, i)) * part_row(gu, F + i);
 }
 
+// Tied f32 lm_head of the fused step: logits[row] = (E[row] . (r * gain)) /
+// rms(r), r the fixed-point residual, E the embedding [V][H] row-major, and
+// the workgroup's top-2 for launch_argmax_advance.  256 threads, 64 rows per
+// workgroup (16 per wave); lane j holds the activations of float4 columns
+// j + 64 c of the row (H = 256 NC), so a row is NC coalesced 1 KiB loads per
+// wave and a butterfly sum (equal in every lane).  Every wave computes the
+// row's sum of squares itself.  The sums run in this tree order (the decoder
+// is graded by tolerance).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+template <int NC>
+__global__ void __launch_bounds__(256)
+    k_hlm_head_top2(const f32x4 *__restrict__ E, int V, const long long *__restrict__ r,
+                    const float *__restrict__ gain, float eps, float *__restrict__ logits,
+                    float *__restrict__ pv, int *__restrict__ pi, float *__restrict__ pv2) {
+  // float4 per row; rows per batch of loads (one batch in registers, no
+  // prefetch: the other waves of the SIMD cover its latency, and the whole
+  // grid stays resident)
+  constexpr int H4 = 64 * NC, RB = NC <= 4 ? 4 : 2;
+  __shared__ float sv1[4], sv2[4];
+  __shared__ int si1[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int row0 = blockIdx.x * 64 + wave * 16;
+  f32x4 w[RB][NC];
+  auto issue = [&](int b) {
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
+      const int row = min(row0 + b + rr, V - 1);
+#pragma unroll
+      for (int c = 0; c < NC; c++)
+        w[rr][c] = __builtin_nontemporal_load(E + (size_t)row * H4 + lane + 64 * c);
+    }
+  };
+  float4 xg[NC];
+  float ss = 0.0f;
+#pragma unroll
+  for (int c = 0; c < NC; c++) {
+    const int i = lane + 64 * c;
+    const long long *rp = r + 4 * (size_t)i;
+    const float4 a = make_float4(kqf_unfix(rp[0]), kqf_unfix(rp[1]), kqf_unfix(rp[2]),
+                                 kqf_unfix(rp[3]));
+    const float4 g = reinterpret_cast<const float4 *>(gain)[i];
+    ss += (a.x * a.x + a.y * a.y) + (a.z * a.z + a.w * a.w);
+    xg[c] = make_float4(a.x * g.x, a.y * g.y, a.z * g.z, a.w * g.w);
+  }
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  const float inv = 1.0f / sqrtf(ss / (float)(4 * H4) + eps);
+  Top2v t{-__builtin_inff(), -1, -__builtin_inff()};
+#pragma unroll 1
+  for (int b = 0; b < 16; b += RB) {
+    issue(b);
+    float dot[RB];
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
+      float a = 0.0f;
+#pragma unroll
+      for (int c = 0; c < NC; c++) {
+        a = __builtin_fmaf(w[rr][c].x, xg[c].x, a);
+        a = __builtin_fmaf(w[rr][c].y, xg[c].y, a);
+        a = __builtin_fmaf(w[rr][c].z, xg[c].z, a);
+        a = __builtin_fmaf(w[rr][c].w, xg[c].w, a);
+      }
+      dot[rr] = a;
+    }
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
+      float a = dot[rr];
+      for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o);
+      const int row = row0 + b + rr;
+      if (row < V) {
+        const float v = a * inv;
+        if (lane == 0) logits[row] = v;
+        t = top2v_merge(t, Top2v{v, row, -__builtin_inff()});
+      }
+    }
+  }
+  if (lane == 0) {
+    sv1[wave] = t.v1;
+    si1[wave] = t.i1;
+    sv2[wave] = t.v2;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    Top2v m{sv1[0], si1[0], sv2[0]};
+    for (int i = 1; i < 4; i++) m = top2v_merge(m, Top2v{sv1[i], si1[i], sv2[i]});
+    pv[blockIdx.x] = m.v1;
+    pi[blockIdx.x] = m.i1;
+    pv2[blockIdx.x] = m.v2;
+  }
+}
+
 }  // namespace syn
 
 using namespace syn;
+
+static syn_status_t launch_hlm_head_top2(const float *E, int V, int H, const long long *r,
+                                         const float *gain, float eps, float *logits, float *pv,
+                                         int *pi, float *pv2, hipStream_t s) {
+  const dim3 grid((unsigned)cdiv((size_t)V, 64));
+#define HLM_HEAD(NC_)                                                                     \
+  hipLaunchKernelGGL((k_hlm_head_top2<NC_>), grid, dim3(256), 0, s,                       \
+                     reinterpret_cast<const f32x4 *>(E), V, r, gain, eps, logits, pv, pi, pv2)
+  switch (H) {
+    case 256: HLM_HEAD(1); break;
+    case 512: HLM_HEAD(2); break;
+    case 768: HLM_HEAD(3); break;
+    case 1024: HLM_HEAD(4); break;
+    case 1536: HLM_HEAD(6); break;
+    case 2048: HLM_HEAD(8); break;
+    default:
+      set_error("hybrid lm_head: hidden must be 256, 512, 768, 1024, 1536 or 2048");
+      return SYN_ERR_INVALID_ARG;
+  }
+#undef HLM_HEAD
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
 
 static syn_status_t launch_hlm_norm(float *x, PartRows delta, const float *w, float eps, int H,
                                    float *normed, hipStream_t s) {
@@ -232,6 +342,13 @@ struct syn_hip_hlm_s {
   hipStream_t stream = nullptr;
   hipGraphExec_t graph = nullptr;
   bool ready = false, use_graph = true;
+  // fused step (klm_fused.hip's GEMV over the Q4_0 planes): the fixed-point
+  // residual r [H], the split-K accumulator of in_proj / q|k|v (cleared by
+  // the projection after its reader), attention chunk partials, lm_head top-2
+  bool use_fused = true, fused_ok = false;
+  KqfPlan fp_in, fp_out, fp_qkv, fp_o, fp_gu, fp_down;
+  DevBuf f_r, f_acc, f_ao, f_aml, f_pv, f_pi, f_pv2;
+  size_t n_qkv = 0;
 
   ~syn_hip_hlm_s() {
     if (graph) (void)hipGraphExecDestroy(graph);
@@ -241,7 +358,120 @@ struct syn_hip_hlm_s {
 
   // HybridModel::decode_one for the token in st()->token at position
   // st()->pos; logits -> argmax -> st()->token, pos += 1
+  // the fused step's plans and buffers, when every shape fits its kernels
+  syn_status_t setup_fused() {
+    fused_ok = false;
+    const int fm[1] = {SYN_HIP_FMT_Q4_0};
+    if (!kqf_fits((int)H, (int)qd, (int)F, (int)nh, (int)nkv, (int)hd, (int)S, fm, 1) ||
+        I % 256 || (H != 256 && H != 512 && H != 768 && H != 1024 && H != 1536 && H != 2048))
+      return SYN_OK;
+    bool any_conv = false, any_gqa = false;
+    for (auto &Ly : layers) {
+      for (QLinearQ4_0 *q : {&Ly.in, &Ly.out, &Ly.qkv, &Ly.o, &Ly.gu, &Ly.down})
+        if (q->n && !q->gemm_ok()) return SYN_OK;  // halved subnormal scales
+      (Ly.kind == 0 ? any_conv : any_gqa) = true;
+    }
+    const Layer *conv = nullptr, *gqa = nullptr;
+    for (auto &Ly : layers) (Ly.kind == 0 ? conv : gqa) = &Ly;
+    if (conv) {
+      fp_in = kqf_plan(conv->in, false);
+      fp_out = kqf_plan(conv->out, false);
+    }
+    if (gqa) {
+      fp_qkv = kqf_plan(gqa->qkv, false);
+      fp_o = kqf_plan(gqa->o, false);
+    }
+    fp_gu = kqf_plan(layers[0].gu, true);
+    fp_down = kqf_plan(layers[0].down, false);
+    n_qkv = std::max(any_conv ? 3 * I : 0, any_gqa ? qd + 2 * kvd : 0);
+    SYN_TRY(f_r.alloc(H * 8));
+    SYN_TRY(f_acc.alloc(n_qkv * 8));
+    SYN_HIP(hipMemset(f_acc.p, 0, f_acc.bytes));  // later steps leave it cleared
+    if (any_gqa) {
+      const size_t nch = (size_t)kqf_chunks((int)S);
+      SYN_TRY(f_ao.alloc(nh * nch * hd * 4));
+      SYN_TRY(f_aml.alloc(nh * nch * 2 * 4));
+      SYN_HIP(hipMemset(f_ao.p, 0, f_ao.bytes));
+      SYN_HIP(hipMemset(f_aml.p, 0, f_aml.bytes));
+    }
+    const size_t panels = cdiv(V, (size_t)64);
+    SYN_TRY(f_pv.alloc(panels * 4));
+    SYN_TRY(f_pi.alloc(panels * 4));
+    SYN_TRY(f_pv2.alloc(panels * 4));
+    fused_ok = true;
+    return SYN_OK;
+  }
+
+  // fused step: per LIV conv layer in_proj of rmsnorm(r) (layer 0: of the
+  // token's embedding row), out_proj of the conv step (in its prologue)
+  // added into r, gate|up of rmsnorm(r) with SwiGLU, down added into r
+  // (clearing the in_proj accumulator); per GQA layer q|k|v, the chunked attention with head norms, RoPE
+  // and KV append, O of the chunk combine added into r, gate|up, down; then
+  // the tied lm_head of rmsnorm(r) with per-panel top-2 and the merge.
+  syn_status_t decode_step_fused(hipStream_t s) {
+    const float eps = c.eps;
+    long long *r = f_r.as<long long>(), *acc = f_acc.as<long long>();
+    for (size_t l = 0; l < L; l++) {
+      Layer &Ly = layers[l];
+      KqfIn a;  // K1: in_proj or q|k|v rows of rmsnorm(r)
+      a.r = r;
+      a.embed = embed.as<float>();
+      a.vocab = (int)V;
+      a.r_out = r;
+      a.st = st();
+      a.gain = Ly.attn_nw.as<float>();
+      a.eps = eps;
+      a.H = (int)H;
+      const int pro = l == 0 ? KQF_PRO_EMBED : KQF_PRO_NORM;
+      long long *zero_after = nullptr;  // the accumulator the down projection clears
+      int nzero = 0;
+      if (Ly.kind == 0) {
+        SYN_TRY(kqf_gemv(Ly.in, fp_in, pro, a, acc, nullptr, 0, s));
+        KqfIn b;  // r += out_proj(conv step of the in_proj accumulator)
+        b.cacc = acc;
+        b.cstate = Ly.conv_state.as<float>();
+        b.cw = Ly.conv_w.as<float>();
+        b.cb = c.conv_bias ? Ly.conv_b.as<float>() : nullptr;
+        b.inner = (int)I;
+        b.ck = (int)ck;
+        b.st = st();
+        SYN_TRY(kqf_gemv(Ly.out, fp_out, KQF_PRO_CONV, b, r, nullptr, 0, s));
+        zero_after = acc;  // every out_proj workgroup reads it in its prologue
+        nzero = (int)(3 * I);
+      } else {
+        SYN_TRY(kqf_gemv(Ly.qkv, fp_qkv, pro, a, acc, nullptr, 0, s));
+        SYN_TRY(kqf_attention(acc, (int)nh, (int)nkv, (int)hd, Ly.q_nw.as<float>(),
+                              Ly.k_nw.as<float>(), eps, rope_cos.as<float>(),
+                              rope_sin.as<float>(), st(), Ly.kc.as<float>(), Ly.vc.as<float>(),
+                              (int)S, f_ao.as<float>(), f_aml.as<float>(), s));
+        KqfIn b;  // r += O(combine of the chunks); the q|k|v accumulator cleared
+        b.ao = f_ao.as<float>();
+        b.aml = f_aml.as<float>();
+        b.hd = (int)hd;
+        b.nch = kqf_chunks((int)S);
+        b.st = st();
+        SYN_TRY(kqf_gemv(Ly.o, fp_o, KQF_PRO_ATTN, b, r, acc, (int)(qd + 2 * kvd), s));
+      }
+      KqfIn g;  // gate|up of rmsnorm(r), SwiGLU
+      g.r = r;
+      g.gain = Ly.ffn_nw.as<float>();
+      g.eps = eps;
+      g.H = (int)H;
+      SYN_TRY(kqf_gate_up(Ly.gu, fp_gu, g, (int)F, hbuf.as<float>(), s));
+      KqfIn d;  // r += down(h)
+      d.x = hbuf.as<float>();
+      SYN_TRY(kqf_gemv(Ly.down, fp_down, KQF_PRO_NONE, d, r, zero_after, nzero, s));
+    }
+    SYN_TRY(launch_hlm_head_top2(embed.as<float>(), (int)V, (int)H, r, final_nw.as<float>(), eps,
+                                 logits.as<float>(), f_pv.as<float>(), f_pi.as<int>(),
+                                 f_pv2.as<float>(), s));
+    return launch_argmax_advance(f_pv.as<float>(), f_pi.as<int>(), f_pv2.as<float>(),
+                                 (int)cdiv(V, (size_t)64), st(), history.as<uint32_t>(),
+                                 mhist.as<float>(), s);
+  }
+
   syn_status_t decode_step(hipStream_t s) {
+    if (use_fused && fused_ok) return decode_step_fused(s);
     const float eps = c.eps;
     // each Q4 GEMV leaves its split-K partials to the kernel that reads its
     // output (PartRows): no reduce launches
@@ -254,8 +484,9 @@ struct syn_hip_hlm_s {
       if (Ly.kind == 0) {
         SYN_TRY(Ly.in.gemv_parts(normed.as<float>(), proj.as<float>(), &pin, s));
         hipLaunchKernelGGL(k_hlm_conv, dim3((unsigned)cdiv(I, 256)), dim3(256), 0, s, pin,
-                           (int)I, (int)ck, Ly.conv_state.as<float>(), Ly.conv_w.as<float>(),
-                           c.conv_bias ? Ly.conv_b.as<float>() : nullptr, conv_out.as<float>());
+                           (int)I, (int)ck, st(), Ly.conv_state.as<float>(),
+                           Ly.conv_w.as<float>(), c.conv_bias ? Ly.conv_b.as<float>() : nullptr,
+                           conv_out.as<float>());
         SYN_LAUNCH_CHECK();
         SYN_TRY(Ly.out.gemv_parts(conv_out.as<float>(), o.as<float>(), &pout, s));
       } else {
@@ -263,12 +494,12 @@ struct syn_hip_hlm_s {
         hipLaunchKernelGGL(k_hlm_qk, dim3((unsigned)(nh + 2 * nkv)), dim3(64),
                            2 * round_up(hd, 4) * 4, s, pin, (int)nh, (int)nkv, (int)hd,
                            Ly.q_nw.as<float>(), Ly.k_nw.as<float>(), eps, rope_cos.as<float>(),
-                           rope_sin.as<float>(), st(), qrot.as<float>(), Ly.kc.as<float>(),
-                           Ly.vc.as<float>());
+                           rope_sin.as<float>(), st(), (int)S, qrot.as<float>(),
+                           Ly.kc.as<float>(), Ly.vc.as<float>());
         SYN_LAUNCH_CHECK();
         hipLaunchKernelGGL(k_hlm_attn, dim3((unsigned)nh), dim3(256), ldw * 4, s,
                            qrot.as<float>(), Ly.kc.as<float>(), Ly.vc.as<float>(), st(), (int)nh,
-                           (int)nkv, (int)hd, 1.0f / sqrtf((float)hd), attn.as<float>());
+                           (int)nkv, (int)hd, (int)S, 1.0f / sqrtf((float)hd), attn.as<float>());
         SYN_LAUNCH_CHECK();
         SYN_TRY(Ly.o.gemv_parts(attn.as<float>(), o.as<float>(), &pout, s));
       }
@@ -329,7 +560,7 @@ struct syn_hip_hlm_s {
   syn_status_t reset() {
     for (auto &Ly : layers)
       if (Ly.kind == 0)
-        SYN_TRY(launch_zero_i32(Ly.conv_state.as<int>(), I * ck, stream));
+        SYN_TRY(launch_zero_i32(Ly.conv_state.as<int>(), 2 * I * ck, stream));
     return set_state(0, 0, 0);
   }
 };
@@ -391,7 +622,7 @@ syn_status_t syn_hip_hlm_create(const syn_hip_hlm_config *cfg, syn_hip_hlm_t **o
 syn_status_t syn_hip_hlm_init_synthetic(syn_hip_hlm_t *m, uint64_t seed_base, float stddev) {
   if (!m) return SYN_ERR_NULL_PTR;
   const size_t H = m->H, I = m->I, F = m->F, V = m->V, hd = m->hd, ck = m->ck;
-  const size_t qd = m->qd, kvd = m->kvd, S = m->S;
+  const size_t qd = m->qd, kvd = m->kvd, S = m->S, nkv_ = m->nkv;
   auto up = [](DevBuf &b, const std::vector<float> &v) -> syn_status_t {
     SYN_TRY(b.alloc(v.size() * 4));
     SYN_HIP(hipMemcpy(b.p, v.data(), v.size() * 4, hipMemcpyHostToDevice));
@@ -446,14 +677,17 @@ syn_status_t syn_hip_hlm_init_synthetic(syn_hip_hlm_t *m, uint64_t seed_base, fl
         fill_normal(cb.data(), I, s + 3, stddev);
         SYN_TRY(up(Ly.conv_b, cb));
       }
-      SYN_TRY(up(Ly.conv_state, std::vector<float>(I * ck, 0.0f)));
+      SYN_TRY(up(Ly.conv_state, std::vector<float>(2 * I * ck, 0.0f)));  // two halves
     } else {
       SYN_TRY(q4_stack(Ly.qkv, {{qd, s + 0}, {kvd, s + 1}, {kvd, s + 2}}, H));
       SYN_TRY(q4_stack(Ly.o, {{H, s + 3}}, qd));
       SYN_TRY(up(Ly.q_nw, gain(hd, s + 6)));
       SYN_TRY(up(Ly.k_nw, gain(hd, s + 7)));
-      SYN_TRY(Ly.kc.alloc(S * kvd * 4));
-      SYN_TRY(Ly.vc.alloc(S * kvd * 4));
+      // the attention kernels' tiled layouts (kv_k_index / kv_v_index)
+      SYN_TRY(Ly.kc.alloc(kv_k_elems((int)nkv_, (int)hd, (int)S) * 4));
+      SYN_TRY(Ly.vc.alloc(kv_v_elems((int)nkv_, (int)hd, (int)S) * 4));
+      SYN_HIP(hipMemset(Ly.kc.p, 0, Ly.kc.bytes));
+      SYN_HIP(hipMemset(Ly.vc.p, 0, Ly.vc.bytes));
     }
     SYN_TRY(up(Ly.attn_nw, gain(H, s + 8)));
     SYN_TRY(up(Ly.ffn_nw, gain(H, s + 9)));
@@ -497,6 +731,11 @@ syn_status_t syn_hip_hlm_init_synthetic(syn_hip_hlm_t *m, uint64_t seed_base, fl
   SYN_TRY(m->pv2.alloc(256 * 4));
   SYN_TRY(m->history.alloc((S + 1) * 4));
   SYN_TRY(m->mhist.alloc((S + 1) * 4));
+  SYN_TRY(m->setup_fused());
+  if (m->graph) {  // weights replaced: the captured step is stale
+    (void)hipGraphExecDestroy(m->graph);
+    m->graph = nullptr;
+  }
   m->ready = true;
   return m->reset();
 }
@@ -587,9 +826,21 @@ syn_status_t syn_hip_hlm_decode_timed(syn_hip_hlm_t *m, size_t steps, float *ela
   return SYN_OK;
 }
 
-syn_status_t syn_hip_hlm_set_options(syn_hip_hlm_t *m, int graph) {
+syn_status_t syn_hip_hlm_set_options(syn_hip_hlm_t *m, int fused, int graph) {
   if (!m) return SYN_ERR_NULL_PTR;
+  if (m->graph && m->use_fused != (fused != 0)) {  // the captured step changes form
+    SYN_HIP(hipStreamSynchronize(m->stream));
+    (void)hipGraphExecDestroy(m->graph);
+    m->graph = nullptr;
+  }
+  m->use_fused = fused != 0;
   m->use_graph = graph != 0;
+  return SYN_OK;
+}
+
+syn_status_t syn_hip_hlm_fused_active(syn_hip_hlm_t *m, int *active) {
+  if (!m || !active) return SYN_ERR_NULL_PTR;
+  *active = m->use_fused && m->fused_ok ? 1 : 0;
   return SYN_OK;
 }
 

@@ -32,6 +32,7 @@
 #include "decode_fused.hpp"
 #include "klm_fused.hpp"
 #include "kq_unit.hpp"
+#include "liv_conv.hpp"
 #include "phase_ts.hpp"
 
 namespace syn {
@@ -64,9 +65,15 @@ template <>
 struct KqfFmt<SYN_HIP_FMT_Q8_0> {
   static constexpr int BPU = 8, NPB = 2, NPU = 16, DPU = 8, GRP = 0;
 };
+template <>  // eight 32-element blocks, one nibble plane each; sums per block
+struct KqfFmt<SYN_HIP_FMT_Q4_0> {
+  static constexpr int BPU = 8, NPB = 1, NPU = 8, DPU = 8, GRP = 32;
+};
 
 int groups_per_unit(int fmt) {
-  return fmt == SYN_HIP_FMT_Q4_K ? 8 : fmt == SYN_HIP_FMT_Q6_K ? 16 : 0;
+  return fmt == SYN_HIP_FMT_Q4_K || fmt == SYN_HIP_FMT_Q4_0 ? 8
+         : fmt == SYN_HIP_FMT_Q6_K                          ? 16
+                                                            : 0;
 }
 
 enum { OUT_ACC = 0, OUT_GU = 1, OUT_TOP2 = 2 };
@@ -122,17 +129,6 @@ __device__ __forceinline__ float wave_max(float v) {
 
 typedef long long i64x2 __attribute__((ext_vector_type(2)));
 
-// fixed point: value * 2^32, saturated far beyond any activation
-__device__ __forceinline__ long long kqf_fix(float v) {
-  const double d = (double)v * 4294967296.0;
-  return __double2ll_rn(fmin(fmax(d, -4.0e18), 4.0e18));
-}
-
-__device__ __forceinline__ float kqf_unfix(long long a) {
-  return (float)((double)a * 2.3283064365386963e-10);
-}
-
-
 // 32 activations of a stage from LDS (all lanes read the same address)
 __device__ __forceinline__ void lds_x32(float (&x)[32], const float *src) {
 #pragma unroll
@@ -162,7 +158,7 @@ __device__ __forceinline__ void kqf_unit(u32x4 *pl, const uint16_t *dh, const fl
   asm volatile("" ::: "memory");  // no LDS read of the unit moves above its branch
   float xb[DB ? 2 : 1][32];
   float av[16];
-  if constexpr (FMT == SYN_HIP_FMT_Q4_K) {
+  if constexpr (FMT == SYN_HIP_FMT_Q4_K || FMT == SYN_HIP_FMT_Q4_0) {
 #pragma unroll
     for (int i = 0; i < 8; i++) av[i] = as[i];
   } else if constexpr (FMT == SYN_HIP_FMT_Q6_K) {
@@ -177,6 +173,16 @@ __device__ __forceinline__ void kqf_unit(u32x4 *pl, const uint16_t *dh, const fl
     dmin = syn_f16_to_f32_rs(pl[0].x >> 16);
   } else if constexpr (FMT == SYN_HIP_FMT_Q6_K) {
     d = syn_f16_to_f32_rs(dh[0]);
+  } else if constexpr (FMT == SYN_HIP_FMT_Q4_0) {
+    // IEEE f16 scales (the Q4 GEMV's reading; handles with halved subnormal
+    // scales are not offered to this kernel), pinned here so the conversion
+    // (and the wait for the loads) is not hoisted into the entry's branch
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      uint32_t h = dh[j];
+      asm volatile("" : "+v"(h));
+      dq[j] = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+    }
   } else {
 #pragma unroll
     for (int j = 0; j < 8; j++) dq[j] = syn_f16_to_f32_rs(dh[j]);
@@ -197,6 +203,8 @@ __device__ __forceinline__ void kqf_unit(u32x4 *pl, const uint16_t *dh, const fl
     } else if constexpr (FMT == SYN_HIP_FMT_Q6_K) {
       pin_plane(pl[t]);
       pin_plane(pl[8 + (t >> 1)]);
+    } else if constexpr (FMT == SYN_HIP_FMT_Q4_0) {
+      pin_plane(pl[t]);
     } else {
       pin_plane(pl[2 * t]);
       pin_plane(pl[2 * t + 1]);
@@ -207,6 +215,8 @@ __device__ __forceinline__ void kqf_unit(u32x4 *pl, const uint16_t *dh, const fl
     } else if constexpr (FMT == SYN_HIP_FMT_Q6_K) {
       kq6_group(pl, 2 * t, d, xc, av[2 * t], acc);
       kq6_group(pl, 2 * t + 1, d, xc + 16, av[2 * t + 1], acc);
+    } else if constexpr (FMT == SYN_HIP_FMT_Q4_0) {
+      kq40_block(pl[t], dq[t], xc, av[t], acc);
     } else {
       kq8_block(pl, t, dq[t], xc, acc);
     }
@@ -255,6 +265,27 @@ __global__ void __launch_bounds__(NW * 64)
   const u32x4 *Wl = W + rbase * F::NPB * 64 + (row & 63);
   const uint16_t *Wdl = Wd + rbase * 64 + (row & 63);
 
+  // 2. this wave's unit in flight: Q4_0 (8 planes) requests it at entry, so
+  // the prologue runs under the weights' HBM latency; the K-quant formats
+  // (up to 16 planes) after the prologue
+  constexpr bool kEarlyW = FMT == SYN_HIP_FMT_Q4_0;
+  const bool has_unit = wave < nu_wg;
+  u32x4 buf[F::NPU];
+  uint16_t dbuf[F::DPU > 0 ? F::DPU : 1];
+  auto issue_unit = [&]() {
+    if (has_unit) {
+      const int u = u0 + wave;
+      const u32x4 *src = Wl + (size_t)u * F::BPU * F::NPB * 64;
+#pragma unroll
+      for (int p = 0; p < F::NPU; p++) buf[p] = __builtin_nontemporal_load(src + p * 64);
+#pragma unroll
+      for (int j = 0; j < F::DPU; j++)
+        dbuf[j] = __builtin_nontemporal_load(Wdl + ((size_t)u * F::BPU + j) * 64);
+    }
+  };
+  if constexpr (kEarlyW) issue_unit();
+  asm volatile("" ::: "memory");
+
   // 1. the prologue's loads, ahead of the weights
   const int H4 = in.H >> 2;
   i64x2 rl[kRounds][2];  // NORM: the residual row, fixed point
@@ -289,7 +320,7 @@ __global__ void __launch_bounds__(NW * 64)
       const int i = tid + r * kNT;
       if (i < nk / 4) el[r] = reinterpret_cast<const float4 *>(in.x + k0)[i];
     }
-  } else {
+  } else if constexpr (PRO == KQF_PRO_ATTN) {
     // the first chunks' partials are read before the position is known
     // (chunk indices clamped in bounds; chunks past the position are masked)
     const int hd = in.hd, hs = __builtin_ctz(hd), h0 = k0 >> hs, nhs = nk >> hs;
@@ -350,6 +381,21 @@ __global__ void __launch_bounds__(NW * 64)
       const int i = tid + r * kNT;
       if (i < nk / 4) put(i, el[r]);
     }
+  } else if constexpr (PRO == KQF_PRO_CONV) {
+    // the slice's channels; row group 0 writes their next state half
+    const int cpos = in.st->pos, inner = in.inner, ck = in.ck;
+    const size_t half = (size_t)inner * ck;
+    const float *sold = in.cstate + (size_t)(cpos & 1) * half;
+    float *snew = blockIdx.x == 0 ? in.cstate + (size_t)((cpos + 1) & 1) * half : nullptr;
+    for (int t = tid; t < nk; t += kNT) {  // one channel per thread
+      const int ch = k0 + t;
+      xs[t] = liv_conv_channel(kqf_unfix(in.cacc[ch]), kqf_unfix(in.cacc[inner + ch]),
+                               kqf_unfix(in.cacc[2 * inner + ch]), ck, sold + (size_t)ch * ck,
+                               snew ? snew + (size_t)ch * ck : nullptr, in.cw + (size_t)ch * ck,
+                               in.cb ? in.cb + ch : nullptr);
+    }
+    __syncthreads();
+    for (int i = tid; i < nk / 4; i += kNT) put(i, xs4[i]);  // nk / 4: a multiple of 64
   } else {  // x = sum_c exp(m_c - M) o_c / sum_c exp(m_c - M) l_c
     const int hd = in.hd, hs = __builtin_ctz(hd), h0 = k0 >> hs, nhs = nk >> hs, nch = in.nch;
     float *cm = as + bs * GPU;  // [nhs][nch] chunk maxima, then weights
@@ -439,19 +485,7 @@ __global__ void __launch_bounds__(NW * 64)
   SYN_TS(2);
   __syncthreads();
   SYN_TS(3);
-  // 2. this wave's unit in flight
-  const bool has_unit = wave < nu_wg;
-  u32x4 buf[F::NPU];
-  uint16_t dbuf[F::DPU > 0 ? F::DPU : 1];
-  if (has_unit) {
-    const int u = u0 + wave;
-    const u32x4 *src = Wl + (size_t)u * F::BPU * F::NPB * 64;
-#pragma unroll
-    for (int p = 0; p < F::NPU; p++) buf[p] = __builtin_nontemporal_load(src + p * 64);
-#pragma unroll
-    for (int j = 0; j < F::DPU; j++)
-      dbuf[j] = __builtin_nontemporal_load(Wdl + ((size_t)u * F::BPU + j) * 64);
-  }
+  if constexpr (!kEarlyW) issue_unit();
   asm volatile("" ::: "memory");
   SYN_TS(1);
 
@@ -731,7 +765,7 @@ void launch_nw(int nw, dim3 grid, size_t lds, hipStream_t s, const u32x4 *W, con
 inline int waves_for(int bs) { return bs <= 4 ? 4 : bs <= 8 ? 8 : bs <= 12 ? 12 : 16; }
 
 template <int PRO, int OUT>
-syn_status_t launch_gemv(const QLinearKQ &w, const KqfPlan &p, const KqfIn &in, const KqfOut &o,
+syn_status_t launch_gemv(const KqfW &w, const KqfPlan &p, const KqfIn &in, const KqfOut &o,
                          hipStream_t s) {
   size_t lds = (size_t)p.bs * (256 + groups_per_unit(w.fmt)) * sizeof(float);
   if (PRO == KQF_PRO_ATTN) {
@@ -744,8 +778,8 @@ syn_status_t launch_gemv(const QLinearKQ &w, const KqfPlan &p, const KqfIn &in, 
   }
   const dim3 grid(p.groups, p.ks);
   const int nw = waves_for(p.bs);
-  const u32x4 *W = w.wq.as<u32x4>();
-  const uint16_t *Wd = w.wd.as<uint16_t>();
+  const u32x4 *W = static_cast<const u32x4 *>(w.wq);
+  const uint16_t *Wd = static_cast<const uint16_t *>(w.wd);
   switch (w.fmt) {
     case SYN_HIP_FMT_Q4_K:
       launch_nw<SYN_HIP_FMT_Q4_K, PRO, OUT>(nw, grid, lds, s, W, Wd, w.blocks, (int)w.n, p.bs, in,
@@ -759,6 +793,10 @@ syn_status_t launch_gemv(const QLinearKQ &w, const KqfPlan &p, const KqfIn &in, 
       launch_nw<SYN_HIP_FMT_Q8_0, PRO, OUT>(nw, grid, lds, s, W, Wd, w.blocks, (int)w.n, p.bs, in,
                                             o);
       break;
+    case SYN_HIP_FMT_Q4_0:
+      launch_nw<SYN_HIP_FMT_Q4_0, PRO, OUT>(nw, grid, lds, s, W, Wd, w.blocks, (int)w.n, p.bs, in,
+                                            o);
+      break;
     default:
       set_error("fused K-quant GEMV: unsupported format");
       return SYN_ERR_INVALID_ARG;
@@ -769,11 +807,16 @@ syn_status_t launch_gemv(const QLinearKQ &w, const KqfPlan &p, const KqfIn &in, 
 
 }  // namespace
 
+KqfW::KqfW(const QLinearKQ &w)
+    : fmt(w.fmt), n(w.n), k(w.k), blocks(w.blocks), wq(w.wq.p), wd(w.wd.p) {}
+KqfW::KqfW(const QLinearQ4_0 &w)
+    : fmt(SYN_HIP_FMT_Q4_0), n(w.n), k(w.k), blocks(w.blocks), wq(w.nib.p), wd(w.sc.p) {}
+
 bool kqf_fits(int H, int qd, int inter, int nh, int nkv, int hd, int max_seq, const int *fmts,
               int nfmt) {
   for (int i = 0; i < nfmt; i++)
     if (fmts[i] != SYN_HIP_FMT_Q4_K && fmts[i] != SYN_HIP_FMT_Q6_K &&
-        fmts[i] != SYN_HIP_FMT_Q8_0)
+        fmts[i] != SYN_HIP_FMT_Q8_0 && fmts[i] != SYN_HIP_FMT_Q4_0)
       return false;
   // whole 256-element units along every K; a norm row in kRounds float4 per
   // thread; the slice of a split-K GEMV without a norm in kRounds too
@@ -783,7 +826,7 @@ bool kqf_fits(int H, int qd, int inter, int nh, int nkv, int hd, int max_seq, co
   return max_seq >= 1;
 }
 
-KqfPlan kqf_plan(const QLinearKQ &w, bool gu) {
+KqfPlan kqf_plan(const KqfW &w, bool gu) {
   KqfPlan p;
   p.units = (int)(w.k / 256);
   if (gu) {  // the SwiGLU epilogue needs whole dot products: no K split
@@ -803,7 +846,7 @@ KqfPlan kqf_plan(const QLinearKQ &w, bool gu) {
   return p;
 }
 
-syn_status_t kqf_gemv(const QLinearKQ &w, const KqfPlan &p, int pro, const KqfIn &in,
+syn_status_t kqf_gemv(const KqfW &w, const KqfPlan &p, int pro, const KqfIn &in,
                       long long *acc, long long *zero, int nzero, hipStream_t s) {
   KqfOut o;
   o.acc = acc;
@@ -813,11 +856,12 @@ syn_status_t kqf_gemv(const QLinearKQ &w, const KqfPlan &p, int pro, const KqfIn
     case KQF_PRO_NORM: return launch_gemv<KQF_PRO_NORM, OUT_ACC>(w, p, in, o, s);
     case KQF_PRO_EMBED: return launch_gemv<KQF_PRO_EMBED, OUT_ACC>(w, p, in, o, s);
     case KQF_PRO_ATTN: return launch_gemv<KQF_PRO_ATTN, OUT_ACC>(w, p, in, o, s);
+    case KQF_PRO_CONV: return launch_gemv<KQF_PRO_CONV, OUT_ACC>(w, p, in, o, s);
     default: return launch_gemv<KQF_PRO_NONE, OUT_ACC>(w, p, in, o, s);
   }
 }
 
-syn_status_t kqf_gate_up(const QLinearKQ &w, const KqfPlan &p, const KqfIn &in, int inter,
+syn_status_t kqf_gate_up(const KqfW &w, const KqfPlan &p, const KqfIn &in, int inter,
                          float *h, hipStream_t s) {
   KqfOut o;
   o.y = h;
@@ -825,7 +869,7 @@ syn_status_t kqf_gate_up(const QLinearKQ &w, const KqfPlan &p, const KqfIn &in, 
   return launch_gemv<KQF_PRO_NORM, OUT_GU>(w, p, in, o, s);
 }
 
-syn_status_t kqf_lm_head(const QLinearKQ &w, const KqfPlan &p, const KqfIn &in, float *logits,
+syn_status_t kqf_lm_head(const KqfW &w, const KqfPlan &p, const KqfIn &in, float *logits,
                          float *pv, int *pi, float *pv2, hipStream_t s) {
   KqfOut o;
   o.y = logits;

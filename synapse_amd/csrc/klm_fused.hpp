@@ -6,6 +6,20 @@
 
 namespace syn {
 
+// A weight matrix as the fused GEMV reads it: 16-byte planes
+// [panel][block][plane][64 rows] and f16 d values [panel][block][64 rows]
+// (QLinearKQ's layout; QLinearQ4_0's nibble planes and scales are the same
+// with one plane per block).  Q4_0 scales are read as IEEE f16 values.
+struct KqfW {
+  int fmt = 0;
+  size_t n = 0, k = 0;
+  int blocks = 0;  // blocks per row
+  const void *wq = nullptr;
+  const void *wd = nullptr;
+  KqfW(const QLinearKQ &w);
+  KqfW(const QLinearQ4_0 &w);
+};
+
 // Launch shape of one split-K GEMV: `groups` row groups (64-row panels, or
 // 32 gate + 32 up rows) x `ks` splits of `bs` 256-element units each.
 struct KqfPlan {
@@ -33,26 +47,43 @@ struct KqfIn {
   const float *ao = nullptr, *aml = nullptr;
   int hd = 0, nch = 0;
   const StepState *st = nullptr;
+  // CONV: the LIV conv step (liv_conv_channel) of the in_proj accumulator
+  // cacc (rows [B | C | x], fixed point) over the state halves cstate
+  // ([2][inner][ck]; row group 0 writes the next half), taps cw [inner][ck],
+  // bias cb (may be null), at st->pos
+  const long long *cacc = nullptr;
+  float *cstate = nullptr;
+  const float *cw = nullptr, *cb = nullptr;
+  int inner = 0, ck = 0;
 };
 
-enum { KQF_PRO_NONE = 0, KQF_PRO_NORM = 1, KQF_PRO_EMBED = 2, KQF_PRO_ATTN = 3 };
+// fixed point: value * 2^32 in an int64, saturated far beyond any activation
+__device__ __forceinline__ long long kqf_fix(float v) {
+  const double d = (double)v * 4294967296.0;
+  return __double2ll_rn(fmin(fmax(d, -4.0e18), 4.0e18));
+}
+__device__ __forceinline__ float kqf_unfix(long long a) {
+  return (float)((double)a * 2.3283064365386963e-10);
+}
+
+enum { KQF_PRO_NONE = 0, KQF_PRO_NORM = 1, KQF_PRO_EMBED = 2, KQF_PRO_ATTN = 3, KQF_PRO_CONV = 4 };
 
 // whether the fused step supports a model of these shapes and formats
 bool kqf_fits(int H, int qd, int inter, int nh, int nkv, int hd, int max_seq, const int *fmts,
               int nfmt);
 // split plan of a GEMV over n rows and k inputs (gu: gate|up pairs, whole K)
-KqfPlan kqf_plan(const QLinearKQ &w, bool gu);
+KqfPlan kqf_plan(const KqfW &w, bool gu);
 // split-K GEMV whose splits add their fixed-point dot products into acc[row]
 // with atomics; zero[0 .. nzero) is cleared first (the QKV accumulator, for
 // the next layer, by the O projection)
-syn_status_t kqf_gemv(const QLinearKQ &w, const KqfPlan &p, int pro, const KqfIn &in,
+syn_status_t kqf_gemv(const KqfW &w, const KqfPlan &p, int pro, const KqfIn &in,
                       long long *acc, long long *zero, int nzero, hipStream_t s);
 // gate|up rows (w = [gate; up], inter rows each) over the whole K of
 // rmsnorm(r) and h = silu(gate) * up
-syn_status_t kqf_gate_up(const QLinearKQ &w, const KqfPlan &p, const KqfIn &in, int inter,
+syn_status_t kqf_gate_up(const KqfW &w, const KqfPlan &p, const KqfIn &in, int inter,
                          float *h, hipStream_t s);
 // lm_head rows of rmsnorm(r) -> logits and the per-panel top-2 (pv, pi, pv2)
-syn_status_t kqf_lm_head(const QLinearKQ &w, const KqfPlan &p, const KqfIn &in, float *logits,
+syn_status_t kqf_lm_head(const KqfW &w, const KqfPlan &p, const KqfIn &in, float *logits,
                          float *pv, int *pi, float *pv2, hipStream_t s);
 // attention of one token per (kv head, 64-position chunk): q/k/v from the
 // fixed-point QKV accumulator, head norms (qn/kn may be null), RoPE, KV

@@ -144,4 +144,32 @@ __device__ __forceinline__ void kq8_block(const u32x4 *pl, int j, float d,
   acc = __builtin_fmaf(s, d, acc);
 }
 
+// Q4_0 block (one 16-byte plane: element 2i in the low nibble of byte i,
+// 2i+1 in the high; value (q - 8) * d): the nibbles as in-place f16
+// subnormals (the masks above), s0 over the even elements at 2^-24, s1 over
+// the odd at 16 * 2^-24, then the -8 offset as 8 * xsum (the caller's sum of
+// the block's 32 activations).
+__device__ __forceinline__ void kq40_block(const u32x4 &pl, float d, const float *__restrict__ xc,
+                                           float xsum, float &acc) {
+  const uint32_t wd[4] = {pl.x, pl.y, pl.z, pl.w};
+  float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll
+  for (int c = 0; c < 4; c++) {
+    const uint32_t w = wd[c], w8 = wd[c] >> 8;
+    const float *x = xc + 8 * c;
+    const kq_h2 p0 = kq_as_h2(w & 0x000f000fu), p1 = kq_as_h2(w & 0x00f000f0u);
+    const kq_h2 p2 = kq_as_h2(w8 & 0x000f000fu), p3 = kq_as_h2(w8 & 0x00f000f0u);
+    s0 = __builtin_fmaf((float)p0.x, x[0], s0);
+    s1 = __builtin_fmaf((float)p1.x, x[1], s1);
+    s0 = __builtin_fmaf((float)p2.x, x[2], s0);
+    s1 = __builtin_fmaf((float)p3.x, x[3], s1);
+    s0 = __builtin_fmaf((float)p0.y, x[4], s0);
+    s1 = __builtin_fmaf((float)p1.y, x[5], s1);
+    s0 = __builtin_fmaf((float)p2.y, x[6], s0);
+    s1 = __builtin_fmaf((float)p3.y, x[7], s1);
+  }
+  const float dot = __builtin_fmaf(s1, 0.0625f, s0) * 16777216.0f;
+  acc = __builtin_fmaf(dot - 8.0f * xsum, d, acc);
+}
+
 }  // namespace syn

@@ -188,7 +188,8 @@ SIGNATURES = {
     "syn_hip_hlm_prefill": (ST, [P, P, SZ, P]),
     "syn_hip_hlm_generate": (ST, [P, P, SZ, SZ, P, P]),
     "syn_hip_hlm_decode_timed": (ST, [P, SZ, C.POINTER(C.c_float)]),
-    "syn_hip_hlm_set_options": (ST, [P, C.c_int]),
+    "syn_hip_hlm_set_options": (ST, [P, C.c_int, C.c_int]),
+    "syn_hip_hlm_fused_active": (ST, [P, C.POINTER(C.c_int)]),
     "syn_hip_hlm_destroy": (ST, [P]),
     "syn_hip_fill_normal": (ST, [P, SZ, C.c_uint64, C.c_float]),
     "syn_hip_probe_mfma": (ST, [C.c_int, SZ, C.POINTER(C.c_double)]),
@@ -1045,8 +1046,14 @@ class HybridLM:
         check(lib().syn_hip_hlm_decode_timed(self.h, steps, C.byref(ms)), "hlm_decode_timed")
         return ms.value
 
-    def set_options(self, graph: bool = True):
-        check(lib().syn_hip_hlm_set_options(self.h, int(graph)), "hlm_set_options")
+    def set_options(self, fused: bool = True, graph: bool = True):
+        check(lib().syn_hip_hlm_set_options(self.h, int(fused), int(graph)), "hlm_set_options")
+
+    @property
+    def fused_active(self) -> bool:
+        v = C.c_int()
+        check(lib().syn_hip_hlm_fused_active(self.h, C.byref(v)), "hlm_fused_active")
+        return bool(v.value)
 
     def close(self):
         if self.h:

@@ -231,15 +231,16 @@ def _decoder_run(which: str, steps: int, graph: bool):
         pf, dec = m.time(ids, steps)
         m.close()
         return {"decoder": "klm", "prefill_ms": round(pf, 3), "decode_ms_per_token": round(dec / steps, 4)}
-    if which == "hlm":
+    if which in ("hlm", "hlm-op"):  # the fused step, or the op-by-op one
         hc = dict(bench.LFM25, max_seq=8 + steps + 1)
         hm = hip.HybridLM(hc)
         hm.init_synthetic(bench.SEED_BASE, 0.02)
-        hm.set_options(graph=graph)
+        hm.set_options(fused=which == "hlm", graph=graph)
         hm.prefill(np.array(bench._ids(8, hc["vocab"], bench.PROMPT_SEED), np.uint32))
         ms = hm.decode_timed(steps)
+        fused = hm.fused_active
         hm.close()
-        return {"decoder": "hlm", "decode_ms_per_token": round(ms / steps, 4)}
+        return {"decoder": which, "fused": fused, "decode_ms_per_token": round(ms / steps, 4)}
     xdt = which == "mamba-int8"
     mc = dict(bench.MAMBA370M, max_tokens=64 + steps + 1)
     mm = hip.QuantizedMamba(mc, int8_xdt=xdt)
@@ -266,9 +267,9 @@ if __name__ == "__main__":
         print(json.dumps(gemv_record(FMT_BY_NAME[a[1]], int(a[2]), int(a[3]), "gemv")))
     elif len(a) == 5 and a[0] == "gemm":  # gemm FMT M N K
         print(json.dumps(gemm_record(FMT_BY_NAME[a[1]], int(a[2]), int(a[3]), int(a[4]), "gemm")))
-    elif len(a) in (2, 3) and a[0] in ("klm", "mamba-ref", "mamba-int8", "hlm"):  # DECODER STEPS [eager]
+    elif len(a) in (2, 3) and a[0] in ("klm", "mamba-ref", "mamba-int8", "hlm", "hlm-op"):  # DECODER STEPS [eager]
         print(json.dumps(_decoder_run(a[0], int(a[1]), graph=not (len(a) == 3 and a[2] == "eager"))))
     else:
         print("usage: python -m synapse_amd.microbench copy NBYTES | gemv FMT N K | "
-              "gemm FMT M N K | {klm,mamba-ref,mamba-int8,hlm} STEPS [eager]", file=sys.stderr)
+              "gemm FMT M N K | {klm,mamba-ref,mamba-int8,hlm,hlm-op} STEPS [eager]", file=sys.stderr)
         sys.exit(2)
