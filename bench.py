@@ -239,13 +239,20 @@ def secondary(hip, np):
     hm.init_synthetic(SEED_BASE, 0.02)
     hm.prefill(np.array(_ids(8, hc["vocab"], PROMPT_SEED), np.uint32))
     ms = hm.decode_timed(128)
+    fused = hm.fused_active
+    hm.reset()
+    hm.set_options(fused=False)
+    hm.prefill(np.array(_ids(8, hc["vocab"], PROMPT_SEED), np.uint32))
+    ms_op = hm.decode_timed(128)
     hm.close()
     hb = hybrid_weight_bytes(LFM25)
     out["hybrid_lfm25_q4_0_decode"] = {
         "decode_tok_s": round(128e3 / ms, 1), "decode_ms_per_token": round(ms / 128, 4),
         "weight_bytes_per_token": hb, "decode_weight_gbs": round(hb / (ms / 128 * 1e-3) / 1e9, 1),
+        "fused": fused, "op_by_op_tok_s": round(128e3 / ms_op, 1),
         "note": "16 layers (10 LIV conv, 6 GQA), Q4_0 projections, tied f32 lm_head (65536 x "
-                "1024), graph replay of the op-by-op step"}
+                "1024), graph replay of the fused five-kernel step (op_by_op_tok_s: the "
+                "op-by-op step)"}
     out["seconds"] = round(time.perf_counter() - t0, 1)
     return out
 

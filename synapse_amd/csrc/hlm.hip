@@ -23,6 +23,7 @@
 
 #include "decode_fused.hpp"
 #include "f32_ops.hpp"
+#include "head_f32.hpp"
 #include "klm_fused.hpp"
 #include "layer_ops.hpp"
 #include "linear.hpp"
@@ -201,123 +202,9 @@ __global__ void __launch_bounds__(256)
   if (i < F) h[i] = syn_silu(part_row(gu, i)) * part_row(gu, F + i);
 }
 
-// Tied f32 lm_head of the fused step: logits[row] = (E[row] . (r * gain)) /
-// rms(r), r the fixed-point residual, E the embedding [V][H] row-major, and
-// the workgroup's top-2 for launch_argmax_advance.  256 threads, 64 rows per
-// workgroup (16 per wave); lane j holds the activations of float4 columns
-// j + 64 c of the row (H = 256 NC), so a row is NC coalesced 1 KiB loads per
-// wave and a butterfly sum (equal in every lane).  Every wave computes the
-// row's sum of squares itself.  The sums run in this tree order (the decoder
-// is graded by tolerance).
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-template <int NC>
-__global__ void __launch_bounds__(256)
-    k_hlm_head_top2(const f32x4 *__restrict__ E, int V, const long long *__restrict__ r,
-                    const float *__restrict__ gain, float eps, float *__restrict__ logits,
-                    float *__restrict__ pv, int *__restrict__ pi, float *__restrict__ pv2) {
-  // float4 per row; rows per batch of loads (one batch in registers, no
-  // prefetch: the other waves of the SIMD cover its latency, and the whole
-  // grid stays resident)
-  constexpr int H4 = 64 * NC, RB = NC <= 4 ? 4 : 2;
-  __shared__ float sv1[4], sv2[4];
-  __shared__ int si1[4];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int row0 = blockIdx.x * 64 + wave * 16;
-  f32x4 w[RB][NC];
-  auto issue = [&](int b) {
-#pragma unroll
-    for (int rr = 0; rr < RB; rr++) {
-      const int row = min(row0 + b + rr, V - 1);
-#pragma unroll
-      for (int c = 0; c < NC; c++)
-        w[rr][c] = __builtin_nontemporal_load(E + (size_t)row * H4 + lane + 64 * c);
-    }
-  };
-  float4 xg[NC];
-  float ss = 0.0f;
-#pragma unroll
-  for (int c = 0; c < NC; c++) {
-    const int i = lane + 64 * c;
-    const long long *rp = r + 4 * (size_t)i;
-    const float4 a = make_float4(kqf_unfix(rp[0]), kqf_unfix(rp[1]), kqf_unfix(rp[2]),
-                                 kqf_unfix(rp[3]));
-    const float4 g = reinterpret_cast<const float4 *>(gain)[i];
-    ss += (a.x * a.x + a.y * a.y) + (a.z * a.z + a.w * a.w);
-    xg[c] = make_float4(a.x * g.x, a.y * g.y, a.z * g.z, a.w * g.w);
-  }
-  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-  const float inv = 1.0f / sqrtf(ss / (float)(4 * H4) + eps);
-  Top2v t{-__builtin_inff(), -1, -__builtin_inff()};
-#pragma unroll 1
-  for (int b = 0; b < 16; b += RB) {
-    issue(b);
-    float dot[RB];
-#pragma unroll
-    for (int rr = 0; rr < RB; rr++) {
-      float a = 0.0f;
-#pragma unroll
-      for (int c = 0; c < NC; c++) {
-        a = __builtin_fmaf(w[rr][c].x, xg[c].x, a);
-        a = __builtin_fmaf(w[rr][c].y, xg[c].y, a);
-        a = __builtin_fmaf(w[rr][c].z, xg[c].z, a);
-        a = __builtin_fmaf(w[rr][c].w, xg[c].w, a);
-      }
-      dot[rr] = a;
-    }
-#pragma unroll
-    for (int rr = 0; rr < RB; rr++) {
-      float a = dot[rr];
-      for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o);
-      const int row = row0 + b + rr;
-      if (row < V) {
-        const float v = a * inv;
-        if (lane == 0) logits[row] = v;
-        t = top2v_merge(t, Top2v{v, row, -__builtin_inff()});
-      }
-    }
-  }
-  if (lane == 0) {
-    sv1[wave] = t.v1;
-    si1[wave] = t.i1;
-    sv2[wave] = t.v2;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    Top2v m{sv1[0], si1[0], sv2[0]};
-    for (int i = 1; i < 4; i++) m = top2v_merge(m, Top2v{sv1[i], si1[i], sv2[i]});
-    pv[blockIdx.x] = m.v1;
-    pi[blockIdx.x] = m.i1;
-    pv2[blockIdx.x] = m.v2;
-  }
-}
-
 }  // namespace syn
 
 using namespace syn;
-
-static syn_status_t launch_hlm_head_top2(const float *E, int V, int H, const long long *r,
-                                         const float *gain, float eps, float *logits, float *pv,
-                                         int *pi, float *pv2, hipStream_t s) {
-  const dim3 grid((unsigned)cdiv((size_t)V, 64));
-#define HLM_HEAD(NC_)                                                                     \
-  hipLaunchKernelGGL((k_hlm_head_top2<NC_>), grid, dim3(256), 0, s,                       \
-                     reinterpret_cast<const f32x4 *>(E), V, r, gain, eps, logits, pv, pi, pv2)
-  switch (H) {
-    case 256: HLM_HEAD(1); break;
-    case 512: HLM_HEAD(2); break;
-    case 768: HLM_HEAD(3); break;
-    case 1024: HLM_HEAD(4); break;
-    case 1536: HLM_HEAD(6); break;
-    case 2048: HLM_HEAD(8); break;
-    default:
-      set_error("hybrid lm_head: hidden must be 256, 512, 768, 1024, 1536 or 2048");
-      return SYN_ERR_INVALID_ARG;
-  }
-#undef HLM_HEAD
-  SYN_LAUNCH_CHECK();
-  return SYN_OK;
-}
 
 static syn_status_t launch_hlm_norm(float *x, PartRows delta, const float *w, float eps, int H,
                                    float *normed, hipStream_t s) {
@@ -363,7 +250,7 @@ struct syn_hip_hlm_s {
     fused_ok = false;
     const int fm[1] = {SYN_HIP_FMT_Q4_0};
     if (!kqf_fits((int)H, (int)qd, (int)F, (int)nh, (int)nkv, (int)hd, (int)S, fm, 1) ||
-        I % 256 || (H != 256 && H != 512 && H != 768 && H != 1024 && H != 1536 && H != 2048))
+        I % 256 || !head_f32_fits((int)H))
       return SYN_OK;
     bool any_conv = false, any_gqa = false;
     for (auto &Ly : layers) {
@@ -462,9 +349,12 @@ struct syn_hip_hlm_s {
       d.x = hbuf.as<float>();
       SYN_TRY(kqf_gemv(Ly.down, fp_down, KQF_PRO_NONE, d, r, zero_after, nzero, s));
     }
-    SYN_TRY(launch_hlm_head_top2(embed.as<float>(), (int)V, (int)H, r, final_nw.as<float>(), eps,
-                                 logits.as<float>(), f_pv.as<float>(), f_pi.as<int>(),
-                                 f_pv2.as<float>(), s));
+    HeadIn hin;  // the tied f32 lm_head of rmsnorm(r)
+    hin.fx = r;
+    hin.gain = final_nw.as<float>();
+    hin.eps = eps;
+    SYN_TRY(launch_head_f32_top2(embed.as<float>(), (int)V, (int)H, hin, logits.as<float>(),
+                                 f_pv.as<float>(), f_pi.as<int>(), f_pv2.as<float>(), s));
     return launch_argmax_advance(f_pv.as<float>(), f_pi.as<int>(), f_pv2.as<float>(),
                                  (int)cdiv(V, (size_t)64), st(), history.as<uint32_t>(),
                                  mhist.as<float>(), s);

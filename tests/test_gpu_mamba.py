@@ -89,9 +89,11 @@ def _bits(a):
 @pytest.mark.parametrize("xdt", [False, True], ids=["ref", "int8xdt"])
 @pytest.mark.parametrize("cfg", [TINY, RAGGED, dict(MAMBA370, n_layers=4)],
                          ids=["tiny", "ragged", "370m4"])
-def test_fused_step_matches_unfused(cfg, xdt):
-    # the fused split-K step computes the unfused step's float operations:
-    # logits and tokens agree bit for bit, graph or eager
+def test_fused_step_tracks_unfused(cfg, xdt):
+    # each form replays bit for bit (graph or eager); the fused step computes
+    # the unfused step's float operations up to its lm_head, which at d_model
+    # 1024 is the tree-ordered f32 GEMV: logits within the float tolerance,
+    # bit-identical where d_model keeps the exact-order head
     print("case", cfg, "int8_xdt", xdt, flush=True)
     g = hip.QuantizedMamba(dict(cfg, max_tokens=64), int8_xdt=xdt)
     g.init_synthetic()
@@ -103,11 +105,17 @@ def test_fused_step_matches_unfused(cfg, xdt):
             lg = g.prefill(ids)
             toks, margins = g.generate(ids, 12)
             runs[(fused, graph)] = (lg, toks, margins)
-    ref = runs[(False, False)]
-    for key, (lg, toks, margins) in runs.items():
-        np.testing.assert_array_equal(_bits(lg), _bits(ref[0]), err_msg=f"fused,graph={key}")
-        np.testing.assert_array_equal(toks, ref[1], err_msg=f"fused,graph={key}")
-        np.testing.assert_array_equal(_bits(margins), _bits(ref[2]), err_msg=f"fused,graph={key}")
+    for fused in (True, False):
+        a, b = runs[(fused, True)], runs[(fused, False)]
+        np.testing.assert_array_equal(_bits(a[0]), _bits(b[0]), err_msg=f"fused={fused}")
+        np.testing.assert_array_equal(a[1], b[1], err_msg=f"fused={fused}")
+        np.testing.assert_array_equal(_bits(a[2]), _bits(b[2]), err_msg=f"fused={fused}")
+    f, u = runs[(True, False)], runs[(False, False)]
+    if cfg["d_model"] % 256:
+        np.testing.assert_array_equal(_bits(f[0]), _bits(u[0]))
+    assert _cos(f[0], u[0]) >= 0.9999
+    thin = next((i for i, m in enumerate(u[2]) if m < 1e-3), len(u[2]))
+    np.testing.assert_array_equal(f[1][:thin], u[1][:thin])
     g.close()
 
 
