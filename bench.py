@@ -251,7 +251,7 @@ def secondary(hip, np):
         "weight_bytes_per_token": hb, "decode_weight_gbs": round(hb / (ms / 128 * 1e-3) / 1e9, 1),
         "fused": fused, "op_by_op_tok_s": round(128e3 / ms_op, 1),
         "note": "16 layers (10 LIV conv, 6 GQA), Q4_0 projections, tied f32 lm_head (65536 x "
-                "1024), graph replay of the fused five-kernel step (op_by_op_tok_s: the "
+                "1024), graph replay of the fused step, 72 kernels (op_by_op_tok_s: the "
                 "op-by-op step)"}
     out["seconds"] = round(time.perf_counter() - t0, 1)
     return out

@@ -597,7 +597,8 @@ syn_status_t syn_hip_hlm_generate(syn_hip_hlm_t *m, const uint32_t *prompt, size
                                   size_t max_new, uint32_t *out_tokens, float *out_margins);
 /* hipEvent time of `steps` greedy decode steps from the current state */
 syn_status_t syn_hip_hlm_decode_timed(syn_hip_hlm_t *m, size_t steps, float *elapsed_ms);
-/* fused != 0 (the default): five kernels per layer when the shapes fit
+/* fused != 0 (the default): four kernels per LIV conv layer and five per
+ * GQA layer when the shapes fit
  * (hidden 256..2048 in whole 256s, inner, inter, n_heads * head_dim multiples
  * of 256, head_dim 16..128, n_heads / n_kv_heads <= 8, IEEE block scales):
  * the Q4_0 rows of split-K workgroups add into fixed-point accumulators,
