@@ -215,6 +215,9 @@ struct syn_hip_klm_s {
     fp_lm = kqf_plan(lm_head, false);
     fp_lm.bs = fp_lm.units;  // the top-2 epilogue needs whole dot products
     fp_lm.ks = 1;
+    // workgroups that each loop over 64-row panels (one prologue per
+    // workgroup); the merge reads one top-2 per workgroup
+    fp_lm.groups = std::min(fp_lm.groups, kKqfTop2Groups);
     const size_t nch = (size_t)kqf_chunks((int)S), nh = c.base.n_heads;
     SYN_TRY(f_r.alloc(h * 8));
     SYN_TRY(f_qkv.alloc(n_qkv * 8));

@@ -261,9 +261,8 @@ __global__ void __launch_bounds__(NW * 64)
   } else {
     row = blockIdx.x * 64 + lane;
   }
-  const size_t rbase = (size_t)(row >> 6) * B;
-  const u32x4 *Wl = W + rbase * F::NPB * 64 + (row & 63);
-  const uint16_t *Wdl = Wd + rbase * 64 + (row & 63);
+  const u32x4 *Wl = W + (size_t)(row >> 6) * B * F::NPB * 64 + (row & 63);
+  const uint16_t *Wdl = Wd + (size_t)(row >> 6) * B * 64 + (row & 63);
 
   // 2. this wave's unit in flight: Q4_0 (8 planes) requests it at entry, so
   // the prologue runs under the weights' HBM latency; the K-quant formats
@@ -497,6 +496,55 @@ __global__ void __launch_bounds__(NW * 64)
   if (has_unit) kqf_unit<FMT, (NW < 16)>(buf, dbuf, xs + wave * 256, as + wave * GPU, acc);
   SYN_TS(5);
 
+  if constexpr (OUT == OUT_TOP2) {
+    // lm_head (no K split): the workgroup takes the 64-row panels blockIdx.x,
+    // + gridDim.x, ... after one prologue; each wave requests its unit of the
+    // next panel before the current panel's reduction
+    const int np = (N + 63) >> 6;
+    float inv = 1.0f;
+    if constexpr (PRO == KQF_PRO_NORM || PRO == KQF_PRO_EMBED) {
+      float t = 0.0f;
+#pragma unroll
+      for (int w = 0; w < NW; w++) t += ssr[w];
+      inv = 1.0f / sqrtf(t / (float)in.H + in.eps);
+    }
+    Top2v best{-__builtin_inff(), -1, -__builtin_inff()};
+    for (int g = blockIdx.x; g < np; g += gridDim.x) {
+      red[wave * 64 + lane] = acc;
+      const int gn = g + gridDim.x;
+      if (gn < np) {
+        Wl = W + (size_t)gn * B * F::NPB * 64 + lane;
+        Wdl = Wd + (size_t)gn * B * 64 + lane;
+        issue_unit();
+      }
+      __syncthreads();
+      if (wave == 0) {
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) v += red[w * 64 + lane];
+        v *= inv;
+        const int r = g * 64 + lane;
+        Top2v c{-__builtin_inff(), -1, -__builtin_inff()};
+        if (r < N) {
+          out.y[r] = v;
+          c = Top2v{v, r, -__builtin_inff()};
+        }
+        best = top2v_merge(best, wave_top2(c));
+      }
+      __syncthreads();  // red is written again for the next panel
+      if (gn < np) {
+        acc = 0.0f;
+        if (has_unit) kqf_unit<FMT, (NW < 16)>(buf, dbuf, xs + wave * 256, as + wave * GPU, acc);
+      }
+    }
+    if (wave == 0 && lane == 0) {
+      out.pv[blockIdx.x] = best.v1;
+      out.pi[blockIdx.x] = best.i1;
+      out.pv2[blockIdx.x] = best.v2;
+    }
+    return;
+  }
+
   // 5. epilogue: waves in order, then the row's consumer form
   red[wave * 64 + lane] = acc;
   __syncthreads();
@@ -527,18 +575,6 @@ __global__ void __launch_bounds__(NW * 64)
       const float sig = 1.0f / (1.0f + syn_expf(-v));  // silu as k_swiglu_f32
       const float t = v * sig;
       out.y[blockIdx.x * 32 + lane] = t * up;
-    }
-  } else {
-    Top2v t{-__builtin_inff(), -1, -__builtin_inff()};
-    if (row < N) {
-      out.y[row] = v;
-      t = Top2v{v, row, -__builtin_inff()};
-    }
-    t = wave_top2(t);
-    if (lane == 0) {
-      out.pv[blockIdx.x] = t.v1;
-      out.pi[blockIdx.x] = t.i1;
-      out.pv2[blockIdx.x] = t.v2;
     }
   }
   SYN_TS(7);

@@ -68,6 +68,8 @@ __device__ __forceinline__ float kqf_unfix(long long a) {
 
 enum { KQF_PRO_NONE = 0, KQF_PRO_NORM = 1, KQF_PRO_EMBED = 2, KQF_PRO_ATTN = 3, KQF_PRO_CONV = 4 };
 
+constexpr int kKqfTop2Groups = 256;  // lm_head workgroups: about one per CU
+
 // whether the fused step supports a model of these shapes and formats
 bool kqf_fits(int H, int qd, int inter, int nh, int nkv, int hd, int max_seq, const int *fmts,
               int nfmt);
@@ -82,7 +84,9 @@ syn_status_t kqf_gemv(const KqfW &w, const KqfPlan &p, int pro, const KqfIn &in,
 // rmsnorm(r) and h = silu(gate) * up
 syn_status_t kqf_gate_up(const KqfW &w, const KqfPlan &p, const KqfIn &in, int inter,
                          float *h, hipStream_t s);
-// lm_head rows of rmsnorm(r) -> logits and the per-panel top-2 (pv, pi, pv2)
+// lm_head rows of rmsnorm(r) -> logits and a top-2 per workgroup (pv, pi,
+// pv2); workgroup b takes the 64-row panels b, b + p.groups, ... (p.groups
+// at most kKqfTop2Groups)
 syn_status_t kqf_lm_head(const KqfW &w, const KqfPlan &p, const KqfIn &in, float *logits,
                          float *pv, int *pi, float *pv2, hipStream_t s);
 // attention of one token per (kv head, 64-position chunk): q/k/v from the
