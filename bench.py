@@ -50,10 +50,15 @@ REF_DECODE_TOKS = 27.3  # Qwen3-0.6B INT8 decode, reference cpu_simd (Apple Sili
 # readings in profiles/lm_head_int8_qwen3_k_lmhead_top2.md
 LM_HEAD_FETCH_KIB, LM_HEAD_FETCH_FACTOR = 76301.0, 262144.0 / 131084.7
 LM_HEAD_WRITE_KIB, LM_HEAD_WRITE_FACTOR = 816.5, 262144.0 / 262144.0
-# HBM traffic per launch of the step's kernels, from the same two counter runs
-# (FETCH_SIZE and WRITE_SIZE per dispatch, scaled as above); None until a
-# counter run of that kernel is recorded under profiles/
-STEP_KERNEL_TRAFFIC = {}
+# HBM traffic per launch of the step's kernels: median FETCH_SIZE and
+# WRITE_SIZE (KiB per dispatch) over the 364 dispatches of each kernel in two
+# counter runs of eager steps at positions 16-29, scaled as above (readings
+# and commands in profiles/qwen3_int8_decode_step_kernels_traffic.md; the
+# attention's traffic grows with the position)
+_STEP_KIB = {"qkv": (2172.0, 132.0), "attention": (655.2, 32.0), "o": (1083.5, 128.0),
+             "gate_up": (3247.5, 22.0), "down": (1605.0, 96.0)}
+STEP_KERNEL_TRAFFIC = {k: round(1024 * (f * LM_HEAD_FETCH_FACTOR + w * LM_HEAD_WRITE_FACTOR))
+                       for k, (f, w) in _STEP_KIB.items()}
 
 
 def step_weight_bytes(c):
