@@ -111,6 +111,35 @@ def test_hybrid_fused_tracks_oracle(kinds):
     print(f"fused {kinds}: worst rel {worst:.2e}")
 
 
+@pytest.mark.parametrize("hidden,hd,group", [(512, 64, 2), (768, 64, 4), (1536, 128, 2)])
+def test_hybrid_fused_other_widths(hidden, hd, group):
+    """Head kernel widths NC = 2, 3, 6 (hidden = 256 NC), head_dim 64 and 128,
+    GQA groups of 2 and 4."""
+    nh = hidden // hd
+    cfg = dict(SMALL, hidden=hidden, inner=hidden, inter=2 * hidden, n_heads=nh,
+               n_kv_heads=nh // group, head_dim=hd, vocab=700, n_layers=2, layer_kinds=[1, 0],
+               max_seq=32)
+    dev, ref = _pair(cfg, 0x5EED0000 + hidden, 0.05)
+    assert dev.fused_active
+    for t, tok in enumerate(O.token_ids(20, hidden, cfg["vocab"])):
+        _cmp(dev.decode_one(int(tok)), ref.decode_one(int(tok)), (hidden, t))
+
+
+def test_hybrid_fused_long_context():
+    """330 positions: the chunked attention combines six 64-position chunks,
+    and the conv state halves alternate 330 times."""
+    cfg = dict(SMALL, n_layers=2, layer_kinds=[0, 1], max_seq=336)
+    dev, ref = _pair(cfg, 9, 0.08)
+    assert dev.fused_active
+    toks = O.token_ids(330, 21, cfg["vocab"])
+    worst = 0.0
+    for t, tok in enumerate(toks):
+        got, want = dev.decode_one(int(tok)), ref.decode_one(int(tok))
+        if t % 10 == 0 or t >= 320:
+            worst = max(worst, _cmp(got, want, ("long", t)))
+    print(f"long context: worst rel {worst:.2e}")
+
+
 def test_hybrid_fused_graph_eager_and_reset_agree():
     """Fixed-point split-K sums are order-free: graph replay, eager launches
     and a replay after reset give the same logits bit for bit."""
