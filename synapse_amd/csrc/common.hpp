@@ -108,6 +108,17 @@ uint16_t f32_to_f16_trunc(float v);
 }  // namespace syn
 
 // ---------------------------------------------------------------- device math
+// Fixed point for order-free float sums (split-K atomics): value * 2^32 in
+// an int64, saturated far beyond any activation; sums of these are exact in
+// any order, so split-K workgroups can add them with integer atomics.
+__device__ __forceinline__ long long kqf_fix(float v) {
+  const double d = (double)v * 4294967296.0;
+  return __double2ll_rn(fmin(fmax(d, -4.0e18), 4.0e18));
+}
+__device__ __forceinline__ float kqf_unfix(long long a) {
+  return (float)((double)a * 2.3283064365386963e-10);
+}
+
 // clang vector types (usable with __builtin_nontemporal_load)
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));

@@ -285,6 +285,7 @@ struct syn_hip_hlm_s {
     SYN_TRY(f_pv.alloc(panels * 4));
     SYN_TRY(f_pi.alloc(panels * 4));
     SYN_TRY(f_pv2.alloc(panels * 4));
+    SYN_HIP(hipDeviceSynchronize());  // the memsets ran on the null stream, not the model's
     fused_ok = true;
     return SYN_OK;
   }

@@ -66,12 +66,21 @@ syn_status_t launch_quantize_rows(const float *d_x, size_t m, size_t k, size_t l
 // grid (panels, ksplit); blockDim = 64 * waves.  Lane = output row of the
 // panel; each wave walks 16-byte K chunks (one 1 KiB load per chunk) and does
 // 4 v_dot4_i32_i8 per activation row.  Waves reduce in LDS (i32, exact).
-template <int M>
+// A K split either writes per-slice partials for k_gemv_reduce (SK false), or
+// (SK true, one launch) adds them into the int32 accumulators part[M][N64]
+// with device-scope atomics, waits for their return (the add has then been
+// performed at the point of coherence every XCD's atomics go to), and counts
+// its arrival on cnt[panel]; the panel's last slice reads the totals back by
+// atomic exchange with 0 (leaving them cleared for the next call), applies
+// the epilogue and clears the counter.  Integer sums are exact in any order.
+template <int M, bool SK>
 __global__ void __launch_bounds__(1024)
     k_gemv_w8a8(const i32x4 *__restrict__ W, const float *__restrict__ ws,
                 const int8_t *__restrict__ xq, int ldx, const float *__restrict__ sx,
-                float *__restrict__ y, int ldy, int *__restrict__ part, int N, int C, int cs) {
+                float *__restrict__ y, int ldy, int *__restrict__ part, int *__restrict__ cnt,
+                int N, int C, int cs) {
   extern __shared__ int red[];  // [waves][M][64]
+  __shared__ int s_last;
   const int panel = blockIdx.x, ks = blockIdx.y;
   const int nw = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -116,6 +125,35 @@ __global__ void __launch_bounds__(1024)
   for (int m = 0; m < M; m++) red[(wave * M + m) * 64 + lane] = acc[m];
   __syncthreads();
   const int N64 = gridDim.x * 64;
+  if constexpr (SK) {
+    int seen = 0;
+    for (int t = threadIdx.x; t < M * 64; t += blockDim.x) {
+      const int m = t >> 6, r = t & 63;
+      int s = 0;
+      for (int w = 0; w < nw; w++) s += red[(w * M + m) * 64 + r];
+      seen |= __hip_atomic_fetch_add(part + (size_t)m * N64 + panel * 64 + r, s, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("" ::"v"(seen));  // every add of this thread has returned
+    __syncthreads();
+    if (threadIdx.x == 0)
+      s_last = __hip_atomic_fetch_add(cnt + panel, 1, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.y - 1;
+    __syncthreads();
+    if (!s_last) return;
+    for (int t = threadIdx.x; t < M * 64; t += blockDim.x) {
+      const int m = t >> 6, r = t & 63, row = panel * 64 + r;
+      const int tot = __hip_atomic_exchange(part + (size_t)m * N64 + row, 0, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+      if (row < N) {
+        const float f = (float)tot * sx[m];
+        y[(size_t)m * ldy + row] = f * ws[row];
+      }
+    }
+    if (threadIdx.x == 0)
+      __hip_atomic_exchange(cnt + panel, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
   for (int t = threadIdx.x; t < M * 64; t += blockDim.x) {
     const int m = t >> 6, r = t & 63;
     int s = 0;
@@ -178,18 +216,23 @@ GemvPlan make_gemv_plan(size_t n, size_t k_chunks, bool chunked_kc) {
   return p;
 }
 
+// cnt != nullptr: the single-launch split-K form (part = the accumulators)
 template <int M>
 static void launch_gemv_m(const GemvPlan &p, const i32x4 *W, const float *ws, const int8_t *xq,
-                          int ldx, const float *sx, float *y, int ldy, int *part, int N,
+                          int ldx, const float *sx, float *y, int ldy, int *part, int *cnt, int N,
                           hipStream_t s) {
   const int waves = std::min(p.waves, M >= 8 ? 8 : 16);
   const size_t shm = (size_t)waves * M * 64 * sizeof(int);
-  hipLaunchKernelGGL(k_gemv_w8a8<M>, dim3(p.panels, p.ksplit), dim3(64 * waves), shm, s, W, ws,
-                     xq, ldx, sx, y, ldy, part, N, p.chunks, p.cs);
+  if (cnt && p.ksplit > 1)
+    hipLaunchKernelGGL((k_gemv_w8a8<M, true>), dim3(p.panels, p.ksplit), dim3(64 * waves), shm, s,
+                       W, ws, xq, ldx, sx, y, ldy, part, cnt, N, p.chunks, p.cs);
+  else
+    hipLaunchKernelGGL((k_gemv_w8a8<M, false>), dim3(p.panels, p.ksplit), dim3(64 * waves), shm,
+                       s, W, ws, xq, ldx, sx, y, ldy, part, nullptr, N, p.chunks, p.cs);
 }
 
 typedef void (*gemv_launcher)(const GemvPlan &, const i32x4 *, const float *, const int8_t *, int,
-                              const float *, float *, int, int *, int, hipStream_t);
+                              const float *, float *, int, int *, int *, int, hipStream_t);
 static const gemv_launcher kGemvLaunch[17] = {
     nullptr,          launch_gemv_m<1>,  launch_gemv_m<2>,  launch_gemv_m<3>,
     launch_gemv_m<4>, launch_gemv_m<5>,  launch_gemv_m<6>,  launch_gemv_m<7>,
@@ -209,7 +252,21 @@ syn_status_t QLinearInt8::prepare(size_t max_m) {
   const size_t mb = std::min<size_t>(16, std::max<size_t>(1, max_m));
   const GemvPlan p = make_gemv_plan(n, (size_t)chunks, false);
   const size_t need = p.ksplit > 1 ? (size_t)p.ksplit * mb * p.panels * 64 : 0;
-  return need ? ensure_part(need) : SYN_OK;
+  if (need) SYN_TRY(ensure_part(need));
+  return ensure_sk();
+}
+
+syn_status_t QLinearInt8::ensure_sk() {
+  const GemvPlan p = make_gemv_plan(n, (size_t)chunks, false);
+  if (p.ksplit <= 1 || sk_panels >= p.panels) return SYN_OK;
+  SYN_HIP(hipDeviceSynchronize());  // the old buffers may still be in use by queued work
+  sk_panels = p.panels;
+  SYN_TRY(sk_acc.alloc((size_t)16 * p.panels * 64 * sizeof(int)));
+  SYN_TRY(sk_cnt.alloc((size_t)p.panels * sizeof(int)));
+  SYN_HIP(hipMemset(sk_acc.p, 0, sk_acc.bytes));  // calls leave them cleared
+  SYN_HIP(hipMemset(sk_cnt.p, 0, sk_cnt.bytes));
+  SYN_HIP(hipDeviceSynchronize());  // the memsets run on the null stream, not the caller's
+  return SYN_OK;
 }
 
 size_t QLinearInt8::part_elems_for(size_t m) const {
@@ -220,8 +277,14 @@ size_t QLinearInt8::part_elems_for(size_t m) const {
 
 syn_status_t QLinearInt8::gemv(size_t m, const int8_t *d_xq, size_t ldx, const float *d_sx,
                                float *d_y, size_t ldy, hipStream_t s) {
-  SYN_TRY(ensure_part(part_elems_for(std::min<size_t>(m, 16))));
-  return gemv_part(m, d_xq, ldx, d_sx, d_y, ldy, part.as<int>(), s);
+  if (m == 0 || n == 0 || k == 0) return SYN_OK;
+  if (m > 16) return gemv_part(m, d_xq, ldx, d_sx, d_y, ldy, nullptr, s);
+  SYN_TRY(ensure_sk());
+  const GemvPlan p = make_gemv_plan(n, (size_t)chunks, false);
+  kGemvLaunch[m](p, w.as<i32x4>(), scales.as<float>(), d_xq, (int)ldx, d_sx, d_y, (int)ldy,
+                 sk_acc.as<int>(), sk_cnt.as<int>(), (int)n, s);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
 }
 
 syn_status_t QLinearInt8::gemv_part(size_t m, const int8_t *d_xq, size_t ldx, const float *d_sx,
@@ -235,7 +298,7 @@ syn_status_t QLinearInt8::gemv_part(size_t m, const int8_t *d_xq, size_t ldx, co
   for (size_t m0 = 0; m0 < m; m0 += 16) {
     const int mb = (int)std::min<size_t>(16, m - m0);
     kGemvLaunch[mb](p, w.as<i32x4>(), scales.as<float>(), d_xq + m0 * ldx, (int)ldx, d_sx + m0,
-                    d_y + m0 * ldy, (int)ldy, d_part, (int)n, s);
+                    d_y + m0 * ldy, (int)ldy, d_part, nullptr, (int)n, s);
     SYN_LAUNCH_CHECK();
     if (p.ksplit > 1) {
       const int total = mb * (int)n;

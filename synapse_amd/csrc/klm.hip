@@ -229,6 +229,7 @@ struct syn_hip_klm_s {
     SYN_TRY(f_pv.alloc((size_t)fp_lm.groups * 4));
     SYN_TRY(f_pi.alloc((size_t)fp_lm.groups * 4));
     SYN_TRY(f_pv2.alloc((size_t)fp_lm.groups * 4));
+    SYN_HIP(hipDeviceSynchronize());  // the memsets ran on the null stream, not the model's
     fused_ok = true;
     return SYN_OK;
   }

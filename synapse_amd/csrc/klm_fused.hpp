@@ -57,15 +57,6 @@ struct KqfIn {
   int inner = 0, ck = 0;
 };
 
-// fixed point: value * 2^32 in an int64, saturated far beyond any activation
-__device__ __forceinline__ long long kqf_fix(float v) {
-  const double d = (double)v * 4294967296.0;
-  return __double2ll_rn(fmin(fmax(d, -4.0e18), 4.0e18));
-}
-__device__ __forceinline__ float kqf_unfix(long long a) {
-  return (float)((double)a * 2.3283064365386963e-10);
-}
-
 enum { KQF_PRO_NONE = 0, KQF_PRO_NORM = 1, KQF_PRO_EMBED = 2, KQF_PRO_ATTN = 3, KQF_PRO_CONV = 4 };
 
 constexpr int kKqfTop2Groups = 256;  // lm_head workgroups: about one per CU

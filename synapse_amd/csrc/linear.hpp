@@ -37,6 +37,12 @@ struct QLinearInt8 {
   size_t part_elems = 0;
   DevBuf xq, sx;        // activation quantization scratch (forward())
   size_t xq_rows = 0;
+  // gemv()'s one-launch K split: int32 accumulators [16][N64] and per-panel
+  // arrival counters, zero between calls (the panel's last slice reads and
+  // clears them)
+  DevBuf sk_acc, sk_cnt;
+  int sk_panels = 0;
+  syn_status_t ensure_sk();
 
   // host_nk: int8 [n,k] row per output; scales f32[n]
   syn_status_t upload_nk(const int8_t *host_nk, const float *host_scales, size_t n_, size_t k_);
@@ -45,11 +51,12 @@ struct QLinearInt8 {
   // QuantizedLinear::from_f32 (int8_linear.rs:35-70) on host, then upload.
   syn_status_t from_f32(const float *w_nk, size_t n_, size_t k_);
   size_t weight_bytes() const { return n * k + n * 4; }
-  // y[m, n] (row stride ldy) from pre-quantized rows xq (row stride ldx).
+  // y[m, n] (row stride ldy) from pre-quantized rows xq (row stride ldx);
+  // m <= 16 is one launch (a K split adds into sk_acc)
   syn_status_t gemv(size_t m, const int8_t *d_xq, size_t ldx, const float *d_sx, float *d_y,
                     size_t ldy, hipStream_t s);
   // the same with the split-K partials in d_part (part_elems_for(min(m, 16))
-  // int32; unused when that is 0)
+  // int32; unused when that is 0) and a second reduce launch
   syn_status_t gemv_part(size_t m, const int8_t *d_xq, size_t ldx, const float *d_sx,
                          float *d_y, size_t ldy, int *d_part, hipStream_t s);
   size_t part_elems_for(size_t m) const;
@@ -99,6 +106,11 @@ struct QLinearQ4_0 {
   bool has_subnormal_scale = false;  // some block scale is an f16 subnormal (set at upload)
   DevBuf xh;                         // f16 activations for the MFMA GEMM
   size_t xh_elems = 0;
+  // gemv()'s one-launch K split at one row: int64 fixed-point accumulators
+  // [N64] and per-panel arrival counters, zero between calls
+  DevBuf sk_acc, sk_cnt;
+  int sk_panels = 0;
+  syn_status_t ensure_sk();
   syn_status_t upload_packed(const uint8_t *packed, size_t n_, size_t k_);
   syn_status_t from_f32(const float *w_nk, size_t n_, size_t k_);
   // allocate the split-K partials of GEMV batches up to max_m rows (so that
