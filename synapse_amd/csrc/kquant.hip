@@ -27,6 +27,7 @@
 
 #include "kq_unit.hpp"
 #include "kquant.hpp"
+#include "split_k.hpp"
 
 namespace syn {
 
@@ -461,11 +462,15 @@ __global__ void __launch_bounds__(1024)
 
 // ------------------------------------------------------------------ batch-1 GEMV
 // Q4_K / Q6_K at M = 1: one lane per row, the unit decoders of kq_unit.hpp.
+// A K split finishes in the same launch (split_k.hpp) when skacc is set,
+// else writes f32 partials for k_kq_reduce.
 template <int FMT, int NW, int U>
 __global__ void __launch_bounds__(NW * 64)
     k_gemv_kqh(const u32x4 *__restrict__ W, const uint16_t *__restrict__ Wd,
                const float *__restrict__ x, float *__restrict__ y, float *__restrict__ part,
-               int N, int B, int bs) {
+               unsigned long long *__restrict__ skacc, int *__restrict__ skcnt, int N, int B,
+               int bs) {
+  __shared__ int s_last;
   constexpr int NT = NW * 64;
   constexpr int NP = FMT == SYN_HIP_FMT_Q4_K ? 9 : 13;
   constexpr int GRP = FMT == SYN_HIP_FMT_Q4_K ? 32 : 16;  // elements per sub-block sum
@@ -541,6 +546,17 @@ __global__ void __launch_bounds__(NW * 64)
   }
   red[wave * 64 + lane] = acc;
   __syncthreads();
+  if (skacc && gridDim.y > 1) {
+    float v = 0.0f, tot = 0.0f;
+    if (tid < 64) {
+#pragma unroll
+      for (int w = 0; w < NW; w++) v += red[w * 64 + tid];
+    }
+    if (sk_fixed_last(v, skacc + panel * 64, skcnt + panel, gridDim.y, &tot, &s_last) &&
+        tid < 64 && panel * 64 + tid < N)
+      y[panel * 64 + tid] = tot;
+    return;
+  }
   if (tid < 64) {
     float sm = 0.0f;
 #pragma unroll
@@ -594,14 +610,16 @@ static void launch_kq_m(int m, const GemvPlan &p, const void *W, const uint16_t 
 // (more workgroups per CU); shorter Q4_K slices 8 waves of one.
 template <int FMT>
 static syn_status_t launch_kqh(const GemvPlan &p, const u32x4 *W, const uint16_t *Wd,
-                               const float *x, float *y, float *part, int N, size_t shm,
-                               hipStream_t s) {
+                               const float *x, float *y, float *part, const SplitKFixed &sk,
+                               int N, size_t shm, hipStream_t s) {
+  unsigned long long *ska = p.ksplit > 1 ? sk.acc.as<unsigned long long>() : nullptr;
+  int *skc = sk.cnt.as<int>();
   if (FMT == SYN_HIP_FMT_Q6_K || p.cs >= 8)
     hipLaunchKernelGGL((k_gemv_kqh<FMT, 4, 2>), dim3(p.panels, p.ksplit), dim3(256), shm, s, W,
-                       Wd, x, y, part, N, p.chunks, p.cs);
+                       Wd, x, y, part, ska, skc, N, p.chunks, p.cs);
   else
     hipLaunchKernelGGL((k_gemv_kqh<FMT, 8, 1>), dim3(p.panels, p.ksplit), dim3(512), shm, s, W,
-                       Wd, x, y, part, N, p.chunks, p.cs);
+                       Wd, x, y, part, ska, skc, N, p.chunks, p.cs);
   return SYN_OK;
 }
 
@@ -624,12 +642,16 @@ syn_status_t QLinearKQ::gemv(size_t m, const float *d_x, size_t ldx, float *d_y,
     const size_t gpb = fmt == SYN_HIP_FMT_Q4_K ? 8 : 16;
     const size_t shm_h = ((size_t)p.cs * gpb + 16 * 64) * sizeof(float);
     if (mb == 1 && fmt != SYN_HIP_FMT_Q8_0 && shm_h <= 60 * 1024) {
+      // one launch (a K split finishes in place, split_k.hpp)
+      if (p.ksplit > 1) SYN_TRY(sk.ensure(p.panels));
       if (fmt == SYN_HIP_FMT_Q4_K)
-        SYN_TRY(launch_kqh<SYN_HIP_FMT_Q4_K>(p, wq.as<u32x4>(), Wd, xm, ym, part.as<float>(),
+        SYN_TRY(launch_kqh<SYN_HIP_FMT_Q4_K>(p, wq.as<u32x4>(), Wd, xm, ym, part.as<float>(), sk,
                                              (int)n, shm_h, s));
       else
-        SYN_TRY(launch_kqh<SYN_HIP_FMT_Q6_K>(p, wq.as<u32x4>(), Wd, xm, ym, part.as<float>(),
+        SYN_TRY(launch_kqh<SYN_HIP_FMT_Q6_K>(p, wq.as<u32x4>(), Wd, xm, ym, part.as<float>(), sk,
                                              (int)n, shm_h, s));
+      SYN_LAUNCH_CHECK();
+      continue;
     } else if (fmt == SYN_HIP_FMT_Q8_0)
       launch_kq_m<SYN_HIP_FMT_Q8_0>(mb, p, wq.p, Wd, xm, (int)ldx, ym, (int)ldy, part.as<float>(),
                                     (int)n, s);
@@ -657,6 +679,7 @@ syn_status_t QLinearKQ::prepare(size_t max_m) {
   }
   const GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
   if (p.ksplit <= 1) return SYN_OK;
+  SYN_TRY(sk.ensure(p.panels));
   const size_t need = (size_t)p.ksplit * 4 * p.panels * 64;
   if (part_elems >= need) return SYN_OK;
   part_elems = need;

@@ -26,6 +26,7 @@ struct QLinearKQ {
   size_t part_elems = 0;
   DevBuf xh;  // f16 activations for the MFMA GEMM
   size_t xh_elems = 0;
+  SplitKFixed sk;  // gemv()'s one-launch K split at one row (split_k.hpp)
   // Q8_0: every block scale (as the reference converts it) is an f16 value,
   // so the GEMM may multiply in f16 (set at upload)
   bool q8_scales_f16_exact = true;

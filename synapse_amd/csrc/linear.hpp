@@ -5,6 +5,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "split_k.hpp"
 
 namespace syn {
 
@@ -106,11 +107,7 @@ struct QLinearQ4_0 {
   bool has_subnormal_scale = false;  // some block scale is an f16 subnormal (set at upload)
   DevBuf xh;                         // f16 activations for the MFMA GEMM
   size_t xh_elems = 0;
-  // gemv()'s one-launch K split at one row: int64 fixed-point accumulators
-  // [N64] and per-panel arrival counters, zero between calls
-  DevBuf sk_acc, sk_cnt;
-  int sk_panels = 0;
-  syn_status_t ensure_sk();
+  SplitKFixed sk;  // gemv()'s one-launch K split at one row (split_k.hpp)
   syn_status_t upload_packed(const uint8_t *packed, size_t n_, size_t k_);
   syn_status_t from_f32(const float *w_nk, size_t n_, size_t k_);
   // allocate the split-K partials of GEMV batches up to max_m rows (so that

@@ -14,6 +14,7 @@
 #include <vector>
 
 #include "linear.hpp"
+#include "split_k.hpp"
 
 namespace syn {
 
@@ -170,11 +171,8 @@ typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ h2_t as_h2(uint32_t v) { return __builtin_bit_cast(h2_t, v); }
 
 // A K split either writes f32 partials (part, for k_q4_reduce or the
-// consumer's PartRows) or, with skacc set (one launch), adds its dot
-// products as int64 fixed point (kqf_fix) into skacc[N64] with device-scope
-// atomics, waits for them to return, counts its arrival on skcnt[panel], and
-// the panel's last slice reads the totals back by atomic exchange with 0,
-// converts them and writes y (the fixed-point sum is exact in any order).
+// consumer's PartRows) or, with skacc set, finishes in the same launch
+// (split_k.hpp: fixed-point atomics, the panel's last slice writes y).
 template <int U>
 __global__ void __launch_bounds__(512)
     k_gemv_q4_0h(const u32x4 *__restrict__ nib, const uint16_t *__restrict__ sc,
@@ -267,29 +265,15 @@ __global__ void __launch_bounds__(512)
   red[wave * 64 + lane] = acc;
   __syncthreads();
   if (skacc && gridDim.y > 1) {
-    unsigned long long *a = reinterpret_cast<unsigned long long *>(skacc) + panel * 64 + tid;
-    unsigned long long seen = 0;
+    float v = 0.0f, tot = 0.0f;
     if (tid < 64) {
-      float s = 0.0f;
 #pragma unroll
-      for (int w = 0; w < NW; w++) s += red[w * 64 + tid];
-      seen = __hip_atomic_fetch_add(a, (unsigned long long)kqf_fix(s), __ATOMIC_RELAXED,
-                                    __HIP_MEMORY_SCOPE_AGENT);
+      for (int w = 0; w < NW; w++) v += red[w * 64 + tid];
     }
-    asm volatile("" ::"v"(seen));  // the add has returned (performed)
-    __syncthreads();
-    if (tid == 0)
-      s_last = __hip_atomic_fetch_add(skcnt + panel, 1, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.y - 1;
-    __syncthreads();
-    if (!s_last) return;
-    if (tid < 64) {
-      const unsigned long long tot =
-          __hip_atomic_exchange(a, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const int row = panel * 64 + tid;
-      if (row < N) y[row] = kqf_unfix((long long)tot);
-    }
-    if (tid == 0) __hip_atomic_exchange(skcnt + panel, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (sk_fixed_last(v, reinterpret_cast<unsigned long long *>(skacc) + panel * 64,
+                      skcnt + panel, gridDim.y, &tot, &s_last) &&
+        tid < 64 && panel * 64 + tid < N)
+      y[panel * 64 + tid] = tot;
     return;
   }
   if (tid < 64) {
@@ -357,11 +341,11 @@ syn_status_t QLinearQ4_0::gemv(size_t m, const float *d_x, size_t ldx, float *d_
     const size_t shm_h = ((size_t)p.cs + 8 * 64) * 4;
     if (mb == 1 && shm_h <= 60 * 1024) {
       // two blocks per wave and round: measured best at the LLaMA shapes;
-      // one launch (the K split adds into sk_acc)
-      SYN_TRY(ensure_sk());
+      // one launch (a K split finishes in place, split_k.hpp)
+      if (p.ksplit > 1) SYN_TRY(sk.ensure(p.panels));
       hipLaunchKernelGGL(k_gemv_q4_0h<2>, dim3(p.panels, p.ksplit), dim3(512), shm_h, s,
                          nib.as<u32x4>(), sc.as<uint16_t>(), d_x + m0 * ldx, d_y + m0 * ldy,
-                         part.as<float>(), sk_acc.as<long long>(), sk_cnt.as<int>(), (int)n,
+                         part.as<float>(), sk.acc.as<long long>(), sk.cnt.as<int>(), (int)n,
                          p.chunks, p.cs, sub);
       SYN_LAUNCH_CHECK();
       continue;
@@ -401,22 +385,9 @@ syn_status_t QLinearQ4_0::gemv_parts(const float *d_x, float *d_y, PartRows *out
   return SYN_OK;
 }
 
-syn_status_t QLinearQ4_0::ensure_sk() {
-  const GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
-  if (p.ksplit <= 1 || sk_panels >= p.panels) return SYN_OK;
-  SYN_HIP(hipDeviceSynchronize());  // the old buffers may still be in use by queued work
-  sk_panels = p.panels;
-  SYN_TRY(sk_acc.alloc((size_t)p.panels * 64 * sizeof(long long)));
-  SYN_TRY(sk_cnt.alloc((size_t)p.panels * sizeof(int)));
-  SYN_HIP(hipMemset(sk_acc.p, 0, sk_acc.bytes));  // calls leave them cleared
-  SYN_HIP(hipMemset(sk_cnt.p, 0, sk_cnt.bytes));
-  SYN_HIP(hipDeviceSynchronize());  // the memsets run on the null stream, not the caller's
-  return SYN_OK;
-}
-
 syn_status_t QLinearQ4_0::prepare(size_t max_m) {
-  SYN_TRY(ensure_sk());
   const GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
+  if (p.ksplit > 1) SYN_TRY(sk.ensure(p.panels));
   const size_t need = (size_t)p.ksplit * std::min<size_t>(8, max_m) * (size_t)p.panels * 64;
   if (p.ksplit > 1 && part_elems < need) {
     part_elems = need;
