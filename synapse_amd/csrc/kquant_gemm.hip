@@ -901,12 +901,17 @@ static syn_status_t kq_gemm_f16(int fmt, bool exact, const u32x4 *W, const uint1
   const _Float16 *X = xh.as<_Float16>();
   // Enough 256 x 256 tiles for three quarters of the CUs: the four-wave
   // kernel, one K pass per tile.  Fewer: 256 x 128 tiles (twice as many),
-  // split over K when even those cannot fill the GPU.
+  // split over K in at most three parts when even those cover under half
+  // the CUs.  Every split adds its partial tile into Y with f32 atomics, and
+  // that traffic outweighs idle CUs beyond that point (Q8_0, M = 512: 224
+  // tiles 78 us unsplit / 115 us in two; 64 tiles 47 us in three, 66 us in
+  // six).
   const bool big = cdiv(n, PG3N) * cdiv(m, PG3M) >= 192;
   const int tiles_n = (int)cdiv(n, big ? PG3N : PGN), tiles_m = (int)cdiv(m, big ? PG3M : PGM);
   int ksplit = 1;
-  if (!big && tiles_n * tiles_m < 256)  // >= 8 steps per split
-    ksplit = std::max(1, std::min((int)cdiv(384, (size_t)(tiles_n * tiles_m)), steps / 8));
+  if (!big && tiles_n * tiles_m < 128)  // >= 8 steps per split
+    ksplit = std::max(1, std::min(3, std::min((int)cdiv(256, (size_t)(tiles_n * tiles_m)),
+                                              steps / 8)));
   const int per = (int)cdiv((size_t)steps, (size_t)ksplit);
   ksplit = (int)cdiv((size_t)steps, (size_t)per);
   if (ksplit > 1) SYN_TRY(zero_y(d_y, m, n, ldy, s));
