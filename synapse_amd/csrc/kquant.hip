@@ -330,12 +330,16 @@ __device__ __forceinline__ void kq_asums(const float *__restrict__ x, int ldx, i
   }
 }
 
-// grid (panels, ksplit); lane = output row; blocks [b0, b1) of this slice
+// grid (panels, ksplit); lane = output row; blocks [b0, b1) of this slice.
+// A K split finishes in the same launch (split_k.hpp; skacc holds M rows of
+// N64 accumulators, skcnt a counter per panel).
 template <int FMT, int M>
 __global__ void __launch_bounds__(1024)
     k_gemv_kq(const u32x4 *__restrict__ W, const uint16_t *__restrict__ Wd,
               const float *__restrict__ x, int ldx, float *__restrict__ y, int ldy,
-              float *__restrict__ part, int N, int B, int bs) {
+              unsigned long long *__restrict__ skacc, int *__restrict__ skcnt, int N, int B,
+              int bs) {
+  __shared__ int s_last;
   constexpr int NP = FMT == SYN_HIP_FMT_Q8_0 ? 2 : FMT == SYN_HIP_FMT_Q4_K ? 9 : 13;
   constexpr int BE = FMT == SYN_HIP_FMT_Q8_0 ? 32 : 256;
   constexpr int GRP = FMT == SYN_HIP_FMT_Q4_K ? 32 : 16;  // asum group (unused for Q8_0)
@@ -447,27 +451,39 @@ __global__ void __launch_bounds__(1024)
   for (int m = 0; m < M; m++) red[(wave * M + m) * 64 + lane] = acc[m];
   __syncthreads();
   const int N64 = gridDim.x * 64;
+  if (gridDim.y > 1) {
+    unsigned long long seen = 0;
+    for (int t = threadIdx.x; t < M * 64; t += blockDim.x) {
+      const int m = t >> 6, r = t & 63;
+      float s = 0.0f;
+      for (int w = 0; w < nw; w++) s += red[(w * M + m) * 64 + r];
+      seen |= sk_add(skacc + (size_t)m * N64 + panel * 64 + r, s);
+    }
+    if (!sk_arrive(seen, skcnt + panel, gridDim.y, &s_last)) return;
+    for (int t = threadIdx.x; t < M * 64; t += blockDim.x) {
+      const int m = t >> 6, r = t & 63, row = panel * 64 + r;
+      const float v = sk_take(skacc + (size_t)m * N64 + row);
+      if (row < N) y[(size_t)m * ldy + row] = v;
+    }
+    sk_reset(skcnt + panel);
+    return;
+  }
   for (int t = threadIdx.x; t < M * 64; t += blockDim.x) {
     const int m = t >> 6, r = t & 63;
     float s = 0.0f;
     for (int w = 0; w < nw; w++) s += red[(w * M + m) * 64 + r];
     const int row = panel * 64 + r;
-    if (gridDim.y == 1) {
-      if (row < N) y[(size_t)m * ldy + row] = s;
-    } else {
-      part[((size_t)ks * M + m) * N64 + row] = s;
-    }
+    if (row < N) y[(size_t)m * ldy + row] = s;
   }
 }
 
 // ------------------------------------------------------------------ batch-1 GEMV
 // Q4_K / Q6_K at M = 1: one lane per row, the unit decoders of kq_unit.hpp.
-// A K split finishes in the same launch (split_k.hpp) when skacc is set,
-// else writes f32 partials for k_kq_reduce.
+// A K split finishes in the same launch (split_k.hpp).
 template <int FMT, int NW, int U>
 __global__ void __launch_bounds__(NW * 64)
     k_gemv_kqh(const u32x4 *__restrict__ W, const uint16_t *__restrict__ Wd,
-               const float *__restrict__ x, float *__restrict__ y, float *__restrict__ part,
+               const float *__restrict__ x, float *__restrict__ y,
                unsigned long long *__restrict__ skacc, int *__restrict__ skcnt, int N, int B,
                int bs) {
   __shared__ int s_last;
@@ -546,7 +562,7 @@ __global__ void __launch_bounds__(NW * 64)
   }
   red[wave * 64 + lane] = acc;
   __syncthreads();
-  if (skacc && gridDim.y > 1) {
+  if (gridDim.y > 1) {
     float v = 0.0f, tot = 0.0f;
     if (tid < 64) {
 #pragma unroll
@@ -562,46 +578,32 @@ __global__ void __launch_bounds__(NW * 64)
 #pragma unroll
     for (int w = 0; w < NW; w++) sm += red[w * 64 + tid];
     const int row = panel * 64 + tid;
-    if (gridDim.y == 1) {
-      if (row < N) y[row] = sm;
-    } else {
-      part[(size_t)ks * gridDim.x * 64 + row] = sm;
-    }
+    if (row < N) y[row] = sm;
   }
-}
-
-__global__ void __launch_bounds__(256)
-    k_kq_reduce(const float *__restrict__ part, int ksplit, int M, int N, int N64,
-                float *__restrict__ y, int ldy) {
-  const int idx = blockIdx.x * 256 + threadIdx.x;
-  if (idx >= M * N) return;
-  const int m = idx / N, row = idx - m * N;
-  float s = 0.0f;
-  for (int k = 0; k < ksplit; k++) s += part[((size_t)k * M + m) * N64 + row];
-  y[(size_t)m * ldy + row] = s;
 }
 
 template <int FMT, int M>
 static void launch_kq(const GemvPlan &p, const void *W, const uint16_t *Wd, const float *x,
-                      int ldx, float *y, int ldy, float *part, int N, hipStream_t s) {
+                      int ldx, float *y, int ldy, const SplitKFixed &sk, int N, hipStream_t s) {
   constexpr int BE = FMT == SYN_HIP_FMT_Q8_0 ? 32 : 256;
   constexpr int GRP = FMT == SYN_HIP_FMT_Q4_K ? 32 : 16;
   const int waves = std::min(p.waves, M >= 4 ? 8 : 16);
   const size_t as = FMT == SYN_HIP_FMT_Q8_0 ? 0 : (size_t)M * p.cs * (BE / GRP);
   const size_t shm = (as + (size_t)waves * M * 64) * sizeof(float);
   hipLaunchKernelGGL((k_gemv_kq<FMT, M>), dim3(p.panels, p.ksplit), dim3(64 * waves), shm, s,
-                     (const u32x4 *)W, Wd, x, ldx, y, ldy, part, N, p.chunks, p.cs);
+                     (const u32x4 *)W, Wd, x, ldx, y, ldy, sk.acc.as<unsigned long long>(),
+                     sk.cnt.as<int>(), N, p.chunks, p.cs);
 }
 
 template <int FMT>
 static void launch_kq_m(int m, const GemvPlan &p, const void *W, const uint16_t *Wd,
-                        const float *x, int ldx, float *y, int ldy, float *part, int N,
+                        const float *x, int ldx, float *y, int ldy, const SplitKFixed &sk, int N,
                         hipStream_t s) {
   switch (m) {
-    case 1: launch_kq<FMT, 1>(p, W, Wd, x, ldx, y, ldy, part, N, s); break;
-    case 2: launch_kq<FMT, 2>(p, W, Wd, x, ldx, y, ldy, part, N, s); break;
-    case 3: launch_kq<FMT, 3>(p, W, Wd, x, ldx, y, ldy, part, N, s); break;
-    default: launch_kq<FMT, 4>(p, W, Wd, x, ldx, y, ldy, part, N, s); break;
+    case 1: launch_kq<FMT, 1>(p, W, Wd, x, ldx, y, ldy, sk, N, s); break;
+    case 2: launch_kq<FMT, 2>(p, W, Wd, x, ldx, y, ldy, sk, N, s); break;
+    case 3: launch_kq<FMT, 3>(p, W, Wd, x, ldx, y, ldy, sk, N, s); break;
+    default: launch_kq<FMT, 4>(p, W, Wd, x, ldx, y, ldy, sk, N, s); break;
   }
 }
 
@@ -610,16 +612,16 @@ static void launch_kq_m(int m, const GemvPlan &p, const void *W, const uint16_t 
 // (more workgroups per CU); shorter Q4_K slices 8 waves of one.
 template <int FMT>
 static syn_status_t launch_kqh(const GemvPlan &p, const u32x4 *W, const uint16_t *Wd,
-                               const float *x, float *y, float *part, const SplitKFixed &sk,
-                               int N, size_t shm, hipStream_t s) {
-  unsigned long long *ska = p.ksplit > 1 ? sk.acc.as<unsigned long long>() : nullptr;
+                               const float *x, float *y, const SplitKFixed &sk, int N, size_t shm,
+                               hipStream_t s) {
+  unsigned long long *ska = sk.acc.as<unsigned long long>();
   int *skc = sk.cnt.as<int>();
   if (FMT == SYN_HIP_FMT_Q6_K || p.cs >= 8)
     hipLaunchKernelGGL((k_gemv_kqh<FMT, 4, 2>), dim3(p.panels, p.ksplit), dim3(256), shm, s, W,
-                       Wd, x, y, part, ska, skc, N, p.chunks, p.cs);
+                       Wd, x, y, ska, skc, N, p.chunks, p.cs);
   else
     hipLaunchKernelGGL((k_gemv_kqh<FMT, 8, 1>), dim3(p.panels, p.ksplit), dim3(512), shm, s, W,
-                       Wd, x, y, part, ska, skc, N, p.chunks, p.cs);
+                       Wd, x, y, ska, skc, N, p.chunks, p.cs);
   return SYN_OK;
 }
 
@@ -628,46 +630,28 @@ syn_status_t QLinearKQ::gemv(size_t m, const float *d_x, size_t ldx, float *d_y,
   if (m == 0 || n == 0 || k == 0) return SYN_OK;
   if (m > 8) return gemm(m, d_x, ldx, d_y, ldy, s);
   const GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
-  const size_t N64 = (size_t)p.panels * 64;
+  // one launch per block of rows: a K split finishes in place (split_k.hpp)
+  if (p.ksplit > 1) SYN_TRY(sk.ensure(p.panels, 4));
+  const uint16_t *Wd = wd.as<uint16_t>();
   for (size_t m0 = 0; m0 < m; m0 += 4) {
     const int mb = (int)std::min<size_t>(4, m - m0);
-    if (p.ksplit > 1 && part_elems < (size_t)p.ksplit * mb * N64) {
-      SYN_HIP(hipDeviceSynchronize());
-      part_elems = (size_t)p.ksplit * 4 * N64;
-      SYN_TRY(part.alloc(part_elems * sizeof(float)));
-    }
     const float *xm = d_x + m0 * ldx;
     float *ym = d_y + m0 * ldy;
-    const uint16_t *Wd = wd.as<uint16_t>();
     const size_t gpb = fmt == SYN_HIP_FMT_Q4_K ? 8 : 16;
     const size_t shm_h = ((size_t)p.cs * gpb + 16 * 64) * sizeof(float);
     if (mb == 1 && fmt != SYN_HIP_FMT_Q8_0 && shm_h <= 60 * 1024) {
-      // one launch (a K split finishes in place, split_k.hpp)
-      if (p.ksplit > 1) SYN_TRY(sk.ensure(p.panels));
       if (fmt == SYN_HIP_FMT_Q4_K)
-        SYN_TRY(launch_kqh<SYN_HIP_FMT_Q4_K>(p, wq.as<u32x4>(), Wd, xm, ym, part.as<float>(), sk,
-                                             (int)n, shm_h, s));
+        SYN_TRY(launch_kqh<SYN_HIP_FMT_Q4_K>(p, wq.as<u32x4>(), Wd, xm, ym, sk, (int)n, shm_h, s));
       else
-        SYN_TRY(launch_kqh<SYN_HIP_FMT_Q6_K>(p, wq.as<u32x4>(), Wd, xm, ym, part.as<float>(), sk,
-                                             (int)n, shm_h, s));
-      SYN_LAUNCH_CHECK();
-      continue;
-    } else if (fmt == SYN_HIP_FMT_Q8_0)
-      launch_kq_m<SYN_HIP_FMT_Q8_0>(mb, p, wq.p, Wd, xm, (int)ldx, ym, (int)ldy, part.as<float>(),
-                                    (int)n, s);
-    else if (fmt == SYN_HIP_FMT_Q4_K)
-      launch_kq_m<SYN_HIP_FMT_Q4_K>(mb, p, wq.p, Wd, xm, (int)ldx, ym, (int)ldy, part.as<float>(),
-                                    (int)n, s);
-    else
-      launch_kq_m<SYN_HIP_FMT_Q6_K>(mb, p, wq.p, Wd, xm, (int)ldx, ym, (int)ldy, part.as<float>(),
-                                    (int)n, s);
-    SYN_LAUNCH_CHECK();
-    if (p.ksplit > 1) {
-      const int total = mb * (int)n;
-      hipLaunchKernelGGL(k_kq_reduce, dim3(cdiv(total, 256)), dim3(256), 0, s, part.as<float>(),
-                         p.ksplit, mb, (int)n, (int)N64, ym, (int)ldy);
-      SYN_LAUNCH_CHECK();
+        SYN_TRY(launch_kqh<SYN_HIP_FMT_Q6_K>(p, wq.as<u32x4>(), Wd, xm, ym, sk, (int)n, shm_h, s));
+    } else if (fmt == SYN_HIP_FMT_Q8_0) {
+      launch_kq_m<SYN_HIP_FMT_Q8_0>(mb, p, wq.p, Wd, xm, (int)ldx, ym, (int)ldy, sk, (int)n, s);
+    } else if (fmt == SYN_HIP_FMT_Q4_K) {
+      launch_kq_m<SYN_HIP_FMT_Q4_K>(mb, p, wq.p, Wd, xm, (int)ldx, ym, (int)ldy, sk, (int)n, s);
+    } else {
+      launch_kq_m<SYN_HIP_FMT_Q6_K>(mb, p, wq.p, Wd, xm, (int)ldx, ym, (int)ldy, sk, (int)n, s);
     }
+    SYN_LAUNCH_CHECK();
   }
   return SYN_OK;
 }
@@ -678,12 +662,7 @@ syn_status_t QLinearKQ::prepare(size_t max_m) {
     xh_elems = max_m * k;
   }
   const GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
-  if (p.ksplit <= 1) return SYN_OK;
-  SYN_TRY(sk.ensure(p.panels));
-  const size_t need = (size_t)p.ksplit * 4 * p.panels * 64;
-  if (part_elems >= need) return SYN_OK;
-  part_elems = need;
-  return part.alloc(need * sizeof(float));
+  return p.ksplit > 1 ? sk.ensure(p.panels, 4) : SYN_OK;
 }
 
 }  // namespace syn

@@ -22,8 +22,6 @@ struct QLinearKQ {
   int planes = 0;  // 16-byte planes per block
   DevBuf wq;       // [P][blocks][planes][64][16]
   DevBuf wd;       // [P][blocks][64] f16 d (Q8_0, Q6_K)
-  DevBuf part;
-  size_t part_elems = 0;
   DevBuf xh;  // f16 activations for the MFMA GEMM
   size_t xh_elems = 0;
   SplitKFixed sk;  // gemv()'s one-launch K split at one row (split_k.hpp)

@@ -56,12 +56,16 @@ __device__ __forceinline__ float q4_scale(uint32_t h, float sub) {
 // so that the block sums only wait for the activations and the weights'
 // HBM latency overlaps them.  The dot products read the activations with
 // wave-uniform addresses (scalar loads).
+// A K split finishes in the same launch (split_k.hpp; skacc holds M rows
+// of N64 accumulators, skcnt a counter per panel).
 template <int M, int U>
 __global__ void __launch_bounds__(1024)
     k_gemv_q4_0(const u32x4 *__restrict__ nib, const uint16_t *__restrict__ sc,
                 const float *__restrict__ x, int ldx, float *__restrict__ y, int ldy,
-                float *__restrict__ part, int N, int B, int bs, float sub) {
+                unsigned long long *__restrict__ skacc, int *__restrict__ skcnt, int N, int B,
+                int bs, float sub) {
   extern __shared__ __align__(16) float smem[];
+  __shared__ int s_last;
   const int NT = blockDim.x;
   const int panel = blockIdx.x, ks = blockIdx.y;
   const int nw = NT >> 6;
@@ -144,16 +148,29 @@ __global__ void __launch_bounds__(1024)
   for (int m = 0; m < M; m++) red[(wave * M + m) * 64 + lane] = acc[m];
   __syncthreads();
   const int N64 = gridDim.x * 64;
+  if (gridDim.y > 1) {
+    unsigned long long seen = 0;
+    for (int t = tid; t < M * 64; t += NT) {
+      const int m = t >> 6, r = t & 63;
+      float s = 0.0f;
+      for (int w = 0; w < nw; w++) s += red[(w * M + m) * 64 + r];
+      seen |= sk_add(skacc + (size_t)m * N64 + panel * 64 + r, s);
+    }
+    if (!sk_arrive(seen, skcnt + panel, gridDim.y, &s_last)) return;
+    for (int t = tid; t < M * 64; t += NT) {
+      const int m = t >> 6, r = t & 63, row = panel * 64 + r;
+      const float v = sk_take(skacc + (size_t)m * N64 + row);
+      if (row < N) y[(size_t)m * ldy + row] = v;
+    }
+    sk_reset(skcnt + panel);
+    return;
+  }
   for (int t = tid; t < M * 64; t += NT) {
     const int m = t >> 6, r = t & 63;
     float s = 0.0f;
     for (int w = 0; w < nw; w++) s += red[(w * M + m) * 64 + r];
     const int row = panel * 64 + r;
-    if (gridDim.y == 1) {
-      if (row < N) y[(size_t)m * ldy + row] = s;
-    } else {
-      part[((size_t)ks * M + m) * N64 + row] = s;
-    }
+    if (row < N) y[(size_t)m * ldy + row] = s;
   }
 }
 
@@ -289,36 +306,27 @@ __global__ void __launch_bounds__(512)
   }
 }
 
-__global__ void __launch_bounds__(256)
-    k_q4_reduce(const float *__restrict__ part, int ksplit, int M, int N, int N64,
-                float *__restrict__ y, int ldy) {
-  const int idx = blockIdx.x * 256 + threadIdx.x;
-  if (idx >= M * N) return;
-  const int m = idx / N, row = idx - m * N;
-  float s = 0.0f;
-  for (int k = 0; k < ksplit; k++) s += part[((size_t)k * M + m) * N64 + row];
-  y[(size_t)m * ldy + row] = s;
-}
-
 // U blocks in flight per wave: 8 with 8 waves when a slice has >= 64
 // blocks (four workgroups per CU stream the matrix), else 4 with up to 16
 template <int M>
 static void launch_q4_m(const GemvPlan &p, const u32x4 *nib, const uint16_t *sc, const float *x,
-                        int ldx, float *y, int ldy, float *part, int N, float sub,
+                        int ldx, float *y, int ldy, const SplitKFixed &sk, int N, float sub,
                         hipStream_t s) {
   const bool wide = p.cs >= 64;
   const int waves = wide ? 8 : std::min(p.waves, M >= 8 ? 8 : 16);
   const size_t shm = ((size_t)M * p.cs + (size_t)waves * M * 64) * sizeof(float);
+  unsigned long long *ska = sk.acc.as<unsigned long long>();
+  int *skc = sk.cnt.as<int>();
   if (wide)
     hipLaunchKernelGGL((k_gemv_q4_0<M, 8>), dim3(p.panels, p.ksplit), dim3(64 * waves), shm, s,
-                       nib, sc, x, ldx, y, ldy, part, N, p.chunks, p.cs, sub);
+                       nib, sc, x, ldx, y, ldy, ska, skc, N, p.chunks, p.cs, sub);
   else
     hipLaunchKernelGGL((k_gemv_q4_0<M, 4>), dim3(p.panels, p.ksplit), dim3(64 * waves), shm, s,
-                       nib, sc, x, ldx, y, ldy, part, N, p.chunks, p.cs, sub);
+                       nib, sc, x, ldx, y, ldy, ska, skc, N, p.chunks, p.cs, sub);
 }
 
 typedef void (*q4_launcher)(const GemvPlan &, const u32x4 *, const uint16_t *, const float *,
-                            int, float *, int, float *, int, float, hipStream_t);
+                            int, float *, int, const SplitKFixed &, int, float, hipStream_t);
 static const q4_launcher kQ4Launch[9] = {nullptr,        launch_q4_m<1>, launch_q4_m<2>,
                                          launch_q4_m<3>, launch_q4_m<4>, launch_q4_m<5>,
                                          launch_q4_m<6>, launch_q4_m<7>, launch_q4_m<8>};
@@ -328,38 +336,24 @@ syn_status_t QLinearQ4_0::gemv(size_t m, const float *d_x, size_t ldx, float *d_
   if (m == 0 || n == 0 || k == 0) return SYN_OK;
   if (m > 16 && gemm_ok() && ldx % 4 == 0) return gemm(m, d_x, ldx, d_y, ldy, s);
   const float sub = rs_f16_scales ? 0.5f : 1.0f;
-  // "chunks" here are 32-element blocks; a K slice holds whole blocks
-  GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
-  const size_t N64 = (size_t)p.panels * 64;
+  // "chunks" here are 32-element blocks; a K slice holds whole blocks.  One
+  // launch per block of up to 8 rows: a K split finishes in place (split_k.hpp)
+  const GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
+  if (p.ksplit > 1) SYN_TRY(sk.ensure(p.panels, 8));
   for (size_t m0 = 0; m0 < m; m0 += 8) {
     const int mb = (int)std::min<size_t>(8, m - m0);
-    if (p.ksplit > 1 && part_elems < (size_t)p.ksplit * mb * N64) {
-      part_elems = (size_t)p.ksplit * mb * N64;
-      SYN_HIP(hipDeviceSynchronize());
-      SYN_TRY(part.alloc(part_elems * sizeof(float)));
-    }
     const size_t shm_h = ((size_t)p.cs + 8 * 64) * 4;
     if (mb == 1 && shm_h <= 60 * 1024) {
-      // two blocks per wave and round: measured best at the LLaMA shapes;
-      // one launch (a K split finishes in place, split_k.hpp)
-      if (p.ksplit > 1) SYN_TRY(sk.ensure(p.panels));
+      // two blocks per wave and round: measured best at the LLaMA shapes
       hipLaunchKernelGGL(k_gemv_q4_0h<2>, dim3(p.panels, p.ksplit), dim3(512), shm_h, s,
                          nib.as<u32x4>(), sc.as<uint16_t>(), d_x + m0 * ldx, d_y + m0 * ldy,
-                         part.as<float>(), sk.acc.as<long long>(), sk.cnt.as<int>(), (int)n,
-                         p.chunks, p.cs, sub);
-      SYN_LAUNCH_CHECK();
-      continue;
+                         nullptr, sk.acc.as<long long>(), sk.cnt.as<int>(), (int)n, p.chunks,
+                         p.cs, sub);
     } else {
       kQ4Launch[mb](p, nib.as<u32x4>(), sc.as<uint16_t>(), d_x + m0 * ldx, (int)ldx,
-                    d_y + m0 * ldy, (int)ldy, part.as<float>(), (int)n, sub, s);
+                    d_y + m0 * ldy, (int)ldy, sk, (int)n, sub, s);
     }
     SYN_LAUNCH_CHECK();
-    if (p.ksplit > 1) {
-      const int total = mb * (int)n;
-      hipLaunchKernelGGL(k_q4_reduce, dim3(cdiv(total, 256)), dim3(256), 0, s, part.as<float>(),
-                         p.ksplit, mb, (int)n, (int)N64, d_y + m0 * ldy, (int)ldy);
-      SYN_LAUNCH_CHECK();
-    }
   }
   return SYN_OK;
 }
@@ -387,7 +381,7 @@ syn_status_t QLinearQ4_0::gemv_parts(const float *d_x, float *d_y, PartRows *out
 
 syn_status_t QLinearQ4_0::prepare(size_t max_m) {
   const GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
-  if (p.ksplit > 1) SYN_TRY(sk.ensure(p.panels));
+  if (p.ksplit > 1) SYN_TRY(sk.ensure(p.panels, 8));
   const size_t need = (size_t)p.ksplit * std::min<size_t>(8, max_m) * (size_t)p.panels * 64;
   if (p.ksplit > 1 && part_elems < need) {
     part_elems = need;
