@@ -137,3 +137,21 @@ def test_int8_prefill_attention_hd128_bit_exact(hd128, t):
     extra = O.token_ids(20, SEED + 0xFFFF + 1000 + t, HD128["vocab"])
     np.testing.assert_array_equal(_bits(g.prefill_append(extra)), _bits(o.prefill_append(extra)))
     np.testing.assert_array_equal(_bits(g.forward_one(7)), _bits(o.forward_one(7)))
+
+
+def test_int8_long_prefill_one_query_kernel_bit_exact():
+    """A 900-token prompt at head_dim 128 is past the row-block kernel's LDS
+    rows (about 824 tokens): the one-query-per-workgroup prefill attention,
+    then appended rows and a decode step past position 900."""
+    cfg = dict(HD128, n_layers=1, max_seq=960)
+    o = O.QuantizedCausalLM(cfg)
+    o.init_synthetic(SEED, 0.15)
+    g = hip.QuantizedCausalLM(cfg)
+    g.init_synthetic(SEED, 0.15)
+    ids = O.token_ids(900, SEED + 0xFFFF + 900, cfg["vocab"])
+    np.testing.assert_array_equal(_bits(g.prefill(ids)), _bits(o.prefill(ids)))
+    extra = O.token_ids(20, SEED + 0xFFFF + 1900, cfg["vocab"])
+    np.testing.assert_array_equal(_bits(g.prefill_append(extra)), _bits(o.prefill_append(extra)))
+    np.testing.assert_array_equal(_bits(g.forward_one(7)), _bits(o.forward_one(7)))
+    o.close()
+    g.close()
