@@ -33,8 +33,8 @@
 namespace syn {
 
 // Output row `row` of a Q4_0 GEMV from its split-K partials (PartRows):
-// summed from 0.0f in slice order, the reduce kernel's order, so a consumer
-// that reads the partials sees the values the reduce launch would write.
+// summed from 0.0f in slice order (deterministic: every consumer of a row
+// sees the same value).
 __device__ __forceinline__ float part_row(const PartRows &r, int row) {
   if (r.ks == 1) return r.p[row];
   float s = 0.0f;
@@ -365,7 +365,7 @@ struct syn_hip_hlm_s {
     if (use_fused && fused_ok) return decode_step_fused(s);
     const float eps = c.eps;
     // each Q4 GEMV leaves its split-K partials to the kernel that reads its
-    // output (PartRows): no reduce launches
+    // output (PartRows): no second launch per GEMV
     PartRows pin, pout, pgu, pdown;
     SYN_TRY(launch_embed(embed.as<float>(), &st()->token, 1, (int)H, (int)V, x.as<float>(), s));
     for (size_t l = 0; l < L; l++) {

@@ -83,7 +83,7 @@ void host_quantize_weights_nk(const float *w, const float *scales, size_t n, siz
 
 // The split-K partials of one GEMV output row set, left for the kernel that
 // consumes the output: row r = sum over k < ks of p[k * stride + r], summed
-// from 0.0f in k order (the order of the reduce kernel); ks = 1 is the output
+// from 0.0f in k order; ks = 1 is the output
 // itself (stride unused).
 struct PartRows {
   const float *p = nullptr;
@@ -117,9 +117,9 @@ struct QLinearQ4_0 {
   // y[m,n] = x[m,k] W^T, f32 activations; m > 16 runs gemm() when gemm_ok()
   syn_status_t gemv(size_t m, const float *d_x, size_t ldx, float *d_y, size_t ldy,
                     hipStream_t s);
-  // one activation row without the reduce launch: the GEMV kernel writes its
-  // split-K partials (prepare(1) must have run) and *out names them; with a
-  // single K slice it writes y[n] and *out names y
+  // one activation row, its K split left to the consumer: the GEMV kernel
+  // writes its split-K partials (prepare(1) must have run) and *out names
+  // them; with a single K slice it writes y[n] and *out names y
   syn_status_t gemv_parts(const float *d_x, float *d_y, PartRows *out, hipStream_t s);
   // f16 MFMA prefill GEMM (kquant_gemm.hip): weights (nibble - 8) * d and
   // activations rounded once to f16, f32 accumulation
