@@ -117,6 +117,21 @@ def test_qlinear_from_f32_forward(m, k, n):
     np.testing.assert_array_equal(_bits(got), _bits(O.qgemm_int8(xq, q_kn, sx, s)))
 
 
+@pytest.mark.parametrize("m", [1, 5])
+def test_int8_split_k_slices_on_every_xcd_twice(m):
+    """Three 64-row panels over K = 16384: the slices of a panel run on all
+    eight XCDs, so the one-launch K split's int32 atomics, arrival counter
+    and read-back cross XCDs; bit-exact on two calls in a row."""
+    n, k = 192, 16384
+    w = O.normal(n * k, 3, 0.02).reshape(n, k)
+    lin = hip.QLinear.from_f32(hip.FMT_INT8, w)
+    q_kn, s = O.quantize_weights_int8(w)
+    for call in range(2):
+        x = O.normal(m * k, 50 + call, 1.0).reshape(m, k)
+        xq, sx = O.quantize_per_channel_int8(x)
+        np.testing.assert_array_equal(_bits(lin.forward(x)), _bits(O.qgemm_int8(xq, q_kn, sx, s)))
+
+
 def test_lm_head_shape_bit_exact():
     # Qwen3 tied lm_head: 151936 x 1024
     n, k = 151936, 1024

@@ -56,6 +56,25 @@ def test_kquant_gemv_vs_reference(name, k, n, m):
         assert _rel(got[i], want[i]) <= TOL * 0.1, (i, _rel(got[i], want[i]))
 
 
+@pytest.mark.parametrize("name,m", [("q4_k", 1), ("q6_k", 1), ("q8_0", 3), ("q4_k", 4)])
+def test_split_k_slices_on_every_xcd_twice(name, m):
+    """Three 64-row panels over a long K: the slices of a panel land on all
+    eight XCDs (workgroup id x + 3y), so the one-launch K split's atomics,
+    arrival counter and read-back cross XCDs; a second call checks that the
+    accumulators and counters were left cleared."""
+    n, k = 192, 16384
+    w = O.normal(n * k, 5, 0.02).reshape(n, k)
+    blocks = hip.kquant_encode(FMTS[name], w)
+    lin = hip.QLinear.gguf(FMTS[name], blocks, n, k)
+    deq = O.dequant(name, blocks, n * k).reshape(n, k)
+    for call in range(2):
+        x = O.normal(m * k, 17 + call, 1.0).reshape(m, k)
+        got = lin.forward(x)
+        want = O.matmul_t(x, deq)
+        for i in range(m):
+            assert _rel(got[i], want[i]) <= TOL * 0.1, (call, i, _rel(got[i], want[i]))
+
+
 def test_q6_k_lm_head_shape():
     # LLaMA-3.2-3B lm_head: 128256 x 3072 Q6_K, random blocks
     n, k = 128256, 3072

@@ -62,6 +62,22 @@ def test_q4_handle_multi_row():
         assert _rel(got[i], O.q4_0_gemv(x[i], packed, n)) <= TOL * 1e-2
 
 
+@pytest.mark.parametrize("m", [1, 3])
+def test_q4_split_k_slices_on_every_xcd_twice(m):
+    """Three 64-row panels over a long K: the slices of a panel run on all
+    eight XCDs (workgroup id x + 3y), so the one-launch K split's atomics,
+    arrival counter and read-back cross XCDs; the second call checks the
+    accumulators and counters were left cleared."""
+    n, k = 192, 16384
+    packed = _random_packed(n, k, 99)
+    lin = hip.QLinear.q4_0(packed, n, k)
+    for call in range(2):
+        x = O.normal(m * k, 40 + call, 1.0).reshape(m, k)
+        got = lin.forward(x)
+        for i in range(m):
+            assert _rel(got[i], O.q4_0_gemv(x[i], packed, n)) <= TOL * 1e-2, (call, i)
+
+
 def test_q4_errors():
     L = hip.lib()
     a = np.zeros(40, np.float32)
