@@ -1,17 +1,26 @@
 // Hybrid LFM2.5 decoder on the device, Q4 decode path: HybridModel::decode_one
 // (models/ssm/hybrid/model.rs:240-290) over LIV conv and GQA decoder layers
 // (layer.rs:593-654, 878-954, 1055-1078) after quantize_for_decode
-// (layer.rs:570-581, 832-846): every projection is a Q4_0 GEMV (the
-// q4_0GemvRow kernel of q4_0.hip, f32 activations), q|k|v and gate|up
-// stacked into one handle each (their rows are independent), the lm_head the
-// tied f32 embedding in f32GemvRow order (the exact-order GEMV of mamba.hip).
-// The small ops follow the reference's float order except RMSNorm's sum of
-// squares (pure_rust_ops.rs:96-112's formula, tree-ordered sum): the double-gated conv
-// step (B*x, shift, sequential tap sum, C*y), head norms with x * (w * s),
-// rotate-half RoPE, attention with sequential dot products, softmax_slice
-// and a sequential P.V, SwiGLU silu(g) * u with glibc's expf.  The Q4 GEMV
-// is held to the float tolerance (its sums run in another order), so the
-// decoder is compared with the oracle by tolerance.
+// (layer.rs:570-581, 832-846): every projection is Q4_0 (f32 activations),
+// q|k|v and gate|up stacked into one handle each (their rows are
+// independent), the lm_head the tied f32 embedding.  Two forms of the step,
+// both compared with the oracle by tolerance:
+//
+// - fused (the default when the shapes fit): four kernels per LIV conv layer
+//   and five per GQA layer on the fused split-K GEMV of klm_fused.hip (the
+//   Q4_0 planes as a fourth format; RMSNorm, the LIV conv step and the
+//   attention chunk combine in GEMV prologues, SwiGLU in an epilogue,
+//   fixed-point split-K atomics), the chunked attention of klm_fused.hip,
+//   and head_f32.hip's tree-ordered f32 lm_head with per-panel top-2;
+// - op-by-op: one kernel per op with the q4_0GemvRow GEMV of q4_0.hip, whose
+//   split-K partials the consuming kernels sum (PartRows), the small ops in
+//   the reference's float order except RMSNorm's sum of squares
+//   (pure_rust_ops.rs:96-112's formula, tree-ordered sum): the double-gated
+//   conv step (B*x, shift, sequential tap sum, C*y), head norms with
+//   x * (w * s), rotate-half RoPE, attention with sequential dot products,
+//   softmax_slice and a sequential P.V, SwiGLU silu(g) * u with glibc's
+//   expf, and the lm_head in f32GemvRow order (the exact-order GEMV of
+//   mamba.hip).
 //
 // The reference prefills on the CPU with f32 weights and then decodes on the
 // GPU (examples/lfm25_inference.rs:86-99); this decoder feeds a prompt
