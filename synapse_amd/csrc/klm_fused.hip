@@ -224,6 +224,38 @@ __device__ __forceinline__ void kqf_unit(u32x4 *pl, const uint16_t *dh, const fl
   }
 }
 
+// Half a Q4_0 unit (four 32-element blocks, stages 4h..4h+3 of the unit) for
+// workgroups that give each unit two waves: pl / dh hold the half's four
+// planes and scales, xs / as its 128 activations and four block sums.
+template <bool DB>
+__device__ __forceinline__ void kqf_q40_half(u32x4 *pl, const uint16_t *dh, const float *xs,
+                                             const float *as, float &acc) {
+  asm volatile("" ::: "memory");  // no LDS read of the half moves above its branch
+  float xb[DB ? 2 : 1][32];
+  float av[4], dq[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) av[i] = as[i];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {  // IEEE f16 scales, converted after the prologue
+    uint32_t h = dh[j];
+    asm volatile("" : "+v"(h));
+    dq[j] = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
+  }
+  if constexpr (DB) lds_x32(xb[0], xs);
+#pragma unroll
+  for (int t = 0; t < 4; t++) {
+    if constexpr (DB) {
+      if (t + 1 < 4) lds_x32(xb[(t + 1) & 1], xs + (t + 1) * 32);
+    } else {
+      lds_x32(xb[0], xs + t * 32);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    pin_plane(pl[t]);
+    kq40_block(pl[t], dq[t], xb[DB ? (t & 1) : 0], av[t], acc);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // ------------------------------------------------------------------ GEMV
 // grid (row groups, K splits), NW waves (NW >= bs).  Row group = a 64-row
 // panel (lane = row), or for OUT_GU 32 gate rows j.. and the 32 up rows
@@ -233,10 +265,11 @@ __device__ __forceinline__ void kqf_unit(u32x4 *pl, const uint16_t *dh, const fl
 // group (32 elements for Q4_K, 16 for Q6_K) is summed across 8 or 4 lanes.
 // dynamic LDS: activation slice [bs*256] | group sums [bs*256/GRP] |
 // (ATTN) chunk logits and weights [2][heads of the slice][nch], 1/den [heads]
-template <int FMT, int PRO, int OUT, int NW>
+template <int FMT, int PRO, int OUT, int NW, bool HALF>
 __global__ void __launch_bounds__(NW * 64)
     k_kqf_gemv(const u32x4 *__restrict__ W, const uint16_t *__restrict__ Wd, int B, int N,
                int bs, KqfIn in, KqfOut out) {
+  static_assert(!HALF || FMT == SYN_HIP_FMT_Q4_0, "half units are Q4_0 only");
   using F = KqfFmt<FMT>;
   constexpr int kNT = NW * 64;
   constexpr int GPU = F::GRP ? 256 / F::GRP : 0;
@@ -268,19 +301,35 @@ __global__ void __launch_bounds__(NW * 64)
   // the prologue runs under the weights' HBM latency; the K-quant formats
   // (up to 16 planes) after the prologue
   constexpr bool kEarlyW = FMT == SYN_HIP_FMT_Q4_0;
-  const bool has_unit = wave < nu_wg;
+  // HALF: two waves per unit, wave w taking half w & 1 of unit w >> 1
+  const int uw = HALF ? wave >> 1 : wave, uh = HALF ? wave & 1 : 0;
+  const bool has_unit = uw < nu_wg;
   u32x4 buf[F::NPU];
   uint16_t dbuf[F::DPU > 0 ? F::DPU : 1];
   auto issue_unit = [&]() {
     if (has_unit) {
-      const int u = u0 + wave;
+      const int u = u0 + uw;
       const u32x4 *src = Wl + (size_t)u * F::BPU * F::NPB * 64;
+      if constexpr (HALF) {
 #pragma unroll
-      for (int p = 0; p < F::NPU; p++) buf[p] = __builtin_nontemporal_load(src + p * 64);
+        for (int p = 0; p < 4; p++) buf[p] = __builtin_nontemporal_load(src + (4 * uh + p) * 64);
 #pragma unroll
-      for (int j = 0; j < F::DPU; j++)
-        dbuf[j] = __builtin_nontemporal_load(Wdl + ((size_t)u * F::BPU + j) * 64);
+        for (int j = 0; j < 4; j++)
+          dbuf[j] = __builtin_nontemporal_load(Wdl + ((size_t)u * F::BPU + 4 * uh + j) * 64);
+      } else {
+#pragma unroll
+        for (int p = 0; p < F::NPU; p++) buf[p] = __builtin_nontemporal_load(src + p * 64);
+#pragma unroll
+        for (int j = 0; j < F::DPU; j++)
+          dbuf[j] = __builtin_nontemporal_load(Wdl + ((size_t)u * F::BPU + j) * 64);
+      }
     }
+  };
+  auto compute_unit = [&](float &a) {
+    if constexpr (HALF)
+      kqf_q40_half<(NW < 16)>(buf, dbuf, xs + uw * 256 + uh * 128, as + uw * GPU + uh * 4, a);
+    else
+      kqf_unit<FMT, (NW < 16)>(buf, dbuf, xs + wave * 256, as + wave * GPU, a);
   };
   if constexpr (kEarlyW) issue_unit();
   asm volatile("" ::: "memory");
@@ -493,7 +542,7 @@ __global__ void __launch_bounds__(NW * 64)
 
   // 4. the unit
   float acc = 0.0f;
-  if (has_unit) kqf_unit<FMT, (NW < 16)>(buf, dbuf, xs + wave * 256, as + wave * GPU, acc);
+  if (has_unit) compute_unit(acc);
   SYN_TS(5);
 
   if constexpr (OUT == OUT_TOP2) {
@@ -534,7 +583,7 @@ __global__ void __launch_bounds__(NW * 64)
       __syncthreads();  // red is written again for the next panel
       if (gn < np) {
         acc = 0.0f;
-        if (has_unit) kqf_unit<FMT, (NW < 16)>(buf, dbuf, xs + wave * 256, as + wave * GPU, acc);
+        if (has_unit) compute_unit(acc);
       }
     }
     if (wave == 0 && lane == 0) {
@@ -776,23 +825,25 @@ __global__ void __launch_bounds__(256)
   SYN_TS_FLUSH_TO(kqf_phase_ts, 80);
 }
 
-template <int FMT, int PRO, int OUT>
+template <int FMT, int PRO, int OUT, bool HALF = false>
 void launch_nw(int nw, dim3 grid, size_t lds, hipStream_t s, const u32x4 *W, const uint16_t *Wd,
                int B, int N, int bs, const KqfIn &in, const KqfOut &o) {
   switch (nw) {
     case 4:
-      SYN_LAUNCH((k_kqf_gemv<FMT, PRO, OUT, 4>), grid, dim3(256), lds, s, W, Wd, B, N, bs, in, o);
+      SYN_LAUNCH((k_kqf_gemv<FMT, PRO, OUT, 4, HALF>), grid, dim3(256), lds, s, W, Wd, B, N, bs,
+                 in, o);
       break;
     case 8:
-      SYN_LAUNCH((k_kqf_gemv<FMT, PRO, OUT, 8>), grid, dim3(512), lds, s, W, Wd, B, N, bs, in, o);
+      SYN_LAUNCH((k_kqf_gemv<FMT, PRO, OUT, 8, HALF>), grid, dim3(512), lds, s, W, Wd, B, N, bs,
+                 in, o);
       break;
     case 12:
-      SYN_LAUNCH((k_kqf_gemv<FMT, PRO, OUT, 12>), grid, dim3(768), lds, s, W, Wd, B, N, bs, in,
-                 o);
+      SYN_LAUNCH((k_kqf_gemv<FMT, PRO, OUT, 12, HALF>), grid, dim3(768), lds, s, W, Wd, B, N, bs,
+                 in, o);
       break;
     default:
-      SYN_LAUNCH((k_kqf_gemv<FMT, PRO, OUT, 16>), grid, dim3(1024), lds, s, W, Wd, B, N, bs, in,
-                 o);
+      SYN_LAUNCH((k_kqf_gemv<FMT, PRO, OUT, 16, HALF>), grid, dim3(1024), lds, s, W, Wd, B, N, bs,
+                 in, o);
       break;
   }
 }
@@ -830,8 +881,13 @@ syn_status_t launch_gemv(const KqfW &w, const KqfPlan &p, const KqfIn &in, const
                                             o);
       break;
     case SYN_HIP_FMT_Q4_0:
-      launch_nw<SYN_HIP_FMT_Q4_0, PRO, OUT>(nw, grid, lds, s, W, Wd, w.blocks, (int)w.n, p.bs, in,
-                                            o);
+      // two waves per unit (half the decode per wave) while they fit
+      if (2 * p.bs <= kMaxNW)
+        launch_nw<SYN_HIP_FMT_Q4_0, PRO, OUT, true>(waves_for(2 * p.bs), grid, lds, s, W, Wd,
+                                                    w.blocks, (int)w.n, p.bs, in, o);
+      else
+        launch_nw<SYN_HIP_FMT_Q4_0, PRO, OUT>(nw, grid, lds, s, W, Wd, w.blocks, (int)w.n, p.bs,
+                                              in, o);
       break;
     default:
       set_error("fused K-quant GEMV: unsupported format");
