@@ -224,28 +224,28 @@ __device__ __forceinline__ void kqf_unit(u32x4 *pl, const uint16_t *dh, const fl
   }
 }
 
-// Half a Q4_0 unit (four 32-element blocks, stages 4h..4h+3 of the unit) for
-// workgroups that give each unit two waves: pl / dh hold the half's four
-// planes and scales, xs / as its 128 activations and four block sums.
-template <bool DB>
-__device__ __forceinline__ void kqf_q40_half(u32x4 *pl, const uint16_t *dh, const float *xs,
+// Part of a Q4_0 unit for workgroups that give each unit WPU waves (2 or 4):
+// NB = 8 / WPU 32-element blocks, the part's planes and scales in pl / dh,
+// its activations and block sums in xs / as.
+template <bool DB, int NB>
+__device__ __forceinline__ void kqf_q40_part(u32x4 *pl, const uint16_t *dh, const float *xs,
                                              const float *as, float &acc) {
-  asm volatile("" ::: "memory");  // no LDS read of the half moves above its branch
+  asm volatile("" ::: "memory");  // no LDS read of the part moves above its branch
   float xb[DB ? 2 : 1][32];
-  float av[4], dq[4];
+  float av[NB], dq[NB];
 #pragma unroll
-  for (int i = 0; i < 4; i++) av[i] = as[i];
+  for (int i = 0; i < NB; i++) av[i] = as[i];
 #pragma unroll
-  for (int j = 0; j < 4; j++) {  // IEEE f16 scales, converted after the prologue
+  for (int j = 0; j < NB; j++) {  // IEEE f16 scales, converted after the prologue
     uint32_t h = dh[j];
     asm volatile("" : "+v"(h));
     dq[j] = (float)__builtin_bit_cast(_Float16, (uint16_t)h);
   }
   if constexpr (DB) lds_x32(xb[0], xs);
 #pragma unroll
-  for (int t = 0; t < 4; t++) {
+  for (int t = 0; t < NB; t++) {
     if constexpr (DB) {
-      if (t + 1 < 4) lds_x32(xb[(t + 1) & 1], xs + (t + 1) * 32);
+      if (t + 1 < NB) lds_x32(xb[(t + 1) & 1], xs + (t + 1) * 32);
     } else {
       lds_x32(xb[0], xs + t * 32);
     }
@@ -265,11 +265,12 @@ __device__ __forceinline__ void kqf_q40_half(u32x4 *pl, const uint16_t *dh, cons
 // group (32 elements for Q4_K, 16 for Q6_K) is summed across 8 or 4 lanes.
 // dynamic LDS: activation slice [bs*256] | group sums [bs*256/GRP] |
 // (ATTN) chunk logits and weights [2][heads of the slice][nch], 1/den [heads]
-template <int FMT, int PRO, int OUT, int NW, bool HALF>
+template <int FMT, int PRO, int OUT, int NW, int WPU>
 __global__ void __launch_bounds__(NW * 64)
     k_kqf_gemv(const u32x4 *__restrict__ W, const uint16_t *__restrict__ Wd, int B, int N,
                int bs, KqfIn in, KqfOut out) {
-  static_assert(!HALF || FMT == SYN_HIP_FMT_Q4_0, "half units are Q4_0 only");
+  static_assert(WPU == 1 || FMT == SYN_HIP_FMT_Q4_0, "split units are Q4_0 only");
+  constexpr int NBP = 8 / WPU;  // Q4_0 blocks per wave when WPU > 1
   using F = KqfFmt<FMT>;
   constexpr int kNT = NW * 64;
   constexpr int GPU = F::GRP ? 256 / F::GRP : 0;
@@ -301,8 +302,8 @@ __global__ void __launch_bounds__(NW * 64)
   // the prologue runs under the weights' HBM latency; the K-quant formats
   // (up to 16 planes) after the prologue
   constexpr bool kEarlyW = FMT == SYN_HIP_FMT_Q4_0;
-  // HALF: two waves per unit, wave w taking half w & 1 of unit w >> 1
-  const int uw = HALF ? wave >> 1 : wave, uh = HALF ? wave & 1 : 0;
+  // WPU waves per unit: wave w takes part w % WPU of unit w / WPU
+  const int uw = wave / WPU, uh = wave % WPU;
   const bool has_unit = uw < nu_wg;
   u32x4 buf[F::NPU];
   uint16_t dbuf[F::DPU > 0 ? F::DPU : 1];
@@ -310,12 +311,13 @@ __global__ void __launch_bounds__(NW * 64)
     if (has_unit) {
       const int u = u0 + uw;
       const u32x4 *src = Wl + (size_t)u * F::BPU * F::NPB * 64;
-      if constexpr (HALF) {
+      if constexpr (WPU > 1) {
 #pragma unroll
-        for (int p = 0; p < 4; p++) buf[p] = __builtin_nontemporal_load(src + (4 * uh + p) * 64);
+        for (int p = 0; p < NBP; p++)
+          buf[p] = __builtin_nontemporal_load(src + (NBP * uh + p) * 64);
 #pragma unroll
-        for (int j = 0; j < 4; j++)
-          dbuf[j] = __builtin_nontemporal_load(Wdl + ((size_t)u * F::BPU + 4 * uh + j) * 64);
+        for (int j = 0; j < NBP; j++)
+          dbuf[j] = __builtin_nontemporal_load(Wdl + ((size_t)u * F::BPU + NBP * uh + j) * 64);
       } else {
 #pragma unroll
         for (int p = 0; p < F::NPU; p++) buf[p] = __builtin_nontemporal_load(src + p * 64);
@@ -326,8 +328,9 @@ __global__ void __launch_bounds__(NW * 64)
     }
   };
   auto compute_unit = [&](float &a) {
-    if constexpr (HALF)
-      kqf_q40_half<(NW < 16)>(buf, dbuf, xs + uw * 256 + uh * 128, as + uw * GPU + uh * 4, a);
+    if constexpr (WPU > 1)
+      kqf_q40_part<(NW < 16), NBP>(buf, dbuf, xs + uw * 256 + uh * (256 / WPU),
+                                   as + uw * GPU + uh * NBP, a);
     else
       kqf_unit<FMT, (NW < 16)>(buf, dbuf, xs + wave * 256, as + wave * GPU, a);
   };
@@ -825,24 +828,24 @@ __global__ void __launch_bounds__(256)
   SYN_TS_FLUSH_TO(kqf_phase_ts, 80);
 }
 
-template <int FMT, int PRO, int OUT, bool HALF = false>
+template <int FMT, int PRO, int OUT, int WPU = 1>
 void launch_nw(int nw, dim3 grid, size_t lds, hipStream_t s, const u32x4 *W, const uint16_t *Wd,
                int B, int N, int bs, const KqfIn &in, const KqfOut &o) {
   switch (nw) {
     case 4:
-      SYN_LAUNCH((k_kqf_gemv<FMT, PRO, OUT, 4, HALF>), grid, dim3(256), lds, s, W, Wd, B, N, bs,
+      SYN_LAUNCH((k_kqf_gemv<FMT, PRO, OUT, 4, WPU>), grid, dim3(256), lds, s, W, Wd, B, N, bs,
                  in, o);
       break;
     case 8:
-      SYN_LAUNCH((k_kqf_gemv<FMT, PRO, OUT, 8, HALF>), grid, dim3(512), lds, s, W, Wd, B, N, bs,
+      SYN_LAUNCH((k_kqf_gemv<FMT, PRO, OUT, 8, WPU>), grid, dim3(512), lds, s, W, Wd, B, N, bs,
                  in, o);
       break;
     case 12:
-      SYN_LAUNCH((k_kqf_gemv<FMT, PRO, OUT, 12, HALF>), grid, dim3(768), lds, s, W, Wd, B, N, bs,
+      SYN_LAUNCH((k_kqf_gemv<FMT, PRO, OUT, 12, WPU>), grid, dim3(768), lds, s, W, Wd, B, N, bs,
                  in, o);
       break;
     default:
-      SYN_LAUNCH((k_kqf_gemv<FMT, PRO, OUT, 16, HALF>), grid, dim3(1024), lds, s, W, Wd, B, N, bs,
+      SYN_LAUNCH((k_kqf_gemv<FMT, PRO, OUT, 16, WPU>), grid, dim3(1024), lds, s, W, Wd, B, N, bs,
                  in, o);
       break;
   }
@@ -881,10 +884,14 @@ syn_status_t launch_gemv(const KqfW &w, const KqfPlan &p, const KqfIn &in, const
                                             o);
       break;
     case SYN_HIP_FMT_Q4_0:
-      // two waves per unit (half the decode per wave) while they fit
-      if (2 * p.bs <= kMaxNW)
-        launch_nw<SYN_HIP_FMT_Q4_0, PRO, OUT, true>(waves_for(2 * p.bs), grid, lds, s, W, Wd,
-                                                    w.blocks, (int)w.n, p.bs, in, o);
+      // four or two waves per unit (a quarter or half of the decode per
+      // wave) while they fit the workgroup
+      if (4 * p.bs <= kMaxNW)
+        launch_nw<SYN_HIP_FMT_Q4_0, PRO, OUT, 4>(waves_for(4 * p.bs), grid, lds, s, W, Wd,
+                                                 w.blocks, (int)w.n, p.bs, in, o);
+      else if (2 * p.bs <= kMaxNW)
+        launch_nw<SYN_HIP_FMT_Q4_0, PRO, OUT, 2>(waves_for(2 * p.bs), grid, lds, s, W, Wd,
+                                                 w.blocks, (int)w.n, p.bs, in, o);
       else
         launch_nw<SYN_HIP_FMT_Q4_0, PRO, OUT>(nw, grid, lds, s, W, Wd, w.blocks, (int)w.n, p.bs,
                                               in, o);
