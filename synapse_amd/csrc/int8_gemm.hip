@@ -2,17 +2,20 @@
 //
 // Reference: int8GemmTiled for M > 16 (qmatmul.zig:68-99, 442-548): the
 // exact i32 sum of each KC = 512 chunk of K is converted and added in chunk
-// order, C += (f32(acc_chunk) * sa[i]) * sb[j].  Here K advances 64 bytes per
-// step through v_mfma_i32_32x32x32_i8 (exact integer products), and every 8
-// steps (one KC chunk) the i32 accumulators are folded into an f32 tile in
-// that order, so the result is bit-identical to the reference.
+// order, C += (f32(acc_chunk) * sa[i]) * sb[j].  Here K advances 128 bytes
+// per step through v_mfma_i32_32x32x32_i8 (exact integer products), and every
+// 4 steps (one KC chunk) the i32 accumulators are folded into an f32 tile in
+// that order, so the result is bit-identical to the reference.  Two forms:
+// k_gemm_w8a8_dl (direct global->LDS loads; K a multiple of 128) and
+// k_gemm_w8a8_ws (producer waves staging through registers; any K).
 //
 // Operands: activations int8 [M, ldx] row-major; weights in the 64-row panel
-// layout (linear.hpp), so a 64-byte K step of a panel is 4 contiguous 1 KiB
+// layout (linear.hpp), so a 128-byte K step of a panel is 8 contiguous 1 KiB
 // chunk blocks.
 #include <algorithm>
 
 #include "linear.hpp"
+#include "lds_dma.hpp"
 
 namespace syn {
 
@@ -198,6 +201,204 @@ __global__ void __launch_bounds__(TM * 2 + 256)
     }
 }
 
+// ---------------------------------------------------------------------------
+// Direct-load form, for K a multiple of 128.  2 WR waves own a TM x TN tile
+// of C; wave (wr, wc) the (TM/WR) x (TN/2) sub-tile at rows wr*TM/WR,
+// columns wc*TN/2, as (TM/WR/32) x (TN/64) MFMA tiles of 32 x 32, so every
+// 16-byte fragment read from LDS feeds that many MFMAs.  Both operands go from
+// global memory straight into LDS (gfx950 global_load_lds_dwordx4: no
+// staging registers, no ds_write), three 128-byte K steps deep:
+//  - activations as TM rows of 128 bytes; the eight 16-byte chunks of row r
+//    sit XOR-swizzled (chunk c at slot c ^ ((r / 2) % 8)): the 64 banks of
+//    4 bytes span two rows, and the fragment reads of 16 consecutive rows
+//    hit 16 distinct 16-byte bank groups (with c ^ (r % 8), rows r and r + 8
+//    collide: 31 % of the LDS cycles were bank conflicts);
+//  - weights as stored, [panel][chunk][64 rows][16 bytes]: one 1 KiB direct
+//    load per (panel, chunk), read back conflict-free.
+// One barrier per step; the i32 sums of each KC = 512 chunk (4 steps) are
+// folded into the f32 tile as in k_gemm_w8a8_ws.  NS stages: the loads run
+// NS - 1 steps ahead (3 stages of the 128 x 128 tile would keep a second
+// workgroup off the CU).
+template <int TM, int TN> constexpr int dl_stage() { return (TM + TN) * 128; }
+template <int TM, int TN, int NS> constexpr size_t dl_lds_bytes() {
+  return (size_t)NS * dl_stage<TM, TN>() + TM * sizeof(float);
+}
+
+template <int TM, int TN, int NS, int WR>
+__global__ void __launch_bounds__(128 * WR)
+    k_gemm_w8a8_dl(const int8_t *__restrict__ xq, int ldx, const float *__restrict__ sx, int M,
+                   const i32x4 *__restrict__ W, const float *__restrict__ ws, int N, int C,
+                   float *__restrict__ y, int ldy) {
+  constexpr int NWAVE = 2 * WR, WM = TM / WR, WN = TN / 2, MT = WM / 32, NT = WN / 32;
+  constexpr int LA = TM / 8 / NWAVE, LB = TN / 8 / NWAVE;  // direct loads per wave and step
+  static_assert(LA * NWAVE * 8 == TM && LB * NWAVE * 8 == TN, "whole loads per wave");
+  constexpr int A_BYTES = TM * 128, STAGE = dl_stage<TM, TN>(), AFTER = LA + LB;
+  extern __shared__ __attribute__((aligned(16))) int8_t dlds[];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int l32 = lane & 31, lh = lane >> 5, wr = wave >> 1, wc = wave & 1;
+  const int n0 = blockIdx.x * TN, m0 = blockIdx.y * TM;
+  const int nsteps = C >> 3;
+  const int last_panel = (N - 1) >> 6;
+  // activation load i of this wave: rows 8 (wave * LA + i) .. + 7, lane l
+  // bringing chunk (l % 8) ^ ((row / 2) % 8) of row 8 (wave * LA + i) + l / 8
+  // into slot l % 8; rows past M read row M - 1 (never stored)
+  uint32_t aoff[LA];
+#pragma unroll
+  for (int i = 0; i < LA; i++) {
+    const int row = (wave * LA + i) * 8 + (lane >> 3), c = (lane & 7) ^ ((row >> 1) & 7);
+    aoff[i] = (uint32_t)min(m0 + row, M - 1) * (uint32_t)ldx + (uint32_t)c * 16u;
+  }
+  // weight load j of this wave: q = wave * LB + j is (panel q / 8 of the
+  // tile, clamped to the matrix's last; chunk q % 8 of the step)
+  const i32x4 *wsrc[LB];
+#pragma unroll
+  for (int j = 0; j < LB; j++) {
+    const int q = wave * LB + j;
+    const size_t panel = (size_t)min((n0 >> 6) + (q >> 3), last_panel);
+    wsrc[j] = W + (panel * C + (q & 7)) * 64 + lane;
+  }
+  const uint32_t lds_base = lds_addr_of(dlds);
+  auto dma = [&](int t, int stage) {
+    const int step = min(t, nsteps - 1);
+    const uint32_t sb = lds_base + (uint32_t)(stage * STAGE);
+    const uint32_t wa = (uint32_t)__builtin_amdgcn_readfirstlane(wave * LA * 1024);
+    const uint32_t wb = (uint32_t)__builtin_amdgcn_readfirstlane(A_BYTES + wave * LB * 1024);
+#pragma unroll
+    for (int i = 0; i < LA; i++)
+      kr_dma(xq + aoff[i] + (size_t)step * 128, sb + wa + (uint32_t)(i * 1024));
+#pragma unroll
+    for (int j = 0; j < LB; j++)
+      kr_dma(wsrc[j] + (size_t)step * 8 * 64, sb + wb + (uint32_t)(j * 1024));
+  };
+#pragma unroll
+  for (int i = 0; i < NS; i++) dma(i, i);
+
+  // row scales of the tile in LDS (read at each chunk fold), the lane's
+  // column scales in registers
+  float *sa_l = reinterpret_cast<float *>(dlds + NS * STAGE);
+  if (tid < TM) sa_l[tid] = sx[min(m0 + tid, M - 1)];
+  float sb[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; nt++)
+    sb[nt] = ws[min(n0 + wc * WN + nt * 32 + l32, (last_panel + 1) * 64 - 1)];
+  i32x16 acc[MT][NT];
+  float cf[MT][NT][16];
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        acc[mt][nt][r] = 0;
+        cf[mt][nt][r] = 0.0f;
+      }
+  // fragment addresses inside a stage: A row (wr*WM + mt*32 + l32), whose
+  // swizzle is (l32 / 2) % 8; B panel col / 64, row col % 64 of column
+  // wc*WN + nt*32 + l32
+  const int arow = (wr * WM + l32) * 128, asw = (l32 >> 1) & 7;
+  int boff[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; nt++) {
+    const int col = wc * WN + nt * 32 + l32;
+    boff[nt] = A_BYTES + (col >> 6) * 8 * 1024 + (col & 63) * 16;
+  }
+  i32x4 fa[2][MT], fb[2][NT];
+  auto read = [&](int stage, int kk, int b) {
+    const int8_t *st = dlds + stage * STAGE;
+    const int c = 2 * kk + lh;
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+      fa[b][mt] = *reinterpret_cast<const i32x4 *>(st + arow + mt * 32 * 128 + ((c ^ asw) << 4));
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++)
+      fb[b][nt] = *reinterpret_cast<const i32x4 *>(st + boff[nt] + c * 1024);
+  };
+  auto mma = [&](int b) {
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int nt = 0; nt < NT; nt++)
+        acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[b][mt], fb[b][nt], acc[mt][nt],
+                                                            0, 0, 0);
+  };
+  auto fold = [&]() {  // C += (f32(acc) * sa) * sb, then a new chunk
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const float f =
+              (float)acc[mt][nt][r] * sa_l[wr * WM + mt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3)];
+          const float t = f * sb[nt];
+          cf[mt][nt][r] = cf[mt][nt][r] + t;
+          acc[mt][nt][r] = 0;
+        }
+  };
+
+  // Step t lives in stage t % NS.  Iteration t: K slices 0-2 of step t
+  // (each beside the reads of the next slice); the barrier that publishes
+  // step t+1 (and the row scales, before the first); the load of step t+NS
+  // into the stage step t has left; step t+1's slice 0 reads beside step
+  // t's slice 3 (clamped, unused data after the last step).
+  kr_publish<(NS - 1) * AFTER>();
+  read(0, 0, 0);
+  for (int t = 0; t < nsteps; t++) {
+    const int cur = t % NS, nxt = cur == NS - 1 ? 0 : cur + 1;
+#pragma unroll
+    for (int kk = 0; kk < 3; kk++) {
+      read(cur, kk + 1, (kk + 1) & 1);
+      mma(kk & 1);
+    }
+    kr_publish<(NS - 2) * AFTER>();
+    dma(t + NS, cur);
+    i32x4 a3[MT], b3[NT];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) a3[mt] = fa[1][mt];
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) b3[nt] = fb[1][nt];
+    read(nxt, 0, 0);
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+      for (int nt = 0; nt < NT; nt++)
+        acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a3[mt], b3[nt], acc[mt][nt], 0, 0, 0);
+    if (((t + 1) & 3) == 0 || t + 1 == nsteps) fold();
+  }
+  // the prefetches past the last step must land before the workgroup's LDS
+  // can go to another workgroup
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+    for (int nt = 0; nt < NT; nt++) {
+      const int n = n0 + wc * WN + nt * 32 + l32;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int m = m0 + wr * WM + mt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
+        if (m < M && n < N) y[(size_t)m * ldy + n] = cf[mt][nt][r];
+      }
+    }
+}
+
+template <int TM, int TN, int NS, int WR>
+static syn_status_t launch_w8a8_dl(const int8_t *xq, size_t ldx, const float *sx, size_t M,
+                                   const void *W, const float *ws, size_t N, int C, float *y,
+                                   size_t ldy, hipStream_t s) {
+  static bool attr_set = false;  // more than the default 64 KiB of dynamic LDS
+  constexpr size_t shm = dl_lds_bytes<TM, TN, NS>();
+  if (!attr_set) {
+    SYN_HIP(hipFuncSetAttribute((const void *)k_gemm_w8a8_dl<TM, TN, NS, WR>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm));
+    attr_set = true;
+  }
+  const dim3 grid((unsigned)cdiv(N, TN), (unsigned)cdiv(M, TM));
+  SYN_LAUNCH((k_gemm_w8a8_dl<TM, TN, NS, WR>), grid, dim3(128 * WR), shm, s, xq, (int)ldx, sx, (int)M,
+             (const i32x4 *)W, ws, (int)N, C, y, (int)ldy);
+  SYN_LAUNCH_CHECK();
+  return SYN_OK;
+}
+
 syn_status_t launch_gemm_w8a8(const int8_t *xq, size_t ldx, const float *sx, size_t M,
                               const void *W, const float *ws, size_t N, int C, float *y,
                               size_t ldy, hipStream_t s) {
@@ -205,8 +406,21 @@ syn_status_t launch_gemm_w8a8(const int8_t *xq, size_t ldx, const float *sx, siz
     set_error("activation row stride must be a multiple of 16 bytes");
     return SYN_ERR_SHAPE_MISMATCH;
   }
-  // 256-row tiles, or 128-row tiles when the larger ones cannot fill the GPU
-  // (K is never split: the chunked f32 epilogue must run in chunk order)
+  // K is never split: the chunked f32 epilogue must run in chunk order.
+  // Direct-load tiles when K is whole 128-byte steps (the loads cannot
+  // zero a K tail) and the byte offsets fit 32 bits: 128 x 128 with two
+  // stages (two workgroups per CU) when that gives every CU a workgroup,
+  // else 128 x 64.  Measured (int8 TOPS): 2048 x 14336 x 4096 1248 against
+  // 968 for 256 x 128 with three stages and four waves (one wave per SIMD),
+  // 1201 for the same tile with eight waves, 988 for k_gemm_w8a8_ws;
+  // 512 x 14336 x 4096 1260 against 914 for 128 x 128 with three stages.
+  if (C % 8 == 0 && (uintptr_t)xq % 16 == 0 && M * ldx < ((size_t)1 << 31)) {
+    if (cdiv(M, 128) * cdiv(N, 128) >= 256)
+      return launch_w8a8_dl<128, 128, 2, 2>(xq, ldx, sx, M, W, ws, N, C, y, ldy, s);
+    return launch_w8a8_dl<128, 64, 3, 2>(xq, ldx, sx, M, W, ws, N, C, y, ldy, s);
+  }
+  // otherwise 256-row tiles, or 128-row tiles when the larger ones cannot
+  // fill the GPU
   // two LDS stages of 128-byte K steps exceed the default 64 KiB
   static bool attr_set[2] = {false, false};
   if (cdiv(M, 256) * cdiv(N, WBN) >= 256) {

@@ -177,7 +177,12 @@ def test_device_expf_matches_glibc():
 
 
 @pytest.mark.parametrize("m,k,n", [(128, 1024, 3072), (300, 2048, 1000), (17, 4096, 513),
-                                   (256, 4096, 1024)])
+                                   (256, 4096, 1024),
+                                   # direct-load tiles 256 x 128 and 128 x 128 (a K of 5 and
+                                   # 9 steps: a partial last KC chunk), ragged M and N
+                                   (300, 640, 16384), (300, 1152, 11000),
+                                   # K not whole 128-byte steps: the register-staged kernel
+                                   (40, 1040, 700), (520, 1040, 9000)])
 def test_int8_gemm_mfma_bit_exact(m, k, n):
     # M > 16: v_mfma_i32_32x32x32_i8 tiles with the KC=512 chunked epilogue
     rng = np.random.default_rng(m + k + n)
