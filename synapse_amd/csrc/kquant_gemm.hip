@@ -15,6 +15,7 @@
 // (relative 2^-11 each) keep the result well inside the 1e-3 per-row
 // tolerance (measured in the tests).
 #include <algorithm>
+#include <type_traits>
 
 #include "decode_fused.hpp"
 #include "kquant.hpp"
@@ -208,12 +209,14 @@ __device__ __forceinline__ void pg_decode_w(const RawW &r, int step, int q, int 
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-// LDS: two stages of A [256][72] and B [128][72] f16 (110,592 bytes)
-constexpr int PG_STAGE = (PGM + PGN) * PGLD;
+// LDS: two stages of A [TM][72] and B [128][72] f16 (110,592 bytes for
+// TM = 256, 73,728 for 128: two workgroups per CU)
+template <int TM> constexpr int pg_stage() { return (TM + PGN) * PGLD; }
 
 // ---------------------------------------------------------------------------
-// Wave-specialised form: 12 waves, 8 consumers and 4 producers.  The eight
-// consumer waves (4 x 2, each a 64 x 64 sub-tile of the 256 x 128 tile) only
+// Wave-specialised form: TM/32 consumer waves and 4 producers (12 waves for
+// TM = 256, 8 for 128).  The consumer waves ((TM/64) x 2, each a 64 x 64
+// sub-tile of the TM x 128 tile) only
 // read operand fragments from LDS and issue MFMAs; the four producer waves
 // only move data: they keep the raw global bytes of the next kPDepth steps in
 // a register ring, write step t+1's activations and decoded f16 weights into
@@ -222,45 +225,47 @@ constexpr int PG_STAGE = (PGM + PGN) * PGLD;
 // core work of two consumer waves overlaps the loads, decode and LDS stores
 // of one producer wave.  Each role runs its own loop (its values stay out of
 // the other role's registers); both meet the same barriers.
-constexpr int PGT2 = 768, kPDepth = 2;
+constexpr int kPDepth = 2;
+template <int TM> constexpr int pg_threads() { return TM * 2 + 256; }
 
-template <int FMT, bool EXACT>
-__global__ void __launch_bounds__(PGT2)
+template <int FMT, bool EXACT, int TM>
+__global__ void __launch_bounds__(pg_threads<TM>())
     k_gemm_kq2(const _Float16 *__restrict__ Xh, int ldh, int M, int K,
                const u32x4 *__restrict__ W, const uint16_t *__restrict__ Wd, int N, int B,
                float *__restrict__ Y, int ldy, int steps_per_split) {
   extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int n0 = blockIdx.x * PGN, m0 = blockIdx.y * PGM;
+  constexpr int NC = TM / 32, AI = TM / 32, PG_STAGE = pg_stage<TM>();
+  const int n0 = blockIdx.x * PGN, m0 = blockIdx.y * TM;
   const int s_begin = blockIdx.z * steps_per_split;
   const int nsteps = min((K + PGK - 1) / PGK - s_begin, steps_per_split);
-  if (wave >= 8) {
+  if (wave >= NC) {
     // ------------------------------------------------------------ producer
-    const int pt = tid - 512;  // 0..255
-    // A: 2048 chunks of 16 B per step, eight per producer thread
-    const _Float16 *arow[8];
+    const int pt = tid - NC * 64;  // 0..255
+    // A: TM * 8 chunks of 16 B per step, TM / 32 per producer thread
+    const _Float16 *arow[AI];
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
+    for (int i = 0; i < AI; i++) {
       const int idx = pt + i * 256;
       arow[i] = Xh + (size_t)min(m0 + (idx >> 3), M - 1) * ldh + (idx & 7) * 8;
     }
     // W: row n0 + pt/2 (clamped), quarters 2*(pt%2), 2*(pt%2)+1 of the step
     const int brow = pt >> 1, bq0 = 2 * (pt & 1);
     const int bn = min(n0 + brow, N - 1);
-    u32x4 ra[kPDepth][8];
+    u32x4 ra[kPDepth][AI];
     RawW rw[kPDepth][2];
     auto load = [&](int slot, int t) {
       const int step = s_begin + min(t, nsteps - 1);
 #pragma unroll
-      for (int i = 0; i < 8; i++)
+      for (int i = 0; i < AI; i++)
         ra[slot][i] = *reinterpret_cast<const u32x4 *>(arow[i] + (size_t)step * PGK);
       pg_load_w<FMT>(rw[slot][0], W, Wd, B, bn, step, bq0);
       pg_load_w<FMT>(rw[slot][1], W, Wd, B, bn, step, bq0 + 1);
     };
     auto stage = [&](int slot, int t, int buf) {
-      _Float16 *As = lds + buf * PG_STAGE, *Bs = As + PGM * PGLD;
+      _Float16 *As = lds + buf * PG_STAGE, *Bs = As + TM * PGLD;
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
+      for (int i = 0; i < AI; i++) {
         const int idx = pt + i * 256;
         *reinterpret_cast<u32x4 *>(&As[(idx >> 3) * PGLD + (idx & 7) * 8]) = ra[slot][i];
       }
@@ -306,15 +311,15 @@ __global__ void __launch_bounds__(PGT2)
     for (int nt = 0; nt < 2; nt++)
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[mt][nt][r] = 0.0f;
-  // Two consumer groups half a step apart: waves 0-3 read step t's
-  // fragments and multiply them; waves 4-7 first multiply step t-1's
-  // fragments (held in registers across the barrier), then read step t's.
-  // Each SIMD holds one wave of each group, so one wave's LDS reads overlap
-  // the other's matrix-core work.
-  const bool lag = wave >= 4;
+  // Two consumer groups half a step apart: the first half of the waves read
+  // step t's fragments and multiply them; the second half first multiply
+  // step t-1's fragments (held in registers across the barrier), then read
+  // step t's.  With eight consumers each SIMD holds one wave of each group,
+  // so one wave's LDS reads overlap the other's matrix-core work.
+  const bool lag = wave >= NC / 2;
   f16x8 fa[4][2], fb[4][2];
   auto read = [&](int t) {
-    const _Float16 *As = lds + (t & 1) * PG_STAGE, *Bs = As + PGM * PGLD;
+    const _Float16 *As = lds + (t & 1) * PG_STAGE, *Bs = As + TM * PGLD;
 #pragma unroll
     for (int k16 = 0; k16 < 4; k16++) {
 #pragma unroll
@@ -856,7 +861,7 @@ static syn_status_t kq_gemm_f16(int fmt, bool exact, const u32x4 *W, const uint1
                                 hipStream_t s) {
   const size_t ldh = round_up(k, PGK);
   const int steps = (int)cdiv(k, PGK);
-  static bool attr[11] = {};
+  static bool attr[21] = {};
   // Q4_0 on enough 256 x 256 tiles for three quarters of the CUs: the
   // direct-load kernel (measured ahead of k_gemm_kq5 there; for Q8_0 the
   // two tie, and k_gemm_kq2 leads on split-K grids)
@@ -872,24 +877,30 @@ static syn_status_t kq_gemm_f16(int fmt, bool exact, const u32x4 *W, const uint1
   SYN_TRY(to_f16_rows(m, k, d_x, ldx, xh, xh_elems, false, s));
   const _Float16 *X = xh.as<_Float16>();
   // Enough 256 x 256 tiles for three quarters of the CUs: the four-wave
-  // kernel, one K pass per tile.  Fewer: 256 x 128 tiles (twice as many),
-  // split over K in at most three parts when even those cover under half
-  // the CUs.  Every split adds its partial tile into Y with f32 atomics, and
-  // that traffic outweighs idle CUs beyond that point (Q8_0, M = 512: 224
-  // tiles 78 us unsplit / 115 us in two; 64 tiles 47 us in three, 66 us in
-  // six).
+  // kernel, one K pass per tile.  Else 256 x 128 tiles (twice as many) when
+  // they cover half the CUs, one K pass.  Fewer: 128 x 128 tiles (two
+  // workgroups per CU), split over K into at most kMaxSplit parts towards
+  // 256 workgroups.  Every split adds its partial tile into Y with f32
+  // atomics, and that traffic outweighs idle CUs beyond one workgroup per
+  // CU (Q8_0, 128 x 128 tiles, M = 512: q 4096 -> 4096 42.0 us in two parts,
+  // 51.4 in four; k/v 4096 -> 1024 23.9 us in four, 29.0 in two; with
+  // 256 x 128 tiles in three parts 46.9 and 29.9).
+  constexpr int kMaxSplit = 4;
   const bool big = cdiv(n, PG3N) * cdiv(m, PG3M) >= 192;
-  const int tiles_n = (int)cdiv(n, big ? PG3N : PGN), tiles_m = (int)cdiv(m, big ? PG3M : PGM);
+  const bool mid = !big && cdiv(n, PGN) * cdiv(m, PGM) >= 128;
+  const int tm = big ? PG3M : mid ? PGM : 128;
+  const int tiles_n = (int)cdiv(n, big ? PG3N : PGN), tiles_m = (int)cdiv(m, (size_t)tm);
   int ksplit = 1;
-  if (!big && tiles_n * tiles_m < 128)  // >= 8 steps per split
-    ksplit = std::max(1, std::min(3, std::min((int)cdiv(256, (size_t)(tiles_n * tiles_m)),
-                                              steps / 8)));
+  if (!big && !mid)  // >= 8 steps per split
+    ksplit = std::max(1, std::min(kMaxSplit, std::min((int)cdiv(256, (size_t)(tiles_n * tiles_m)),
+                                                      steps / 8)));
   const int per = (int)cdiv((size_t)steps, (size_t)ksplit);
   ksplit = (int)cdiv((size_t)steps, (size_t)per);
   if (ksplit > 1) SYN_TRY(zero_y(d_y, m, n, ldy, s));
   const dim3 grid((unsigned)tiles_n, (unsigned)tiles_m, (unsigned)ksplit);
-  const size_t shm = 2 * (size_t)(big ? PG3_STAGE : PG_STAGE) * sizeof(_Float16);
-  const unsigned threads = big ? 256 : PGT2;
+  const size_t shm =
+      2 * (size_t)(big ? PG3_STAGE : mid ? pg_stage<256>() : pg_stage<128>()) * sizeof(_Float16);
+  const unsigned threads = big ? 256 : mid ? pg_threads<256>() : pg_threads<128>();
   auto launch = [&](auto kern, bool &attr_set) -> syn_status_t {
     return launch_gemm(kern, attr_set, grid, threads, shm, X, ldh, m, k, W, Wd, n, blocks, d_y,
                        ldy, per, s);
@@ -901,11 +912,16 @@ static syn_status_t kq_gemm_f16(int fmt, bool exact, const u32x4 *W, const uint1
     if (fmt == SYN_HIP_FMT_Q4_K) return launch(k_gemm_kq5<SYN_HIP_FMT_Q4_K, true>, attr[2]);
     return launch(k_gemm_kq5<SYN_HIP_FMT_Q6_K, true>, attr[3]);
   }
-  if (fmt == SYN_HIP_FMT_Q8_0 && exact) return launch(k_gemm_kq2<SYN_HIP_FMT_Q8_0, true>, attr[4]);
-  if (fmt == SYN_HIP_FMT_Q8_0) return launch(k_gemm_kq2<SYN_HIP_FMT_Q8_0, false>, attr[5]);
-  if (fmt == SYN_HIP_FMT_Q4_0) return launch(k_gemm_kq2<SYN_HIP_FMT_Q4_0, true>, attr[9]);
-  if (fmt == SYN_HIP_FMT_Q4_K) return launch(k_gemm_kq2<SYN_HIP_FMT_Q4_K, true>, attr[6]);
-  return launch(k_gemm_kq2<SYN_HIP_FMT_Q6_K, true>, attr[7]);
+  auto kq2 = [&](auto tmc, int a) -> syn_status_t {
+    constexpr int T = decltype(tmc)::value;
+    if (fmt == SYN_HIP_FMT_Q8_0 && exact) return launch(k_gemm_kq2<SYN_HIP_FMT_Q8_0, true, T>, attr[a]);
+    if (fmt == SYN_HIP_FMT_Q8_0) return launch(k_gemm_kq2<SYN_HIP_FMT_Q8_0, false, T>, attr[a + 1]);
+    if (fmt == SYN_HIP_FMT_Q4_0) return launch(k_gemm_kq2<SYN_HIP_FMT_Q4_0, true, T>, attr[a + 2]);
+    if (fmt == SYN_HIP_FMT_Q4_K) return launch(k_gemm_kq2<SYN_HIP_FMT_Q4_K, true, T>, attr[a + 3]);
+    return launch(k_gemm_kq2<SYN_HIP_FMT_Q6_K, true, T>, attr[a + 4]);
+  };
+  return mid ? kq2(std::integral_constant<int, 256>{}, 11)
+             : kq2(std::integral_constant<int, 128>{}, 16);
 }
 
 syn_status_t QLinearKQ::gemm(size_t m, const float *d_x, size_t ldx, float *d_y, size_t ldy,
