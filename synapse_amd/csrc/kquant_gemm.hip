@@ -878,7 +878,9 @@ static syn_status_t kq_gemm_f16(int fmt, bool exact, const u32x4 *W, const uint1
   const _Float16 *X = xh.as<_Float16>();
   // Enough 256 x 256 tiles for three quarters of the CUs: the four-wave
   // kernel, one K pass per tile.  Else 256 x 128 tiles (twice as many) when
-  // they cover half the CUs, one K pass.  Fewer: 128 x 128 tiles (two
+  // they cover three quarters of the CUs, one K pass (Q8_0, 2048 x 4096 x
+  // 4096: 727 against 620 TF/s on 128 x 128 tiles; 1024 x 4096 x 4096, 128
+  // tiles of 256 x 128: 500 against 605).  Fewer: 128 x 128 tiles (two
   // workgroups per CU), split over K into at most kMaxSplit parts towards
   // 256 workgroups.  Every split adds its partial tile into Y with f32
   // atomics, and that traffic outweighs idle CUs beyond one workgroup per
@@ -887,7 +889,7 @@ static syn_status_t kq_gemm_f16(int fmt, bool exact, const u32x4 *W, const uint1
   // 256 x 128 tiles in three parts 46.9 and 29.9).
   constexpr int kMaxSplit = 4;
   const bool big = cdiv(n, PG3N) * cdiv(m, PG3M) >= 192;
-  const bool mid = !big && cdiv(n, PGN) * cdiv(m, PGM) >= 128;
+  const bool mid = !big && cdiv(n, PGN) * cdiv(m, PGM) >= 192;
   const int tm = big ? PG3M : mid ? PGM : 128;
   const int tiles_n = (int)cdiv(n, big ? PG3N : PGN), tiles_m = (int)cdiv(m, (size_t)tm);
   int ksplit = 1;
