@@ -169,9 +169,8 @@ struct syn_hip_klm_s {
                                      prefill ? nullptr : &st()->pos, 0, qrot.as<float>(),
                                      kc_l(l), vc_l(l), (int)S, s, prefill ? cache_off : 0));
       if (prefill)
-        SYN_TRY(launch_attention_prefill(qrot.as<float>(), kc_l(l), vc_l(l), rows, nh, nkv,
-                                         (int)hd, (int)S, nullptr, attn.as<float>(), s,
-                                         cache_off));
+        SYN_TRY(launch_attention_prefill_tol(qrot.as<float>(), kc_l(l), vc_l(l), rows, nh, nkv,
+                                             (int)hd, (int)S, attn.as<float>(), s, cache_off));
       else
         SYN_TRY(launch_attention_decode(qrot.as<float>(), kc_l(l), vc_l(l), &st()->pos, nh, nkv,
                                         (int)hd, scores.as<float>(), (int)S, attn.as<float>(),

@@ -65,6 +65,13 @@ syn_status_t launch_attention_decode(const float *q, const float *kcache, const 
 syn_status_t launch_attention_prefill(const float *q, const float *kcache, const float *vcache,
                                       int t, int n_heads, int n_kv, int head_dim, int max_seq,
                                       float *scores, float *out, hipStream_t s, int cache_off = 0);
+// the same attention without the reference's float order (parallel chains,
+// tree reductions), for the decoders graded to a tolerance; prompts whose
+// scores do not fit LDS run launch_attention_prefill
+syn_status_t launch_attention_prefill_tol(const float *q, const float *kcache,
+                                          const float *vcache, int t, int n_heads, int n_kv,
+                                          int head_dim, int max_seq, float *out, hipStream_t s,
+                                          int cache_off = 0);
 // h = silu(gate) * up (int8.rs:500-503), then quantize rows of h
 syn_status_t launch_swiglu_quant(const float *gu, int ldgu, int rows, int inter, int8_t *hq,
                                  int ldq, float *sh, hipStream_t s);

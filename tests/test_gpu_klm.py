@@ -76,6 +76,26 @@ def test_tiny_llama_style(prompt_len):
         tok = O.argmax(lo)
 
 
+def test_prefill_attention_hd128_row_blocks_and_append():
+    # the tolerance-graded prefill attention (32-row blocks, 64-position
+    # chunks) at head dim 128 with GQA: a 150-token prompt (five row blocks,
+    # three chunks) and a 70-token append at cache offset 150
+    cfg = dict(hidden=512, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=128, inter=512,
+               vocab=300, max_seq=232, eps=1e-5, rope_theta=5e5)
+    o, g = build_pair(cfg, LLAMA_FMTS)
+    ids = O.token_ids(150, 0x5EED0000 + 0xFFFF, cfg["vocab"])
+    lo, lg = o.prefill(ids), g.prefill(ids)
+    assert _cos(lo, lg) >= 0.9999 and _rel(lg, lo) < 5e-3, (_cos(lo, lg), _rel(lg, lo))
+    extra = O.token_ids(70, 0x5EED0000 + 0x1234, cfg["vocab"])
+    lo, lg = o.prefill_append(extra), g.prefill_append(extra)
+    assert _cos(lo, lg) >= 0.9999 and _rel(lg, lo) < 5e-3, (_cos(lo, lg), _rel(lg, lo))
+    tok = O.argmax(lo)
+    for step in range(4):
+        lo, lg = o.forward_one(tok), g.forward_one(tok)
+        assert _cos(lo, lg) >= 0.9999 and _rel(lg, lo) < 5e-3, (step, _rel(lg, lo))
+        tok = O.argmax(lo)
+
+
 def test_tiny_q8_0_with_qk_norm_greedy():
     fm = (hip.FMT_Q8_0,) * 5
     o, g = build_pair(TINY, fm, qk_norm=True)
