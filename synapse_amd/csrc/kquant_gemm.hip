@@ -861,6 +861,8 @@ static syn_status_t kq_gemm_f16(int fmt, bool exact, const u32x4 *W, const uint1
                                 hipStream_t s) {
   const size_t ldh = round_up(k, PGK);
   const int steps = (int)cdiv(k, PGK);
+  // dynamic-LDS attribute set per kernel: k_gemm_kq5 0-3 and 8, k_gemm_kqr
+  // 10, k_gemm_kq2 11-15 (256-row tiles) and 16-20 (128-row tiles)
   static bool attr[21] = {};
   // Q4_0 on enough 256 x 256 tiles for three quarters of the CUs: the
   // direct-load kernel (measured ahead of k_gemm_kq5 there; for Q8_0 the
