@@ -137,6 +137,7 @@ def _declare(L):
         "orc_mamba_init_synthetic": (C.c_int, [P, C.c_uint64]),
         "orc_mamba_init_synthetic_std": (C.c_int, [P, C.c_uint64, C.c_float]),
         "orc_mamba_reset": (None, [P]),
+        "orc_mamba_set_int8_xdt": (C.c_int, [P]),
         "orc_mamba_prefill": (C.c_int, [P, P, SZ, P]),
         "orc_mamba_decode_one": (C.c_int, [P, C.c_uint32, P]),
         "orc_mamba_generate": (C.c_int, [P, P, SZ, SZ, P, P]),
@@ -735,6 +736,16 @@ class QuantizedMamba:
         """std: the projections' and conv taps' (the embedding keeps 0.02)"""
         if lib().orc_mamba_init_synthetic_std(self.h, seed_base, std):
             raise RuntimeError("orc_mamba_init_synthetic failed")
+
+    def set_int8_xdt(self):
+        """BASELINE config 5's variant: x_proj and dt_proj quantized by
+        QuantizedLinear::from_f32 and run through its forward (the reference
+        keeps them f32, int8_mamba.rs:33-34)"""
+        if lib().orc_mamba_set_int8_xdt(self.h):
+            raise RuntimeError("orc_mamba_set_int8_xdt failed")
+
+    def reset(self):
+        lib().orc_mamba_reset(self.h)
 
     def prefill(self, ids):
         ids = np.ascontiguousarray(ids, np.uint32)

@@ -1416,6 +1416,7 @@ typedef struct {
   float *x_proj, *dt_proj, *dt_bias;     /* [dt_rank+2*d_state, d_inner], [d_inner, dt_rank], [d_inner] */
   float *a_log, *d_param, *norm_w;       /* [d_inner, d_state], [d_inner], [d_model] */
   float *conv_state, *ssm_state;         /* [d_inner, d_conv], [d_inner, d_state] */
+  orc_qlin x_i8, dt_i8;                  /* INT8 x_proj / dt_proj (int8_xdt variant) */
 } orc_mblock;
 
 struct orc_mamba {
@@ -1423,6 +1424,7 @@ struct orc_mamba {
   float *embed, *final_norm;
   orc_qlin lm_dummy;
   orc_mblock *blk;
+  int int8_xdt; /* x_proj and dt_proj as QuantizedLinear */
 };
 
 orc_mamba *orc_mamba_create(const orc_mamba_cfg *cfg) {
@@ -1440,6 +1442,7 @@ void orc_mamba_destroy(orc_mamba *m) {
     free(b->in_proj.w); free(b->in_proj.s); free(b->out_proj.w); free(b->out_proj.s);
     free(b->conv_w); free(b->conv_b); free(b->x_proj); free(b->dt_proj); free(b->dt_bias);
     free(b->a_log); free(b->d_param); free(b->norm_w); free(b->conv_state); free(b->ssm_state);
+    free(b->x_i8.w); free(b->x_i8.s); free(b->dt_i8.w); free(b->dt_i8.s);
   }
   free(m->blk);
   free(m->embed);
@@ -1500,6 +1503,28 @@ int orc_mamba_init_synthetic_std(orc_mamba *m, uint64_t seed_base, float std) {
   return bad ? ORC_ERR_OUT_OF_MEMORY : ORC_OK;
 }
 
+/* The config-5 variant: x_proj and dt_proj become W8A8 QuantizedLinears of
+   their f32 weights, built with the same from_f32 as in_proj/out_proj
+   (int8_mamba.rs:136-171 -> int8_linear.rs:35-70), and run through the same
+   forward (int8_linear.rs:87-117: A1 row quantizer, exact i32 products,
+   (f32(acc)*sx)*sw).  dt_proj's input is the dt_rank head of x_proj's
+   output, as in ssm_forward_step (int8_mamba.rs:59-75).  The reference keeps
+   these two projections f32 (:33-34); this is the variant the benchmark
+   config names.  Call after init; idempotent. */
+int orc_mamba_set_int8_xdt(orc_mamba *m) {
+  const orc_mamba_cfg *c = &m->c;
+  size_t di = c->d_inner, ds = c->d_state, dr = c->dt_rank;
+  if (m->int8_xdt) return ORC_OK;
+  for (size_t l = 0; l < c->n_layers; l++) {
+    orc_mblock *b = &m->blk[l];
+    if (!b->x_proj || !b->dt_proj) return ORC_ERR_INVALID_ARG;
+    if (qlin_from_f32(&b->x_i8, b->x_proj, dr + 2 * ds, di)) return ORC_ERR_OUT_OF_MEMORY;
+    if (qlin_from_f32(&b->dt_i8, b->dt_proj, di, dr)) return ORC_ERR_OUT_OF_MEMORY;
+  }
+  m->int8_xdt = 1;
+  return ORC_OK;
+}
+
 void orc_mamba_reset(orc_mamba *m) {
   for (size_t l = 0; l < m->c.n_layers; l++) {
     memset(m->blk[l].conv_state, 0, m->c.d_inner * m->c.d_conv * 4);
@@ -1534,17 +1559,24 @@ static void mamba_block_one(const orc_mamba *m, orc_mblock *b, const float *hid,
   float *xc = (float *)malloc(di * 4), *xp = (float *)malloc((dr + 2 * ds) * 4);
   float *dtp = (float *)malloc(di * 4), *delta = (float *)malloc(di * 4);
   float *y = (float *)malloc(di * 4), *g = (float *)malloc(di * 4), *o = (float *)malloc(dm * 4);
-  int8_t *xq = (int8_t *)malloc(2 * di > dm ? 2 * di : dm);
+  size_t xqn = 2 * di > dm ? 2 * di : dm;
+  int8_t *xq = (int8_t *)malloc(xqn > dr + 2 * ds ? xqn : dr + 2 * ds);
   float sx;
   orc_rmsnorm_seq(hid, b->norm_w, c->eps, dm, normed);
   qlin_forward(&b->in_proj, normed, 1, proj, xq, &sx);
   orc_conv1d_step(proj, b->conv_w, b->conv_b, b->conv_state, di, dc, xc);
   for (size_t i = 0; i < di; i++) xc[i] = orc_silu(xc[i]);
-  /* ssm_forward_step :59-75: x_proj and dt_proj are f32 matmul_t */
-  memset(xp, 0, (dr + 2 * ds) * 4);
-  orc_sgemm(1, dr + 2 * ds, di, xc, di, 0, b->x_proj, di, 1, xp, dr + 2 * ds);
-  memset(dtp, 0, di * 4);
-  orc_sgemm(1, di, dr, xp, dr, 0, b->dt_proj, dr, 1, dtp, di);
+  if (m->int8_xdt) {
+    /* config-5 variant: both projections through QuantizedLinear::forward */
+    qlin_forward(&b->x_i8, xc, 1, xp, xq, &sx);
+    qlin_forward(&b->dt_i8, xp, 1, dtp, xq, &sx);
+  } else {
+    /* ssm_forward_step :59-75: x_proj and dt_proj are f32 matmul_t */
+    memset(xp, 0, (dr + 2 * ds) * 4);
+    orc_sgemm(1, dr + 2 * ds, di, xc, di, 0, b->x_proj, di, 1, xp, dr + 2 * ds);
+    memset(dtp, 0, di * 4);
+    orc_sgemm(1, di, dr, xp, dr, 0, b->dt_proj, dr, 1, dtp, di);
+  }
   for (size_t i = 0; i < di; i++) delta[i] = orc_softplus(dtp[i] + b->dt_bias[i]);
   orc_selective_scan_step(xc, delta, b->a_log, xp + dr, xp + dr + ds, b->d_param, b->ssm_state, y,
                           di, ds);

@@ -162,6 +162,8 @@ void orc_mamba_destroy(orc_mamba *m);
 /* synthetic weights (seed spec documented in oracle.c) */
 int orc_mamba_init_synthetic(orc_mamba *m, uint64_t seed_base);
 int orc_mamba_init_synthetic_std(orc_mamba *m, uint64_t seed_base, float std);
+/* BASELINE config 5's variant: x_proj and dt_proj as W8A8 QuantizedLinears */
+int orc_mamba_set_int8_xdt(orc_mamba *m);
 void orc_mamba_reset(orc_mamba *m);
 int orc_mamba_prefill(orc_mamba *m, const uint32_t *ids, size_t n, float *logits);
 int orc_mamba_decode_one(orc_mamba *m, uint32_t token, float *logits);

@@ -108,12 +108,17 @@ uint16_t f32_to_f16_trunc(float v);
 }  // namespace syn
 
 // ---------------------------------------------------------------- device math
-// Fixed point for order-free float sums (split-K atomics): value * 2^32 in
-// an int64, saturated far beyond any activation; sums of these are exact in
-// any order, so split-K workgroups can add them with integer atomics.
+// Fixed point for order-free float sums (the fused f32 decoders' split-K
+// atomics): value * 2^32 in an int64; sums of these are exact in any order,
+// so split-K workgroups can add them with integer atomics.  A value is
+// saturated at +-2^27 (2^59 fixed), far beyond any activation, so that up to
+// 16 saturated addends cannot wrap the int64; NaN saturates to +2^27 (the
+// fused decoders turn a non-finite activation into a saturated finite one
+// instead of propagating it).
 __device__ __forceinline__ long long kqf_fix(float v) {
   const double d = (double)v * 4294967296.0;
-  return __double2ll_rn(fmin(fmax(d, -4.0e18), 4.0e18));
+  constexpr double lim = 576460752303423488.0;  // 2^59
+  return d != d ? (long long)lim : __double2ll_rn(fmin(fmax(d, -lim), lim));
 }
 __device__ __forceinline__ float kqf_unfix(long long a) {
   return (float)((double)a * 2.3283064365386963e-10);

@@ -332,12 +332,12 @@ __device__ __forceinline__ void kq_asums(const float *__restrict__ x, int ldx, i
 
 // grid (panels, ksplit); lane = output row; blocks [b0, b1) of this slice.
 // A K split finishes in the same launch (split_k.hpp; skacc holds M rows of
-// N64 accumulators, skcnt a counter per panel).
+// ksplit slices of N64 slots, skcnt a counter per panel).
 template <int FMT, int M>
 __global__ void __launch_bounds__(1024)
     k_gemv_kq(const u32x4 *__restrict__ W, const uint16_t *__restrict__ Wd,
               const float *__restrict__ x, int ldx, float *__restrict__ y, int ldy,
-              unsigned long long *__restrict__ skacc, int *__restrict__ skcnt, int N, int B,
+              unsigned *__restrict__ skacc, int *__restrict__ skcnt, int N, int B,
               int bs) {
   __shared__ int s_last;
   constexpr int NP = FMT == SYN_HIP_FMT_Q8_0 ? 2 : FMT == SYN_HIP_FMT_Q4_K ? 9 : 13;
@@ -452,17 +452,18 @@ __global__ void __launch_bounds__(1024)
   __syncthreads();
   const int N64 = gridDim.x * 64;
   if (gridDim.y > 1) {
-    unsigned long long seen = 0;
+    unsigned seen = 0;
+    const int S = gridDim.y;
     for (int t = threadIdx.x; t < M * 64; t += blockDim.x) {
       const int m = t >> 6, r = t & 63;
       float s = 0.0f;
       for (int w = 0; w < nw; w++) s += red[(w * M + m) * 64 + r];
-      seen |= sk_add(skacc + (size_t)m * N64 + panel * 64 + r, s);
+      seen |= sk_put(skacc + ((size_t)m * S + blockIdx.y) * N64 + panel * 64 + r, s);
     }
-    if (!sk_arrive(seen, skcnt + panel, gridDim.y, &s_last)) return;
+    if (!sk_arrive(seen, skcnt + panel, S, &s_last)) return;
     for (int t = threadIdx.x; t < M * 64; t += blockDim.x) {
       const int m = t >> 6, r = t & 63, row = panel * 64 + r;
-      const float v = sk_take(skacc + (size_t)m * N64 + row);
+      const float v = sk_sum(skacc + (size_t)m * S * N64 + row, N64, S);
       if (row < N) y[(size_t)m * ldy + row] = v;
     }
     sk_reset(skcnt + panel);
@@ -484,7 +485,7 @@ template <int FMT, int NW, int U>
 __global__ void __launch_bounds__(NW * 64)
     k_gemv_kqh(const u32x4 *__restrict__ W, const uint16_t *__restrict__ Wd,
                const float *__restrict__ x, float *__restrict__ y,
-               unsigned long long *__restrict__ skacc, int *__restrict__ skcnt, int N, int B,
+               unsigned *__restrict__ skacc, int *__restrict__ skcnt, int N, int B,
                int bs) {
   __shared__ int s_last;
   constexpr int NT = NW * 64;
@@ -568,7 +569,8 @@ __global__ void __launch_bounds__(NW * 64)
 #pragma unroll
       for (int w = 0; w < NW; w++) v += red[w * 64 + tid];
     }
-    if (sk_fixed_last(v, skacc + panel * 64, skcnt + panel, gridDim.y, &tot, &s_last) &&
+    if (sk_slots_last(v, skacc + panel * 64, (size_t)gridDim.x * 64, blockIdx.y, skcnt + panel,
+                      gridDim.y, &tot, &s_last) &&
         tid < 64 && panel * 64 + tid < N)
       y[panel * 64 + tid] = tot;
     return;
@@ -584,20 +586,20 @@ __global__ void __launch_bounds__(NW * 64)
 
 template <int FMT, int M>
 static void launch_kq(const GemvPlan &p, const void *W, const uint16_t *Wd, const float *x,
-                      int ldx, float *y, int ldy, const SplitKFixed &sk, int N, hipStream_t s) {
+                      int ldx, float *y, int ldy, const SplitKSlots &sk, int N, hipStream_t s) {
   constexpr int BE = FMT == SYN_HIP_FMT_Q8_0 ? 32 : 256;
   constexpr int GRP = FMT == SYN_HIP_FMT_Q4_K ? 32 : 16;
   const int waves = std::min(p.waves, M >= 4 ? 8 : 16);
   const size_t as = FMT == SYN_HIP_FMT_Q8_0 ? 0 : (size_t)M * p.cs * (BE / GRP);
   const size_t shm = (as + (size_t)waves * M * 64) * sizeof(float);
   hipLaunchKernelGGL((k_gemv_kq<FMT, M>), dim3(p.panels, p.ksplit), dim3(64 * waves), shm, s,
-                     (const u32x4 *)W, Wd, x, ldx, y, ldy, sk.acc.as<unsigned long long>(),
-                     sk.cnt.as<int>(), N, p.chunks, p.cs);
+                     (const u32x4 *)W, Wd, x, ldx, y, ldy, sk.slots(),
+                     sk.counters(), N, p.chunks, p.cs);
 }
 
 template <int FMT>
 static void launch_kq_m(int m, const GemvPlan &p, const void *W, const uint16_t *Wd,
-                        const float *x, int ldx, float *y, int ldy, const SplitKFixed &sk, int N,
+                        const float *x, int ldx, float *y, int ldy, const SplitKSlots &sk, int N,
                         hipStream_t s) {
   switch (m) {
     case 1: launch_kq<FMT, 1>(p, W, Wd, x, ldx, y, ldy, sk, N, s); break;
@@ -612,10 +614,10 @@ static void launch_kq_m(int m, const GemvPlan &p, const void *W, const uint16_t 
 // (more workgroups per CU); shorter Q4_K slices 8 waves of one.
 template <int FMT>
 static syn_status_t launch_kqh(const GemvPlan &p, const u32x4 *W, const uint16_t *Wd,
-                               const float *x, float *y, const SplitKFixed &sk, int N, size_t shm,
+                               const float *x, float *y, const SplitKSlots &sk, int N, size_t shm,
                                hipStream_t s) {
-  unsigned long long *ska = sk.acc.as<unsigned long long>();
-  int *skc = sk.cnt.as<int>();
+  unsigned *ska = sk.slots();
+  int *skc = sk.counters();
   if (FMT == SYN_HIP_FMT_Q6_K || p.cs >= 8)
     hipLaunchKernelGGL((k_gemv_kqh<FMT, 4, 2>), dim3(p.panels, p.ksplit), dim3(256), shm, s, W,
                        Wd, x, y, ska, skc, N, p.chunks, p.cs);
@@ -631,7 +633,7 @@ syn_status_t QLinearKQ::gemv(size_t m, const float *d_x, size_t ldx, float *d_y,
   if (m > 8) return gemm(m, d_x, ldx, d_y, ldy, s);
   const GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
   // one launch per block of rows: a K split finishes in place (split_k.hpp)
-  if (p.ksplit > 1) SYN_TRY(sk.ensure(p.panels, 4));
+  if (p.ksplit > 1) SYN_TRY(sk.ensure(p.panels, 4, p.ksplit));
   const uint16_t *Wd = wd.as<uint16_t>();
   for (size_t m0 = 0; m0 < m; m0 += 4) {
     const int mb = (int)std::min<size_t>(4, m - m0);
@@ -657,12 +659,12 @@ syn_status_t QLinearKQ::gemv(size_t m, const float *d_x, size_t ldx, float *d_y,
 }
 
 syn_status_t QLinearKQ::prepare(size_t max_m) {
-  if (max_m > 8 && xh_elems < max_m * k) {
-    SYN_TRY(xh.alloc(max_m * k * 2));
-    xh_elems = max_m * k;
+  if (max_m > 8 && xh_bytes < f16_rows_bytes(max_m, k)) {
+    SYN_TRY(xh.alloc(f16_rows_bytes(max_m, k)));
+    xh_bytes = f16_rows_bytes(max_m, k);
   }
   const GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
-  return p.ksplit > 1 ? sk.ensure(p.panels, 4) : SYN_OK;
+  return p.ksplit > 1 ? sk.ensure(p.panels, 4, p.ksplit) : SYN_OK;
 }
 
 }  // namespace syn

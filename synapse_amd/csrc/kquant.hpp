@@ -15,6 +15,10 @@ void kq_dequant(int fmt, const uint8_t *bytes, size_t nblocks, float *out);
 // the reference's f16 -> f32 converter (converter.rs:12-40, subnormals halve)
 float f16_to_f32_reference(uint16_t h);
 
+// bytes of a GEMM's f16 activation rows plus their per-row scales
+// (kquant_gemm.hip), m rows of k elements
+size_t f16_rows_bytes(size_t m, size_t k);
+
 struct QLinearKQ {
   int fmt = 0;
   size_t n = 0, k = 0;
@@ -23,8 +27,8 @@ struct QLinearKQ {
   DevBuf wq;       // [P][blocks][planes][64][16]
   DevBuf wd;       // [P][blocks][64] f16 d (Q8_0, Q6_K)
   DevBuf xh;  // f16 activations for the MFMA GEMM
-  size_t xh_elems = 0;
-  SplitKFixed sk;  // gemv()'s one-launch K split at one row (split_k.hpp)
+  size_t xh_bytes = 0;  // its size (f16_rows_bytes)
+  SplitKSlots sk;  // gemv()'s one-launch K split at one row (split_k.hpp)
   // Q8_0: every block scale (as the reference converts it) is an f16 value,
   // so the GEMM may multiply in f16 (set at upload)
   bool q8_scales_f16_exact = true;

@@ -27,25 +27,52 @@ typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // x f32 [M, ldx] -> xh f16 [M, ldh], columns K..ldh-1 zero (K a multiple of
-// 8, ldh of 64, ldx of 4).  perm8: each 8-element chunk is stored in the k
-// order 0,2,4,6,1,3,5,7 of the Q4_0 direct-load kernel's fragments (k_gemm_kqr).
-__global__ void k_f32_to_f16(const float *__restrict__ x, int ldx, _Float16 *__restrict__ xh,
-                             int ldh, int M, int K, int perm8) {
-  const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  const int per_row = ldh / 8;
-  if (i >= M * per_row) return;
-  const int m = i / per_row, c = (i - m * per_row) * 8;
-  float4 a = float4{0.0f, 0.0f, 0.0f, 0.0f}, b = a;
-  if (c < K) {
-    a = *reinterpret_cast<const float4 *>(x + (size_t)m * ldx + c);
-    b = *reinterpret_cast<const float4 *>(x + (size_t)m * ldx + c + 4);
+// 8, ldh of 64, ldx of 4), one workgroup per row.  Each row is scaled by a
+// power of two that puts its largest magnitude in [2^14, 2^15) before the
+// f16 rounding, and rowmul[m] holds the inverse power for the GEMM epilogue:
+// rows far above f16's range (which would round to inf) or far below it
+// (subnormal f16, lost precision) keep f16's full relative precision, and
+// both scalings are exact in f32.  A row whose maximum is zero or not finite
+// is not scaled.  perm8: each 8-element chunk is stored in the k order
+// 0,2,4,6,1,3,5,7 of the Q4_0 direct-load kernel's fragments (k_gemm_kqr).
+__global__ void __launch_bounds__(256)
+    k_f32_to_f16(const float *__restrict__ x, int ldx, _Float16 *__restrict__ xh, int ldh,
+                 float *__restrict__ rowmul, int K, int perm8) {
+  __shared__ float red[4];
+  const int m = blockIdx.x, tid = threadIdx.x;
+  const float *xr = x + (size_t)m * ldx;
+  float mx = 0.0f;
+  for (int c = tid * 4; c < K; c += 1024) {
+    const float4 a = *reinterpret_cast<const float4 *>(xr + c);
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a.x), fabsf(a.y)), fmaxf(fabsf(a.z), fabsf(a.w))));
   }
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float up = 1.0f, down = 1.0f;  // x * up rounds to f16; y * down undoes it
+  if (mx > 0.0f && mx <= 3.4028235e38f) {
+    int e;
+    (void)frexpf(mx, &e);  // mx = f * 2^e, f in [0.5, 1)
+    up = ldexpf(1.0f, 15 - e);
+    down = ldexpf(1.0f, e - 15);
+  }
+  if (tid == 0) rowmul[m] = down;
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-  const h8 o = perm8 ? h8{(_Float16)a.x, (_Float16)a.z, (_Float16)b.x, (_Float16)b.z,
-                          (_Float16)a.y, (_Float16)a.w, (_Float16)b.y, (_Float16)b.w}
-                     : h8{(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
-                          (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
-  *reinterpret_cast<h8 *>(xh + (size_t)m * ldh + c) = o;
+  for (int c = tid * 8; c < ldh; c += 2048) {
+    float4 a = float4{0.0f, 0.0f, 0.0f, 0.0f}, b = a;
+    if (c < K) {
+      a = *reinterpret_cast<const float4 *>(xr + c);
+      b = *reinterpret_cast<const float4 *>(xr + c + 4);
+    }
+    a.x *= up; a.y *= up; a.z *= up; a.w *= up;
+    b.x *= up; b.y *= up; b.z *= up; b.w *= up;
+    const h8 o = perm8 ? h8{(_Float16)a.x, (_Float16)a.z, (_Float16)b.x, (_Float16)b.z,
+                            (_Float16)a.y, (_Float16)a.w, (_Float16)b.y, (_Float16)b.w}
+                       : h8{(_Float16)a.x, (_Float16)a.y, (_Float16)a.z, (_Float16)a.w,
+                            (_Float16)b.x, (_Float16)b.y, (_Float16)b.z, (_Float16)b.w};
+    *reinterpret_cast<h8 *>(xh + (size_t)m * ldh + c) = o;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -232,7 +259,8 @@ template <int FMT, bool EXACT, int TM>
 __global__ void __launch_bounds__(pg_threads<TM>())
     k_gemm_kq2(const _Float16 *__restrict__ Xh, int ldh, int M, int K,
                const u32x4 *__restrict__ W, const uint16_t *__restrict__ Wd, int N, int B,
-               float *__restrict__ Y, int ldy, int steps_per_split) {
+               float *__restrict__ Y, int ldy, const float *__restrict__ rowmul,
+               int steps_per_split) {
   extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   constexpr int NC = TM / 32, AI = TM / 32, PG_STAGE = pg_stage<TM>();
@@ -369,8 +397,9 @@ __global__ void __launch_bounds__(pg_threads<TM>())
       for (int r = 0; r < 16; r++) {
         const int m = m0 + wm + mt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
         if (m < M && n < N) {
-          if (atomic) atomicAdd(&Y[(size_t)m * ldy + n], acc[mt][nt][r]);
-          else Y[(size_t)m * ldy + n] = acc[mt][nt][r];
+          const float v = acc[mt][nt][r] * rowmul[m];
+          if (atomic) atomicAdd(&Y[(size_t)m * ldy + n], v);
+          else Y[(size_t)m * ldy + n] = v;
         }
       }
     }
@@ -488,7 +517,8 @@ template <int FMT, bool EXACT>
 __global__ void __launch_bounds__(256)
     k_gemm_kq5(const _Float16 *__restrict__ Xh, int ldh, int M, int K,
                const u32x4 *__restrict__ W, const uint16_t *__restrict__ Wd, int N, int B,
-               float *__restrict__ Y, int ldy, int steps_per_split) {
+               float *__restrict__ Y, int ldy, const float *__restrict__ rowmul,
+               int steps_per_split) {
   extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int n0 = blockIdx.x * PG3N, m0 = blockIdx.y * PG3M;
@@ -596,8 +626,9 @@ __global__ void __launch_bounds__(256)
       for (int r = 0; r < 16; r++) {
         const int m = m0 + wm + mt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
         if (m < M && n < N) {
-          if (atomic) atomicAdd(&Y[(size_t)m * ldy + n], acc[mt][nt][r]);
-          else Y[(size_t)m * ldy + n] = acc[mt][nt][r];
+          const float v = acc[mt][nt][r] * rowmul[m];
+          if (atomic) atomicAdd(&Y[(size_t)m * ldy + n], v);
+          else Y[(size_t)m * ldy + n] = v;
         }
       }
     }
@@ -656,7 +687,8 @@ __device__ __forceinline__ f16x8 kr_decode(const u32x4 &q, int g, f16x2 d) {
 __global__ void __launch_bounds__(256)
     k_gemm_kqr(const _Float16 *__restrict__ Xh, int ldh, int M, int K,
                const u32x4 *__restrict__ W, const uint16_t *__restrict__ Wd, int N, int B,
-               float *__restrict__ Y, int ldy, int steps_per_split) {
+               float *__restrict__ Y, int ldy, const float *__restrict__ rowmul,
+               int steps_per_split) {
   extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
   constexpr int WCH = KR_WCH, STAGE = KR_STAGE_BYTES;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -797,30 +829,38 @@ __global__ void __launch_bounds__(256)
       for (int r = 0; r < 16; r++) {
         const int m = m0 + wr * 128 + mt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
         if (m < M && n < N) {
-          if (atomic) atomicAdd(&Y[(size_t)m * ldy + n], acc[mt][nt][r]);
-          else Y[(size_t)m * ldy + n] = acc[mt][nt][r];
+          const float v = acc[mt][nt][r] * rowmul[m];
+          if (atomic) atomicAdd(&Y[(size_t)m * ldy + n], v);
+          else Y[(size_t)m * ldy + n] = v;
         }
       }
     }
 }
 
 // f32 activation rows -> zero-padded f16 rows of ldh = round_up(k, PGK)
-// halfs in xh (grown on demand), in the k_gemm_kqr Q4_0 chunk order if perm8
+// halfs in xh (grown on demand; xh_bytes its size), each row scaled by a
+// power of two whose inverse lands in *rowmul (m floats after the rows), in
+// the k_gemm_kqr Q4_0 chunk order if perm8
+size_t f16_rows_bytes(size_t m, size_t k) {
+  return round_up(m * round_up(k, PGK) * 2, 256) + m * sizeof(float);
+}
 static syn_status_t to_f16_rows(size_t m, size_t k, const float *d_x, size_t ldx, DevBuf &xh,
-                                size_t &xh_elems, bool perm8, hipStream_t s) {
+                                size_t &xh_bytes, bool perm8, float **rowmul, hipStream_t s) {
   if (ldx % 4 || k % 8) {
     set_error("GEMM activation stride must be a multiple of 4 floats and K of 8");
     return SYN_ERR_SHAPE_MISMATCH;
   }
+  if (m > 0x7fffffffu) return SYN_ERR_INVALID_ARG;
   const size_t ldh = round_up(k, PGK);  // zero-padded to whole K steps
-  if (xh_elems < m * ldh) {
+  const size_t need = f16_rows_bytes(m, k);
+  if (xh_bytes < need) {
     SYN_HIP(hipDeviceSynchronize());
-    SYN_TRY(xh.alloc(m * ldh * 2));
-    xh_elems = m * ldh;
+    SYN_TRY(xh.alloc(need));
+    xh_bytes = need;
   }
-  const int total = (int)(m * (ldh / 8));
-  hipLaunchKernelGGL(k_f32_to_f16, dim3(cdiv(total, 256)), dim3(256), 0, s, d_x, (int)ldx,
-                     xh.as<_Float16>(), (int)ldh, (int)m, (int)k, perm8 ? 1 : 0);
+  *rowmul = reinterpret_cast<float *>(xh.as<unsigned char>() + round_up(m * ldh * 2, 256));
+  hipLaunchKernelGGL(k_f32_to_f16, dim3((unsigned)m), dim3(256), 0, s, d_x, (int)ldx,
+                     xh.as<_Float16>(), (int)ldh, *rowmul, (int)k, perm8 ? 1 : 0);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
 }
@@ -840,14 +880,15 @@ template <class Kern>
 static syn_status_t launch_gemm(Kern kern, bool &attr_set, dim3 grid, unsigned threads, size_t shm,
                                 const _Float16 *X, size_t ldh, size_t m, size_t k,
                                 const u32x4 *W, const uint16_t *Wd, size_t n, int blocks,
-                                float *d_y, size_t ldy, int per, hipStream_t s) {
+                                float *d_y, size_t ldy, const float *rowmul, int per,
+                                hipStream_t s) {
   if (!attr_set) {  // more than the default 64 KiB of dynamic LDS
     SYN_HIP(hipFuncSetAttribute((const void *)kern, hipFuncAttributeMaxDynamicSharedMemorySize,
                                 (int)shm));
     attr_set = true;
   }
   hipLaunchKernelGGL(kern, grid, dim3(threads), shm, s, X, (int)ldh, (int)m, (int)k, W, Wd,
-                     (int)n, blocks, d_y, (int)ldy, per);
+                     (int)n, blocks, d_y, (int)ldy, rowmul, per);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
 }
@@ -857,7 +898,7 @@ static syn_status_t launch_gemm(Kern kern, bool &attr_set, dim3 grid, unsigned t
 // exact: the weights decode with f16 products (see pg_decode_w)
 static syn_status_t kq_gemm_f16(int fmt, bool exact, const u32x4 *W, const uint16_t *Wd,
                                 int blocks, size_t n, size_t k, const float *d_x, size_t ldx,
-                                DevBuf &xh, size_t &xh_elems, size_t m, float *d_y, size_t ldy,
+                                DevBuf &xh, size_t &xh_bytes, size_t m, float *d_y, size_t ldy,
                                 hipStream_t s) {
   const size_t ldh = round_up(k, PGK);
   const int steps = (int)cdiv(k, PGK);
@@ -869,14 +910,17 @@ static syn_status_t kq_gemm_f16(int fmt, bool exact, const u32x4 *W, const uint1
   // two tie, and k_gemm_kq2 leads on split-K grids)
   const int tiles256 = (int)(cdiv(n, PG3N) * cdiv(m, PG3M));
   if (fmt == SYN_HIP_FMT_Q4_0 && tiles256 >= 192 && m * ldh < (1u << 31)) {
-    SYN_TRY(to_f16_rows(m, k, d_x, ldx, xh, xh_elems, true, s));
+    float *rowmul = nullptr;
+    SYN_TRY(to_f16_rows(m, k, d_x, ldx, xh, xh_bytes, true, &rowmul, s));
     const int tiles_n = (int)cdiv(n, PG3N), tiles_m = (int)cdiv(m, PG3M);
     const dim3 grid((unsigned)tiles_n, (unsigned)tiles_m, 1);
     const int per = steps;
     return launch_gemm(k_gemm_kqr, attr[10], grid, 256, (size_t)KR_NS * KR_STAGE_BYTES,
-                       xh.as<_Float16>(), ldh, m, k, W, Wd, n, blocks, d_y, ldy, per, s);
+                       xh.as<_Float16>(), ldh, m, k, W, Wd, n, blocks, d_y, ldy, rowmul, per,
+                       s);
   }
-  SYN_TRY(to_f16_rows(m, k, d_x, ldx, xh, xh_elems, false, s));
+  float *rowmul = nullptr;
+  SYN_TRY(to_f16_rows(m, k, d_x, ldx, xh, xh_bytes, false, &rowmul, s));
   const _Float16 *X = xh.as<_Float16>();
   // Enough 256 x 256 tiles for three quarters of the CUs: the four-wave
   // kernel, one K pass per tile.  Else 256 x 128 tiles (twice as many) when
@@ -907,7 +951,7 @@ static syn_status_t kq_gemm_f16(int fmt, bool exact, const u32x4 *W, const uint1
   const unsigned threads = big ? 256 : mid ? pg_threads<256>() : pg_threads<128>();
   auto launch = [&](auto kern, bool &attr_set) -> syn_status_t {
     return launch_gemm(kern, attr_set, grid, threads, shm, X, ldh, m, k, W, Wd, n, blocks, d_y,
-                       ldy, per, s);
+                       ldy, rowmul, per, s);
   };
   if (big) {
     if (fmt == SYN_HIP_FMT_Q8_0 && exact) return launch(k_gemm_kq5<SYN_HIP_FMT_Q8_0, true>, attr[0]);
@@ -932,7 +976,7 @@ syn_status_t QLinearKQ::gemm(size_t m, const float *d_x, size_t ldx, float *d_y,
                              hipStream_t s) {
   const bool exact = fmt != SYN_HIP_FMT_Q8_0 || q8_scales_f16_exact;
   return kq_gemm_f16(fmt, exact, wq.as<u32x4>(), wd.as<uint16_t>(), blocks, n, k, d_x, ldx, xh,
-                     xh_elems, m, d_y, ldy, s);
+                     xh_bytes, m, d_y, ldy, s);
 }
 
 // Q4_0 rows on the same GEMM (its nibble planes sit in the Q8_0 plane layout
@@ -945,7 +989,7 @@ syn_status_t QLinearQ4_0::gemm(size_t m, const float *d_x, size_t ldx, float *d_
     return SYN_ERR_INVALID_ARG;
   }
   return kq_gemm_f16(SYN_HIP_FMT_Q4_0, true, nib.as<u32x4>(), sc.as<uint16_t>(), blocks, n, k,
-                     d_x, ldx, xh, xh_elems, m, d_y, ldy, s);
+                     d_x, ldx, xh, xh_bytes, m, d_y, ldy, s);
 }
 
 }  // namespace syn

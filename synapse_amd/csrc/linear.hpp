@@ -106,8 +106,8 @@ struct QLinearQ4_0 {
   bool rs_f16_scales = false;
   bool has_subnormal_scale = false;  // some block scale is an f16 subnormal (set at upload)
   DevBuf xh;                         // f16 activations for the MFMA GEMM
-  size_t xh_elems = 0;
-  SplitKFixed sk;  // gemv()'s one-launch K split at one row (split_k.hpp)
+  size_t xh_bytes = 0;  // its size (f16_rows_bytes)
+  SplitKSlots sk;  // gemv()'s one-launch K split at one row (split_k.hpp)
   syn_status_t upload_packed(const uint8_t *packed, size_t n_, size_t k_);
   syn_status_t from_f32(const float *w_nk, size_t n_, size_t k_);
   // allocate the split-K partials of GEMV batches up to max_m rows (so that

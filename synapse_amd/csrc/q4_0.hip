@@ -57,12 +57,12 @@ __device__ __forceinline__ float q4_scale(uint32_t h, float sub) {
 // HBM latency overlaps them.  The dot products read the activations with
 // wave-uniform addresses (scalar loads).
 // A K split finishes in the same launch (split_k.hpp; skacc holds M rows
-// of N64 accumulators, skcnt a counter per panel).
+// of ksplit slices of N64 slots, skcnt a counter per panel).
 template <int M, int U>
 __global__ void __launch_bounds__(1024)
     k_gemv_q4_0(const u32x4 *__restrict__ nib, const uint16_t *__restrict__ sc,
                 const float *__restrict__ x, int ldx, float *__restrict__ y, int ldy,
-                unsigned long long *__restrict__ skacc, int *__restrict__ skcnt, int N, int B,
+                unsigned *__restrict__ skacc, int *__restrict__ skcnt, int N, int B,
                 int bs, float sub) {
   extern __shared__ __align__(16) float smem[];
   __shared__ int s_last;
@@ -149,17 +149,18 @@ __global__ void __launch_bounds__(1024)
   __syncthreads();
   const int N64 = gridDim.x * 64;
   if (gridDim.y > 1) {
-    unsigned long long seen = 0;
+    unsigned seen = 0;
+    const int S = gridDim.y;
     for (int t = tid; t < M * 64; t += NT) {
       const int m = t >> 6, r = t & 63;
       float s = 0.0f;
       for (int w = 0; w < nw; w++) s += red[(w * M + m) * 64 + r];
-      seen |= sk_add(skacc + (size_t)m * N64 + panel * 64 + r, s);
+      seen |= sk_put(skacc + ((size_t)m * S + blockIdx.y) * N64 + panel * 64 + r, s);
     }
-    if (!sk_arrive(seen, skcnt + panel, gridDim.y, &s_last)) return;
+    if (!sk_arrive(seen, skcnt + panel, S, &s_last)) return;
     for (int t = tid; t < M * 64; t += NT) {
       const int m = t >> 6, r = t & 63, row = panel * 64 + r;
-      const float v = sk_take(skacc + (size_t)m * N64 + row);
+      const float v = sk_sum(skacc + (size_t)m * S * N64 + row, N64, S);
       if (row < N) y[(size_t)m * ldy + row] = v;
     }
     sk_reset(skcnt + panel);
@@ -189,12 +190,13 @@ __device__ __forceinline__ h2_t as_h2(uint32_t v) { return __builtin_bit_cast(h2
 
 // A K split either writes f32 partials (part, for k_q4_reduce or the
 // consumer's PartRows) or, with skacc set, finishes in the same launch
-// (split_k.hpp: fixed-point atomics, the panel's last slice writes y).
+// (split_k.hpp: per-slice slots, the panel's last slice adds them in slice
+// order and writes y).
 template <int U>
 __global__ void __launch_bounds__(512)
     k_gemv_q4_0h(const u32x4 *__restrict__ nib, const uint16_t *__restrict__ sc,
                  const float *__restrict__ x, float *__restrict__ y, float *__restrict__ part,
-                 long long *__restrict__ skacc, int *__restrict__ skcnt, int N, int B, int bs,
+                 unsigned *__restrict__ skacc, int *__restrict__ skcnt, int N, int B, int bs,
                  float sub) {
   extern __shared__ __align__(16) float hsm[];
   __shared__ int s_last;
@@ -287,8 +289,8 @@ __global__ void __launch_bounds__(512)
 #pragma unroll
       for (int w = 0; w < NW; w++) v += red[w * 64 + tid];
     }
-    if (sk_fixed_last(v, reinterpret_cast<unsigned long long *>(skacc) + panel * 64,
-                      skcnt + panel, gridDim.y, &tot, &s_last) &&
+    if (sk_slots_last(v, skacc + panel * 64, (size_t)gridDim.x * 64, blockIdx.y, skcnt + panel,
+                      gridDim.y, &tot, &s_last) &&
         tid < 64 && panel * 64 + tid < N)
       y[panel * 64 + tid] = tot;
     return;
@@ -310,13 +312,13 @@ __global__ void __launch_bounds__(512)
 // blocks (four workgroups per CU stream the matrix), else 4 with up to 16
 template <int M>
 static void launch_q4_m(const GemvPlan &p, const u32x4 *nib, const uint16_t *sc, const float *x,
-                        int ldx, float *y, int ldy, const SplitKFixed &sk, int N, float sub,
+                        int ldx, float *y, int ldy, const SplitKSlots &sk, int N, float sub,
                         hipStream_t s) {
   const bool wide = p.cs >= 64;
   const int waves = wide ? 8 : std::min(p.waves, M >= 8 ? 8 : 16);
   const size_t shm = ((size_t)M * p.cs + (size_t)waves * M * 64) * sizeof(float);
-  unsigned long long *ska = sk.acc.as<unsigned long long>();
-  int *skc = sk.cnt.as<int>();
+  unsigned *ska = sk.slots();
+  int *skc = sk.counters();
   if (wide)
     hipLaunchKernelGGL((k_gemv_q4_0<M, 8>), dim3(p.panels, p.ksplit), dim3(64 * waves), shm, s,
                        nib, sc, x, ldx, y, ldy, ska, skc, N, p.chunks, p.cs, sub);
@@ -326,7 +328,7 @@ static void launch_q4_m(const GemvPlan &p, const u32x4 *nib, const uint16_t *sc,
 }
 
 typedef void (*q4_launcher)(const GemvPlan &, const u32x4 *, const uint16_t *, const float *,
-                            int, float *, int, const SplitKFixed &, int, float, hipStream_t);
+                            int, float *, int, const SplitKSlots &, int, float, hipStream_t);
 static const q4_launcher kQ4Launch[9] = {nullptr,        launch_q4_m<1>, launch_q4_m<2>,
                                          launch_q4_m<3>, launch_q4_m<4>, launch_q4_m<5>,
                                          launch_q4_m<6>, launch_q4_m<7>, launch_q4_m<8>};
@@ -339,7 +341,7 @@ syn_status_t QLinearQ4_0::gemv(size_t m, const float *d_x, size_t ldx, float *d_
   // "chunks" here are 32-element blocks; a K slice holds whole blocks.  One
   // launch per block of up to 8 rows: a K split finishes in place (split_k.hpp)
   const GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
-  if (p.ksplit > 1) SYN_TRY(sk.ensure(p.panels, 8));
+  if (p.ksplit > 1) SYN_TRY(sk.ensure(p.panels, 8, p.ksplit));
   for (size_t m0 = 0; m0 < m; m0 += 8) {
     const int mb = (int)std::min<size_t>(8, m - m0);
     const size_t shm_h = ((size_t)p.cs + 8 * 64) * 4;
@@ -347,7 +349,7 @@ syn_status_t QLinearQ4_0::gemv(size_t m, const float *d_x, size_t ldx, float *d_
       // two blocks per wave and round: measured best at the LLaMA shapes
       hipLaunchKernelGGL(k_gemv_q4_0h<2>, dim3(p.panels, p.ksplit), dim3(512), shm_h, s,
                          nib.as<u32x4>(), sc.as<uint16_t>(), d_x + m0 * ldx, d_y + m0 * ldy,
-                         nullptr, sk.acc.as<long long>(), sk.cnt.as<int>(), (int)n, p.chunks,
+                         nullptr, sk.slots(), sk.counters(), (int)n, p.chunks,
                          p.cs, sub);
     } else {
       kQ4Launch[mb](p, nib.as<u32x4>(), sc.as<uint16_t>(), d_x + m0 * ldx, (int)ldx,
@@ -381,7 +383,7 @@ syn_status_t QLinearQ4_0::gemv_parts(const float *d_x, float *d_y, PartRows *out
 
 syn_status_t QLinearQ4_0::prepare(size_t max_m) {
   const GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
-  if (p.ksplit > 1) SYN_TRY(sk.ensure(p.panels, 8));
+  if (p.ksplit > 1) SYN_TRY(sk.ensure(p.panels, 8, p.ksplit));
   const size_t need = (size_t)p.ksplit * std::min<size_t>(8, max_m) * (size_t)p.panels * 64;
   if (p.ksplit > 1 && part_elems < need) {
     part_elems = need;

@@ -166,3 +166,61 @@ def test_kquant_gemm_256x256_tiles(name):
     want = x[1792:1800].astype(np.float64) @ deq.T
     worst = max(_rel(got[1792 + i], want[i]) for i in range(8))
     assert worst <= TOL, worst
+
+
+# ---------------------------------------------------------------- output range
+# The one-launch K split adds per-slice f32 sums in slice order (split_k.hpp),
+# so rows keep f32's range: outputs ~1e-7 (activations x 1e-6), ~1e6
+# (activations x 1e6) and rows fed a few 1e4 outliers stay within the float
+# bar of the reference chain (qmatmul.zig:276-343 for Q4_0, matmul_t over
+# the dequantized weights for the GGUF formats).
+RANGE_SCALES = [("tiny", 1e-6), ("huge", 1e6), ("outliers", 1.0)]
+
+
+def _range_rows(m, k, seed, kind, scale):
+    x = O.normal(m * k, seed, 1.0).reshape(m, k) * np.float32(scale)
+    if kind == "outliers":
+        rng = np.random.default_rng(seed)
+        for i in range(m):
+            idx = rng.choice(k, 3, replace=False)
+            x[i, idx] = np.float32(1e4) * rng.choice([-1, 1], 3)
+    return np.ascontiguousarray(x, np.float32)
+
+
+# shapes whose GEMV runs as a K split (k large against n)
+RANGE_CASES = [("q8_0", 4096, 1024, 1), ("q8_0", 8192, 512, 3), ("q4_k", 3072, 1024, 1),
+               ("q4_k", 8192, 512, 2), ("q6_k", 8192, 1024, 1), ("q6_k", 8192, 300, 3)]
+
+
+@pytest.mark.parametrize("kind,scale", RANGE_SCALES, ids=[r[0] for r in RANGE_SCALES])
+@pytest.mark.parametrize("name,k,n,m", RANGE_CASES)
+def test_kquant_gemv_output_range(name, k, n, m, kind, scale):
+    print("case", name, k, n, m, kind, flush=True)
+    w = O.normal(n * k, k + n + 1, 0.02).reshape(n, k)
+    blocks = hip.kquant_encode(FMTS[name], w)
+    lin = hip.QLinear.gguf(FMTS[name], blocks, n, k)
+    x = _range_rows(m, k, 3 * m + k, kind, scale)
+    got = lin.forward(x)
+    deq = O.dequant(name, blocks, n * k).reshape(n, k)
+    want = O.matmul_t(x, deq)
+    assert np.isfinite(got).all()
+    for i in range(m):
+        assert _rel(got[i], want[i]) <= TOL, (i, _rel(got[i], want[i]))
+
+
+@pytest.mark.parametrize("kind,scale", RANGE_SCALES, ids=[r[0] for r in RANGE_SCALES])
+@pytest.mark.parametrize("name", list(FMTS))
+def test_kquant_gemm_output_range(name, kind, scale):
+    # M > 8 rows run the f16 MFMA GEMM with power-of-two row scaling
+    print("case", name, kind, flush=True)
+    n, k, m = 384, 1024, 40
+    w = O.normal(n * k, 57, 0.02).reshape(n, k)
+    blocks = hip.kquant_encode(FMTS[name], w)
+    lin = hip.QLinear.gguf(FMTS[name], blocks, n, k)
+    x = _range_rows(m, k, 58, kind, scale)
+    got = lin.forward(x)
+    assert np.isfinite(got).all()
+    deq = O.dequant(name, blocks, n * k).reshape(n, k)
+    want = O.matmul_t(x, deq)
+    for i in range(m):
+        assert _rel(got[i], want[i]) <= TOL, (i, _rel(got[i], want[i]))

@@ -157,3 +157,56 @@ def test_q4_gemm_halved_subnormal_scales_use_the_gemv():
     ieee = hip.QLinear.q4_0(packed, n, k).forward(x)
     for i in (0, m - 1):
         assert _rel(ieee[i], O.q4_0_gemv(x[i], packed, n)) <= TOL
+
+
+# ---------------------------------------------------------------- output range
+# Rows of ~1e-7 and ~1e6, and rows fed a few 1e4 outliers, through the K
+# split (split_k.hpp: per-slice f32 slots added in slice order) against
+# q4_0GemvRow (qmatmul.zig:276-343), both through the reference-signature
+# export and a handle at several rows.
+def _range_rows(m, k, seed, kind, scale):
+    x = O.normal(m * k, seed, 1.0).reshape(m, k) * np.float32(scale)
+    if kind == "outliers":
+        rng = np.random.default_rng(seed)
+        for i in range(m):
+            idx = rng.choice(k, 3, replace=False)
+            x[i, idx] = np.float32(1e4) * rng.choice([-1, 1], 3)
+    return np.ascontiguousarray(x, np.float32)
+
+
+@pytest.mark.parametrize("kind,scale", [("tiny", 1e-6), ("huge", 1e6), ("outliers", 1.0)])
+@pytest.mark.parametrize("k,n", [(2048, 512), (8192, 2048), (8192, 300)])
+def test_q4_gemv_output_range(k, n, kind, scale):
+    print("case", k, n, kind, flush=True)
+    w = O.normal(n * k, k + n + 2, 0.02).reshape(n, k)
+    packed = O.q4_pack(w)
+    a = _range_rows(1, k, k + 9, kind, scale)[0]
+    got = hip.q4_0_gemv(a, packed, n)
+    want = O.q4_0_gemv(a, packed, n)
+    assert np.isfinite(got).all()
+    assert _rel(got, want) <= TOL, _rel(got, want)
+    lin = hip.QLinear.from_f32(hip.FMT_Q4_0, w)
+    x = _range_rows(3, k, k + 10, kind, scale)
+    got = lin.forward(x)
+    for i in range(3):
+        want = O.q4_0_gemv(x[i], packed, n)
+        assert _rel(got[i], want) <= TOL, (i, _rel(got[i], want))
+
+
+@pytest.mark.parametrize("kind,scale", [("tiny", 1e-6), ("huge", 1e5), ("outliers", 1.0)])
+@pytest.mark.parametrize("m", [20, 300])
+def test_q4_gemm_rows_output_range(m, kind, scale):
+    # M > 16 rows run the f16 MFMA GEMM; each activation row is scaled by a
+    # power of two into f16's range first (|x| ~ 1e5 would round to inf,
+    # ~1e-6 to subnormal f16), and the rows still match q4_0GemvRow
+    print("case", m, kind, flush=True)
+    n, k = 512, 2048
+    w = O.normal(n * k, 91, 0.02).reshape(n, k)
+    packed = O.q4_pack(w)
+    lin = hip.QLinear.from_f32(hip.FMT_Q4_0, w)
+    x = _range_rows(m, k, 92 + m, kind, scale)
+    got = lin.forward(x)
+    assert np.isfinite(got).all()
+    for i in sorted({0, 1, m // 2, m - 1}):
+        want = O.q4_0_gemv(x[i], packed, n)
+        assert _rel(got[i], want) <= TOL, (i, _rel(got[i], want))

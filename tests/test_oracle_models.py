@@ -304,6 +304,8 @@ def mamba_weights(c, seed_base, std):
             conv_w=O.normal(di * dc, sb + 1, std).reshape(di, dc).astype(np.float64),
             x_proj=O.normal((dr + 2 * ds) * di, sb + 2, std).reshape(dr + 2 * ds, di).astype(np.float64),
             dt_proj=O.normal(di * dr, sb + 3, std).reshape(di, dr).astype(np.float64),
+            x_i8=quant_weights(O.normal((dr + 2 * ds) * di, sb + 2, std).reshape(dr + 2 * ds, di)),
+            dt_i8=quant_weights(O.normal(di * dr, sb + 3, std).reshape(di, dr)),
             out_proj=quant_weights(O.normal(dm * di, sb + 4, std).reshape(dm, di)),
             dt_bias=np.full(di, np.log(np.expm1(0.01))),
             a_log=np.tile(np.log(np.arange(1, ds + 1, dtype=np.float64)), (di, 1))))
@@ -314,9 +316,11 @@ def softplus(x):
     return np.where(x > 20.0, x, np.log1p(np.exp(np.minimum(x, 20.0))))
 
 
-def mamba_ref(c, W, ids, mutate=()):
+def mamba_ref(c, W, ids, mutate=(), int8_xdt=False):
     """QuantizedMambaModel prefill (int8_mamba.rs:177-203): per token, per block
-    forward_one (:78-109), then the final norm and the f32 lm_head"""
+    forward_one (:78-109), then the final norm and the f32 lm_head.  With
+    int8_xdt, x_proj and dt_proj are QuantizedLinears like in_proj (the
+    benchmark's config-5 variant; int8_linear.rs:35-117)"""
     di, ds, dc, dr, eps = c["d_inner"], c["d_state"], c["d_conv"], c["dt_rank"], c["eps"]
     conv = [np.zeros((di, dc)) for _ in W["layers"]]
     ssm = [np.zeros((di, ds)) for _ in W["layers"]]
@@ -329,9 +333,17 @@ def mamba_ref(c, W, ids, mutate=()):
             conv[l] = np.concatenate([conv[l][:, 1:], xp[:, None]], axis=1)  # shift, append
             taps = L["conv_w"][:, ::-1] if "reverse_conv_taps" in mutate else L["conv_w"]
             xa = silu((conv[l] * taps).sum(axis=1))  # conv bias 0
-            xpo = L["x_proj"] @ xa
-            dt, B, C = xpo[:dr], xpo[dr:dr + ds], xpo[dr + ds:]
-            delta = softplus(L["dt_proj"] @ dt + L["dt_bias"])
+            if int8_xdt:
+                xpo = qlinear(xa, L["x_i8"])[0]
+                dt, B, C = xpo[:dr], xpo[dr:dr + ds], xpo[dr + ds:]
+                if "dt_from_b" in mutate:
+                    dt = xpo[ds:dr + ds]
+                dtp = qlinear(dt, L["dt_i8"])[0]
+            else:
+                xpo = L["x_proj"] @ xa
+                dt, B, C = xpo[:dr], xpo[dr:dr + ds], xpo[dr + ds:]
+                dtp = L["dt_proj"] @ dt
+            delta = softplus(dtp + L["dt_bias"])
             a_disc = np.exp(-delta[:, None] * np.exp(L["a_log"]))
             ssm[l] = a_disc * ssm[l] + (delta * xa)[:, None] * B[None, :]
             y = ssm[l] @ C + 1.0 * xa
@@ -365,6 +377,35 @@ def test_mamba_comparison_catches_wiring_mistakes(mamba, mistake):
     m, W = mamba
     ids = [5, 199, 64, 3, 120, 77]
     cos, rel = cmp(m.prefill(ids), mamba_ref(MCFG, W, ids, mutate=(mistake,)))
+    assert cos < 0.999 or rel > 20 * MAMBA_TOL, (mistake, cos, rel)
+
+
+@pytest.fixture(scope="module")
+def mamba_xdt():
+    m = O.QuantizedMamba(MCFG)
+    m.init_synthetic(MSEED, MSTD)
+    m.set_int8_xdt()
+    return m, mamba_weights(MCFG, MSEED, MSTD)
+
+
+def test_mamba_int8_xdt_oracle_matches_float64_forward(mamba_xdt):
+    """the config-5 variant (x_proj and dt_proj through QuantizedLinear) against
+    the float64 forward with qlinear on those two projections; the f32 form
+    of the same forward does not pass, so the variant is really taken"""
+    m, W = mamba_xdt
+    ids = [5, 199, 64, 3, 120, 77]
+    got = m.prefill(ids)
+    cos, rel = cmp(got, mamba_ref(MCFG, W, ids, int8_xdt=True))
+    assert cos > 0.99999 and rel < MAMBA_TOL, (cos, rel)
+    cos_f, rel_f = cmp(got, mamba_ref(MCFG, W, ids))
+    assert rel_f > 20 * MAMBA_TOL, (cos_f, rel_f)
+
+
+@pytest.mark.parametrize("mistake", ["reverse_conv_taps", "no_residual", "dt_from_b"])
+def test_mamba_int8_xdt_comparison_catches_wiring_mistakes(mamba_xdt, mistake):
+    m, W = mamba_xdt
+    ids = [5, 199, 64, 3, 120, 77]
+    cos, rel = cmp(m.prefill(ids), mamba_ref(MCFG, W, ids, mutate=(mistake,), int8_xdt=True))
     assert cos < 0.999 or rel > 20 * MAMBA_TOL, (mistake, cos, rel)
 
 

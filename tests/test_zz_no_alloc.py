@@ -1,7 +1,9 @@
 """syn_hip_qlinear_forward_noalloc (INT8, no allocation: the library's fixed
 device scratch) against syn_hip_qlinear_forward and the oracle, bit for bit,
 over consecutive calls that shrink (the scratch keeps the previous call's
-contents) and across the GEMV (M <= 16, split-K partials) and GEMM paths."""
+contents) and across the GEMV (M <= 16, split-K partials) and both GEMM
+paths (K a multiple of 128: direct global->LDS loads; other K: register
+staging)."""
 import numpy as np
 import pytest
 
@@ -37,8 +39,10 @@ def _both(lin, x):
 
 
 # each case: two calls in a row, the second with a smaller input
+# (4096, 1024, 128, 40): M > 16 with K a multiple of 128, the direct-load GEMM
 @pytest.mark.parametrize("n,k,m1,m2", [(3072, 1024, 16, 1), (1024, 3072, 16, 3),
-                                       (300, 700, 40, 5), (2048 + 17, 1000, 33, 17)])
+                                       (300, 700, 40, 5), (2048 + 17, 1000, 33, 17),
+                                       (4096, 1024, 128, 40), (1000, 2048, 64, 17)])
 def test_noalloc_matches_forward_on_shrinking_calls(n, k, m1, m2):
     print("case", n, k, m1, m2, flush=True)
     lin, w = _linear(n, k, 7)
