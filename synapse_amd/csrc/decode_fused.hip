@@ -253,7 +253,7 @@ __device__ __forceinline__ void norm_prologue_load(const ProArgs &a, int H, floa
 // sq: LDS, round4(H) floats.
 template <int NT, bool SEQ>
 __device__ float norm_quant(float eps, int H, const float (&x)[RB], const float (&nwv)[RB],
-                            float *sq, int8_t *xq, float *red) {
+                            float *sq, int8_t *xq, float *red SYN_TS_PARAM) {
   const int tid = threadIdx.x;
   float t[RB];
 #pragma unroll
@@ -263,7 +263,9 @@ __device__ float norm_quant(float eps, int H, const float (&x)[RB], const float 
     t[u] = x[u] * nwv[u];
   }
   wg_max_post<NT>(local_absmax<NT>(t, H), red, 0);
+  SYN_TS(10);
   bar<NT>();
+  SYN_TS(11);
   float ss;
   if constexpr (SEQ) {
     if (tid < 64) {  // wave 0 runs the single chain
@@ -275,6 +277,7 @@ __device__ float norm_quant(float eps, int H, const float (&x)[RB], const float 
   } else {
     ss = sumsq_chains<NT>(sq, H, red);
   }
+  SYN_TS(12);
   const float scale = 1.0f / sqrtf(ss / (float)H + eps);
   float nv[RB];
 #pragma unroll
@@ -285,6 +288,7 @@ __device__ float norm_quant(float eps, int H, const float (&x)[RB], const float 
     bar<NT>();
     mx = wg_max_get<NT>(red, 16);
   }
+  SYN_TS(13);
   return quantize_regs_with_max<NT>(nv, H, mx, xq);
 }
 
@@ -466,7 +470,7 @@ __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
 
   float sv;
   if constexpr (NORM) {
-    sv = norm_quant<NT, PRO == PRO_MNORM>(a.eps, H, x, nwv, sq, xq, red);
+    sv = norm_quant<NT, PRO == PRO_MNORM>(a.eps, H, x, nwv, sq, xq, red SYN_TS_PASS);
   } else if constexpr (PRO == PRO_HQ) {
     sv = hq;
   } else {
@@ -745,7 +749,7 @@ __global__ void __launch_bounds__(256) k_gu_swiglu(ProArgs a, GuArgs g) {
   SYN_TS(1);
   if (tid < 32) exp_tab[tid] = tv;
   for (int i = H + tid; i < g.C * 16; i += NT) xq[i] = 0;
-  const float sv = norm_quant<NT, false>(a.eps, H, x, nwv, sq, xq, red);
+  const float sv = norm_quant<NT, false>(a.eps, H, x, nwv, sq, xq, red SYN_TS_PASS);
   SYN_TS(2);
   bar<NT>();
   SYN_TS(3);
@@ -1207,6 +1211,10 @@ __global__ void __launch_bounds__(kAttnNT)
   SYN_TS(0);
   SYN_TSR(14);
 
+  // 0. the decode position, requested first (a vector load: waves 1-3 need
+  //    it before they can issue their K rows)
+  const int pos = __builtin_amdgcn_readfirstlane(
+      __hip_atomic_load(&st->pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
   // 1. what does not depend on the decode position: the q / k / v row
   //    values and gains, the expf table word, the K row of position tid and
   //    the V of the first 64 positions of this block's columns (straight
@@ -1242,7 +1250,6 @@ __global__ void __launch_bounds__(kAttnNT)
     load_k_rows(tid);
     stage_v_chunk<CB>(V4, HD, s4, cb0, 0, vbuf, 0, 0, 1, lane, 16);
   }
-  const int pos = st->pos;
   const int len = pos + 1;
   SYN_TS(1);
   // then the rest of the first pass of K rows and of the first V chunk,
@@ -1340,7 +1347,10 @@ __global__ void __launch_bounds__(kAttnNT)
   for (int i = tid; i < len; i += kAttnNT) e[i] = syn_expf_tab(e[i] - mx, exp_tab);
   __syncthreads();
   SYN_TS(7);
-  if (tid == 0) red[12] = lds_seq_sum(e, len, 0.0f);
+  if (wave == 0) {  // the sequential sum, run from registers by the whole wave
+    const float r = wave_seq_sum(e, len, 0.0f);
+    if (lane == 0) red[12] = r;
+  }
   __syncthreads();
   SYN_TS(8);
   const float sum = red[12];

@@ -9,6 +9,9 @@
 #define SYN_TS_DECL unsigned long long syn_ts_[16] = {};
 #define SYN_TS(i) syn_ts_[(i)] = __builtin_amdgcn_s_memtime()
 #define SYN_TSR(i) syn_ts_[(i)] = __builtin_amdgcn_s_memrealtime()
+// pass the kernel's timestamp registers into an inlined helper
+#define SYN_TS_PARAM , unsigned long long *syn_ts_
+#define SYN_TS_PASS , syn_ts_
 #define SYN_TS_FLUSH_TO(arr, base)                                      \
   do {                                                                  \
     if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0)         \
@@ -16,6 +19,8 @@
   } while (0)
 #else
 #define SYN_TS_DECL
+#define SYN_TS_PARAM
+#define SYN_TS_PASS
 #define SYN_TS(i) \
   do {            \
   } while (0)

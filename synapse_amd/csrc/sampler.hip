@@ -13,9 +13,10 @@
 // the top k are all among them); those candidates are sorted in LDS.  When
 // more than kSortMax values are >= L, a 32-step binary search over the order
 // of the value keys finds the threshold instead.  top-p sorts the candidates
-// by probability in LDS (probability descending, index ascending), so it
-// needs at most kSortMax candidates (top-k on); otherwise the call reports
-// SYN_ERR_INVALID_ARG.
+// by probability (descending, index ascending among equal probabilities):
+// up to kSortMax of them with a bitonic sort in LDS, more (top-p without
+// top-k over a large vocabulary) with a stable radix sort in global memory,
+// one bit per pass over the candidates' list.
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -142,6 +143,53 @@ __device__ int compact(const float *w, int V, Keep keep, uint32_t *cidx, float *
   return total;
 }
 
+// exclusive prefix sum of one int per thread over the block; *total gets the
+// sum (every thread)
+__device__ int block_excl_scan(int v, int *scan, int *total) {
+  scan[threadIdx.x] = v;
+  __syncthreads();
+  for (int o = 1; o < kSampNT; o <<= 1) {
+    const int t = threadIdx.x >= o ? scan[threadIdx.x - o] : 0;
+    __syncthreads();
+    scan[threadIdx.x] += t;
+    __syncthreads();
+  }
+  *total = scan[kSampNT - 1];
+  const int r = scan[threadIdx.x] - v;
+  __syncthreads();
+  return r;
+}
+
+// Stable ascending sort of the n (key, index) pairs in (ka, va) by the key
+// bits below `bits`: one stable partition per bit (zeros before ones, each
+// in their order), ping-ponging with (kb, vb).  Thread t owns a contiguous
+// range, so a block scan of the zero counts places every element.  Returns
+// the buffer pair that holds the result (0: ka/va, 1: kb/vb).
+__device__ int radix_sort_global(uint32_t *ka, uint32_t *va, uint32_t *kb, uint32_t *vb, int n,
+                                 int bits, int *scan) {
+  const int chunk = (n + kSampNT - 1) / kSampNT;
+  const int b = min(n, (int)threadIdx.x * chunk), e = min(n, b + chunk);
+  int cur = 0;
+  for (int bit = 0; bit < bits; bit++) {
+    const uint32_t *ks = cur ? kb : ka, *vs = cur ? vb : va;
+    uint32_t *kd = cur ? ka : kb, *vd = cur ? va : vb;
+    int z = 0;
+    for (int i = b; i < e; i++) z += ((ks[i] >> bit) & 1u) ? 0 : 1;
+    int zeros;
+    int zo = block_excl_scan(z, scan, &zeros);
+    int oo = zeros + (b - zo);  // ones before this range: elements before it minus zeros
+    for (int i = b; i < e; i++) {
+      const uint32_t k = ks[i], v = vs[i];
+      const int d = ((k >> bit) & 1u) ? oo++ : zo++;
+      kd[d] = k;
+      vd[d] = v;
+    }
+    __syncthreads();
+    cur ^= 1;
+  }
+  return cur;
+}
+
 // softmax's exponentials exp(v - mx) in place (all threads), then their
 // sequential sum in list order (thread 0, loads 16 ahead of the adds);
 // every thread gets the sum
@@ -170,7 +218,8 @@ __global__ void __launch_bounds__(kSampNT)
              SampleArgs a, const float *__restrict__ u_src, StepState *st, int add_pos,
              uint32_t *__restrict__ history, float *__restrict__ mhist, float *__restrict__ w,
              uint32_t *__restrict__ cidx, float *__restrict__ cval, int *__restrict__ status,
-             uint32_t *__restrict__ token_out) {
+             uint32_t *__restrict__ token_out, uint32_t *__restrict__ ka,
+             uint32_t *__restrict__ kb, uint32_t *__restrict__ va, uint32_t *__restrict__ vb) {
   __shared__ unsigned long long sbuf[kSortMax];
   __shared__ int scan[kSampNT];
   __shared__ float redf[32];
@@ -261,67 +310,91 @@ __global__ void __launch_bounds__(kSampNT)
     }
 
     if (a.top_p > 0.0f && a.top_p < 1.0f) {  // top_p_filter (sampler.rs:279-319)
-      if (nc > kSortMax) {
-        if (tid == 0) s_err = 1;
-        __syncthreads();
-      } else {
-        // softmax over the candidates: max, exp, sequential sum, division
-        float mx = -__builtin_inff();
-        for (int i = tid; i < nc; i += kSampNT) mx = fmaxf(mx, cval[i]);
-        for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-        __syncthreads();
-        if ((tid & 63) == 0) redf[tid >> 6] = mx;
-        __syncthreads();
-        mx = redf[0];
-        for (int i = 1; i < kSampNT / 64; i++) mx = fmaxf(mx, redf[i]);
-        float *pr = w;  // the probabilities, in the free working vector
-        for (int i = tid; i < nc; i += kSampNT) pr[i] = cval[i];
-        __syncthreads();
-        const float sum = exp_then_seq_sum(pr, nc, mx, bcast_f);
-        if (sum > 0.0f)
-          for (int i = tid; i < nc; i += kSampNT) pr[i] = pr[i] / sum;
+      // softmax over the candidates: max, exp, sequential sum, division
+      float mx = -__builtin_inff();
+      for (int i = tid; i < nc; i += kSampNT) mx = fmaxf(mx, cval[i]);
+      for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+      __syncthreads();
+      if ((tid & 63) == 0) redf[tid >> 6] = mx;
+      __syncthreads();
+      mx = redf[0];
+      for (int i = 1; i < kSampNT / 64; i++) mx = fmaxf(mx, redf[i]);
+      float *pr = w;  // the probabilities, in the free working vector
+      for (int i = tid; i < nc; i += kSampNT) pr[i] = cval[i];
+      __syncthreads();
+      const float sum = exp_then_seq_sum(pr, nc, mx, bcast_f);
+      if (sum > 0.0f)
+        for (int i = tid; i < nc; i += kSampNT) pr[i] = pr[i] / sum;
+      __syncthreads();
+      // the candidates sorted by probability descending, index ascending
+      // among equal ones: rank r holds token sidx[r] with probability sp[r]
+      const uint32_t *sidx;
+      const uint32_t *skey;
+      if (nc <= kSortMax) {
         int n2 = 1;
         while (n2 < nc) n2 <<= 1;
-        __syncthreads();
         for (int i = tid; i < n2; i += kSampNT)
           sbuf[i] = i < nc ? ((unsigned long long)(~fkey(pr[i])) << 32) | cidx[i] : ~0ull;
         __syncthreads();
         bitonic_sort(sbuf, n2);
-        // cumulative probability in sorted order until it reaches p
-        if (tid == 0) {
-          float cum = 0.0f;
-          int j = 0;
-          for (; j < nc; j++) {
-            const float p = fkey_inv(~(uint32_t)(sbuf[j] >> 32));
-            cum += p;
-            if (cum >= a.top_p) {
-              j++;
-              break;
-            }
-          }
-          bcast_i[0] = j;
+        for (int i = tid; i < nc; i += kSampNT) {
+          ka[i] = ~(uint32_t)(sbuf[i] >> 32);  // fkey of the probability
+          va[i] = (uint32_t)(sbuf[i] & 0xffffffffu);
         }
         __syncthreads();
-        const int keep_n = bcast_i[0];
-        // drop the candidates outside the nucleus: mark through w (value -inf)
-        for (int i = tid; i < nc; i += kSampNT) w[i] = 0.0f;
-        __syncthreads();
-        for (int r = tid; r < keep_n; r += kSampNT) {
-          // rank r holds token idx; find its candidate slot by binary search
-          const uint32_t idx = (uint32_t)(sbuf[r] & 0xffffffffu);
-          int lo = 0, hi = nc - 1;
-          while (lo < hi) {
-            const int mid = (lo + hi) >> 1;
-            if (cidx[mid] < idx) lo = mid + 1;
-            else hi = mid;
-          }
-          w[lo] = 1.0f;
+        sidx = va;
+        skey = ka;
+      } else {
+        // probabilities are >= +0, so ~bits orders them descending; the
+        // sign bit is set in every key and needs no pass
+        for (int i = tid; i < nc; i += kSampNT) {
+          ka[i] = ~__float_as_uint(pr[i]);
+          va[i] = cidx[i];
         }
         __syncthreads();
-        for (int i = tid; i < nc; i += kSampNT)
-          if (w[i] == 0.0f) cval[i] = -__builtin_inff();
+        const int in_b = radix_sort_global(ka, va, kb, vb, nc, 31, scan);
+        for (int i = tid; i < nc; i += kSampNT) {  // as fkey, like the LDS route
+          const uint32_t k = in_b ? kb[i] : ka[i];
+          (in_b ? kb : ka)[i] = ~k | 0x80000000u;
+        }
         __syncthreads();
+        sidx = in_b ? vb : va;
+        skey = in_b ? kb : ka;
       }
+      // cumulative probability in sorted order until it reaches p
+      if (tid == 0) {
+        float cum = 0.0f;
+        int j = 0;
+        for (; j < nc; j++) {
+          const float p = fkey_inv(skey[j]);
+          cum += p;
+          if (cum >= a.top_p) {
+            j++;
+            break;
+          }
+        }
+        bcast_i[0] = j;
+      }
+      __syncthreads();
+      const int keep_n = bcast_i[0];
+      // drop the candidates outside the nucleus: mark through w
+      for (int i = tid; i < nc; i += kSampNT) w[i] = 0.0f;
+      __syncthreads();
+      for (int r = tid; r < keep_n; r += kSampNT) {
+        // rank r holds token idx; find its candidate slot by binary search
+        const uint32_t idx = sidx[r];
+        int lo = 0, hi = nc - 1;
+        while (lo < hi) {
+          const int mid = (lo + hi) >> 1;
+          if (cidx[mid] < idx) lo = mid + 1;
+          else hi = mid;
+        }
+        w[lo] = 1.0f;
+      }
+      __syncthreads();
+      for (int i = tid; i < nc; i += kSampNT)
+        if (w[i] == 0.0f) cval[i] = -__builtin_inff();
+      __syncthreads();
     }
 
     // softmax_sample (sampler.rs:227-259) over the candidates in index order
@@ -392,6 +465,10 @@ syn_status_t SampleScratch::ensure(size_t v) {
   SYN_TRY(cidx.alloc(v * 4));
   SYN_TRY(cval.alloc(v * 4));
   SYN_TRY(status.alloc(64));
+  SYN_TRY(ka.alloc(v * 4));
+  SYN_TRY(kb.alloc(v * 4));
+  SYN_TRY(va.alloc(v * 4));
+  SYN_TRY(vb.alloc(v * 4));
   vocab = v;
   return SYN_OK;
 }
@@ -407,7 +484,9 @@ syn_status_t launch_sample(const float *logits, int V, const uint32_t *hist, int
   }
   hipLaunchKernelGGL(k_sample, dim3(1), dim3(kSampNT), 0, s, logits, V, hist, nh, a, u, st,
                      add_pos, history, mhist, scr.w.as<float>(), scr.cidx.as<uint32_t>(),
-                     scr.cval.as<float>(), scr.status.as<int>(), token_out);
+                     scr.cval.as<float>(), scr.status.as<int>(), token_out,
+                     scr.ka.as<uint32_t>(), scr.kb.as<uint32_t>(), scr.va.as<uint32_t>(),
+                     scr.vb.as<uint32_t>());
   SYN_LAUNCH_CHECK();
   return SYN_OK;
 }

@@ -19,10 +19,10 @@ struct SampleArgs {
 
 SampleArgs make_sample_args(const syn_hip_sampler &p);
 
-// Scratch of one sampler: a working copy of the logits and the candidate
-// list, sized for `vocab`.
+// Scratch of one sampler: a working copy of the logits, the candidate list
+// and the key / index buffers of the large top-p sort, sized for `vocab`.
 struct SampleScratch {
-  DevBuf w, cidx, cval, status;
+  DevBuf w, cidx, cval, status, ka, kb, va, vb;
   size_t vocab = 0;
   syn_status_t ensure(size_t v);
 };

@@ -62,10 +62,16 @@ def test_top_p_without_top_k_small_vocab():
             O.sample_combined(x, temperature=1.0, top_p=0.8, u=float(u))
 
 
-def test_top_p_without_top_k_large_vocab_reports_error():
-    x = logits_for(6, 10000, ties=False)
-    with pytest.raises(hip.SynapseError):
-        hip.sample(x, temperature=1.0, top_p=0.8, u=0.3)
+@pytest.mark.parametrize("n,ties", [(10000, False), (151936, False), (151936, True)])
+def test_top_p_without_top_k_large_vocab(n, ties):
+    # a nucleus of far more than 4096 candidates (top_p_filter over the whole
+    # vocabulary, sampler.rs:279-319): the stable radix sort in global memory
+    x = logits_for(6, n, scale=1.0, ties=ties)
+    for tp in (0.5, 0.8, 0.95):
+        for u in O.stdrng_f32(11, 4):
+            want = O.sample_combined(x, temperature=1.0, top_p=tp, u=float(u))
+            got = hip.sample(x, temperature=1.0, top_p=tp, u=float(u))
+            assert got == want, (n, ties, tp, float(u), got, want)
 
 
 def test_sampled_generate_matches_oracle():
