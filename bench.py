@@ -86,7 +86,8 @@ STEP_KERNEL_NAMES = {
     "qkv": "k_fused_gemv<0,256,U> (residual + RMSNorm + quantize + QKV GEMV)",
     "attention": "k_attn_head<false,128> (head norms, RoPE, KV append, attention)",
     "o": "k_fused_gemv<1,256,U> (quantize + O GEMV)",
-    "gate_up": "k_gu_swiglu<8> (residual + RMSNorm + quantize + gate|up GEMV + SwiGLU)",
+    "gate_up": "k_fused_gemv<0,256,U,true> (residual + RMSNorm + quantize + gate|up GEMV in "
+               "panel pairs, split K, SwiGLU in each pair's last slice)",
     "down": "k_fused_gemv<5,512,U> (quantize h range + down GEMV)",
     "lm_head": "k_lmhead_top2<8,8> (lm_head GEMV + per-panel top-2)"}
 

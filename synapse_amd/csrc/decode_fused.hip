@@ -88,17 +88,17 @@ __device__ __forceinline__ float wg_max_get(const float *red, int slot) {
 // quantizePerChannelInt8 (quantize.zig:12-47) of a row held in registers
 // (element j = threadIdx.x + u*NT, valid for j < n), given the row's max|v|:
 // writes q[j] and returns the row scale.
-template <int NT>
-__device__ float quantize_regs_with_max(const float (&v)[RB], int n, float mx, int8_t *q) {
+template <int NT, int R>
+__device__ float quantize_regs_with_max(const float (&v)[R], int n, float mx, int8_t *q) {
   if (mx == 0.0f) {
 #pragma unroll
-    for (int u = 0; u < RB; u++)
+    for (int u = 0; u < R; u++)
       if (threadIdx.x + u * NT < n) q[threadIdx.x + u * NT] = 0;
     return 1.0f;
   }
   const float inv = 127.0f / mx;
 #pragma unroll
-  for (int u = 0; u < RB; u++) {
+  for (int u = 0; u < R; u++) {
     const int j = threadIdx.x + u * NT;
     if (j < n) {
       float r = roundf(v[u] * inv);
@@ -110,11 +110,11 @@ __device__ float quantize_regs_with_max(const float (&v)[RB], int n, float mx, i
 }
 
 // per-thread max|v[u]| over its valid elements (the reference's `if a > m`)
-template <int NT>
-__device__ __forceinline__ float local_absmax(const float (&v)[RB], int n) {
+template <int NT, int R>
+__device__ __forceinline__ float local_absmax(const float (&v)[R], int n) {
   float mx = 0.0f;
 #pragma unroll
-  for (int u = 0; u < RB; u++) {
+  for (int u = 0; u < R; u++) {
     const float a = fabsf(v[u]);
     if (threadIdx.x + u * NT < n && a > mx) mx = a;
   }
@@ -122,11 +122,11 @@ __device__ __forceinline__ float local_absmax(const float (&v)[RB], int n) {
 }
 
 // the whole quantizer: workgroup max (one barrier), then quantize_regs_with_max
-template <int NT>
-__device__ float quantize_regs(const float (&v)[RB], int n, int8_t *q, float *red, int slot) {
-  wg_max_post<NT>(local_absmax<NT>(v, n), red, slot);
+template <int NT, int R>
+__device__ float quantize_regs(const float (&v)[R], int n, int8_t *q, float *red, int slot) {
+  wg_max_post<NT>(local_absmax<NT, R>(v, n), red, slot);
   bar<NT>();
-  return quantize_regs_with_max<NT>(v, n, wg_max_get<NT>(red, slot), q);
+  return quantize_regs_with_max<NT, R>(v, n, wg_max_get<NT>(red, slot), q);
 }
 
 // device address of the expf table (per device; resolved once)
@@ -197,6 +197,16 @@ struct GemvArgs {
   const i32x4 *W;
   int C, cs;
   int *acc;
+  // gate|up pairs (GU kernels): grid panel p covers gate panel p and up
+  // panel `pairs` + p of the stacked [gate | up] matrix; cnt[p] counts the
+  // arrived K slices of pair p; the pair's last slice writes h = silu(gate)
+  // * up for its 64 rows (ws: the stacked rows' scales) and max |h| to hmax
+  int pairs = 0;
+  int *cnt = nullptr;
+  const float *ws = nullptr;
+  float *h = nullptr;
+  unsigned *hmax = nullptr;
+  const uint64_t *exp_tab = nullptr;
 };
 
 // ------------------------------------------------------------------ prologue parts
@@ -204,9 +214,9 @@ struct GemvArgs {
 // + delta rows, the norm gains; issue() is called once these are requested,
 // so the caller's weight loads queue behind them (element j = tid + u*NT,
 // clamped to H-1)
-template <int NT, class Issue>
-__device__ __forceinline__ void norm_prologue_load(const ProArgs &a, int H, float (&x)[RB],
-                                                   float (&nwv)[RB], Issue issue) {
+template <int NT, int R, class Issue>
+__device__ __forceinline__ void norm_prologue_load(const ProArgs &a, int H, float (&x)[R],
+                                                   float (&nwv)[R], Issue issue) {
   const int tid = threadIdx.x;
   const float *src = a.base;
   if (!src) {
@@ -214,7 +224,7 @@ __device__ __forceinline__ void norm_prologue_load(const ProArgs &a, int H, floa
     src = tok < (uint32_t)a.vocab ? a.embed + (size_t)tok * H : a.zero_row;
   }
 #pragma unroll
-  for (int u = 0; u < RB; u++) {
+  for (int u = 0; u < R; u++) {
     const int j = min(tid + u * NT, H - 1);
     x[u] = src[j];
     nwv[u] = a.nw[j];
@@ -225,10 +235,10 @@ __device__ __forceinline__ void norm_prologue_load(const ProArgs &a, int H, floa
   const int *dacc = has_delta ? a.delta.acc : reinterpret_cast<const int *>(a.nw);
   const float *dws = has_delta ? a.delta.ws : a.nw;
   const float *dsxp = has_delta ? a.delta.sx : a.nw;
-  int da[RB];
-  float dw[RB];
+  int da[R];
+  float dw[R];
 #pragma unroll
-  for (int u = 0; u < RB; u++) {
+  for (int u = 0; u < R; u++) {
     const int j = min(tid + u * NT, H - 1);
     da[u] = dacc[j];
     dw[u] = dws[j];
@@ -237,7 +247,7 @@ __device__ __forceinline__ void norm_prologue_load(const ProArgs &a, int H, floa
   issue();
   if (has_delta) {
 #pragma unroll
-    for (int u = 0; u < RB; u++) {
+    for (int u = 0; u < R; u++) {
       const float f = (float)da[u] * dsx;
       const float d = f * dw[u];
       x[u] = x[u] + d;
@@ -251,18 +261,18 @@ __device__ __forceinline__ void norm_prologue_load(const ProArgs &a, int H, floa
 // = fl(max|t| * scale): the max of t = x*w is reduced while lanes 0-3 run
 // the sum-of-squares chains (or lane 0 the single sequential sum, SEQ).
 // sq: LDS, round4(H) floats.
-template <int NT, bool SEQ>
-__device__ float norm_quant(float eps, int H, const float (&x)[RB], const float (&nwv)[RB],
+template <int NT, int R, bool SEQ>
+__device__ float norm_quant(float eps, int H, const float (&x)[R], const float (&nwv)[R],
                             float *sq, int8_t *xq, float *red SYN_TS_PARAM) {
   const int tid = threadIdx.x;
-  float t[RB];
+  float t[R];
 #pragma unroll
-  for (int u = 0; u < RB; u++) {
+  for (int u = 0; u < R; u++) {
     const int j = tid + u * NT;
     if (j < H) sq[SEQ ? j : sq_slot(j, H)] = x[u] * x[u];
     t[u] = x[u] * nwv[u];
   }
-  wg_max_post<NT>(local_absmax<NT>(t, H), red, 0);
+  wg_max_post<NT>(local_absmax<NT, R>(t, H), red, 0);
   SYN_TS(10);
   bar<NT>();
   SYN_TS(11);
@@ -279,35 +289,35 @@ __device__ float norm_quant(float eps, int H, const float (&x)[RB], const float 
   }
   SYN_TS(12);
   const float scale = 1.0f / sqrtf(ss / (float)H + eps);
-  float nv[RB];
+  float nv[R];
 #pragma unroll
-  for (int u = 0; u < RB; u++) nv[u] = t[u] * scale;
+  for (int u = 0; u < R; u++) nv[u] = t[u] * scale;
   float mx = wg_max_get<NT>(red, 0) * scale;
   if (!(mx <= 3.402823466e38f) || !(scale > 0.0f)) {  // inf/nan rows: reduce explicitly
-    wg_max_post<NT>(local_absmax<NT>(nv, H), red, 16);
+    wg_max_post<NT>(local_absmax<NT, R>(nv, H), red, 16);
     bar<NT>();
     mx = wg_max_get<NT>(red, 16);
   }
   SYN_TS(13);
-  return quantize_regs_with_max<NT>(nv, H, mx, xq);
+  return quantize_regs_with_max<NT, R>(nv, H, mx, xq);
 }
 
 // quantizePerChannelInt8 (quantize.zig:12-47) of elements [k0, k1) of a row
 // whose max|v| is mx, held as element j = k0 + tid + u*NT; writes xq[j] and
 // returns the row scale
-template <int NT>
-__device__ float quantize_range_with_max(const float (&v)[RB], int k0, int k1, float mx,
+template <int NT, int R>
+__device__ float quantize_range_with_max(const float (&v)[R], int k0, int k1, float mx,
                                          int8_t *xq) {
   const int tid = threadIdx.x;
   if (mx == 0.0f) {
 #pragma unroll
-    for (int u = 0; u < RB; u++)
+    for (int u = 0; u < R; u++)
       if (k0 + tid + u * NT < k1) xq[k0 + tid + u * NT] = 0;
     return 1.0f;
   }
   const float inv = 127.0f / mx;
 #pragma unroll
-  for (int u = 0; u < RB; u++) {
+  for (int u = 0; u < R; u++) {
     const int j = k0 + tid + u * NT;
     if (j < k1) {
       float r = roundf(v[u] * inv);
@@ -325,13 +335,26 @@ __device__ float quantize_range_with_max(const float (&v)[RB], int k0, int k1, f
 // Loads are unconditional from clamped (in-bounds) addresses and the values
 // of out-of-range lanes are ignored where they are used: a conditional load
 // would make the compiler wait for it on the spot.
-template <int PRO, int NT, int U>
+//
+// GU (with PRO_NORM): the gate|up GEMV of the SwiGLU FFN.  A workgroup runs
+// the same prologue, then the dot products of gate panel p and up panel
+// pairs + p over its K slice; it adds them into the pair's accumulators,
+// waits for the atomics to return and counts its arrival (the split_k.hpp
+// protocol).  The pair's last slice reads the 2 x 64 exact int32 totals back
+// by atomic exchange with 0 (leaving them clear), applies the M <= 16
+// epilogue (f32(acc)*sx)*sw to both, h[j] = silu(gate_j) * up_j
+// (int8.rs:500-503), writes h and folds max |h| into hmax by an atomic max
+// of the f32 bits (|h| >= 0, so the bit order is the value order; NaN is
+// skipped as the reference quantizer's `if a > m` skips it).
+template <int PRO, int NT, int U, bool GU, int R>
 __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
   constexpr int NW = NT / 64;
   constexpr bool NORM = PRO == PRO_NORM || PRO == PRO_MNORM;
+  static_assert(!GU || PRO == PRO_NORM, "gate|up pairs take the RMSNorm prologue");
   extern __shared__ __align__(16) unsigned char smem[];
   __shared__ float red[64];
-  __shared__ int redi[NW * 64];
+  __shared__ int redi[(GU ? 2 : 1) * NW * 64];
+  __shared__ uint64_t gu_tab[GU ? 32 : 1];  // GU: expf's table for the last slice's SiLU
   const int H = a.H;
   float *sq = reinterpret_cast<float *>(smem);
   int8_t *xq = reinterpret_cast<int8_t *>(smem) + (NORM ? ((H + 3) & ~3) * 4 : 0);
@@ -347,13 +370,23 @@ __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
   // Vector loads retire in issue order, so the prologue's inputs (L2 hits)
   // are requested before the weight chunks (HBM): the prologue then waits
   // only for its own data while the weights stream in behind it.
-  i32x4 w[U];
+  i32x4 w[U], w2[GU ? U : 1];
   const i32x4 *Wp = g.W + (size_t)panel * g.C * 64 + lane;
+  const i32x4 *Wp2 = g.W + (size_t)(panel + g.pairs) * g.C * 64 + lane;
+  // GU: the expf table word and the pair's row scales, for the last slice
+  uint64_t gu_tv = 0;
+  float gu_wsg = 0.0f, gu_wsu = 0.0f;
+  if constexpr (GU) {
+    gu_tv = g.exp_tab[tid & 31];
+    gu_wsg = g.ws[panel * 64 + lane];
+    gu_wsu = g.ws[(g.pairs + panel) * 64 + lane];
+  }
   auto issue_weights = [&]() {
 #pragma unroll
     for (int u = 0; u < U; u++) {
       const int c = min(c0 + wave + u * NW, c1 - 1);
       w[u] = __builtin_nontemporal_load(Wp + (size_t)c * 64);
+      if constexpr (GU) w2[u] = __builtin_nontemporal_load(Wp2 + (size_t)c * 64);
     }
     asm volatile("" ::: "memory");  // keep the weight requests here, ahead of the prologue
     SYN_TS(1);
@@ -361,33 +394,33 @@ __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
 
   // 1. prologue inputs (element j = tid + u*NT, clamped to H-1), 2. the
   //    weight chunks, 3. the activation row x[] in registers
-  float x[RB];
-  float nwv[RB];
+  float x[R];
+  float nwv[R];
   float hq = 1.0f;
   if constexpr (NORM) {
-    norm_prologue_load<NT>(a, H, x, nwv, issue_weights);
+    norm_prologue_load<NT, R>(a, H, x, nwv, issue_weights);
   } else if constexpr (PRO == PRO_HQ) {
     // element j = c0*16 + tid + u*NT of this split's K range
     const int k0 = c0 * 16, k1 = min(c1 * 16, H);
 #pragma unroll
-    for (int u = 0; u < RB; u++) x[u] = a.vec[min(k0 + tid + u * NT, H - 1)];
+    for (int u = 0; u < R; u++) x[u] = a.vec[min(k0 + tid + u * NT, H - 1)];
     const float mx = __uint_as_float(a.hmax[0]);
     issue_weights();
-    hq = quantize_range_with_max<NT>(x, k0, k1, mx, xq);
+    hq = quantize_range_with_max<NT, R>(x, k0, k1, mx, xq);
   } else if constexpr (PRO == PRO_QUANT) {
 #pragma unroll
-    for (int u = 0; u < RB; u++) x[u] = a.vec[min(tid + u * NT, H - 1)];
+    for (int u = 0; u < R; u++) x[u] = a.vec[min(tid + u * NT, H - 1)];
     issue_weights();
   } else if constexpr (PRO == PRO_CONV) {
     // expf's table to LDS first (a global lookup would wait behind the weights)
     __shared__ uint64_t exp_tab[32];
     const uint64_t tv = a.exp_tab[tid & 31];
-    int ra[RB];
-    float rw[RB];
-    float4 tp[RB], cw[RB];
-    float cb[RB];
+    int ra[R];
+    float rw[R];
+    float4 tp[R], cw[R];
+    float cb[R];
 #pragma unroll
-    for (int u = 0; u < RB; u++) {
+    for (int u = 0; u < R; u++) {
       const int j = min(tid + u * NT, H - 1);
       ra[u] = a.rows.acc[j];
       rw[u] = a.rows.ws[j];
@@ -406,7 +439,7 @@ __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
     };
     const int k0 = (pos + 1) & 3, k1 = (pos + 2) & 3, k2 = (pos + 3) & 3;
 #pragma unroll
-    for (int u = 0; u < RB; u++) {
+    for (int u = 0; u < R; u++) {
       const float f = (float)ra[u] * rsx;
       const float xt = f * rw[u];
       float sum = 0.0f, t;
@@ -422,10 +455,10 @@ __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
       nwv[u] = xt;  // the new ring entry, published by workgroup 0
     }
   } else if constexpr (PRO == PRO_ROWS) {
-    int ra[RB];
-    float rw[RB];
+    int ra[R];
+    float rw[R];
 #pragma unroll
-    for (int u = 0; u < RB; u++) {
+    for (int u = 0; u < R; u++) {
       const int j = min(tid + u * NT, H - 1);
       ra[u] = a.rows.acc[j];
       rw[u] = a.rows.ws[j];
@@ -433,7 +466,7 @@ __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
     const float rsx = a.rows.sx[0];
     issue_weights();
 #pragma unroll
-    for (int u = 0; u < RB; u++) {
+    for (int u = 0; u < R; u++) {
       const float f = (float)ra[u] * rsx;
       x[u] = f * rw[u];
     }
@@ -442,10 +475,10 @@ __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
     // would wait behind the outstanding weight loads
     __shared__ uint64_t exp_tab[32];
     const uint64_t tv = a.exp_tab[tid & 31];
-    int ga[RB], ua[RB];
-    float gw[RB], uw[RB];
+    int ga[R], ua[R];
+    float gw[R], uw[R];
 #pragma unroll
-    for (int u = 0; u < RB; u++) {
+    for (int u = 0; u < R; u++) {
       const int j = min(tid + u * NT, H - 1);
       ga[u] = a.gu.acc[j];
       ua[u] = a.gu.acc[H + j];
@@ -457,7 +490,7 @@ __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
     if (tid < 32) exp_tab[tid] = tv;
     bar<NT>();
 #pragma unroll
-    for (int u = 0; u < RB; u++) {
+    for (int u = 0; u < R; u++) {
       // silu(gate) * up (int8.rs:500-503), each factor the GEMV epilogue
       const float fg = (float)ga[u] * gsx, fu = (float)ua[u] * gsx;
       const float gv = fg * gw[u], uv = fu * uw[u];
@@ -470,18 +503,18 @@ __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
 
   float sv;
   if constexpr (NORM) {
-    sv = norm_quant<NT, PRO == PRO_MNORM>(a.eps, H, x, nwv, sq, xq, red SYN_TS_PASS);
+    sv = norm_quant<NT, R, PRO == PRO_MNORM>(a.eps, H, x, nwv, sq, xq, red SYN_TS_PASS);
   } else if constexpr (PRO == PRO_HQ) {
     sv = hq;
   } else {
-    sv = quantize_regs<NT>(x, H, xq, red, 0);
+    sv = quantize_regs<NT, R>(x, H, xq, red, 0);
   }
   SYN_TS(5);
   bar<NT>();
   SYN_TS(6);
 
   // 3. integer dot products of this wave's chunks, reduced over the waves
-  int acc = 0;
+  int acc = 0, acc2 = 0;
 #pragma unroll
   for (int u = 0; u < U; u++) {
     const int c = c0 + wave + u * NW;
@@ -491,13 +524,60 @@ __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
       acc = __builtin_amdgcn_sdot4(w[u].y, xv.y, acc, false);
       acc = __builtin_amdgcn_sdot4(w[u].z, xv.z, acc, false);
       acc = __builtin_amdgcn_sdot4(w[u].w, xv.w, acc, false);
+      if constexpr (GU) {
+        acc2 = __builtin_amdgcn_sdot4(w2[u].x, xv.x, acc2, false);
+        acc2 = __builtin_amdgcn_sdot4(w2[u].y, xv.y, acc2, false);
+        acc2 = __builtin_amdgcn_sdot4(w2[u].z, xv.z, acc2, false);
+        acc2 = __builtin_amdgcn_sdot4(w2[u].w, xv.w, acc2, false);
+      }
     }
   }
   SYN_TS(7);
   redi[wave * 64 + lane] = acc;
+  if constexpr (GU) {
+    redi[(NW + wave) * 64 + lane] = acc2;
+    if (tid < 32) gu_tab[tid] = gu_tv;
+  }
   bar<NT>();
   SYN_TS(8);
-  if (wave == 0) {
+  if constexpr (GU) {
+    if (wave == 0) {
+      int sg = 0, su = 0;
+#pragma unroll
+      for (int i = 0; i < NW; i++) {
+        sg += redi[i * 64 + lane];
+        su += redi[(NW + i) * 64 + lane];
+      }
+      int *ag = g.acc + panel * 64 + lane, *au = g.acc + (g.pairs + panel) * 64 + lane;
+      const int r0 = __hip_atomic_fetch_add(ag, sg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const int r1 = __hip_atomic_fetch_add(au, su, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      asm volatile("" ::"v"(r0), "v"(r1));  // both adds of this lane have returned
+      __builtin_amdgcn_wave_barrier();
+      int old = 0;
+      if (lane == 0)
+        old = __hip_atomic_fetch_add(g.cnt + panel, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      old = __shfl(old, 0);
+      if (old == (int)gridDim.y - 1) {  // the pair's last slice: totals, SwiGLU, max |h|
+        const int tg = __hip_atomic_exchange(ag, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int tu = __hip_atomic_exchange(au, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0)
+          __hip_atomic_exchange(g.cnt + panel, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const int j = panel * 64 + lane;
+        float m = 0.0f;
+        if (j < g.pairs * 64) {
+          const float fg = (float)tg * sv, fu = (float)tu * sv;
+          const float gv = fg * gu_wsg, uv = fu * gu_wsu;
+          const float act = syn_silu_tab(gv, gu_tab);
+          const float hv = act * uv;
+          g.h[j] = hv;
+          const float av = fabsf(hv);
+          if (av > m) m = av;
+        }
+        m = wave_max_nonneg(m);
+        if (lane == 0) atomicMax(g.hmax, __float_as_uint(m));
+      }
+    }
+  } else if (wave == 0) {
     int s = 0;
 #pragma unroll
     for (int i = 0; i < NW; i++) s += redi[i * 64 + lane];
@@ -510,14 +590,14 @@ __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
     if constexpr (NORM) {
       if (a.res_out) {
 #pragma unroll
-        for (int u = 0; u < RB; u++)
+        for (int u = 0; u < R; u++)
           if (tid + u * NT < H) a.res_out[tid + u * NT] = x[u];
       }
     }
     if constexpr (PRO == PRO_CONV) {
       const int ps = a.st->pos & 3;
 #pragma unroll
-      for (int u = 0; u < RB; u++) {
+      for (int u = 0; u < R; u++) {
         const int j = tid + u * NT;
         if (j < H) {
           a.conv_out[j] = x[u];
@@ -573,17 +653,29 @@ bool fused_gemv_fits(int H) {
   return H <= RB * 1024 && fused_lds_bytes(H, (int)cdiv((size_t)H, 16)) <= 60 * 1024;
 }
 
-template <int PRO, int NT>
-static syn_status_t launch_fused_nt(const ProArgs &a, const SplitGemv &g, hipStream_t s) {
-  GemvArgs ga{reinterpret_cast<const i32x4 *>(g.W), g.C, g.cs, g.acc};
+template <int PRO, int NT, bool GU = false>
+static syn_status_t launch_fused_nt(const ProArgs &a, const SplitGemv &g, hipStream_t s,
+                                    const GemvArgs *gu = nullptr) {
+  GemvArgs ga = gu ? *gu : GemvArgs{};
+  ga.W = reinterpret_cast<const i32x4 *>(g.W);
+  ga.C = g.C;
+  ga.cs = g.cs;
+  ga.acc = g.acc;
   const dim3 grid(g.N64 / 64, g.ks);
   const size_t shm = fused_lds_bytes(a.H, g.C);
-  switch (g.u) {
-    case 1: SYN_LAUNCH((k_fused_gemv<PRO, NT, 1>), grid, dim3(NT), shm, s, a, ga); break;
-    case 2: SYN_LAUNCH((k_fused_gemv<PRO, NT, 2>), grid, dim3(NT), shm, s, a, ga); break;
-    case 4: SYN_LAUNCH((k_fused_gemv<PRO, NT, 4>), grid, dim3(NT), shm, s, a, ga); break;
-    default: SYN_LAUNCH((k_fused_gemv<PRO, NT, 8>), grid, dim3(NT), shm, s, a, ga); break;
-  }
+  // R = prologue elements per thread: the fewest of {2, 4, 8} that cover H
+  auto go = [&](auto rc) {
+    constexpr int R = decltype(rc)::value;
+    switch (g.u) {
+      case 1: SYN_LAUNCH((k_fused_gemv<PRO, NT, 1, GU, R>), grid, dim3(NT), shm, s, a, ga); break;
+      case 2: SYN_LAUNCH((k_fused_gemv<PRO, NT, 2, GU, R>), grid, dim3(NT), shm, s, a, ga); break;
+      case 4: SYN_LAUNCH((k_fused_gemv<PRO, NT, 4, GU, R>), grid, dim3(NT), shm, s, a, ga); break;
+      default: SYN_LAUNCH((k_fused_gemv<PRO, NT, 8, GU, R>), grid, dim3(NT), shm, s, a, ga); break;
+    }
+  };
+  if (a.H <= 2 * NT) go(std::integral_constant<int, 2>{});
+  else if (a.H <= 4 * NT) go(std::integral_constant<int, 4>{});
+  else go(std::integral_constant<int, RB>{});
   SYN_LAUNCH_CHECK();
   return SYN_OK;
 }
@@ -684,146 +776,25 @@ syn_status_t launch_fused_swiglu_gemv(RowSrc gu, int inter, float *s_out, const 
 }
 
 // ------------------------------------------------------------------ gate|up + SwiGLU
-// x_mid = x + delta, RMSNorm, quantize (the PRO_NORM prologue), then for 16
-// rows j of the intermediate size both GEMVs over the whole K: gate row j
-// and up row inter + j of the stacked [gate | up] matrix, and the SwiGLU
-// epilogue h[j] = silu(gate_j) * up_j (int8.rs:500-503), each factor the
-// M <= 16 epilogue (f32(acc)*sx)*sw.  No K split, so a workgroup holds the
-// final values of its rows: SwiGLU runs once per element instead of once
-// per down-GEMV workgroup.  The workgroup's max |h| goes to hmax by an
-// atomic max of the f32 bits (|h| >= 0, so the bit order is the value
-// order; NaN is skipped as the reference quantizer's `if a > m` skips it),
-// so the down GEMV quantizes h without reducing it again.
-struct GuArgs {
-  const i32x4 *W;   // stacked [gate | up] rows, panel layout
-  const float *ws;  // per-row scales of the stacked rows
-  int C, inter;
-  float *h;
-  unsigned *hmax;
-  const uint64_t *exp_tab;
-};
-
-// 16 rows j per workgroup, 256 threads.  Load instruction t (of 2*CG, CG =
-// ceil(C/4) chunk groups per matrix) covers matrix t / CG (gate, up) and
-// chunks 4*(t % CG) .. +3 of the 16 rows: lane l reads row l % 16, chunk
-// 4*(t % CG) + l / 16 (four 256-byte runs of the panel layout).  Wave w
-// takes instructions w, w + 4, ...; the partial sums of a row meet over
-// lanes (xor 16, 32) and waves (LDS).
-constexpr int kGuRows = 16;
-
-// grid (ceil(inter / 16)); dynamic LDS: sq[round4(H)] floats | xq[C*16]
-template <int UI>
-__global__ void __launch_bounds__(256) k_gu_swiglu(ProArgs a, GuArgs g) {
-  constexpr int NT = 256, NW = NT / 64;
-  extern __shared__ __align__(16) unsigned char smem[];
-  __shared__ float red[64];
-  __shared__ int redi[2 * NW * kGuRows];
-  __shared__ uint64_t exp_tab[32];
-  const int H = a.H;
-  float *sq = reinterpret_cast<float *>(smem);
-  int8_t *xq = reinterpret_cast<int8_t *>(smem) + ((H + 3) & ~3) * 4;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int r = lane & (kGuRows - 1), cp = lane >> 4;
-  const int j0 = blockIdx.x * kGuRows;
-  const int jc = min(j0 + r, g.inter - 1);
-  const int CG = (g.C + 3) >> 2, T = 2 * CG;
-  SYN_TS_DECL
-  SYN_TS(0);
-  SYN_TSR(14);
-  const uint64_t tv = g.exp_tab[tid & 31];
-  const float wsg = g.ws[jc], wsu = g.ws[g.inter + jc];
-  i32x4 w[UI];
-  auto issue = [&]() {
-#pragma unroll
-    for (int i = 0; i < UI; i++) {
-      const int t = min(wave + i * NW, T - 1);
-      const int m = t >= CG, c = min(4 * (t - m * CG) + cp, g.C - 1);
-      const int row = m * g.inter + jc;
-      w[i] = __builtin_nontemporal_load(g.W + ((size_t)(row >> 6) * g.C + c) * 64 + (row & 63));
-    }
-    asm volatile("" ::: "memory");  // keep the weight requests ahead of the prologue
-  };
-  float x[RB], nwv[RB];
-  norm_prologue_load<NT>(a, H, x, nwv, issue);
-  SYN_TS(1);
-  if (tid < 32) exp_tab[tid] = tv;
-  for (int i = H + tid; i < g.C * 16; i += NT) xq[i] = 0;
-  const float sv = norm_quant<NT, false>(a.eps, H, x, nwv, sq, xq, red SYN_TS_PASS);
-  SYN_TS(2);
-  bar<NT>();
-  SYN_TS(3);
-  int ag = 0, au = 0;
-#pragma unroll
-  for (int i = 0; i < UI; i++) {
-    const int t = wave + i * NW;
-    if (t < T) {
-      const int m = t >= CG, c = 4 * (t - m * CG) + cp;
-      const i32x4 xv = *reinterpret_cast<const i32x4 *>(xq + min(c, g.C - 1) * 16);
-      int d = 0;
-      d = __builtin_amdgcn_sdot4(w[i].x, xv.x, d, false);
-      d = __builtin_amdgcn_sdot4(w[i].y, xv.y, d, false);
-      d = __builtin_amdgcn_sdot4(w[i].z, xv.z, d, false);
-      d = __builtin_amdgcn_sdot4(w[i].w, xv.w, d, false);
-      d = c < g.C ? d : 0;
-      if (m) au += d;
-      else ag += d;
-    }
-  }
-  SYN_TS(4);
-  ag += __shfl_xor(ag, 16);
-  au += __shfl_xor(au, 16);
-  ag += __shfl_xor(ag, 32);
-  au += __shfl_xor(au, 32);
-  if (lane < kGuRows) {
-    redi[wave * kGuRows + lane] = ag;
-    redi[(NW + wave) * kGuRows + lane] = au;
-  }
-  bar<NT>();
-  SYN_TS(5);
-  if (wave == 0) {
-    float m = 0.0f;
-    if (lane < kGuRows) {
-      int sg = 0, su = 0;
-#pragma unroll
-      for (int i = 0; i < NW; i++) {
-        sg += redi[i * kGuRows + lane];
-        su += redi[(NW + i) * kGuRows + lane];
-      }
-      const int j = j0 + lane;
-      if (j < g.inter) {
-        const float fg = (float)sg * sv, fu = (float)su * sv;
-        const float gv = fg * wsg, uv = fu * wsu;
-        const float act = syn_silu_tab(gv, exp_tab);
-        const float hv = act * uv;
-        g.h[j] = hv;
-        const float av = fabsf(hv);
-        if (av > m) m = av;
-      }
-    }
-    m = wave_max_nonneg(m);
-    if (lane == 0) atomicMax(g.hmax, __float_as_uint(m));
-  }
-  SYN_TS(6);
-  if (blockIdx.x == 0) {  // the residual row for the next layer, the scale
-    if (a.res_out) {
-#pragma unroll
-      for (int u = 0; u < RB; u++)
-        if (tid + u * NT < H) a.res_out[tid + u * NT] = x[u];
-    }
-    if (tid == 0) a.s_out[0] = sv;
-  }
-  SYN_TSR(15);
-  SYN_TS_FLUSH(112);
+// x_mid = x + delta (res_out, workgroup 0), RMSNorm, quantize (the PRO_NORM
+// prologue), then the gate|up GEMV split over K in pairs of panels (gate
+// rows 64p.., up rows inter + 64p..), the pair's last slice writing
+// h = silu(gate) * up and max |h| (k_fused_gemv with GU).  The down GEMV
+// then quantizes its K range of h with that max (PRO_HQ).
+bool gu_swiglu_fits(int H, int inter) {
+  return fused_gemv_fits(H) && H <= RB * 256 && inter > 0 && inter % 64 == 0;
 }
 
-bool gu_swiglu_fits(int H) { return H <= RB * 256; }
+SplitGemv plan_gu_pairs(const void *W, const float *ws, int inter, int C, int target_wg, int nt) {
+  return plan_split_gemv(W, ws, inter, C, target_wg, nt);
+}
 
 syn_status_t launch_gu_swiglu(const float *base, RowSrc delta, float *res_out, const float *nw,
-                              float eps, int H, float *s_out, const void *W, const float *ws,
-                              int C, int inter, float *h, unsigned *hmax, hipStream_t s) {
-  if (!gu_swiglu_fits(H) || inter <= 0 || C != (int)cdiv((size_t)H, 16)) {
-    set_error("gate|up SwiGLU GEMV: hidden size outside the kernel's limits");
+                              float eps, int H, float *s_out, const SplitGemv &g, const float *ws,
+                              int inter, int *cnt, float *h, unsigned *hmax, hipStream_t s) {
+  if (!gu_swiglu_fits(H, inter) || g.C != (int)cdiv((size_t)H, 16) || g.N64 != inter ||
+      (g.nt != 256 && g.nt != 512) || !g.acc || !cnt || !h || !hmax || !ws) {
+    set_error("gate|up SwiGLU GEMV: shapes outside the kernel's limits or plan not prepared");
     return SYN_ERR_INVALID_ARG;
   }
   ProArgs a{};
@@ -834,20 +805,19 @@ syn_status_t launch_gu_swiglu(const float *base, RowSrc delta, float *res_out, c
   a.eps = eps;
   a.H = H;
   a.s_out = s_out;
-  GuArgs g{reinterpret_cast<const i32x4 *>(W), ws, C, inter, h, hmax, exp_table_address()};
-  if (!g.exp_tab) {
+  GemvArgs gu{};
+  gu.pairs = inter / 64;
+  gu.cnt = cnt;
+  gu.ws = ws;
+  gu.h = h;
+  gu.hmax = hmax;
+  gu.exp_tab = exp_table_address();
+  if (!gu.exp_tab) {
     set_error("fused decode: expf table address unavailable");
     return SYN_ERR_HIP;
   }
-  const size_t shm = round_up((size_t)H, 4) * 4 + (size_t)g.C * 16;
-  const dim3 grid((unsigned)cdiv((size_t)inter, kGuRows));
-  const int ui = (int)cdiv(2 * cdiv((size_t)g.C, 4), 4);  // load instructions per wave
-  if (ui <= 2) SYN_LAUNCH((k_gu_swiglu<2>), grid, dim3(256), shm, s, a, g);
-  else if (ui <= 4) SYN_LAUNCH((k_gu_swiglu<4>), grid, dim3(256), shm, s, a, g);
-  else if (ui <= 8) SYN_LAUNCH((k_gu_swiglu<8>), grid, dim3(256), shm, s, a, g);
-  else SYN_LAUNCH((k_gu_swiglu<16>), grid, dim3(256), shm, s, a, g);
-  SYN_LAUNCH_CHECK();
-  return SYN_OK;
+  if (g.nt == 512) return launch_fused_nt<PRO_NORM, 512, true>(a, g, s, &gu);
+  return launch_fused_nt<PRO_NORM, 256, true>(a, g, s, &gu);
 }
 
 syn_status_t launch_fused_hq_gemv(const float *vec, const unsigned *hmax, int H, float *s_out,
@@ -1511,7 +1481,7 @@ __global__ void __launch_bounds__(1024)
   float t[RB];
 #pragma unroll
   for (int u = 0; u < RB; u++) t[u] = x[u] * nwv[u];
-  wg_max_post<NT>(local_absmax<NT>(t, H), red, 0);
+  wg_max_post<NT>(local_absmax<NT, RB>(t, H), red, 0);
   __syncthreads();
   const float ss = sumsq_chains<NT>(fsm, H, red);
   const float scale = 1.0f / sqrtf(ss / (float)H + eps);
@@ -1520,11 +1490,11 @@ __global__ void __launch_bounds__(1024)
   for (int u = 0; u < RB; u++) nv[u] = t[u] * scale;
   float mx = wg_max_get<NT>(red, 0) * scale;  // max|t*scale| = fl(max|t| * scale)
   if (!(mx <= 3.402823466e38f) || !(scale > 0.0f)) {
-    wg_max_post<NT>(local_absmax<NT>(nv, H), red, 16);
+    wg_max_post<NT>(local_absmax<NT, RB>(nv, H), red, 16);
     __syncthreads();
     mx = wg_max_get<NT>(red, 16);
   }
-  const float sv = quantize_regs_with_max<NT>(nv, H, mx, xq);
+  const float sv = quantize_regs_with_max<NT, RB>(nv, H, mx, xq);
   if (tid == 0) s_out[0] = sv;
 }
 

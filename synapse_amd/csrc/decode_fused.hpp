@@ -81,14 +81,18 @@ syn_status_t launch_fused_quant_gemv(const float *vec, int H, float *s_out, cons
 // h = silu(gate) * up from the stacked [gate | up] rows ; xq = q8(h) ; acc += xq . W
 syn_status_t launch_fused_swiglu_gemv(RowSrc gu, int inter, float *s_out, const SplitGemv &g,
                                       hipStream_t s);
-// x_mid = x + delta (res_out, workgroup 0); xq = q8(rmsnorm(x_mid));
-// h = silu(gate) * up over whole rows of the stacked [gate | up] matrix W
-// (int8 panel layout, 2*inter rows of C = ceil(H/16) chunks); hmax = max |h|
-// as f32 bits (atomic max; zero before the step); s_out = xq's scale
+// x_mid = x + delta (res_out, workgroup 0); xq = q8(rmsnorm(x_mid)); the
+// stacked [gate | up] GEMV (int8 panel layout, 2*inter rows) split over K in
+// pairs of panels (gate panel p with up panel inter/64 + p; g planned by
+// plan_gu_pairs, g.acc the 2*inter int32 accumulators, zero before the
+// step); the pair's last slice writes h = silu(gate) * up and folds max |h|
+// into hmax (f32 bits, atomic max; zero before the step); cnt[inter/64]
+// counters, zero before the step and left zero; s_out = xq's scale
 syn_status_t launch_gu_swiglu(const float *base, RowSrc delta, float *res_out, const float *nw,
-                              float eps, int H, float *s_out, const void *W, const float *ws,
-                              int C, int inter, float *h, unsigned *hmax, hipStream_t s);
-bool gu_swiglu_fits(int H);
+                              float eps, int H, float *s_out, const SplitGemv &g, const float *ws,
+                              int inter, int *cnt, float *h, unsigned *hmax, hipStream_t s);
+bool gu_swiglu_fits(int H, int inter);
+SplitGemv plan_gu_pairs(const void *W, const float *ws, int inter, int C, int target_wg, int nt);
 // xq = q8(vec) over this split's K range with the max *hmax reduced
 // elsewhere ; s_out ; acc += xq . W
 syn_status_t launch_fused_hq_gemv(const float *vec, const unsigned *hmax, int H, float *s_out,

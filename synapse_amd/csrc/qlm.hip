@@ -30,6 +30,8 @@ namespace syn {
 struct QLayer {
   QLinearInt8 qkv, o, gu, down;
   SplitGemv f_qkv, f_o, f_gu, f_down;  // fused decode plans over these weights
+  SplitGemv f_gup;                      // gate|up as pairs of panels (launch_gu_swiglu)
+  int *gu_cnt = nullptr;                // its per-pair arrival counters
 };
 
 }  // namespace syn
@@ -260,16 +262,28 @@ struct syn_hip_qlm_s {
     int dev = 0;
     if (hipGetDevice(&dev) == hipSuccess)
       (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    // grids of about half a workgroup per CU: every workgroup repeats the
+    // prologue (the RMSNorm chains read the whole row), and at the Qwen3
+    // shape the QKV kernel measured 4.87 us on 256 workgroups against 5.68
+    // on 512, gate|up 7.51 on 192 pairs' slices against 8.13 on 384 (a
+    // quarter of the CUs: 5.39 and 7.83); O and down did not change
+    const int target = std::max(1, cus / 2);
     size_t per_layer = 0;
     for (auto &Ly : layers) {
       Ly.f_qkv = plan_split_gemv(Ly.qkv.w.p, Ly.qkv.scales.as<float>(), (int)n_qkv,
-                                 Ly.qkv.chunks, cus, 256);
-      Ly.f_o = plan_split_gemv(Ly.o.w.p, Ly.o.scales.as<float>(), (int)h, Ly.o.chunks, cus, 256);
+                                 Ly.qkv.chunks, target, 256);
+      Ly.f_o =
+          plan_split_gemv(Ly.o.w.p, Ly.o.scales.as<float>(), (int)h, Ly.o.chunks, target, 256);
       Ly.f_gu = plan_split_gemv(Ly.gu.w.p, Ly.gu.scales.as<float>(), (int)(2 * inter),
-                                Ly.gu.chunks, cus, 256);
+                                Ly.gu.chunks, target, 256);
       Ly.f_down = plan_split_gemv(Ly.down.w.p, Ly.down.scales.as<float>(), (int)h,
-                                  Ly.down.chunks, cus, 512);
+                                  Ly.down.chunks, target, 512);
       per_layer = (size_t)Ly.f_qkv.N64 + Ly.f_o.N64 + Ly.f_gu.N64 + Ly.f_down.N64;
+      if (gu_swiglu_fits((int)h, (int)inter)) {
+        Ly.f_gup = plan_gu_pairs(Ly.gu.w.p, Ly.gu.scales.as<float>(), (int)inter, Ly.gu.chunks,
+                                 target, 256);
+        per_layer += round_up(inter / 64, 64);  // the pairs' arrival counters
+      }
     }
     // then one max |h| slot per layer for the gate|up SwiGLU kernel
     acc_elems = per_layer * L + round_up(L, 64);
@@ -280,6 +294,11 @@ struct syn_hip_qlm_s {
       for (int i = 0; i < 4; i++) {
         g[i]->acc = p;
         p += g[i]->N64;
+      }
+      if (gu_swiglu_fits((int)h, (int)inter)) {
+        Ly.f_gup.acc = Ly.f_gu.acc;  // the 2*inter gate|up accumulators
+        Ly.gu_cnt = p;
+        p += round_up(inter / 64, 64);
       }
     }
     return SYN_OK;
@@ -316,15 +335,16 @@ struct syn_hip_qlm_s {
       SYN_TRY(trace_begin(s));
       SYN_TRY(launch_fused_quant_gemv(attn.as<float>(), (int)qd, s_o, Ly.f_o, s));
       SYN_TRY(trace_end(SYN_HIP_STEP_O, s));
-      if (gu_swiglu_fits((int)h)) {
-        // gate|up over whole rows with the SwiGLU epilogue, then the down
-        // GEMV quantizes only its K range of h with the published max
+      if (gu_swiglu_fits((int)h, (int)inter)) {
+        // gate|up split over K in pairs of panels with the SwiGLU epilogue in
+        // each pair's last slice, then the down GEMV quantizes only its K
+        // range of h with the published max
         unsigned *hmax = reinterpret_cast<unsigned *>(acc.as<int>() + acc_elems) -
                          round_up(L, 64) + l;
         SYN_TRY(trace_begin(s));
         SYN_TRY(launch_gu_swiglu(xin.as<float>(), Ly.f_o.rows(s_o), xmid.as<float>(), fn(l), eps,
-                                 (int)h, s_gu, Ly.gu.w.p, Ly.gu.scales.as<float>(), Ly.gu.chunks,
-                                 (int)inter, gu.as<float>(), hmax, s));
+                                 (int)h, s_gu, Ly.f_gup, Ly.gu.scales.as<float>(), (int)inter,
+                                 Ly.gu_cnt, gu.as<float>(), hmax, s));
         SYN_TRY(trace_end(SYN_HIP_STEP_GATE_UP, s));
         SYN_TRY(trace_begin(s));
         SYN_TRY(launch_fused_hq_gemv(gu.as<float>(), hmax, (int)inter, s_down, Ly.f_down, s));
