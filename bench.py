@@ -53,10 +53,14 @@ LM_HEAD_WRITE_KIB, LM_HEAD_WRITE_FACTOR = 816.5, 262144.0 / 262144.0
 # HBM traffic per launch of the step's kernels: median FETCH_SIZE and
 # WRITE_SIZE (KiB per dispatch) over the 364 dispatches of each kernel in two
 # counter runs of eager steps at positions 16-29, scaled as above (readings
-# and commands in profiles/qwen3_int8_decode_step_kernels_traffic.md; the
-# attention's traffic grows with the position)
-_STEP_KIB = {"qkv": (2172.0, 132.0), "attention": (655.2, 32.0), "o": (1083.5, 128.0),
-             "gate_up": (3247.5, 22.0), "down": (1605.0, 96.0)}
+# and commands in profiles/qwen3_int8_decode_step_kernels_traffic.md, taken
+# on the kernels of this source tree; the attention's traffic grows with the
+# position).  These are recorded readings, reported as `traffic` with
+# `traffic_source` naming the profile: re-run its commands when a step
+# kernel changes.
+TRAFFIC_SOURCE = "profiles/qwen3_int8_decode_step_kernels_traffic.md (recorded rocprofv3 --pmc)"
+_STEP_KIB = {"qkv": (2159.6, 68.0), "attention": (647.5, 32.0), "o": (1084.0, 64.0),
+             "gate_up": (3204.5, 145.0), "down": (1605.5, 48.0)}
 STEP_KERNEL_TRAFFIC = {k: round(1024 * (f * LM_HEAD_FETCH_FACTOR + w * LM_HEAD_WRITE_FACTOR))
                        for k, (f, w) in _STEP_KIB.items()}
 
@@ -83,12 +87,12 @@ def step_kernel_bytes(c, pos):
 
 
 STEP_KERNEL_NAMES = {
-    "qkv": "k_fused_gemv<0,256,U> (residual + RMSNorm + quantize + QKV GEMV)",
+    "qkv": "k_fused_gemv<0,256,U,false,R> (residual + RMSNorm + quantize + QKV GEMV)",
     "attention": "k_attn_head<false,128> (head norms, RoPE, KV append, attention)",
-    "o": "k_fused_gemv<1,256,U> (quantize + O GEMV)",
-    "gate_up": "k_fused_gemv<0,256,U,true> (residual + RMSNorm + quantize + gate|up GEMV in "
+    "o": "k_fused_gemv<1,256,U,false,R> (quantize + O GEMV)",
+    "gate_up": "k_fused_gemv<0,256,U,true,R> (residual + RMSNorm + quantize + gate|up GEMV in "
                "panel pairs, split K, SwiGLU in each pair's last slice)",
-    "down": "k_fused_gemv<5,512,U> (quantize h range + down GEMV)",
+    "down": "k_fused_gemv<5,512,U,false,R> (quantize h range + down GEMV)",
     "lm_head": "k_lmhead_top2<8,8> (lm_head GEMV + per-panel top-2)"}
 
 
@@ -534,6 +538,8 @@ def main():
               "traffic": None if args.unfused else round(
                   1024 * (LM_HEAD_FETCH_KIB * LM_HEAD_FETCH_FACTOR
                           + LM_HEAD_WRITE_KIB * LM_HEAD_WRITE_FACTOR)),
+              "traffic_source": None if args.unfused else
+                  "profiles/lm_head_int8_qwen3_k_lmhead_top2.md (recorded rocprofv3 --pmc)",
               "avg_launch_us": round(lm_ms * 1e3, 2), "bytes_per_launch": lm_head_bytes(QWEN3),
               "timing": "hipEvent pair around back-to-back launches alternating two weight "
                         "copies (2 x 156 MB > the 256 MB Infinity Cache)"}
@@ -549,7 +555,8 @@ def main():
         line["roofline"] = {
             "bound": "hbm", "kernel": STEP_KERNEL_NAMES[dom], "achieved": d["gb_s"],
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": d["hbm_frac"],
-            "traffic": STEP_KERNEL_TRAFFIC.get(dom), "avg_launch_us": d["avg_us"],
+            "traffic": STEP_KERNEL_TRAFFIC.get(dom), "traffic_source": TRAFFIC_SOURCE,
+            "avg_launch_us": d["avg_us"],
             "bytes_per_launch": d["bytes_per_launch"],
             "share_of_step": round(d["us_per_step"] / (ms_per_step * 1e3), 4),
             "timing": "start/stop hipEvents of every launch (hipExtLaunchKernelGGL: the "

@@ -638,6 +638,16 @@ syn_status_t syn_hip_probe_hbm_read(size_t bytes, double *gb_s);
  * out3[0] = one lane's chain, out3[1] = the wave-cooperative chain of the
  * Mamba norms, out3[2] = that chain's clocks (a check of the summation order). */
 syn_status_t syn_hip_probe_seq_sum(const float *host, size_t n, float *out3);
+/* What ordering the decode step's dependency levels costs: the graph replay
+   of n dependent tiny kernels of `wgs` workgroups (us per kernel), and nbar
+   grid barriers among `wgs` <= CU-count co-resident workgroups of one
+   cooperative launch (mode 0: one arrival counter; mode 1: eight counters
+   and a top counter), us per barrier; every wait is bounded and a timed-out
+   wait is counted in *timeouts instead of hanging.  No reference
+   counterpart (harness measurements). */
+syn_status_t syn_hip_probe_graph_floor(int n, int wgs, double *us_per_kernel);
+syn_status_t syn_hip_probe_grid_barrier(int wgs, int mode, int nbar, double *us_per_barrier,
+                                        int *timeouts);
 /* SplitMix64 + Box-Muller (f64, cast to f32) into host memory. */
 syn_status_t syn_hip_fill_normal(float *host_dst, size_t n, uint64_t seed, float stddev);
 

@@ -2,6 +2,9 @@
 // no reference counterpart): dense MFMA loops for f16 and i8, and an HBM
 // streaming read.  The roofline fractions the benchmark reports use the
 // published peaks; these give the measured ceilings beside them.
+#include <algorithm>
+#include <vector>
+
 #include "common.hpp"
 #include "reduce_order.hpp"
 
@@ -224,5 +227,146 @@ extern "C" syn_status_t syn_hip_probe_hbm_read(size_t bytes, double *gb_s) {
   (void)hipEventDestroy(a);
   (void)hipEventDestroy(b);
   *gb_s = (double)bytes / ((double)best * 1e-3) / 1e9;
+  return SYN_OK;
+}
+
+// ---------------------------------------------------------------- step structure
+// What a dependency level of the decode step costs when it is a kernel
+// boundary, and what it would cost as a grid barrier inside one persistent
+// kernel (the two ways to order the step's stages).
+namespace syn {
+
+__global__ void k_probe_tiny(float *out, int i) {
+  if (threadIdx.x == 0) out[blockIdx.x] = (float)i;
+}
+
+// mode 0: one arrival counter, the last arrival publishes the generation,
+// the others poll it with device-scope atomic reads; mode 1: eight arrival
+// counters (by workgroup id), their last arrivals count on a top counter,
+// whose last arrival publishes; everyone polls with a short sleep.  Every
+// poll gives up after a bounded number of tries (counted in *timeouts, and
+// the workgroup leaves), so a wait cannot hang the GPU.
+__global__ void k_probe_barrier(unsigned *cnt, int nbar, int mode, unsigned *timeouts,
+                                unsigned long long *ts) {
+  const unsigned G = gridDim.x;
+  __shared__ unsigned s_stop;
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+  for (int b = 0; b < nbar; b++) {
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const unsigned target = (unsigned)(b + 1);
+      bool late = false;
+      bool arrive_top = true;
+      if (mode == 1) {
+        const unsigned grp = blockIdx.x & 7, gsz = (G - grp + 7) / 8;
+        const unsigned old = __hip_atomic_fetch_add(cnt + 128 + 64 * grp, 1u, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+        arrive_top = old == target * gsz - 1;
+      }
+      const unsigned need = mode == 1 ? 8u : G;
+      if (arrive_top) {
+        const unsigned o2 =
+            __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (o2 == target * need - 1)
+          __hip_atomic_exchange(cnt + 64, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+      for (long n = 0;; n++) {
+        const unsigned g = __hip_atomic_fetch_or(cnt + 64, 0u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT);
+        if (g >= target) break;
+        if (mode == 1) __builtin_amdgcn_s_sleep(1);
+        if (n > 200000) {
+          late = true;
+          break;
+        }
+      }
+      if (late) atomicAdd(timeouts, 1u);
+      s_stop = late ? 1u : 0u;
+    }
+    __syncthreads();
+    if (s_stop) return;
+  }
+  const unsigned long long t1 = __builtin_amdgcn_s_memrealtime();
+  if (threadIdx.x == 0) {
+    ts[2 * blockIdx.x] = t0;
+    ts[2 * blockIdx.x + 1] = t1;
+  }
+}
+
+}  // namespace syn
+
+// Graph replay of n dependent tiny kernels of `wgs` workgroups: us per kernel.
+extern "C" syn_status_t syn_hip_probe_graph_floor(int n, int wgs, double *us_per_kernel) {
+  if (!us_per_kernel) return SYN_ERR_NULL_PTR;
+  if (n < 1 || n > 4096 || wgs < 1 || wgs > 65536) return SYN_ERR_INVALID_ARG;
+  SYN_TRY(ensure_init());
+  hipStream_t s;
+  SYN_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+  DevBuf out;
+  SYN_TRY(out.alloc((size_t)wgs * 4));
+  hipGraph_t g;
+  hipGraphExec_t ge = nullptr;
+  SYN_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+  for (int i = 0; i < n; i++)
+    hipLaunchKernelGGL(k_probe_tiny, dim3(wgs), dim3(256), 0, s, out.as<float>(), i);
+  SYN_HIP(hipStreamEndCapture(s, &g));
+  hipError_t e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (e != hipSuccess) return hip_fail(e, "hipGraphInstantiate", __FILE__, __LINE__);
+  hipEvent_t a, b;
+  SYN_HIP(hipEventCreate(&a));
+  SYN_HIP(hipEventCreate(&b));
+  for (int w = 0; w < 3; w++) SYN_HIP(hipGraphLaunch(ge, s));
+  SYN_HIP(hipEventRecord(a, s));
+  const int reps = 20;
+  for (int r = 0; r < reps; r++) SYN_HIP(hipGraphLaunch(ge, s));
+  SYN_HIP(hipEventRecord(b, s));
+  SYN_HIP(hipEventSynchronize(b));
+  float ms = 0.0f;
+  SYN_HIP(hipEventElapsedTime(&ms, a, b));
+  *us_per_kernel = (double)ms * 1e3 / ((double)reps * n);
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  (void)hipGraphExecDestroy(ge);
+  (void)hipStreamDestroy(s);
+  return SYN_OK;
+}
+
+// nbar grid barriers among `wgs` co-resident workgroups (cooperative launch):
+// us per barrier, from the first workgroup's start to the last one's end
+extern "C" syn_status_t syn_hip_probe_grid_barrier(int wgs, int mode, int nbar,
+                                                   double *us_per_barrier, int *timeouts) {
+  if (!us_per_barrier || !timeouts) return SYN_ERR_NULL_PTR;
+  if (wgs < 8 || nbar < 1 || nbar > 100000 || (mode != 0 && mode != 1))
+    return SYN_ERR_INVALID_ARG;
+  SYN_TRY(ensure_init());
+  int dev = 0, cus = 0;
+  SYN_HIP(hipGetDevice(&dev));
+  SYN_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+  if (wgs > cus) return SYN_ERR_INVALID_ARG;  // one workgroup per CU: all co-resident
+  DevBuf cnt, to, ts;
+  SYN_TRY(cnt.alloc(4096 * 4));
+  SYN_TRY(to.alloc(4));
+  SYN_TRY(ts.alloc((size_t)wgs * 16));
+  SYN_HIP(hipMemset(cnt.p, 0, cnt.bytes));
+  SYN_HIP(hipMemset(to.p, 0, 4));
+  SYN_HIP(hipDeviceSynchronize());
+  unsigned *pc = cnt.as<unsigned>(), *pt = to.as<unsigned>();
+  unsigned long long *pts = ts.as<unsigned long long>();
+  void *args[] = {&pc, &nbar, &mode, &pt, &pts};
+  SYN_HIP(hipLaunchCooperativeKernel((const void *)k_probe_barrier, dim3(wgs), dim3(256), args,
+                                     0, default_stream()));
+  SYN_HIP(hipStreamSynchronize(default_stream()));
+  std::vector<unsigned long long> h((size_t)wgs * 2);
+  SYN_HIP(hipMemcpy(h.data(), ts.p, h.size() * 8, hipMemcpyDeviceToHost));
+  unsigned ht = 0;
+  SYN_HIP(hipMemcpy(&ht, to.p, 4, hipMemcpyDeviceToHost));
+  unsigned long long lo = ~0ull, hi = 0;
+  for (int i = 0; i < wgs; i++) {
+    lo = std::min(lo, h[2 * i]);
+    hi = std::max(hi, h[2 * i + 1]);
+  }
+  *timeouts = (int)ht;
+  *us_per_barrier = ht ? 0.0 : (double)(hi - lo) * 0.01 / nbar;  // s_memrealtime: 100 MHz
   return SYN_OK;
 }

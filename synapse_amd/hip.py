@@ -195,6 +195,9 @@ SIGNATURES = {
     "syn_hip_probe_mfma": (ST, [C.c_int, SZ, C.POINTER(C.c_double)]),
     "syn_hip_probe_hbm_read": (ST, [SZ, C.POINTER(C.c_double)]),
     "syn_hip_probe_seq_sum": (ST, [P, SZ, P]),
+    "syn_hip_probe_graph_floor": (ST, [C.c_int, C.c_int, C.POINTER(C.c_double)]),
+    "syn_hip_probe_grid_barrier": (ST, [C.c_int, C.c_int, C.c_int, C.POINTER(C.c_double),
+                                        C.POINTER(C.c_int)]),
     "syn_hip_eval_expf": (ST, [P, P, SZ, P]),
     "syn_hip_kquant_encode": (ST, [C.c_int, SZ, SZ, P, P]),
     "syn_hip_kquant_decode": (ST, [C.c_int, SZ, P, P]),
@@ -1143,6 +1146,21 @@ def probe_seq_sum(values):
     out = np.zeros(3, np.float32)
     check(lib().syn_hip_probe_seq_sum(ptr(v), v.size, ptr(out)), "probe_seq_sum")
     return float(out[0]), float(out[1]), float(out[2])
+
+
+def probe_graph_floor(n: int = 140, wgs: int = 256) -> float:
+    """us per kernel of a graph replay of n dependent tiny kernels"""
+    v = C.c_double()
+    check(lib().syn_hip_probe_graph_floor(n, wgs, C.byref(v)), "probe_graph_floor")
+    return v.value
+
+
+def probe_grid_barrier(wgs: int, mode: int, nbar: int = 200):
+    """(us per grid barrier, timed-out waits) inside one cooperative launch"""
+    v, t = C.c_double(), C.c_int()
+    check(lib().syn_hip_probe_grid_barrier(wgs, mode, nbar, C.byref(v), C.byref(t)),
+          "probe_grid_barrier")
+    return v.value, t.value
 
 
 def probe_hbm_read(nbytes: int = 4 << 30) -> float:

@@ -263,6 +263,14 @@ if __name__ == "__main__":
         ms = copy_calibration(n)
         print(json.dumps({"copy_bytes": n, "ms": round(ms, 4),
                           "gb_s_read_plus_write": round(2 * n / (ms * 1e-3) / 1e9, 1)}))
+    elif len(a) == 1 and a[0] == "sync":  # what a dependency level of the step costs
+        rec = {"graph_kernel_us": {w: round(hip.probe_graph_floor(140, w), 3)
+                                   for w in (32, 256, 512)}}
+        for mode in (0, 1):
+            for w in (64, 128, 256):
+                us, to = hip.probe_grid_barrier(w, mode, 200)
+                rec[f"barrier_mode{mode}_{w}wg_us"] = round(us, 3) if not to else f"{to} timeouts"
+        print(json.dumps(rec))
     elif len(a) == 4 and a[0] == "gemv":  # gemv FMT N K
         print(json.dumps(gemv_record(FMT_BY_NAME[a[1]], int(a[2]), int(a[3]), "gemv")))
     elif len(a) == 5 and a[0] == "gemm":  # gemm FMT M N K
@@ -270,6 +278,6 @@ if __name__ == "__main__":
     elif len(a) in (2, 3) and a[0] in ("klm", "mamba-ref", "mamba-int8", "hlm", "hlm-op"):  # DECODER STEPS [eager]
         print(json.dumps(_decoder_run(a[0], int(a[1]), graph=not (len(a) == 3 and a[2] == "eager"))))
     else:
-        print("usage: python -m synapse_amd.microbench copy NBYTES | gemv FMT N K | "
+        print("usage: python -m synapse_amd.microbench copy NBYTES | sync | gemv FMT N K | "
               "gemm FMT M N K | {klm,mamba-ref,mamba-int8,hlm,hlm-op} STEPS [eager]", file=sys.stderr)
         sys.exit(2)
