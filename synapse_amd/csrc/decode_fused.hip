@@ -29,105 +29,40 @@
 #include <algorithm>
 #include <type_traits>
 
-#include "decode_fused.hpp"
-#include "phase_ts.hpp"
+#include "fused_dev.hpp"
 #include "linear.hpp"
-#include "reduce_order.hpp"
 
 namespace syn {
 
 #ifdef SYN_PHASE_TIMING
 static __device__ unsigned long long syn_phase_ts[256];
 #define SYN_TS_FLUSH(base) SYN_TS_FLUSH_TO(syn_phase_ts, base)
+// timeline of the step: workgroup (0, 0) of every kernel appends (kind,
+// entry, exit) in s_memrealtime ticks (100 MHz)
+static __device__ unsigned long long syn_tl[3 * 8192];
+static __device__ unsigned syn_tl_n;
+#define SYN_TL_ENTER() const unsigned long long syn_tl_e_ = __builtin_amdgcn_s_memrealtime()
+#define SYN_TL_EXIT(kind)                                                          \
+  do {                                                                             \
+    if (blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) {                  \
+      const unsigned i_ = atomicAdd(&syn_tl_n, 1u);                                \
+      if (i_ < 8192) {                                                             \
+        syn_tl[3 * i_] = (kind);                                                   \
+        syn_tl[3 * i_ + 1] = syn_tl_e_;                                            \
+        syn_tl[3 * i_ + 2] = __builtin_amdgcn_s_memrealtime();                     \
+      }                                                                            \
+    }                                                                              \
+  } while (0)
 #else
 #define SYN_TS_FLUSH(base) SYN_TS_FLUSH_TO(unused, base)
+#define SYN_TL_ENTER() \
+  do {                 \
+  } while (0)
+#define SYN_TL_EXIT(kind) \
+  do {                    \
+  } while (0)
 #endif
 
-// ------------------------------------------------------------------ helpers
-
-// Rows of a prologue vector held per thread: element j = threadIdx.x + u*NT.
-constexpr int RB = 8;
-
-// One step of a wave max over non-negative values through a DPP lane move;
-// lanes whose source is outside the row/wave read 0, which max ignores.
-template <int CTRL>
-__device__ __forceinline__ float dpp_fmax(float v) {
-  const int s = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true);
-  return fmaxf(v, __int_as_float(s));
-}
-
-// max over the 64 lanes of non-negative values: row_shr 1/2/4/8 leave each
-// row's max in its lane 15, row_bcast 15/31 carry them to lane 63
-__device__ __forceinline__ float wave_max_nonneg(float v) {
-  v = dpp_fmax<0x111>(v);
-  v = dpp_fmax<0x112>(v);
-  v = dpp_fmax<0x114>(v);
-  v = dpp_fmax<0x118>(v);
-  v = dpp_fmax<0x142>(v);
-  v = dpp_fmax<0x143>(v);
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-
-// Workgroup max of non-negative values, first half: each wave leaves its max
-// in red[slot + wave].  The caller's next barrier publishes it.
-template <int NT>
-__device__ __forceinline__ void wg_max_post(float v, float *red, int slot) {
-  v = wave_max_nonneg(v);
-  if ((threadIdx.x & 63) == 0) red[slot + (threadIdx.x >> 6)] = v;
-}
-
-// second half (after a barrier)
-template <int NT>
-__device__ __forceinline__ float wg_max_get(const float *red, int slot) {
-  float m = red[slot];
-#pragma unroll
-  for (int i = 1; i < NT / 64; i++) m = fmaxf(m, red[slot + i]);
-  return m;
-}
-
-// quantizePerChannelInt8 (quantize.zig:12-47) of a row held in registers
-// (element j = threadIdx.x + u*NT, valid for j < n), given the row's max|v|:
-// writes q[j] and returns the row scale.
-template <int NT, int R>
-__device__ float quantize_regs_with_max(const float (&v)[R], int n, float mx, int8_t *q) {
-  if (mx == 0.0f) {
-#pragma unroll
-    for (int u = 0; u < R; u++)
-      if (threadIdx.x + u * NT < n) q[threadIdx.x + u * NT] = 0;
-    return 1.0f;
-  }
-  const float inv = 127.0f / mx;
-#pragma unroll
-  for (int u = 0; u < R; u++) {
-    const int j = threadIdx.x + u * NT;
-    if (j < n) {
-      float r = roundf(v[u] * inv);
-      r = fminf(127.0f, fmaxf(-127.0f, r));
-      q[j] = (int8_t)(int)r;
-    }
-  }
-  return mx / 127.0f;
-}
-
-// per-thread max|v[u]| over its valid elements (the reference's `if a > m`)
-template <int NT, int R>
-__device__ __forceinline__ float local_absmax(const float (&v)[R], int n) {
-  float mx = 0.0f;
-#pragma unroll
-  for (int u = 0; u < R; u++) {
-    const float a = fabsf(v[u]);
-    if (threadIdx.x + u * NT < n && a > mx) mx = a;
-  }
-  return mx;
-}
-
-// the whole quantizer: workgroup max (one barrier), then quantize_regs_with_max
-template <int NT, int R>
-__device__ float quantize_regs(const float (&v)[R], int n, int8_t *q, float *red, int slot) {
-  wg_max_post<NT>(local_absmax<NT, R>(v, n), red, slot);
-  bar<NT>();
-  return quantize_regs_with_max<NT, R>(v, n, wg_max_get<NT>(red, slot), q);
-}
 
 // device address of the expf table (per device; resolved once)
 const uint64_t *exp_table_address() {
@@ -142,191 +77,6 @@ const uint64_t *exp_table_address() {
   return addr[dev];
 }
 
-// ------------------------------------------------------------------ split-K GEMV
-// PRO_NORM: residual + RMSNorm (sum of squares in the 4-chain order of
-// ops/norm.rs) + quantize; PRO_MNORM: the same with one sequential sum of
-// squares (pure_rust_ops.rs:96-112, the Mamba blocks' norm); PRO_QUANT:
-// quantize an f32 vector; PRO_SWIGLU: silu(gate) * up of GEMV rows, then
-// quantize; PRO_ROWS: quantize GEMV rows (RowSrc values); PRO_HQ: quantize
-// this split's K range of an f32 vector whose max |v| another kernel has
-// already reduced (hmax); PRO_CONV: the Mamba block's conv1d step + SiLU of
-// GEMV rows over a 4-tap ring state (int8_mamba.rs:43-56), then quantize
-enum {
-  PRO_NORM = 0,
-  PRO_QUANT = 1,
-  PRO_SWIGLU = 2,
-  PRO_MNORM = 3,
-  PRO_ROWS = 4,
-  PRO_HQ = 5,
-  PRO_CONV = 6
-};
-
-struct ProArgs {
-  // PRO_NORM: x = (base ? base : embed[st->token]) + delta
-  const float *base;
-  const float *embed;
-  const StepState *st;
-  int vocab;
-  RowSrc delta;
-  float *res_out;
-  const float *nw;
-  const float *zero_row;  // H zeros (the embedding row of an id >= vocab)
-  float eps;
-  // PRO_QUANT, PRO_HQ (with hmax = max |vec| as f32 bits)
-  const float *vec;
-  const unsigned *hmax;
-  // PRO_ROWS
-  RowSrc rows;
-  // PRO_SWIGLU, PRO_CONV; exp_tab = device address of syn_exp2_tab, passed as a plain
-  // pointer so its load is ordered like any other (a __constant__ load may be
-  // moved behind the weight loads)
-  RowSrc gu;
-  const uint64_t *exp_tab;
-  // PRO_CONV: rows (the new inputs), ring [H][4] (slot p % 4 holds the input
-  // of position p), conv weights [H][4] and bias, conv_out = the conv + SiLU
-  // values (workgroup 0, with the new ring slot)
-  float *ring;
-  const float *conv_w, *conv_b;
-  float *conv_out;
-  // all: prologue vector length (the GEMV's K) and the scale output
-  int H;
-  float *s_out;
-};
-
-struct GemvArgs {
-  const i32x4 *W;
-  int C, cs;
-  int *acc;
-  // gate|up pairs (GU kernels): grid panel p covers gate panel p and up
-  // panel `pairs` + p of the stacked [gate | up] matrix; cnt[p] counts the
-  // arrived K slices of pair p; the pair's last slice writes h = silu(gate)
-  // * up for its 64 rows (ws: the stacked rows' scales) and max |h| to hmax
-  int pairs = 0;
-  int *cnt = nullptr;
-  const float *ws = nullptr;
-  float *h = nullptr;
-  unsigned *hmax = nullptr;
-  const uint64_t *exp_tab = nullptr;
-};
-
-// ------------------------------------------------------------------ prologue parts
-// PRO_NORM / PRO_MNORM loads: x = (base | embed row of st->token | zero row)
-// + delta rows, the norm gains; issue() is called once these are requested,
-// so the caller's weight loads queue behind them (element j = tid + u*NT,
-// clamped to H-1)
-template <int NT, int R, class Issue>
-__device__ __forceinline__ void norm_prologue_load(const ProArgs &a, int H, float (&x)[R],
-                                                   float (&nwv)[R], Issue issue) {
-  const int tid = threadIdx.x;
-  const float *src = a.base;
-  if (!src) {
-    const uint32_t tok = a.st->token;
-    src = tok < (uint32_t)a.vocab ? a.embed + (size_t)tok * H : a.zero_row;
-  }
-#pragma unroll
-  for (int u = 0; u < R; u++) {
-    const int j = min(tid + u * NT, H - 1);
-    x[u] = src[j];
-    nwv[u] = a.nw[j];
-  }
-  // without a delta the loads below read the norm gains instead (in-bounds,
-  // values unused), so that no load sits behind a branch
-  const bool has_delta = a.delta.acc != nullptr;
-  const int *dacc = has_delta ? a.delta.acc : reinterpret_cast<const int *>(a.nw);
-  const float *dws = has_delta ? a.delta.ws : a.nw;
-  const float *dsxp = has_delta ? a.delta.sx : a.nw;
-  int da[R];
-  float dw[R];
-#pragma unroll
-  for (int u = 0; u < R; u++) {
-    const int j = min(tid + u * NT, H - 1);
-    da[u] = dacc[j];
-    dw[u] = dws[j];
-  }
-  const float dsx = dsxp[0];
-  issue();
-  if (has_delta) {
-#pragma unroll
-    for (int u = 0; u < R; u++) {
-      const float f = (float)da[u] * dsx;
-      const float d = f * dw[u];
-      x[u] = x[u] + d;
-    }
-  }
-}
-
-// RMSNorm (ops/norm.rs:8-38): out = (x*w) * (1/sqrt(sumsq/n + eps)), then
-// the quantizer's max|out|; returns the row scale with xq[0..H) written.
-// Scaling by the positive `scale` is a monotonic rounding, so max|t*scale|
-// = fl(max|t| * scale): the max of t = x*w is reduced while lanes 0-3 run
-// the sum-of-squares chains (or lane 0 the single sequential sum, SEQ).
-// sq: LDS, round4(H) floats.
-template <int NT, int R, bool SEQ>
-__device__ float norm_quant(float eps, int H, const float (&x)[R], const float (&nwv)[R],
-                            float *sq, int8_t *xq, float *red SYN_TS_PARAM) {
-  const int tid = threadIdx.x;
-  float t[R];
-#pragma unroll
-  for (int u = 0; u < R; u++) {
-    const int j = tid + u * NT;
-    if (j < H) sq[SEQ ? j : sq_slot(j, H)] = x[u] * x[u];
-    t[u] = x[u] * nwv[u];
-  }
-  wg_max_post<NT>(local_absmax<NT, R>(t, H), red, 0);
-  SYN_TS(10);
-  bar<NT>();
-  SYN_TS(11);
-  float ss;
-  if constexpr (SEQ) {
-    if (tid < 64) {  // wave 0 runs the single chain
-      const float r = wave_seq_sum(sq, H, 0.0f);
-      if (tid == 0) red[36] = r;
-    }
-    bar<NT>();
-    ss = red[36];
-  } else {
-    ss = sumsq_chains<NT>(sq, H, red);
-  }
-  SYN_TS(12);
-  const float scale = 1.0f / sqrtf(ss / (float)H + eps);
-  float nv[R];
-#pragma unroll
-  for (int u = 0; u < R; u++) nv[u] = t[u] * scale;
-  float mx = wg_max_get<NT>(red, 0) * scale;
-  if (!(mx <= 3.402823466e38f) || !(scale > 0.0f)) {  // inf/nan rows: reduce explicitly
-    wg_max_post<NT>(local_absmax<NT, R>(nv, H), red, 16);
-    bar<NT>();
-    mx = wg_max_get<NT>(red, 16);
-  }
-  SYN_TS(13);
-  return quantize_regs_with_max<NT, R>(nv, H, mx, xq);
-}
-
-// quantizePerChannelInt8 (quantize.zig:12-47) of elements [k0, k1) of a row
-// whose max|v| is mx, held as element j = k0 + tid + u*NT; writes xq[j] and
-// returns the row scale
-template <int NT, int R>
-__device__ float quantize_range_with_max(const float (&v)[R], int k0, int k1, float mx,
-                                         int8_t *xq) {
-  const int tid = threadIdx.x;
-  if (mx == 0.0f) {
-#pragma unroll
-    for (int u = 0; u < R; u++)
-      if (k0 + tid + u * NT < k1) xq[k0 + tid + u * NT] = 0;
-    return 1.0f;
-  }
-  const float inv = 127.0f / mx;
-#pragma unroll
-  for (int u = 0; u < R; u++) {
-    const int j = k0 + tid + u * NT;
-    if (j < k1) {
-      float r = roundf(v[u] * inv);
-      r = fminf(127.0f, fmaxf(-127.0f, r));
-      xq[j] = (int8_t)(int)r;
-    }
-  }
-  return mx / 127.0f;
-}
 
 
 // grid (panels, ks).  dynamic LDS: sq[round4(H)] floats (PRO_NORM) | xq[C*16].
@@ -366,6 +116,7 @@ __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
   SYN_TS_DECL
   SYN_TS(0);
   SYN_TSR(14);
+  SYN_TL_ENTER();
 
   // Vector loads retire in issue order, so the prologue's inputs (L2 hits)
   // are requested before the weight chunks (HBM): the prologue then waits
@@ -609,6 +360,7 @@ __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
   }
   SYN_TSR(15);
   SYN_TS_FLUSH(PRO * 16);
+  SYN_TL_EXIT(PRO + (GU ? 10 : 0));
 }
 
 // threads per workgroup for a prologue row of H elements (RB rows each)
@@ -977,22 +729,6 @@ __global__ void __launch_bounds__(256)
   }
 }
 
-// max over the wave of any floats (invalid DPP sources keep -inf)
-template <int CTRL>
-__device__ __forceinline__ float dpp_fmax_any(float v) {
-  const int s = __builtin_amdgcn_update_dpp((int)0xff800000u, __float_as_int(v), CTRL, 0xf, 0xf,
-                                            false);
-  return fmaxf(v, __int_as_float(s));
-}
-__device__ __forceinline__ float wave_max_any(float v) {
-  v = dpp_fmax_any<0x111>(v);
-  v = dpp_fmax_any<0x112>(v);
-  v = dpp_fmax_any<0x114>(v);
-  v = dpp_fmax_any<0x118>(v);
-  v = dpp_fmax_any<0x142>(v);
-  v = dpp_fmax_any<0x143>(v);
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
 
 // ------------------------------------------------------------------ head attention
 // Decode attention in one kernel: grid (query heads, HD / CB column blocks),
@@ -1011,148 +747,6 @@ __device__ __forceinline__ float wave_max_any(float v) {
 // rounded product and add otherwise; softmax_slice; P.V: fused multiply-adds
 // over the positions when len >= 64 and the column lies in a whole 32-column
 // block).
-constexpr int kAttnNT = 256;
-constexpr int kPvChunk = 128;            // positions per staged V chunk
-constexpr int kPvGroups = kPvChunk / 4;  // 4-position groups per chunk
-
-// V groups [g0, g0 + ngroups) (4 positions of one column per 16 bytes,
-// indices clamped to the cache; ngroups rounded up to whole wave
-// instructions) of columns [cb0, cb0 + CB) into dst[group][CB], issued by
-// waves w0 .. w0 + nw - 1
-template <int CB>
-__device__ __forceinline__ void stage_v_chunk(const f32x4 *V4, int hd, int s4, int cb0, int g0,
-                                              f32x4 *dst, int wave, int w0, int nw, int lane,
-                                              int ngroups) {
-  constexpr int GPI = 64 / CB;  // groups per wave instruction
-  const int gl = lane / CB, col = lane % CB;
-  for (int gi = (wave - w0) * GPI; gi < ngroups; gi += nw * GPI) {
-    const int g = min(g0 + gi + gl, s4 - 1);
-    g2lds16(V4 + (size_t)g * hd + cb0 + col, dst + gi * CB);
-  }
-}
-
-// score chain sum_d q[d] * k[d], d = 0 .. HD-1 in order: q from LDS
-// (broadcast), the K row in registers
-template <int HD, bool FUSED>
-__device__ __forceinline__ float q_dot_chain(const f32x4 *q4, const f32x4 (&kr)[HD / 4]) {
-  constexpr int NB = HD / 4;
-  constexpr int BS = NB < 8 ? NB : 8;
-  constexpr int NBLK = NB / BS;
-  float acc = 0.0f;
-  f32x4 qa[BS], qb[BS];
-  auto load = [&](f32x4(&r)[BS], int blk) {
-#pragma unroll
-    for (int k = 0; k < BS; k++) r[k] = q4[blk * BS + k];
-  };
-  auto step = [&](f32x4(&r)[BS], int blk) {
-#pragma unroll
-    for (int k = 0; k < BS; k++) {
-      const f32x4 kv = kr[blk * BS + k];
-      if constexpr (FUSED) {
-        acc = __builtin_fmaf(r[k].x, kv.x, acc);
-        acc = __builtin_fmaf(r[k].y, kv.y, acc);
-        acc = __builtin_fmaf(r[k].z, kv.z, acc);
-        acc = __builtin_fmaf(r[k].w, kv.w, acc);
-      } else {
-        float t;
-        t = r[k].x * kv.x; acc = acc + t;
-        t = r[k].y * kv.y; acc = acc + t;
-        t = r[k].z * kv.z; acc = acc + t;
-        t = r[k].w * kv.w; acc = acc + t;
-      }
-    }
-  };
-  load(qa, 0);
-#pragma unroll
-  for (int blk = 0; blk < NBLK; blk += 2) {
-    if (blk + 1 < NBLK) load(qb, blk + 1);
-    __builtin_amdgcn_sched_barrier(0);
-    pin_regs(qa);
-    step(qa, blk);
-    if (blk + 1 < NBLK) {
-      if (blk + 2 < NBLK) load(qa, blk + 2);
-      __builtin_amdgcn_sched_barrier(0);
-      pin_regs(qb);
-      step(qb, blk + 1);
-    }
-  }
-  return acc;
-}
-
-// P.V chain of one column over whole 4-position groups [0, ng) of a staged
-// chunk: probabilities e4 (LDS, broadcast), the column's V at vt[g * CB]
-template <bool FUSED, int CB>
-__device__ __forceinline__ float pv_chain(const f32x4 *e4, const f32x4 *vt, int ng, float acc) {
-  auto step = [&](const f32x4 &E, const f32x4 &Vv) {
-    if constexpr (FUSED) {
-      acc = __builtin_fmaf(E.x, Vv.x, acc);
-      acc = __builtin_fmaf(E.y, Vv.y, acc);
-      acc = __builtin_fmaf(E.z, Vv.z, acc);
-      acc = __builtin_fmaf(E.w, Vv.w, acc);
-    } else {
-      float t;
-      t = E.x * Vv.x; acc = acc + t;
-      t = E.y * Vv.y; acc = acc + t;
-      t = E.z * Vv.z; acc = acc + t;
-      t = E.w * Vv.w; acc = acc + t;
-    }
-  };
-  f32x4 ea[8], va[8], eb[8], vb[8];
-  auto load = [&](f32x4(&E)[8], f32x4(&Vr)[8], int blk) {
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-      E[k] = e4[blk * 8 + k];
-      Vr[k] = vt[(blk * 8 + k) * CB];
-    }
-  };
-  auto run = [&](f32x4(&E)[8], f32x4(&Vr)[8]) {
-#pragma unroll
-    for (int k = 0; k < 8; k++) step(E[k], Vr[k]);
-  };
-  const int nb = ng >> 3;
-  int blk = 0;
-  if (nb > 0) {
-    load(ea, va, 0);
-    for (; blk + 1 < nb; blk += 2) {
-      load(eb, vb, blk + 1);
-      __builtin_amdgcn_sched_barrier(0);
-      pin_regs(ea);
-      pin_regs(va);
-      run(ea, va);
-      load(ea, va, min(blk + 2, nb - 1));  // in bounds; unused past the end
-      __builtin_amdgcn_sched_barrier(0);
-      pin_regs(eb);
-      pin_regs(vb);
-      run(eb, vb);
-    }
-    if (blk < nb) {
-      pin_regs(ea);
-      pin_regs(va);
-      run(ea, va);
-    }
-  }
-  // the last ng % 8 groups: one batch of reads, then the chains
-  const int rg = ng - nb * 8;
-  if (rg > 0) {
-#pragma unroll
-    for (int k = 0; k < 8; k++) {
-      const int g = nb * 8 + min(k, rg - 1);
-      ea[k] = e4[g];
-      va[k] = vt[g * CB];
-    }
-    pin_regs(ea);
-    pin_regs(va);
-#pragma unroll
-    for (int k = 0; k < 8; k++)
-      if (k < rg) step(ea[k], va[k]);
-  }
-  return acc;
-}
-
-template <int HD>
-constexpr int attn_cb() {
-  return HD < 64 ? HD : 64;
-}
 
 // dynamic LDS: e[round_up4(max_seq)] | V chunks [2][kPvGroups][CB] f32x4
 template <bool F32, int HD>
@@ -1180,35 +774,19 @@ __global__ void __launch_bounds__(kAttnNT)
   SYN_TS_DECL
   SYN_TS(0);
   SYN_TSR(14);
+  SYN_TL_ENTER();
 
-  // 0. the decode position, requested first (a vector load: waves 1-3 need
-  //    it before they can issue their K rows)
-  const int pos = __builtin_amdgcn_readfirstlane(
-      __hip_atomic_load(&st->pos, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-  // 1. what does not depend on the decode position: the q / k / v row
-  //    values and gains, the expf table word, the K row of position tid and
-  //    the V of the first 64 positions of this block's columns (straight
-  //    into LDS) for wave 0 (every decode attends to position 0)
-  // threads 0-127 own q[d], threads 128-255 own k[d] and v[d]
-  const bool is_q = tid < 128;
-  const int d = tid & 127;
-  const int dc = min(d, HD - 1), hc = min(d, HALF - 1);
-  const int r0 = is_q ? head * HD + dc : qd + kvh * HD + dc;
-  const int r1 = qd + kvd + kvh * HD + dc;
-  float x0, x1;
-  if constexpr (F32) {
-    x0 = qkv.f[r0];
-    x1 = qkv.f[r1];
-  } else {
-    const int a0 = qkv.acc[r0], a1 = qkv.acc[r1];
-    const float w0 = qkv.ws[r0], w1 = qkv.ws[r1], sx = qkv.sx[0];
-    float f;
-    f = (float)a0 * sx; x0 = f * w0;
-    f = (float)a1 * sx; x1 = f * w1;
-  }
-  const float *gn = is_q ? qn : kn;
-  const float g = gn ? gn[dc] : 0.0f;
-  const uint64_t tv = exp_tab_g[tid & 31];
+  // 0. the decode position, requested first (waves 1-3 need it before they
+  //    can issue their K rows); written by an earlier kernel of the stream,
+  //    so a plain (scalar) load sees it
+  const int pos = st->pos;
+  // 1. what does not depend on the decode position, in the order it is
+  //    needed last-first: wave 0's K rows (position tid) and the V of the
+  //    first 64 positions of this block's columns (straight into LDS; every
+  //    decode attends to position 0), then the q / k / v accumulator rows,
+  //    their scales and gains and the expf table word.  Threads 0-127 own
+  //    q[d], threads 128-255 own k[d] and v[d]; the rows' epilogue runs
+  //    after the later loads are issued, so nothing waits here.
   f32x4 kr[HD4];
   auto load_k_rows = [&](int p) {
     const int pc = min(p, max_seq - 1);
@@ -1220,6 +798,27 @@ __global__ void __launch_bounds__(kAttnNT)
     load_k_rows(tid);
     stage_v_chunk<CB>(V4, HD, s4, cb0, 0, vbuf, 0, 0, 1, lane, 16);
   }
+  const bool is_q = tid < 128;
+  const int d = tid & 127;
+  const int dc = min(d, HD - 1), hc = min(d, HALF - 1);
+  const int r0 = is_q ? head * HD + dc : qd + kvh * HD + dc;
+  const int r1 = qd + kvd + kvh * HD + dc;
+  float x0, x1;
+  int a0 = 0, a1 = 0;
+  float w0 = 0.0f, w1 = 0.0f, sx = 0.0f;
+  if constexpr (F32) {
+    x0 = qkv.f[r0];
+    x1 = qkv.f[r1];
+  } else {
+    a0 = qkv.acc[r0];
+    a1 = qkv.acc[r1];
+    w0 = qkv.ws[r0];
+    w1 = qkv.ws[r1];
+    sx = qkv.sx[0];
+  }
+  const float *gn = is_q ? qn : kn;
+  const float g = gn ? gn[dc] : 0.0f;
+  const uint64_t tv = exp_tab_g[tid & 31];
   const int len = pos + 1;
   SYN_TS(1);
   // then the rest of the first pass of K rows and of the first V chunk,
@@ -1234,6 +833,11 @@ __global__ void __launch_bounds__(kAttnNT)
   //    the k chains on wave 2 at the same time) and rotate-half RoPE at pos
   //    (rope.rs:13-43)
   const float cs = cosT[(size_t)pos * HALF + hc], sn = sinT[(size_t)pos * HALF + hc];
+  if constexpr (!F32) {  // the M <= 16 epilogue of the q / k / v rows
+    float f;
+    f = (float)a0 * sx; x0 = f * w0;
+    f = (float)a1 * sx; x1 = f * w1;
+  }
   float *myv = is_q ? qv : kv;
   float *mysq = is_q ? sqq : sqk;
   if (d < HD) {
@@ -1285,18 +889,18 @@ __global__ void __launch_bounds__(kAttnNT)
     const int w0 = base + wave * 64;  // first position of this wave
     if (w0 < len) {
       const int p = base + tid;
-      if (w0 <= pos && pos < w0 + 64) {
-        const bool is_new = p == pos;
+      if (p == pos) {
+        // only this lane reads the new row from LDS, straight into its K
+        // registers: all HD/4 reads in flight at once (a select over every
+        // lane needs a second row of registers, and the reads then go out
+        // two at a time)
         const f32x4 *k4 = reinterpret_cast<const f32x4 *>(kv);
 #pragma unroll
-        for (int c = 0; c < HD4; c++) {
-          const f32x4 kn4 = k4[c];
-          kr[c] = is_new ? kn4 : kr[c];
-        }
+        for (int c = 0; c < HD4; c++) kr[c] = k4[c];
       }
       float sf = 0.0f, sp = 0.0f;
       if (simd && w0 < n8) sf = q_dot_chain<HD, true>(q4, kr);
-      if (!simd || w0 + 63 >= n8) sp = q_dot_chain<HD, false>(q4, kr);
+      if (!simd || w0 + 63 >= n8) sp = q_dot_chain_plain<HD>(q4, kr);  // last: clobbers kr
       const float acc = simd && p < n8 ? sf : sp;
       if (p < len) {
         const float sc = acc * scale;
@@ -1375,6 +979,7 @@ __global__ void __launch_bounds__(kAttnNT)
   SYN_TS(11);
   SYN_TSR(15);
   SYN_TS_FLUSH(48);
+  SYN_TL_EXIT(20);
 }
 
 static size_t attn_head_lds_bytes(int hd, int max_seq) {
@@ -1451,6 +1056,7 @@ __global__ void __launch_bounds__(1024)
   constexpr int NT = 1024;
   extern __shared__ __align__(16) float fsm[];
   __shared__ float red[64];
+  SYN_TL_ENTER();
   const int tid = threadIdx.x;
   float x[RB], nwv[RB];
   int da[RB];
@@ -1496,6 +1102,7 @@ __global__ void __launch_bounds__(1024)
   }
   const float sv = quantize_regs_with_max<NT, RB>(nv, H, mx, xq);
   if (tid == 0) s_out[0] = sv;
+  SYN_TL_EXIT(31);
 }
 
 syn_status_t launch_fused_final_norm(const float *base, RowSrc delta, const float *nw, float eps,
@@ -1511,6 +1118,7 @@ syn_status_t launch_fused_final_norm(const float *base, RowSrc delta, const floa
 }
 
 __global__ void __launch_bounds__(256) k_zero_i32(int *__restrict__ p, size_t n) {
+  SYN_TL_ENTER();
   const size_t n4 = n / 4;
   i32x4 *p4 = reinterpret_cast<i32x4 *>(p);
   for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += (size_t)gridDim.x * 256)
@@ -1518,6 +1126,7 @@ __global__ void __launch_bounds__(256) k_zero_i32(int *__restrict__ p, size_t n)
   for (size_t i = n4 * 4 + (size_t)blockIdx.x * 256 + threadIdx.x; i < n;
        i += (size_t)gridDim.x * 256)
     p[i] = 0;
+  SYN_TL_EXIT(30);
 }
 
 syn_status_t launch_zero_i32(int *p, size_t n, hipStream_t s) {
@@ -1540,6 +1149,7 @@ __global__ void __launch_bounds__(NW * 64)
                   float *__restrict__ logits, float *__restrict__ pv, int *__restrict__ pi,
                   float *__restrict__ pv2) {
   __shared__ int redi[NW * 64];
+  SYN_TL_ENTER();
   const int panel = blockIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -1586,6 +1196,7 @@ __global__ void __launch_bounds__(NW * 64)
       pv2[panel] = t.v2;
     }
   }
+  SYN_TL_EXIT(32);
 }
 
 syn_status_t launch_lmhead_top2(const void *W, const float *ws, int N, int C, const int8_t *xq,
@@ -1604,6 +1215,7 @@ __global__ void __launch_bounds__(1024)
                      uint32_t *__restrict__ history, float *__restrict__ mhist) {
   __shared__ float s1[16], s2[16];
   __shared__ int si[16];
+  SYN_TL_ENTER();
   Top2v t{-__builtin_inff(), -1, -__builtin_inff()};
   for (int i = threadIdx.x; i < np; i += 1024) t = top2v_merge(t, Top2v{pv[i], pi[i], pv2[i]});
   t = wave_top2(t);
@@ -1627,6 +1239,7 @@ __global__ void __launch_bounds__(1024)
     st->pos += 1;
     st->step = step + 1;
   }
+  SYN_TL_EXIT(33);
 }
 
 syn_status_t launch_argmax_advance(const float *pv, const int *pi, const float *pv2, int np,
@@ -1641,6 +1254,22 @@ syn_status_t launch_argmax_advance(const float *pv, const int *pi, const float *
 }  // namespace syn
 
 #ifdef SYN_PHASE_TIMING
+// the step timeline: n entries of (kind, entry, exit); resets the ring
+extern "C" syn_status_t syn_hip_debug_timeline(unsigned long long *host, int max_entries,
+                                               int *n_out) {
+  if (!host || !n_out || max_entries <= 0) return SYN_ERR_INVALID_ARG;
+  SYN_HIP(hipDeviceSynchronize());
+  unsigned n = 0;
+  SYN_HIP(hipMemcpyFromSymbol(&n, HIP_SYMBOL(syn::syn_tl_n), 4, 0, hipMemcpyDeviceToHost));
+  n = std::min<unsigned>(n, std::min<unsigned>(8192u, (unsigned)max_entries));
+  if (n) SYN_HIP(hipMemcpyFromSymbol(host, HIP_SYMBOL(syn::syn_tl), (size_t)n * 24, 0,
+                                     hipMemcpyDeviceToHost));
+  const unsigned zero = 0;
+  SYN_HIP(hipMemcpyToSymbol(HIP_SYMBOL(syn::syn_tl_n), &zero, 4, 0, hipMemcpyHostToDevice));
+  *n_out = (int)n;
+  return SYN_OK;
+}
+
 extern "C" syn_status_t syn_hip_debug_phase_ts(unsigned long long *host, int n) {
   if (!host || n <= 0 || n > 256) return SYN_ERR_INVALID_ARG;
   SYN_HIP(hipDeviceSynchronize());

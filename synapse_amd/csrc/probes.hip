@@ -241,11 +241,14 @@ __global__ void k_probe_tiny(float *out, int i) {
 }
 
 // mode 0: one arrival counter, the last arrival publishes the generation,
-// the others poll it with device-scope atomic reads; mode 1: eight arrival
-// counters (by workgroup id), their last arrivals count on a top counter,
-// whose last arrival publishes; everyone polls with a short sleep.  Every
-// poll gives up after a bounded number of tries (counted in *timeouts, and
-// the workgroup leaves), so a wait cannot hang the GPU.
+// the others poll it with device-scope read-modify-writes (fetch_or 0);
+// mode 1: eight arrival counters (by workgroup id), their last arrivals
+// count on a top counter, whose last arrival publishes; everyone polls with
+// a short sleep; modes 2 and 3: as 0 and 1, but the generation is published
+// by a device-scope atomic store and polled by device-scope atomic loads
+// (no read-modify-write traffic on the polled word), no sleep.  Every poll
+// gives up after a bounded number of tries (counted in *timeouts, and the
+// workgroup leaves), so a wait cannot hang the GPU.
 __global__ void k_probe_barrier(unsigned *cnt, int nbar, int mode, unsigned *timeouts,
                                 unsigned long long *ts) {
   const unsigned G = gridDim.x;
@@ -257,25 +260,31 @@ __global__ void k_probe_barrier(unsigned *cnt, int nbar, int mode, unsigned *tim
       const unsigned target = (unsigned)(b + 1);
       bool late = false;
       bool arrive_top = true;
-      if (mode == 1) {
+      const bool grouped = mode == 1 || mode == 3, loads = mode >= 2;
+      if (grouped) {
         const unsigned grp = blockIdx.x & 7, gsz = (G - grp + 7) / 8;
         const unsigned old = __hip_atomic_fetch_add(cnt + 128 + 64 * grp, 1u, __ATOMIC_RELAXED,
                                                     __HIP_MEMORY_SCOPE_AGENT);
         arrive_top = old == target * gsz - 1;
       }
-      const unsigned need = mode == 1 ? 8u : G;
+      const unsigned need = grouped ? 8u : G;
       if (arrive_top) {
         const unsigned o2 =
             __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (o2 == target * need - 1)
-          __hip_atomic_exchange(cnt + 64, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (o2 == target * need - 1) {
+          if (loads)
+            __hip_atomic_store(cnt + 64, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          else
+            __hip_atomic_exchange(cnt + 64, target, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
       for (long n = 0;; n++) {
-        const unsigned g = __hip_atomic_fetch_or(cnt + 64, 0u, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
+        const unsigned g =
+            loads ? __hip_atomic_load(cnt + 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                  : __hip_atomic_fetch_or(cnt + 64, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (g >= target) break;
         if (mode == 1) __builtin_amdgcn_s_sleep(1);
-        if (n > 200000) {
+        if (n > 1000000) {
           late = true;
           break;
         }
@@ -337,7 +346,7 @@ extern "C" syn_status_t syn_hip_probe_graph_floor(int n, int wgs, double *us_per
 extern "C" syn_status_t syn_hip_probe_grid_barrier(int wgs, int mode, int nbar,
                                                    double *us_per_barrier, int *timeouts) {
   if (!us_per_barrier || !timeouts) return SYN_ERR_NULL_PTR;
-  if (wgs < 8 || nbar < 1 || nbar > 100000 || (mode != 0 && mode != 1))
+  if (wgs < 8 || nbar < 1 || nbar > 100000 || mode < 0 || mode > 3)
     return SYN_ERR_INVALID_ARG;
   SYN_TRY(ensure_init());
   int dev = 0, cus = 0;

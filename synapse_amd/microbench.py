@@ -266,7 +266,7 @@ if __name__ == "__main__":
     elif len(a) == 1 and a[0] == "sync":  # what a dependency level of the step costs
         rec = {"graph_kernel_us": {w: round(hip.probe_graph_floor(140, w), 3)
                                    for w in (32, 256, 512)}}
-        for mode in (0, 1):
+        for mode in (0, 1, 2, 3):
             for w in (64, 128, 256):
                 us, to = hip.probe_grid_barrier(w, mode, 200)
                 rec[f"barrier_mode{mode}_{w}wg_us"] = round(us, 3) if not to else f"{to} timeouts"
