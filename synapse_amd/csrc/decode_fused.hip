@@ -88,14 +88,16 @@ const uint64_t *exp_table_address() {
 //
 // GU (with PRO_NORM): the gate|up GEMV of the SwiGLU FFN.  A workgroup runs
 // the same prologue, then the dot products of gate panel p and up panel
-// pairs + p over its K slice; it adds them into the pair's accumulators,
-// waits for the atomics to return and counts its arrival (the split_k.hpp
-// protocol).  The pair's last slice reads the 2 x 64 exact int32 totals back
-// by atomic exchange with 0 (leaving them clear), applies the M <= 16
+// pairs + p over its K slice.  Row j of the pair has one 64-bit accumulator
+// holding its gate sum, its up sum and the number of slices added (gu_pack);
+// each slice adds its two partial sums and one arrival with a single
+// device-scope atomic and waits for the old value.  The slice whose add
+// completes the count holds row j's exact totals: it applies the M <= 16
 // epilogue (f32(acc)*sx)*sw to both, h[j] = silu(gate_j) * up_j
 // (int8.rs:500-503), writes h and folds max |h| into hmax by an atomic max
 // of the f32 bits (|h| >= 0, so the bit order is the value order; NaN is
-// skipped as the reference quantizer's `if a > m` skips it).
+// skipped as the reference quantizer's `if a > m` skips it).  Different
+// rows of a pair may be completed by different slices.
 template <int PRO, int NT, int U, bool GU, int R>
 __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
   constexpr int NW = NT / 64;
@@ -299,34 +301,31 @@ __global__ void __launch_bounds__(NT) k_fused_gemv(ProArgs a, GemvArgs g) {
         sg += redi[i * 64 + lane];
         su += redi[(NW + i) * 64 + lane];
       }
-      int *ag = g.acc + panel * 64 + lane, *au = g.acc + (g.pairs + panel) * 64 + lane;
-      const int r0 = __hip_atomic_fetch_add(ag, sg, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      const int r1 = __hip_atomic_fetch_add(au, su, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      asm volatile("" ::"v"(r0), "v"(r1));  // both adds of this lane have returned
-      __builtin_amdgcn_wave_barrier();
-      int old = 0;
-      if (lane == 0)
-        old = __hip_atomic_fetch_add(g.cnt + panel, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      old = __shfl(old, 0);
-      if (old == (int)gridDim.y - 1) {  // the pair's last slice: totals, SwiGLU, max |h|
-        const int tg = __hip_atomic_exchange(ag, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int tu = __hip_atomic_exchange(au, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (lane == 0)
-          __hip_atomic_exchange(g.cnt + panel, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const int j = panel * 64 + lane;
-        float m = 0.0f;
-        if (j < g.pairs * 64) {
-          const float fg = (float)tg * sv, fu = (float)tu * sv;
-          const float gv = fg * gu_wsg, uv = fu * gu_wsu;
-          const float act = syn_silu_tab(gv, gu_tab);
-          const float hv = act * uv;
-          g.h[j] = hv;
-          const float av = fabsf(hv);
-          if (av > m) m = av;
-        }
-        m = wave_max_nonneg(m);
-        if (lane == 0) atomicMax(g.hmax, __float_as_uint(m));
+      // row j's gate sum, up sum and one arrival in a single 64-bit add
+      // (gu_pack); the returned value plus this add is the row's running
+      // total, so the slice that completes the row knows it and has both
+      // exact sums without another round trip
+      const unsigned long long add = gu_pack(sg, su);
+      const unsigned long long tot =
+          __hip_atomic_fetch_add(g.acc64 + panel * 64 + lane, add, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT) + add;
+      int tg, tu, arrived;
+      gu_unpack(tot, tg, tu, arrived);
+      const bool last = arrived == (int)gridDim.y;
+      const int j = panel * 64 + lane;
+      float m = 0.0f;
+      if (last && j < g.pairs * 64) {  // this row's SwiGLU and |h|
+        const float fg = (float)tg * sv, fu = (float)tu * sv;
+        const float gv = fg * gu_wsg, uv = fu * gu_wsu;
+        const float act = syn_silu_tab(gv, gu_tab);
+        const float hv = act * uv;
+        g.h[j] = hv;
+        const float av = fabsf(hv);
+        if (av > m) m = av;
       }
+      const bool any = __ballot(last) != 0;
+      m = wave_max_nonneg(m);
+      if (any && lane == 0) atomicMax(g.hmax, __float_as_uint(m));
     }
   } else if (wave == 0) {
     int s = 0;
@@ -530,8 +529,8 @@ syn_status_t launch_fused_swiglu_gemv(RowSrc gu, int inter, float *s_out, const 
 // ------------------------------------------------------------------ gate|up + SwiGLU
 // x_mid = x + delta (res_out, workgroup 0), RMSNorm, quantize (the PRO_NORM
 // prologue), then the gate|up GEMV split over K in pairs of panels (gate
-// rows 64p.., up rows inter + 64p..), the pair's last slice writing
-// h = silu(gate) * up and max |h| (k_fused_gemv with GU).  The down GEMV
+// rows 64p.., up rows inter + 64p..), the slice that completes a row
+// writing h = silu(gate) * up and max |h| (k_fused_gemv with GU).  The down GEMV
 // then quantizes its K range of h with that max (PRO_HQ).
 bool gu_swiglu_fits(int H, int inter) {
   return fused_gemv_fits(H) && H <= RB * 256 && inter > 0 && inter % 64 == 0;
@@ -543,9 +542,10 @@ SplitGemv plan_gu_pairs(const void *W, const float *ws, int inter, int C, int ta
 
 syn_status_t launch_gu_swiglu(const float *base, RowSrc delta, float *res_out, const float *nw,
                               float eps, int H, float *s_out, const SplitGemv &g, const float *ws,
-                              int inter, int *cnt, float *h, unsigned *hmax, hipStream_t s) {
+                              int inter, float *h, unsigned *hmax, hipStream_t s) {
   if (!gu_swiglu_fits(H, inter) || g.C != (int)cdiv((size_t)H, 16) || g.N64 != inter ||
-      (g.nt != 256 && g.nt != 512) || !g.acc || !cnt || !h || !hmax || !ws) {
+      (g.nt != 256 && g.nt != 512) || g.ks > 255 || !g.acc ||
+      reinterpret_cast<uintptr_t>(g.acc) % 8 || !h || !hmax || !ws) {
     set_error("gate|up SwiGLU GEMV: shapes outside the kernel's limits or plan not prepared");
     return SYN_ERR_INVALID_ARG;
   }
@@ -559,7 +559,7 @@ syn_status_t launch_gu_swiglu(const float *base, RowSrc delta, float *res_out, c
   a.s_out = s_out;
   GemvArgs gu{};
   gu.pairs = inter / 64;
-  gu.cnt = cnt;
+  gu.acc64 = reinterpret_cast<unsigned long long *>(g.acc);
   gu.ws = ws;
   gu.h = h;
   gu.hmax = hmax;

@@ -84,13 +84,13 @@ syn_status_t launch_fused_swiglu_gemv(RowSrc gu, int inter, float *s_out, const 
 // x_mid = x + delta (res_out, workgroup 0); xq = q8(rmsnorm(x_mid)); the
 // stacked [gate | up] GEMV (int8 panel layout, 2*inter rows) split over K in
 // pairs of panels (gate panel p with up panel inter/64 + p; g planned by
-// plan_gu_pairs, g.acc the 2*inter int32 accumulators, zero before the
-// step); the pair's last slice writes h = silu(gate) * up and folds max |h|
-// into hmax (f32 bits, atomic max; zero before the step); cnt[inter/64]
-// counters, zero before the step and left zero; s_out = xq's scale
+// plan_gu_pairs; g.acc holds inter 64-bit packed row accumulators (8-byte
+// aligned, zero before the step); the slice that completes row j writes
+// h[j] = silu(gate_j) * up_j and folds max |h| into hmax (f32 bits, atomic
+// max; zero before the step); s_out = xq's scale
 syn_status_t launch_gu_swiglu(const float *base, RowSrc delta, float *res_out, const float *nw,
                               float eps, int H, float *s_out, const SplitGemv &g, const float *ws,
-                              int inter, int *cnt, float *h, unsigned *hmax, hipStream_t s);
+                              int inter, float *h, unsigned *hmax, hipStream_t s);
 bool gu_swiglu_fits(int H, int inter);
 SplitGemv plan_gu_pairs(const void *W, const float *ws, int inter, int C, int target_wg, int nt);
 // xq = q8(vec) over this split's K range with the max *hmax reduced

@@ -152,16 +152,39 @@ struct GemvArgs {
   int C, cs;
   int *acc;
   // gate|up pairs (GU kernels): grid panel p covers gate panel p and up
-  // panel `pairs` + p of the stacked [gate | up] matrix; cnt[p] counts the
-  // arrived K slices of pair p; the pair's last slice writes h = silu(gate)
-  // * up for its 64 rows (ws: the stacked rows' scales) and max |h| to hmax
+  // panel `pairs` + p of the stacked [gate | up] matrix; acc64[64p + r]
+  // packs row 64p + r's gate and up sums and arrivals (gu_pack); the slice
+  // that completes a row writes h = silu(gate) * up for it (ws: the stacked
+  // rows' scales) and max |h| to hmax
   int pairs = 0;
-  int *cnt = nullptr;
+  unsigned long long *acc64 = nullptr;
   const float *ws = nullptr;
   float *h = nullptr;
   unsigned *hmax = nullptr;
   const uint64_t *exp_tab = nullptr;
 };
+
+// One 64-bit accumulator per gate|up row: bits 0-27 the gate sum, 28-55 the
+// up sum (two's complement fields), 56-63 the number of K slices added.
+// Every field is added in the same integer add: the total is
+// count * 2^56 + up * 2^28 + gate modulo 2^64, and |gate|, |up| < 2^27
+// (K <= 8322 int8 products of magnitude <= 127 * 127) with at most 255
+// slices recover each field exactly.
+__device__ __forceinline__ unsigned long long gu_pack(int gate, int up) {
+  return (1ull << 56) + ((unsigned long long)(long long)up << 28) +
+         (unsigned long long)(long long)gate;
+}
+__device__ __forceinline__ long long gu_sext28(unsigned long long v) {
+  return (long long)(v << 36) >> 36;
+}
+__device__ __forceinline__ void gu_unpack(unsigned long long t, int &gate, int &up, int &count) {
+  const long long g = gu_sext28(t);
+  const unsigned long long t1 = (t - (unsigned long long)g) >> 28;
+  const long long u = gu_sext28(t1);
+  gate = (int)g;
+  up = (int)u;
+  count = (int)((t1 - (unsigned long long)u) >> 28);
+}
 
 // ------------------------------------------------------------------ prologue parts
 // PRO_NORM / PRO_MNORM loads: x = (base | embed row of st->token | zero row)

@@ -31,7 +31,6 @@ struct QLayer {
   QLinearInt8 qkv, o, gu, down;
   SplitGemv f_qkv, f_o, f_gu, f_down;  // fused decode plans over these weights
   SplitGemv f_gup;                      // gate|up as pairs of panels (launch_gu_swiglu)
-  int *gu_cnt = nullptr;                // its per-pair arrival counters
 };
 
 }  // namespace syn
@@ -279,11 +278,9 @@ struct syn_hip_qlm_s {
       Ly.f_down = plan_split_gemv(Ly.down.w.p, Ly.down.scales.as<float>(), (int)h,
                                   Ly.down.chunks, target, 512);
       per_layer = (size_t)Ly.f_qkv.N64 + Ly.f_o.N64 + Ly.f_gu.N64 + Ly.f_down.N64;
-      if (gu_swiglu_fits((int)h, (int)inter)) {
+      if (gu_swiglu_fits((int)h, (int)inter))
         Ly.f_gup = plan_gu_pairs(Ly.gu.w.p, Ly.gu.scales.as<float>(), (int)inter, Ly.gu.chunks,
                                  target, 256);
-        per_layer += round_up(inter / 64, 64);  // the pairs' arrival counters
-      }
     }
     // then one max |h| slot per layer for the gate|up SwiGLU kernel
     acc_elems = per_layer * L + round_up(L, 64);
@@ -295,11 +292,9 @@ struct syn_hip_qlm_s {
         g[i]->acc = p;
         p += g[i]->N64;
       }
-      if (gu_swiglu_fits((int)h, (int)inter)) {
-        Ly.f_gup.acc = Ly.f_gu.acc;  // the 2*inter gate|up accumulators
-        Ly.gu_cnt = p;
-        p += round_up(inter / 64, 64);
-      }
+      // the gate|up pairs' inter packed 64-bit row accumulators take the
+      // 2*inter int32 words (N64 is a multiple of 64: 256-byte aligned)
+      if (gu_swiglu_fits((int)h, (int)inter)) Ly.f_gup.acc = Ly.f_gu.acc;
     }
     return SYN_OK;
   }
@@ -344,7 +339,7 @@ struct syn_hip_qlm_s {
         SYN_TRY(trace_begin(s));
         SYN_TRY(launch_gu_swiglu(xin.as<float>(), Ly.f_o.rows(s_o), xmid.as<float>(), fn(l), eps,
                                  (int)h, s_gu, Ly.f_gup, Ly.gu.scales.as<float>(), (int)inter,
-                                 Ly.gu_cnt, gu.as<float>(), hmax, s));
+                                 gu.as<float>(), hmax, s));
         SYN_TRY(trace_end(SYN_HIP_STEP_GATE_UP, s));
         SYN_TRY(trace_begin(s));
         SYN_TRY(launch_fused_hq_gemv(gu.as<float>(), hmax, (int)inter, s_down, Ly.f_down, s));
