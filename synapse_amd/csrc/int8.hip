@@ -67,20 +67,21 @@ syn_status_t launch_quantize_rows(const float *d_x, size_t m, size_t k, size_t l
 // panel; each wave walks 16-byte K chunks (one 1 KiB load per chunk) and does
 // 4 v_dot4_i32_i8 per activation row.  Waves reduce in LDS (i32, exact).
 // A K split either writes per-slice partials for k_gemv_reduce (SK false), or
-// (SK true, one launch) adds them into the int32 accumulators part[M][N64]
-// with device-scope atomics, waits for their return (the add has then been
-// performed at the point of coherence every XCD's atomics go to), and counts
-// its arrival on cnt[panel]; the panel's last slice reads the totals back by
-// atomic exchange with 0 (leaving them cleared for the next call), applies
-// the epilogue and clears the counter.  Integer sums are exact in any order.
+// (SK true, one launch) adds them into 64-bit accumulators acc64[M][N64]
+// with device-scope atomics: one add carries a row's exact partial sum (bits
+// 0-39, two's complement: |sum| < 2^39) and one arrival (bits 40-63), so the
+// returned old value plus the add is the row's running total and arrival
+// count.  The slice whose add completes the count (the row's last, which
+// need not be the same workgroup for every row) applies the epilogue and
+// clears the accumulator for the next call with a device-scope atomic
+// store.  Integer sums are exact in any order.
 template <int M, bool SK>
 __global__ void __launch_bounds__(1024)
     k_gemv_w8a8(const i32x4 *__restrict__ W, const float *__restrict__ ws,
                 const int8_t *__restrict__ xq, int ldx, const float *__restrict__ sx,
-                float *__restrict__ y, int ldy, int *__restrict__ part, int *__restrict__ cnt,
-                int N, int C, int cs) {
+                float *__restrict__ y, int ldy, int *__restrict__ part,
+                unsigned long long *__restrict__ acc64, int N, int C, int cs) {
   extern __shared__ int red[];  // [waves][M][64]
-  __shared__ int s_last;
   const int panel = blockIdx.x, ks = blockIdx.y;
   const int nw = blockDim.x >> 6;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -126,32 +127,23 @@ __global__ void __launch_bounds__(1024)
   __syncthreads();
   const int N64 = gridDim.x * 64;
   if constexpr (SK) {
-    int seen = 0;
-    for (int t = threadIdx.x; t < M * 64; t += blockDim.x) {
-      const int m = t >> 6, r = t & 63;
-      int s = 0;
-      for (int w = 0; w < nw; w++) s += red[(w * M + m) * 64 + r];
-      seen |= __hip_atomic_fetch_add(part + (size_t)m * N64 + panel * 64 + r, s, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
-    }
-    asm volatile("" ::"v"(seen));  // every add of this thread has returned
-    __syncthreads();
-    if (threadIdx.x == 0)
-      s_last = __hip_atomic_fetch_add(cnt + panel, 1, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.y - 1;
-    __syncthreads();
-    if (!s_last) return;
     for (int t = threadIdx.x; t < M * 64; t += blockDim.x) {
       const int m = t >> 6, r = t & 63, row = panel * 64 + r;
-      const int tot = __hip_atomic_exchange(part + (size_t)m * N64 + row, 0, __ATOMIC_RELAXED,
-                                            __HIP_MEMORY_SCOPE_AGENT);
-      if (row < N) {
-        const float f = (float)tot * sx[m];
-        y[(size_t)m * ldy + row] = f * ws[row];
+      int s = 0;
+      for (int w = 0; w < nw; w++) s += red[(w * M + m) * 64 + r];
+      unsigned long long *a = acc64 + (size_t)m * N64 + row;
+      const unsigned long long add = (1ull << 40) + (unsigned long long)(long long)s;
+      const unsigned long long tot =
+          __hip_atomic_fetch_add(a, add, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + add;
+      const long long sum = (long long)(tot << 24) >> 24;
+      if ((int)((tot - (unsigned long long)sum) >> 40) == (int)gridDim.y) {  // the row is complete
+        __hip_atomic_store(a, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (row < N) {
+          const float f = (float)(int)sum * sx[m];
+          y[(size_t)m * ldy + row] = f * ws[row];
+        }
       }
     }
-    if (threadIdx.x == 0)
-      __hip_atomic_exchange(cnt + panel, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
   for (int t = threadIdx.x; t < M * 64; t += blockDim.x) {
@@ -216,23 +208,25 @@ GemvPlan make_gemv_plan(size_t n, size_t k_chunks, bool chunked_kc) {
   return p;
 }
 
-// cnt != nullptr: the single-launch split-K form (part = the accumulators)
+// acc64 != nullptr: the single-launch split-K form (the packed accumulators);
+// otherwise per-slice partials in part (or none without a split)
 template <int M>
 static void launch_gemv_m(const GemvPlan &p, const i32x4 *W, const float *ws, const int8_t *xq,
-                          int ldx, const float *sx, float *y, int ldy, int *part, int *cnt, int N,
-                          hipStream_t s) {
+                          int ldx, const float *sx, float *y, int ldy, int *part,
+                          unsigned long long *acc64, int N, hipStream_t s) {
   const int waves = std::min(p.waves, M >= 8 ? 8 : 16);
   const size_t shm = (size_t)waves * M * 64 * sizeof(int);
-  if (cnt && p.ksplit > 1)
+  if (acc64 && p.ksplit > 1)
     hipLaunchKernelGGL((k_gemv_w8a8<M, true>), dim3(p.panels, p.ksplit), dim3(64 * waves), shm, s,
-                       W, ws, xq, ldx, sx, y, ldy, part, cnt, N, p.chunks, p.cs);
+                       W, ws, xq, ldx, sx, y, ldy, nullptr, acc64, N, p.chunks, p.cs);
   else
     hipLaunchKernelGGL((k_gemv_w8a8<M, false>), dim3(p.panels, p.ksplit), dim3(64 * waves), shm,
                        s, W, ws, xq, ldx, sx, y, ldy, part, nullptr, N, p.chunks, p.cs);
 }
 
 typedef void (*gemv_launcher)(const GemvPlan &, const i32x4 *, const float *, const int8_t *, int,
-                              const float *, float *, int, int *, int *, int, hipStream_t);
+                              const float *, float *, int, int *, unsigned long long *, int,
+                              hipStream_t);
 static const gemv_launcher kGemvLaunch[17] = {
     nullptr,          launch_gemv_m<1>,  launch_gemv_m<2>,  launch_gemv_m<3>,
     launch_gemv_m<4>, launch_gemv_m<5>,  launch_gemv_m<6>,  launch_gemv_m<7>,
@@ -261,11 +255,9 @@ syn_status_t QLinearInt8::ensure_sk() {
   if (p.ksplit <= 1 || sk_panels >= p.panels) return SYN_OK;
   SYN_HIP(hipDeviceSynchronize());  // the old buffers may still be in use by queued work
   sk_panels = p.panels;
-  SYN_TRY(sk_acc.alloc((size_t)16 * p.panels * 64 * sizeof(int)));
-  SYN_TRY(sk_cnt.alloc((size_t)p.panels * sizeof(int)));
+  SYN_TRY(sk_acc.alloc((size_t)16 * p.panels * 64 * sizeof(unsigned long long)));
   SYN_HIP(hipMemset(sk_acc.p, 0, sk_acc.bytes));  // calls leave them cleared
-  SYN_HIP(hipMemset(sk_cnt.p, 0, sk_cnt.bytes));
-  SYN_HIP(hipDeviceSynchronize());  // the memsets run on the null stream, not the caller's
+  SYN_HIP(hipDeviceSynchronize());  // the memset runs on the null stream, not the caller's
   return SYN_OK;
 }
 
@@ -282,7 +274,7 @@ syn_status_t QLinearInt8::gemv(size_t m, const int8_t *d_xq, size_t ldx, const f
   SYN_TRY(ensure_sk());
   const GemvPlan p = make_gemv_plan(n, (size_t)chunks, false);
   kGemvLaunch[m](p, w.as<i32x4>(), scales.as<float>(), d_xq, (int)ldx, d_sx, d_y, (int)ldy,
-                 sk_acc.as<int>(), sk_cnt.as<int>(), (int)n, s);
+                 nullptr, sk_acc.as<unsigned long long>(), (int)n, s);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
 }

@@ -38,10 +38,10 @@ struct QLinearInt8 {
   size_t part_elems = 0;
   DevBuf xq, sx;        // activation quantization scratch (forward())
   size_t xq_rows = 0;
-  // gemv()'s one-launch K split: int32 accumulators [16][N64] and per-panel
-  // arrival counters, zero between calls (the panel's last slice reads and
-  // clears them)
-  DevBuf sk_acc, sk_cnt;
+  // gemv()'s one-launch K split: packed 64-bit row accumulators [16][N64]
+  // (exact sum and arrivals), zero between calls (the slice that completes a
+  // row reads and clears it)
+  DevBuf sk_acc;
   int sk_panels = 0;
   syn_status_t ensure_sk();
 

@@ -5,8 +5,10 @@
 // XCD's atomics go to (plain stores and loads go through each XCD's own L2,
 // and a load there can return a stale copy of a line another XCD's slice
 // wrote).  The slice then counts its arrival on the panel's counter; the one
-// that arrives last reads every slot back with atomic exchanges, adds them in
-// slice order in f32 and clears the counter for the next call.  The total
+// that arrives last reads every slot back with device-scope atomic loads,
+// adds them in slice order in f32 and clears the counter for the next call
+// (slots are written before they are read in every call, so they need no
+// clearing).  The total
 // therefore does not depend on which slice finishes when (the sum order is
 // fixed), and it has f32's range: no fixed-point scale limits tiny or huge
 // rows, and NaN / Inf partials reach the output as they do in a plain f32
@@ -14,11 +16,13 @@
 //
 // Memory order: the atomics are relaxed, with no release / acquire fences.
 // Every word the slices share (slots, counters) is only ever touched by
-// device-scope read-modify-write atomics, and a slice waits for the return of
+// device-scope atomics (read-modify-writes, and the last slice's loads), and
+// a slice waits for the return of
 // each of its slot exchanges before its counter add is issued (the value
 // dependency in sk_arrive); on gfx950 a returned device-scope RMW has been
 // performed at the coherence point, where all RMWs to one address are
-// ordered.  So the last slice's exchanges observe every slot.  An agent-scope
+// ordered, and a device-scope atomic load is served there too.  So the last
+// slice's loads observe every slot.  An agent-scope
 // release / acquire pair would instead write back and invalidate the whole
 // L2 of each XCD, at several times the kernel's cost.  A counter is left
 // non-zero only by a grid that stops part way, which on this device means a
@@ -48,12 +52,23 @@ __device__ __forceinline__ bool sk_arrive(unsigned seen, int *cnt, int nslices, 
   __syncthreads();
   return *s_flag != 0;
 }
-// the slots of one entry, slice 0 first, `stride` apart, added in slice order
+// the slots of one entry, slice 0 first, `stride` apart, added in slice
+// order; the loads go out 16 at a time (clamped indices, every one issued
+// before the first add), so the sum waits for one round trip per 16 slices
 __device__ __forceinline__ float sk_sum(unsigned *slot0, size_t stride, int nslices) {
   float t = 0.0f;
-  for (int s = 0; s < nslices; s++)
-    t += __uint_as_float(__hip_atomic_exchange(slot0 + (size_t)s * stride, 0u, __ATOMIC_RELAXED,
-                                               __HIP_MEMORY_SCOPE_AGENT));
+  for (int s0 = 0; s0 < nslices; s0 += 16) {
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; i++)
+      v[i] = __uint_as_float(__hip_atomic_load(slot0 + (size_t)min(s0 + i, nslices - 1) * stride,
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+      const float r = t + v[i];
+      t = s0 + i < nslices ? r : t;
+    }
+  }
   return t;
 }
 __device__ __forceinline__ void sk_reset(int *cnt) {
