@@ -28,6 +28,7 @@ GEMMs, the INT8 prefill GEMM, and the config-5 Mamba decoder
 from __future__ import annotations
 
 import argparse
+import hashlib
 import json
 import os
 import sys
@@ -56,13 +57,28 @@ LM_HEAD_WRITE_KIB, LM_HEAD_WRITE_FACTOR = 816.5, 262144.0 / 262144.0
 # and commands in profiles/qwen3_int8_decode_step_kernels_traffic.md, taken
 # on the kernels of this source tree; the attention's traffic grows with the
 # position).  These are recorded readings, reported as `traffic` with
-# `traffic_source` naming the profile: re-run its commands when a step
-# kernel changes.
+# `traffic_source` naming the profile, and only while the step kernels'
+# sources hash to STEP_SOURCES_SHA16 (the hash of the build the readings were
+# taken on): after a change to those files the field is null until the
+# profile's commands are run again and the readings and hash updated here.
 TRAFFIC_SOURCE = "profiles/qwen3_int8_decode_step_kernels_traffic.md (recorded rocprofv3 --pmc)"
-_STEP_KIB = {"qkv": (2159.6, 68.0), "attention": (647.5, 32.0), "o": (1084.0, 64.0),
-             "gate_up": (3204.5, 145.0), "down": (1605.5, 48.0)}
-STEP_KERNEL_TRAFFIC = {k: round(1024 * (f * LM_HEAD_FETCH_FACTOR + w * LM_HEAD_WRITE_FACTOR))
-                       for k, (f, w) in _STEP_KIB.items()}
+_STEP_KIB = {"qkv": (2159.6, 68.0), "attention": (638.0, 32.0), "o": (1084.0, 64.0),
+             "gate_up": (3205.0, 113.5), "down": (1605.5, 48.0)}
+STEP_SOURCES = ("synapse_amd/csrc/decode_fused.hip", "synapse_amd/csrc/fused_dev.hpp")
+STEP_SOURCES_SHA16 = "9e62826af1dd28ff"
+
+
+def step_sources_sha16() -> str:
+    h = hashlib.sha256()
+    for f in STEP_SOURCES:
+        with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), f), "rb") as fh:
+            h.update(fh.read())
+    return h.hexdigest()[:16]
+
+
+STEP_KERNEL_TRAFFIC = ({k: round(1024 * (f * LM_HEAD_FETCH_FACTOR + w * LM_HEAD_WRITE_FACTOR))
+                        for k, (f, w) in _STEP_KIB.items()}
+                       if step_sources_sha16() == STEP_SOURCES_SHA16 else {})
 
 
 def step_weight_bytes(c):
@@ -555,7 +571,9 @@ def main():
         line["roofline"] = {
             "bound": "hbm", "kernel": STEP_KERNEL_NAMES[dom], "achieved": d["gb_s"],
             "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": d["hbm_frac"],
-            "traffic": STEP_KERNEL_TRAFFIC.get(dom), "traffic_source": TRAFFIC_SOURCE,
+            "traffic": STEP_KERNEL_TRAFFIC.get(dom),
+            "traffic_source": TRAFFIC_SOURCE if STEP_KERNEL_TRAFFIC else
+                "none: the step kernels' sources differ from the build the readings were taken on",
             "avg_launch_us": d["avg_us"],
             "bytes_per_launch": d["bytes_per_launch"],
             "share_of_step": round(d["us_per_step"] / (ms_per_step * 1e3), 4),

@@ -12,7 +12,9 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libsynapse_hip.so")
+# SYN_HIP_LIBRARY may name another build of the same sources (the
+# instrumented profiling build, `python -m synapse_amd.build --phase-timing`)
+LIB_PATH = os.environ.get("SYN_HIP_LIBRARY") or os.path.join(HERE, "libsynapse_hip.so")
 HEADER = os.path.join(os.path.dirname(HERE), "include", "synapse_hip.h")
 
 SYN_OK = 0

@@ -252,6 +252,57 @@ def _decoder_run(which: str, steps: int, graph: bool):
     return {"decoder": which, "decode_ms_per_token": round(ms / steps, 4)}
 
 
+# kernel kinds of the decode-step timeline (decode_fused.hip SYN_TL_EXIT ids)
+TL_KINDS = {0: "qkv", 1: "o", 5: "down", 2: "down_swiglu", 10: "gate_up", 3: "in_proj",
+            6: "x_proj", 20: "attention", 30: "zero", 31: "final_norm", 32: "lm_head",
+            33: "select"}
+
+
+def qwen3_timeline(steps_before: int = 20, graph: bool = True) -> dict:
+    """One Qwen3 INT8 decode step after the 16-token prompt and
+    `steps_before` steps: for every kernel kind the mean period (start of its
+    workgroup (0, 0) to the next kernel's) and workgroup (0, 0)'s time in the
+    kernel, from s_memrealtime stamps (the instrumented build:
+    `python -m synapse_amd.build --phase-timing`, loaded with
+    SYN_HIP_LIBRARY=synapse_amd/libsynapse_hip_pt.so)."""
+    import ctypes as C
+    import bench
+    L = hip.lib()
+    if not hasattr(L, "syn_hip_debug_timeline"):
+        raise RuntimeError("timeline: load the phase-timing build (SYN_HIP_LIBRARY)")
+    L.syn_hip_debug_timeline.restype = C.c_int
+    L.syn_hip_debug_phase_ts.restype = C.c_int
+    cfg = dict(bench.QWEN3, max_seq=bench.PROMPT + steps_before + 8)
+    m = hip.QuantizedCausalLM(cfg)
+    m.init_synthetic(bench.SEED_BASE, 0.02)
+    m.set_options(fused=True, graph=graph)
+    m.prefill(np.array(bench.prompt_ids(), np.uint32))
+    m.decode_timed(steps_before)
+    buf = (C.c_uint64 * (3 * 8192))()
+    n = C.c_int()
+    hip.check(L.syn_hip_debug_timeline(buf, 8192, C.byref(n)), "timeline")  # clears the ring
+    ms = m.decode_timed(1)
+    hip.check(L.syn_hip_debug_timeline(buf, 8192, C.byref(n)), "timeline")
+    t = np.array(buf[:3 * n.value], np.int64).reshape(-1, 3)
+    t = t[np.argsort(t[:, 1], kind="stable")]
+    agg = {}
+    for i in range(len(t) - 1):
+        k = TL_KINDS.get(int(t[i, 0]), str(int(t[i, 0])))
+        a = agg.setdefault(k, [0, 0, 0])
+        a[0] += 1
+        a[1] += (t[i + 1, 1] - t[i, 1]) * 10  # 100 MHz ticks -> ns
+        a[2] += (t[i, 2] - t[i, 1]) * 10
+    ph = (C.c_uint64 * 256)()
+    hip.check(L.syn_hip_debug_phase_ts(ph, 256), "phase_ts")
+    attn = [int(ph[48 + i] - ph[48]) for i in range(12)]  # k_attn_head stamps, core clocks
+    m.close()
+    return {"position": bench.PROMPT + steps_before, "graph": graph, "step_ms": round(ms, 4),
+            "kernels": int(n.value), "span_us": round(float(t[-1, 2] - t[0, 1]) / 100.0, 2),
+            "per_kind": {k: {"launches": v[0], "period_us": round(v[1] / v[0] / 1e3, 3),
+                             "wg0_us": round(v[2] / v[0] / 1e3, 3)} for k, v in agg.items()},
+            "attention_phase_clocks": attn}
+
+
 if __name__ == "__main__":
     import json
     import sys
@@ -271,6 +322,8 @@ if __name__ == "__main__":
                 us, to = hip.probe_grid_barrier(w, mode, 200)
                 rec[f"barrier_mode{mode}_{w}wg_us"] = round(us, 3) if not to else f"{to} timeouts"
         print(json.dumps(rec))
+    elif len(a) == 1 and a[0] == "timeline":  # the phase-timing build's step timeline
+        print(json.dumps(qwen3_timeline()))
     elif len(a) == 4 and a[0] == "gemv":  # gemv FMT N K
         print(json.dumps(gemv_record(FMT_BY_NAME[a[1]], int(a[2]), int(a[3]), "gemv")))
     elif len(a) == 5 and a[0] == "gemm":  # gemm FMT M N K
@@ -278,6 +331,6 @@ if __name__ == "__main__":
     elif len(a) in (2, 3) and a[0] in ("klm", "mamba-ref", "mamba-int8", "hlm", "hlm-op"):  # DECODER STEPS [eager]
         print(json.dumps(_decoder_run(a[0], int(a[1]), graph=not (len(a) == 3 and a[2] == "eager"))))
     else:
-        print("usage: python -m synapse_amd.microbench copy NBYTES | sync | gemv FMT N K | "
+        print("usage: python -m synapse_amd.microbench copy NBYTES | sync | timeline | gemv FMT N K | "
               "gemm FMT M N K | {klm,mamba-ref,mamba-int8,hlm,hlm-op} STEPS [eager]", file=sys.stderr)
         sys.exit(2)
