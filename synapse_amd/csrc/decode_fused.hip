@@ -731,7 +731,8 @@ __global__ void __launch_bounds__(256)
 
 
 // ------------------------------------------------------------------ head attention
-// Decode attention in one kernel: grid (query heads, HD / CB column blocks),
+// Decode attention in one kernel: one workgroup per (query head, HD / CB
+// column block), grouped by KV head (see the index decode below),
 // 256 threads.  Every workgroup of a head computes the head's prologue (q/k/v
 // rows, head RMSNorms, RoPE), all of its scores and the softmax, then the P.V
 // chains of its CB columns; the workgroup of column block 0 of the first
@@ -763,8 +764,12 @@ __global__ void __launch_bounds__(kAttnNT)
   __shared__ uint64_t exp_tab[32];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int head = blockIdx.x, cb0 = blockIdx.y * CB;
-  const int grp = nh / nkv, kvh = head / grp;
+  // workgroup w: KV group w % nkv, then (query head of the group, column
+  // block) from w / nkv.  Workgroups go to the XCDs round-robin by id, so
+  // with nkv a multiple of 8 all workgroups of a KV group share an XCD and
+  // its K and V rows come through that XCD's L2 once.
+  const int grp = nh / nkv, wj = blockIdx.x / nkv;
+  const int kvh = blockIdx.x % nkv, head = kvh * grp + wj / (HD / CB), cb0 = (wj % (HD / CB)) * CB;
   const int qd = nh * HD, kvd = nkv * HD;
   const int tiles = (max_seq + 63) >> 6, s4 = (max_seq + 3) >> 2;
   float *e = dsm;
@@ -868,7 +873,7 @@ __global__ void __launch_bounds__(kAttnNT)
     myv[HALF + d] = rr + tt;
   }
   __syncthreads();
-  if (head % grp == 0 && blockIdx.y == 0 && !is_q && d < HD) {  // one writer per KV head
+  if (wj == 0 && !is_q && d < HD) {  // one writer per KV head
     kc[kv_k_index(pos, kvh, d, HD, max_seq)] = kv[d];
     vc[kv_v_index(pos, kvh, d, HD, max_seq)] = x1;
   }
@@ -1024,7 +1029,7 @@ syn_status_t launch_fused_attention(RowSrc qkv, int nh, int nkv, int hd, const f
         done = true;
       }
       const int cb = hd < 64 ? hd : 64;
-      SYN_LAUNCH(kern, dim3((unsigned)nh, (unsigned)(hd / cb)), dim3(kAttnNT), shm, s, qkv,
+      SYN_LAUNCH(kern, dim3((unsigned)(nh * (hd / cb))), dim3(kAttnNT), shm, s, qkv,
                          nh, nkv, qn, kn, eps, cosT, sinT, st, kc, vc, max_seq, tab, out);
       SYN_LAUNCH_CHECK();
       return SYN_OK;
