@@ -107,12 +107,73 @@ __device__ __forceinline__ float sumsq_combine(const float *r4, const float *sq,
   return s;
 }
 
-// The whole reference-order sum of squares: lanes 0-3 run the chains, every
-// thread gets the result.  Callers place a barrier between writing sq and
-// this call; red[32..35] is used.
+// The four chains of sumsq_chain at once on one wave, chain l on the lanes
+// of 16-lane row l, from registers: lane j of the row holds values 16j ..
+// 16j+15 of each 256-value pass; the running sum visits the row's lanes in
+// order (lane j adds its 16 values, then a DPP row_ror:1 hands the sum to
+// lane j+1), so every add is one dependent VALU op and no LDS read sits in
+// the chain (the sumsq_chain form reads its values from LDS in blocks of 32
+// between the adds).  Same adds in the same order.  Requires q4 = n/4
+// rounded down to be a multiple of 4 (16-byte aligned chains); returns chain
+// l's sum in every lane of row l.  Call with all 64 lanes of the wave.
+__device__ __forceinline__ float sumsq_chain_rows(const float *sq, int n) {
+  const int lane = threadIdx.x & 63, l = lane >> 4, j = lane & 15;
+  const int q4 = (n & ~3) >> 2;
+  const float *p = sq + l * q4;
+  auto rot = [](float x) {  // lane j <- lane j-1 of the same 16-lane row
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x121, 0xf, 0xf,
+                                                      false));
+  };
+  float acc = 0.0f;
+  for (int base = 0; base < q4; base += 256) {
+    f32x4 r[4];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+      const int i = min(base + 16 * j + 4 * k, (q4 - 1) & ~3);  // in bounds; unused past q4
+      r[k] = *reinterpret_cast<const f32x4 *>(p + i);
+    }
+    pin_regs(r);
+    const int left = min(q4 - base, 256), full = left >> 4;
+    for (int t = 0; t < full; t++) {
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        acc = acc + r[k].x;
+        acc = acc + r[k].y;
+        acc = acc + r[k].z;
+        acc = acc + r[k].w;
+      }
+      acc = rot(acc);
+    }
+    if (left & 15) {  // the last, partial turn
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        const float c[4] = {r[k].x, r[k].y, r[k].z, r[k].w};
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          if (4 * k + i < (left & 15)) acc = acc + c[i];
+      }
+      acc = rot(acc);
+    }
+    // the pass's sum sits in the row's lane after its last turn
+    acc = __shfl(acc, (l << 4) | (((left + 15) >> 4) & 15));
+  }
+  return acc;
+}
+
+// The whole reference-order sum of squares: the four chains on wave 0
+// (sumsq_chain_rows, or lanes 0-3 reading LDS when the chains are not
+// 16-byte aligned), every thread gets the result.  Callers place a barrier
+// between writing sq and this call; red[32..35] is used.
 template <int NT>
 __device__ float sumsq_chains(const float *sq, int n, float *red) {
-  if (threadIdx.x < 4) red[32 + threadIdx.x] = sumsq_chain(sq, n, threadIdx.x);
+  if (((n >> 2) & 3) == 0) {
+    if (threadIdx.x < 64) {
+      const float s = sumsq_chain_rows(sq, n);
+      if ((threadIdx.x & 15) == 0) red[32 + (threadIdx.x >> 4)] = s;
+    }
+  } else if (threadIdx.x < 4) {
+    red[32 + threadIdx.x] = sumsq_chain(sq, n, threadIdx.x);
+  }
   bar<NT>();
   return sumsq_combine(red + 32, sq, n);
 }

@@ -96,6 +96,23 @@ def test_prefill_attention_hd128_row_blocks_and_append():
         tok = O.argmax(lo)
 
 
+@pytest.mark.parametrize("t", [752, 753])
+def test_prefill_attention_hd128_tile_switch_point(t):
+    # head dim 128: the tile kernel holds 32 score rows of round_up4(t) + 1
+    # floats beside its K / V chunks in 144 KiB of LDS, which fits up to 752
+    # tokens; 753 takes the bit-exact row kernel.  Both sides of the switch
+    # against the oracle.
+    cfg = dict(hidden=256, n_layers=1, n_heads=2, n_kv_heads=1, head_dim=128, inter=256,
+               vocab=300, max_seq=760, eps=1e-5, rope_theta=5e5)
+    o, g = build_pair(cfg, LLAMA_FMTS)
+    ids = O.token_ids(t, 0x5EED0000 + 0xFFFF, cfg["vocab"])
+    lo, lg = o.prefill(ids), g.prefill(ids)
+    assert _cos(lo, lg) >= 0.9999 and _rel(lg, lo) < 5e-3, (_cos(lo, lg), _rel(lg, lo))
+    tok = O.argmax(lo)
+    lo, lg = o.forward_one(tok), g.forward_one(tok)
+    assert _cos(lo, lg) >= 0.9999 and _rel(lg, lo) < 5e-3, (_cos(lo, lg), _rel(lg, lo))
+
+
 def test_tiny_q8_0_with_qk_norm_greedy():
     fm = (hip.FMT_Q8_0,) * 5
     o, g = build_pair(TINY, fm, qk_norm=True)
