@@ -605,7 +605,11 @@ static void launch_kq_m(int m, const GemvPlan &p, const void *W, const uint16_t 
     case 1: launch_kq<FMT, 1>(p, W, Wd, x, ldx, y, ldy, sk, N, s); break;
     case 2: launch_kq<FMT, 2>(p, W, Wd, x, ldx, y, ldy, sk, N, s); break;
     case 3: launch_kq<FMT, 3>(p, W, Wd, x, ldx, y, ldy, sk, N, s); break;
-    default: launch_kq<FMT, 4>(p, W, Wd, x, ldx, y, ldy, sk, N, s); break;
+    case 4: launch_kq<FMT, 4>(p, W, Wd, x, ldx, y, ldy, sk, N, s); break;
+    case 5: launch_kq<FMT, 5>(p, W, Wd, x, ldx, y, ldy, sk, N, s); break;
+    case 6: launch_kq<FMT, 6>(p, W, Wd, x, ldx, y, ldy, sk, N, s); break;
+    case 7: launch_kq<FMT, 7>(p, W, Wd, x, ldx, y, ldy, sk, N, s); break;
+    default: launch_kq<FMT, 8>(p, W, Wd, x, ldx, y, ldy, sk, N, s); break;
   }
 }
 
@@ -632,11 +636,12 @@ syn_status_t QLinearKQ::gemv(size_t m, const float *d_x, size_t ldx, float *d_y,
   if (m == 0 || n == 0 || k == 0) return SYN_OK;
   if (m > 8) return gemm(m, d_x, ldx, d_y, ldy, s);
   const GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
-  // one launch per block of rows: a K split finishes in place (split_k.hpp)
-  if (p.ksplit > 1) SYN_TRY(sk.ensure(p.panels, 4, p.ksplit));
+  // one launch for all (up to 8) rows: the weights stream once, and a K
+  // split finishes in place (split_k.hpp)
+  if (p.ksplit > 1) SYN_TRY(sk.ensure(p.panels, 8, p.ksplit));
   const uint16_t *Wd = wd.as<uint16_t>();
-  for (size_t m0 = 0; m0 < m; m0 += 4) {
-    const int mb = (int)std::min<size_t>(4, m - m0);
+  for (size_t m0 = 0; m0 < m; m0 += 8) {
+    const int mb = (int)std::min<size_t>(8, m - m0);
     const float *xm = d_x + m0 * ldx;
     float *ym = d_y + m0 * ldy;
     const size_t gpb = fmt == SYN_HIP_FMT_Q4_K ? 8 : 16;
@@ -664,7 +669,7 @@ syn_status_t QLinearKQ::prepare(size_t max_m) {
     xh_bytes = f16_rows_bytes(max_m, k);
   }
   const GemvPlan p = make_gemv_plan(n, (size_t)blocks, false);
-  return p.ksplit > 1 ? sk.ensure(p.panels, 4, p.ksplit) : SYN_OK;
+  return p.ksplit > 1 ? sk.ensure(p.panels, 8, p.ksplit) : SYN_OK;
 }
 
 }  // namespace syn
