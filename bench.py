@@ -223,15 +223,19 @@ def secondary(hip, np):
     # speculative decode with the reference's default draft (first L/3 layers)
     spec = {}
     for name, fn in (("generate", lambda: m.generate(ids, 64)),
-                     ("speculative_k4", lambda: m.generate_speculative(ids, 64, 4))):
+                     ("speculative_k4", lambda: m.generate_speculative(ids, 64, 4)),
+                     ("speculative_k7", lambda: m.generate_speculative(ids, 64, 7))):
         fn()
-        t = time.perf_counter()
-        fn()
-        spec[name] = {"ms": round((time.perf_counter() - t) * 1e3, 2)}
-        spec[name]["tok_s"] = round(64e3 / spec[name]["ms"], 1)
-    spec["note"] = ("256-token prompt + 64 greedy tokens per call; drafts from the first "
-                    f"{LLAMA3B['n_layers'] // 3} of {LLAMA3B['n_layers']} layers "
-                    "(forward_one_draft), every draft accepted")
+        best = float("inf")
+        for _ in range(3):
+            t = time.perf_counter()
+            fn()
+            best = min(best, time.perf_counter() - t)
+        spec[name] = {"ms": round(best * 1e3, 2), "tok_s": round(64 / best, 1)}
+    spec["note"] = ("256-token prompt + 64 greedy tokens per call, best of 3; drafts from the "
+                    f"first {LLAMA3B['n_layers'] // 3} of {LLAMA3B['n_layers']} layers "
+                    "(forward_one_draft), every draft accepted; k = 7 verifies 8 rows, one "
+                    "K-quant GEMV launch per projection")
     m.close()
     wb = kquant_weight_bytes(LLAMA3B)
     out["config3_kquant_decode_llama3b"] = {

@@ -791,7 +791,8 @@ __global__ void __launch_bounds__(kAttnNT)
   //    decode attends to position 0), then the q / k / v accumulator rows,
   //    their scales and gains and the expf table word.  Threads 0-127 own
   //    q[d], threads 128-255 own k[d] and v[d]; the rows' epilogue runs
-  //    after the later loads are issued, so nothing waits here.
+  //    after the later loads are issued, so nothing waits here.  (Issuing
+  //    the rows first, ahead of the K rows, measured slower.)
   f32x4 kr[HD4];
   auto load_k_rows = [&](int p) {
     const int pc = min(p, max_seq - 1);
@@ -825,11 +826,22 @@ __global__ void __launch_bounds__(kAttnNT)
   const float g = gn ? gn[dc] : 0.0f;
   const uint64_t tv = exp_tab_g[tid & 31];
   const int len = pos + 1;
+  // score chain kinds (ops/attention.rs:24-147): fused multiply-adds for
+  // positions below n8 when len >= 64, a rounded product and add for the
+  // others.  The last len % 8 positions [n8, len) of a long decode need the
+  // second kind; when wave 3 has no positions of its own in the last pass,
+  // its lanes run those, so no wave runs both chains.
+  const bool simd = len >= 64;
+  const int n32 = len - len % 32;
+  const int n8 = n32 + ((len - n32) / 8) * 8;
+  const int last_base = (len - 1) / kAttnNT * kAttnNT;
+  const bool tail_w3 = simd && n8 < len && len - last_base <= kAttnNT - 64;
   SYN_TS(1);
   // then the rest of the first pass of K rows and of the first V chunk,
   // for the positions the decode attends to
   if (wave != 0) {
     if (wave * 64 < len) load_k_rows(tid);
+    else if (wave == 3 && tail_w3 && last_base == 0) load_k_rows(n8 + lane);
     if (len > 64) stage_v_chunk<CB>(V4, HD, s4, cb0, 16, vbuf + 16 * CB, wave, 1, 3, lane,
                                     min(kPvGroups, (len + 3) >> 2) - 16);
   }
@@ -881,19 +893,20 @@ __global__ void __launch_bounds__(kAttnNT)
 
   // 3. scores, kAttnNT positions per pass (lane = position).  A wave runs
   //    the fused chain if any of its positions is below n8 and the plain
-  //    one if any is not; each lane keeps its own kind.  The lane of the
-  //    new position takes the K row from LDS.
+  //    one if any is not (unless wave 3 takes the tail, above); each lane
+  //    keeps its own kind.  The lane of the new position takes the K row
+  //    from LDS.
   const float scale = 1.0f / sqrtf((float)HD);
-  const bool simd = len >= 64;
-  const int n32 = len - len % 32;
-  const int n8 = n32 + ((len - n32) / 8) * 8;
   const f32x4 *q4 = reinterpret_cast<const f32x4 *>(qv);
   float mx = -__builtin_inff();
   for (int base = 0; base < len; base += kAttnNT) {
-    if (base > 0) load_k_rows(base + tid);
+    const bool last = base == last_base;
+    const bool tw = last && tail_w3 && wave == 3;  // this wave runs the tail
+    if (base > 0) load_k_rows(tw ? n8 + lane : base + tid);
     const int w0 = base + wave * 64;  // first position of this wave
-    if (w0 < len) {
-      const int p = base + tid;
+    if (w0 < len || tw) {
+      const int p = tw ? n8 + lane : base + tid;
+      const int lim = last && tail_w3 && !tw ? n8 : len;  // positions this wave scores
       if (p == pos) {
         // only this lane reads the new row from LDS, straight into its K
         // registers: all HD/4 reads in flight at once (a select over every
@@ -904,10 +917,11 @@ __global__ void __launch_bounds__(kAttnNT)
         for (int c = 0; c < HD4; c++) kr[c] = k4[c];
       }
       float sf = 0.0f, sp = 0.0f;
-      if (simd && w0 < n8) sf = q_dot_chain<HD, true>(q4, kr);
-      if (!simd || w0 + 63 >= n8) sp = q_dot_chain_plain<HD>(q4, kr);  // last: clobbers kr
+      if (!tw && simd && w0 < n8) sf = q_dot_chain<HD, true>(q4, kr);
+      if (tw || !simd || (w0 + 63 >= n8 && !(last && tail_w3)))
+        sp = q_dot_chain_plain<HD>(q4, kr);  // last: clobbers kr
       const float acc = simd && p < n8 ? sf : sp;
-      if (p < len) {
+      if (p < lim) {
         const float sc = acc * scale;
         e[p] = sc;
         mx = fmaxf(mx, sc);

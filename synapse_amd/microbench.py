@@ -322,8 +322,8 @@ if __name__ == "__main__":
                 us, to = hip.probe_grid_barrier(w, mode, 200)
                 rec[f"barrier_mode{mode}_{w}wg_us"] = round(us, 3) if not to else f"{to} timeouts"
         print(json.dumps(rec))
-    elif len(a) == 1 and a[0] == "timeline":  # the phase-timing build's step timeline
-        print(json.dumps(qwen3_timeline()))
+    elif len(a) in (1, 2) and a[0] == "timeline":  # the phase-timing build's step timeline
+        print(json.dumps(qwen3_timeline(int(a[1]) if len(a) == 2 else 20)))
     elif len(a) == 4 and a[0] == "gemv":  # gemv FMT N K
         print(json.dumps(gemv_record(FMT_BY_NAME[a[1]], int(a[2]), int(a[3]), "gemv")))
     elif len(a) == 5 and a[0] == "gemm":  # gemm FMT M N K
@@ -331,6 +331,6 @@ if __name__ == "__main__":
     elif len(a) in (2, 3) and a[0] in ("klm", "mamba-ref", "mamba-int8", "hlm", "hlm-op"):  # DECODER STEPS [eager]
         print(json.dumps(_decoder_run(a[0], int(a[1]), graph=not (len(a) == 3 and a[2] == "eager"))))
     else:
-        print("usage: python -m synapse_amd.microbench copy NBYTES | sync | timeline | gemv FMT N K | "
+        print("usage: python -m synapse_amd.microbench copy NBYTES | sync | timeline [STEPS] | gemv FMT N K | "
               "gemm FMT M N K | {klm,mamba-ref,mamba-int8,hlm,hlm-op} STEPS [eager]", file=sys.stderr)
         sys.exit(2)
