@@ -35,12 +35,21 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // both scalings are exact in f32.  A row whose maximum is zero or not finite
 // is not scaled.  perm8: each 8-element chunk is stored in the k order
 // 0,2,4,6,1,3,5,7 of the Q4_0 direct-load kernel's fragments (k_gemm_kqr).
+// y0 (when not null): row m of the GEMM's output [M, ldy] is cleared (its
+// first ny floats; ldy a multiple of 4, y0 16-byte aligned) for a K-split
+// GEMM that adds its partial tiles into it, saving a kernel of its own.
 __global__ void __launch_bounds__(256)
     k_f32_to_f16(const float *__restrict__ x, int ldx, _Float16 *__restrict__ xh, int ldh,
-                 float *__restrict__ rowmul, int K, int perm8) {
+                 float *__restrict__ rowmul, int K, int perm8, float *__restrict__ y0, int ldy,
+                 int ny) {
   __shared__ float red[4];
   const int m = blockIdx.x, tid = threadIdx.x;
   const float *xr = x + (size_t)m * ldx;
+  if (y0) {
+    float4 *yr = reinterpret_cast<float4 *>(y0 + (size_t)m * ldy);
+    for (int c = tid; c < ny / 4; c += 256) yr[c] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int c = (ny & ~3) + tid; c < ny; c += 256) y0[(size_t)m * ldy + c] = 0.0f;
+  }
   float mx = 0.0f;
   for (int c = tid * 4; c < K; c += 1024) {
     const float4 a = *reinterpret_cast<const float4 *>(xr + c);
@@ -845,7 +854,8 @@ size_t f16_rows_bytes(size_t m, size_t k) {
   return round_up(m * round_up(k, PGK) * 2, 256) + m * sizeof(float);
 }
 static syn_status_t to_f16_rows(size_t m, size_t k, const float *d_x, size_t ldx, DevBuf &xh,
-                                size_t &xh_bytes, bool perm8, float **rowmul, hipStream_t s) {
+                                size_t &xh_bytes, bool perm8, float **rowmul, hipStream_t s,
+                                float *zero_y0 = nullptr, size_t ldy = 0, size_t ny = 0) {
   if (ldx % 4 || k % 8) {
     set_error("GEMM activation stride must be a multiple of 4 floats and K of 8");
     return SYN_ERR_SHAPE_MISMATCH;
@@ -860,7 +870,8 @@ static syn_status_t to_f16_rows(size_t m, size_t k, const float *d_x, size_t ldx
   }
   *rowmul = reinterpret_cast<float *>(xh.as<unsigned char>() + round_up(m * ldh * 2, 256));
   hipLaunchKernelGGL(k_f32_to_f16, dim3((unsigned)m), dim3(256), 0, s, d_x, (int)ldx,
-                     xh.as<_Float16>(), (int)ldh, *rowmul, (int)k, perm8 ? 1 : 0);
+                     xh.as<_Float16>(), (int)ldh, *rowmul, (int)k, perm8 ? 1 : 0, zero_y0,
+                     (int)ldy, (int)ny);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
 }
@@ -919,9 +930,6 @@ static syn_status_t kq_gemm_f16(int fmt, bool exact, const u32x4 *W, const uint1
                        xh.as<_Float16>(), ldh, m, k, W, Wd, n, blocks, d_y, ldy, rowmul, per,
                        s);
   }
-  float *rowmul = nullptr;
-  SYN_TRY(to_f16_rows(m, k, d_x, ldx, xh, xh_bytes, false, &rowmul, s));
-  const _Float16 *X = xh.as<_Float16>();
   // Enough 256 x 256 tiles for three quarters of the CUs: the four-wave
   // kernel, one K pass per tile.  Else 256 x 128 tiles (twice as many) when
   // they cover three quarters of the CUs, one K pass (Q8_0, 2048 x 4096 x
@@ -944,7 +952,15 @@ static syn_status_t kq_gemm_f16(int fmt, bool exact, const u32x4 *W, const uint1
                                                       steps / 8)));
   const int per = (int)cdiv((size_t)steps, (size_t)ksplit);
   ksplit = (int)cdiv((size_t)steps, (size_t)per);
-  if (ksplit > 1) SYN_TRY(zero_y(d_y, m, n, ldy, s));
+  // a K split adds its partial tiles into Y: the conversion kernel clears Y
+  // (row-aligned 16-byte rows), else a kernel of its own does
+  const bool zero_in_conv =
+      ksplit > 1 && ldy % 4 == 0 && reinterpret_cast<uintptr_t>(d_y) % 16 == 0 && n < (1u << 31);
+  float *rowmul = nullptr;
+  SYN_TRY(to_f16_rows(m, k, d_x, ldx, xh, xh_bytes, false, &rowmul, s,
+                      zero_in_conv ? d_y : nullptr, ldy, n));
+  const _Float16 *X = xh.as<_Float16>();
+  if (ksplit > 1 && !zero_in_conv) SYN_TRY(zero_y(d_y, m, n, ldy, s));
   const dim3 grid((unsigned)tiles_n, (unsigned)tiles_m, (unsigned)ksplit);
   const size_t shm =
       2 * (size_t)(big ? PG3_STAGE : mid ? pg_stage<256>() : pg_stage<128>()) * sizeof(_Float16);
