@@ -635,9 +635,11 @@ syn_status_t syn_hip_eval_expf(const float *d_x, float *d_y, size_t n, void *str
 syn_status_t syn_hip_probe_mfma(int kind, size_t iters, double *tflops);
 syn_status_t syn_hip_probe_hbm_read(size_t bytes, double *gb_s);
 /* The device's reference-order sequential sum of n <= 16384 host values:
- * out3[0] = one lane's chain, out3[1] = the wave-cooperative chain of the
- * Mamba norms, out3[2] = that chain's clocks (a check of the summation order). */
-syn_status_t syn_hip_probe_seq_sum(const float *host, size_t n, float *out3);
+ * out5[0] = one lane's chain, out5[1] = the wave-cooperative chain of the
+ * attention's softmax sum, out5[2] = that chain's clocks, out5[3] = the
+ * long-row wave chain of the Mamba norms, out5[4] = its clocks (a check of
+ * the summation order). */
+syn_status_t syn_hip_probe_seq_sum(const float *host, size_t n, float *out5);
 /* What ordering the decode step's dependency levels costs: the graph replay
    of n dependent tiny kernels of `wgs` workgroups (us per kernel), and nbar
    grid barriers among `wgs` <= CU-count co-resident workgroups of one

@@ -256,7 +256,7 @@ __device__ float norm_quant(float eps, int H, const float (&x)[R], const float (
   float ss;
   if constexpr (SEQ) {
     if (tid < 64) {  // wave 0 runs the single chain
-      const float r = wave_seq_sum(sq, H, 0.0f);
+      const float r = wave_seq_sum_long(sq, H, 0.0f);
       if (tid == 0) red[36] = r;
     }
     bar<NT>();

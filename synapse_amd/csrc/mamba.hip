@@ -52,11 +52,11 @@ __global__ void __launch_bounds__(256)
   }
   __syncthreads();
   // one sequential sum of the rounded squares; the squares are formed in
-  // parallel first, then wave 0 adds them in index order (wave_seq_sum)
+  // parallel first, then wave 0 adds them in index order (wave_seq_sum_long)
   for (int j = threadIdx.x; j < H; j += blockDim.x) sq[j] = sm[j] * sm[j];
   __syncthreads();
   if (threadIdx.x < 64) {
-    const float s = wave_seq_sum(sq, H, 0.0f);
+    const float s = wave_seq_sum_long(sq, H, 0.0f);
     if (threadIdx.x == 0) s_scale = 1.0f / sqrtf(s / (float)H + eps);
   }
   __syncthreads();

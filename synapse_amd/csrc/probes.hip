@@ -114,8 +114,9 @@ __global__ void __launch_bounds__(256) k_probe_read(const i32x4 *__restrict__ p,
 }
 
 // the reference-order sequential sums of n values: out[0] one lane's chain
-// (seq_sum), out[1] the wave-cooperative chain (wave_seq_sum); out[2] the
-// clocks of the wave chain
+// (seq_sum), out[1] the wave-cooperative chain (wave_seq_sum), out[2] its
+// clocks, out[3] the long-row wave chain (wave_seq_sum_long), out[4] its
+// clocks
 __global__ void __launch_bounds__(64) k_probe_seq_sum(const float *v, int n, float *out) {
   extern __shared__ __align__(16) float sv[];
   for (int j = threadIdx.x; j < ((n + 3) & ~3); j += 64) sv[j] = j < n ? v[j] : 0.0f;
@@ -123,10 +124,14 @@ __global__ void __launch_bounds__(64) k_probe_seq_sum(const float *v, int n, flo
   const unsigned long long t0 = __builtin_amdgcn_s_memtime();
   const float w = wave_seq_sum(sv, n, 0.0f);
   const unsigned long long t1 = __builtin_amdgcn_s_memtime();
+  const float wl = wave_seq_sum_long(sv, n, 0.0f);
+  const unsigned long long t2 = __builtin_amdgcn_s_memtime();
   if (threadIdx.x == 0) {
     out[0] = seq_sum(sv, n);
     out[1] = w;
     out[2] = (float)(t1 - t0);
+    out[3] = wl;
+    out[4] = (float)(t2 - t1);
   }
 }
 
@@ -134,18 +139,18 @@ __global__ void __launch_bounds__(64) k_probe_seq_sum(const float *v, int n, flo
 
 using namespace syn;
 
-extern "C" syn_status_t syn_hip_probe_seq_sum(const float *host, size_t n, float *out3) {
-  if (!host || !out3) return SYN_ERR_NULL_PTR;
+extern "C" syn_status_t syn_hip_probe_seq_sum(const float *host, size_t n, float *out5) {
+  if (!host || !out5) return SYN_ERR_NULL_PTR;
   if (n == 0 || n > 16384) return SYN_ERR_INVALID_ARG;
   SYN_TRY(ensure_init());
   DevBuf dv, dout;
   SYN_TRY(dv.alloc(n * 4));
-  SYN_TRY(dout.alloc(16));
+  SYN_TRY(dout.alloc(32));
   SYN_HIP(hipMemcpy(dv.p, host, n * 4, hipMemcpyHostToDevice));
   hipLaunchKernelGGL(k_probe_seq_sum, dim3(1), dim3(64), ((n + 3) & ~(size_t)3) * 4, 0,
                      dv.as<float>(), (int)n, dout.as<float>());
   SYN_LAUNCH_CHECK();
-  SYN_HIP(hipMemcpy(out3, dout.p, 12, hipMemcpyDeviceToHost));
+  SYN_HIP(hipMemcpy(out5, dout.p, 20, hipMemcpyDeviceToHost));
   return SYN_OK;
 }
 

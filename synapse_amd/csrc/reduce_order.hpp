@@ -246,6 +246,58 @@ __device__ __forceinline__ float wave_seq_sum(const float *v, int n, float acc0)
   return acc;
 }
 
+// wave_seq_sum for long rows (a model width, ~1024 values): the same adds in
+// the same order (v in LDS, 16-byte aligned, readable up to round_up4(n)).
+// Lane j of each 16-lane row holds v[64j .. 64j+64) of each 1024-value pass
+// in registers; lane j adds its 64 values, then a DPP row_ror:1 hands the
+// sum to lane j+1 (lane 15 to lane 0 for the next pass): 16 hand-offs per
+// pass instead of wave_seq_sum's 64 wave-wide rotates (~31 cycles each,
+// which made a 1024-long chain 7.0 cycles per add against 5.0 for the adds
+// alone).  Short rows keep wave_seq_sum: their partial turn would run 64
+// guarded adds instead of 16.  Returns the sum in every lane.
+__device__ __forceinline__ float wave_seq_sum_long(const float *v, int n, float acc0) {
+  const int j = threadIdx.x & 15;
+  float acc = acc0;
+  auto rot = [](float x) {  // lane j+1 <- lane j of the same row, lane 0 <- lane 15
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x121, 0xf, 0xf,
+                                                      false));
+  };
+  for (int base = 0; base < n; base += 1024) {
+    f32x4 r[16];
+#pragma unroll
+    for (int k = 0; k < 16; k++) {
+      const int i = min(base + 64 * j + 4 * k, (n - 1) & ~3);  // in bounds; unused past n
+      r[k] = *reinterpret_cast<const f32x4 *>(v + i);
+    }
+    pin_regs(r);
+    const int left = min(n - base, 1024), full = left >> 6;
+    for (int t = 0; t < full; t++) {  // turns of 64 values
+#pragma unroll
+      for (int k = 0; k < 16; k++) {
+        acc = acc + r[k].x;
+        acc = acc + r[k].y;
+        acc = acc + r[k].z;
+        acc = acc + r[k].w;
+      }
+      acc = rot(acc);
+    }
+    if (left & 63) {  // the last, partial turn
+#pragma unroll
+      for (int k = 0; k < 16; k++) {
+        const float c[4] = {r[k].x, r[k].y, r[k].z, r[k].w};
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+          if (4 * k + i < (left & 63)) acc = acc + c[i];
+      }
+      acc = rot(acc);
+    }
+    // the pass's sum now sits in the row's lane after its last turn
+    const int turns = (left + 63) >> 6;
+    acc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(acc), turns & 15));
+  }
+  return acc;
+}
+
 // Sequential sum of v[0..n) (a single accumulator, in index order).
 __device__ __forceinline__ float seq_sum(const float *v, int n) {
   if ((reinterpret_cast<uintptr_t>(v) & 15) == 0) return lds_seq_sum(v, n, 0.0f);

@@ -1142,12 +1142,13 @@ def probe_mfma(kind: int, iters: int = 20000) -> float:
 
 
 def probe_seq_sum(values):
-    """(one-lane chain, wave chain, wave-chain clocks) of the device's
-    reference-order sequential sum of `values` (float32)."""
+    """(one-lane chain, wave chain, its clocks, long-row wave chain, its
+    clocks) of the device's reference-order sequential sum of `values`
+    (float32)."""
     v = np.ascontiguousarray(values, np.float32)
-    out = np.zeros(3, np.float32)
+    out = np.zeros(5, np.float32)
     check(lib().syn_hip_probe_seq_sum(ptr(v), v.size, ptr(out)), "probe_seq_sum")
-    return float(out[0]), float(out[1]), float(out[2])
+    return tuple(float(o) for o in out)
 
 
 def probe_graph_floor(n: int = 140, wgs: int = 256) -> float:

@@ -170,9 +170,11 @@ def test_sequential_sum_order(n):
     rng = np.random.default_rng(n)
     v = (rng.standard_normal(n) * np.exp(rng.uniform(-8, 8, n))).astype(np.float32) ** 2
     want = np.add.accumulate(v, dtype=np.float32)[-1]
-    lane, wave, clk = hip.probe_seq_sum(v)
+    lane, wave, clk, wave_long, clk_long = hip.probe_seq_sum(v)
     assert np.float32(lane).view(np.uint32) == want.view(np.uint32), (lane, want)
     assert np.float32(wave).view(np.uint32) == want.view(np.uint32), (wave, want)
+    assert np.float32(wave_long).view(np.uint32) == want.view(np.uint32), (wave_long, want)
     tree = np.float32(np.sum(v, dtype=np.float32))  # numpy's pairwise order
     if n >= 64:
-        print(n, "wave chain clocks", clk, "pairwise differs:", tree != want)
+        print(n, "wave chain clocks", clk, "long-row chain clocks", clk_long,
+              "pairwise differs:", tree != want)
