@@ -40,7 +40,9 @@ def test_encoder_roundtrip_quality(name):
 CASES = [("q8_0", 4096, 4096, 1), ("q8_0", 4096, 1024, 3), ("q8_0", 14336, 4096, 1),
          ("q8_0", 96, 100, 4), ("q4_k", 3072, 3072, 1), ("q4_k", 3072, 1024, 2),
          ("q4_k", 3072, 8192, 1), ("q4_k", 512, 67, 5), ("q6_k", 8192, 3072, 1),
-         ("q6_k", 3072, 1000, 3), ("q6_k", 256, 65, 7)]
+         ("q6_k", 3072, 1000, 3), ("q6_k", 256, 65, 7),
+         # up to 8 rows run as one launch (a speculative verify of k = 7)
+         ("q4_k", 3072, 5120, 8), ("q8_0", 4096, 1024, 6)]
 
 
 @pytest.mark.parametrize("name,k,n,m", CASES)
@@ -56,7 +58,8 @@ def test_kquant_gemv_vs_reference(name, k, n, m):
         assert _rel(got[i], want[i]) <= TOL * 0.1, (i, _rel(got[i], want[i]))
 
 
-@pytest.mark.parametrize("name,m", [("q4_k", 1), ("q6_k", 1), ("q8_0", 3), ("q4_k", 4)])
+@pytest.mark.parametrize("name,m", [("q4_k", 1), ("q6_k", 1), ("q8_0", 3), ("q4_k", 4),
+                                    ("q8_0", 6), ("q6_k", 8)])
 def test_split_k_slices_on_every_xcd_twice(name, m):
     """Three 64-row panels over a long K: the slices of a panel land on all
     eight XCDs (workgroup id x + 3y), so the one-launch K split's atomics,
