@@ -84,6 +84,18 @@ __global__ void __launch_bounds__(256)
   }
 }
 
+// The row multipliers (rowmul) of a lane's epilogue rows in MFMA tile mt,
+// requested together before the tile's stores (a load per element, each
+// waited for before its multiply, put ~64 dependent L2 round trips into
+// every lane's epilogue): row mbase + mt*32 + 8*(r/4) + 4*lh + r%4 for
+// accumulator r, clamped in bounds (rows past M are not stored)
+__device__ __forceinline__ void load_rowmul(const float *__restrict__ rowmul, int mbase, int lh,
+                                            int M, float (&rm)[16]) {
+#pragma unroll
+  for (int r = 0; r < 16; r++)
+    rm[r] = rowmul[min(mbase + 8 * (r >> 2) + 4 * lh + (r & 3), M - 1)];
+}
+
 // ---------------------------------------------------------------------------
 // Tiling.  A workgroup owns a 256 x 128 tile of Y and walks its K range 64
 // elements per step through two LDS stages of A [256][72] and B [128][72]
@@ -398,7 +410,9 @@ __global__ void __launch_bounds__(pg_threads<TM>())
   }
   const bool atomic = gridDim.z > 1;
 #pragma unroll
-  for (int mt = 0; mt < 2; mt++)
+  for (int mt = 0; mt < 2; mt++) {
+    float rm[16];
+    load_rowmul(rowmul, m0 + wm + mt * 32, lh, M, rm);
 #pragma unroll
     for (int nt = 0; nt < 2; nt++) {
       const int n = n0 + wn + nt * 32 + l32;
@@ -406,12 +420,13 @@ __global__ void __launch_bounds__(pg_threads<TM>())
       for (int r = 0; r < 16; r++) {
         const int m = m0 + wm + mt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
         if (m < M && n < N) {
-          const float v = acc[mt][nt][r] * rowmul[m];
+          const float v = acc[mt][nt][r] * rm[r];
           if (atomic) atomicAdd(&Y[(size_t)m * ldy + n], v);
           else Y[(size_t)m * ldy + n] = v;
         }
       }
     }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -627,7 +642,9 @@ __global__ void __launch_bounds__(256)
   if (kDefer) mma(1);
   const bool atomic = gridDim.z > 1;
 #pragma unroll
-  for (int mt = 0; mt < 4; mt++)
+  for (int mt = 0; mt < 4; mt++) {
+    float rm[16];
+    load_rowmul(rowmul, m0 + wm + mt * 32, lh, M, rm);
 #pragma unroll
     for (int nt = 0; nt < 4; nt++) {
       const int n = n0 + wn + nt * 32 + l32;
@@ -635,12 +652,13 @@ __global__ void __launch_bounds__(256)
       for (int r = 0; r < 16; r++) {
         const int m = m0 + wm + mt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
         if (m < M && n < N) {
-          const float v = acc[mt][nt][r] * rowmul[m];
+          const float v = acc[mt][nt][r] * rm[r];
           if (atomic) atomicAdd(&Y[(size_t)m * ldy + n], v);
           else Y[(size_t)m * ldy + n] = v;
         }
       }
     }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -830,7 +848,9 @@ __global__ void __launch_bounds__(256)
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   const bool atomic = gridDim.z > 1;
 #pragma unroll
-  for (int mt = 0; mt < 4; mt++)
+  for (int mt = 0; mt < 4; mt++) {
+    float rm[16];
+    load_rowmul(rowmul, m0 + wr * 128 + mt * 32, lh, M, rm);
 #pragma unroll
     for (int nt = 0; nt < 4; nt++) {
       const int n = n0 + wc * 128 + nt * 32 + l32;
@@ -838,12 +858,13 @@ __global__ void __launch_bounds__(256)
       for (int r = 0; r < 16; r++) {
         const int m = m0 + wr * 128 + mt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3);
         if (m < M && n < N) {
-          const float v = acc[mt][nt][r] * rowmul[m];
+          const float v = acc[mt][nt][r] * rm[r];
           if (atomic) atomicAdd(&Y[(size_t)m * ldy + n], v);
           else Y[(size_t)m * ldy + n] = v;
         }
       }
     }
+  }
 }
 
 // f32 activation rows -> zero-padded f16 rows of ldh = round_up(k, PGK)
