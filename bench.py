@@ -62,10 +62,10 @@ LM_HEAD_WRITE_KIB, LM_HEAD_WRITE_FACTOR = 816.5, 262144.0 / 262144.0
 # taken on): after a change to those files the field is null until the
 # profile's commands are run again and the readings and hash updated here.
 TRAFFIC_SOURCE = "profiles/qwen3_int8_decode_step_kernels_traffic.md (recorded rocprofv3 --pmc)"
-_STEP_KIB = {"qkv": (2157.1, 68.0), "attention": (390.5, 32.0), "o": (1084.0, 64.0),
-             "gate_up": (3206.6, 113.5), "down": (1603.5, 48.0)}
+_STEP_KIB = {"qkv": (2157.1, 68.0), "attention": (377.5, 32.0), "o": (1084.0, 64.0),
+             "gate_up": (3206.6, 113.5), "down": (1605.5, 48.0)}
 STEP_SOURCES = ("synapse_amd/csrc/decode_fused.hip", "synapse_amd/csrc/fused_dev.hpp")
-STEP_SOURCES_SHA16 = "806cbb3ebd7219ae"
+STEP_SOURCES_SHA16 = "971fb96b6fe6cf07"
 
 
 def step_sources_sha16() -> str:
