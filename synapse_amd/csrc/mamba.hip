@@ -258,7 +258,8 @@ __device__ __forceinline__ float syn_softplus_tab(float v, const uint64_t *tab) 
 // are requested at entry (up to DR dt_proj weights and DS state and A_log
 // values in registers; DR = 0 streams longer dt_proj rows).
 // x_proj's output (dt_rank + 2*d_state values, the same for every channel)
-// is staged in LDS.
+// is staged in LDS, and so is expf's table (a lookup in global memory waits
+// for its own round trip, ~34 of them per lane in the scan).
 constexpr int kScanDs = 16, kScanDr = 64;
 
 template <int DR, bool CHAIN, bool ZACC, bool XACC>
@@ -270,6 +271,8 @@ __global__ void __launch_bounds__(64)
                  float *__restrict__ gated) {
   constexpr int DS = kScanDs;
   extern __shared__ float xp[];  // dr + 2*ds
+  __shared__ uint64_t etab[32];
+  if (threadIdx.x < 32) etab[threadIdx.x] = syn_exp2_tab[threadIdx.x];
   const int i0 = blockIdx.x * 64 + threadIdx.x;
   const int i = min(i0, di - 1);
   float wr[DR > 0 ? DR : 1], al[DS], hs[DS];
@@ -311,7 +314,7 @@ __global__ void __launch_bounds__(64)
     }
     dtp = fused ? pf : pp;
   }
-  const float dt = syn_softplus(dtp + dtbi);
+  const float dt = syn_softplus_tab(dtp + dtbi, etab);
   const float dt_x = dt * xi;
   const float *b = xp + dr, *c = xp + dr + ds;
   float yi = 0.0f;
@@ -322,8 +325,8 @@ __global__ void __launch_bounds__(64)
       float contrib[4];
 #pragma unroll
       for (int l = 0; l < 4; l++) {
-        const float e = syn_expf(al[jj + l]);
-        const float ad = syn_expf(-dt * e);
+        const float e = syn_expf_tab(al[jj + l], etab);
+        const float ad = syn_expf_tab(-dt * e, etab);
         const float p1 = ad * hs[jj + l], p2 = dt_x * b[jj + l];
         const float hn = p1 + p2;
         hs[jj + l] = hn;
@@ -336,8 +339,8 @@ __global__ void __launch_bounds__(64)
 #pragma unroll
   for (int jj = 0; jj < DS; jj++) {
     if (jj >= j4 && jj < ds) {
-      const float a = -syn_expf(al[jj]);
-      const float ad = syn_expf(dt * a);
+      const float a = -syn_expf_tab(al[jj], etab);
+      const float ad = syn_expf_tab(dt * a, etab);
       const float p1 = ad * hs[jj], p2 = (dt * b[jj]) * xi;
       const float hn = p1 + p2;
       hs[jj] = hn;
@@ -350,7 +353,7 @@ __global__ void __launch_bounds__(64)
   for (int j = 0; j < DS; j++)
     if (j < ds) hT[(size_t)i * ds + j] = hs[j];
   const float y = yi + dpi * xi;
-  gated[i] = syn_silu(zi) * y;  // int8_mamba.rs:102
+  gated[i] = syn_silu_tab(zi, etab) * y;  // int8_mamba.rs:102
 }
 
 // Fused step of the INT8 x_proj / dt_proj variant: dt_proj (W8A8 over the
