@@ -181,6 +181,9 @@ def test_device_expf_matches_glibc():
                                    # direct-load tiles 256 x 128 and 128 x 128 (a K of 5 and
                                    # 9 steps: a partial last KC chunk), ragged M and N
                                    (300, 640, 16384), (300, 1152, 11000),
+                                   # 128 x 64 tiles with eight waves (fewer than 256 tiles
+                                   # of 128 x 128, at least 256 of 128 x 64), ragged
+                                   (300, 1152, 6000),
                                    # K not whole 128-byte steps: the register-staged kernel
                                    (40, 1040, 700), (520, 1040, 9000)])
 def test_int8_gemm_mfma_bit_exact(m, k, n):
