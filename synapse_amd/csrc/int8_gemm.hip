@@ -408,22 +408,28 @@ syn_status_t launch_gemm_w8a8(const int8_t *xq, size_t ldx, const float *sx, siz
   }
   // K is never split: the chunked f32 epilogue must run in chunk order.
   // Direct-load tiles when K is whole 128-byte steps (the loads cannot
-  // zero a K tail) and the byte offsets fit 32 bits: 128 x 128 with two
-  // stages (two workgroups per CU) when that gives every CU a workgroup,
-  // else 128 x 64 with eight waves (two per SIMD) and four stages when
-  // that does, else 64 x 64 with four stages (two workgroups per CU).
-  // Measured (int8 TOPS): 2048 x 14336 x 4096 1248 against 968 for 256 x
-  // 128 with three stages and four waves (one wave per SIMD), 1201 for the
-  // same tile with eight waves, 988 for k_gemm_w8a8_ws; 512 x 14336 x 4096
-  // 1260 against 914 for 128 x 128 with three stages; 512 x 4096 x 4096
-  // 787-798 against 695-708 for 128 x 64 with four waves and three stages
-  // (one wave per SIMD: nothing hides its barriers and LDS waits; more
-  // stages alone did not help), 767-773 with eight waves and three,
-  // 767-779 for 64 x 64; 128 x 3072 x 1024 119 for 64 x 64 against 110
-  // and 93.
+  // zero a K tail) and the byte offsets fit 32 bits, eight waves (2 x 4
+  // sub-tiles) on 128 x 128 when that gives every CU a workgroup: three
+  // stages when the tiles fit one workgroup per CU, else two (two
+  // workgroups per CU); else 128 x 64 with eight waves and four stages when
+  // that gives every CU a workgroup, else 64 x 64 with four stages (two
+  // workgroups per CU).  Measured (int8 TOPS): 2048 x 4096 x 4096 1351-1354
+  // with eight waves and two stages against 1185-1232 with four waves,
+  // 2048 x 14336 x 4096 1298-1357 against 1236-1290, 512 x 14336 x 4096
+  // 1339-1344 against 1248 (with four waves there is one wave per SIMD per
+  // workgroup: little hides the barriers and LDS waits); 1024 x 4096 x 4096
+  // (256 tiles) 1151-1154 with three stages against 926-932 with two;
+  // earlier, 256 x 128 tiles 968 (four waves) and 1201 (eight), 988 for
+  // k_gemm_w8a8_ws.  512 x 4096 x 4096 787-798 against 695-708 for 128 x
+  // 64 with four waves and three stages (more stages alone did not help),
+  // 767-773 with eight waves and three, 767-779 for 64 x 64; 128 x 3072 x
+  // 1024 119 for 64 x 64 against 110 and 93.
   if (C % 8 == 0 && (uintptr_t)xq % 16 == 0 && M * ldx < ((size_t)1 << 31)) {
-    if (cdiv(M, 128) * cdiv(N, 128) >= 256)
-      return launch_w8a8_dl<128, 128, 2, 2>(xq, ldx, sx, M, W, ws, N, C, y, ldy, s);
+    const size_t tiles = cdiv(M, 128) * cdiv(N, 128);
+    if (tiles == 256)
+      return launch_w8a8_dl<128, 128, 3, 4>(xq, ldx, sx, M, W, ws, N, C, y, ldy, s);
+    if (tiles > 256)
+      return launch_w8a8_dl<128, 128, 2, 4>(xq, ldx, sx, M, W, ws, N, C, y, ldy, s);
     if (cdiv(M, 128) * cdiv(N, 64) >= 256)
       return launch_w8a8_dl<128, 64, 4, 4>(xq, ldx, sx, M, W, ws, N, C, y, ldy, s);
     return launch_w8a8_dl<64, 64, 4, 2>(xq, ldx, sx, M, W, ws, N, C, y, ldy, s);

@@ -184,6 +184,8 @@ def test_device_expf_matches_glibc():
                                    # 128 x 64 tiles with eight waves (fewer than 256 tiles
                                    # of 128 x 128, at least 256 of 128 x 64), ragged
                                    (300, 1152, 6000),
+                                   # exactly 256 tiles of 128 x 128: three stages
+                                   (250, 640, 16384),
                                    # K not whole 128-byte steps: the register-staged kernel
                                    (40, 1040, 700), (520, 1040, 9000)])
 def test_int8_gemm_mfma_bit_exact(m, k, n):
