@@ -207,7 +207,7 @@ __global__ void __launch_bounds__(TM * 2 + 256)
 // columns wc*TN/2, as (TM/WR/32) x (TN/64) MFMA tiles of 32 x 32, so every
 // 16-byte fragment read from LDS feeds that many MFMAs.  Both operands go from
 // global memory straight into LDS (gfx950 global_load_lds_dwordx4: no
-// staging registers, no ds_write), three 128-byte K steps deep:
+// staging registers, no ds_write), NS 128-byte K steps deep:
 //  - activations as TM rows of 128 bytes; the eight 16-byte chunks of row r
 //    sit XOR-swizzled (chunk c at slot c ^ ((r / 2) % 8)): the 64 banks of
 //    4 bytes span two rows, and the fragment reads of 16 consecutive rows
@@ -217,8 +217,10 @@ __global__ void __launch_bounds__(TM * 2 + 256)
 //    load per (panel, chunk), read back conflict-free.
 // One barrier per step; the i32 sums of each KC = 512 chunk (4 steps) are
 // folded into the f32 tile as in k_gemm_w8a8_ws.  NS stages: the loads run
-// NS - 1 steps ahead (3 stages of the 128 x 128 tile would keep a second
-// workgroup off the CU).
+// NS - 1 steps ahead (3 stages of the 128 x 128 tile keep a second
+// workgroup off the CU).  WR = 4 gives two waves per SIMD in one workgroup,
+// which is what hides the per-step barrier and the LDS waits (WR = 2 with a
+// single workgroup per CU leaves one wave per SIMD).
 template <int TM, int TN> constexpr int dl_stage() { return (TM + TN) * 128; }
 template <int TM, int TN, int NS> constexpr size_t dl_lds_bytes() {
   return (size_t)NS * dl_stage<TM, TN>() + TM * sizeof(float);
