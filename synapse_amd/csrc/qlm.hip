@@ -271,8 +271,11 @@ struct syn_hip_qlm_s {
     for (auto &Ly : layers) {
       Ly.f_qkv = plan_split_gemv(Ly.qkv.w.p, Ly.qkv.scales.as<float>(), (int)n_qkv,
                                  Ly.qkv.chunks, target, 256);
+      // O on 512 threads (two waves per SIMD): 658.4 against 659.8 us per
+      // token at positions 20-84; 512 measured slower for QKV (669 against
+      // 660) and gate|up (663)
       Ly.f_o =
-          plan_split_gemv(Ly.o.w.p, Ly.o.scales.as<float>(), (int)h, Ly.o.chunks, target, 256);
+          plan_split_gemv(Ly.o.w.p, Ly.o.scales.as<float>(), (int)h, Ly.o.chunks, target, 512);
       Ly.f_gu = plan_split_gemv(Ly.gu.w.p, Ly.gu.scales.as<float>(), (int)(2 * inter),
                                 Ly.gu.chunks, target, 256);
       Ly.f_down = plan_split_gemv(Ly.down.w.p, Ly.down.scales.as<float>(), (int)h,
