@@ -62,10 +62,11 @@ LM_HEAD_WRITE_KIB, LM_HEAD_WRITE_FACTOR = 816.5, 262144.0 / 262144.0
 # taken on): after a change to those files the field is null until the
 # profile's commands are run again and the readings and hash updated here.
 TRAFFIC_SOURCE = "profiles/qwen3_int8_decode_step_kernels_traffic.md (recorded rocprofv3 --pmc)"
-_STEP_KIB = {"qkv": (2157.1, 68.0), "attention": (377.5, 32.0), "o": (1084.0, 64.0),
+_STEP_KIB = {"qkv": (2157.1, 68.0), "attention": (377.5, 32.0), "o": (1078.0, 64.0),
              "gate_up": (3206.6, 113.5), "down": (1605.5, 48.0)}
-STEP_SOURCES = ("synapse_amd/csrc/decode_fused.hip", "synapse_amd/csrc/fused_dev.hpp")
-STEP_SOURCES_SHA16 = "971fb96b6fe6cf07"
+STEP_SOURCES = ("synapse_amd/csrc/decode_fused.hip", "synapse_amd/csrc/fused_dev.hpp",
+                "synapse_amd/csrc/qlm.hip")
+STEP_SOURCES_SHA16 = "43f9074b6c63b25e"
 
 
 def step_sources_sha16() -> str:
@@ -105,7 +106,7 @@ def step_kernel_bytes(c, pos):
 STEP_KERNEL_NAMES = {
     "qkv": "k_fused_gemv<0,256,U,false,R> (residual + RMSNorm + quantize + QKV GEMV)",
     "attention": "k_attn_head<false,128> (head norms, RoPE, KV append, attention)",
-    "o": "k_fused_gemv<1,256,U,false,R> (quantize + O GEMV)",
+    "o": "k_fused_gemv<1,512,U,false,R> (quantize + O GEMV)",
     "gate_up": "k_fused_gemv<0,256,U,true,R> (residual + RMSNorm + quantize + gate|up GEMV in "
                "panel pairs, split K, SwiGLU in each pair's last slice)",
     "down": "k_fused_gemv<5,512,U,false,R> (quantize h range + down GEMV)",
