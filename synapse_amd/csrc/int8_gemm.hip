@@ -13,6 +13,7 @@
 // layout (linear.hpp), so a 128-byte K step of a panel is 8 contiguous 1 KiB
 // chunk blocks.
 #include <algorithm>
+#include <type_traits>
 
 #include "linear.hpp"
 #include "lds_dma.hpp"
@@ -216,7 +217,10 @@ __global__ void __launch_bounds__(TM * 2 + 256)
 //  - weights as stored, [panel][chunk][64 rows][16 bytes]: one 1 KiB direct
 //    load per (panel, chunk), read back conflict-free.
 // One barrier per step; the i32 sums of each KC = 512 chunk (4 steps) are
-// folded into the f32 tile as in k_gemm_w8a8_ws.  NS stages: the loads run
+// folded into the f32 tile as in k_gemm_w8a8_ws: after the chunk's last
+// step, or (DF) from a second accumulator set, four elements per step
+// between the next chunk's MFMAs, so that the fold's VALU work overlaps the
+// matrix cores (every fold still adds the chunks in order).  NS stages: the loads run
 // NS - 1 steps ahead (3 stages of the 128 x 128 tile keep a second
 // workgroup off the CU).  WR = 4 gives two waves per SIMD in one workgroup,
 // which is what hides the per-step barrier and the LDS waits (WR = 2 with a
@@ -226,7 +230,7 @@ template <int TM, int TN, int NS> constexpr size_t dl_lds_bytes() {
   return (size_t)NS * dl_stage<TM, TN>() + TM * sizeof(float);
 }
 
-template <int TM, int TN, int NS, int WR>
+template <int TM, int TN, int NS, int WR, bool DF>
 __global__ void __launch_bounds__(128 * WR)
     k_gemm_w8a8_dl(const int8_t *__restrict__ xq, int ldx, const float *__restrict__ sx, int M,
                    const i32x4 *__restrict__ W, const float *__restrict__ ws, int N, int C,
@@ -275,15 +279,17 @@ __global__ void __launch_bounds__(128 * WR)
 #pragma unroll
   for (int i = 0; i < NS; i++) dma(i, i);
 
-  // row scales of the tile in LDS (read at each chunk fold), the lane's
-  // column scales in registers
+  // row scales of the tile through LDS (into registers after the first
+  // barrier), the lane's column scales in registers
   float *sa_l = reinterpret_cast<float *>(dlds + NS * STAGE);
   if (tid < TM) sa_l[tid] = sx[min(m0 + tid, M - 1)];
   float sb[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; nt++)
     sb[nt] = ws[min(n0 + wc * WN + nt * 32 + l32, (last_panel + 1) * 64 - 1)];
-  i32x16 acc[MT][NT];
+  // two accumulator sets: chunk c adds into acc[c % 2] while the fold of
+  // chunk c - 1 (VALU) runs between its MFMAs
+  i32x16 acc[2][MT][NT];
   float cf[MT][NT][16];
 #pragma unroll
   for (int mt = 0; mt < MT; mt++)
@@ -291,7 +297,8 @@ __global__ void __launch_bounds__(128 * WR)
     for (int nt = 0; nt < NT; nt++)
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        acc[mt][nt][r] = 0;
+        acc[0][mt][nt][r] = 0;
+        acc[1][mt][nt][r] = 0;
         cf[mt][nt][r] = 0.0f;
       }
   // fragment addresses inside a stage: A row (wr*WM + mt*32 + l32), whose
@@ -315,42 +322,54 @@ __global__ void __launch_bounds__(128 * WR)
     for (int nt = 0; nt < NT; nt++)
       fb[b][nt] = *reinterpret_cast<const i32x4 *>(st + boff[nt] + c * 1024);
   };
-  auto mma = [&](int b) {
+  auto mma = [&](auto Pc, const i32x4 (&a)[MT], const i32x4 (&b)[NT]) {
+    constexpr int P = decltype(Pc)::value;
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
       for (int nt = 0; nt < NT; nt++)
-        acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[b][mt], fb[b][nt], acc[mt][nt],
-                                                            0, 0, 0);
+        acc[P][mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[mt], b[nt], acc[P][mt][nt],
+                                                               0, 0, 0);
   };
-  auto fold = [&]() {  // C += (f32(acc) * sa) * sb, then a new chunk
+  // fold of accumulator element r of set Q: C += (f32(acc) * sa) * sb, and
+  // the element starts the set's next chunk at zero
+  float sar[MT][16];
+  auto fold_el = [&](auto Qc, int r) {
+    constexpr int Q = decltype(Qc)::value;
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-      for (int nt = 0; nt < NT; nt++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const float f =
-              (float)acc[mt][nt][r] * sa_l[wr * WM + mt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3)];
-          const float t = f * sb[nt];
-          cf[mt][nt][r] = cf[mt][nt][r] + t;
-          acc[mt][nt][r] = 0;
-        }
+      for (int nt = 0; nt < NT; nt++) {
+        const float sa =
+            DF ? sar[mt][r] : sa_l[wr * WM + mt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3)];
+        const float f = (float)acc[Q][mt][nt][r] * sa;
+        const float t = f * sb[nt];
+        cf[mt][nt][r] = cf[mt][nt][r] + t;
+        acc[Q][mt][nt][r] = 0;
+      }
   };
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  using NoFold = std::false_type;
+  using Fold = std::true_type;
 
-  // Step t lives in stage t % NS.  Iteration t: K slices 0-2 of step t
-  // (each beside the reads of the next slice); the barrier that publishes
-  // step t+1 (and the row scales, before the first); the load of step t+NS
-  // into the stage step t has left; step t+1's slice 0 reads beside step
-  // t's slice 3 (clamped, unused data after the last step).
-  kr_publish<(NS - 1) * AFTER>();
-  read(0, 0, 0);
-  for (int t = 0; t < nsteps; t++) {
+  // Step t lives in stage t % NS.  Step t: K slices 0-2 (each beside the
+  // reads of the next slice); the barrier that publishes step t+1 (and the
+  // row scales, before the first); the load of step t+NS into the stage
+  // step t has left; step t+1's slice 0 reads beside step t's slice 3
+  // (clamped, unused data after the last step).  Step s of a chunk also
+  // folds elements 4s .. 4s+3 of the other set (the previous chunk), one
+  // after each slice's MFMAs.
+  auto step = [&](int t, int s, auto Pc, auto Fc) {
+    constexpr int P = decltype(Pc)::value;
+    constexpr bool F = decltype(Fc)::value;
+    using Q = std::integral_constant<int, 1 - P>;
     const int cur = t % NS, nxt = cur == NS - 1 ? 0 : cur + 1;
 #pragma unroll
     for (int kk = 0; kk < 3; kk++) {
       read(cur, kk + 1, (kk + 1) & 1);
-      mma(kk & 1);
+      mma(Pc, fa[kk & 1], fb[kk & 1]);
+      if constexpr (F) fold_el(Q{}, 4 * s + kk);
     }
     kr_publish<(NS - 2) * AFTER>();
     dma(t + NS, cur);
@@ -360,12 +379,67 @@ __global__ void __launch_bounds__(128 * WR)
 #pragma unroll
     for (int nt = 0; nt < NT; nt++) b3[nt] = fb[1][nt];
     read(nxt, 0, 0);
+    mma(Pc, a3, b3);
+    if constexpr (F) fold_el(Q{}, 4 * s + 3);
+  };
+  // whole chunk c (steps 4c .. 4c+3) into set P, folding the other set
+  // (the previous chunk) when F
+  auto chunk = [&](int c, auto Pc, auto Fc) {
+#pragma unroll
+    for (int s = 0; s < 4; s++) step(4 * c + s, s, Pc, Fc);
+  };
+  auto fold_all = [&](auto Qc) {
+#pragma unroll
+    for (int r = 0; r < 16; r++) fold_el(Qc, r);
+  };
+  // a last, shorter chunk c into set P: the previous chunk's fold first
+  auto tail = [&](int c, auto Pc) {
+    using Q = std::integral_constant<int, 1 - decltype(Pc)::value>;
+    if (c > 0) fold_all(Q{});
+    for (int t = 4 * c; t < nsteps; t++) step(t, 0, Pc, NoFold{});
+    fold_all(Pc);
+  };
+
+  kr_publish<(NS - 1) * AFTER>();
+  if constexpr (DF) {
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
-      for (int nt = 0; nt < NT; nt++)
-        acc[mt][nt] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a3[mt], b3[nt], acc[mt][nt], 0, 0, 0);
-    if (((t + 1) & 3) == 0 || t + 1 == nsteps) fold();
+      for (int r = 0; r < 16; r++)
+        sar[mt][r] = sa_l[wr * WM + mt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3)];
+  }
+  read(0, 0, 0);
+  if constexpr (!DF) {
+    // one accumulator set, folded after each chunk's last step
+    for (int t = 0; t < nsteps; t++) {
+      step(t, 0, P0{}, NoFold{});
+      if (((t + 1) & 3) == 0 || t + 1 == nsteps) fold_all(P0{});
+    }
+  } else {
+    const int nfull = nsteps >> 2;
+    int c = 0;
+    if (nfull > 0) {
+      chunk(0, P0{}, NoFold{});
+      for (c = 1; c + 1 < nfull; c += 2) {
+        chunk(c, P1{}, Fold{});
+        chunk(c + 1, P0{}, Fold{});
+      }
+      if (c < nfull) {
+        chunk(c, P1{}, Fold{});
+        c++;
+      }
+    }
+    // c == nfull: set (nfull - 1) % 2 holds the last whole chunk
+    if (nsteps & 3) {
+      if (c & 1)
+        tail(c, P1{});
+      else
+        tail(c, P0{});
+    } else if (c & 1) {
+      fold_all(P0{});
+    } else if (c > 0) {
+      fold_all(P1{});
+    }
   }
   // the prefetches past the last step must land before the workgroup's LDS
   // can go to another workgroup
@@ -383,19 +457,19 @@ __global__ void __launch_bounds__(128 * WR)
     }
 }
 
-template <int TM, int TN, int NS, int WR>
+template <int TM, int TN, int NS, int WR, bool DF>
 static syn_status_t launch_w8a8_dl(const int8_t *xq, size_t ldx, const float *sx, size_t M,
                                    const void *W, const float *ws, size_t N, int C, float *y,
                                    size_t ldy, hipStream_t s) {
   static bool attr_set = false;  // more than the default 64 KiB of dynamic LDS
   constexpr size_t shm = dl_lds_bytes<TM, TN, NS>();
   if (!attr_set) {
-    SYN_HIP(hipFuncSetAttribute((const void *)k_gemm_w8a8_dl<TM, TN, NS, WR>,
+    SYN_HIP(hipFuncSetAttribute((const void *)k_gemm_w8a8_dl<TM, TN, NS, WR, DF>,
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)shm));
     attr_set = true;
   }
   const dim3 grid((unsigned)cdiv(N, TN), (unsigned)cdiv(M, TM));
-  SYN_LAUNCH((k_gemm_w8a8_dl<TM, TN, NS, WR>), grid, dim3(128 * WR), shm, s, xq, (int)ldx, sx, (int)M,
+  SYN_LAUNCH((k_gemm_w8a8_dl<TM, TN, NS, WR, DF>), grid, dim3(128 * WR), shm, s, xq, (int)ldx, sx, (int)M,
              (const i32x4 *)W, ws, (int)N, C, y, (int)ldy);
   SYN_LAUNCH_CHECK();
   return SYN_OK;
@@ -425,16 +499,23 @@ syn_status_t launch_gemm_w8a8(const int8_t *xq, size_t ldx, const float *sx, siz
   // k_gemm_w8a8_ws.  512 x 4096 x 4096 787-798 against 695-708 for 128 x
   // 64 with four waves and three stages (more stages alone did not help),
   // 767-773 with eight waves and three, 767-779 for 64 x 64; 128 x 3072 x
-  // 1024 119 for 64 x 64 against 110 and 93.
+  // 1024 119 for 64 x 64 against 110 and 93.  The fold of a chunk runs
+  // under the next chunk's MFMAs (DF) where one workgroup's waves are all
+  // a SIMD has: 512 x 4096 x 4096 936-943 against 785-793, 1024 x 4096 x
+  // 4096 1158-1164 against 1097-1105 (three stages; 1005-1037 with two),
+  // 128 x 3072 x 1024 128 against 122.  With two workgroups per CU the other
+  // workgroup hides the fold, and DF's second accumulator set (221 VGPRs
+  // on 128 x 128) would leave room for one: 2048 x 4096 x 4096 1047-1076
+  // with DF and three stages, 1033-1103 with two.
   if (C % 8 == 0 && (uintptr_t)xq % 16 == 0 && M * ldx < ((size_t)1 << 31)) {
     const size_t tiles = cdiv(M, 128) * cdiv(N, 128);
     if (tiles == 256)
-      return launch_w8a8_dl<128, 128, 3, 4>(xq, ldx, sx, M, W, ws, N, C, y, ldy, s);
+      return launch_w8a8_dl<128, 128, 3, 4, true>(xq, ldx, sx, M, W, ws, N, C, y, ldy, s);
     if (tiles > 256)
-      return launch_w8a8_dl<128, 128, 2, 4>(xq, ldx, sx, M, W, ws, N, C, y, ldy, s);
+      return launch_w8a8_dl<128, 128, 2, 4, false>(xq, ldx, sx, M, W, ws, N, C, y, ldy, s);
     if (cdiv(M, 128) * cdiv(N, 64) >= 256)
-      return launch_w8a8_dl<128, 64, 4, 4>(xq, ldx, sx, M, W, ws, N, C, y, ldy, s);
-    return launch_w8a8_dl<64, 64, 4, 2>(xq, ldx, sx, M, W, ws, N, C, y, ldy, s);
+      return launch_w8a8_dl<128, 64, 4, 4, true>(xq, ldx, sx, M, W, ws, N, C, y, ldy, s);
+    return launch_w8a8_dl<64, 64, 4, 2, true>(xq, ldx, sx, M, W, ws, N, C, y, ldy, s);
   }
   // otherwise 256-row tiles, or 128-row tiles when the larger ones cannot
   // fill the GPU

@@ -186,6 +186,11 @@ def test_device_expf_matches_glibc():
                                    (300, 1152, 6000),
                                    # exactly 256 tiles of 128 x 128: three stages
                                    (250, 640, 16384),
+                                   # chunk counts: K of 1 step (no whole KC chunk), 3, 12
+                                   # (three whole chunks, no tail) and 14 (three and a tail
+                                   # of two), on each direct-load tile shape
+                                   (200, 128, 20000), (40, 384, 700), (300, 1536, 9000),
+                                   (300, 1792, 11000),
                                    # K not whole 128-byte steps: the register-staged kernel
                                    (40, 1040, 700), (520, 1040, 9000)])
 def test_int8_gemm_mfma_bit_exact(m, k, n):
