@@ -108,9 +108,12 @@ constexpr int PGM = 256, PGN = 128, PGK = 64, PGLD = PGK + 8;  // LDS row stride
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
+// (d as a 16-bit field: held as a 32-bit value, the ring's copies at the
+// producer loop's back edge zero-extended each pending scale load, and the
+// wait for it drained the ring every iteration)
 struct RawW {
   u32x4 q0, q1, q2;  // quant planes (format-dependent)
-  uint32_t d;        // f16 bits of the block scale (Q8_0, Q6_K)
+  uint16_t d;        // f16 bits of the block scale (Q8_0, Q6_K)
 };
 
 __device__ __forceinline__ uint32_t u32x4_word(const u32x4 &v, int i) {
@@ -272,8 +275,13 @@ template <int TM> constexpr int pg_stage() { return (TM + PGN) * PGLD; }
 // ring.  One barrier per step separates the stages.  On each SIMD the matrix
 // core work of two consumer waves overlaps the loads, decode and LDS stores
 // of one producer wave.  Each role runs its own loop (its values stay out of
-// the other role's registers); both meet the same barriers.
-constexpr int kPDepth = 2;
+// the other role's registers); both meet the same barriers.  Ring depth:
+// four steps for TM = 128 (its 137 consumer VGPRs already keep a second
+// workgroup off the CU, so the producers' extra registers cost nothing),
+// two for TM = 256 (three waves per SIMD: at most 170 VGPRs).  Measured at
+// M = 512 (Q8_0 Mistral set): 597-603 TF/s against 593-596 with two steps
+// and 584-587 before the scale fix in RawW.
+template <int TM> constexpr int pg_depth() { return TM == 128 ? 4 : 2; }
 template <int TM> constexpr int pg_threads() { return TM * 2 + 256; }
 
 template <int FMT, bool EXACT, int TM>
@@ -284,7 +292,7 @@ __global__ void __launch_bounds__(pg_threads<TM>())
                int steps_per_split) {
   extern __shared__ __attribute__((aligned(16))) _Float16 lds[];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  constexpr int NC = TM / 32, AI = TM / 32, PG_STAGE = pg_stage<TM>();
+  constexpr int NC = TM / 32, AI = TM / 32, PG_STAGE = pg_stage<TM>(), kPDepth = pg_depth<TM>();
   const int n0 = blockIdx.x * PGN, m0 = blockIdx.y * TM;
   const int s_begin = blockIdx.z * steps_per_split;
   const int nsteps = min((K + PGK - 1) / PGK - s_begin, steps_per_split);
