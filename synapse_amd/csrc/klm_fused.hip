@@ -28,6 +28,7 @@
 // results agree with it to rounding (tests grade this path by tolerance
 // against the oracle).
 #include <algorithm>
+#include <type_traits>
 
 #include "decode_fused.hpp"
 #include "klm_fused.hpp"
@@ -146,13 +147,14 @@ __device__ __forceinline__ void pin_plane(const u32x4 &v) {
   asm volatile("" : "+v"(w));
 }
 
-// One 256-element unit in eight stages of 32 activations: with DB the
+// One 256-element unit in eight stages of 32 activations (or stages
+// [T0, T0 + NS) of it, for a wave that takes part of a unit): with DB the
 // activations of stage t+1 are read from LDS before stage t's FMAs (two
 // register buffers), else each stage reads its own (one buffer, for
 // workgroups of 16 waves whose register budget is 128; other waves hide the
 // LDS latency).  The scheduling barriers keep the compiler from hoisting all
 // 256 reads.
-template <int FMT, bool DB>
+template <int FMT, bool DB, int T0 = 0, int NS = 8>
 __device__ __forceinline__ void kqf_unit(u32x4 *pl, const uint16_t *dh, const float *xs,
                                          const float *as, float &acc) {
   asm volatile("" ::: "memory");  // no LDS read of the unit moves above its branch
@@ -187,11 +189,11 @@ __device__ __forceinline__ void kqf_unit(u32x4 *pl, const uint16_t *dh, const fl
 #pragma unroll
     for (int j = 0; j < 8; j++) dq[j] = syn_f16_to_f32_rs(dh[j]);
   }
-  if constexpr (DB) lds_x32(xb[0], xs);
+  if constexpr (DB) lds_x32(xb[T0 & 1], xs + T0 * 32);
 #pragma unroll
-  for (int t = 0; t < 8; t++) {
+  for (int t = T0; t < T0 + NS; t++) {
     if constexpr (DB) {
-      if (t + 1 < 8) lds_x32(xb[(t + 1) & 1], xs + (t + 1) * 32);
+      if (t + 1 < T0 + NS) lds_x32(xb[(t + 1) & 1], xs + (t + 1) * 32);
     } else {
       lds_x32(xb[0], xs + t * 32);
     }
@@ -260,7 +262,8 @@ __device__ __forceinline__ void kqf_q40_part(u32x4 *pl, const uint16_t *dh, cons
 // grid (row groups, K splits), NW waves (NW >= bs).  Row group = a 64-row
 // panel (lane = row), or for OUT_GU 32 gate rows j.. and the 32 up rows
 // inter+j.. in lanes 32..63 (two 512-byte halves of a plane load).  Split s
-// covers the units [s*bs, s*bs + bs), one per wave, all requested at entry.
+// covers the units [s*bs, s*bs + bs), one per wave (or WPU waves per unit,
+// each a part of its stages), all requested at entry.
 // Prologue threads hold 4 consecutive elements per round, so an activation
 // group (32 elements for Q4_K, 16 for Q6_K) is summed across 8 or 4 lanes.
 // dynamic LDS: activation slice [bs*256] | group sums [bs*256/GRP] |
@@ -269,7 +272,9 @@ template <int FMT, int PRO, int OUT, int NW, int WPU>
 __global__ void __launch_bounds__(NW * 64)
     k_kqf_gemv(const u32x4 *__restrict__ W, const uint16_t *__restrict__ Wd, int B, int N,
                int bs, KqfIn in, KqfOut out) {
-  static_assert(WPU == 1 || FMT == SYN_HIP_FMT_Q4_0, "split units are Q4_0 only");
+  static_assert(WPU == 1 || FMT == SYN_HIP_FMT_Q4_0 ||
+                    ((FMT == SYN_HIP_FMT_Q4_K || FMT == SYN_HIP_FMT_Q6_K) && OUT == OUT_ACC),
+                "split units: Q4_0, or Q4_K / Q6_K into the split-K accumulator");
   constexpr int NBP = 8 / WPU;  // Q4_0 blocks per wave when WPU > 1
   using F = KqfFmt<FMT>;
   constexpr int kNT = NW * 64;
@@ -307,7 +312,33 @@ __global__ void __launch_bounds__(NW * 64)
   const bool has_unit = uw < nu_wg;
   u32x4 buf[F::NPU];
   uint16_t dbuf[F::DPU > 0 ? F::DPU : 1];
+  // Q4_K / Q6_K parts: stages [T0, T0 + 8 / WPU) of the unit, with only the
+  // planes those stages read (Q4_K: plane 0 and the stages' sub-block
+  // planes; Q6_K: the stages' ql planes, their qh planes, the scale plane
+  // and d), requested right before they are decoded
+  constexpr bool kKqPart = WPU > 1 && FMT != SYN_HIP_FMT_Q4_0;
+  auto kq_part = [&](auto T0c, float &a) {
+    constexpr int T0 = decltype(T0c)::value;
+    const int u = u0 + uw;
+    const u32x4 *src = Wl + (size_t)u * F::NPB * 64;
+    if constexpr (FMT == SYN_HIP_FMT_Q4_K) {
+      buf[0] = __builtin_nontemporal_load(src);
+#pragma unroll
+      for (int t = T0; t < T0 + NBP; t++) buf[1 + t] = __builtin_nontemporal_load(src + (1 + t) * 64);
+    } else if constexpr (FMT == SYN_HIP_FMT_Q6_K) {
+#pragma unroll
+      for (int t = T0; t < T0 + NBP; t++) {
+        buf[t] = __builtin_nontemporal_load(src + t * 64);
+        if (t == T0 || (t & 1) == 0)
+          buf[8 + (t >> 1)] = __builtin_nontemporal_load(src + (8 + (t >> 1)) * 64);
+      }
+      buf[12] = __builtin_nontemporal_load(src + 12 * 64);
+      dbuf[0] = __builtin_nontemporal_load(Wdl + (size_t)u * 64);
+    }
+    kqf_unit<FMT, (NW < 16), T0, NBP>(buf, dbuf, xs + uw * 256, as + uw * GPU, a);
+  };
   auto issue_unit = [&]() {
+    if (kKqPart) return;
     if (has_unit) {
       const int u = u0 + uw;
       const u32x4 *src = Wl + (size_t)u * F::BPU * F::NPB * 64;
@@ -328,7 +359,15 @@ __global__ void __launch_bounds__(NW * 64)
     }
   };
   auto compute_unit = [&](float &a) {
-    if constexpr (WPU > 1)
+    if constexpr (kKqPart && WPU == 2) {
+      if (uh == 0) kq_part(std::integral_constant<int, 0>{}, a);
+      else kq_part(std::integral_constant<int, 4>{}, a);
+    } else if constexpr (kKqPart) {
+      if (uh == 0) kq_part(std::integral_constant<int, 0>{}, a);
+      else if (uh == 1) kq_part(std::integral_constant<int, 2>{}, a);
+      else if (uh == 2) kq_part(std::integral_constant<int, 4>{}, a);
+      else kq_part(std::integral_constant<int, 6>{}, a);
+    } else if constexpr (WPU > 1)
       kqf_q40_part<(NW < 16), NBP>(buf, dbuf, xs + uw * 256 + uh * (256 / WPU),
                                    as + uw * GPU + uh * NBP, a);
     else
@@ -871,11 +910,41 @@ syn_status_t launch_gemv(const KqfW &w, const KqfPlan &p, const KqfIn &in, const
   const u32x4 *W = static_cast<const u32x4 *>(w.wq);
   const uint16_t *Wd = static_cast<const uint16_t *>(w.wd);
   switch (w.fmt) {
+    // Q4_K / Q6_K into the split-K accumulator: four (else two) waves per
+    // unit while they fit the workgroup, each decoding a quarter (half) of
+    // it, so the decode left after the last weights land is shorter
+    // (LLaMA-3.2-3B step: 1.002-1.007 ms/token against 1.015 with two and
+    // 1.051-1.055 with one; with four, splitting K towards 128, 300 or 400
+    // workgroups instead of 200 measured 1.061, 1.155 and 1.094)
     case SYN_HIP_FMT_Q4_K:
+      if constexpr (OUT == OUT_ACC) {
+        if (4 * p.bs <= kMaxNW) {
+          launch_nw<SYN_HIP_FMT_Q4_K, PRO, OUT, 4>(waves_for(4 * p.bs), grid, lds, s, W, Wd,
+                                                   w.blocks, (int)w.n, p.bs, in, o);
+          break;
+        }
+        if (2 * p.bs <= kMaxNW) {
+          launch_nw<SYN_HIP_FMT_Q4_K, PRO, OUT, 2>(waves_for(2 * p.bs), grid, lds, s, W, Wd,
+                                                   w.blocks, (int)w.n, p.bs, in, o);
+          break;
+        }
+      }
       launch_nw<SYN_HIP_FMT_Q4_K, PRO, OUT>(nw, grid, lds, s, W, Wd, w.blocks, (int)w.n, p.bs, in,
                                             o);
       break;
     case SYN_HIP_FMT_Q6_K:
+      if constexpr (OUT == OUT_ACC) {
+        if (4 * p.bs <= kMaxNW) {
+          launch_nw<SYN_HIP_FMT_Q6_K, PRO, OUT, 4>(waves_for(4 * p.bs), grid, lds, s, W, Wd,
+                                                   w.blocks, (int)w.n, p.bs, in, o);
+          break;
+        }
+        if (2 * p.bs <= kMaxNW) {
+          launch_nw<SYN_HIP_FMT_Q6_K, PRO, OUT, 2>(waves_for(2 * p.bs), grid, lds, s, W, Wd,
+                                                   w.blocks, (int)w.n, p.bs, in, o);
+          break;
+        }
+      }
       launch_nw<SYN_HIP_FMT_Q6_K, PRO, OUT>(nw, grid, lds, s, W, Wd, w.blocks, (int)w.n, p.bs, in,
                                             o);
       break;
