@@ -93,6 +93,8 @@ def _declare(L):
                                              C.c_float]),
         "orc_chacha_block": (None, [P, C.c_uint64, C.c_uint64, C.c_int, P]),
         "orc_stdrng_f32": (None, [C.c_uint64, SZ, P]),
+        "orc_pcg32_step": (C.c_uint64, [C.c_uint64, C.c_uint64]),
+        "orc_pcg32_xsh_rr": (C.c_uint32, [C.c_uint64]),
         "orc_ternary_from_f32": (None, [P, SZ, SZ, P]),
         "orc_ternary_forward": (None, [P, SZ, SZ, P, SZ, P]),
         "orc_attention_decode": (None, [P, P, P, SZ, SZ, SZ, SZ, P]),
@@ -357,6 +359,16 @@ def chacha_block(key, counter: int, stream: int, rounds: int) -> np.ndarray:
     out = np.zeros(16, np.uint32)
     lib().orc_chacha_block(_p(k), counter, stream, rounds, _p(out))
     return out
+
+
+def pcg32_step(state: int, inc: int) -> int:
+    """PCG32's LCG step: state * 6364136223846793005 + inc (mod 2^64)."""
+    return int(lib().orc_pcg32_step(state, inc))
+
+
+def pcg32_xsh_rr(state: int) -> int:
+    """PCG32's XSH-RR output of a 64-bit state."""
+    return int(lib().orc_pcg32_xsh_rr(state))
 
 
 def stdrng_f32(seed: int, n: int) -> np.ndarray:

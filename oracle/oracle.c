@@ -1778,7 +1778,8 @@ uint32_t orc_sample_combined(float *logits, size_t n, const uint32_t *hist, size
 /* ---- the random stream: rand 0.8.5 StdRng = rand_chacha 0.3.1 ChaCha12Rng,
  * seeded by rand_core 0.6.4 SeedableRng::seed_from_u64 (third-party crates,
  * not vendored in the reference; restated from their published algorithms,
- * parity unpinned beyond the ChaCha block test vector of RFC 8439) ---- */
+ * parity unpinned beyond the ChaCha block test vector of RFC 8439 and
+ * PCG32's demo stream) ---- */
 
 static uint32_t rotl32(uint32_t x, int r) { return (x << r) | (x >> (32 - r)); }
 
@@ -1806,15 +1807,26 @@ void orc_chacha_block(const uint32_t key[8], uint64_t counter, uint64_t stream, 
   for (int i = 0; i < 16; i++) out[i] = x[i] + s[i];
 }
 
+/* PCG32's LCG step (multiplier 6364136223846793005, increment inc) and its
+ * XSH-RR output function (O'Neill's pcg32_random_r), exported so that the
+ * tests can pin both against the PCG reference implementation's published
+ * demo stream */
+uint64_t orc_pcg32_step(uint64_t state, uint64_t inc) {
+  return state * 6364136223846793005ull + inc;
+}
+uint32_t orc_pcg32_xsh_rr(uint64_t state) {
+  const uint32_t xorshifted = (uint32_t)(((state >> 18) ^ state) >> 27);
+  const uint32_t rot = (uint32_t)(state >> 59);
+  return (xorshifted >> rot) | (xorshifted << ((32 - rot) & 31));
+}
+
 /* seed_from_u64: the 32-byte seed from a PCG32 sequence (state advanced
- * first, XSH-RR output), little-endian words */
+ * first, then the XSH-RR output of the new state), little-endian words */
 static void seed_from_u64(uint64_t state, uint32_t key[8]) {
-  const uint64_t MUL = 6364136223846793005ull, INC = 11634580027462260723ull;
+  const uint64_t INC = 11634580027462260723ull;
   for (int i = 0; i < 8; i++) {
-    state = state * MUL + INC;
-    const uint32_t xorshifted = (uint32_t)(((state >> 18) ^ state) >> 27);
-    const uint32_t rot = (uint32_t)(state >> 59);
-    key[i] = (xorshifted >> rot) | (xorshifted << ((32 - rot) & 31));
+    state = orc_pcg32_step(state, INC);
+    key[i] = orc_pcg32_xsh_rr(state);
   }
 }
 

@@ -193,6 +193,8 @@ uint32_t orc_sample_combined(float *logits, size_t n, const uint32_t *hist, size
 void orc_chacha_block(const uint32_t key[8], uint64_t counter, uint64_t stream, int rounds,
                       uint32_t out[16]);
 void orc_stdrng_f32(uint64_t seed, size_t n, float *out);
+uint64_t orc_pcg32_step(uint64_t state, uint64_t inc);
+uint32_t orc_pcg32_xsh_rr(uint64_t state);
 
 /* ---- ternary linear (quantization/primitives/ternary_linear.rs) ---- */
 void orc_ternary_from_f32(const float *w, size_t n, size_t k, uint8_t *blocks);

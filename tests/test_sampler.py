@@ -126,6 +126,21 @@ def test_chacha20_block_rfc8439():
     assert out.tolist() == want
 
 
+def test_pcg32_demo_stream():
+    """The seed expansion's PCG32 pieces (the LCG multiplier and the XSH-RR
+    output) against the PCG reference implementation's demo stream
+    (pcg32_srandom_r(&rng, 42, 54), then pcg32_random_r: the output of the
+    state before each step)."""
+    inc = (54 << 1) | 1
+    state = O.pcg32_step(0, inc)
+    state = O.pcg32_step((state + 42) % 2**64, inc)
+    got = []
+    for _ in range(6):
+        got.append(O.pcg32_xsh_rr(state))
+        state = O.pcg32_step(state, inc)
+    assert got == [0xA15C02B7, 0x7B47F409, 0xBA1D3330, 0x83D2F293, 0xBFA4784B, 0xCBED606E]
+
+
 def test_stdrng_stream_shape():
     u = O.stdrng_f32(42, 300)
     assert ((u >= 0) & (u < 1)).all()
