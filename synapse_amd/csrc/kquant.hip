@@ -22,6 +22,7 @@
 //   Q6_K 13 planes (ql, qh, sc) + f16 d in a [panel][block][64] array
 // so every wave64 load (lane = row) is one contiguous 1 KiB.
 #include <algorithm>
+#include <type_traits>
 #include <cmath>
 #include <vector>
 
@@ -331,14 +332,19 @@ __device__ __forceinline__ void kq_asums(const float *__restrict__ x, int ldx, i
 }
 
 // grid (panels, ksplit); lane = output row; blocks [b0, b1) of this slice.
+// WPU waves share each Q4_K / Q6_K block (wave part p decodes sub-blocks /
+// groups [p, p + 1) * 8 / WPU or 16 / WPU from only the planes they read),
+// so more waves per SIMD hide the activations' scalar-load latency: at eight
+// rows a block is ~2,800 VALU ops per lane.
 // A K split finishes in the same launch (split_k.hpp; skacc holds M rows of
 // ksplit slices of N64 slots, skcnt a counter per panel).
-template <int FMT, int M>
+template <int FMT, int M, int WPU>
 __global__ void __launch_bounds__(1024)
     k_gemv_kq(const u32x4 *__restrict__ W, const uint16_t *__restrict__ Wd,
               const float *__restrict__ x, int ldx, float *__restrict__ y, int ldy,
               unsigned *__restrict__ skacc, int *__restrict__ skcnt, int N, int B,
               int bs) {
+  static_assert(WPU == 1 || FMT != SYN_HIP_FMT_Q8_0, "Q8_0 blocks are not split");
   __shared__ int s_last;
   constexpr int NP = FMT == SYN_HIP_FMT_Q8_0 ? 2 : FMT == SYN_HIP_FMT_Q4_K ? 9 : 13;
   constexpr int BE = FMT == SYN_HIP_FMT_Q8_0 ? 32 : 256;
@@ -360,9 +366,90 @@ __global__ void __launch_bounds__(1024)
 #pragma unroll
   for (int m = 0; m < M; m++) acc[m] = 0.0f;
   const size_t pbase = (size_t)panel * B;
-  for (int b = b0 + wave; b < b1; b += nw) {
+  // Q4_K sub-blocks [S0, S0 + 8 / WPU) of block b
+  auto q4k_part = [&](auto S0c, int b) {
+    constexpr int S0 = decltype(S0c)::value, NS = 8 / WPU;
     const u32x4 *Wb = W + ((pbase + b) * NP) * 64 + lane;
-    if (FMT == SYN_HIP_FMT_Q8_0) {
+    u32x4 pl[9];
+    pl[0] = __builtin_nontemporal_load(Wb);
+#pragma unroll
+    for (int sb = S0; sb < S0 + NS; sb++) pl[1 + sb] = __builtin_nontemporal_load(Wb + (1 + sb) * 64);
+    const float d = syn_f16_to_f32_rs(pl[0].x & 0xffffu);
+    const float dmin = syn_f16_to_f32_rs(pl[0].x >> 16);
+    // 12 scale bytes = bytes 4..15 of plane 0 (gguf.rs:405-410, u8 arithmetic)
+    uint32_t sbw[3] = {pl[0].y, pl[0].z, pl[0].w};
+    auto SB = [&](int i) -> uint32_t { return (sbw[i >> 2] >> (8 * (i & 3))) & 0xffu; };
+#pragma unroll
+    for (int sb = S0; sb < S0 + NS; sb++) {
+      uint32_t sc, mn;
+      if (sb < 4) {
+        sc = SB(sb) & 63u;
+        mn = ((SB(sb + 4) >> 4) | ((SB(sb + 8) & 15u) << 4)) & 0xffu;
+      } else {
+        sc = (SB(sb) & 15u) | ((SB(sb - 4) >> 6) << 4);
+        mn = ((SB(sb + 4) >> 4) | (((SB(sb - 4) >> 4) & 12u) << 4)) & 0xffu;
+      }
+      const float scf = d * (float)sc;
+      const float mf = dmin * (float)mn;
+      const u32x4 q = pl[1 + sb];
+#pragma unroll
+      for (int m = 0; m < M; m++) {
+        const float *xa = x + (size_t)m * ldx + (size_t)b * 256 + sb * 32;
+        float t = 0.0f;
+        t = kq_dot8_nib(q.x, xa, t);
+        t = kq_dot8_nib(q.y, xa + 8, t);
+        t = kq_dot8_nib(q.z, xa + 16, t);
+        t = kq_dot8_nib(q.w, xa + 24, t);
+        const float as = asum[m * bs * GPB + (b - b0) * GPB + sb];
+        acc[m] = __builtin_fmaf(scf, t, acc[m]);
+        acc[m] = __builtin_fmaf(-mf, as, acc[m]);
+      }
+    }
+  };
+  // Q6_K groups [G0, G0 + 16 / WPU) of block b
+  auto q6k_part = [&](auto G0c, int b) {
+    constexpr int G0 = decltype(G0c)::value, NG = 16 / WPU;
+    const u32x4 *Wb = W + ((pbase + b) * NP) * 64 + lane;
+    u32x4 pl[13];
+#pragma unroll
+    for (int g = G0; g < G0 + NG; g++) {
+      if (g == G0 || (g & 1) == 0) pl[g >> 1] = __builtin_nontemporal_load(Wb + (g >> 1) * 64);
+      if (g == G0 || (g & 3) == 0)
+        pl[8 + (g >> 2)] = __builtin_nontemporal_load(Wb + (8 + (g >> 2)) * 64);
+    }
+    pl[12] = __builtin_nontemporal_load(Wb + 12 * 64);
+    const float d = syn_f16_to_f32_rs(Wd[(pbase + b) * 64 + lane]);
+    const uint32_t scw[4] = {pl[12].x, pl[12].y, pl[12].z, pl[12].w};
+#pragma unroll
+    for (int g = G0; g < G0 + NG; g++) {
+      // ql bytes 8g..8g+7: plane g/2, dwords 2*(g%2), 2*(g%2)+1
+      const u32x4 qp = pl[g >> 1];
+      const uint32_t lo0 = (g & 1) ? qp.z : qp.x, lo1 = (g & 1) ? qp.w : qp.y;
+      // qh bytes 4g..4g+3: plane 8 + g/4, dword g%4
+      const u32x4 hp = pl[8 + (g >> 2)];
+      const uint32_t hi = (g & 3) == 0 ? hp.x : (g & 3) == 1 ? hp.y : (g & 3) == 2 ? hp.z : hp.w;
+      const float scale = (float)(int8_t)(scw[g >> 2] >> (8 * (g & 3))) * d;
+#pragma unroll
+      for (int m = 0; m < M; m++) {
+        const float *xa = x + (size_t)m * ldx + (size_t)b * 256 + g * 16;
+        float t = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+          const uint32_t lo = ((i < 8 ? lo0 : lo1) >> (4 * (i & 7))) & 15u;
+          const uint32_t h2 = (hi >> (2 * i)) & 3u;
+          t = __builtin_fmaf(xa[i], (float)(lo | (h2 << 4)), t);
+        }
+        const float as = asum[m * bs * GPB + (b - b0) * GPB + g];
+        const float v = t - 32.0f * as;
+        acc[m] = __builtin_fmaf(v, scale, acc[m]);
+      }
+    }
+  };
+  using I0 = std::integral_constant<int, 0>;
+  for (int t = wave; t < nb * WPU; t += nw) {
+    const int b = b0 + t / WPU, part = t % WPU;
+    if constexpr (FMT == SYN_HIP_FMT_Q8_0) {
+      const u32x4 *Wb = W + ((pbase + b) * NP) * 64 + lane;
       const u32x4 q0 = __builtin_nontemporal_load(Wb);
       const u32x4 q1 = __builtin_nontemporal_load(Wb + 64);
       const float d = syn_f16_to_f32_rs(Wd[(pbase + b) * 64 + lane]);
@@ -380,70 +467,30 @@ __global__ void __launch_bounds__(1024)
         s = kq_dot4_i8(q1.w, xa + 28, s);
         acc[m] = __builtin_fmaf(s, d, acc[m]);
       }
-    } else if (FMT == SYN_HIP_FMT_Q4_K) {
-      u32x4 pl[9];
-#pragma unroll
-      for (int p = 0; p < 9; p++) pl[p] = __builtin_nontemporal_load(Wb + p * 64);
-      const float d = syn_f16_to_f32_rs(pl[0].x & 0xffffu);
-      const float dmin = syn_f16_to_f32_rs(pl[0].x >> 16);
-      // 12 scale bytes = bytes 4..15 of plane 0 (gguf.rs:405-410, u8 arithmetic)
-      uint32_t sbw[3] = {pl[0].y, pl[0].z, pl[0].w};
-      auto SB = [&](int i) -> uint32_t { return (sbw[i >> 2] >> (8 * (i & 3))) & 0xffu; };
-#pragma unroll
-      for (int s = 0; s < 8; s++) {
-        uint32_t sc, mn;
-        if (s < 4) {
-          sc = SB(s) & 63u;
-          mn = ((SB(s + 4) >> 4) | ((SB(s + 8) & 15u) << 4)) & 0xffu;
-        } else {
-          sc = (SB(s) & 15u) | ((SB(s - 4) >> 6) << 4);
-          mn = ((SB(s + 4) >> 4) | (((SB(s - 4) >> 4) & 12u) << 4)) & 0xffu;
-        }
-        const float scf = d * (float)sc;
-        const float mf = dmin * (float)mn;
-        const u32x4 q = pl[1 + s];
-#pragma unroll
-        for (int m = 0; m < M; m++) {
-          const float *xa = x + (size_t)m * ldx + (size_t)b * 256 + s * 32;
-          float t = 0.0f;
-          t = kq_dot8_nib(q.x, xa, t);
-          t = kq_dot8_nib(q.y, xa + 8, t);
-          t = kq_dot8_nib(q.z, xa + 16, t);
-          t = kq_dot8_nib(q.w, xa + 24, t);
-          const float as = asum[m * bs * GPB + (b - b0) * GPB + s];
-          acc[m] = __builtin_fmaf(scf, t, acc[m]);
-          acc[m] = __builtin_fmaf(-mf, as, acc[m]);
-        }
+    } else if constexpr (WPU == 1) {
+      if constexpr (FMT == SYN_HIP_FMT_Q4_K) q4k_part(I0{}, b);
+      else q6k_part(I0{}, b);
+    } else if constexpr (WPU == 2) {
+      if (part == 0) {
+        if constexpr (FMT == SYN_HIP_FMT_Q4_K) q4k_part(I0{}, b);
+        else q6k_part(I0{}, b);
+      } else {
+        if constexpr (FMT == SYN_HIP_FMT_Q4_K) q4k_part(std::integral_constant<int, 4>{}, b);
+        else q6k_part(std::integral_constant<int, 8>{}, b);
       }
-    } else {  // Q6_K
-      u32x4 pl[13];
-#pragma unroll
-      for (int p = 0; p < 13; p++) pl[p] = __builtin_nontemporal_load(Wb + p * 64);
-      const float d = syn_f16_to_f32_rs(Wd[(pbase + b) * 64 + lane]);
-      const uint32_t scw[4] = {pl[12].x, pl[12].y, pl[12].z, pl[12].w};
-#pragma unroll
-      for (int s = 0; s < 16; s++) {
-        // ql bytes 8s..8s+7: plane s/2, dwords 2*(s%2), 2*(s%2)+1
-        const u32x4 qp = pl[s >> 1];
-        const uint32_t lo0 = (s & 1) ? qp.z : qp.x, lo1 = (s & 1) ? qp.w : qp.y;
-        // qh bytes 4s..4s+3: plane 8 + s/4, dword s%4
-        const u32x4 hp = pl[8 + (s >> 2)];
-        const uint32_t hi = (s & 3) == 0 ? hp.x : (s & 3) == 1 ? hp.y : (s & 3) == 2 ? hp.z : hp.w;
-        const float scale = (float)(int8_t)(scw[s >> 2] >> (8 * (s & 3))) * d;
-#pragma unroll
-        for (int m = 0; m < M; m++) {
-          const float *xa = x + (size_t)m * ldx + (size_t)b * 256 + s * 16;
-          float t = 0.0f;
-#pragma unroll
-          for (int i = 0; i < 16; i++) {
-            const uint32_t lo = ((i < 8 ? lo0 : lo1) >> (4 * (i & 7))) & 15u;
-            const uint32_t h2 = (hi >> (2 * i)) & 3u;
-            t = __builtin_fmaf(xa[i], (float)(lo | (h2 << 4)), t);
-          }
-          const float as = asum[m * bs * GPB + (b - b0) * GPB + s];
-          const float v = t - 32.0f * as;
-          acc[m] = __builtin_fmaf(v, scale, acc[m]);
-        }
+    } else {  // WPU == 4
+      if (part == 0) {
+        if constexpr (FMT == SYN_HIP_FMT_Q4_K) q4k_part(I0{}, b);
+        else q6k_part(I0{}, b);
+      } else if (part == 1) {
+        if constexpr (FMT == SYN_HIP_FMT_Q4_K) q4k_part(std::integral_constant<int, 2>{}, b);
+        else q6k_part(std::integral_constant<int, 4>{}, b);
+      } else if (part == 2) {
+        if constexpr (FMT == SYN_HIP_FMT_Q4_K) q4k_part(std::integral_constant<int, 4>{}, b);
+        else q6k_part(std::integral_constant<int, 8>{}, b);
+      } else {
+        if constexpr (FMT == SYN_HIP_FMT_Q4_K) q4k_part(std::integral_constant<int, 6>{}, b);
+        else q6k_part(std::integral_constant<int, 12>{}, b);
       }
     }
   }
@@ -584,15 +631,19 @@ __global__ void __launch_bounds__(NW * 64)
   }
 }
 
+// Q4_K / Q6_K: four waves per block (LLaMA-3B shapes, eight rows: gate
+// 8192 x 3072 16.2 us against 16.7 with two and 24.4 with one, q 11.8
+// against 13.8 and 21.9, down 23.2 against 30.1 and 28.5)
 template <int FMT, int M>
 static void launch_kq(const GemvPlan &p, const void *W, const uint16_t *Wd, const float *x,
                       int ldx, float *y, int ldy, const SplitKSlots &sk, int N, hipStream_t s) {
   constexpr int BE = FMT == SYN_HIP_FMT_Q8_0 ? 32 : 256;
   constexpr int GRP = FMT == SYN_HIP_FMT_Q4_K ? 32 : 16;
-  const int waves = std::min(p.waves, M >= 4 ? 8 : 16);
+  constexpr int WPU = FMT == SYN_HIP_FMT_Q8_0 ? 1 : 4;
+  const int waves = WPU == 1 ? std::min(p.waves, M >= 4 ? 8 : 16) : std::min(16, p.cs * WPU);
   const size_t as = FMT == SYN_HIP_FMT_Q8_0 ? 0 : (size_t)M * p.cs * (BE / GRP);
   const size_t shm = (as + (size_t)waves * M * 64) * sizeof(float);
-  hipLaunchKernelGGL((k_gemv_kq<FMT, M>), dim3(p.panels, p.ksplit), dim3(64 * waves), shm, s,
+  hipLaunchKernelGGL((k_gemv_kq<FMT, M, WPU>), dim3(p.panels, p.ksplit), dim3(64 * waves), shm, s,
                      (const u32x4 *)W, Wd, x, ldx, y, ldy, sk.slots(),
                      sk.counters(), N, p.chunks, p.cs);
 }
