@@ -526,7 +526,8 @@ __global__ void __launch_bounds__(1024)
 }
 
 // ------------------------------------------------------------------ batch-1 GEMV
-// Q4_K / Q6_K at M = 1: one lane per row, the unit decoders of kq_unit.hpp.
+// Q4_K / Q6_K at M = 1 on grids without a K split (lm_head-sized N): one lane
+// per row, the unit decoders of kq_unit.hpp.
 // A K split finishes in the same launch (split_k.hpp).
 template <int FMT, int NW, int U>
 __global__ void __launch_bounds__(NW * 64)
@@ -697,7 +698,11 @@ syn_status_t QLinearKQ::gemv(size_t m, const float *d_x, size_t ldx, float *d_y,
     float *ym = d_y + m0 * ldy;
     const size_t gpb = fmt == SYN_HIP_FMT_Q4_K ? 8 : 16;
     const size_t shm_h = ((size_t)p.cs * gpb + 16 * 64) * sizeof(float);
-    if (mb == 1 && fmt != SYN_HIP_FMT_Q8_0 && shm_h <= 60 * 1024) {
+    // one row: the one-lane-per-row kernel on grids without a K split (the
+    // lm_head, 128256 x 3072 Q6_K: 60.6 us against 70.4 for the split
+    // blocks); split grids take the split blocks (LLaMA-3B q 6.42 against
+    // 7.18 us, gate 8.02 against 8.49, down 10.74 against 13.64)
+    if (mb == 1 && fmt != SYN_HIP_FMT_Q8_0 && p.ksplit == 1 && shm_h <= 60 * 1024) {
       if (fmt == SYN_HIP_FMT_Q4_K)
         SYN_TRY(launch_kqh<SYN_HIP_FMT_Q4_K>(p, wq.as<u32x4>(), Wd, xm, ym, sk, (int)n, shm_h, s));
       else
