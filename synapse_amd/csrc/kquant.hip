@@ -376,6 +376,20 @@ __global__ void __launch_bounds__(1024)
     for (int sb = S0; sb < S0 + NS; sb++) pl[1 + sb] = __builtin_nontemporal_load(Wb + (1 + sb) * 64);
     const float d = syn_f16_to_f32_rs(pl[0].x & 0xffffu);
     const float dmin = syn_f16_to_f32_rs(pl[0].x >> 16);
+    if constexpr (true) {
+      // the in-place f16 subnormal decode of kq_unit.hpp (one v_fma_mix per
+      // element and row; the masks are shared by the rows): per Q4_K block
+      // ~7 % fewer VALU ops than extract + convert + FMA at eight rows, ~27 %
+      // at one (gate 8192 x 3072: 7.69 against 8.0 us at one row, 15.4
+      // against 16.1 at eight)
+#pragma unroll
+      for (int sb = S0; sb < S0 + NS; sb++)
+#pragma unroll
+        for (int m = 0; m < M; m++)
+          kq4_stage(pl, sb, d, dmin, x + (size_t)m * ldx + (size_t)b * 256 + sb * 32,
+                    asum[m * bs * GPB + (b - b0) * GPB + sb], acc[m]);
+      return;
+    }
     // 12 scale bytes = bytes 4..15 of plane 0 (gguf.rs:405-410, u8 arithmetic)
     uint32_t sbw[3] = {pl[0].y, pl[0].z, pl[0].w};
     auto SB = [&](int i) -> uint32_t { return (sbw[i >> 2] >> (8 * (i & 3))) & 0xffu; };
@@ -419,6 +433,19 @@ __global__ void __launch_bounds__(1024)
     }
     pl[12] = __builtin_nontemporal_load(Wb + 12 * 64);
     const float d = syn_f16_to_f32_rs(Wd[(pbase + b) * 64 + lane]);
+    if constexpr (M == 1) {
+      // the subnormal decode takes two v_fma_mix per element and row (low and
+      // high bit classes): ~25 % fewer VALU ops than extract + convert + FMA
+      // at one row (down 8192 -> 3072: 9.27 against 10.71 us), more from two
+      // rows on (11.67 against 10.81 us at two)
+#pragma unroll
+      for (int g = G0; g < G0 + NG; g++)
+#pragma unroll
+        for (int m = 0; m < M; m++)
+          kq6_group(pl, g, d, x + (size_t)m * ldx + (size_t)b * 256 + g * 16,
+                    asum[m * bs * GPB + (b - b0) * GPB + g], acc[m]);
+      return;
+    }
     const uint32_t scw[4] = {pl[12].x, pl[12].y, pl[12].z, pl[12].w};
 #pragma unroll
     for (int g = G0; g < G0 + NG; g++) {
