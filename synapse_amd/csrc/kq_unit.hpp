@@ -11,9 +11,10 @@
 // few masks per dword instead of an extract, a convert and an FMA:
 //   nibbles (Q4_K, Q6_K low bits), element k at bits 4k of a dword:
 //     w & 0x000f000f -> (e0, e4)   w & 0x00f000f0 -> 16 (e1, e5)   (w>>8): (e2,e6), 16 (e3,e7)
-//   Q6_K high 2-bit fields, element k at bits 2k of a 16-bit half:
-//     h & 0x00030003 -> (m0, m8)   & 0x000c000c -> 4 (m1, m9)   & 0x00300030 -> 16 (m2, m10)
-//     & 0x00c000c0 -> 64 (m3, m11)                               (h>>8): m4..m7 with m12..m15
+//   Q6_K: each ql dword's nibbles joined in place with their two-bit qh
+//     fields (the two qh bytes spread to the two halves, one byte permute),
+//     so the six-bit value lo + 16 hi of a pair of elements is one masked
+//     dword of class 1 or 16 and each element still costs one FMA
 // Each power-of-two class has its own f32 accumulator; the classes are
 // combined with exact power-of-two FMAs, so the values are the f32 path's
 // (up to summation order).  Sub-block sums of the activations (`as`: Q4_K's
@@ -94,30 +95,32 @@ __device__ __forceinline__ void kq6_group(const u32x4 *pl, int g, float d,
   const u32x4 hp = pl[8 + (g >> 2)];
   const uint32_t hi = (g & 3) == 0 ? hp.x : (g & 3) == 1 ? hp.y : (g & 3) == 2 ? hp.z : hp.w;
   const float scale = (float)(int8_t)(scw[g >> 2] >> (8 * (g & 3))) * d;
-  float l1 = 0.0f, l16 = 0.0f;
-  kq_nib8(lo0, xc, l1, l16);
-  kq_nib8(lo1, xc + 8, l1, l16);
-  float h1 = 0.0f, h4 = 0.0f, h16 = 0.0f, h64 = 0.0f;
+  // the six-bit value lo + 16 hi assembled in place: for the eight elements
+  // of one ql dword L (nibble of element i at bits 4i), H = the two qh bytes
+  // of those elements in the two 16-bit halves (field of element i at bits
+  // 2(i % 4) of its half); each pair (i, i + 4) then sits in one dword as
+  // two f16 subnormals of class 1 (bits 0-5) or 16 (bits 4-9)
+  float a1 = 0.0f, a16 = 0.0f;
 #pragma unroll
   for (int half = 0; half < 2; half++) {
-    const uint32_t hw = hi >> (8 * half);
-    const float *xh = xc + 4 * half;
-    const kq_h2 a0 = kq_as_h2(hw & 0x00030003u), a1 = kq_as_h2(hw & 0x000c000cu);
-    const kq_h2 a2 = kq_as_h2(hw & 0x00300030u), a3 = kq_as_h2(hw & 0x00c000c0u);
-    h1 = __builtin_fmaf((float)a0.x, xh[0], h1);
-    h4 = __builtin_fmaf((float)a1.x, xh[1], h4);
-    h16 = __builtin_fmaf((float)a2.x, xh[2], h16);
-    h64 = __builtin_fmaf((float)a3.x, xh[3], h64);
-    h1 = __builtin_fmaf((float)a0.y, xh[8], h1);
-    h4 = __builtin_fmaf((float)a1.y, xh[9], h4);
-    h16 = __builtin_fmaf((float)a2.y, xh[10], h16);
-    h64 = __builtin_fmaf((float)a3.y, xh[11], h64);
+    const uint32_t L = half ? lo1 : lo0, L8 = L >> 8;
+    const uint32_t hb = half ? hi >> 16 : hi;
+    const uint32_t H = (hb & 0xffu) | ((hb << 8) & 0x00ff0000u);
+    const kq_h2 p0 = kq_as_h2((L & 0x000f000fu) | ((H << 4) & 0x00300030u));   // (e0, e4) x1
+    const kq_h2 p1 = kq_as_h2((L & 0x00f000f0u) | ((H << 6) & 0x03000300u));   // (e1, e5) x16
+    const kq_h2 p2 = kq_as_h2((L8 & 0x000f000fu) | (H & 0x00300030u));         // (e2, e6) x1
+    const kq_h2 p3 = kq_as_h2((L8 & 0x00f000f0u) | ((H << 2) & 0x03000300u));  // (e3, e7) x16
+    const float *x = xc + 8 * half;
+    a1 = __builtin_fmaf((float)p0.x, x[0], a1);
+    a16 = __builtin_fmaf((float)p1.x, x[1], a16);
+    a1 = __builtin_fmaf((float)p2.x, x[2], a1);
+    a16 = __builtin_fmaf((float)p3.x, x[3], a16);
+    a1 = __builtin_fmaf((float)p0.y, x[4], a1);
+    a16 = __builtin_fmaf((float)p1.y, x[5], a16);
+    a1 = __builtin_fmaf((float)p2.y, x[6], a1);
+    a16 = __builtin_fmaf((float)p3.y, x[7], a16);
   }
-  // q = lo + 16 hi; sum q x = 2^24 * (lo + 16 hi) with the classes rescaled
-  const float hs = __builtin_fmaf(
-      h64, 0.015625f, __builtin_fmaf(h16, 0.0625f, __builtin_fmaf(h4, 0.25f, h1)));
-  const float ls = __builtin_fmaf(l16, 0.0625f, l1);
-  const float t = __builtin_fmaf(hs, 16.0f, ls) * 16777216.0f;
+  const float t = __builtin_fmaf(a16, 0.0625f, a1) * 16777216.0f;
   const float v = t - 32.0f * as;
   acc = __builtin_fmaf(v, scale, acc);
 }

@@ -433,11 +433,12 @@ __global__ void __launch_bounds__(1024)
     }
     pl[12] = __builtin_nontemporal_load(Wb + 12 * 64);
     const float d = syn_f16_to_f32_rs(Wd[(pbase + b) * 64 + lane]);
-    if constexpr (M == 1) {
-      // the subnormal decode takes two v_fma_mix per element and row (low and
-      // high bit classes): ~25 % fewer VALU ops than extract + convert + FMA
-      // at one row (down 8192 -> 3072: 9.27 against 10.71 us), more from two
-      // rows on (11.67 against 10.81 us at two)
+    if constexpr (true) {
+      // the in-place six-bit decode of kq_unit.hpp (one v_fma_mix per element
+      // and row, the masks shared by the rows; down 8192 -> 3072: 8.9, 10.0
+      // and 23.0 us at one, two and eight rows against 9.2, 10.8 and 23.3
+      // with two bit classes per element, 10.7, 10.8 and 23.3 with extract +
+      // convert + FMA)
 #pragma unroll
       for (int g = G0; g < G0 + NG; g++)
 #pragma unroll
