@@ -968,7 +968,7 @@ static syn_status_t kq_gemm_f16(int fmt, bool exact, const u32x4 *W, const uint1
   // 256 workgroups.  Every split adds its partial tile into Y with f32
   // atomics, and that traffic outweighs idle CUs beyond one workgroup per
   // CU (Q8_0, 128 x 128 tiles, M = 512: q 4096 -> 4096 42.0 us in two parts,
-  // 51.4 in four; k/v 4096 -> 1024 23.9 us in four, 29.0 in two; with
+  // 51.4 in four; k/v 4096 -> 1024 23.9 us in four, 29.0 in two, 28.3 in eight; with
   // 256 x 128 tiles in three parts 46.9 and 29.9).
   constexpr int kMaxSplit = 4;
   const bool big = cdiv(n, PG3N) * cdiv(m, PG3M) >= 192;
