@@ -184,8 +184,10 @@ def test_device_expf_matches_glibc():
                                    # 128 x 64 tiles with eight waves (fewer than 256 tiles
                                    # of 128 x 128, at least 256 of 128 x 64), ragged
                                    (300, 1152, 6000),
-                                   # exactly 256 tiles of 128 x 128: three stages
-                                   (250, 640, 16384),
+                                   # exactly 256 tiles of 128 x 128: three stages (and
+                                   # the two accumulator sets over two whole chunks
+                                   # and a tail)
+                                   (250, 640, 16384), (250, 1152, 16384),
                                    # chunk counts: K of 1 step (no whole KC chunk), 3, 12
                                    # (three whole chunks, no tail) and 14 (three and a tail
                                    # of two), on each direct-load tile shape
