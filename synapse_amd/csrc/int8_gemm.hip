@@ -410,10 +410,25 @@ __global__ void __launch_bounds__(128 * WR)
   }
   read(0, 0, 0);
   if constexpr (!DF) {
-    // one accumulator set, folded after each chunk's last step
+    // one accumulator set, folded after each chunk's last step (element
+    // order mt, nt, r)
+    auto fold1 = [&]() {
+#pragma unroll
+      for (int mt = 0; mt < MT; mt++)
+#pragma unroll
+        for (int nt = 0; nt < NT; nt++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) {
+            const float f = (float)acc[0][mt][nt][r] *
+                            sa_l[wr * WM + mt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3)];
+            const float t = f * sb[nt];
+            cf[mt][nt][r] = cf[mt][nt][r] + t;
+            acc[0][mt][nt][r] = 0;
+          }
+    };
     for (int t = 0; t < nsteps; t++) {
       step(t, 0, P0{}, NoFold{});
-      if (((t + 1) & 3) == 0 || t + 1 == nsteps) fold_all(P0{});
+      if (((t + 1) & 3) == 0 || t + 1 == nsteps) fold1();
     }
   } else {
     const int nfull = nsteps >> 2;
