@@ -333,6 +333,10 @@ __global__ void __launch_bounds__(128 * WR)
   };
   // fold of accumulator element r of set Q: C += (f32(acc) * sa) * sb, and
   // the element starts the set's next chunk at zero
+  // the row scales of the fold in registers, except with three stages,
+  // whose 256 VGPRs then spill (13 against 3; 256 x 4096 x 16384: 992-999
+  // TOP/s with them in registers against 1032-1044 from LDS)
+  constexpr bool kSar = DF && NS < 3;
   float sar[MT][16];
   auto fold_el = [&](auto Qc, int r) {
     constexpr int Q = decltype(Qc)::value;
@@ -340,8 +344,7 @@ __global__ void __launch_bounds__(128 * WR)
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
       for (int nt = 0; nt < NT; nt++) {
-        const float sa =
-            DF ? sar[mt][r] : sa_l[wr * WM + mt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3)];
+        const float sa = kSar ? sar[mt][r] : sa_l[wr * WM + mt * 32 + 8 * (r >> 2) + 4 * lh + (r & 3)];
         const float f = (float)acc[Q][mt][nt][r] * sa;
         const float t = f * sb[nt];
         cf[mt][nt][r] = cf[mt][nt][r] + t;
@@ -401,7 +404,7 @@ __global__ void __launch_bounds__(128 * WR)
   };
 
   kr_publish<(NS - 1) * AFTER>();
-  if constexpr (DF) {
+  if constexpr (kSar) {
 #pragma unroll
     for (int mt = 0; mt < MT; mt++)
 #pragma unroll
